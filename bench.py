@@ -1,0 +1,249 @@
+"""FFN-layer throughput of the MI355X FfnAgent path at the Qwen3-8B shape.
+
+One step = one hipGraph replay of the Dense mailbox step for a batch of T
+tokens: gather T seeded slots of an 8192-slot bf16 mailbox with the fused
+RMSNorm, gate_up [4096 -> 2 x 12288] + SiLU*mul, down [12288 -> 4096],
+scatter back into the same slots.  Inputs are resident in HBM before timing.
+
+Prints ONE JSON line: the headline at T = --tokens (default 2048, the
+MFMA-bound north-star point), a ``decode`` entry at T = 32 (HBM-bound), the
+batch sweep of BASELINE config 3, the roofline of the dominant kernel
+(measured with HIP events on the Lane stream it runs on) and the CPU
+baseline (the oracle's torch-CPU restatement on the host cores).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO_ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO_ROOT))
+
+HIDDEN, INTERMEDIATE = 4096, 12288
+POOL_SLOTS = 8192
+SWEEP = (1, 4, 16, 32, 64, 256, 1024, 2048, 4096)
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def parse_args() -> argparse.Namespace:
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=200)
+    parser.add_argument("--warmup", type=int, default=20)
+    parser.add_argument("--tokens", type=int, default=2048)
+    parser.add_argument("--decode-tokens", type=int, default=32)
+    parser.add_argument("--sweep-steps", type=int, default=30)
+    parser.add_argument("--no-sweep", action="store_true")
+    parser.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample length")
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    return parser.parse_args()
+
+
+def layer_flops(tokens: int) -> float:
+    return 6.0 * tokens * HIDDEN * INTERMEDIATE
+
+
+def layer_bytes(tokens: int) -> float:
+    # weights + norm weight + gathered rows + scattered rows + int32 slot ids
+    return 6.0 * HIDDEN * INTERMEDIATE + 2 * HIDDEN + 4.0 * tokens * HIDDEN + 4.0 * tokens
+
+
+def gate_up_flops(tokens: int) -> float:
+    return 4.0 * tokens * HIDDEN * INTERMEDIATE
+
+
+def gate_up_bytes(tokens: int) -> float:
+    # i_proj weights + the gathered batch read + the activated intermediate written
+    return 4.0 * HIDDEN * INTERMEDIATE + 2.0 * tokens * HIDDEN + 2.0 * tokens * INTERMEDIATE
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(
+            "bench.py measures one MI355X: the FfnAgent path here is single-GPU (no collectives); "
+            "run it with --gpus 1.",
+            file=sys.stderr,
+        )
+        return 2
+
+    import torch
+
+    from crosspool_amd import _native, dense
+    from crosspool_amd.agent import FfnAgent
+    from crosspool_amd.weights import DenseFfnWeights
+    from oracle import ffn_oracle as o
+
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    max_tokens = max(SWEEP + (args.tokens, args.decode_tokens))
+
+    pool_cpu = o.generate_hidden_states(POOL_SLOTS, HIDDEN, 17)
+    w_gate_up, w_down, norm_weight = o.generate_layer(HIDDEN, INTERMEDIATE, 18)
+    slots_cpu = o.generate_slots(POOL_SLOTS, max_tokens, 19)
+    pool = pool_cpu.to(device)
+    slots = torch.from_numpy(slots_cpu).to(device)
+    weights = DenseFfnWeights.from_tensors(w_gate_up.to(device), w_down.to(device))
+    norm = norm_weight.to(device)
+
+    agent = FfnAgent(device)
+    agent.register_layer(instance_index=0, layer_ordinal=0, weights=weights, norm_weight=norm, eps=1e-6)
+    agent.materialize(maximum_row_capacity=max_tokens)
+    lane = agent.lanes[0]
+    torch.cuda.synchronize()
+
+    def replay(tokens: int) -> None:
+        lane.replay(instance_index=0, layer_ordinal=0, pool=pool, slots=slots, rows=tokens, stream=lane.stream)
+
+    def time_replays(tokens: int, steps: int, warmup: int) -> float:
+        for _ in range(warmup):
+            replay(tokens)
+        torch.cuda.synchronize()
+        start = time.perf_counter()
+        for _ in range(steps):
+            replay(tokens)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - start) / steps
+
+    # ---------------------------------------------------------------- headline
+    tokens = args.tokens
+    seconds = time_replays(tokens, args.steps, args.warmup)
+    agent.check_health()
+
+    # ---------------------------------------------------------------- dominant kernel (events)
+    def kernel_roofline(tokens: int, steps: int) -> dict:
+        x = torch.empty((tokens, HIDDEN), dtype=torch.bfloat16, device=device)
+        dense.gather_rmsnorm(pool, slots[:tokens], norm_weight=norm, out=x, stream=lane.stream)
+        h = torch.empty((tokens, INTERMEDIATE), dtype=torch.bfloat16, device=device)
+        for _ in range(3):
+            dense.gate_up_silu(x, weights.i_proj.values, out=h, stream=lane.stream)
+        begin = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        begin.record(lane.stream)
+        for _ in range(steps):
+            dense.gate_up_silu(x, weights.i_proj.values, out=h, stream=lane.stream)
+        end.record(lane.stream)
+        end.synchronize()
+        per_launch = begin.elapsed_time(end) / 1e3 / steps
+        variant = _native.gemm_variant(tokens, 2 * INTERMEDIATE, HIDDEN, True)
+        if variant.startswith("tile"):
+            achieved = gate_up_flops(tokens) / per_launch / 1e12
+            return {
+                "kernel": variant, "tokens": tokens, "bound": "mfma", "achieved": round(achieved, 1),
+                "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
+                "traffic": None, "avg_launch_us": round(per_launch * 1e6, 2),
+            }
+        achieved = gate_up_bytes(tokens) / per_launch / 1e9
+        return {
+            "kernel": variant, "tokens": tokens, "bound": "hbm", "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None, "avg_launch_us": round(per_launch * 1e6, 2),
+        }
+
+    roofline = kernel_roofline(tokens, max(20, min(args.steps, 200)))
+
+    # ---------------------------------------------------------------- decode point
+    decode_seconds = time_replays(args.decode_tokens, args.steps, args.warmup)
+    decode = {
+        "tokens": args.decode_tokens,
+        "tokens_per_s": round(args.decode_tokens / decode_seconds, 1),
+        "us_per_layer": round(decode_seconds * 1e6, 2),
+        "layer_hbm_frac": round(layer_bytes(args.decode_tokens) / decode_seconds / 1e9 / HBM_PEAK_GBS, 4),
+        "roofline": kernel_roofline(args.decode_tokens, 200),
+    }
+
+    # ---------------------------------------------------------------- sweep
+    sweep = []
+    if not args.no_sweep:
+        for t in SWEEP:
+            s = time_replays(t, args.sweep_steps, 5)
+            hbm = layer_bytes(t) / s / 1e9 / HBM_PEAK_GBS
+            mfma = layer_flops(t) / s / 1e12 / MFMA_BF16_PEAK_TFLOPS
+            sweep.append({
+                "tokens": t, "us": round(s * 1e6, 2), "tokens_per_s": round(t / s, 1),
+                "hbm_frac": round(hbm, 4), "mfma_frac": round(mfma, 4),
+            })
+    agent.check_health()
+
+    # ---------------------------------------------------------------- CPU baseline
+    cpu_baseline = None
+    if not args.no_cpu_baseline:
+        threads = len(os.sched_getaffinity(0))
+        torch.set_num_threads(threads)
+        sample_tokens = 256
+        gate_up_f32 = w_gate_up.float()
+        down_f32 = w_down.float()
+        sample_slots = slots_cpu[:sample_tokens]
+        work_pool = pool_cpu.clone()
+
+        def cpu_step() -> None:
+            x = o.rmsnorm(o.gather(work_pool, sample_slots), norm_weight, 1e-6)
+            projected = torch.mm(x.float(), gate_up_f32.t())
+            activated = o.gated_silu(projected[:, 0::2].bfloat16(), projected[:, 1::2].bfloat16())
+            y = torch.mm(activated.float(), down_f32.t()).bfloat16()
+            o.scatter(work_pool, sample_slots, y)
+
+        for _ in range(2):
+            cpu_step()
+        durations = []
+        deadline = time.perf_counter() + args.cpu_seconds
+        while len(durations) < 3 or time.perf_counter() < deadline:
+            started = time.perf_counter()
+            cpu_step()
+            durations.append(time.perf_counter() - started)
+        median = statistics.median(durations)
+        cpu_baseline = {
+            "value": round(sample_tokens / median, 1),
+            "unit": "tokens/s",
+            "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": (
+                f"{len(durations)} runs of one {sample_tokens}-token Qwen3-8B mailbox step (gather, RMSNorm, fp32 "
+                f"matmuls with bf16 stage rounding, scatter) on {threads} affinity cores of {os.cpu_count()}; "
+                "median; weights pre-widened to fp32 outside the timing"
+            ),
+        }
+
+    result = {
+        "metric": "FFN-layer tokens/sec at Qwen3-8B shape",
+        "value": round(tokens / seconds, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(seconds * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights, random-init)",
+        "config": {
+            "workload": "qwen3-8b-ffn-layer (BASELINE config 3)",
+            "hidden": HIDDEN,
+            "intermediate": INTERMEDIATE,
+            "tokens": tokens,
+            "mailbox_slots": POOL_SLOTS,
+            "rmsnorm_fused_into_gather": True,
+            "execution": "hipGraph replay per layer signature",
+            "layer_mfma_frac": round(layer_flops(tokens) / seconds / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+            "layer_hbm_frac": round(layer_bytes(tokens) / seconds / 1e9 / HBM_PEAK_GBS, 4),
+        },
+        "roofline": roofline,
+        "cpu_baseline": cpu_baseline,
+        "decode": decode,
+        "sweep": sweep,
+    }
+    agent.close()
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

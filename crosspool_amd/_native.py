@@ -1,0 +1,128 @@
+"""ctypes binding of the C ABI in ``include/xpool_amd.h``.
+
+Replaces the pybind11 module ``xpool.native`` (src/cext-bindings/module.cpp:16)
+for the FfnAgent execution path.  The library is loaded lazily from
+``crosspool_amd/_lib/libxpool_amd.so``; when it is missing every entry point
+raises :class:`NativeUnavailableError` -- there is no CPU fallback.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+LIBRARY_PATH = Path(__file__).resolve().parent / "_lib" / "libxpool_amd.so"
+HEADER_PATH = Path(__file__).resolve().parent.parent / "include" / "xpool_amd.h"
+
+XP_OK = 0
+XP_ERROR_INVALID_ARGUMENT = 1
+XP_ERROR_HIP = 2
+XP_ERROR_STATE = 3
+XP_ERROR_NOT_FOUND = 4
+XP_ERROR_CAPACITY = 5
+XP_ERROR_UNSUPPORTED = 6
+XP_FAULT_SLOT_OUT_OF_RANGE = 1
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_INT = ctypes.c_int
+_F32 = ctypes.c_float
+_SIZE = ctypes.c_size_t
+
+# name -> (restype, argtypes)
+SIGNATURES: dict[str, tuple[object, list[object]]] = {
+    "xp_abi_version": (_INT, []),
+    "xp_last_error": (_SIZE, [ctypes.c_char_p, _SIZE]),
+    "xp_copy_bytes": (_INT, [_P, _P, _SIZE, _P]),
+    "xp_gather_rmsnorm": (_INT, [_P, _I64, _I64, _P, _I64, _P, _F32, _P, _P, _P]),
+    "xp_scatter": (_INT, [_P, _I64, _I64, _P, _P, _I64, _P, _P]),
+    "xp_gemm_gate_up_silu": (_INT, [_P, _I64, _I64, _P, _I64, _P, _F32, _F32, _F32, _P]),
+    "xp_gemm_down": (_INT, [_P, _I64, _I64, _P, _I64, _P, _P, _I64, _P]),
+    "xp_dense_workspace_bytes": (_SIZE, [_I64, _I64, _I64]),
+    "xp_dense_step": (_INT, [_P, _P, _I64, _P, _I64, _I64, _I64, _P, _P, _P, _F32, _P, _SIZE, _P, _P]),
+    "xp_gemm_variant": (_SIZE, [_I64, _I64, _I64, _INT, ctypes.c_char_p, _SIZE]),
+    "xp_agent_create": (_INT, [_INT, ctypes.POINTER(_P)]),
+    "xp_agent_destroy": (_INT, [_P]),
+    "xp_layer_register": (_INT, [_P, _INT, _INT, _I64, _I64, _P, _P, _P, _F32]),
+    "xp_lane_create": (_INT, [_P, _P, _SIZE, ctypes.POINTER(_P)]),
+    "xp_lane_destroy": (_INT, [_P]),
+    "xp_lane_stream": (_INT, [_P, ctypes.POINTER(_P)]),
+    "xp_lane_check_health": (_INT, [_P, ctypes.POINTER(ctypes.c_uint32)]),
+    "xp_lane_clear_fault": (_INT, [_P]),
+    "xp_lane_synchronize": (_INT, [_P]),
+    "xp_template_capture": (_INT, [_P, _I64, _I64, _I64]),
+    "xp_template_capacities": (_INT, [_P, _I64, _I64, ctypes.POINTER(_I64), _INT, ctypes.POINTER(_INT)]),
+    "xp_replay": (_INT, [_P, _INT, _INT, _I64, _P, _P, _I64, _P, _P]),
+}
+
+
+class NativeUnavailableError(RuntimeError):
+    """The HIP library has not been built (run ``__graft_entry__.build()``)."""
+
+
+class NativeError(RuntimeError):
+    """A C-ABI call returned a non-zero status; ``status`` holds it."""
+
+    def __init__(self, status: int, message: str) -> None:
+        super().__init__(message)
+        self.status = status
+
+
+_lock = threading.Lock()
+_library: ctypes.CDLL | None = None
+
+
+def library() -> ctypes.CDLL:
+    """Load (once) and return the native library, raising if it is absent."""
+
+    global _library
+    if _library is not None:
+        return _library
+    with _lock:
+        if _library is None:
+            if not LIBRARY_PATH.exists():
+                raise NativeUnavailableError(
+                    f"{LIBRARY_PATH} is missing; build it with `python -c 'import __graft_entry__ as g; g.build()'`"
+                )
+            lib = ctypes.CDLL(str(LIBRARY_PATH))
+            for name, (restype, argtypes) in SIGNATURES.items():
+                function = getattr(lib, name)
+                function.restype = restype
+                function.argtypes = argtypes
+            _library = lib
+    return _library
+
+
+def last_error() -> str:
+    lib = library()
+    size = lib.xp_last_error(None, 0)
+    buffer = ctypes.create_string_buffer(size + 1)
+    lib.xp_last_error(buffer, size + 1)
+    return buffer.value.decode(errors="replace")
+
+
+def check(status: int, what: str) -> None:
+    """Raise :class:`NativeError` (a RuntimeError) for a failed C-ABI call."""
+
+    if status != XP_OK:
+        raise NativeError(status, f"{what}: {last_error()}")
+
+
+def call(name: str, *args: object) -> int:
+    """Call ``name`` and raise on a non-zero status."""
+
+    status = getattr(library(), name)(*args)
+    check(status, name)
+    return status
+
+
+def gemm_variant(capacity: int, n: int, k: int, gated: bool) -> str:
+    lib = library()
+    buffer = ctypes.create_string_buffer(64)
+    lib.xp_gemm_variant(capacity, n, k, int(gated), buffer, 64)
+    return buffer.value.decode()
+
+
+def dense_workspace_bytes(capacity: int, hidden: int, intermediate: int) -> int:
+    return int(library().xp_dense_workspace_bytes(capacity, hidden, intermediate))

@@ -1,0 +1,312 @@
+"""FfnAgent, Executor Lanes and GraphTemplates on one MI355X.
+
+Mirrors the FfnAgent execution API of the reference:
+``FfnExecutionRegistry`` (src/xpool/runtime/ffnagent/registry.py:348-584),
+``LaneCaptureResources`` (registry.py:25-137) and ``capture_dense_signature``
+(registry.py:189-239), with the native install / replay of
+src/cext/ffnagent/runtime.cu.  A layer signature maps to one GraphTemplate;
+each Lane instantiates one hipGraph per template and replays it with the
+layer's weights bound.  Python retains every tensor the native side borrows
+(weights, workspaces, slot buffers) until the Lane is destroyed.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import logging
+from dataclasses import dataclass
+from time import monotonic
+
+import torch
+
+from crosspool_amd import _native
+from crosspool_amd.execution import DenseFfnExecutionSignature, derive_payload_row_capacities
+from crosspool_amd.ffn import ResultCode
+from crosspool_amd.weights import DenseFfnWeights, validate_weight_tensor
+
+logger = logging.getLogger(__name__)
+
+
+@dataclass(frozen=True, slots=True)
+class GraphTemplate:
+    """One captured graph identity: the Execution Signature (execution.py:73-95)."""
+
+    signature: DenseFfnExecutionSignature
+
+    @property
+    def key(self) -> tuple[int, int, int]:
+        s = self.signature
+        return s.hidden_size, s.local_intermediate_size, s.payload_row_capacity
+
+    @property
+    def workspace_bytes(self) -> int:
+        return self.signature.workspace_layout().nbytes
+
+
+@dataclass(frozen=True, slots=True)
+class LayerBinding:
+    instance_index: int
+    layer_ordinal: int
+    weights: DenseFfnWeights
+    norm_weight: torch.Tensor | None
+    eps: float
+
+
+class FfnHealthError(RuntimeError):
+    """A Lane's sticky device fault word is set (canonical asynchronous failure)."""
+
+    def __init__(self, fault_bits: int) -> None:
+        super().__init__(f"FfnAgent Lane reported fault bits {fault_bits:#x} (slot id outside the mailbox)")
+        self.fault_bits = fault_bits
+        self.result = ResultCode.PROTOCOL_MISMATCH
+
+
+class ExecutorLane:
+    """One concurrent execution context: stream, workspace and instantiated templates."""
+
+    def __init__(self, agent: FfnAgent, workspace_bytes: int) -> None:
+        self.agent = agent
+        self.workspace = torch.empty(max(workspace_bytes, 16), dtype=torch.uint8, device=agent.device)
+        handle = ctypes.c_void_p()
+        _native.call(
+            "xp_lane_create", agent.handle, ctypes.c_void_p(self.workspace.data_ptr()), self.workspace.numel(),
+            ctypes.byref(handle),
+        )
+        self.handle = handle
+        stream = ctypes.c_void_p()
+        _native.call("xp_lane_stream", self.handle, ctypes.byref(stream))
+        self.stream = torch.cuda.ExternalStream(stream.value or 0, device=agent.device)
+        self.templates: dict[tuple[int, int, int], GraphTemplate] = {}
+
+    def capture(self, template: GraphTemplate) -> None:
+        """Instantiate the template's hipGraph on this Lane (idempotent)."""
+
+        self._require_open()
+        hidden, intermediate, capacity = template.key
+        _native.call("xp_template_capture", self.handle, hidden, intermediate, capacity)
+        self.templates[template.key] = template
+
+    def capacities(self, hidden: int, intermediate: int) -> tuple[int, ...]:
+        self._require_open()
+        count = ctypes.c_int()
+        buffer = (ctypes.c_int64 * 64)()
+        _native.call("xp_template_capacities", self.handle, hidden, intermediate, buffer, 64, ctypes.byref(count))
+        return tuple(buffer[index] for index in range(min(count.value, 64)))
+
+    def replay(
+        self,
+        *,
+        instance_index: int,
+        layer_ordinal: int,
+        pool: torch.Tensor,
+        slots: torch.Tensor,
+        rows: int | None = None,
+        out_pool: torch.Tensor | None = None,
+        stream: torch.cuda.Stream | None = None,
+    ) -> None:
+        """Run one mailbox step of a registered layer (stream-ordered, no host sync).
+
+        ``rows`` live slot ids of ``slots`` are gathered from ``pool`` (with the
+        layer's RMSNorm when it has one), run through the Dense FFN and written
+        back to the same slots of ``out_pool`` (default: ``pool``).
+
+        With ``stream=None`` the replay runs on the Lane's stream after the
+        current torch stream's pending work; results are visible to other
+        streams after :meth:`synchronize` or ``wait_stream(lane.stream)``.  The
+        tensors must stay alive until then.  With an explicit ``stream`` the
+        replay is ordered on that stream only; replays of one Lane must not
+        overlap (they share its workspace).
+        """
+
+        self._require_open()
+        out_pool = pool if out_pool is None else out_pool
+        for name, tensor in (("pool", pool), ("out_pool", out_pool)):
+            if tensor.device != self.agent.device or tensor.dtype is not torch.bfloat16 or tensor.ndim != 2:
+                raise ValueError(f"{name} must be a bf16 matrix on the agent's device")
+            if not tensor.is_contiguous():
+                raise ValueError(f"{name} must be contiguous")
+        if out_pool.shape != pool.shape:
+            raise ValueError("input and output mailboxes must have one shape")
+        if slots.device != self.agent.device or slots.dtype is not torch.int32 or slots.ndim != 1:
+            raise ValueError("slots must be a device int32 vector")
+        rows = slots.numel() if rows is None else rows
+        if not 0 < rows <= slots.numel():
+            raise ValueError("row count must be positive and covered by the slot ids")
+        if stream is None:
+            # Lane stream: order after the caller's pending work on the current stream.
+            self.stream.wait_stream(torch.cuda.current_stream(self.agent.device))
+            stream_handle = None
+        else:
+            stream_handle = ctypes.c_void_p(stream.cuda_stream)
+        _native.call(
+            "xp_replay", self.handle, instance_index, layer_ordinal, rows, ctypes.c_void_p(pool.data_ptr()),
+            ctypes.c_void_p(out_pool.data_ptr()), pool.shape[0], ctypes.c_void_p(slots.data_ptr()), stream_handle,
+        )
+
+    def check_health(self) -> int:
+        """Synchronise the Lane and return its sticky fault bits (0 = healthy)."""
+
+        self._require_open()
+        bits = ctypes.c_uint32()
+        _native.call("xp_lane_check_health", self.handle, ctypes.byref(bits))
+        return int(bits.value)
+
+    def clear_fault(self) -> None:
+        self._require_open()
+        _native.call("xp_lane_clear_fault", self.handle)
+
+    def synchronize(self) -> None:
+        self._require_open()
+        _native.call("xp_lane_synchronize", self.handle)
+
+    def close(self) -> None:
+        if self.handle is not None:
+            _native.call("xp_lane_destroy", self.handle)
+            self.handle = None
+            self.templates.clear()
+
+    def _require_open(self) -> None:
+        if self.handle is None:
+            raise RuntimeError("Executor Lane is closed")
+
+
+class FfnAgent:
+    """FFN execution owner on one device: layer weights, GraphTemplates and Lanes.
+
+    ``executor_lane_count`` plays the role of ``scheduler.ffn_concurrency``
+    (src/xpool/config.py:457): independent Lanes may replay concurrently on
+    their own streams.
+    """
+
+    def __init__(self, device: int | torch.device | None = None, *, executor_lane_count: int = 1) -> None:
+        if executor_lane_count <= 0:
+            raise ValueError("an FfnAgent needs at least one Executor Lane")
+        if device is None:
+            device = torch.cuda.current_device()
+        self.device = torch.device("cuda", device if isinstance(device, int) else device.index)
+        handle = ctypes.c_void_p()
+        _native.call("xp_agent_create", self.device.index, ctypes.byref(handle))
+        self.handle = handle
+        self.executor_lane_count = executor_lane_count
+        self.layers: dict[tuple[int, int], LayerBinding] = {}
+        self.templates: dict[tuple[int, int, int], GraphTemplate] = {}
+        self.lanes: list[ExecutorLane] = []
+        self.materialized = False
+
+    # -------------------------------------------------------------- layers
+    def register_layer(
+        self,
+        *,
+        instance_index: int,
+        layer_ordinal: int,
+        weights: DenseFfnWeights,
+        norm_weight: torch.Tensor | None = None,
+        eps: float = 1e-6,
+    ) -> None:
+        """Bind one Dense layer's weights (and optional fused RMSNorm weight)."""
+
+        if weights.device != self.device:
+            raise ValueError("local FFN resources must reside on the agent's device")
+        if norm_weight is not None:
+            validate_weight_tensor(norm_weight, name="RMSNorm weight")
+            if norm_weight.dtype is not torch.bfloat16 or tuple(norm_weight.shape) != (weights.hidden_size,):
+                raise ValueError("RMSNorm weight must be a bf16 [H] vector")
+            if norm_weight.device != self.device:
+                raise ValueError("RMSNorm weight must reside on the agent's device")
+        _native.call(
+            "xp_layer_register", self.handle, instance_index, layer_ordinal, weights.hidden_size,
+            weights.local_intermediate_size, ctypes.c_void_p(weights.i_proj.values.data_ptr()),
+            ctypes.c_void_p(weights.o_proj.values.data_ptr()),
+            None if norm_weight is None else ctypes.c_void_p(norm_weight.data_ptr()), float(eps),
+        )
+        self.layers[(instance_index, layer_ordinal)] = LayerBinding(
+            instance_index, layer_ordinal, weights, norm_weight, float(eps)
+        )
+
+    # -------------------------------------------------------------- bring-up
+    def materialize(self, *, maximum_row_capacity: int) -> tuple[GraphTemplate, ...]:
+        """Create the Lanes and capture every signature of every registered layer.
+
+        Signatures are deduplicated across layers (registry.py:466-474): layers of
+        one shape share templates.  One attempt only (registry.py:400-402).
+        """
+
+        if self.materialized:
+            raise RuntimeError("FFN execution materialization cannot be retried")
+        if not self.layers:
+            raise RuntimeError("register at least one layer before materializing")
+        self.materialized = True
+        started = monotonic()
+        shapes = sorted({(b.weights.hidden_size, b.weights.local_intermediate_size) for b in self.layers.values()})
+        capacities = derive_payload_row_capacities(maximum_row_capacity)
+        for hidden, intermediate in shapes:
+            for capacity in capacities:
+                signature = DenseFfnExecutionSignature(
+                    payload_dtype=torch.bfloat16,
+                    payload_row_capacity=capacity,
+                    hidden_size=hidden,
+                    local_intermediate_size=intermediate,
+                )
+                template = GraphTemplate(signature)
+                self.templates[template.key] = template
+        workspace_bytes = max(t.workspace_bytes for t in self.templates.values())
+        for _ in range(self.executor_lane_count):
+            lane = ExecutorLane(self, workspace_bytes)
+            self.lanes.append(lane)
+            for template in self.templates.values():
+                lane.capture(template)
+        logger.info(
+            "graph templates captured device=%s signature_count=%s lane_count=%s row_capacities=%s elapsed=%.3fs",
+            self.device, len(self.templates), len(self.lanes), list(capacities), monotonic() - started,
+        )
+        return tuple(self.templates.values())
+
+    # -------------------------------------------------------------- execution
+    def execute(
+        self,
+        *,
+        instance_index: int,
+        layer_ordinal: int,
+        pool: torch.Tensor,
+        slots: torch.Tensor,
+        rows: int | None = None,
+        out_pool: torch.Tensor | None = None,
+        lane: int = 0,
+        stream: torch.cuda.Stream | None = None,
+    ) -> None:
+        """Replay one layer on ``lane`` (see :meth:`ExecutorLane.replay`)."""
+
+        if not self.materialized:
+            raise RuntimeError("FfnAgent has not been materialized")
+        if (instance_index, layer_ordinal) not in self.layers:
+            raise KeyError(f"no layer registered for instance {instance_index} ordinal {layer_ordinal}")
+        self.lanes[lane].replay(
+            instance_index=instance_index, layer_ordinal=layer_ordinal, pool=pool, slots=slots, rows=rows,
+            out_pool=out_pool, stream=stream,
+        )
+
+    def check_health(self) -> None:
+        """Raise :class:`FfnHealthError` if any Lane raised a fault (reference ``check_health``)."""
+
+        for lane in self.lanes:
+            bits = lane.check_health()
+            if bits:
+                raise FfnHealthError(bits)
+
+    def close(self) -> None:
+        """Destroy Lanes (after their streams drain), then the agent; weights are released last."""
+
+        while self.lanes:
+            self.lanes[-1].close()
+            self.lanes.pop()
+        if self.handle is not None:
+            _native.call("xp_agent_destroy", self.handle)
+            self.handle = None
+        self.layers.clear()
+        self.templates.clear()
+
+    def __enter__(self) -> FfnAgent:
+        return self
+
+    def __exit__(self, *exc: object) -> None:
+        self.close()

@@ -1,0 +1,691 @@
+// C ABI, FfnAgent layer table, Executor Lanes and GraphTemplates.
+//
+// Reference (CrossPool checkout): the native FfnAgent runtime embeds one
+// captured CUDA graph per Execution Signature as a SWITCH branch inside a
+// resident WHILE graph and patches weight pointers on the device
+// (src/cext/ffnagent/runtime.cu:199-369, 701-1047).  HIP has neither
+// conditional nor device-updatable graph nodes, so here a Lane owns one
+// instantiated hipGraphExec per signature, built from explicit kernel nodes;
+// the host selects the layer and the smallest capacity that holds the live rows
+// (the rule of runtime.cu:246-253) and rebinds the three kernel nodes' argument
+// records with hipGraphExecKernelNodeSetParams before hipGraphLaunch.
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/xpool_amd.h"
+#include "xp_kernels.hpp"
+
+namespace xp {
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string &message) {
+  g_last_error = message;
+  return code;
+}
+
+#define XP_HIP_CHECK(expr)                                                                   \
+  do {                                                                                       \
+    const hipError_t xp_error_ = (expr);                                                     \
+    if (xp_error_ != hipSuccess) {                                                           \
+      return fail(XP_ERROR_HIP, std::string(#expr) + " failed: " + hipGetErrorString(xp_error_)); \
+    }                                                                                        \
+  } while (0)
+
+#define XP_REQUIRE(condition, message)                  \
+  do {                                                  \
+    if (!(condition)) {                                 \
+      return fail(XP_ERROR_INVALID_ARGUMENT, message);  \
+    }                                                   \
+  } while (0)
+
+bool aligned16(const void *pointer) { return (reinterpret_cast<uintptr_t>(pointer) & 15u) == 0; }
+
+// Region alignment of the Lane workspace, the reference's OPERATOR_ALIGNMENT_BYTES
+// (src/xpool/runtime/ffnagent/execution.py:16).
+constexpr size_t kRegionAlignment = 16;
+
+size_t align_up(size_t value, size_t alignment) { return (value + alignment - 1) / alignment * alignment; }
+
+// Workspace regions of one Dense step at `capacity`: gathered batch [capacity, hidden],
+// then the activated intermediate [capacity, intermediate], each 16-byte aligned.
+struct DenseWorkspace {
+  size_t batch_offset;
+  size_t activated_offset;
+  size_t bytes;
+};
+
+DenseWorkspace dense_workspace(int64_t capacity, int64_t hidden, int64_t intermediate) {
+  DenseWorkspace layout{};
+  layout.batch_offset = 0;
+  layout.activated_offset = align_up(static_cast<size_t>(capacity * hidden) * 2, kRegionAlignment);
+  layout.bytes = layout.activated_offset + static_cast<size_t>(capacity * intermediate) * 2;
+  return layout;
+}
+
+int validate_geometry(int64_t hidden, int64_t intermediate) {
+  XP_REQUIRE(hidden > 0 && hidden % 8 == 0, "hidden size must be a positive multiple of 8");
+  XP_REQUIRE(intermediate > 0 && intermediate % 8 == 0, "intermediate size must be a positive multiple of 8");
+  XP_REQUIRE(gather_supported(hidden), "hidden size exceeds the gather kernel's register row (16384)");
+  return XP_OK;
+}
+
+GatedSilu default_activation() { return GatedSilu{1.0f, 0.0f, 0.0f}; }
+
+// The three kernels of one mailbox step, for a given capacity.
+struct DenseLaunches {
+  KernelLaunch gather;
+  KernelLaunch gate_up;
+  KernelLaunch down;
+};
+
+struct DenseBinding {
+  const uint16_t *pool_in;
+  uint16_t *pool_out;
+  int64_t pool_rows;
+  const int32_t *slots;
+  int64_t rows;
+  int64_t hidden;
+  int64_t intermediate;
+  const uint16_t *gate_up;
+  const uint16_t *down;
+  const uint16_t *norm;
+  float eps;
+  uint8_t *workspace;
+  uint32_t *fault;
+};
+
+DenseLaunches make_dense_launches(const DenseBinding &b, int64_t capacity) {
+  const DenseWorkspace layout = dense_workspace(capacity, b.hidden, b.intermediate);
+  uint16_t *batch = reinterpret_cast<uint16_t *>(b.workspace + layout.batch_offset);
+  uint16_t *activated = reinterpret_cast<uint16_t *>(b.workspace + layout.activated_offset);
+  DenseLaunches launches;
+
+  GatherArgs gather{};
+  gather.pool = b.pool_in;
+  gather.slots = b.slots;
+  gather.norm = b.norm;
+  gather.out = batch;
+  gather.fault = b.fault;
+  gather.pool_rows = b.pool_rows;
+  gather.hidden = b.hidden;
+  gather.rows = b.rows;
+  gather.eps = b.eps;
+  launches.gather = make_gather(gather, capacity);
+
+  GemmArgs gate_up{};
+  gate_up.x = batch;
+  gate_up.w = b.gate_up;
+  gate_up.out = activated;
+  gate_up.scatter_slots = nullptr;
+  gate_up.ldx = b.hidden;
+  gate_up.ldo = b.intermediate;
+  gate_up.rows = b.rows;
+  gate_up.out_rows = capacity;
+  gate_up.n = 2 * b.intermediate;
+  gate_up.k = b.hidden;
+  gate_up.act = default_activation();
+  launches.gate_up = make_gemm(gate_up, capacity, true, choose_gemm(capacity, gate_up.n, gate_up.k, true));
+
+  GemmArgs down{};
+  down.x = activated;
+  down.w = b.down;
+  down.out = b.pool_out;
+  down.scatter_slots = b.slots;
+  down.ldx = b.intermediate;
+  down.ldo = b.hidden;
+  down.rows = b.rows;
+  down.out_rows = b.pool_rows;
+  down.n = b.hidden;
+  down.k = b.intermediate;
+  down.act = default_activation();
+  launches.down = make_gemm(down, capacity, false, choose_gemm(capacity, down.n, down.k, false));
+  return launches;
+}
+
+hipKernelNodeParams node_params(const KernelLaunch &kernel, void **params) {
+  hipKernelNodeParams node{};
+  node.func = const_cast<void *>(kernel.func);
+  node.gridDim = kernel.grid;
+  node.blockDim = kernel.block;
+  node.sharedMemBytes = kernel.shmem;
+  params[0] = const_cast<unsigned char *>(kernel.args);
+  node.kernelParams = params;
+  node.extra = nullptr;
+  return node;
+}
+
+}  // namespace
+}  // namespace xp
+
+using namespace xp;
+
+struct Layer {
+  int instance_index;
+  int layer_ordinal;
+  int64_t hidden;
+  int64_t intermediate;
+  const uint16_t *gate_up;
+  const uint16_t *down;
+  const uint16_t *norm;
+  float eps;
+};
+
+struct xp_agent {
+  int device = 0;
+  std::mutex mutex;
+  std::vector<Layer> layers;
+  int live_lanes = 0;
+};
+
+struct Template {
+  int64_t hidden = 0;
+  int64_t intermediate = 0;
+  int64_t capacity = 0;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  hipGraphNode_t nodes[3] = {nullptr, nullptr, nullptr};
+};
+
+struct xp_lane {
+  xp_agent *agent = nullptr;
+  hipStream_t stream = nullptr;
+  uint8_t *workspace = nullptr;
+  size_t workspace_bytes = 0;
+  uint32_t *fault = nullptr;
+  std::mutex mutex;
+  std::vector<std::unique_ptr<Template>> templates;  // sorted by (hidden, intermediate, capacity)
+};
+
+namespace {
+
+void destroy_template(Template &t) {
+  if (t.exec != nullptr) {
+    (void)hipGraphExecDestroy(t.exec);
+    t.exec = nullptr;
+  }
+  if (t.graph != nullptr) {
+    (void)hipGraphDestroy(t.graph);
+    t.graph = nullptr;
+  }
+}
+
+const Layer *find_layer(const xp_agent *agent, int instance_index, int layer_ordinal) {
+  for (const Layer &layer : agent->layers) {
+    if (layer.instance_index == instance_index && layer.layer_ordinal == layer_ordinal) {
+      return &layer;
+    }
+  }
+  return nullptr;
+}
+
+}  // namespace
+
+extern "C" {
+
+int xp_abi_version(void) { return XP_ABI_VERSION; }
+
+size_t xp_last_error(char *buffer, size_t size) {
+  const std::string &message = g_last_error;
+  if (buffer != nullptr && size > 0) {
+    const size_t count = std::min(size - 1, message.size());
+    std::memcpy(buffer, message.data(), count);
+    buffer[count] = '\0';
+  }
+  return message.size();
+}
+
+// ------------------------------------------------------------------ kernels
+
+int xp_copy_bytes(void *dst, const void *src, size_t bytes, xp_stream_t stream) {
+  if (bytes == 0) {
+    return XP_OK;
+  }
+  XP_REQUIRE(dst != nullptr && src != nullptr, "copy pointers must be non-null for a non-empty range");
+  const uint8_t *s = static_cast<const uint8_t *>(src);
+  uint8_t *d = static_cast<uint8_t *>(dst);
+  XP_REQUIRE(d + bytes <= s || s + bytes <= d, "copy ranges must not overlap");
+  CopyArgs args{d, s, bytes};
+  XP_HIP_CHECK(launch(make_copy(args), static_cast<hipStream_t>(stream)));
+  return XP_OK;
+}
+
+int xp_gather_rmsnorm(const void *pool, int64_t pool_rows, int64_t hidden, const int32_t *slots, int64_t rows,
+                      const void *norm_weight, float eps, void *out, uint32_t *fault_word, xp_stream_t stream) {
+  XP_REQUIRE(rows >= 0 && pool_rows >= 0, "row counts must be non-negative");
+  if (rows == 0) {
+    return XP_OK;
+  }
+  XP_REQUIRE(hidden > 0 && hidden % 8 == 0 && gather_supported(hidden),
+             "hidden size must be a positive multiple of 8 and at most 16384");
+  XP_REQUIRE(pool != nullptr && slots != nullptr && out != nullptr, "gather pointers must be non-null");
+  XP_REQUIRE(aligned16(pool) && aligned16(out) && (norm_weight == nullptr || aligned16(norm_weight)),
+             "gather rows must be 16-byte aligned");
+  XP_REQUIRE(norm_weight == nullptr || eps >= 0.0f, "RMSNorm epsilon must be non-negative");
+  GatherArgs args{};
+  args.pool = static_cast<const uint16_t *>(pool);
+  args.slots = slots;
+  args.norm = static_cast<const uint16_t *>(norm_weight);
+  args.out = static_cast<uint16_t *>(out);
+  args.fault = fault_word;
+  args.pool_rows = pool_rows;
+  args.hidden = hidden;
+  args.rows = rows;
+  args.eps = eps;
+  XP_HIP_CHECK(launch(make_gather(args, rows), static_cast<hipStream_t>(stream)));
+  return XP_OK;
+}
+
+int xp_scatter(const void *values, int64_t rows, int64_t hidden, const int32_t *slots, void *pool,
+               int64_t pool_rows, uint32_t *fault_word, xp_stream_t stream) {
+  XP_REQUIRE(rows >= 0 && pool_rows >= 0, "row counts must be non-negative");
+  if (rows == 0) {
+    return XP_OK;
+  }
+  XP_REQUIRE(hidden > 0 && hidden % 8 == 0, "hidden size must be a positive multiple of 8");
+  XP_REQUIRE(values != nullptr && slots != nullptr && pool != nullptr, "scatter pointers must be non-null");
+  XP_REQUIRE(aligned16(values) && aligned16(pool), "scatter rows must be 16-byte aligned");
+  ScatterArgs args{};
+  args.values = static_cast<const uint16_t *>(values);
+  args.slots = slots;
+  args.pool = static_cast<uint16_t *>(pool);
+  args.fault = fault_word;
+  args.pool_rows = pool_rows;
+  args.hidden = hidden;
+  args.rows = rows;
+  XP_HIP_CHECK(launch(make_scatter(args, rows), static_cast<hipStream_t>(stream)));
+  return XP_OK;
+}
+
+int xp_gemm_gate_up_silu(const void *x, int64_t rows, int64_t hidden, const void *w_gate_up, int64_t intermediate,
+                         void *activated, float alpha, float limit, float up_offset, xp_stream_t stream) {
+  XP_REQUIRE(rows >= 0, "row count must be non-negative");
+  if (rows == 0) {
+    return XP_OK;
+  }
+  if (const int status = validate_geometry(hidden, intermediate); status != XP_OK) {
+    return status;
+  }
+  XP_REQUIRE(x != nullptr && w_gate_up != nullptr && activated != nullptr, "projection pointers must be non-null");
+  XP_REQUIRE(aligned16(x) && aligned16(w_gate_up) && aligned16(activated), "projection operands must be 16-byte aligned");
+  XP_REQUIRE(alpha > 0.0f, "SiLU alpha must be positive");
+  GemmArgs args{};
+  args.x = static_cast<const uint16_t *>(x);
+  args.w = static_cast<const uint16_t *>(w_gate_up);
+  args.out = static_cast<uint16_t *>(activated);
+  args.ldx = hidden;
+  args.ldo = intermediate;
+  args.rows = rows;
+  args.out_rows = rows;
+  args.n = 2 * intermediate;
+  args.k = hidden;
+  args.act = GatedSilu{alpha, limit, up_offset};
+  const GemmChoice choice = choose_gemm(rows, args.n, args.k, true);
+  XP_HIP_CHECK(launch(make_gemm(args, rows, true, choice), static_cast<hipStream_t>(stream)));
+  return XP_OK;
+}
+
+int xp_gemm_down(const void *activated, int64_t rows, int64_t intermediate, const void *w_down, int64_t hidden,
+                 void *out, const int32_t *slots, int64_t out_rows, xp_stream_t stream) {
+  XP_REQUIRE(rows >= 0, "row count must be non-negative");
+  if (rows == 0) {
+    return XP_OK;
+  }
+  if (const int status = validate_geometry(hidden, intermediate); status != XP_OK) {
+    return status;
+  }
+  XP_REQUIRE(activated != nullptr && w_down != nullptr && out != nullptr, "projection pointers must be non-null");
+  XP_REQUIRE(aligned16(activated) && aligned16(w_down) && aligned16(out), "projection operands must be 16-byte aligned");
+  XP_REQUIRE(slots == nullptr || out_rows >= 0, "scatter output rows must be non-negative");
+  GemmArgs args{};
+  args.x = static_cast<const uint16_t *>(activated);
+  args.w = static_cast<const uint16_t *>(w_down);
+  args.out = static_cast<uint16_t *>(out);
+  args.scatter_slots = slots;
+  args.ldx = intermediate;
+  args.ldo = hidden;
+  args.rows = rows;
+  args.out_rows = slots != nullptr ? out_rows : rows;
+  args.n = hidden;
+  args.k = intermediate;
+  args.act = default_activation();
+  const GemmChoice choice = choose_gemm(rows, args.n, args.k, false);
+  XP_HIP_CHECK(launch(make_gemm(args, rows, false, choice), static_cast<hipStream_t>(stream)));
+  return XP_OK;
+}
+
+size_t xp_dense_workspace_bytes(int64_t capacity, int64_t hidden, int64_t intermediate) {
+  if (capacity <= 0 || hidden <= 0 || intermediate <= 0) {
+    return 0;
+  }
+  return dense_workspace(capacity, hidden, intermediate).bytes;
+}
+
+int xp_dense_step(const void *pool_in, void *pool_out, int64_t pool_rows, const int32_t *slots, int64_t rows,
+                  int64_t hidden, int64_t intermediate, const void *w_gate_up, const void *w_down,
+                  const void *norm_weight, float eps, void *workspace, size_t workspace_bytes, uint32_t *fault_word,
+                  xp_stream_t stream) {
+  XP_REQUIRE(rows >= 0 && pool_rows >= 0, "row counts must be non-negative");
+  if (rows == 0) {
+    return XP_OK;
+  }
+  if (const int status = validate_geometry(hidden, intermediate); status != XP_OK) {
+    return status;
+  }
+  XP_REQUIRE(pool_in != nullptr && pool_out != nullptr && slots != nullptr && w_gate_up != nullptr &&
+                 w_down != nullptr && workspace != nullptr,
+             "dense step pointers must be non-null");
+  XP_REQUIRE(aligned16(pool_in) && aligned16(pool_out) && aligned16(w_gate_up) && aligned16(w_down) &&
+                 aligned16(workspace) && (norm_weight == nullptr || aligned16(norm_weight)),
+             "dense step operands must be 16-byte aligned");
+  XP_REQUIRE(workspace_bytes >= dense_workspace(rows, hidden, intermediate).bytes,
+             "workspace is smaller than xp_dense_workspace_bytes(rows, hidden, intermediate)");
+  DenseBinding binding{};
+  binding.pool_in = static_cast<const uint16_t *>(pool_in);
+  binding.pool_out = static_cast<uint16_t *>(pool_out);
+  binding.pool_rows = pool_rows;
+  binding.slots = slots;
+  binding.rows = rows;
+  binding.hidden = hidden;
+  binding.intermediate = intermediate;
+  binding.gate_up = static_cast<const uint16_t *>(w_gate_up);
+  binding.down = static_cast<const uint16_t *>(w_down);
+  binding.norm = static_cast<const uint16_t *>(norm_weight);
+  binding.eps = eps;
+  binding.workspace = static_cast<uint8_t *>(workspace);
+  binding.fault = fault_word;
+  const DenseLaunches launches = make_dense_launches(binding, rows);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  XP_HIP_CHECK(launch(launches.gather, s));
+  XP_HIP_CHECK(launch(launches.gate_up, s));
+  XP_HIP_CHECK(launch(launches.down, s));
+  return XP_OK;
+}
+
+size_t xp_gemm_variant(int64_t capacity, int64_t n, int64_t k, int gated, char *buffer, size_t size) {
+  const std::string name = capacity > 0 ? gemm_name(choose_gemm(capacity, n, k, gated != 0), gated != 0) : "";
+  if (buffer != nullptr && size > 0) {
+    const size_t count = std::min(size - 1, name.size());
+    std::memcpy(buffer, name.data(), count);
+    buffer[count] = '\0';
+  }
+  return name.size();
+}
+
+// ------------------------------------------------------------------ runtime
+
+int xp_agent_create(int device, xp_agent_t *out) {
+  XP_REQUIRE(out != nullptr, "agent output pointer must be non-null");
+  int count = 0;
+  XP_HIP_CHECK(hipGetDeviceCount(&count));
+  XP_REQUIRE(device >= 0 && device < count, "device ordinal is out of range");
+  auto agent = std::make_unique<xp_agent>();
+  agent->device = device;
+  *out = agent.release();
+  return XP_OK;
+}
+
+int xp_agent_destroy(xp_agent_t agent) {
+  if (agent == nullptr) {
+    return XP_OK;
+  }
+  {
+    std::lock_guard<std::mutex> guard(agent->mutex);
+    if (agent->live_lanes != 0) {
+      return fail(XP_ERROR_STATE, "destroy every Lane before its agent");
+    }
+  }
+  delete agent;
+  return XP_OK;
+}
+
+int xp_layer_register(xp_agent_t agent, int instance_index, int layer_ordinal, int64_t hidden, int64_t intermediate,
+                      const void *gate_up, const void *down, const void *norm_weight, float eps) {
+  XP_REQUIRE(agent != nullptr, "agent must be non-null");
+  XP_REQUIRE(instance_index >= 0 && layer_ordinal >= 0, "instance index and layer ordinal must be non-negative");
+  if (const int status = validate_geometry(hidden, intermediate); status != XP_OK) {
+    return status;
+  }
+  XP_REQUIRE(gate_up != nullptr && down != nullptr, "layer weights must be non-null");
+  XP_REQUIRE(aligned16(gate_up) && aligned16(down) && (norm_weight == nullptr || aligned16(norm_weight)),
+             "layer weights must be 16-byte aligned");
+  XP_REQUIRE(norm_weight == nullptr || eps >= 0.0f, "RMSNorm epsilon must be non-negative");
+  std::lock_guard<std::mutex> guard(agent->mutex);
+  Layer layer{instance_index,
+              layer_ordinal,
+              hidden,
+              intermediate,
+              static_cast<const uint16_t *>(gate_up),
+              static_cast<const uint16_t *>(down),
+              static_cast<const uint16_t *>(norm_weight),
+              eps};
+  for (Layer &existing : agent->layers) {
+    if (existing.instance_index == instance_index && existing.layer_ordinal == layer_ordinal) {
+      existing = layer;
+      return XP_OK;
+    }
+  }
+  agent->layers.push_back(layer);
+  return XP_OK;
+}
+
+int xp_lane_create(xp_agent_t agent, void *workspace, size_t workspace_bytes, xp_lane_t *out) {
+  XP_REQUIRE(agent != nullptr && out != nullptr, "agent and output pointer must be non-null");
+  XP_REQUIRE(workspace != nullptr || workspace_bytes == 0, "workspace must be non-null when sized");
+  XP_REQUIRE(aligned16(workspace), "workspace must be 16-byte aligned");
+  XP_HIP_CHECK(hipSetDevice(agent->device));
+  auto lane = std::make_unique<xp_lane>();
+  lane->agent = agent;
+  lane->workspace = static_cast<uint8_t *>(workspace);
+  lane->workspace_bytes = workspace_bytes;
+  XP_HIP_CHECK(hipStreamCreateWithFlags(&lane->stream, hipStreamNonBlocking));
+  void *fault = nullptr;
+  const hipError_t allocated = hipMalloc(&fault, sizeof(uint32_t));
+  if (allocated != hipSuccess) {
+    (void)hipStreamDestroy(lane->stream);
+    return fail(XP_ERROR_HIP, std::string("hipMalloc of the Lane fault word failed: ") + hipGetErrorString(allocated));
+  }
+  lane->fault = static_cast<uint32_t *>(fault);
+  const hipError_t cleared = hipMemset(lane->fault, 0, sizeof(uint32_t));
+  if (cleared != hipSuccess) {
+    (void)hipFree(lane->fault);
+    (void)hipStreamDestroy(lane->stream);
+    return fail(XP_ERROR_HIP, std::string("clearing the Lane fault word failed: ") + hipGetErrorString(cleared));
+  }
+  {
+    std::lock_guard<std::mutex> guard(agent->mutex);
+    agent->live_lanes += 1;
+  }
+  *out = lane.release();
+  return XP_OK;
+}
+
+int xp_lane_destroy(xp_lane_t lane) {
+  if (lane == nullptr) {
+    return XP_OK;
+  }
+  XP_HIP_CHECK(hipSetDevice(lane->agent->device));
+  XP_HIP_CHECK(hipStreamSynchronize(lane->stream));
+  for (auto &t : lane->templates) {
+    destroy_template(*t);
+  }
+  lane->templates.clear();
+  (void)hipFree(lane->fault);
+  (void)hipStreamDestroy(lane->stream);
+  {
+    std::lock_guard<std::mutex> guard(lane->agent->mutex);
+    lane->agent->live_lanes -= 1;
+  }
+  delete lane;
+  return XP_OK;
+}
+
+int xp_lane_stream(xp_lane_t lane, xp_stream_t *out) {
+  XP_REQUIRE(lane != nullptr && out != nullptr, "lane and output pointer must be non-null");
+  *out = lane->stream;
+  return XP_OK;
+}
+
+int xp_lane_synchronize(xp_lane_t lane) {
+  XP_REQUIRE(lane != nullptr, "lane must be non-null");
+  XP_HIP_CHECK(hipSetDevice(lane->agent->device));
+  XP_HIP_CHECK(hipStreamSynchronize(lane->stream));
+  return XP_OK;
+}
+
+int xp_lane_check_health(xp_lane_t lane, uint32_t *fault_bits) {
+  XP_REQUIRE(lane != nullptr && fault_bits != nullptr, "lane and output pointer must be non-null");
+  XP_HIP_CHECK(hipSetDevice(lane->agent->device));
+  XP_HIP_CHECK(hipStreamSynchronize(lane->stream));
+  uint32_t value = 0;
+  XP_HIP_CHECK(hipMemcpy(&value, lane->fault, sizeof value, hipMemcpyDeviceToHost));
+  *fault_bits = value;
+  return XP_OK;
+}
+
+int xp_lane_clear_fault(xp_lane_t lane) {
+  XP_REQUIRE(lane != nullptr, "lane must be non-null");
+  XP_HIP_CHECK(hipSetDevice(lane->agent->device));
+  XP_HIP_CHECK(hipStreamSynchronize(lane->stream));
+  XP_HIP_CHECK(hipMemset(lane->fault, 0, sizeof(uint32_t)));
+  return XP_OK;
+}
+
+int xp_template_capture(xp_lane_t lane, int64_t hidden, int64_t intermediate, int64_t capacity) {
+  XP_REQUIRE(lane != nullptr, "lane must be non-null");
+  if (const int status = validate_geometry(hidden, intermediate); status != XP_OK) {
+    return status;
+  }
+  XP_REQUIRE(capacity > 0, "template capacity must be positive");
+  const size_t needed = dense_workspace(capacity, hidden, intermediate).bytes;
+  if (needed > lane->workspace_bytes) {
+    return fail(XP_ERROR_CAPACITY, "Lane workspace is smaller than the template needs (" + std::to_string(needed) +
+                                       " bytes)");
+  }
+  std::lock_guard<std::mutex> guard(lane->mutex);
+  for (const auto &t : lane->templates) {
+    if (t->hidden == hidden && t->intermediate == intermediate && t->capacity == capacity) {
+      return XP_OK;
+    }
+  }
+  XP_HIP_CHECK(hipSetDevice(lane->agent->device));
+  // Placeholder binding: a replay rebinds every argument record before launching.
+  DenseBinding binding{};
+  binding.hidden = hidden;
+  binding.intermediate = intermediate;
+  binding.rows = 0;
+  binding.workspace = lane->workspace;
+  binding.fault = lane->fault;
+  const DenseLaunches launches = make_dense_launches(binding, capacity);
+
+  auto t = std::make_unique<Template>();
+  t->hidden = hidden;
+  t->intermediate = intermediate;
+  t->capacity = capacity;
+  XP_HIP_CHECK(hipGraphCreate(&t->graph, 0));
+  const KernelLaunch *chain[3] = {&launches.gather, &launches.gate_up, &launches.down};
+  for (int index = 0; index < 3; ++index) {
+    void *params[1];
+    hipKernelNodeParams node = node_params(*chain[index], params);
+    const hipGraphNode_t *dependencies = index == 0 ? nullptr : &t->nodes[index - 1];
+    const hipError_t added = hipGraphAddKernelNode(&t->nodes[index], t->graph, dependencies, index == 0 ? 0 : 1, &node);
+    if (added != hipSuccess) {
+      destroy_template(*t);
+      return fail(XP_ERROR_HIP, std::string("hipGraphAddKernelNode failed: ") + hipGetErrorString(added));
+    }
+  }
+  const hipError_t instantiated = hipGraphInstantiate(&t->exec, t->graph, nullptr, nullptr, 0);
+  if (instantiated != hipSuccess) {
+    destroy_template(*t);
+    return fail(XP_ERROR_HIP, std::string("hipGraphInstantiate failed: ") + hipGetErrorString(instantiated));
+  }
+  lane->templates.push_back(std::move(t));
+  std::sort(lane->templates.begin(), lane->templates.end(), [](const auto &left, const auto &right) {
+    if (left->hidden != right->hidden) return left->hidden < right->hidden;
+    if (left->intermediate != right->intermediate) return left->intermediate < right->intermediate;
+    return left->capacity < right->capacity;
+  });
+  return XP_OK;
+}
+
+int xp_template_capacities(xp_lane_t lane, int64_t hidden, int64_t intermediate, int64_t *capacities,
+                           int max_count, int *count) {
+  XP_REQUIRE(lane != nullptr && count != nullptr, "lane and count pointer must be non-null");
+  std::lock_guard<std::mutex> guard(lane->mutex);
+  int found = 0;
+  for (const auto &t : lane->templates) {
+    if (t->hidden == hidden && t->intermediate == intermediate) {
+      if (capacities != nullptr && found < max_count) {
+        capacities[found] = t->capacity;
+      }
+      ++found;
+    }
+  }
+  *count = found;
+  return XP_OK;
+}
+
+int xp_replay(xp_lane_t lane, int instance_index, int layer_ordinal, int64_t rows, const void *pool_in,
+              void *pool_out, int64_t pool_rows, const int32_t *slots, xp_stream_t stream) {
+  XP_REQUIRE(lane != nullptr, "lane must be non-null");
+  XP_REQUIRE(pool_in != nullptr && pool_out != nullptr && slots != nullptr, "replay pointers must be non-null");
+  XP_REQUIRE(aligned16(pool_in) && aligned16(pool_out), "mailbox rows must be 16-byte aligned");
+  XP_REQUIRE(pool_rows > 0, "mailbox must have rows");
+  Layer layer{};
+  {
+    std::lock_guard<std::mutex> guard(lane->agent->mutex);
+    const Layer *found = find_layer(lane->agent, instance_index, layer_ordinal);
+    if (found == nullptr) {
+      return fail(XP_ERROR_NOT_FOUND, "no layer is registered for (instance " + std::to_string(instance_index) +
+                                          ", ordinal " + std::to_string(layer_ordinal) + ")");
+    }
+    layer = *found;
+  }
+  std::lock_guard<std::mutex> guard(lane->mutex);
+  Template *selected = nullptr;
+  int64_t largest = 0;
+  for (const auto &t : lane->templates) {
+    if (t->hidden == layer.hidden && t->intermediate == layer.intermediate) {
+      largest = std::max(largest, t->capacity);
+      if (selected == nullptr && rows <= t->capacity) {
+        selected = t.get();
+      }
+    }
+  }
+  if (rows < 1 || selected == nullptr) {
+    return fail(XP_ERROR_CAPACITY, "row count " + std::to_string(rows) + " is outside the installed capacities [1, " +
+                                       std::to_string(largest) + "]");
+  }
+  DenseBinding binding{};
+  binding.pool_in = static_cast<const uint16_t *>(pool_in);
+  binding.pool_out = static_cast<uint16_t *>(pool_out);
+  binding.pool_rows = pool_rows;
+  binding.slots = slots;
+  binding.rows = rows;
+  binding.hidden = layer.hidden;
+  binding.intermediate = layer.intermediate;
+  binding.gate_up = layer.gate_up;
+  binding.down = layer.down;
+  binding.norm = layer.norm;
+  binding.eps = layer.eps;
+  binding.workspace = lane->workspace;
+  binding.fault = lane->fault;
+  const DenseLaunches launches = make_dense_launches(binding, selected->capacity);
+  const KernelLaunch *chain[3] = {&launches.gather, &launches.gate_up, &launches.down};
+  for (int index = 0; index < 3; ++index) {
+    void *params[1];
+    hipKernelNodeParams node = node_params(*chain[index], params);
+    XP_HIP_CHECK(hipGraphExecKernelNodeSetParams(selected->exec, selected->nodes[index], &node));
+  }
+  XP_HIP_CHECK(hipGraphLaunch(selected->exec, stream != nullptr ? static_cast<hipStream_t>(stream) : lane->stream));
+  return XP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,182 @@
+// Transport kernels: byte copy, mailbox gather (+ fused RMSNorm) and scatter.
+//
+// Reference behaviour (CrossPool checkout):
+//   * row copies of the Transport/Fabric payload, src/cext/transport/instance.cu:83-84,184-186
+//     and src/cext/fabric/atnagent.cu:215,275, all through xpool::utils::cooperative::copy
+//     (src/cext-include/xpool/utils/cooperative.cuh:37-55);
+//   * the reference copies one contiguous row prefix with one 256-thread CTA; here a row is
+//     gathered from an arbitrary mailbox slot by one 64-lane wavefront with 16-byte loads, no
+//     LDS, and the whole grid participates.
+// RMSNorm has no counterpart on the reference path (SGLang applies it before the shim); it is
+// fused here so the GEMM reads normalised rows straight from the gathered batch.
+
+#include "xp_kernels.hpp"
+
+namespace xp {
+namespace {
+
+__global__ __launch_bounds__(256) void copy_bytes_kernel(CopyArgs a) {
+  const uint64_t thread = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+  const bool aligned =
+      ((reinterpret_cast<uintptr_t>(a.destination) | reinterpret_cast<uintptr_t>(a.source) | a.bytes) & 15u) == 0;
+  if (aligned) {
+    const uint64_t vectors = a.bytes >> 4;
+    for (uint64_t index = thread; index < vectors; index += stride) {
+      store16(a.destination + (index << 4), load16(a.source + (index << 4)));
+    }
+  } else {
+    for (uint64_t index = thread; index < a.bytes; index += stride) {
+      a.destination[index] = a.source[index];
+    }
+  }
+}
+
+// One wavefront per row; CHUNKS 16-byte chunks per lane stay in registers between the
+// sum-of-squares reduction and the normalised store (hidden <= CHUNKS * 512).
+template <int CHUNKS>
+__global__ __launch_bounds__(256) void gather_rows_kernel(GatherArgs a) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= a.rows) {
+    return;
+  }
+  const int64_t chunks = a.hidden >> 3;
+  uint16_t *destination = a.out + row * a.hidden;
+  const int32_t slot = a.slots[row];
+  if (slot < 0 || static_cast<int64_t>(slot) >= a.pool_rows) {
+    // Canonical failure: poison the row with quiet NaNs and raise the sticky fault bit.
+    const u32x4 poison = {0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u};
+    for (int64_t chunk = lane; chunk < chunks; chunk += kWave) {
+      store16(destination + chunk * 8, poison);
+    }
+    if (lane == 0) {
+      raise_fault(a.fault, kFaultSlotOutOfRange);
+    }
+    return;
+  }
+  const uint16_t *source = a.pool + static_cast<int64_t>(slot) * a.hidden;
+  u32x4 values[CHUNKS];
+#pragma unroll
+  for (int index = 0; index < CHUNKS; ++index) {
+    const int64_t chunk = lane + index * kWave;
+    values[index] = chunk < chunks ? load16(source + chunk * 8) : u32x4{0u, 0u, 0u, 0u};
+  }
+  if (a.norm == nullptr) {
+#pragma unroll
+    for (int index = 0; index < CHUNKS; ++index) {
+      const int64_t chunk = lane + index * kWave;
+      if (chunk < chunks) {
+        store16(destination + chunk * 8, values[index]);
+      }
+    }
+    return;
+  }
+  float squares = 0.0f;
+#pragma unroll
+  for (int index = 0; index < CHUNKS; ++index) {
+#pragma unroll
+    for (int word = 0; word < 4; ++word) {
+      const float lo = bf16_to_float(values[index][word] & 0xffffu);
+      const float hi = bf16_to_float(values[index][word] >> 16);
+      squares += lo * lo;
+      squares += hi * hi;
+    }
+  }
+  squares = wave_sum(squares);
+  const float inverse = 1.0f / sqrtf(squares / static_cast<float>(a.hidden) + a.eps);
+#pragma unroll
+  for (int index = 0; index < CHUNKS; ++index) {
+    const int64_t chunk = lane + index * kWave;
+    if (chunk < chunks) {
+      const u32x4 weight = load16(a.norm + chunk * 8);
+      u32x4 result;
+#pragma unroll
+      for (int word = 0; word < 4; ++word) {
+        const float lo = bf16_to_float(values[index][word] & 0xffffu) * inverse;
+        const float hi = bf16_to_float(values[index][word] >> 16) * inverse;
+        result[word] = pack_bf16x2(lo * bf16_to_float(weight[word] & 0xffffu), hi * bf16_to_float(weight[word] >> 16));
+      }
+      store16(destination + chunk * 8, result);
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void scatter_rows_kernel(ScatterArgs a) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= a.rows) {
+    return;
+  }
+  const int32_t slot = a.slots[row];
+  if (slot < 0 || static_cast<int64_t>(slot) >= a.pool_rows) {
+    if (lane == 0) {
+      raise_fault(a.fault, kFaultSlotOutOfRange);
+    }
+    return;
+  }
+  const int64_t chunks = a.hidden >> 3;
+  const uint16_t *source = a.values + row * a.hidden;
+  uint16_t *destination = a.pool + static_cast<int64_t>(slot) * a.hidden;
+  for (int64_t chunk = lane; chunk < chunks; chunk += kWave) {
+    store16(destination + chunk * 8, load16(source + chunk * 8));
+  }
+}
+
+constexpr int64_t kMaxGatherChunks = 32;
+
+template <int CHUNKS>
+const void *gather_kernel_for() {
+  return reinterpret_cast<const void *>(&gather_rows_kernel<CHUNKS>);
+}
+
+}  // namespace
+
+KernelLaunch make_copy(const CopyArgs &args) {
+  KernelLaunch kernel;
+  kernel.func = reinterpret_cast<const void *>(&copy_bytes_kernel);
+  const uint64_t units = (args.bytes + 15) / 16;
+  uint64_t blocks = (units + 255) / 256;
+  if (blocks > 2048) {
+    blocks = 2048;
+  }
+  kernel.grid = dim3(static_cast<unsigned>(blocks), 1, 1);
+  kernel.block = dim3(256, 1, 1);
+  kernel.set_args(args);
+  return kernel;
+}
+
+bool gather_supported(int64_t hidden) { return hidden > 0 && hidden % 8 == 0 && hidden <= kMaxGatherChunks * 512; }
+
+KernelLaunch make_gather(const GatherArgs &args, int64_t capacity) {
+  KernelLaunch kernel;
+  const int64_t chunks_per_lane = (args.hidden / 8 + kWave - 1) / kWave;
+  if (chunks_per_lane <= 1) {
+    kernel.func = gather_kernel_for<1>();
+  } else if (chunks_per_lane <= 2) {
+    kernel.func = gather_kernel_for<2>();
+  } else if (chunks_per_lane <= 4) {
+    kernel.func = gather_kernel_for<4>();
+  } else if (chunks_per_lane <= 8) {
+    kernel.func = gather_kernel_for<8>();
+  } else if (chunks_per_lane <= 16) {
+    kernel.func = gather_kernel_for<16>();
+  } else {
+    kernel.func = gather_kernel_for<32>();
+  }
+  kernel.grid = dim3(static_cast<unsigned>((capacity + 3) / 4), 1, 1);
+  kernel.block = dim3(256, 1, 1);
+  kernel.set_args(args);
+  return kernel;
+}
+
+KernelLaunch make_scatter(const ScatterArgs &args, int64_t capacity) {
+  KernelLaunch kernel;
+  kernel.func = reinterpret_cast<const void *>(&scatter_rows_kernel);
+  kernel.grid = dim3(static_cast<unsigned>((capacity + 3) / 4), 1, 1);
+  kernel.block = dim3(256, 1, 1);
+  kernel.set_args(args);
+  return kernel;
+}
+
+}  // namespace xp

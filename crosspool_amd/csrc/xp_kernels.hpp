@@ -1,0 +1,110 @@
+// Kernel argument records and host-side launch builders shared by the C ABI
+// and the Lane/GraphTemplate runtime.  Every kernel takes exactly one argument
+// record by value, so a launch is (function, grid, block, LDS bytes, record):
+// the same description drives an eager launch and a hipGraph kernel node, and
+// rebinding a captured node is a record overwrite.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <cstring>
+
+#include "xp_common.hpp"
+
+namespace xp {
+
+struct KernelLaunch {
+  const void *func = nullptr;
+  dim3 grid{1, 1, 1};
+  dim3 block{1, 1, 1};
+  unsigned shmem = 0;
+  alignas(16) unsigned char args[160] = {};
+  size_t args_size = 0;
+
+  template <class Args>
+  void set_args(const Args &value) {
+    static_assert(sizeof(Args) <= sizeof(args), "kernel argument record too large");
+    std::memcpy(args, &value, sizeof(Args));
+    args_size = sizeof(Args);
+  }
+  bool empty() const { return func == nullptr || grid.x == 0; }
+};
+
+inline hipError_t launch(const KernelLaunch &kernel, hipStream_t stream) {
+  if (kernel.empty()) {
+    return hipSuccess;
+  }
+  void *params[] = {const_cast<unsigned char *>(kernel.args)};
+  return hipLaunchKernel(kernel.func, kernel.grid, kernel.block, params, kernel.shmem, stream);
+}
+
+// ---------------------------------------------------------------- transport
+struct CopyArgs {
+  uint8_t *destination;
+  const uint8_t *source;
+  uint64_t bytes;
+};
+
+struct GatherArgs {
+  const uint16_t *pool;      // [pool_rows, hidden] bf16 mailbox
+  const int32_t *slots;      // [rows] slot ids
+  const uint16_t *norm;      // [hidden] RMSNorm weight, or null for a plain gather
+  uint16_t *out;             // [rows, hidden] contiguous batch
+  uint32_t *fault;           // sticky fault word, may be null
+  int64_t pool_rows;
+  int64_t hidden;
+  int64_t rows;              // live rows
+  float eps;
+};
+
+struct ScatterArgs {
+  const uint16_t *values;    // [rows, hidden] contiguous batch
+  const int32_t *slots;      // [rows] slot ids
+  uint16_t *pool;            // [pool_rows, hidden] mailbox
+  uint32_t *fault;
+  int64_t pool_rows;
+  int64_t hidden;
+  int64_t rows;
+};
+
+KernelLaunch make_copy(const CopyArgs &args);
+// `capacity` sizes the grid (graph templates keep one grid per capacity);
+// workgroups beyond the live rows exit immediately.
+KernelLaunch make_gather(const GatherArgs &args, int64_t capacity);
+KernelLaunch make_scatter(const ScatterArgs &args, int64_t capacity);
+bool gather_supported(int64_t hidden);
+
+// ---------------------------------------------------------------- GEMMs
+// out[t, :] = epilogue(sum_k x[t, k] * w[n, k]) for the live rows t < rows.
+// With `gated`, w rows are interleaved Gate/Up (row 2j = gate_j, row 2j+1 = up_j)
+// and out[t, j] = silu(gate_j) * up_j; otherwise out[t, n] is the projection.
+// `scatter_slots`, when set, redirects output row t to out + slots[t] * ldo.
+struct GemmArgs {
+  const uint16_t *x;
+  const uint16_t *w;
+  uint16_t *out;
+  const int32_t *scatter_slots;
+  int64_t ldx;
+  int64_t ldo;
+  int64_t rows;      // live rows
+  int64_t capacity;  // rows the grid was sized for (>= rows)
+  int64_t out_rows;  // bound on scatter slot ids (rows of `out` when scattering)
+  int64_t n;         // weight rows
+  int64_t k;         // reduction length
+  GatedSilu act;
+};
+
+enum class GemmKind : int { Skinny = 1, Tile = 2 };
+
+struct GemmChoice {
+  GemmKind kind;
+  int variant;  // index into the kind's instantiation table
+};
+
+GemmChoice choose_gemm(int64_t capacity, int64_t n, int64_t k, bool gated);
+KernelLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmChoice choice);
+const char *gemm_name(GemmChoice choice, bool gated);
+
+}  // namespace xp

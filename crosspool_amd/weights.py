@@ -1,0 +1,92 @@
+"""FfnAgent-owned Dense weight tensors (mirrors src/xpool/runtime/ffnagent/weights.py)."""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+
+def validate_weight_tensor(tensor: torch.Tensor, *, name: str) -> None:
+    """Device-resident, contiguous, positive-sized, 16-byte aligned (weights.py:232-247)."""
+
+    if tensor.device.type != "cuda":
+        raise ValueError(f"{name} must be GPU-resident")
+    if not tensor.is_contiguous() or any(size <= 0 for size in tensor.shape):
+        raise ValueError(f"{name} must have contiguous positive dimensions")
+    if tensor.data_ptr() % 16:
+        raise ValueError(f"{name} must be 16-byte aligned")
+
+
+@dataclass(frozen=True, slots=True)
+class ProjectionWeights:
+    """One projection's retained storage (weights.py:294-328).
+
+    ``values`` is ``[N, K]`` bf16 with K contiguous.  Scales (MXFP4) and
+    additive biases are not part of the Dense path measured here; passing them
+    raises.
+    """
+
+    values: torch.Tensor
+    scales: torch.Tensor | None = None
+    bias: torch.Tensor | None = None
+
+    def __post_init__(self) -> None:
+        validate_weight_tensor(self.values, name="projection values")
+        if self.values.dtype is not torch.bfloat16 or self.values.ndim != 2:
+            raise ValueError("projection values must be a bf16 matrix")
+        if self.scales is not None:
+            raise ValueError("quantised projections are not supported on the MI355X Dense path")
+        if self.bias is not None:
+            raise ValueError("projection biases are not supported on the MI355X Dense path")
+
+
+@dataclass(frozen=True, slots=True)
+class DenseFfnWeights:
+    """Retained input and output resources of one local Dense shard (weights.py:331-366).
+
+    ``i_proj.values`` is ``[2 I, H]`` with INTERLEAVED Gate/Up rows (row 2j =
+    gate_j, row 2j+1 = up_j, runtime/ffnagent/preparation.py:227);
+    ``o_proj.values`` is ``[H, I]``.
+    """
+
+    i_proj: ProjectionWeights
+    o_proj: ProjectionWeights
+
+    def __post_init__(self) -> None:
+        two_i, hidden = self.i_proj.values.shape
+        out_hidden, intermediate = self.o_proj.values.shape
+        if two_i != 2 * intermediate or out_hidden != hidden:
+            raise ValueError("Dense projections disagree: i_proj must be [2I, H] and o_proj [H, I]")
+        if self.o_proj.values.device != self.i_proj.values.device:
+            raise ValueError("Dense projections must share one device")
+        if self.i_proj.values.data_ptr() == self.o_proj.values.data_ptr():
+            raise ValueError("Dense projections must own independent storages")
+
+    @property
+    def hidden_size(self) -> int:
+        return int(self.i_proj.values.shape[1])
+
+    @property
+    def local_intermediate_size(self) -> int:
+        return int(self.o_proj.values.shape[1])
+
+    @property
+    def device(self) -> torch.device:
+        return self.i_proj.values.device
+
+    @classmethod
+    def from_tensors(cls, gate_up: torch.Tensor, down: torch.Tensor) -> DenseFfnWeights:
+        return cls(i_proj=ProjectionWeights(gate_up), o_proj=ProjectionWeights(down))
+
+
+def interleave_gate_up(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """Prepare the INTERLEAVED i_proj from separate Gate and Up ``[I, H]`` matrices.
+
+    The loader's Gate/Up normalisation (runtime/ffnagent/preparation.py:194-241,
+    src/xpool/ffn.py:57-68): row 2j = gate_j, row 2j+1 = up_j.
+    """
+
+    if gate.shape != up.shape or gate.ndim != 2:
+        raise ValueError("gate and up must be matrices of one shape")
+    return torch.stack((gate, up), dim=1).flatten(0, 1).contiguous()

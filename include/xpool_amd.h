@@ -1,0 +1,180 @@
+/*
+ * xpool_amd.h -- C ABI of the MI355X (gfx950) FfnAgent Dense-FFN path.
+ *
+ * This library replaces the pybind11 extension `xpool.native` (src/cext-bindings/)
+ * for the FfnAgent execution path only.  Every entry point takes plain device
+ * pointers, sizes and a HIP stream (`void *` = hipStream_t; NULL = the legacy
+ * default stream for kernel-level calls, the Lane's own stream for replays).
+ * No torch types cross this boundary.  References are file:line in the
+ * CrossPool checkout.
+ *
+ * Conventions
+ *   - Every function returns an xp_status (0 = success).  On failure the
+ *     calling thread's message is available through xp_last_error().
+ *     (Replaces the synchronous TORCH_CHECK -> RuntimeError errors of
+ *     src/cext/transport/instance.cpp:82-119 and src/cext-bindings/ops.cpp:17-26.)
+ *   - Payload rows are bf16 (`uint16_t` bit patterns), rows contiguous,
+ *     hidden and intermediate sizes multiples of 8, pointers 16-byte aligned.
+ *   - Work is stream-ordered and never synchronises the host, except the
+ *     functions documented as synchronous (health / synchronize).
+ *   - Kernels that find a slot id outside the mailbox poison the gathered row
+ *     with NaNs, skip the out-of-range write and OR XP_FAULT_SLOT_OUT_OF_RANGE
+ *     into a sticky device fault word (the reference's NaN-poisoned, sticky
+ *     canonical failure: src/cext/transport/instance.cu:28-31,75-77).
+ *   - Caller-owned memory (weights, workspace, mailboxes, outputs) is borrowed:
+ *     it must outlive every replay that reads it
+ *     (docs/designs/ffn-execution.md:243-296 ownership rule).
+ */
+#ifndef XPOOL_AMD_H
+#define XPOOL_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define XP_ABI_VERSION 1
+
+/* Status codes. */
+enum {
+  XP_OK = 0,
+  XP_ERROR_INVALID_ARGUMENT = 1,
+  XP_ERROR_HIP = 2,
+  XP_ERROR_STATE = 3,
+  XP_ERROR_NOT_FOUND = 4,
+  XP_ERROR_CAPACITY = 5,
+  XP_ERROR_UNSUPPORTED = 6
+};
+
+/* Closed FFN vocabulary, values identical to src/cext-include/xpool/ffn.hpp:15-54. */
+enum { XP_FORWARD_PREFILL = 1, XP_FORWARD_DECODE = 2, XP_FORWARD_IDLE = 4 };
+enum { XP_OUTPUT_PER_RANK_COMPLETE = 1, XP_OUTPUT_GROUP_SUM_COMPLETE = 2 };
+enum { XP_DP_ROWS_NONE = 0, XP_DP_ROWS_UNIFORM_BY_RANK = 1, XP_DP_ROWS_PACKED_BY_RANK = 2 };
+enum { XP_RESULT_OK = 0, XP_RESULT_SHUTDOWN = 1, XP_RESULT_PROTOCOL_MISMATCH = 2, XP_RESULT_TIMEOUT = 3 };
+enum { XP_LAYER_DENSE = 1, XP_LAYER_MOE = 2 };
+enum { XP_DTYPE_BF16 = 1 };
+
+/* Sticky device fault bits. */
+#define XP_FAULT_SLOT_OUT_OF_RANGE 1u
+
+typedef void *xp_stream_t;
+typedef struct xp_agent *xp_agent_t;
+typedef struct xp_lane *xp_lane_t;
+
+/* ABI version of this library (XP_ABI_VERSION).  Replaces ABI_VERSION of
+ * src/cext-bindings/module.cpp:16-79. */
+int xp_abi_version(void);
+
+/* Copy the calling thread's last error message; returns its full length. */
+size_t xp_last_error(char *buffer, size_t size);
+
+/* ------------------------------------------------------------------ kernels */
+
+/* Byte copy of `bytes` from src to dst (non-overlapping), any alignment; a zero
+ * length with NULL pointers is a no-op.  Replaces xpool::utils::cooperative::copy
+ * (src/cext-include/xpool/utils/cooperative.cuh:37-55), the primitive behind the
+ * Transport payload copies (src/cext/transport/instance.cu:83-84,184-186). */
+int xp_copy_bytes(void *dst, const void *src, size_t bytes, xp_stream_t stream);
+
+/* out[i, :] = pool[slots[i], :] for i < rows, then, when norm_weight is not
+ * NULL, out[i, :] = bf16(out_f32[i, :] / sqrt(mean(out_f32[i, :]^2) + eps) * w).
+ * Without norm_weight the rows are copied bit-exactly.  Replaces the row-prefix
+ * staging copy of src/cext/transport/instance.cu:83-84 and
+ * src/cext/fabric/atnagent.cu:215 (identity slots reproduce it); the fused
+ * RMSNorm replaces SGLang's post_attention_layernorm called before the shim
+ * (src/xpool/integrations/sglang/models/qwen2.py:125-126).  fault_word may be NULL. */
+int xp_gather_rmsnorm(const void *pool, int64_t pool_rows, int64_t hidden, const int32_t *slots, int64_t rows,
+                      const void *norm_weight, float eps, void *out, uint32_t *fault_word, xp_stream_t stream);
+
+/* pool[slots[i], :] = values[i, :] for i < rows, bit-exact.  Replaces the output
+ * copies of src/cext/fabric/atnagent.cu:275 and src/cext/transport/instance.cu:184-186.
+ * Slot ids must be distinct. */
+int xp_scatter(const void *values, int64_t rows, int64_t hidden, const int32_t *slots, void *pool,
+               int64_t pool_rows, uint32_t *fault_word, xp_stream_t stream);
+
+/* activated[t, j] = bf16(act(bf16(x[t] . w[2j]), bf16(x[t] . w[2j+1]))) with
+ * act(g, u) = silu_alpha(min(g, limit)) * (clamp(u, -limit, limit) + up_offset)
+ * (limit <= 0: no clipping).  w is the INTERLEAVED i_proj [2*intermediate, hidden].
+ * Replaces Gemm.run_into for i_proj with the fused epilogue
+ * (src/xpool/runtime/ffnagent/operators/linear.py:163-257,
+ *  operators/activation.py:112-173, operators/simt.py:13-45). */
+int xp_gemm_gate_up_silu(const void *x, int64_t rows, int64_t hidden, const void *w_gate_up, int64_t intermediate,
+                         void *activated, float alpha, float limit, float up_offset, xp_stream_t stream);
+
+/* out[t, n] = bf16(activated[t] . w_down[n]), w_down [hidden, intermediate].
+ * When slots is not NULL, row t is written to out + slots[t] * hidden instead
+ * (the scatter fused into the epilogue; out then has out_rows rows).
+ * Replaces Gemm.run_into for o_proj (operators/linear.py:163-257, dense.py:86). */
+int xp_gemm_down(const void *activated, int64_t rows, int64_t intermediate, const void *w_down, int64_t hidden,
+                 void *out, const int32_t *slots, int64_t out_rows, xp_stream_t stream);
+
+/* Bytes of Lane workspace one Dense step at `capacity` rows needs
+ * (gathered batch + activated intermediate).  Replaces DenseExecutionPlan's
+ * WorkspaceLayout (src/xpool/runtime/ffnagent/operators/dense.py:24-52). */
+size_t xp_dense_workspace_bytes(int64_t capacity, int64_t hidden, int64_t intermediate);
+
+/* One eager mailbox step: gather(+RMSNorm) -> gate_up+SiLU -> down -> scatter to
+ * pool_out rows slots[i] (pool_out may equal pool_in).  Same kernels as a replay.
+ * Replaces Dense.run_into (operators/dense.py:70-86) plus the Transport copies. */
+int xp_dense_step(const void *pool_in, void *pool_out, int64_t pool_rows, const int32_t *slots, int64_t rows,
+                  int64_t hidden, int64_t intermediate, const void *w_gate_up, const void *w_down,
+                  const void *norm_weight, float eps, void *workspace, size_t workspace_bytes, uint32_t *fault_word,
+                  xp_stream_t stream);
+
+/* Name of the kernel variant chosen for a projection ("skinny_..." / "tile_...").
+ * Returns the full name length. */
+size_t xp_gemm_variant(int64_t capacity, int64_t n, int64_t k, int gated, char *buffer, size_t size);
+
+/* ------------------------------------------------------------------ runtime */
+
+/* FfnAgent execution state on one device: the layer table shared by its Lanes.
+ * Replaces ExecutionRuntime::install's layer tables
+ * (src/cext/ffnagent/runtime.cu:627-699, 1008-1039). */
+int xp_agent_create(int device, xp_agent_t *out);
+int xp_agent_destroy(xp_agent_t agent);
+
+/* Register (or rebind) one Dense layer's borrowed weights.  gate_up is the
+ * INTERLEAVED i_proj [2*intermediate, hidden], down is o_proj [hidden,
+ * intermediate], norm_weight [hidden] or NULL.  Replaces
+ * LayerExecutionDescriptor + DenseBindingView (src/cext-bindings/ffnagent.cpp:44-210)
+ * and the device-side weight rebinding of bind_compute (src/cext/ffnagent/runtime.cu:336-369). */
+int xp_layer_register(xp_agent_t agent, int instance_index, int layer_ordinal, int64_t hidden, int64_t intermediate,
+                      const void *gate_up, const void *down, const void *norm_weight, float eps);
+
+/* Executor Lane: an owned HIP stream (default priority), a borrowed workspace
+ * and a sticky device fault word.  Replaces LaneCaptureResources
+ * (src/xpool/runtime/ffnagent/registry.py:25-137) and OwnedCudaStream
+ * (src/cext-bindings/cuda.cpp:13-41). */
+int xp_lane_create(xp_agent_t agent, void *workspace, size_t workspace_bytes, xp_lane_t *out);
+int xp_lane_destroy(xp_lane_t lane);
+int xp_lane_stream(xp_lane_t lane, xp_stream_t *out);
+/* Synchronous: waits for the Lane stream, then reads the fault word. */
+int xp_lane_check_health(xp_lane_t lane, uint32_t *fault_bits);
+int xp_lane_clear_fault(xp_lane_t lane);
+int xp_lane_synchronize(xp_lane_t lane);
+
+/* GraphTemplate: build and instantiate this Lane's hipGraph for the Execution
+ * Signature (bf16, capacity, hidden, intermediate).  Idempotent per signature.
+ * Replaces capture_dense_signature (src/xpool/runtime/ffnagent/registry.py:189-239)
+ * and materialize_lane's graph embedding (src/cext/ffnagent/runtime.cu:701-1006). */
+int xp_template_capture(xp_lane_t lane, int64_t hidden, int64_t intermediate, int64_t capacity);
+/* Number of captured templates; capacities of those matching (hidden, intermediate). */
+int xp_template_capacities(xp_lane_t lane, int64_t hidden, int64_t intermediate, int64_t *capacities,
+                           int max_count, int *count);
+
+/* Replay the smallest captured capacity >= rows for the layer: gather rows
+ * slots[0..rows) of pool_in (+ RMSNorm), Dense FFN, write them to the same slots
+ * of pool_out.  stream NULL = the Lane's stream.  1 <= rows <= largest capacity.
+ * Replaces wait_pre_compute's layer + capacity selection
+ * (src/cext/ffnagent/runtime.cu:232-258), bind_compute (:336-369) and the
+ * captured Dense body (registry.py:212-217). */
+int xp_replay(xp_lane_t lane, int instance_index, int layer_ordinal, int64_t rows, const void *pool_in,
+              void *pool_out, int64_t pool_rows, const int32_t *slots, xp_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* XPOOL_AMD_H */

@@ -1,0 +1,79 @@
+"""Parity helpers shared by the GPU tests (tolerances stated here, used everywhere).
+
+FFN output gates
+----------------
+* North star: rel-L2 <= 5e-3 against the pure-fp32 oracle (no intermediate
+  rounding), and max-abs <= 2e-2 against the oracle with the reference's
+  precision contract (qualification.py:290-314: fp64 projections, bf16 stage
+  rounding of gate/up, activated h and the output).  Both sides round the
+  output to bf16, so an element whose exact value sits next to a rounding
+  boundary may come out one bf16 ulp apart; where one ulp exceeds 2e-2
+  (|y| >= 4) such an element is allowed exactly one ulp, and at most 0.1 % of
+  elements may exceed 2e-2 at all.  Without this allowance no bf16-output
+  implementation can meet 2e-2 at Qwen3-8B scale (|y| reaches ~11, where half
+  an ulp is already 0.031).
+* Reference gates: ``assert_close(rtol=0.02, atol=0.1)``
+  (tests/suites/integration/runtime/ffnagent/test_operators.py:70) and
+  nRMSE <= 0.01, max-scaled error <= 0.10
+  (src/xpool-dev/xtest/harness/support/ffn.py:23-26,357).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from oracle import ffn_oracle as o
+
+NORTH_STAR_MAX_ABS = 2e-2
+NORTH_STAR_REL_L2 = 5e-3
+MAX_FRACTION_OVER_ABS = 1e-3
+
+
+def assert_bitwise_equal(actual: torch.Tensor, expected: torch.Tensor) -> None:
+    a = actual.detach().cpu().contiguous().view(torch.int16)
+    e = expected.detach().cpu().contiguous().view(torch.int16)
+    assert a.shape == e.shape
+    mismatches = int((a != e).sum().item())
+    assert mismatches == 0, f"{mismatches} of {a.numel()} 16-bit patterns differ"
+
+
+def assert_ffn_parity(actual: torch.Tensor, stage_reference: torch.Tensor, fp32_reference: torch.Tensor) -> None:
+    actual = actual.detach().cpu()
+    assert torch.isfinite(actual.float()).all(), "FFN output holds non-finite values"
+    stage = o.compare(stage_reference, actual, abs_limit=NORTH_STAR_MAX_ABS)
+    pure = o.compare(fp32_reference, actual.float(), abs_limit=NORTH_STAR_MAX_ABS)
+    assert pure.rel_l2 <= NORTH_STAR_REL_L2, f"rel-L2 vs fp32 oracle {pure.rel_l2:.3e}"
+    assert stage.over_ulp == 0, f"{stage.over_ulp} elements beyond max(2e-2, 1 ulp) (max-abs {stage.max_abs:.3e})"
+    assert stage.over_abs <= MAX_FRACTION_OVER_ABS * stage.elements, f"{stage.over_abs} elements above 2e-2"
+    assert stage.normalized_rmse <= o.FFN_OUTPUT_NORMALIZED_RMSE_LIMIT
+    assert stage.maximum_scaled_error <= o.FFN_OUTPUT_MAXIMUM_SCALED_ERROR_LIMIT
+    torch.testing.assert_close(actual, stage_reference, rtol=0.02, atol=0.1)
+
+
+def assert_within_ulps(actual: torch.Tensor, expected: torch.Tensor, ulps: float = 1.0, exact_fraction: float = 0.99):
+    """Elementwise |a - e| <= ulps * ulp(e) and at least ``exact_fraction`` bit-identical."""
+
+    a = actual.detach().cpu().float()
+    e = expected.detach().cpu().float()
+    assert torch.isfinite(a).all()
+    bound = ulps * o.bf16_ulp(e)
+    over = int(((a - e).abs() > bound).sum().item())
+    assert over == 0, f"{over} elements beyond {ulps} bf16 ulp (max diff {(a - e).abs().max().item():.3e})"
+    exact = float((actual.detach().cpu().view(torch.int16) == expected.detach().cpu().view(torch.int16)).float().mean())
+    assert exact >= exact_fraction, f"only {exact:.4f} of elements are bit-identical"
+
+
+def stage_activated(x: torch.Tensor, w_gate_up: torch.Tensor, **act) -> torch.Tensor:
+    """Oracle gate_up + gated SiLU with the reference's rounding points."""
+
+    projected = x.double() @ w_gate_up.double().t()
+    return o.gated_silu(projected[:, 0::2].to(torch.bfloat16), projected[:, 1::2].to(torch.bfloat16), **act)
+
+
+def to_device(tensor: torch.Tensor, device) -> torch.Tensor:
+    return tensor.contiguous().to(device)
+
+
+def slots_tensor(slots: np.ndarray, device) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(slots, dtype=np.int32)).to(device)

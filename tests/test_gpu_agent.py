@@ -1,0 +1,269 @@
+"""GPU parity of the full FfnAgent path: GraphTemplates, Lanes, replays, ffn_shim.
+
+Each case runs the hipGraph replay and compares with the oracle's mailbox step
+(gather -> RMSNorm -> Dense with the reference's rounding points -> scatter):
+rows outside the gathered slots must be untouched bit-for-bit, gathered rows
+meet the FFN gates of tests/parity.py.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from crosspool_amd import _native
+from crosspool_amd.agent import FfnAgent, FfnHealthError
+from crosspool_amd.ffn import DpRowLayout, ForwardMode, OutputRequirement
+from crosspool_amd.ops import attach, detach, ffn_shim
+from crosspool_amd.transport import FfnRequestMetadata
+from crosspool_amd.weights import DenseFfnWeights
+from oracle import ffn_oracle as o
+from parity import assert_bitwise_equal, assert_ffn_parity, slots_tensor, to_device
+
+from conftest import GOLDEN_DIR
+
+pytestmark = pytest.mark.gpu
+
+
+def _weights(w_gate_up, w_down, device):
+    return DenseFfnWeights.from_tensors(to_device(w_gate_up, device), to_device(w_down, device))
+
+
+def _check_mailbox(new_pool_gpu, pool, slots, w_gate_up, w_down, norm_weight, eps=1e-6):
+    new_pool = new_pool_gpu.cpu()
+    expected_pool, normalized, stage_rows = o.mailbox_step(
+        pool, slots, w_gate_up, w_down, norm_weight=norm_weight, eps=eps
+    )
+    untouched = np.setdiff1d(np.arange(pool.shape[0]), slots)
+    assert_bitwise_equal(new_pool[untouched], pool[untouched])
+    fp32_rows = o.dense_fp32(normalized, w_gate_up, w_down)
+    assert_ffn_parity(o.gather(new_pool, slots), stage_rows, fp32_rows)
+
+
+def test_golden_mailbox_fixture(device):
+    golden = np.load(GOLDEN_DIR / "mailbox_32x128.npz")
+    pool = o.bf16_from_bits(golden["pool"])
+    w_gate_up = o.bf16_from_bits(golden["w_gate_up"])
+    w_down = o.bf16_from_bits(golden["w_down"])
+    norm_weight = o.bf16_from_bits(golden["norm_weight"])
+    slots = golden["slots"]
+    with FfnAgent(device) as agent:
+        agent.register_layer(
+            instance_index=0, layer_ordinal=0, weights=_weights(w_gate_up, w_down, device),
+            norm_weight=to_device(norm_weight, device), eps=float(golden["eps"][0]),
+        )
+        agent.materialize(maximum_row_capacity=8)
+        pool_gpu = to_device(pool, device)
+        agent.execute(instance_index=0, layer_ordinal=0, pool=pool_gpu, slots=slots_tensor(slots, device))
+        agent.lanes[0].synchronize()
+        new_pool = pool_gpu.cpu()
+    expected_pool = o.bf16_from_bits(golden["new_pool"])
+    untouched = np.setdiff1d(np.arange(32), slots)
+    assert_bitwise_equal(new_pool[untouched], expected_pool[untouched])
+    normalized = o.bf16_from_bits(golden["normalized"])
+    assert_ffn_parity(
+        o.gather(new_pool, slots), o.bf16_from_bits(golden["ffn_rows"]), o.dense_fp32(normalized, w_gate_up, w_down)
+    )
+
+
+def test_config1_qwen3_0_6b_mailbox(device):
+    # 256-slot mailbox, hidden 1024, 64 seeded slots, RMSNorm eps 1e-6,
+    # gate_up [1024 -> 2x3072], down [3072 -> 1024], scattered back to the same slots.
+    hidden, intermediate = 1024, 3072
+    pool = o.generate_hidden_states(256, hidden, 17)
+    w_gate_up, w_down, norm_weight = o.generate_layer(hidden, intermediate, 18)
+    slots = o.generate_slots(256, 64, 19)
+    with FfnAgent(device) as agent:
+        agent.register_layer(
+            instance_index=0, layer_ordinal=0, weights=_weights(w_gate_up, w_down, device),
+            norm_weight=to_device(norm_weight, device),
+        )
+        agent.materialize(maximum_row_capacity=64)
+        pool_gpu = to_device(pool, device)
+        agent.execute(instance_index=0, layer_ordinal=0, pool=pool_gpu, slots=slots_tensor(slots, device))
+        agent.check_health()
+    _check_mailbox(pool_gpu, pool, slots, w_gate_up, w_down, norm_weight)
+
+
+@pytest.mark.parametrize("rows", [1, 4, 16, 32, 64, 256])
+def test_config3_qwen3_8b_layer(device, rows):
+    hidden, intermediate, pool_rows = 4096, 12288, 512
+    pool = o.generate_hidden_states(pool_rows, hidden, 17)
+    w_gate_up, w_down, norm_weight = o.generate_layer(hidden, intermediate, 18)
+    slots = o.generate_slots(pool_rows, rows, 19)
+    with FfnAgent(device) as agent:
+        agent.register_layer(
+            instance_index=0, layer_ordinal=0, weights=_weights(w_gate_up, w_down, device),
+            norm_weight=to_device(norm_weight, device),
+        )
+        agent.materialize(maximum_row_capacity=rows)
+        pool_gpu = to_device(pool, device)
+        agent.execute(instance_index=0, layer_ordinal=0, pool=pool_gpu, slots=slots_tensor(slots, device))
+        agent.check_health()
+    _check_mailbox(pool_gpu, pool, slots, w_gate_up, w_down, norm_weight)
+
+
+def test_config5_qwen3_32b_tp_shard_partial(device):
+    # one of 8 TP shards, hidden 5120, shard intermediate 3200, unreduced partial.
+    hidden, intermediate, rows = 5120, 3200, 8
+    pool = o.generate_hidden_states(64, hidden, 17)
+    w_gate_up, w_down, _ = o.generate_layer(hidden, intermediate, 18)
+    slots = np.arange(rows, dtype=np.int32)
+    with FfnAgent(device) as agent:
+        agent.register_layer(instance_index=0, layer_ordinal=0, weights=_weights(w_gate_up, w_down, device))
+        agent.materialize(maximum_row_capacity=8)
+        pool_gpu = to_device(pool, device)
+        out_gpu = torch.zeros_like(pool_gpu)
+        agent.execute(
+            instance_index=0, layer_ordinal=0, pool=pool_gpu, out_pool=out_gpu, slots=slots_tensor(slots, device)
+        )
+        agent.check_health()
+    assert_bitwise_equal(pool_gpu.cpu(), pool)  # the input mailbox is read-only here
+    partial = out_gpu.cpu()[:rows]
+    x = pool[:rows]
+    assert_ffn_parity(partial, o.dense_partial_reference(x, w_gate_up, w_down), o.dense_fp32(x, w_gate_up, w_down))
+
+
+def test_replay_uses_smallest_capacity_and_is_repeatable(device):
+    hidden, intermediate = 1024, 3072
+    pool = o.generate_hidden_states(128, hidden, 17)
+    w_gate_up, w_down, norm_weight = o.generate_layer(hidden, intermediate, 18)
+    slots = o.generate_slots(128, 100, 19)
+    with FfnAgent(device) as agent:
+        agent.register_layer(
+            instance_index=0, layer_ordinal=0, weights=_weights(w_gate_up, w_down, device),
+            norm_weight=to_device(norm_weight, device),
+        )
+        templates = agent.materialize(maximum_row_capacity=100)
+        assert sorted(t.signature.payload_row_capacity for t in templates) == [1, 2, 4, 8, 16, 32, 64, 100]
+        assert agent.lanes[0].capacities(hidden, intermediate) == (1, 2, 4, 8, 16, 32, 64, 100)
+        outputs = []
+        for live in (5, 5, 100, 37):
+            pool_gpu = to_device(pool, device)
+            agent.execute(
+                instance_index=0, layer_ordinal=0, pool=pool_gpu, slots=slots_tensor(slots, device), rows=live
+            )
+            agent.lanes[0].synchronize()
+            outputs.append(pool_gpu.cpu())
+        # Run-to-run equality of Lane outputs (test_fabric_execution.py:81).
+        assert_bitwise_equal(outputs[0], outputs[1])
+        for live, new_pool in zip((5, 100, 37), outputs[1:]):
+            _check_mailbox(new_pool, pool, slots[:live], w_gate_up, w_down, norm_weight)
+        with pytest.raises(RuntimeError, match="capacit"):
+            agent.execute(instance_index=0, layer_ordinal=0, pool=to_device(pool, device),
+                          slots=slots_tensor(o.generate_slots(128, 101, 3), device))
+
+
+def test_layers_share_templates_and_bind_their_own_weights(device):
+    # Config 2 pattern: many layers of one shape replayed through one template per capacity.
+    hidden, intermediate, layers = 1024, 3072, 4
+    pool = o.generate_hidden_states(4096, hidden, 17)
+    slots = o.generate_slots(4096, 32, 19)
+    weights = [o.generate_layer(hidden, intermediate, 100 + layer) for layer in range(layers)]
+    with FfnAgent(device) as agent:
+        for ordinal, (w_gate_up, w_down, norm_weight) in enumerate(weights):
+            agent.register_layer(
+                instance_index=0, layer_ordinal=ordinal, weights=_weights(w_gate_up, w_down, device),
+                norm_weight=to_device(norm_weight, device),
+            )
+        templates = agent.materialize(maximum_row_capacity=256)
+        assert len(templates) == 9  # capacities 1..256, shared by all four layers
+        pool_gpu = to_device(pool, device)
+        expected = pool
+        for ordinal, (w_gate_up, w_down, norm_weight) in enumerate(weights):
+            agent.execute(instance_index=0, layer_ordinal=ordinal, pool=pool_gpu, slots=slots_tensor(slots, device))
+            expected, _, _ = o.mailbox_step(expected, slots, w_gate_up, w_down, norm_weight=norm_weight)
+        agent.check_health()
+    got = pool_gpu.cpu()
+    untouched = np.setdiff1d(np.arange(4096), slots)
+    assert_bitwise_equal(got[untouched], pool[untouched])
+    # Four chained layers: compare with the chained stage oracle through the reference gates.
+    error = o.compare(o.gather(expected, slots), o.gather(got, slots))
+    assert error.normalized_rmse <= o.FFN_OUTPUT_NORMALIZED_RMSE_LIMIT
+
+
+def test_two_models_on_two_lanes(device):
+    # Qwen3-1.7B and Qwen3-4B shaped layers share one GPU; ragged
+    # per-step batches in disjoint slot ranges of an 8192-slot pool, one Lane each.
+    shapes = {0: (2048, 6144), 1: (2560, 9728)}
+    generator = np.random.default_rng(7)
+    with FfnAgent(device, executor_lane_count=2) as agent:
+        layers = {}
+        for instance, (hidden, intermediate) in shapes.items():
+            w_gate_up, w_down, norm_weight = o.generate_layer(hidden, intermediate, 200 + instance)
+            layers[instance] = (w_gate_up, w_down, norm_weight)
+            agent.register_layer(
+                instance_index=instance, layer_ordinal=0, weights=_weights(w_gate_up, w_down, device),
+                norm_weight=to_device(norm_weight, device),
+            )
+        agent.materialize(maximum_row_capacity=512)
+        pools = {i: o.generate_hidden_states(8192, h, 40 + i) for i, (h, _) in shapes.items()}
+        pools_gpu = {i: to_device(p, device) for i, p in pools.items()}
+        chosen = {}
+        for instance in shapes:
+            rows = int(generator.integers(1, 513))
+            base = instance * 4096
+            chosen[instance] = (base + generator.permutation(4096)[:rows]).astype(np.int32)
+        for instance in shapes:
+            agent.execute(
+                instance_index=instance, layer_ordinal=0, pool=pools_gpu[instance],
+                slots=slots_tensor(chosen[instance], device), lane=instance,
+            )
+        agent.check_health()
+    for instance, (w_gate_up, w_down, norm_weight) in layers.items():
+        _check_mailbox(pools_gpu[instance], pools[instance], chosen[instance], w_gate_up, w_down, norm_weight)
+
+
+def test_out_of_range_slot_sets_sticky_fault(device):
+    hidden, intermediate = 1024, 3072
+    pool = o.generate_hidden_states(64, hidden, 17)
+    w_gate_up, w_down, _ = o.generate_layer(hidden, intermediate, 18)
+    with FfnAgent(device) as agent:
+        agent.register_layer(instance_index=0, layer_ordinal=0, weights=_weights(w_gate_up, w_down, device))
+        agent.materialize(maximum_row_capacity=4)
+        pool_gpu = to_device(pool, device)
+        bad = slots_tensor(np.array([1, 64, 2], dtype=np.int32), device)
+        agent.execute(instance_index=0, layer_ordinal=0, pool=pool_gpu, slots=bad)
+        with pytest.raises(FfnHealthError):
+            agent.check_health()
+        assert agent.lanes[0].check_health() == _native.XP_FAULT_SLOT_OUT_OF_RANGE  # sticky
+        agent.lanes[0].clear_fault()
+        assert agent.lanes[0].check_health() == 0
+    got = pool_gpu.cpu()
+    untouched = np.setdiff1d(np.arange(64), [1, 2])
+    assert_bitwise_equal(got[untouched], pool[untouched])
+
+
+def test_ffn_shim_matches_dense_partial(device):
+    hidden, intermediate = 1024, 3072
+    w_gate_up, w_down, _ = o.generate_layer(hidden, intermediate, 18)
+    agent = FfnAgent(device)
+    try:
+        agent.register_layer(instance_index=0, layer_ordinal=3, weights=_weights(w_gate_up, w_down, device))
+        agent.materialize(maximum_row_capacity=128)
+        attach(agent)
+        metadata = FfnRequestMetadata(3, ForwardMode.DECODE, OutputRequirement.PER_RANK_COMPLETE, DpRowLayout.NONE)
+        for rows in (1, 7, 128):
+            x = o.generate_hidden_states(rows, hidden, 50 + rows)
+            x_gpu = to_device(x, device)
+            out = ffn_shim(x_gpu, None, metadata)
+            torch.cuda.synchronize()
+            assert out.shape == x.shape and out.dtype == torch.bfloat16
+            assert_bitwise_equal(x_gpu.cpu(), x)
+            assert_ffn_parity(
+                out.cpu(), o.dense_partial_reference(x, w_gate_up, w_down), o.dense_fp32(x, w_gate_up, w_down)
+            )
+        with pytest.raises(RuntimeError, match="capacity"):
+            ffn_shim(torch.zeros((129, hidden), dtype=torch.bfloat16, device=device), None, metadata)
+        with pytest.raises(RuntimeError, match="hidden size"):
+            ffn_shim(torch.zeros((4, 512), dtype=torch.bfloat16, device=device), None, metadata)
+        with pytest.raises(RuntimeError, match="NONE"):
+            ffn_shim(
+                torch.zeros((4, hidden), dtype=torch.bfloat16, device=device),
+                torch.ones(2, dtype=torch.int32, device=device),
+                metadata,
+            )
+    finally:
+        detach()
+        agent.close()
