@@ -14,6 +14,7 @@ from __future__ import annotations
 
 import ctypes
 import logging
+from collections import deque
 from dataclasses import dataclass
 from time import monotonic
 
@@ -77,6 +78,7 @@ class ExecutorLane:
         _native.call("xp_lane_stream", self.handle, ctypes.byref(stream))
         self.stream = torch.cuda.ExternalStream(stream.value or 0, device=agent.device)
         self.templates: dict[tuple[int, int, int], GraphTemplate] = {}
+        self._in_flight: deque[tuple[torch.cuda.Event, tuple[torch.Tensor, ...]]] = deque()
 
     def capture(self, template: GraphTemplate) -> None:
         """Instantiate the template's hipGraph on this Lane (idempotent)."""
@@ -132,9 +134,11 @@ class ExecutorLane:
         rows = slots.numel() if rows is None else rows
         if not 0 < rows <= slots.numel():
             raise ValueError("row count must be positive and covered by the slot ids")
+        current = torch.cuda.current_stream(self.agent.device)
+        run_on = self.stream if stream is None else stream
         if stream is None:
             # Lane stream: order after the caller's pending work on the current stream.
-            self.stream.wait_stream(torch.cuda.current_stream(self.agent.device))
+            self.stream.wait_stream(current)
             stream_handle = None
         else:
             stream_handle = ctypes.c_void_p(stream.cuda_stream)
@@ -142,6 +146,25 @@ class ExecutorLane:
             "xp_replay", self.handle, instance_index, layer_ordinal, rows, ctypes.c_void_p(pool.data_ptr()),
             ctypes.c_void_p(out_pool.data_ptr()), pool.shape[0], ctypes.c_void_p(slots.data_ptr()), stream_handle,
         )
+        if run_on.cuda_stream != current.cuda_stream:
+            self._retain(run_on, (pool, out_pool, slots))
+
+    def _retain(self, stream: torch.cuda.Stream, tensors: tuple[torch.Tensor, ...]) -> None:
+        """Keep borrowed tensors alive until the replay that reads them has run.
+
+        The caching allocator only tracks the stream a tensor was allocated on;
+        without this a tensor freed by the caller could be handed out again
+        while this Lane's stream still reads it.
+        """
+
+        while self._in_flight and self._in_flight[0][0].query():
+            self._in_flight.popleft()
+        event = torch.cuda.Event()
+        event.record(stream)
+        self._in_flight.append((event, tensors))
+
+    def _release_retained(self) -> None:
+        self._in_flight.clear()
 
     def check_health(self) -> int:
         """Synchronise the Lane and return its sticky fault bits (0 = healthy)."""
@@ -149,6 +172,7 @@ class ExecutorLane:
         self._require_open()
         bits = ctypes.c_uint32()
         _native.call("xp_lane_check_health", self.handle, ctypes.byref(bits))
+        self._release_retained()
         return int(bits.value)
 
     def clear_fault(self) -> None:
@@ -158,12 +182,18 @@ class ExecutorLane:
     def synchronize(self) -> None:
         self._require_open()
         _native.call("xp_lane_synchronize", self.handle)
+        self._release_retained()
 
     def close(self) -> None:
+        """Drain the Lane (its stream is destroyed), then drop retained tensors."""
+
         if self.handle is not None:
+            for event, _ in self._in_flight:
+                event.synchronize()
             _native.call("xp_lane_destroy", self.handle)
             self.handle = None
             self.templates.clear()
+            self._release_retained()
 
     def _require_open(self) -> None:
         if self.handle is None:

@@ -64,6 +64,99 @@ def assert_within_ulps(actual: torch.Tensor, expected: torch.Tensor, ulps: float
     assert exact >= exact_fraction, f"only {exact:.4f} of elements are bit-identical"
 
 
+# --------------------------------------------------------------------------- #
+# Rigorous bounds for the projections
+#
+# The kernels accumulate in fp32 and the oracle in fp64.  For a dot product S
+# with magnitude sum M = sum |x_k w_k|, the fp32 result lies within
+# delta = 2^-17 M of S (a bound of 128 full-magnitude fp32 roundings, far above
+# the real blocked-summation error).  So a rounded projection must be one of
+# the bf16 values in [floor_bf16(S - delta), ceil_bf16(S + delta)], and the
+# gated activation must lie between the smallest and largest
+# bf16(silu(g') * u') over the bf16 values g', u' reachable that way, widened
+# by one bf16 ulp for the fp32 exp / divide of the epilogue.
+# --------------------------------------------------------------------------- #
+ACCUMULATION_BOUND = 2.0**-17
+
+
+def _bf16_key(b: torch.Tensor) -> torch.Tensor:
+    bits = b.contiguous().view(torch.int16).to(torch.int32) & 0xFFFF
+    magnitude = bits & 0x7FFF
+    return torch.where(bits >= 0x8000, -magnitude, magnitude)
+
+
+def _bf16_from_key(key: torch.Tensor) -> torch.Tensor:
+    bits = torch.where(key >= 0, key, 0x8000 | (-key))
+    signed = bits - 0x10000 * (bits >= 0x8000).to(torch.int32)  # two's-complement int16 range
+    return signed.to(torch.int16).view(torch.bfloat16)
+
+
+def bf16_step(b: torch.Tensor, steps: int) -> torch.Tensor:
+    """The bf16 value ``steps`` representable values above (negative: below) ``b``."""
+
+    return _bf16_from_key(_bf16_key(b) + steps)
+
+
+def bf16_floor(v: torch.Tensor) -> torch.Tensor:
+    b = v.to(torch.bfloat16)
+    return torch.where(b.double() > v, bf16_step(b, -1), b)
+
+
+def bf16_ceil(v: torch.Tensor) -> torch.Tensor:
+    b = v.to(torch.bfloat16)
+    return torch.where(b.double() < v, bf16_step(b, 1), b)
+
+
+def projection_interval(x: torch.Tensor, w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """bf16 interval a correctly implemented fp32-accumulated ``round(x w^T)`` must land in."""
+
+    exact = x.double() @ w.double().t()
+    delta = (x.double().abs() @ w.double().abs().t()) * ACCUMULATION_BOUND
+    return bf16_floor(exact - delta), bf16_ceil(exact + delta)
+
+
+def assert_projection_within_bounds(actual: torch.Tensor, x: torch.Tensor, w: torch.Tensor, exact_fraction=0.99):
+    lo, hi = projection_interval(x, w)
+    a = actual.detach().cpu()
+    assert torch.isfinite(a.float()).all()
+    outside = int(((a.double() < lo.double()) | (a.double() > hi.double())).sum().item())
+    assert outside == 0, f"{outside} of {a.numel()} projections outside their fp32-accumulation interval"
+    nominal = (x.double() @ w.double().t()).to(torch.bfloat16)
+    exact = float((a.view(torch.int16) == nominal.view(torch.int16)).float().mean())
+    assert exact >= exact_fraction, f"only {exact:.4f} of projections are bit-identical to the fp64 oracle"
+
+
+def _candidates(lo: torch.Tensor, hi: torch.Tensor) -> list[torch.Tensor]:
+    values = [lo, hi]
+    for steps in (1, 2):
+        stepped = bf16_step(lo, steps)
+        values.append(torch.where(stepped.double() <= hi.double(), stepped, hi))
+    return values
+
+
+def assert_activated_within_bounds(
+    actual: torch.Tensor, x: torch.Tensor, w_gate_up: torch.Tensor, exact_fraction: float = 0.99, **act
+) -> None:
+    g_lo, g_hi = projection_interval(x, w_gate_up[0::2])
+    u_lo, u_hi = projection_interval(x, w_gate_up[1::2])
+    low = high = None
+    for g in _candidates(g_lo, g_hi):
+        for u in _candidates(u_lo, u_hi):
+            h = o.gated_silu(g, u, **act).double()
+            low = h if low is None else torch.minimum(low, h)
+            high = h if high is None else torch.maximum(high, h)
+    slack_low = o.bf16_ulp(low.float()).double()
+    slack_high = o.bf16_ulp(high.float()).double()
+    a = actual.detach().cpu()
+    assert torch.isfinite(a.float()).all()
+    value = a.double()
+    outside = int(((value < low - slack_low) | (value > high + slack_high)).sum().item())
+    assert outside == 0, f"{outside} of {a.numel()} activations outside their rounding-point interval"
+    nominal = stage_activated(x, w_gate_up, **act)
+    exact = float((a.view(torch.int16) == nominal.view(torch.int16)).float().mean())
+    assert exact >= exact_fraction, f"only {exact:.4f} of activations are bit-identical to the oracle"
+
+
 def stage_activated(x: torch.Tensor, w_gate_up: torch.Tensor, **act) -> torch.Tensor:
     """Oracle gate_up + gated SiLU with the reference's rounding points."""
 

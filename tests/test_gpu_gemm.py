@@ -1,9 +1,10 @@
 """GPU parity of the MFMA projections (skinny and tile kernels).
 
-Bar: the activated output and the down projection within one bf16 ulp of the
-oracle with the reference's rounding points (fp64 sums rounded once), >= 99 %
-bit-identical; the fp32-accumulation order of the kernels is the only
-difference allowed.
+Bar (tests/parity.py): every projection lies in the bf16 interval that fp32
+accumulation of the exact fp64 sum can round to, every activation lies between
+the gated-SiLU values of the gate/up roundings reachable that way (+-1 bf16 ulp
+for the fp32 exp and divide), and >= 99 % of elements are bit-identical to the
+oracle with the reference's rounding points.
 """
 
 from __future__ import annotations
@@ -13,7 +14,13 @@ import torch
 
 from crosspool_amd import _native, dense
 from oracle import ffn_oracle as o
-from parity import assert_bitwise_equal, assert_within_ulps, slots_tensor, stage_activated, to_device
+from parity import (
+    assert_activated_within_bounds,
+    assert_bitwise_equal,
+    assert_projection_within_bounds,
+    slots_tensor,
+    to_device,
+)
 
 pytestmark = pytest.mark.gpu
 
@@ -33,7 +40,7 @@ def test_gate_up_silu_matches_stage_oracle(device, hidden, intermediate, rows):
     w_gate_up, _ = _layer(hidden, intermediate)
     out = dense.gate_up_silu(to_device(x, device), to_device(w_gate_up, device))
     torch.cuda.synchronize()
-    assert_within_ulps(out, stage_activated(x, w_gate_up), ulps=1.0, exact_fraction=0.99)
+    assert_activated_within_bounds(out, x, w_gate_up)
 
 
 @pytest.mark.parametrize("hidden,intermediate", SMALL_SHAPES)
@@ -43,8 +50,7 @@ def test_down_matches_oracle(device, hidden, intermediate, rows):
     _, w_down = _layer(hidden, intermediate)
     out = dense.down(to_device(h, device), to_device(w_down, device))
     torch.cuda.synchronize()
-    expected = (h.double() @ w_down.double().t()).to(torch.bfloat16)
-    assert_within_ulps(out, expected, ulps=1.0, exact_fraction=0.99)
+    assert_projection_within_bounds(out, h, w_down)
 
 
 @pytest.mark.parametrize("rows", [1, 4, 32, 64, 256, 512])
@@ -56,10 +62,8 @@ def test_qwen3_8b_projections(device, rows):
     activated = dense.gate_up_silu(x_d, gu_d)
     out = dense.down(activated, dn_d)
     torch.cuda.synchronize()
-    expected_h = stage_activated(x, w_gate_up)
-    assert_within_ulps(activated, expected_h, ulps=1.0, exact_fraction=0.99)
-    expected_y = (activated.cpu().double() @ w_down.double().t()).to(torch.bfloat16)
-    assert_within_ulps(out, expected_y, ulps=1.0, exact_fraction=0.99)
+    assert_activated_within_bounds(activated, x, w_gate_up)
+    assert_projection_within_bounds(out, activated.cpu(), w_down)
 
 
 @pytest.mark.parametrize("weight_std", [0.1, 3.0])
@@ -81,8 +85,7 @@ def test_reference_linear_case_with_alpha_limit_and_offset(device, weight_std):
         gate=GateTransform(limit=4.0, up_offset=-0.5),
     )
     torch.cuda.synchronize()
-    expected = stage_activated(x, w, alpha=1.3, limit=4.0, up_offset=-0.5)
-    assert_within_ulps(out, expected, ulps=1.0, exact_fraction=0.99)
+    assert_activated_within_bounds(out, x, w, alpha=1.3, limit=4.0, up_offset=-0.5)
 
 
 @pytest.mark.parametrize("rows", [7, 64, 300])

@@ -1,0 +1,189 @@
+"""Host logic and the C-ABI boundary without a GPU.
+
+Covers the Python mirror of the reference interface (capacity buckets,
+workspace geometry, signatures, request metadata, enums) and that the HIP
+library loads and exports every symbol ``include/xpool_amd.h`` declares.  The
+only native calls made are argument-validation paths that return before any
+HIP call, plus pure queries.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+
+import pytest
+import torch
+
+from crosspool_amd import _native
+from crosspool_amd.execution import (
+    DenseFfnExecutionSignature,
+    WorkspaceLayout,
+    dense_signatures,
+    derive_payload_row_capacities,
+    select_capacity,
+)
+from crosspool_amd.ffn import (
+    DpRowLayout,
+    ForwardMode,
+    GateTransform,
+    GateUpOrder,
+    LayerKind,
+    OutputRequirement,
+    ResultCode,
+    SiluActivation,
+    activation_arguments,
+)
+from crosspool_amd.transport import FfnRequestMetadata
+
+
+def _declared_functions() -> list[str]:
+    text = _native.HEADER_PATH.read_text()
+    return sorted(set(re.findall(r"^(?:int|size_t)\s+(xp_\w+)\s*\(", text, flags=re.MULTILINE)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _native.library()
+    declared = _declared_functions()
+    assert len(declared) >= 20
+    for name in declared:
+        assert hasattr(lib, name), f"{name} missing from {_native.LIBRARY_PATH}"
+    assert set(declared) == set(_native.SIGNATURES), "ctypes signatures and header disagree"
+    assert lib.xp_abi_version() == 1
+
+
+def test_header_enums_match_the_reference_values():
+    # src/cext-include/xpool/ffn.hpp:15-54
+    text = _native.HEADER_PATH.read_text()
+    expected = {
+        "XP_FORWARD_PREFILL": ForwardMode.PREFILL, "XP_FORWARD_DECODE": ForwardMode.DECODE,
+        "XP_FORWARD_IDLE": ForwardMode.IDLE, "XP_OUTPUT_PER_RANK_COMPLETE": OutputRequirement.PER_RANK_COMPLETE,
+        "XP_OUTPUT_GROUP_SUM_COMPLETE": OutputRequirement.GROUP_SUM_COMPLETE, "XP_DP_ROWS_NONE": DpRowLayout.NONE,
+        "XP_DP_ROWS_UNIFORM_BY_RANK": DpRowLayout.UNIFORM_BY_RANK,
+        "XP_DP_ROWS_PACKED_BY_RANK": DpRowLayout.PACKED_BY_RANK, "XP_RESULT_TIMEOUT": ResultCode.TIMEOUT,
+        "XP_LAYER_DENSE": LayerKind.DENSE, "XP_LAYER_MOE": LayerKind.MOE,
+    }
+    for name, value in expected.items():
+        match = re.search(rf"{name}\s*=\s*(\d+)", text)
+        assert match and int(match.group(1)) == int(value), name
+    assert (ForwardMode.PREFILL, ForwardMode.DECODE, ForwardMode.IDLE) == (1, 2, 4)
+
+
+def test_capacity_buckets_match_reference():
+    # tests/suites/unit/runtime/ffnagent/test_execution.py:18-24
+    assert derive_payload_row_capacities(1) == (1,)
+    assert derive_payload_row_capacities(5) == (1, 2, 4, 5)
+    assert derive_payload_row_capacities(8) == (1, 2, 4, 8)
+    assert derive_payload_row_capacities(4096)[-3:] == (1024, 2048, 4096)
+    with pytest.raises(ValueError, match="positive"):
+        derive_payload_row_capacities(0)
+    with pytest.raises(TypeError):
+        derive_payload_row_capacities(True)
+    assert select_capacity((1, 2, 4, 5), 3) == 4
+    with pytest.raises(ValueError):
+        select_capacity((1, 2, 4, 5), 6)
+
+
+def test_workspace_layout_matches_reference_known_answers():
+    # test_execution.py:26-60: the gated CONCATENATED 4x16x8 plan needs 192 bytes, the
+    # activated view starts 128 bytes in, a short or misaligned backing is refused.
+    layout = WorkspaceLayout.from_regions(((torch.bfloat16, (4, 16)), (torch.bfloat16, (4, 8)), (torch.uint8, (0,))))
+    assert layout.nbytes == 192
+    backing = torch.empty(layout.nbytes, dtype=torch.uint8)
+    projected, activated, _ = layout.views(backing)
+    assert projected.data_ptr() == backing.data_ptr()
+    assert activated.data_ptr() == backing.data_ptr() + 128
+    assert projected.shape == (4, 16) and activated.shape == (4, 8)
+    with pytest.raises(ValueError, match="extent"):
+        layout.views(backing[:-1])
+    misaligned = torch.empty(layout.nbytes + 1, dtype=torch.uint8)[1:]
+    with pytest.raises(ValueError, match="aligned"):
+        layout.views(misaligned)
+
+
+@pytest.mark.parametrize("capacity,hidden,intermediate", [(1, 1024, 3072), (4096, 4096, 12288), (8, 5120, 3200), (3, 8, 8)])
+def test_native_workspace_equals_signature_layout(capacity, hidden, intermediate):
+    signature = DenseFfnExecutionSignature(torch.bfloat16, capacity, hidden, intermediate)
+    assert _native.dense_workspace_bytes(capacity, hidden, intermediate) == signature.workspace_layout().nbytes
+
+
+def test_signature_validation():
+    with pytest.raises(ValueError, match="bf16"):
+        DenseFfnExecutionSignature(torch.float16, 4, 16, 8)
+    with pytest.raises(ValueError, match="multiples of 8"):
+        DenseFfnExecutionSignature(torch.bfloat16, 4, 12, 8)
+    with pytest.raises(ValueError, match="positive"):
+        DenseFfnExecutionSignature(torch.bfloat16, 0, 16, 8)
+    with pytest.raises(ValueError, match="default SiLU"):
+        DenseFfnExecutionSignature(torch.bfloat16, 4, 16, 8, activation=SiluActivation(alpha=1.3))
+    signatures = dense_signatures(hidden_size=1024, local_intermediate_size=3072, maximum_row_capacity=5)
+    assert [s.payload_row_capacity for s in signatures] == [1, 2, 4, 5]
+    assert len(set(signatures)) == 4  # hashable GraphTemplate keys
+
+
+def test_request_metadata_validation():
+    # src/xpool/transport.py:32-42
+    FfnRequestMetadata(0, ForwardMode.DECODE, OutputRequirement.PER_RANK_COMPLETE, DpRowLayout.NONE)
+    with pytest.raises(ValueError):
+        FfnRequestMetadata(-1, ForwardMode.DECODE, OutputRequirement.PER_RANK_COMPLETE, DpRowLayout.NONE)
+    with pytest.raises(ValueError):
+        FfnRequestMetadata(True, ForwardMode.DECODE, OutputRequirement.PER_RANK_COMPLETE, DpRowLayout.NONE)
+    with pytest.raises(TypeError):
+        FfnRequestMetadata(0, 2, OutputRequirement.PER_RANK_COMPLETE, DpRowLayout.NONE)
+    with pytest.raises(TypeError):
+        FfnRequestMetadata(0, ForwardMode.DECODE, 1, DpRowLayout.NONE)
+    with pytest.raises(TypeError):
+        FfnRequestMetadata(0, ForwardMode.DECODE, OutputRequirement.PER_RANK_COMPLETE, 0)
+
+
+def test_gate_up_order_and_activation_arguments():
+    gate, up = GateUpOrder.INTERLEAVED.row_indices(width=8, start=2, length=3)
+    assert list(range(16))[gate] == [4, 6, 8] and list(range(16))[up] == [5, 7, 9]
+    gate, up = GateUpOrder.CONCATENATED.row_indices(width=8, start=2, length=3)
+    assert list(range(16))[gate] == [2, 3, 4] and list(range(16))[up] == [10, 11, 12]
+    assert activation_arguments(SiluActivation(), GateTransform()) == (1.0, 0.0, 0.0)
+    assert activation_arguments(SiluActivation(1.3), GateTransform(4.0, -0.5)) == (1.3, 4.0, -0.5)
+    with pytest.raises(ValueError):
+        SiluActivation(alpha=0.0)
+    with pytest.raises(ValueError):
+        GateTransform(limit=-1.0)
+
+
+def test_abi_rejects_invalid_arguments_before_touching_the_device():
+    lib = _native.library()
+    p = ctypes.c_void_p
+    # hidden not a multiple of 8
+    assert lib.xp_gather_rmsnorm(p(16), 4, 12, p(16), 2, None, 1e-6, p(16), None, None) == _native.XP_ERROR_INVALID_ARGUMENT
+    assert "multiple of 8" in _native.last_error()
+    # misaligned rows
+    assert lib.xp_scatter(p(8), 1, 8, p(16), p(16), 4, None, None) == _native.XP_ERROR_INVALID_ARGUMENT
+    # overlapping copy ranges
+    assert lib.xp_copy_bytes(p(4096), p(4100), 64, None) == _native.XP_ERROR_INVALID_ARGUMENT
+    assert "overlap" in _native.last_error()
+    # zero rows are no-ops; zero-length copies accept null pointers
+    assert lib.xp_gather_rmsnorm(None, 0, 8, None, 0, None, 1e-6, None, None, None) == _native.XP_OK
+    assert lib.xp_copy_bytes(None, None, 0, None) == _native.XP_OK
+    # SiLU alpha must be positive
+    assert lib.xp_gemm_gate_up_silu(p(16), 1, 16, p(16), 8, p(16), 0.0, 0.0, 0.0, None) == _native.XP_ERROR_INVALID_ARGUMENT
+    # null handles
+    assert lib.xp_layer_register(None, 0, 0, 16, 8, p(16), p(16), None, 1e-6) == _native.XP_ERROR_INVALID_ARGUMENT
+    assert lib.xp_replay(None, 0, 0, 1, p(16), p(16), 1, p(16), None) == _native.XP_ERROR_INVALID_ARGUMENT
+    assert lib.xp_dense_workspace_bytes(0, 16, 8) == 0
+    with pytest.raises(_native.NativeError) as error:
+        _native.check(_native.XP_ERROR_CAPACITY, "probe")
+    assert error.value.status == _native.XP_ERROR_CAPACITY
+
+
+def test_gemm_variant_selection():
+    assert _native.gemm_variant(1, 24576, 4096, True).startswith("skinny_gated_t16")
+    assert _native.gemm_variant(64, 4096, 12288, False).startswith("skinny_t64")
+    assert _native.gemm_variant(2048, 24576, 4096, True).startswith("tile_gated")
+    assert _native.gemm_variant(4096, 4096, 12288, False).startswith("tile")
+
+
+def test_ffn_shim_requires_an_attachment():
+    from crosspool_amd.ops import ffn_shim
+
+    metadata = FfnRequestMetadata(0, ForwardMode.PREFILL, OutputRequirement.PER_RANK_COMPLETE, DpRowLayout.NONE)
+    with pytest.raises(RuntimeError, match="no attached"):
+        ffn_shim(torch.zeros((2, 16), dtype=torch.bfloat16), None, metadata)
