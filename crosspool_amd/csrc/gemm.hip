@@ -162,19 +162,64 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_gemm_kernel(GemmArgs a) {
 }
 
 // ------------------------------------------------------------------ tile
-template <int BM, int BN, bool GATED>
-__global__ __launch_bounds__(256) void tile_gemm_kernel(GemmArgs a) {
+// Raw buffer resource over `bytes` bytes: loads past the end return zero, which
+// masks rows beyond the live rows (activations) or beyond N (weights) without
+// branches.  Word 3 is the gfx9 raw-buffer format.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0), static_cast<int>(bytes),
+                                           0x00020000);
+}
+
+__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, uint32_t offset) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, static_cast<int>(offset), 0, 0));
+}
+
+using lds_void_t = __attribute__((address_space(3))) void *;
+
+// Direct global -> LDS load of 16 bytes per lane through a buffer resource: lane i's
+// data lands at `lds_row_base + 16 i`; offsets past the resource's end write zeros.
+__device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t rsrc, void *lds_base, uint32_t voffset,
+                                                  uint32_t soffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t)(lds_base), 16, static_cast<int>(voffset),
+                                           static_cast<int>(soffset), 0, 0);
+}
+
+// LDS tiles are rows of 64 bf16 (128 bytes = eight 16-byte chunks).  gfx950 serves
+// ds_read_b128 sixteen lanes at a time from a 256-byte bank line, i.e. two tile rows, so
+// the 16 rows one MFMA fragment read touches must occupy 16 distinct 16-byte slots:
+// logical chunk c of row r is stored at physical chunk c ^ ((r / 2) % 8).
+__device__ __forceinline__ int swizzle(int row) { return (row >> 1) & 7; }
+
+// s_waitcnt with vmcnt <= N and the LDS / export counters left unconstrained (gfx9 encoding:
+// vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit counter");
+  __builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+}
+
+// Offset that is always past a tile resource's end (resources stay below 2^31 bytes).
+constexpr uint32_t kOutOfRange = 0x7ffffff0u;
+
+// BM x BN block tile, BK = 64, WAVES_M x WAVES_N waves (two per SIMD at 8 waves) each
+// owning a (BM / WAVES_M) x (BN / WAVES_N) tile of 32x32x16 MFMA accumulators.
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool GATED>
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmArgs a) {
   constexpr int BK = 64;
-  constexpr int WTM = BM / 2;
-  constexpr int WTN = BN / 2;
+  constexpr int WAVES = WAVES_M * WAVES_N;
+  constexpr int WTM = BM / WAVES_M;
+  constexpr int WTN = BN / WAVES_N;
   constexpr int MT = WTM / 32;
   constexpr int NT = WTN / 32;
-  constexpr int APASS = BM / 32;
-  constexpr int BPASS = BN / 32;
-  constexpr int STAGE = (BM + BN) * BK;  // bf16 elements per LDS stage
+  constexpr int ROWS = BM + BN;                    // LDS rows per stage (A rows then B rows)
+  constexpr int STAGE = ROWS * BK;                 // bf16 elements per stage
+  constexpr int LOADS = ROWS / 8 / WAVES;          // 1 KB (8-row) load instructions per wave per stage
+  static_assert(MT >= 1 && NT >= 1, "wave tile must hold at least one 32x32 MFMA tile");
   static_assert(!GATED || NT % 2 == 0, "gated tiles need whole Gate/Up column groups per wave");
+  static_assert(ROWS % (8 * WAVES) == 0, "stage rows must split evenly over the waves");
+  static_assert(BM % 8 == 0, "8-row load groups must not straddle the A/B boundary");
 
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
+  __shared__ __attribute__((aligned(1024))) uint16_t lds[2 * STAGE];
 
   const int tiles_m = static_cast<int>((a.capacity + BM - 1) / BM);
   const int tile = xcd_major_tile(blockIdx.x, gridDim.x);
@@ -186,69 +231,62 @@ __global__ __launch_bounds__(256) void tile_gemm_kernel(GemmArgs a) {
   }
   const int64_t w0 = static_cast<int64_t>(tn) * BN;
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave >> 1;
-  const int wn = wave & 1;
+  const int lane = threadIdx.x & 63;
+  // Wave-uniform by construction; readfirstlane lets the compiler keep it (and the load
+  // descriptors and LDS bases derived from it) in scalar registers.
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int wm = wave % WAVES_M;
+  const int wn = wave / WAVES_M;
 
-  // Global -> register staging: thread t moves 16-byte chunk (t & 7) of rows (t >> 3) + 32 p.
-  const int lchunk = tid & 7;
-  const int lrow = tid >> 3;
-  const uint16_t *a_base = a.x + (m0 + lrow) * a.ldx + lchunk * 8;
-  const uint16_t *b_base = a.w + (w0 + lrow) * a.k + lchunk * 8;
-  uint32_t a_ok = 0;
-  uint32_t b_ok = 0;
+  // ---- loads: wave `wave` fills stage rows [wave * 8 * LOADS, +8 * LOADS).  Lane i of a load
+  // writes LDS row r0 + i / 8, physical chunk i % 8, which holds logical k chunk
+  // (i % 8) ^ swizzle(row): the swizzle is applied by choosing the global chunk.
+  const int64_t a_rows_left = a.rows - m0;
+  const int64_t b_rows_left = a.n - w0;
+  const __amdgpu_buffer_rsrc_t a_rsrc =
+      make_rsrc(a.x + m0 * a.ldx, static_cast<uint32_t>((a_rows_left < BM ? a_rows_left : BM) * a.ldx * 2));
+  const __amdgpu_buffer_rsrc_t b_rsrc =
+      make_rsrc(a.w + w0 * a.k, static_cast<uint32_t>((b_rows_left < BN ? b_rows_left : BN) * a.k * 2));
+  const int first_row = wave * 8 * LOADS;
+  const int row_in_load = lane >> 3;
+  uint32_t load_offset[LOADS];
+  bool load_is_a[LOADS];
+  int load_chunk[LOADS];
 #pragma unroll
-  for (int p = 0; p < APASS; ++p) {
-    a_ok |= (m0 + lrow + 32 * p < a.rows ? 1u : 0u) << p;
-  }
-#pragma unroll
-  for (int p = 0; p < BPASS; ++p) {
-    b_ok |= (w0 + lrow + 32 * p < a.n ? 1u : 0u) << p;
-  }
-  const int a_lds0 = lrow * BK + ((lchunk ^ (lrow & 7)) << 3);
-  // Weight rows: identity placement, or (gated) Gate rows of a wave's j range
-  // followed by the Up rows of the same range.
-  auto b_lds_row = [&](int p) -> int {
-    const int rr = lrow + 32 * p;
-    if constexpr (GATED) {
-      const int jrel = rr >> 1;
-      const int s = rr & 1;
-      const int wq = jrel / (BN / 4);
-      const int jj = jrel % (BN / 4);
-      return wq * (BN / 2) + s * (BN / 4) + jj;
+  for (int q = 0; q < LOADS; ++q) {
+    const int group_row = first_row + q * 8;  // 8-row groups never straddle the A/B boundary
+    const int row = group_row + row_in_load;
+    const int k_chunk = (lane & 7) ^ swizzle(row);
+    load_chunk[q] = k_chunk;
+    load_is_a[q] = group_row < BM;
+    if (load_is_a[q]) {
+      load_offset[q] = static_cast<uint32_t>((row * a.ldx + k_chunk * 8) * 2);
     } else {
-      return rr;
+      const int p = row - BM;  // LDS row within the B tile
+      int rr = p;              // weight row within the tile
+      if constexpr (GATED) {
+        // LDS row p = wq * (BN / WAVES_N) + s * (BN / WAVES_N / 2) + jj holds Gate (s = 0) or Up
+        // (s = 1) of j = wq * (BN / WAVES_N / 2) + jj, i.e. weight row 2 j + s.
+        constexpr int group = BN / WAVES_N;
+        const int wq = p / group;
+        const int s = (p % group) / (group / 2);
+        const int jj = p % (group / 2);
+        rr = 2 * (wq * (group / 2) + jj) + s;
+      }
+      load_offset[q] = static_cast<uint32_t>((rr * a.k + k_chunk * 8) * 2);
     }
-  };
-
-  const u32x4 zero = {0u, 0u, 0u, 0u};
-  u32x4 a_reg[APASS];
-  u32x4 b_reg[BPASS];
-  auto global_load = [&](int64_t kt) {
-    const int64_t k0 = kt * BK;
-    const bool k_ok = k0 + lchunk * 8 < a.k;
+  }
+  const bool k_whole = (a.k % BK) == 0;
+  auto issue_loads = [&](int64_t kt, int stage) {
+    const uint32_t k_bytes = static_cast<uint32_t>(kt * BK * 2);
+    uint16_t *base = lds + stage * STAGE + first_row * BK;
 #pragma unroll
-    for (int p = 0; p < APASS; ++p) {
-      a_reg[p] = (k_ok && ((a_ok >> p) & 1u)) ? load16(a_base + 32 * p * a.ldx + k0) : zero;
-    }
-#pragma unroll
-    for (int p = 0; p < BPASS; ++p) {
-      b_reg[p] = (k_ok && ((b_ok >> p) & 1u)) ? load16(b_base + 32 * p * a.k + k0) : zero;
-    }
-  };
-  auto lds_store = [&](int stage) {
-    uint16_t *as = lds + stage * STAGE;
-    uint16_t *bs = as + BM * BK;
-#pragma unroll
-    for (int p = 0; p < APASS; ++p) {
-      store16(as + a_lds0 + 32 * p * BK, a_reg[p]);
-    }
-#pragma unroll
-    for (int p = 0; p < BPASS; ++p) {
-      const int row = b_lds_row(p);
-      store16(bs + row * BK + ((lchunk ^ (row & 7)) << 3), b_reg[p]);
+    for (int q = 0; q < LOADS; ++q) {
+      const bool k_ok = k_whole || (kt * BK + load_chunk[q] * 8 < a.k);
+      // The scalar offset must stay wave-uniform; masking goes through the per-lane offset
+      // (kOutOfRange + k_bytes is still past the resource end).
+      buffer_load_lds16(load_is_a[q] ? a_rsrc : b_rsrc, base + q * 8 * BK, k_ok ? load_offset[q] : kOutOfRange,
+                        k_bytes);
     }
   };
 
@@ -266,49 +304,62 @@ __global__ __launch_bounds__(256) void tile_gemm_kernel(GemmArgs a) {
 
   const int frag_row = lane & 31;
   const int frag_half = lane >> 5;
-  auto compute = [&](int stage) {
+  bf16x8 af[2][MT];
+  bf16x8 bfrag[2][NT];
+  auto read_fragments = [&](int stage, int ks, int slot) {
     const uint16_t *as = lds + stage * STAGE;
     const uint16_t *bs = as + BM * BK;
+    const int chunk = ks * 2 + frag_half;
 #pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      const int chunk = ks * 2 + frag_half;
-      bf16x8 af[MT];
-      bf16x8 bfrag[NT];
+    for (int mt = 0; mt < MT; ++mt) {
+      const int row = wm * WTM + mt * 32 + frag_row;
+      af[slot][mt] = as_bf16x8(load16(as + row * BK + ((chunk ^ swizzle(row)) << 3)));
+    }
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const int row = wm * WTM + mt * 32 + frag_row;
-        af[mt] = as_bf16x8(load16(as + row * BK + ((chunk ^ (row & 7)) << 3)));
-      }
+    for (int nt = 0; nt < NT; ++nt) {
+      const int row = wn * WTN + nt * 32 + frag_row;
+      bfrag[slot][nt] = as_bf16x8(load16(bs + row * BK + ((chunk ^ swizzle(row)) << 3)));
+    }
+  };
+  auto mfma_step = [&](int slot) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
-        const int row = wn * WTN + nt * 32 + frag_row;
-        bfrag[nt] = as_bf16x8(load16(bs + row * BK + ((chunk ^ (row & 7)) << 3)));
-      }
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-          acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mt], bfrag[nt], acc[mt][nt], 0, 0, 0);
-        }
+        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[slot][mt], bfrag[slot][nt], acc[mt][nt], 0, 0, 0);
       }
     }
   };
 
+  // Prologue: tiles 0 and 1 in flight, wait for tile 0, read its first fragments.
   const int64_t ktiles = (a.k + BK - 1) / BK;
-  global_load(0);
-  lds_store(0);
+  issue_loads(0, 0);
+  if (ktiles > 1) {
+    issue_loads(1, 1);
+    wait_vmcnt<LOADS>();  // tile 0 landed; tile 1 may still be in flight
+  }
   __syncthreads();
+  read_fragments(0, 0, 0);
+
   for (int64_t kt = 0; kt < ktiles; ++kt) {
     const int stage = static_cast<int>(kt & 1);
-    const bool more = kt + 1 < ktiles;
-    if (more) {
-      global_load(kt + 1);
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      if (ks + 1 < BK / 16) {
+        read_fragments(stage, ks + 1, (ks + 1) & 1);
+      }
+      mfma_step(ks & 1);
     }
-    compute(stage);
-    if (more) {
-      lds_store(stage ^ 1);
+    if (kt + 1 < ktiles) {
+      // Tile kt+1 (our loads) has landed; after the barrier everyone's has, and nobody reads
+      // this stage any more, so tile kt+2 may refill it.
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if (kt + 2 < ktiles) {
+        issue_loads(kt + 2, stage);
+      }
+      read_fragments(stage ^ 1, 0, 0);
     }
-    __syncthreads();
   }
 
   // Epilogue: lane holds D[8 (r / 4) + 4 (lane / 32) + r % 4][lane % 32] of each 32x32 tile.
@@ -327,7 +378,7 @@ __global__ __launch_bounds__(256) void tile_gemm_kernel(GemmArgs a) {
       if constexpr (GATED) {
 #pragma unroll
         for (int nt = 0; nt < NT / 2; ++nt) {
-          const int64_t j = w0 / 2 + wn * (BN / 4) + nt * 32 + frag_row;
+          const int64_t j = w0 / 2 + wn * (WTN / 2) + nt * 32 + frag_row;
           if (2 * j < a.n) {
             row[j] = static_cast<uint16_t>(float_to_bf16(gated_silu(acc[mt][nt][r], acc[mt][nt + NT / 2][r], a.act)));
           }
@@ -372,22 +423,23 @@ const void *skinny_kernel(int variant) {
 struct TileShape {
   int bm;
   int bn;
+  int waves;
   int per_cu;       // resident workgroups per CU (LDS-limited)
   double quality;   // relative per-CU efficiency of the tile shape
 };
 constexpr TileShape kTileShapes[] = {
-    {256, 256, 1, 1.00},
-    {256, 128, 1, 0.90},
-    {128, 128, 2, 0.80},
+    {256, 256, 8, 1, 1.00},
+    {256, 128, 8, 1, 0.90},
+    {128, 128, 4, 2, 0.80},
 };
 
 template <bool GATED>
 const void *tile_kernel(int variant) {
   using Kernel = void (*)(GemmArgs);
   static const Kernel table[] = {
-      &tile_gemm_kernel<256, 256, GATED>,
-      &tile_gemm_kernel<256, 128, GATED>,
-      &tile_gemm_kernel<128, 128, GATED>,
+      &tile_gemm_kernel<256, 256, 2, 4, GATED>,
+      &tile_gemm_kernel<256, 128, 4, 2, GATED>,
+      &tile_gemm_kernel<128, 128, 2, 2, GATED>,
   };
   return reinterpret_cast<const void *>(table[variant]);
 }
@@ -446,7 +498,7 @@ KernelLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmC
     kernel.func = gated ? tile_kernel<true>(choice.variant) : tile_kernel<false>(choice.variant);
     const int64_t tiles = ((capacity + shape.bm - 1) / shape.bm) * ((args.n + shape.bn - 1) / shape.bn);
     kernel.grid = dim3(static_cast<unsigned>(tiles), 1, 1);
-    kernel.block = dim3(256, 1, 1);
+    kernel.block = dim3(static_cast<unsigned>(64 * shape.waves), 1, 1);
   }
   GemmArgs record = args;
   record.capacity = capacity;
