@@ -37,8 +37,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "xp_copy_bytes": (_INT, [_P, _P, _SIZE, _P]),
     "xp_gather_rmsnorm": (_INT, [_P, _I64, _I64, _P, _I64, _P, _F32, _P, _P, _P]),
     "xp_scatter": (_INT, [_P, _I64, _I64, _P, _P, _I64, _P, _P]),
-    "xp_gemm_gate_up_silu": (_INT, [_P, _I64, _I64, _P, _I64, _P, _F32, _F32, _F32, _P]),
-    "xp_gemm_down": (_INT, [_P, _I64, _I64, _P, _I64, _P, _P, _I64, _P]),
+    "xp_gemm_gate_up_silu": (_INT, [_P, _I64, _I64, _P, _I64, _P, _F32, _F32, _F32, _P, _SIZE, _P]),
+    "xp_gemm_down": (_INT, [_P, _I64, _I64, _P, _I64, _P, _P, _I64, _P, _SIZE, _P]),
+    "xp_gemm_workspace_bytes": (_SIZE, [_I64, _I64, _I64, _INT]),
     "xp_dense_workspace_bytes": (_SIZE, [_I64, _I64, _I64]),
     "xp_dense_step": (_INT, [_P, _P, _I64, _P, _I64, _I64, _I64, _P, _P, _P, _F32, _P, _SIZE, _P, _P]),
     "xp_gemm_variant": (_SIZE, [_I64, _I64, _I64, _INT, ctypes.c_char_p, _SIZE]),
@@ -122,6 +123,10 @@ def gemm_variant(capacity: int, n: int, k: int, gated: bool) -> str:
     buffer = ctypes.create_string_buffer(64)
     lib.xp_gemm_variant(capacity, n, k, int(gated), buffer, 64)
     return buffer.value.decode()
+
+
+def gemm_workspace_bytes(rows: int, n: int, k: int, gated: bool) -> int:
+    return int(library().xp_gemm_workspace_bytes(rows, n, k, int(gated)))
 
 
 def dense_workspace_bytes(capacity: int, hidden: int, intermediate: int) -> int:

@@ -41,7 +41,10 @@ class GraphTemplate:
 
     @property
     def workspace_bytes(self) -> int:
-        return self.signature.workspace_layout().nbytes
+        """Lane workspace bytes of this template, K-slice partial sums included (native query)."""
+
+        s = self.signature
+        return _native.dense_workspace_bytes(s.payload_row_capacity, s.hidden_size, s.local_intermediate_size)
 
 
 @dataclass(frozen=True, slots=True)

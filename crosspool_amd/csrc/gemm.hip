@@ -9,13 +9,13 @@
 // Gate/Up (runtime/ffnagent/preparation.py:227).  Accumulation is fp32.
 //
 // Two kernel families, chosen per GraphTemplate capacity:
-//  * skinny (capacity <= 64, HBM-bound): weight rows are the MFMA M operand
+//  * split (capacity <= 64, HBM-bound): weight rows are the MFMA M operand
 //    (v_mfma_f32_16x16x32_bf16), each lane streams 64 contiguous bytes of one
-//    weight row per 128-wide K chunk, the few token rows are the N operand
-//    and come from L2.  A workgroup splits K across its waves and reduces the
-//    partial tiles through LDS in a fixed order (deterministic).  A Gate/Up
-//    pair lands in one lane's accumulator registers, so the SiLU epilogue
-//    needs no data exchange.
+//    weight row per 128-wide K chunk with several chunks of loads in flight, the
+//    few token rows are the N operand and come from L2.  A workgroup splits K
+//    across its waves and sums the ranges through LDS in a fixed order
+//    (deterministic).  A Gate/Up pair lands in one lane's accumulator registers,
+//    so the SiLU epilogue needs no data exchange.
 //  * tile (capacity > 64, MFMA-bound): BMxBN block tiles, BK = 64, four waves
 //    (2x2) each owning a (BM/2)x(BN/2) tile of v_mfma_f32_32x32x16_bf16
 //    accumulators, register-staged global loads double-buffered through LDS
@@ -42,128 +42,8 @@ __device__ __forceinline__ uint16_t *output_row(const GemmArgs &a, int64_t token
   return a.out + token * a.ldo;
 }
 
-// ------------------------------------------------------------------ skinny
-template <int TB, int WAVES, bool GATED>
-__global__ __launch_bounds__(WAVES * 64) void skinny_gemm_kernel(GemmArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int r16 = lane & 15;
-  const int kq = lane >> 4;
-  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 16;
-
-  const int64_t wn = n0 + r16;
-  const bool w_ok = wn < a.n;
-  const uint16_t *w_row = a.w + (w_ok ? wn : 0) * a.k + kq * 32;
-  const uint16_t *x_row[TB];
-  bool x_ok[TB];
-#pragma unroll
-  for (int tb = 0; tb < TB; ++tb) {
-    const int64_t token = tb * 16 + r16;
-    x_ok[tb] = token < a.rows;
-    x_row[tb] = a.x + (x_ok[tb] ? token : 0) * a.ldx + kq * 32;
-  }
-
-  f32x4 acc[TB];
-#pragma unroll
-  for (int tb = 0; tb < TB; ++tb) {
-    acc[tb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  }
-
-  const int64_t chunks = (a.k + 127) >> 7;
-  const bool whole = (a.k & 127) == 0;
-  const u32x4 zero = {0u, 0u, 0u, 0u};
-
-  u32x4 wf[4], xf[TB][4];
-  auto load_chunk = [&](int64_t chunk, u32x4 (&w)[4], u32x4 (&x)[TB][4]) {
-    const int64_t kb = chunk * 128;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const bool k_ok = whole || (kb + kq * 32 + s * 8 < a.k);
-      w[s] = (w_ok && k_ok) ? load16_stream(w_row + kb + s * 8) : zero;
-#pragma unroll
-      for (int tb = 0; tb < TB; ++tb) {
-        x[tb][s] = (x_ok[tb] && k_ok) ? load16(x_row[tb] + kb + s * 8) : zero;
-      }
-    }
-  };
-
-  int64_t chunk = wave;
-  if (chunk < chunks) {
-    load_chunk(chunk, wf, xf);
-  }
-  for (; chunk < chunks; chunk += WAVES) {
-    u32x4 wn_[4], xn_[TB][4];
-    const bool more = chunk + WAVES < chunks;
-    if (more) {
-      load_chunk(chunk + WAVES, wn_, xn_);
-    }
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-#pragma unroll
-      for (int tb = 0; tb < TB; ++tb) {
-        acc[tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(wf[s]), as_bf16x8(xf[tb][s]), acc[tb], 0, 0, 0);
-      }
-    }
-    if (more) {
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        wf[s] = wn_[s];
-#pragma unroll
-        for (int tb = 0; tb < TB; ++tb) {
-          xf[tb][s] = xn_[tb][s];
-        }
-      }
-    }
-  }
-
-  // Fixed-order reduction of the K-split partial tiles.
-  __shared__ float partial[WAVES > 1 ? WAVES : 1][TB * 4][64];
-  if constexpr (WAVES > 1) {
-#pragma unroll
-    for (int tb = 0; tb < TB; ++tb) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        partial[wave][tb * 4 + i][lane] = acc[tb][i];
-      }
-    }
-    __syncthreads();
-  }
-  for (int tb = (WAVES > 1 ? wave : 0); tb < TB; tb += WAVES) {
-    f32x4 sum;
-    if constexpr (WAVES > 1) {
-      sum = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      for (int w = 0; w < WAVES; ++w) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          sum[i] += partial[w][tb * 4 + i][lane];
-        }
-      }
-    } else {
-      sum = acc[tb];
-    }
-    const int64_t token = tb * 16 + r16;
-    const int64_t n = n0 + 4 * kq;  // this lane holds weight rows n .. n+3
-    if (token >= a.rows || n >= a.n) {
-      continue;
-    }
-    uint16_t *row = output_row(a, token);
-    if (row == nullptr) {
-      continue;
-    }
-    if constexpr (GATED) {
-      const float h0 = gated_silu(sum[0], sum[1], a.act);
-      const float h1 = gated_silu(sum[2], sum[3], a.act);
-      *reinterpret_cast<uint32_t *>(row + n / 2) = pack_bf16x2(h0, h1);
-    } else {
-      u32x2 packed = {pack_bf16x2(sum[0], sum[1]), pack_bf16x2(sum[2], sum[3])};
-      *reinterpret_cast<u32x2 *>(row + n) = packed;
-    }
-  }
-}
-
-// ------------------------------------------------------------------ tile
-// Raw buffer resource over `bytes` bytes: loads past the end return zero, which
-// masks rows beyond the live rows (activations) or beyond N (weights) without
+// Raw buffer resource over `bytes` bytes: loads past the end return zero without a memory
+// access, which masks token rows beyond the live rows and weight rows beyond N without
 // branches.  Word 3 is the gfx9 raw-buffer format.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0), static_cast<int>(bytes),
@@ -174,6 +54,344 @@ __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, uint
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, static_cast<int>(offset), 0, 0));
 }
 
+// ------------------------------------------------------------------ split (decode)
+// Weight-streaming projection for at most 64 live rows (HBM-bound).  A workgroup of 8
+// waves covers 8 / KSPLIT weight-row blocks of 16 rows; the KSPLIT waves of a block each
+// stream one contiguous K range of `k_slice` columns.  Per 128-wide K chunk a lane loads
+// 16 bytes of its weight row (16 rows x 64 contiguous bytes per load instruction) and the
+// matching token fragments (L2-resident; token rows past the live rows cost no memory
+// access), and the wave multiplies them on v_mfma_f32_16x16x32_bf16 with the weights as
+// the M operand.  DEPTH chunks of loads stay in flight.  The K ranges of a row block are
+// summed through LDS in a fixed order (deterministic), all within the workgroup, so no
+// partial sums leave the chip.
+constexpr int kSplitWaves = 8;
+
+template <int TB, int DEPTH, bool GATED>
+__global__ __launch_bounds__(64 * kSplitWaves) void split_gemm_kernel(GemmArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int r16 = lane & 15;
+  const int kq = lane >> 4;
+  const int ksplit = static_cast<int>(a.k_split);
+  const int part = wave % ksplit;
+  const int64_t rb = static_cast<int64_t>(blockIdx.x) * (kSplitWaves / ksplit) + wave / ksplit;
+  const int64_t row_blocks = (a.n + 15) / 16;
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+
+  f32x4 acc[TB];
+#pragma unroll
+  for (int tb = 0; tb < TB; ++tb) {
+    acc[tb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+
+  if (rb < row_blocks) {
+    const int k0 = part * static_cast<int>(a.k_slice);
+    const int chunks = static_cast<int>(a.k_slice / 128);  // a multiple of DEPTH
+    // Columns at or past K in the last range read the next row (or past the end): zero
+    // both operands there.
+    const int lane_valid = static_cast<int>(a.k) - k0 - kq * 8;
+    // Row blocks start at different chunks of their range (stride-7 rotation), spreading
+    // the concurrently streamed addresses over the memory channels.
+    const int rotation = static_cast<int>((rb * 7) % chunks);
+    const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(a.w, static_cast<uint32_t>(a.n * a.k * 2));
+    const __amdgpu_buffer_rsrc_t x_rsrc = make_rsrc(a.x, static_cast<uint32_t>(a.rows * a.ldx * 2));
+    const uint32_t w_off = static_cast<uint32_t>(((rb * 16 + r16) * a.k + k0 + kq * 8) * 2);
+    uint32_t x_off[TB];
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) {
+      x_off[tb] = static_cast<uint32_t>(((tb * 16 + r16) * a.ldx + k0 + kq * 8) * 2);
+    }
+    auto column_of = [&](int chunk) {
+      const int c = chunk + rotation;
+      return (c < chunks ? c : c - chunks) * 128;
+    };
+
+    u32x4 wbuf[DEPTH][4];
+    u32x4 xbuf[DEPTH][TB][4];
+    auto load_chunk = [&](int chunk, u32x4 (&w)[4], u32x4 (&x)[TB][4]) {
+      const uint32_t column = static_cast<uint32_t>(column_of(chunk)) * 2;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        w[s] = buffer_load16(w_rsrc, w_off + column + s * 64);
+#pragma unroll
+        for (int tb = 0; tb < TB; ++tb) {
+          x[tb][s] = buffer_load16(x_rsrc, x_off[tb] + column + s * 64);
+        }
+      }
+    };
+    auto compute_chunk = [&](int chunk, const u32x4 (&w)[4], const u32x4 (&x)[TB][4]) {
+      const int column = column_of(chunk);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const bool valid = column + s * 32 < lane_valid;
+        const u32x4 wk = valid ? w[s] : zero;
+#pragma unroll
+        for (int tb = 0; tb < TB; ++tb) {
+          const u32x4 xk = valid ? x[tb][s] : zero;
+          acc[tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(wk), as_bf16x8(xk), acc[tb], 0, 0, 0);
+        }
+      }
+    };
+
+    // Every load is unconditional and the trip count has no partial group, so the wait
+    // counts track exactly DEPTH chunks in flight.
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      load_chunk(d, wbuf[d], xbuf[d]);
+    }
+    int c0 = 0;
+    for (; c0 < chunks - DEPTH; c0 += DEPTH) {
+#pragma unroll
+      for (int d = 0; d < DEPTH; ++d) {
+        compute_chunk(c0 + d, wbuf[d], xbuf[d]);
+        load_chunk(c0 + d + DEPTH, wbuf[d], xbuf[d]);
+        // Keep each refill right behind the chunk it replaces (DEPTH - 1 chunks stay in
+        // flight) instead of letting the scheduler batch all refills at the loop end.
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      compute_chunk(c0 + d, wbuf[d], xbuf[d]);
+    }
+  }
+
+  // Fixed-order sum of the K ranges of each row block: range 0's wave adds ranges
+  // 1 .. KSPLIT-1 in order.
+  __shared__ f32x4 partial[kSplitWaves][TB][64];
+  if (ksplit > 1) {
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) {
+      partial[wave][tb][lane] = acc[tb];
+    }
+    __syncthreads();
+    if (part != 0) {
+      return;
+    }
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) {
+      for (int p = 1; p < ksplit; ++p) {
+        acc[tb] += partial[wave + p][tb][lane];
+      }
+    }
+  }
+  if (rb >= row_blocks) {
+    return;
+  }
+
+  // lane holds D[4 kq + i][r16] of each token block: weight rows n .. n+3, one token.
+  const int64_t n = rb * 16 + 4 * kq;
+#pragma unroll
+  for (int tb = 0; tb < TB; ++tb) {
+    const int64_t token = tb * 16 + r16;
+    if (token >= a.rows || n >= a.n) {
+      continue;
+    }
+    uint16_t *row = output_row(a, token);
+    if (row == nullptr) {
+      continue;
+    }
+    if constexpr (GATED) {
+      const float h0 = gated_silu(acc[tb][0], acc[tb][1], a.act);
+      const float h1 = gated_silu(acc[tb][2], acc[tb][3], a.act);
+      *reinterpret_cast<uint32_t *>(row + n / 2) = pack_bf16x2(h0, h1);
+    } else {
+      u32x2 packed = {pack_bf16x2(acc[tb][0], acc[tb][1]), pack_bf16x2(acc[tb][2], acc[tb][3])};
+      *reinterpret_cast<u32x2 *>(row + n) = packed;
+    }
+  }
+}
+
+// ------------------------------------------------------------------ stream (decode)
+// Weight-streaming projection for 5 to 64 live rows.  Workgroup g works on K slice
+// g / groups_per_slice: it stages the activations of that slice in LDS once (rows padded
+// by 16 bytes so the 16 token rows one fragment read touches fall in distinct bank
+// slots), then each of its 8 waves streams one 16-row weight block of the slice with
+// DEPTH 128-wide K chunks of loads in flight (16 rows x 64 contiguous bytes per load
+// instruction), multiplying on v_mfma_f32_16x16x32_bf16 with the weights as the M
+// operand.  With several slices the fp32 partial tiles go to scratch and
+// stream_reduce_kernel, launched next on the same stream, finishes the projection.  (A
+// last-arriver reduction inside this kernel would need an agent-scope release per wave,
+// which writes back the XCD's whole L2 on this part and cost more than the stream itself.)
+constexpr int kStreamWaves = 8;
+constexpr int kStreamDepth = 4;
+
+template <int TB, bool GATED>
+__global__ __launch_bounds__(64 * kStreamWaves) void stream_gemm_kernel(GemmArgs a) {
+  constexpr int TP = 16 * TB;
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int r16 = lane & 15;
+  const int kq = lane >> 4;
+  const int64_t ks = a.k_slice;
+  const int64_t slices = (a.k + ks - 1) / ks;
+  const int64_t row_blocks = (a.n + 15) / 16;
+  const int64_t groups_per_slice = (row_blocks + kStreamWaves - 1) / kStreamWaves;
+  const int64_t slice = blockIdx.x / groups_per_slice;
+  const int64_t rb = (blockIdx.x % groups_per_slice) * kStreamWaves + wave;
+  const int64_t k0 = slice * ks;
+  const int64_t klen = (a.k - k0) < ks ? (a.k - k0) : ks;
+  const int64_t rs = ks + 8;  // LDS row stride in elements
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+
+  // Stage activations [0, TP) x [k0, k0 + ks) of this slice.  Rows past the live rows read
+  // as zero through the buffer range; columns past K are zeroed explicitly.
+  const __amdgpu_buffer_rsrc_t x_rsrc = make_rsrc(a.x, static_cast<uint32_t>(a.rows * a.ldx * 2));
+  const int vectors_per_row = static_cast<int>(ks / 8);
+  const int ldx = static_cast<int>(a.ldx);
+  const int kbase = static_cast<int>(k0);
+  const int kvalid = static_cast<int>(klen);
+  for (int index = threadIdx.x; index < TP * vectors_per_row; index += 64 * kStreamWaves) {
+    const int t = index / vectors_per_row;
+    const int c = index - t * vectors_per_row;
+    u32x4 value = buffer_load16(x_rsrc, static_cast<uint32_t>((t * ldx + kbase + c * 8) * 2));
+    value = c * 8 < kvalid ? value : zero;
+    store16(xs + t * rs + c * 8, value);
+  }
+  __syncthreads();
+  if (rb >= row_blocks) {
+    return;
+  }
+
+  // Every slice runs ks / 128 chunks (a multiple of DEPTH, so the loop has no partial
+  // group): weight loads go through a buffer resource over all N rows, rows past N read
+  // as zero, and all loads are unconditional, which lets the wait counts track exactly
+  // DEPTH chunks in flight.  Columns past K in the last slice are zeroed by a select.
+  const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(a.w, static_cast<uint32_t>(a.n * a.k * 2));
+  const uint32_t w_off = static_cast<uint32_t>(((rb * 16 + r16) * a.k + k0 + kq * 8) * 2);
+  const int chunks = static_cast<int>(ks / 128);
+  const int lane_valid = kvalid - kq * 8;
+  // Waves start at different chunks of the slice (a stride-7 rotation by row block), so the
+  // concurrently streamed addresses spread over the memory channels instead of every wave
+  // reading the same column range of its rows at the same time.
+  const int rotation = static_cast<int>((rb * 7) % chunks);
+  auto rotated = [&](int chunk) { return chunk + rotation < chunks ? chunk + rotation : chunk + rotation - chunks; };
+
+  u32x4 wbuf[kStreamDepth][4];
+  auto load_chunk = [&](int chunk, u32x4 (&w)[4]) {
+    const int column = rotated(chunk) * 128;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      w[s] = buffer_load16(w_rsrc, w_off + static_cast<uint32_t>((column + s * 32) * 2));
+    }
+  };
+  f32x4 acc[TB];
+#pragma unroll
+  for (int tb = 0; tb < TB; ++tb) {
+    acc[tb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+  auto compute_chunk = [&](int chunk, const u32x4 (&w)[4]) {
+    const int column = rotated(chunk) * 128;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const u32x4 wk = column + s * 32 < lane_valid ? w[s] : zero;
+#pragma unroll
+      for (int tb = 0; tb < TB; ++tb) {
+        const u32x4 x = load16(xs + (tb * 16 + r16) * rs + column + s * 32 + kq * 8);
+        acc[tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(wk), as_bf16x8(x), acc[tb], 0, 0, 0);
+      }
+    }
+  };
+
+#pragma unroll
+  for (int d = 0; d < kStreamDepth; ++d) {
+    load_chunk(d, wbuf[d]);
+  }
+  int c0 = 0;
+  for (; c0 < chunks - kStreamDepth; c0 += kStreamDepth) {
+#pragma unroll
+    for (int d = 0; d < kStreamDepth; ++d) {
+      compute_chunk(c0 + d, wbuf[d]);
+      load_chunk(c0 + d + kStreamDepth, wbuf[d]);
+      // Keep each refill right behind the chunk it replaces, so DEPTH - 1 chunks stay in
+      // flight throughout instead of the scheduler batching all refills at the end.
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < kStreamDepth; ++d) {
+    compute_chunk(c0 + d, wbuf[d]);
+  }
+
+  // lane holds D[4 kq + i][r16] of each token block: weight rows n .. n+3, one token.
+  const int64_t n = rb * 16 + 4 * kq;
+  if (slices > 1) {
+    // Partial tile of this slice; stream_reduce_kernel sums the slices in order.
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) {
+      const int64_t token = tb * 16 + r16;
+      if (token < a.rows && n < a.n) {
+        *reinterpret_cast<f32x4 *>(a.partials + (slice * a.rows + token) * a.n + n) = acc[tb];
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int tb = 0; tb < TB; ++tb) {
+    const int64_t token = tb * 16 + r16;
+    if (token >= a.rows || n >= a.n) {
+      continue;
+    }
+    uint16_t *row = output_row(a, token);
+    if (row == nullptr) {
+      continue;
+    }
+    if constexpr (GATED) {
+      const float h0 = gated_silu(acc[tb][0], acc[tb][1], a.act);
+      const float h1 = gated_silu(acc[tb][2], acc[tb][3], a.act);
+      *reinterpret_cast<uint32_t *>(row + n / 2) = pack_bf16x2(h0, h1);
+    } else {
+      u32x2 packed = {pack_bf16x2(acc[tb][0], acc[tb][1]), pack_bf16x2(acc[tb][2], acc[tb][3])};
+      *reinterpret_cast<u32x2 *>(row + n) = packed;
+    }
+  }
+}
+
+// Sum of the split-K partials [slices, rows, n] in slice order (so results do not depend
+// on which slice finished first), then the projection's epilogue.  One thread per four
+// consecutive outputs of one row: 16-byte partial loads, coalesced along n.
+template <bool GATED>
+__global__ __launch_bounds__(256) void stream_reduce_kernel(GemmArgs a) {
+  const int64_t quads = a.n / 4;
+  const int64_t index = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t token = index / quads;
+  if (token >= a.rows) {
+    return;
+  }
+  const int64_t n = (index - token * quads) * 4;
+  const int64_t slices = (a.k + a.k_slice - 1) / a.k_slice;
+  const int64_t plane = a.rows * a.n;
+  const float *source = a.partials + token * a.n + n;
+  auto partial = [&](int64_t slice) { return *reinterpret_cast<const f32x4 *>(source + slice * plane); };
+  // Loads issued four slices at a time; the additions keep slice order.
+  f32x4 sum = partial(0);
+  int64_t slice = 1;
+  for (; slice + 4 <= slices; slice += 4) {
+    const f32x4 p0 = partial(slice), p1 = partial(slice + 1), p2 = partial(slice + 2), p3 = partial(slice + 3);
+    sum += p0;
+    sum += p1;
+    sum += p2;
+    sum += p3;
+  }
+  for (; slice < slices; ++slice) {
+    sum += partial(slice);
+  }
+  uint16_t *row = output_row(a, token);
+  if (row == nullptr) {
+    return;
+  }
+  if constexpr (GATED) {
+    const float h0 = gated_silu(sum[0], sum[1], a.act);
+    const float h1 = gated_silu(sum[2], sum[3], a.act);
+    *reinterpret_cast<uint32_t *>(row + n / 2) = pack_bf16x2(h0, h1);
+  } else {
+    u32x2 packed = {pack_bf16x2(sum[0], sum[1]), pack_bf16x2(sum[2], sum[3])};
+    *reinterpret_cast<u32x2 *>(row + n) = packed;
+  }
+}
+
+// ------------------------------------------------------------------ tile
 using lds_void_t = __attribute__((address_space(3))) void *;
 
 // Direct global -> LDS load of 16 bytes per lane through a buffer resource: lane i's
@@ -341,18 +559,19 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
   __syncthreads();
   read_fragments(0, 0, 0);
 
+  constexpr int KSTEPS = BK / 16;
   for (int64_t kt = 0; kt < ktiles; ++kt) {
     const int stage = static_cast<int>(kt & 1);
 #pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      if (ks + 1 < BK / 16) {
-        read_fragments(stage, ks + 1, (ks + 1) & 1);
-      }
+    for (int ks = 0; ks + 1 < KSTEPS; ++ks) {
+      read_fragments(stage, ks + 1, (ks + 1) & 1);
       mfma_step(ks & 1);
     }
     if (kt + 1 < ktiles) {
-      // Tile kt+1 (our loads) has landed; after the barrier everyone's has, and nobody reads
-      // this stage any more, so tile kt+2 may refill it.
+      // The last k step's fragments are being read and tile kt+1 (our loads) is landing.
+      // Once both are done everywhere (barrier), nobody reads this stage any more: refill
+      // it with tile kt+2 and start on tile kt+1's fragments while the last k step's
+      // MFMAs run.
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
       if (kt + 2 < ktiles) {
@@ -360,6 +579,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
       }
       read_fragments(stage ^ 1, 0, 0);
     }
+    mfma_step((KSTEPS - 1) & 1);
   }
 
   // Epilogue: lane holds D[8 (r / 4) + 4 (lane / 32) + r % 4][lane % 32] of each 32x32 tile.
@@ -397,26 +617,16 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
 }
 
 // ------------------------------------------------------------------ tables
-struct SkinnyShape {
-  int token_blocks;  // 16-token MFMA column blocks (capacity <= 16 * token_blocks)
-  int waves;         // K-split waves per workgroup
-};
-// 64-token tiles stop at 8 waves: 16 waves would cap a 1024-thread workgroup at
-// 128 VGPRs and spill.
-constexpr SkinnyShape kSkinnyShapes[] = {
-    {1, 4}, {1, 8}, {1, 16}, {2, 4}, {2, 8}, {2, 16}, {4, 4}, {4, 8},
-};
-constexpr int kSkinnyShapeCount = sizeof(kSkinnyShapes) / sizeof(kSkinnyShapes[0]);
+template <bool GATED>
+const void *split_kernel() {
+  return reinterpret_cast<const void *>(&split_gemm_kernel<1, 4, GATED>);
+}
 
 template <bool GATED>
-const void *skinny_kernel(int variant) {
+const void *stream_kernel(int variant) {
   using Kernel = void (*)(GemmArgs);
-  static const Kernel table[] = {
-      &skinny_gemm_kernel<1, 4, GATED>, &skinny_gemm_kernel<1, 8, GATED>, &skinny_gemm_kernel<1, 16, GATED>,
-      &skinny_gemm_kernel<2, 4, GATED>, &skinny_gemm_kernel<2, 8, GATED>, &skinny_gemm_kernel<2, 16, GATED>,
-      &skinny_gemm_kernel<4, 4, GATED>, &skinny_gemm_kernel<4, 8, GATED>,
-  };
-  static_assert(sizeof(table) / sizeof(table[0]) == kSkinnyShapeCount, "skinny table mismatch");
+  static const Kernel table[] = {&stream_gemm_kernel<1, GATED>, &stream_gemm_kernel<2, GATED>,
+                                 &stream_gemm_kernel<4, GATED>};
   return reinterpret_cast<const void *>(table[variant]);
 }
 
@@ -446,28 +656,77 @@ const void *tile_kernel(int variant) {
 
 constexpr int kComputeUnits = 256;
 
+// Live rows up to which the split kernel (token fragments from L2) beats the stream
+// kernel (token slice staged in LDS): its token traffic grows with the rows while the
+// stream kernel pays for staging, partial sums and the reduction launch.  Measured on
+// the Qwen3-8B projections: gate_up (few long rows of K = 4096, a one-workgroup-per-CU
+// grid) crosses over after 4 rows, down (K = 12288 split 8 ways) after 8.
+constexpr int64_t kSplitMaxRowsGated = 4;
+constexpr int64_t kSplitMaxRows = 8;
+constexpr int kSplitDepth = 4;
+
+// K split of the split kernel.  Its load registers (170 VGPRs) leave room for one 8-wave
+// workgroup per CU, and 8 waves with DEPTH chunks in flight already cover the HBM
+// latency, so the choice is the largest K split (1, 2, 4 or 8 ranges per 16-row block)
+// that still fits the grid in the fewest rounds of 256 workgroups, with every range
+// holding columns and a whole number of load groups.
+GemmChoice choose_split(int64_t n, int64_t k) {
+  const int64_t quantum = 128 * kSplitDepth;
+  const int64_t row_blocks = (n + 15) / 16;
+  auto rounds = [&](int64_t ksplit) {
+    const int64_t groups = (row_blocks * ksplit + kSplitWaves - 1) / kSplitWaves;
+    return (groups + kComputeUnits - 1) / kComputeUnits;
+  };
+  auto slice = [&](int64_t ksplit) { return ((k + ksplit - 1) / ksplit + quantum - 1) / quantum * quantum; };
+  int64_t ksplit = 1;
+  while (ksplit < kSplitWaves && rounds(2 * ksplit) <= rounds(1) && (2 * ksplit - 1) * slice(2 * ksplit) < k) {
+    ksplit *= 2;
+  }
+  return {GemmKind::Split, 0, slice(ksplit), ksplit};
+}
+
+constexpr int64_t kStreamLdsBytes = 160 * 1024;
+constexpr int64_t kStreamSliceQuantum = 128 * kStreamDepth;  // a whole number of load groups
+
+int64_t stream_slices(int64_t k, int64_t k_slice) { return (k + k_slice - 1) / k_slice; }
+
+// K slice of the stream kernel.  The whole of K when the staged token rows fit LDS: the
+// reduction launch a sliced projection adds costs more than the unfilled CUs (measured on
+// gate_up, K = 4096: 192 one-slice workgroups beat 768 quarter slices plus the reduction).
+// Otherwise workgroups (8 row blocks x one slice) are spread over the 256 CUs, the busiest
+// CU streams ceil(workgroups / 256) slices of 128 weight rows, and the slice length
+// minimising that load wins, ties going to fewer slices (less partial traffic).
+GemmChoice choose_stream(int64_t capacity, int64_t n, int64_t k) {
+  const int variant = capacity <= 16 ? 0 : (capacity <= 32 ? 1 : 2);
+  const int64_t tp = 16 << variant;
+  const int64_t groups = ((n + 15) / 16 + kStreamWaves - 1) / kStreamWaves;
+  int64_t best_slice = 0;
+  int64_t best_load = 0;
+  for (int64_t slices = 1; slices <= 64; ++slices) {
+    const int64_t k_slice = ((k + slices - 1) / slices + kStreamSliceQuantum - 1) / kStreamSliceQuantum *
+                            kStreamSliceQuantum;
+    if (tp * (k_slice + 8) * 2 > kStreamLdsBytes || stream_slices(k, k_slice) != slices) {
+      continue;  // does not fit LDS, or the same slice length as fewer slices
+    }
+    if (slices == 1) {
+      return {GemmKind::Stream, variant, k_slice, 1};
+    }
+    const int64_t load = (slices * groups + kComputeUnits - 1) / kComputeUnits * k_slice;
+    if (best_slice == 0 || load < best_load) {
+      best_slice = k_slice;
+      best_load = load;
+    }
+  }
+  return {GemmKind::Stream, variant, best_slice, 1};
+}
+
 }  // namespace
 
 GemmChoice choose_gemm(int64_t capacity, int64_t n, int64_t k, bool gated) {
-  (void)gated;
-  if (capacity <= 64) {
-    const int token_blocks = capacity <= 16 ? 1 : (capacity <= 32 ? 2 : 4);
-    const int64_t blocks = (n + 15) / 16;
-    const int64_t chunks = (k + 127) / 128;
-    // Fewest K-split waves that still put >= 4096 waves in flight, without
-    // leaving a wave fewer than four 128-wide K chunks.
-    int chosen = -1;
-    for (int index = 0; index < kSkinnyShapeCount; ++index) {
-      const SkinnyShape &shape = kSkinnyShapes[index];
-      if (shape.token_blocks != token_blocks) {
-        continue;
-      }
-      chosen = index;
-      if (blocks * shape.waves >= 4096 || chunks < 4 * shape.waves * 2) {
-        break;
-      }
-    }
-    return {GemmKind::Skinny, chosen};
+  // The decode kernels address the weights through one 32-bit buffer range.
+  if (capacity <= 64 && n * k * 2 <= INT32_MAX) {
+    return capacity <= (gated ? kSplitMaxRowsGated : kSplitMaxRows) ? choose_split(n, k)
+                                                                     : choose_stream(capacity, n, k);
   }
   int best = 0;
   double best_cost = 0.0;
@@ -483,16 +742,53 @@ GemmChoice choose_gemm(int64_t capacity, int64_t n, int64_t k, bool gated) {
       best_cost = cost;
     }
   }
-  return {GemmKind::Tile, best};
+  return {GemmKind::Tile, best, 0, 1};
 }
 
-KernelLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmChoice choice) {
-  KernelLaunch kernel;
-  if (choice.kind == GemmKind::Skinny) {
-    const int waves = kSkinnyShapes[choice.variant].waves;
-    kernel.func = gated ? skinny_kernel<true>(choice.variant) : skinny_kernel<false>(choice.variant);
-    kernel.grid = dim3(static_cast<unsigned>((args.n + 15) / 16), 1, 1);
-    kernel.block = dim3(static_cast<unsigned>(waves * 64), 1, 1);
+size_t gemm_scratch_bytes(GemmChoice choice, int64_t capacity, int64_t n, int64_t k) {
+  if (choice.kind != GemmKind::Stream || stream_slices(k, choice.k_slice) == 1) {
+    return 0;
+  }
+  const size_t partial_bytes = static_cast<size_t>(stream_slices(k, choice.k_slice) * capacity * n) * sizeof(float);
+  return (partial_bytes + 255) / 256 * 256;
+}
+
+GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmChoice choice) {
+  GemmLaunch launches;
+  KernelLaunch &kernel = launches.main;
+  GemmArgs record = args;
+  record.capacity = capacity;
+  record.k_slice = choice.k_slice;
+  record.k_split = choice.k_split;
+  if (choice.kind == GemmKind::Split) {
+    const int64_t row_blocks = (args.n + 15) / 16;
+    const int64_t per_group = kSplitWaves / choice.k_split;
+    kernel.func = gated ? split_kernel<true>() : split_kernel<false>();
+    kernel.grid = dim3(static_cast<unsigned>((row_blocks + per_group - 1) / per_group), 1, 1);
+    kernel.block = dim3(64 * kSplitWaves, 1, 1);
+  } else if (choice.kind == GemmKind::Stream) {
+    const int64_t tp = 16 << choice.variant;
+    const int64_t groups = ((args.n + 15) / 16 + kStreamWaves - 1) / kStreamWaves;
+    const int64_t slices = stream_slices(args.k, choice.k_slice);
+    kernel.func = gated ? stream_kernel<true>(choice.variant) : stream_kernel<false>(choice.variant);
+    kernel.grid = dim3(static_cast<unsigned>(slices * groups), 1, 1);
+    kernel.block = dim3(64 * kStreamWaves, 1, 1);
+    kernel.shmem = static_cast<unsigned>(tp * (choice.k_slice + 8) * 2);
+    // Dynamic LDS beyond 64 KB must be allowed per function (idempotent, set on first use).
+    static bool configured[2][3] = {};
+    if (!configured[gated][choice.variant]) {
+      (void)hipFuncSetAttribute(kernel.func, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                static_cast<int>(kStreamLdsBytes));
+      configured[gated][choice.variant] = true;
+    }
+    if (slices > 1) {
+      KernelLaunch &reduce = launches.reduce;
+      reduce.func = gated ? reinterpret_cast<const void *>(&stream_reduce_kernel<true>)
+                          : reinterpret_cast<const void *>(&stream_reduce_kernel<false>);
+      reduce.grid = dim3(static_cast<unsigned>((capacity * (args.n / 4) + 255) / 256), 1, 1);
+      reduce.block = dim3(256, 1, 1);
+      reduce.set_args(record);
+    }
   } else {
     const TileShape &shape = kTileShapes[choice.variant];
     kernel.func = gated ? tile_kernel<true>(choice.variant) : tile_kernel<false>(choice.variant);
@@ -500,24 +796,29 @@ KernelLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmC
     kernel.grid = dim3(static_cast<unsigned>(tiles), 1, 1);
     kernel.block = dim3(static_cast<unsigned>(64 * shape.waves), 1, 1);
   }
-  GemmArgs record = args;
-  record.capacity = capacity;
   kernel.set_args(record);
-  return kernel;
+  return launches;
 }
 
 const char *gemm_name(GemmChoice choice, bool gated) {
-  static const char *skinny_names[2][kSkinnyShapeCount] = {
-      {"skinny_t16_w4", "skinny_t16_w8", "skinny_t16_w16", "skinny_t32_w4", "skinny_t32_w8", "skinny_t32_w16",
-       "skinny_t64_w4", "skinny_t64_w8"},
-      {"skinny_gated_t16_w4", "skinny_gated_t16_w8", "skinny_gated_t16_w16", "skinny_gated_t32_w4",
-       "skinny_gated_t32_w8", "skinny_gated_t32_w16", "skinny_gated_t64_w4", "skinny_gated_t64_w8"},
+  static const char *split_names[2][4] = {
+      {"split_t16_k1", "split_t16_k2", "split_t16_k4", "split_t16_k8"},
+      {"split_gated_t16_k1", "split_gated_t16_k2", "split_gated_t16_k4", "split_gated_t16_k8"},
   };
+  static const char *stream_names[2][3] = {{"stream_t16", "stream_t32", "stream_t64"},
+                                           {"stream_gated_t16", "stream_gated_t32", "stream_gated_t64"}};
   static const char *tile_names[2][3] = {
       {"tile_256x256", "tile_256x128", "tile_128x128"},
       {"tile_gated_256x256", "tile_gated_256x128", "tile_gated_128x128"},
   };
-  return choice.kind == GemmKind::Skinny ? skinny_names[gated][choice.variant] : tile_names[gated][choice.variant];
+  if (choice.kind == GemmKind::Split) {
+    const int split_index = choice.k_split == 1 ? 0 : (choice.k_split == 2 ? 1 : (choice.k_split == 4 ? 2 : 3));
+    return split_names[gated][split_index];
+  }
+  if (choice.kind == GemmKind::Stream) {
+    return stream_names[gated][choice.variant];
+  }
+  return tile_names[gated][choice.variant];
 }
 
 }  // namespace xp

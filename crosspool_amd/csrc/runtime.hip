@@ -7,8 +7,8 @@
 // conditional nor device-updatable graph nodes, so here a Lane owns one
 // instantiated hipGraphExec per signature, built from explicit kernel nodes;
 // the host selects the layer and the smallest capacity that holds the live rows
-// (the rule of runtime.cu:246-253) and rebinds the three kernel nodes' argument
-// records with hipGraphExecKernelNodeSetParams before hipGraphLaunch.
+// (the rule of runtime.cu:246-253) and rebinds the kernel nodes' argument records
+// with hipGraphExecKernelNodeSetParams before hipGraphLaunch.
 
 #include <algorithm>
 #include <cstdio>
@@ -55,10 +55,14 @@ constexpr size_t kRegionAlignment = 16;
 size_t align_up(size_t value, size_t alignment) { return (value + alignment - 1) / alignment * alignment; }
 
 // Workspace regions of one Dense step at `capacity`: gathered batch [capacity, hidden],
-// then the activated intermediate [capacity, intermediate], each 16-byte aligned.
+// then the activated intermediate [capacity, intermediate], each 16-byte aligned; then,
+// when the capacity takes the sliced stream kernel, its fp32 partial sums (256-byte
+// aligned, gate_up's then down's).
 struct DenseWorkspace {
   size_t batch_offset;
   size_t activated_offset;
+  size_t gate_up_partials_offset;
+  size_t down_partials_offset;
   size_t bytes;
 };
 
@@ -66,7 +70,19 @@ DenseWorkspace dense_workspace(int64_t capacity, int64_t hidden, int64_t interme
   DenseWorkspace layout{};
   layout.batch_offset = 0;
   layout.activated_offset = align_up(static_cast<size_t>(capacity * hidden) * 2, kRegionAlignment);
-  layout.bytes = layout.activated_offset + static_cast<size_t>(capacity * intermediate) * 2;
+  size_t cursor = layout.activated_offset + static_cast<size_t>(capacity * intermediate) * 2;
+  const size_t gate_up = gemm_scratch_bytes(choose_gemm(capacity, 2 * intermediate, hidden, true), capacity,
+                                            2 * intermediate, hidden);
+  const size_t down = gemm_scratch_bytes(choose_gemm(capacity, hidden, intermediate, false), capacity, hidden,
+                                         intermediate);
+  if (gate_up + down > 0) {
+    cursor = align_up(cursor, 256);
+    layout.gate_up_partials_offset = cursor;
+    cursor += gate_up;
+    layout.down_partials_offset = cursor;
+    cursor += down;
+  }
+  layout.bytes = cursor;
   return layout;
 }
 
@@ -79,12 +95,26 @@ int validate_geometry(int64_t hidden, int64_t intermediate) {
 
 GatedSilu default_activation() { return GatedSilu{1.0f, 0.0f, 0.0f}; }
 
-// The three kernels of one mailbox step, for a given capacity.
+// The kernels of one mailbox step, for a given capacity: gather (+ RMSNorm), gate_up
+// with the gated SiLU fused (+ its K-slice reduction), down with the scatter fused (+ its
+// reduction).  The sequence depends only on the capacity and geometry, so a template's
+// node list matches every replay's.
 struct DenseLaunches {
   KernelLaunch gather;
-  KernelLaunch gate_up;
-  KernelLaunch down;
+  GemmLaunch gate_up;
+  GemmLaunch down;
+
+  int chain(const KernelLaunch **out) const {
+    int count = 0;
+    for (const KernelLaunch *kernel : {&gather, &gate_up.main, &gate_up.reduce, &down.main, &down.reduce}) {
+      if (!kernel->empty()) {
+        out[count++] = kernel;
+      }
+    }
+    return count;
+  }
 };
+constexpr int kMaxStepKernels = 5;
 
 struct DenseBinding {
   const uint16_t *pool_in;
@@ -132,6 +162,7 @@ DenseLaunches make_dense_launches(const DenseBinding &b, int64_t capacity) {
   gate_up.n = 2 * b.intermediate;
   gate_up.k = b.hidden;
   gate_up.act = default_activation();
+  gate_up.partials = reinterpret_cast<float *>(b.workspace + layout.gate_up_partials_offset);
   launches.gate_up = make_gemm(gate_up, capacity, true, choose_gemm(capacity, gate_up.n, gate_up.k, true));
 
   GemmArgs down{};
@@ -146,8 +177,30 @@ DenseLaunches make_dense_launches(const DenseBinding &b, int64_t capacity) {
   down.n = b.hidden;
   down.k = b.intermediate;
   down.act = default_activation();
+  down.partials = reinterpret_cast<float *>(b.workspace + layout.down_partials_offset);
   launches.down = make_gemm(down, capacity, false, choose_gemm(capacity, down.n, down.k, false));
   return launches;
+}
+
+// Point a kernel-level projection at its caller-provided scratch for K-slice partials.
+int bind_scratch(GemmArgs &args, GemmChoice choice, void *workspace, size_t workspace_bytes) {
+  const size_t needed = gemm_scratch_bytes(choice, args.rows, args.n, args.k);
+  if (needed == 0) {
+    return XP_OK;
+  }
+  if (workspace == nullptr || workspace_bytes < needed) {
+    return fail(XP_ERROR_CAPACITY, "projection workspace is smaller than xp_gemm_workspace_bytes (" +
+                                       std::to_string(needed) + " bytes)");
+  }
+  XP_REQUIRE(aligned16(workspace), "projection workspace must be 16-byte aligned");
+  args.partials = static_cast<float *>(workspace);
+  return XP_OK;
+}
+
+int launch_gemm(const GemmLaunch &kernels, hipStream_t stream) {
+  XP_HIP_CHECK(launch(kernels.main, stream));
+  XP_HIP_CHECK(launch(kernels.reduce, stream));
+  return XP_OK;
 }
 
 hipKernelNodeParams node_params(const KernelLaunch &kernel, void **params) {
@@ -191,7 +244,8 @@ struct Template {
   int64_t capacity = 0;
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
-  hipGraphNode_t nodes[3] = {nullptr, nullptr, nullptr};
+  hipGraphNode_t nodes[kMaxStepKernels] = {};
+  int node_count = 0;
 };
 
 struct xp_lane {
@@ -304,8 +358,16 @@ int xp_scatter(const void *values, int64_t rows, int64_t hidden, const int32_t *
   return XP_OK;
 }
 
+size_t xp_gemm_workspace_bytes(int64_t rows, int64_t n, int64_t k, int gated) {
+  if (rows <= 0 || n <= 0 || k <= 0) {
+    return 0;
+  }
+  return gemm_scratch_bytes(choose_gemm(rows, n, k, gated != 0), rows, n, k);
+}
+
 int xp_gemm_gate_up_silu(const void *x, int64_t rows, int64_t hidden, const void *w_gate_up, int64_t intermediate,
-                         void *activated, float alpha, float limit, float up_offset, xp_stream_t stream) {
+                         void *activated, float alpha, float limit, float up_offset, void *workspace,
+                         size_t workspace_bytes, xp_stream_t stream) {
   XP_REQUIRE(rows >= 0, "row count must be non-negative");
   if (rows == 0) {
     return XP_OK;
@@ -328,12 +390,15 @@ int xp_gemm_gate_up_silu(const void *x, int64_t rows, int64_t hidden, const void
   args.k = hidden;
   args.act = GatedSilu{alpha, limit, up_offset};
   const GemmChoice choice = choose_gemm(rows, args.n, args.k, true);
-  XP_HIP_CHECK(launch(make_gemm(args, rows, true, choice), static_cast<hipStream_t>(stream)));
-  return XP_OK;
+  if (const int status = bind_scratch(args, choice, workspace, workspace_bytes); status != XP_OK) {
+    return status;
+  }
+  return launch_gemm(make_gemm(args, rows, true, choice), static_cast<hipStream_t>(stream));
 }
 
 int xp_gemm_down(const void *activated, int64_t rows, int64_t intermediate, const void *w_down, int64_t hidden,
-                 void *out, const int32_t *slots, int64_t out_rows, xp_stream_t stream) {
+                 void *out, const int32_t *slots, int64_t out_rows, void *workspace, size_t workspace_bytes,
+                 xp_stream_t stream) {
   XP_REQUIRE(rows >= 0, "row count must be non-negative");
   if (rows == 0) {
     return XP_OK;
@@ -357,8 +422,10 @@ int xp_gemm_down(const void *activated, int64_t rows, int64_t intermediate, cons
   args.k = intermediate;
   args.act = default_activation();
   const GemmChoice choice = choose_gemm(rows, args.n, args.k, false);
-  XP_HIP_CHECK(launch(make_gemm(args, rows, false, choice), static_cast<hipStream_t>(stream)));
-  return XP_OK;
+  if (const int status = bind_scratch(args, choice, workspace, workspace_bytes); status != XP_OK) {
+    return status;
+  }
+  return launch_gemm(make_gemm(args, rows, false, choice), static_cast<hipStream_t>(stream));
 }
 
 size_t xp_dense_workspace_bytes(int64_t capacity, int64_t hidden, int64_t intermediate) {
@@ -402,10 +469,11 @@ int xp_dense_step(const void *pool_in, void *pool_out, int64_t pool_rows, const 
   binding.workspace = static_cast<uint8_t *>(workspace);
   binding.fault = fault_word;
   const DenseLaunches launches = make_dense_launches(binding, rows);
-  const hipStream_t s = static_cast<hipStream_t>(stream);
-  XP_HIP_CHECK(launch(launches.gather, s));
-  XP_HIP_CHECK(launch(launches.gate_up, s));
-  XP_HIP_CHECK(launch(launches.down, s));
+  const KernelLaunch *chain[kMaxStepKernels];
+  const int count = launches.chain(chain);
+  for (int index = 0; index < count; ++index) {
+    XP_HIP_CHECK(launch(*chain[index], static_cast<hipStream_t>(stream)));
+  }
   return XP_OK;
 }
 
@@ -590,8 +658,9 @@ int xp_template_capture(xp_lane_t lane, int64_t hidden, int64_t intermediate, in
   t->intermediate = intermediate;
   t->capacity = capacity;
   XP_HIP_CHECK(hipGraphCreate(&t->graph, 0));
-  const KernelLaunch *chain[3] = {&launches.gather, &launches.gate_up, &launches.down};
-  for (int index = 0; index < 3; ++index) {
+  const KernelLaunch *chain[kMaxStepKernels];
+  t->node_count = launches.chain(chain);
+  for (int index = 0; index < t->node_count; ++index) {
     void *params[1];
     hipKernelNodeParams node = node_params(*chain[index], params);
     const hipGraphNode_t *dependencies = index == 0 ? nullptr : &t->nodes[index - 1];
@@ -678,8 +747,11 @@ int xp_replay(xp_lane_t lane, int instance_index, int layer_ordinal, int64_t row
   binding.workspace = lane->workspace;
   binding.fault = lane->fault;
   const DenseLaunches launches = make_dense_launches(binding, selected->capacity);
-  const KernelLaunch *chain[3] = {&launches.gather, &launches.gate_up, &launches.down};
-  for (int index = 0; index < 3; ++index) {
+  const KernelLaunch *chain[kMaxStepKernels];
+  if (launches.chain(chain) != selected->node_count) {
+    return fail(XP_ERROR_STATE, "replay kernel sequence differs from the captured template");
+  }
+  for (int index = 0; index < selected->node_count; ++index) {
     void *params[1];
     hipKernelNodeParams node = node_params(*chain[index], params);
     XP_HIP_CHECK(hipGraphExecKernelNodeSetParams(selected->exec, selected->nodes[index], &node));

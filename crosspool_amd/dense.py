@@ -28,6 +28,31 @@ def _ptr(tensor: torch.Tensor | None) -> ctypes.c_void_p | None:
     return None if tensor is None else ctypes.c_void_p(tensor.data_ptr())
 
 
+_scratch: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def _projection_scratch(
+    device: torch.device, stream: torch.cuda.Stream | None, rows: int, n: int, k: int, gated: bool
+) -> tuple[ctypes.c_void_p | None, int]:
+    """Scratch for the K-slice partial sums of a kernel-level projection.
+
+    One buffer per (device, stream), grown on demand: calls ordered on one stream may reuse
+    it (its contents do not matter on entry); calls on different streams may overlap, so
+    they get separate buffers.
+    """
+
+    needed = _native.gemm_workspace_bytes(rows, n, k, gated)
+    if needed == 0:
+        return None, 0
+    stream = stream if stream is not None else torch.cuda.current_stream(device)
+    key = (device.index, stream.cuda_stream)
+    scratch = _scratch.get(key)
+    if scratch is None or scratch.numel() < needed:
+        scratch = torch.empty(needed, dtype=torch.uint8, device=device)
+        _scratch[key] = scratch
+    return ctypes.c_void_p(scratch.data_ptr()), scratch.numel()
+
+
 def _require(tensor: torch.Tensor, name: str, dtype: torch.dtype, ndim: int) -> None:
     if tensor.device.type != "cuda":
         raise ValueError(f"{name} must be GPU-resident")
@@ -62,9 +87,11 @@ def gate_up_silu(
     if tuple(out.shape) != (rows, intermediate):
         raise ValueError("out must be [rows, I]")
     alpha, limit, up_offset = activation_arguments(activation, gate)
+    scratch, scratch_bytes = _projection_scratch(x.device, stream, rows, 2 * intermediate, hidden, True)
     _native.call(
         "xp_gemm_gate_up_silu",
-        _ptr(x), rows, hidden, _ptr(w_gate_up), intermediate, _ptr(out), alpha, limit, up_offset, _stream(stream),
+        _ptr(x), rows, hidden, _ptr(w_gate_up), intermediate, _ptr(out), alpha, limit, up_offset, scratch,
+        scratch_bytes, _stream(stream),
     )
     return out
 
@@ -96,10 +123,11 @@ def down(
         _require(slots, "slots", torch.int32, 1)
         if slots.numel() < rows:
             raise ValueError("slots must name one destination row per input row")
+    scratch, scratch_bytes = _projection_scratch(activated.device, stream, rows, hidden, intermediate, False)
     _native.call(
         "xp_gemm_down",
-        _ptr(activated), rows, intermediate, _ptr(w_down), hidden, _ptr(out), _ptr(slots), out.shape[0],
-        _stream(stream),
+        _ptr(activated), rows, intermediate, _ptr(w_down), hidden, _ptr(out), _ptr(slots), out.shape[0], scratch,
+        scratch_bytes, _stream(stream),
     )
     return out
 
@@ -110,11 +138,15 @@ class DenseExecutionPlan:
 
     Regions: the gathered (normalised) batch ``[capacity, H]`` and the
     activated intermediate ``[capacity, I]``; SiLU*mul is always fused into
-    the gate_up epilogue, so no separate projected buffer exists.
+    the gate_up epilogue, so no separate projected buffer exists.  Capacities
+    served by the sliced stream kernel append the fp32 partial sums of its K
+    slices (``workspace_bytes`` covers them, as GemmPlan's split-K workspace
+    does in operators/linear.py:111-131).
     """
 
     signature: DenseFfnExecutionSignature
     workspace: WorkspaceLayout
+    workspace_bytes: int
 
     @classmethod
     def prepare(cls, signature: DenseFfnExecutionSignature) -> DenseExecutionPlan:
@@ -122,9 +154,9 @@ class DenseExecutionPlan:
         native = _native.dense_workspace_bytes(
             signature.payload_row_capacity, signature.hidden_size, signature.local_intermediate_size
         )
-        if native != layout.nbytes:
-            raise RuntimeError(f"native workspace ({native} B) disagrees with the prepared layout ({layout.nbytes} B)")
-        return cls(signature=signature, workspace=layout)
+        if native < layout.nbytes:
+            raise RuntimeError(f"native workspace ({native} B) is smaller than the prepared layout ({layout.nbytes} B)")
+        return cls(signature=signature, workspace=layout, workspace_bytes=native)
 
 
 class Dense:
@@ -133,6 +165,8 @@ class Dense:
     def __init__(self, plan: DenseExecutionPlan, workspace: torch.Tensor) -> None:
         if workspace.device.type != "cuda":
             raise ValueError("Dense workspace must reside on its execution device")
+        if workspace.numel() < plan.workspace_bytes:
+            raise ValueError("Dense workspace is smaller than the plan's workspace_bytes")
         self.plan = plan
         self.workspace = workspace
         self.batch, self.activated = plan.workspace.views(workspace)

@@ -101,17 +101,27 @@ int xp_scatter(const void *values, int64_t rows, int64_t hidden, const int32_t *
  * (src/xpool/runtime/ffnagent/operators/linear.py:163-257,
  *  operators/activation.py:112-173, operators/simt.py:13-45). */
 int xp_gemm_gate_up_silu(const void *x, int64_t rows, int64_t hidden, const void *w_gate_up, int64_t intermediate,
-                         void *activated, float alpha, float limit, float up_offset, xp_stream_t stream);
+                         void *activated, float alpha, float limit, float up_offset, void *workspace,
+                         size_t workspace_bytes, xp_stream_t stream);
 
 /* out[t, n] = bf16(activated[t] . w_down[n]), w_down [hidden, intermediate].
  * When slots is not NULL, row t is written to out + slots[t] * hidden instead
  * (the scatter fused into the epilogue; out then has out_rows rows).
  * Replaces Gemm.run_into for o_proj (operators/linear.py:163-257, dense.py:86). */
 int xp_gemm_down(const void *activated, int64_t rows, int64_t intermediate, const void *w_down, int64_t hidden,
-                 void *out, const int32_t *slots, int64_t out_rows, xp_stream_t stream);
+                 void *out, const int32_t *slots, int64_t out_rows, void *workspace, size_t workspace_bytes,
+                 xp_stream_t stream);
+
+/* Scratch bytes the two projections above need for `rows` rows, n weight rows and
+ * reduction length k (0 when the chosen kernel keeps the K reduction inside one
+ * workgroup; pass workspace NULL then).  The scratch (16-byte aligned, contents irrelevant
+ * on entry) holds fp32 partial sums of K slices; calls that may overlap in time must not
+ * share one.  Replaces GemmPlan.split_k_workspace_bytes
+ * (src/xpool/runtime/ffnagent/operators/linear.py:111-131). */
+size_t xp_gemm_workspace_bytes(int64_t rows, int64_t n, int64_t k, int gated);
 
 /* Bytes of Lane workspace one Dense step at `capacity` rows needs
- * (gathered batch + activated intermediate).  Replaces DenseExecutionPlan's
+ * (gathered batch + activated intermediate + K-slice partial sums).  Replaces DenseExecutionPlan's
  * WorkspaceLayout (src/xpool/runtime/ffnagent/operators/dense.py:24-52). */
 size_t xp_dense_workspace_bytes(int64_t capacity, int64_t hidden, int64_t intermediate);
 
@@ -123,7 +133,7 @@ int xp_dense_step(const void *pool_in, void *pool_out, int64_t pool_rows, const 
                   const void *norm_weight, float eps, void *workspace, size_t workspace_bytes, uint32_t *fault_word,
                   xp_stream_t stream);
 
-/* Name of the kernel variant chosen for a projection ("skinny_..." / "tile_...").
+/* Name of the kernel variant chosen for a projection ("split_..." / "stream_..." / "tile_...").
  * Returns the full name length. */
 size_t xp_gemm_variant(int64_t capacity, int64_t n, int64_t k, int gated, char *buffer, size_t size);
 

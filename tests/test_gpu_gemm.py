@@ -1,4 +1,4 @@
-"""GPU parity of the MFMA projections (skinny and tile kernels).
+"""GPU parity of the MFMA projections (split and tile kernels).
 
 Bar (tests/parity.py): every projection lies in the bf16 interval that fp32
 accumulation of the exact fp64 sum can round to, every activation lies between
@@ -121,6 +121,32 @@ def test_zero_weights_give_zero_output(device):
     assert torch.equal(out.float().cpu(), torch.zeros((100, 1024)))
 
 
-def test_variant_selection_covers_both_families(device):
-    assert _native.gemm_variant(1, 24576, 4096, True).startswith("skinny")
+def test_variant_selection_covers_every_family(device):
+    assert _native.gemm_variant(1, 24576, 4096, True).startswith("split")
+    assert _native.gemm_variant(48, 24576, 4096, True).startswith("stream")
     assert _native.gemm_variant(2048, 24576, 4096, True).startswith("tile")
+
+
+# Ragged geometries of the decode kernels: K not a multiple of their 512-column load
+# groups (a partial last K range), N not a multiple of 16 (weight rows past N), one to
+# many K ranges; few rows take the split kernel (gate_up <= 4, down <= 8), up to 64 the
+# stream kernel.
+DECODE_SHAPES = [(1032, 1000), (2056, 9992), (4096, 12288), (264, 40)]
+
+
+@pytest.mark.parametrize("hidden,intermediate", DECODE_SHAPES)
+@pytest.mark.parametrize("rows", [1, 3, 4, 5, 8, 9, 16, 17, 32, 33, 64])
+def test_decode_projections_on_ragged_geometry(device, hidden, intermediate, rows):
+    x = o.generate_hidden_states(rows, hidden, 17)
+    w_gate_up, w_down = _layer(hidden, intermediate)
+    gu_d, dn_d = to_device(w_gate_up, device), to_device(w_down, device)
+    assert _native.gemm_variant(rows, 2 * intermediate, hidden, True).startswith("split" if rows <= 4 else "stream")
+    assert _native.gemm_variant(rows, hidden, intermediate, False).startswith("split" if rows <= 8 else "stream")
+    activated = dense.gate_up_silu(to_device(x, device), gu_d)
+    out = dense.down(activated, dn_d)
+    # A second call gives the identical bits (fixed-order K reduction).
+    again = dense.down(dense.gate_up_silu(to_device(x, device), gu_d), dn_d)
+    torch.cuda.synchronize()
+    assert_activated_within_bounds(activated, x, w_gate_up)
+    assert_projection_within_bounds(out, activated.cpu(), w_down)
+    assert_bitwise_equal(again.cpu(), out.cpu())

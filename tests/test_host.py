@@ -102,9 +102,17 @@ def test_workspace_layout_matches_reference_known_answers():
 
 
 @pytest.mark.parametrize("capacity,hidden,intermediate", [(1, 1024, 3072), (4096, 4096, 12288), (8, 5120, 3200), (3, 8, 8)])
-def test_native_workspace_equals_signature_layout(capacity, hidden, intermediate):
+def test_native_workspace_covers_signature_layout(capacity, hidden, intermediate):
     signature = DenseFfnExecutionSignature(torch.bfloat16, capacity, hidden, intermediate)
-    assert _native.dense_workspace_bytes(capacity, hidden, intermediate) == signature.workspace_layout().nbytes
+    native = _native.dense_workspace_bytes(capacity, hidden, intermediate)
+    layout = signature.workspace_layout().nbytes
+    gate_up = _native.gemm_workspace_bytes(capacity, 2 * intermediate, hidden, True)
+    down = _native.gemm_workspace_bytes(capacity, hidden, intermediate, False)
+    if gate_up + down == 0:
+        assert native == layout
+    else:
+        # the sliced stream kernel's partial sums follow the two regions, 256-byte aligned
+        assert layout + gate_up + down <= native < layout + gate_up + down + 256
 
 
 def test_signature_validation():
@@ -164,7 +172,10 @@ def test_abi_rejects_invalid_arguments_before_touching_the_device():
     assert lib.xp_gather_rmsnorm(None, 0, 8, None, 0, None, 1e-6, None, None, None) == _native.XP_OK
     assert lib.xp_copy_bytes(None, None, 0, None) == _native.XP_OK
     # SiLU alpha must be positive
-    assert lib.xp_gemm_gate_up_silu(p(16), 1, 16, p(16), 8, p(16), 0.0, 0.0, 0.0, None) == _native.XP_ERROR_INVALID_ARGUMENT
+    assert lib.xp_gemm_gate_up_silu(p(16), 1, 16, p(16), 8, p(16), 0.0, 0.0, 0.0, None, 0, None) == _native.XP_ERROR_INVALID_ARGUMENT
+    # a sliced projection without its scratch
+    assert lib.xp_gemm_down(p(16), 32, 12288, p(16), 4096, p(16), None, 32, None, 0, None) == _native.XP_ERROR_CAPACITY
+    assert "xp_gemm_workspace_bytes" in _native.last_error()
     # null handles
     assert lib.xp_layer_register(None, 0, 0, 16, 8, p(16), p(16), None, 1e-6) == _native.XP_ERROR_INVALID_ARGUMENT
     assert lib.xp_replay(None, 0, 0, 1, p(16), p(16), 1, p(16), None) == _native.XP_ERROR_INVALID_ARGUMENT
@@ -175,8 +186,14 @@ def test_abi_rejects_invalid_arguments_before_touching_the_device():
 
 
 def test_gemm_variant_selection():
-    assert _native.gemm_variant(1, 24576, 4096, True).startswith("skinny_gated_t16")
-    assert _native.gemm_variant(64, 4096, 12288, False).startswith("skinny_t64")
+    assert _native.gemm_variant(1, 24576, 4096, True) == "split_gated_t16_k1"
+    assert _native.gemm_variant(8, 4096, 12288, False) == "split_t16_k8"
+    assert _native.gemm_variant(8, 24576, 4096, True) == "stream_gated_t16"
+    assert _native.gemm_variant(16, 24576, 4096, True) == "stream_gated_t16"
+    assert _native.gemm_variant(32, 4096, 12288, False) == "stream_t32"
+    assert _native.gemm_variant(64, 4096, 12288, False) == "stream_t64"
+    assert _native.gemm_workspace_bytes(1, 24576, 4096, True) == 0
+    assert _native.gemm_workspace_bytes(32, 4096, 12288, False) > 0
     assert _native.gemm_variant(2048, 24576, 4096, True).startswith("tile_gated")
     assert _native.gemm_variant(4096, 4096, 12288, False).startswith("tile")
 
