@@ -10,6 +10,11 @@ MFMA-bound north-star point), a ``decode`` entry at T = 32 (HBM-bound), the
 batch sweep of BASELINE config 3, the roofline of the dominant kernel
 (measured with HIP events on the Lane stream it runs on) and the CPU
 baseline (the oracle's torch-CPU restatement on the host cores).
+
+``--kernels-only`` instead launches just the kernels whose hardware counters
+the roofline's ``traffic`` figure comes from (a byte copy of known size for
+calibration, then gate_up at the headline and decode sizes), for
+``rocprofv3 --pmc`` runs; ``profiles/traffic.json`` records their result.
 """
 
 from __future__ import annotations
@@ -30,6 +35,11 @@ POOL_SLOTS = 8192
 SWEEP = (1, 4, 16, 32, 64, 256, 1024, 2048, 4096)
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+# Copies of the gate_up weights the decode roofline rotates through (3 x 201 MB exceeds
+# the 256 MB last-level cache, so every launch streams its weights from HBM).
+DECODE_WEIGHT_SETS = 3
+CALIBRATION_COPY_BYTES = 256 << 20
+TRAFFIC_FILE = REPO_ROOT / "profiles" / "traffic.json"
 
 
 def parse_args() -> argparse.Namespace:
@@ -43,7 +53,21 @@ def parse_args() -> argparse.Namespace:
     parser.add_argument("--no-sweep", action="store_true")
     parser.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample length")
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--kernels-only", action="store_true", help="launch only the profiled kernels, then exit")
     return parser.parse_args()
+
+
+def measured_traffic(variant: str, tokens: int) -> float | None:
+    """HBM bytes per launch of `variant` at `tokens` from the committed counter summary."""
+
+    try:
+        entries = json.loads(TRAFFIC_FILE.read_text())["kernels"]
+    except (OSError, ValueError, KeyError):
+        return None
+    for entry in entries:
+        if entry.get("kernel") == variant and entry.get("tokens") == tokens:
+            return float(entry["bytes_per_launch"])
+    return None
 
 
 def layer_flops(tokens: int) -> float:
@@ -112,41 +136,70 @@ def main() -> int:
         torch.cuda.synchronize()
         return (time.perf_counter() - start) / steps
 
-    # ---------------------------------------------------------------- headline
     tokens = args.tokens
-    seconds = time_replays(tokens, args.steps, args.warmup)
-    agent.check_health()
 
     # ---------------------------------------------------------------- dominant kernel (events)
-    def kernel_roofline(tokens: int, steps: int) -> dict:
+    decode_weight_sets = [weights.i_proj.values] + [
+        weights.i_proj.values.clone() for _ in range(DECODE_WEIGHT_SETS - 1)
+    ]
+
+    def gate_up_launches(tokens: int, steps: int) -> float:
+        """Average seconds per gate_up launch (its reduction launch included when it has
+        one), timed with HIP events on the Lane stream.  HBM-bound sizes rotate through
+        weight copies larger than the last-level cache together."""
+
         x = torch.empty((tokens, HIDDEN), dtype=torch.bfloat16, device=device)
         dense.gather_rmsnorm(pool, slots[:tokens], norm_weight=norm, out=x, stream=lane.stream)
         h = torch.empty((tokens, INTERMEDIATE), dtype=torch.bfloat16, device=device)
-        for _ in range(3):
-            dense.gate_up_silu(x, weights.i_proj.values, out=h, stream=lane.stream)
+        sets = [weights.i_proj.values] if tokens > 64 else decode_weight_sets
+        for index in range(3):
+            dense.gate_up_silu(x, sets[index % len(sets)], out=h, stream=lane.stream)
         begin = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
         begin.record(lane.stream)
-        for _ in range(steps):
-            dense.gate_up_silu(x, weights.i_proj.values, out=h, stream=lane.stream)
+        for index in range(steps):
+            dense.gate_up_silu(x, sets[index % len(sets)], out=h, stream=lane.stream)
         end.record(lane.stream)
         end.synchronize()
-        per_launch = begin.elapsed_time(end) / 1e3 / steps
+        return begin.elapsed_time(end) / 1e3 / steps
+
+    def kernel_roofline(tokens: int, steps: int) -> dict:
+        per_launch = gate_up_launches(tokens, steps)
         variant = _native.gemm_variant(tokens, 2 * INTERMEDIATE, HIDDEN, True)
+        traffic = measured_traffic(variant, tokens)
         if variant.startswith("tile"):
             achieved = gate_up_flops(tokens) / per_launch / 1e12
             return {
                 "kernel": variant, "tokens": tokens, "bound": "mfma", "achieved": round(achieved, 1),
                 "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
-                "traffic": None, "avg_launch_us": round(per_launch * 1e6, 2),
+                "traffic": traffic, "avg_launch_us": round(per_launch * 1e6, 2),
+                "algorithmic_flops": gate_up_flops(tokens),
             }
         achieved = gate_up_bytes(tokens) / per_launch / 1e9
         return {
             "kernel": variant, "tokens": tokens, "bound": "hbm", "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None, "avg_launch_us": round(per_launch * 1e6, 2),
+            "traffic": traffic, "avg_launch_us": round(per_launch * 1e6, 2),
+            "algorithmic_bytes": gate_up_bytes(tokens),
         }
 
+    if args.kernels_only:
+        # Calibration copy of known size, then the roofline kernels, a few launches each.
+        source = torch.empty(CALIBRATION_COPY_BYTES, dtype=torch.uint8, device=device)
+        target = torch.empty_like(source)
+        for _ in range(5):
+            dense.copy_bytes(target, source, stream=lane.stream)
+        for t in (tokens, args.decode_tokens):
+            gate_up_launches(t, 6)
+        torch.cuda.synchronize()
+        agent.close()
+        print(json.dumps({"kernels_only": True, "copy_bytes": CALIBRATION_COPY_BYTES,
+                          "gate_up_tokens": [tokens, args.decode_tokens]}), flush=True)
+        return 0
+
+    # ---------------------------------------------------------------- headline
+    seconds = time_replays(tokens, args.steps, args.warmup)
+    agent.check_health()
     roofline = kernel_roofline(tokens, max(20, min(args.steps, 200)))
 
     # ---------------------------------------------------------------- decode point
@@ -212,7 +265,7 @@ def main() -> int:
         }
 
     result = {
-        "metric": "FFN-layer tokens/sec at Qwen3-8B shape",
+        "metric": "FFN-layer tokens/sec at Qwen3-8B shape; % HBM BW (decode) / % MFMA peak (prefill)",
         "value": round(tokens / seconds, 1),
         "unit": "tokens/s",
         "n_gpus": 1,
