@@ -431,18 +431,22 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
   constexpr int NT = WTN / 32;
   constexpr int ROWS = BM + BN;                    // LDS rows per stage (A rows then B rows)
   constexpr int STAGE = ROWS * BK;                 // bf16 elements per stage
-  constexpr int LOADS = ROWS / 8 / WAVES;          // 1 KB (8-row) load instructions per wave per stage
+  constexpr int A_LOADS = BM / 8 / WAVES;          // 1 KB (8-row) load instructions per wave per stage
+  constexpr int B_LOADS = BN / 8 / WAVES;
+  constexpr int LOADS = A_LOADS + B_LOADS;
   static_assert(MT >= 1 && NT >= 1, "wave tile must hold at least one 32x32 MFMA tile");
   static_assert(!GATED || NT % 2 == 0, "gated tiles need whole Gate/Up column groups per wave");
-  static_assert(ROWS % (8 * WAVES) == 0, "stage rows must split evenly over the waves");
-  static_assert(BM % 8 == 0, "8-row load groups must not straddle the A/B boundary");
+  static_assert(BM % (8 * WAVES) == 0 && BN % (8 * WAVES) == 0, "stage rows must split evenly over the waves");
 
   __shared__ __attribute__((aligned(1024))) uint16_t lds[2 * STAGE];
 
-  const int tiles_m = static_cast<int>((a.capacity + BM - 1) / BM);
-  const int tile = xcd_major_tile(blockIdx.x, gridDim.x);
-  const int tm = tile % tiles_m;
-  const int tn = tile / tiles_m;
+  // Grid x walks weight tiles, grid y token tiles.  Workgroups go to the 8 XCDs round
+  // robin by linear id, so consecutive weight tiles land on different XCDs and every token
+  // tile of one weight tile runs on the same XCD: each weight tile is fetched into one
+  // L2 only.  Taking the coordinates straight from the block id keeps them (and the
+  // buffer resources built from them) in scalar registers, with no integer division.
+  const int tn = blockIdx.x;
+  const int tm = blockIdx.y;
   const int64_t m0 = static_cast<int64_t>(tm) * BM;
   if (m0 >= a.rows) {
     return;
@@ -456,28 +460,29 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
   const int wm = wave % WAVES_M;
   const int wn = wave / WAVES_M;
 
-  // ---- loads: wave `wave` fills stage rows [wave * 8 * LOADS, +8 * LOADS).  Lane i of a load
-  // writes LDS row r0 + i / 8, physical chunk i % 8, which holds logical k chunk
-  // (i % 8) ^ swizzle(row): the swizzle is applied by choosing the global chunk.
+  // ---- loads: every wave fills A_LOADS 8-row groups of the A tile (rows from
+  // wave * BM / WAVES) and B_LOADS of the B tile, so which resource a load uses is a
+  // compile-time fact.  Lane i of a load writes LDS row r0 + i / 8, physical chunk i % 8,
+  // which holds logical k chunk (i % 8) ^ swizzle(row): the swizzle is applied by choosing
+  // the global chunk.
   const int64_t a_rows_left = a.rows - m0;
   const int64_t b_rows_left = a.n - w0;
   const __amdgpu_buffer_rsrc_t a_rsrc =
       make_rsrc(a.x + m0 * a.ldx, static_cast<uint32_t>((a_rows_left < BM ? a_rows_left : BM) * a.ldx * 2));
   const __amdgpu_buffer_rsrc_t b_rsrc =
       make_rsrc(a.w + w0 * a.k, static_cast<uint32_t>((b_rows_left < BN ? b_rows_left : BN) * a.k * 2));
-  const int first_row = wave * 8 * LOADS;
   const int row_in_load = lane >> 3;
+  const int a_first = wave * (BM / WAVES);
+  const int b_first = BM + wave * (BN / WAVES);
   uint32_t load_offset[LOADS];
-  bool load_is_a[LOADS];
   int load_chunk[LOADS];
 #pragma unroll
   for (int q = 0; q < LOADS; ++q) {
-    const int group_row = first_row + q * 8;  // 8-row groups never straddle the A/B boundary
-    const int row = group_row + row_in_load;
+    const bool is_a = q < A_LOADS;
+    const int row = (is_a ? a_first + q * 8 : b_first + (q - A_LOADS) * 8) + row_in_load;  // LDS row
     const int k_chunk = (lane & 7) ^ swizzle(row);
     load_chunk[q] = k_chunk;
-    load_is_a[q] = group_row < BM;
-    if (load_is_a[q]) {
+    if (is_a) {
       load_offset[q] = static_cast<uint32_t>((row * a.ldx + k_chunk * 8) * 2);
     } else {
       const int p = row - BM;  // LDS row within the B tile
@@ -497,13 +502,19 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
   const bool k_whole = (a.k % BK) == 0;
   auto issue_loads = [&](int64_t kt, int stage) {
     const uint32_t k_bytes = static_cast<uint32_t>(kt * BK * 2);
-    uint16_t *base = lds + stage * STAGE + first_row * BK;
+    uint16_t *base = lds + stage * STAGE;
+    // The scalar offset must stay wave-uniform; masking goes through the per-lane offset
+    // (kOutOfRange + k_bytes is still past the resource end).  A and B loads are separate
+    // loops so that each names one resource (no select between descriptors).
 #pragma unroll
-    for (int q = 0; q < LOADS; ++q) {
+    for (int q = 0; q < A_LOADS; ++q) {
       const bool k_ok = k_whole || (kt * BK + load_chunk[q] * 8 < a.k);
-      // The scalar offset must stay wave-uniform; masking goes through the per-lane offset
-      // (kOutOfRange + k_bytes is still past the resource end).
-      buffer_load_lds16(load_is_a[q] ? a_rsrc : b_rsrc, base + q * 8 * BK, k_ok ? load_offset[q] : kOutOfRange,
+      buffer_load_lds16(a_rsrc, base + (a_first + q * 8) * BK, k_ok ? load_offset[q] : kOutOfRange, k_bytes);
+    }
+#pragma unroll
+    for (int q = A_LOADS; q < LOADS; ++q) {
+      const bool k_ok = k_whole || (kt * BK + load_chunk[q] * 8 < a.k);
+      buffer_load_lds16(b_rsrc, base + (b_first + (q - A_LOADS) * 8) * BK, k_ok ? load_offset[q] : kOutOfRange,
                         k_bytes);
     }
   };
@@ -582,35 +593,47 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
     mfma_step((KSTEPS - 1) & 1);
   }
 
-  // Epilogue: lane holds D[8 (r / 4) + 4 (lane / 32) + r % 4][lane % 32] of each 32x32 tile.
+  // Epilogue.  Lane holds D[8 (r / 4) + 4 (lane / 32) + r % 4][lane % 32] of each 32x32
+  // tile.  Each wave rounds its tile to bf16 (gate_up: after the activation), writes it to
+  // its own region of the now idle stage buffers and reads it back by rows, so results
+  // leave in 16-byte chunks, 128 contiguous bytes per 8 lanes (to the slot rows when the
+  // scatter is fused).  Bounds are checked per chunk on the way out.
+  constexpr int OUT_N = GATED ? WTN / 2 : WTN;  // output columns of a wave tile
+  constexpr int CPR = OUT_N / 8;                // 16-byte chunks per output row
+  static_assert(WTM * OUT_N * WAVES <= 2 * STAGE, "epilogue tiles must fit the stage buffers");
+  static_assert((WTM * CPR) % 64 == 0, "output chunks must split evenly over the lanes");
+  __syncthreads();  // every wave is done reading the stage buffers
+  uint16_t *out_tile = lds + wave * (WTM * OUT_N);
+  // Chunk c of row r sits at physical chunk c ^ ((r / 4) % CPR): the two row groups one
+  // write instruction covers (rows r and r + 4) then fall in different banks.
+  auto slot_of = [](int row, int chunk) { return row * OUT_N + ((chunk ^ ((row >> 2) & (CPR - 1))) << 3); };
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int64_t token = m0 + wm * WTM + mt * 32 + 8 * (r >> 2) + 4 * frag_half + (r & 3);
-      if (token >= a.rows) {
-        continue;
-      }
-      uint16_t *row = output_row(a, token);
-      if (row == nullptr) {
-        continue;
-      }
-      if constexpr (GATED) {
+      const int row = mt * 32 + 8 * (r >> 2) + 4 * frag_half + (r & 3);
 #pragma unroll
-        for (int nt = 0; nt < NT / 2; ++nt) {
-          const int64_t j = w0 / 2 + wn * (WTN / 2) + nt * 32 + frag_row;
-          if (2 * j < a.n) {
-            row[j] = static_cast<uint16_t>(float_to_bf16(gated_silu(acc[mt][nt][r], acc[mt][nt + NT / 2][r], a.act)));
-          }
-        }
-      } else {
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-          const int64_t n = w0 + wn * WTN + nt * 32 + frag_row;
-          if (n < a.n) {
-            row[n] = static_cast<uint16_t>(float_to_bf16(acc[mt][nt][r]));
-          }
-        }
+      for (int nt = 0; nt < OUT_N / 32; ++nt) {
+        const int col = nt * 32 + frag_row;
+        const float value = GATED ? gated_silu(acc[mt][nt][r], acc[mt][nt + NT / 2][r], a.act) : acc[mt][nt][r];
+        out_tile[slot_of(row, col >> 3) + (col & 7)] = static_cast<uint16_t>(float_to_bf16(value));
+      }
+    }
+  }
+  __syncthreads();
+  const int64_t row0 = m0 + wm * WTM;
+  const int64_t col0 = GATED ? w0 / 2 + wn * (WTN / 2) : w0 + wn * WTN;
+  const int64_t out_cols = GATED ? a.n / 2 : a.n;
+#pragma unroll 4
+  for (int index = lane; index < WTM * CPR; index += 64) {
+    const int row = index / CPR;
+    const int chunk = index % CPR;
+    const int64_t token = row0 + row;
+    const int64_t col = col0 + chunk * 8;
+    if (token < a.rows && col < out_cols) {
+      uint16_t *destination = output_row(a, token);
+      if (destination != nullptr) {
+        store16(destination + col, load16(out_tile + slot_of(row, chunk)));
       }
     }
   }
@@ -792,8 +815,8 @@ GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmCho
   } else {
     const TileShape &shape = kTileShapes[choice.variant];
     kernel.func = gated ? tile_kernel<true>(choice.variant) : tile_kernel<false>(choice.variant);
-    const int64_t tiles = ((capacity + shape.bm - 1) / shape.bm) * ((args.n + shape.bn - 1) / shape.bn);
-    kernel.grid = dim3(static_cast<unsigned>(tiles), 1, 1);
+    kernel.grid = dim3(static_cast<unsigned>((args.n + shape.bn - 1) / shape.bn),
+                       static_cast<unsigned>((capacity + shape.bm - 1) / shape.bm), 1);
     kernel.block = dim3(static_cast<unsigned>(64 * shape.waves), 1, 1);
   }
   kernel.set_args(record);

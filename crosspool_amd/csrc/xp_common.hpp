@@ -23,13 +23,9 @@ constexpr uint32_t kFaultSlotOutOfRange = 1u;
 __device__ __forceinline__ float bf16_to_float(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
 
 // Round-to-nearest-even fp32 -> bf16; NaN stays a quiet NaN of the same sign.
+// Round to nearest even on the gfx950 converter (v_cvt_pk_bf16_f32); NaNs stay NaN.
 __device__ __forceinline__ uint32_t float_to_bf16(float value) {
-  uint32_t bits = __float_as_uint(value);
-  if ((bits & 0x7fffffffu) > 0x7f800000u) {
-    return (bits >> 16) | 0x0040u;
-  }
-  bits += 0x7fffu + ((bits >> 16) & 1u);
-  return bits >> 16;
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(value));
 }
 
 // Round through bf16 and back: the payload-dtype rounding point of the
@@ -37,7 +33,9 @@ __device__ __forceinline__ uint32_t float_to_bf16(float value) {
 __device__ __forceinline__ float round_bf16(float value) { return bf16_to_float(float_to_bf16(value)); }
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return float_to_bf16(lo) | (float_to_bf16(hi) << 16);
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{lo, hi}), bf16x2_t));
 }
 
 // Gated activation parameters: silu(min(g, limit)) * (clamp(u, -limit, limit) + up_offset),
@@ -56,7 +54,9 @@ __device__ __forceinline__ float gated_silu(float gate, float up, const GatedSil
     g = fminf(g, act.limit);
     u = fminf(fmaxf(u, -act.limit), act.limit);
   }
-  return g / (1.0f + __expf(-act.alpha * g)) * (u + act.up_offset);
+  // silu(g) = g / (1 + exp(-alpha g)) with the reciprocal instruction (1 ulp) instead of an
+  // IEEE divide; exp overflow gives 1 / inf = 0, the limit of the quotient.
+  return g * __builtin_amdgcn_rcpf(1.0f + __expf(-act.alpha * g)) * (u + act.up_offset);
 }
 
 __device__ __forceinline__ u32x4 load16(const void *address) {
@@ -81,18 +81,6 @@ __device__ __forceinline__ void raise_fault(uint32_t *fault, uint32_t bits) {
   if (fault != nullptr) {
     __hip_atomic_fetch_or(fault, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-}
-
-// Map a linear workgroup id so that consecutive logical tiles land on the same
-// XCD.  Workgroups are dispatched round-robin over the 8 XCDs of an MI355X, so
-// workgroup b runs on XCD b % 8; the returned id enumerates tiles XCD-major.
-__device__ __forceinline__ int xcd_major_tile(int block, int blocks) {
-  constexpr int kXcds = 8;
-  const int xcd = block % kXcds;
-  const int index = block / kXcds;
-  const int per = blocks / kXcds;
-  const int extra = blocks % kXcds;
-  return xcd < extra ? xcd * (per + 1) + index : extra * (per + 1) + (xcd - extra) * per + index;
 }
 
 }  // namespace xp

@@ -150,3 +150,28 @@ def test_decode_projections_on_ragged_geometry(device, hidden, intermediate, row
     assert_activated_within_bounds(activated, x, w_gate_up)
     assert_projection_within_bounds(out, activated.cpu(), w_down)
     assert_bitwise_equal(again.cpu(), out.cpu())
+
+
+@pytest.mark.parametrize("rows", [1, 16, 128])
+def test_projection_rounds_to_nearest_even(device, rows):
+    # Every output is a + b * c with a, b, c chosen so the fp32 sum is exact and often lands
+    # exactly halfway between two bf16 values: the stored bits must be the round-to-nearest-
+    # even of that sum (what torch's float -> bf16 conversion produces), for the split, stream
+    # and tile kernels alike.
+    hidden, intermediate = 64, 64
+    generator = torch.Generator().manual_seed(7)
+    mantissa = torch.randint(0, 128, (rows,), generator=generator).double()
+    a = (1.0 + mantissa / 128) * torch.where(torch.rand(rows, generator=generator) < 0.5, -1.0, 1.0)
+    b = torch.tensor([2.0**-9, -(2.0**-9), 3 * 2.0**-10, 2.0**-10, 2.0**-20, 0.0, 5 * 2.0**-10, -(2.0**-8)])
+    b = b[torch.arange(rows) % len(b)]
+    h = torch.zeros((rows, intermediate), dtype=torch.float64)
+    h[:, 0], h[:, 1] = a, b
+    c = torch.tensor([2.0 ** (-(n % 4)) * (-1 if n % 3 == 0 else 1) for n in range(hidden)], dtype=torch.float64)
+    w = torch.zeros((hidden, intermediate), dtype=torch.float64)
+    w[:, 0], w[:, 1] = 1.0, c
+    h_bf, w_bf = h.to(torch.bfloat16), w.to(torch.bfloat16)
+    assert torch.equal(h_bf.double(), h) and torch.equal(w_bf.double(), w)
+    expected = (h @ w.t()).float().to(torch.bfloat16)  # exact in fp32, one rounding
+    out = dense.down(to_device(h_bf, device), to_device(w_bf, device))
+    torch.cuda.synchronize()
+    assert_bitwise_equal(out.cpu(), expected)
