@@ -420,8 +420,10 @@ __device__ __forceinline__ void wait_vmcnt() {
 constexpr uint32_t kOutOfRange = 0x7ffffff0u;
 
 // BM x BN block tile, BK = 64, WAVES_M x WAVES_N waves (two per SIMD at 8 waves) each
-// owning a (BM / WAVES_M) x (BN / WAVES_N) tile of 32x32x16 MFMA accumulators.
-template <int BM, int BN, int WAVES_M, int WAVES_N, bool GATED>
+// owning a (BM / WAVES_M) x (BN / WAVES_N) tile of 32x32x16 MFMA accumulators.  With
+// PINGPONG (8 waves), the two waves sharing a SIMD alternate between a slab of MFMAs and
+// the LDS reads of their next slab, so the matrix pipe and LDS work at the same time.
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool GATED, bool PINGPONG = false>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmArgs a) {
   constexpr int BK = 64;
   constexpr int WAVES = WAVES_M * WAVES_N;
@@ -429,14 +431,17 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
   constexpr int WTN = BN / WAVES_N;
   constexpr int MT = WTM / 32;
   constexpr int NT = WTN / 32;
+  constexpr int KSTEPS_MAX = 4;                    // 16-wide k steps per slab (BK / 16)
   constexpr int ROWS = BM + BN;                    // LDS rows per stage (A rows then B rows)
   constexpr int STAGE = ROWS * BK;                 // bf16 elements per stage
-  constexpr int A_LOADS = BM / 8 / WAVES;          // 1 KB (8-row) load instructions per wave per stage
-  constexpr int B_LOADS = BN / 8 / WAVES;
+  constexpr int LOAD_WAVES = PINGPONG ? WAVES / 2 : WAVES;  // waves that fill the stages
+  constexpr int A_LOADS = BM / 8 / LOAD_WAVES;     // 1 KB (8-row) load instructions per loading wave per stage
+  constexpr int B_LOADS = BN / 8 / LOAD_WAVES;
   constexpr int LOADS = A_LOADS + B_LOADS;
   static_assert(MT >= 1 && NT >= 1, "wave tile must hold at least one 32x32 MFMA tile");
   static_assert(!GATED || NT % 2 == 0, "gated tiles need whole Gate/Up column groups per wave");
-  static_assert(BM % (8 * WAVES) == 0 && BN % (8 * WAVES) == 0, "stage rows must split evenly over the waves");
+  static_assert(BM % (8 * LOAD_WAVES) == 0 && BN % (8 * LOAD_WAVES) == 0, "stage rows must split evenly");
+  static_assert(!PINGPONG || WAVES == 8, "ping-pong pairs the two waves of each SIMD");
 
   __shared__ __attribute__((aligned(1024))) uint16_t lds[2 * STAGE];
 
@@ -471,51 +476,49 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
       make_rsrc(a.x + m0 * a.ldx, static_cast<uint32_t>((a_rows_left < BM ? a_rows_left : BM) * a.ldx * 2));
   const __amdgpu_buffer_rsrc_t b_rsrc =
       make_rsrc(a.w + w0 * a.k, static_cast<uint32_t>((b_rows_left < BN ? b_rows_left : BN) * a.k * 2));
+  // Load q of a wave covers the 8-row group starting at LDS row g (a multiple of 8); lane
+  // i takes row g + i / 8 and k chunk (i % 8) ^ swizzle(row).  Because g is a multiple of
+  // 8, swizzle(g + i / 8) = (i / 16) ^ (4 if g / 8 is odd), so the per-lane part of every
+  // offset takes one of two values and the group part is wave-uniform.
+  const int load_wave = wave % LOAD_WAVES;
+  const int a_first = load_wave * (BM / LOAD_WAVES);
+  const int b_first = BM + load_wave * (BN / LOAD_WAVES);
   const int row_in_load = lane >> 3;
-  const int a_first = wave * (BM / WAVES);
-  const int b_first = BM + wave * (BN / WAVES);
-  uint32_t load_offset[LOADS];
-  int load_chunk[LOADS];
-#pragma unroll
-  for (int q = 0; q < LOADS; ++q) {
-    const bool is_a = q < A_LOADS;
-    const int row = (is_a ? a_first + q * 8 : b_first + (q - A_LOADS) * 8) + row_in_load;  // LDS row
-    const int k_chunk = (lane & 7) ^ swizzle(row);
-    load_chunk[q] = k_chunk;
-    if (is_a) {
-      load_offset[q] = static_cast<uint32_t>((row * a.ldx + k_chunk * 8) * 2);
+  const int lane_chunk[2] = {(lane & 7) ^ (row_in_load >> 1), (lane & 7) ^ (row_in_load >> 1) ^ 4};
+  // B rows of a gated tile are permuted: LDS row p = wq * G + s * G / 2 + jj (G = BN /
+  // WAVES_N) holds weight row 2 (wq * G / 2 + jj) + s, i.e. within an 8-row group the weight
+  // row is the group's first weight row plus 2 (i / 8).
+  constexpr int B_ROW_STEP = GATED ? 2 : 1;
+  auto b_group_row = [](int p) {
+    if constexpr (GATED) {
+      constexpr int group = BN / WAVES_N;
+      return 2 * ((p / group) * (group / 2) + p % (group / 2)) + (p % group) / (group / 2);
     } else {
-      const int p = row - BM;  // LDS row within the B tile
-      int rr = p;              // weight row within the tile
-      if constexpr (GATED) {
-        // LDS row p = wq * (BN / WAVES_N) + s * (BN / WAVES_N / 2) + jj holds Gate (s = 0) or Up
-        // (s = 1) of j = wq * (BN / WAVES_N / 2) + jj, i.e. weight row 2 j + s.
-        constexpr int group = BN / WAVES_N;
-        const int wq = p / group;
-        const int s = (p % group) / (group / 2);
-        const int jj = p % (group / 2);
-        rr = 2 * (wq * (group / 2) + jj) + s;
-      }
-      load_offset[q] = static_cast<uint32_t>((rr * a.k + k_chunk * 8) * 2);
+      return p;
     }
-  }
-  const bool k_whole = (a.k % BK) == 0;
+  };
   auto issue_loads = [&](int64_t kt, int stage) {
     const uint32_t k_bytes = static_cast<uint32_t>(kt * BK * 2);
+    // 16-byte chunks of this slab that lie inside K (8 except in a ragged last slab).
+    const int chunks_left = static_cast<int>((a.k - kt * BK) >> 3);
     uint16_t *base = lds + stage * STAGE;
     // The scalar offset must stay wave-uniform; masking goes through the per-lane offset
-    // (kOutOfRange + k_bytes is still past the resource end).  A and B loads are separate
-    // loops so that each names one resource (no select between descriptors).
+    // (kOutOfRange + k_bytes is still past the resource end), as a select, not a branch.
+    // A and B loads are separate loops so that each names one resource.
 #pragma unroll
     for (int q = 0; q < A_LOADS; ++q) {
-      const bool k_ok = k_whole || (kt * BK + load_chunk[q] * 8 < a.k);
-      buffer_load_lds16(a_rsrc, base + (a_first + q * 8) * BK, k_ok ? load_offset[q] : kOutOfRange, k_bytes);
+      const int g = a_first + q * 8;
+      const int chunk = lane_chunk[(g >> 3) & 1];
+      const uint32_t offset = static_cast<uint32_t>(((g + row_in_load) * a.ldx + chunk * 8) * 2);
+      buffer_load_lds16(a_rsrc, base + g * BK, chunk < chunks_left ? offset : kOutOfRange, k_bytes);
     }
 #pragma unroll
-    for (int q = A_LOADS; q < LOADS; ++q) {
-      const bool k_ok = k_whole || (kt * BK + load_chunk[q] * 8 < a.k);
-      buffer_load_lds16(b_rsrc, base + (b_first + (q - A_LOADS) * 8) * BK, k_ok ? load_offset[q] : kOutOfRange,
-                        k_bytes);
+    for (int q = 0; q < B_LOADS; ++q) {
+      const int g = b_first + q * 8;
+      const int chunk = lane_chunk[(g >> 3) & 1];
+      const int weight_row = b_group_row(g - BM) + B_ROW_STEP * row_in_load;
+      const uint32_t offset = static_cast<uint32_t>((weight_row * a.k + chunk * 8) * 2);
+      buffer_load_lds16(b_rsrc, base + g * BK, chunk < chunks_left ? offset : kOutOfRange, k_bytes);
     }
   };
 
@@ -531,23 +534,34 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
     }
   }
 
+  // Fragment rows are frag_row plus multiples of 16 (wave and tile offsets), which leave
+  // swizzle(row) unchanged, so one per-lane term per k step addresses every fragment.
+  static_assert(WTM % 16 == 0 && WTN % 16 == 0, "fragment row offsets must keep the swizzle");
   const int frag_row = lane & 31;
   const int frag_half = lane >> 5;
+  int frag_lane[KSTEPS_MAX];
+#pragma unroll
+  for (int ks = 0; ks < KSTEPS_MAX; ++ks) {
+    frag_lane[ks] = frag_row * BK + (((ks * 2 + frag_half) ^ swizzle(frag_row)) << 3);
+  }
+  const int a_frag_base = wm * WTM * BK;
+  const int b_frag_base = BM * BK + wn * WTN * BK;
+  auto frag_a = [&](int stage, int ks, int mt) {
+    return as_bf16x8(load16(lds + stage * STAGE + a_frag_base + mt * 32 * BK + frag_lane[ks]));
+  };
+  auto frag_b = [&](int stage, int ks, int nt) {
+    return as_bf16x8(load16(lds + stage * STAGE + b_frag_base + nt * 32 * BK + frag_lane[ks]));
+  };
   bf16x8 af[2][MT];
   bf16x8 bfrag[2][NT];
   auto read_fragments = [&](int stage, int ks, int slot) {
-    const uint16_t *as = lds + stage * STAGE;
-    const uint16_t *bs = as + BM * BK;
-    const int chunk = ks * 2 + frag_half;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      const int row = wm * WTM + mt * 32 + frag_row;
-      af[slot][mt] = as_bf16x8(load16(as + row * BK + ((chunk ^ swizzle(row)) << 3)));
+      af[slot][mt] = frag_a(stage, ks, mt);
     }
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      const int row = wn * WTN + nt * 32 + frag_row;
-      bfrag[slot][nt] = as_bf16x8(load16(bs + row * BK + ((chunk ^ swizzle(row)) << 3)));
+      bfrag[slot][nt] = frag_b(stage, ks, nt);
     }
   };
   auto mfma_step = [&](int slot) {
@@ -560,37 +574,133 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
     }
   };
 
-  // Prologue: tiles 0 and 1 in flight, wait for tile 0, read its first fragments.
   const int64_t ktiles = (a.k + BK - 1) / BK;
-  issue_loads(0, 0);
-  if (ktiles > 1) {
-    issue_loads(1, 1);
-    wait_vmcnt<LOADS>();  // tile 0 landed; tile 1 may still be in flight
-  }
-  __syncthreads();
-  read_fragments(0, 0, 0);
-
   constexpr int KSTEPS = BK / 16;
-  for (int64_t kt = 0; kt < ktiles; ++kt) {
-    const int stage = static_cast<int>(kt & 1);
+  if constexpr (PINGPONG) {
+    // Waves w and w + 4 run on SIMD w % 4.  Barriers split time into phases of half a slab
+    // (two k steps).  In phase 2u the first group (waves 0-3) multiplies half slab u from
+    // registers while the second group reads half slab u's fragments; in phase 2u + 1 the
+    // roles swap, the first group reading half slab u + 1 and, after the second group's last
+    // read of slab s, refilling that stage with slab s + 2.  Only the first group loads from
+    // memory, so its waits cover every write of a stage before the barrier publishing it.
+    constexpr int HALF = KSTEPS / 2;
+    const bool first_group = wave < WAVES / 2;
+    bf16x8 fa[HALF][MT];
+    bf16x8 fb[HALF][NT];
+    auto read_half = [&](int64_t u) {
+      const int stage = static_cast<int>((u >> 1) & 1);
+      const int first = static_cast<int>(u & 1) * HALF;
 #pragma unroll
-    for (int ks = 0; ks + 1 < KSTEPS; ++ks) {
-      read_fragments(stage, ks + 1, (ks + 1) & 1);
-      mfma_step(ks & 1);
+      for (int h = 0; h < HALF; ++h) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          fa[h][mt] = first == 0 ? frag_a(stage, h, mt) : frag_a(stage, HALF + h, mt);
+        }
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          fb[h][nt] = first == 0 ? frag_b(stage, h, nt) : frag_b(stage, HALF + h, nt);
+        }
+      }
+    };
+    auto mfma_half = [&]() {
+#pragma unroll
+      for (int h = 0; h < HALF; ++h) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) {
+            acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[h][mt], fb[h][nt], acc[mt][nt], 0, 0, 0);
+          }
+        }
+      }
+    };
+    // A bare s_barrier: unlike __syncthreads it does not wait for the loads in flight.  The
+    // memory clobber keeps the compiler from moving LDS accesses across it and the
+    // scheduling barriers keep the MFMAs of a phase inside it.
+    auto barrier = [] {
+      __builtin_amdgcn_sched_barrier(0);
+      __asm__ volatile("s_barrier" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    auto wait_lds = [] { __builtin_amdgcn_s_waitcnt(0xc07f); };  // lgkmcnt(0)
+
+    // The two groups run separate loops with the same barrier count per half slab.
+    const int64_t halves = 2 * ktiles;
+    if (first_group) {
+      issue_loads(0, 0);
+      if (ktiles > 1) {
+        issue_loads(1, 1);
+        wait_vmcnt<LOADS>();  // slab 0 landed; slab 1 may still be in flight
+      } else {
+        wait_vmcnt<0>();
+      }
+      barrier();
+      read_half(0);
+      for (int64_t u = 0; u < halves; ++u) {
+        const int64_t s = u >> 1;
+        const bool second_half = (u & 1) != 0;
+        mfma_half();
+        if (second_half) {
+          wait_vmcnt<0>();  // slab s + 1 landed (issued during slab s - 1)
+        }
+        barrier();
+        if (second_half && s + 2 < ktiles) {
+          issue_loads(s + 2, static_cast<int>(s & 1));
+        }
+        if (u + 1 < halves) {
+          read_half(u + 1);
+        }
+        barrier();
+      }
+    } else {
+      barrier();
+      for (int64_t u = 0; u < halves; ++u) {
+        read_half(u);
+        wait_lds();  // done reading before the stage may be refilled
+        barrier();
+        mfma_half();
+        barrier();
+      }
     }
-    if (kt + 1 < ktiles) {
-      // The last k step's fragments are being read and tile kt+1 (our loads) is landing.
-      // Once both are done everywhere (barrier), nobody reads this stage any more: refill
-      // it with tile kt+2 and start on tile kt+1's fragments while the last k step's
-      // MFMAs run.
+  } else {
+    // Prologue: tiles 0 and 1 in flight, wait for tile 0, read its first fragments.
+    issue_loads(0, 0);
+    issue_loads(1, 1);    // a K of one tile makes these loads all out of range (zeros)
+    wait_vmcnt<LOADS>();  // tile 0 landed; tile 1 may still be in flight
+    __syncthreads();
+    read_fragments(0, 0, 0);
+
+    auto inner_steps = [&](int stage) {
+#pragma unroll
+      for (int ks = 0; ks + 1 < KSTEPS; ++ks) {
+        read_fragments(stage, ks + 1, (ks + 1) & 1);
+        mfma_step(ks & 1);
+      }
+    };
+    for (int64_t kt = 0; kt + 1 < ktiles; ++kt) {
+      const int stage = static_cast<int>(kt & 1);
+      inner_steps(stage);
+      // Tile kt+1 (our loads) has landed once the counters drain; after the barrier nobody
+      // reads this stage any more.  The last k step's MFMAs then run interleaved with the
+      // reads of tile kt+1's first fragments and the refill of this stage with tile kt+2
+      // (out of range, so zeros, past the last tile), keeping the matrix pipe busy while
+      // the loads issue.
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
-      if (kt + 2 < ktiles) {
-        issue_loads(kt + 2, stage);
-      }
       read_fragments(stage ^ 1, 0, 0);
+      issue_loads(kt + 2, stage);
+      mfma_step((KSTEPS - 1) & 1);
+#pragma unroll
+      for (int i = 0; i < MT * NT; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one memory load
+      }
     }
+    inner_steps(static_cast<int>((ktiles - 1) & 1));
     mfma_step((KSTEPS - 1) & 1);
+    // Past-the-end refills may still be landing in the stage buffers the epilogue reuses.
+    __builtin_amdgcn_s_waitcnt(0);
   }
 
   // Epilogue.  Lane holds D[8 (r / 4) + 4 (lane / 32) + r % 4][lane % 32] of each 32x32
