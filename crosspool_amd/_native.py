@@ -52,6 +52,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "xp_lane_check_health": (_INT, [_P, ctypes.POINTER(ctypes.c_uint32)]),
     "xp_lane_clear_fault": (_INT, [_P]),
     "xp_lane_synchronize": (_INT, [_P]),
+    "xp_lane_set_graph_dispatch": (_INT, [_P, _INT]),
     "xp_template_capture": (_INT, [_P, _I64, _I64, _I64]),
     "xp_template_capacities": (_INT, [_P, _I64, _I64, ctypes.POINTER(_I64), _INT, ctypes.POINTER(_INT)]),
     "xp_replay": (_INT, [_P, _INT, _INT, _I64, _P, _P, _I64, _P, _P]),

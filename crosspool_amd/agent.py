@@ -68,7 +68,7 @@ class FfnHealthError(RuntimeError):
 class ExecutorLane:
     """One concurrent execution context: stream, workspace and instantiated templates."""
 
-    def __init__(self, agent: FfnAgent, workspace_bytes: int) -> None:
+    def __init__(self, agent: FfnAgent, workspace_bytes: int, *, graph_dispatch: bool = False) -> None:
         self.agent = agent
         self.workspace = torch.empty(max(workspace_bytes, 16), dtype=torch.uint8, device=agent.device)
         handle = ctypes.c_void_p()
@@ -77,11 +77,15 @@ class ExecutorLane:
             ctypes.byref(handle),
         )
         self.handle = handle
+        # Replays launch the template's kernels directly unless graph dispatch is asked for
+        # (each hipGraphLaunch costs ~13 us of GPU idle time on ROCm; same kernels either way).
+        self.graph_dispatch = bool(graph_dispatch)
+        _native.call("xp_lane_set_graph_dispatch", self.handle, int(self.graph_dispatch))
         stream = ctypes.c_void_p()
         _native.call("xp_lane_stream", self.handle, ctypes.byref(stream))
         self.stream = torch.cuda.ExternalStream(stream.value or 0, device=agent.device)
         self.templates: dict[tuple[int, int, int], GraphTemplate] = {}
-        self._in_flight: deque[tuple[torch.cuda.Event, tuple[torch.Tensor, ...]]] = deque()
+        self._in_flight: deque[tuple[torch.cuda.Event | None, tuple[torch.Tensor, ...], torch.cuda.Stream]] = deque()
 
     def capture(self, template: GraphTemplate) -> None:
         """Instantiate the template's hipGraph on this Lane (idempotent)."""
@@ -160,13 +164,28 @@ class ExecutorLane:
         while this Lane's stream still reads it.
         """
 
-        while self._in_flight and self._in_flight[0][0].query():
+        while self._in_flight and self._in_flight[0][0] is not None and self._in_flight[0][0].query():
             self._in_flight.popleft()
+        if self._in_flight:
+            _, last_tensors, last_stream = self._in_flight[-1]
+            if last_stream == stream and all(a is b for a, b in zip(last_tensors, tensors)):
+                # Same tensors on the same stream as the previous replay (the common
+                # layer-after-layer case): hold them until that stream is drained instead of
+                # recording an event per replay, a marker packet that delays the next kernels.
+                self._in_flight[-1] = (None, tensors, stream)
+                return
         event = torch.cuda.Event()
         event.record(stream)
-        self._in_flight.append((event, tensors))
+        self._in_flight.append((event, tensors, stream))
 
     def _release_retained(self) -> None:
+        """Drop retained tensors once the work that reads them has run."""
+
+        for event, _, stream in self._in_flight:
+            if event is None:
+                stream.synchronize()
+            else:
+                event.synchronize()
         self._in_flight.clear()
 
     def check_health(self) -> int:
@@ -191,12 +210,10 @@ class ExecutorLane:
         """Drain the Lane (its stream is destroyed), then drop retained tensors."""
 
         if self.handle is not None:
-            for event, _ in self._in_flight:
-                event.synchronize()
+            self._release_retained()
             _native.call("xp_lane_destroy", self.handle)
             self.handle = None
             self.templates.clear()
-            self._release_retained()
 
     def _require_open(self) -> None:
         if self.handle is None:
@@ -211,7 +228,9 @@ class FfnAgent:
     their own streams.
     """
 
-    def __init__(self, device: int | torch.device | None = None, *, executor_lane_count: int = 1) -> None:
+    def __init__(
+        self, device: int | torch.device | None = None, *, executor_lane_count: int = 1, graph_dispatch: bool = False
+    ) -> None:
         if executor_lane_count <= 0:
             raise ValueError("an FfnAgent needs at least one Executor Lane")
         if device is None:
@@ -221,6 +240,7 @@ class FfnAgent:
         _native.call("xp_agent_create", self.device.index, ctypes.byref(handle))
         self.handle = handle
         self.executor_lane_count = executor_lane_count
+        self.graph_dispatch = graph_dispatch
         self.layers: dict[tuple[int, int], LayerBinding] = {}
         self.templates: dict[tuple[int, int, int], GraphTemplate] = {}
         self.lanes: list[ExecutorLane] = []
@@ -284,7 +304,7 @@ class FfnAgent:
                 self.templates[template.key] = template
         workspace_bytes = max(t.workspace_bytes for t in self.templates.values())
         for _ in range(self.executor_lane_count):
-            lane = ExecutorLane(self, workspace_bytes)
+            lane = ExecutorLane(self, workspace_bytes, graph_dispatch=self.graph_dispatch)
             self.lanes.append(lane)
             for template in self.templates.values():
                 lane.capture(template)

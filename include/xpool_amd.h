@@ -164,6 +164,12 @@ int xp_lane_stream(xp_lane_t lane, xp_stream_t *out);
 int xp_lane_check_health(xp_lane_t lane, uint32_t *fault_bits);
 int xp_lane_clear_fault(xp_lane_t lane);
 int xp_lane_synchronize(xp_lane_t lane);
+/* Replay dispatch of this Lane: 0 (default) launches a template's kernels directly on the
+ * stream, nonzero launches its instantiated hipGraph (rebinding only the kernel nodes whose
+ * arguments changed).  Both run the same kernels with the same arguments.  No counterpart
+ * in the reference, whose CUDA graphs are always launched (runtime.cu:701-1006); on this
+ * runtime a hipGraphLaunch adds ~13 us of GPU idle time per replay. */
+int xp_lane_set_graph_dispatch(xp_lane_t lane, int use_graph);
 
 /* GraphTemplate: build and instantiate this Lane's hipGraph for the Execution
  * Signature (bf16, capacity, hidden, intermediate).  Idempotent per signature.

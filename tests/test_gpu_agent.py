@@ -1,6 +1,7 @@
 """GPU parity of the full FfnAgent path: GraphTemplates, Lanes, replays, ffn_shim.
 
-Each case runs the hipGraph replay and compares with the oracle's mailbox step
+Each case replays a template (direct kernel dispatch by default, the hipGraph where
+graph dispatch is selected) and compares with the oracle's mailbox step
 (gather -> RMSNorm -> Dense with the reference's rounding points -> scatter):
 rows outside the gathered slots must be untouched bit-for-bit, gathered rows
 meet the FFN gates of tests/parity.py.
@@ -267,3 +268,34 @@ def test_ffn_shim_matches_dense_partial(device):
     finally:
         detach()
         agent.close()
+
+
+def test_graph_dispatch_matches_direct_dispatch(device):
+    # The same replays through the instantiated hipGraphs (rebinding only changed nodes) and
+    # through direct kernel launches give identical bits; alternating layers and row counts
+    # exercise the rebinding.
+    hidden, intermediate = 1024, 3072
+    pool = o.generate_hidden_states(256, hidden, 17)
+    layers = [o.generate_layer(hidden, intermediate, 40 + index) for index in range(2)]
+    slots = slots_tensor(o.generate_slots(256, 200, 19), device)
+    results = {}
+    for graph_dispatch in (False, True):
+        with FfnAgent(device, graph_dispatch=graph_dispatch) as agent:
+            for ordinal, (w_gate_up, w_down, norm_weight) in enumerate(layers):
+                agent.register_layer(
+                    instance_index=0, layer_ordinal=ordinal, weights=_weights(w_gate_up, w_down, device),
+                    norm_weight=to_device(norm_weight, device),
+                )
+            agent.materialize(maximum_row_capacity=200)
+            assert agent.lanes[0].graph_dispatch is graph_dispatch
+            outputs = []
+            for ordinal, rows in ((0, 3), (1, 3), (0, 3), (0, 150), (1, 17), (1, 17)):
+                pool_gpu = to_device(pool, device)
+                agent.execute(instance_index=0, layer_ordinal=ordinal, pool=pool_gpu, slots=slots, rows=rows)
+                agent.lanes[0].synchronize()
+                outputs.append(pool_gpu.cpu())
+            results[graph_dispatch] = outputs
+    for direct, graph in zip(results[False], results[True]):
+        assert_bitwise_equal(graph, direct)
+    w_gate_up, w_down, norm_weight = layers[1]
+    _check_mailbox(results[True][4], pool, slots.cpu().numpy()[:17], w_gate_up, w_down, norm_weight)
