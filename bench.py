@@ -1,7 +1,7 @@
 """FFN-layer throughput of the MI355X FfnAgent path at the Qwen3-8B shape.
 
-One step = one hipGraph replay of the Dense mailbox step for a batch of T
-tokens: gather T seeded slots of an 8192-slot bf16 mailbox with the fused
+One step = one replay of the Dense mailbox step's GraphTemplate (its captured
+kernels launched on the Lane stream) for a batch of T tokens: gather T seeded slots of an 8192-slot bf16 mailbox with the fused
 RMSNorm, gate_up [4096 -> 2 x 12288] + SiLU*mul, down [12288 -> 4096],
 scatter back into the same slots.  Inputs are resident in HBM before timing.
 
@@ -284,7 +284,7 @@ def main() -> int:
             "tokens": tokens,
             "mailbox_slots": POOL_SLOTS,
             "rmsnorm_fused_into_gather": True,
-            "execution": "hipGraph replay per layer signature",
+            "execution": "GraphTemplate replay per layer signature (captured kernels launched directly)",
             "layer_mfma_frac": round(layer_flops(tokens) / seconds / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
             "layer_hbm_frac": round(layer_bytes(tokens) / seconds / 1e9 / HBM_PEAK_GBS, 4),
         },

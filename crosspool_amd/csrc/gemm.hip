@@ -8,21 +8,22 @@
 // Weights are [N, K] row-major with K contiguous; i_proj rows are interleaved
 // Gate/Up (runtime/ffnagent/preparation.py:227).  Accumulation is fp32.
 //
-// Two kernel families, chosen per GraphTemplate capacity:
-//  * split (capacity <= 64, HBM-bound): weight rows are the MFMA M operand
-//    (v_mfma_f32_16x16x32_bf16), each lane streams 64 contiguous bytes of one
-//    weight row per 128-wide K chunk with several chunks of loads in flight, the
-//    few token rows are the N operand and come from L2.  A workgroup splits K
-//    across its waves and sums the ranges through LDS in a fixed order
-//    (deterministic).  A Gate/Up pair lands in one lane's accumulator registers,
-//    so the SiLU epilogue needs no data exchange.
-//  * tile (capacity > 64, MFMA-bound): BMxBN block tiles, BK = 64, four waves
-//    (2x2) each owning a (BM/2)x(BN/2) tile of v_mfma_f32_32x32x16_bf16
-//    accumulators, register-staged global loads double-buffered through LDS
-//    with an XOR swizzle of 16-byte chunks (conflict-free ds_read_b128), and
-//    an XCD-major tile order for L2 reuse.  For gate_up the weight tile is
-//    permuted while staging so that a wave's Gate and Up columns for the same
-//    j sit in the same lane and register.
+// Three kernel families, chosen per GraphTemplate capacity (choose_gemm):
+//  * split (up to 4 / 8 live rows, HBM-bound): weight rows are the MFMA M operand
+//    (v_mfma_f32_16x16x32_bf16), each lane streams 64 contiguous bytes of one weight row
+//    per 128-wide K chunk with several chunks of loads in flight, the few token rows are
+//    the N operand and come from L2.  A workgroup splits K across its waves and sums the
+//    ranges through LDS in a fixed order (deterministic).  A Gate/Up pair lands in one
+//    lane's accumulator registers, so the SiLU epilogue needs no data exchange.
+//  * stream (up to 64 live rows, HBM-bound): the same weight streaming with the token
+//    rows of a K slice staged in LDS once per workgroup; sliced K goes through fp32
+//    partial sums and an ordered reduction kernel.
+//  * tile (more rows, MFMA-bound): BM x BN block tiles, BK = 64, 32x32x16 MFMA wave
+//    tiles, direct global-to-LDS loads into a ring of stages with an XOR swizzle of
+//    16-byte chunks (conflict-free ds_read_b128), and an optional K split across
+//    workgroups (fp32 partials and the same ordered reduction) for grids smaller than
+//    the chip.  For gate_up the weight tile is permuted while staging so that a wave's
+//    Gate and Up columns for the same j sit in the same lane and register.
 
 #include "xp_kernels.hpp"
 
@@ -420,10 +421,12 @@ __device__ __forceinline__ void wait_vmcnt() {
 constexpr uint32_t kOutOfRange = 0x7ffffff0u;
 
 // BM x BN block tile, BK = 64, WAVES_M x WAVES_N waves (two per SIMD at 8 waves) each
-// owning a (BM / WAVES_M) x (BN / WAVES_N) tile of 32x32x16 MFMA accumulators.  With
-// PINGPONG (8 waves), the two waves sharing a SIMD alternate between a slab of MFMAs and
-// the LDS reads of their next slab, so the matrix pipe and LDS work at the same time.
-template <int BM, int BN, int WAVES_M, int WAVES_N, bool GATED, bool PINGPONG = false>
+// owning a (BM / WAVES_M) x (BN / WAVES_N) tile of 32x32x16 MFMA accumulators.  STAGES
+// slabs of A and B live in LDS: while one is multiplied, the loads of the next STAGES - 1
+// are in flight.  Grid z splits K into ranges of `k_slice` columns; with more than one
+// range each workgroup writes the fp32 partial tile of its range and
+// stream_reduce_kernel, launched next, adds the ranges in order and applies the epilogue.
+template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, bool GATED>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmArgs a) {
   constexpr int BK = 64;
   constexpr int WAVES = WAVES_M * WAVES_N;
@@ -431,19 +434,19 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
   constexpr int WTN = BN / WAVES_N;
   constexpr int MT = WTM / 32;
   constexpr int NT = WTN / 32;
-  constexpr int KSTEPS_MAX = 4;                    // 16-wide k steps per slab (BK / 16)
+  constexpr int KSTEPS = BK / 16;                  // 16-wide k steps per slab
   constexpr int ROWS = BM + BN;                    // LDS rows per stage (A rows then B rows)
   constexpr int STAGE = ROWS * BK;                 // bf16 elements per stage
-  constexpr int LOAD_WAVES = PINGPONG ? WAVES / 2 : WAVES;  // waves that fill the stages
-  constexpr int A_LOADS = BM / 8 / LOAD_WAVES;     // 1 KB (8-row) load instructions per loading wave per stage
-  constexpr int B_LOADS = BN / 8 / LOAD_WAVES;
+  constexpr int A_LOADS = BM / 8 / WAVES;          // 1 KB (8-row) load instructions per wave per stage
+  constexpr int B_LOADS = BN / 8 / WAVES;
   constexpr int LOADS = A_LOADS + B_LOADS;
   static_assert(MT >= 1 && NT >= 1, "wave tile must hold at least one 32x32 MFMA tile");
   static_assert(!GATED || NT % 2 == 0, "gated tiles need whole Gate/Up column groups per wave");
-  static_assert(BM % (8 * LOAD_WAVES) == 0 && BN % (8 * LOAD_WAVES) == 0, "stage rows must split evenly");
-  static_assert(!PINGPONG || WAVES == 8, "ping-pong pairs the two waves of each SIMD");
+  static_assert(BM % (8 * WAVES) == 0 && BN % (8 * WAVES) == 0, "stage rows must split evenly");
+  static_assert(STAGES >= 2 && LOADS * (STAGES - 1) < 64, "in-flight loads must fit the vmcnt counter");
+  static_assert(STAGES * STAGE * 2 <= 160 * 1024, "stages must fit the CU's LDS");
 
-  __shared__ __attribute__((aligned(1024))) uint16_t lds[2 * STAGE];
+  __shared__ __attribute__((aligned(1024))) uint16_t lds[STAGES * STAGE];
 
   // Grid x walks weight tiles, grid y token tiles.  Workgroups go to the 8 XCDs round
   // robin by linear id, so consecutive weight tiles land on different XCDs and every token
@@ -457,6 +460,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
     return;
   }
   const int64_t w0 = static_cast<int64_t>(tn) * BN;
+  const int64_t k_begin = static_cast<int64_t>(blockIdx.z) * a.k_slice;
+  const int64_t k_end = a.k - k_begin < a.k_slice ? a.k : k_begin + a.k_slice;
 
   const int lane = threadIdx.x & 63;
   // Wave-uniform by construction; readfirstlane lets the compiler keep it (and the load
@@ -480,9 +485,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
   // i takes row g + i / 8 and k chunk (i % 8) ^ swizzle(row).  Because g is a multiple of
   // 8, swizzle(g + i / 8) = (i / 16) ^ (4 if g / 8 is odd), so the per-lane part of every
   // offset takes one of two values and the group part is wave-uniform.
-  const int load_wave = wave % LOAD_WAVES;
-  const int a_first = load_wave * (BM / LOAD_WAVES);
-  const int b_first = BM + load_wave * (BN / LOAD_WAVES);
+  const int a_first = wave * (BM / WAVES);
+  const int b_first = BM + wave * (BN / WAVES);
   const int row_in_load = lane >> 3;
   const int lane_chunk[2] = {(lane & 7) ^ (row_in_load >> 1), (lane & 7) ^ (row_in_load >> 1) ^ 4};
   // B rows of a gated tile are permuted: LDS row p = wq * G + s * G / 2 + jj (G = BN /
@@ -497,10 +501,13 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
       return p;
     }
   };
+  // Slab kt of this workgroup's K range.  Slabs at or past the range end (the prologue of
+  // a short range, the refills after the last slab) load zeros without memory traffic.
   auto issue_loads = [&](int64_t kt, int stage) {
-    const uint32_t k_bytes = static_cast<uint32_t>(kt * BK * 2);
-    // 16-byte chunks of this slab that lie inside K (8 except in a ragged last slab).
-    const int chunks_left = static_cast<int>((a.k - kt * BK) >> 3);
+    const int64_t k_pos = k_begin + kt * BK;
+    const uint32_t k_bytes = static_cast<uint32_t>(k_pos * 2);
+    // 16-byte chunks of this slab that lie inside the range (8 except in a ragged last slab).
+    const int64_t chunks_left = (k_end - k_pos) >> 3;
     uint16_t *base = lds + stage * STAGE;
     // The scalar offset must stay wave-uniform; masking goes through the per-lane offset
     // (kOutOfRange + k_bytes is still past the resource end), as a select, not a branch.
@@ -539,29 +546,24 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
   static_assert(WTM % 16 == 0 && WTN % 16 == 0, "fragment row offsets must keep the swizzle");
   const int frag_row = lane & 31;
   const int frag_half = lane >> 5;
-  int frag_lane[KSTEPS_MAX];
+  int frag_lane[KSTEPS];
 #pragma unroll
-  for (int ks = 0; ks < KSTEPS_MAX; ++ks) {
+  for (int ks = 0; ks < KSTEPS; ++ks) {
     frag_lane[ks] = frag_row * BK + (((ks * 2 + frag_half) ^ swizzle(frag_row)) << 3);
   }
   const int a_frag_base = wm * WTM * BK;
   const int b_frag_base = BM * BK + wn * WTN * BK;
-  auto frag_a = [&](int stage, int ks, int mt) {
-    return as_bf16x8(load16(lds + stage * STAGE + a_frag_base + mt * 32 * BK + frag_lane[ks]));
-  };
-  auto frag_b = [&](int stage, int ks, int nt) {
-    return as_bf16x8(load16(lds + stage * STAGE + b_frag_base + nt * 32 * BK + frag_lane[ks]));
-  };
   bf16x8 af[2][MT];
   bf16x8 bfrag[2][NT];
   auto read_fragments = [&](int stage, int ks, int slot) {
+    const uint16_t *base = lds + stage * STAGE;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      af[slot][mt] = frag_a(stage, ks, mt);
+      af[slot][mt] = as_bf16x8(load16(base + a_frag_base + mt * 32 * BK + frag_lane[ks]));
     }
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      bfrag[slot][nt] = frag_b(stage, ks, nt);
+      bfrag[slot][nt] = as_bf16x8(load16(base + b_frag_base + nt * 32 * BK + frag_lane[ks]));
     }
   };
   auto mfma_step = [&](int slot) {
@@ -573,134 +575,96 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
       }
     }
   };
+  auto inner_steps = [&](int stage) {
+#pragma unroll
+    for (int ks = 0; ks + 1 < KSTEPS; ++ks) {
+      read_fragments(stage, ks + 1, (ks + 1) & 1);
+      mfma_step(ks & 1);
+    }
+  };
+  // Workgroup barrier for the stage ring.  Before it each wave waits for its loads of the
+  // next slab (leaving the STAGES - 2 younger slabs in flight, which a __syncthreads would
+  // also drain) and for its own LDS reads, so that after it every wave may read the next
+  // slab and refill the stage just read.  The memory clobber keeps the compiler from
+  // moving LDS accesses across it; the scheduling barriers keep instructions on their side.
+  auto stage_barrier = [] {
+    constexpr int N = LOADS * (STAGES - 2);
+    __builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4));  // vmcnt(N) lgkmcnt(0)
+    __builtin_amdgcn_sched_barrier(0);
+    __asm__ volatile("s_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
 
-  const int64_t ktiles = (a.k + BK - 1) / BK;
-  constexpr int KSTEPS = BK / 16;
-  if constexpr (PINGPONG) {
-    // Waves w and w + 4 run on SIMD w % 4.  Barriers split time into phases of half a slab
-    // (two k steps).  In phase 2u the first group (waves 0-3) multiplies half slab u from
-    // registers while the second group reads half slab u's fragments; in phase 2u + 1 the
-    // roles swap, the first group reading half slab u + 1 and, after the second group's last
-    // read of slab s, refilling that stage with slab s + 2.  Only the first group loads from
-    // memory, so its waits cover every write of a stage before the barrier publishing it.
-    constexpr int HALF = KSTEPS / 2;
-    const bool first_group = wave < WAVES / 2;
-    bf16x8 fa[HALF][MT];
-    bf16x8 fb[HALF][NT];
-    auto read_half = [&](int64_t u) {
-      const int stage = static_cast<int>((u >> 1) & 1);
-      const int first = static_cast<int>(u & 1) * HALF;
+  // The chooser never makes an empty K range, so every workgroup runs at least one slab.
+  const int64_t ktiles = (k_end - k_begin + BK - 1) / BK;
+  // Prologue: slabs 0 .. STAGES-1 in flight, wait for slab 0, read its first fragments.
 #pragma unroll
-      for (int h = 0; h < HALF; ++h) {
+  for (int s = 0; s < STAGES; ++s) {
+    issue_loads(s, s);
+  }
+  wait_vmcnt<LOADS * (STAGES - 1)>();
+  __syncthreads();
+  read_fragments(0, 0, 0);
+
+  int stage = 0;
+  for (int64_t kt = 0; kt + 1 < ktiles; ++kt) {
+    inner_steps(stage);
+    // After the barrier slab kt+1 is in LDS and nobody reads this stage any more.  The last
+    // k step's MFMAs then run interleaved with the reads of slab kt+1's first fragments and
+    // the refill of this stage with slab kt+STAGES (zeros past the range end), keeping the
+    // matrix pipe busy while the loads issue.
+    stage_barrier();
+    const int next = stage + 1 == STAGES ? 0 : stage + 1;
+    read_fragments(next, 0, 0);
+    issue_loads(kt + STAGES, stage);
+    mfma_step((KSTEPS - 1) & 1);
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          fa[h][mt] = first == 0 ? frag_a(stage, h, mt) : frag_a(stage, HALF + h, mt);
+    for (int i = 0; i < MT * NT; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one memory load
+    }
+    stage = next;
+  }
+  inner_steps(stage);
+  mfma_step((KSTEPS - 1) & 1);
+  // Past-the-end refills may still be landing in the stage buffers the epilogue reuses.
+  __builtin_amdgcn_s_waitcnt(0);
+
+  if (a.k_split > 1) {
+    // fp32 partial tile of this K range, [range][token][weight row]: for each (mt, r, nt)
+    // the 32 lanes of a half-wave write 32 consecutive columns of one row (a Gate/Up pair
+    // per lane for gate_up, in the weights' interleaved order).
+    float *plane = a.partials + static_cast<int64_t>(blockIdx.z) * a.rows * a.n;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t token = m0 + wm * WTM + mt * 32 + 8 * (r >> 2) + 4 * frag_half + (r & 3);
+        if (token >= a.rows) {
+          continue;
         }
+        float *row = plane + token * a.n;
+        if constexpr (GATED) {
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-          fb[h][nt] = first == 0 ? frag_b(stage, h, nt) : frag_b(stage, HALF + h, nt);
-        }
-      }
-    };
-    auto mfma_half = [&]() {
-#pragma unroll
-      for (int h = 0; h < HALF; ++h) {
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
+          for (int nt = 0; nt < NT / 2; ++nt) {
+            const int64_t column = w0 + 2 * (wn * (WTN / 2) + nt * 32 + frag_row);
+            if (column < a.n) {
+              *reinterpret_cast<f32x2 *>(row + column) = f32x2{acc[mt][nt][r], acc[mt][nt + NT / 2][r]};
+            }
+          }
+        } else {
 #pragma unroll
           for (int nt = 0; nt < NT; ++nt) {
-            acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[h][mt], fb[h][nt], acc[mt][nt], 0, 0, 0);
+            const int64_t column = w0 + wn * WTN + nt * 32 + frag_row;
+            if (column < a.n) {
+              row[column] = acc[mt][nt][r];
+            }
           }
         }
       }
-    };
-    // A bare s_barrier: unlike __syncthreads it does not wait for the loads in flight.  The
-    // memory clobber keeps the compiler from moving LDS accesses across it and the
-    // scheduling barriers keep the MFMAs of a phase inside it.
-    auto barrier = [] {
-      __builtin_amdgcn_sched_barrier(0);
-      __asm__ volatile("s_barrier" ::: "memory");
-      __builtin_amdgcn_sched_barrier(0);
-    };
-    auto wait_lds = [] { __builtin_amdgcn_s_waitcnt(0xc07f); };  // lgkmcnt(0)
-
-    // The two groups run separate loops with the same barrier count per half slab.
-    const int64_t halves = 2 * ktiles;
-    if (first_group) {
-      issue_loads(0, 0);
-      if (ktiles > 1) {
-        issue_loads(1, 1);
-        wait_vmcnt<LOADS>();  // slab 0 landed; slab 1 may still be in flight
-      } else {
-        wait_vmcnt<0>();
-      }
-      barrier();
-      read_half(0);
-      for (int64_t u = 0; u < halves; ++u) {
-        const int64_t s = u >> 1;
-        const bool second_half = (u & 1) != 0;
-        mfma_half();
-        if (second_half) {
-          wait_vmcnt<0>();  // slab s + 1 landed (issued during slab s - 1)
-        }
-        barrier();
-        if (second_half && s + 2 < ktiles) {
-          issue_loads(s + 2, static_cast<int>(s & 1));
-        }
-        if (u + 1 < halves) {
-          read_half(u + 1);
-        }
-        barrier();
-      }
-    } else {
-      barrier();
-      for (int64_t u = 0; u < halves; ++u) {
-        read_half(u);
-        wait_lds();  // done reading before the stage may be refilled
-        barrier();
-        mfma_half();
-        barrier();
-      }
     }
-  } else {
-    // Prologue: tiles 0 and 1 in flight, wait for tile 0, read its first fragments.
-    issue_loads(0, 0);
-    issue_loads(1, 1);    // a K of one tile makes these loads all out of range (zeros)
-    wait_vmcnt<LOADS>();  // tile 0 landed; tile 1 may still be in flight
-    __syncthreads();
-    read_fragments(0, 0, 0);
-
-    auto inner_steps = [&](int stage) {
-#pragma unroll
-      for (int ks = 0; ks + 1 < KSTEPS; ++ks) {
-        read_fragments(stage, ks + 1, (ks + 1) & 1);
-        mfma_step(ks & 1);
-      }
-    };
-    for (int64_t kt = 0; kt + 1 < ktiles; ++kt) {
-      const int stage = static_cast<int>(kt & 1);
-      inner_steps(stage);
-      // Tile kt+1 (our loads) has landed once the counters drain; after the barrier nobody
-      // reads this stage any more.  The last k step's MFMAs then run interleaved with the
-      // reads of tile kt+1's first fragments and the refill of this stage with tile kt+2
-      // (out of range, so zeros, past the last tile), keeping the matrix pipe busy while
-      // the loads issue.
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
-      read_fragments(stage ^ 1, 0, 0);
-      issue_loads(kt + 2, stage);
-      mfma_step((KSTEPS - 1) & 1);
-#pragma unroll
-      for (int i = 0; i < MT * NT; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
-        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one memory load
-      }
-    }
-    inner_steps(static_cast<int>((ktiles - 1) & 1));
-    mfma_step((KSTEPS - 1) & 1);
-    // Past-the-end refills may still be landing in the stage buffers the epilogue reuses.
-    __builtin_amdgcn_s_waitcnt(0);
+    return;
   }
 
   // Epilogue.  Lane holds D[8 (r / 4) + 4 (lane / 32) + r % 4][lane % 32] of each 32x32
@@ -710,7 +674,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
   // scatter is fused).  Bounds are checked per chunk on the way out.
   constexpr int OUT_N = GATED ? WTN / 2 : WTN;  // output columns of a wave tile
   constexpr int CPR = OUT_N / 8;                // 16-byte chunks per output row
-  static_assert(WTM * OUT_N * WAVES <= 2 * STAGE, "epilogue tiles must fit the stage buffers");
+  static_assert(WTM * OUT_N * WAVES <= STAGES * STAGE, "epilogue tiles must fit the stage buffers");
   static_assert((WTM * CPR) % 64 == 0, "output chunks must split evenly over the lanes");
   __syncthreads();  // every wave is done reading the stage buffers
   uint16_t *out_tile = lds + wave * (WTM * OUT_N);
@@ -767,23 +731,25 @@ struct TileShape {
   int bm;
   int bn;
   int waves;
-  int per_cu;       // resident workgroups per CU (LDS-limited)
-  double quality;   // relative per-CU efficiency of the tile shape
+  int stages;           // LDS slabs (STAGES - 1 of them in flight); one workgroup per CU
+  double flops_per_us;  // one CU's rate on this shape with every CU busy, measured on MI355X
 };
 constexpr TileShape kTileShapes[] = {
-    {256, 256, 8, 1, 1.00},
-    {256, 128, 8, 1, 0.90},
-    {128, 128, 4, 2, 0.80},
+    {256, 256, 8, 2, 4.6e6},
+    {256, 128, 8, 3, 4.0e6},
+    {128, 128, 4, 3, 3.4e6},
 };
+constexpr int kTileShapeCount = sizeof(kTileShapes) / sizeof(kTileShapes[0]);
 
 template <bool GATED>
 const void *tile_kernel(int variant) {
   using Kernel = void (*)(GemmArgs);
   static const Kernel table[] = {
-      &tile_gemm_kernel<256, 256, 2, 4, GATED>,
-      &tile_gemm_kernel<256, 128, 4, 2, GATED>,
-      &tile_gemm_kernel<128, 128, 2, 2, GATED>,
+      &tile_gemm_kernel<256, 256, 2, 4, 2, GATED>,
+      &tile_gemm_kernel<256, 128, 4, 2, 3, GATED>,
+      &tile_gemm_kernel<128, 128, 2, 2, 3, GATED>,
   };
+  static_assert(sizeof(table) / sizeof(table[0]) == kTileShapeCount, "one kernel per tile shape");
   return reinterpret_cast<const void *>(table[variant]);
 }
 
@@ -853,6 +819,47 @@ GemmChoice choose_stream(int64_t capacity, int64_t n, int64_t k) {
   return {GemmKind::Stream, variant, best_slice, 1};
 }
 
+// Tile shape and K split for a projection at `capacity` rows, from a cost model in
+// microseconds: whole rounds of one tile per CU at the shape's measured rate, but never
+// less than the time to stream the weights once, plus the fp32 partial traffic and the
+// reduction launch a K split adds.  Splitting K fills the CUs when the tile grid is
+// smaller than the chip (the down projection has 16 to 32 weight tiles at H = 4096).
+// Fitted to forced-choice timings of the Qwen3 0.6B / 4B / 8B / 32B-shard projections at
+// 128 to 4096 rows, where it picks the fastest measured choice or one within 7 % of it.
+constexpr double kWeightBytesPerUs = 5.0e6;   // weights streamed from HBM
+constexpr double kPartialBytesPerUs = 6.0e6;  // partial sums written, then read by the reduction
+constexpr double kReduceLaunchUs = 4.0;
+constexpr int64_t kMaxTileSplit = 16;
+
+GemmChoice choose_tile(int64_t capacity, int64_t n, int64_t k) {
+  GemmChoice best{GemmKind::Tile, 0, k, 1};
+  double best_cost = 0.0;
+  for (int index = 0; index < kTileShapeCount; ++index) {
+    const TileShape &shape = kTileShapes[index];
+    const int64_t base_tiles = ((capacity + shape.bm - 1) / shape.bm) * ((n + shape.bn - 1) / shape.bn);
+    for (int64_t split = 1; split <= kMaxTileSplit; split *= 2) {
+      const int64_t k_slice = ((k + split - 1) / split + 63) / 64 * 64;
+      if ((split - 1) * k_slice >= k) {
+        break;  // the last range would be empty
+      }
+      const int64_t rounds = (base_tiles * split + kComputeUnits - 1) / kComputeUnits;
+      const double compute = static_cast<double>(rounds) * 2.0 * shape.bm * shape.bn *
+                             static_cast<double>(k_slice) / shape.flops_per_us;
+      const double stream = 2.0 * static_cast<double>(n) * static_cast<double>(k) / kWeightBytesPerUs;
+      double cost = compute > stream ? compute : stream;
+      if (split > 1) {
+        cost += 8.0 * split * static_cast<double>(capacity) * static_cast<double>(n) / kPartialBytesPerUs +
+                kReduceLaunchUs;
+      }
+      if ((index == 0 && split == 1) || cost < best_cost) {
+        best = {GemmKind::Tile, index, k_slice, split};
+        best_cost = cost;
+      }
+    }
+  }
+  return best;
+}
+
 }  // namespace
 
 GemmChoice choose_gemm(int64_t capacity, int64_t n, int64_t k, bool gated) {
@@ -861,28 +868,27 @@ GemmChoice choose_gemm(int64_t capacity, int64_t n, int64_t k, bool gated) {
     return capacity <= (gated ? kSplitMaxRowsGated : kSplitMaxRows) ? choose_split(n, k)
                                                                      : choose_stream(capacity, n, k);
   }
-  int best = 0;
-  double best_cost = 0.0;
-  for (int index = 0; index < 3; ++index) {
-    const TileShape &shape = kTileShapes[index];
-    const int64_t tiles = ((capacity + shape.bm - 1) / shape.bm) * ((n + shape.bn - 1) / shape.bn);
-    const int64_t slots = static_cast<int64_t>(kComputeUnits) * shape.per_cu;
-    const int64_t rounds = (tiles + slots - 1) / slots;
-    // A round runs `per_cu` co-resident tiles on each CU, sharing its MFMA pipes.
-    const double cost = static_cast<double>(rounds) * shape.per_cu * shape.bm * shape.bn / shape.quality;
-    if (index == 0 || cost < best_cost) {
-      best = index;
-      best_cost = cost;
-    }
+  return choose_tile(capacity, n, k);
+}
+
+// K ranges whose fp32 partial sums go through scratch and the reduction kernel.
+int64_t scratch_slices(GemmChoice choice, int64_t k) {
+  switch (choice.kind) {
+    case GemmKind::Stream:
+      return stream_slices(k, choice.k_slice);
+    case GemmKind::Tile:
+      return choice.k_split;
+    default:
+      return 1;  // the split kernel sums its K ranges in LDS
   }
-  return {GemmKind::Tile, best, 0, 1};
 }
 
 size_t gemm_scratch_bytes(GemmChoice choice, int64_t capacity, int64_t n, int64_t k) {
-  if (choice.kind != GemmKind::Stream || stream_slices(k, choice.k_slice) == 1) {
+  const int64_t slices = scratch_slices(choice, k);
+  if (slices == 1) {
     return 0;
   }
-  const size_t partial_bytes = static_cast<size_t>(stream_slices(k, choice.k_slice) * capacity * n) * sizeof(float);
+  const size_t partial_bytes = static_cast<size_t>(slices * capacity * n) * sizeof(float);
   return (partial_bytes + 255) / 256 * 256;
 }
 
@@ -914,44 +920,40 @@ GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmCho
                                 static_cast<int>(kStreamLdsBytes));
       configured[gated][choice.variant] = true;
     }
-    if (slices > 1) {
-      KernelLaunch &reduce = launches.reduce;
-      reduce.func = gated ? reinterpret_cast<const void *>(&stream_reduce_kernel<true>)
-                          : reinterpret_cast<const void *>(&stream_reduce_kernel<false>);
-      reduce.grid = dim3(static_cast<unsigned>((capacity * (args.n / 4) + 255) / 256), 1, 1);
-      reduce.block = dim3(256, 1, 1);
-      reduce.set_args(record);
-    }
   } else {
     const TileShape &shape = kTileShapes[choice.variant];
     kernel.func = gated ? tile_kernel<true>(choice.variant) : tile_kernel<false>(choice.variant);
     kernel.grid = dim3(static_cast<unsigned>((args.n + shape.bn - 1) / shape.bn),
-                       static_cast<unsigned>((capacity + shape.bm - 1) / shape.bm), 1);
+                       static_cast<unsigned>((capacity + shape.bm - 1) / shape.bm),
+                       static_cast<unsigned>(choice.k_split));
     kernel.block = dim3(static_cast<unsigned>(64 * shape.waves), 1, 1);
+  }
+  if (scratch_slices(choice, args.k) > 1) {
+    KernelLaunch &reduce = launches.reduce;
+    reduce.func = gated ? reinterpret_cast<const void *>(&stream_reduce_kernel<true>)
+                        : reinterpret_cast<const void *>(&stream_reduce_kernel<false>);
+    reduce.grid = dim3(static_cast<unsigned>((capacity * (args.n / 4) + 255) / 256), 1, 1);
+    reduce.block = dim3(256, 1, 1);
+    reduce.set_args(record);
   }
   kernel.set_args(record);
   return launches;
 }
 
-const char *gemm_name(GemmChoice choice, bool gated) {
-  static const char *split_names[2][4] = {
-      {"split_t16_k1", "split_t16_k2", "split_t16_k4", "split_t16_k8"},
-      {"split_gated_t16_k1", "split_gated_t16_k2", "split_gated_t16_k4", "split_gated_t16_k8"},
-  };
-  static const char *stream_names[2][3] = {{"stream_t16", "stream_t32", "stream_t64"},
-                                           {"stream_gated_t16", "stream_gated_t32", "stream_gated_t64"}};
-  static const char *tile_names[2][3] = {
-      {"tile_256x256", "tile_256x128", "tile_128x128"},
-      {"tile_gated_256x256", "tile_gated_256x128", "tile_gated_128x128"},
-  };
+std::string gemm_name(GemmChoice choice, bool gated) {
+  const std::string prefix = gated ? "_gated" : "";
   if (choice.kind == GemmKind::Split) {
-    const int split_index = choice.k_split == 1 ? 0 : (choice.k_split == 2 ? 1 : (choice.k_split == 4 ? 2 : 3));
-    return split_names[gated][split_index];
+    return "split" + prefix + "_t16_k" + std::to_string(choice.k_split);
   }
   if (choice.kind == GemmKind::Stream) {
-    return stream_names[gated][choice.variant];
+    return "stream" + prefix + "_t" + std::to_string(16 << choice.variant);
   }
-  return tile_names[gated][choice.variant];
+  const TileShape &shape = kTileShapes[choice.variant];
+  std::string name = "tile" + prefix + "_" + std::to_string(shape.bm) + "x" + std::to_string(shape.bn);
+  if (choice.k_split > 1) {
+    name += "_k" + std::to_string(choice.k_split);
+  }
+  return name;
 }
 
 }  // namespace xp

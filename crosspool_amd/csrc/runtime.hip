@@ -58,8 +58,9 @@ size_t align_up(size_t value, size_t alignment) { return (value + alignment - 1)
 
 // Workspace regions of one Dense step at `capacity`: gathered batch [capacity, hidden],
 // then the activated intermediate [capacity, intermediate], each 16-byte aligned; then,
-// when the capacity takes the sliced stream kernel, its fp32 partial sums (256-byte
-// aligned, gate_up's then down's).
+// when a projection at this capacity splits K across workgroups (sliced stream or split
+// tile kernel), the fp32 partial sums of its K ranges (256-byte aligned, gate_up's then
+// down's).
 struct DenseWorkspace {
   size_t batch_offset;
   size_t activated_offset;

@@ -10,6 +10,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <cstring>
+#include <string>
 
 #include "xp_common.hpp"
 
@@ -86,9 +87,10 @@ struct GemmArgs {
   const uint16_t *w;
   uint16_t *out;
   const int32_t *scatter_slots;
-  float *partials;   // stream kernel: fp32 partial sums [slices, rows, n] when K is sliced
-  int64_t k_slice;   // split / stream kernels: K columns per range (a multiple of the load group)
-  int64_t k_split;   // split kernel: K ranges per 16-row weight block (1, 2, 4 or 8)
+  float *partials;   // fp32 partial sums [ranges, rows, n] when K is split across workgroups
+  int64_t k_slice;   // K columns per range (a multiple of the kernel's load group)
+  int64_t k_split;   // split kernel: K ranges per 16-row weight block (1, 2, 4 or 8);
+                     // tile kernel: K ranges (grid z)
   int64_t ldx;
   int64_t ldo;
   int64_t rows;      // live rows
@@ -104,8 +106,9 @@ enum class GemmKind : int { Split = 1, Tile = 2, Stream = 3 };
 struct GemmChoice {
   GemmKind kind;
   int variant;      // index into the kind's instantiation table
-  int64_t k_slice;  // split / stream kernels: K columns per range (0 for tiles)
-  int64_t k_split;  // split kernel: K ranges per weight-row block (1 otherwise)
+  int64_t k_slice;  // K columns per range
+  int64_t k_split;  // split kernel: K ranges per weight-row block; tile kernel: K ranges
+                    // (grid z); 1 for the stream kernel, whose ranges follow from k_slice
 };
 
 GemmChoice choose_gemm(int64_t capacity, int64_t n, int64_t k, bool gated);
@@ -113,14 +116,14 @@ GemmChoice choose_gemm(int64_t capacity, int64_t n, int64_t k, bool gated);
 // needs; 0 when its kernel reduces K inside one workgroup.
 size_t gemm_scratch_bytes(GemmChoice choice, int64_t capacity, int64_t n, int64_t k);
 
-// A projection is one kernel, or the sliced stream kernel writing partial sums followed by
-// the kernel that adds them in slice order and applies the epilogue (`reduce`, empty
-// otherwise).  The kernel boundary orders the partials: no cross-workgroup fences.
+// A projection is one kernel, or a kernel writing the partial sums of K ranges (sliced
+// stream, split tile) followed by the kernel that adds them in range order and applies the
+// epilogue (`reduce`, empty otherwise).  The kernel boundary orders the partials: no cross-workgroup fences.
 struct GemmLaunch {
   KernelLaunch main;
   KernelLaunch reduce;
 };
 GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmChoice choice);
-const char *gemm_name(GemmChoice choice, bool gated);
+std::string gemm_name(GemmChoice choice, bool gated);
 
 }  // namespace xp

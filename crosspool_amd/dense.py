@@ -139,9 +139,10 @@ class DenseExecutionPlan:
     Regions: the gathered (normalised) batch ``[capacity, H]`` and the
     activated intermediate ``[capacity, I]``; SiLU*mul is always fused into
     the gate_up epilogue, so no separate projected buffer exists.  Capacities
-    served by the sliced stream kernel append the fp32 partial sums of its K
-    slices (``workspace_bytes`` covers them, as GemmPlan's split-K workspace
-    does in operators/linear.py:111-131).
+    whose projections split K across workgroups (sliced stream or split tile
+    kernels) append the fp32 partial sums of the K ranges (``workspace_bytes``
+    covers them, as GemmPlan's split-K workspace does in
+    operators/linear.py:111-131).
     """
 
     signature: DenseFfnExecutionSignature

@@ -1,4 +1,4 @@
-"""GPU parity of the MFMA projections (split and tile kernels).
+"""GPU parity of the MFMA projections (split, stream and tile kernels, K-split tiles).
 
 Bar (tests/parity.py): every projection lies in the bf16 interval that fp32
 accumulation of the exact fp64 sum can round to, every activation lies between
@@ -53,7 +53,7 @@ def test_down_matches_oracle(device, hidden, intermediate, rows):
     assert_projection_within_bounds(out, h, w_down)
 
 
-@pytest.mark.parametrize("rows", [1, 4, 32, 64, 256, 512])
+@pytest.mark.parametrize("rows", [1, 4, 32, 64, 128, 256, 512])
 def test_qwen3_8b_projections(device, rows):
     hidden, intermediate = 4096, 12288
     x = o.generate_hidden_states(rows, hidden, 17)
@@ -102,6 +102,25 @@ def test_scattering_down_projection_writes_only_its_slots(device, rows):
     assert_bitwise_equal(pool_d.cpu(), o.scatter(pool, slots, direct.cpu()))
 
 
+@pytest.mark.parametrize("rows", [65, 200, 256, 300])
+def test_k_split_tiles_with_ragged_ranges(device, rows):
+    # K = 3000 (down) splits into ranges of 384 (or 192) columns with a 312- (120-) column
+    # last range ending in a partial slab; 200 and 300 rows leave the last row tile partly
+    # filled.
+    hidden, intermediate = 1024, 3000
+    assert "_k" in _native.gemm_variant(rows, hidden, intermediate, False)
+    x = o.generate_hidden_states(rows, hidden, 17)
+    w_gate_up, w_down = _layer(hidden, intermediate)
+    x_d, gu_d, dn_d = to_device(x, device), to_device(w_gate_up, device), to_device(w_down, device)
+    activated = dense.gate_up_silu(x_d, gu_d)
+    out = dense.down(activated, dn_d)
+    again = dense.down(activated, dn_d)
+    torch.cuda.synchronize()
+    assert_activated_within_bounds(activated, x, w_gate_up)
+    assert_projection_within_bounds(out, activated.cpu(), w_down)
+    assert_bitwise_equal(out, again)
+
+
 def test_projections_are_deterministic(device):
     x = to_device(o.generate_hidden_states(256, 4096, 17), device)
     w_gate_up, w_down = (to_device(t, device) for t in _layer(4096, 1024))
@@ -125,6 +144,10 @@ def test_variant_selection_covers_every_family(device):
     assert _native.gemm_variant(1, 24576, 4096, True).startswith("split")
     assert _native.gemm_variant(48, 24576, 4096, True).startswith("stream")
     assert _native.gemm_variant(2048, 24576, 4096, True).startswith("tile")
+    # the Qwen3-8B cases of test_qwen3_8b_projections reach every tile shape and a K split
+    chosen = {_native.gemm_variant(rows, n, k, gated) for rows in (128, 256, 512)
+              for n, k, gated in ((24576, 4096, True), (4096, 12288, False))}
+    assert {"tile_gated_128x128", "tile_gated_256x128", "tile_gated_256x256", "tile_128x128_k8", "tile_256x128_k4"} <= chosen
 
 
 # Ragged geometries of the decode kernels: K not a multiple of their 512-column load

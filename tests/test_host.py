@@ -111,7 +111,7 @@ def test_native_workspace_covers_signature_layout(capacity, hidden, intermediate
     if gate_up + down == 0:
         assert native == layout
     else:
-        # the sliced stream kernel's partial sums follow the two regions, 256-byte aligned
+        # the partial sums of K-split projections follow the two regions, 256-byte aligned
         assert layout + gate_up + down <= native < layout + gate_up + down + 256
 
 
@@ -194,8 +194,22 @@ def test_gemm_variant_selection():
     assert _native.gemm_variant(64, 4096, 12288, False) == "stream_t64"
     assert _native.gemm_workspace_bytes(1, 24576, 4096, True) == 0
     assert _native.gemm_workspace_bytes(32, 4096, 12288, False) > 0
-    assert _native.gemm_variant(2048, 24576, 4096, True).startswith("tile_gated")
+    assert _native.gemm_variant(2048, 24576, 4096, True) == "tile_gated_256x256"
     assert _native.gemm_variant(4096, 4096, 12288, False).startswith("tile")
+    assert _native.gemm_workspace_bytes(2048, 24576, 4096, True) == 0
+
+
+def test_k_split_tiles_fill_the_chip_and_size_their_partials():
+    # Qwen3-8B down at 256 rows has only 16 to 64 weight x token tiles: K is split so that
+    # the grid covers the 256 CUs, and each range leaves an fp32 partial tile in scratch.
+    name = _native.gemm_variant(256, 4096, 12288, False)
+    shape, split = name.split("_")[1], int(name.rsplit("_k", 1)[1])
+    bm, bn = (int(v) for v in shape.split("x"))
+    tiles = -(-256 // bm) * (4096 // bn)
+    assert tiles < 256 <= tiles * split
+    assert _native.gemm_workspace_bytes(256, 4096, 12288, False) == split * 256 * 4096 * 4
+    # with a K of one slab there is nothing to split
+    assert "_k" not in _native.gemm_variant(300, 128, 64, False)
 
 
 def test_ffn_shim_requires_an_attachment():
