@@ -9,16 +9,17 @@
 // Gate/Up (runtime/ffnagent/preparation.py:227).  Accumulation is fp32.
 //
 // Three kernel families, chosen per GraphTemplate capacity (choose_gemm):
-//  * split (up to 4 / 8 live rows, HBM-bound): weight rows are the MFMA M operand
+//  * split (up to 4 / 8 rows, HBM-bound): weight rows are the MFMA M operand
 //    (v_mfma_f32_16x16x32_bf16), each lane streams 64 contiguous bytes of one weight row
 //    per 128-wide K chunk with several chunks of loads in flight, the few token rows are
 //    the N operand and come from L2.  A workgroup splits K across its waves and sums the
 //    ranges through LDS in a fixed order (deterministic).  A Gate/Up pair lands in one
 //    lane's accumulator registers, so the SiLU epilogue needs no data exchange.
-//  * stream (up to 64 live rows, HBM-bound): the same weight streaming with the token
-//    rows of a K slice staged in LDS once per workgroup; sliced K goes through fp32
-//    partial sums and an ordered reduction kernel.
-//  * tile (more rows, MFMA-bound): BM x BN block tiles, BK = 64, 32x32x16 MFMA wave
+//  * stream (up to 16 rows, HBM-bound): the same weight streaming with the token rows of
+//    a K slice staged in LDS once per workgroup; sliced K goes through fp32 partial sums
+//    and an ordered reduction kernel.
+//  * tile (more rows: HBM-bound up to a few hundred, then MFMA-bound): BM x BN block
+//    tiles from 64 x 128 to 256 x 256, BK = 64, 32x32x16 MFMA wave
 //    tiles, direct global-to-LDS loads into a ring of stages with an XOR swizzle of
 //    16-byte chunks (conflict-free ds_read_b128), and an optional K split across
 //    workgroups (fp32 partials and the same ordered reduction) for grids smaller than
@@ -204,7 +205,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) void split_gemm_kernel(GemmArgs a
 }
 
 // ------------------------------------------------------------------ stream (decode)
-// Weight-streaming projection for 5 to 64 live rows.  Workgroup g works on K slice
+// Weight-streaming projection for 5 to 16 live rows.  Workgroup g works on K slice
 // g / groups_per_slice: it stages the activations of that slice in LDS once (rows padded
 // by 16 bytes so the 16 token rows one fragment read touches fall in distinct bank
 // slots), then each of its 8 waves streams one 16-row weight block of the slice with
@@ -720,11 +721,8 @@ const void *split_kernel() {
 }
 
 template <bool GATED>
-const void *stream_kernel(int variant) {
-  using Kernel = void (*)(GemmArgs);
-  static const Kernel table[] = {&stream_gemm_kernel<1, GATED>, &stream_gemm_kernel<2, GATED>,
-                                 &stream_gemm_kernel<4, GATED>};
-  return reinterpret_cast<const void *>(table[variant]);
+const void *stream_kernel() {
+  return reinterpret_cast<const void *>(&stream_gemm_kernel<1, GATED>);
 }
 
 struct TileShape {
@@ -738,6 +736,7 @@ constexpr TileShape kTileShapes[] = {
     {256, 256, 8, 2, 4.6e6},
     {256, 128, 8, 3, 4.0e6},
     {128, 128, 4, 3, 3.4e6},
+    {64, 128, 4, 6, 2.4e6},
 };
 constexpr int kTileShapeCount = sizeof(kTileShapes) / sizeof(kTileShapes[0]);
 
@@ -748,6 +747,7 @@ const void *tile_kernel(int variant) {
       &tile_gemm_kernel<256, 256, 2, 4, 2, GATED>,
       &tile_gemm_kernel<256, 128, 4, 2, 3, GATED>,
       &tile_gemm_kernel<128, 128, 2, 2, 3, GATED>,
+      &tile_gemm_kernel<64, 128, 2, 2, 6, GATED>,
   };
   static_assert(sizeof(table) / sizeof(table[0]) == kTileShapeCount, "one kernel per tile shape");
   return reinterpret_cast<const void *>(table[variant]);
@@ -762,6 +762,9 @@ constexpr int kComputeUnits = 256;
 // grid) crosses over after 4 rows, down (K = 12288 split 8 ways) after 8.
 constexpr int64_t kSplitMaxRowsGated = 4;
 constexpr int64_t kSplitMaxRows = 8;
+// Rows up to which the stream kernel beats the deep-staged 64 x 128 tile (measured on the
+// Qwen3 4B / 8B / 32B-shard projections with weights streamed from HBM: even at 16 rows,
+// from 17 the tile wins).
 constexpr int kSplitDepth = 4;
 
 // K split of the split kernel.  Its load registers (170 VGPRs) leave room for one 8-wave
@@ -784,6 +787,7 @@ GemmChoice choose_split(int64_t n, int64_t k) {
   return {GemmKind::Split, 0, slice(ksplit), ksplit};
 }
 
+constexpr int64_t kStreamMaxRows = 16;
 constexpr int64_t kStreamLdsBytes = 160 * 1024;
 constexpr int64_t kStreamSliceQuantum = 128 * kStreamDepth;  // a whole number of load groups
 
@@ -795,9 +799,8 @@ int64_t stream_slices(int64_t k, int64_t k_slice) { return (k + k_slice - 1) / k
 // Otherwise workgroups (8 row blocks x one slice) are spread over the 256 CUs, the busiest
 // CU streams ceil(workgroups / 256) slices of 128 weight rows, and the slice length
 // minimising that load wins, ties going to fewer slices (less partial traffic).
-GemmChoice choose_stream(int64_t capacity, int64_t n, int64_t k) {
-  const int variant = capacity <= 16 ? 0 : (capacity <= 32 ? 1 : 2);
-  const int64_t tp = 16 << variant;
+GemmChoice choose_stream(int64_t n, int64_t k) {
+  constexpr int64_t tp = 16;  // staged token rows
   const int64_t groups = ((n + 15) / 16 + kStreamWaves - 1) / kStreamWaves;
   int64_t best_slice = 0;
   int64_t best_load = 0;
@@ -808,7 +811,7 @@ GemmChoice choose_stream(int64_t capacity, int64_t n, int64_t k) {
       continue;  // does not fit LDS, or the same slice length as fewer slices
     }
     if (slices == 1) {
-      return {GemmKind::Stream, variant, k_slice, 1};
+      return {GemmKind::Stream, 0, k_slice, 1};
     }
     const int64_t load = (slices * groups + kComputeUnits - 1) / kComputeUnits * k_slice;
     if (best_slice == 0 || load < best_load) {
@@ -816,19 +819,21 @@ GemmChoice choose_stream(int64_t capacity, int64_t n, int64_t k) {
       best_load = load;
     }
   }
-  return {GemmKind::Stream, variant, best_slice, 1};
+  return {GemmKind::Stream, 0, best_slice, 1};
 }
 
 // Tile shape and K split for a projection at `capacity` rows, from a cost model in
-// microseconds: whole rounds of one tile per CU at the shape's measured rate, but never
-// less than the time to stream the weights once, plus the fp32 partial traffic and the
-// reduction launch a K split adds.  Splitting K fills the CUs when the tile grid is
-// smaller than the chip (the down projection has 16 to 32 weight tiles at H = 4096).
-// Fitted to forced-choice timings of the Qwen3 0.6B / 4B / 8B / 32B-shard projections at
-// 128 to 4096 rows, where it picks the fastest measured choice or one within 7 % of it.
-constexpr double kWeightBytesPerUs = 5.0e6;   // weights streamed from HBM
+// microseconds.  Compute: whole rounds of one tile per CU at the shape's measured rate.
+// Weights: streamed from HBM once.  The two overlap only in part (the slower counts fully,
+// the faster by half).  A K split adds its fp32 partial traffic and the reduction launch;
+// it fills the CUs when the tile grid is smaller than the chip (the down projection has 16
+// to 32 weight tiles at H = 4096).  Fitted to forced-choice timings of the Qwen3 0.6B /
+// 4B / 8B / 32B-shard projections at 32 to 4096 rows (weights streamed from HBM at the
+// HBM-bound sizes), where it picks the fastest measured choice or one within 7 % of it.
+constexpr double kWeightBytesPerUs = 4.5e6;   // weights streamed from HBM by the tile kernel
 constexpr double kPartialBytesPerUs = 6.0e6;  // partial sums written, then read by the reduction
 constexpr double kReduceLaunchUs = 4.0;
+constexpr double kOverlap = 0.5;              // share of the faster of compute and streaming exposed
 constexpr int64_t kMaxTileSplit = 16;
 
 GemmChoice choose_tile(int64_t capacity, int64_t n, int64_t k) {
@@ -846,7 +851,7 @@ GemmChoice choose_tile(int64_t capacity, int64_t n, int64_t k) {
       const double compute = static_cast<double>(rounds) * 2.0 * shape.bm * shape.bn *
                              static_cast<double>(k_slice) / shape.flops_per_us;
       const double stream = 2.0 * static_cast<double>(n) * static_cast<double>(k) / kWeightBytesPerUs;
-      double cost = compute > stream ? compute : stream;
+      double cost = compute > stream ? compute + kOverlap * stream : stream + kOverlap * compute;
       if (split > 1) {
         cost += 8.0 * split * static_cast<double>(capacity) * static_cast<double>(n) / kPartialBytesPerUs +
                 kReduceLaunchUs;
@@ -863,10 +868,9 @@ GemmChoice choose_tile(int64_t capacity, int64_t n, int64_t k) {
 }  // namespace
 
 GemmChoice choose_gemm(int64_t capacity, int64_t n, int64_t k, bool gated) {
-  // The decode kernels address the weights through one 32-bit buffer range.
-  if (capacity <= 64 && n * k * 2 <= INT32_MAX) {
-    return capacity <= (gated ? kSplitMaxRowsGated : kSplitMaxRows) ? choose_split(n, k)
-                                                                     : choose_stream(capacity, n, k);
+  // The split and stream kernels address the weights through one 32-bit buffer range.
+  if (capacity <= kStreamMaxRows && n * k * 2 <= INT32_MAX) {
+    return capacity <= (gated ? kSplitMaxRowsGated : kSplitMaxRows) ? choose_split(n, k) : choose_stream(n, k);
   }
   return choose_tile(capacity, n, k);
 }
@@ -906,19 +910,18 @@ GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmCho
     kernel.grid = dim3(static_cast<unsigned>((row_blocks + per_group - 1) / per_group), 1, 1);
     kernel.block = dim3(64 * kSplitWaves, 1, 1);
   } else if (choice.kind == GemmKind::Stream) {
-    const int64_t tp = 16 << choice.variant;
     const int64_t groups = ((args.n + 15) / 16 + kStreamWaves - 1) / kStreamWaves;
     const int64_t slices = stream_slices(args.k, choice.k_slice);
-    kernel.func = gated ? stream_kernel<true>(choice.variant) : stream_kernel<false>(choice.variant);
+    kernel.func = gated ? stream_kernel<true>() : stream_kernel<false>();
     kernel.grid = dim3(static_cast<unsigned>(slices * groups), 1, 1);
     kernel.block = dim3(64 * kStreamWaves, 1, 1);
-    kernel.shmem = static_cast<unsigned>(tp * (choice.k_slice + 8) * 2);
+    kernel.shmem = static_cast<unsigned>(16 * (choice.k_slice + 8) * 2);
     // Dynamic LDS beyond 64 KB must be allowed per function (idempotent, set on first use).
-    static bool configured[2][3] = {};
-    if (!configured[gated][choice.variant]) {
+    static bool configured[2] = {};
+    if (!configured[gated]) {
       (void)hipFuncSetAttribute(kernel.func, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 static_cast<int>(kStreamLdsBytes));
-      configured[gated][choice.variant] = true;
+      configured[gated] = true;
     }
   } else {
     const TileShape &shape = kTileShapes[choice.variant];
@@ -946,7 +949,7 @@ std::string gemm_name(GemmChoice choice, bool gated) {
     return "split" + prefix + "_t16_k" + std::to_string(choice.k_split);
   }
   if (choice.kind == GemmKind::Stream) {
-    return "stream" + prefix + "_t" + std::to_string(16 << choice.variant);
+    return "stream" + prefix + "_t16";
   }
   const TileShape &shape = kTileShapes[choice.variant];
   std::string name = "tile" + prefix + "_" + std::to_string(shape.bm) + "x" + std::to_string(shape.bn);

@@ -142,19 +142,24 @@ def test_zero_weights_give_zero_output(device):
 
 def test_variant_selection_covers_every_family(device):
     assert _native.gemm_variant(1, 24576, 4096, True).startswith("split")
-    assert _native.gemm_variant(48, 24576, 4096, True).startswith("stream")
+    assert _native.gemm_variant(16, 24576, 4096, True).startswith("stream")
     assert _native.gemm_variant(2048, 24576, 4096, True).startswith("tile")
-    # the Qwen3-8B cases of test_qwen3_8b_projections reach every tile shape and a K split
-    chosen = {_native.gemm_variant(rows, n, k, gated) for rows in (128, 256, 512)
+    # the Qwen3-8B cases of test_qwen3_8b_projections reach every tile shape and K splits
+    chosen = {_native.gemm_variant(rows, n, k, gated) for rows in (32, 64, 128, 256, 512)
               for n, k, gated in ((24576, 4096, True), (4096, 12288, False))}
-    assert {"tile_gated_128x128", "tile_gated_256x128", "tile_gated_256x256", "tile_128x128_k8", "tile_256x128_k4"} <= chosen
+    assert {"tile_gated_64x128", "tile_gated_128x128", "tile_gated_256x128", "tile_gated_256x256", "tile_64x128_k8",
+            "tile_128x128_k8", "tile_256x128_k4"} <= chosen
 
 
 # Ragged geometries of the decode kernels: K not a multiple of their 512-column load
-# groups (a partial last K range), N not a multiple of 16 (weight rows past N), one to
-# many K ranges; few rows take the split kernel (gate_up <= 4, down <= 8), up to 64 the
-# stream kernel.
+# groups (a partial last K range) or of the tiles' 64-column slabs, N not a multiple of 16
+# (weight rows past N), one to many K ranges; few rows take the split kernel (gate_up
+# <= 4, down <= 8), up to 16 the stream kernel, from 17 the deep-staged small tiles.
 DECODE_SHAPES = [(1032, 1000), (2056, 9992), (4096, 12288), (264, 40)]
+
+
+def _decode_family(rows: int, split_rows: int) -> str:
+    return "split" if rows <= split_rows else ("stream" if rows <= 16 else "tile")
 
 
 @pytest.mark.parametrize("hidden,intermediate", DECODE_SHAPES)
@@ -163,8 +168,8 @@ def test_decode_projections_on_ragged_geometry(device, hidden, intermediate, row
     x = o.generate_hidden_states(rows, hidden, 17)
     w_gate_up, w_down = _layer(hidden, intermediate)
     gu_d, dn_d = to_device(w_gate_up, device), to_device(w_down, device)
-    assert _native.gemm_variant(rows, 2 * intermediate, hidden, True).startswith("split" if rows <= 4 else "stream")
-    assert _native.gemm_variant(rows, hidden, intermediate, False).startswith("split" if rows <= 8 else "stream")
+    assert _native.gemm_variant(rows, 2 * intermediate, hidden, True).startswith(_decode_family(rows, 4))
+    assert _native.gemm_variant(rows, hidden, intermediate, False).startswith(_decode_family(rows, 8))
     activated = dense.gate_up_silu(to_device(x, device), gu_d)
     out = dense.down(activated, dn_d)
     # A second call gives the identical bits (fixed-order K reduction).

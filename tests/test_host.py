@@ -190,10 +190,11 @@ def test_gemm_variant_selection():
     assert _native.gemm_variant(8, 4096, 12288, False) == "split_t16_k8"
     assert _native.gemm_variant(8, 24576, 4096, True) == "stream_gated_t16"
     assert _native.gemm_variant(16, 24576, 4096, True) == "stream_gated_t16"
-    assert _native.gemm_variant(32, 4096, 12288, False) == "stream_t32"
-    assert _native.gemm_variant(64, 4096, 12288, False) == "stream_t64"
+    assert _native.gemm_variant(16, 4096, 12288, False) == "stream_t16"
+    assert _native.gemm_variant(17, 24576, 4096, True).startswith("tile_gated_64x128")
+    assert _native.gemm_variant(64, 4096, 12288, False).startswith("tile_64x128_k")
     assert _native.gemm_workspace_bytes(1, 24576, 4096, True) == 0
-    assert _native.gemm_workspace_bytes(32, 4096, 12288, False) > 0
+    assert _native.gemm_workspace_bytes(16, 4096, 12288, False) > 0
     assert _native.gemm_variant(2048, 24576, 4096, True) == "tile_gated_256x256"
     assert _native.gemm_variant(4096, 4096, 12288, False).startswith("tile")
     assert _native.gemm_workspace_bytes(2048, 24576, 4096, True) == 0
