@@ -28,6 +28,9 @@
 
 #include "xp_kernels.hpp"
 
+#include <type_traits>
+#include <utility>
+
 namespace xp {
 namespace {
 
@@ -418,13 +421,26 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
 }
 
+// Calls f(std::integral_constant<int, 0>{}) .. f(std::integral_constant<int, N - 1>{}).
+template <class F, int... I>
+__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
 // Offset that is always past a tile resource's end (resources stay below 2^31 bytes).
 constexpr uint32_t kOutOfRange = 0x7ffffff0u;
 
 // BM x BN block tile, BK = 64, WAVES_M x WAVES_N waves (two per SIMD at 8 waves) each
 // owning a (BM / WAVES_M) x (BN / WAVES_N) tile of 32x32x16 MFMA accumulators.  STAGES
 // slabs of A and B live in LDS: while one is multiplied, the loads of the next STAGES - 1
-// are in flight.  Grid z splits K into ranges of `k_slice` columns; with more than one
+// are in flight.  With 8 waves only waves 0-3 load: the refill issued after each barrier
+// goes through the CU's one vector memory path at ~1 KB per 16 cycles and stalls the
+// waves issuing it, and a SIMD whose other wave does not load keeps its matrix pipe fed
+// meanwhile.  Grid z splits K into ranges of `k_slice` columns; with more than one
 // range each workgroup writes the fp32 partial tile of its range and
 // stream_reduce_kernel, launched next, adds the ranges in order and applies the epilogue.
 template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, bool GATED>
@@ -436,14 +452,19 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
   constexpr int MT = WTM / 32;
   constexpr int NT = WTN / 32;
   constexpr int KSTEPS = BK / 16;                  // 16-wide k steps per slab
-  constexpr int ROWS = BM + BN;                    // LDS rows per stage (A rows then B rows)
+  constexpr int ROWS = BM + BN;                    // LDS rows per stage
   constexpr int STAGE = ROWS * BK;                 // bf16 elements per stage
-  constexpr int A_LOADS = BM / 8 / WAVES;          // 1 KB (8-row) load instructions per wave per stage
-  constexpr int B_LOADS = BN / 8 / WAVES;
+  // LDS holds the A slabs of all stages, then the B slabs: a fragment read is then one
+  // per-lane base per k step and operand plus an immediate offset below 64 KB (except for
+  // A slabs past the first 64 KB), which keeps the address registers few.
+  constexpr int B_REGION = STAGES * BM * BK;
+  constexpr int LOAD_WAVES = WAVES == 8 ? 4 : WAVES;  // waves 0 .. LOAD_WAVES-1 fill the stages
+  constexpr int A_LOADS = BM / 8 / LOAD_WAVES;     // 1 KB (8-row) load instructions per loading wave per stage
+  constexpr int B_LOADS = BN / 8 / LOAD_WAVES;
   constexpr int LOADS = A_LOADS + B_LOADS;
   static_assert(MT >= 1 && NT >= 1, "wave tile must hold at least one 32x32 MFMA tile");
   static_assert(!GATED || NT % 2 == 0, "gated tiles need whole Gate/Up column groups per wave");
-  static_assert(BM % (8 * WAVES) == 0 && BN % (8 * WAVES) == 0, "stage rows must split evenly");
+  static_assert(BM % (8 * LOAD_WAVES) == 0 && BN % (8 * LOAD_WAVES) == 0, "stage rows must split evenly");
   static_assert(STAGES >= 2 && LOADS * (STAGES - 1) < 64, "in-flight loads must fit the vmcnt counter");
   static_assert(STAGES * STAGE * 2 <= 160 * 1024, "stages must fit the CU's LDS");
 
@@ -471,8 +492,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
   const int wm = wave % WAVES_M;
   const int wn = wave / WAVES_M;
 
-  // ---- loads: every wave fills A_LOADS 8-row groups of the A tile (rows from
-  // wave * BM / WAVES) and B_LOADS of the B tile, so which resource a load uses is a
+  // ---- loads: loading wave w fills A_LOADS 8-row groups of the A tile (rows from
+  // w * BM / LOAD_WAVES) and B_LOADS of the B tile, so which resource a load uses is a
   // compile-time fact.  Lane i of a load writes LDS row r0 + i / 8, physical chunk i % 8,
   // which holds logical k chunk (i % 8) ^ swizzle(row): the swizzle is applied by choosing
   // the global chunk.
@@ -486,8 +507,9 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
   // i takes row g + i / 8 and k chunk (i % 8) ^ swizzle(row).  Because g is a multiple of
   // 8, swizzle(g + i / 8) = (i / 16) ^ (4 if g / 8 is odd), so the per-lane part of every
   // offset takes one of two values and the group part is wave-uniform.
-  const int a_first = wave * (BM / WAVES);
-  const int b_first = BM + wave * (BN / WAVES);
+  const int a_first = (wave % LOAD_WAVES) * (BM / LOAD_WAVES);
+  const int b_first = BM + (wave % LOAD_WAVES) * (BN / LOAD_WAVES);
+  const bool loading_wave = wave < LOAD_WAVES;
   const int row_in_load = lane >> 3;
   const int lane_chunk[2] = {(lane & 7) ^ (row_in_load >> 1), (lane & 7) ^ (row_in_load >> 1) ^ 4};
   // B rows of a gated tile are permuted: LDS row p = wq * G + s * G / 2 + jj (G = BN /
@@ -509,7 +531,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
     const uint32_t k_bytes = static_cast<uint32_t>(k_pos * 2);
     // 16-byte chunks of this slab that lie inside the range (8 except in a ragged last slab).
     const int64_t chunks_left = (k_end - k_pos) >> 3;
-    uint16_t *base = lds + stage * STAGE;
+    uint16_t *a_stage = lds + stage * BM * BK;
+    uint16_t *b_stage = lds + B_REGION + stage * BN * BK - BM * BK;  // indexed by g >= BM
     // The scalar offset must stay wave-uniform; masking goes through the per-lane offset
     // (kOutOfRange + k_bytes is still past the resource end), as a select, not a branch.
     // A and B loads are separate loops so that each names one resource.
@@ -518,7 +541,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
       const int g = a_first + q * 8;
       const int chunk = lane_chunk[(g >> 3) & 1];
       const uint32_t offset = static_cast<uint32_t>(((g + row_in_load) * a.ldx + chunk * 8) * 2);
-      buffer_load_lds16(a_rsrc, base + g * BK, chunk < chunks_left ? offset : kOutOfRange, k_bytes);
+      buffer_load_lds16(a_rsrc, a_stage + g * BK, chunk < chunks_left ? offset : kOutOfRange, k_bytes);
     }
 #pragma unroll
     for (int q = 0; q < B_LOADS; ++q) {
@@ -526,7 +549,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
       const int chunk = lane_chunk[(g >> 3) & 1];
       const int weight_row = b_group_row(g - BM) + B_ROW_STEP * row_in_load;
       const uint32_t offset = static_cast<uint32_t>((weight_row * a.k + chunk * 8) * 2);
-      buffer_load_lds16(b_rsrc, base + g * BK, chunk < chunks_left ? offset : kOutOfRange, k_bytes);
+      buffer_load_lds16(b_rsrc, b_stage + g * BK, chunk < chunks_left ? offset : kOutOfRange, k_bytes);
     }
   };
 
@@ -552,19 +575,48 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
   for (int ks = 0; ks < KSTEPS; ++ks) {
     frag_lane[ks] = frag_row * BK + (((ks * 2 + frag_half) ^ swizzle(frag_row)) << 3);
   }
-  const int a_frag_base = wm * WTM * BK;
-  const int b_frag_base = BM * BK + wn * WTN * BK;
-  bf16x8 af[2][MT];
-  bf16x8 bfrag[2][NT];
+  // Per-lane LDS byte bases of the fragment reads: one per k step, operand and 64 KB window
+  // that the operand's stages reach.  They are opaque to the compiler, so every other term
+  // of a read's address (stage, fragment, window remainder) goes into the instruction's
+  // 16-bit offset instead of a register of its own.
+  constexpr int A_SPAN = (STAGES - 1) * BM * BK * 2 + (MT - 1) * 32 * BK * 2;  // largest constant A offset
+  constexpr int B_SPAN = B_REGION * 2 + (STAGES - 1) * BN * BK * 2 + (NT - 1) * 32 * BK * 2;
+  constexpr int A_WINDOWS = A_SPAN / 65536 + 1;
+  constexpr int B_WINDOWS = B_SPAN / 65536 + 1;
+  uint32_t a_base[A_WINDOWS][KSTEPS];
+  uint32_t b_base[B_WINDOWS][KSTEPS];
+#pragma unroll
+  for (int ks = 0; ks < KSTEPS; ++ks) {
+#pragma unroll
+    for (int w = 0; w < A_WINDOWS; ++w) {
+      a_base[w][ks] = static_cast<uint32_t>((frag_lane[ks] + wm * WTM * BK) * 2 + w * 65536);
+      __asm__ volatile("" : "+v"(a_base[w][ks]));
+    }
+#pragma unroll
+    for (int w = 0; w < B_WINDOWS; ++w) {
+      b_base[w][ks] = static_cast<uint32_t>((frag_lane[ks] + wn * WTN * BK) * 2 + w * 65536);
+      __asm__ volatile("" : "+v"(b_base[w][ks]));
+    }
+  }
+  const char *lds_bytes = reinterpret_cast<const char *>(lds);
+  // Three fragment slots: the fragments of k step g live in slot g % 3 and are read two k
+  // steps ahead of their MFMAs, so a wave running alone on its SIMD (its partner blocked on
+  // the barrier or on issuing loads) does not wait on LDS latency.
+  static_assert(KSTEPS == 4, "the slab schedule below is written for four k steps");
+  bf16x8 af[3][MT];
+  bf16x8 bfrag[3][NT];
   auto read_fragments = [&](int stage, int ks, int slot) {
-    const uint16_t *base = lds + stage * STAGE;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      af[slot][mt] = as_bf16x8(load16(base + a_frag_base + mt * 32 * BK + frag_lane[ks]));
+      const int offset = stage * BM * BK * 2 + mt * 32 * BK * 2;
+      af[slot][mt] = as_bf16x8(
+          *reinterpret_cast<const u32x4 *>(lds_bytes + a_base[offset >> 16][ks] + (offset & 0xffff)));
     }
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      bfrag[slot][nt] = as_bf16x8(load16(base + b_frag_base + nt * 32 * BK + frag_lane[ks]));
+      const int offset = B_REGION * 2 + stage * BN * BK * 2 + nt * 32 * BK * 2;
+      bfrag[slot][nt] = as_bf16x8(
+          *reinterpret_cast<const u32x4 *>(lds_bytes + b_base[offset >> 16][ks] + (offset & 0xffff)));
     }
   };
   auto mfma_step = [&](int slot) {
@@ -574,13 +626,6 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
       for (int nt = 0; nt < NT; ++nt) {
         acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[slot][mt], bfrag[slot][nt], acc[mt][nt], 0, 0, 0);
       }
-    }
-  };
-  auto inner_steps = [&](int stage) {
-#pragma unroll
-    for (int ks = 0; ks + 1 < KSTEPS; ++ks) {
-      read_fragments(stage, ks + 1, (ks + 1) & 1);
-      mfma_step(ks & 1);
     }
   };
   // Workgroup barrier for the stage ring.  Before it each wave waits for its loads of the
@@ -599,36 +644,86 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
   // The chooser never makes an empty K range, so every workgroup runs at least one slab.
   const int64_t ktiles = (k_end - k_begin + BK - 1) / BK;
   // Prologue: slabs 0 .. STAGES-1 in flight, wait for slab 0, read its first fragments.
+  if (loading_wave) {
 #pragma unroll
-  for (int s = 0; s < STAGES; ++s) {
-    issue_loads(s, s);
+    for (int s = 0; s < STAGES; ++s) {
+      issue_loads(s, s);
+    }
   }
   wait_vmcnt<LOADS * (STAGES - 1)>();
   __syncthreads();
   read_fragments(0, 0, 0);
+  read_fragments(0, 1, 1);
 
-  int stage = 0;
-  for (int64_t kt = 0; kt + 1 < ktiles; ++kt) {
-    inner_steps(stage);
-    // After the barrier slab kt+1 is in LDS and nobody reads this stage any more.  The last
-    // k step's MFMAs then run interleaved with the reads of slab kt+1's first fragments and
-    // the refill of this stage with slab kt+STAGES (zeros past the range end), keeping the
-    // matrix pipe busy while the loads issue.
+  // Slab kt runs k steps 4 kt .. 4 kt + 3 from stage kt % STAGES, its fragment slots
+  // starting at phase kt % 3.  After k step 1 every fragment of the slab has been read, so
+  // the stage barrier sits there: past it slab kt+1 is in LDS (its first two fragment sets
+  // are read during k steps 2 and 3) and this stage may be refilled with slab kt+STAGES
+  // (zeros past the range end), which the loading waves issue interleaved with k step 2's
+  // MFMAs.  The loop is unrolled over lcm(3, STAGES) slabs so that slots and stages, and
+  // with them every LDS address but one per-lane term per k step, are compile-time
+  // constants.  The loading and the other waves run the same loop (the same barriers),
+  // with and without the refills, as separate code so that each has a fixed interleave.
+  constexpr int UNROLL = STAGES % 3 == 0 ? STAGES : 3 * STAGES;
+  auto slab = [&](auto index, auto loads, int64_t kt) {
+    constexpr int P = decltype(index)::value % 3;
+    constexpr int S = decltype(index)::value % STAGES;
+    constexpr int NEXT = (S + 1) % STAGES;
+    constexpr bool LOADING = decltype(loads)::value;
+    read_fragments(S, 2, (P + 2) % 3);
+    mfma_step(P);
+    __builtin_amdgcn_sched_barrier(0);
+    read_fragments(S, 3, P);
+    mfma_step((P + 1) % 3);
     stage_barrier();
-    const int next = stage + 1 == STAGES ? 0 : stage + 1;
-    read_fragments(next, 0, 0);
-    issue_loads(kt + STAGES, stage);
-    mfma_step((KSTEPS - 1) & 1);
+    read_fragments(NEXT, 0, (P + 1) % 3);
+    if constexpr (LOADING) {
+      issue_loads(kt + STAGES, S);
+    }
+    mfma_step((P + 2) % 3);
 #pragma unroll
     for (int i = 0; i < MT * NT; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
-      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one memory load
+      if constexpr (LOADING) {
+        __builtin_amdgcn_sched_group_barrier(0x020, (LOADS + MT * NT - 1) / (MT * NT), 0);  // memory loads
+      }
     }
-    stage = next;
+    __builtin_amdgcn_sched_barrier(0);
+    read_fragments(NEXT, 1, (P + 2) % 3);
+    mfma_step(P);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  int64_t kt = 0;
+  auto main_loop = [&](auto loads) {
+    for (; kt + UNROLL < ktiles; kt += UNROLL) {
+      static_for<UNROLL>([&](auto j) { slab(j, loads, kt + decltype(j)::value); });
+    }
+    // The remaining slabs before the last (fewer than UNROLL), continuing the pattern.
+    static_for<UNROLL - 1>([&](auto j) {
+      if (kt + decltype(j)::value + 1 < ktiles) {
+        slab(j, loads, kt + decltype(j)::value);
+      }
+    });
+  };
+  if (loading_wave) {
+    main_loop(std::true_type{});
+  } else {
+    main_loop(std::false_type{});
   }
-  inner_steps(stage);
-  mfma_step((KSTEPS - 1) & 1);
+  // Last slab (index ktiles - 1): no barrier and no refill.
+  static_for<UNROLL>([&](auto j) {
+    if ((ktiles - 1) % UNROLL == decltype(j)::value) {
+      constexpr int P = decltype(j)::value % 3;
+      constexpr int S = decltype(j)::value % STAGES;
+      read_fragments(S, 2, (P + 2) % 3);
+      mfma_step(P);
+      read_fragments(S, 3, P);
+      mfma_step((P + 1) % 3);
+      mfma_step((P + 2) % 3);
+      mfma_step(P);
+    }
+  });
   // Past-the-end refills may still be landing in the stage buffers the epilogue reuses.
   __builtin_amdgcn_s_waitcnt(0);
 
