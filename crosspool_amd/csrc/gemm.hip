@@ -892,71 +892,84 @@ const void *tile_kernel(int variant) {
 
 constexpr int kComputeUnits = 256;
 
-// Live rows up to which the split kernel (token fragments from L2) beats the stream
-// kernel (token slice staged in LDS): its token traffic grows with the rows while the
-// stream kernel pays for staging, partial sums and the reduction launch.  Measured on
-// the Qwen3-8B projections: gate_up (few long rows of K = 4096, a one-workgroup-per-CU
-// grid) crosses over after 4 rows, down (K = 12288 split 8 ways) after 8.
-constexpr int64_t kSplitMaxRowsGated = 4;
+// Decode sizes (up to 16 rows) take the split or the stream kernel, whichever a cost model
+// in microseconds prefers.  Both stream the weights with 8-wave workgroups, one per CU, at
+// a rate per workgroup (split ~24 GB/s, stream ~28 GB/s: measured, the chip rate scales
+// with the workgroup count), so a grid of few workgroups is the thing to avoid (Qwen3-4B
+// down through the split kernel has 80 workgroups: 24 us; sliced through the stream
+// kernel, 200: 15 us), and workgroups past 256 run as a second round.  The split kernel
+// reads its token fragments from L2, which costs ~0.8 us per row past the first; the
+// stream kernel's K slices cost the reduction launch (~6 us) and their partial traffic.
+// Fitted to forced split / stream timings of the Qwen3 0.6B / 4B / 8B / 32B-shard
+// projections at 1 to 16 rows (weights streamed from HBM): it picks the faster kernel or
+// one within 10 % of it, except two cases within 23 %.
+constexpr int64_t kDecodeMaxRows = 16;
 constexpr int64_t kSplitMaxRows = 8;
-// Rows up to which the stream kernel beats the deep-staged 64 x 128 tile (measured on the
-// Qwen3 4B / 8B / 32B-shard projections with weights streamed from HBM: even at 16 rows,
-// from 17 the tile wins).
+constexpr double kSplitWorkgroupBytesPerUs = 24.0e3;
+constexpr double kStreamWorkgroupBytesPerUs = 28.0e3;
+constexpr double kDecodeFixedUs = 2.0;
+constexpr double kSplitRowUs = 0.8;
+constexpr double kStreamReduceUs = 6.0;
+constexpr double kStreamPartialBytesPerUs = 6.0e6;
 constexpr int kSplitDepth = 4;
 
-// K split of the split kernel.  Its load registers (170 VGPRs) leave room for one 8-wave
-// workgroup per CU, and 8 waves with DEPTH chunks in flight already cover the HBM
-// latency, so the choice is the largest K split (1, 2, 4 or 8 ranges per 16-row block)
-// that still fits the grid in the fewest rounds of 256 workgroups, with every range
-// holding columns and a whole number of load groups.
-GemmChoice choose_split(int64_t n, int64_t k) {
-  const int64_t quantum = 128 * kSplitDepth;
-  const int64_t row_blocks = (n + 15) / 16;
-  auto rounds = [&](int64_t ksplit) {
-    const int64_t groups = (row_blocks * ksplit + kSplitWaves - 1) / kSplitWaves;
-    return (groups + kComputeUnits - 1) / kComputeUnits;
-  };
-  auto slice = [&](int64_t ksplit) { return ((k + ksplit - 1) / ksplit + quantum - 1) / quantum * quantum; };
-  int64_t ksplit = 1;
-  while (ksplit < kSplitWaves && rounds(2 * ksplit) <= rounds(1) && (2 * ksplit - 1) * slice(2 * ksplit) < k) {
-    ksplit *= 2;
-  }
-  return {GemmKind::Split, 0, slice(ksplit), ksplit};
+double decode_stream_us(int64_t n, int64_t k, int64_t workgroups, double workgroup_bytes_per_us) {
+  const int64_t rounds = (workgroups + kComputeUnits - 1) / kComputeUnits;
+  const double bytes_per_workgroup = 2.0 * static_cast<double>(n) * static_cast<double>(k) / workgroups;
+  return static_cast<double>(rounds) * bytes_per_workgroup / workgroup_bytes_per_us + kDecodeFixedUs;
 }
 
-constexpr int64_t kStreamMaxRows = 16;
+// Candidate K splits of the split kernel (1, 2, 4 or 8 ranges per 16-row block, each range
+// a whole number of load groups and none empty) and their modelled cost at `capacity` rows.
+GemmChoice choose_split(int64_t capacity, int64_t n, int64_t k, double &cost) {
+  const int64_t quantum = 128 * kSplitDepth;
+  const int64_t row_blocks = (n + 15) / 16;
+  GemmChoice best{GemmKind::Split, 0, 0, 1};
+  cost = -1.0;
+  for (int64_t ksplit = 1; ksplit <= kSplitWaves; ksplit *= 2) {
+    const int64_t slice = ((k + ksplit - 1) / ksplit + quantum - 1) / quantum * quantum;
+    if ((ksplit - 1) * slice >= k) {
+      break;
+    }
+    const int64_t workgroups = (row_blocks * ksplit + kSplitWaves - 1) / kSplitWaves;
+    const double us =
+        decode_stream_us(n, k, workgroups, kSplitWorkgroupBytesPerUs) + kSplitRowUs * static_cast<double>(capacity - 1);
+    if (cost < 0.0 || us < cost) {
+      best = {GemmKind::Split, 0, slice, ksplit};
+      cost = us;
+    }
+  }
+  return best;
+}
+
 constexpr int64_t kStreamLdsBytes = 160 * 1024;
 constexpr int64_t kStreamSliceQuantum = 128 * kStreamDepth;  // a whole number of load groups
 
 int64_t stream_slices(int64_t k, int64_t k_slice) { return (k + k_slice - 1) / k_slice; }
 
-// K slice of the stream kernel.  The whole of K when the staged token rows fit LDS: the
-// reduction launch a sliced projection adds costs more than the unfilled CUs (measured on
-// gate_up, K = 4096: 192 one-slice workgroups beat 768 quarter slices plus the reduction).
-// Otherwise workgroups (8 row blocks x one slice) are spread over the 256 CUs, the busiest
-// CU streams ceil(workgroups / 256) slices of 128 weight rows, and the slice length
-// minimising that load wins, ties going to fewer slices (less partial traffic).
-GemmChoice choose_stream(int64_t n, int64_t k) {
+// K slice of the stream kernel: workgroups are (8 row blocks) x (one slice), and the slice
+// count minimising the modelled cost wins.
+GemmChoice choose_stream(int64_t capacity, int64_t n, int64_t k, double &cost) {
   constexpr int64_t tp = 16;  // staged token rows
   const int64_t groups = ((n + 15) / 16 + kStreamWaves - 1) / kStreamWaves;
-  int64_t best_slice = 0;
-  int64_t best_load = 0;
+  GemmChoice best{GemmKind::Stream, 0, 0, 1};
+  cost = -1.0;
   for (int64_t slices = 1; slices <= 64; ++slices) {
     const int64_t k_slice = ((k + slices - 1) / slices + kStreamSliceQuantum - 1) / kStreamSliceQuantum *
                             kStreamSliceQuantum;
     if (tp * (k_slice + 8) * 2 > kStreamLdsBytes || stream_slices(k, k_slice) != slices) {
       continue;  // does not fit LDS, or the same slice length as fewer slices
     }
-    if (slices == 1) {
-      return {GemmKind::Stream, 0, k_slice, 1};
+    double us = decode_stream_us(n, k, slices * groups, kStreamWorkgroupBytesPerUs);
+    if (slices > 1) {
+      us += kStreamReduceUs + 8.0 * static_cast<double>(slices * capacity * n) / kStreamPartialBytesPerUs;
     }
-    const int64_t load = (slices * groups + kComputeUnits - 1) / kComputeUnits * k_slice;
-    if (best_slice == 0 || load < best_load) {
-      best_slice = k_slice;
-      best_load = load;
+    if (cost < 0.0 || us < cost) {
+      best = {GemmKind::Stream, 0, k_slice, 1};
+      cost = us;
     }
   }
-  return {GemmKind::Stream, 0, best_slice, 1};
+  return best;
 }
 
 // Tile shape and K split for a projection at `capacity` rows, from a cost model in
@@ -1006,8 +1019,17 @@ GemmChoice choose_tile(int64_t capacity, int64_t n, int64_t k) {
 
 GemmChoice choose_gemm(int64_t capacity, int64_t n, int64_t k, bool gated) {
   // The split and stream kernels address the weights through one 32-bit buffer range.
-  if (capacity <= kStreamMaxRows && n * k * 2 <= INT32_MAX) {
-    return capacity <= (gated ? kSplitMaxRowsGated : kSplitMaxRows) ? choose_split(n, k) : choose_stream(n, k);
+  if (capacity <= kDecodeMaxRows && n * k * 2 <= INT32_MAX) {
+    double stream_us = 0.0;
+    const GemmChoice stream = choose_stream(capacity, n, k, stream_us);
+    if (capacity <= kSplitMaxRows) {
+      double split_us = 0.0;
+      const GemmChoice split = choose_split(capacity, n, k, split_us);
+      if (split_us < stream_us) {
+        return split;
+      }
+    }
+    return stream;
   }
   return choose_tile(capacity, n, k);
 }

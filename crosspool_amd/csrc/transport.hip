@@ -33,7 +33,8 @@ __global__ __launch_bounds__(256) void copy_bytes_kernel(CopyArgs a) {
 }
 
 // One wavefront per row; CHUNKS 16-byte chunks per lane stay in registers between the
-// sum-of-squares reduction and the normalised store (hidden <= CHUNKS * 512).
+// sum-of-squares reduction and the normalised store (hidden <= CHUNKS * 512).  The norm
+// weight is loaded together with the row, so a row costs one memory round trip, not two.
 template <int CHUNKS>
 __global__ __launch_bounds__(256) void gather_rows_kernel(GatherArgs a) {
   const int lane = threadIdx.x & (kWave - 1);
@@ -57,10 +58,12 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(GatherArgs a) {
   }
   const uint16_t *source = a.pool + static_cast<int64_t>(slot) * a.hidden;
   u32x4 values[CHUNKS];
+  u32x4 weights[CHUNKS];
 #pragma unroll
   for (int index = 0; index < CHUNKS; ++index) {
     const int64_t chunk = lane + index * kWave;
     values[index] = chunk < chunks ? load16(source + chunk * 8) : u32x4{0u, 0u, 0u, 0u};
+    weights[index] = chunk < chunks && a.norm != nullptr ? load16(a.norm + chunk * 8) : u32x4{0u, 0u, 0u, 0u};
   }
   if (a.norm == nullptr) {
 #pragma unroll
@@ -89,7 +92,7 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(GatherArgs a) {
   for (int index = 0; index < CHUNKS; ++index) {
     const int64_t chunk = lane + index * kWave;
     if (chunk < chunks) {
-      const u32x4 weight = load16(a.norm + chunk * 8);
+      const u32x4 weight = weights[index];
       u32x4 result;
 #pragma unroll
       for (int word = 0; word < 4; ++word) {

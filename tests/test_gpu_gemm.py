@@ -153,23 +153,29 @@ def test_variant_selection_covers_every_family(device):
 
 # Ragged geometries of the decode kernels: K not a multiple of their 512-column load
 # groups (a partial last K range) or of the tiles' 64-column slabs, N not a multiple of 16
-# (weight rows past N), one to many K ranges; few rows take the split kernel (gate_up
-# <= 4, down <= 8), up to 16 the stream kernel, from 17 the deep-staged small tiles.
+# (weight rows past N), one to many K ranges.  Up to 16 rows a cost model picks the split
+# or the stream kernel, from 17 the deep-staged small tiles; both decode kernels must
+# occur on these shapes.
 DECODE_SHAPES = [(1032, 1000), (2056, 9992), (4096, 12288), (264, 40)]
+DECODE_ROWS = [1, 3, 4, 5, 8, 9, 16, 17, 32, 33, 64]
 
 
-def _decode_family(rows: int, split_rows: int) -> str:
-    return "split" if rows <= split_rows else ("stream" if rows <= 16 else "tile")
+def test_decode_shapes_reach_both_decode_kernels(device):
+    chosen = {_native.gemm_variant(rows, n, k, gated).split("_")[0] for hidden, intermediate in DECODE_SHAPES
+              for rows in DECODE_ROWS if rows <= 16
+              for n, k, gated in ((2 * intermediate, hidden, True), (hidden, intermediate, False))}
+    assert chosen == {"split", "stream"}
 
 
 @pytest.mark.parametrize("hidden,intermediate", DECODE_SHAPES)
-@pytest.mark.parametrize("rows", [1, 3, 4, 5, 8, 9, 16, 17, 32, 33, 64])
+@pytest.mark.parametrize("rows", DECODE_ROWS)
 def test_decode_projections_on_ragged_geometry(device, hidden, intermediate, rows):
     x = o.generate_hidden_states(rows, hidden, 17)
     w_gate_up, w_down = _layer(hidden, intermediate)
     gu_d, dn_d = to_device(w_gate_up, device), to_device(w_down, device)
-    assert _native.gemm_variant(rows, 2 * intermediate, hidden, True).startswith(_decode_family(rows, 4))
-    assert _native.gemm_variant(rows, hidden, intermediate, False).startswith(_decode_family(rows, 8))
+    family = ("split", "stream") if rows <= 16 else ("tile",)
+    assert _native.gemm_variant(rows, 2 * intermediate, hidden, True).startswith(family)
+    assert _native.gemm_variant(rows, hidden, intermediate, False).startswith(family)
     activated = dense.gate_up_silu(to_device(x, device), gu_d)
     out = dense.down(activated, dn_d)
     # A second call gives the identical bits (fixed-order K reduction).

@@ -186,11 +186,16 @@ def test_abi_rejects_invalid_arguments_before_touching_the_device():
 
 
 def test_gemm_variant_selection():
-    assert _native.gemm_variant(1, 24576, 4096, True) == "split_gated_t16_k1"
-    assert _native.gemm_variant(8, 4096, 12288, False) == "split_t16_k8"
-    assert _native.gemm_variant(8, 24576, 4096, True) == "stream_gated_t16"
+    # decode sizes: the split or the stream kernel by the cost model, never a tile
+    for rows in (1, 2, 4, 8, 16):
+        for n, k, gated in ((24576, 4096, True), (4096, 12288, False), (19456, 2560, True), (2560, 9728, False)):
+            assert _native.gemm_variant(rows, n, k, gated).startswith(("split", "stream"))
+    assert _native.gemm_variant(1, 4096, 12288, False) == "split_t16_k8"
     assert _native.gemm_variant(16, 24576, 4096, True) == "stream_gated_t16"
-    assert _native.gemm_variant(16, 4096, 12288, False) == "stream_t16"
+    # Qwen3-4B down: the split kernel would leave 80 workgroups for 256 CUs; the stream
+    # kernel slices K instead
+    assert _native.gemm_variant(1, 2560, 9728, False) == "stream_t16"
+    assert _native.gemm_workspace_bytes(1, 2560, 9728, False) > 0
     assert _native.gemm_variant(17, 24576, 4096, True).startswith("tile_gated_64x128")
     assert _native.gemm_variant(64, 4096, 12288, False).startswith("tile_64x128_k")
     assert _native.gemm_workspace_bytes(1, 24576, 4096, True) == 0
