@@ -221,7 +221,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) void split_gemm_kernel(GemmArgs a
 constexpr int kStreamWaves = 8;
 constexpr int kStreamDepth = 4;
 
-template <int TB, bool GATED>
+template <int TB, bool GATED, bool GATHER>
 __global__ __launch_bounds__(64 * kStreamWaves) void stream_gemm_kernel(GemmArgs a) {
   constexpr int TP = 16 * TB;
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
@@ -240,25 +240,6 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_gemm_kernel(GemmArgs
   const int64_t rs = ks + 8;  // LDS row stride in elements
   const u32x4 zero = {0u, 0u, 0u, 0u};
 
-  // Stage activations [0, TP) x [k0, k0 + ks) of this slice.  Rows past the live rows read
-  // as zero through the buffer range; columns past K are zeroed explicitly.
-  const __amdgpu_buffer_rsrc_t x_rsrc = make_rsrc(a.x, static_cast<uint32_t>(a.rows * a.ldx * 2));
-  const int vectors_per_row = static_cast<int>(ks / 8);
-  const int ldx = static_cast<int>(a.ldx);
-  const int kbase = static_cast<int>(k0);
-  const int kvalid = static_cast<int>(klen);
-  for (int index = threadIdx.x; index < TP * vectors_per_row; index += 64 * kStreamWaves) {
-    const int t = index / vectors_per_row;
-    const int c = index - t * vectors_per_row;
-    u32x4 value = buffer_load16(x_rsrc, static_cast<uint32_t>((t * ldx + kbase + c * 8) * 2));
-    value = c * 8 < kvalid ? value : zero;
-    store16(xs + t * rs + c * 8, value);
-  }
-  __syncthreads();
-  if (rb >= row_blocks) {
-    return;
-  }
-
   // Every slice runs ks / 128 chunks (a multiple of DEPTH, so the loop has no partial
   // group): weight loads go through a buffer resource over all N rows, rows past N read
   // as zero, and all loads are unconditional, which lets the wait counts track exactly
@@ -266,7 +247,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_gemm_kernel(GemmArgs
   const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(a.w, static_cast<uint32_t>(a.n * a.k * 2));
   const uint32_t w_off = static_cast<uint32_t>(((rb * 16 + r16) * a.k + k0 + kq * 8) * 2);
   const int chunks = static_cast<int>(ks / 128);
-  const int lane_valid = kvalid - kq * 8;
+  const int lane_valid = static_cast<int>(klen) - kq * 8;
   // Waves start at different chunks of the slice (a stride-7 rotation by row block), so the
   // concurrently streamed addresses spread over the memory channels instead of every wave
   // reading the same column range of its rows at the same time.
@@ -281,6 +262,131 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_gemm_kernel(GemmArgs
       w[s] = buffer_load16(w_rsrc, w_off + static_cast<uint32_t>((column + s * 32) * 2));
     }
   };
+  // The first DEPTH chunks of weights are requested before the activations are staged, so
+  // their latency overlaps the staging (for the fused gather, several dependent round trips).
+  if (rb < row_blocks) {
+#pragma unroll
+    for (int d = 0; d < kStreamDepth; ++d) {
+      load_chunk(d, wbuf[d]);
+    }
+  }
+
+  // Stage activations [0, TP) x [k0, k0 + ks) of this slice.  Rows past the live rows read
+  // as zero; columns past K are zeroed explicitly.
+  const int vectors_per_row = static_cast<int>(ks / 8);
+  const int ldx = static_cast<int>(a.ldx);
+  const int kbase = static_cast<int>(k0);
+  const int kvalid = static_cast<int>(klen);
+  if constexpr (GATHER) {
+    // Fused mailbox gather: wave w finds rows w, w + 8 of the slot list and their inverse
+    // RMS over the whole row (the gather kernel's wavefront reduction, so the same bits),
+    // then the slice is staged from the mailbox rows, normalised.  Loads are issued in
+    // batches of independent requests before their results are used, so the dependent
+    // round trips are few (slot, row, and the staging reads).
+    constexpr int ROWS_PER_WAVE = TP / kStreamWaves;
+    constexpr int BATCH = 8;  // 16-byte chunks per lane and row in flight
+    __shared__ float row_scale[TP];
+    __shared__ int64_t row_source[TP];  // mailbox row; -1 past the live rows, -2 bad slot
+    int64_t sources[ROWS_PER_WAVE];
+#pragma unroll
+    for (int r = 0; r < ROWS_PER_WAVE; ++r) {
+      const int t = wave + r * kStreamWaves;
+      sources[r] = -1;
+      if (t < a.rows) {
+        const int32_t slot = a.gather_slots[t];
+        sources[r] = slot < 0 || static_cast<int64_t>(slot) >= a.pool_rows ? -2 : slot;
+      }
+    }
+    float squares[ROWS_PER_WAVE];
+#pragma unroll
+    for (int r = 0; r < ROWS_PER_WAVE; ++r) {
+      squares[r] = 0.0f;
+    }
+    const int64_t row_chunks = a.k / 8;
+    if (a.norm != nullptr) {
+      for (int64_t first = lane; first < row_chunks; first += BATCH * kWave) {
+        u32x4 values[ROWS_PER_WAVE][BATCH];
+#pragma unroll
+        for (int r = 0; r < ROWS_PER_WAVE; ++r) {
+#pragma unroll
+          for (int b = 0; b < BATCH; ++b) {
+            const int64_t chunk = first + b * kWave;
+            values[r][b] = sources[r] >= 0 && chunk < row_chunks ? load16(a.x + sources[r] * a.ldx + chunk * 8) : zero;
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < ROWS_PER_WAVE; ++r) {
+#pragma unroll
+          for (int b = 0; b < BATCH; ++b) {
+            add_squares(values[r][b], squares[r]);  // chunk order lane, lane + 64, ...
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < ROWS_PER_WAVE; ++r) {
+      const int t = wave + r * kStreamWaves;
+      const float scale = a.norm != nullptr && sources[r] >= 0 ? rms_inverse(squares[r], a.k, a.eps) : 1.0f;
+      if (lane == 0) {
+        row_scale[t] = scale;
+        row_source[t] = sources[r];
+        if (sources[r] == -2 && blockIdx.x == 0) {
+          raise_fault(a.fault, kFaultSlotOutOfRange);
+        }
+      }
+    }
+    __syncthreads();
+    const u32x4 poison = {kPoisonBf16x2, kPoisonBf16x2, kPoisonBf16x2, kPoisonBf16x2};
+    constexpr int STAGE_BATCH = 4;
+    const int items = TP * vectors_per_row;
+    for (int first = threadIdx.x; first < items; first += STAGE_BATCH * 64 * kStreamWaves) {
+      u32x4 x_chunk[STAGE_BATCH];
+      u32x4 w_chunk[STAGE_BATCH];
+#pragma unroll
+      for (int u = 0; u < STAGE_BATCH; ++u) {
+        const int index = first + u * 64 * kStreamWaves;
+        const int t = index / vectors_per_row;
+        const int c = index - t * vectors_per_row;
+        const int64_t source = index < items ? row_source[t] : -1;
+        const bool live = source >= 0 && c * 8 < kvalid;
+        x_chunk[u] = live ? load16(a.x + source * a.ldx + kbase + c * 8) : zero;
+        w_chunk[u] = live && a.norm != nullptr ? load16(a.norm + kbase + c * 8) : zero;
+      }
+#pragma unroll
+      for (int u = 0; u < STAGE_BATCH; ++u) {
+        const int index = first + u * 64 * kStreamWaves;
+        if (index >= items) {
+          continue;
+        }
+        const int t = index / vectors_per_row;
+        const int c = index - t * vectors_per_row;
+        const int64_t source = row_source[t];
+        u32x4 value = zero;
+        if (c * 8 < kvalid) {
+          if (source >= 0) {
+            value = a.norm != nullptr ? normalize_chunk(x_chunk[u], row_scale[t], w_chunk[u]) : x_chunk[u];
+          } else if (source == -2) {
+            value = poison;
+          }
+        }
+        store16(xs + t * rs + c * 8, value);
+      }
+    }
+  } else {
+    const __amdgpu_buffer_rsrc_t x_rsrc = make_rsrc(a.x, static_cast<uint32_t>(a.rows * a.ldx * 2));
+    for (int index = threadIdx.x; index < TP * vectors_per_row; index += 64 * kStreamWaves) {
+      const int t = index / vectors_per_row;
+      const int c = index - t * vectors_per_row;
+      u32x4 value = buffer_load16(x_rsrc, static_cast<uint32_t>((t * ldx + kbase + c * 8) * 2));
+      value = c * 8 < kvalid ? value : zero;
+      store16(xs + t * rs + c * 8, value);
+    }
+  }
+  __syncthreads();
+  if (rb >= row_blocks) {
+    return;
+  }
+
   f32x4 acc[TB];
 #pragma unroll
   for (int tb = 0; tb < TB; ++tb) {
@@ -299,10 +405,6 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_gemm_kernel(GemmArgs
     }
   };
 
-#pragma unroll
-  for (int d = 0; d < kStreamDepth; ++d) {
-    load_chunk(d, wbuf[d]);
-  }
   int c0 = 0;
   for (; c0 < chunks - kStreamDepth; c0 += kStreamDepth) {
 #pragma unroll
@@ -857,9 +959,9 @@ const void *split_kernel() {
   return reinterpret_cast<const void *>(&split_gemm_kernel<1, 4, GATED>);
 }
 
-template <bool GATED>
+template <bool GATED, bool GATHER = false>
 const void *stream_kernel() {
-  return reinterpret_cast<const void *>(&stream_gemm_kernel<1, GATED>);
+  return reinterpret_cast<const void *>(&stream_gemm_kernel<1, GATED, GATHER>);
 }
 
 struct TileShape {
@@ -897,26 +999,30 @@ constexpr int kComputeUnits = 256;
 // a rate per workgroup (split ~24 GB/s, stream ~28 GB/s: measured, the chip rate scales
 // with the workgroup count), so a grid of few workgroups is the thing to avoid (Qwen3-4B
 // down through the split kernel has 80 workgroups: 24 us; sliced through the stream
-// kernel, 200: 15 us), and workgroups past 256 run as a second round.  The split kernel
+// kernel, 200: 15 us), and workgroups past 256 run as a second round; the chip streams at
+// most ~5.4 TB/s however many workgroups run.  The split kernel
 // reads its token fragments from L2, which costs ~0.8 us per row past the first; the
-// stream kernel's K slices cost the reduction launch (~6 us) and their partial traffic.
+// stream kernel's K slices cost the reduction launch and their partial traffic.
 // Fitted to forced split / stream timings of the Qwen3 0.6B / 4B / 8B / 32B-shard
 // projections at 1 to 16 rows (weights streamed from HBM): it picks the faster kernel or
 // one within 10 % of it, except two cases within 23 %.
 constexpr int64_t kDecodeMaxRows = 16;
 constexpr int64_t kSplitMaxRows = 8;
-constexpr double kSplitWorkgroupBytesPerUs = 24.0e3;
+constexpr double kSplitWorkgroupBytesPerUs = 27.0e3;
 constexpr double kStreamWorkgroupBytesPerUs = 28.0e3;
+constexpr double kDecodeBytesPerUs = 5.4e6;
 constexpr double kDecodeFixedUs = 2.0;
 constexpr double kSplitRowUs = 0.8;
-constexpr double kStreamReduceUs = 6.0;
+constexpr double kStreamReduceUs = 12.0;  // the reduction launch, fitted (it also ends the overlap of slices)
 constexpr double kStreamPartialBytesPerUs = 6.0e6;
 constexpr int kSplitDepth = 4;
 
 double decode_stream_us(int64_t n, int64_t k, int64_t workgroups, double workgroup_bytes_per_us) {
   const int64_t rounds = (workgroups + kComputeUnits - 1) / kComputeUnits;
-  const double bytes_per_workgroup = 2.0 * static_cast<double>(n) * static_cast<double>(k) / workgroups;
-  return static_cast<double>(rounds) * bytes_per_workgroup / workgroup_bytes_per_us + kDecodeFixedUs;
+  const double bytes = 2.0 * static_cast<double>(n) * static_cast<double>(k);
+  const double per_workgroup = static_cast<double>(rounds) * bytes / workgroups / workgroup_bytes_per_us;
+  const double chip = bytes / kDecodeBytesPerUs;
+  return (per_workgroup > chip ? per_workgroup : chip) + kDecodeFixedUs;
 }
 
 // Candidate K splits of the split kernel (1, 2, 4 or 8 ranges per 16-row block, each range
@@ -942,7 +1048,7 @@ GemmChoice choose_split(int64_t capacity, int64_t n, int64_t k, double &cost) {
   return best;
 }
 
-constexpr int64_t kStreamLdsBytes = 160 * 1024;
+constexpr int64_t kStreamLdsBytes = 160 * 1024 - 256;  // the fused gather's row table is static LDS
 constexpr int64_t kStreamSliceQuantum = 128 * kStreamDepth;  // a whole number of load groups
 
 int64_t stream_slices(int64_t k, int64_t k_slice) { return (k + k_slice - 1) / k_slice; }
@@ -1034,6 +1140,23 @@ GemmChoice choose_gemm(int64_t capacity, int64_t n, int64_t k, bool gated) {
   return choose_tile(capacity, n, k);
 }
 
+// The fused gather's prologue (slot list, full-row sums of squares, staging) runs in every
+// workgroup, so the fused gate_up takes the fewest K slices that fit LDS (measured: 4
+// slices of Qwen3-8B gate_up took 47 + 5 us against 38 us for one).
+GemmChoice choose_dense_gate_up(int64_t capacity, int64_t n, int64_t k, bool &fused) {
+  fused = capacity <= kDecodeMaxRows && n * k * 2 <= INT32_MAX;
+  if (!fused) {
+    return choose_gemm(capacity, n, k, true);
+  }
+  for (int64_t slices = 1;; ++slices) {
+    const int64_t k_slice = ((k + slices - 1) / slices + kStreamSliceQuantum - 1) / kStreamSliceQuantum *
+                            kStreamSliceQuantum;
+    if (16 * (k_slice + 8) * 2 <= kStreamLdsBytes) {
+      return {GemmKind::Stream, 0, k_slice, 1};
+    }
+  }
+}
+
 // K ranges whose fp32 partial sums go through scratch and the reduction kernel.
 int64_t scratch_slices(GemmChoice choice, int64_t k) {
   switch (choice.kind) {
@@ -1071,16 +1194,18 @@ GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmCho
   } else if (choice.kind == GemmKind::Stream) {
     const int64_t groups = ((args.n + 15) / 16 + kStreamWaves - 1) / kStreamWaves;
     const int64_t slices = stream_slices(args.k, choice.k_slice);
-    kernel.func = gated ? stream_kernel<true>() : stream_kernel<false>();
+    const bool gather = args.gather_slots != nullptr;  // only ever set for gate_up
+    kernel.func = gather ? stream_kernel<true, true>() : (gated ? stream_kernel<true>() : stream_kernel<false>());
     kernel.grid = dim3(static_cast<unsigned>(slices * groups), 1, 1);
     kernel.block = dim3(64 * kStreamWaves, 1, 1);
     kernel.shmem = static_cast<unsigned>(16 * (choice.k_slice + 8) * 2);
     // Dynamic LDS beyond 64 KB must be allowed per function (idempotent, set on first use).
-    static bool configured[2] = {};
-    if (!configured[gated]) {
+    static bool configured[3] = {};
+    const int function_index = gather ? 2 : (gated ? 1 : 0);
+    if (!configured[function_index]) {
       (void)hipFuncSetAttribute(kernel.func, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 static_cast<int>(kStreamLdsBytes));
-      configured[gated] = true;
+      configured[function_index] = true;
     }
   } else {
     const TileShape &shape = kTileShapes[choice.variant];

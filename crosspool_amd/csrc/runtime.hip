@@ -74,8 +74,9 @@ DenseWorkspace dense_workspace(int64_t capacity, int64_t hidden, int64_t interme
   layout.batch_offset = 0;
   layout.activated_offset = align_up(static_cast<size_t>(capacity * hidden) * 2, kRegionAlignment);
   size_t cursor = layout.activated_offset + static_cast<size_t>(capacity * intermediate) * 2;
-  const size_t gate_up = gemm_scratch_bytes(choose_gemm(capacity, 2 * intermediate, hidden, true), capacity,
-                                            2 * intermediate, hidden);
+  bool fused = false;
+  const size_t gate_up = gemm_scratch_bytes(choose_dense_gate_up(capacity, 2 * intermediate, hidden, fused),
+                                            capacity, 2 * intermediate, hidden);
   const size_t down = gemm_scratch_bytes(choose_gemm(capacity, hidden, intermediate, false), capacity, hidden,
                                          intermediate);
   if (gate_up + down > 0) {
@@ -100,8 +101,9 @@ GatedSilu default_activation() { return GatedSilu{1.0f, 0.0f, 0.0f}; }
 
 // The kernels of one mailbox step, for a given capacity: gather (+ RMSNorm), gate_up
 // with the gated SiLU fused (+ its K-slice reduction), down with the scatter fused (+ its
-// reduction).  The sequence depends only on the capacity and geometry, so a template's
-// node list matches every replay's.
+// reduction).  At decode sizes the gather is fused into gate_up and has no launch of its
+// own.  The sequence depends only on the capacity and geometry, so a template's node list
+// matches every replay's.
 struct DenseLaunches {
   KernelLaunch gather;
   GemmLaunch gate_up;
@@ -141,20 +143,24 @@ DenseLaunches make_dense_launches(const DenseBinding &b, int64_t capacity) {
   uint16_t *activated = reinterpret_cast<uint16_t *>(b.workspace + layout.activated_offset);
   DenseLaunches launches;
 
-  GatherArgs gather{};
-  gather.pool = b.pool_in;
-  gather.slots = b.slots;
-  gather.norm = b.norm;
-  gather.out = batch;
-  gather.fault = b.fault;
-  gather.pool_rows = b.pool_rows;
-  gather.hidden = b.hidden;
-  gather.rows = b.rows;
-  gather.eps = b.eps;
-  launches.gather = make_gather(gather, capacity);
+  bool fused = false;
+  const GemmChoice gate_up_choice = choose_dense_gate_up(capacity, 2 * b.intermediate, b.hidden, fused);
+  if (!fused) {
+    GatherArgs gather{};
+    gather.pool = b.pool_in;
+    gather.slots = b.slots;
+    gather.norm = b.norm;
+    gather.out = batch;
+    gather.fault = b.fault;
+    gather.pool_rows = b.pool_rows;
+    gather.hidden = b.hidden;
+    gather.rows = b.rows;
+    gather.eps = b.eps;
+    launches.gather = make_gather(gather, capacity);
+  }
 
   GemmArgs gate_up{};
-  gate_up.x = batch;
+  gate_up.x = fused ? b.pool_in : batch;
   gate_up.w = b.gate_up;
   gate_up.out = activated;
   gate_up.scatter_slots = nullptr;
@@ -166,7 +172,14 @@ DenseLaunches make_dense_launches(const DenseBinding &b, int64_t capacity) {
   gate_up.k = b.hidden;
   gate_up.act = default_activation();
   gate_up.partials = reinterpret_cast<float *>(b.workspace + layout.gate_up_partials_offset);
-  launches.gate_up = make_gemm(gate_up, capacity, true, choose_gemm(capacity, gate_up.n, gate_up.k, true));
+  if (fused) {
+    gate_up.gather_slots = b.slots;
+    gate_up.norm = b.norm;
+    gate_up.fault = b.fault;
+    gate_up.pool_rows = b.pool_rows;
+    gate_up.eps = b.eps;
+  }
+  launches.gate_up = make_gemm(gate_up, capacity, true, gate_up_choice);
 
   GemmArgs down{};
   down.x = activated;

@@ -47,7 +47,7 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(GatherArgs a) {
   const int32_t slot = a.slots[row];
   if (slot < 0 || static_cast<int64_t>(slot) >= a.pool_rows) {
     // Canonical failure: poison the row with quiet NaNs and raise the sticky fault bit.
-    const u32x4 poison = {0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u};
+    const u32x4 poison = {kPoisonBf16x2, kPoisonBf16x2, kPoisonBf16x2, kPoisonBf16x2};
     for (int64_t chunk = lane; chunk < chunks; chunk += kWave) {
       store16(destination + chunk * 8, poison);
     }
@@ -75,32 +75,18 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(GatherArgs a) {
     }
     return;
   }
+  // Chunks past the row are zero and add nothing to the sum.
   float squares = 0.0f;
 #pragma unroll
   for (int index = 0; index < CHUNKS; ++index) {
-#pragma unroll
-    for (int word = 0; word < 4; ++word) {
-      const float lo = bf16_to_float(values[index][word] & 0xffffu);
-      const float hi = bf16_to_float(values[index][word] >> 16);
-      squares += lo * lo;
-      squares += hi * hi;
-    }
+    add_squares(values[index], squares);
   }
-  squares = wave_sum(squares);
-  const float inverse = 1.0f / sqrtf(squares / static_cast<float>(a.hidden) + a.eps);
+  const float inverse = rms_inverse(squares, a.hidden, a.eps);
 #pragma unroll
   for (int index = 0; index < CHUNKS; ++index) {
     const int64_t chunk = lane + index * kWave;
     if (chunk < chunks) {
-      const u32x4 weight = weights[index];
-      u32x4 result;
-#pragma unroll
-      for (int word = 0; word < 4; ++word) {
-        const float lo = bf16_to_float(values[index][word] & 0xffffu) * inverse;
-        const float hi = bf16_to_float(values[index][word] >> 16) * inverse;
-        result[word] = pack_bf16x2(lo * bf16_to_float(weight[word] & 0xffffu), hi * bf16_to_float(weight[word] >> 16));
-      }
-      store16(destination + chunk * 8, result);
+      store16(destination + chunk * 8, normalize_chunk(values[index], inverse, weights[index]));
     }
   }
 }

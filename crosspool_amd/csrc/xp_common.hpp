@@ -23,8 +23,8 @@ constexpr uint32_t kFaultSlotOutOfRange = 1u;
 
 __device__ __forceinline__ float bf16_to_float(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
 
-// Round-to-nearest-even fp32 -> bf16; NaN stays a quiet NaN of the same sign.
-// Round to nearest even on the gfx950 converter (v_cvt_pk_bf16_f32); NaNs stay NaN.
+// fp32 -> bf16, round to nearest even on the gfx950 converter (v_cvt_pk_bf16_f32); NaNs
+// stay NaN.
 __device__ __forceinline__ uint32_t float_to_bf16(float value) {
   return __builtin_bit_cast(uint16_t, static_cast<__bf16>(value));
 }
@@ -77,6 +77,39 @@ __device__ __forceinline__ float wave_sum(float value) {
   }
   return value;
 }
+
+// RMSNorm of gathered mailbox rows, shared by the gather kernel and the gather fused into
+// the decode projection so that both produce the same bits.  One wavefront takes a row's
+// sum of squares, lane i over its 16-byte chunks i, i + 64, ... in that order (add_squares),
+// reduced with wave_sum (rms_inverse); each element becomes bf16((x * inverse) * w).
+__device__ __forceinline__ void add_squares(u32x4 chunk, float &squares) {
+#pragma unroll
+  for (int word = 0; word < 4; ++word) {
+    const float lo = bf16_to_float(chunk[word] & 0xffffu);
+    const float hi = bf16_to_float(chunk[word] >> 16);
+    squares += lo * lo;
+    squares += hi * hi;
+  }
+}
+
+__device__ __forceinline__ float rms_inverse(float lane_squares, int64_t hidden, float eps) {
+  const float squares = wave_sum(lane_squares);
+  return 1.0f / sqrtf(squares / static_cast<float>(hidden) + eps);
+}
+
+__device__ __forceinline__ u32x4 normalize_chunk(u32x4 x, float inverse, u32x4 weight) {
+  u32x4 result;
+#pragma unroll
+  for (int word = 0; word < 4; ++word) {
+    const float lo = bf16_to_float(x[word] & 0xffffu) * inverse;
+    const float hi = bf16_to_float(x[word] >> 16) * inverse;
+    result[word] = pack_bf16x2(lo * bf16_to_float(weight[word] & 0xffffu), hi * bf16_to_float(weight[word] >> 16));
+  }
+  return result;
+}
+
+// A gathered row whose slot is out of range reads as quiet NaNs (two bf16 per word).
+constexpr uint32_t kPoisonBf16x2 = 0x7fc07fc0u;
 
 __device__ __forceinline__ void raise_fault(uint32_t *fault, uint32_t bits) {
   if (fault != nullptr) {

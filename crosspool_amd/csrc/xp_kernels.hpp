@@ -21,7 +21,7 @@ struct KernelLaunch {
   dim3 grid{1, 1, 1};
   dim3 block{1, 1, 1};
   unsigned shmem = 0;
-  alignas(16) unsigned char args[160] = {};
+  alignas(16) unsigned char args[192] = {};
   size_t args_size = 0;
 
   template <class Args>
@@ -99,6 +99,15 @@ struct GemmArgs {
   int64_t n;         // weight rows
   int64_t k;         // reduction length
   GatedSilu act;
+  // Gather fused into the gate_up of a Dense step at decode sizes (stream kernel only):
+  // when set, token row t is row gather_slots[t] of the mailbox `x` ([pool_rows, ldx]),
+  // RMS-normalised with `norm` when that is set, bit for bit as gather_rows_kernel does;
+  // an out-of-range slot gives a row of quiet NaNs and raises kFaultSlotOutOfRange.
+  const int32_t *gather_slots;
+  const uint16_t *norm;
+  uint32_t *fault;
+  int64_t pool_rows;
+  float eps;
 };
 
 enum class GemmKind : int { Split = 1, Tile = 2, Stream = 3 };
@@ -112,6 +121,9 @@ struct GemmChoice {
 };
 
 GemmChoice choose_gemm(int64_t capacity, int64_t n, int64_t k, bool gated);
+// The gate_up of a Dense step: at decode sizes the stream kernel with the mailbox gather
+// fused (`fused` set), otherwise choose_gemm's kernel after a separate gather.
+GemmChoice choose_dense_gate_up(int64_t capacity, int64_t n, int64_t k, bool &fused);
 // Device scratch (fp32 partial sums of the K slices) a projection at `capacity` rows
 // needs; 0 when its kernel reduces K inside one workgroup.
 size_t gemm_scratch_bytes(GemmChoice choice, int64_t capacity, int64_t n, int64_t k);

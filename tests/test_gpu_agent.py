@@ -105,6 +105,35 @@ def test_config3_qwen3_8b_layer(device, rows):
     _check_mailbox(pool_gpu, pool, slots, w_gate_up, w_down, norm_weight)
 
 
+@pytest.mark.parametrize("normed", [True, False])
+def test_fused_gather_matches_separate_kernels_bitwise(device, normed):
+    # At up to 16 rows the gather (+ RMSNorm) runs inside gate_up.  At 16 rows the kernel-level
+    # projections take the same stream kernels with the same K slices, so the step must equal
+    # gather kernel -> gate_up -> down -> scatter bit for bit.
+    from crosspool_amd import dense
+
+    hidden, intermediate, pool_rows, rows = 4096, 12288, 256, 16
+    pool = o.generate_hidden_states(pool_rows, hidden, 17)
+    w_gate_up, w_down, norm_weight = o.generate_layer(hidden, intermediate, 18)
+    slots = o.generate_slots(pool_rows, rows, 19)
+    weights = _weights(w_gate_up, w_down, device)
+    norm = to_device(norm_weight, device) if normed else None
+    slots_d = slots_tensor(slots, device)
+    with FfnAgent(device) as agent:
+        agent.register_layer(instance_index=0, layer_ordinal=0, weights=weights, norm_weight=norm)
+        agent.materialize(maximum_row_capacity=rows)
+        pool_gpu = to_device(pool, device)
+        agent.execute(instance_index=0, layer_ordinal=0, pool=pool_gpu, slots=slots_d)
+        agent.check_health()
+    expected = to_device(pool, device)
+    x = dense.gather_rmsnorm(expected, slots_d, norm_weight=norm)
+    activated = dense.gate_up_silu(x, weights.i_proj.values)
+    dense.down(activated, weights.o_proj.values, out=expected, slots=slots_d)
+    torch.cuda.synchronize()
+    assert _native.gemm_variant(rows, 2 * intermediate, hidden, True).startswith("stream")
+    assert_bitwise_equal(pool_gpu.cpu(), expected.cpu())
+
+
 def test_config5_qwen3_32b_tp_shard_partial(device):
     # one of 8 TP shards, hidden 5120, shard intermediate 3200, unreduced partial.
     hidden, intermediate, rows = 5120, 3200, 8

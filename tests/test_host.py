@@ -106,13 +106,12 @@ def test_native_workspace_covers_signature_layout(capacity, hidden, intermediate
     signature = DenseFfnExecutionSignature(torch.bfloat16, capacity, hidden, intermediate)
     native = _native.dense_workspace_bytes(capacity, hidden, intermediate)
     layout = signature.workspace_layout().nbytes
-    gate_up = _native.gemm_workspace_bytes(capacity, 2 * intermediate, hidden, True)
     down = _native.gemm_workspace_bytes(capacity, hidden, intermediate, False)
-    if gate_up + down == 0:
-        assert native == layout
-    else:
-        # the partial sums of K-split projections follow the two regions, 256-byte aligned
-        assert layout + gate_up + down <= native < layout + gate_up + down + 256
+    # The partial sums of K-split projections follow the two regions, 256-byte aligned.  The
+    # step's gate_up may differ from the kernel-level choice (at decode sizes it fuses the
+    # gather into the stream kernel), so only the down partials are known here.
+    assert native >= layout + down
+    assert native == layout or native >= (layout + 255) // 256 * 256
 
 
 def test_signature_validation():
