@@ -282,7 +282,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_gemm_kernel(GemmArgs
     // RMS over the whole row (the gather kernel's wavefront reduction, so the same bits),
     // then the slice is staged from the mailbox rows, normalised.  Loads are issued in
     // batches of independent requests before their results are used, so the dependent
-    // round trips are few (slot, row, and the staging reads).
+    // round trips are few (slot, row, and for rows longer than one batch the staging reads).
     constexpr int ROWS_PER_WAVE = TP / kStreamWaves;
     constexpr int BATCH = 8;  // 16-byte chunks per lane and row in flight
     __shared__ float row_scale[TP];
@@ -303,17 +303,24 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_gemm_kernel(GemmArgs
       squares[r] = 0.0f;
     }
     const int64_t row_chunks = a.k / 8;
-    if (a.norm != nullptr) {
-      for (int64_t first = lane; first < row_chunks; first += BATCH * kWave) {
-        u32x4 values[ROWS_PER_WAVE][BATCH];
+    // Rows of at most BATCH * 64 chunks (hidden <= 4096) stay in registers between their sum
+    // of squares and their normalised store into LDS: one round trip for the rows, none for
+    // a second staging pass.  Longer rows are summed in batches and staged in a second pass.
+    const bool one_batch = row_chunks <= BATCH * kWave;
+    u32x4 values[ROWS_PER_WAVE][BATCH];
+    u32x4 weights[BATCH];
+    for (int64_t first = lane; first < row_chunks; first += BATCH * kWave) {
+#pragma unroll
+      for (int b = 0; b < BATCH; ++b) {
+        const int64_t chunk = first + b * kWave;
+        weights[b] = one_batch && a.norm != nullptr && chunk < row_chunks ? load16(a.norm + chunk * 8) : zero;
 #pragma unroll
         for (int r = 0; r < ROWS_PER_WAVE; ++r) {
-#pragma unroll
-          for (int b = 0; b < BATCH; ++b) {
-            const int64_t chunk = first + b * kWave;
-            values[r][b] = sources[r] >= 0 && chunk < row_chunks ? load16(a.x + sources[r] * a.ldx + chunk * 8) : zero;
-          }
+          const bool live = sources[r] >= 0 && chunk < row_chunks && (one_batch || a.norm != nullptr);
+          values[r][b] = live ? load16(a.x + sources[r] * a.ldx + chunk * 8) : zero;
         }
+      }
+      if (a.norm != nullptr) {
 #pragma unroll
         for (int r = 0; r < ROWS_PER_WAVE; ++r) {
 #pragma unroll
@@ -323,53 +330,85 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_gemm_kernel(GemmArgs
         }
       }
     }
+    float scales[ROWS_PER_WAVE];
 #pragma unroll
     for (int r = 0; r < ROWS_PER_WAVE; ++r) {
       const int t = wave + r * kStreamWaves;
-      const float scale = a.norm != nullptr && sources[r] >= 0 ? rms_inverse(squares[r], a.k, a.eps) : 1.0f;
+      scales[r] = a.norm != nullptr && sources[r] >= 0 ? rms_inverse(squares[r], a.k, a.eps) : 1.0f;
       if (lane == 0) {
-        row_scale[t] = scale;
-        row_source[t] = sources[r];
+        if (!one_batch) {
+          row_scale[t] = scales[r];
+          row_source[t] = sources[r];
+        }
         if (sources[r] == -2 && blockIdx.x == 0) {
           raise_fault(a.fault, kFaultSlotOutOfRange);
         }
       }
     }
-    __syncthreads();
     const u32x4 poison = {kPoisonBf16x2, kPoisonBf16x2, kPoisonBf16x2, kPoisonBf16x2};
-    constexpr int STAGE_BATCH = 4;
-    const int items = TP * vectors_per_row;
-    for (int first = threadIdx.x; first < items; first += STAGE_BATCH * 64 * kStreamWaves) {
-      u32x4 x_chunk[STAGE_BATCH];
-      u32x4 w_chunk[STAGE_BATCH];
+    if (one_batch) {
+      // Each wave stores its own rows' part of the slice (zeros past the live rows).
 #pragma unroll
-      for (int u = 0; u < STAGE_BATCH; ++u) {
-        const int index = first + u * 64 * kStreamWaves;
-        const int t = index / vectors_per_row;
-        const int c = index - t * vectors_per_row;
-        const int64_t source = index < items ? row_source[t] : -1;
-        const bool live = source >= 0 && c * 8 < kvalid;
-        x_chunk[u] = live ? load16(a.x + source * a.ldx + kbase + c * 8) : zero;
-        w_chunk[u] = live && a.norm != nullptr ? load16(a.norm + kbase + c * 8) : zero;
-      }
+      for (int r = 0; r < ROWS_PER_WAVE; ++r) {
+        const int t = wave + r * kStreamWaves;
 #pragma unroll
-      for (int u = 0; u < STAGE_BATCH; ++u) {
-        const int index = first + u * 64 * kStreamWaves;
-        if (index >= items) {
-          continue;
-        }
-        const int t = index / vectors_per_row;
-        const int c = index - t * vectors_per_row;
-        const int64_t source = row_source[t];
-        u32x4 value = zero;
-        if (c * 8 < kvalid) {
-          if (source >= 0) {
-            value = a.norm != nullptr ? normalize_chunk(x_chunk[u], row_scale[t], w_chunk[u]) : x_chunk[u];
-          } else if (source == -2) {
+        for (int b = 0; b < BATCH; ++b) {
+          const int64_t chunk = lane + b * kWave;
+          const int64_t c = chunk - kbase / 8;  // chunk within this slice
+          if (chunk >= row_chunks || c < 0 || c >= vectors_per_row) {
+            continue;
+          }
+          u32x4 value = zero;
+          if (sources[r] >= 0) {
+            value = a.norm != nullptr ? normalize_chunk(values[r][b], scales[r], weights[b]) : values[r][b];
+          } else if (sources[r] == -2) {
             value = poison;
           }
+          store16(xs + t * rs + c * 8, value);
         }
-        store16(xs + t * rs + c * 8, value);
+        // Slice columns past the row (the last slice's tail) are zero.
+        for (int64_t c = row_chunks - kbase / 8 + lane; c < vectors_per_row; c += kWave) {
+          if (c >= 0) {
+            store16(xs + t * rs + c * 8, zero);
+          }
+        }
+      }
+    } else {
+      __syncthreads();
+      constexpr int STAGE_BATCH = 4;
+      const int items = TP * vectors_per_row;
+      for (int first = threadIdx.x; first < items; first += STAGE_BATCH * 64 * kStreamWaves) {
+        u32x4 x_chunk[STAGE_BATCH];
+        u32x4 w_chunk[STAGE_BATCH];
+#pragma unroll
+        for (int u = 0; u < STAGE_BATCH; ++u) {
+          const int index = first + u * 64 * kStreamWaves;
+          const int t = index / vectors_per_row;
+          const int c = index - t * vectors_per_row;
+          const int64_t source = index < items ? row_source[t] : -1;
+          const bool live = source >= 0 && c * 8 < kvalid;
+          x_chunk[u] = live ? load16(a.x + source * a.ldx + kbase + c * 8) : zero;
+          w_chunk[u] = live && a.norm != nullptr ? load16(a.norm + kbase + c * 8) : zero;
+        }
+#pragma unroll
+        for (int u = 0; u < STAGE_BATCH; ++u) {
+          const int index = first + u * 64 * kStreamWaves;
+          if (index >= items) {
+            continue;
+          }
+          const int t = index / vectors_per_row;
+          const int c = index - t * vectors_per_row;
+          const int64_t source = row_source[t];
+          u32x4 value = zero;
+          if (c * 8 < kvalid) {
+            if (source >= 0) {
+              value = a.norm != nullptr ? normalize_chunk(x_chunk[u], row_scale[t], w_chunk[u]) : x_chunk[u];
+            } else if (source == -2) {
+              value = poison;
+            }
+          }
+          store16(xs + t * rs + c * 8, value);
+        }
       }
     }
   } else {

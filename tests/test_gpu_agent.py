@@ -134,6 +134,28 @@ def test_fused_gather_matches_separate_kernels_bitwise(device, normed):
     assert_bitwise_equal(pool_gpu.cpu(), expected.cpu())
 
 
+@pytest.mark.parametrize("rows", [3, 16])
+def test_fused_gather_rows_longer_than_one_batch(device, rows):
+    # Hidden 5120 is more than one load batch per lane (4096 columns), so the fused gather
+    # sums the squares in batches and stages the slice in a second pass.
+    hidden, intermediate, pool_rows = 5120, 3200, 64
+    pool = o.generate_hidden_states(pool_rows, hidden, 27)
+    w_gate_up, w_down, norm_weight = o.generate_layer(hidden, intermediate, 28)
+    slots = o.generate_slots(pool_rows, rows, 29)
+    with FfnAgent(device) as agent:
+        agent.register_layer(
+            instance_index=0,
+            layer_ordinal=0,
+            weights=_weights(w_gate_up, w_down, device),
+            norm_weight=to_device(norm_weight, device),
+        )
+        agent.materialize(maximum_row_capacity=16)
+        pool_gpu = to_device(pool, device)
+        agent.execute(instance_index=0, layer_ordinal=0, pool=pool_gpu, slots=slots_tensor(slots, device))
+        agent.check_health()
+    _check_mailbox(pool_gpu, pool, slots, w_gate_up, w_down, norm_weight)
+
+
 def test_config5_qwen3_32b_tp_shard_partial(device):
     # one of 8 TP shards, hidden 5120, shard intermediate 3200, unreduced partial.
     hidden, intermediate, rows = 5120, 3200, 8
