@@ -35,6 +35,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "xp_abi_version": (_INT, []),
     "xp_last_error": (_SIZE, [ctypes.c_char_p, _SIZE]),
     "xp_copy_bytes": (_INT, [_P, _P, _SIZE, _P]),
+    "xp_reduce_partials": (_INT, [ctypes.POINTER(_P), _INT, _P, _I64, _P]),
     "xp_gather_rmsnorm": (_INT, [_P, _I64, _I64, _P, _I64, _P, _F32, _P, _P, _P]),
     "xp_scatter": (_INT, [_P, _I64, _I64, _P, _P, _I64, _P, _P]),
     "xp_gemm_gate_up_silu": (_INT, [_P, _I64, _I64, _P, _I64, _P, _F32, _F32, _F32, _P, _SIZE, _P]),

@@ -276,6 +276,42 @@ class FfnAgent:
             instance_index, layer_ordinal, weights, norm_weight, float(eps)
         )
 
+    def register_checkpoint(
+        self,
+        model_path,
+        *,
+        instance_index: int,
+        tp_size: int = 1,
+        tp_rank: int = 0,
+        layers=None,
+        fuse_norm: bool = True,
+        parallelism: int = 4,
+    ):
+        """Load a local checkpoint's Dense layers and bind each at ``layer_ordinal`` = its layer id.
+
+        The loading follows the reference's Plan materialisation for one FfnAgent
+        (loader.py:148-284) through ``crosspool_amd.checkpoint.load_dense_layers``.  With
+        ``fuse_norm`` the post-attention RMSNorm weight and ``rms_norm_eps`` of the
+        checkpoint are bound for the fused gather; without it the caller applies the
+        norm, as SGLang does for the reference.  Returns the loaded layers.
+        """
+
+        from crosspool_amd.checkpoint import load_dense_layers
+
+        loaded = load_dense_layers(
+            model_path, device=self.device, tp_size=tp_size, tp_rank=tp_rank, layers=layers, norm=fuse_norm,
+            parallelism=parallelism,
+        )
+        for layer in loaded:
+            self.register_layer(
+                instance_index=instance_index,
+                layer_ordinal=layer.layer_id,
+                weights=DenseFfnWeights.from_tensors(layer.i_proj, layer.o_proj),
+                norm_weight=layer.norm_weight,
+                eps=layer.eps,
+            )
+        return tuple(loaded)
+
     # -------------------------------------------------------------- bring-up
     def materialize(self, *, maximum_row_capacity: int) -> tuple[GraphTemplate, ...]:
         """Create the Lanes and capture every signature of every registered layer.

@@ -334,6 +334,26 @@ int xp_copy_bytes(void *dst, const void *src, size_t bytes, xp_stream_t stream) 
   return XP_OK;
 }
 
+int xp_reduce_partials(const void *const *partials, int count, void *out, int64_t elements, xp_stream_t stream) {
+  XP_REQUIRE(count >= 1 && count <= kMaxPartials, "partial count must be between 1 and 16");
+  XP_REQUIRE(elements >= 0 && elements % 8 == 0, "element count must be a non-negative multiple of 8");
+  if (elements == 0) {
+    return XP_OK;
+  }
+  XP_REQUIRE(partials != nullptr && out != nullptr, "reduction pointers must be non-null");
+  ReduceArgs args{};
+  for (int k = 0; k < count; ++k) {
+    XP_REQUIRE(partials[k] != nullptr && aligned16(partials[k]), "partials must be non-null and 16-byte aligned");
+    args.partials[k] = static_cast<const uint16_t *>(partials[k]);
+  }
+  XP_REQUIRE(aligned16(out), "the output must be 16-byte aligned");
+  args.out = static_cast<uint16_t *>(out);
+  args.vectors = static_cast<uint64_t>(elements / 8);
+  args.count = count;
+  XP_HIP_CHECK(launch(make_reduce_partials(args), static_cast<hipStream_t>(stream)));
+  return XP_OK;
+}
+
 int xp_gather_rmsnorm(const void *pool, int64_t pool_rows, int64_t hidden, const int32_t *slots, int64_t rows,
                       const void *norm_weight, float eps, void *out, uint32_t *fault_word, xp_stream_t stream) {
   XP_REQUIRE(rows >= 0 && pool_rows >= 0, "row counts must be non-negative");

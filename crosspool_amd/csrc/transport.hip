@@ -119,6 +119,43 @@ const void *gather_kernel_for() {
   return reinterpret_cast<const void *>(&gather_rows_kernel<CHUNKS>);
 }
 
+// Fixed-order TP partial sum (the exchange step's arithmetic, src/cext/ffnagent/
+// delivery.cu:74-127): each thread takes 8 consecutive elements (16 bytes) of every
+// partial, issues all the partials' loads before the first add, and folds them in partial
+// order into fp32 sums that start from 0, then rounds once to bf16 (nearest even).  The
+// vectorisation changes the memory traffic, not the association order.  HBM-bound:
+// (count + 1) * 2 bytes per element.
+__global__ __launch_bounds__(256) void reduce_partials_kernel(ReduceArgs a) {
+  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+  for (uint64_t index = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; index < a.vectors;
+       index += stride) {
+    u32x4 chunks[kMaxPartials];
+#pragma unroll
+    for (int k = 0; k < kMaxPartials; ++k) {
+      if (k < a.count) {
+        chunks[k] = load16(a.partials[k] + index * 8);
+      }
+    }
+    float sums[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int k = 0; k < kMaxPartials; ++k) {
+      if (k < a.count) {
+#pragma unroll
+        for (int word = 0; word < 4; ++word) {
+          sums[2 * word] += bf16_to_float(chunks[k][word] & 0xffffu);
+          sums[2 * word + 1] += bf16_to_float(chunks[k][word] >> 16);
+        }
+      }
+    }
+    u32x4 packed;
+#pragma unroll
+    for (int word = 0; word < 4; ++word) {
+      packed[word] = pack_bf16x2(sums[2 * word], sums[2 * word + 1]);
+    }
+    store16(a.out + index * 8, packed);
+  }
+}
+
 }  // namespace
 
 KernelLaunch make_copy(const CopyArgs &args) {
@@ -163,6 +200,19 @@ KernelLaunch make_scatter(const ScatterArgs &args, int64_t capacity) {
   KernelLaunch kernel;
   kernel.func = reinterpret_cast<const void *>(&scatter_rows_kernel);
   kernel.grid = dim3(static_cast<unsigned>((capacity + 3) / 4), 1, 1);
+  kernel.block = dim3(256, 1, 1);
+  kernel.set_args(args);
+  return kernel;
+}
+
+KernelLaunch make_reduce_partials(const ReduceArgs &args) {
+  KernelLaunch kernel;
+  kernel.func = reinterpret_cast<const void *>(&reduce_partials_kernel);
+  uint64_t blocks = (args.vectors + 255) / 256;
+  if (blocks > 4096) {
+    blocks = 4096;
+  }
+  kernel.grid = dim3(static_cast<unsigned>(blocks), 1, 1);
   kernel.block = dim3(256, 1, 1);
   kernel.set_args(args);
   return kernel;

@@ -70,7 +70,18 @@ struct ScatterArgs {
   int64_t rows;
 };
 
+// Fixed-order sum of tensor-parallel partials: out[i] = bf16(sum over k in order of
+// float(partials[k][i])), the fp32 sum starting from 0 and rounded once.
+constexpr int kMaxPartials = 16;
+struct ReduceArgs {
+  const uint16_t *partials[kMaxPartials];  // count of them used
+  uint16_t *out;
+  uint64_t vectors;  // 16-byte groups of 8 bf16
+  int count;
+};
+
 KernelLaunch make_copy(const CopyArgs &args);
+KernelLaunch make_reduce_partials(const ReduceArgs &args);
 // `capacity` sizes the grid (graph templates keep one grid per capacity);
 // workgroups beyond the live rows exit immediately.
 KernelLaunch make_gather(const GatherArgs &args, int64_t capacity);

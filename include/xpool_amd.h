@@ -78,6 +78,16 @@ size_t xp_last_error(char *buffer, size_t size);
  * Transport payload copies (src/cext/transport/instance.cu:83-84,184-186). */
 int xp_copy_bytes(void *dst, const void *src, size_t bytes, xp_stream_t stream);
 
+/* Fixed-order sum of tensor-parallel partials: out[i] = bf16(((0 + p0[i]) + p1[i]) + ...
+ * + p_{count-1}[i]), accumulated in fp32 from +0 in partial order and rounded once to
+ * nearest even.  `partials` is a host array of `count` (1..16) device pointers to bf16
+ * arrays of `elements` values (a multiple of 8); every pointer is 16-byte aligned; `out`
+ * may be one of the partials.  Replaces the fixed PE-order fold of the true-TP delivery
+ * (src/cext/ffnagent/delivery.cu:74-127, ordered_sum / reduce_tp_partials) for partials
+ * already in this device's memory; the exchange that brings peer partials there is not
+ * part of this single-GPU build. */
+int xp_reduce_partials(const void *const *partials, int count, void *out, int64_t elements, xp_stream_t stream);
+
 /* out[i, :] = pool[slots[i], :] for i < rows, then, when norm_weight is not
  * NULL, out[i, :] = bf16(out_f32[i, :] / sqrt(mean(out_f32[i, :]^2) + eps) * w).
  * Without norm_weight the rows are copied bit-exactly.  Replaces the row-prefix

@@ -263,6 +263,19 @@ def dense_layer_weights(
     return interleave_gate_up(gate[begin:end], up[begin:end]), down[:, begin:end].contiguous()
 
 
+def ordered_partial_sum(partials: list[torch.Tensor]) -> torch.Tensor:
+    """Fixed PE-order fold of bf16 TP partials (delivery.cu:74-83, ``ordered_sum``).
+
+    Per element: an fp32 sum starting from +0, each partial widened to fp32 and added in
+    list order with fp32 rounding after every add, then one cast to bf16 (nearest even).
+    """
+
+    total = np.zeros(partials[0].shape, dtype=np.float32)
+    for partial in partials:
+        total = (total + partial.float().numpy()).astype(np.float32)
+    return torch.from_numpy(total).to(torch.bfloat16)
+
+
 def dense_reference_sum(x: torch.Tensor, shards: list[tuple[torch.Tensor, torch.Tensor]]) -> torch.Tensor:
     """Ordered fp32 sum of TP partials, rounded once (qualification.py:267-287)."""
 

@@ -247,6 +247,34 @@ def test_tp_partials_sum_to_the_full_layer():
     assert torch.equal(summed.float(), manual.to(torch.bfloat16).float())
 
 
+def _bf16(values) -> torch.Tensor:
+    return torch.tensor(values, dtype=torch.float32).to(torch.bfloat16)
+
+
+def test_ordered_partial_sum_closed_forms():
+    # delivery.cu:74-83: fp32 fold from +0 in PE order, one final bf16 cast.
+    big = float(2**24)
+    # (2^24 + 1) rounds to 2^24 in fp32, so the fold in order gives 0 and the reverse 1.
+    assert torch.equal(o.ordered_partial_sum([_bf16([big]), _bf16([1.0]), _bf16([-big])]).float(), torch.tensor([0.0]))
+    assert torch.equal(o.ordered_partial_sum([_bf16([-big]), _bf16([1.0]), _bf16([big])]).float(), torch.tensor([1.0]))
+    # One rounding at the end: 1 + 2^-8 + 2^-8 = 1 + 2^-7 exactly (bf16 after every add
+    # would round each 1 + 2^-8 tie back to 1).
+    tiny = 2.0**-8
+    assert o.ordered_partial_sum([_bf16([1.0]), _bf16([tiny]), _bf16([tiny])]).item() == 1.0 + 2.0**-7
+    # A single partial is the identity, except that -0 becomes +0 (0.0 + -0.0).
+    single = _bf16([-0.0, 3.5, -7.25, float("inf")])
+    folded = o.ordered_partial_sum([single])
+    assert o.bf16_bits(folded).tolist() == [0x0000] + o.bf16_bits(single).tolist()[1:]
+
+
+def test_ordered_partial_sum_is_the_tp_layer_reference():
+    # qualification.py:267-287: dense_reference sums the ordered partials the same way.
+    x = o.generate_hidden_states(3, 16, 17)
+    shards = [o.dense_layer_weights(hidden_size=16, intermediate_size=8, tp_size=4, tp_rank=r) for r in range(4)]
+    partials = [o.dense_partial_reference(x, *shard) for shard in shards]
+    assert torch.equal(o.ordered_partial_sum(partials), o.dense_reference_sum(x, shards))
+
+
 def test_deterministic_weights_are_exact_bf16():
     gate, up, down = o.dense_full_weights(hidden_size=16, intermediate_size=8)
     for tensor, offset in ((gate, 3), (up, 11), (down, 19)):
