@@ -39,6 +39,10 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0
 # the 256 MB last-level cache, so every launch streams its weights from HBM).
 DECODE_WEIGHT_SETS = 3
 CALIBRATION_COPY_BYTES = 256 << 20
+# TP partial fold measured at BASELINE config 5 (Qwen3-32B, 8 shards of H = 5120, T = 8192).
+TP_REDUCE_PARTIALS = 8
+TP_REDUCE_SHAPE = (8192, 5120)
+TP_REDUCE_LAUNCHES = 20
 TRAFFIC_FILE = REPO_ROOT / "profiles" / "traffic.json"
 
 
@@ -226,6 +230,33 @@ def main() -> int:
             })
     agent.check_health()
 
+    # ---------------------------------------------------------------- TP partial fold
+    # xp_reduce_partials at the Qwen3-32B 1/8-shard partial shape (
+    # T = 8192): 8 bf16 partials folded in rank order; (8 + 1) x 2 bytes per element.
+    tp_reduce = None
+    if not args.no_sweep:
+        from crosspool_amd.delivery import reduce_tp_partials
+
+        partials = [torch.randn(TP_REDUCE_SHAPE, device=device).bfloat16() for _ in range(TP_REDUCE_PARTIALS)]
+        folded = torch.empty_like(partials[0])
+        for _ in range(3):
+            reduce_tp_partials(partials, out=folded, stream=lane.stream)
+        begin = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        begin.record(lane.stream)
+        for _ in range(TP_REDUCE_LAUNCHES):
+            reduce_tp_partials(partials, out=folded, stream=lane.stream)
+        end.record(lane.stream)
+        end.synchronize()
+        per_launch = begin.elapsed_time(end) / 1e3 / TP_REDUCE_LAUNCHES
+        moved = (TP_REDUCE_PARTIALS + 1) * folded.numel() * 2
+        tp_reduce = {
+            "partials": TP_REDUCE_PARTIALS, "shape": list(TP_REDUCE_SHAPE), "us": round(per_launch * 1e6, 2),
+            "achieved": round(moved / per_launch / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(moved / per_launch / 1e9 / HBM_PEAK_GBS, 4), "algorithmic_bytes": moved,
+        }
+        del partials, folded
+
     # ---------------------------------------------------------------- CPU baseline
     cpu_baseline = None
     if not args.no_cpu_baseline:
@@ -293,6 +324,7 @@ def main() -> int:
         "cpu_baseline": cpu_baseline,
         "decode": decode,
         "sweep": sweep,
+        "tp_reduce": tp_reduce,
     }
     agent.close()
     print(json.dumps(result), flush=True)

@@ -124,7 +124,10 @@ const void *gather_kernel_for() {
 // partial, issues all the partials' loads before the first add, and folds them in partial
 // order into fp32 sums that start from 0, then rounds once to bf16 (nearest even).  The
 // vectorisation changes the memory traffic, not the association order.  HBM-bound:
-// (count + 1) * 2 bytes per element.
+// (count + 1) * 2 bytes per element.  STREAMING uses nontemporal loads and stores, for
+// folds larger than the last-level cache (measured at 8 x 84 MB: 138 against 156 us;
+// for a fold that fits the cache they cost 13 %).
+template <bool STREAMING>
 __global__ __launch_bounds__(256) void reduce_partials_kernel(ReduceArgs a) {
   const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
   for (uint64_t index = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; index < a.vectors;
@@ -133,7 +136,7 @@ __global__ __launch_bounds__(256) void reduce_partials_kernel(ReduceArgs a) {
 #pragma unroll
     for (int k = 0; k < kMaxPartials; ++k) {
       if (k < a.count) {
-        chunks[k] = load16(a.partials[k] + index * 8);
+        chunks[k] = STREAMING ? load16_stream(a.partials[k] + index * 8) : load16(a.partials[k] + index * 8);
       }
     }
     float sums[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
@@ -152,7 +155,11 @@ __global__ __launch_bounds__(256) void reduce_partials_kernel(ReduceArgs a) {
     for (int word = 0; word < 4; ++word) {
       packed[word] = pack_bf16x2(sums[2 * word], sums[2 * word + 1]);
     }
-    store16(a.out + index * 8, packed);
+    if constexpr (STREAMING) {
+      __builtin_nontemporal_store(packed, reinterpret_cast<u32x4 *>(a.out + index * 8));
+    } else {
+      store16(a.out + index * 8, packed);
+    }
   }
 }
 
@@ -207,7 +214,10 @@ KernelLaunch make_scatter(const ScatterArgs &args, int64_t capacity) {
 
 KernelLaunch make_reduce_partials(const ReduceArgs &args) {
   KernelLaunch kernel;
-  kernel.func = reinterpret_cast<const void *>(&reduce_partials_kernel);
+  constexpr uint64_t kLastLevelCacheBytes = 256ull << 20;
+  const bool streaming = (static_cast<uint64_t>(args.count) + 1) * args.vectors * 16 > kLastLevelCacheBytes;
+  kernel.func = streaming ? reinterpret_cast<const void *>(&reduce_partials_kernel<true>)
+                          : reinterpret_cast<const void *>(&reduce_partials_kernel<false>);
   uint64_t blocks = (args.vectors + 255) / 256;
   if (blocks > 4096) {
     blocks = 4096;

@@ -25,7 +25,9 @@ def _partials(count: int, shape: tuple[int, ...], seed: int) -> list[torch.Tenso
 
 @pytest.mark.parametrize(
     ("count", "shape"),
-    [(1, (8,)), (2, (3, 1024)), (3, (17, 2560)), (8, (512, 5120)), (16, (64, 4096))],
+    # The last case (4 x 84 MB) is larger than the last-level cache, so the kernel takes its
+    # nontemporal loads and stores.
+    [(1, (8,)), (2, (3, 1024)), (3, (17, 2560)), (8, (512, 5120)), (16, (64, 4096)), (4, (8192, 5120))],
 )
 def test_reduction_matches_the_ordered_fold(device, count, shape):
     print(f"reduce partials count={count} shape={shape}", flush=True)
