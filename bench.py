@@ -257,6 +257,36 @@ def main() -> int:
         }
         del partials, folded
 
+    # ---------------------------------------------------------------- ffn_shim transaction
+    # Host-timed ffn_shim calls on resident [T, H] hidden states: through the Transport
+    # mailbox on the caller's stream (submit -> Dense step -> settle), through it with the
+    # step on the Lane's stream (two cross-stream hops), and without it.
+    shim = None
+    if not args.no_sweep:
+        from crosspool_amd.ffn import DpRowLayout, ForwardMode, OutputRequirement
+        from crosspool_amd.ops import attach, detach, ffn_shim
+        from crosspool_amd.transport import FfnRequestMetadata
+
+        metadata = FfnRequestMetadata(0, ForwardMode.DECODE, OutputRequirement.PER_RANK_COMPLETE, DpRowLayout.NONE)
+        shim = {}
+        for mode in ("mailbox", "mailbox_lane_stream", "direct"):
+            attach(agent, mailbox=mode != "direct", lane_stream=mode == "mailbox_lane_stream")
+            for t in (1, args.decode_tokens):
+                x = pool[:t]
+                for _ in range(10):
+                    ffn_shim(x, None, metadata)
+                torch.cuda.synchronize()
+                calls = 3 * args.sweep_steps
+                start = time.perf_counter()
+                for _ in range(calls):
+                    ffn_shim(x, None, metadata)
+                torch.cuda.synchronize()
+                shim[f"{mode}_tokens{t}_us"] = round(
+                    (time.perf_counter() - start) / calls * 1e6, 2
+                )
+            detach()
+        agent.check_health()
+
     # ---------------------------------------------------------------- CPU baseline
     cpu_baseline = None
     if not args.no_cpu_baseline:
@@ -325,6 +355,7 @@ def main() -> int:
         "decode": decode,
         "sweep": sweep,
         "tp_reduce": tp_reduce,
+        "shim": shim,
     }
     agent.close()
     print(json.dumps(result), flush=True)

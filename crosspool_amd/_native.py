@@ -57,6 +57,18 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "xp_template_capture": (_INT, [_P, _I64, _I64, _I64]),
     "xp_template_capacities": (_INT, [_P, _I64, _I64, ctypes.POINTER(_I64), _INT, ctypes.POINTER(_INT)]),
     "xp_replay": (_INT, [_P, _INT, _INT, _I64, _P, _P, _I64, _P, _P]),
+    "xp_lane_fault_word": (_INT, [_P, ctypes.POINTER(_P)]),
+    "xp_transport_create": (_INT, [_INT, _INT, ctypes.POINTER(_I64), ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(_P)]),
+    "xp_transport_destroy": (_INT, [_P]),
+    "xp_transport_open": (_INT, [_P, _P]),
+    "xp_transport_submit": (_INT, [_P, _INT, _I64, _I64, _INT, _INT, _INT, _P, _I64, _INT, _P]),
+    "xp_transport_evaluate": (_INT, [_P, _INT, _P, _P]),
+    "xp_transport_complete": (_INT, [_P, _INT, _P, _I64, _I64, _P]),
+    "xp_transport_settle": (_INT, [_P, _INT, _P, _P, _I64, _P]),
+    "xp_transport_drain": (_INT, [_P, _P]),
+    "xp_transport_publish_failure": (_INT, [_P, _INT, _INT, _P]),
+    "xp_transport_snapshot": (_INT, [_P, _INT, _P]),
+    "xp_transport_probe": (_INT, [_P, _INT, _INT, ctypes.POINTER(ctypes.c_uint32), _INT]),
 }
 
 

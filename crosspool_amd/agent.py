@@ -84,6 +84,10 @@ class ExecutorLane:
         stream = ctypes.c_void_p()
         _native.call("xp_lane_stream", self.handle, ctypes.byref(stream))
         self.stream = torch.cuda.ExternalStream(stream.value or 0, device=agent.device)
+        fault = ctypes.c_void_p()
+        _native.call("xp_lane_fault_word", self.handle, ctypes.byref(fault))
+        # Device address of the Lane's sticky fault word (read by the Transport's evaluate).
+        self.fault_word = int(fault.value or 0)
         self.templates: dict[tuple[int, int, int], GraphTemplate] = {}
         self._in_flight: deque[tuple[torch.cuda.Event | None, tuple[torch.Tensor, ...], torch.cuda.Stream]] = deque()
 
@@ -146,9 +150,8 @@ class ExecutorLane:
         if stream is None:
             # Lane stream: order after the caller's pending work on the current stream.
             self.stream.wait_stream(current)
-            stream_handle = None
-        else:
-            stream_handle = ctypes.c_void_p(stream.cuda_stream)
+        # A handle of 0 is the legacy default stream (torch's default stream).
+        stream_handle = ctypes.c_void_p(run_on.cuda_stream)
         _native.call(
             "xp_replay", self.handle, instance_index, layer_ordinal, rows, ctypes.c_void_p(pool.data_ptr()),
             ctypes.c_void_p(out_pool.data_ptr()), pool.shape[0], ctypes.c_void_p(slots.data_ptr()), stream_handle,

@@ -281,7 +281,39 @@ struct xp_lane {
   bool graph_dispatch = false;
 };
 
+// A Transport resident: the device array of arenas it serves (one per Instance rank) and
+// the host facts the C ABI validates against.  Replaces the AtnAgent-owned arenas and the
+// TransportResident of src/cext/transport/atnagent.cpp (one Resident block per arena).
+struct xp_transport {
+  int device = 0;
+  int arena_count = 0;
+  TransportArena *arenas = nullptr;
+  std::vector<int64_t> capacities;
+  std::vector<int32_t> atn_dp_sizes;
+  uint64_t wall_clock_khz = 0;
+  std::mutex mutex;  // serialises host calls, as the Attachment mutex does (instance.hpp:113-114)
+};
+
 namespace {
+
+TransportArgs transport_args(xp_transport_t transport, int arena) {
+  TransportArgs args{};
+  args.arenas = transport->arenas;
+  args.arena = arena;
+  args.arena_count = transport->arena_count;
+  return args;
+}
+
+int launch_transport(xp_transport_t transport, const KernelLaunch &kernel, xp_stream_t stream) {
+  XP_HIP_CHECK(hipSetDevice(transport->device));
+  XP_HIP_CHECK(launch(kernel, static_cast<hipStream_t>(stream)));
+  return XP_OK;
+}
+
+bool valid_arena(xp_transport_t transport, int arena) {
+  return transport != nullptr && arena >= 0 && arena < transport->arena_count;
+}
+
 
 void destroy_template(Template &t) {
   if (t.exec != nullptr) {
@@ -802,7 +834,8 @@ int xp_replay(xp_lane_t lane, int instance_index, int layer_ordinal, int64_t row
   if (launches.chain(chain) != selected->node_count) {
     return fail(XP_ERROR_STATE, "replay kernel sequence differs from the captured template");
   }
-  const hipStream_t target = stream != nullptr ? static_cast<hipStream_t>(stream) : lane->stream;
+  // NULL is the legacy default stream, as for every other entry point.
+  const hipStream_t target = static_cast<hipStream_t>(stream);
   if (!lane->graph_dispatch) {
     for (int index = 0; index < selected->node_count; ++index) {
       XP_HIP_CHECK(launch(*chain[index], target));
@@ -821,6 +854,215 @@ int xp_replay(xp_lane_t lane, int instance_index, int layer_ordinal, int64_t row
     bound = *chain[index];
   }
   XP_HIP_CHECK(hipGraphLaunch(selected->exec, target));
+  return XP_OK;
+}
+
+
+// ------------------------------------------------------------------ transport
+
+int xp_lane_fault_word(xp_lane_t lane, uint32_t **out) {
+  XP_REQUIRE(lane != nullptr && out != nullptr, "lane and output pointer must be non-null");
+  *out = lane->fault;
+  return XP_OK;
+}
+
+int xp_transport_create(int device, int arena_count, const int64_t *payload_row_capacities,
+                        const int32_t *atn_dp_sizes, xp_transport_t *out) {
+  XP_REQUIRE(out != nullptr, "output pointer must be non-null");
+  XP_REQUIRE(arena_count >= 1 && arena_count <= 1024, "a transport serves 1 to 1024 arenas");
+  XP_REQUIRE(payload_row_capacities != nullptr && atn_dp_sizes != nullptr, "arena geometry must be given");
+  for (int index = 0; index < arena_count; ++index) {
+    XP_REQUIRE(payload_row_capacities[index] > 0, "arena payload row capacity must be positive");
+    XP_REQUIRE(atn_dp_sizes[index] >= 1 && atn_dp_sizes[index] <= kMaxDpRanks,
+               "attention DP size must be between 1 and 64");
+  }
+  XP_HIP_CHECK(hipSetDevice(device));
+  auto transport = std::make_unique<xp_transport>();
+  transport->device = device;
+  transport->arena_count = arena_count;
+  int rate_khz = 0;
+  XP_HIP_CHECK(hipDeviceGetAttribute(&rate_khz, hipDeviceAttributeWallClockRate, device));
+  XP_REQUIRE(rate_khz > 0, "device reports no wall clock rate");
+  transport->wall_clock_khz = static_cast<uint64_t>(rate_khz);
+  std::vector<TransportArena> image(static_cast<size_t>(arena_count));
+  for (int index = 0; index < arena_count; ++index) {
+    std::memset(&image[index], 0, sizeof(TransportArena));  // Dormant, Ok, no shutdown
+    image[index].payload_row_capacity = static_cast<uint64_t>(payload_row_capacities[index]);
+    image[index].atn_dp_size = static_cast<uint32_t>(atn_dp_sizes[index]);
+    image[index].instance_outcome = kResultOk;
+    transport->capacities.push_back(payload_row_capacities[index]);
+    transport->atn_dp_sizes.push_back(atn_dp_sizes[index]);
+  }
+  void *memory = nullptr;
+  XP_HIP_CHECK(hipMalloc(&memory, sizeof(TransportArena) * image.size()));
+  const hipError_t copied = hipMemcpy(memory, image.data(), sizeof(TransportArena) * image.size(),
+                                      hipMemcpyHostToDevice);
+  if (copied != hipSuccess) {
+    (void)hipFree(memory);
+    return fail(XP_ERROR_HIP, std::string("initialising the transport arenas failed: ") + hipGetErrorString(copied));
+  }
+  transport->arenas = static_cast<TransportArena *>(memory);
+  *out = transport.release();
+  return XP_OK;
+}
+
+int xp_transport_destroy(xp_transport_t transport) {
+  if (transport == nullptr) {
+    return XP_OK;
+  }
+  XP_HIP_CHECK(hipSetDevice(transport->device));
+  XP_HIP_CHECK(hipDeviceSynchronize());
+  (void)hipFree(transport->arenas);
+  delete transport;
+  return XP_OK;
+}
+
+
+int xp_transport_open(xp_transport_t transport, xp_stream_t stream) {
+  XP_REQUIRE(transport != nullptr, "transport must be non-null");
+  std::lock_guard<std::mutex> guard(transport->mutex);
+  return launch_transport(transport, make_transport_open(transport_args(transport, 0)), stream);
+}
+
+int xp_transport_submit(xp_transport_t transport, int arena, int64_t payload_rows, int64_t layer_ordinal,
+                        int forward_mode, int output_requirement, int dp_row_layout,
+                        const void *dp_rank_payload_rows, int64_t dp_rank_count, int dp_rows_i64,
+                        xp_stream_t stream) {
+  XP_REQUIRE(valid_arena(transport, arena), "arena index is outside the transport");
+  XP_REQUIRE(layer_ordinal >= 0, "layer ordinal must be non-negative");
+  XP_REQUIRE(forward_mode == XP_FORWARD_PREFILL || forward_mode == XP_FORWARD_DECODE || forward_mode == XP_FORWARD_IDLE,
+             "forward mode is outside the FFN vocabulary");
+  XP_REQUIRE(output_requirement == XP_OUTPUT_PER_RANK_COMPLETE || output_requirement == XP_OUTPUT_GROUP_SUM_COMPLETE,
+             "output requirement is outside the FFN vocabulary");
+  XP_REQUIRE(dp_row_layout >= XP_DP_ROWS_NONE && dp_row_layout <= XP_DP_ROWS_PACKED_BY_RANK,
+             "DP row layout is outside the FFN vocabulary");
+  const int64_t capacity = transport->capacities[arena];
+  const int32_t dp_size = transport->atn_dp_sizes[arena];
+  XP_REQUIRE(payload_rows > 0 && payload_rows <= capacity, "xpool FFN request row count exceeds Transport capacity");
+  const bool present = dp_rank_payload_rows != nullptr && dp_rank_count != 0;
+  if (dp_size == 1) {
+    XP_REQUIRE(dp_row_layout == XP_DP_ROWS_NONE && !present,
+               "xpool DP-one request must use NONE without a per-rank row vector");
+  } else {
+    XP_REQUIRE(dp_row_layout != XP_DP_ROWS_NONE, "xpool DP request requires UNIFORM_BY_RANK or PACKED_BY_RANK");
+    XP_REQUIRE(present && dp_rank_count == dp_size,
+               "xpool FFN shim DP-rank payload rows must have one entry per attention DP rank");
+  }
+  TransportArgs args = transport_args(transport, arena);
+  args.payload_rows = static_cast<uint64_t>(payload_rows);
+  args.request = RequestMetadata{static_cast<uint64_t>(layer_ordinal), static_cast<uint32_t>(forward_mode),
+                                 static_cast<uint32_t>(output_requirement), static_cast<uint32_t>(dp_row_layout), 0};
+  args.dp_rows = present ? dp_rank_payload_rows : nullptr;
+  args.dp_rows_count = present ? static_cast<uint32_t>(dp_rank_count) : 0;
+  args.dp_rows_i64 = dp_rows_i64 != 0 ? 1u : 0u;
+  std::lock_guard<std::mutex> guard(transport->mutex);
+  return launch_transport(transport, make_transport_submit(args), stream);
+}
+
+int xp_transport_evaluate(xp_transport_t transport, int arena, const uint32_t *fault_word, xp_stream_t stream) {
+  XP_REQUIRE(valid_arena(transport, arena), "arena index is outside the transport");
+  TransportArgs args = transport_args(transport, arena);
+  args.fault = fault_word;
+  std::lock_guard<std::mutex> guard(transport->mutex);
+  return launch_transport(transport, make_transport_evaluate(args), stream);
+}
+
+int xp_transport_complete(xp_transport_t transport, int arena, void *output, int64_t output_elements,
+                          int64_t timeout_ns, xp_stream_t stream) {
+  XP_REQUIRE(valid_arena(transport, arena), "arena index is outside the transport");
+  XP_REQUIRE(output_elements >= 0, "output element count must be non-negative");
+  XP_REQUIRE(output != nullptr || output_elements == 0, "output must be non-null when it has elements");
+  XP_REQUIRE((reinterpret_cast<uintptr_t>(output) & 1u) == 0, "output must be 2-byte aligned bf16");
+  TransportArgs args = transport_args(transport, arena);
+  args.output = static_cast<uint16_t *>(output);
+  args.output_elements = static_cast<uint64_t>(output_elements);
+  const uint64_t nanoseconds = timeout_ns > 0 ? static_cast<uint64_t>(timeout_ns) : kTransportDefaultTimeoutNs;
+  // ticks = ns * kHz / 1e6, kept in range for timeouts up to hours.
+  args.timeout_ticks = nanoseconds / 1000 * transport->wall_clock_khz / 1000 + 1;
+  std::lock_guard<std::mutex> guard(transport->mutex);
+  return launch_transport(transport, make_transport_complete(args), stream);
+}
+
+int xp_transport_settle(xp_transport_t transport, int arena, const uint32_t *fault_word, void *output,
+                        int64_t output_elements, xp_stream_t stream) {
+  XP_REQUIRE(valid_arena(transport, arena), "arena index is outside the transport");
+  XP_REQUIRE(output_elements >= 0, "output element count must be non-negative");
+  XP_REQUIRE(output != nullptr || output_elements == 0, "output must be non-null when it has elements");
+  XP_REQUIRE((reinterpret_cast<uintptr_t>(output) & 1u) == 0, "output must be 2-byte aligned bf16");
+  TransportArgs args = transport_args(transport, arena);
+  args.fault = fault_word;
+  args.output = static_cast<uint16_t *>(output);
+  args.output_elements = static_cast<uint64_t>(output_elements);
+  args.timeout_ticks = kTransportDefaultTimeoutNs / 1000 * transport->wall_clock_khz / 1000 + 1;
+  std::lock_guard<std::mutex> guard(transport->mutex);
+  return launch_transport(transport, make_transport_settle(args), stream);
+}
+
+int xp_transport_drain(xp_transport_t transport, xp_stream_t stream) {
+  XP_REQUIRE(transport != nullptr, "transport must be non-null");
+  std::lock_guard<std::mutex> guard(transport->mutex);
+  return launch_transport(transport, make_transport_drain(transport_args(transport, 0)), stream);
+}
+
+int xp_transport_publish_failure(xp_transport_t transport, int arena, int result_code, xp_stream_t stream) {
+  XP_REQUIRE(valid_arena(transport, arena), "arena index is outside the transport");
+  XP_REQUIRE(result_code >= XP_RESULT_OK && result_code <= XP_RESULT_TIMEOUT, "result code is outside the vocabulary");
+  TransportArgs args = transport_args(transport, arena);
+  args.code = static_cast<uint32_t>(result_code);
+  std::lock_guard<std::mutex> guard(transport->mutex);
+  return launch_transport(transport, make_transport_publish_failure(args), stream);
+}
+
+int xp_transport_snapshot(xp_transport_t transport, int arena, xp_arena_snapshot *out) {
+  XP_REQUIRE(valid_arena(transport, arena), "arena index is outside the transport");
+  XP_REQUIRE(out != nullptr, "output pointer must be non-null");
+  XP_HIP_CHECK(hipSetDevice(transport->device));
+  XP_HIP_CHECK(hipDeviceSynchronize());
+  TransportArena image{};
+  XP_HIP_CHECK(hipMemcpy(&image, transport->arenas + arena, sizeof image, hipMemcpyDeviceToHost));
+  std::memset(out, 0, sizeof *out);
+  out->mailbox_status = image.mailbox.status;
+  out->result_code = image.mailbox.result_code;
+  out->payload_rows = image.mailbox.payload_rows;
+  out->layer_ordinal = image.mailbox.request.layer_ordinal;
+  out->forward_mode = image.mailbox.request.forward_mode;
+  out->output_requirement = image.mailbox.request.output_requirement;
+  out->dp_row_layout = image.mailbox.request.dp_row_layout;
+  out->shutdown = image.shutdown;
+  out->generation_failure = image.generation_failure;
+  out->violations = image.violations;
+  out->instance_outcome = image.instance_outcome;
+  out->atn_dp_size = image.atn_dp_size;
+  out->payload_row_capacity = image.payload_row_capacity;
+  std::memcpy(out->dp_rank_payload_rows, image.dp_rank_payload_rows, sizeof out->dp_rank_payload_rows);
+  return XP_OK;
+}
+
+int xp_transport_probe(xp_transport_t transport, int arena, int scenario, uint32_t *observed, int max_words) {
+  XP_REQUIRE(valid_arena(transport, arena), "arena index is outside the transport");
+  XP_REQUIRE(scenario >= 0 && scenario <= 6, "probe scenario must be between 0 and 6");
+  XP_REQUIRE(observed != nullptr && max_words >= 16, "observation buffer must hold 16 words");
+  XP_HIP_CHECK(hipSetDevice(transport->device));
+  void *words = nullptr;
+  XP_HIP_CHECK(hipMalloc(&words, 16 * sizeof(uint32_t)));
+  TransportArgs args = transport_args(transport, arena);
+  args.output = static_cast<uint16_t *>(words);
+  args.code = static_cast<uint32_t>(scenario);
+  hipError_t status = hipMemset(words, 0xff, 16 * sizeof(uint32_t));
+  if (status == hipSuccess) {
+    std::lock_guard<std::mutex> guard(transport->mutex);
+    status = launch(make_transport_probe(args), nullptr);
+  }
+  if (status == hipSuccess) {
+    status = hipDeviceSynchronize();
+  }
+  if (status == hipSuccess) {
+    status = hipMemcpy(observed, words, 16 * sizeof(uint32_t), hipMemcpyDeviceToHost);
+  }
+  (void)hipFree(words);
+  if (status != hipSuccess) {
+    return fail(XP_ERROR_HIP, std::string("transport probe failed: ") + hipGetErrorString(status));
+  }
   return XP_OK;
 }
 

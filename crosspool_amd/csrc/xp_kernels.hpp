@@ -82,6 +82,79 @@ struct ReduceArgs {
 
 KernelLaunch make_copy(const CopyArgs &args);
 KernelLaunch make_reduce_partials(const ReduceArgs &args);
+
+// ---------------------------------------------------------------- mailbox protocol
+// Device image of one Transport arena's control words and request mailbox, shared by the
+// Instance side (submit / complete) and the Agent side (evaluate / drain).  Values of the
+// status and result words follow src/cext-include/xpool/transport/protocol.hpp:33-49 and
+// src/cext-include/xpool/ffn.hpp:43-48.
+enum : uint32_t {
+  kMailboxDormant = 0,
+  kMailboxIdle = 1,
+  kMailboxStaging = 2,
+  kMailboxPublished = 3,
+  kMailboxEvaluated = 4,
+  kMailboxClosed = 5,
+};
+enum : uint32_t { kResultOk = 0, kResultShutdown = 1, kResultProtocolMismatch = 2, kResultTimeout = 3 };
+// Instance outcome word while a request is between submit and complete.
+constexpr uint32_t kOutcomePending = 0xffffffffu;
+constexpr int kMaxDpRanks = 64;
+// Liveness deadline of the completion's wait (the reference's kDefaultTimeoutNanoseconds,
+// src/cext-include/xpool/utils/wait.cuh:17).
+constexpr uint64_t kTransportDefaultTimeoutNs = 5000000000ull;
+
+struct RequestMetadata {
+  uint64_t layer_ordinal;
+  uint32_t forward_mode;
+  uint32_t output_requirement;
+  uint32_t dp_row_layout;
+  uint32_t reserved;
+};
+
+struct alignas(8) Mailbox {
+  uint32_t status;       // MailboxStatus, accessed with system-scope acquire / release atomics
+  uint32_t result_code;  // published with Evaluated
+  uint64_t payload_rows;
+  RequestMetadata request;
+};
+
+struct alignas(256) TransportArena {
+  uint32_t shutdown;            // monotonic terminal fact (arena.hpp ArenaState)
+  uint32_t generation_failure;  // sticky canonical failure (ResultCode)
+  uint32_t violations;          // sticky count of protocol preconditions found broken
+  uint32_t instance_outcome;    // Instance-private: kOutcomePending, then the last request's result
+  uint64_t payload_row_capacity;
+  uint32_t atn_dp_size;
+  uint32_t reserved;
+  Mailbox mailbox;
+  uint32_t dp_rank_payload_rows[kMaxDpRanks];
+};
+
+struct TransportArgs {
+  TransportArena *arenas;       // every arena of the resident (drain walks them all)
+  int32_t arena;                // the arena this call serves
+  int32_t arena_count;
+  const void *dp_rows;          // submit: per-DP-rank physical rows (int32 or int64) or null
+  uint16_t *output;             // complete: caller output, NaN-filled on failure; probe: observations
+  const uint32_t *fault;        // evaluate: the Lane's sticky fault word, or null
+  uint64_t output_elements;     // complete
+  uint64_t payload_rows;        // submit
+  uint64_t timeout_ticks;       // complete: wall-clock ticks before the wait gives up
+  RequestMetadata request;      // submit
+  uint32_t dp_rows_i64;         // submit
+  uint32_t dp_rows_count;       // submit: entries of dp_rows (0 = absent)
+  uint32_t code;                // publish_failure: result code; probe: scenario
+};
+
+KernelLaunch make_transport_open(const TransportArgs &args);
+KernelLaunch make_transport_submit(const TransportArgs &args);
+KernelLaunch make_transport_evaluate(const TransportArgs &args);
+KernelLaunch make_transport_complete(const TransportArgs &args);
+KernelLaunch make_transport_settle(const TransportArgs &args);
+KernelLaunch make_transport_drain(const TransportArgs &args);
+KernelLaunch make_transport_publish_failure(const TransportArgs &args);
+KernelLaunch make_transport_probe(const TransportArgs &args);
 // `capacity` sizes the grid (graph templates keep one grid per capacity);
 // workgroups beyond the live rows exit immediately.
 KernelLaunch make_gather(const GatherArgs &args, int64_t capacity);

@@ -6,6 +6,15 @@ checks of ``InstanceRankRuntime::Attachment::submit``
 attachment is an in-process :class:`~crosspool_amd.agent.FfnAgent`: the
 caller's hidden states are the mailbox and rows ``0..T-1`` are its slots, which
 is exactly the reference's contiguous row-prefix Transport copy.
+
+By default each call runs the reference's Transport mailbox transaction
+(instance.cu:36-201, atnagent.cu:48-90) around the Dense step, all on the
+caller's stream: the request is claimed and published, the Lane's kernels run the
+step, and one launch answers the request and completes it (acknowledge, or the
+NaN-filled canonical failure output).  With ``lane_stream=True`` the step and the
+answer run on the Lane's own stream between two events instead (two cross-stream
+hops, ~35 us more per call on MI355X).  ``attach(..., mailbox=False)`` runs the
+step on the caller's stream without the mailbox.
 """
 
 from __future__ import annotations
@@ -17,9 +26,9 @@ import torch
 
 from crosspool_amd.agent import FfnAgent
 from crosspool_amd.ffn import DpRowLayout
-from crosspool_amd.transport import FfnRequestMetadata
+from crosspool_amd.transport import FfnRequestMetadata, TransportResident
 
-__all__ = ["attach", "detach", "ffn_shim"]
+__all__ = ["attach", "attached_transport", "detach", "ffn_shim"]
 
 
 @dataclass
@@ -31,14 +40,32 @@ class _Attachment:
     atn_dp_size: int
     lane: int
     identity_slots: torch.Tensor
+    transport: TransportResident | None
+    timeout_ns: int
+    lane_stream: bool
 
 
 _lock = threading.Lock()
 _attachment: _Attachment | None = None
 
 
-def attach(agent: FfnAgent, *, instance_index: int = 0, atn_dp_size: int = 1, lane: int = 0) -> None:
-    """Attach this process's shim to a materialized agent (Attachment::attach analogue)."""
+def attach(
+    agent: FfnAgent,
+    *,
+    instance_index: int = 0,
+    atn_dp_size: int = 1,
+    lane: int = 0,
+    mailbox: bool = True,
+    lane_stream: bool = False,
+    timeout_ns: int = 0,
+) -> None:
+    """Attach this process's shim to a materialized agent (Attachment::attach analogue).
+
+    With ``mailbox`` a one-arena :class:`TransportResident` is created and opened, and
+    every call runs the mailbox transaction, with the Dense step on the caller's stream
+    or, with ``lane_stream``, on the Lane's stream; ``timeout_ns`` bounds the two-stream
+    completion's wait (0: the reference's 5 s).
+    """
 
     global _attachment
     if not agent.materialized:
@@ -48,7 +75,12 @@ def attach(agent: FfnAgent, *, instance_index: int = 0, atn_dp_size: int = 1, la
         raise ValueError("the attached instance must have registered layers of one hidden size")
     hidden_size = shapes.pop()
     capacity = max(t.signature.payload_row_capacity for t in agent.templates.values())
+    transport = None
+    if mailbox:
+        transport = TransportResident(agent.device, [(capacity, atn_dp_size)])
+        transport.open()
     with _lock:
+        previous = _attachment
         _attachment = _Attachment(
             agent=agent,
             instance_index=instance_index,
@@ -57,13 +89,31 @@ def attach(agent: FfnAgent, *, instance_index: int = 0, atn_dp_size: int = 1, la
             atn_dp_size=atn_dp_size,
             lane=lane,
             identity_slots=torch.arange(capacity, dtype=torch.int32, device=agent.device),
+            transport=transport,
+            timeout_ns=int(timeout_ns),
+            lane_stream=bool(lane_stream),
         )
+    if previous is not None and previous.transport is not None:
+        previous.transport.close()
 
 
 def detach() -> None:
+    """Drop the attachment; its Transport is drained and released."""
+
     global _attachment
     with _lock:
+        previous = _attachment
         _attachment = None
+    if previous is not None and previous.transport is not None:
+        previous.transport.drain()
+        previous.transport.close()
+
+
+def attached_transport() -> TransportResident | None:
+    """The attachment's Transport resident (``None`` without a mailbox)."""
+
+    attachment = _attachment
+    return None if attachment is None else attachment.transport
 
 
 def ffn_shim(
@@ -125,10 +175,42 @@ def ffn_shim(
         raise RuntimeError(f"xpool FFN shim layer {request_metadata.layer_ordinal} is not installed")
 
     output = torch.empty_like(hidden_states)
+    agent = attachment.agent
+    caller = torch.cuda.current_stream(hidden_states.device)
+    transport = attachment.transport
     # The FFN is row-independent, so every DP row layout is served by running
     # all physical rows; padding rows of UNIFORM_BY_RANK spans compute garbage
     # that the producer never reads.
-    attachment.agent.execute(
+    if transport is None:
+        agent.execute(
+            instance_index=attachment.instance_index,
+            layer_ordinal=request_metadata.layer_ordinal,
+            pool=hidden_states,
+            out_pool=output,
+            slots=attachment.identity_slots,
+            rows=payload_rows,
+            lane=attachment.lane,
+            stream=caller,
+        )
+        return output
+    lane = agent.lanes[attachment.lane]
+    rows_vector = dp_rank_payload_rows if present else None
+    transport.submit(0, payload_rows, request_metadata, rows_vector, stream=caller)
+    if not attachment.lane_stream:
+        agent.execute(
+            instance_index=attachment.instance_index,
+            layer_ordinal=request_metadata.layer_ordinal,
+            pool=hidden_states,
+            out_pool=output,
+            slots=attachment.identity_slots,
+            rows=payload_rows,
+            lane=attachment.lane,
+            stream=caller,
+        )
+        transport.settle(0, output, lane.fault_word, stream=caller)
+        return output
+    # The Lane stream waits for the published request, runs the Dense step and answers it.
+    agent.execute(
         instance_index=attachment.instance_index,
         layer_ordinal=request_metadata.layer_ordinal,
         pool=hidden_states,
@@ -136,6 +218,8 @@ def ffn_shim(
         slots=attachment.identity_slots,
         rows=payload_rows,
         lane=attachment.lane,
-        stream=torch.cuda.current_stream(hidden_states.device),
     )
+    transport.evaluate(0, lane.fault_word, stream=lane.stream)
+    caller.wait_stream(lane.stream)
+    transport.complete(0, output, timeout_ns=attachment.timeout_ns, stream=caller)
     return output

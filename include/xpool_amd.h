@@ -4,7 +4,7 @@
  * This library replaces the pybind11 extension `xpool.native` (src/cext-bindings/)
  * for the FfnAgent execution path only.  Every entry point takes plain device
  * pointers, sizes and a HIP stream (`void *` = hipStream_t; NULL = the legacy
- * default stream for kernel-level calls, the Lane's own stream for replays).
+ * default stream; a Lane's own stream comes from xp_lane_stream).
  * No torch types cross this boundary.  References are file:line in the
  * CrossPool checkout.
  *
@@ -192,12 +192,115 @@ int xp_template_capacities(xp_lane_t lane, int64_t hidden, int64_t intermediate,
 
 /* Replay the smallest captured capacity >= rows for the layer: gather rows
  * slots[0..rows) of pool_in (+ RMSNorm), Dense FFN, write them to the same slots
- * of pool_out.  stream NULL = the Lane's stream.  1 <= rows <= largest capacity.
+ * of pool_out on `stream` (NULL = the legacy default stream; the Lane's own stream is
+ * xp_lane_stream's).  1 <= rows <= largest capacity.
  * Replaces wait_pre_compute's layer + capacity selection
  * (src/cext/ffnagent/runtime.cu:232-258), bind_compute (:336-369) and the
  * captured Dense body (registry.py:212-217). */
 int xp_replay(xp_lane_t lane, int instance_index, int layer_ordinal, int64_t rows, const void *pool_in,
               void *pool_out, int64_t pool_rows, const int32_t *slots, xp_stream_t stream);
+
+/* Device address of the Lane's sticky fault word, for xp_transport_evaluate.  Replaces the
+ * Lane fault observation the reference's check_health reads (src/cext/ffnagent/runtime.cu
+ * health path, src/cext-bindings/ffnagent.cpp:231). */
+int xp_lane_fault_word(xp_lane_t lane, uint32_t **out);
+
+/* ------------------------------------------------------------------ transport mailbox */
+
+/* Mailbox lifecycle values (src/cext-include/xpool/transport/protocol.hpp:33-49). */
+enum {
+  XP_MAILBOX_DORMANT = 0,
+  XP_MAILBOX_IDLE = 1,
+  XP_MAILBOX_STAGING = 2,
+  XP_MAILBOX_PUBLISHED = 3,
+  XP_MAILBOX_EVALUATED = 4,
+  XP_MAILBOX_CLOSED = 5
+};
+
+typedef struct xp_transport *xp_transport_t;
+
+/* Host copy of one arena: the mailbox (protocol.hpp:52-62), the arena state words
+ * (arena.hpp ArenaState: shutdown, generation_failure_code), the staged per-DP-rank rows,
+ * and two words of this build: `violations` counts broken protocol preconditions (where the
+ * reference traps with xpool::abort_if these kernels count and publish ProtocolMismatch),
+ * `instance_outcome` is the last completed request's result (0xffffffff while one is in
+ * flight). */
+typedef struct {
+  uint32_t mailbox_status;
+  uint32_t result_code;
+  uint64_t payload_rows;
+  uint64_t layer_ordinal;
+  uint32_t forward_mode;
+  uint32_t output_requirement;
+  uint32_t dp_row_layout;
+  uint32_t shutdown;
+  uint32_t generation_failure;
+  uint32_t violations;
+  uint32_t instance_outcome;
+  uint32_t atn_dp_size;
+  uint64_t payload_row_capacity;
+  uint32_t dp_rank_payload_rows[64];
+} xp_arena_snapshot;
+
+/* A Transport resident on `device` serving `arena_count` arenas (one per Instance rank),
+ * arena i with payload row capacity capacities[i] and attention DP size dp_sizes[i] (1..64).
+ * Every mailbox starts Dormant.  Replaces the AtnAgent's arena allocation and
+ * TransportResident (src/cext/transport/arena.cpp, atnagent.cpp). */
+int xp_transport_create(int device, int arena_count, const int64_t *payload_row_capacities,
+                        const int32_t *atn_dp_sizes, xp_transport_t *out);
+/* Synchronous: waits for the device, then frees the arenas. */
+int xp_transport_destroy(xp_transport_t transport);
+
+/* Resident startup: every Dormant mailbox becomes Idle (src/cext/transport/atnagent.cu:124-129). */
+int xp_transport_open(xp_transport_t transport, xp_stream_t stream);
+
+/* Instance side, first half of one request (src/cext/transport/instance.cu:46-128 with the
+ * host checks of instance.cpp:82-119): reject before staging on a canonical failure or
+ * shutdown, else claim the mailbox (Idle -> Staging), stage the per-DP-rank rows (int32 or
+ * int64 device vector of dp_rank_count entries, or NULL), write the request facts and
+ * publish (Staging -> Published).  The payload itself is not copied: on one device the Lane
+ * reads the caller's rows in place. */
+int xp_transport_submit(xp_transport_t transport, int arena, int64_t payload_rows, int64_t layer_ordinal,
+                        int forward_mode, int output_requirement, int dp_row_layout,
+                        const void *dp_rank_payload_rows, int64_t dp_rank_count, int dp_rows_i64,
+                        xp_stream_t stream);
+
+/* Agent side, after the Lane's Dense step (src/cext/transport/atnagent.cu:34-90,155-170):
+ * answer a Published request with OK, or PROTOCOL_MISMATCH when the request is invalid
+ * (request_valid, atnagent.cu:34-46) or the Lane's fault word (may be NULL) is set; a
+ * mismatch drains every arena of the transport. */
+int xp_transport_evaluate(xp_transport_t transport, int arena, const uint32_t *fault_word, xp_stream_t stream);
+
+/* Instance side, second half (src/cext/transport/instance.cu:130-201): wait up to timeout_ns
+ * (<= 0: 5 s, wait.cuh:17) for the result; OK acknowledges (Evaluated -> Idle, request facts
+ * reset) or, after shutdown, closes; any other result closes the mailbox and fills the
+ * `output_elements` bf16 values of `output` with quiet NaNs (instance.cu:28-31).  A wait that
+ * times out publishes TIMEOUT as the canonical failure (the reference traps there). */
+int xp_transport_complete(xp_transport_t transport, int arena, void *output, int64_t output_elements,
+                          int64_t timeout_ns, xp_stream_t stream);
+
+/* xp_transport_evaluate then xp_transport_complete in one launch on one stream, for a
+ * request whose Dense step ran on that same stream (the completion then never waits). */
+int xp_transport_settle(xp_transport_t transport, int arena, const uint32_t *fault_word, void *output,
+                        int64_t output_elements, xp_stream_t stream);
+
+/* Resident drain (atnagent.cu:92-147): publish shutdown to every arena, close Idle
+ * mailboxes, answer Published ones with the canonical failure or SHUTDOWN. */
+int xp_transport_drain(xp_transport_t transport, xp_stream_t stream);
+
+/* Publish a canonical failure (PROTOCOL_MISMATCH or TIMEOUT) into one arena; the first one
+ * sticks (src/cext-include/xpool/transport/arena.cuh:55-62). */
+int xp_transport_publish_failure(xp_transport_t transport, int arena, int result_code, xp_stream_t stream);
+
+/* Synchronous: waits for the device, then copies one arena to the host
+ * (Arena::state / mailbox_status / read_generation_failure of transport/arena.hpp). */
+int xp_transport_snapshot(xp_transport_t transport, int arena, xp_arena_snapshot *out);
+
+/* Synchronous test entry: runs one of the reference's device-side protocol scenarios on one
+ * arena and copies its observation words (unused ones read 0xffffffff) to `observed`
+ * (at least 16 words): 0-4 tests/suites/cext/transport/view_test.cu:68-150, 5 and 6 the
+ * producer and consumer kernels of tests/suites/cext/transport/shutdown_test.cu:173-191. */
+int xp_transport_probe(xp_transport_t transport, int arena, int scenario, uint32_t *observed, int max_words);
 
 #ifdef __cplusplus
 }

@@ -223,3 +223,19 @@ def test_ffn_shim_requires_an_attachment():
     metadata = FfnRequestMetadata(0, ForwardMode.PREFILL, OutputRequirement.PER_RANK_COMPLETE, DpRowLayout.NONE)
     with pytest.raises(RuntimeError, match="no attached"):
         ffn_shim(torch.zeros((2, 16), dtype=torch.bfloat16), None, metadata)
+
+
+def test_transport_entry_points_validate_before_any_device_call():
+    lib = _native.library()
+    handle = ctypes.c_void_p()
+    capacities = (ctypes.c_int64 * 1)(4)
+    dp_sizes = (ctypes.c_int32 * 1)(1)
+    assert lib.xp_transport_create(0, 0, capacities, dp_sizes, ctypes.byref(handle)) == _native.XP_ERROR_INVALID_ARGUMENT
+    assert "1 to 1024 arenas" in _native.last_error()
+    bad_dp = (ctypes.c_int32 * 1)(65)
+    assert lib.xp_transport_create(0, 1, capacities, bad_dp, ctypes.byref(handle)) == _native.XP_ERROR_INVALID_ARGUMENT
+    assert lib.xp_transport_submit(None, 0, 1, 0, 2, 1, 0, None, 0, 0, None) == _native.XP_ERROR_INVALID_ARGUMENT
+    assert lib.xp_transport_evaluate(None, 0, None, None) == _native.XP_ERROR_INVALID_ARGUMENT
+    assert lib.xp_transport_complete(None, 0, None, 0, 0, None) == _native.XP_ERROR_INVALID_ARGUMENT
+    assert lib.xp_transport_probe(None, 0, 0, None, 0) == _native.XP_ERROR_INVALID_ARGUMENT
+    assert lib.xp_transport_destroy(None) == _native.XP_OK
