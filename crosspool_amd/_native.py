@@ -69,6 +69,15 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "xp_transport_publish_failure": (_INT, [_P, _INT, _INT, _P]),
     "xp_transport_snapshot": (_INT, [_P, _INT, _P]),
     "xp_transport_probe": (_INT, [_P, _INT, _INT, ctypes.POINTER(ctypes.c_uint32), _INT]),
+    "xp_moe_router_topk": (_INT, [_P, _INT, _I64, _I64, _I64, _INT, _P, _INT, _INT, _P, _P, _P]),
+    "xp_moe_router_workspace_bytes": (_SIZE, [_I64, _I64, _I64, _INT]),
+    "xp_moe_router": (_INT, [_P, _I64, _I64, _P, _I64, _I64, _INT, _INT, _P, _INT, _INT, _P, _P, _P, _SIZE, _P]),
+    "xp_moe_finalize_routing": (_INT, [_P, _P, _I64, _I64, _P, _P, _I64, _P, _I64, _F32, _P]),
+    "xp_moe_workspace_bytes": (_SIZE, [_I64, _I64, _I64, _I64, _I64]),
+    "xp_moe_workspace_layout": (_INT, [_I64, _I64, _I64, _I64, _I64, ctypes.POINTER(_SIZE)]),
+    "xp_moe_experts": (
+        _INT, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _F32, _F32, _F32, _F32, _P, _P, _SIZE, _P]
+    ),
 }
 
 

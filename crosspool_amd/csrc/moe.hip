@@ -1,0 +1,600 @@
+// MoE Router and Experts of the FfnAgent path on gfx950.
+//
+// Reference (CrossPool checkout):
+//   * Router: src/xpool/runtime/ffnagent/operators/routing.py:21-89 (router_topk_kernel:
+//     softmax or sigmoid scores, selection-only correction bias, tie policy, renormalisation,
+//     optional rounding to the logits dtype) and :148-190 (Router.run_into: the projection at
+//     the declared precision, then TopK);
+//   * routing finalisation: routing.py:193-307 (routed plus always-selected shared experts,
+//     invalid rows past the live count);
+//   * Experts: src/xpool/runtime/ffnagent/operators/moe.py:168-343 (routes grouped by expert,
+//     grouped i_proj with the row gather and the fused activation, grouped o_proj with the
+//     route scatter and the route weight, sum over a row's routes with the routed scaling
+//     factor), whose numerics the reference spells out in
+//     tests/suites/integration/runtime/ffnagent/test_operators.py:255-281.
+//
+// The reference sorts routes with a bitmatrix and drives triton_kernels' ragged matmul;
+// here one workgroup counts routes per expert in LDS, scans the counts into sorted offsets
+// and an expert tile table, and places each route; the grouped projections are 32x32x16
+// bf16 MFMA tiles over (expert tile, weight tile) with register-staged loads into a
+// double-buffered, XOR-swizzled LDS slab.  A route's output row depends only on its own
+// token row and expert, so the order of routes within an expert does not change any bit.
+
+#include "xp_kernels.hpp"
+
+namespace xp {
+namespace {
+
+constexpr float kNegativeInfinity = -__builtin_inff();
+
+__device__ __forceinline__ float wave_max(float value) {
+#pragma unroll
+  for (int offset = 32; offset > 0; offset >>= 1) {
+    value = fmaxf(value, __shfl_xor(value, offset, kWave));
+  }
+  return value;
+}
+
+__device__ __forceinline__ int wave_min_int(int value) {
+#pragma unroll
+  for (int offset = 32; offset > 0; offset >>= 1) {
+    value = min(value, __shfl_xor(value, offset, kWave));
+  }
+  return value;
+}
+
+__device__ __forceinline__ int wave_max_int(int value) {
+#pragma unroll
+  for (int offset = 32; offset > 0; offset >>= 1) {
+    value = max(value, __shfl_xor(value, offset, kWave));
+  }
+  return value;
+}
+
+// ------------------------------------------------------------------ router
+// One wavefront per row; lane l holds experts l, l + 64, ... (up to 16 each).
+constexpr int kTopkPerLane = kMoeMaxExperts / kWave;
+
+__global__ __launch_bounds__(256) void router_topk_kernel(RouterTopkArgs a) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= a.rows) {
+    return;
+  }
+  const int experts = a.experts;
+  float logit[kTopkPerLane];
+  float maximum = kNegativeInfinity;
+#pragma unroll
+  for (int i = 0; i < kTopkPerLane; ++i) {
+    const int expert = lane + i * kWave;
+    float value = kNegativeInfinity;
+    if (expert < experts) {
+      const int64_t index = row * experts + expert;
+      value = a.logits_f32 != 0 ? static_cast<const float *>(a.logits)[index]
+                                : bf16_to_float(static_cast<const uint16_t *>(a.logits)[index]);
+    }
+    logit[i] = value;
+    maximum = fmaxf(maximum, value);
+  }
+  float score[kTopkPerLane];
+  float selection[kTopkPerLane];
+  if (a.softmax != 0) {
+    maximum = wave_max(maximum);
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kTopkPerLane; ++i) {
+      score[i] = lane + i * kWave < experts ? expf(logit[i] - maximum) : 0.0f;
+      sum += score[i];
+    }
+    sum = wave_sum(sum);
+#pragma unroll
+    for (int i = 0; i < kTopkPerLane; ++i) {
+      score[i] = score[i] / sum;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kTopkPerLane; ++i) {
+      score[i] = 1.0f / (1.0f + expf(-logit[i]));
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kTopkPerLane; ++i) {
+    const int expert = lane + i * kWave;
+    float value = score[i];
+    if (expert < experts && a.correction_bias != nullptr) {
+      value += a.correction_bias[expert];
+    }
+    // Sigmoid stores the selection into the logits buffer and reads it back
+    // (routing.py:62-65): bf16 logits round it there.
+    if (a.softmax == 0 && a.logits_f32 == 0) {
+      value = round_bf16(value);
+    }
+    selection[i] = expert < experts ? value : kNegativeInfinity;
+  }
+
+  // Lane `slot` keeps slot `slot`'s id and weight (topk <= 64).
+  float normalizer = 0.0f;
+  float chosen_weight = 0.0f;
+  int chosen_id = -1;
+  for (int slot = 0; slot < a.topk; ++slot) {
+    float best = kNegativeInfinity;
+#pragma unroll
+    for (int i = 0; i < kTopkPerLane; ++i) {
+      best = fmaxf(best, selection[i]);
+    }
+    best = wave_max(best);
+    // Softmax breaks ties by the lower id, sigmoid by the higher one; padding never wins.
+    int candidate = a.softmax != 0 ? experts : -1;
+#pragma unroll
+    for (int i = 0; i < kTopkPerLane; ++i) {
+      const int expert = lane + i * kWave;
+      if (expert < experts && selection[i] == best) {
+        candidate = a.softmax != 0 ? min(candidate, expert) : max(candidate, expert);
+      }
+    }
+    const int expert = a.softmax != 0 ? wave_min_int(candidate) : wave_max_int(candidate);
+    float own = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kTopkPerLane; ++i) {
+      if (lane + i * kWave == expert) {
+        own = score[i];
+        selection[i] = kNegativeInfinity;
+      }
+    }
+    const float weight =
+        a.softmax != 0 && a.correction_bias == nullptr ? best : __shfl(own, expert & (kWave - 1), kWave);
+    normalizer += weight;
+    if (lane == slot) {
+      chosen_weight = weight;
+      chosen_id = expert;
+    }
+  }
+  if (lane < a.topk) {
+    float weight = chosen_weight;
+    if (a.renormalize != 0) {
+      weight = weight / (normalizer > 0.0f ? normalizer : 1.0f);
+    }
+    if (a.round_to_logits != 0 && a.logits_f32 == 0) {
+      weight = round_bf16(weight);
+    }
+    a.ids[row * a.topk + lane] = chosen_id;
+    a.weights[row * a.topk + lane] = weight;
+  }
+}
+
+// Router logits for the FP32 and FP32_LOGITS precisions, and for PAYLOAD when the geometry
+// does not suit the MFMA projection (hidden or expert count not a multiple of 8): a
+// workgroup computes a 16-row x 64-expert block; thread t owns row t / 16 and experts
+// 4 (t % 16) .. + 3, each a sequential fp32 sum over the hidden dimension staged through LDS
+// 64 columns at a time, stored as fp32 or rounded once to bf16.
+__global__ __launch_bounds__(256) void router_logits_kernel(RouterLogitsArgs a) {
+  constexpr int ROWS = 16;
+  constexpr int EXPERTS = 64;
+  constexpr int CHUNK = 64;
+  __shared__ float xs[ROWS][CHUNK + 1];
+  __shared__ float ws[EXPERTS][CHUNK + 1];
+  const int tid = threadIdx.x;
+  const int64_t row0 = static_cast<int64_t>(blockIdx.y) * ROWS;
+  const int expert0 = static_cast<int>(blockIdx.x) * EXPERTS;
+  const int my_row = tid / 16;
+  const int my_expert = (tid % 16) * 4;
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int64_t k0 = 0; k0 < a.hidden; k0 += CHUNK) {
+    for (int index = tid; index < ROWS * CHUNK; index += 256) {
+      const int r = index / CHUNK;
+      const int c = index % CHUNK;
+      const int64_t row = row0 + r;
+      xs[r][c] = row < a.rows && k0 + c < a.hidden ? bf16_to_float(a.x[row * a.hidden + k0 + c]) : 0.0f;
+    }
+    for (int index = tid; index < EXPERTS * CHUNK; index += 256) {
+      const int e = index / CHUNK;
+      const int c = index % CHUNK;
+      const int expert = expert0 + e;
+      float value = 0.0f;
+      if (expert < a.experts && k0 + c < a.hidden) {
+        const int64_t offset = static_cast<int64_t>(expert) * a.hidden + k0 + c;
+        value = a.weights_f32 != 0 ? static_cast<const float *>(a.w)[offset]
+                                   : bf16_to_float(static_cast<const uint16_t *>(a.w)[offset]);
+      }
+      ws[e][c] = value;
+    }
+    __syncthreads();
+    const int columns = a.hidden - k0 < CHUNK ? static_cast<int>(a.hidden - k0) : CHUNK;
+    for (int c = 0; c < columns; ++c) {
+      const float x = xs[my_row][c];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc[j] = fmaf(x, ws[my_expert + j][c], acc[j]);
+      }
+    }
+    __syncthreads();
+  }
+  const int64_t row = row0 + my_row;
+  if (row < a.rows) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int expert = expert0 + my_expert + j;
+      if (expert < a.experts) {
+        if (a.out_bf16 != 0) {
+          static_cast<uint16_t *>(a.logits)[row * a.experts + expert] = static_cast<uint16_t>(float_to_bf16(acc[j]));
+        } else {
+          static_cast<float *>(a.logits)[row * a.experts + expert] = acc[j];
+        }
+      }
+    }
+  }
+}
+
+// finalize_moe_routing_kernel (routing.py:193-227): routed slots keep their ids and
+// weights, shared slots name experts routed_experts + s with weight 1 / scaling, rows at or
+// past the live count read -1 / 0.
+__global__ __launch_bounds__(256) void finalize_routing_kernel(FinalizeRoutingArgs a) {
+  const int64_t index = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (index >= a.capacity * a.effective_topk) {
+    return;
+  }
+  const int64_t row = index / a.effective_topk;
+  const int slot = static_cast<int>(index % a.effective_topk);
+  const bool live = row < *a.payload_rows;
+  const bool routed = slot < a.routed_topk;
+  int32_t id = -1;
+  float weight = 0.0f;
+  if (live) {
+    if (routed) {
+      id = a.routed_ids[row * a.routed_topk + slot];
+      weight = a.routed_weights[row * a.routed_topk + slot];
+    } else {
+      id = a.routed_experts + slot - a.routed_topk;
+      weight = a.shared_weight;
+    }
+  }
+  a.final_ids[index] = id;
+  a.final_weights[index] = weight;
+}
+
+// ------------------------------------------------------------------ route sort
+// Inclusive scan of one value per thread over a 1024-thread workgroup.
+__device__ int block_inclusive_scan(int value, int *wave_totals) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int offset = 1; offset < kWave; offset <<= 1) {
+    const int other = __shfl_up(value, offset, kWave);
+    if (lane >= offset) {
+      value += other;
+    }
+  }
+  if (lane == kWave - 1) {
+    wave_totals[wave] = value;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int running = 0;
+    for (int w = 0; w < 1024 / kWave; ++w) {
+      const int total = wave_totals[w];
+      wave_totals[w] = running;
+      running += total;
+    }
+  }
+  __syncthreads();
+  return value + wave_totals[wave];
+}
+
+__global__ __launch_bounds__(1024) void moe_sort_kernel(MoeSortArgs a) {
+  __shared__ int counts[kMoeMaxExperts];
+  __shared__ int offsets[kMoeMaxExperts + 1];
+  __shared__ int tiles[kMoeMaxExperts + 1];
+  __shared__ int totals[1024 / kWave];
+  const int tid = threadIdx.x;
+  counts[tid] = 0;
+  __syncthreads();
+  for (int64_t route = tid; route < a.routes; route += 1024) {
+    const int expert = a.ids[route];
+    if (expert >= 0 && expert < a.experts) {
+      atomicAdd(&counts[expert], 1);
+    }
+  }
+  __syncthreads();
+  const int count = tid < a.experts ? counts[tid] : 0;
+  const int row_end = block_inclusive_scan(count, totals);
+  __syncthreads();
+  const int tile_end = block_inclusive_scan((count + a.tile_rows - 1) / a.tile_rows, totals);
+  offsets[tid + 1] = row_end;
+  tiles[tid + 1] = tile_end;
+  if (tid == 0) {
+    offsets[0] = 0;
+    tiles[0] = 0;
+  }
+  __syncthreads();
+  if (tid < a.experts) {
+    a.expert_end[tid] = offsets[tid + 1];
+    counts[tid] = offsets[tid];  // placement cursor
+  }
+  const int total_tiles = tiles[a.experts];
+  for (int tile = tid; tile < a.max_tiles; tile += 1024) {
+    if (tile >= total_tiles) {
+      a.tile_expert[tile] = -1;
+      a.tile_row0[tile] = 0;
+      continue;
+    }
+    // The last expert whose first tile is at or before this one owns it.
+    int low = 0;
+    int high = a.experts - 1;
+    while (low < high) {
+      const int middle = (low + high + 1) / 2;
+      if (tiles[middle] <= tile) {
+        low = middle;
+      } else {
+        high = middle - 1;
+      }
+    }
+    a.tile_expert[tile] = low;
+    a.tile_row0[tile] = offsets[low] + (tile - tiles[low]) * a.tile_rows;
+  }
+  __syncthreads();
+  for (int64_t route = tid; route < a.routes; route += 1024) {
+    const int expert = a.ids[route];
+    if (expert >= 0 && expert < a.experts) {
+      const int position = atomicAdd(&counts[expert], 1);
+      a.sorted_route[position] = static_cast<int32_t>(route);
+    }
+  }
+}
+
+// ------------------------------------------------------------------ grouped projection
+__device__ __forceinline__ int moe_swizzle(int row) { return (row >> 1) & 7; }
+
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool GATED>
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void moe_gemm_kernel(MoeGemmArgs a) {
+  constexpr int THREADS = 64 * WAVES_M * WAVES_N;
+  constexpr int BK = 64;
+  constexpr int WTM = BM / WAVES_M;
+  constexpr int WTN = BN / WAVES_N;
+  constexpr int MT = WTM / 32;
+  constexpr int NT = WTN / 32;
+  constexpr int ROW_STEP = THREADS / 8;  // rows one load pass covers (8 chunks per row)
+  constexpr int A_LOADS = BM / ROW_STEP;
+  constexpr int B_LOADS = BN / ROW_STEP;
+  static_assert(MT >= 1 && NT >= 1 && A_LOADS >= 1 && B_LOADS >= 1, "tile shape");
+  static_assert(A_LOADS * ROW_STEP == BM && B_LOADS * ROW_STEP == BN, "loads must cover the tile");
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2][(BM + BN) * BK];
+
+  const int tile = static_cast<int>(blockIdx.y);
+  const int expert = a.tile_expert[tile];
+  if (expert < 0) {
+    return;
+  }
+  const int row0 = a.tile_row0[tile];
+  const int end = a.expert_end[expert];
+  const int live = end - row0 < BM ? end - row0 : BM;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * BN;
+  const int tid = static_cast<int>(threadIdx.x);
+  const int chunk = tid & 7;
+  const int load_row = tid >> 3;
+
+  const uint16_t *a_source[A_LOADS];
+#pragma unroll
+  for (int j = 0; j < A_LOADS; ++j) {
+    const int r = load_row + j * ROW_STEP;
+    if (r < live) {
+      const int64_t source_row = GATED ? a.sorted_route[row0 + r] / a.topk : static_cast<int64_t>(row0 + r);
+      a_source[j] = a.x + source_row * a.k;
+    } else {
+      a_source[j] = nullptr;
+    }
+  }
+  const uint16_t *b_source[B_LOADS];
+  const uint16_t *w_expert = a.w + static_cast<int64_t>(expert) * a.n * a.k;
+#pragma unroll
+  for (int j = 0; j < B_LOADS; ++j) {
+    const int64_t n = n0 + load_row + j * ROW_STEP;
+    b_source[j] = n < a.n ? w_expert + n * a.k : nullptr;
+  }
+
+  u32x4 a_stage[A_LOADS];
+  u32x4 b_stage[B_LOADS];
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+  auto load = [&](int64_t kt) {
+    const int64_t column = kt * BK + chunk * 8;
+    const bool inside = column < a.k;
+#pragma unroll
+    for (int j = 0; j < A_LOADS; ++j) {
+      a_stage[j] = a_source[j] != nullptr && inside ? load16(a_source[j] + column) : zero;
+    }
+#pragma unroll
+    for (int j = 0; j < B_LOADS; ++j) {
+      b_stage[j] = b_source[j] != nullptr && inside ? load16(b_source[j] + column) : zero;
+    }
+  };
+  auto store = [&](int stage) {
+#pragma unroll
+    for (int j = 0; j < A_LOADS; ++j) {
+      const int r = load_row + j * ROW_STEP;
+      store16(&lds[stage][r * BK + ((chunk ^ moe_swizzle(r)) << 3)], a_stage[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < B_LOADS; ++j) {
+      const int r = BM + load_row + j * ROW_STEP;
+      store16(&lds[stage][r * BK + ((chunk ^ moe_swizzle(r)) << 3)], b_stage[j]);
+    }
+  };
+
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave % WAVES_M;
+  const int wn = wave / WAVES_M;
+  const int frag_row = lane & 31;
+  const int frag_half = lane >> 5;
+  f32x16 acc[MT][NT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        acc[mt][nt][r] = 0.0f;
+      }
+    }
+  }
+
+  const int64_t ktiles = (a.k + BK - 1) / BK;
+  load(0);
+  store(0);
+  __syncthreads();
+  for (int64_t kt = 0; kt < ktiles; ++kt) {
+    const bool more = kt + 1 < ktiles;
+    if (more) {
+      load(kt + 1);
+    }
+    const int stage = static_cast<int>(kt & 1);
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      const int logical = ks * 2 + frag_half;
+      bf16x8 af[MT];
+      bf16x8 bf[NT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int r = wm * WTM + mt * 32 + frag_row;
+        af[mt] = as_bf16x8(load16(&lds[stage][r * BK + ((logical ^ moe_swizzle(r)) << 3)]));
+      }
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const int r = BM + wn * WTN + nt * 32 + frag_row;
+        bf[nt] = as_bf16x8(load16(&lds[stage][r * BK + ((logical ^ moe_swizzle(r)) << 3)]));
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mt], bf[nt], acc[mt][nt], 0, 0, 0);
+        }
+      }
+    }
+    if (more) {
+      store(stage ^ 1);
+    }
+    __syncthreads();
+  }
+
+  // Lane holds D[8 (r / 4) + 4 (lane / 32) + r % 4][lane % 32] of each 32x32 tile.
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int64_t column = n0 + wn * WTN + nt * 32 + frag_row;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = wm * WTM + mt * 32 + 8 * (r >> 2) + 4 * frag_half + (r & 3);
+        const float value = acc[mt][nt][r];
+        if constexpr (GATED) {
+          // Interleaved i_proj: column 2j is gate_j, 2j + 1 is up_j, held by lanes l, l ^ 1.
+          const float partner = __shfl_xor(value, 1, kWave);
+          if ((frag_row & 1) == 0 && m < live && column < a.n) {
+            const float activated = gated_silu(value, partner, a.act);
+            a.out[static_cast<int64_t>(row0 + m) * (a.n / 2) + column / 2] =
+                static_cast<uint16_t>(float_to_bf16(activated));
+          }
+        } else {
+          if (m < live && column < a.n) {
+            const int32_t route = a.sorted_route[row0 + m];
+            a.out[static_cast<int64_t>(route) * a.n + column] =
+                static_cast<uint16_t>(float_to_bf16(value * a.gammas[route]));
+          }
+        }
+      }
+    }
+  }
+}
+
+// out[row] = bf16(scale * sum over the row's live routes, in slot order, of float(route
+// output)) -- the route reduction with the routed scaling factor (moe.py:336-343); rows
+// whose slots are all -1 read 0.
+__global__ __launch_bounds__(256) void moe_combine_kernel(MoeCombineArgs a) {
+  const int64_t chunks = a.hidden / 8;
+  const int64_t index = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (index >= a.rows * chunks) {
+    return;
+  }
+  const int64_t row = index / chunks;
+  const int64_t chunk = index % chunks;
+  float sum[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+  for (int slot = 0; slot < a.topk; ++slot) {
+    const int64_t route = row * a.topk + slot;
+    const int32_t expert = a.ids[route];
+    if (expert < 0 || expert >= a.experts) {
+      continue;
+    }
+    const u32x4 values = load16(a.routes + route * a.hidden + chunk * 8);
+#pragma unroll
+    for (int word = 0; word < 4; ++word) {
+      sum[2 * word] += bf16_to_float(values[word] & 0xffffu);
+      sum[2 * word + 1] += bf16_to_float(values[word] >> 16);
+    }
+  }
+  u32x4 packed;
+#pragma unroll
+  for (int word = 0; word < 4; ++word) {
+    packed[word] = pack_bf16x2(sum[2 * word] * a.scale, sum[2 * word + 1] * a.scale);
+  }
+  store16(a.out + row * a.hidden + chunk * 8, packed);
+}
+
+template <class Args>
+KernelLaunch launch_of(const void *kernel, dim3 grid, unsigned threads, const Args &args) {
+  KernelLaunch launch;
+  launch.func = kernel;
+  launch.grid = grid;
+  launch.block = dim3(threads, 1, 1);
+  launch.set_args(args);
+  return launch;
+}
+
+unsigned blocks_for(int64_t items, int64_t per_block) {
+  return static_cast<unsigned>((items + per_block - 1) / per_block);
+}
+
+}  // namespace
+
+int moe_tile_rows(MoeTile tile) { return tile == MoeTile::Small ? 32 : 128; }
+
+// Few routes per expert (decode) take 32-row tiles over 64 weight rows, which spread each
+// expert's weight stream over more workgroups; otherwise 128 x 128 tiles.
+MoeTile choose_moe_tile(int64_t routes, int64_t experts) {
+  return routes <= 16 * experts ? MoeTile::Small : MoeTile::Large;
+}
+
+KernelLaunch make_router_topk(const RouterTopkArgs &args) {
+  return launch_of(reinterpret_cast<const void *>(&router_topk_kernel), dim3(blocks_for(args.rows, 4)), 256, args);
+}
+
+KernelLaunch make_router_logits(const RouterLogitsArgs &args) {
+  return launch_of(reinterpret_cast<const void *>(&router_logits_kernel),
+                   dim3(blocks_for(args.experts, 64), blocks_for(args.rows, 16)), 256, args);
+}
+
+KernelLaunch make_finalize_routing(const FinalizeRoutingArgs &args) {
+  return launch_of(reinterpret_cast<const void *>(&finalize_routing_kernel),
+                   dim3(blocks_for(args.capacity * args.effective_topk, 256)), 256, args);
+}
+
+KernelLaunch make_moe_sort(const MoeSortArgs &args) {
+  return launch_of(reinterpret_cast<const void *>(&moe_sort_kernel), dim3(1), 1024, args);
+}
+
+KernelLaunch make_moe_gemm(const MoeGemmArgs &args, MoeTile tile, bool gated, int max_tiles) {
+  if (tile == MoeTile::Small) {
+    const void *kernel = gated ? reinterpret_cast<const void *>(&moe_gemm_kernel<32, 64, 1, 2, true>)
+                               : reinterpret_cast<const void *>(&moe_gemm_kernel<32, 64, 1, 2, false>);
+    return launch_of(kernel, dim3(blocks_for(args.n, 64), static_cast<unsigned>(max_tiles)), 128, args);
+  }
+  const void *kernel = gated ? reinterpret_cast<const void *>(&moe_gemm_kernel<128, 128, 2, 2, true>)
+                             : reinterpret_cast<const void *>(&moe_gemm_kernel<128, 128, 2, 2, false>);
+  return launch_of(kernel, dim3(blocks_for(args.n, 128), static_cast<unsigned>(max_tiles)), 256, args);
+}
+
+KernelLaunch make_moe_combine(const MoeCombineArgs &args) {
+  return launch_of(reinterpret_cast<const void *>(&moe_combine_kernel),
+                   dim3(blocks_for(args.rows * (args.hidden / 8), 256)), 256, args);
+}
+
+}  // namespace xp

@@ -296,6 +296,67 @@ struct xp_transport {
 
 namespace {
 
+// Workspace of one Experts call: expert ends, sorted routes, the tile table (sized for the
+// smaller tile, an upper bound for both), the activated routes [routes, intermediate] and
+// the route outputs [routes, hidden], each 256-byte aligned.
+struct MoeWorkspace {
+  size_t expert_end;
+  size_t sorted_route;
+  size_t tile_expert;
+  size_t tile_row0;
+  size_t activated;
+  size_t route_out;
+  size_t bytes;
+  int max_tiles;
+};
+
+MoeWorkspace moe_workspace(int64_t rows, int64_t hidden, int64_t intermediate, int64_t experts, int64_t topk) {
+  MoeWorkspace layout{};
+  const int64_t routes = rows * topk;
+  const int64_t small_rows = moe_tile_rows(MoeTile::Small);
+  layout.max_tiles = static_cast<int>((routes + small_rows - 1) / small_rows + experts);
+  size_t cursor = 0;
+  auto region = [&](size_t bytes) {
+    const size_t offset = cursor;
+    cursor = align_up(cursor + bytes, 256);
+    return offset;
+  };
+  layout.expert_end = region(static_cast<size_t>(experts) * 4);
+  layout.sorted_route = region(static_cast<size_t>(routes) * 4);
+  layout.tile_expert = region(static_cast<size_t>(layout.max_tiles) * 4);
+  layout.tile_row0 = region(static_cast<size_t>(layout.max_tiles) * 4);
+  layout.activated = region(static_cast<size_t>(routes * intermediate) * 2);
+  layout.route_out = region(static_cast<size_t>(routes * hidden) * 2);
+  layout.bytes = cursor;
+  return layout;
+}
+
+// Router workspace: the logits [rows, experts] (bf16 for the PAYLOAD precision, fp32
+// otherwise), then the PAYLOAD projection's K-slice scratch.
+struct RouterWorkspace {
+  size_t logits;
+  size_t scratch;
+  size_t scratch_bytes;
+  size_t bytes;
+};
+
+// PAYLOAD logits go through the MFMA projection kernels when their geometry allows it.
+bool router_uses_mfma(int64_t hidden, int64_t experts, int precision) {
+  return precision == XP_ROUTER_PRECISION_PAYLOAD && hidden % 8 == 0 && experts % 8 == 0;
+}
+
+RouterWorkspace router_workspace(int64_t rows, int64_t hidden, int64_t experts, int precision) {
+  RouterWorkspace layout{};
+  const bool payload = precision == XP_ROUTER_PRECISION_PAYLOAD;
+  layout.logits = 0;
+  layout.scratch = align_up(static_cast<size_t>(rows * experts) * (payload ? 2 : 4), 256);
+  layout.scratch_bytes = router_uses_mfma(hidden, experts, precision)
+                             ? gemm_scratch_bytes(choose_gemm(rows, experts, hidden, false), rows, experts, hidden)
+                             : 0;
+  layout.bytes = layout.scratch + layout.scratch_bytes;
+  return layout;
+}
+
 TransportArgs transport_args(xp_transport_t transport, int arena) {
   TransportArgs args{};
   args.arenas = transport->arenas;
@@ -1063,6 +1124,237 @@ int xp_transport_probe(xp_transport_t transport, int arena, int scenario, uint32
   if (status != hipSuccess) {
     return fail(XP_ERROR_HIP, std::string("transport probe failed: ") + hipGetErrorString(status));
   }
+  return XP_OK;
+}
+
+
+// ------------------------------------------------------------------ MoE
+
+size_t xp_moe_router_workspace_bytes(int64_t rows, int64_t hidden, int64_t experts, int precision) {
+  if (rows <= 0 || hidden <= 0 || experts <= 0) {
+    return 0;
+  }
+  return router_workspace(rows, hidden, experts, precision).bytes;
+}
+
+int xp_moe_router_topk(const void *logits, int logits_f32, int64_t rows, int64_t experts, int64_t topk, int algorithm,
+                       const float *correction_bias, int renormalize, int weight_rounding, int32_t *ids,
+                       float *weights, xp_stream_t stream) {
+  XP_REQUIRE(rows >= 0, "row count must be non-negative");
+  XP_REQUIRE(experts >= 1 && experts <= kMoeMaxExperts, "the router supports 1 to 1024 experts");
+  XP_REQUIRE(topk >= 1 && topk <= experts && topk <= 64, "topk must be between 1 and min(experts, 64)");
+  XP_REQUIRE(algorithm == XP_ROUTER_SOFTMAX || algorithm == XP_ROUTER_SIGMOID, "router algorithm is unknown");
+  XP_REQUIRE(weight_rounding == XP_TOPK_ROUNDING_NONE || weight_rounding == XP_TOPK_ROUNDING_LOGITS_DTYPE,
+             "TopK weight rounding is unknown");
+  if (rows == 0) {
+    return XP_OK;
+  }
+  XP_REQUIRE(logits != nullptr && ids != nullptr && weights != nullptr, "router pointers must be non-null");
+  RouterTopkArgs args{};
+  args.logits = logits;
+  args.correction_bias = correction_bias;
+  args.ids = ids;
+  args.weights = weights;
+  args.rows = rows;
+  args.experts = static_cast<int32_t>(experts);
+  args.topk = static_cast<int32_t>(topk);
+  args.logits_f32 = logits_f32 != 0 ? 1 : 0;
+  args.softmax = algorithm == XP_ROUTER_SOFTMAX ? 1 : 0;
+  args.renormalize = renormalize != 0 ? 1 : 0;
+  args.round_to_logits = weight_rounding == XP_TOPK_ROUNDING_LOGITS_DTYPE ? 1 : 0;
+  XP_HIP_CHECK(launch(make_router_topk(args), static_cast<hipStream_t>(stream)));
+  return XP_OK;
+}
+
+int xp_moe_router(const void *hidden_states, int64_t rows, int64_t hidden, const void *router_weights,
+                  int64_t experts, int64_t topk, int algorithm, int precision, const float *correction_bias,
+                  int renormalize, int weight_rounding, int32_t *ids, float *weights, void *workspace,
+                  size_t workspace_bytes, xp_stream_t stream) {
+  XP_REQUIRE(rows >= 0, "row count must be non-negative");
+  XP_REQUIRE(hidden > 0, "hidden size must be positive");
+  XP_REQUIRE(precision == XP_ROUTER_PRECISION_PAYLOAD || precision == XP_ROUTER_PRECISION_FP32 ||
+                 precision == XP_ROUTER_PRECISION_FP32_LOGITS,
+             "router projection precision is unknown");
+  XP_REQUIRE(experts >= 1 && experts <= kMoeMaxExperts, "the router supports 1 to 1024 experts");
+  XP_REQUIRE(topk >= 1 && topk <= experts && topk <= 64, "topk must be between 1 and min(experts, 64)");
+  if (rows == 0) {
+    return XP_OK;
+  }
+  XP_REQUIRE(hidden_states != nullptr && router_weights != nullptr, "router inputs must be non-null");
+  const bool mfma = router_uses_mfma(hidden, experts, precision);
+  XP_REQUIRE(!mfma || (aligned16(hidden_states) && aligned16(router_weights)),
+             "router inputs must be 16-byte aligned");
+  const RouterWorkspace layout = router_workspace(rows, hidden, experts, precision);
+  XP_REQUIRE(workspace != nullptr && workspace_bytes >= layout.bytes && aligned16(workspace),
+             "router workspace is missing or smaller than xp_moe_router_workspace_bytes");
+  uint8_t *base = static_cast<uint8_t *>(workspace);
+  const hipStream_t hip_stream = static_cast<hipStream_t>(stream);
+  void *logits = base + layout.logits;
+  if (mfma) {
+    // logits = bf16(x . w^T): the Dense projection kernels, no epilogue.
+    const GemmChoice choice = choose_gemm(rows, experts, hidden, false);
+    GemmArgs args{};
+    args.x = static_cast<const uint16_t *>(hidden_states);
+    args.w = static_cast<const uint16_t *>(router_weights);
+    args.out = static_cast<uint16_t *>(logits);
+    args.partials = layout.scratch_bytes > 0 ? reinterpret_cast<float *>(base + layout.scratch) : nullptr;
+    args.ldx = hidden;
+    args.ldo = experts;
+    args.rows = rows;
+    args.capacity = rows;
+    args.out_rows = rows;
+    args.n = experts;
+    args.k = hidden;
+    args.act = default_activation();
+    const GemmLaunch gemm = make_gemm(args, rows, false, choice);
+    XP_HIP_CHECK(launch(gemm.main, hip_stream));
+    XP_HIP_CHECK(launch(gemm.reduce, hip_stream));
+  } else {
+    RouterLogitsArgs args{};
+    args.x = static_cast<const uint16_t *>(hidden_states);
+    args.w = router_weights;
+    args.logits = logits;
+    args.rows = rows;
+    args.hidden = hidden;
+    args.experts = static_cast<int32_t>(experts);
+    args.weights_f32 = precision == XP_ROUTER_PRECISION_FP32 ? 1 : 0;
+    args.out_bf16 = precision == XP_ROUTER_PRECISION_PAYLOAD ? 1 : 0;
+    XP_HIP_CHECK(launch(make_router_logits(args), hip_stream));
+  }
+  return xp_moe_router_topk(logits, precision == XP_ROUTER_PRECISION_PAYLOAD ? 0 : 1, rows, experts, topk, algorithm,
+                            correction_bias, renormalize, weight_rounding, ids, weights, stream);
+}
+
+int xp_moe_finalize_routing(const int32_t *routed_ids, const float *routed_weights, int64_t capacity,
+                            int64_t routed_topk, int32_t *final_ids, float *final_weights, int64_t effective_topk,
+                            const int64_t *payload_rows, int64_t routed_expert_count, float routed_scaling_factor,
+                            xp_stream_t stream) {
+  XP_REQUIRE(capacity >= 0 && routed_topk >= 1 && effective_topk >= routed_topk, "routing geometry is inconsistent");
+  XP_REQUIRE(routed_expert_count >= routed_topk, "Routing Metadata Expert counts are inconsistent");
+  XP_REQUIRE(routed_scaling_factor > 0.0f && routed_scaling_factor < __builtin_inff(),
+             "routed scaling factor must be finite and positive");
+  if (capacity == 0) {
+    return XP_OK;
+  }
+  XP_REQUIRE(routed_ids != nullptr && routed_weights != nullptr && final_ids != nullptr && final_weights != nullptr &&
+                 payload_rows != nullptr,
+             "routing pointers must be non-null");
+  FinalizeRoutingArgs args{};
+  args.routed_ids = routed_ids;
+  args.routed_weights = routed_weights;
+  args.final_ids = final_ids;
+  args.final_weights = final_weights;
+  args.payload_rows = payload_rows;
+  args.capacity = capacity;
+  args.routed_topk = static_cast<int32_t>(routed_topk);
+  args.effective_topk = static_cast<int32_t>(effective_topk);
+  args.routed_experts = static_cast<int32_t>(routed_expert_count);
+  args.shared_weight = 1.0f / routed_scaling_factor;
+  XP_HIP_CHECK(launch(make_finalize_routing(args), static_cast<hipStream_t>(stream)));
+  return XP_OK;
+}
+
+size_t xp_moe_workspace_bytes(int64_t rows, int64_t hidden, int64_t intermediate, int64_t experts, int64_t topk) {
+  if (rows <= 0 || hidden <= 0 || intermediate <= 0 || experts <= 0 || topk <= 0) {
+    return 0;
+  }
+  return moe_workspace(rows, hidden, intermediate, experts, topk).bytes;
+}
+
+int xp_moe_workspace_layout(int64_t rows, int64_t hidden, int64_t intermediate, int64_t experts, int64_t topk,
+                            size_t *offsets) {
+  XP_REQUIRE(rows > 0 && hidden > 0 && intermediate > 0 && experts > 0 && topk > 0, "geometry must be positive");
+  XP_REQUIRE(offsets != nullptr, "output pointer must be non-null");
+  const MoeWorkspace layout = moe_workspace(rows, hidden, intermediate, experts, topk);
+  offsets[0] = layout.expert_end;
+  offsets[1] = layout.sorted_route;
+  offsets[2] = layout.tile_expert;
+  offsets[3] = layout.tile_row0;
+  offsets[4] = layout.activated;
+  offsets[5] = layout.route_out;
+  return XP_OK;
+}
+
+int xp_moe_experts(const void *hidden_states, int64_t rows, int64_t hidden, int64_t intermediate, int64_t experts,
+                   int64_t topk, const void *w_gate_up, const void *w_down, const int32_t *topk_ids,
+                   const float *topk_weights, float routed_scaling_factor, float alpha, float limit, float up_offset,
+                   void *output, void *workspace, size_t workspace_bytes, xp_stream_t stream) {
+  XP_REQUIRE(rows >= 0, "row count must be non-negative");
+  XP_REQUIRE(hidden > 0 && hidden % 8 == 0 && intermediate > 0 && intermediate % 8 == 0,
+             "hidden and intermediate sizes must be positive multiples of 8");
+  XP_REQUIRE(experts >= 1 && experts <= kMoeMaxExperts, "Experts support 1 to 1024 experts");
+  XP_REQUIRE(topk >= 1 && topk <= experts, "topk must be between 1 and the expert count");
+  XP_REQUIRE(rows * topk <= (int64_t{1} << 30), "too many routes for one call");
+  XP_REQUIRE(alpha > 0.0f, "SiLU alpha must be positive");
+  if (rows == 0) {
+    return XP_OK;
+  }
+  XP_REQUIRE(hidden_states != nullptr && w_gate_up != nullptr && w_down != nullptr && topk_ids != nullptr &&
+                 topk_weights != nullptr && output != nullptr,
+             "Experts pointers must be non-null");
+  XP_REQUIRE(aligned16(hidden_states) && aligned16(w_gate_up) && aligned16(w_down) && aligned16(output),
+             "Experts tensors must be 16-byte aligned");
+  const MoeWorkspace layout = moe_workspace(rows, hidden, intermediate, experts, topk);
+  XP_REQUIRE(workspace != nullptr && workspace_bytes >= layout.bytes && aligned16(workspace),
+             "Experts workspace is missing or smaller than xp_moe_workspace_bytes");
+  uint8_t *base = static_cast<uint8_t *>(workspace);
+  int32_t *expert_end = reinterpret_cast<int32_t *>(base + layout.expert_end);
+  int32_t *sorted_route = reinterpret_cast<int32_t *>(base + layout.sorted_route);
+  int32_t *tile_expert = reinterpret_cast<int32_t *>(base + layout.tile_expert);
+  int32_t *tile_row0 = reinterpret_cast<int32_t *>(base + layout.tile_row0);
+  uint16_t *activated = reinterpret_cast<uint16_t *>(base + layout.activated);
+  uint16_t *route_out = reinterpret_cast<uint16_t *>(base + layout.route_out);
+  const int64_t routes = rows * topk;
+  const MoeTile tile = choose_moe_tile(routes, experts);
+  const int tile_rows = moe_tile_rows(tile);
+  const int max_tiles = static_cast<int>((routes + tile_rows - 1) / tile_rows + experts);
+  const hipStream_t hip_stream = static_cast<hipStream_t>(stream);
+
+  MoeSortArgs sort{};
+  sort.ids = topk_ids;
+  sort.expert_end = expert_end;
+  sort.sorted_route = sorted_route;
+  sort.tile_expert = tile_expert;
+  sort.tile_row0 = tile_row0;
+  sort.routes = routes;
+  sort.experts = static_cast<int32_t>(experts);
+  sort.tile_rows = tile_rows;
+  sort.max_tiles = max_tiles;
+  XP_HIP_CHECK(launch(make_moe_sort(sort), hip_stream));
+
+  MoeGemmArgs gate_up{};
+  gate_up.x = static_cast<const uint16_t *>(hidden_states);
+  gate_up.w = static_cast<const uint16_t *>(w_gate_up);
+  gate_up.out = activated;
+  gate_up.tile_expert = tile_expert;
+  gate_up.tile_row0 = tile_row0;
+  gate_up.expert_end = expert_end;
+  gate_up.sorted_route = sorted_route;
+  gate_up.n = 2 * intermediate;
+  gate_up.k = hidden;
+  gate_up.topk = topk;
+  gate_up.act = GatedSilu{alpha, limit, up_offset};
+  XP_HIP_CHECK(launch(make_moe_gemm(gate_up, tile, true, max_tiles), hip_stream));
+
+  MoeGemmArgs down = gate_up;
+  down.x = activated;
+  down.w = static_cast<const uint16_t *>(w_down);
+  down.out = route_out;
+  down.gammas = topk_weights;
+  down.n = hidden;
+  down.k = intermediate;
+  XP_HIP_CHECK(launch(make_moe_gemm(down, tile, false, max_tiles), hip_stream));
+
+  MoeCombineArgs combine{};
+  combine.routes = route_out;
+  combine.ids = topk_ids;
+  combine.out = static_cast<uint16_t *>(output);
+  combine.rows = rows;
+  combine.hidden = hidden;
+  combine.topk = static_cast<int32_t>(topk);
+  combine.experts = static_cast<int32_t>(experts);
+  combine.scale = routed_scaling_factor;
+  XP_HIP_CHECK(launch(make_moe_combine(combine), hip_stream));
   return XP_OK;
 }
 

@@ -70,6 +70,20 @@ __device__ __forceinline__ u32x4 load16_stream(const void *address) {
 
 __device__ __forceinline__ void store16(void *address, u32x4 value) { *reinterpret_cast<u32x4 *>(address) = value; }
 
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 value) { return __builtin_bit_cast(bf16x8, value); }
+
+// Raw buffer resource over `bytes` bytes: loads past the end return zero without a memory
+// access, which masks token rows beyond the live rows and weight rows beyond N without
+// branches.  Word 3 is the gfx9 raw-buffer format.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0), static_cast<int>(bytes),
+                                           0x00020000);
+}
+
+__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, uint32_t offset) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, static_cast<int>(offset), 0, 0));
+}
+
 __device__ __forceinline__ float wave_sum(float value) {
 #pragma unroll
   for (int offset = 32; offset > 0; offset >>= 1) {

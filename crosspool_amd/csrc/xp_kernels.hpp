@@ -155,6 +155,104 @@ KernelLaunch make_transport_settle(const TransportArgs &args);
 KernelLaunch make_transport_drain(const TransportArgs &args);
 KernelLaunch make_transport_publish_failure(const TransportArgs &args);
 KernelLaunch make_transport_probe(const TransportArgs &args);
+// ---------------------------------------------------------------- MoE
+constexpr int kMoeMaxExperts = 1024;
+
+// Router TopK over [rows, experts] logits (bf16 or fp32), one wavefront per row.
+struct RouterTopkArgs {
+  const void *logits;
+  const float *correction_bias;  // [experts] selection-only bias, or null
+  int32_t *ids;                  // [rows, topk]
+  float *weights;                // [rows, topk]
+  int64_t rows;
+  int32_t experts;
+  int32_t topk;
+  int32_t logits_f32;
+  int32_t softmax;  // 1: softmax scores, ties to the lower id; 0: sigmoid, ties to the higher id
+  int32_t renormalize;
+  int32_t round_to_logits;
+};
+
+// Router logits[rows, experts] = x[rows, hidden] . w[experts, hidden] (w bf16 or fp32) as
+// fp32 sums, stored as fp32 or rounded to bf16.
+struct RouterLogitsArgs {
+  const uint16_t *x;
+  const void *w;
+  void *logits;
+  int64_t rows;
+  int64_t hidden;
+  int32_t experts;
+  int32_t weights_f32;
+  int32_t out_bf16;
+};
+
+struct FinalizeRoutingArgs {
+  const int32_t *routed_ids;     // [capacity, routed_topk]
+  const float *routed_weights;
+  int32_t *final_ids;            // [capacity, effective_topk]
+  float *final_weights;
+  const int64_t *payload_rows;   // one device value: live rows
+  int64_t capacity;
+  int32_t routed_topk;
+  int32_t effective_topk;
+  int32_t routed_experts;
+  float shared_weight;           // 1 / routed_scaling_factor
+};
+
+// Route sort: routes (row * topk + slot) grouped by expert, and the expert tile table of
+// the grouped projections.
+struct MoeSortArgs {
+  const int32_t *ids;        // [routes] expert of each route, -1 = no route
+  int32_t *expert_end;       // [experts] one past the expert's last sorted position
+  int32_t *sorted_route;     // [routes] route at each sorted position
+  int32_t *tile_expert;      // [max_tiles] expert of each tile, -1 past the last tile
+  int32_t *tile_row0;        // [max_tiles] first sorted position of each tile
+  int64_t routes;
+  int32_t experts;
+  int32_t tile_rows;         // BM of the grouped projections
+  int32_t max_tiles;
+};
+
+// Grouped projection over the sorted routes of one expert tile: gate_up gathers token rows
+// (row = route / topk of x) and writes bf16(act) at the sorted positions; down reads the
+// sorted activated rows and writes bf16(acc * gamma[route]) to the route's row.
+struct MoeGemmArgs {
+  const uint16_t *x;
+  const uint16_t *w;          // [experts, n, k]
+  uint16_t *out;
+  const int32_t *tile_expert;
+  const int32_t *tile_row0;
+  const int32_t *expert_end;
+  const int32_t *sorted_route;
+  const float *gammas;        // down: [routes] route weights
+  int64_t n;
+  int64_t k;
+  int64_t topk;
+  GatedSilu act;
+};
+
+struct MoeCombineArgs {
+  const uint16_t *routes;    // [rows * topk, hidden] route outputs
+  const int32_t *ids;        // [rows, topk]
+  uint16_t *out;             // [rows, hidden]
+  int64_t rows;
+  int64_t hidden;
+  int32_t topk;
+  int32_t experts;
+  float scale;               // routed scaling factor
+};
+
+enum class MoeTile : int { Small = 0, Large = 1 };  // 32 x 64 / 128 x 128 expert tiles
+int moe_tile_rows(MoeTile tile);
+MoeTile choose_moe_tile(int64_t routes, int64_t experts);
+
+KernelLaunch make_router_topk(const RouterTopkArgs &args);
+KernelLaunch make_router_logits(const RouterLogitsArgs &args);
+KernelLaunch make_finalize_routing(const FinalizeRoutingArgs &args);
+KernelLaunch make_moe_sort(const MoeSortArgs &args);
+KernelLaunch make_moe_gemm(const MoeGemmArgs &args, MoeTile tile, bool gated, int max_tiles);
+KernelLaunch make_moe_combine(const MoeCombineArgs &args);
+
 // `capacity` sizes the grid (graph templates keep one grid per capacity);
 // workgroups beyond the live rows exit immediately.
 KernelLaunch make_gather(const GatherArgs &args, int64_t capacity);

@@ -49,6 +49,32 @@ class LayerKind(IntEnum):
     MOE = 2
 
 
+class RouterAlgorithm(IntEnum):
+    """Activated scoring rule of a MoE Router (src/xpool/ffn.py:78-82)."""
+
+    SOFTMAX = 1
+    SIGMOID = 2
+
+
+class RouterProjectionPrecision(IntEnum):
+    """Router projection input / weight / logits dtypes (src/xpool/ffn.py:85-102).
+
+    PAYLOAD: bf16 weights and bf16 logits; FP32: fp32 weights over the widened input, fp32
+    logits; FP32_LOGITS: bf16 weights, fp32 logits.
+    """
+
+    PAYLOAD = 1
+    FP32 = 2
+    FP32_LOGITS = 3
+
+
+class TopKWeightRounding(IntEnum):
+    """Extra rounding of routed mixing weights to the logits dtype (src/xpool/ffn.py:105-115)."""
+
+    NONE = 1
+    LOGITS_DTYPE = 2
+
+
 class ActivationKind(IntEnum):
     """FFN activation semantics (src/xpool/ffn.py:43-48)."""
 

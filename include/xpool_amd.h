@@ -302,6 +302,74 @@ int xp_transport_snapshot(xp_transport_t transport, int arena, xp_arena_snapshot
  * producer and consumer kernels of tests/suites/cext/transport/shutdown_test.cu:173-191. */
 int xp_transport_probe(xp_transport_t transport, int arena, int scenario, uint32_t *observed, int max_words);
 
+/* ------------------------------------------------------------------ MoE */
+
+/* Router vocabulary, values of src/xpool/ffn.py:78-115 (RouterAlgorithm,
+ * RouterProjectionPrecision, TopKWeightRounding). */
+enum { XP_ROUTER_SOFTMAX = 1, XP_ROUTER_SIGMOID = 2 };
+enum { XP_ROUTER_PRECISION_PAYLOAD = 1, XP_ROUTER_PRECISION_FP32 = 2, XP_ROUTER_PRECISION_FP32_LOGITS = 3 };
+enum { XP_TOPK_ROUNDING_NONE = 1, XP_TOPK_ROUNDING_LOGITS_DTYPE = 2 };
+
+/* TopK over logits [rows, experts] (bf16, or fp32 when logits_f32): scores are softmax or
+ * sigmoid in fp32; selection = score (+ correction_bias[e], fp32, may be NULL; sigmoid over
+ * bf16 logits rounds the selection to bf16); ties go to the lower id for softmax and the
+ * higher id for sigmoid; the weight of a pick is its score (softmax without correction: the
+ * selected maximum); renormalize divides by the sum of picked weights when positive;
+ * LOGITS_DTYPE rounding then rounds weights through bf16 for bf16 logits.  Writes ids
+ * [rows, topk] int32 and weights [rows, topk] fp32.  experts <= 1024, topk <= 64.
+ * Replaces router_topk_kernel (src/xpool/runtime/ffnagent/operators/routing.py:21-89). */
+int xp_moe_router_topk(const void *logits, int logits_f32, int64_t rows, int64_t experts, int64_t topk, int algorithm,
+                       const float *correction_bias, int renormalize, int weight_rounding, int32_t *ids,
+                       float *weights, xp_stream_t stream);
+
+/* Workspace bytes of xp_moe_router (the logits and the projection's K-slice scratch). */
+size_t xp_moe_router_workspace_bytes(int64_t rows, int64_t hidden, int64_t experts, int precision);
+
+/* Router: logits = hidden_states [rows, hidden] bf16 . router_weights^T, where the weights
+ * are [experts, hidden] bf16 (PAYLOAD: bf16 logits, through the MFMA projection kernels
+ * when hidden and experts are multiples of 8; FP32_LOGITS: fp32 logits) or fp32 (FP32: fp32
+ * logits of the widened input), then xp_moe_router_topk.  Replaces Router.run_into
+ * (routing.py:148-190). */
+int xp_moe_router(const void *hidden_states, int64_t rows, int64_t hidden, const void *router_weights,
+                  int64_t experts, int64_t topk, int algorithm, int precision, const float *correction_bias,
+                  int renormalize, int weight_rounding, int32_t *ids, float *weights, void *workspace,
+                  size_t workspace_bytes, xp_stream_t stream);
+
+/* Final Routing Metadata [capacity, effective_topk]: routed slots copy the Router's ids and
+ * weights, shared slots s name expert routed_expert_count + s with weight
+ * 1 / routed_scaling_factor, rows at or past *payload_rows (a device int64) read -1 / 0.
+ * Replaces finalize_moe_routing (routing.py:193-307). */
+int xp_moe_finalize_routing(const int32_t *routed_ids, const float *routed_weights, int64_t capacity,
+                            int64_t routed_topk, int32_t *final_ids, float *final_weights, int64_t effective_topk,
+                            const int64_t *payload_rows, int64_t routed_expert_count, float routed_scaling_factor,
+                            xp_stream_t stream);
+
+/* Workspace bytes of xp_moe_experts for rows x topk routes. */
+size_t xp_moe_workspace_bytes(int64_t rows, int64_t hidden, int64_t intermediate, int64_t experts, int64_t topk);
+
+/* Byte offsets of the Experts workspace regions, for inspection after a call (the workspace
+ * keeps them until the next call): [0] expert ends (int32 [experts], one past each expert's
+ * last sorted position), [1] sorted routes (int32 [rows * topk], route = row * topk + slot
+ * at each sorted position), [2] tile experts and [3] tile first positions (int32), [4] the
+ * activated routes (bf16 [rows * topk, intermediate], sorted order), [5] the route outputs
+ * (bf16 [rows * topk, hidden], by route).  No counterpart in the reference, whose test
+ * harness reads its workspace views directly (moe.py:181-215). */
+int xp_moe_workspace_layout(int64_t rows, int64_t hidden, int64_t intermediate, int64_t experts, int64_t topk,
+                            size_t *offsets);
+
+/* Experts: for every route (row, slot) with 0 <= e = topk_ids[row, slot] < experts,
+ * h = bf16(act(bf16(x[row] . w_gate_up[e][2j]), bf16(x[row] . w_gate_up[e][2j+1]))) and
+ * r = bf16((h . w_down[e][n]) * topk_weights[row, slot]); then
+ * output[row] = bf16(routed_scaling_factor * sum over slots in order of float(r)), 0 for
+ * rows without routes.  w_gate_up is [experts, 2*intermediate, hidden] (Gate/Up
+ * INTERLEAVED), w_down [experts, hidden, intermediate], all bf16; act as in
+ * xp_gemm_gate_up_silu.  Replaces Experts.run_into
+ * (src/xpool/runtime/ffnagent/operators/moe.py:168-343). */
+int xp_moe_experts(const void *hidden_states, int64_t rows, int64_t hidden, int64_t intermediate, int64_t experts,
+                   int64_t topk, const void *w_gate_up, const void *w_down, const int32_t *topk_ids,
+                   const float *topk_weights, float routed_scaling_factor, float alpha, float limit, float up_offset,
+                   void *output, void *workspace, size_t workspace_bytes, xp_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,233 @@
+"""torch-CPU restatement of the reference MoE Router, routing finalisation and Experts.
+
+TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).  Paths are relative to the CrossPool
+checkout:
+
+* ``router_topk`` follows router_topk_kernel, src/xpool/runtime/ffnagent/operators/
+  routing.py:21-89: fp32 softmax (ties to the lower id) or sigmoid (ties to the higher id),
+  selection-only correction bias, a sigmoid selection over bf16 logits stored through the
+  bf16 logits buffer, the selected score as weight, renormalisation by the positive sum,
+  optional rounding of the weights to the logits dtype.  A per-slot loop, not torch.topk,
+  so the tie policy is explicit.
+* ``router_logits`` follows Router.run_into (routing.py:148-190): PAYLOAD rounds the
+  projection to bf16, FP32 / FP32_LOGITS keep fp32 logits (fp64 sums rounded once).
+* ``finalize_routing`` follows finalize_moe_routing_kernel (routing.py:193-227).
+* ``experts_reference`` is the reference's own expected-value formula for Experts,
+  tests/suites/integration/runtime/ffnagent/test_operators.py:255-281, with fp64 instead of
+  fp32 matrix-vector products: projection rounded to bf16, activation in fp32 rounded to
+  bf16, down projection times the route weight rounded to bf16, fp32 sum over the row's
+  slots in order, times the routed scaling factor, rounded to bf16.
+* ``experts_fp32`` is the same without any intermediate rounding (the pure-fp32 side of the
+  parity bar).
+
+Pinned in tests/test_moe_oracle.py by the known answers of the reference's routing tests
+(routing/test_softmax_payload.py, test_softmax_fp32.py, test_sigmoid.py tie-policy case,
+test_metadata.py), by torch.softmax / torch.topk / torch.sigmoid on tie-free inputs, by a
+second, literal fp32 transcription of the reference's Experts formula on its own 4-expert
+test case (which must stay within ``rounding_slack``), by the reduction to the Dense oracle
+(one expert, one route, weight and scale 1: bit-identical), and by planted mistakes.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from oracle import ffn_oracle as o
+
+
+def router_logits(x: torch.Tensor, w: torch.Tensor, *, payload: bool) -> torch.Tensor:
+    """fp32 logits as the Router projection produces them (bf16-rounded for PAYLOAD)."""
+
+    exact = x.double() @ w.double().t()
+    return exact.to(torch.bfloat16).float() if payload else exact.float()
+
+
+def router_topk(
+    logits: torch.Tensor,
+    *,
+    topk: int,
+    softmax: bool,
+    correction_bias: torch.Tensor | None = None,
+    renormalize: bool = True,
+    round_weights: bool = False,
+    logits_bf16: bool = False,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """ids [rows, topk] int32 and weights [rows, topk] fp32 of router_topk_kernel."""
+
+    logits = logits.float()
+    rows, experts = logits.shape
+    if softmax:
+        shifted = logits - logits.max(dim=1, keepdim=True).values
+        exponentials = torch.exp(shifted)
+        scores = exponentials / exponentials.sum(dim=1, keepdim=True)
+    else:
+        scores = torch.sigmoid(logits)
+    selection = scores.clone()
+    if correction_bias is not None:
+        selection = selection + correction_bias.float()
+    if not softmax and logits_bf16:
+        selection = selection.to(torch.bfloat16).float()
+    ids = torch.empty((rows, topk), dtype=torch.int32)
+    weights = torch.empty((rows, topk), dtype=torch.float32)
+    for row in range(rows):
+        remaining = selection[row].clone()
+        normalizer = torch.zeros((), dtype=torch.float32)
+        for slot in range(topk):
+            maximum = remaining.max()
+            tied = torch.nonzero(remaining == maximum).flatten()
+            expert = int(tied.min()) if softmax else int(tied.max())
+            weight = maximum if softmax and correction_bias is None else scores[row, expert]
+            ids[row, slot] = expert
+            weights[row, slot] = weight
+            normalizer = normalizer + weight
+            remaining[expert] = float("-inf")
+        if renormalize:
+            weights[row] = weights[row] / (normalizer if normalizer > 0 else torch.ones(()))
+        if round_weights and logits_bf16:
+            weights[row] = weights[row].to(torch.bfloat16).float()
+    return ids, weights
+
+
+def finalize_routing(
+    routed_ids: torch.Tensor,
+    routed_weights: torch.Tensor,
+    *,
+    payload_rows: int,
+    routed_expert_count: int,
+    shared_expert_count: int,
+    routed_scaling_factor: float,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Final Routing Metadata [capacity, routed_topk + shared] (routing.py:193-227)."""
+
+    capacity, routed_topk = routed_ids.shape
+    effective = routed_topk + shared_expert_count
+    ids = torch.full((capacity, effective), -1, dtype=torch.int32)
+    weights = torch.zeros((capacity, effective), dtype=torch.float32)
+    live = min(payload_rows, capacity)
+    ids[:live, :routed_topk] = routed_ids[:live]
+    weights[:live, :routed_topk] = routed_weights[:live].float()
+    for shared in range(shared_expert_count):
+        ids[:live, routed_topk + shared] = routed_expert_count + shared
+        weights[:live, routed_topk + shared] = torch.tensor(1.0 / routed_scaling_factor, dtype=torch.float32)
+    return ids, weights
+
+
+def _routes_by_expert(topk_ids: torch.Tensor, experts: int):
+    rows, slots = topk_ids.shape
+    for expert in range(experts):
+        where = torch.nonzero(topk_ids == expert)
+        if where.numel():
+            yield expert, where[:, 0], where[:, 1]
+
+
+def experts_routes(
+    x: torch.Tensor,
+    w_gate_up: torch.Tensor,
+    w_down: torch.Tensor,
+    topk_ids: torch.Tensor,
+    topk_weights: torch.Tensor,
+    *,
+    alpha: float = 1.0,
+    limit: float | None = None,
+    up_offset: float = 0.0,
+) -> torch.Tensor:
+    """Route outputs [rows, slots, hidden] (bf16 values held in fp32; 0 where no route).
+
+    Projection rounded to bf16, activation in fp32 rounded to bf16, down projection times
+    the route weight in fp32 rounded to bf16 (test_operators.py:266-278).
+    """
+
+    rows, hidden = x.shape
+    experts = w_gate_up.shape[0]
+    routes = torch.zeros((rows, topk_ids.shape[1], hidden), dtype=torch.float32)
+    for expert, row_index, slot_index in _routes_by_expert(topk_ids, experts):
+        projected = (x[row_index].double() @ w_gate_up[expert].double().t()).to(torch.bfloat16)
+        activated = o.gated_silu(
+            projected[:, 0::2], projected[:, 1::2], alpha=alpha, limit=limit, up_offset=up_offset
+        )
+        route = activated.double() @ w_down[expert].double().t()
+        gamma = topk_weights[row_index, slot_index].double().unsqueeze(1)
+        routes[row_index, slot_index] = (route.float() * gamma.float()).to(torch.bfloat16).float()
+    return routes
+
+
+def experts_reference(
+    x: torch.Tensor,
+    w_gate_up: torch.Tensor,
+    w_down: torch.Tensor,
+    topk_ids: torch.Tensor,
+    topk_weights: torch.Tensor,
+    *,
+    routed_scaling_factor: float = 1.0,
+    alpha: float = 1.0,
+    limit: float | None = None,
+    up_offset: float = 0.0,
+) -> torch.Tensor:
+    """Expected Experts output with the reference's rounding points (bf16 [rows, hidden])."""
+
+    routes = experts_routes(x, w_gate_up, w_down, topk_ids, topk_weights, alpha=alpha, limit=limit,
+                            up_offset=up_offset)
+    total = torch.zeros(routes.shape[::2], dtype=torch.float32)
+    for slot in range(topk_ids.shape[1]):
+        total = total + routes[:, slot]
+    return (total * routed_scaling_factor).to(torch.bfloat16)
+
+
+def rounding_slack(routes: torch.Tensor, expected: torch.Tensor, routed_scaling_factor: float = 1.0) -> torch.Tensor:
+    """Per-element gap two correct implementations may show at the reference's rounding points.
+
+    Each route output is rounded to bf16 before the sum, so an implementation whose fp32
+    accumulation differs may land one bf16 ulp away on every route; the scaled sum is then
+    rounded once more: scale * sum_k ulp(r_k) + ulp(y).
+    """
+
+    route_ulps = o.bf16_ulp(routes.abs()) * (routes != 0)
+    return routed_scaling_factor * route_ulps.sum(dim=1) + o.bf16_ulp(expected.float().abs())
+
+
+def experts_fp32(
+    x: torch.Tensor,
+    w_gate_up: torch.Tensor,
+    w_down: torch.Tensor,
+    topk_ids: torch.Tensor,
+    topk_weights: torch.Tensor,
+    *,
+    routed_scaling_factor: float = 1.0,
+    alpha: float = 1.0,
+    limit: float | None = None,
+    up_offset: float = 0.0,
+) -> torch.Tensor:
+    """The same Experts output in fp32 with no intermediate rounding."""
+
+    rows, hidden = x.shape
+    experts = w_gate_up.shape[0]
+    total = torch.zeros((rows, hidden), dtype=torch.float64)
+    for expert, row_index, slot_index in _routes_by_expert(topk_ids, experts):
+        projected = x[row_index].double() @ w_gate_up[expert].double().t()
+        gate, up = projected[:, 0::2], projected[:, 1::2]
+        if limit is not None:
+            gate = torch.clamp(gate, max=limit)
+            up = torch.clamp(up, -limit, limit)
+        activated = gate * torch.sigmoid(alpha * gate) * (up + up_offset)
+        route = activated @ w_down[expert].double().t()
+        total.index_add_(0, row_index, route * topk_weights[row_index, slot_index].double().unsqueeze(1))
+    return (total * routed_scaling_factor).float()
+
+
+def generate_moe_layer(hidden: int, intermediate: int, experts: int, seed: int, std: float = 0.02):
+    """Seeded bf16 Expert weights: i_proj [E, 2I, H] (interleaved), o_proj [E, H, I]."""
+
+    generator = torch.Generator().manual_seed(seed)
+    w_gate_up = (torch.randn((experts, 2 * intermediate, hidden), generator=generator) * std).to(torch.bfloat16)
+    w_down = (torch.randn((experts, hidden, intermediate), generator=generator) * std).to(torch.bfloat16)
+    return w_gate_up, w_down
+
+
+def generate_routes(rows: int, experts: int, topk: int, seed: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Seeded distinct expert ids per row and positive weights summing to one."""
+
+    generator = torch.Generator().manual_seed(seed)
+    scores = torch.rand((rows, experts), generator=generator)
+    ids = torch.argsort(scores, dim=1, descending=True)[:, :topk].to(torch.int32)
+    weights = torch.rand((rows, topk), generator=generator) + 0.05
+    return ids, (weights / weights.sum(dim=1, keepdim=True)).float()

@@ -51,6 +51,35 @@ def assert_ffn_parity(actual: torch.Tensor, stage_reference: torch.Tensor, fp32_
     torch.testing.assert_close(actual, stage_reference, rtol=0.02, atol=0.1)
 
 
+def assert_moe_parity(actual: torch.Tensor, stage_reference: torch.Tensor, fp32_reference: torch.Tensor,
+                      slack: torch.Tensor) -> None:
+    """The MoE Experts end-to-end bar.
+
+    Every route output is rounded to bf16 before the row sum (test_operators.py:278), so an
+    element may differ from the oracle by one bf16 ulp per route (scaled) plus one for the
+    final rounding: ``slack`` is that bound per element (moe_oracle.rounding_slack).  A
+    legitimate one-ulp flip of an activation (fp32 accumulation order, the epilogue's exp)
+    moves every column of its route a little further, so up to 0.1 % of elements may exceed
+    the slack; the stages themselves are checked rigorously by assert_moe_stages.  On top:
+    rel-L2 <= 5e-3 against the pure-fp32 oracle (north star), the reference harness's
+    nRMSE / max-scaled gates and its operator tolerance (rtol 0.02, atol 0.1).
+    """
+
+    actual = actual.detach().cpu()
+    assert torch.isfinite(actual.float()).all(), "Experts output holds non-finite values"
+    pure = o.compare(fp32_reference, actual.float())
+    assert pure.rel_l2 <= NORTH_STAR_REL_L2, f"rel-L2 vs fp32 oracle {pure.rel_l2:.3e}"
+    gap = (actual.float() - stage_reference.float()).abs()
+    over = int((gap > slack).sum().item())
+    assert over <= MAX_FRACTION_OVER_ABS * gap.numel(), (
+        f"{over} elements beyond their rounding-point slack (max gap {gap.max().item():.3e})"
+    )
+    stage = o.compare(stage_reference, actual)
+    assert stage.normalized_rmse <= o.FFN_OUTPUT_NORMALIZED_RMSE_LIMIT
+    assert stage.maximum_scaled_error <= o.FFN_OUTPUT_MAXIMUM_SCALED_ERROR_LIMIT
+    torch.testing.assert_close(actual, stage_reference, rtol=0.02, atol=0.1)
+
+
 def assert_within_ulps(actual: torch.Tensor, expected: torch.Tensor, ulps: float = 1.0, exact_fraction: float = 0.99):
     """Elementwise |a - e| <= ulps * ulp(e) and at least ``exact_fraction`` bit-identical."""
 
@@ -155,6 +184,60 @@ def assert_activated_within_bounds(
     nominal = stage_activated(x, w_gate_up, **act)
     exact = float((a.view(torch.int16) == nominal.view(torch.int16)).float().mean())
     assert exact >= exact_fraction, f"only {exact:.4f} of activations are bit-identical to the oracle"
+
+
+def assert_moe_stages(intermediates: dict, x, w_gate_up, w_down, ids, weights, output, scale: float = 1.0,
+                      **act) -> None:
+    """Each Experts stage against the oracle, fed with the GPU's own previous stage.
+
+    * the sort: every live route appears once, grouped by expert, ``expert_end`` consistent;
+    * activations within their fp32-accumulation intervals (assert_activated_within_bounds);
+    * route outputs ``bf16(fp32(h . w_down[e]) * gamma)`` within the interval of the GPU's
+      activations (widened by the fp32 product's rounding);
+    * the combine ``bf16(scale * sum over slots in order of float(route))`` bit for bit.
+    """
+
+    rows, topk = ids.shape
+    experts = w_gate_up.shape[0]
+    flat_ids = ids.flatten()
+    live = int(((flat_ids >= 0) & (flat_ids < experts)).sum())
+    sorted_route = intermediates["sorted_route"].cpu().long()[:live]
+    activated = intermediates["activated"].cpu()[:live]
+    route_out = intermediates["route_out"].cpu()
+    expert_end = intermediates["expert_end"].cpu().long()
+    assert torch.equal(sorted_route.sort().values, torch.nonzero(flat_ids >= 0).flatten())
+    experts_of = flat_ids[sorted_route]
+    assert bool((experts_of[1:] >= experts_of[:-1]).all()), "routes are not grouped by expert"
+    assert torch.equal(expert_end, torch.bincount(experts_of, minlength=experts).cumsum(0))
+    by_route = torch.zeros((rows * topk, activated.shape[1]), dtype=torch.bfloat16)
+    by_route[sorted_route] = activated
+    gammas = weights.flatten().double()
+    identical = 0
+    for expert in range(experts):
+        q = torch.nonzero(flat_ids == expert).flatten()
+        if q.numel() == 0:
+            continue
+        assert_activated_within_bounds(by_route[q], x[q // topk], w_gate_up[expert], exact_fraction=0.0, **act)
+        nominal = stage_activated(x[q // topk], w_gate_up[expert], **act)
+        identical += int((by_route[q].view(torch.int16) == nominal.view(torch.int16)).sum())
+        h = by_route[q].double()
+        w = w_down[expert].double()
+        exact = h @ w.t()
+        delta = (h.abs() @ w.abs().t()) * ACCUMULATION_BOUND
+        gamma = gammas[q].unsqueeze(1)
+        low, high = (exact - delta) * gamma, (exact + delta) * gamma
+        low = low - low.abs() * 2.0**-23
+        high = high + high.abs() * 2.0**-23
+        got = route_out[q].double()
+        outside = int(((got < bf16_floor(low).double()) | (got > bf16_ceil(high).double())).sum())
+        assert outside == 0, f"expert {expert}: {outside} route outputs outside their interval"
+    assert identical >= 0.99 * live * activated.shape[1], "fewer than 99 % of activations match the oracle's bits"
+    total = torch.zeros((rows, route_out.shape[1]), dtype=torch.float32)
+    for slot in range(topk):
+        valid = ((ids[:, slot] >= 0) & (ids[:, slot] < experts)).unsqueeze(1)
+        routes = route_out[torch.arange(rows) * topk + slot].float()
+        total = total + torch.where(valid, routes, torch.zeros_like(routes))
+    assert_bitwise_equal(output, (total * torch.tensor(scale, dtype=torch.float32)).to(torch.bfloat16))
 
 
 def stage_activated(x: torch.Tensor, w_gate_up: torch.Tensor, **act) -> torch.Tensor:

@@ -1,0 +1,238 @@
+"""GPU parity of the MoE Router, routing finalisation and Experts against oracle/moe_oracle.py.
+
+Router cases are the reference's own routing tests (routing/test_softmax_payload.py,
+test_softmax_fp32.py, test_sigmoid.py, test_metadata.py): ids must match exactly and
+weights within rtol 1e-5 / atol 1e-6, the reference's tolerance.  On random Qwen3-MoE-shaped
+inputs the projection's bf16 logits must lie in their fp32-accumulation intervals and the
+TopK over those logits must match the oracle's TopK on the same logits.  Experts outputs meet
+the MoE bar of tests/parity.py against the reference's expected-value formula
+(test_operators.py:255-281) and its pure-fp32 counterpart, every stage (sort, activations,
+route outputs, combine) is checked rigorously on the GPU's own intermediates, and outputs
+repeat bit for bit.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from crosspool_amd.ffn import GateTransform, RouterAlgorithm, RouterProjectionPrecision, SiluActivation
+from crosspool_amd.ffn import TopKWeightRounding
+from crosspool_amd.moe import Experts, MoeFfnWeights, MoeRouterWeights, Router, finalize_moe_routing, router_topk
+from oracle import ffn_oracle as o
+from oracle import moe_oracle as m
+from parity import assert_bitwise_equal, assert_moe_parity, assert_moe_stages, assert_projection_within_bounds
+from parity import to_device
+
+pytestmark = pytest.mark.gpu
+
+TWO_ROWS = ((3.0, 1.0, -1.0, -3.0), (-2.0, 0.0, 2.0, 4.0))
+
+
+def _router(device, hidden_states, projection, **kwargs):
+    rows, hidden = hidden_states.shape
+    router = Router(row_capacity=rows, hidden_size=hidden, routed_expert_count=projection.shape[0], device=device,
+                    **kwargs)
+    return router
+
+
+@pytest.mark.parametrize("rounding", tuple(TopKWeightRounding))
+def test_softmax_payload_router(device, rounding):
+    hidden = torch.tensor(TWO_ROWS, dtype=torch.bfloat16)
+    projection = torch.eye(4, dtype=torch.bfloat16)
+    router = _router(device, hidden, projection, routed_topk=2, algorithm=RouterAlgorithm.SOFTMAX,
+                     precision=RouterProjectionPrecision.PAYLOAD, renormalize=True, weight_rounding=rounding)
+    router.run_into(hidden_states=to_device(hidden, device), router_weights=MoeRouterWeights(to_device(projection, device)))
+    ids, weights = m.router_topk(m.router_logits(hidden, projection, payload=True), topk=2, softmax=True,
+                                 round_weights=rounding is TopKWeightRounding.LOGITS_DTYPE, logits_bf16=True)
+    assert torch.equal(router.ids.cpu(), ids) and ids.tolist() == [[0, 1], [3, 2]]
+    torch.testing.assert_close(router.weights.cpu(), weights, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("corrected", (False, True))
+def test_softmax_fp32_logits_router_with_correction(device, corrected):
+    hidden = torch.tensor(TWO_ROWS, dtype=torch.bfloat16)
+    projection = torch.eye(4, dtype=torch.bfloat16)
+    bias = torch.tensor((-0.75, -0.25, 0.5, 0.8)) if corrected else None
+    router = _router(device, hidden, projection, routed_topk=2, algorithm=RouterAlgorithm.SOFTMAX,
+                     precision=RouterProjectionPrecision.FP32_LOGITS, renormalize=False)
+    weights_gpu = MoeRouterWeights(to_device(projection, device), None if bias is None else to_device(bias, device))
+    router.run_into(hidden_states=to_device(hidden, device), router_weights=weights_gpu)
+    ids, weights = m.router_topk(m.router_logits(hidden, projection, payload=False), topk=2, softmax=True,
+                                 correction_bias=bias, renormalize=False)
+    assert torch.equal(router.ids.cpu(), ids)
+    torch.testing.assert_close(router.weights.cpu(), weights, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("experts,topk,scale", ((64, 4, 4096.0), (48, 3, None), (17, 1, 1.0), (17, 17, 1.0)))
+def test_sigmoid_fp32_router_diagonal(device, experts, topk, scale):
+    hidden = (torch.arange(2 * experts, dtype=torch.float32).view(2, experts) / (2 * experts)).to(torch.bfloat16)
+    bias = torch.linspace(-0.25, 0.25, experts) * scale if scale is not None else None
+    projection = torch.diag(torch.linspace(0.101, 1.909, experts))
+    router = _router(device, hidden, projection, routed_topk=topk, algorithm=RouterAlgorithm.SIGMOID,
+                     precision=RouterProjectionPrecision.FP32, renormalize=True)
+    weights_gpu = MoeRouterWeights(to_device(projection, device), None if bias is None else to_device(bias, device))
+    router.run_into(hidden_states=to_device(hidden, device), router_weights=weights_gpu)
+    ids, weights = m.router_topk(m.router_logits(hidden, projection, payload=False), topk=topk, softmax=False,
+                                 correction_bias=bias, renormalize=True)
+    assert torch.equal(router.ids.cpu(), ids)
+    torch.testing.assert_close(router.weights.cpu(), weights, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("algorithm", (RouterAlgorithm.SOFTMAX, RouterAlgorithm.SIGMOID))
+def test_router_tie_policy(device, algorithm):
+    # routing/test_sigmoid.py:76-117
+    hidden = torch.tensor(((0.0,) * 17, (-1000.0,) * 17), dtype=torch.bfloat16)
+    softmax = algorithm is RouterAlgorithm.SOFTMAX
+    precision = RouterProjectionPrecision.PAYLOAD if softmax else RouterProjectionPrecision.FP32
+    projection = torch.eye(17, dtype=torch.bfloat16 if softmax else torch.float32)
+    router = _router(device, hidden, projection, routed_topk=3, algorithm=algorithm, precision=precision,
+                     renormalize=True)
+    router.run_into(hidden_states=to_device(hidden, device), router_weights=MoeRouterWeights(to_device(projection, device)))
+    expected_ids = (0, 1, 2) if softmax else (16, 15, 14)
+    second = (1 / 3, 1 / 3, 1 / 3) if softmax else (0.0, 0.0, 0.0)
+    assert router.ids.cpu().tolist() == [list(expected_ids)] * 2
+    torch.testing.assert_close(router.weights.cpu(), torch.tensor(((1 / 3, 1 / 3, 1 / 3), second)), rtol=1e-5,
+                               atol=1e-6)
+
+
+@pytest.mark.parametrize("rows", (1, 16, 200))
+def test_qwen3_moe_router_projection_and_topk(device, rows):
+    # Qwen3-30B-A3B router: 128 experts over hidden 2048, top-8, softmax, renormalised.
+    hidden, experts = 2048, 128
+    x = o.generate_hidden_states(rows, hidden, 70 + rows)
+    generator = torch.Generator().manual_seed(71)
+    projection = (torch.randn((experts, hidden), generator=generator) * 0.02).to(torch.bfloat16)
+    router = Router(row_capacity=rows, hidden_size=hidden, routed_expert_count=experts, routed_topk=8, device=device)
+    router.run_into(hidden_states=to_device(x, device), router_weights=MoeRouterWeights(to_device(projection, device)))
+    logits = router.logits.cpu()
+    assert_projection_within_bounds(logits, x, projection)
+    ids, weights = m.router_topk(logits.float(), topk=8, softmax=True, logits_bf16=True)
+    assert torch.equal(router.ids.cpu(), ids)
+    torch.testing.assert_close(router.weights.cpu(), weights, rtol=1e-5, atol=1e-6)
+    # TopK alone over the same logits.
+    ids_only, weights_only = router_topk(router.logits, topk=8, algorithm=RouterAlgorithm.SOFTMAX)
+    assert torch.equal(ids_only.cpu(), ids)
+    torch.testing.assert_close(weights_only.cpu(), weights, rtol=1e-5, atol=1e-6)
+
+
+def test_finalize_routing_dynamic_live_rows(device):
+    # routing/test_metadata.py:8-80
+    routed_ids = torch.tensor(((0, 2), (1, 3), (2, 0), (3, 1)), dtype=torch.int32, device=device)
+    routed_weights = torch.tensor(((0.75, 0.25), (0.6, 0.4), (0.9, 0.1), (0.55, 0.45)), device=device)
+    final_ids = torch.empty((4, 3), dtype=torch.int32, device=device)
+    final_weights = torch.empty((4, 3), dtype=torch.float32, device=device)
+    payload_rows = torch.tensor((2,), dtype=torch.int64, device=device)
+    kwargs = dict(routed_expert_count=4, shared_expert_count=1, routed_scaling_factor=2.0)
+    for live in (2, 3):
+        payload_rows.fill_(live)
+        finalize_moe_routing(routed_ids=routed_ids, routed_weights=routed_weights, final_ids=final_ids,
+                             final_weights=final_weights, payload_rows=payload_rows, **kwargs)
+        ids, weights = m.finalize_routing(routed_ids.cpu(), routed_weights.cpu(), payload_rows=live, **kwargs)
+        assert torch.equal(final_ids.cpu(), ids)
+        torch.testing.assert_close(final_weights.cpu(), weights, rtol=0, atol=0)
+    assert final_ids.cpu()[:2].tolist() == [[0, 2, 4], [1, 3, 4]]
+
+
+def _run_experts(device, x, w_gate_up, w_down, ids, weights, scale=1.0, activation=None, gate=None):
+    rows, hidden = x.shape
+    experts, two_i, _ = w_gate_up.shape
+    operator = Experts(row_capacity=rows, hidden_size=hidden, local_intermediate_size=two_i // 2,
+                       expert_count=experts, effective_topk=ids.shape[1], routed_scaling_factor=scale,
+                       activation=activation, gate=gate, device=device)
+    weights_gpu = MoeFfnWeights(to_device(w_gate_up, device), to_device(w_down, device))
+    output = torch.empty((rows, hidden), dtype=torch.bfloat16, device=device)
+    operator.run_into(hidden_states=to_device(x, device), weights=weights_gpu, topk_ids=to_device(ids, device),
+                      topk_weights=to_device(weights, device), output=output)
+    return output.cpu(), operator, weights_gpu
+
+
+def _check_experts(got, x, w_gate_up, w_down, ids, weights, scale=1.0, **act):
+    routes = m.experts_routes(x, w_gate_up, w_down, ids, weights, **act)
+    stage = m.experts_reference(x, w_gate_up, w_down, ids, weights, routed_scaling_factor=scale, **act)
+    pure = m.experts_fp32(x, w_gate_up, w_down, ids, weights, routed_scaling_factor=scale, **act)
+    assert_moe_parity(got, stage, pure, m.rounding_slack(routes, stage, scale))
+
+
+@pytest.mark.parametrize("act", ({}, {"alpha": 1.702, "limit": 7.0, "up_offset": 1.0}))
+def test_experts_reference_operator_case(device, act):
+    # test_operators.py:121-281: four experts, two slots, a dead row, scale 1.5.
+    generator = torch.Generator().manual_seed(31)
+    x = (torch.randn((4, 16), generator=generator) / 4).to(torch.bfloat16)
+    w_gate_up = (torch.randn((4, 16, 16), generator=generator) / 4).to(torch.bfloat16)
+    w_down = (torch.randn((4, 16, 8), generator=generator) / 4).to(torch.bfloat16)
+    ids = torch.tensor(((0, 1), (2, 3), (1, 3), (-1, -1)), dtype=torch.int32)
+    weights = torch.tensor(((0.75, 0.25), (0.6, 0.4), (0.9, 0.1), (0.0, 0.0)))
+    activation = SiluActivation(act.get("alpha", 1.0))
+    gate = GateTransform(limit=act.get("limit"), up_offset=act.get("up_offset", 0.0))
+    got, operator, _ = _run_experts(device, x, w_gate_up, w_down, ids, weights, 1.5, activation, gate)
+    assert_moe_stages(operator.intermediates(), x, w_gate_up, w_down, ids, weights, got, 1.5, **act)
+    stage = m.experts_reference(x, w_gate_up, w_down, ids, weights, routed_scaling_factor=1.5, **act)
+    routes = m.experts_routes(x, w_gate_up, w_down, ids, weights, **act)
+    torch.testing.assert_close(got, stage, rtol=0.02, atol=0.1)
+    gap = (got.float() - stage.float()).abs()
+    assert (gap <= m.rounding_slack(routes, stage, 1.5)).all()
+    assert o.compare(stage, got).normalized_rmse <= 0.01
+    assert got[3].abs().sum() == 0
+
+
+@pytest.mark.parametrize("rows", (1, 7, 48))
+def test_experts_qwen3_moe_shape(device, rows):
+    # Qwen3-30B-A3B expert layer: hidden 2048, moe_intermediate 768, 128 experts, top-8.
+    hidden, intermediate, experts, topk = 2048, 768, 128, 8
+    w_gate_up, w_down = m.generate_moe_layer(hidden, intermediate, experts, 90)
+    x = o.generate_hidden_states(rows, hidden, 91 + rows)
+    ids, weights = m.generate_routes(rows, experts, topk, 92 + rows)
+    got, operator, weights_gpu = _run_experts(device, x, w_gate_up, w_down, ids, weights)
+    _check_experts(got, x, w_gate_up, w_down, ids, weights)
+    assert_moe_stages(operator.intermediates(), x, w_gate_up, w_down, ids, weights, got)
+    again = torch.empty((rows, hidden), dtype=torch.bfloat16, device=device)
+    operator.run_into(hidden_states=to_device(x, device), weights=weights_gpu, topk_ids=to_device(ids, device),
+                      topk_weights=to_device(weights, device), output=again)
+    assert_bitwise_equal(again.cpu(), got)
+
+
+@pytest.mark.parametrize("rows", (96, 1024))
+def test_experts_large_tiles_with_dead_rows(device, rows):
+    # 128-row expert tiles (routes > 16 per expert on average), several tiles per expert,
+    # ragged tails, and a band of rows without routes.
+    hidden, intermediate, experts, topk = 256, 128, 8, 2
+    w_gate_up, w_down = m.generate_moe_layer(hidden, intermediate, experts, 93, std=0.1)
+    x = o.generate_hidden_states(rows, hidden, 94)
+    ids, weights = m.generate_routes(rows, experts, topk, 95)
+    ids[rows // 3: rows // 3 + 5] = -1
+    weights[rows // 3: rows // 3 + 5] = 0.0
+    got, operator, _ = _run_experts(device, x, w_gate_up, w_down, ids, weights, scale=2.5)
+    _check_experts(got, x, w_gate_up, w_down, ids, weights, scale=2.5)
+    assert_moe_stages(operator.intermediates(), x, w_gate_up, w_down, ids, weights, got, 2.5)
+    assert got[rows // 3: rows // 3 + 5].abs().sum() == 0
+
+
+def test_moe_layer_router_finalize_experts(device):
+    # The reference's MoE body (registry.py:296-316): Router -> finalize -> Experts, with a
+    # live-row count below the capacity.
+    capacity, live, hidden, intermediate, experts, topk = 64, 40, 512, 256, 16, 4
+    w_gate_up, w_down = m.generate_moe_layer(hidden, intermediate, experts, 96, std=0.05)
+    generator = torch.Generator().manual_seed(97)
+    projection = (torch.randn((experts, hidden), generator=generator) * 0.05).to(torch.bfloat16)
+    x = o.generate_hidden_states(capacity, hidden, 98)
+    x_gpu = to_device(x, device)
+    router = Router(row_capacity=capacity, hidden_size=hidden, routed_expert_count=experts, routed_topk=topk,
+                    device=device)
+    router.run_into(hidden_states=x_gpu, router_weights=MoeRouterWeights(to_device(projection, device)))
+    final_ids = torch.empty((capacity, topk), dtype=torch.int32, device=device)
+    final_weights = torch.empty((capacity, topk), dtype=torch.float32, device=device)
+    finalize_moe_routing(routed_ids=router.ids, routed_weights=router.weights, final_ids=final_ids,
+                         final_weights=final_weights, payload_rows=torch.tensor((live,), device=device),
+                         routed_expert_count=experts, shared_expert_count=0, routed_scaling_factor=1.0)
+    operator = Experts(row_capacity=capacity, hidden_size=hidden, local_intermediate_size=intermediate,
+                       expert_count=experts, effective_topk=topk, device=device)
+    output = torch.empty_like(x_gpu)
+    operator.run_into(hidden_states=x_gpu, weights=MoeFfnWeights(to_device(w_gate_up, device), to_device(w_down, device)),
+                      topk_ids=final_ids, topk_weights=final_weights, output=output)
+    ids, weights = m.router_topk(router.logits.cpu().float(), topk=topk, softmax=True, logits_bf16=True)
+    ids, weights = m.finalize_routing(ids, weights, payload_rows=live, routed_expert_count=experts,
+                                      shared_expert_count=0, routed_scaling_factor=1.0)
+    assert torch.equal(final_ids.cpu(), ids)
+    _check_experts(output.cpu()[:live], x[:live], w_gate_up, w_down, ids[:live], final_weights.cpu()[:live])
+    assert output.cpu()[live:].abs().sum() == 0
