@@ -44,6 +44,9 @@ TP_REDUCE_PARTIALS = 8
 TP_REDUCE_SHAPE = (8192, 5120)
 TP_REDUCE_LAUNCHES = 20
 TRAFFIC_FILE = REPO_ROOT / "profiles" / "traffic.json"
+# Qwen3-30B-A3B MoE layer (hidden, moe_intermediate, experts, top-k) and its token points.
+MOE_SHAPE = (2048, 768, 128, 8)
+MOE_TOKENS = (1, 32, 2048)
 
 
 def parse_args() -> argparse.Namespace:
@@ -257,6 +260,62 @@ def main() -> int:
         }
         del partials, folded
 
+    # ---------------------------------------------------------------- MoE layer
+    # Qwen3-30B-A3B-shaped MoE layer (no BASELINE config names one; reported beside the
+    # Dense path): Router (128 experts, softmax top-8, renormalised) + Experts (hidden 2048,
+    # moe_intermediate 768), timed with HIP events on the current stream.
+    moe = None
+    if not args.no_sweep:
+        from crosspool_amd.moe import Experts, MoeFfnWeights, MoeRouterWeights, Router
+
+        m_hidden, m_inter, m_experts, m_topk = MOE_SHAPE
+        generator = torch.Generator(device=device).manual_seed(18)
+        moe_weights = MoeFfnWeights(
+            (torch.randn((m_experts, 2 * m_inter, m_hidden), device=device, generator=generator) * 0.02).bfloat16(),
+            (torch.randn((m_experts, m_hidden, m_inter), device=device, generator=generator) * 0.02).bfloat16(),
+        )
+        router_weights = MoeRouterWeights(
+            (torch.randn((m_experts, m_hidden), device=device, generator=generator) * 0.02).bfloat16()
+        )
+        moe = {"shape": {"hidden": m_hidden, "moe_intermediate": m_inter, "experts": m_experts, "topk": m_topk},
+               "points": []}
+        for t in MOE_TOKENS:
+            x = torch.randn((t, m_hidden), device=device, generator=generator).bfloat16()
+            router = Router(row_capacity=t, hidden_size=m_hidden, routed_expert_count=m_experts, routed_topk=m_topk,
+                            device=device)
+            experts_op = Experts(row_capacity=t, hidden_size=m_hidden, local_intermediate_size=m_inter,
+                                 expert_count=m_experts, effective_topk=m_topk, device=device)
+            out = torch.empty_like(x)
+
+            def moe_step() -> None:
+                router.run_into(hidden_states=x, router_weights=router_weights)
+                experts_op.run_into(hidden_states=x, weights=moe_weights, topk_ids=router.ids,
+                                    topk_weights=router.weights, output=out)
+
+            for _ in range(3):
+                moe_step()
+            launches = max(10, min(100, 20000 // t))
+            begin = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            begin.record()
+            for _ in range(launches):
+                moe_step()
+            end.record()
+            end.synchronize()
+            moe_seconds = begin.elapsed_time(end) / 1e3 / launches
+            active = int(torch.unique(router.ids).numel())
+            flops = 2.0 * t * m_experts * m_hidden + 6.0 * t * m_topk * m_hidden * m_inter
+            weight_bytes = 2.0 * m_experts * m_hidden + 6.0 * active * m_hidden * m_inter
+            moe["points"].append({
+                "tokens": t, "us": round(moe_seconds * 1e6, 2), "tokens_per_s": round(t / moe_seconds, 1),
+                "active_experts": active,
+                "hbm_frac": round((weight_bytes + 4.0 * t * m_hidden) / moe_seconds / 1e9 / HBM_PEAK_GBS, 4),
+                "mfma_frac": round(flops / moe_seconds / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+            })
+            del router, experts_op, x, out
+        del moe_weights, router_weights
+        agent.check_health()
+
     # ---------------------------------------------------------------- ffn_shim transaction
     # Host-timed ffn_shim calls on resident [T, H] hidden states: through the Transport
     # mailbox on the caller's stream (submit -> Dense step -> settle), through it with the
@@ -356,6 +415,7 @@ def main() -> int:
         "sweep": sweep,
         "tp_reduce": tp_reduce,
         "shim": shim,
+        "moe": moe,
     }
     agent.close()
     print(json.dumps(result), flush=True)
