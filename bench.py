@@ -44,6 +44,9 @@ TP_REDUCE_PARTIALS = 8
 TP_REDUCE_SHAPE = (8192, 5120)
 TP_REDUCE_LAUNCHES = 20
 TRAFFIC_FILE = REPO_ROOT / "profiles" / "traffic.json"
+# Qwen3-0.6B FFN (hidden, intermediate) x 28 layers, and its batch sizes.
+STACK_SHAPE = (1024, 3072, 28)
+STACK_TOKENS = (1, 8, 32, 128, 256)
 # Qwen3-30B-A3B MoE layer (hidden, moe_intermediate, experts, top-k) and its token points.
 MOE_SHAPE = (2048, 768, 128, 8)
 MOE_TOKENS = (1, 32, 2048)
@@ -260,6 +263,73 @@ def main() -> int:
         }
         del partials, folded
 
+    # ---------------------------------------------------------------- config 2 stack
+    # the 28-layer Qwen3-0.6B FFN stack, independent weights per layer,
+    # T rows of a 4096-slot mailbox; one step = all 28 layers replayed in order on the Lane,
+    # timed as one captured hipGraph per step (and, for reference, issued from the host).
+    stack = None
+    if not args.no_sweep:
+        s_hidden, s_inter, s_layers = STACK_SHAPE
+        generator = torch.Generator(device=device).manual_seed(18)
+        stack_agent = FfnAgent(device)
+        for ordinal in range(s_layers):
+            stack_agent.register_layer(
+                instance_index=0, layer_ordinal=ordinal,
+                weights=DenseFfnWeights.from_tensors(
+                    (torch.randn((2 * s_inter, s_hidden), device=device, generator=generator) * 0.02).bfloat16(),
+                    (torch.randn((s_hidden, s_inter), device=device, generator=generator) * 0.02).bfloat16(),
+                ),
+                norm_weight=(1 + 0.1 * torch.randn(s_hidden, device=device, generator=generator)).bfloat16(),
+            )
+        stack_agent.materialize(maximum_row_capacity=max(STACK_TOKENS))
+        stack_lane = stack_agent.lanes[0]
+        stack_pool = torch.randn((4096, s_hidden), device=device, generator=generator).bfloat16()
+        stack_slots = torch.randperm(4096, device=device, generator=generator)[: max(STACK_TOKENS)].int()
+        stack = {"layers": s_layers, "hidden": s_hidden, "intermediate": s_inter, "points": []}
+        for t in STACK_TOKENS:
+            def stack_step() -> None:
+                for ordinal in range(s_layers):
+                    stack_lane.replay(instance_index=0, layer_ordinal=ordinal, pool=stack_pool, slots=stack_slots,
+                                      rows=t, stream=stack_lane.stream)
+
+            for _ in range(3):
+                stack_step()
+            torch.cuda.synchronize()
+            started = time.perf_counter()
+            for _ in range(args.sweep_steps):
+                stack_step()
+            torch.cuda.synchronize()
+            eager_seconds = (time.perf_counter() - started) / args.sweep_steps
+            # The same 28 replays captured into one hipGraph, as a serving step under graph
+            # capture issues them: one launch per stack step instead of ~100 from the host.
+            graph = torch.cuda.CUDAGraph()
+            capture = torch.cuda.Stream()
+            capture.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.graph(graph, stream=capture):
+                for ordinal in range(s_layers):
+                    stack_lane.replay(instance_index=0, layer_ordinal=ordinal, pool=stack_pool, slots=stack_slots,
+                                      rows=t, stream=torch.cuda.current_stream())
+            for _ in range(3):
+                graph.replay()
+            torch.cuda.synchronize()
+            started = time.perf_counter()
+            for _ in range(args.sweep_steps):
+                graph.replay()
+            torch.cuda.synchronize()
+            step_seconds = (time.perf_counter() - started) / args.sweep_steps
+            del graph
+            stack_bytes = s_layers * (6.0 * s_hidden * s_inter + 2 * s_hidden + 4.0 * t * s_hidden + 4.0 * t)
+            stack["points"].append({
+                "tokens": t, "us_per_stack": round(step_seconds * 1e6, 2),
+                "us_per_layer": round(step_seconds * 1e6 / s_layers, 2),
+                "tokens_per_s": round(t / step_seconds, 1),
+                "hbm_frac": round(stack_bytes / step_seconds / 1e9 / HBM_PEAK_GBS, 4),
+                "host_issued_us_per_stack": round(eager_seconds * 1e6, 2),
+            })
+        stack_agent.check_health()
+        stack_agent.close()
+        del stack_pool
+
     # ---------------------------------------------------------------- MoE layer
     # Qwen3-30B-A3B-shaped MoE layer (no BASELINE config names one; reported beside the
     # Dense path): Router (128 experts, softmax top-8, renormalised) + Experts (hidden 2048,
@@ -416,6 +486,7 @@ def main() -> int:
         "tp_reduce": tp_reduce,
         "shim": shim,
         "moe": moe,
+        "config2_stack": stack,
     }
     agent.close()
     print(json.dumps(result), flush=True)

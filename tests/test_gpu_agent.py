@@ -235,6 +235,74 @@ def test_layers_share_templates_and_bind_their_own_weights(device):
     assert error.normalized_rmse <= o.FFN_OUTPUT_NORMALIZED_RMSE_LIMIT
 
 
+@pytest.mark.parametrize("rows", (1, 8))
+def test_config2_qwen3_0_6b_28_layer_stack(device, rows):
+    # 28 independent Qwen3-0.6B FFN layers replayed through the templates of
+    # one capacity set, chained on the same mailbox slots of a 4096-slot pool; every layer's
+    # step is checked against the oracle fed with the GPU's own previous layer output.
+    hidden, intermediate, layers = 1024, 3072, 28
+    pool = o.generate_hidden_states(4096, hidden, 17)
+    slots = o.generate_slots(4096, rows, 19)
+    weights = [o.generate_layer(hidden, intermediate, 200 + layer) for layer in range(layers)]
+    with FfnAgent(device) as agent:
+        for ordinal, (w_gate_up, w_down, norm_weight) in enumerate(weights):
+            agent.register_layer(
+                instance_index=0, layer_ordinal=ordinal, weights=_weights(w_gate_up, w_down, device),
+                norm_weight=to_device(norm_weight, device),
+            )
+        templates = agent.materialize(maximum_row_capacity=256)
+        assert sorted(t.signature.payload_row_capacity for t in templates) == [1, 2, 4, 8, 16, 32, 64, 128, 256]
+        pool_gpu = to_device(pool, device)
+        slot_ids = slots_tensor(slots, device)
+        previous = pool
+        for ordinal, (w_gate_up, w_down, norm_weight) in enumerate(weights):
+            agent.execute(instance_index=0, layer_ordinal=ordinal, pool=pool_gpu, slots=slot_ids)
+            agent.lanes[0].synchronize()
+            current = pool_gpu.cpu()
+            _check_mailbox(current, previous, slots, w_gate_up, w_down, norm_weight)
+            previous = current
+        agent.check_health()
+
+
+def test_layer_stack_captured_in_one_graph_matches_eager(device):
+    # The replays of a layer stack captured into one hipGraph (stream capture of the direct
+    # launches, as a serving step under graph capture would take them) and replayed several
+    # times, with eager work and synchronisation in between: every replay equals the eager
+    # stack bit for bit.
+    hidden, intermediate, layers, rows = 1024, 3072, 6, 8
+    pool = o.generate_hidden_states(512, hidden, 17)
+    slots = slots_tensor(o.generate_slots(512, rows, 19), device)
+    weights = [o.generate_layer(hidden, intermediate, 300 + layer) for layer in range(layers)]
+    with FfnAgent(device) as agent:
+        for ordinal, (w_gate_up, w_down, norm_weight) in enumerate(weights):
+            agent.register_layer(
+                instance_index=0, layer_ordinal=ordinal, weights=_weights(w_gate_up, w_down, device),
+                norm_weight=to_device(norm_weight, device),
+            )
+        agent.materialize(maximum_row_capacity=rows)
+        lane = agent.lanes[0]
+        eager = to_device(pool, device)
+        for ordinal in range(layers):
+            lane.replay(instance_index=0, layer_ordinal=ordinal, pool=eager, slots=slots,
+                        stream=torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        graph_pool = to_device(pool, device)
+        graph = torch.cuda.CUDAGraph()
+        capture = torch.cuda.Stream()
+        capture.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.graph(graph, stream=capture):
+            for ordinal in range(layers):
+                lane.replay(instance_index=0, layer_ordinal=ordinal, pool=graph_pool, slots=slots,
+                            stream=torch.cuda.current_stream())
+        for _ in range(3):
+            graph_pool.copy_(to_device(pool, device))
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert_bitwise_equal(graph_pool.cpu(), eager.cpu())
+        agent.check_health()
+
+
 def test_two_models_on_two_lanes(device):
     # Qwen3-1.7B and Qwen3-4B shaped layers share one GPU; ragged
     # per-step batches in disjoint slot ranges of an 8192-slot pool, one Lane each.
