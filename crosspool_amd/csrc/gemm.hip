@@ -592,14 +592,75 @@ __device__ __forceinline__ void tile_coordinates(int &tn, int &tm) {
   tn = __builtin_amdgcn_readfirstlane(xcd + 8 * (block * block_tiles + rest % tiles));
 }
 
+// Weight tile tn and expert tile tm of a grouped projection's workgroup.  Every weight tile
+// of one expert tile reads the same rows, so they go to one XCD, one after another in its
+// dispatch order: XCD c = L mod 8 takes expert tiles tm = c (mod 8), each with all its
+// weight tiles, and fetches those rows into its L2 once (the grid's y extent is a multiple
+// of 8, which makes the mapping a bijection).
+__device__ __forceinline__ void grouped_tile_coordinates(int &tn, int &tm) {
+  const int nx = static_cast<int>(gridDim.x);
+  const int linear = static_cast<int>(blockIdx.x) + nx * static_cast<int>(blockIdx.y);
+  const int k = linear / 8;  // place in the XCD's dispatch order
+  tm = __builtin_amdgcn_readfirstlane(linear % 8 + 8 * (k / nx));
+  tn = __builtin_amdgcn_readfirstlane(k % nx);
+}
+
 // Epilogue of a tile kernel whose waves each hold an MT x NT grid of 32x32 accumulator
 // tiles (wave tile WTM x WTN at rows m0 + wm WTM, weight rows w0 + wn WTN).  With a K split
 // the fp32 partial tile of this workgroup's range goes to scratch; otherwise the bf16
 // result (gate_up: after the activation) goes out through `lds` (LDS_ELEMENTS bf16 of
 // stage buffers that every wave is done with once this is called).
+// Rows of a wave tile held per lane for the epilogue's row lookups (lane l: rows l, l + 64).
+template <int WTM>
+struct RowMeta {
+  static constexpr int kPerLane = (WTM + 63) / 64;
+  int32_t slot[kPerLane];   // scatter slot of the row, -1 for none
+  float factor[kPerLane];   // row weight (grouped down projection), else 1
+};
+
+// Loads the scatter slots (and row weights) of wave tile rows [m0 + wm WTM, + WTM): one
+// batch of independent loads, issued before the main loop so that they complete under it.
+template <int WTM>
+__device__ __forceinline__ void load_row_meta(const GemmArgs &a, int64_t m0, int64_t row_end, int wm,
+                                              RowMeta<WTM> &meta) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int i = 0; i < RowMeta<WTM>::kPerLane; ++i) {
+    const int64_t token = m0 + wm * WTM + lane + 64 * i;
+    const bool live = lane + 64 * i < WTM && token < row_end;
+    meta.slot[i] = live ? a.scatter_slots[token] : -1;
+    meta.factor[i] = live && a.row_scale != nullptr ? a.row_scale[token] : 1.0f;
+  }
+}
+
+// Row `row`'s slot / weight from the lane that loaded it.  Every lane of the wave must call
+// these together (no divergent branch around them): a shuffle only reads active lanes.
+template <int WTM>
+__device__ __forceinline__ int32_t row_slot(const RowMeta<WTM> &meta, int row) {
+  int32_t value = __shfl(meta.slot[0], row & 63, kWave);
+#pragma unroll
+  for (int i = 1; i < RowMeta<WTM>::kPerLane; ++i) {
+    const int32_t other = __shfl(meta.slot[i], row & 63, kWave);
+    value = row >= 64 * i ? other : value;
+  }
+  return value;
+}
+
+template <int WTM>
+__device__ __forceinline__ float row_factor(const RowMeta<WTM> &meta, int row) {
+  float value = __shfl(meta.factor[0], row & 63, kWave);
+#pragma unroll
+  for (int i = 1; i < RowMeta<WTM>::kPerLane; ++i) {
+    const float other = __shfl(meta.factor[i], row & 63, kWave);
+    value = row >= 64 * i ? other : value;
+  }
+  return value;
+}
+
 template <int MT, int NT, int WTM, int WTN, int WAVES, int LDS_ELEMENTS, bool GATED>
 __device__ __forceinline__ void tile_epilogue(const GemmArgs &a, const f32x16 (&acc)[MT][NT], uint16_t *lds,
-                                              int64_t m0, int64_t w0, int wave, int wm, int wn) {
+                                              int64_t m0, int64_t row_end, int64_t w0, int wave, int wm, int wn,
+                                              const RowMeta<WTM> &meta) {
   const int lane = threadIdx.x & 63;
   const int frag_row = lane & 31;
   const int frag_half = lane >> 5;
@@ -649,6 +710,9 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs &a, const f32x16 (&
   
   static_assert((WTM * CPR) % 64 == 0, "output chunks must split evenly over the lanes");
   static_assert(WTM * OUT_N * WAVES <= LDS_ELEMENTS, "epilogue tiles must fit the stage buffers");
+  // With a scatter the rows' slots (and weights) come from `meta`, loaded at the start of the
+  // kernel, so the epilogue does not wait on a dependent load per row.
+  const bool scatter = a.scatter_slots != nullptr;
   __syncthreads();  // every wave is done reading the stage buffers
   uint16_t *out_tile = lds + wave * (WTM * OUT_N);
   // Chunk c of row r sits at physical chunk c ^ ((r / 4) % CPR): the two row groups one
@@ -659,10 +723,13 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs &a, const f32x16 (&
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int row = mt * 32 + 8 * (r >> 2) + 4 * frag_half + (r & 3);
+      // Row weight (grouped down projection); 1 elsewhere.
+      const float factor = !GATED && a.row_scale != nullptr ? row_factor(meta, row) : 1.0f;
 #pragma unroll
       for (int nt = 0; nt < OUT_N / 32; ++nt) {
         const int col = nt * 32 + frag_row;
-        const float value = GATED ? gated_silu(acc[mt][nt][r], acc[mt][nt + NT / 2][r], a.act) : acc[mt][nt][r];
+        const float value =
+            GATED ? gated_silu(acc[mt][nt][r], acc[mt][nt + NT / 2][r], a.act) : acc[mt][nt][r] * factor;
         out_tile[slot_of(row, col >> 3) + (col & 7)] = static_cast<uint16_t>(float_to_bf16(value));
       }
     }
@@ -677,8 +744,13 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs &a, const f32x16 (&
     const int chunk = index % CPR;
     const int64_t token = row0 + row;
     const int64_t col = col0 + chunk * 8;
-    if (token < a.rows && col < out_cols) {
-      uint16_t *destination = output_row(a, token);
+    const int32_t slot = scatter ? row_slot(meta, row) : -1;  // all lanes, before the branch
+    if (token < row_end && col < out_cols) {
+      uint16_t *destination = a.out + token * a.ldo;
+      if (scatter) {
+        destination = slot >= 0 && static_cast<int64_t>(slot) < a.out_rows ? a.out + static_cast<int64_t>(slot) * a.ldo
+                                                                            : nullptr;
+      }
       if (destination != nullptr) {
         store16(destination + col, load16(out_tile + slot_of(row, chunk)));
       }
@@ -724,9 +796,26 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
 
   int tn;
   int tm;
-  tile_coordinates(tn, tm);
-  const int64_t m0 = static_cast<int64_t>(tm) * BM;
-  if (m0 >= a.rows) {
+  if (a.tile_expert != nullptr) {
+    grouped_tile_coordinates(tn, tm);
+  } else {
+    tile_coordinates(tn, tm);
+  }
+  // Rows [m0, row_end) and the weights of this tile: the live rows of the projection, or
+  // for a grouped projection the rows of one expert tile and that expert's weights.
+  int64_t m0 = static_cast<int64_t>(tm) * BM;
+  int64_t row_end = a.rows;
+  const uint16_t *weights = a.w;
+  if (a.tile_expert != nullptr) {
+    const int expert = __builtin_amdgcn_readfirstlane(a.tile_expert[tm]);
+    if (expert < 0) {
+      return;
+    }
+    m0 = __builtin_amdgcn_readfirstlane(a.tile_row0[tm]);
+    row_end = __builtin_amdgcn_readfirstlane(a.expert_end[expert]);
+    weights = a.w + static_cast<int64_t>(expert) * a.n * a.k;
+  }
+  if (m0 >= row_end) {
     return;
   }
   const int64_t w0 = static_cast<int64_t>(tn) * BN;
@@ -745,12 +834,12 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
   // compile-time fact.  Lane i of a load writes LDS row r0 + i / 8, physical chunk i % 8,
   // which holds logical k chunk (i % 8) ^ swizzle(row): the swizzle is applied by choosing
   // the global chunk.
-  const int64_t a_rows_left = a.rows - m0;
+  const int64_t a_rows_left = row_end - m0;
   const int64_t b_rows_left = a.n - w0;
   const __amdgpu_buffer_rsrc_t a_rsrc =
       make_rsrc(a.x + m0 * a.ldx, static_cast<uint32_t>((a_rows_left < BM ? a_rows_left : BM) * a.ldx * 2));
   const __amdgpu_buffer_rsrc_t b_rsrc =
-      make_rsrc(a.w + w0 * a.k, static_cast<uint32_t>((b_rows_left < BN ? b_rows_left : BN) * a.k * 2));
+      make_rsrc(weights + w0 * a.k, static_cast<uint32_t>((b_rows_left < BN ? b_rows_left : BN) * a.k * 2));
   // Load q of a wave covers the 8-row group starting at LDS row g (a multiple of 8); lane
   // i takes row g + i / 8 and k chunk (i % 8) ^ swizzle(row).  Because g is a multiple of
   // 8, swizzle(g + i / 8) = (i / 16) ^ (4 if g / 8 is odd), so the per-lane part of every
@@ -889,6 +978,12 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
     __builtin_amdgcn_sched_barrier(0);
   };
 
+  // Scatter slots and row weights of this wave's rows, for the epilogue (split-K tiles
+  // write partials and need none).
+  RowMeta<WTM> meta;
+  if (a.scatter_slots != nullptr && a.k_split == 1) {
+    load_row_meta<WTM>(a, m0, row_end, wm, meta);
+  }
   // The chooser never makes an empty K range, so every workgroup runs at least one slab.
   const int64_t ktiles = (k_end - k_begin + BK - 1) / BK;
   // Prologue: slabs 0 .. STAGES-1 in flight, wait for slab 0, read its first fragments.
@@ -975,7 +1070,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
   // Past-the-end refills may still be landing in the stage buffers the epilogue reuses.
   __builtin_amdgcn_s_waitcnt(0);
 
-  tile_epilogue<MT, NT, WTM, WTN, WAVES, STAGES * STAGE, GATED>(a, acc, lds, m0, w0, wave, wm, wn);
+  tile_epilogue<MT, NT, WTM, WTN, WAVES, STAGES * STAGE, GATED>(a, acc, lds, m0, row_end, w0, wave, wm, wn, meta);
 }
 
 // ------------------------------------------------------------------ tables
@@ -1250,6 +1345,32 @@ GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmCho
   }
   kernel.set_args(record);
   return launches;
+}
+
+// Grouped projections run on the 256 x 128 tile.  An expert sees ~T K / E rows (Qwen3-MoE:
+// 128 at 2048 tokens), far below the MFMA ridge, so the projections are bound by streaming
+// each expert's weights: a tile tall enough to hold all of an expert's rows streams them
+// once, where 128-row tiles split about half the experts over two tiles and read their
+// weights twice (Qwen3-30B-A3B at 2048 tokens: down 297 us on 128-row tiles).
+constexpr int kGroupedTileVariant = 1;
+
+int grouped_tile_rows() { return kTileShapes[kGroupedTileVariant].bm; }
+
+KernelLaunch make_grouped_gemm(const GemmArgs &args, bool gated, int max_tiles) {
+  const TileShape &shape = kTileShapes[kGroupedTileVariant];
+  if (max_tiles % 8 != 0) {
+    return KernelLaunch{};  // grouped_tile_coordinates needs a multiple of 8 (callers pad)
+  }
+  GemmArgs record = args;
+  record.k_slice = args.k;
+  record.k_split = 1;
+  record.partials = nullptr;
+  KernelLaunch kernel;
+  kernel.func = gated ? tile_kernel<true>(kGroupedTileVariant) : tile_kernel<false>(kGroupedTileVariant);
+  kernel.grid = dim3(static_cast<unsigned>((args.n + shape.bn - 1) / shape.bn), static_cast<unsigned>(max_tiles), 1);
+  kernel.block = dim3(static_cast<unsigned>(64 * shape.waves), 1, 1);
+  kernel.set_args(record);
+  return kernel;
 }
 
 std::string gemm_name(GemmChoice choice, bool gated) {

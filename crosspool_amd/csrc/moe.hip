@@ -15,10 +15,12 @@
 //
 // The reference sorts routes with a bitmatrix and drives triton_kernels' ragged matmul;
 // here one workgroup counts routes per expert in LDS, scans the counts into sorted offsets
-// and an expert tile table, and places each route; the grouped projections are 32x32x16
-// bf16 MFMA tiles over (expert tile, weight tile) with register-staged loads into a
-// double-buffered, XOR-swizzled LDS slab.  A route's output row depends only on its own
-// token row and expert, so the order of routes within an expert does not change any bit.
+// and an expert tile table, and places each route.  With many routes per expert the
+// projections run on the Dense path's 256 x 128 tile kernel in its grouped mode (token rows
+// first gathered into sorted order); with few (decode) on moe_gemm_kernel below: 32 x 64
+// tiles of 32x32x16 bf16 MFMAs over (expert tile, weight tile) with register-staged loads
+// into a double-buffered, XOR-swizzled LDS slab.  A route's output row depends only on its
+// own token row and expert, so the order of routes within an expert does not change any bit.
 
 #include "xp_kernels.hpp"
 
@@ -337,6 +339,7 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(MoeSortArgs a) {
     if (expert >= 0 && expert < a.experts) {
       const int position = atomicAdd(&counts[expert], 1);
       a.sorted_route[position] = static_cast<int32_t>(route);
+      a.sorted_weight[position] = a.weights[route];
     }
   }
 }
@@ -506,6 +509,19 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void moe_gemm_kernel(MoeGem
   }
 }
 
+// Token rows gathered into sorted route order, 16 bytes per thread.
+__global__ __launch_bounds__(256) void moe_gather_kernel(MoeGatherArgs a) {
+  const int64_t chunks = a.hidden / 8;
+  const int64_t index = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t position = index / chunks;
+  if (position >= a.routes || position >= a.expert_end[a.experts - 1]) {
+    return;
+  }
+  const int64_t chunk = index % chunks;
+  const int64_t token = a.sorted_route[position] / a.topk;
+  store16(a.out + position * a.hidden + chunk * 8, load16(a.x + token * a.hidden + chunk * 8));
+}
+
 // out[row] = bf16(scale * sum over the row's live routes, in slot order, of float(route
 // output)) -- the route reduction with the routed scaling factor (moe.py:336-343); rows
 // whose slots are all -1 read 0.
@@ -555,10 +571,10 @@ unsigned blocks_for(int64_t items, int64_t per_block) {
 
 }  // namespace
 
-int moe_tile_rows(MoeTile tile) { return tile == MoeTile::Small ? 32 : 128; }
+int moe_tile_rows(MoeTile tile) { return tile == MoeTile::Small ? 32 : grouped_tile_rows(); }
 
 // Few routes per expert (decode) take 32-row tiles over 64 weight rows, which spread each
-// expert's weight stream over more workgroups; otherwise 128 x 128 tiles.
+// expert's weight stream over more workgroups; otherwise the grouped 256 x 128 tiles.
 MoeTile choose_moe_tile(int64_t routes, int64_t experts) {
   return routes <= 16 * experts ? MoeTile::Small : MoeTile::Large;
 }
@@ -590,6 +606,11 @@ KernelLaunch make_moe_gemm(const MoeGemmArgs &args, MoeTile tile, bool gated, in
   const void *kernel = gated ? reinterpret_cast<const void *>(&moe_gemm_kernel<128, 128, 2, 2, true>)
                              : reinterpret_cast<const void *>(&moe_gemm_kernel<128, 128, 2, 2, false>);
   return launch_of(kernel, dim3(blocks_for(args.n, 128), static_cast<unsigned>(max_tiles)), 256, args);
+}
+
+KernelLaunch make_moe_gather(const MoeGatherArgs &args) {
+  return launch_of(reinterpret_cast<const void *>(&moe_gather_kernel),
+                   dim3(blocks_for(args.routes * (args.hidden / 8), 256)), 256, args);
 }
 
 KernelLaunch make_moe_combine(const MoeCombineArgs &args) {

@@ -302,6 +302,7 @@ namespace {
 struct MoeWorkspace {
   size_t expert_end;
   size_t sorted_route;
+  size_t sorted_weight;
   size_t tile_expert;
   size_t tile_row0;
   size_t activated;
@@ -314,7 +315,9 @@ MoeWorkspace moe_workspace(int64_t rows, int64_t hidden, int64_t intermediate, i
   MoeWorkspace layout{};
   const int64_t routes = rows * topk;
   const int64_t small_rows = moe_tile_rows(MoeTile::Small);
-  layout.max_tiles = static_cast<int>((routes + small_rows - 1) / small_rows + experts);
+  // Tile table entries: a bound on the tiles of either tile size, rounded up to a multiple
+  // of 8 for the grouped tile kernel's XCD mapping.
+  layout.max_tiles = static_cast<int>(((routes + small_rows - 1) / small_rows + experts + 7) / 8 * 8);
   size_t cursor = 0;
   auto region = [&](size_t bytes) {
     const size_t offset = cursor;
@@ -323,6 +326,7 @@ MoeWorkspace moe_workspace(int64_t rows, int64_t hidden, int64_t intermediate, i
   };
   layout.expert_end = region(static_cast<size_t>(experts) * 4);
   layout.sorted_route = region(static_cast<size_t>(routes) * 4);
+  layout.sorted_weight = region(static_cast<size_t>(routes) * 4);
   layout.tile_expert = region(static_cast<size_t>(layout.max_tiles) * 4);
   layout.tile_row0 = region(static_cast<size_t>(layout.max_tiles) * 4);
   layout.activated = region(static_cast<size_t>(routes * intermediate) * 2);
@@ -1300,6 +1304,7 @@ int xp_moe_experts(const void *hidden_states, int64_t rows, int64_t hidden, int6
   uint8_t *base = static_cast<uint8_t *>(workspace);
   int32_t *expert_end = reinterpret_cast<int32_t *>(base + layout.expert_end);
   int32_t *sorted_route = reinterpret_cast<int32_t *>(base + layout.sorted_route);
+  float *sorted_weight = reinterpret_cast<float *>(base + layout.sorted_weight);
   int32_t *tile_expert = reinterpret_cast<int32_t *>(base + layout.tile_expert);
   int32_t *tile_row0 = reinterpret_cast<int32_t *>(base + layout.tile_row0);
   uint16_t *activated = reinterpret_cast<uint16_t *>(base + layout.activated);
@@ -1307,11 +1312,15 @@ int xp_moe_experts(const void *hidden_states, int64_t rows, int64_t hidden, int6
   const int64_t routes = rows * topk;
   const MoeTile tile = choose_moe_tile(routes, experts);
   const int tile_rows = moe_tile_rows(tile);
-  const int max_tiles = static_cast<int>((routes + tile_rows - 1) / tile_rows + experts);
+  const int64_t tiles = ((routes + tile_rows - 1) / tile_rows + experts + 7) / 8 * 8;
+  XP_REQUIRE(tiles <= 65535, "too many expert tiles for one call");
+  const int max_tiles = static_cast<int>(tiles);
   const hipStream_t hip_stream = static_cast<hipStream_t>(stream);
 
   MoeSortArgs sort{};
   sort.ids = topk_ids;
+  sort.weights = topk_weights;
+  sort.sorted_weight = sorted_weight;
   sort.expert_end = expert_end;
   sort.sorted_route = sorted_route;
   sort.tile_expert = tile_expert;
@@ -1322,28 +1331,77 @@ int xp_moe_experts(const void *hidden_states, int64_t rows, int64_t hidden, int6
   sort.max_tiles = max_tiles;
   XP_HIP_CHECK(launch(make_moe_sort(sort), hip_stream));
 
-  MoeGemmArgs gate_up{};
-  gate_up.x = static_cast<const uint16_t *>(hidden_states);
-  gate_up.w = static_cast<const uint16_t *>(w_gate_up);
-  gate_up.out = activated;
-  gate_up.tile_expert = tile_expert;
-  gate_up.tile_row0 = tile_row0;
-  gate_up.expert_end = expert_end;
-  gate_up.sorted_route = sorted_route;
-  gate_up.n = 2 * intermediate;
-  gate_up.k = hidden;
-  gate_up.topk = topk;
-  gate_up.act = GatedSilu{alpha, limit, up_offset};
-  XP_HIP_CHECK(launch(make_moe_gemm(gate_up, tile, true, max_tiles), hip_stream));
+  if (tile == MoeTile::Large) {
+    // Many routes per expert: the Dense tile kernel in its grouped mode.  The token rows are
+    // first gathered into sorted order (into the route-output region, which down overwrites
+    // only after gate_up has read them).
+    if (moe_tile_rows(MoeTile::Large) != grouped_tile_rows()) {
+      return fail(XP_ERROR_STATE, "expert tile table and grouped tile kernel disagree on the tile rows");
+    }
+    MoeGatherArgs gather{};
+    gather.x = static_cast<const uint16_t *>(hidden_states);
+    gather.sorted_route = sorted_route;
+    gather.expert_end = expert_end;
+    gather.out = route_out;
+    gather.routes = routes;
+    gather.hidden = hidden;
+    gather.topk = static_cast<int32_t>(topk);
+    gather.experts = static_cast<int32_t>(experts);
+    XP_HIP_CHECK(launch(make_moe_gather(gather), hip_stream));
 
-  MoeGemmArgs down = gate_up;
-  down.x = activated;
-  down.w = static_cast<const uint16_t *>(w_down);
-  down.out = route_out;
-  down.gammas = topk_weights;
-  down.n = hidden;
-  down.k = intermediate;
-  XP_HIP_CHECK(launch(make_moe_gemm(down, tile, false, max_tiles), hip_stream));
+    GemmArgs up{};
+    up.x = route_out;
+    up.w = static_cast<const uint16_t *>(w_gate_up);
+    up.out = activated;
+    up.ldx = hidden;
+    up.ldo = intermediate;
+    up.rows = routes;
+    up.capacity = routes;
+    up.out_rows = routes;
+    up.n = 2 * intermediate;
+    up.k = hidden;
+    up.act = GatedSilu{alpha, limit, up_offset};
+    up.tile_expert = tile_expert;
+    up.tile_row0 = tile_row0;
+    up.expert_end = expert_end;
+    XP_HIP_CHECK(launch(make_grouped_gemm(up, true, max_tiles), hip_stream));
+
+    GemmArgs dn = up;
+    dn.x = activated;
+    dn.w = static_cast<const uint16_t *>(w_down);
+    dn.out = route_out;
+    dn.scatter_slots = sorted_route;
+    dn.row_scale = sorted_weight;
+    dn.ldx = intermediate;
+    dn.ldo = hidden;
+    dn.n = hidden;
+    dn.k = intermediate;
+    dn.act = default_activation();
+    XP_HIP_CHECK(launch(make_grouped_gemm(dn, false, max_tiles), hip_stream));
+  } else {
+    MoeGemmArgs gate_up{};
+    gate_up.x = static_cast<const uint16_t *>(hidden_states);
+    gate_up.w = static_cast<const uint16_t *>(w_gate_up);
+    gate_up.out = activated;
+    gate_up.tile_expert = tile_expert;
+    gate_up.tile_row0 = tile_row0;
+    gate_up.expert_end = expert_end;
+    gate_up.sorted_route = sorted_route;
+    gate_up.n = 2 * intermediate;
+    gate_up.k = hidden;
+    gate_up.topk = topk;
+    gate_up.act = GatedSilu{alpha, limit, up_offset};
+    XP_HIP_CHECK(launch(make_moe_gemm(gate_up, tile, true, max_tiles), hip_stream));
+
+    MoeGemmArgs down = gate_up;
+    down.x = activated;
+    down.w = static_cast<const uint16_t *>(w_down);
+    down.out = route_out;
+    down.gammas = topk_weights;
+    down.n = hidden;
+    down.k = intermediate;
+    XP_HIP_CHECK(launch(make_moe_gemm(down, tile, false, max_tiles), hip_stream));
+  }
 
   MoeCombineArgs combine{};
   combine.routes = route_out;

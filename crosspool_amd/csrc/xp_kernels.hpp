@@ -21,7 +21,7 @@ struct KernelLaunch {
   dim3 grid{1, 1, 1};
   dim3 block{1, 1, 1};
   unsigned shmem = 0;
-  alignas(16) unsigned char args[192] = {};
+  alignas(16) unsigned char args[256] = {};
   size_t args_size = 0;
 
   template <class Args>
@@ -203,6 +203,8 @@ struct FinalizeRoutingArgs {
 // the grouped projections.
 struct MoeSortArgs {
   const int32_t *ids;        // [routes] expert of each route, -1 = no route
+  const float *weights;      // [routes] route weights
+  float *sorted_weight;      // [routes] weight of the route at each sorted position
   int32_t *expert_end;       // [experts] one past the expert's last sorted position
   int32_t *sorted_route;     // [routes] route at each sorted position
   int32_t *tile_expert;      // [max_tiles] expert of each tile, -1 past the last tile
@@ -231,6 +233,19 @@ struct MoeGemmArgs {
   GatedSilu act;
 };
 
+// Token rows in sorted route order (the A operand of the grouped gate_up on tiles):
+// out[p] = x[sorted_route[p] / topk] for the sorted positions p that hold a route.
+struct MoeGatherArgs {
+  const uint16_t *x;
+  const int32_t *sorted_route;
+  const int32_t *expert_end;
+  uint16_t *out;
+  int64_t routes;
+  int64_t hidden;
+  int32_t topk;
+  int32_t experts;
+};
+
 struct MoeCombineArgs {
   const uint16_t *routes;    // [rows * topk, hidden] route outputs
   const int32_t *ids;        // [rows, topk]
@@ -252,6 +267,7 @@ KernelLaunch make_finalize_routing(const FinalizeRoutingArgs &args);
 KernelLaunch make_moe_sort(const MoeSortArgs &args);
 KernelLaunch make_moe_gemm(const MoeGemmArgs &args, MoeTile tile, bool gated, int max_tiles);
 KernelLaunch make_moe_combine(const MoeCombineArgs &args);
+KernelLaunch make_moe_gather(const MoeGatherArgs &args);
 
 // `capacity` sizes the grid (graph templates keep one grid per capacity);
 // workgroups beyond the live rows exit immediately.
@@ -290,6 +306,16 @@ struct GemmArgs {
   uint32_t *fault;
   int64_t pool_rows;
   float eps;
+  // Grouped projection (MoE experts, tile kernel only, no K split): grid row y is entry y
+  // of an expert tile table over rows sorted by expert; the tile multiplies rows
+  // [tile_row0[y], min(tile_row0[y] + BM, expert_end[e])) by the weights w + e n k of its
+  // expert e = tile_expert[y] (-1: no tile).  With row_scale set (together with
+  // scatter_slots), output row t's fp32 result is multiplied by row_scale[t] before
+  // rounding.
+  const int32_t *tile_expert;
+  const int32_t *tile_row0;
+  const int32_t *expert_end;
+  const float *row_scale;
 };
 
 enum class GemmKind : int { Split = 1, Tile = 2, Stream = 3 };
@@ -318,6 +344,11 @@ struct GemmLaunch {
   KernelLaunch reduce;
 };
 GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmChoice choice);
+// The grouped projection over an expert tile table of `max_tiles` entries (a multiple of
+// 8; otherwise an empty launch), on the tile kernel whose BM is grouped_tile_rows() (the
+// table must be built for that BM).
+KernelLaunch make_grouped_gemm(const GemmArgs &args, bool gated, int max_tiles);
+int grouped_tile_rows();
 std::string gemm_name(GemmChoice choice, bool gated);
 
 }  // namespace xp

@@ -176,9 +176,10 @@ def test_experts_reference_operator_case(device, act):
     assert got[3].abs().sum() == 0
 
 
-@pytest.mark.parametrize("rows", (1, 7, 48))
+@pytest.mark.parametrize("rows", (1, 7, 48, 320))
 def test_experts_qwen3_moe_shape(device, rows):
     # Qwen3-30B-A3B expert layer: hidden 2048, moe_intermediate 768, 128 experts, top-8.
+    # 320 rows (20 routes per expert on average) take the grouped tile kernel.
     hidden, intermediate, experts, topk = 2048, 768, 128, 8
     w_gate_up, w_down = m.generate_moe_layer(hidden, intermediate, experts, 90)
     x = o.generate_hidden_states(rows, hidden, 91 + rows)
