@@ -657,7 +657,7 @@ __device__ __forceinline__ float row_factor(const RowMeta<WTM> &meta, int row) {
   return value;
 }
 
-template <int MT, int NT, int WTM, int WTN, int WAVES, int LDS_ELEMENTS, bool GATED>
+template <int MT, int NT, int WTM, int WTN, int WAVES, int LDS_ELEMENTS, bool GATED, bool GROUPED>
 __device__ __forceinline__ void tile_epilogue(const GemmArgs &a, const f32x16 (&acc)[MT][NT], uint16_t *lds,
                                               int64_t m0, int64_t row_end, int64_t w0, int wave, int wm, int wn,
                                               const RowMeta<WTM> &meta) {
@@ -724,7 +724,10 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs &a, const f32x16 (&
     for (int r = 0; r < 16; ++r) {
       const int row = mt * 32 + 8 * (r >> 2) + 4 * frag_half + (r & 3);
       // Row weight (grouped down projection); 1 elsewhere.
-      const float factor = !GATED && a.row_scale != nullptr ? row_factor(meta, row) : 1.0f;
+      float factor = 1.0f;
+      if constexpr (GROUPED && !GATED) {
+        factor = a.row_scale != nullptr ? row_factor(meta, row) : 1.0f;
+      }
 #pragma unroll
       for (int nt = 0; nt < OUT_N / 32; ++nt) {
         const int col = nt * 32 + frag_row;
@@ -767,7 +770,7 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs &a, const f32x16 (&
 // meanwhile.  Grid z splits K into ranges of `k_slice` columns; with more than one
 // range each workgroup writes the fp32 partial tile of its range and
 // stream_reduce_kernel, launched next, adds the ranges in order and applies the epilogue.
-template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, bool GATED>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, bool GATED, bool GROUPED = false>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmArgs a) {
   constexpr int BK = 64;
   constexpr int WAVES = WAVES_M * WAVES_N;
@@ -796,7 +799,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
 
   int tn;
   int tm;
-  if (a.tile_expert != nullptr) {
+  if constexpr (GROUPED) {
     grouped_tile_coordinates(tn, tm);
   } else {
     tile_coordinates(tn, tm);
@@ -806,7 +809,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
   int64_t m0 = static_cast<int64_t>(tm) * BM;
   int64_t row_end = a.rows;
   const uint16_t *weights = a.w;
-  if (a.tile_expert != nullptr) {
+  if constexpr (GROUPED) {
     const int expert = __builtin_amdgcn_readfirstlane(a.tile_expert[tm]);
     if (expert < 0) {
       return;
@@ -836,8 +839,12 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
   // the global chunk.
   const int64_t a_rows_left = row_end - m0;
   const int64_t b_rows_left = a.n - w0;
+  // A grouped projection may gather its A rows: tile row r is row gather_slots[m0 + r] /
+  // gather_divisor of x ([pool_rows, ldx]); otherwise the tile's rows are contiguous.
+  const bool gathered = GROUPED && a.gather_slots != nullptr;
   const __amdgpu_buffer_rsrc_t a_rsrc =
-      make_rsrc(a.x + m0 * a.ldx, static_cast<uint32_t>((a_rows_left < BM ? a_rows_left : BM) * a.ldx * 2));
+      gathered ? make_rsrc(a.x, static_cast<uint32_t>(a.pool_rows * a.ldx * 2))
+               : make_rsrc(a.x + m0 * a.ldx, static_cast<uint32_t>((a_rows_left < BM ? a_rows_left : BM) * a.ldx * 2));
   const __amdgpu_buffer_rsrc_t b_rsrc =
       make_rsrc(weights + w0 * a.k, static_cast<uint32_t>((b_rows_left < BN ? b_rows_left : BN) * a.k * 2));
   // Load q of a wave covers the 8-row group starting at LDS row g (a multiple of 8); lane
@@ -849,6 +856,22 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
   const bool loading_wave = wave < LOAD_WAVES;
   const int row_in_load = lane >> 3;
   const int lane_chunk[2] = {(lane & 7) ^ (row_in_load >> 1), (lane & 7) ^ (row_in_load >> 1) ^ 4};
+  // Grouped tiles: byte offset of the A row each lane loads in load q (rows past the tile's
+  // live rows of a gathered tile read as zeros through an out-of-range offset).
+  uint32_t a_row_bytes[GROUPED ? A_LOADS : 1];
+  if constexpr (GROUPED) {
+#pragma unroll
+    for (int q = 0; q < A_LOADS; ++q) {
+      const int row = a_first + q * 8 + row_in_load;
+      if (gathered) {
+        a_row_bytes[q] = row < a_rows_left
+                             ? static_cast<uint32_t>(a.gather_slots[m0 + row] / a.gather_divisor * a.ldx * 2)
+                             : kOutOfRange;
+      } else {
+        a_row_bytes[q] = static_cast<uint32_t>(row * a.ldx * 2);
+      }
+    }
+  }
   // B rows of a gated tile are permuted: LDS row p = wq * G + s * G / 2 + jj (G = BN /
   // WAVES_N) holds weight row 2 (wq * G / 2 + jj) + s, i.e. within an 8-row group the weight
   // row is the group's first weight row plus 2 (i / 8).
@@ -877,7 +900,12 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
     for (int q = 0; q < A_LOADS; ++q) {
       const int g = a_first + q * 8;
       const int chunk = lane_chunk[(g >> 3) & 1];
-      const uint32_t offset = static_cast<uint32_t>(((g + row_in_load) * a.ldx + chunk * 8) * 2);
+      uint32_t offset;
+      if constexpr (GROUPED) {
+        offset = a_row_bytes[q] + static_cast<uint32_t>(chunk * 16);
+      } else {
+        offset = static_cast<uint32_t>(((g + row_in_load) * a.ldx + chunk * 8) * 2);
+      }
       buffer_load_lds16(a_rsrc, a_stage + g * BK, chunk < chunks_left ? offset : kOutOfRange, k_bytes);
     }
 #pragma unroll
@@ -1070,7 +1098,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
   // Past-the-end refills may still be landing in the stage buffers the epilogue reuses.
   __builtin_amdgcn_s_waitcnt(0);
 
-  tile_epilogue<MT, NT, WTM, WTN, WAVES, STAGES * STAGE, GATED>(a, acc, lds, m0, row_end, w0, wave, wm, wn, meta);
+  tile_epilogue<MT, NT, WTM, WTN, WAVES, STAGES * STAGE, GATED, GROUPED>(a, acc, lds, m0, row_end, w0, wave, wm, wn,
+                                                                         meta);
 }
 
 // ------------------------------------------------------------------ tables
@@ -1365,8 +1394,11 @@ KernelLaunch make_grouped_gemm(const GemmArgs &args, bool gated, int max_tiles) 
   record.k_slice = args.k;
   record.k_split = 1;
   record.partials = nullptr;
+  static_assert(kTileShapes[kGroupedTileVariant].bm == 256 && kTileShapes[kGroupedTileVariant].bn == 128,
+                "the grouped instantiations below are the 256 x 128 tile");
   KernelLaunch kernel;
-  kernel.func = gated ? tile_kernel<true>(kGroupedTileVariant) : tile_kernel<false>(kGroupedTileVariant);
+  kernel.func = gated ? reinterpret_cast<const void *>(&tile_gemm_kernel<256, 128, 4, 2, 3, true, true>)
+                      : reinterpret_cast<const void *>(&tile_gemm_kernel<256, 128, 4, 2, 3, false, true>);
   kernel.grid = dim3(static_cast<unsigned>((args.n + shape.bn - 1) / shape.bn), static_cast<unsigned>(max_tiles), 1);
   kernel.block = dim3(static_cast<unsigned>(64 * shape.waves), 1, 1);
   kernel.set_args(record);

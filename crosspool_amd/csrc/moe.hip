@@ -16,8 +16,8 @@
 // The reference sorts routes with a bitmatrix and drives triton_kernels' ragged matmul;
 // here one workgroup counts routes per expert in LDS, scans the counts into sorted offsets
 // and an expert tile table, and places each route.  With many routes per expert the
-// projections run on the Dense path's 256 x 128 tile kernel in its grouped mode (token rows
-// first gathered into sorted order); with few (decode) on moe_gemm_kernel below: 32 x 64
+// projections run on the Dense path's 256 x 128 tile kernel in its grouped mode (gate_up
+// gathering each route's token row itself); with few (decode) on moe_gemm_kernel below: 32 x 64
 // tiles of 32x32x16 bf16 MFMAs over (expert tile, weight tile) with register-staged loads
 // into a double-buffered, XOR-swizzled LDS slab.  A route's output row depends only on its
 // own token row and expert, so the order of routes within an expert does not change any bit.
@@ -282,6 +282,10 @@ __device__ int block_inclusive_scan(int value, int *wave_totals) {
   return value + wave_totals[wave];
 }
 
+// Routes held in registers per thread between the count and the placement (16384 routes,
+// 2048 rows at top-8, in one pass; more are read again).
+constexpr int kSortRoutesPerThread = 16;
+
 __global__ __launch_bounds__(1024) void moe_sort_kernel(MoeSortArgs a) {
   __shared__ int counts[kMoeMaxExperts];
   __shared__ int offsets[kMoeMaxExperts + 1];
@@ -289,8 +293,22 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(MoeSortArgs a) {
   __shared__ int totals[1024 / kWave];
   const int tid = threadIdx.x;
   counts[tid] = 0;
+  int32_t held_expert[kSortRoutesPerThread];
+  float held_weight[kSortRoutesPerThread];
+#pragma unroll
+  for (int i = 0; i < kSortRoutesPerThread; ++i) {
+    const int64_t route = tid + static_cast<int64_t>(i) * 1024;
+    held_expert[i] = route < a.routes ? a.ids[route] : -1;
+    held_weight[i] = route < a.routes ? a.weights[route] : 0.0f;
+  }
   __syncthreads();
-  for (int64_t route = tid; route < a.routes; route += 1024) {
+#pragma unroll
+  for (int i = 0; i < kSortRoutesPerThread; ++i) {
+    if (held_expert[i] >= 0 && held_expert[i] < a.experts) {
+      atomicAdd(&counts[held_expert[i]], 1);
+    }
+  }
+  for (int64_t route = tid + 1024 * kSortRoutesPerThread; route < a.routes; route += 1024) {
     const int expert = a.ids[route];
     if (expert >= 0 && expert < a.experts) {
       atomicAdd(&counts[expert], 1);
@@ -334,7 +352,15 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(MoeSortArgs a) {
     a.tile_row0[tile] = offsets[low] + (tile - tiles[low]) * a.tile_rows;
   }
   __syncthreads();
-  for (int64_t route = tid; route < a.routes; route += 1024) {
+#pragma unroll
+  for (int i = 0; i < kSortRoutesPerThread; ++i) {
+    if (held_expert[i] >= 0 && held_expert[i] < a.experts) {
+      const int position = atomicAdd(&counts[held_expert[i]], 1);
+      a.sorted_route[position] = static_cast<int32_t>(tid + i * 1024);
+      a.sorted_weight[position] = held_weight[i];
+    }
+  }
+  for (int64_t route = tid + 1024 * kSortRoutesPerThread; route < a.routes; route += 1024) {
     const int expert = a.ids[route];
     if (expert >= 0 && expert < a.experts) {
       const int position = atomicAdd(&counts[expert], 1);
@@ -509,19 +535,6 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void moe_gemm_kernel(MoeGem
   }
 }
 
-// Token rows gathered into sorted route order, 16 bytes per thread.
-__global__ __launch_bounds__(256) void moe_gather_kernel(MoeGatherArgs a) {
-  const int64_t chunks = a.hidden / 8;
-  const int64_t index = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  const int64_t position = index / chunks;
-  if (position >= a.routes || position >= a.expert_end[a.experts - 1]) {
-    return;
-  }
-  const int64_t chunk = index % chunks;
-  const int64_t token = a.sorted_route[position] / a.topk;
-  store16(a.out + position * a.hidden + chunk * 8, load16(a.x + token * a.hidden + chunk * 8));
-}
-
 // out[row] = bf16(scale * sum over the row's live routes, in slot order, of float(route
 // output)) -- the route reduction with the routed scaling factor (moe.py:336-343); rows
 // whose slots are all -1 read 0.
@@ -606,11 +619,6 @@ KernelLaunch make_moe_gemm(const MoeGemmArgs &args, MoeTile tile, bool gated, in
   const void *kernel = gated ? reinterpret_cast<const void *>(&moe_gemm_kernel<128, 128, 2, 2, true>)
                              : reinterpret_cast<const void *>(&moe_gemm_kernel<128, 128, 2, 2, false>);
   return launch_of(kernel, dim3(blocks_for(args.n, 128), static_cast<unsigned>(max_tiles)), 256, args);
-}
-
-KernelLaunch make_moe_gather(const MoeGatherArgs &args) {
-  return launch_of(reinterpret_cast<const void *>(&moe_gather_kernel),
-                   dim3(blocks_for(args.routes * (args.hidden / 8), 256)), 256, args);
 }
 
 KernelLaunch make_moe_combine(const MoeCombineArgs &args) {

@@ -1332,25 +1332,16 @@ int xp_moe_experts(const void *hidden_states, int64_t rows, int64_t hidden, int6
   XP_HIP_CHECK(launch(make_moe_sort(sort), hip_stream));
 
   if (tile == MoeTile::Large) {
-    // Many routes per expert: the Dense tile kernel in its grouped mode.  The token rows are
-    // first gathered into sorted order (into the route-output region, which down overwrites
-    // only after gate_up has read them).
+    // Many routes per expert: the Dense tile kernel in its grouped mode; gate_up gathers the
+    // token row of each sorted route (route / topk) itself.
     if (moe_tile_rows(MoeTile::Large) != grouped_tile_rows()) {
       return fail(XP_ERROR_STATE, "expert tile table and grouped tile kernel disagree on the tile rows");
     }
-    MoeGatherArgs gather{};
-    gather.x = static_cast<const uint16_t *>(hidden_states);
-    gather.sorted_route = sorted_route;
-    gather.expert_end = expert_end;
-    gather.out = route_out;
-    gather.routes = routes;
-    gather.hidden = hidden;
-    gather.topk = static_cast<int32_t>(topk);
-    gather.experts = static_cast<int32_t>(experts);
-    XP_HIP_CHECK(launch(make_moe_gather(gather), hip_stream));
-
     GemmArgs up{};
-    up.x = route_out;
+    up.x = static_cast<const uint16_t *>(hidden_states);
+    up.gather_slots = sorted_route;
+    up.gather_divisor = topk;
+    up.pool_rows = rows;
     up.w = static_cast<const uint16_t *>(w_gate_up);
     up.out = activated;
     up.ldx = hidden;
@@ -1368,6 +1359,7 @@ int xp_moe_experts(const void *hidden_states, int64_t rows, int64_t hidden, int6
 
     GemmArgs dn = up;
     dn.x = activated;
+    dn.gather_slots = nullptr;
     dn.w = static_cast<const uint16_t *>(w_down);
     dn.out = route_out;
     dn.scatter_slots = sorted_route;

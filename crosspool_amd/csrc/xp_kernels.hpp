@@ -233,19 +233,6 @@ struct MoeGemmArgs {
   GatedSilu act;
 };
 
-// Token rows in sorted route order (the A operand of the grouped gate_up on tiles):
-// out[p] = x[sorted_route[p] / topk] for the sorted positions p that hold a route.
-struct MoeGatherArgs {
-  const uint16_t *x;
-  const int32_t *sorted_route;
-  const int32_t *expert_end;
-  uint16_t *out;
-  int64_t routes;
-  int64_t hidden;
-  int32_t topk;
-  int32_t experts;
-};
-
 struct MoeCombineArgs {
   const uint16_t *routes;    // [rows * topk, hidden] route outputs
   const int32_t *ids;        // [rows, topk]
@@ -267,7 +254,6 @@ KernelLaunch make_finalize_routing(const FinalizeRoutingArgs &args);
 KernelLaunch make_moe_sort(const MoeSortArgs &args);
 KernelLaunch make_moe_gemm(const MoeGemmArgs &args, MoeTile tile, bool gated, int max_tiles);
 KernelLaunch make_moe_combine(const MoeCombineArgs &args);
-KernelLaunch make_moe_gather(const MoeGatherArgs &args);
 
 // `capacity` sizes the grid (graph templates keep one grid per capacity);
 // workgroups beyond the live rows exit immediately.
@@ -309,13 +295,15 @@ struct GemmArgs {
   // Grouped projection (MoE experts, tile kernel only, no K split): grid row y is entry y
   // of an expert tile table over rows sorted by expert; the tile multiplies rows
   // [tile_row0[y], min(tile_row0[y] + BM, expert_end[e])) by the weights w + e n k of its
-  // expert e = tile_expert[y] (-1: no tile).  With row_scale set (together with
-  // scatter_slots), output row t's fp32 result is multiplied by row_scale[t] before
+  // expert e = tile_expert[y] (-1: no tile).  With gather_slots set, tile row t reads row
+  // gather_slots[t] / gather_divisor of x ([pool_rows, ldx]).  With row_scale set (together
+  // with scatter_slots), output row t's fp32 result is multiplied by row_scale[t] before
   // rounding.
   const int32_t *tile_expert;
   const int32_t *tile_row0;
   const int32_t *expert_end;
   const float *row_scale;
+  int64_t gather_divisor;
 };
 
 enum class GemmKind : int { Split = 1, Tile = 2, Stream = 3 };
