@@ -24,33 +24,28 @@
 
 #include "xp_kernels.hpp"
 
+// Wavefront reductions of the ROCm device library (ockl), linked into every HIP device build.
+extern "C" __device__ __attribute__((const)) float __ockl_wfred_max_f32(float);
+extern "C" __device__ __attribute__((const)) float __ockl_wfred_add_f32(float);
+extern "C" __device__ __attribute__((const)) unsigned long long __ockl_wfred_max_u64(unsigned long long);
+
 namespace xp {
 namespace {
 
 constexpr float kNegativeInfinity = -__builtin_inff();
 
-__device__ __forceinline__ float wave_max(float value) {
-#pragma unroll
-  for (int offset = 32; offset > 0; offset >>= 1) {
-    value = fmaxf(value, __shfl_xor(value, offset, kWave));
-  }
-  return value;
+// Wavefront reductions through the device library's DPP sequences (a handful of cycles per
+// step, where a shuffle goes through the LDS crossbar); every lane receives the result.
+__device__ __forceinline__ float wave_max_f32(float value) { return __ockl_wfred_max_f32(value); }
+__device__ __forceinline__ float wave_add_f32(float value) { return __ockl_wfred_add_f32(value); }
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long value) {
+  return __ockl_wfred_max_u64(value);
 }
 
-__device__ __forceinline__ int wave_min_int(int value) {
-#pragma unroll
-  for (int offset = 32; offset > 0; offset >>= 1) {
-    value = min(value, __shfl_xor(value, offset, kWave));
-  }
-  return value;
-}
-
-__device__ __forceinline__ int wave_max_int(int value) {
-#pragma unroll
-  for (int offset = 32; offset > 0; offset >>= 1) {
-    value = max(value, __shfl_xor(value, offset, kWave));
-  }
-  return value;
+// fp32 bits mapped to an unsigned integer of the same order (-inf lowest, +inf highest).
+__device__ __forceinline__ uint32_t ordered_bits(float value) {
+  const uint32_t bits = __float_as_uint(value);
+  return (bits & 0x80000000u) != 0 ? ~bits : bits | 0x80000000u;
 }
 
 // ------------------------------------------------------------------ router
@@ -79,16 +74,15 @@ __global__ __launch_bounds__(256) void router_topk_kernel(RouterTopkArgs a) {
     maximum = fmaxf(maximum, value);
   }
   float score[kTopkPerLane];
-  float selection[kTopkPerLane];
   if (a.softmax != 0) {
-    maximum = wave_max(maximum);
+    maximum = wave_max_f32(maximum);
     float sum = 0.0f;
 #pragma unroll
     for (int i = 0; i < kTopkPerLane; ++i) {
       score[i] = lane + i * kWave < experts ? expf(logit[i] - maximum) : 0.0f;
       sum += score[i];
     }
-    sum = wave_sum(sum);
+    sum = wave_add_f32(sum);
 #pragma unroll
     for (int i = 0; i < kTopkPerLane; ++i) {
       score[i] = score[i] / sum;
@@ -99,6 +93,10 @@ __global__ __launch_bounds__(256) void router_topk_kernel(RouterTopkArgs a) {
       score[i] = 1.0f / (1.0f + expf(-logit[i]));
     }
   }
+  // Selection keys: the selection's ordered bits above a tie-break field that favours the
+  // lower id (softmax) or the higher id (sigmoid), so one 64-bit wavefront maximum picks the
+  // expert.  Padding experts never win: their key is 0.
+  unsigned long long key[kTopkPerLane];
 #pragma unroll
   for (int i = 0; i < kTopkPerLane; ++i) {
     const int expert = lane + i * kWave;
@@ -111,7 +109,9 @@ __global__ __launch_bounds__(256) void router_topk_kernel(RouterTopkArgs a) {
     if (a.softmax == 0 && a.logits_f32 == 0) {
       value = round_bf16(value);
     }
-    selection[i] = expert < experts ? value : kNegativeInfinity;
+    const uint32_t tie = a.softmax != 0 ? static_cast<uint32_t>(kMoeMaxExperts - 1 - expert)
+                                        : static_cast<uint32_t>(expert);
+    key[i] = expert < experts ? (static_cast<unsigned long long>(ordered_bits(value)) << 32) | (tie + 1) : 0ull;
   }
 
   // Lane `slot` keeps slot `slot`'s id and weight (topk <= 64).
@@ -119,32 +119,25 @@ __global__ __launch_bounds__(256) void router_topk_kernel(RouterTopkArgs a) {
   float chosen_weight = 0.0f;
   int chosen_id = -1;
   for (int slot = 0; slot < a.topk; ++slot) {
-    float best = kNegativeInfinity;
+    unsigned long long best = 0ull;
 #pragma unroll
     for (int i = 0; i < kTopkPerLane; ++i) {
-      best = fmaxf(best, selection[i]);
+      best = key[i] > best ? key[i] : best;
     }
-    best = wave_max(best);
-    // Softmax breaks ties by the lower id, sigmoid by the higher one; padding never wins.
-    int candidate = a.softmax != 0 ? experts : -1;
-#pragma unroll
-    for (int i = 0; i < kTopkPerLane; ++i) {
-      const int expert = lane + i * kWave;
-      if (expert < experts && selection[i] == best) {
-        candidate = a.softmax != 0 ? min(candidate, expert) : max(candidate, expert);
-      }
-    }
-    const int expert = a.softmax != 0 ? wave_min_int(candidate) : wave_max_int(candidate);
+    best = wave_max_u64(best);
+    const uint32_t tie = static_cast<uint32_t>(best & 0xffffffffull) - 1;
+    const int expert = a.softmax != 0 ? kMoeMaxExperts - 1 - static_cast<int>(tie) : static_cast<int>(tie);
     float own = 0.0f;
 #pragma unroll
     for (int i = 0; i < kTopkPerLane; ++i) {
       if (lane + i * kWave == expert) {
         own = score[i];
-        selection[i] = kNegativeInfinity;
+        key[i] = 0ull;
       }
     }
-    const float weight =
-        a.softmax != 0 && a.correction_bias == nullptr ? best : __shfl(own, expert & (kWave - 1), kWave);
+    // The weight is the picked expert's score (for softmax without correction that is the
+    // selected maximum itself).
+    const float weight = __shfl(own, expert & (kWave - 1), kWave);
     normalizer += weight;
     if (lane == slot) {
       chosen_weight = weight;
@@ -547,17 +540,31 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(MoeCombineArgs a) {
   const int64_t row = index / chunks;
   const int64_t chunk = index % chunks;
   float sum[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-  for (int slot = 0; slot < a.topk; ++slot) {
-    const int64_t route = row * a.topk + slot;
-    const int32_t expert = a.ids[route];
-    if (expert < 0 || expert >= a.experts) {
-      continue;
-    }
-    const u32x4 values = load16(a.routes + route * a.hidden + chunk * 8);
+  // Slots in batches: the batch's ids first, then its route rows, then the sums in slot
+  // order (two memory round trips per batch instead of two per slot).
+  constexpr int BATCH = 8;
+  for (int first = 0; first < a.topk; first += BATCH) {
+    int32_t expert[BATCH];
 #pragma unroll
-    for (int word = 0; word < 4; ++word) {
-      sum[2 * word] += bf16_to_float(values[word] & 0xffffu);
-      sum[2 * word + 1] += bf16_to_float(values[word] >> 16);
+    for (int b = 0; b < BATCH; ++b) {
+      expert[b] = first + b < a.topk ? a.ids[row * a.topk + first + b] : -1;
+    }
+    u32x4 values[BATCH];
+#pragma unroll
+    for (int b = 0; b < BATCH; ++b) {
+      const bool live = expert[b] >= 0 && expert[b] < a.experts;
+      values[b] = live ? load16(a.routes + (row * a.topk + first + b) * a.hidden + chunk * 8) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int b = 0; b < BATCH; ++b) {
+      if (expert[b] < 0 || expert[b] >= a.experts) {
+        continue;
+      }
+#pragma unroll
+      for (int word = 0; word < 4; ++word) {
+        sum[2 * word] += bf16_to_float(values[b][word] & 0xffffu);
+        sum[2 * word + 1] += bf16_to_float(values[b][word] >> 16);
+      }
     }
   }
   u32x4 packed;
