@@ -45,6 +45,10 @@ __device__ __forceinline__ uint16_t *output_row(const GemmArgs &a, int64_t token
   return a.out + token * a.ldo;
 }
 
+// Offset that is always past a buffer resource's end (resources stay below 2^31 bytes, and
+// adding a row's byte offset keeps it below 2^32).
+constexpr uint32_t kOutOfRange = 0x7ffffff0u;
+
 // ------------------------------------------------------------------ split (decode)
 // Weight-streaming projection for at most 64 live rows (HBM-bound).  A workgroup of 8
 // waves covers 8 / KSPLIT weight-row blocks of 16 rows; the KSPLIT waves of a block each
@@ -190,6 +194,156 @@ __global__ __launch_bounds__(64 * kSplitWaves) void split_gemm_kernel(GemmArgs a
       u32x2 packed = {pack_bf16x2(acc[tb][0], acc[tb][1]), pack_bf16x2(acc[tb][2], acc[tb][3])};
       *reinterpret_cast<u32x2 *>(row + n) = packed;
     }
+  }
+}
+
+// ------------------------------------------------------------------ grouped split (MoE decode)
+// The split kernel over an expert tile table, for few routes per expert.  Grid y is entry y
+// of the table: up to 16 sorted positions of one expert e (GemmArgs describes the table);
+// grid x covers e's 16-row weight blocks and their K ranges as in split_gemm_kernel.  The
+// token operand row of lane r16 is sorted position p = tile_row0[y] + r16 while p <
+// expert_end[e]: row gather_slots[p] / gather_divisor of x when gather_slots is set, else
+// row p.  The result goes to row p of out, or to row scatter_slots[p] when that is set,
+// times row_scale[p] when that is set.  A wave's chunk count is rounded up to whole groups
+// of DEPTH; the chunks past its range load through an out-of-range offset, which reads
+// zeros without a memory access.
+template <int DEPTH, bool GATED>
+__global__ __launch_bounds__(64 * kSplitWaves) void grouped_split_kernel(GemmArgs a) {
+  // Both table words are loaded before the branch: the loads that follow depend on them,
+  // and each dependent level costs a memory round trip before the weight stream starts.
+  const int expert = __builtin_amdgcn_readfirstlane(a.tile_expert[blockIdx.y]);
+  const int64_t m0 = __builtin_amdgcn_readfirstlane(a.tile_row0[blockIdx.y]);
+  if (expert < 0) {
+    return;  // uniform over the workgroup: no tile
+  }
+  const int64_t row_end = __builtin_amdgcn_readfirstlane(a.expert_end[expert]);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int r16 = lane & 15;
+  const int kq = lane >> 4;
+  const int ksplit = static_cast<int>(a.k_split);
+  const int part = wave % ksplit;
+  const int64_t rb = static_cast<int64_t>(blockIdx.x) * (kSplitWaves / ksplit) + wave / ksplit;
+  const int64_t row_blocks = (a.n + 15) / 16;
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+
+  // This lane's route: its token row, and for the epilogue its output row and factor, all
+  // loaded before the stream starts.
+  const int64_t position = m0 + r16;
+  const bool live = position < row_end;
+  int64_t x_row = position;
+  if (a.gather_slots != nullptr) {
+    x_row = live ? a.gather_slots[position] / a.gather_divisor : 0;
+  }
+  int64_t out_row = position;
+  if (a.scatter_slots != nullptr) {
+    out_row = live ? a.scatter_slots[position] : -1;
+  }
+  const float factor = live && a.row_scale != nullptr ? a.row_scale[position] : 1.0f;
+
+  f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  if (rb < row_blocks) {
+    const int k0 = part * static_cast<int>(a.k_slice);
+    const int k_range = static_cast<int>(a.k - k0 < a.k_slice ? a.k - k0 : a.k_slice);
+    const int chunks = (k_range + 127) / 128;  // >= 1: the host makes no empty range
+    const int groups = (chunks + DEPTH - 1) / DEPTH;
+    // Columns at or past K in the last chunk read the next row (or past the end): zero
+    // both operands there.
+    const int lane_valid = static_cast<int>(a.k) - k0 - kq * 8;
+    const int rotation = static_cast<int>((rb * 7) % chunks);
+    const uint16_t *weights = a.w + static_cast<int64_t>(expert) * a.n * a.k;
+    const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(weights, static_cast<uint32_t>(a.n * a.k * 2));
+    const __amdgpu_buffer_rsrc_t x_rsrc =
+        make_rsrc(a.x, static_cast<uint32_t>((a.gather_slots != nullptr ? a.pool_rows : a.rows) * a.ldx * 2));
+    const uint32_t w_off = static_cast<uint32_t>(((rb * 16 + r16) * a.k + k0 + kq * 8) * 2);
+    const uint32_t x_off = live ? static_cast<uint32_t>((x_row * a.ldx + k0 + kq * 8) * 2) : kOutOfRange;
+    auto column_of = [&](int chunk) {
+      const int c = chunk + rotation;
+      return (c < chunks ? c : c - chunks) * 128;
+    };
+
+    u32x4 wbuf[DEPTH][4];
+    u32x4 xbuf[DEPTH][4];
+    auto load_w = [&](int chunk, u32x4 (&w)[4]) {
+      const bool in_range = chunk < chunks;
+      const uint32_t base = in_range ? w_off + static_cast<uint32_t>(column_of(chunk)) * 2 : kOutOfRange;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        w[s] = buffer_load16(w_rsrc, base + s * 64);
+      }
+    };
+    auto load_x = [&](int chunk, u32x4 (&x)[4]) {
+      const bool in_range = chunk < chunks;
+      const uint32_t base = in_range ? x_off + static_cast<uint32_t>(column_of(chunk)) * 2 : kOutOfRange;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        x[s] = buffer_load16(x_rsrc, base + s * 64);
+      }
+    };
+    auto compute_chunk = [&](int chunk, const u32x4 (&w)[4], const u32x4 (&x)[4]) {
+      const int column = chunk < chunks ? column_of(chunk) : 0;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const bool valid = column + s * 32 < lane_valid;
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(valid ? w[s] : zero), as_bf16x8(valid ? x[s] : zero),
+                                                      acc, 0, 0, 0);
+      }
+    };
+
+    // The weight loads of the first group go out before the token loads, whose offsets
+    // wait on the gather slot load.
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      load_w(d, wbuf[d]);
+    }
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      load_x(d, xbuf[d]);
+    }
+    for (int g = 1; g < groups; ++g) {
+#pragma unroll
+      for (int d = 0; d < DEPTH; ++d) {
+        const int chunk = (g - 1) * DEPTH + d;
+        compute_chunk(chunk, wbuf[d], xbuf[d]);
+        load_w(chunk + DEPTH, wbuf[d]);
+        load_x(chunk + DEPTH, xbuf[d]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      compute_chunk((groups - 1) * DEPTH + d, wbuf[d], xbuf[d]);
+    }
+  }
+
+  // Fixed-order sum of the K ranges of each row block, as in split_gemm_kernel.
+  __shared__ f32x4 partial[kSplitWaves][64];
+  if (ksplit > 1) {
+    partial[wave][lane] = acc;
+    __syncthreads();
+    if (part != 0) {
+      return;
+    }
+    for (int p = 1; p < ksplit; ++p) {
+      acc += partial[wave + p][lane];
+    }
+  }
+  if (rb >= row_blocks || !live || out_row < 0 || out_row >= a.out_rows) {
+    return;
+  }
+  // lane holds D[4 kq + i][r16]: weight rows n .. n+3 of this lane's route.
+  const int64_t n = rb * 16 + 4 * kq;
+  if (n >= a.n) {
+    return;
+  }
+  uint16_t *row = a.out + out_row * a.ldo;
+  if constexpr (GATED) {
+    const float h0 = gated_silu(acc[0], acc[1], a.act);
+    const float h1 = gated_silu(acc[2], acc[3], a.act);
+    *reinterpret_cast<uint32_t *>(row + n / 2) = pack_bf16x2(h0, h1);
+  } else {
+    u32x2 packed = {pack_bf16x2(acc[0] * factor, acc[1] * factor), pack_bf16x2(acc[2] * factor, acc[3] * factor)};
+    *reinterpret_cast<u32x2 *>(row + n) = packed;
   }
 }
 
@@ -557,9 +711,6 @@ template <int N, class F>
 __device__ __forceinline__ void static_for(F &&f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
-
-// Offset that is always past a tile resource's end (resources stay below 2^31 bytes).
-constexpr uint32_t kOutOfRange = 0x7ffffff0u;
 
 // Weight tile tn and token tile tm of this workgroup (grid x spans the weight tiles, y the
 // token tiles).  Workgroups go to the 8 XCDs round robin by linear id L = x + y gridDim.x,
@@ -1401,6 +1552,39 @@ KernelLaunch make_grouped_gemm(const GemmArgs &args, bool gated, int max_tiles) 
                       : reinterpret_cast<const void *>(&tile_gemm_kernel<256, 128, 4, 2, 3, false, true>);
   kernel.grid = dim3(static_cast<unsigned>((args.n + shape.bn - 1) / shape.bn), static_cast<unsigned>(max_tiles), 1);
   kernel.block = dim3(static_cast<unsigned>(64 * shape.waves), 1, 1);
+  kernel.set_args(record);
+  return kernel;
+}
+
+// Routes per expert tile of the grouped split kernel: one 16-column MFMA token block.
+int grouped_split_rows() { return 16; }
+
+// K ranges per weight block: the most (1, 2, 4 or 8) that keep the expected live tiles'
+// workgroups within one round of one per CU, with every range at least two 128-wide chunks
+// long.  A workgroup at decode sizes is latency-bound (the tile table, the route slots,
+// then the weights and tokens, each a memory round trip), so a second round of
+// workgroups costs nearly as much as the first (Qwen3-30B-A3B gate_up at 1 token: 384
+// workgroups in two rounds 17.8 us).
+KernelLaunch make_grouped_split(const GemmArgs &args, bool gated, int max_tiles, int64_t live_tiles) {
+  const int64_t row_blocks = (args.n + 15) / 16;
+  const int64_t chunks = (args.k + 127) / 128;
+  auto nonempty = [&](int64_t ranges) { return (ranges - 1) * ((chunks + ranges - 1) / ranges) < chunks; };
+  auto workgroups = [&](int64_t ranges) { return (row_blocks * ranges + kSplitWaves - 1) / kSplitWaves * live_tiles; };
+  int64_t ksplit = 1;
+  while (ksplit < kSplitWaves && 4 * ksplit <= chunks && nonempty(2 * ksplit) &&
+         workgroups(2 * ksplit) <= kComputeUnits) {
+    ksplit *= 2;
+  }
+  GemmArgs record = args;
+  record.k_split = ksplit;
+  record.k_slice = (chunks + ksplit - 1) / ksplit * 128;
+  record.partials = nullptr;
+  KernelLaunch kernel;
+  kernel.func = gated ? reinterpret_cast<const void *>(&grouped_split_kernel<kSplitDepth, true>)
+                      : reinterpret_cast<const void *>(&grouped_split_kernel<kSplitDepth, false>);
+  kernel.grid = dim3(static_cast<unsigned>((row_blocks * ksplit + kSplitWaves - 1) / kSplitWaves),
+                     static_cast<unsigned>(max_tiles), 1);
+  kernel.block = dim3(64 * kSplitWaves, 1, 1);
   kernel.set_args(record);
   return kernel;
 }

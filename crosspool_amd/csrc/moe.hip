@@ -17,9 +17,9 @@
 // here one workgroup counts routes per expert in LDS, scans the counts into sorted offsets
 // and an expert tile table, and places each route.  With many routes per expert the
 // projections run on the Dense path's 256 x 128 tile kernel in its grouped mode (gate_up
-// gathering each route's token row itself); with few (decode) on moe_gemm_kernel below: 32 x 64
-// tiles of 32x32x16 bf16 MFMAs over (expert tile, weight tile) with register-staged loads
-// into a double-buffered, XOR-swizzled LDS slab.  A route's output row depends only on its
+// gathering each route's token row itself); with few (decode) on the grouped split kernel,
+// which streams each touched expert's weight rows as the MFMA M operand against 16-route
+// token blocks read from L2.  A route's output row depends only on its
 // own token row and expert, so the order of routes within an expert does not change any bit.
 
 #include "xp_kernels.hpp"
@@ -363,171 +363,7 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(MoeSortArgs a) {
   }
 }
 
-// ------------------------------------------------------------------ grouped projection
-__device__ __forceinline__ int moe_swizzle(int row) { return (row >> 1) & 7; }
-
-template <int BM, int BN, int WAVES_M, int WAVES_N, bool GATED>
-__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void moe_gemm_kernel(MoeGemmArgs a) {
-  constexpr int THREADS = 64 * WAVES_M * WAVES_N;
-  constexpr int BK = 64;
-  constexpr int WTM = BM / WAVES_M;
-  constexpr int WTN = BN / WAVES_N;
-  constexpr int MT = WTM / 32;
-  constexpr int NT = WTN / 32;
-  constexpr int ROW_STEP = THREADS / 8;  // rows one load pass covers (8 chunks per row)
-  constexpr int A_LOADS = BM / ROW_STEP;
-  constexpr int B_LOADS = BN / ROW_STEP;
-  static_assert(MT >= 1 && NT >= 1 && A_LOADS >= 1 && B_LOADS >= 1, "tile shape");
-  static_assert(A_LOADS * ROW_STEP == BM && B_LOADS * ROW_STEP == BN, "loads must cover the tile");
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2][(BM + BN) * BK];
-
-  const int tile = static_cast<int>(blockIdx.y);
-  const int expert = a.tile_expert[tile];
-  if (expert < 0) {
-    return;
-  }
-  const int row0 = a.tile_row0[tile];
-  const int end = a.expert_end[expert];
-  const int live = end - row0 < BM ? end - row0 : BM;
-  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * BN;
-  const int tid = static_cast<int>(threadIdx.x);
-  const int chunk = tid & 7;
-  const int load_row = tid >> 3;
-
-  const uint16_t *a_source[A_LOADS];
-#pragma unroll
-  for (int j = 0; j < A_LOADS; ++j) {
-    const int r = load_row + j * ROW_STEP;
-    if (r < live) {
-      const int64_t source_row = GATED ? a.sorted_route[row0 + r] / a.topk : static_cast<int64_t>(row0 + r);
-      a_source[j] = a.x + source_row * a.k;
-    } else {
-      a_source[j] = nullptr;
-    }
-  }
-  const uint16_t *b_source[B_LOADS];
-  const uint16_t *w_expert = a.w + static_cast<int64_t>(expert) * a.n * a.k;
-#pragma unroll
-  for (int j = 0; j < B_LOADS; ++j) {
-    const int64_t n = n0 + load_row + j * ROW_STEP;
-    b_source[j] = n < a.n ? w_expert + n * a.k : nullptr;
-  }
-
-  u32x4 a_stage[A_LOADS];
-  u32x4 b_stage[B_LOADS];
-  const u32x4 zero = {0u, 0u, 0u, 0u};
-  auto load = [&](int64_t kt) {
-    const int64_t column = kt * BK + chunk * 8;
-    const bool inside = column < a.k;
-#pragma unroll
-    for (int j = 0; j < A_LOADS; ++j) {
-      a_stage[j] = a_source[j] != nullptr && inside ? load16(a_source[j] + column) : zero;
-    }
-#pragma unroll
-    for (int j = 0; j < B_LOADS; ++j) {
-      b_stage[j] = b_source[j] != nullptr && inside ? load16(b_source[j] + column) : zero;
-    }
-  };
-  auto store = [&](int stage) {
-#pragma unroll
-    for (int j = 0; j < A_LOADS; ++j) {
-      const int r = load_row + j * ROW_STEP;
-      store16(&lds[stage][r * BK + ((chunk ^ moe_swizzle(r)) << 3)], a_stage[j]);
-    }
-#pragma unroll
-    for (int j = 0; j < B_LOADS; ++j) {
-      const int r = BM + load_row + j * ROW_STEP;
-      store16(&lds[stage][r * BK + ((chunk ^ moe_swizzle(r)) << 3)], b_stage[j]);
-    }
-  };
-
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave % WAVES_M;
-  const int wn = wave / WAVES_M;
-  const int frag_row = lane & 31;
-  const int frag_half = lane >> 5;
-  f32x16 acc[MT][NT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        acc[mt][nt][r] = 0.0f;
-      }
-    }
-  }
-
-  const int64_t ktiles = (a.k + BK - 1) / BK;
-  load(0);
-  store(0);
-  __syncthreads();
-  for (int64_t kt = 0; kt < ktiles; ++kt) {
-    const bool more = kt + 1 < ktiles;
-    if (more) {
-      load(kt + 1);
-    }
-    const int stage = static_cast<int>(kt & 1);
-#pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      const int logical = ks * 2 + frag_half;
-      bf16x8 af[MT];
-      bf16x8 bf[NT];
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const int r = wm * WTM + mt * 32 + frag_row;
-        af[mt] = as_bf16x8(load16(&lds[stage][r * BK + ((logical ^ moe_swizzle(r)) << 3)]));
-      }
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        const int r = BM + wn * WTN + nt * 32 + frag_row;
-        bf[nt] = as_bf16x8(load16(&lds[stage][r * BK + ((logical ^ moe_swizzle(r)) << 3)]));
-      }
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-          acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mt], bf[nt], acc[mt][nt], 0, 0, 0);
-        }
-      }
-    }
-    if (more) {
-      store(stage ^ 1);
-    }
-    __syncthreads();
-  }
-
-  // Lane holds D[8 (r / 4) + 4 (lane / 32) + r % 4][lane % 32] of each 32x32 tile.
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      const int64_t column = n0 + wn * WTN + nt * 32 + frag_row;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = wm * WTM + mt * 32 + 8 * (r >> 2) + 4 * frag_half + (r & 3);
-        const float value = acc[mt][nt][r];
-        if constexpr (GATED) {
-          // Interleaved i_proj: column 2j is gate_j, 2j + 1 is up_j, held by lanes l, l ^ 1.
-          const float partner = __shfl_xor(value, 1, kWave);
-          if ((frag_row & 1) == 0 && m < live && column < a.n) {
-            const float activated = gated_silu(value, partner, a.act);
-            a.out[static_cast<int64_t>(row0 + m) * (a.n / 2) + column / 2] =
-                static_cast<uint16_t>(float_to_bf16(activated));
-          }
-        } else {
-          if (m < live && column < a.n) {
-            const int32_t route = a.sorted_route[row0 + m];
-            a.out[static_cast<int64_t>(route) * a.n + column] =
-                static_cast<uint16_t>(float_to_bf16(value * a.gammas[route]));
-          }
-        }
-      }
-    }
-  }
-}
-
+// ------------------------------------------------------------------ combine
 // out[row] = bf16(scale * sum over the row's live routes, in slot order, of float(route
 // output)) -- the route reduction with the routed scaling factor (moe.py:336-343); rows
 // whose slots are all -1 read 0.
@@ -591,12 +427,16 @@ unsigned blocks_for(int64_t items, int64_t per_block) {
 
 }  // namespace
 
-int moe_tile_rows(MoeTile tile) { return tile == MoeTile::Small ? 32 : grouped_tile_rows(); }
+int moe_tile_rows(MoeTile tile) { return tile == MoeTile::Small ? grouped_split_rows() : grouped_tile_rows(); }
 
-// Few routes per expert (decode) take 32-row tiles over 64 weight rows, which spread each
-// expert's weight stream over more workgroups; otherwise the grouped 256 x 128 tiles.
+// Few routes per expert (at most 8 on average) stream each expert's weights through the
+// grouped split kernel in 16-route tiles; more take the grouped 256 x 128 tiles, which
+// stream an expert's weights once for up to 256 routes.  Measured at the Qwen3-30B-A3B
+// shape (128 experts, top-8): 128 tokens 267 us on 16-route tiles; 256 tokens 388 us on
+// 16-route tiles (experts past 16 routes stream their weights twice) against about 340 us
+// on the grouped tiles.
 MoeTile choose_moe_tile(int64_t routes, int64_t experts) {
-  return routes <= 16 * experts ? MoeTile::Small : MoeTile::Large;
+  return routes <= 8 * experts ? MoeTile::Small : MoeTile::Large;
 }
 
 KernelLaunch make_router_topk(const RouterTopkArgs &args) {
@@ -615,17 +455,6 @@ KernelLaunch make_finalize_routing(const FinalizeRoutingArgs &args) {
 
 KernelLaunch make_moe_sort(const MoeSortArgs &args) {
   return launch_of(reinterpret_cast<const void *>(&moe_sort_kernel), dim3(1), 1024, args);
-}
-
-KernelLaunch make_moe_gemm(const MoeGemmArgs &args, MoeTile tile, bool gated, int max_tiles) {
-  if (tile == MoeTile::Small) {
-    const void *kernel = gated ? reinterpret_cast<const void *>(&moe_gemm_kernel<32, 64, 1, 2, true>)
-                               : reinterpret_cast<const void *>(&moe_gemm_kernel<32, 64, 1, 2, false>);
-    return launch_of(kernel, dim3(blocks_for(args.n, 64), static_cast<unsigned>(max_tiles)), 128, args);
-  }
-  const void *kernel = gated ? reinterpret_cast<const void *>(&moe_gemm_kernel<128, 128, 2, 2, true>)
-                             : reinterpret_cast<const void *>(&moe_gemm_kernel<128, 128, 2, 2, false>);
-  return launch_of(kernel, dim3(blocks_for(args.n, 128), static_cast<unsigned>(max_tiles)), 256, args);
 }
 
 KernelLaunch make_moe_combine(const MoeCombineArgs &args) {

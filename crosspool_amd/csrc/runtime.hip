@@ -311,13 +311,21 @@ struct MoeWorkspace {
   int max_tiles;
 };
 
+// Entries of an expert tile table of `tile_rows`-route tiles: every expert with c >= 1
+// routes takes ceil(c / tile_rows) <= c / tile_rows + 1 tiles, so the table needs at most
+// ceil(routes / tile_rows) + min(experts, routes) entries; rounded up to a multiple of 8 for
+// the grouped tile kernel's XCD mapping.  Grid rows past the table's live entries exit at
+// once, so a tight bound keeps decode grids small.
+int moe_tile_bound(int64_t routes, int64_t experts, int64_t tile_rows) {
+  const int64_t live_experts = experts < routes ? experts : routes;
+  return static_cast<int>(((routes + tile_rows - 1) / tile_rows + live_experts + 7) / 8 * 8);
+}
+
 MoeWorkspace moe_workspace(int64_t rows, int64_t hidden, int64_t intermediate, int64_t experts, int64_t topk) {
   MoeWorkspace layout{};
   const int64_t routes = rows * topk;
-  const int64_t small_rows = moe_tile_rows(MoeTile::Small);
-  // Tile table entries: a bound on the tiles of either tile size, rounded up to a multiple
-  // of 8 for the grouped tile kernel's XCD mapping.
-  layout.max_tiles = static_cast<int>(((routes + small_rows - 1) / small_rows + experts + 7) / 8 * 8);
+  // Tile table entries: the bound for the smaller tile size covers both.
+  layout.max_tiles = moe_tile_bound(routes, experts, moe_tile_rows(MoeTile::Small));
   size_t cursor = 0;
   auto region = [&](size_t bytes) {
     const size_t offset = cursor;
@@ -1312,9 +1320,9 @@ int xp_moe_experts(const void *hidden_states, int64_t rows, int64_t hidden, int6
   const int64_t routes = rows * topk;
   const MoeTile tile = choose_moe_tile(routes, experts);
   const int tile_rows = moe_tile_rows(tile);
-  const int64_t tiles = ((routes + tile_rows - 1) / tile_rows + experts + 7) / 8 * 8;
-  XP_REQUIRE(tiles <= 65535, "too many expert tiles for one call");
-  const int max_tiles = static_cast<int>(tiles);
+  const int max_tiles = moe_tile_bound(routes, experts, tile_rows);
+  XP_REQUIRE(max_tiles <= 65535, "too many expert tiles for one call");
+  XP_REQUIRE(2 * intermediate * hidden * 2 < (int64_t{1} << 31), "an expert's weights must stay below 2 GiB");
   const hipStream_t hip_stream = static_cast<hipStream_t>(stream);
 
   MoeSortArgs sort{};
@@ -1331,68 +1339,57 @@ int xp_moe_experts(const void *hidden_states, int64_t rows, int64_t hidden, int6
   sort.max_tiles = max_tiles;
   XP_HIP_CHECK(launch(make_moe_sort(sort), hip_stream));
 
+  // gate_up gathers the token row of each sorted route (route / topk) itself and writes the
+  // activated rows in sorted order; down scales each sorted row by its route weight and
+  // writes it to the route's row.
+  GemmArgs up{};
+  up.x = static_cast<const uint16_t *>(hidden_states);
+  up.gather_slots = sorted_route;
+  up.gather_divisor = topk;
+  up.pool_rows = rows;
+  up.w = static_cast<const uint16_t *>(w_gate_up);
+  up.out = activated;
+  up.ldx = hidden;
+  up.ldo = intermediate;
+  up.rows = routes;
+  up.capacity = routes;
+  up.out_rows = routes;
+  up.n = 2 * intermediate;
+  up.k = hidden;
+  up.act = GatedSilu{alpha, limit, up_offset};
+  up.tile_expert = tile_expert;
+  up.tile_row0 = tile_row0;
+  up.expert_end = expert_end;
+
+  GemmArgs dn = up;
+  dn.x = activated;
+  dn.gather_slots = nullptr;
+  dn.w = static_cast<const uint16_t *>(w_down);
+  dn.out = route_out;
+  dn.scatter_slots = sorted_route;
+  dn.row_scale = sorted_weight;
+  dn.ldx = intermediate;
+  dn.ldo = hidden;
+  dn.n = hidden;
+  dn.k = intermediate;
+  dn.act = default_activation();
+
   if (tile == MoeTile::Large) {
-    // Many routes per expert: the Dense tile kernel in its grouped mode; gate_up gathers the
-    // token row of each sorted route (route / topk) itself.
+    // Many routes per expert: the Dense tile kernel in its grouped mode.
     if (moe_tile_rows(MoeTile::Large) != grouped_tile_rows()) {
       return fail(XP_ERROR_STATE, "expert tile table and grouped tile kernel disagree on the tile rows");
     }
-    GemmArgs up{};
-    up.x = static_cast<const uint16_t *>(hidden_states);
-    up.gather_slots = sorted_route;
-    up.gather_divisor = topk;
-    up.pool_rows = rows;
-    up.w = static_cast<const uint16_t *>(w_gate_up);
-    up.out = activated;
-    up.ldx = hidden;
-    up.ldo = intermediate;
-    up.rows = routes;
-    up.capacity = routes;
-    up.out_rows = routes;
-    up.n = 2 * intermediate;
-    up.k = hidden;
-    up.act = GatedSilu{alpha, limit, up_offset};
-    up.tile_expert = tile_expert;
-    up.tile_row0 = tile_row0;
-    up.expert_end = expert_end;
     XP_HIP_CHECK(launch(make_grouped_gemm(up, true, max_tiles), hip_stream));
-
-    GemmArgs dn = up;
-    dn.x = activated;
-    dn.gather_slots = nullptr;
-    dn.w = static_cast<const uint16_t *>(w_down);
-    dn.out = route_out;
-    dn.scatter_slots = sorted_route;
-    dn.row_scale = sorted_weight;
-    dn.ldx = intermediate;
-    dn.ldo = hidden;
-    dn.n = hidden;
-    dn.k = intermediate;
-    dn.act = default_activation();
     XP_HIP_CHECK(launch(make_grouped_gemm(dn, false, max_tiles), hip_stream));
   } else {
-    MoeGemmArgs gate_up{};
-    gate_up.x = static_cast<const uint16_t *>(hidden_states);
-    gate_up.w = static_cast<const uint16_t *>(w_gate_up);
-    gate_up.out = activated;
-    gate_up.tile_expert = tile_expert;
-    gate_up.tile_row0 = tile_row0;
-    gate_up.expert_end = expert_end;
-    gate_up.sorted_route = sorted_route;
-    gate_up.n = 2 * intermediate;
-    gate_up.k = hidden;
-    gate_up.topk = topk;
-    gate_up.act = GatedSilu{alpha, limit, up_offset};
-    XP_HIP_CHECK(launch(make_moe_gemm(gate_up, tile, true, max_tiles), hip_stream));
-
-    MoeGemmArgs down = gate_up;
-    down.x = activated;
-    down.w = static_cast<const uint16_t *>(w_down);
-    down.out = route_out;
-    down.gammas = topk_weights;
-    down.n = hidden;
-    down.k = intermediate;
-    XP_HIP_CHECK(launch(make_moe_gemm(down, tile, false, max_tiles), hip_stream));
+    // Few routes per expert: each touched expert's weights streamed by the grouped split
+    // kernel; about one tile per touched expert.
+    if (moe_tile_rows(MoeTile::Small) != grouped_split_rows()) {
+      return fail(XP_ERROR_STATE, "expert tile table and grouped split kernel disagree on the tile rows");
+    }
+    const int64_t live_tiles = experts < routes ? experts : routes;
+    XP_HIP_CHECK(launch(make_grouped_split(up, true, max_tiles, live_tiles), hip_stream));
+    XP_HIP_CHECK(launch(make_grouped_split(dn, false, max_tiles, live_tiles), hip_stream));
   }
 
   MoeCombineArgs combine{};

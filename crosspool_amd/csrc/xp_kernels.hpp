@@ -215,24 +215,6 @@ struct MoeSortArgs {
   int32_t max_tiles;
 };
 
-// Grouped projection over the sorted routes of one expert tile: gate_up gathers token rows
-// (row = route / topk of x) and writes bf16(act) at the sorted positions; down reads the
-// sorted activated rows and writes bf16(acc * gamma[route]) to the route's row.
-struct MoeGemmArgs {
-  const uint16_t *x;
-  const uint16_t *w;          // [experts, n, k]
-  uint16_t *out;
-  const int32_t *tile_expert;
-  const int32_t *tile_row0;
-  const int32_t *expert_end;
-  const int32_t *sorted_route;
-  const float *gammas;        // down: [routes] route weights
-  int64_t n;
-  int64_t k;
-  int64_t topk;
-  GatedSilu act;
-};
-
 struct MoeCombineArgs {
   const uint16_t *routes;    // [rows * topk, hidden] route outputs
   const int32_t *ids;        // [rows, topk]
@@ -244,7 +226,9 @@ struct MoeCombineArgs {
   float scale;               // routed scaling factor
 };
 
-enum class MoeTile : int { Small = 0, Large = 1 };  // 32 x 64 / 128 x 128 expert tiles
+// Expert tiles of the grouped projections: Small (16 sorted positions, grouped split
+// kernel) for few routes per expert, Large (grouped tile kernel) otherwise.
+enum class MoeTile : int { Small = 0, Large = 1 };
 int moe_tile_rows(MoeTile tile);
 MoeTile choose_moe_tile(int64_t routes, int64_t experts);
 
@@ -252,7 +236,6 @@ KernelLaunch make_router_topk(const RouterTopkArgs &args);
 KernelLaunch make_router_logits(const RouterLogitsArgs &args);
 KernelLaunch make_finalize_routing(const FinalizeRoutingArgs &args);
 KernelLaunch make_moe_sort(const MoeSortArgs &args);
-KernelLaunch make_moe_gemm(const MoeGemmArgs &args, MoeTile tile, bool gated, int max_tiles);
 KernelLaunch make_moe_combine(const MoeCombineArgs &args);
 
 // `capacity` sizes the grid (graph templates keep one grid per capacity);
@@ -292,9 +275,10 @@ struct GemmArgs {
   uint32_t *fault;
   int64_t pool_rows;
   float eps;
-  // Grouped projection (MoE experts, tile kernel only, no K split): grid row y is entry y
-  // of an expert tile table over rows sorted by expert; the tile multiplies rows
-  // [tile_row0[y], min(tile_row0[y] + BM, expert_end[e])) by the weights w + e n k of its
+  // Grouped projection (MoE experts: the tile kernel without a K split, or the grouped
+  // split kernel): grid row y is entry y of an expert tile table over rows sorted by
+  // expert; the tile multiplies rows [tile_row0[y], min(tile_row0[y] + BM,
+  // expert_end[e])) by the weights w + e n k of its
   // expert e = tile_expert[y] (-1: no tile).  With gather_slots set, tile row t reads row
   // gather_slots[t] / gather_divisor of x ([pool_rows, ldx]).  With row_scale set (together
   // with scatter_slots), output row t's fp32 result is multiplied by row_scale[t] before
@@ -337,6 +321,11 @@ GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmCho
 // table must be built for that BM).
 KernelLaunch make_grouped_gemm(const GemmArgs &args, bool gated, int max_tiles);
 int grouped_tile_rows();
+// The grouped projection for few routes per expert, on the grouped split kernel: tiles of
+// grouped_split_rows() sorted positions, `live_tiles` the expected number of table entries
+// in use (it sizes the K split).
+KernelLaunch make_grouped_split(const GemmArgs &args, bool gated, int max_tiles, int64_t live_tiles);
+int grouped_split_rows();
 std::string gemm_name(GemmChoice choice, bool gated);
 
 }  // namespace xp
