@@ -81,8 +81,13 @@ __global__ __launch_bounds__(64 * kSplitWaves) void split_gemm_kernel(GemmArgs a
 
   if (rb < row_blocks) {
     const int k0 = part * static_cast<int>(a.k_slice);
-    const int chunks = static_cast<int>(a.k_slice / 128);  // a multiple of DEPTH
-    // Columns at or past K in the last range read the next row (or past the end): zero
+    // 128-wide chunks of this range (k_slice is a multiple of 128; the last range may be
+    // shorter), rounded up to whole groups of DEPTH: the chunks past the range load
+    // through an out-of-range offset, which reads zeros without a memory access.
+    const int k_range = static_cast<int>(a.k - k0 < a.k_slice ? a.k - k0 : a.k_slice);
+    const int chunks = (k_range + 127) / 128;  // >= 1: the host makes no empty range
+    const int padded = (chunks + DEPTH - 1) / DEPTH * DEPTH;
+    // Columns at or past K in the last chunk read the next row (or past the end): zero
     // both operands there.
     const int lane_valid = static_cast<int>(a.k) - k0 - kq * 8;
     // Row blocks start at different chunks of their range (stride-7 rotation), spreading
@@ -104,18 +109,19 @@ __global__ __launch_bounds__(64 * kSplitWaves) void split_gemm_kernel(GemmArgs a
     u32x4 wbuf[DEPTH][4];
     u32x4 xbuf[DEPTH][TB][4];
     auto load_chunk = [&](int chunk, u32x4 (&w)[4], u32x4 (&x)[TB][4]) {
+      const bool in_range = chunk < chunks;
       const uint32_t column = static_cast<uint32_t>(column_of(chunk)) * 2;
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        w[s] = buffer_load16(w_rsrc, w_off + column + s * 64);
+        w[s] = buffer_load16(w_rsrc, in_range ? w_off + column + s * 64 : kOutOfRange);
 #pragma unroll
         for (int tb = 0; tb < TB; ++tb) {
-          x[tb][s] = buffer_load16(x_rsrc, x_off[tb] + column + s * 64);
+          x[tb][s] = buffer_load16(x_rsrc, in_range ? x_off[tb] + column + s * 64 : kOutOfRange);
         }
       }
     };
     auto compute_chunk = [&](int chunk, const u32x4 (&w)[4], const u32x4 (&x)[TB][4]) {
-      const int column = column_of(chunk);
+      const int column = chunk < chunks ? column_of(chunk) : 0;
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         const bool valid = column + s * 32 < lane_valid;
@@ -135,7 +141,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) void split_gemm_kernel(GemmArgs a
       load_chunk(d, wbuf[d], xbuf[d]);
     }
     int c0 = 0;
-    for (; c0 < chunks - DEPTH; c0 += DEPTH) {
+    for (; c0 < padded - DEPTH; c0 += DEPTH) {
 #pragma unroll
       for (int d = 0; d < DEPTH; ++d) {
         compute_chunk(c0 + d, wbuf[d], xbuf[d]);
@@ -1326,9 +1332,11 @@ double decode_stream_us(int64_t n, int64_t k, int64_t workgroups, double workgro
 }
 
 // Candidate K splits of the split kernel (1, 2, 4 or 8 ranges per 16-row block, each range
-// a whole number of load groups and none empty) and their modelled cost at `capacity` rows.
+// a whole number of 128-wide chunks and none empty) and their modelled cost at `capacity`
+// rows.  (With ranges of whole load groups only, Qwen3-0.6B down, K = 3072, could not be
+// split more than twice: 16 workgroups, 15.8 us at one row.)
 GemmChoice choose_split(int64_t capacity, int64_t n, int64_t k, double &cost) {
-  const int64_t quantum = 128 * kSplitDepth;
+  const int64_t quantum = 128;
   const int64_t row_blocks = (n + 15) / 16;
   GemmChoice best{GemmKind::Split, 0, 0, 1};
   cost = -1.0;
