@@ -195,8 +195,8 @@ def test_experts_qwen3_moe_shape(device, rows):
 
 @pytest.mark.parametrize("rows", (96, 1024))
 def test_experts_large_tiles_with_dead_rows(device, rows):
-    # 128-row expert tiles (routes > 16 per expert on average), several tiles per expert,
-    # ragged tails, and a band of rows without routes.
+    # 256-row grouped tiles (more than 8 routes per expert on average), several tiles per
+    # expert at 1024 rows, ragged tails, and a band of rows without routes.
     hidden, intermediate, experts, topk = 256, 128, 8, 2
     w_gate_up, w_down = m.generate_moe_layer(hidden, intermediate, experts, 93, std=0.1)
     x = o.generate_hidden_states(rows, hidden, 94)
@@ -207,6 +207,28 @@ def test_experts_large_tiles_with_dead_rows(device, rows):
     _check_experts(got, x, w_gate_up, w_down, ids, weights, scale=2.5)
     assert_moe_stages(operator.intermediates(), x, w_gate_up, w_down, ids, weights, got, 2.5)
     assert got[rows // 3: rows // 3 + 5].abs().sum() == 0
+
+
+@pytest.mark.parametrize("hidden,intermediate", ((512, 192), (1000, 264)))
+def test_experts_decode_tiles_skewed_routing(device, hidden, intermediate):
+    # Few routes per expert on average (16-route tiles of the grouped split kernel), but
+    # slot 0 of every row goes to expert 3: that expert spans several tiles, the last one
+    # ragged, while the others hold one or two routes.  1000 / 264 make the K ranges end
+    # inside a 128-wide chunk.
+    rows, experts, topk = 60, 16, 2
+    w_gate_up, w_down = m.generate_moe_layer(hidden, intermediate, experts, 99, std=0.05)
+    x = o.generate_hidden_states(rows, hidden, 100)
+    ids, weights = m.generate_routes(rows, experts, topk, 101)
+    ids[:, 0] = 3
+    ids[:, 1] = torch.where(ids[:, 1] == 3, torch.full_like(ids[:, 1], 5), ids[:, 1])
+    assert rows * topk <= 8 * experts and int((ids == 3).sum()) > 3 * 16
+    got, operator, weights_gpu = _run_experts(device, x, w_gate_up, w_down, ids, weights, scale=1.25)
+    _check_experts(got, x, w_gate_up, w_down, ids, weights, scale=1.25)
+    assert_moe_stages(operator.intermediates(), x, w_gate_up, w_down, ids, weights, got, 1.25)
+    again = torch.empty((rows, hidden), dtype=torch.bfloat16, device=device)
+    operator.run_into(hidden_states=to_device(x, device), weights=weights_gpu, topk_ids=to_device(ids, device),
+                      topk_weights=to_device(weights, device), output=again)
+    assert_bitwise_equal(again.cpu(), got)
 
 
 def test_moe_layer_router_finalize_experts(device):
