@@ -1322,6 +1322,7 @@ constexpr double kSplitRowUs = 0.8;
 constexpr double kStreamReduceUs = 12.0;  // the reduction launch, fitted (it also ends the overlap of slices)
 constexpr double kStreamPartialBytesPerUs = 6.0e6;
 constexpr int kSplitDepth = 4;
+constexpr double kGatherUs = 4.0;  // a separate gather launch at decode sizes (measured 3.8-4.0 us)
 
 double decode_stream_us(int64_t n, int64_t k, int64_t workgroups, double workgroup_bytes_per_us) {
   const int64_t rounds = (workgroups + kComputeUnits - 1) / kComputeUnits;
@@ -1431,19 +1432,26 @@ GemmChoice choose_tile(int64_t capacity, int64_t n, int64_t k) {
 
 }  // namespace
 
+// The split or the stream kernel for a decode size, whichever the cost model prefers, and
+// its modelled cost in microseconds.
+GemmChoice choose_decode(int64_t capacity, int64_t n, int64_t k, double &cost) {
+  const GemmChoice stream = choose_stream(capacity, n, k, cost);
+  if (capacity <= kSplitMaxRows) {
+    double split_us = 0.0;
+    const GemmChoice split = choose_split(capacity, n, k, split_us);
+    if (split_us < cost) {
+      cost = split_us;
+      return split;
+    }
+  }
+  return stream;
+}
+
 GemmChoice choose_gemm(int64_t capacity, int64_t n, int64_t k, bool gated) {
   // The split and stream kernels address the weights through one 32-bit buffer range.
   if (capacity <= kDecodeMaxRows && n * k * 2 <= INT32_MAX) {
-    double stream_us = 0.0;
-    const GemmChoice stream = choose_stream(capacity, n, k, stream_us);
-    if (capacity <= kSplitMaxRows) {
-      double split_us = 0.0;
-      const GemmChoice split = choose_split(capacity, n, k, split_us);
-      if (split_us < stream_us) {
-        return split;
-      }
-    }
-    return stream;
+    double cost = 0.0;
+    return choose_decode(capacity, n, k, cost);
   }
   return choose_tile(capacity, n, k);
 }
@@ -1456,13 +1464,31 @@ GemmChoice choose_dense_gate_up(int64_t capacity, int64_t n, int64_t k, bool &fu
   if (!fused) {
     return choose_gemm(capacity, n, k, true);
   }
+  GemmChoice fused_choice{GemmKind::Stream, 0, 0, 1};
   for (int64_t slices = 1;; ++slices) {
     const int64_t k_slice = ((k + slices - 1) / slices + kStreamSliceQuantum - 1) / kStreamSliceQuantum *
                             kStreamSliceQuantum;
     if (16 * (k_slice + 8) * 2 <= kStreamLdsBytes) {
-      return {GemmKind::Stream, 0, k_slice, 1};
+      fused_choice.k_slice = k_slice;
+      break;
     }
   }
+  // The fused launch streams the weights with one workgroup per 8 weight-row blocks (and K
+  // slice); a separate gather launch lets the split kernel spread a small projection over
+  // more workgroups (Qwen3-0.6B gate_up at one row: 48 fused workgroups, 13.6 us).
+  const int64_t groups = ((n + 15) / 16 + kStreamWaves - 1) / kStreamWaves;
+  const int64_t slices = stream_slices(k, fused_choice.k_slice);
+  double fused_us = decode_stream_us(n, k, slices * groups, kStreamWorkgroupBytesPerUs);
+  if (slices > 1) {
+    fused_us += kStreamReduceUs + 8.0 * static_cast<double>(slices * capacity * n) / kStreamPartialBytesPerUs;
+  }
+  double separate_us = 0.0;
+  const GemmChoice separate = choose_decode(capacity, n, k, separate_us);
+  if (kGatherUs + separate_us < fused_us) {
+    fused = false;
+    return separate;
+  }
+  return fused_choice;
 }
 
 // K ranges whose fp32 partial sums go through scratch and the reduction kernel.

@@ -191,10 +191,11 @@ def test_gemm_variant_selection():
             assert _native.gemm_variant(rows, n, k, gated).startswith(("split", "stream"))
     assert _native.gemm_variant(1, 4096, 12288, False) == "split_t16_k8"
     assert _native.gemm_variant(16, 24576, 4096, True) == "stream_gated_t16"
-    # Qwen3-4B down: the split kernel would leave 80 workgroups for 256 CUs; the stream
-    # kernel slices K instead
-    assert _native.gemm_variant(1, 2560, 9728, False) == "stream_t16"
-    assert _native.gemm_workspace_bytes(1, 2560, 9728, False) > 0
+    # Qwen3-4B and Qwen3-0.6B down: K ranges of whole 128-wide chunks let the split kernel
+    # take 8 ranges (160 and 64 workgroups), with no scratch
+    assert _native.gemm_variant(1, 2560, 9728, False) == "split_t16_k8"
+    assert _native.gemm_variant(1, 1024, 3072, False) == "split_t16_k8"
+    assert _native.gemm_workspace_bytes(1, 2560, 9728, False) == 0
     assert _native.gemm_variant(17, 24576, 4096, True).startswith("tile_gated_64x128")
     assert _native.gemm_variant(64, 4096, 12288, False).startswith("tile_64x128_k")
     assert _native.gemm_workspace_bytes(1, 24576, 4096, True) == 0
