@@ -986,20 +986,17 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
   // Wave-uniform by construction; readfirstlane lets the compiler keep it (and the load
   // descriptors and LDS bases derived from it) in scalar registers.
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-  // A grouped 4 x 2 tile pairs each SIMD's two waves (w and w + 4) as one wave of the upper
-  // half of the rows and one of the lower half: an expert tile's rows end anywhere, and a
-  // wave whose rows are all past the end skips its fragment reads and MFMAs, which leaves
-  // the SIMD's matrix pipe to its partner (at Qwen3-30B-A3B's ~128 routes per expert, half
-  // of each 256-row tile).
-  constexpr bool PAIRED = GROUPED && WAVES_M == 4 && WAVES_N == 2;
-  const int wm = PAIRED ? ((wave & 3) >> 1) + 2 * (wave >> 2) : wave % WAVES_M;
-  const int wn = PAIRED ? wave & 1 : wave / WAVES_M;
-  // 32-row MFMA blocks of this wave that hold live rows (all of them outside grouped tiles).
-  int live_mt = MT;
-  if constexpr (GROUPED) {
-    const int64_t left = row_end - (m0 + wm * WTM);
-    live_mt = __builtin_amdgcn_readfirstlane(left <= 0 ? 0 : left >= MT * 32 ? MT : static_cast<int>((left + 31) / 32));
-  }
+  // A grouped 8-wave tile pairs each SIMD's two waves (w and w + 4) as one wave of the
+  // upper half of the rows and one of the lower half: an expert tile's rows end anywhere,
+  // and a wave whose rows are all past the end skips its fragment reads and MFMAs, which
+  // leaves the SIMD's matrix pipe to its partner (at Qwen3-30B-A3B's ~128 routes per
+  // expert, half of each 256-row tile).
+  constexpr bool PAIRED = GROUPED && WAVES == 8 && WAVES_M % 2 == 0;
+  constexpr int HALF_M = WAVES_M / 2;  // row bands per half
+  const int wm = PAIRED ? (wave & 3) / WAVES_N + HALF_M * (wave >> 2) : wave % WAVES_M;
+  const int wn = PAIRED ? (wave & 3) % WAVES_N : wave / WAVES_M;
+  // Whether this wave's row band holds a live row (always outside grouped tiles).
+  const bool wave_live = !GROUPED || __builtin_amdgcn_readfirstlane(static_cast<int>(m0 + wm * WTM < row_end)) != 0;
 
   // ---- loads: loading wave w fills A_LOADS 8-row groups of the A tile (rows from
   // w * BM / LOAD_WAVES) and B_LOADS of the B tile, so which resource a load uses is a
@@ -1139,33 +1136,34 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
   static_assert(KSTEPS == 4, "the slab schedule below is written for four k steps");
   bf16x8 af[3][MT];
   bf16x8 bfrag[3][NT];
+  // A grouped tile's wave whose rows all lie past the expert's last route reads no
+  // fragments and issues no MFMAs (one wave-uniform branch around the unrolled loops).
   auto read_fragments = [&](int stage, int ks, int slot) {
+    if (!wave_live) {
+      return;
+    }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      if (!GROUPED || mt < live_mt) {
-        const int offset = stage * BM * BK * 2 + mt * 32 * BK * 2;
-        af[slot][mt] = as_bf16x8(
-            *reinterpret_cast<const u32x4 *>(lds_bytes + a_base[offset >> 16][ks] + (offset & 0xffff)));
-      }
+      const int offset = stage * BM * BK * 2 + mt * 32 * BK * 2;
+      af[slot][mt] = as_bf16x8(
+          *reinterpret_cast<const u32x4 *>(lds_bytes + a_base[offset >> 16][ks] + (offset & 0xffff)));
     }
-    if (!GROUPED || live_mt > 0) {
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        const int offset = B_REGION * 2 + stage * BN * BK * 2 + nt * 32 * BK * 2;
-        bfrag[slot][nt] = as_bf16x8(
-            *reinterpret_cast<const u32x4 *>(lds_bytes + b_base[offset >> 16][ks] + (offset & 0xffff)));
-      }
+    for (int nt = 0; nt < NT; ++nt) {
+      const int offset = B_REGION * 2 + stage * BN * BK * 2 + nt * 32 * BK * 2;
+      bfrag[slot][nt] = as_bf16x8(
+          *reinterpret_cast<const u32x4 *>(lds_bytes + b_base[offset >> 16][ks] + (offset & 0xffff)));
     }
   };
   auto mfma_step = [&](int slot) {
+    if (!wave_live) {
+      return;
+    }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      if (!GROUPED || mt < live_mt) {
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-          acc[mt][nt] =
-              __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[slot][mt], bfrag[slot][nt], acc[mt][nt], 0, 0, 0);
-        }
+      for (int nt = 0; nt < NT; ++nt) {
+        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[slot][mt], bfrag[slot][nt], acc[mt][nt], 0, 0, 0);
       }
     }
   };
