@@ -1335,7 +1335,12 @@ constexpr double kSplitWorkgroupBytesPerUs = 27.0e3;
 constexpr double kStreamWorkgroupBytesPerUs = 28.0e3;
 constexpr double kDecodeBytesPerUs = 5.4e6;
 constexpr double kDecodeFixedUs = 2.0;
-constexpr double kSplitRowUs = 0.8;
+// Token fragments per row past the first: 0.8 us at the 12 chunks per range of Qwen3-8B
+// down (fitted), scaled by the chunks a wave issues, padding included (Qwen3-0.6B gate_up at
+// 8 rows, 2 chunks per range padded to 4: a separate gather plus the split kernel, 20.0 us
+// per layer, against 22.5 us with the gather fused into the stream kernel; 8 ranges of one
+// chunk, each padded to 4, took 23.6 us).
+constexpr double kSplitRowUsPerChunk = 0.8 / 12.0;
 constexpr double kStreamReduceUs = 12.0;  // the reduction launch, fitted (it also ends the overlap of slices)
 constexpr double kStreamPartialBytesPerUs = 6.0e6;
 constexpr int kSplitDepth = 4;
@@ -1365,7 +1370,9 @@ GemmChoice choose_split(int64_t capacity, int64_t n, int64_t k, double &cost) {
     }
     const int64_t workgroups = (row_blocks * ksplit + kSplitWaves - 1) / kSplitWaves;
     const double us =
-        decode_stream_us(n, k, workgroups, kSplitWorkgroupBytesPerUs) + kSplitRowUs * static_cast<double>(capacity - 1);
+        decode_stream_us(n, k, workgroups, kSplitWorkgroupBytesPerUs) +
+        kSplitRowUsPerChunk * static_cast<double>((slice / 128 + kSplitDepth - 1) / kSplitDepth * kSplitDepth) *
+            static_cast<double>(capacity - 1);
     if (cost < 0.0 || us < cost) {
       best = {GemmKind::Split, 0, slice, ksplit};
       cost = us;
