@@ -1297,6 +1297,11 @@ int xp_moe_experts(const void *hidden_states, int64_t rows, int64_t hidden, int6
   XP_REQUIRE(experts >= 1 && experts <= kMoeMaxExperts, "Experts support 1 to 1024 experts");
   XP_REQUIRE(topk >= 1 && topk <= experts, "topk must be between 1 and the expert count");
   XP_REQUIRE(rows * topk <= (int64_t{1} << 30), "too many routes for one call");
+  // The projections address the token rows, the activated routes and one expert's weights
+  // through 32-bit buffer ranges.
+  XP_REQUIRE(rows * hidden * 2 < (int64_t{1} << 31) && rows * topk * intermediate * 2 < (int64_t{1} << 31) &&
+                 2 * intermediate * hidden * 2 < (int64_t{1} << 31),
+             "Experts tensors must stay below 2 GiB per buffer range");
   XP_REQUIRE(alpha > 0.0f, "SiLU alpha must be positive");
   if (rows == 0) {
     return XP_OK;
@@ -1322,7 +1327,6 @@ int xp_moe_experts(const void *hidden_states, int64_t rows, int64_t hidden, int6
   const int tile_rows = moe_tile_rows(tile);
   const int max_tiles = moe_tile_bound(routes, experts, tile_rows);
   XP_REQUIRE(max_tiles <= 65535, "too many expert tiles for one call");
-  XP_REQUIRE(2 * intermediate * hidden * 2 < (int64_t{1} << 31), "an expert's weights must stay below 2 GiB");
   const hipStream_t hip_stream = static_cast<hipStream_t>(stream);
 
   MoeSortArgs sort{};
