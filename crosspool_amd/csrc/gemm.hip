@@ -1052,7 +1052,9 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
   };
   // Slab kt of this workgroup's K range.  Slabs at or past the range end (the prologue of
   // a short range, the refills after the last slab) load zeros without memory traffic.
-  auto issue_loads = [&](int64_t kt, int stage) {
+  // PART selects the A loads (1), the B loads (2) or both (3).
+  auto issue_part = [&](int64_t kt, int stage, auto part) {
+    constexpr int PART = decltype(part)::value;
     const int64_t k_pos = k_begin + kt * BK;
     const uint32_t k_bytes = static_cast<uint32_t>(k_pos * 2);
     // 16-byte chunks of this slab that lie inside the range (8 except in a ragged last slab).
@@ -1063,7 +1065,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
     // (kOutOfRange + k_bytes is still past the resource end), as a select, not a branch.
     // A and B loads are separate loops so that each names one resource.
 #pragma unroll
-    for (int q = 0; q < A_LOADS; ++q) {
+    for (int q = 0; q < ((PART & 1) ? A_LOADS : 0); ++q) {
       const int g = a_first + q * 8;
       const int chunk = lane_chunk[(g >> 3) & 1];
       uint32_t offset;
@@ -1075,7 +1077,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
       buffer_load_lds16(a_rsrc, a_stage + g * BK, chunk < chunks_left ? offset : kOutOfRange, k_bytes);
     }
 #pragma unroll
-    for (int q = 0; q < B_LOADS; ++q) {
+    for (int q = 0; q < ((PART & 2) ? B_LOADS : 0); ++q) {
       const int g = b_first + q * 8;
       const int chunk = lane_chunk[(g >> 3) & 1];
       const int weight_row = b_group_row(g - BM) + B_ROW_STEP * row_in_load;
@@ -1083,6 +1085,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
       buffer_load_lds16(b_rsrc, b_stage + g * BK, chunk < chunks_left ? offset : kOutOfRange, k_bytes);
     }
   };
+  auto issue_loads = [&](int64_t kt, int stage) { issue_part(kt, stage, std::integral_constant<int, 3>{}); };
 
   f32x16 acc[MT][NT];
 #pragma unroll
@@ -1221,9 +1224,15 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
     read_fragments(S, 3, P);
     mfma_step((P + 1) % 3);
     stage_barrier();
+    // With three or more stages the A refill goes out under k step 2's MFMAs and the B
+    // refill under k step 3's (one load per MFMA: Qwen3-8B down at 2048 rows on 256 x 128
+    // tiles, 176 -> 169 us); the two-stage 256 x 256 tile issues both under k step 2
+    // (spread, it was 1 % slower).
+    constexpr bool SPREAD = STAGES >= 3;
+    constexpr int FIRST_LOADS = SPREAD ? A_LOADS : LOADS;
     read_fragments(NEXT, 0, (P + 1) % 3);
     if constexpr (LOADING) {
-      issue_loads(kt + STAGES, S);
+      issue_part(kt + STAGES, S, std::integral_constant<int, SPREAD ? 1 : 3>{});
     }
     mfma_step((P + 2) % 3);
 #pragma unroll
@@ -1231,12 +1240,25 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
       if constexpr (LOADING) {
-        __builtin_amdgcn_sched_group_barrier(0x020, (LOADS + MT * NT - 1) / (MT * NT), 0);  // memory loads
+        __builtin_amdgcn_sched_group_barrier(0x020, (FIRST_LOADS + MT * NT - 1) / (MT * NT), 0);  // memory loads
       }
     }
     __builtin_amdgcn_sched_barrier(0);
     read_fragments(NEXT, 1, (P + 2) % 3);
+    if constexpr (LOADING && SPREAD) {
+      issue_part(kt + STAGES, S, std::integral_constant<int, 2>{});
+    }
     mfma_step(P);
+    if constexpr (SPREAD) {
+#pragma unroll
+      for (int i = 0; i < MT * NT; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        if constexpr (LOADING) {
+          __builtin_amdgcn_sched_group_barrier(0x020, (B_LOADS + MT * NT - 1) / (MT * NT), 0);
+        }
+      }
+    }
     __builtin_amdgcn_sched_barrier(0);
   };
   int64_t kt = 0;
