@@ -42,6 +42,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "xp_gemm_down": (_INT, [_P, _I64, _I64, _P, _I64, _P, _P, _I64, _P, _SIZE, _P]),
     "xp_gemm_workspace_bytes": (_SIZE, [_I64, _I64, _I64, _INT]),
     "xp_dense_workspace_bytes": (_SIZE, [_I64, _I64, _I64]),
+    "xp_dense_workspace_layout": (_INT, [_I64, _I64, _I64, ctypes.POINTER(_SIZE)]),
     "xp_dense_step": (_INT, [_P, _P, _I64, _P, _I64, _I64, _I64, _P, _P, _P, _F32, _P, _SIZE, _P, _P]),
     "xp_gemm_variant": (_SIZE, [_I64, _I64, _I64, _INT, ctypes.c_char_p, _SIZE]),
     "xp_agent_create": (_INT, [_INT, ctypes.POINTER(_P)]),
@@ -154,3 +155,11 @@ def gemm_workspace_bytes(rows: int, n: int, k: int, gated: bool) -> int:
 
 def dense_workspace_bytes(capacity: int, hidden: int, intermediate: int) -> int:
     return int(library().xp_dense_workspace_bytes(capacity, hidden, intermediate))
+
+
+def dense_workspace_layout(capacity: int, hidden: int, intermediate: int) -> tuple[int, ...]:
+    """(batch, activated, gate_up partials, down partials, total) byte offsets of a Lane workspace."""
+
+    offsets = (_SIZE * 5)()
+    call("xp_dense_workspace_layout", capacity, hidden, intermediate, offsets)
+    return tuple(int(value) for value in offsets)

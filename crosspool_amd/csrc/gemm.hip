@@ -28,6 +28,7 @@
 
 #include "xp_kernels.hpp"
 
+#include <mutex>
 #include <type_traits>
 #include <utility>
 
@@ -1558,6 +1559,35 @@ size_t gemm_scratch_bytes(GemmChoice choice, int64_t capacity, int64_t n, int64_
   return (partial_bytes + 255) / 256 * 256;
 }
 
+hipError_t enable_large_lds(const void *func) {
+  // (function, device) pairs already opted in: a few stream kernels on a few devices, kept in
+  // a fixed table so that no launch path allocates.  Past its end the attribute is set again
+  // on every launch (harmless, only slower).
+  struct Enabled {
+    const void *func;
+    int device;
+  };
+  static std::mutex mutex;
+  static Enabled enabled[128];
+  static int count = 0;
+  int device = 0;
+  if (const hipError_t status = hipGetDevice(&device); status != hipSuccess) {
+    return status;
+  }
+  std::lock_guard<std::mutex> guard(mutex);
+  for (int index = 0; index < count; ++index) {
+    if (enabled[index].func == func && enabled[index].device == device) {
+      return hipSuccess;
+    }
+  }
+  const hipError_t status =
+      hipFuncSetAttribute(func, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kStreamLdsBytes));
+  if (status == hipSuccess && count < static_cast<int>(sizeof(enabled) / sizeof(enabled[0]))) {
+    enabled[count++] = Enabled{func, device};
+  }
+  return status;
+}
+
 GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmChoice choice) {
   GemmLaunch launches;
   KernelLaunch &kernel = launches.main;
@@ -1578,15 +1608,8 @@ GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmCho
     kernel.func = gather ? stream_kernel<true, true>() : (gated ? stream_kernel<true>() : stream_kernel<false>());
     kernel.grid = dim3(static_cast<unsigned>(slices * groups), 1, 1);
     kernel.block = dim3(64 * kStreamWaves, 1, 1);
+    // Dynamic LDS beyond 64 KB: launch() opts the function in (enable_large_lds).
     kernel.shmem = static_cast<unsigned>(16 * (choice.k_slice + 8) * 2);
-    // Dynamic LDS beyond 64 KB must be allowed per function (idempotent, set on first use).
-    static bool configured[3] = {};
-    const int function_index = gather ? 2 : (gated ? 1 : 0);
-    if (!configured[function_index]) {
-      (void)hipFuncSetAttribute(kernel.func, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                static_cast<int>(kStreamLdsBytes));
-      configured[function_index] = true;
-    }
   } else {
     const TileShape &shape = kTileShapes[choice.variant];
     kernel.func = gated ? tile_kernel<true>(choice.variant) : tile_kernel<false>(choice.variant);

@@ -90,10 +90,18 @@ DenseWorkspace dense_workspace(int64_t capacity, int64_t hidden, int64_t interme
   return layout;
 }
 
+// Buffer resources are 32-bit.  The split and stream kernels address a whole weight matrix
+// through one resource, so choose_gemm gives them only matrices below 2^31 bytes and takes
+// the tile kernel otherwise; the tile kernel's resources span one tile (at most 256 weight
+// or token rows of the reduction length), which the bound on the intermediate size keeps
+// below 2^30 bytes (hidden is bounded by the gather's 16384).
+constexpr int64_t kMaxIntermediate = int64_t{1} << 21;
+
 int validate_geometry(int64_t hidden, int64_t intermediate) {
   XP_REQUIRE(hidden > 0 && hidden % 8 == 0, "hidden size must be a positive multiple of 8");
   XP_REQUIRE(intermediate > 0 && intermediate % 8 == 0, "intermediate size must be a positive multiple of 8");
   XP_REQUIRE(gather_supported(hidden), "hidden size exceeds the gather kernel's register row (16384)");
+  XP_REQUIRE(intermediate <= kMaxIntermediate, "intermediate size exceeds 2^21 (32-bit tile buffer ranges)");
   return XP_OK;
 }
 
@@ -583,10 +591,29 @@ size_t xp_dense_workspace_bytes(int64_t capacity, int64_t hidden, int64_t interm
   return dense_workspace(capacity, hidden, intermediate).bytes;
 }
 
-int xp_dense_step(const void *pool_in, void *pool_out, int64_t pool_rows, const int32_t *slots, int64_t rows,
-                  int64_t hidden, int64_t intermediate, const void *w_gate_up, const void *w_down,
-                  const void *norm_weight, float eps, void *workspace, size_t workspace_bytes, uint32_t *fault_word,
-                  xp_stream_t stream) {
+int xp_dense_workspace_layout(int64_t capacity, int64_t hidden, int64_t intermediate, size_t *offsets) {
+  XP_REQUIRE(capacity > 0, "capacity must be positive");
+  if (const int status = validate_geometry(hidden, intermediate); status != XP_OK) {
+    return status;
+  }
+  XP_REQUIRE(offsets != nullptr, "offsets pointer must be non-null");
+  const DenseWorkspace layout = dense_workspace(capacity, hidden, intermediate);
+  const bool partials = layout.bytes > layout.activated_offset + static_cast<size_t>(capacity * intermediate) * 2;
+  offsets[0] = layout.batch_offset;
+  offsets[1] = layout.activated_offset;
+  offsets[2] = partials ? layout.gate_up_partials_offset : layout.bytes;
+  offsets[3] = partials ? layout.down_partials_offset : layout.bytes;
+  offsets[4] = layout.bytes;
+  return XP_OK;
+}
+
+namespace {
+
+// Checks and launches shared by xp_dense_step and xp_dense_step_static: the same kernels
+// on the same arguments, over a workspace the caller has already sized.
+int dense_step_checks(const void *pool_in, const void *pool_out, int64_t pool_rows, const int32_t *slots,
+                      int64_t rows, int64_t hidden, int64_t intermediate, const void *w_gate_up, const void *w_down,
+                      const void *norm_weight) {
   XP_REQUIRE(rows >= 0 && pool_rows >= 0, "row counts must be non-negative");
   if (rows == 0) {
     return XP_OK;
@@ -595,13 +622,17 @@ int xp_dense_step(const void *pool_in, void *pool_out, int64_t pool_rows, const 
     return status;
   }
   XP_REQUIRE(pool_in != nullptr && pool_out != nullptr && slots != nullptr && w_gate_up != nullptr &&
-                 w_down != nullptr && workspace != nullptr,
+                 w_down != nullptr,
              "dense step pointers must be non-null");
   XP_REQUIRE(aligned16(pool_in) && aligned16(pool_out) && aligned16(w_gate_up) && aligned16(w_down) &&
-                 aligned16(workspace) && (norm_weight == nullptr || aligned16(norm_weight)),
+                 (norm_weight == nullptr || aligned16(norm_weight)),
              "dense step operands must be 16-byte aligned");
-  XP_REQUIRE(workspace_bytes >= dense_workspace(rows, hidden, intermediate).bytes,
-             "workspace is smaller than xp_dense_workspace_bytes(rows, hidden, intermediate)");
+  return XP_OK;
+}
+
+int run_dense_step(const void *pool_in, void *pool_out, int64_t pool_rows, const int32_t *slots, int64_t rows,
+                   int64_t hidden, int64_t intermediate, const void *w_gate_up, const void *w_down,
+                   const void *norm_weight, float eps, void *workspace, uint32_t *fault_word, xp_stream_t stream) {
   DenseBinding binding{};
   binding.pool_in = static_cast<const uint16_t *>(pool_in);
   binding.pool_out = static_cast<uint16_t *>(pool_out);
@@ -623,6 +654,25 @@ int xp_dense_step(const void *pool_in, void *pool_out, int64_t pool_rows, const 
     XP_HIP_CHECK(launch(*chain[index], static_cast<hipStream_t>(stream)));
   }
   return XP_OK;
+}
+
+}  // namespace
+
+int xp_dense_step(const void *pool_in, void *pool_out, int64_t pool_rows, const int32_t *slots, int64_t rows,
+                  int64_t hidden, int64_t intermediate, const void *w_gate_up, const void *w_down,
+                  const void *norm_weight, float eps, void *workspace, size_t workspace_bytes, uint32_t *fault_word,
+                  xp_stream_t stream) {
+  if (const int status = dense_step_checks(pool_in, pool_out, pool_rows, slots, rows, hidden, intermediate, w_gate_up,
+                                           w_down, norm_weight);
+      status != XP_OK || rows == 0) {
+    return status;
+  }
+  XP_REQUIRE(workspace != nullptr, "dense step pointers must be non-null");
+  XP_REQUIRE(aligned16(workspace), "dense step operands must be 16-byte aligned");
+  XP_REQUIRE(workspace_bytes >= dense_workspace(rows, hidden, intermediate).bytes,
+             "workspace is smaller than xp_dense_workspace_bytes(rows, hidden, intermediate)");
+  return run_dense_step(pool_in, pool_out, pool_rows, slots, rows, hidden, intermediate, w_gate_up, w_down,
+                        norm_weight, eps, workspace, fault_word, stream);
 }
 
 size_t xp_gemm_variant(int64_t capacity, int64_t n, int64_t k, int gated, char *buffer, size_t size) {
@@ -816,6 +866,13 @@ int xp_template_capture(xp_lane_t lane, int64_t hidden, int64_t intermediate, in
   const KernelLaunch *chain[kMaxStepKernels];
   t->node_count = launches.chain(chain);
   for (int index = 0; index < t->node_count; ++index) {
+    if (chain[index]->shmem > 64 * 1024) {
+      const hipError_t enabled = enable_large_lds(chain[index]->func);
+      if (enabled != hipSuccess) {
+        destroy_template(*t);
+        return fail(XP_ERROR_HIP, std::string("enabling dynamic LDS above 64 KB failed: ") + hipGetErrorString(enabled));
+      }
+    }
     void *params[1];
     hipKernelNodeParams node = node_params(*chain[index], params);
     const hipGraphNode_t *dependencies = index == 0 ? nullptr : &t->nodes[index - 1];

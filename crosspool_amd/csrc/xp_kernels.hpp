@@ -33,9 +33,19 @@ struct KernelLaunch {
   bool empty() const { return func == nullptr || grid.x == 0; }
 };
 
+// Dynamic LDS above 64 KB must be allowed per function before a launch or a graph node
+// uses it.  Sets the maximum once per (function, current device) under a lock and returns
+// the runtime's status; a failed attempt is not remembered, so the next call retries.
+hipError_t enable_large_lds(const void *func);
+
 inline hipError_t launch(const KernelLaunch &kernel, hipStream_t stream) {
   if (kernel.empty()) {
     return hipSuccess;
+  }
+  if (kernel.shmem > 64 * 1024) {
+    if (const hipError_t status = enable_large_lds(kernel.func); status != hipSuccess) {
+      return status;
+    }
   }
   void *params[] = {const_cast<unsigned char *>(kernel.args)};
   return hipLaunchKernel(kernel.func, kernel.grid, kernel.block, params, kernel.shmem, stream);

@@ -135,6 +135,15 @@ size_t xp_gemm_workspace_bytes(int64_t rows, int64_t n, int64_t k, int gated);
  * WorkspaceLayout (src/xpool/runtime/ffnagent/operators/dense.py:24-52). */
 size_t xp_dense_workspace_bytes(int64_t capacity, int64_t hidden, int64_t intermediate);
 
+/* Byte offsets of that workspace's regions: [0] the gathered (normalised) batch
+ * [capacity, hidden] bf16, [1] the activated intermediate [capacity, intermediate] bf16,
+ * [2] gate_up's and [3] down's fp32 K-range partial sums (equal to [4] when the capacity
+ * splits no K), [4] the total.  A Dense step leaves the batch and the activated rows of its
+ * live rows there until the next step on the same workspace.  Replaces the region views of
+ * WorkspaceLayout.views (src/xpool/runtime/ffnagent/execution.py:60-70), which the
+ * reference's tests read directly. */
+int xp_dense_workspace_layout(int64_t capacity, int64_t hidden, int64_t intermediate, size_t *offsets);
+
 /* One eager mailbox step: gather(+RMSNorm) -> gate_up+SiLU -> down -> scatter to
  * pool_out rows slots[i] (pool_out may equal pool_in).  Same kernels as a replay.
  * Replaces Dense.run_into (operators/dense.py:70-86) plus the Transport copies. */

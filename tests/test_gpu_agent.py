@@ -235,7 +235,7 @@ def test_layers_share_templates_and_bind_their_own_weights(device):
     assert error.normalized_rmse <= o.FFN_OUTPUT_NORMALIZED_RMSE_LIMIT
 
 
-@pytest.mark.parametrize("rows", (1, 8))
+@pytest.mark.parametrize("rows", (1, 8, 32, 128, 256))
 def test_config2_qwen3_0_6b_28_layer_stack(device, rows):
     # 28 independent Qwen3-0.6B FFN layers replayed through the templates of
     # one capacity set, chained on the same mailbox slots of a 4096-slot pool; every layer's

@@ -149,6 +149,13 @@ def test_variant_selection_covers_every_family(device):
               for n, k, gated in ((24576, 4096, True), (4096, 12288, False))}
     assert {"tile_gated_64x128", "tile_gated_128x128", "tile_gated_256x128", "tile_gated_256x256", "tile_64x128_k8",
             "tile_128x128_k8", "tile_256x128_k4"} <= chosen
+    # The headline sizes of tests/test_gpu_headline.py (config 3 at 1024 / 2048 / 4096 rows,
+    # config 5 at 512 / 8192) reach the unsplit tiles and the split 256 x 256 down tile.
+    headline = {_native.gemm_variant(rows, n, k, gated) for (hidden, intermediate), sizes in
+                (((4096, 12288), (1024, 2048, 4096)), ((5120, 3200), (512, 8192))) for rows in sizes
+                for n, k, gated in ((2 * intermediate, hidden, True), (hidden, intermediate, False))}
+    assert {"tile_256x128", "tile_128x128", "tile_256x256", "tile_256x256_k4", "tile_gated_128x128",
+            "tile_gated_256x128", "tile_gated_256x256"} <= headline
 
 
 # Ragged geometries of the decode kernels: K not a multiple of their 512-column load

@@ -170,6 +170,43 @@ def test_moe_experts_rejects_buffer_ranges_past_2_gib():
     assert status == _native.XP_ERROR_INVALID_ARGUMENT
 
 
+def test_dense_projections_past_one_buffer_range_take_the_tile_kernel():
+    # The split and stream kernels address the whole weight matrix through one 32-bit buffer
+    # resource; a gate_up of 2 x 53248 x 16384 bf16 (3.5 GB, a TP-1 shard of a very wide model)
+    # or a 4 GiB down must go to the tile kernel, whose resources span one tile, at every
+    # decode size, and the Dense step's gate_up must not fuse the gather into a stream kernel.
+    for rows in (1, 4, 8, 16):
+        assert _native.gemm_variant(rows, 2 * 53248, 16384, True).startswith("tile_gated")
+        assert _native.gemm_variant(rows, 16384, 131072, False).startswith("tile")
+    # Just below one range the decode kernels stay eligible.
+    assert _native.gemm_variant(1, 2 * 8192, 65528, True).startswith(("split", "stream"))
+    # The tile kernel's per-tile ranges are bounded through the intermediate size.
+    assert _native.dense_workspace_bytes(16, 16384, 53248) > 0
+    offsets = (ctypes.c_size_t * 5)()
+    assert _native.library().xp_dense_workspace_layout(16, 1024, (1 << 21) + 8, offsets) == (
+        _native.XP_ERROR_INVALID_ARGUMENT
+    )
+    assert "2^21" in _native.last_error()
+
+
+def test_dense_workspace_layout_matches_the_region_rules():
+    # Batch at 0, activated after it (16-byte aligned), fp32 partials 256-byte aligned after
+    # that when a projection at this capacity splits K, total = xp_dense_workspace_bytes.
+    for capacity, hidden, intermediate in ((1, 1024, 3072), (32, 4096, 12288), (2048, 4096, 12288), (3, 1032, 1000)):
+        batch, activated, gate_up, down, total = _native.dense_workspace_layout(capacity, hidden, intermediate)
+        assert batch == 0
+        assert activated == (capacity * hidden * 2 + 15) // 16 * 16
+        assert total == _native.dense_workspace_bytes(capacity, hidden, intermediate)
+        if gate_up == total:
+            assert down == total and total == activated + capacity * intermediate * 2
+        else:
+            assert gate_up % 256 == 0 and gate_up >= activated + capacity * intermediate * 2
+            assert gate_up <= down <= total
+    # Qwen3-8B at 32 rows splits down over 8 K ranges: 8 x 32 x 4096 fp32 partials.
+    _, _, gate_up, down, total = _native.dense_workspace_layout(32, 4096, 12288)
+    assert total - down == 8 * 32 * 4096 * 4 and gate_up == down
+
+
 def test_abi_rejects_invalid_arguments_before_touching_the_device():
     lib = _native.library()
     p = ctypes.c_void_p
