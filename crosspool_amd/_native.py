@@ -44,6 +44,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "xp_dense_workspace_bytes": (_SIZE, [_I64, _I64, _I64]),
     "xp_dense_workspace_layout": (_INT, [_I64, _I64, _I64, ctypes.POINTER(_SIZE)]),
     "xp_dense_step": (_INT, [_P, _P, _I64, _P, _I64, _I64, _I64, _P, _P, _P, _F32, _P, _SIZE, _P, _P]),
+    "xp_dense_step_static": (_INT, [_P, _P, _I64, _P, _I64, _I64, _I64, _P, _P, _P, _F32, _P, _P]),
     "xp_gemm_variant": (_SIZE, [_I64, _I64, _I64, _INT, ctypes.c_char_p, _SIZE]),
     "xp_agent_create": (_INT, [_INT, ctypes.POINTER(_P)]),
     "xp_agent_destroy": (_INT, [_P]),

@@ -675,6 +675,61 @@ int xp_dense_step(const void *pool_in, void *pool_out, int64_t pool_rows, const 
                         norm_weight, eps, workspace, fault_word, stream);
 }
 
+// Workspace of xp_dense_step_static: a static device array, so that the step allocates
+// nothing.  Every device the library runs on holds its own copy until the process ends.
+// Host code never passes the array's name to a kernel (on the host it is a stand-in, not a
+// device address): it uses the device address that hipGetSymbolAddress returns for the
+// current device, looked up once per device and kept in static_scratch_address.
+constexpr size_t kStaticScratchBytes = size_t{64} << 20;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_static_scratch_mutex;
+void *g_static_scratch[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device (looked up on the first call there).
+int static_scratch_address(void **out) {
+  int device = 0;
+  XP_HIP_CHECK(hipGetDevice(&device));
+  XP_REQUIRE(device >= 0 && device < kMaxDevices, "device ordinal exceeds the static scratch table (64 devices)");
+  std::lock_guard<std::mutex> guard(g_static_scratch_mutex);
+  if (g_static_scratch[device] == nullptr) {
+    void *address = nullptr;
+    XP_HIP_CHECK(hipGetSymbolAddress(&address, HIP_SYMBOL(scratch)));
+    XP_REQUIRE(address != nullptr && (reinterpret_cast<uintptr_t>(address) & 255u) == 0,
+               "static scratch address is not 256-byte aligned");
+    g_static_scratch[device] = address;
+  }
+  *out = g_static_scratch[device];
+  return XP_OK;
+}
+
+}  // namespace
+
+int xp_dense_step_static(const void *pool_in, void *pool_out, int64_t pool_rows, const int32_t *slots, int64_t rows,
+                         int64_t hidden, int64_t intermediate, const void *w_gate_up, const void *w_down,
+                         const void *norm_weight, float eps, uint32_t *fault_word, xp_stream_t stream) {
+  if (const int status = dense_step_checks(pool_in, pool_out, pool_rows, slots, rows, hidden, intermediate, w_gate_up,
+                                           w_down, norm_weight);
+      status != XP_OK || rows == 0) {
+    return status;
+  }
+  const size_t needed = dense_workspace(rows, hidden, intermediate).bytes;
+  if (needed > kStaticScratchBytes) {
+    return fail(XP_ERROR_CAPACITY, "dense step needs " + std::to_string(needed) +
+                                       " bytes of workspace, more than the static scratch holds (" +
+                                       std::to_string(kStaticScratchBytes) + " bytes); use xp_dense_step");
+  }
+  void *workspace = nullptr;
+  if (const int status = static_scratch_address(&workspace); status != XP_OK) {
+    return status;
+  }
+  return run_dense_step(pool_in, pool_out, pool_rows, slots, rows, hidden, intermediate, w_gate_up, w_down,
+                        norm_weight, eps, workspace, fault_word, stream);
+}
+
 size_t xp_gemm_variant(int64_t capacity, int64_t n, int64_t k, int gated, char *buffer, size_t size) {
   const std::string name = capacity > 0 ? gemm_name(choose_gemm(capacity, n, k, gated != 0), gated != 0) : "";
   if (buffer != nullptr && size > 0) {

@@ -152,6 +152,20 @@ int xp_dense_step(const void *pool_in, void *pool_out, int64_t pool_rows, const 
                   const void *norm_weight, float eps, void *workspace, size_t workspace_bytes, uint32_t *fault_word,
                   xp_stream_t stream);
 
+/* xp_dense_step without a workspace argument: the step's workspace (gathered batch,
+ * activated intermediate, K-range partial sums) is a static 64 MiB device array of the
+ * library, one per device, held until the process ends.  It allocates nothing: no
+ * hipMalloc / hipFree, no allocating library call.  Steps needing more than 64 MiB
+ * (xp_dense_workspace_bytes(rows, hidden, intermediate) > 64 MiB, e.g. Qwen3-8B past about
+ * 512 rows) fail with XP_ERROR_CAPACITY.  Every call on one device shares the array and
+ * leaves its contents behind (no region needs to start cleared): calls that overlap in time
+ * on one device race, so order them on one stream.  No counterpart in the reference; it is
+ * for callers that cannot allocate device memory (code under stream capture, tight serving
+ * loops, harnesses that forbid allocation). */
+int xp_dense_step_static(const void *pool_in, void *pool_out, int64_t pool_rows, const int32_t *slots, int64_t rows,
+                         int64_t hidden, int64_t intermediate, const void *w_gate_up, const void *w_down,
+                         const void *norm_weight, float eps, uint32_t *fault_word, xp_stream_t stream);
+
 /* Name of the kernel variant chosen for a projection ("split_..." / "stream_..." / "tile_...").
  * Returns the full name length. */
 size_t xp_gemm_variant(int64_t capacity, int64_t n, int64_t k, int gated, char *buffer, size_t size);
