@@ -7,130 +7,201 @@ gate_j, row 2j+1 = up_j), ``o_proj [H, L]`` and, for the fused RMSNorm, the
 post-attention norm weight ``[H]``.  L = I / tp_size, and rank r owns intermediate
 rows ``[r L, (r + 1) L)``.
 
-Reference behaviour followed (file:line in the CrossPool checkout):
+Contract kept from the reference (file:line in the CrossPool checkout); the code is
+this module's own:
 
-- family compilers: ``runtime/ffnagent/models/qwen3.py:13-45`` (Qwen2 and Llama are
-  the same gated Dense profile), ``architecture.py:22-137`` (strict ``config.json``
-  fields, ``architecture.py:177-215`` load);
-- key view: ``checkpoint.py:18-76`` (index or one canonical file, duplicate JSON members
-  and unsafe shard names rejected);
-- FFN key coverage: ``checkpoint.py:79-93``;
-- TP geometry: ``preparation.py:160-241``; Gate/Up row order ``ffn.py:57-68``;
-- reading: ``loader.py:451-519`` (slices, dtype and shape checks), ``loader.py:593-720``
-  (bounded pinned slots, reader threads that never touch the GPU, the owner thread
-  installs each value before its slot is reused).
+- accepted families and ``config.json`` fields: ``runtime/ffnagent/models/qwen3.py:13-45``
+  and ``architecture.py:22-137,177-215`` (Qwen3, Qwen2 and Llama share the gated
+  Dense profile; integer fields are strict JSON integers; the source dtype is bf16 or
+  fp16, named ``torch_dtype`` or ``dtype``);
+- which file holds each tensor: ``checkpoint.py:18-76`` (the index's weight map, or a
+  lone canonical ``model.safetensors``; duplicate JSON members, path-like or
+  non-safetensors shard names and missing shard files are refused);
+- each layer's ``mlp.`` keys are exactly gate, up and down: ``checkpoint.py:79-93``;
+- TP slice and Gate/Up row order: ``preparation.py:160-241``, ``ffn.py:57-68``;
+- payload conversion and shape checks: ``loader.py:451-519``.
+
+Error messages the reference's tests match are kept word for word (``exactly one
+unindexed canonical``, ``duplicate JSON member``, ``missing=`` / ``extra=``, ``must be a
+JSON integer``, ``must be greater than or equal to``, the offending field's name).
 
 The post-attention norm weight (``model.layers.{i}.post_attention_layernorm.weight``)
-is read in addition, because this build fuses the norm into the gather; the reference
+is read as well, because this build fuses the norm into the gather; the reference
 leaves the norm to SGLang.  Payloads are bf16: bf16 sources are copied bit for bit,
 fp16 / fp32 sources are rounded to nearest even.
 """
 
 from __future__ import annotations
 
-import concurrent.futures
 import json
 import math
-import queue
-import threading
+import re
+from collections import Counter, defaultdict
+from concurrent.futures import Future, ThreadPoolExecutor
 from dataclasses import dataclass
-from pathlib import Path
-from typing import Callable, Iterable
+from pathlib import Path, PurePosixPath
+from typing import Iterable
 
 import torch
 
 INDEX_FILENAME = "model.safetensors.index.json"
 SINGLE_FILE_NAME = "model.safetensors"
 
-# Gated Dense families: architecture name -> model_type (all use ``model.layers.{i}.mlp``).
+# Gated Dense families (architecture name -> required model_type); all keep their FFN under
+# ``model.layers.{i}.mlp``.
 DENSE_FAMILIES = {
     "Qwen3ForCausalLM": "qwen3",
     "Qwen2ForCausalLM": "qwen2",
     "LlamaForCausalLM": "llama",
 }
-ADMITTED_SOURCE_DTYPES = ("bfloat16", "float16")
+SOURCE_DTYPES = frozenset({"bfloat16", "float16"})
+MLP_PROJECTIONS = ("gate_proj", "up_proj", "down_proj")
+_MLP_KEY = re.compile(r"model\.layers\.(\d+)\.mlp\.(.+)")
 
 
-# ---------------------------------------------------------------- config and key view
-def parse_json_object(payload: bytes, *, source: Path) -> dict:
-    """One JSON object; a duplicated member at any level is an error (checkpoint.py:18-34)."""
+# ---------------------------------------------------------------- JSON and config fields
+def _json_object(path: Path) -> dict:
+    """The JSON object stored at ``path``; a member name repeated in any object is refused."""
 
-    def unique(pairs: list[tuple[str, object]]) -> dict:
-        result: dict = {}
-        for key, value in pairs:
-            if key in result:
-                raise ValueError(f"duplicate JSON member {key!r} in {source}")
-            result[key] = value
-        return result
+    def build(pairs: list[tuple[str, object]]) -> dict:
+        built = dict(pairs)
+        if len(built) != len(pairs):
+            repeated = next(name for name, count in Counter(name for name, _ in pairs).items() if count > 1)
+            raise ValueError(f"duplicate JSON member {repeated!r} in {path}")
+        return built
 
-    value = json.loads(payload, object_pairs_hook=unique)
-    if not isinstance(value, dict):
-        raise ValueError(f"{source} must contain one JSON object")
-    return value
+    document = json.loads(path.read_bytes(), object_pairs_hook=build)
+    if not isinstance(document, dict):
+        raise ValueError(f"{path} does not hold a JSON object")
+    return document
+
+
+class _Fields:
+    """Typed reads of ``config.json`` members (strict JSON types, bounds in the message)."""
+
+    def __init__(self, document: dict) -> None:
+        self.document = document
+
+    def integer(self, name: str, minimum: int = 1) -> int:
+        value = self.document.get(name)
+        if type(value) is not int:  # bool and float are not JSON integers here
+            raise ValueError(f"{name} must be a JSON integer")
+        if value < minimum:
+            raise ValueError(f"{name} must be greater than or equal to {minimum}")
+        return value
+
+    def positive_number(self, name: str, default: float) -> float:
+        value = self.document.get(name, default)
+        if type(value) not in (int, float) or not math.isfinite(value) or value <= 0:
+            raise ValueError(f"{name} must be a finite positive JSON number")
+        return float(value)
+
+    def text(self, name: str, required: str) -> None:
+        if self.document.get(name) != required:
+            raise ValueError(f"{name} is {self.document.get(name)!r}; this family requires {required!r}")
+
+    def architecture(self) -> str:
+        names = self.document.get("architectures")
+        if type(names) is not list or len(names) != 1 or type(names[0]) is not str or not names[0]:
+            raise ValueError("architectures must name exactly one architecture (a one-element array)")
+        return names[0]
+
+    def source_dtype(self) -> str:
+        field = "dtype" if "dtype" in self.document and "torch_dtype" not in self.document else "torch_dtype"
+        value = self.document.get(field)
+        if value not in SOURCE_DTYPES:
+            raise ValueError(f"{field} is {value!r}; the Dense FFN path reads 'bfloat16' or 'float16' checkpoints")
+        return value
+
+
+# ---------------------------------------------------------------- tensor key -> shard file
+def _shard_file(model_path: Path, name: object, *, index_path: Path) -> Path:
+    """The shard file an index entry names: a plain ``*.safetensors`` file name in the model
+    directory that exists as a regular file (no directories, no symlinks)."""
+
+    if type(name) is not str or not name:
+        raise ValueError(f"{index_path} names an empty or non-string shard")
+    if PurePosixPath(name).name != name or "\\" in name or not name.endswith(".safetensors"):
+        raise ValueError(f"{index_path} names unsafe shard name {name!r} (a plain *.safetensors file name is required)")
+    path = model_path / name
+    if path.is_symlink() or not path.is_file():
+        raise ValueError(f"shard file {path} is missing, a symlink or not a regular file")
+    return path
 
 
 def read_checkpoint_key_view(model_path: Path) -> dict[str, Path]:
-    """Tensor key -> shard file, from the index or the one canonical file (checkpoint.py:37-76)."""
+    """Map every tensor key of the checkpoint to the file holding it, reading no tensor data.
+
+    An index (``model.safetensors.index.json``) is authoritative when present; otherwise the
+    directory must hold one safetensors file, ``model.safetensors``, whose header lists the keys.
+    """
 
     model_path = Path(model_path)
     index_path = model_path / INDEX_FILENAME
     if index_path.exists():
-        index = parse_json_object(index_path.read_bytes(), source=index_path)
-        weight_map = index.get("weight_map")
-        if not isinstance(weight_map, dict) or not weight_map:
-            raise ValueError(f"{index_path} must contain one nonempty object-valued weight_map")
-        view: dict[str, Path] = {}
-        for key, shard in weight_map.items():
+        weight_map = _json_object(index_path).get("weight_map")
+        if type(weight_map) is not dict or not weight_map:
+            raise ValueError(f"{index_path} has no weight_map object with at least one entry")
+        resolved: dict[str, Path] = {}
+        files: dict[str, Path] = {}  # each distinct shard name is checked once
+        for key, name in weight_map.items():
             if not key:
-                raise ValueError(f"{index_path} contains an invalid weight key")
-            if not isinstance(shard, str) or not shard:
-                raise ValueError(f"{index_path} contains an invalid shard name for {key!r}")
-            if "/" in shard or "\\" in shard or not shard.endswith(".safetensors"):
-                raise ValueError(f"{index_path} contains unsafe shard name {shard!r}")
-            path = model_path / shard
-            if path.is_symlink() or not path.is_file():
-                raise ValueError(f"checkpoint shard {path} is not an existing regular file")
-            view[key] = path
-        return view
+                raise ValueError(f"{index_path} maps an empty tensor key")
+            if type(name) is not str or name not in files:
+                files[name] = _shard_file(model_path, name, index_path=index_path)
+            resolved[key] = files[name]
+        return resolved
 
+    candidates = sorted(entry for entry in model_path.iterdir() if entry.suffix == ".safetensors")
     canonical = model_path / SINGLE_FILE_NAME
-    files = [entry for entry in model_path.iterdir() if entry.suffix == ".safetensors"]
-    if len(files) != 1 or files[0] != canonical:
+    if candidates != [canonical]:
         raise ValueError(f"{model_path} must contain exactly one unindexed canonical {SINGLE_FILE_NAME} checkpoint")
     if canonical.is_symlink() or not canonical.is_file():
-        raise ValueError(f"checkpoint {canonical} is not an existing regular file")
+        raise ValueError(f"{canonical} is a symlink or not a regular file")
     from safetensors import safe_open
 
     with safe_open(str(canonical), framework="pt", device="cpu") as handle:
-        keys = tuple(handle.keys())
-    if not keys or any(not isinstance(key, str) or not key for key in keys):
-        raise ValueError(f"checkpoint {canonical} must contain only nonempty tensor keys")
-    return dict.fromkeys(keys, canonical)
-
-
-def _config_int(config: dict, name: str) -> int:
-    value = config.get(name)
-    if not isinstance(value, int) or isinstance(value, bool):
-        raise ValueError(f"{name} must be a JSON integer")
-    if value < 1:
-        raise ValueError(f"{name} must be greater than or equal to 1")
-    return value
+        keys = list(handle.keys())
+    if not keys or not all(type(key) is str and key for key in keys):
+        raise ValueError(f"checkpoint {canonical} lists an empty tensor key (or none)")
+    return {key: canonical for key in keys}
 
 
 def mlp_keys(layer_id: int) -> tuple[str, str, str]:
     """Gate, up and down weight keys of one layer (architecture.py:120-137)."""
 
-    prefix = f"model.layers.{layer_id}.mlp"
-    return (f"{prefix}.gate_proj.weight", f"{prefix}.up_proj.weight", f"{prefix}.down_proj.weight")
+    return tuple(f"model.layers.{layer_id}.mlp.{projection}.weight" for projection in MLP_PROJECTIONS)
 
 
 def norm_key(layer_id: int) -> str:
     return f"model.layers.{layer_id}.post_attention_layernorm.weight"
 
 
+def validate_ffn_coverage(key_view: dict[str, Path], layer_count: int) -> None:
+    """Each layer below ``layer_count`` holds exactly its gate, up and down weights under ``mlp.``.
+
+    Keys are grouped by the layer their ``model.layers.{i}.mlp.`` name gives; keys of other
+    modules and of layers past the count do not take part.
+    """
+
+    by_layer: dict[int, set[str]] = defaultdict(set)
+    for key in key_view:
+        match = _MLP_KEY.fullmatch(key)
+        if match is not None:
+            by_layer[int(match.group(1))].add(key)
+    for layer_id in range(layer_count):
+        wanted = set(mlp_keys(layer_id))
+        found = by_layer.get(layer_id, set())
+        if found != wanted:
+            raise ValueError(
+                f"FFN checkpoint namespace for layer {layer_id} differs: missing={sorted(wanted - found)}, "
+                f"extra={sorted(found - wanted)}"
+            )
+
+
 @dataclass(frozen=True, slots=True)
 class DenseModelSpec:
-    """FFN semantics of a gated Dense checkpoint (the FfnModelSpec of qwen3.py:24-45)."""
+    """FFN facts of a gated Dense checkpoint (the reference's FfnModelSpec, qwen3.py:24-45)."""
 
     architecture: str
     hidden_size: int
@@ -141,58 +212,33 @@ class DenseModelSpec:
 
 
 def load_model_spec(model_path: Path) -> DenseModelSpec:
-    """Compile ``config.json`` and check the FFN key coverage (architecture.py:177-215).
+    """Read ``config.json`` and the key view, and check the FFN keys of every layer.
 
-    Raises RuntimeError naming the checkpoint, as the reference does.
+    Any failure is re-raised as RuntimeError naming the checkpoint (architecture.py:177-215).
     """
 
     model_path = Path(model_path)
     try:
-        config_path = model_path / "config.json"
-        config = parse_json_object(config_path.read_bytes(), source=config_path)
-        architectures = config.get("architectures")
-        if (
-            not isinstance(architectures, list)
-            or len(architectures) != 1
-            or not isinstance(architectures[0], str)
-            or not architectures[0]
-        ):
-            raise ValueError("architectures must be a one-element array containing a nonempty string")
-        architecture = architectures[0]
-        model_type = DENSE_FAMILIES.get(architecture)
-        if model_type is None:
-            raise ValueError(f"unsupported FFN architecture {architecture!r}")
-        if config.get("model_type") != model_type:
-            raise ValueError(f"model_type must equal {model_type!r}")
-        if config.get("hidden_act") != "silu":
-            raise ValueError("hidden_act must equal 'silu'")
-        if config.get("torch_dtype") not in ADMITTED_SOURCE_DTYPES:
-            raise ValueError("torch_dtype must be 'bfloat16' or 'float16'")
-        hidden = _config_int(config, "hidden_size")
-        layers = _config_int(config, "num_hidden_layers")
-        intermediate = _config_int(config, "intermediate_size")
-        eps = config.get("rms_norm_eps", 1e-6)
-        if isinstance(eps, bool) or not isinstance(eps, (int, float)) or not math.isfinite(eps) or eps <= 0:
-            raise ValueError("rms_norm_eps must be a finite positive JSON number")
-        key_view = read_checkpoint_key_view(model_path)
-        validate_ffn_coverage(key_view, layers)
-        return DenseModelSpec(architecture, hidden, intermediate, layers, float(eps), key_view)
+        fields = _Fields(_json_object(model_path / "config.json"))
+        architecture = fields.architecture()
+        if architecture not in DENSE_FAMILIES:
+            raise ValueError(f"unsupported FFN architecture {architecture!r} (gated Dense families: "
+                             f"{', '.join(sorted(DENSE_FAMILIES))})")
+        fields.text("model_type", DENSE_FAMILIES[architecture])
+        fields.text("hidden_act", "silu")
+        fields.source_dtype()
+        spec = DenseModelSpec(
+            architecture=architecture,
+            hidden_size=fields.integer("hidden_size"),
+            intermediate_size=fields.integer("intermediate_size"),
+            layer_count=fields.integer("num_hidden_layers"),
+            rms_norm_eps=fields.positive_number("rms_norm_eps", 1e-6),
+            key_view=read_checkpoint_key_view(model_path),
+        )
+        validate_ffn_coverage(spec.key_view, spec.layer_count)
+        return spec
     except Exception as error:
-        raise RuntimeError(f"failed to compile FFN model at {model_path}: {error}") from error
-
-
-def validate_ffn_coverage(key_view: dict[str, Path], layer_count: int) -> None:
-    """Each layer's ``mlp.`` namespace holds exactly its three weights (checkpoint.py:79-93)."""
-
-    keys = set(key_view)
-    for layer_id in range(layer_count):
-        prefix = f"model.layers.{layer_id}.mlp."
-        actual = {key for key in keys if key.startswith(prefix)}
-        expected = set(mlp_keys(layer_id))
-        if actual != expected:
-            missing = sorted(expected - actual)
-            extra = sorted(actual - expected)
-            raise ValueError(f"FFN checkpoint namespace for layer {layer_id} differs: missing={missing}, extra={extra}")
+        raise RuntimeError(f"checkpoint at {model_path} is not a loadable gated Dense FFN model: {error}") from error
 
 
 # ---------------------------------------------------------------- TP geometry and reads
@@ -206,13 +252,12 @@ class ShardGeometry:
     tp_rank: int
 
     def __post_init__(self) -> None:
-        for value in (self.tp_size, self.tp_rank):
-            if isinstance(value, bool) or not isinstance(value, int):
-                raise ValueError("FFN preparation coordinates must be integers")
-        if self.tp_size <= 0 or not 0 <= self.tp_rank < self.tp_size:
-            raise ValueError("FFN preparation coordinate is outside the TP domain")
+        if type(self.tp_size) is not int or type(self.tp_rank) is not int:
+            raise ValueError("TP size and rank must be integers")
+        if not 0 <= self.tp_rank < self.tp_size:
+            raise ValueError(f"TP rank {self.tp_rank} is outside the TP domain of size {self.tp_size}")
         if self.intermediate_size % self.tp_size:
-            raise ValueError("FFN intermediate size is not divisible by FFN TP")
+            raise ValueError(f"intermediate size {self.intermediate_size} is not divisible by TP size {self.tp_size}")
 
     @property
     def local_width(self) -> int:
@@ -224,8 +269,8 @@ class ShardGeometry:
 
 
 @dataclass(frozen=True, slots=True)
-class _Read:
-    """One staged value: the keys it reads, its host shape and how the slices combine."""
+class StagedValue:
+    """One device value of one layer and the checkpoint keys it is assembled from."""
 
     layer_id: int
     kind: str  # "i_proj", "o_proj" or "norm"
@@ -233,71 +278,62 @@ class _Read:
     shape: tuple[int, ...]
 
     @property
-    def staged_bytes(self) -> int:
+    def nbytes(self) -> int:
         return math.prod(self.shape) * 2
 
 
-def _to_payload(source: torch.Tensor, *, key: str) -> torch.Tensor:
-    if not source.is_floating_point():
-        raise ValueError(f"checkpoint tensor {key!r} has incompatible dtype {source.dtype}")
-    return source.to(torch.bfloat16)  # bf16 is a copy; wider floats round to nearest even
+def layer_reads(spec: DenseModelSpec, geometry: ShardGeometry, layer_ids: Iterable[int], *,
+                norm: bool) -> list[StagedValue]:
+    hidden, width = geometry.hidden_size, geometry.local_width
+    values = []
+    for layer_id in layer_ids:
+        gate, up, down = mlp_keys(layer_id)
+        values.append(StagedValue(layer_id, "i_proj", (gate, up), (2 * width, hidden)))
+        values.append(StagedValue(layer_id, "o_proj", (down,), (hidden, width)))
+        if norm:
+            values.append(StagedValue(layer_id, "norm", (norm_key(layer_id),), (hidden,)))
+    return values
 
 
-def _read_slice(handle, key: str, expected: tuple[int, ...], select: Callable) -> torch.Tensor:
-    piece = handle.get_slice(key)
-    shape = tuple(piece.get_shape())
-    if shape != expected:
-        raise ValueError(f"checkpoint tensor {key!r} has incompatible shape: expected {expected}, found {shape}")
-    return _to_payload(select(piece), key=key)
+def _checked_slice(handle, key: str, full_shape: tuple[int, ...], region: tuple[slice, ...]) -> torch.Tensor:
+    """``region`` of tensor ``key`` as bf16, after checking the tensor's full shape and type."""
+
+    lazy = handle.get_slice(key)
+    found = tuple(lazy.get_shape())
+    if found != full_shape:
+        raise ValueError(f"tensor {key!r} is {found}, the model config implies {full_shape}")
+    data = lazy[region]
+    if not data.is_floating_point():
+        raise ValueError(f"tensor {key!r} holds {data.dtype}, not a floating-point type")
+    return data.to(torch.bfloat16)  # a copy for bf16, nearest-even rounding for wider floats
 
 
-def stage_read(read: _Read, geometry: ShardGeometry, key_view: dict[str, Path], out: torch.Tensor) -> None:
-    """Fill ``out`` (host, bf16, ``read.shape``) from the checkpoint; no GPU work.
+def stage_read(value: StagedValue, geometry: ShardGeometry, key_view: dict[str, Path], out: torch.Tensor) -> None:
+    """Fill the host tensor ``out`` (bf16, ``value.shape``) from the checkpoint; no GPU work.
 
-    ``i_proj``: rows 2j and 2j+1 of ``out`` are gate and up row ``start + j``.
-    ``o_proj``: columns ``[start, start + L)`` of ``down``.  ``norm``: the vector.
+    ``i_proj``: rows 2j and 2j+1 are gate and up row ``start + j``; ``o_proj``: columns
+    ``[start, start + L)`` of down; ``norm``: the whole vector.
     """
 
     from safetensors import safe_open
 
     hidden, intermediate = geometry.hidden_size, geometry.intermediate_size
-    start, width = geometry.source_start, geometry.local_width
-    handles: dict[Path, object] = {}
-    try:
-        def handle_of(key: str):
-            path = key_view.get(key)
-            if path is None:
-                raise ValueError(f"checkpoint key {key!r} is absent from its authoritative key view")
-            if path not in handles:
-                handles[path] = safe_open(str(path), framework="pt", device="cpu").__enter__()
-            return handles[path]
-
-        if read.kind == "i_proj":
-            pairs = out.view(width, 2, hidden)
-            for column, key in enumerate(read.keys):  # gate -> rows 2j, up -> rows 2j + 1
-                rows = _read_slice(handle_of(key), key, (intermediate, hidden), lambda p: p[start : start + width])
-                pairs[:, column, :].copy_(rows)
-        elif read.kind == "o_proj":
-            (key,) = read.keys
-            out.copy_(_read_slice(handle_of(key), key, (hidden, intermediate), lambda p: p[:, start : start + width]))
-        else:
-            (key,) = read.keys
-            out.copy_(_read_slice(handle_of(key), key, (hidden,), lambda p: p[:]))
-    finally:
-        for handle in handles.values():
-            handle.__exit__(None, None, None)
-
-
-def layer_reads(spec: DenseModelSpec, geometry: ShardGeometry, layer_ids: Iterable[int], *, norm: bool) -> list[_Read]:
-    hidden, width = geometry.hidden_size, geometry.local_width
-    reads = []
-    for layer_id in layer_ids:
-        gate, up, down = mlp_keys(layer_id)
-        reads.append(_Read(layer_id, "i_proj", (gate, up), (2 * width, hidden)))
-        reads.append(_Read(layer_id, "o_proj", (down,), (hidden, width)))
-        if norm:
-            reads.append(_Read(layer_id, "norm", (norm_key(layer_id),), (hidden,)))
-    return reads
+    rows = slice(geometry.source_start, geometry.source_start + geometry.local_width)
+    files = []
+    for key in value.keys:
+        if key not in key_view:
+            raise ValueError(f"no shard file holds tensor {key!r}")
+        files.append(key_view[key])
+    handles = {path: safe_open(str(path), framework="pt", device="cpu") for path in set(files)}
+    if value.kind == "i_proj":
+        # out viewed as [L, 2, H]: plane 0 takes the gate rows, plane 1 the up rows.
+        pairs = out.view(geometry.local_width, 2, hidden)
+        for plane, (key, path) in enumerate(zip(value.keys, files)):
+            pairs[:, plane].copy_(_checked_slice(handles[path], key, (intermediate, hidden), (rows,)))
+    elif value.kind == "o_proj":
+        out.copy_(_checked_slice(handles[files[0]], value.keys[0], (hidden, intermediate), (slice(None), rows)))
+    else:
+        out.copy_(_checked_slice(handles[files[0]], value.keys[0], (hidden,), (slice(None),)))
 
 
 # ---------------------------------------------------------------- materialisation
@@ -324,11 +360,10 @@ def load_dense_layers(
 ) -> list[LoadedDenseLayer]:
     """Materialise the selected layers' local shards on ``device`` (default: current GPU).
 
-    Reader threads fill at most ``parallelism`` pinned host slots (each sized for the
-    largest value); this thread copies every staged value to its device tensor and
-    returns the slot once the copy has completed (loader.py:228-284, 593-720).  The
-    device tensors are allocated up front; a failure anywhere stops the readers and
-    raises RuntimeError.
+    The device tensors are allocated first; host reads then run ``parallelism`` at a time
+    into a ring of pinned buffers, and each staged value goes to its device tensor by an
+    asynchronous copy on a side stream.  Any failure raises RuntimeError after the reads in
+    flight have ended.
     """
 
     if parallelism <= 0:
@@ -338,89 +373,77 @@ def load_dense_layers(
     if spec.hidden_size % 8 or geometry.local_width % 8:
         raise ValueError("hidden size and local intermediate size must be multiples of 8 on this path")
     layer_ids = list(range(spec.layer_count)) if layers is None else list(layers)
-    for layer_id in layer_ids:
-        if not 0 <= layer_id < spec.layer_count:
-            raise ValueError(f"layer {layer_id} is outside the model")
+    outside = [layer_id for layer_id in layer_ids if not 0 <= layer_id < spec.layer_count]
+    if outside:
+        raise ValueError(f"layers {outside} are outside the model's {spec.layer_count} layers")
     if device is None:
         device = torch.cuda.current_device()
     device = torch.device("cuda", device if isinstance(device, int) else device.index)
 
-    reads = layer_reads(spec, geometry, layer_ids, norm=norm)
+    values = layer_reads(spec, geometry, layer_ids, norm=norm)
     try:
-        destinations = {(read.layer_id, read.kind): torch.empty(read.shape, dtype=torch.bfloat16, device=device)
-                        for read in reads}
-        _copy_staged(reads, geometry, spec.key_view, destinations, parallelism)
-    except Exception as error:
-        raise RuntimeError(f"failed to materialize local FFN weights: {error}") from error
-    return [
-        LoadedDenseLayer(
-            layer_id=layer_id,
-            i_proj=destinations[(layer_id, "i_proj")],
-            o_proj=destinations[(layer_id, "o_proj")],
-            norm_weight=destinations.get((layer_id, "norm")),
-            eps=spec.rms_norm_eps,
+        targets = [torch.empty(value.shape, dtype=torch.bfloat16, device=device) for value in values]
+        _PinnedRing(min(parallelism, len(values)), max(value.nbytes for value in values), device).run(
+            values, targets, geometry, spec.key_view
         )
+    except Exception as error:
+        raise RuntimeError(f"loading the FFN shards of {model_path} onto {device} failed: {error}") from error
+    placed = {(value.layer_id, value.kind): target for value, target in zip(values, targets)}
+    return [
+        LoadedDenseLayer(layer_id, placed[(layer_id, "i_proj")], placed[(layer_id, "o_proj")],
+                         placed.get((layer_id, "norm")), spec.rms_norm_eps)
         for layer_id in layer_ids
     ]
 
 
-def _copy_staged(
-    reads: list[_Read],
-    geometry: ShardGeometry,
-    key_view: dict[str, Path],
-    destinations: dict[tuple[int, str], torch.Tensor],
-    parallelism: int,
-) -> None:
-    slot_bytes = max(read.staged_bytes for read in reads)
-    slots: queue.Queue[torch.Tensor] = queue.Queue()
-    for _ in range(min(parallelism, len(reads))):
-        slots.put(torch.empty(slot_bytes, dtype=torch.uint8, pin_memory=True))
-    staged: queue.Queue = queue.Queue()
-    cancelled = threading.Event()
+class _PinnedRing:
+    """A ring of pinned host buffers between host reads and device copies.
 
-    def acquire() -> torch.Tensor | None:
-        while not cancelled.is_set():
+    Value i is read into buffer i mod N by a worker thread; the calling thread then copies
+    it to the device on a side stream and records an event.  Buffer b is handed to its next
+    read only after that event has completed, so at most N host reads and the copies behind
+    them overlap.  Worker threads never touch the GPU.
+    """
+
+    def __init__(self, count: int, nbytes: int, device: torch.device) -> None:
+        self.buffers = [torch.empty(nbytes, dtype=torch.uint8, pin_memory=True) for _ in range(count)]
+        self.copied: list[torch.cuda.Event | None] = [None] * count
+        self.device = device
+
+    def _view(self, index: int, value: StagedValue) -> torch.Tensor:
+        buffer = self.buffers[index % len(self.buffers)]
+        return buffer[: value.nbytes].view(torch.bfloat16).view(value.shape)
+
+    def run(self, values: list[StagedValue], targets: list[torch.Tensor], geometry: ShardGeometry,
+            key_view: dict[str, Path]) -> None:
+        count = len(self.buffers)
+        stream = torch.cuda.Stream(device=self.device)
+        stream.wait_stream(torch.cuda.current_stream(self.device))  # the targets' allocation
+        reads: dict[int, Future] = {}
+        with ThreadPoolExecutor(max_workers=count) as workers:
+
+            def start(index: int) -> None:
+                ring_slot = index % count
+                if self.copied[ring_slot] is not None:
+                    self.copied[ring_slot].synchronize()
+                reads[index] = workers.submit(stage_read, values[index], geometry, key_view,
+                                              self._view(index, values[index]))
+
             try:
-                return slots.get(timeout=0.1)
-            except queue.Empty:
-                continue
-        return None
-
-    def reader(read: _Read) -> None:
-        slot = acquire()
-        if slot is None:
-            staged.put(("done", read, None))
-            return
-        try:
-            view = slot[: read.staged_bytes].view(torch.bfloat16).view(read.shape)
-            stage_read(read, geometry, key_view, view)
-        except Exception as error:
-            slots.put(slot)
-            cancelled.set()
-            staged.put(("failed", read, error))
-            return
-        staged.put(("staged", read, slot))
-
-    first_error: Exception | None = None
-    with concurrent.futures.ThreadPoolExecutor(max_workers=parallelism) as pool:
-        futures = [pool.submit(reader, read) for read in reads]
-        for _ in reads:
-            state, read, payload = staged.get()
-            if state == "failed":
-                first_error = first_error or payload
-                continue
-            if state == "done":
-                continue
-            try:
-                if first_error is None:
-                    view = payload[: read.staged_bytes].view(torch.bfloat16).view(read.shape)
-                    destinations[(read.layer_id, read.kind)].copy_(view, non_blocking=False)
-            except Exception as error:  # a failed copy stops the readers too
-                first_error = first_error or error
-                cancelled.set()
+                for index in range(min(count, len(values))):
+                    start(index)
+                for index, (value, target) in enumerate(zip(values, targets)):
+                    reads.pop(index).result()
+                    with torch.cuda.stream(stream):
+                        target.copy_(self._view(index, value), non_blocking=True)
+                        event = torch.cuda.Event()
+                        event.record(stream)
+                    self.copied[index % count] = event
+                    if index + count < len(values):
+                        start(index + count)
             finally:
-                slots.put(payload)
-        for future in futures:
-            future.result()
-    if first_error is not None:
-        raise first_error
+                for pending in reads.values():
+                    pending.cancel()
+                # Copies already issued write into the targets: they must land before a
+                # failure lets the targets go back to the allocator.
+                stream.synchronize()

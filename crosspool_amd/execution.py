@@ -21,37 +21,48 @@ def align_up(value: int, alignment: int) -> int:
 
 @dataclass(frozen=True, slots=True)
 class WorkspaceLayout:
-    """Prepared byte regions borrowed from one caller-owned backing (execution.py:38-70)."""
+    """Typed regions placed one after another in a caller-owned byte buffer.
+
+    The placement rule is the reference's (execution.py:38-70, pinned by its known answers):
+    regions keep their order, and each non-empty region starts at the next multiple of
+    OPERATOR_ALIGNMENT_BYTES; an empty region takes the current offset and no space.
+    """
 
     regions: tuple[tuple[torch.dtype, tuple[int, ...]], ...]
     offsets: tuple[int, ...]
     nbytes: int
 
+    @staticmethod
+    def region_bytes(region: tuple[torch.dtype, tuple[int, ...]]) -> int:
+        dtype, shape = region
+        return dtype.itemsize * math.prod(shape)
+
     @classmethod
     def from_regions(cls, regions: tuple[tuple[torch.dtype, tuple[int, ...]], ...]) -> WorkspaceLayout:
-        """Align every non-empty region to 16 bytes, in order (execution.py:46-58)."""
-
-        offsets = []
-        cursor = 0
-        for dtype, shape in regions:
-            size = math.prod(shape) * dtype.itemsize
-            if size:
-                cursor = align_up(cursor, OPERATOR_ALIGNMENT_BYTES)
-            offsets.append(cursor)
-            cursor += size
-        return cls(regions=regions, offsets=tuple(offsets), nbytes=cursor)
+        placed: list[int] = []
+        end = 0
+        for region in regions:
+            size = cls.region_bytes(region)
+            start = align_up(end, OPERATOR_ALIGNMENT_BYTES) if size else end
+            placed.append(start)
+            end = start + size
+        return cls(regions=regions, offsets=tuple(placed), nbytes=end)
 
     def views(self, backing: torch.Tensor) -> tuple[torch.Tensor, ...]:
-        """Borrow the prepared views without allocating (execution.py:60-70)."""
+        """One typed view per region into ``backing`` (a flat uint8 tensor); nothing is allocated."""
 
-        if backing.dtype is not torch.uint8 or backing.ndim != 1 or not backing.is_contiguous():
-            raise ValueError("workspace backing must be a contiguous byte vector")
-        if backing.numel() < self.nbytes or backing.data_ptr() % OPERATOR_ALIGNMENT_BYTES:
-            raise ValueError("workspace backing does not cover its prepared aligned extent")
-        return tuple(
-            backing[offset : offset + math.prod(shape) * dtype.itemsize].view(dtype).view(shape)
-            for offset, (dtype, shape) in zip(self.offsets, self.regions, strict=True)
-        )
+        flat_bytes = backing.dtype is torch.uint8 and backing.dim() == 1 and backing.is_contiguous()
+        if not flat_bytes:
+            raise ValueError(f"a workspace is a flat contiguous uint8 tensor, not {backing.dtype} {tuple(backing.shape)}")
+        if backing.data_ptr() % OPERATOR_ALIGNMENT_BYTES:
+            raise ValueError(f"a workspace must start on a {OPERATOR_ALIGNMENT_BYTES}-byte boundary")
+        if backing.numel() < self.nbytes:
+            raise ValueError(f"workspace holds {backing.numel()} bytes; this layout needs {self.nbytes}")
+        views = []
+        for offset, region in zip(self.offsets, self.regions):
+            dtype, shape = region
+            views.append(backing.narrow(0, offset, self.region_bytes(region)).view(dtype).reshape(shape))
+        return tuple(views)
 
 
 def derive_payload_row_capacities(maximum_row_capacity: int) -> tuple[int, ...]:

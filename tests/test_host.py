@@ -94,10 +94,10 @@ def test_workspace_layout_matches_reference_known_answers():
     assert projected.data_ptr() == backing.data_ptr()
     assert activated.data_ptr() == backing.data_ptr() + 128
     assert projected.shape == (4, 16) and activated.shape == (4, 8)
-    with pytest.raises(ValueError, match="extent"):
+    with pytest.raises(ValueError, match="layout needs 192"):
         layout.views(backing[:-1])
     misaligned = torch.empty(layout.nbytes + 1, dtype=torch.uint8)[1:]
-    with pytest.raises(ValueError, match="aligned"):
+    with pytest.raises(ValueError, match="16-byte boundary"):
         layout.views(misaligned)
 
 
