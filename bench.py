@@ -15,6 +15,10 @@ baseline (the oracle's torch-CPU restatement on the host cores).
 the roofline's ``traffic`` figure comes from (a byte copy of known size for
 calibration, then gate_up at the headline and decode sizes), for
 ``rocprofv3 --pmc`` runs; ``profiles/traffic.json`` records their result.
+
+``--ceilings`` instead measures the hardware limits the kernels are judged
+against (libxpool_probes.so): a pure-MFMA loop, two HBM read patterns and the
+GPU idle time a hipGraphLaunch adds per replay, and prints them as one JSON line.
 """
 
 from __future__ import annotations
@@ -47,6 +51,16 @@ TRAFFIC_FILE = REPO_ROOT / "profiles" / "traffic.json"
 # Qwen3-0.6B FFN (hidden, intermediate) x 28 layers, and its batch sizes.
 STACK_SHAPE = (1024, 3072, 28)
 STACK_TOKENS = (1, 8, 32, 128, 256)
+# one of 8 tensor-parallel shards of a Qwen3-32B FFN, its batch sizes, and
+# the weight copies rotated at HBM-bound sizes (4 x 98 MB exceeds the last-level cache).
+SHARD_SHAPE = (5120, 3200)
+SHARD_TOKENS = (8, 512, 8192)
+SHARD_COPIES = 4
+# two co-located models on two Lanes, ragged 1..512 rows per step each.
+COLOCATED_SHAPES = ((2048, 6144), (2560, 9728))
+COLOCATED_MAX_ROWS = 512
+COLOCATED_LAYERS = 3  # distinct weight sets per model, rotated per step
+COLOCATED_STEPS = 60
 # Qwen3-30B-A3B MoE layer (hidden, moe_intermediate, experts, top-k) and its token points.
 MOE_SHAPE = (2048, 768, 128, 8)
 MOE_TOKENS = (1, 32, 2048)
@@ -64,6 +78,9 @@ def parse_args() -> argparse.Namespace:
     parser.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample length")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--kernels-only", action="store_true", help="launch only the profiled kernels, then exit")
+    parser.add_argument("--ceilings", action="store_true", help="measure the hardware ceilings, then exit")
+    parser.add_argument("--prewarm-seconds", type=float, default=2.0,
+                        help="untimed replays before the headline's warmup, so clocks are at steady state")
     return parser.parse_args()
 
 
@@ -98,6 +115,103 @@ def gate_up_bytes(tokens: int) -> float:
     return 4.0 * HIDDEN * INTERMEDIATE + 2.0 * tokens * HIDDEN + 2.0 * tokens * INTERMEDIATE
 
 
+def run_ceilings(device) -> dict:
+    """Hardware limits measured with HIP events on the current stream (see the module doc)."""
+
+    import ctypes
+
+    import torch
+
+    from crosspool_amd import build
+    from crosspool_amd.agent import FfnAgent
+    from crosspool_amd.weights import DenseFfnWeights
+
+    probes = ctypes.CDLL(str(build.PROBE_LIBRARY))
+    stream = torch.cuda.current_stream(device)
+    handle = ctypes.c_void_p(stream.cuda_stream)
+
+    def per_launch(launch, repeats: int) -> float:
+        for _ in range(2):
+            launch()
+        begin = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        begin.record(stream)
+        for index in range(repeats):
+            launch(index)
+        end.record(stream)
+        end.synchronize()
+        return begin.elapsed_time(end) / 1e3 / repeats
+
+    def checked(status: int) -> None:
+        if status != 0:
+            raise RuntimeError(f"probe launch failed with status {status}")
+
+    result: dict = {}
+    # bf16 MFMA: 4-wave workgroups, 8 independent 32x32x16 chains per wave.
+    mfma = []
+    for workgroups, rounds in ((1024, 20000), (2048, 20000)):
+        seconds = per_launch(lambda index=0: checked(probes.xp_probe_mfma(workgroups, rounds, handle)), 5)
+        flops = workgroups * 4 * rounds * 8 * 2.0 * 32 * 32 * 16
+        mfma.append({"workgroups": workgroups, "tflops": round(flops / seconds / 1e12, 1)})
+    best = max(point["tflops"] for point in mfma)
+    result["mfma_bf16"] = {"points": mfma, "best_tflops": best, "frac_of_2500": round(best / MFMA_BF16_PEAK_TFLOPS, 4)}
+
+    # HBM reads: a 2 GiB buffer (past the 256 MB last-level cache), 1 KB per wave instruction.
+    buffer = torch.empty(2 << 30, dtype=torch.uint8, device=device)
+    contiguous = []
+    for workgroups in (1024, 2048, 4096, 8192):
+        seconds = per_launch(lambda index=0: checked(probes.xp_probe_read_contiguous(
+            ctypes.c_void_p(buffer.data_ptr()), ctypes.c_uint64(buffer.numel()), workgroups, handle)), 10)
+        contiguous.append({"workgroups": workgroups, "gbs": round(buffer.numel() / seconds / 1e9, 1)})
+    del buffer
+    # The decode weight-stream pattern over three copies of the Qwen3-8B gate_up matrix
+    # ([24576, 4096] bf16, 201 MB each, rotated so each launch streams from HBM).
+    rows, row_bytes = 2 * INTERMEDIATE, 2 * HIDDEN
+    copies = [torch.empty(rows * row_bytes, dtype=torch.uint8, device=device) for _ in range(3)]
+    row_points = []
+    for ranges in (1, 2, 4, 8):
+        seconds = per_launch(lambda index=0: checked(probes.xp_probe_read_rows(
+            ctypes.c_void_p(copies[index % 3].data_ptr()), ctypes.c_int64(rows), ctypes.c_int64(row_bytes), ranges,
+            handle)), 30)
+        row_points.append({"ranges": ranges, "workgroups": (rows // 16 + 7) // 8 * ranges,
+                           "gbs": round(rows * row_bytes / seconds / 1e9, 1)})
+    del copies
+    best_read = max(point["gbs"] for point in contiguous + row_points)
+    result["hbm_read"] = {"contiguous_2gib": contiguous, "weight_rows_qwen3_8b_gate_up": row_points,
+                          "best_gbs": best_read, "frac_of_8000": round(best_read / HBM_PEAK_GBS, 4)}
+
+    # GPU time a hipGraphLaunch adds per replay: one Qwen3-0.6B layer at one row replayed
+    # back to back through direct kernel launches and through its instantiated hipGraph.
+    generator = torch.Generator(device=device).manual_seed(18)
+    graph_points = {}
+    for graph_dispatch in (False, True):
+        with FfnAgent(device, graph_dispatch=graph_dispatch) as agent:
+            agent.register_layer(
+                instance_index=0, layer_ordinal=0,
+                weights=DenseFfnWeights.from_tensors(
+                    (torch.randn((6144, 1024), device=device, generator=generator) * 0.02).bfloat16(),
+                    (torch.randn((1024, 3072), device=device, generator=generator) * 0.02).bfloat16()),
+            )
+            agent.materialize(maximum_row_capacity=1)
+            lane = agent.lanes[0]
+            pool = torch.randn((64, 1024), device=device, generator=generator).bfloat16()
+            slots = torch.arange(1, dtype=torch.int32, device=device)
+            lane_stream = lane.stream
+            begin = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            for _ in range(20):
+                lane.replay(instance_index=0, layer_ordinal=0, pool=pool, slots=slots, stream=lane_stream)
+            begin.record(lane_stream)
+            for _ in range(200):
+                lane.replay(instance_index=0, layer_ordinal=0, pool=pool, slots=slots, stream=lane_stream)
+            end.record(lane_stream)
+            end.synchronize()
+            graph_points["graph" if graph_dispatch else "direct"] = begin.elapsed_time(end) * 1e3 / 200
+    result["replay_us_qwen3_0_6b_t1"] = {key: round(value, 2) for key, value in graph_points.items()}
+    result["graph_launch_extra_us"] = round(graph_points["graph"] - graph_points["direct"], 2)
+    return result
+
+
 def main() -> int:
     args = parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -117,6 +231,9 @@ def main() -> int:
 
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
+    if args.ceilings:
+        print(json.dumps({"ceilings": run_ceilings(device)}), flush=True)
+        return 0
     max_tokens = max(SWEEP + (args.tokens, args.decode_tokens))
 
     pool_cpu = o.generate_hidden_states(POOL_SLOTS, HIDDEN, 17)
@@ -129,20 +246,34 @@ def main() -> int:
 
     agent = FfnAgent(device)
     agent.register_layer(instance_index=0, layer_ordinal=0, weights=weights, norm_weight=norm, eps=1e-6)
+    # Layer 1: the same values in a second copy.  Layer timings at HBM-bound sizes alternate
+    # the two layers, so each replay streams its 302 MB of weights from HBM instead of
+    # partly from the 256 MB last-level cache, as a stack of distinct layers does.
+    agent.register_layer(
+        instance_index=0, layer_ordinal=1,
+        weights=DenseFfnWeights.from_tensors(weights.i_proj.values.clone(), weights.o_proj.values.clone()),
+        norm_weight=norm, eps=1e-6,
+    )
     agent.materialize(maximum_row_capacity=max_tokens)
     lane = agent.lanes[0]
     torch.cuda.synchronize()
 
-    def replay(tokens: int) -> None:
-        lane.replay(instance_index=0, layer_ordinal=0, pool=pool, slots=slots, rows=tokens, stream=lane.stream)
+    def replay(tokens: int, ordinal: int = 0) -> None:
+        lane.replay(instance_index=0, layer_ordinal=ordinal, pool=pool, slots=slots, rows=tokens, stream=lane.stream)
 
-    def time_replays(tokens: int, steps: int, warmup: int) -> float:
-        for _ in range(warmup):
-            replay(tokens)
+    def time_replays(tokens: int, steps: int, warmup: int, prewarm_seconds: float = 0.0) -> float:
+        ordinals = (0, 1) if tokens <= 256 else (0,)
+        deadline = time.perf_counter() + prewarm_seconds
+        while time.perf_counter() < deadline:  # untimed: clocks reach steady state
+            for _ in range(10):
+                replay(tokens)
+            torch.cuda.synchronize()
+        for step in range(warmup):
+            replay(tokens, ordinals[step % len(ordinals)])
         torch.cuda.synchronize()
         start = time.perf_counter()
-        for _ in range(steps):
-            replay(tokens)
+        for step in range(steps):
+            replay(tokens, ordinals[step % len(ordinals)])
         torch.cuda.synchronize()
         return (time.perf_counter() - start) / steps
 
@@ -209,12 +340,12 @@ def main() -> int:
         return 0
 
     # ---------------------------------------------------------------- headline
-    seconds = time_replays(tokens, args.steps, args.warmup)
+    seconds = time_replays(tokens, args.steps, args.warmup, prewarm_seconds=args.prewarm_seconds)
     agent.check_health()
     roofline = kernel_roofline(tokens, max(20, min(args.steps, 200)))
 
     # ---------------------------------------------------------------- decode point
-    decode_seconds = time_replays(args.decode_tokens, args.steps, args.warmup)
+    decode_seconds = time_replays(args.decode_tokens, args.steps, args.warmup, prewarm_seconds=0.5)
     decode = {
         "tokens": args.decode_tokens,
         "tokens_per_s": round(args.decode_tokens / decode_seconds, 1),
@@ -330,6 +461,119 @@ def main() -> int:
         stack_agent.close()
         del stack_pool
 
+    # ---------------------------------------------------------------- config 5 shard
+    # the unreduced partial of one Qwen3-32B TP shard (hidden 5120, shard
+    # intermediate 3200) at T = 8, 512, 8192 rows of an 8192-slot mailbox, written to a
+    # separate output mailbox; weight copies rotated per replay.
+    shard = None
+    if not args.no_sweep:
+        p_hidden, p_inter = SHARD_SHAPE
+        generator = torch.Generator(device=device).manual_seed(18)
+        shard_agent = FfnAgent(device)
+        base_gate_up = (torch.randn((2 * p_inter, p_hidden), device=device, generator=generator) * 0.02).bfloat16()
+        base_down = (torch.randn((p_hidden, p_inter), device=device, generator=generator) * 0.02).bfloat16()
+        for ordinal in range(SHARD_COPIES):
+            shard_agent.register_layer(
+                instance_index=0, layer_ordinal=ordinal,
+                weights=DenseFfnWeights.from_tensors(base_gate_up.clone(), base_down.clone()),
+            )
+        shard_agent.materialize(maximum_row_capacity=max(SHARD_TOKENS))
+        shard_lane = shard_agent.lanes[0]
+        shard_pool = torch.randn((max(SHARD_TOKENS), p_hidden), device=device, generator=generator).bfloat16()
+        shard_out = torch.empty_like(shard_pool)
+        shard_slots = torch.randperm(max(SHARD_TOKENS), device=device, generator=generator).int()
+        shard = {"hidden": p_hidden, "shard_intermediate": p_inter, "tp_shards": 8, "points": []}
+        for t in SHARD_TOKENS:
+            def shard_replay(step: int) -> None:
+                shard_lane.replay(instance_index=0, layer_ordinal=step % SHARD_COPIES, pool=shard_pool,
+                                  out_pool=shard_out, slots=shard_slots, rows=t, stream=shard_lane.stream)
+
+            steps = max(20, min(200, 400000 // t))
+            for step in range(10):
+                shard_replay(step)
+            torch.cuda.synchronize()
+            started = time.perf_counter()
+            for step in range(steps):
+                shard_replay(step)
+            torch.cuda.synchronize()
+            per = (time.perf_counter() - started) / steps
+            p_bytes = 6.0 * p_hidden * p_inter + 4.0 * t * p_hidden + 4.0 * t
+            p_flops = 6.0 * t * p_hidden * p_inter
+            shard["points"].append({
+                "tokens": t, "us": round(per * 1e6, 2), "tokens_per_s": round(t / per, 1),
+                "hbm_frac": round(p_bytes / per / 1e9 / HBM_PEAK_GBS, 4),
+                "mfma_frac": round(p_flops / per / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+                "bound": "hbm" if t <= 64 else "mfma",
+            })
+        shard_agent.check_health()
+        shard_agent.close()
+        del shard_pool, shard_out, base_gate_up, base_down
+
+    # ---------------------------------------------------------------- config 4 co-location
+    # a Qwen3-1.7B-shaped and a Qwen3-4B-shaped layer on one GPU, each on
+    # its own Lane (own stream).  Per step each instance submits T ~ U{1..512} rows (seeded)
+    # from a disjoint half of an 8192-slot mailbox of its width; both Lanes replay
+    # concurrently.  Each model rotates through distinct weight copies.  Reported: per-model
+    # tokens/s with the Lanes concurrent and alone, and the combined HBM fraction.
+    colocated = None
+    if not args.no_sweep:
+        import numpy as np
+
+        rng = np.random.default_rng(7)
+        generator = torch.Generator(device=device).manual_seed(18)
+        co_agent = FfnAgent(device, executor_lane_count=2)
+        co_pools, co_slots = [], []
+        for instance, (c_hidden, c_inter) in enumerate(COLOCATED_SHAPES):
+            for ordinal in range(COLOCATED_LAYERS):
+                co_agent.register_layer(
+                    instance_index=instance, layer_ordinal=ordinal,
+                    weights=DenseFfnWeights.from_tensors(
+                        (torch.randn((2 * c_inter, c_hidden), device=device, generator=generator) * 0.02).bfloat16(),
+                        (torch.randn((c_hidden, c_inter), device=device, generator=generator) * 0.02).bfloat16()),
+                    norm_weight=(1 + 0.1 * torch.randn(c_hidden, device=device, generator=generator)).bfloat16(),
+                )
+            co_pools.append(torch.randn((8192, c_hidden), device=device, generator=generator).bfloat16())
+            first = instance * 4096
+            co_slots.append((first + torch.randperm(4096, device=device, generator=generator)).int())
+        co_agent.materialize(maximum_row_capacity=COLOCATED_MAX_ROWS)
+        rows_per_step = rng.integers(1, COLOCATED_MAX_ROWS + 1, size=(COLOCATED_STEPS, 2))
+
+        def run_steps(instances: tuple[int, ...]) -> float:
+            torch.cuda.synchronize()
+            started = time.perf_counter()
+            for step in range(COLOCATED_STEPS):
+                for instance in instances:
+                    lane = co_agent.lanes[instance]
+                    lane.replay(instance_index=instance, layer_ordinal=step % COLOCATED_LAYERS,
+                                pool=co_pools[instance], slots=co_slots[instance],
+                                rows=int(rows_per_step[step, instance]), stream=lane.stream)
+            torch.cuda.synchronize()
+            return time.perf_counter() - started
+
+        run_steps((0, 1))  # warm-up
+        together = run_steps((0, 1))
+        alone = [run_steps((instance,)) for instance in range(2)]
+        co_agent.check_health()
+        colocated = {"steps": COLOCATED_STEPS, "rows_per_step": "U{1..512} per model, seed 7", "models": []}
+        total_bytes = 0.0
+        for instance, (c_hidden, c_inter) in enumerate(COLOCATED_SHAPES):
+            rows = rows_per_step[:, instance].astype(float)
+            model_bytes = float(sum(6.0 * c_hidden * c_inter + 4.0 * r * c_hidden + 4.0 * r for r in rows))
+            model_flops = float(sum(6.0 * r * c_hidden * c_inter for r in rows))
+            total_bytes += model_bytes
+            colocated["models"].append({
+                "hidden": c_hidden, "intermediate": c_inter, "tokens": int(rows.sum()),
+                "tokens_per_s_concurrent": round(rows.sum() / together, 1),
+                "tokens_per_s_alone": round(rows.sum() / alone[instance], 1),
+                "us_per_step_alone": round(alone[instance] / COLOCATED_STEPS * 1e6, 2),
+                "hbm_frac_alone": round(model_bytes / alone[instance] / 1e9 / HBM_PEAK_GBS, 4),
+                "mfma_frac_alone": round(model_flops / alone[instance] / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+            })
+        colocated["us_per_step_concurrent"] = round(together / COLOCATED_STEPS * 1e6, 2)
+        colocated["combined_hbm_frac_concurrent"] = round(total_bytes / together / 1e9 / HBM_PEAK_GBS, 4)
+        co_agent.close()
+        del co_pools, co_slots
+
     # ---------------------------------------------------------------- MoE layer
     # Qwen3-30B-A3B-shaped MoE layer (no BASELINE config names one; reported beside the
     # Dense path): Router (128 experts, softmax top-8, renormalised) + Experts (hidden 2048,
@@ -417,42 +661,50 @@ def main() -> int:
         agent.check_health()
 
     # ---------------------------------------------------------------- CPU baseline
+    # The oracle's torch-CPU restatement of one mailbox step (gather, RMSNorm, fp32 matmuls
+    # with the reference's bf16 stage rounding, scatter) on every affinity core of the host,
+    # at the headline and at each sweep point: 3 untimed runs, then the median of 10.
     cpu_baseline = None
     if not args.no_cpu_baseline:
         threads = len(os.sched_getaffinity(0))
         torch.set_num_threads(threads)
-        sample_tokens = 256
         gate_up_f32 = w_gate_up.float()
         down_f32 = w_down.float()
-        sample_slots = slots_cpu[:sample_tokens]
         work_pool = pool_cpu.clone()
 
-        def cpu_step() -> None:
-            x = o.rmsnorm(o.gather(work_pool, sample_slots), norm_weight, 1e-6)
+        def cpu_step(rows: int) -> None:
+            index = torch.from_numpy(slots_cpu[:rows].astype("int64"))
+            x = o.rmsnorm(work_pool[index], norm_weight, 1e-6)
             projected = torch.mm(x.float(), gate_up_f32.t())
             activated = o.gated_silu(projected[:, 0::2].bfloat16(), projected[:, 1::2].bfloat16())
-            y = torch.mm(activated.float(), down_f32.t()).bfloat16()
-            o.scatter(work_pool, sample_slots, y)
+            work_pool[index] = torch.mm(activated.float(), down_f32.t()).bfloat16()
 
-        for _ in range(2):
-            cpu_step()
-        durations = []
-        deadline = time.perf_counter() + args.cpu_seconds
-        while len(durations) < 3 or time.perf_counter() < deadline:
-            started = time.perf_counter()
-            cpu_step()
-            durations.append(time.perf_counter() - started)
-        median = statistics.median(durations)
+        cpu_points = []
+        for t in sorted(set(SWEEP + (tokens,))):
+            for _ in range(3):
+                cpu_step(t)
+            durations = []
+            for _ in range(10):
+                started = time.perf_counter()
+                cpu_step(t)
+                durations.append(time.perf_counter() - started)
+            median = statistics.median(durations)
+            cpu_points.append({
+                "tokens": t, "tokens_per_s": round(t / median, 1), "ms": round(median * 1e3, 2),
+                "gbs": round(layer_bytes(t) / median / 1e9, 2), "gflops": round(layer_flops(t) / median / 1e9, 1),
+            })
+        headline_cpu = next(point for point in cpu_points if point["tokens"] == tokens)
         cpu_baseline = {
-            "value": round(sample_tokens / median, 1),
+            "value": headline_cpu["tokens_per_s"],
             "unit": "tokens/s",
             "cores": torch.get_num_threads(),
             "kind": "port",
             "sample": (
-                f"{len(durations)} runs of one {sample_tokens}-token Qwen3-8B mailbox step (gather, RMSNorm, fp32 "
-                f"matmuls with bf16 stage rounding, scatter) on {threads} affinity cores of {os.cpu_count()}; "
-                "median; weights pre-widened to fp32 outside the timing"
+                f"one {tokens}-token Qwen3-8B mailbox step (gather, RMSNorm, fp32 matmuls with bf16 stage rounding, "
+                f"scatter), 3 warm-up runs then the median of 10, on {threads} affinity cores of {os.cpu_count()}; "
+                "weights pre-widened to fp32 outside the timing; 'points' repeats it at every sweep size"
             ),
+            "points": cpu_points,
         }
 
     result = {
@@ -487,6 +739,8 @@ def main() -> int:
         "shim": shim,
         "moe": moe,
         "config2_stack": stack,
+        "config4_colocated": colocated,
+        "config5_shard": shard,
     }
     agent.close()
     print(json.dumps(result), flush=True)

@@ -78,7 +78,7 @@ class ExecutorLane:
         )
         self.handle = handle
         # Replays launch the template's kernels directly unless graph dispatch is asked for
-        # (each hipGraphLaunch costs ~13 us of GPU idle time on ROCm; same kernels either way).
+        # (each hipGraphLaunch adds ~9 us of GPU time per replay on ROCm; same kernels either way).
         self.graph_dispatch = bool(graph_dispatch)
         _native.call("xp_lane_set_graph_dispatch", self.handle, int(self.graph_dispatch))
         stream = ctypes.c_void_p()

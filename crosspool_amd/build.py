@@ -19,6 +19,9 @@ PACKAGE_DIR = Path(__file__).resolve().parent
 SOURCE_DIR = PACKAGE_DIR / "csrc"
 OBJECT_DIR = PACKAGE_DIR / "_build"
 LIBRARY = PACKAGE_DIR / "_lib" / "libxpool_amd.so"
+# Hardware-ceiling probes launched by `bench.py --ceilings` (not part of the C ABI).
+PROBE_SOURCE = PACKAGE_DIR / "probes" / "ceilings.hip"
+PROBE_LIBRARY = PACKAGE_DIR / "_lib" / "libxpool_probes.so"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -48,21 +51,26 @@ def _compile(source: Path) -> Path:
     return target
 
 
+def _link(objects: list[Path], library: Path) -> None:
+    temporary = library.with_name(library.name + ".tmp")
+    command = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(temporary)]
+    result = subprocess.run(command, capture_output=True, text=True)
+    if result.returncode != 0:
+        raise RuntimeError(f"hipcc link of {library.name} failed:\n{result.stderr}")
+    temporary.replace(library)
+
+
 def build(verbose: bool = False) -> Path:
-    """Compile every HIP source and link the shared library; returns its path."""
+    """Compile every HIP source and link the shared library (and the probe library); returns its path."""
 
     OBJECT_DIR.mkdir(parents=True, exist_ok=True)
     LIBRARY.parent.mkdir(parents=True, exist_ok=True)
     units = sources()
     workers = min(len(units), max(1, min(os.cpu_count() or 1, 8)))
     with ThreadPoolExecutor(max_workers=workers) as pool:
-        objects = list(pool.map(_compile, units))
-    temporary = LIBRARY.with_name(LIBRARY.name + ".tmp")
-    command = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(temporary)]
-    result = subprocess.run(command, capture_output=True, text=True)
-    if result.returncode != 0:
-        raise RuntimeError(f"hipcc link failed:\n{result.stderr}")
-    temporary.replace(LIBRARY)
+        objects = list(pool.map(_compile, [*units, PROBE_SOURCE]))
+    _link(objects[:-1], LIBRARY)
+    _link(objects[-1:], PROBE_LIBRARY)
     if verbose:
         print(f"built {LIBRARY}", file=sys.stderr)
     return LIBRARY

@@ -1,0 +1,152 @@
+// Hardware ceilings of the MI355X that the kernel design is measured against, launched by
+// `bench.py --ceilings` (a separate library, libxpool_probes.so: none of this is on the
+// FfnAgent path).
+//
+//  * probe_mfma: every wave issues rounds of 8 independent v_mfma_f32_32x32x16_bf16 on
+//    register operands, no memory traffic: the sustained bf16 matrix rate of the chip at the
+//    clock it holds under that load.
+//  * probe_read_contiguous: a grid-stride read of a buffer, each wave instruction 1 KB of
+//    consecutive bytes, UNROLL loads in flight per lane: the HBM read rate of the plainest
+//    streaming pattern.
+//  * probe_read_rows: the weight-streaming pattern of the decode projection kernels: a wave
+//    owns 16 rows of a row-major matrix and reads 16 rows x 64 contiguous bytes per
+//    instruction, four 256-byte chunks per row in flight; grid y splits each row into
+//    `ranges` contiguous parts (more workgroups for the same bytes).
+//
+// Each kernel folds what it reads (or computes) into registers and stores it only when
+// `write` is set, which the host never does; the compiler cannot drop the work.
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace {
+
+using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
+using bf16x8 = __bf16 __attribute__((ext_vector_type(8)));
+using f32x16 = float __attribute__((ext_vector_type(16)));
+
+constexpr int kMfmaChains = 8;
+
+__global__ __launch_bounds__(256) void probe_mfma_kernel(int rounds, float *sink, int write) {
+  bf16x8 a;
+  bf16x8 b;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    a[i] = static_cast<__bf16>(static_cast<float>((threadIdx.x + i) & 7) * 0.125f);
+    b[i] = static_cast<__bf16>(static_cast<float>((threadIdx.x * 3 + i) & 7) * 0.0625f);
+  }
+  f32x16 acc[kMfmaChains];
+#pragma unroll
+  for (int c = 0; c < kMfmaChains; ++c) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      acc[c][r] = 0.0f;
+    }
+  }
+  for (int round = 0; round < rounds; ++round) {
+#pragma unroll
+    for (int c = 0; c < kMfmaChains; ++c) {
+      acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[c], 0, 0, 0);
+    }
+  }
+  if (write) {
+    float total = 0.0f;
+#pragma unroll
+    for (int c = 0; c < kMfmaChains; ++c) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        total += acc[c][r];
+      }
+    }
+    sink[blockIdx.x * blockDim.x + threadIdx.x] = total;
+  }
+}
+
+template <int UNROLL>
+__global__ __launch_bounds__(256) void probe_read_contiguous_kernel(const u32x4 *source, uint64_t vectors,
+                                                                    uint32_t *sink, int write) {
+  const uint64_t thread = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+  u32x4 folded = {0u, 0u, 0u, 0u};
+  for (uint64_t first = thread; first < vectors; first += stride * UNROLL) {
+    u32x4 values[UNROLL];
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const uint64_t index = first + u * stride;
+      values[u] = index < vectors ? source[index] : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      folded ^= values[u];
+    }
+  }
+  if (write) {
+    sink[thread] = folded[0] ^ folded[1] ^ folded[2] ^ folded[3];
+  }
+}
+
+// 8 waves per workgroup, wave w of workgroup x owns row block 8 x + w (16 rows); grid y is
+// the part of each row (row_bytes / ranges bytes, a multiple of 1 KB).
+__global__ __launch_bounds__(512) void probe_read_rows_kernel(const char *matrix, int64_t rows, int64_t row_bytes,
+                                                              int64_t part_bytes, uint32_t *sink, int write) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t block = static_cast<int64_t>(blockIdx.x) * 8 + wave;
+  if (block * 16 >= rows) {
+    return;
+  }
+  const char *row = matrix + (block * 16 + (lane & 15)) * row_bytes + blockIdx.y * part_bytes + (lane >> 4) * 16;
+  u32x4 folded = {0u, 0u, 0u, 0u};
+  for (int64_t column = 0; column < part_bytes; column += 1024) {
+    u32x4 values[16];
+#pragma unroll
+    for (int chunk = 0; chunk < 4; ++chunk) {
+#pragma unroll
+      for (int piece = 0; piece < 4; ++piece) {
+        values[chunk * 4 + piece] =
+            *reinterpret_cast<const u32x4 *>(row + column + chunk * 256 + piece * 64);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      folded ^= values[i];
+    }
+  }
+  if (write) {
+    sink[(blockIdx.y * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x] = folded[0] ^ folded[1] ^ folded[2] ^ folded[3];
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+// rounds of 8 MFMAs per wave over `workgroups` 4-wave workgroups.
+int xp_probe_mfma(int workgroups, int rounds, void *stream) {
+  hipLaunchKernelGGL(probe_mfma_kernel, dim3(workgroups), dim3(256), 0, static_cast<hipStream_t>(stream), rounds,
+                     static_cast<float *>(nullptr), 0);
+  return static_cast<int>(hipGetLastError());
+}
+
+// Reads `bytes` (a multiple of 16) from `source` with `workgroups` 256-thread workgroups.
+int xp_probe_read_contiguous(const void *source, uint64_t bytes, int workgroups, void *stream) {
+  hipLaunchKernelGGL(probe_read_contiguous_kernel<8>, dim3(workgroups), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const u32x4 *>(source), bytes / 16, static_cast<uint32_t *>(nullptr), 0);
+  return static_cast<int>(hipGetLastError());
+}
+
+// Reads a [rows, row_bytes] matrix (rows a multiple of 16, row_bytes a multiple of
+// 1024 * ranges) in the weight-streaming pattern.
+int xp_probe_read_rows(const void *matrix, int64_t rows, int64_t row_bytes, int ranges, void *stream) {
+  if (rows % 16 != 0 || ranges < 1 || row_bytes % (1024 * static_cast<int64_t>(ranges)) != 0) {
+    return -1;
+  }
+  const dim3 grid(static_cast<unsigned>((rows / 16 + 7) / 8), static_cast<unsigned>(ranges));
+  hipLaunchKernelGGL(probe_read_rows_kernel, grid, dim3(512), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const char *>(matrix), rows, row_bytes, row_bytes / ranges,
+                     static_cast<uint32_t *>(nullptr), 0);
+  return static_cast<int>(hipGetLastError());
+}
+
+}  // extern "C"
