@@ -24,6 +24,26 @@ XP_ERROR_CAPACITY = 5
 XP_ERROR_UNSUPPORTED = 6
 XP_FAULT_SLOT_OUT_OF_RANGE = 1
 
+class ActivationDesc(ctypes.Structure):
+    """``xp_activation_desc`` of the header."""
+
+    _fields_ = [
+        ("function", ctypes.c_int),
+        ("approximate_tanh", ctypes.c_int),
+        ("gated", ctypes.c_int),
+        ("has_limit", ctypes.c_int),
+        ("alpha", ctypes.c_float),
+        ("limit", ctypes.c_float),
+        ("up_offset", ctypes.c_float),
+    ]
+
+
+XP_DTYPE_BF16 = 1
+XP_DTYPE_F16 = 2
+XP_DTYPE_F32 = 3
+XP_GATE_UP_CONCATENATED = 1
+XP_GATE_UP_INTERLEAVED = 2
+
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 _INT = ctypes.c_int
@@ -41,6 +61,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "xp_gemm_gate_up_silu": (_INT, [_P, _I64, _I64, _P, _I64, _P, _F32, _F32, _F32, _P, _SIZE, _P]),
     "xp_gemm_down": (_INT, [_P, _I64, _I64, _P, _I64, _P, _P, _I64, _P, _SIZE, _P]),
     "xp_gemm_workspace_bytes": (_SIZE, [_I64, _I64, _I64, _INT]),
+    "xp_projection": (_INT, [_P, _I64, _I64, _P, _I64, _P, _P, _INT, ctypes.POINTER(ActivationDesc), _P]),
+    "xp_activation": (_INT, [_P, _P, _I64, _I64, _INT, _INT, ctypes.POINTER(ActivationDesc), _P]),
     "xp_dense_workspace_bytes": (_SIZE, [_I64, _I64, _I64]),
     "xp_dense_workspace_layout": (_INT, [_I64, _I64, _I64, ctypes.POINTER(_SIZE)]),
     "xp_dense_step": (_INT, [_P, _P, _I64, _P, _I64, _I64, _I64, _P, _P, _P, _F32, _P, _SIZE, _P, _P]),

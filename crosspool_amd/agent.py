@@ -263,6 +263,11 @@ class FfnAgent:
 
         if weights.device != self.device:
             raise ValueError("local FFN resources must reside on the agent's device")
+        if not weights.template_ready:
+            raise ValueError(
+                "captured Dense templates take gated bf16 INTERLEAVED weights without biases and 16-byte rows; "
+                "run other layers through crosspool_amd.operators"
+            )
         if norm_weight is not None:
             validate_weight_tensor(norm_weight, name="RMSNorm weight")
             if norm_weight.dtype is not torch.bfloat16 or tuple(norm_weight.shape) != (weights.hidden_size,):

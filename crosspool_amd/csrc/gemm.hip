@@ -709,6 +709,10 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
 }
 
+// Lambdas of the kernels below are forced inline: a lambda left out of line takes the
+// accumulator array by reference, which then lives in scratch memory instead of registers.
+#define XP_INLINE __attribute__((always_inline))
+
 // Calls f(std::integral_constant<int, 0>{}) .. f(std::integral_constant<int, N - 1>{}).
 template <class F, int... I>
 __device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, I...>) {
@@ -1043,7 +1047,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
   // WAVES_N) holds weight row 2 (wq * G / 2 + jj) + s, i.e. within an 8-row group the weight
   // row is the group's first weight row plus 2 (i / 8).
   constexpr int B_ROW_STEP = GATED ? 2 : 1;
-  auto b_group_row = [](int p) {
+  auto b_group_row = [](int p) XP_INLINE {
     if constexpr (GATED) {
       constexpr int group = BN / WAVES_N;
       return 2 * ((p / group) * (group / 2) + p % (group / 2)) + (p % group) / (group / 2);
@@ -1054,7 +1058,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
   // Slab kt of this workgroup's K range.  Slabs at or past the range end (the prologue of
   // a short range, the refills after the last slab) load zeros without memory traffic.
   // PART selects the A loads (1), the B loads (2) or both (3).
-  auto issue_part = [&](int64_t kt, int stage, auto part) {
+  auto issue_part = [&](int64_t kt, int stage, auto part) XP_INLINE {
     constexpr int PART = decltype(part)::value;
     const int64_t k_pos = k_begin + kt * BK;
     const uint32_t k_bytes = static_cast<uint32_t>(k_pos * 2);
@@ -1086,7 +1090,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
       buffer_load_lds16(b_rsrc, b_stage + g * BK, chunk < chunks_left ? offset : kOutOfRange, k_bytes);
     }
   };
-  auto issue_loads = [&](int64_t kt, int stage) { issue_part(kt, stage, std::integral_constant<int, 3>{}); };
+  auto issue_loads = [&](int64_t kt, int stage) XP_INLINE { issue_part(kt, stage, std::integral_constant<int, 3>{}); };
 
   f32x16 acc[MT][NT];
 #pragma unroll
@@ -1142,7 +1146,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
   bf16x8 bfrag[3][NT];
   // A grouped tile's wave whose rows all lie past the expert's last route reads no
   // fragments and issues no MFMAs (one wave-uniform branch around the unrolled loops).
-  auto read_fragments = [&](int stage, int ks, int slot) {
+  auto read_fragments = [&](int stage, int ks, int slot) XP_INLINE {
     if (!wave_live) {
       return;
     }
@@ -1159,7 +1163,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
           *reinterpret_cast<const u32x4 *>(lds_bytes + b_base[offset >> 16][ks] + (offset & 0xffff)));
     }
   };
-  auto mfma_step = [&](int slot) {
+  auto mfma_step = [&](int slot) XP_INLINE {
     if (!wave_live) {
       return;
     }
@@ -1176,7 +1180,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
   // also drain) and for its own LDS reads, so that after it every wave may read the next
   // slab and refill the stage just read.  The memory clobber keeps the compiler from
   // moving LDS accesses across it; the scheduling barriers keep instructions on their side.
-  auto stage_barrier = [] {
+  auto stage_barrier = []() XP_INLINE {
     constexpr int N = LOADS * (STAGES - 2);
     __builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4));  // vmcnt(N) lgkmcnt(0)
     __builtin_amdgcn_sched_barrier(0);
@@ -1214,7 +1218,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
   // constants.  The loading and the other waves run the same loop (the same barriers),
   // with and without the refills, as separate code so that each has a fixed interleave.
   constexpr int UNROLL = STAGES % 3 == 0 ? STAGES : 3 * STAGES;
-  auto slab = [&](auto index, auto loads, int64_t kt) {
+  auto slab = [&](auto index, auto loads, int64_t kt) XP_INLINE {
     constexpr int P = decltype(index)::value % 3;
     constexpr int S = decltype(index)::value % STAGES;
     constexpr int NEXT = (S + 1) % STAGES;
@@ -1263,12 +1267,12 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
     __builtin_amdgcn_sched_barrier(0);
   };
   int64_t kt = 0;
-  auto main_loop = [&](auto loads) {
+  auto main_loop = [&](auto loads) XP_INLINE {
     for (; kt + UNROLL < ktiles; kt += UNROLL) {
-      static_for<UNROLL>([&](auto j) { slab(j, loads, kt + decltype(j)::value); });
+      static_for<UNROLL>([&](auto j) XP_INLINE { slab(j, loads, kt + decltype(j)::value); });
     }
     // The remaining slabs before the last (fewer than UNROLL), continuing the pattern.
-    static_for<UNROLL - 1>([&](auto j) {
+    static_for<UNROLL - 1>([&](auto j) XP_INLINE {
       if (kt + decltype(j)::value + 1 < ktiles) {
         slab(j, loads, kt + decltype(j)::value);
       }
@@ -1280,7 +1284,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
     main_loop(std::false_type{});
   }
   // Last slab (index ktiles - 1): no barrier and no refill.
-  static_for<UNROLL>([&](auto j) {
+  static_for<UNROLL>([&](auto j) XP_INLINE {
     if ((ktiles - 1) % UNROLL == decltype(j)::value) {
       constexpr int P = decltype(j)::value % 3;
       constexpr int S = decltype(j)::value % STAGES;

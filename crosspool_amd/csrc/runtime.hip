@@ -13,6 +13,7 @@
 // records with hipGraphExecKernelNodeSetParams and launches the graph.
 
 #include <algorithm>
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <memory>
@@ -582,6 +583,113 @@ int xp_gemm_down(const void *activated, int64_t rows, int64_t intermediate, cons
     return status;
   }
   return launch_gemm(make_gemm(args, rows, false, choice), static_cast<hipStream_t>(stream));
+}
+
+namespace {
+
+size_t dtype_bytes(int dtype) {
+  switch (dtype) {
+    case XP_DTYPE_BF16:
+    case XP_DTYPE_F16:
+      return 2;
+    case XP_DTYPE_F32:
+      return 4;
+    default:
+      return 0;
+  }
+}
+
+bool aligned_to(const void *pointer, size_t bytes) { return (reinterpret_cast<uintptr_t>(pointer) % bytes) == 0; }
+
+// The activation descriptor of the C ABI as the kernels take it (checked).
+int activation_record(const xp_activation_desc *desc, ActivationArgs &out) {
+  out = ActivationArgs{};
+  if (desc == nullptr) {
+    out.function = kActivationNone;
+    return XP_OK;
+  }
+  XP_REQUIRE(desc->function == XP_ACTIVATION_SILU || desc->function == XP_ACTIVATION_RELU ||
+                 desc->function == XP_ACTIVATION_GELU,
+             "activation function must be SiLU, ReLU or GELU");
+  XP_REQUIRE(desc->function != XP_ACTIVATION_SILU || (desc->alpha > 0.0f && std::isfinite(desc->alpha)),
+             "SiLU alpha must be positive and finite");
+  XP_REQUIRE(!desc->has_limit || (desc->limit > 0.0f && std::isfinite(desc->limit)), "gate limit must be positive");
+  XP_REQUIRE(std::isfinite(desc->up_offset), "up offset must be finite");
+  XP_REQUIRE(desc->gated || (!desc->has_limit && desc->up_offset == 0.0f),
+             "a gate transform needs a gated activation");
+  out.function = desc->function;
+  out.approximate_tanh = desc->approximate_tanh != 0;
+  out.gated = desc->gated != 0;
+  out.has_limit = desc->has_limit != 0;
+  out.alpha = desc->alpha;
+  out.limit = desc->has_limit ? desc->limit : 0.0f;
+  out.up_offset = desc->up_offset;
+  return XP_OK;
+}
+
+}  // namespace
+
+int xp_projection(const void *x, int64_t rows, int64_t k, const void *w, int64_t n, const float *bias, void *out,
+                  int dtype, const xp_activation_desc *activation, xp_stream_t stream) {
+  XP_REQUIRE(rows >= 0 && k > 0 && n > 0, "projection rows must be non-negative and K, N positive");
+  const size_t element = dtype_bytes(dtype);
+  XP_REQUIRE(element != 0, "payload dtype must be bf16, fp16 or fp32");
+  ProjectionArgs args{};
+  if (const int status = activation_record(activation, args.act); status != XP_OK) {
+    return status;
+  }
+  XP_REQUIRE(!args.act.gated || n % 2 == 0, "a gated projection needs an even number of (INTERLEAVED) weight rows");
+  if (rows == 0) {
+    return XP_OK;
+  }
+  XP_REQUIRE(x != nullptr && w != nullptr && out != nullptr, "projection pointers must be non-null");
+  XP_REQUIRE(aligned_to(x, element) && aligned_to(w, element) && aligned_to(out, element) &&
+                 (bias == nullptr || aligned_to(bias, 4)),
+             "projection operands must be aligned to their element size");
+  args.x = x;
+  args.w = w;
+  args.bias = bias;
+  args.out = out;
+  args.rows = rows;
+  args.n = n;
+  args.k = k;
+  args.dtype = dtype;
+  XP_HIP_CHECK(launch(make_projection(args), static_cast<hipStream_t>(stream)));
+  return XP_OK;
+}
+
+int xp_activation(const void *inputs, void *output, int64_t rows, int64_t width, int dtype, int order,
+                  const xp_activation_desc *activation, xp_stream_t stream) {
+  XP_REQUIRE(activation != nullptr, "activation descriptor must be non-null");
+  XP_REQUIRE(rows >= 0 && width >= 0, "activation extents must be non-negative");
+  XP_REQUIRE(dtype == XP_DTYPE_BF16 || dtype == XP_DTYPE_F16, "standalone activations take bf16 or fp16 payloads");
+  ActivationLaunchArgs args{};
+  if (const int status = activation_record(activation, args.act); status != XP_OK) {
+    return status;
+  }
+  XP_REQUIRE(!args.act.gated || order == XP_GATE_UP_INTERLEAVED || order == XP_GATE_UP_CONCATENATED,
+             "gated activation requires a Gate/Up order");
+  const int64_t elements = rows * width;
+  if (elements == 0) {
+    return XP_OK;
+  }
+  XP_REQUIRE(inputs != nullptr && output != nullptr, "activation pointers must be non-null");
+  XP_REQUIRE(aligned_to(inputs, 2) && aligned_to(output, 2), "activation payloads must be 2-byte aligned");
+  const uintptr_t in_begin = reinterpret_cast<uintptr_t>(inputs);
+  const uintptr_t in_end = in_begin + static_cast<uintptr_t>(elements * (args.act.gated ? 2 : 1) * 2);
+  const uintptr_t out_begin = reinterpret_cast<uintptr_t>(output);
+  const uintptr_t out_end = out_begin + static_cast<uintptr_t>(elements * 2);
+  const bool overlap = in_begin < out_end && out_begin < in_end;
+  XP_REQUIRE(!overlap || (!args.act.gated && in_begin == out_begin),
+             "only an ungated activation may run in place, and only on the same range");
+  args.inputs = inputs;
+  args.output = output;
+  args.elements = elements;
+  args.width = width;
+  args.dtype = dtype;
+  args.interleaved = order == XP_GATE_UP_INTERLEAVED;
+  XP_HIP_CHECK(launch(make_activation(args), static_cast<hipStream_t>(stream)));
+  return XP_OK;
 }
 
 size_t xp_dense_workspace_bytes(int64_t capacity, int64_t hidden, int64_t intermediate) {

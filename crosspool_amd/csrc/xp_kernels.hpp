@@ -254,6 +254,55 @@ KernelLaunch make_gather(const GatherArgs &args, int64_t capacity);
 KernelLaunch make_scatter(const ScatterArgs &args, int64_t capacity);
 bool gather_supported(int64_t hidden);
 
+// ---------------------------------------------------------------- general projection, activation
+// Payload dtypes and activation functions of the operator contract (values of the C ABI's
+// XP_DTYPE_* and of src/xpool/ffn.py ActivationKind: SILU 1, RELU 2, GELU 3).
+constexpr int kDtypeBf16 = 1;
+constexpr int kDtypeF16 = 2;
+constexpr int kDtypeF32 = 3;
+constexpr int kActivationNone = 0;
+constexpr int kActivationSilu = 1;
+constexpr int kActivationRelu = 2;
+constexpr int kActivationGelu = 3;
+
+struct ActivationArgs {
+  int32_t function;          // kActivation*
+  int32_t approximate_tanh;  // GELU: tanh approximation instead of erf
+  int32_t gated;             // Gate/Up pairs: out = f(min(g, limit)) * (clamp(u) + up_offset)
+  int32_t has_limit;
+  float alpha;               // SiLU slope
+  float limit;
+  float up_offset;
+};
+
+// out = epilogue(bias + x . w^T): x [rows, k], w [n, k], out [rows, n] (gated: [rows, n / 2],
+// weights INTERLEAVED), all of `dtype`; bias fp32 [n] or null.
+struct ProjectionArgs {
+  const void *x;
+  const void *w;
+  const float *bias;
+  void *out;
+  int64_t rows;
+  int64_t n;
+  int64_t k;
+  int32_t dtype;
+  ActivationArgs act;
+};
+
+// output [elements] = activation of inputs ([elements] ungated, [rows, 2 width] gated).
+struct ActivationLaunchArgs {
+  const void *inputs;
+  void *output;
+  int64_t elements;
+  int64_t width;     // gated: output columns per row
+  int32_t dtype;
+  int32_t interleaved;
+  ActivationArgs act;
+};
+
+KernelLaunch make_projection(const ProjectionArgs &args);
+KernelLaunch make_activation(const ActivationLaunchArgs &args);
+
 // ---------------------------------------------------------------- GEMMs
 // out[t, :] = epilogue(sum_k x[t, k] * w[n, k]) for the live rows t < rows.
 // With `gated`, w rows are interleaved Gate/Up (row 2j = gate_j, row 2j+1 = up_j)

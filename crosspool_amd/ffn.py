@@ -111,6 +111,26 @@ class SiluActivation:
 
 
 @dataclass(frozen=True)
+class ReluActivation:
+    """ReLU of one projection, NaN payloads kept (src/xpool/ffn.py:140-143)."""
+
+    kind = ActivationKind.RELU
+
+
+@dataclass(frozen=True)
+class GeluActivation:
+    """GELU with the erf definition (``"none"``) or the tanh approximation (ffn.py:146-150)."""
+
+    approximate: str = "none"
+
+    def __post_init__(self) -> None:
+        if self.approximate not in ("none", "tanh"):
+            raise ValueError("GELU approximation must be 'none' or 'tanh'")
+
+    kind = ActivationKind.GELU
+
+
+@dataclass(frozen=True)
 class GateTransform:
     """Clip Gate above ``limit``, Up to ``[-limit, limit]``, then add ``up_offset`` (ffn.py:130-137)."""
 

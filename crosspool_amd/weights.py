@@ -18,13 +18,18 @@ def validate_weight_tensor(tensor: torch.Tensor, *, name: str) -> None:
         raise ValueError(f"{name} must be 16-byte aligned")
 
 
+PAYLOAD_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
+
+
 @dataclass(frozen=True, slots=True)
 class ProjectionWeights:
     """One projection's retained storage (weights.py:294-328).
 
-    ``values`` is ``[N, K]`` bf16 with K contiguous.  Scales (MXFP4) and
-    additive biases are not part of the Dense path measured here; passing them
-    raises.
+    ``values`` is ``[N, K]`` (bf16, fp16 or fp32) with K contiguous; ``bias`` is an optional
+    fp32 ``[N]`` vector added to the fp32 sum before any rounding.  Scales (MXFP4) are not
+    part of this build and are refused.  The FfnAgent's captured templates take bf16 values
+    without a bias (``DenseFfnWeights.template_ready``); the operator path
+    (``crosspool_amd.operators``) takes the rest.
     """
 
     values: torch.Tensor
@@ -32,13 +37,19 @@ class ProjectionWeights:
     bias: torch.Tensor | None = None
 
     def __post_init__(self) -> None:
-        validate_weight_tensor(self.values, name="projection values")
-        if self.values.dtype is not torch.bfloat16 or self.values.ndim != 2:
-            raise ValueError("projection values must be a bf16 matrix")
+        if self.values.device.type != "cuda" or not self.values.is_contiguous() or self.values.ndim != 2:
+            raise ValueError("projection values must be a contiguous GPU matrix")
+        if any(size <= 0 for size in self.values.shape):
+            raise ValueError("projection values must have positive dimensions")
+        if self.values.dtype not in PAYLOAD_DTYPES:
+            raise ValueError("projection values must be bf16, fp16 or fp32")
         if self.scales is not None:
             raise ValueError("quantised projections are not supported on the MI355X Dense path")
         if self.bias is not None:
-            raise ValueError("projection biases are not supported on the MI355X Dense path")
+            if self.bias.dtype is not torch.float32 or tuple(self.bias.shape) != (self.values.shape[0],):
+                raise ValueError("a projection bias must be an fp32 vector with one value per output row")
+            if self.bias.device != self.values.device or not self.bias.is_contiguous():
+                raise ValueError("a projection bias must be contiguous on the values' device")
 
 
 @dataclass(frozen=True, slots=True)
@@ -54,10 +65,10 @@ class DenseFfnWeights:
     o_proj: ProjectionWeights
 
     def __post_init__(self) -> None:
-        two_i, hidden = self.i_proj.values.shape
+        rows, hidden = self.i_proj.values.shape
         out_hidden, intermediate = self.o_proj.values.shape
-        if two_i != 2 * intermediate or out_hidden != hidden:
-            raise ValueError("Dense projections disagree: i_proj must be [2I, H] and o_proj [H, I]")
+        if rows not in (intermediate, 2 * intermediate) or out_hidden != hidden:
+            raise ValueError("Dense projections disagree: i_proj must be [2I, H] (gated) or [I, H] and o_proj [H, I]")
         if self.o_proj.values.device != self.i_proj.values.device:
             raise ValueError("Dense projections must share one device")
         if self.i_proj.values.data_ptr() == self.o_proj.values.data_ptr():
@@ -74,6 +85,20 @@ class DenseFfnWeights:
     @property
     def device(self) -> torch.device:
         return self.i_proj.values.device
+
+    @property
+    def template_ready(self) -> bool:
+        """Whether the FfnAgent's captured templates can run these weights: gated bf16
+        INTERLEAVED i_proj ``[2I, H]``, bf16 o_proj, no biases, 16-byte aligned rows."""
+
+        i_proj, o_proj = self.i_proj, self.o_proj
+        return (
+            i_proj.values.dtype is torch.bfloat16 and o_proj.values.dtype is torch.bfloat16
+            and i_proj.bias is None and o_proj.bias is None
+            and i_proj.values.shape[0] == 2 * self.local_intermediate_size
+            and self.hidden_size % 8 == 0 and self.local_intermediate_size % 8 == 0
+            and i_proj.values.data_ptr() % 16 == 0 and o_proj.values.data_ptr() % 16 == 0
+        )
 
     @classmethod
     def from_tensors(cls, gate_up: torch.Tensor, down: torch.Tensor) -> DenseFfnWeights:

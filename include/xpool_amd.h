@@ -54,12 +54,32 @@ enum { XP_OUTPUT_PER_RANK_COMPLETE = 1, XP_OUTPUT_GROUP_SUM_COMPLETE = 2 };
 enum { XP_DP_ROWS_NONE = 0, XP_DP_ROWS_UNIFORM_BY_RANK = 1, XP_DP_ROWS_PACKED_BY_RANK = 2 };
 enum { XP_RESULT_OK = 0, XP_RESULT_SHUTDOWN = 1, XP_RESULT_PROTOCOL_MISMATCH = 2, XP_RESULT_TIMEOUT = 3 };
 enum { XP_LAYER_DENSE = 1, XP_LAYER_MOE = 2 };
-enum { XP_DTYPE_BF16 = 1 };
+enum { XP_DTYPE_BF16 = 1, XP_DTYPE_F16 = 2, XP_DTYPE_F32 = 3 };
+/* Activation functions (values of src/xpool/ffn.py:43-48 ActivationKind) and Gate/Up row
+ * orders (ffn.py:51-68 GateUpOrder). */
+enum { XP_ACTIVATION_NONE = 0, XP_ACTIVATION_SILU = 1, XP_ACTIVATION_RELU = 2, XP_ACTIVATION_GELU = 3 };
+enum { XP_GATE_UP_CONCATENATED = 1, XP_GATE_UP_INTERLEAVED = 2 };
 
 /* Sticky device fault bits. */
 #define XP_FAULT_SLOT_OUT_OF_RANGE 1u
 
 typedef void *xp_stream_t;
+
+/* One activation with its optional Gate/Up combination (src/xpool/runtime/ffnagent/operators/
+ * activation.py:87-173 Activation; ffn.py:118-151 SiluActivation / ReluActivation /
+ * GeluActivation; ffn.py:130-137 GateTransform).  Gated: f(min(g, limit)) *
+ * (clamp(u, -limit, limit) + up_offset) (clipping only with has_limit); ungated: f(v).
+ * SiLU: v / (1 + exp(-alpha v)); ReLU keeps NaN payloads; GELU: erf form or, with
+ * approximate_tanh, the tanh form. */
+typedef struct {
+  int function;         /* XP_ACTIVATION_SILU / RELU / GELU */
+  int approximate_tanh; /* GELU only */
+  int gated;
+  int has_limit;
+  float alpha;          /* SiLU slope (> 0) */
+  float limit;          /* > 0 when has_limit */
+  float up_offset;      /* gated only */
+} xp_activation_desc;
 typedef struct xp_agent *xp_agent_t;
 typedef struct xp_lane *xp_lane_t;
 
@@ -121,6 +141,27 @@ int xp_gemm_gate_up_silu(const void *x, int64_t rows, int64_t hidden, const void
 int xp_gemm_down(const void *activated, int64_t rows, int64_t intermediate, const void *w_down, int64_t hidden,
                  void *out, const int32_t *slots, int64_t out_rows, void *workspace, size_t workspace_bytes,
                  xp_stream_t stream);
+
+/* General projection: out = epilogue(bias + x . w^T) with x [rows, k], w [n, k], out
+ * [rows, n] (gated: [rows, n / 2] over INTERLEAVED Gate/Up rows), all of one payload dtype
+ * (XP_DTYPE_BF16 / F16 / F32), bias fp32 [n] or NULL, any K and N, element-aligned rows.
+ * The fp32 sum plus bias is stored rounded to the dtype; with an activation (NULL: none) it is
+ * first rounded to the dtype (the projection rounding point), then activated in fp32, then
+ * stored.  For the operator contract's shapes, dtypes and biases; bf16 SiLU projections of
+ * aligned shapes without bias take xp_gemm_gate_up_silu / xp_gemm_down.  Replaces Gemm.run_into
+ * for unquantized weights (src/xpool/runtime/ffnagent/operators/linear.py:163-257,
+ * operators/simt.py:13-80) with the epilogue of operators/activation.py:112-173. */
+int xp_projection(const void *x, int64_t rows, int64_t k, const void *w, int64_t n, const float *bias, void *out,
+                  int dtype, const xp_activation_desc *activation, xp_stream_t stream);
+
+/* Standalone activation over projected bf16 / fp16 values: gated, inputs [rows, 2 * width] in
+ * the given Gate/Up order (INTERLEAVED: gate 2j, up 2j + 1; CONCATENATED: gate j, up width + j)
+ * and output [rows, width], distinct storage; ungated, inputs and output [rows, width], which
+ * may be the same storage.  Replaces activation_kernel / Activation.apply_into
+ * (src/xpool/runtime/ffnagent/operators/activation.py:55-84, 175-207), which the CONCATENATED
+ * Dense order runs between its projections (operators/dense.py:80-85). */
+int xp_activation(const void *inputs, void *output, int64_t rows, int64_t width, int dtype, int order,
+                  const xp_activation_desc *activation, xp_stream_t stream);
 
 /* Scratch bytes the two projections above need for `rows` rows, n weight rows and
  * reduction length k (0 when the chosen kernel keeps the K reduction inside one

@@ -145,6 +145,103 @@ def gated_silu(
     return (silu(gate, alpha) * (up + up_offset)).to(torch.bfloat16)
 
 
+def activation_function(value: torch.Tensor, function: str, *, alpha: float = 1.0,
+                        approximate: str = "none") -> torch.Tensor:
+    """One activation in fp32 (operators/activation.py:19-41).
+
+    ``relu``: the value where it is > 0 or NaN (payload kept), +0 otherwise
+    (``compute_relu``, activation.py:19-27); ``silu``: ``v / (1 + exp(-alpha v))``
+    (``compute_silu``); ``gelu``: ``0.5 v (1 + erf(v / sqrt 2))`` or, approximated,
+    ``0.5 v (1 + tanh(0.7978845608028654 (v + 0.044715 v^3)))`` (``compute_gelu``).
+    """
+
+    value = value.float()
+    if function == "relu":
+        return torch.where((value > 0) | (value != value), value, torch.zeros_like(value))
+    if function == "silu":
+        return value / (1 + torch.exp(-alpha * value))
+    if function == "gelu":
+        if approximate == "tanh":
+            inner = 0.7978845608028654 * (value + 0.044715 * value * value * value)
+            return 0.5 * value * (1 + torch.tanh(inner))
+        return 0.5 * value * (1 + torch.erf(value * 0.7071067811865476))
+    raise ValueError(f"unknown activation {function!r}")
+
+
+def relu_bits(values: torch.Tensor) -> torch.Tensor:
+    """Ungated ReLU of bf16 / fp16 values on their raw patterns (activation.py:19-27, 80-82):
+    the pattern where the value is > 0 or NaN, +0 otherwise."""
+
+    bits = values.contiguous().view(torch.int16)
+    keep = (values.float() > 0) | (values.float() != values.float())
+    return torch.where(keep, bits, torch.zeros_like(bits)).view(values.dtype)
+
+
+def standalone_activation(inputs: torch.Tensor, *, width: int, function: str, gated: bool, order: str | None = None,
+                          alpha: float = 1.0, approximate: str = "none", limit: float | None = None,
+                          up_offset: float = 0.0) -> torch.Tensor:
+    """``activation_kernel`` (operators/activation.py:55-84) over projected bf16 / fp16 values.
+
+    Gated: Gate and Up of output column j are inputs ``[2j, 2j + 1]`` (INTERLEAVED) or
+    ``[j, width + j]`` (CONCATENATED) of the row, combined by ``compute_gated``
+    (activation.py:44-51); the fp32 result is stored in the payload dtype.  Ungated ReLU is
+    the bitwise rule of :func:`relu_bits`; other ungated functions compute in fp32.
+    """
+
+    dtype = inputs.dtype
+    rows = inputs.numel() // (2 * width if gated else width)
+    if not gated:
+        flat = inputs.reshape(rows, width)
+        if function == "relu":
+            return relu_bits(flat)
+        return activation_function(flat, function, alpha=alpha, approximate=approximate).to(dtype)
+    pairs = inputs.reshape(rows, 2 * width)
+    if order == "interleaved":
+        gate, up = pairs[:, 0::2], pairs[:, 1::2]
+    elif order == "concatenated":
+        gate, up = pairs[:, :width], pairs[:, width:]
+    else:
+        raise ValueError("gated activation requires a Gate/Up order")
+    return gated_activation(gate, up, function=function, alpha=alpha, approximate=approximate, limit=limit,
+                            up_offset=up_offset).to(dtype)
+
+
+def gated_activation(gate: torch.Tensor, up: torch.Tensor, *, function: str, alpha: float = 1.0,
+                     approximate: str = "none", limit: float | None = None, up_offset: float = 0.0) -> torch.Tensor:
+    """``compute_gated`` (activation.py:44-51) in fp32: Gate clipped above at ``limit``, Up to
+    ``[-limit, limit]``, ``f(gate) * (up + up_offset)``; fp32 result."""
+
+    gate = gate.float()
+    up = up.float()
+    if limit is not None:
+        gate = torch.clamp(gate, max=limit)
+        up = torch.clamp(up, -limit, limit)
+    return activation_function(gate, function, alpha=alpha, approximate=approximate) * (up + up_offset)
+
+
+def projection_reference(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None = None, *,
+                         function: str | None = None, gated: bool = False, **activation) -> torch.Tensor:
+    """A projection with the reference's epilogue (operators/linear.py:42-96, simt.py:13-45,
+    activation.py:112-173), the sum in fp64.
+
+    ``value = x . w^T + bias``; without an activation the value is rounded once to the payload
+    dtype; with one it is rounded to the payload dtype (the projection rounding point), then
+    activated in fp32 (gated: INTERLEAVED Gate/Up pairs), then rounded to the payload dtype.
+    """
+
+    dtype = x.dtype
+    value = x.double() @ w.double().t()
+    if bias is not None:
+        value = value + bias.double()
+    if function is None:
+        return value.to(dtype)
+    rounded = value.to(dtype)
+    if gated:
+        return gated_activation(rounded[:, 0::2], rounded[:, 1::2], function=function, **activation).to(dtype)
+    return activation_function(rounded, function, **{k: v for k, v in activation.items()
+                                                     if k in ("alpha", "approximate")}).to(dtype)
+
+
 def dense_partial_reference(x: torch.Tensor, w_gate_up: torch.Tensor, w_down: torch.Tensor) -> torch.Tensor:
     """Dense partial with fp64 projections and payload stage rounding.
 

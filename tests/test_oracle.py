@@ -332,3 +332,77 @@ def test_golden_mailbox_fixture_reproduces():
     assert np.array_equal(o.bf16_bits(new_pool), golden["new_pool"])
     c_rows, _ = c_oracle.dense_partial(normalized, o.bf16_from_bits(golden["w_gate_up"]), o.bf16_from_bits(golden["w_down"]))
     assert np.array_equal(o.bf16_bits(c_rows), golden["ffn_rows"])
+
+
+# --------------------------------------------------------------------------- #
+# Activations and the general projection (operators/activation.py, linear.py)
+# --------------------------------------------------------------------------- #
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_relu_bits_match_torch_except_where_the_reference_rule_differs(dtype):
+    # activation.py:19-27: the pattern where v > 0 or v is NaN, +0 otherwise.  torch's CPU
+    # relu agrees on every other pattern; it keeps -0 and canonicalises NaNs, where the
+    # reference's rule gives +0 and keeps the payload (what its all-pattern test pins on CUDA).
+    values = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(dtype)
+    got = o.relu_bits(values).view(torch.int16)
+    f = values.float()
+    ordinary = (f == f) & ~((f == 0) & (values.view(torch.int16) < 0))
+    assert torch.equal(got[ordinary], values.relu().view(torch.int16)[ordinary])
+    nan = f != f
+    assert int(nan.sum()) > 0 and torch.equal(got[nan], values.view(torch.int16)[nan])
+    negative_zero = torch.tensor([-0.0], dtype=dtype)
+    assert int(o.relu_bits(negative_zero).view(torch.int16).item()) == 0
+
+
+def test_activation_functions_match_torch_library_routines():
+    x = torch.linspace(-12, 12, 4801, dtype=torch.float32)
+    torch.testing.assert_close(o.activation_function(x, "silu"), torch.nn.functional.silu(x), rtol=2e-6, atol=1e-7)
+    torch.testing.assert_close(o.activation_function(x, "silu", alpha=1.702), x * torch.sigmoid(1.702 * x),
+                               rtol=2e-6, atol=1e-7)
+    for approximate in ("none", "tanh"):
+        torch.testing.assert_close(o.activation_function(x, "gelu", approximate=approximate),
+                                   torch.nn.functional.gelu(x, approximate=approximate), rtol=2e-6, atol=1e-6)
+    # a wrong slope or the other GELU form fails the same check
+    assert not torch.allclose(o.activation_function(x, "silu", alpha=1.3), torch.nn.functional.silu(x), atol=1e-3)
+    assert not torch.allclose(o.activation_function(x, "gelu", approximate="tanh"),
+                              torch.nn.functional.gelu(x), rtol=0, atol=1e-6)
+
+
+def test_gated_activation_clip_and_offset_closed_forms():
+    gate = torch.tensor([10.0, -10.0, 2.0, 0.5])
+    up = torch.tensor([9.0, -9.0, 1.0, -0.25])
+    got = o.gated_activation(gate, up, function="relu", limit=4.0, up_offset=-0.5)
+    # gate clipped above only (10 -> 4, -10 stays), up clamped to [-4, 4], then + offset
+    expected = torch.tensor([4.0 * (4.0 - 0.5), 0.0 * (-4.0 - 0.5), 2.0 * (1.0 - 0.5), 0.5 * (-0.25 - 0.5)])
+    assert torch.equal(got, expected)
+    # no limit: identity transform
+    assert torch.equal(o.gated_activation(gate, up, function="relu"), torch.relu(gate) * up)
+
+
+def test_standalone_activation_orders_agree_on_permuted_inputs():
+    g = torch.Generator().manual_seed(3)
+    gate = torch.randn((6, 40), generator=g).to(torch.bfloat16)
+    up = torch.randn((6, 40), generator=g).to(torch.bfloat16)
+    interleaved = torch.stack((gate, up), dim=2).reshape(6, 80)
+    concatenated = torch.cat((gate, up), dim=1)
+    kwargs = dict(width=40, function="silu", gated=True, alpha=1.3, limit=4.0, up_offset=-0.5)
+    a = o.standalone_activation(interleaved, order="interleaved", **kwargs)
+    b = o.standalone_activation(concatenated, order="concatenated", **kwargs)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    # reading the other order's layout gives a different result
+    c = o.standalone_activation(interleaved, order="concatenated", **kwargs)
+    assert not torch.equal(a.view(torch.int16), c.view(torch.int16))
+
+
+def test_projection_reference_adds_the_bias_before_the_rounding_point():
+    # x . w = 1 + 2^-8 exactly (halfway between bf16 1 and 1 + 2^-7: rounds to 1, even);
+    # a bias of 2^-9 lifts it past the halfway point, so the result must be 1 + 2^-7.  Adding the
+    # bias after rounding would give 1 + 2^-9 -> 1.
+    x = torch.tensor([[1.0, 2.0**-8]], dtype=torch.bfloat16)
+    w = torch.tensor([[1.0, 1.0]], dtype=torch.bfloat16)
+    assert o.projection_reference(x, w).float().item() == 1.0
+    bias = torch.tensor([2.0**-9])
+    assert o.projection_reference(x, w, bias).float().item() == 1.0 + 2.0**-7
+    # gated epilogue: the projection is rounded before the activation (relu of the rounded sum)
+    w2 = torch.tensor([[1.0, 1.0], [1.0, 0.0]], dtype=torch.bfloat16)  # gate row, up row
+    out = o.projection_reference(x, w2, function="relu", gated=True)
+    assert out.float().item() == 1.0 * 1.0  # gate rounds to 1 (not 1 + 2^-8), up = 1
