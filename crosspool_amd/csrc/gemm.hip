@@ -880,24 +880,37 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs &a, const f32x16 (&
   // Chunk c of row r sits at physical chunk c ^ ((r / 4) % CPR): the two row groups one
   // write instruction covers (rows r and r + 4) then fall in different banks.
   auto slot_of = [](int row, int chunk) { return row * OUT_N + ((chunk ^ ((row >> 2) & (CPR - 1))) << 3); };
+  // The gated activation is the epilogue's VALU cost (two quarter-rate transcendentals per
+  // output); its clipping is chosen once per tile, not per element.
+  auto stage = [&](auto clip) XP_INLINE {
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
+    for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int row = mt * 32 + 8 * (r >> 2) + 4 * frag_half + (r & 3);
-      // Row weight (grouped down projection); 1 elsewhere.
-      float factor = 1.0f;
-      if constexpr (GROUPED && !GATED) {
-        factor = a.row_scale != nullptr ? row_factor(meta, row) : 1.0f;
-      }
+      for (int r = 0; r < 16; ++r) {
+        const int row = mt * 32 + 8 * (r >> 2) + 4 * frag_half + (r & 3);
+        // Row weight (grouped down projection); 1 elsewhere.
+        float factor = 1.0f;
+        if constexpr (GROUPED && !GATED) {
+          factor = a.row_scale != nullptr ? row_factor(meta, row) : 1.0f;
+        }
 #pragma unroll
-      for (int nt = 0; nt < OUT_N / 32; ++nt) {
-        const int col = nt * 32 + frag_row;
-        const float value =
-            GATED ? gated_silu(acc[mt][nt][r], acc[mt][nt + NT / 2][r], a.act) : acc[mt][nt][r] * factor;
-        out_tile[slot_of(row, col >> 3) + (col & 7)] = static_cast<uint16_t>(float_to_bf16(value));
+        for (int nt = 0; nt < OUT_N / 32; ++nt) {
+          const int col = nt * 32 + frag_row;
+          float value;
+          if constexpr (GATED) {
+            value = gated_silu_fixed<decltype(clip)::value>(acc[mt][nt][r], acc[mt][nt + NT / 2][r], a.act);
+          } else {
+            value = acc[mt][nt][r] * factor;
+          }
+          out_tile[slot_of(row, col >> 3) + (col & 7)] = static_cast<uint16_t>(float_to_bf16(value));
+        }
       }
     }
+  };
+  if (GATED && a.act.limit > 0.0f) {
+    stage(std::true_type{});
+  } else {
+    stage(std::false_type{});
   }
   __syncthreads();
   const int64_t row0 = m0 + wm * WTM;

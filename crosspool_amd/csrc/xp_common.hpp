@@ -47,7 +47,22 @@ struct GatedSilu {
   float up_offset;
 };
 
-// The projection is first rounded to bf16 (payload dtype), then evaluated in fp32.
+// The projection is first rounded to bf16 (payload dtype), then evaluated in fp32.  CLIP is
+// whether the gate transform clips (act.limit > 0), fixed at compile time so that tile
+// epilogues without a limit carry no clamp or select per element; both bf16 roundings come
+// from one packed conversion.
+template <bool CLIP>
+__device__ __forceinline__ float gated_silu_fixed(float gate, float up, const GatedSilu &act) {
+  const uint32_t both = pack_bf16x2(gate, up);
+  float g = __uint_as_float(both << 16);
+  float u = __uint_as_float(both & 0xffff0000u);
+  if constexpr (CLIP) {
+    g = fminf(g, act.limit);
+    u = fminf(fmaxf(u, -act.limit), act.limit);
+  }
+  return g * __builtin_amdgcn_rcpf(1.0f + __expf(-act.alpha * g)) * (u + act.up_offset);
+}
+
 __device__ __forceinline__ float gated_silu(float gate, float up, const GatedSilu &act) {
   float g = round_bf16(gate);
   float u = round_bf16(up);
