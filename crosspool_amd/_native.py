@@ -38,6 +38,26 @@ class ActivationDesc(ctypes.Structure):
     ]
 
 
+class MoeLayerDesc(ctypes.Structure):
+    """``xp_moe_layer_desc`` of the header."""
+
+    _fields_ = [
+        ("hidden", ctypes.c_int64),
+        ("intermediate", ctypes.c_int64),
+        ("experts", ctypes.c_int64),
+        ("routed_experts", ctypes.c_int64),
+        ("routed_topk", ctypes.c_int64),
+        ("algorithm", ctypes.c_int),
+        ("precision", ctypes.c_int),
+        ("renormalize", ctypes.c_int),
+        ("weight_rounding", ctypes.c_int),
+        ("routed_scaling_factor", ctypes.c_float),
+        ("alpha", ctypes.c_float),
+        ("limit", ctypes.c_float),
+        ("up_offset", ctypes.c_float),
+    ]
+
+
 XP_DTYPE_BF16 = 1
 XP_DTYPE_F16 = 2
 XP_DTYPE_F32 = 3
@@ -102,6 +122,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "xp_moe_experts": (
         _INT, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _F32, _F32, _F32, _F32, _P, _P, _SIZE, _P]
     ),
+    "xp_moe_layer_register": (_INT, [_P, _INT, _INT, ctypes.POINTER(MoeLayerDesc), _P, _P, _P, _P, _P, _F32]),
+    "xp_moe_step_workspace_bytes": (_SIZE, [ctypes.POINTER(MoeLayerDesc), _I64]),
+    "xp_moe_step_workspace_layout": (_INT, [ctypes.POINTER(MoeLayerDesc), _I64, ctypes.POINTER(_SIZE)]),
+    "xp_moe_template_capture": (_INT, [_P, ctypes.POINTER(MoeLayerDesc), _I64]),
 }
 
 
@@ -185,4 +209,18 @@ def dense_workspace_layout(capacity: int, hidden: int, intermediate: int) -> tup
 
     offsets = (_SIZE * 5)()
     call("xp_dense_workspace_layout", capacity, hidden, intermediate, offsets)
+    return tuple(int(value) for value in offsets)
+
+
+def moe_step_workspace_bytes(desc: MoeLayerDesc, capacity: int) -> int:
+    """Lane workspace bytes of one MoE template (0 for an invalid descriptor)."""
+
+    return int(library().xp_moe_step_workspace_bytes(ctypes.byref(desc), capacity))
+
+
+def moe_step_workspace_layout(desc: MoeLayerDesc, capacity: int) -> tuple[int, ...]:
+    """(batch, logits, routed ids, routed weights, final ids, final weights, experts, total) offsets."""
+
+    offsets = (_SIZE * 8)()
+    call("xp_moe_step_workspace_layout", ctypes.byref(desc), capacity, offsets)
     return tuple(int(value) for value in offsets)

@@ -21,8 +21,13 @@ from time import monotonic
 import torch
 
 from crosspool_amd import _native
-from crosspool_amd.execution import DenseFfnExecutionSignature, derive_payload_row_capacities
-from crosspool_amd.ffn import ResultCode
+from crosspool_amd.execution import (
+    DenseFfnExecutionSignature,
+    MoeFfnExecutionSignature,
+    derive_payload_row_capacities,
+)
+from crosspool_amd.ffn import LayerKind, ResultCode
+from crosspool_amd.moe import MoeFfnWeights, MoeLayerSpec
 from crosspool_amd.weights import DenseFfnWeights, validate_weight_tensor
 
 logger = logging.getLogger(__name__)
@@ -30,13 +35,23 @@ logger = logging.getLogger(__name__)
 
 @dataclass(frozen=True, slots=True)
 class GraphTemplate:
-    """One captured graph identity: the Execution Signature (execution.py:73-95)."""
+    """One captured graph identity: the Execution Signature (execution.py:73-149).
 
-    signature: DenseFfnExecutionSignature
+    Dense templates are keyed by (hidden, intermediate, capacity); MoE templates by their
+    whole signature.
+    """
+
+    signature: DenseFfnExecutionSignature | MoeFfnExecutionSignature
 
     @property
-    def key(self) -> tuple[int, int, int]:
+    def kind(self) -> LayerKind:
+        return LayerKind.MOE if isinstance(self.signature, MoeFfnExecutionSignature) else LayerKind.DENSE
+
+    @property
+    def key(self) -> tuple[int, int, int] | MoeFfnExecutionSignature:
         s = self.signature
+        if isinstance(s, MoeFfnExecutionSignature):
+            return s
         return s.hidden_size, s.local_intermediate_size, s.payload_row_capacity
 
     @property
@@ -44,6 +59,11 @@ class GraphTemplate:
         """Lane workspace bytes of this template, K-slice partial sums included (native query)."""
 
         s = self.signature
+        if isinstance(s, MoeFfnExecutionSignature):
+            nbytes = _native.moe_step_workspace_bytes(s.native_descriptor(), s.payload_row_capacity)
+            if nbytes == 0:
+                raise ValueError(f"MoE signature is outside the native limits: {s}")
+            return nbytes
         return _native.dense_workspace_bytes(s.payload_row_capacity, s.hidden_size, s.local_intermediate_size)
 
 
@@ -51,9 +71,14 @@ class GraphTemplate:
 class LayerBinding:
     instance_index: int
     layer_ordinal: int
-    weights: DenseFfnWeights
+    weights: DenseFfnWeights | MoeFfnWeights
     norm_weight: torch.Tensor | None
     eps: float
+    moe: MoeLayerSpec | None = None
+
+    @property
+    def kind(self) -> LayerKind:
+        return LayerKind.DENSE if self.moe is None else LayerKind.MOE
 
 
 class FfnHealthError(RuntimeError):
@@ -88,15 +113,20 @@ class ExecutorLane:
         _native.call("xp_lane_fault_word", self.handle, ctypes.byref(fault))
         # Device address of the Lane's sticky fault word (read by the Transport's evaluate).
         self.fault_word = int(fault.value or 0)
-        self.templates: dict[tuple[int, int, int], GraphTemplate] = {}
+        self.templates: dict[object, GraphTemplate] = {}
         self._in_flight: deque[tuple[torch.cuda.Event | None, tuple[torch.Tensor, ...], torch.cuda.Stream]] = deque()
 
     def capture(self, template: GraphTemplate) -> None:
         """Instantiate the template's hipGraph on this Lane (idempotent)."""
 
         self._require_open()
-        hidden, intermediate, capacity = template.key
-        _native.call("xp_template_capture", self.handle, hidden, intermediate, capacity)
+        s = template.signature
+        if isinstance(s, MoeFfnExecutionSignature):
+            _native.call("xp_moe_template_capture", self.handle, ctypes.byref(s.native_descriptor()),
+                         s.payload_row_capacity)
+        else:
+            _native.call("xp_template_capture", self.handle, s.hidden_size, s.local_intermediate_size,
+                         s.payload_row_capacity)
         self.templates[template.key] = template
 
     def capacities(self, hidden: int, intermediate: int) -> tuple[int, ...]:
@@ -120,8 +150,9 @@ class ExecutorLane:
         """Run one mailbox step of a registered layer (stream-ordered, no host sync).
 
         ``rows`` live slot ids of ``slots`` are gathered from ``pool`` (with the
-        layer's RMSNorm when it has one), run through the Dense FFN and written
-        back to the same slots of ``out_pool`` (default: ``pool``).
+        layer's RMSNorm when it has one), run through the layer's FFN (Dense, or MoE:
+        Router, routing finalisation, Experts) and written back to the same slots of
+        ``out_pool`` (default: ``pool``).
 
         With ``stream=None`` the replay runs on the Lane's stream after the
         current torch stream's pending work; results are visible to other
@@ -245,7 +276,7 @@ class FfnAgent:
         self.executor_lane_count = executor_lane_count
         self.graph_dispatch = graph_dispatch
         self.layers: dict[tuple[int, int], LayerBinding] = {}
-        self.templates: dict[tuple[int, int, int], GraphTemplate] = {}
+        self.templates: dict[object, GraphTemplate] = {}
         self.lanes: list[ExecutorLane] = []
         self.materialized = False
 
@@ -282,6 +313,47 @@ class FfnAgent:
         )
         self.layers[(instance_index, layer_ordinal)] = LayerBinding(
             instance_index, layer_ordinal, weights, norm_weight, float(eps)
+        )
+
+    def register_moe_layer(
+        self,
+        *,
+        instance_index: int,
+        layer_ordinal: int,
+        weights: MoeFfnWeights,
+        spec: MoeLayerSpec,
+        norm_weight: torch.Tensor | None = None,
+        eps: float = 1e-6,
+    ) -> None:
+        """Bind one MoE layer: expert projections, Router (+ correction bias), optional fused RMSNorm.
+
+        On one device the Lane owns the Router: each replay projects and routes the gathered
+        rows itself (the reference's TP rank 0 role, src/cext/ffnagent/runtime.cu:649).
+        """
+
+        if weights.i_proj.device != self.device:
+            raise ValueError("local FFN resources must reside on the agent's device")
+        spec.validate_weights(weights)
+        if norm_weight is not None:
+            validate_weight_tensor(norm_weight, name="RMSNorm weight")
+            if norm_weight.dtype is not torch.bfloat16 or tuple(norm_weight.shape) != (weights.hidden_size,):
+                raise ValueError("RMSNorm weight must be a bf16 [H] vector")
+            if norm_weight.device != self.device:
+                raise ValueError("RMSNorm weight must reside on the agent's device")
+        signature = spec.signature(
+            hidden_size=weights.hidden_size, local_intermediate_size=weights.local_intermediate_size,
+            payload_row_capacity=1,
+        )
+        router = weights.router
+        _native.call(
+            "xp_moe_layer_register", self.handle, instance_index, layer_ordinal,
+            ctypes.byref(signature.native_descriptor()), ctypes.c_void_p(weights.i_proj.data_ptr()),
+            ctypes.c_void_p(weights.o_proj.data_ptr()), ctypes.c_void_p(router.projection.data_ptr()),
+            None if router.correction_bias is None else ctypes.c_void_p(router.correction_bias.data_ptr()),
+            None if norm_weight is None else ctypes.c_void_p(norm_weight.data_ptr()), float(eps),
+        )
+        self.layers[(instance_index, layer_ordinal)] = LayerBinding(
+            instance_index, layer_ordinal, weights, norm_weight, float(eps), spec
         )
 
     def register_checkpoint(
@@ -334,8 +406,9 @@ class FfnAgent:
             raise RuntimeError("register at least one layer before materializing")
         self.materialized = True
         started = monotonic()
-        shapes = sorted({(b.weights.hidden_size, b.weights.local_intermediate_size) for b in self.layers.values()})
         capacities = derive_payload_row_capacities(maximum_row_capacity)
+        dense = self._dense_layers()
+        shapes = sorted({(b.weights.hidden_size, b.weights.local_intermediate_size) for b in dense})
         for hidden, intermediate in shapes:
             for capacity in capacities:
                 signature = DenseFfnExecutionSignature(
@@ -346,6 +419,16 @@ class FfnAgent:
                 )
                 template = GraphTemplate(signature)
                 self.templates[template.key] = template
+        for binding in self.layers.values():
+            if binding.moe is None:
+                continue
+            for capacity in capacities:
+                template = GraphTemplate(binding.moe.signature(
+                    hidden_size=binding.weights.hidden_size,
+                    local_intermediate_size=binding.weights.local_intermediate_size,
+                    payload_row_capacity=capacity,
+                ))
+                self.templates.setdefault(template.key, template)
         workspace_bytes = max(t.workspace_bytes for t in self.templates.values())
         for _ in range(self.executor_lane_count):
             lane = ExecutorLane(self, workspace_bytes, graph_dispatch=self.graph_dispatch)
@@ -353,10 +436,17 @@ class FfnAgent:
             for template in self.templates.values():
                 lane.capture(template)
         logger.info(
-            "graph templates captured device=%s signature_count=%s lane_count=%s row_capacities=%s elapsed=%.3fs",
-            self.device, len(self.templates), len(self.lanes), list(capacities), monotonic() - started,
+            "graph templates captured device=%s signature_count=%s dense_count=%s moe_count=%s lane_count=%s "
+            "row_capacities=%s elapsed=%.3fs",
+            self.device, len(self.templates),
+            sum(t.kind is LayerKind.DENSE for t in self.templates.values()),
+            sum(t.kind is LayerKind.MOE for t in self.templates.values()),
+            len(self.lanes), list(capacities), monotonic() - started,
         )
         return tuple(self.templates.values())
+
+    def _dense_layers(self) -> list[LayerBinding]:
+        return [binding for binding in self.layers.values() if binding.moe is None]
 
     # -------------------------------------------------------------- execution
     def execute(
@@ -375,8 +465,11 @@ class FfnAgent:
 
         if not self.materialized:
             raise RuntimeError("FfnAgent has not been materialized")
-        if (instance_index, layer_ordinal) not in self.layers:
+        binding = self.layers.get((instance_index, layer_ordinal))
+        if binding is None:
             raise KeyError(f"no layer registered for instance {instance_index} ordinal {layer_ordinal}")
+        if pool.ndim != 2 or pool.shape[1] != binding.weights.hidden_size:
+            raise ValueError(f"mailbox rows must hold the layer's hidden size {binding.weights.hidden_size}")
         self.lanes[lane].replay(
             instance_index=instance_index, layer_ordinal=layer_ordinal, pool=pool, slots=slots, rows=rows,
             out_pool=out_pool, stream=stream,

@@ -230,7 +230,7 @@ __global__ __launch_bounds__(256) void finalize_routing_kernel(FinalizeRoutingAr
   }
   const int64_t row = index / a.effective_topk;
   const int slot = static_cast<int>(index % a.effective_topk);
-  const bool live = row < *a.payload_rows;
+  const bool live = a.payload_rows == nullptr || row < *a.payload_rows;
   const bool routed = slot < a.routed_topk;
   int32_t id = -1;
   float weight = 0.0f;
@@ -366,7 +366,9 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(MoeSortArgs a) {
 // ------------------------------------------------------------------ combine
 // out[row] = bf16(scale * sum over the row's live routes, in slot order, of float(route
 // output)) -- the route reduction with the routed scaling factor (moe.py:336-343); rows
-// whose slots are all -1 read 0.
+// whose slots are all -1 read 0.  With slots the sum of row r goes to out row slots[r]
+// (the mailbox scatter); a slot outside the mailbox is skipped (the gather that read it
+// has raised the Lane's fault bit).
 __global__ __launch_bounds__(256) void moe_combine_kernel(MoeCombineArgs a) {
   const int64_t chunks = a.hidden / 8;
   const int64_t index = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
@@ -375,6 +377,13 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(MoeCombineArgs a) {
   }
   const int64_t row = index / chunks;
   const int64_t chunk = index % chunks;
+  int64_t out_row = row;
+  if (a.slots != nullptr) {
+    out_row = a.slots[row];
+    if (out_row < 0 || out_row >= a.out_rows) {
+      return;
+    }
+  }
   float sum[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
   // Slots in batches: the batch's ids first, then its route rows, then the sums in slot
   // order (two memory round trips per batch instead of two per slot).
@@ -408,7 +417,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(MoeCombineArgs a) {
   for (int word = 0; word < 4; ++word) {
     packed[word] = pack_bf16x2(sum[2 * word] * a.scale, sum[2 * word + 1] * a.scale);
   }
-  store16(a.out + row * a.hidden + chunk * 8, packed);
+  store16(a.out + out_row * a.hidden + chunk * 8, packed);
 }
 
 template <class Args>

@@ -130,6 +130,20 @@ struct DenseLaunches {
 };
 constexpr int kMaxStepKernels = 5;
 
+// The kernels of one template's step in launch order (a Dense step has at most 5; a MoE
+// step at most 9: gather, Router projection and its reduction, TopK, finalisation, sort,
+// gate_up, down, combine).
+constexpr int kMaxTemplateKernels = 9;
+struct StepChain {
+  KernelLaunch kernels[kMaxTemplateKernels];
+  int count = 0;
+  void add(const KernelLaunch &kernel) {
+    if (!kernel.empty()) {
+      kernels[count++] = kernel;
+    }
+  }
+};
+
 struct DenseBinding {
   const uint16_t *pool_in;
   uint16_t *pool_out;
@@ -254,6 +268,11 @@ struct Layer {
   const uint16_t *down;
   const uint16_t *norm;
   float eps;
+  int kind = XP_LAYER_DENSE;
+  // MoE layers: the execution identity, the Router projection and its correction bias.
+  xp_moe_layer_desc moe{};
+  const void *router = nullptr;
+  const float *correction_bias = nullptr;
 };
 
 struct xp_agent {
@@ -264,16 +283,18 @@ struct xp_agent {
 };
 
 struct Template {
+  int kind = XP_LAYER_DENSE;
   int64_t hidden = 0;
   int64_t intermediate = 0;
   int64_t capacity = 0;
+  xp_moe_layer_desc moe{};  // MoE templates: the signature they were captured for
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
-  hipGraphNode_t nodes[kMaxStepKernels] = {};
+  hipGraphNode_t nodes[kMaxTemplateKernels] = {};
   int node_count = 0;
   // Argument records last bound to each node: a replay rebinds only the nodes whose
   // record changed.
-  KernelLaunch bound[kMaxStepKernels];
+  KernelLaunch bound[kMaxTemplateKernels];
 };
 
 struct xp_lane {
@@ -378,6 +399,421 @@ RouterWorkspace router_workspace(int64_t rows, int64_t hidden, int64_t experts, 
   return layout;
 }
 
+int validate_router(int64_t experts, int64_t topk, int algorithm, int precision, int weight_rounding) {
+  XP_REQUIRE(precision == XP_ROUTER_PRECISION_PAYLOAD || precision == XP_ROUTER_PRECISION_FP32 ||
+                 precision == XP_ROUTER_PRECISION_FP32_LOGITS,
+             "router projection precision is unknown");
+  XP_REQUIRE(experts >= 1 && experts <= kMoeMaxExperts, "the router supports 1 to 1024 experts");
+  XP_REQUIRE(topk >= 1 && topk <= experts && topk <= 64, "topk must be between 1 and min(experts, 64)");
+  XP_REQUIRE(algorithm == XP_ROUTER_SOFTMAX || algorithm == XP_ROUTER_SIGMOID, "router algorithm is unknown");
+  XP_REQUIRE(weight_rounding == XP_TOPK_ROUNDING_NONE || weight_rounding == XP_TOPK_ROUNDING_LOGITS_DTYPE,
+             "TopK weight rounding is unknown");
+  return XP_OK;
+}
+
+int validate_experts(int64_t rows, int64_t hidden, int64_t intermediate, int64_t experts, int64_t topk) {
+  XP_REQUIRE(hidden > 0 && hidden % 8 == 0 && intermediate > 0 && intermediate % 8 == 0,
+             "hidden and intermediate sizes must be positive multiples of 8");
+  XP_REQUIRE(experts >= 1 && experts <= kMoeMaxExperts, "Experts support 1 to 1024 experts");
+  XP_REQUIRE(topk >= 1 && topk <= experts, "topk must be between 1 and the expert count");
+  XP_REQUIRE(rows * topk <= (int64_t{1} << 30), "too many routes for one call");
+  // The projections address the token rows, the activated routes and one expert's weights
+  // through 32-bit buffer ranges.
+  XP_REQUIRE(rows * hidden * 2 < (int64_t{1} << 31) && rows * topk * intermediate * 2 < (int64_t{1} << 31) &&
+                 2 * intermediate * hidden * 2 < (int64_t{1} << 31),
+             "Experts tensors must stay below 2 GiB per buffer range");
+  XP_REQUIRE(moe_tile_bound(rows * topk, experts, moe_tile_rows(MoeTile::Small)) <= 65535,
+             "too many expert tiles for one call");
+  return XP_OK;
+}
+
+// Router kernels for `rows` live rows with grids for `capacity` rows (the kernels bound
+// themselves by the live rows), so that one template's nodes serve every smaller replay.
+struct RouterBinding {
+  const uint16_t *x;
+  const void *w;
+  const float *correction_bias;
+  int32_t *ids;
+  float *weights;
+  uint8_t *workspace;  // router_workspace(capacity, ...)
+  int64_t rows;
+  int64_t hidden;
+  int64_t experts;
+  int64_t topk;
+  int algorithm;
+  int precision;
+  int renormalize;
+  int weight_rounding;
+};
+
+struct RouterLaunches {
+  KernelLaunch logits;         // MFMA projection or the fp32 logits kernel
+  KernelLaunch logits_reduce;  // K-slice reduction of the MFMA projection, or empty
+  KernelLaunch topk;
+};
+
+RouterLaunches make_router_launches(const RouterBinding &b, int64_t capacity) {
+  const RouterWorkspace layout = router_workspace(capacity, b.hidden, b.experts, b.precision);
+  void *logits = b.workspace + layout.logits;
+  RouterLaunches launches;
+  if (router_uses_mfma(b.hidden, b.experts, b.precision)) {
+    // logits = bf16(x . w^T): the Dense projection kernels, no epilogue.
+    GemmArgs args{};
+    args.x = b.x;
+    args.w = static_cast<const uint16_t *>(b.w);
+    args.out = static_cast<uint16_t *>(logits);
+    args.partials = layout.scratch_bytes > 0 ? reinterpret_cast<float *>(b.workspace + layout.scratch) : nullptr;
+    args.ldx = b.hidden;
+    args.ldo = b.experts;
+    args.rows = b.rows;
+    args.out_rows = capacity;
+    args.n = b.experts;
+    args.k = b.hidden;
+    args.act = default_activation();
+    const GemmLaunch gemm = make_gemm(args, capacity, false, choose_gemm(capacity, b.experts, b.hidden, false));
+    launches.logits = gemm.main;
+    launches.logits_reduce = gemm.reduce;
+  } else {
+    RouterLogitsArgs args{};
+    args.x = b.x;
+    args.w = b.w;
+    args.logits = logits;
+    args.rows = capacity;
+    args.hidden = b.hidden;
+    args.experts = static_cast<int32_t>(b.experts);
+    args.weights_f32 = b.precision == XP_ROUTER_PRECISION_FP32 ? 1 : 0;
+    args.out_bf16 = b.precision == XP_ROUTER_PRECISION_PAYLOAD ? 1 : 0;
+    launches.logits = make_router_logits(args);
+    args.rows = b.rows;
+    launches.logits.set_args(args);
+  }
+  RouterTopkArgs topk{};
+  topk.logits = logits;
+  topk.correction_bias = b.correction_bias;
+  topk.ids = b.ids;
+  topk.weights = b.weights;
+  topk.rows = capacity;
+  topk.experts = static_cast<int32_t>(b.experts);
+  topk.topk = static_cast<int32_t>(b.topk);
+  topk.logits_f32 = b.precision == XP_ROUTER_PRECISION_PAYLOAD ? 0 : 1;
+  topk.softmax = b.algorithm == XP_ROUTER_SOFTMAX ? 1 : 0;
+  topk.renormalize = b.renormalize != 0 ? 1 : 0;
+  topk.round_to_logits = b.weight_rounding == XP_TOPK_ROUNDING_LOGITS_DTYPE ? 1 : 0;
+  launches.topk = make_router_topk(topk);
+  topk.rows = b.rows;
+  launches.topk.set_args(topk);
+  return launches;
+}
+
+// Experts kernels (route sort, grouped gate_up, grouped down, combine) for `rows` live rows,
+// with the tile choice, the tile table bound and the grids of `capacity` rows.
+struct ExpertsBinding {
+  const uint16_t *x;  // [rows, hidden] token rows
+  const uint16_t *w_gate_up;
+  const uint16_t *w_down;
+  const int32_t *ids;  // [rows, topk]
+  const float *weights;
+  uint16_t *out;             // [rows, hidden], or the mailbox when out_slots is set
+  const int32_t *out_slots;  // mailbox row of each row, or null
+  int64_t out_rows;
+  uint8_t *workspace;  // moe_workspace(capacity, ...)
+  int64_t rows;
+  int64_t hidden;
+  int64_t intermediate;
+  int64_t experts;
+  int64_t topk;
+  float scale;
+  GatedSilu act;
+};
+
+struct ExpertsLaunches {
+  KernelLaunch sort;
+  KernelLaunch gate_up;
+  KernelLaunch down;
+  KernelLaunch combine;
+};
+
+int make_experts_launches(const ExpertsBinding &b, int64_t capacity, ExpertsLaunches &out) {
+  const MoeWorkspace layout = moe_workspace(capacity, b.hidden, b.intermediate, b.experts, b.topk);
+  int32_t *expert_end = reinterpret_cast<int32_t *>(b.workspace + layout.expert_end);
+  int32_t *sorted_route = reinterpret_cast<int32_t *>(b.workspace + layout.sorted_route);
+  float *sorted_weight = reinterpret_cast<float *>(b.workspace + layout.sorted_weight);
+  int32_t *tile_expert = reinterpret_cast<int32_t *>(b.workspace + layout.tile_expert);
+  int32_t *tile_row0 = reinterpret_cast<int32_t *>(b.workspace + layout.tile_row0);
+  uint16_t *activated = reinterpret_cast<uint16_t *>(b.workspace + layout.activated);
+  uint16_t *route_out = reinterpret_cast<uint16_t *>(b.workspace + layout.route_out);
+  const int64_t routes = b.rows * b.topk;
+  const int64_t capacity_routes = capacity * b.topk;
+  const MoeTile tile = choose_moe_tile(capacity_routes, b.experts);
+  const int tile_rows = moe_tile_rows(tile);
+  const int max_tiles = moe_tile_bound(capacity_routes, b.experts, tile_rows);
+  XP_REQUIRE(max_tiles <= 65535, "too many expert tiles for one call");
+
+  MoeSortArgs sort{};
+  sort.ids = b.ids;
+  sort.weights = b.weights;
+  sort.sorted_weight = sorted_weight;
+  sort.expert_end = expert_end;
+  sort.sorted_route = sorted_route;
+  sort.tile_expert = tile_expert;
+  sort.tile_row0 = tile_row0;
+  sort.routes = routes;
+  sort.experts = static_cast<int32_t>(b.experts);
+  sort.tile_rows = tile_rows;
+  sort.max_tiles = max_tiles;
+  out.sort = make_moe_sort(sort);
+
+  // gate_up gathers the token row of each sorted route (route / topk) itself and writes the
+  // activated rows in sorted order; down scales each sorted row by its route weight and
+  // writes it to the route's row.
+  GemmArgs up{};
+  up.x = b.x;
+  up.gather_slots = sorted_route;
+  up.gather_divisor = b.topk;
+  up.pool_rows = b.rows;
+  up.w = b.w_gate_up;
+  up.out = activated;
+  up.ldx = b.hidden;
+  up.ldo = b.intermediate;
+  up.rows = routes;
+  up.capacity = routes;
+  up.out_rows = routes;
+  up.n = 2 * b.intermediate;
+  up.k = b.hidden;
+  up.act = b.act;
+  up.tile_expert = tile_expert;
+  up.tile_row0 = tile_row0;
+  up.expert_end = expert_end;
+
+  GemmArgs dn = up;
+  dn.x = activated;
+  dn.gather_slots = nullptr;
+  dn.w = b.w_down;
+  dn.out = route_out;
+  dn.scatter_slots = sorted_route;
+  dn.row_scale = sorted_weight;
+  dn.ldx = b.intermediate;
+  dn.ldo = b.hidden;
+  dn.n = b.hidden;
+  dn.k = b.intermediate;
+  dn.act = default_activation();
+
+  if (tile == MoeTile::Large) {
+    // Many routes per expert: the Dense tile kernel in its grouped mode.
+    if (moe_tile_rows(MoeTile::Large) != grouped_tile_rows()) {
+      return fail(XP_ERROR_STATE, "expert tile table and grouped tile kernel disagree on the tile rows");
+    }
+    out.gate_up = make_grouped_gemm(up, true, max_tiles);
+    out.down = make_grouped_gemm(dn, false, max_tiles);
+  } else {
+    // Few routes per expert: each touched expert's weights streamed by the grouped split
+    // kernel; about one tile per touched expert.
+    if (moe_tile_rows(MoeTile::Small) != grouped_split_rows()) {
+      return fail(XP_ERROR_STATE, "expert tile table and grouped split kernel disagree on the tile rows");
+    }
+    const int64_t live_tiles = b.experts < capacity_routes ? b.experts : capacity_routes;
+    out.gate_up = make_grouped_split(up, true, max_tiles, live_tiles);
+    out.down = make_grouped_split(dn, false, max_tiles, live_tiles);
+  }
+
+  MoeCombineArgs combine{};
+  combine.routes = route_out;
+  combine.ids = b.ids;
+  combine.out = b.out;
+  combine.slots = b.out_slots;
+  combine.out_rows = b.out_rows;
+  combine.rows = capacity;
+  combine.hidden = b.hidden;
+  combine.topk = static_cast<int32_t>(b.topk);
+  combine.experts = static_cast<int32_t>(b.experts);
+  combine.scale = b.scale;
+  out.combine = make_moe_combine(combine);
+  combine.rows = b.rows;
+  out.combine.set_args(combine);
+  return XP_OK;
+}
+
+// ------------------------------------------------------------------ MoE step
+int64_t effective_topk(const xp_moe_layer_desc &d) { return d.routed_topk + (d.experts - d.routed_experts); }
+
+bool same_moe(const xp_moe_layer_desc &a, const xp_moe_layer_desc &b) {
+  return a.hidden == b.hidden && a.intermediate == b.intermediate && a.experts == b.experts &&
+         a.routed_experts == b.routed_experts && a.routed_topk == b.routed_topk && a.algorithm == b.algorithm &&
+         a.precision == b.precision && (a.renormalize != 0) == (b.renormalize != 0) &&
+         a.weight_rounding == b.weight_rounding && a.routed_scaling_factor == b.routed_scaling_factor &&
+         a.alpha == b.alpha && a.limit == b.limit && a.up_offset == b.up_offset;
+}
+
+int validate_moe_desc(const xp_moe_layer_desc *d) {
+  XP_REQUIRE(d != nullptr, "MoE layer descriptor must be non-null");
+  XP_REQUIRE(d->hidden > 0 && d->hidden % 8 == 0 && d->intermediate > 0 && d->intermediate % 8 == 0,
+             "hidden and intermediate sizes must be positive multiples of 8");
+  XP_REQUIRE(gather_supported(d->hidden), "hidden size exceeds the gather kernel's register row (16384)");
+  XP_REQUIRE(d->experts >= 1 && d->experts <= kMoeMaxExperts, "Experts support 1 to 1024 experts");
+  XP_REQUIRE(d->routed_experts >= 1 && d->routed_experts <= d->experts,
+             "routed experts must be between 1 and the expert count");
+  if (const int status = validate_router(d->routed_experts, d->routed_topk, d->algorithm, d->precision,
+                                         d->weight_rounding);
+      status != XP_OK) {
+    return status;
+  }
+  XP_REQUIRE(d->routed_scaling_factor > 0.0f && d->routed_scaling_factor < __builtin_inff(),
+             "routed scaling factor must be finite and positive");
+  XP_REQUIRE(d->alpha > 0.0f && d->alpha < __builtin_inff(), "SiLU alpha must be positive and finite");
+  XP_REQUIRE(d->limit >= 0.0f && d->limit < __builtin_inff() && std::isfinite(d->up_offset),
+             "gate limit must be finite and non-negative (0 = none) and the up offset finite");
+  XP_REQUIRE(2 * d->intermediate * d->hidden * 2 < (int64_t{1} << 31),
+             "one expert's gate_up must stay below 2 GiB (32-bit buffer range)");
+  return XP_OK;
+}
+
+// Lane workspace of a MoE step at `capacity`: the gathered batch, the Router workspace
+// (logits first), routed ids and weights, final ids and weights when shared experts add
+// slots, then the Experts workspace; each region 256-byte aligned.
+struct MoeStepWorkspace {
+  size_t batch;
+  size_t router;
+  size_t routed_ids;
+  size_t routed_weights;
+  size_t final_ids;
+  size_t final_weights;
+  size_t experts;
+  size_t bytes;
+};
+
+MoeStepWorkspace moe_step_workspace(const xp_moe_layer_desc &d, int64_t capacity) {
+  MoeStepWorkspace layout{};
+  size_t cursor = 0;
+  auto region = [&](size_t bytes) {
+    const size_t offset = cursor;
+    cursor = align_up(cursor + bytes, 256);
+    return offset;
+  };
+  const int64_t topk = effective_topk(d);
+  layout.batch = region(static_cast<size_t>(capacity * d.hidden) * 2);
+  layout.router = region(router_workspace(capacity, d.hidden, d.routed_experts, d.precision).bytes);
+  layout.routed_ids = region(static_cast<size_t>(capacity * d.routed_topk) * 4);
+  layout.routed_weights = region(static_cast<size_t>(capacity * d.routed_topk) * 4);
+  if (topk > d.routed_topk) {
+    layout.final_ids = region(static_cast<size_t>(capacity * topk) * 4);
+    layout.final_weights = region(static_cast<size_t>(capacity * topk) * 4);
+  } else {
+    layout.final_ids = layout.routed_ids;
+    layout.final_weights = layout.routed_weights;
+  }
+  layout.experts = region(moe_workspace(capacity, d.hidden, d.intermediate, d.experts, topk).bytes);
+  layout.bytes = cursor;
+  return layout;
+}
+
+int validate_moe_capacity(const xp_moe_layer_desc &d, int64_t capacity) {
+  XP_REQUIRE(capacity > 0, "template capacity must be positive");
+  return validate_experts(capacity, d.hidden, d.intermediate, d.experts, effective_topk(d));
+}
+
+// One MoE mailbox step: gather (+ RMSNorm) into the batch, Router, finalisation (shared
+// experts only), Experts with the combine scattered to the slots of pool_out.  Grids and
+// kernel choices follow `capacity`; the argument records carry the live rows.
+struct MoeStepBinding {
+  const uint16_t *pool_in;
+  uint16_t *pool_out;
+  int64_t pool_rows;
+  const int32_t *slots;
+  int64_t rows;
+  uint8_t *workspace;
+  uint32_t *fault;
+};
+
+int make_moe_step(const Layer &layer, const MoeStepBinding &b, int64_t capacity, StepChain &chain) {
+  const xp_moe_layer_desc &d = layer.moe;
+  const MoeStepWorkspace layout = moe_step_workspace(d, capacity);
+  uint16_t *batch = reinterpret_cast<uint16_t *>(b.workspace + layout.batch);
+  int32_t *routed_ids = reinterpret_cast<int32_t *>(b.workspace + layout.routed_ids);
+  float *routed_weights = reinterpret_cast<float *>(b.workspace + layout.routed_weights);
+  int32_t *final_ids = reinterpret_cast<int32_t *>(b.workspace + layout.final_ids);
+  float *final_weights = reinterpret_cast<float *>(b.workspace + layout.final_weights);
+  const int64_t topk = effective_topk(d);
+
+  GatherArgs gather{};
+  gather.pool = b.pool_in;
+  gather.slots = b.slots;
+  gather.norm = layer.norm;
+  gather.out = batch;
+  gather.fault = b.fault;
+  gather.pool_rows = b.pool_rows;
+  gather.hidden = d.hidden;
+  gather.rows = b.rows;
+  gather.eps = layer.eps;
+  chain.add(make_gather(gather, capacity));
+
+  RouterBinding router{};
+  router.x = batch;
+  router.w = layer.router;
+  router.correction_bias = layer.correction_bias;
+  router.ids = routed_ids;
+  router.weights = routed_weights;
+  router.workspace = b.workspace + layout.router;
+  router.rows = b.rows;
+  router.hidden = d.hidden;
+  router.experts = d.routed_experts;
+  router.topk = d.routed_topk;
+  router.algorithm = d.algorithm;
+  router.precision = d.precision;
+  router.renormalize = d.renormalize;
+  router.weight_rounding = d.weight_rounding;
+  const RouterLaunches routing = make_router_launches(router, capacity);
+  chain.add(routing.logits);
+  chain.add(routing.logits_reduce);
+  chain.add(routing.topk);
+
+  if (topk > d.routed_topk) {
+    // Shared experts: every live row also takes slots routed_experts + s (weight
+    // 1 / scaling, which the combine's scale cancels).
+    FinalizeRoutingArgs finalize{};
+    finalize.routed_ids = routed_ids;
+    finalize.routed_weights = routed_weights;
+    finalize.final_ids = final_ids;
+    finalize.final_weights = final_weights;
+    finalize.payload_rows = nullptr;
+    finalize.capacity = capacity;
+    finalize.routed_topk = static_cast<int32_t>(d.routed_topk);
+    finalize.effective_topk = static_cast<int32_t>(topk);
+    finalize.routed_experts = static_cast<int32_t>(d.routed_experts);
+    finalize.shared_weight = 1.0f / d.routed_scaling_factor;
+    KernelLaunch kernel = make_finalize_routing(finalize);
+    finalize.capacity = b.rows;
+    kernel.set_args(finalize);
+    chain.add(kernel);
+  }
+
+  ExpertsBinding experts{};
+  experts.x = batch;
+  experts.w_gate_up = layer.gate_up;
+  experts.w_down = layer.down;
+  experts.ids = final_ids;
+  experts.weights = final_weights;
+  experts.out = b.pool_out;
+  experts.out_slots = b.slots;
+  experts.out_rows = b.pool_rows;
+  experts.workspace = b.workspace + layout.experts;
+  experts.rows = b.rows;
+  experts.hidden = d.hidden;
+  experts.intermediate = d.intermediate;
+  experts.experts = d.experts;
+  experts.topk = topk;
+  experts.scale = d.routed_scaling_factor;
+  experts.act = GatedSilu{d.alpha, d.limit, d.up_offset};
+  ExpertsLaunches launches;
+  if (const int status = make_experts_launches(experts, capacity, launches); status != XP_OK) {
+    return status;
+  }
+  chain.add(launches.sort);
+  chain.add(launches.gate_up);
+  chain.add(launches.down);
+  chain.add(launches.combine);
+  return XP_OK;
+}
+
 TransportArgs transport_args(xp_transport_t transport, int arena) {
   TransportArgs args{};
   args.arenas = transport->arenas;
@@ -406,6 +842,89 @@ void destroy_template(Template &t) {
     (void)hipGraphDestroy(t.graph);
     t.graph = nullptr;
   }
+}
+
+StepChain dense_chain(const DenseBinding &binding, int64_t capacity) {
+  const DenseLaunches launches = make_dense_launches(binding, capacity);
+  const KernelLaunch *kernels[kMaxStepKernels];
+  const int count = launches.chain(kernels);
+  StepChain chain;
+  for (int index = 0; index < count; ++index) {
+    chain.add(*kernels[index]);
+  }
+  return chain;
+}
+
+// Build and instantiate a template's hipGraph: one kernel node per chain entry, each
+// depending on the previous one.
+int instantiate_template(Template &t, const StepChain &chain) {
+  XP_HIP_CHECK(hipGraphCreate(&t.graph, 0));
+  t.node_count = chain.count;
+  for (int index = 0; index < chain.count; ++index) {
+    const KernelLaunch &kernel = chain.kernels[index];
+    if (kernel.shmem > 64 * 1024) {
+      const hipError_t enabled = enable_large_lds(kernel.func);
+      if (enabled != hipSuccess) {
+        destroy_template(t);
+        return fail(XP_ERROR_HIP, std::string("enabling dynamic LDS above 64 KB failed: ") + hipGetErrorString(enabled));
+      }
+    }
+    void *params[1];
+    hipKernelNodeParams node = node_params(kernel, params);
+    const hipGraphNode_t *dependencies = index == 0 ? nullptr : &t.nodes[index - 1];
+    const hipError_t added = hipGraphAddKernelNode(&t.nodes[index], t.graph, dependencies, index == 0 ? 0 : 1, &node);
+    if (added != hipSuccess) {
+      destroy_template(t);
+      return fail(XP_ERROR_HIP, std::string("hipGraphAddKernelNode failed: ") + hipGetErrorString(added));
+    }
+    t.bound[index] = kernel;
+  }
+  const hipError_t instantiated = hipGraphInstantiate(&t.exec, t.graph, nullptr, nullptr, 0);
+  if (instantiated != hipSuccess) {
+    destroy_template(t);
+    return fail(XP_ERROR_HIP, std::string("hipGraphInstantiate failed: ") + hipGetErrorString(instantiated));
+  }
+  return XP_OK;
+}
+
+void insert_template(xp_lane *lane, std::unique_ptr<Template> t) {
+  lane->templates.push_back(std::move(t));
+  std::stable_sort(lane->templates.begin(), lane->templates.end(), [](const auto &left, const auto &right) {
+    if (left->kind != right->kind) return left->kind < right->kind;
+    if (left->hidden != right->hidden) return left->hidden < right->hidden;
+    if (left->intermediate != right->intermediate) return left->intermediate < right->intermediate;
+    return left->capacity < right->capacity;
+  });
+}
+
+// Launch a replay's chain: directly on the stream, or (graph dispatch) by rebinding the
+// template's nodes whose argument record changed and launching its graph.
+int run_chain(xp_lane *lane, Template &t, const StepChain &chain, hipStream_t target) {
+  if (chain.count != t.node_count) {
+    return fail(XP_ERROR_STATE, "replay kernel sequence differs from the captured template");
+  }
+  if (!lane->graph_dispatch) {
+    for (int index = 0; index < chain.count; ++index) {
+      XP_HIP_CHECK(launch(chain.kernels[index], target));
+    }
+    return XP_OK;
+  }
+  for (int index = 0; index < chain.count; ++index) {
+    const KernelLaunch &kernel = chain.kernels[index];
+    KernelLaunch &bound = t.bound[index];
+    if (bound.func != kernel.func) {
+      return fail(XP_ERROR_STATE, "replay kernel differs from the captured template's node");
+    }
+    if (bound.args_size == kernel.args_size && std::memcmp(bound.args, kernel.args, bound.args_size) == 0) {
+      continue;
+    }
+    void *params[1];
+    hipKernelNodeParams node = node_params(kernel, params);
+    XP_HIP_CHECK(hipGraphExecKernelNodeSetParams(t.exec, t.nodes[index], &node));
+    bound = kernel;
+  }
+  XP_HIP_CHECK(hipGraphLaunch(t.exec, target));
+  return XP_OK;
 }
 
 const Layer *find_layer(const xp_agent *agent, int instance_index, int layer_ordinal) {
@@ -1007,7 +1526,8 @@ int xp_template_capture(xp_lane_t lane, int64_t hidden, int64_t intermediate, in
   }
   std::lock_guard<std::mutex> guard(lane->mutex);
   for (const auto &t : lane->templates) {
-    if (t->hidden == hidden && t->intermediate == intermediate && t->capacity == capacity) {
+    if (t->kind == XP_LAYER_DENSE && t->hidden == hidden && t->intermediate == intermediate &&
+        t->capacity == capacity) {
       return XP_OK;
     }
   }
@@ -1019,44 +1539,15 @@ int xp_template_capture(xp_lane_t lane, int64_t hidden, int64_t intermediate, in
   binding.rows = 0;
   binding.workspace = lane->workspace;
   binding.fault = lane->fault;
-  const DenseLaunches launches = make_dense_launches(binding, capacity);
-
   auto t = std::make_unique<Template>();
+  t->kind = XP_LAYER_DENSE;
   t->hidden = hidden;
   t->intermediate = intermediate;
   t->capacity = capacity;
-  XP_HIP_CHECK(hipGraphCreate(&t->graph, 0));
-  const KernelLaunch *chain[kMaxStepKernels];
-  t->node_count = launches.chain(chain);
-  for (int index = 0; index < t->node_count; ++index) {
-    if (chain[index]->shmem > 64 * 1024) {
-      const hipError_t enabled = enable_large_lds(chain[index]->func);
-      if (enabled != hipSuccess) {
-        destroy_template(*t);
-        return fail(XP_ERROR_HIP, std::string("enabling dynamic LDS above 64 KB failed: ") + hipGetErrorString(enabled));
-      }
-    }
-    void *params[1];
-    hipKernelNodeParams node = node_params(*chain[index], params);
-    const hipGraphNode_t *dependencies = index == 0 ? nullptr : &t->nodes[index - 1];
-    const hipError_t added = hipGraphAddKernelNode(&t->nodes[index], t->graph, dependencies, index == 0 ? 0 : 1, &node);
-    if (added != hipSuccess) {
-      destroy_template(*t);
-      return fail(XP_ERROR_HIP, std::string("hipGraphAddKernelNode failed: ") + hipGetErrorString(added));
-    }
-    t->bound[index] = *chain[index];
+  if (const int status = instantiate_template(*t, dense_chain(binding, capacity)); status != XP_OK) {
+    return status;
   }
-  const hipError_t instantiated = hipGraphInstantiate(&t->exec, t->graph, nullptr, nullptr, 0);
-  if (instantiated != hipSuccess) {
-    destroy_template(*t);
-    return fail(XP_ERROR_HIP, std::string("hipGraphInstantiate failed: ") + hipGetErrorString(instantiated));
-  }
-  lane->templates.push_back(std::move(t));
-  std::sort(lane->templates.begin(), lane->templates.end(), [](const auto &left, const auto &right) {
-    if (left->hidden != right->hidden) return left->hidden < right->hidden;
-    if (left->intermediate != right->intermediate) return left->intermediate < right->intermediate;
-    return left->capacity < right->capacity;
-  });
+  insert_template(lane, std::move(t));
   return XP_OK;
 }
 
@@ -1066,7 +1557,7 @@ int xp_template_capacities(xp_lane_t lane, int64_t hidden, int64_t intermediate,
   std::lock_guard<std::mutex> guard(lane->mutex);
   int found = 0;
   for (const auto &t : lane->templates) {
-    if (t->hidden == hidden && t->intermediate == intermediate) {
+    if (t->kind == XP_LAYER_DENSE && t->hidden == hidden && t->intermediate == intermediate) {
       if (capacities != nullptr && found < max_count) {
         capacities[found] = t->capacity;
       }
@@ -1097,7 +1588,10 @@ int xp_replay(xp_lane_t lane, int instance_index, int layer_ordinal, int64_t row
   Template *selected = nullptr;
   int64_t largest = 0;
   for (const auto &t : lane->templates) {
-    if (t->hidden == layer.hidden && t->intermediate == layer.intermediate) {
+    const bool serves = t->kind == layer.kind &&
+                        (layer.kind == XP_LAYER_MOE ? same_moe(t->moe, layer.moe)
+                                                    : t->hidden == layer.hidden && t->intermediate == layer.intermediate);
+    if (serves) {
       largest = std::max(largest, t->capacity);
       if (selected == nullptr && rows <= t->capacity) {
         selected = t.get();
@@ -1107,6 +1601,23 @@ int xp_replay(xp_lane_t lane, int instance_index, int layer_ordinal, int64_t row
   if (rows < 1 || selected == nullptr) {
     return fail(XP_ERROR_CAPACITY, "row count " + std::to_string(rows) + " is outside the installed capacities [1, " +
                                        std::to_string(largest) + "]");
+  }
+  // NULL is the legacy default stream, as for every other entry point.
+  const hipStream_t target = static_cast<hipStream_t>(stream);
+  if (layer.kind == XP_LAYER_MOE) {
+    MoeStepBinding binding{};
+    binding.pool_in = static_cast<const uint16_t *>(pool_in);
+    binding.pool_out = static_cast<uint16_t *>(pool_out);
+    binding.pool_rows = pool_rows;
+    binding.slots = slots;
+    binding.rows = rows;
+    binding.workspace = lane->workspace;
+    binding.fault = lane->fault;
+    StepChain chain;
+    if (const int status = make_moe_step(layer, binding, selected->capacity, chain); status != XP_OK) {
+      return status;
+    }
+    return run_chain(lane, *selected, chain, target);
   }
   DenseBinding binding{};
   binding.pool_in = static_cast<const uint16_t *>(pool_in);
@@ -1122,32 +1633,7 @@ int xp_replay(xp_lane_t lane, int instance_index, int layer_ordinal, int64_t row
   binding.eps = layer.eps;
   binding.workspace = lane->workspace;
   binding.fault = lane->fault;
-  const DenseLaunches launches = make_dense_launches(binding, selected->capacity);
-  const KernelLaunch *chain[kMaxStepKernels];
-  if (launches.chain(chain) != selected->node_count) {
-    return fail(XP_ERROR_STATE, "replay kernel sequence differs from the captured template");
-  }
-  // NULL is the legacy default stream, as for every other entry point.
-  const hipStream_t target = static_cast<hipStream_t>(stream);
-  if (!lane->graph_dispatch) {
-    for (int index = 0; index < selected->node_count; ++index) {
-      XP_HIP_CHECK(launch(*chain[index], target));
-    }
-    return XP_OK;
-  }
-  for (int index = 0; index < selected->node_count; ++index) {
-    KernelLaunch &bound = selected->bound[index];
-    if (bound.args_size == chain[index]->args_size && bound.func == chain[index]->func &&
-        std::memcmp(bound.args, chain[index]->args, bound.args_size) == 0) {
-      continue;
-    }
-    void *params[1];
-    hipKernelNodeParams node = node_params(*chain[index], params);
-    XP_HIP_CHECK(hipGraphExecKernelNodeSetParams(selected->exec, selected->nodes[index], &node));
-    bound = *chain[index];
-  }
-  XP_HIP_CHECK(hipGraphLaunch(selected->exec, target));
-  return XP_OK;
+  return run_chain(lane, *selected, dense_chain(binding, selected->capacity), target);
 }
 
 
@@ -1404,57 +1890,40 @@ int xp_moe_router(const void *hidden_states, int64_t rows, int64_t hidden, const
                   size_t workspace_bytes, xp_stream_t stream) {
   XP_REQUIRE(rows >= 0, "row count must be non-negative");
   XP_REQUIRE(hidden > 0, "hidden size must be positive");
-  XP_REQUIRE(precision == XP_ROUTER_PRECISION_PAYLOAD || precision == XP_ROUTER_PRECISION_FP32 ||
-                 precision == XP_ROUTER_PRECISION_FP32_LOGITS,
-             "router projection precision is unknown");
-  XP_REQUIRE(experts >= 1 && experts <= kMoeMaxExperts, "the router supports 1 to 1024 experts");
-  XP_REQUIRE(topk >= 1 && topk <= experts && topk <= 64, "topk must be between 1 and min(experts, 64)");
+  if (const int status = validate_router(experts, topk, algorithm, precision, weight_rounding); status != XP_OK) {
+    return status;
+  }
   if (rows == 0) {
     return XP_OK;
   }
-  XP_REQUIRE(hidden_states != nullptr && router_weights != nullptr, "router inputs must be non-null");
-  const bool mfma = router_uses_mfma(hidden, experts, precision);
-  XP_REQUIRE(!mfma || (aligned16(hidden_states) && aligned16(router_weights)),
+  XP_REQUIRE(hidden_states != nullptr && router_weights != nullptr && ids != nullptr && weights != nullptr,
+             "router pointers must be non-null");
+  XP_REQUIRE(!router_uses_mfma(hidden, experts, precision) || (aligned16(hidden_states) && aligned16(router_weights)),
              "router inputs must be 16-byte aligned");
   const RouterWorkspace layout = router_workspace(rows, hidden, experts, precision);
   XP_REQUIRE(workspace != nullptr && workspace_bytes >= layout.bytes && aligned16(workspace),
              "router workspace is missing or smaller than xp_moe_router_workspace_bytes");
-  uint8_t *base = static_cast<uint8_t *>(workspace);
+  RouterBinding binding{};
+  binding.x = static_cast<const uint16_t *>(hidden_states);
+  binding.w = router_weights;
+  binding.correction_bias = correction_bias;
+  binding.ids = ids;
+  binding.weights = weights;
+  binding.workspace = static_cast<uint8_t *>(workspace);
+  binding.rows = rows;
+  binding.hidden = hidden;
+  binding.experts = experts;
+  binding.topk = topk;
+  binding.algorithm = algorithm;
+  binding.precision = precision;
+  binding.renormalize = renormalize;
+  binding.weight_rounding = weight_rounding;
+  const RouterLaunches launches = make_router_launches(binding, rows);
   const hipStream_t hip_stream = static_cast<hipStream_t>(stream);
-  void *logits = base + layout.logits;
-  if (mfma) {
-    // logits = bf16(x . w^T): the Dense projection kernels, no epilogue.
-    const GemmChoice choice = choose_gemm(rows, experts, hidden, false);
-    GemmArgs args{};
-    args.x = static_cast<const uint16_t *>(hidden_states);
-    args.w = static_cast<const uint16_t *>(router_weights);
-    args.out = static_cast<uint16_t *>(logits);
-    args.partials = layout.scratch_bytes > 0 ? reinterpret_cast<float *>(base + layout.scratch) : nullptr;
-    args.ldx = hidden;
-    args.ldo = experts;
-    args.rows = rows;
-    args.capacity = rows;
-    args.out_rows = rows;
-    args.n = experts;
-    args.k = hidden;
-    args.act = default_activation();
-    const GemmLaunch gemm = make_gemm(args, rows, false, choice);
-    XP_HIP_CHECK(launch(gemm.main, hip_stream));
-    XP_HIP_CHECK(launch(gemm.reduce, hip_stream));
-  } else {
-    RouterLogitsArgs args{};
-    args.x = static_cast<const uint16_t *>(hidden_states);
-    args.w = router_weights;
-    args.logits = logits;
-    args.rows = rows;
-    args.hidden = hidden;
-    args.experts = static_cast<int32_t>(experts);
-    args.weights_f32 = precision == XP_ROUTER_PRECISION_FP32 ? 1 : 0;
-    args.out_bf16 = precision == XP_ROUTER_PRECISION_PAYLOAD ? 1 : 0;
-    XP_HIP_CHECK(launch(make_router_logits(args), hip_stream));
+  for (const KernelLaunch *kernel : {&launches.logits, &launches.logits_reduce, &launches.topk}) {
+    XP_HIP_CHECK(launch(*kernel, hip_stream));
   }
-  return xp_moe_router_topk(logits, precision == XP_ROUTER_PRECISION_PAYLOAD ? 0 : 1, rows, experts, topk, algorithm,
-                            correction_bias, renormalize, weight_rounding, ids, weights, stream);
+  return XP_OK;
 }
 
 int xp_moe_finalize_routing(const int32_t *routed_ids, const float *routed_weights, int64_t capacity,
@@ -1512,16 +1981,9 @@ int xp_moe_experts(const void *hidden_states, int64_t rows, int64_t hidden, int6
                    const float *topk_weights, float routed_scaling_factor, float alpha, float limit, float up_offset,
                    void *output, void *workspace, size_t workspace_bytes, xp_stream_t stream) {
   XP_REQUIRE(rows >= 0, "row count must be non-negative");
-  XP_REQUIRE(hidden > 0 && hidden % 8 == 0 && intermediate > 0 && intermediate % 8 == 0,
-             "hidden and intermediate sizes must be positive multiples of 8");
-  XP_REQUIRE(experts >= 1 && experts <= kMoeMaxExperts, "Experts support 1 to 1024 experts");
-  XP_REQUIRE(topk >= 1 && topk <= experts, "topk must be between 1 and the expert count");
-  XP_REQUIRE(rows * topk <= (int64_t{1} << 30), "too many routes for one call");
-  // The projections address the token rows, the activated routes and one expert's weights
-  // through 32-bit buffer ranges.
-  XP_REQUIRE(rows * hidden * 2 < (int64_t{1} << 31) && rows * topk * intermediate * 2 < (int64_t{1} << 31) &&
-                 2 * intermediate * hidden * 2 < (int64_t{1} << 31),
-             "Experts tensors must stay below 2 GiB per buffer range");
+  if (const int status = validate_experts(rows, hidden, intermediate, experts, topk); status != XP_OK) {
+    return status;
+  }
   XP_REQUIRE(alpha > 0.0f, "SiLU alpha must be positive");
   if (rows == 0) {
     return XP_OK;
@@ -1534,98 +1996,145 @@ int xp_moe_experts(const void *hidden_states, int64_t rows, int64_t hidden, int6
   const MoeWorkspace layout = moe_workspace(rows, hidden, intermediate, experts, topk);
   XP_REQUIRE(workspace != nullptr && workspace_bytes >= layout.bytes && aligned16(workspace),
              "Experts workspace is missing or smaller than xp_moe_workspace_bytes");
-  uint8_t *base = static_cast<uint8_t *>(workspace);
-  int32_t *expert_end = reinterpret_cast<int32_t *>(base + layout.expert_end);
-  int32_t *sorted_route = reinterpret_cast<int32_t *>(base + layout.sorted_route);
-  float *sorted_weight = reinterpret_cast<float *>(base + layout.sorted_weight);
-  int32_t *tile_expert = reinterpret_cast<int32_t *>(base + layout.tile_expert);
-  int32_t *tile_row0 = reinterpret_cast<int32_t *>(base + layout.tile_row0);
-  uint16_t *activated = reinterpret_cast<uint16_t *>(base + layout.activated);
-  uint16_t *route_out = reinterpret_cast<uint16_t *>(base + layout.route_out);
-  const int64_t routes = rows * topk;
-  const MoeTile tile = choose_moe_tile(routes, experts);
-  const int tile_rows = moe_tile_rows(tile);
-  const int max_tiles = moe_tile_bound(routes, experts, tile_rows);
-  XP_REQUIRE(max_tiles <= 65535, "too many expert tiles for one call");
-  const hipStream_t hip_stream = static_cast<hipStream_t>(stream);
-
-  MoeSortArgs sort{};
-  sort.ids = topk_ids;
-  sort.weights = topk_weights;
-  sort.sorted_weight = sorted_weight;
-  sort.expert_end = expert_end;
-  sort.sorted_route = sorted_route;
-  sort.tile_expert = tile_expert;
-  sort.tile_row0 = tile_row0;
-  sort.routes = routes;
-  sort.experts = static_cast<int32_t>(experts);
-  sort.tile_rows = tile_rows;
-  sort.max_tiles = max_tiles;
-  XP_HIP_CHECK(launch(make_moe_sort(sort), hip_stream));
-
-  // gate_up gathers the token row of each sorted route (route / topk) itself and writes the
-  // activated rows in sorted order; down scales each sorted row by its route weight and
-  // writes it to the route's row.
-  GemmArgs up{};
-  up.x = static_cast<const uint16_t *>(hidden_states);
-  up.gather_slots = sorted_route;
-  up.gather_divisor = topk;
-  up.pool_rows = rows;
-  up.w = static_cast<const uint16_t *>(w_gate_up);
-  up.out = activated;
-  up.ldx = hidden;
-  up.ldo = intermediate;
-  up.rows = routes;
-  up.capacity = routes;
-  up.out_rows = routes;
-  up.n = 2 * intermediate;
-  up.k = hidden;
-  up.act = GatedSilu{alpha, limit, up_offset};
-  up.tile_expert = tile_expert;
-  up.tile_row0 = tile_row0;
-  up.expert_end = expert_end;
-
-  GemmArgs dn = up;
-  dn.x = activated;
-  dn.gather_slots = nullptr;
-  dn.w = static_cast<const uint16_t *>(w_down);
-  dn.out = route_out;
-  dn.scatter_slots = sorted_route;
-  dn.row_scale = sorted_weight;
-  dn.ldx = intermediate;
-  dn.ldo = hidden;
-  dn.n = hidden;
-  dn.k = intermediate;
-  dn.act = default_activation();
-
-  if (tile == MoeTile::Large) {
-    // Many routes per expert: the Dense tile kernel in its grouped mode.
-    if (moe_tile_rows(MoeTile::Large) != grouped_tile_rows()) {
-      return fail(XP_ERROR_STATE, "expert tile table and grouped tile kernel disagree on the tile rows");
-    }
-    XP_HIP_CHECK(launch(make_grouped_gemm(up, true, max_tiles), hip_stream));
-    XP_HIP_CHECK(launch(make_grouped_gemm(dn, false, max_tiles), hip_stream));
-  } else {
-    // Few routes per expert: each touched expert's weights streamed by the grouped split
-    // kernel; about one tile per touched expert.
-    if (moe_tile_rows(MoeTile::Small) != grouped_split_rows()) {
-      return fail(XP_ERROR_STATE, "expert tile table and grouped split kernel disagree on the tile rows");
-    }
-    const int64_t live_tiles = experts < routes ? experts : routes;
-    XP_HIP_CHECK(launch(make_grouped_split(up, true, max_tiles, live_tiles), hip_stream));
-    XP_HIP_CHECK(launch(make_grouped_split(dn, false, max_tiles, live_tiles), hip_stream));
+  ExpertsBinding binding{};
+  binding.x = static_cast<const uint16_t *>(hidden_states);
+  binding.w_gate_up = static_cast<const uint16_t *>(w_gate_up);
+  binding.w_down = static_cast<const uint16_t *>(w_down);
+  binding.ids = topk_ids;
+  binding.weights = topk_weights;
+  binding.out = static_cast<uint16_t *>(output);
+  binding.workspace = static_cast<uint8_t *>(workspace);
+  binding.rows = rows;
+  binding.hidden = hidden;
+  binding.intermediate = intermediate;
+  binding.experts = experts;
+  binding.topk = topk;
+  binding.scale = routed_scaling_factor;
+  binding.act = GatedSilu{alpha, limit, up_offset};
+  ExpertsLaunches launches;
+  if (const int status = make_experts_launches(binding, rows, launches); status != XP_OK) {
+    return status;
   }
+  const hipStream_t hip_stream = static_cast<hipStream_t>(stream);
+  for (const KernelLaunch *kernel : {&launches.sort, &launches.gate_up, &launches.down, &launches.combine}) {
+    XP_HIP_CHECK(launch(*kernel, hip_stream));
+  }
+  return XP_OK;
+}
 
-  MoeCombineArgs combine{};
-  combine.routes = route_out;
-  combine.ids = topk_ids;
-  combine.out = static_cast<uint16_t *>(output);
-  combine.rows = rows;
-  combine.hidden = hidden;
-  combine.topk = static_cast<int32_t>(topk);
-  combine.experts = static_cast<int32_t>(experts);
-  combine.scale = routed_scaling_factor;
-  XP_HIP_CHECK(launch(make_moe_combine(combine), hip_stream));
+// ------------------------------------------------------------------ MoE layer kind
+
+int xp_moe_layer_register(xp_agent_t agent, int instance_index, int layer_ordinal, const xp_moe_layer_desc *desc,
+                          const void *gate_up, const void *down, const void *router, const float *correction_bias,
+                          const void *norm_weight, float eps) {
+  XP_REQUIRE(agent != nullptr, "agent must be non-null");
+  XP_REQUIRE(instance_index >= 0 && layer_ordinal >= 0, "instance index and layer ordinal must be non-negative");
+  if (const int status = validate_moe_desc(desc); status != XP_OK) {
+    return status;
+  }
+  XP_REQUIRE(gate_up != nullptr && down != nullptr && router != nullptr, "MoE layer weights must be non-null");
+  XP_REQUIRE(aligned16(gate_up) && aligned16(down) && aligned16(router) &&
+                 (norm_weight == nullptr || aligned16(norm_weight)) && aligned_to(correction_bias, 4),
+             "MoE layer weights must be 16-byte aligned (the correction bias 4-byte aligned)");
+  XP_REQUIRE(norm_weight == nullptr || eps >= 0.0f, "RMSNorm epsilon must be non-negative");
+  Layer layer{instance_index,
+              layer_ordinal,
+              desc->hidden,
+              desc->intermediate,
+              static_cast<const uint16_t *>(gate_up),
+              static_cast<const uint16_t *>(down),
+              static_cast<const uint16_t *>(norm_weight),
+              eps};
+  layer.kind = XP_LAYER_MOE;
+  layer.moe = *desc;
+  layer.moe.renormalize = desc->renormalize != 0 ? 1 : 0;
+  layer.router = router;
+  layer.correction_bias = correction_bias;
+  std::lock_guard<std::mutex> guard(agent->mutex);
+  for (Layer &existing : agent->layers) {
+    if (existing.instance_index == instance_index && existing.layer_ordinal == layer_ordinal) {
+      existing = layer;
+      return XP_OK;
+    }
+  }
+  agent->layers.push_back(layer);
+  return XP_OK;
+}
+
+size_t xp_moe_step_workspace_bytes(const xp_moe_layer_desc *desc, int64_t capacity) {
+  if (validate_moe_desc(desc) != XP_OK || validate_moe_capacity(*desc, capacity) != XP_OK) {
+    return 0;
+  }
+  return moe_step_workspace(*desc, capacity).bytes;
+}
+
+int xp_moe_step_workspace_layout(const xp_moe_layer_desc *desc, int64_t capacity, size_t *offsets) {
+  if (const int status = validate_moe_desc(desc); status != XP_OK) {
+    return status;
+  }
+  if (const int status = validate_moe_capacity(*desc, capacity); status != XP_OK) {
+    return status;
+  }
+  XP_REQUIRE(offsets != nullptr, "output pointer must be non-null");
+  const MoeStepWorkspace layout = moe_step_workspace(*desc, capacity);
+  offsets[0] = layout.batch;
+  offsets[1] = layout.router + router_workspace(capacity, desc->hidden, desc->routed_experts, desc->precision).logits;
+  offsets[2] = layout.routed_ids;
+  offsets[3] = layout.routed_weights;
+  offsets[4] = layout.final_ids;
+  offsets[5] = layout.final_weights;
+  offsets[6] = layout.experts;
+  offsets[7] = layout.bytes;
+  return XP_OK;
+}
+
+int xp_moe_template_capture(xp_lane_t lane, const xp_moe_layer_desc *desc, int64_t capacity) {
+  XP_REQUIRE(lane != nullptr, "lane must be non-null");
+  if (const int status = validate_moe_desc(desc); status != XP_OK) {
+    return status;
+  }
+  if (const int status = validate_moe_capacity(*desc, capacity); status != XP_OK) {
+    return status;
+  }
+  xp_moe_layer_desc signature = *desc;
+  signature.renormalize = desc->renormalize != 0 ? 1 : 0;
+  const size_t needed = moe_step_workspace(signature, capacity).bytes;
+  if (needed > lane->workspace_bytes) {
+    return fail(XP_ERROR_CAPACITY, "Lane workspace is smaller than the template needs (" + std::to_string(needed) +
+                                       " bytes)");
+  }
+  std::lock_guard<std::mutex> guard(lane->mutex);
+  for (const auto &t : lane->templates) {
+    if (t->kind == XP_LAYER_MOE && t->capacity == capacity && same_moe(t->moe, signature)) {
+      return XP_OK;
+    }
+  }
+  XP_HIP_CHECK(hipSetDevice(lane->agent->device));
+  // Placeholder layer and binding: a replay rebinds every argument record before launching.
+  Layer placeholder{};
+  placeholder.kind = XP_LAYER_MOE;
+  placeholder.moe = signature;
+  placeholder.hidden = signature.hidden;
+  placeholder.intermediate = signature.intermediate;
+  MoeStepBinding binding{};
+  binding.rows = capacity;
+  binding.pool_rows = capacity;
+  binding.workspace = lane->workspace;
+  binding.fault = lane->fault;
+  StepChain chain;
+  if (const int status = make_moe_step(placeholder, binding, capacity, chain); status != XP_OK) {
+    return status;
+  }
+  auto t = std::make_unique<Template>();
+  t->kind = XP_LAYER_MOE;
+  t->hidden = signature.hidden;
+  t->intermediate = signature.intermediate;
+  t->capacity = capacity;
+  t->moe = signature;
+  if (const int status = instantiate_template(*t, chain); status != XP_OK) {
+    return status;
+  }
+  insert_template(lane, std::move(t));
   return XP_OK;
 }
 

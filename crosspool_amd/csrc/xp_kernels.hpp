@@ -201,7 +201,7 @@ struct FinalizeRoutingArgs {
   const float *routed_weights;
   int32_t *final_ids;            // [capacity, effective_topk]
   float *final_weights;
-  const int64_t *payload_rows;   // one device value: live rows
+  const int64_t *payload_rows;   // one device value: live rows; null: every row below capacity
   int64_t capacity;
   int32_t routed_topk;
   int32_t effective_topk;
@@ -228,7 +228,9 @@ struct MoeSortArgs {
 struct MoeCombineArgs {
   const uint16_t *routes;    // [rows * topk, hidden] route outputs
   const int32_t *ids;        // [rows, topk]
-  uint16_t *out;             // [rows, hidden]
+  uint16_t *out;             // [rows, hidden], or [out_rows, hidden] rows slots[0..rows)
+  const int32_t *slots;      // [rows] output row of each row, or null (row r -> r)
+  int64_t out_rows;          // rows of `out` when scattering
   int64_t rows;
   int64_t hidden;
   int32_t topk;

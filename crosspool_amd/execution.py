@@ -1,6 +1,6 @@
 """Execution Signatures (GraphTemplate keys), capacity buckets and workspace geometry.
 
-Mirrors src/xpool/runtime/ffnagent/execution.py for the Dense path.
+Mirrors src/xpool/runtime/ffnagent/execution.py for the Dense and MoE layer kinds.
 """
 
 from __future__ import annotations
@@ -10,7 +10,14 @@ from dataclasses import dataclass
 
 import torch
 
-from crosspool_amd.ffn import GateTransform, SiluActivation
+from crosspool_amd.ffn import (
+    GateTransform,
+    RouterAlgorithm,
+    RouterProjectionPrecision,
+    SiluActivation,
+    TopKWeightRounding,
+    activation_arguments,
+)
 
 OPERATOR_ALIGNMENT_BYTES = 16  # execution.py:16
 
@@ -150,3 +157,86 @@ def dense_signatures(
         )
         for capacity in derive_payload_row_capacities(maximum_row_capacity)
     )
+
+
+@dataclass(frozen=True, slots=True)
+class MoeRouterExecutionSignature:
+    """Router-owner part of a MoE graph identity (execution.py:98-108).
+
+    On one device the Lane always owns the Router.  Whether a correction bias is bound does
+    not change the captured body (the bias is an argument of the TopK kernel), so it is not
+    part of the identity here.
+    """
+
+    algorithm: RouterAlgorithm
+    projection_precision: RouterProjectionPrecision
+    weight_rounding: TopKWeightRounding
+    routed_expert_count: int
+    routed_topk: int
+    renormalize: bool
+
+
+@dataclass(frozen=True, slots=True)
+class MoeFfnExecutionSignature:
+    """Complete reusable MoE graph identity (execution.py:111-149)."""
+
+    payload_dtype: torch.dtype
+    payload_row_capacity: int
+    hidden_size: int
+    local_intermediate_size: int
+    expert_count: int
+    effective_topk: int
+    routed_scaling_factor: float
+    router: MoeRouterExecutionSignature
+    activation: SiluActivation = SiluActivation()
+    gate: GateTransform = GateTransform()
+
+    def __post_init__(self) -> None:
+        if self.payload_dtype is not torch.bfloat16:
+            raise ValueError("the MI355X MoE path executes bf16 payloads")
+        for name in ("payload_row_capacity", "hidden_size", "local_intermediate_size", "expert_count", "effective_topk"):
+            value = getattr(self, name)
+            if isinstance(value, bool) or not isinstance(value, int) or value <= 0:
+                raise ValueError(f"{name} must be a positive integer")
+        shared = self.expert_count - self.router.routed_expert_count
+        if shared < 0 or self.effective_topk != self.router.routed_topk + shared:
+            raise ValueError("effective TopK must be the routed TopK plus the shared expert count")
+
+    @property
+    def payload_shape(self) -> tuple[int, int]:
+        return self.payload_row_capacity, self.hidden_size
+
+    @property
+    def routing_shape(self) -> tuple[int, int]:
+        """Route ids / weights geometry (execution.py:131-135)."""
+
+        return self.payload_row_capacity, self.effective_topk
+
+    @property
+    def routing_storage_bytes(self) -> int:
+        """Packed int32 ids and fp32 weights (execution.py:137-141)."""
+
+        return math.prod(self.routing_shape) * (torch.int32.itemsize + torch.float32.itemsize)
+
+    def native_descriptor(self):
+        """The ``xp_moe_layer_desc`` of this signature."""
+
+        from crosspool_amd import _native
+
+        alpha, limit, up_offset = activation_arguments(self.activation, self.gate)
+        router = self.router
+        return _native.MoeLayerDesc(
+            hidden=self.hidden_size,
+            intermediate=self.local_intermediate_size,
+            experts=self.expert_count,
+            routed_experts=router.routed_expert_count,
+            routed_topk=router.routed_topk,
+            algorithm=int(router.algorithm),
+            precision=int(router.projection_precision),
+            renormalize=int(router.renormalize),
+            weight_rounding=int(router.weight_rounding),
+            routed_scaling_factor=float(self.routed_scaling_factor),
+            alpha=alpha,
+            limit=limit,
+            up_offset=up_offset,
+        )

@@ -34,6 +34,7 @@ from crosspool_amd.weights import validate_weight_tensor
 __all__ = [
     "Experts",
     "MoeFfnWeights",
+    "MoeLayerSpec",
     "MoeRouterWeights",
     "Router",
     "finalize_moe_routing",
@@ -112,6 +113,91 @@ class MoeFfnWeights:
     @property
     def local_intermediate_size(self) -> int:
         return int(self.o_proj.shape[2])
+
+
+@dataclass(frozen=True, slots=True)
+class MoeLayerSpec:
+    """Routing and activation declaration of one MoE layer.
+
+    The fields of the reference's MoeFfnSpec (src/xpool/ffn.py:251-275) that execution
+    reads, with the model-wide SiLU and GateTransform (ffn.py:346-356).  Experts
+    ``[routed_expert_count, routed_expert_count + shared_expert_count)`` of the layer's
+    weights are the always-selected shared ones.
+    """
+
+    routed_expert_count: int
+    routed_topk: int
+    shared_expert_count: int = 0
+    renormalize: bool = True
+    routed_scaling_factor: float = 1.0
+    router_algorithm: RouterAlgorithm = RouterAlgorithm.SOFTMAX
+    router_projection_precision: RouterProjectionPrecision = RouterProjectionPrecision.PAYLOAD
+    topk_weight_rounding: TopKWeightRounding = TopKWeightRounding.NONE
+    activation: SiluActivation = SiluActivation()
+    gate: GateTransform = GateTransform()
+
+    def __post_init__(self) -> None:
+        if not 1 <= self.routed_topk <= min(self.routed_expert_count, 64):
+            raise ValueError("routed TopK must be between 1 and min(routed experts, 64)")
+        if self.shared_expert_count < 0 or self.routed_expert_count + self.shared_expert_count > 1024:
+            raise ValueError("a MoE layer holds at most 1024 experts, shared ones included")
+        if not (math.isfinite(self.routed_scaling_factor) and self.routed_scaling_factor > 0):
+            raise ValueError("routed scaling factor must be finite and positive")
+
+    @property
+    def expert_count(self) -> int:
+        return self.routed_expert_count + self.shared_expert_count
+
+    @property
+    def effective_topk(self) -> int:
+        return self.routed_topk + self.shared_expert_count
+
+    def validate_weights(self, weights: MoeFfnWeights) -> None:
+        """Check a layer's resources against this declaration (registry.py:153-174)."""
+
+        if weights.expert_count != self.expert_count:
+            raise ValueError(
+                f"MoE weights hold {weights.expert_count} experts; the layer declares {self.expert_count}"
+            )
+        if weights.router is None:
+            raise ValueError("the Lane owns the Router on one device: MoE weights need a Router projection")
+        weight_dtype = (
+            torch.float32 if self.router_projection_precision is RouterProjectionPrecision.FP32 else torch.bfloat16
+        )
+        projection = weights.router.projection
+        if projection.dtype is not weight_dtype or tuple(projection.shape) != (
+            self.routed_expert_count, weights.hidden_size
+        ):
+            raise ValueError(
+                f"router projection must be {weight_dtype} [{self.routed_expert_count}, {weights.hidden_size}]"
+            )
+        if weights.router.projection.device != weights.i_proj.device:
+            raise ValueError("Router and Expert resources must share one device")
+
+    def signature(self, *, hidden_size: int, local_intermediate_size: int, payload_row_capacity: int):
+        """The MoeFfnExecutionSignature of this layer at one capacity."""
+
+        from crosspool_amd.execution import MoeFfnExecutionSignature, MoeRouterExecutionSignature
+
+        return MoeFfnExecutionSignature(
+            payload_dtype=torch.bfloat16,
+            payload_row_capacity=payload_row_capacity,
+            hidden_size=hidden_size,
+            local_intermediate_size=local_intermediate_size,
+            expert_count=self.expert_count,
+            effective_topk=self.effective_topk,
+            routed_scaling_factor=float(self.routed_scaling_factor),
+            router=MoeRouterExecutionSignature(
+                algorithm=RouterAlgorithm(self.router_algorithm),
+                projection_precision=RouterProjectionPrecision(self.router_projection_precision),
+                weight_rounding=TopKWeightRounding(self.topk_weight_rounding),
+                routed_expert_count=self.routed_expert_count,
+                routed_topk=self.routed_topk,
+                renormalize=bool(self.renormalize),
+            ),
+            activation=self.activation,
+            gate=self.gate,
+        )
 
 
 class Router:

@@ -255,8 +255,8 @@ int xp_template_capacities(xp_lane_t lane, int64_t hidden, int64_t intermediate,
                            int max_count, int *count);
 
 /* Replay the smallest captured capacity >= rows for the layer: gather rows
- * slots[0..rows) of pool_in (+ RMSNorm), Dense FFN, write them to the same slots
- * of pool_out on `stream` (NULL = the legacy default stream; the Lane's own stream is
+ * slots[0..rows) of pool_in (+ RMSNorm), the layer's FFN (Dense, or MoE from its
+ * xp_moe_template_capture templates), write them to the same slots of pool_out on `stream` (NULL = the legacy default stream; the Lane's own stream is
  * xp_lane_stream's).  1 <= rows <= largest capacity.
  * Replaces wait_pre_compute's layer + capacity selection
  * (src/cext/ffnagent/runtime.cu:232-258), bind_compute (:336-369) and the
@@ -433,6 +433,62 @@ int xp_moe_experts(const void *hidden_states, int64_t rows, int64_t hidden, int6
                    int64_t topk, const void *w_gate_up, const void *w_down, const int32_t *topk_ids,
                    const float *topk_weights, float routed_scaling_factor, float alpha, float limit, float up_offset,
                    void *output, void *workspace, size_t workspace_bytes, xp_stream_t stream);
+
+/* ---------------------------------------------------------------- MoE layer kind
+ * One MoE layer's execution identity: the fields of MoeFfnExecutionSignature
+ * (src/xpool/runtime/ffnagent/execution.py:98-123, router signature included) that the
+ * captured body depends on, with the layer's MoeFfnSpec (src/xpool/ffn.py:251-275) and the
+ * model's SiLU / GateTransform.  experts counts the routed experts and then the shared ones
+ * (experts - routed_experts always-selected slots); effective topk = routed_topk + shared.
+ * On one device the Lane owns the Router (the reference's TP rank 0 role,
+ * src/cext/ffnagent/runtime.cu:649). */
+typedef struct {
+  int64_t hidden;
+  int64_t intermediate;     /* one expert's intermediate width */
+  int64_t experts;          /* routed + shared, <= 1024 */
+  int64_t routed_experts;   /* Router output width */
+  int64_t routed_topk;      /* <= min(routed_experts, 64) */
+  int algorithm;            /* XP_ROUTER_SOFTMAX / SIGMOID */
+  int precision;            /* XP_ROUTER_PRECISION_* */
+  int renormalize;
+  int weight_rounding;      /* XP_TOPK_ROUNDING_* */
+  float routed_scaling_factor;
+  float alpha;              /* SiLU slope */
+  float limit;              /* Gate/Up clip, 0 = none */
+  float up_offset;
+} xp_moe_layer_desc;
+
+/* Register (or rebind) one MoE layer's borrowed weights: gate_up [experts, 2*intermediate,
+ * hidden] bf16 (Gate/Up INTERLEAVED per expert), down [experts, hidden, intermediate] bf16,
+ * router [routed_experts, hidden] (fp32 for the FP32 precision, bf16 otherwise),
+ * correction_bias [routed_experts] fp32 or NULL, norm_weight [hidden] bf16 or NULL.
+ * Replaces LayerExecutionDescriptor + MoeBindingView (src/cext-bindings/ffnagent.cpp) and
+ * the MoE branch of validate_layer_weights_against_layout (registry.py:153-174). */
+int xp_moe_layer_register(xp_agent_t agent, int instance_index, int layer_ordinal, const xp_moe_layer_desc *desc,
+                          const void *gate_up, const void *down, const void *router, const float *correction_bias,
+                          const void *norm_weight, float eps);
+
+/* Lane workspace bytes of one MoE template at `capacity` rows (0 for an invalid
+ * descriptor).  Replaces the MoE branch of the capture workspace sizing
+ * (execution.py:124-149, plan.workspace). */
+size_t xp_moe_step_workspace_bytes(const xp_moe_layer_desc *desc, int64_t capacity);
+
+/* Byte offsets of the MoE step's workspace regions: [0] the gathered (normalised) batch
+ * bf16 [capacity, hidden], [1] the Router logits ([capacity, routed_experts], bf16 for the
+ * PAYLOAD precision, fp32 otherwise), [2] routed ids int32 and [3] routed weights fp32
+ * [capacity, routed_topk], [4] final ids int32 and [5] final weights fp32 [capacity,
+ * effective topk] (the routed ones when there are no shared experts), [6] the Experts
+ * workspace (xp_moe_workspace_layout's regions at capacity rows), [7] the total.  No
+ * counterpart in the reference (its tests read workspace views directly). */
+int xp_moe_step_workspace_layout(const xp_moe_layer_desc *desc, int64_t capacity, size_t *offsets);
+
+/* GraphTemplate of the MoE kind: this Lane's hipGraph for (desc, capacity) -- gather
+ * (+ RMSNorm), Router projection and TopK, routing finalisation when there are shared
+ * experts, route sort, grouped gate_up and down, combine scattered to the slots.
+ * Idempotent per signature.  xp_replay serves registered MoE layers from these templates
+ * (smallest captured capacity >= rows among templates whose descriptor equals the layer's).
+ * Replaces capture_moe_signature (src/xpool/runtime/ffnagent/registry.py:242-339). */
+int xp_moe_template_capture(xp_lane_t lane, const xp_moe_layer_desc *desc, int64_t capacity);
 
 #ifdef __cplusplus
 }

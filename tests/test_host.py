@@ -207,6 +207,63 @@ def test_dense_workspace_layout_matches_the_region_rules():
     assert total - down == 8 * 32 * 4096 * 4 and gate_up == down
 
 
+def test_moe_step_workspace_layout_and_descriptor_checks():
+    # Regions in order, each 256-byte aligned: batch [C, H] bf16, Router workspace (logits
+    # first), routed ids / weights [C, routed_topk], final ids / weights [C, effective] only
+    # with shared experts, then the Experts workspace at C rows; total = the bytes query.
+    from crosspool_amd.moe import MoeLayerSpec
+
+    def align(value):
+        return (value + 255) // 256 * 256
+
+    for capacity, hidden, intermediate, routed, shared, topk in ((1, 2048, 768, 128, 0, 8), (37, 512, 256, 16, 2, 3)):
+        spec = MoeLayerSpec(routed_expert_count=routed, routed_topk=topk, shared_expert_count=shared)
+        signature = spec.signature(hidden_size=hidden, local_intermediate_size=intermediate,
+                                   payload_row_capacity=capacity)
+        assert signature.effective_topk == topk + shared and signature.expert_count == routed + shared
+        assert signature.routing_storage_bytes == capacity * (topk + shared) * 8
+        desc = signature.native_descriptor()
+        batch, logits, rid, rw, fid, fw, experts, total = _native.moe_step_workspace_layout(desc, capacity)
+        assert batch == 0 and logits == align(capacity * hidden * 2)
+        router_bytes = _native.library().xp_moe_router_workspace_bytes(capacity, hidden, routed, 1)
+        assert rid == align(logits + router_bytes) and rw == align(rid + capacity * topk * 4)
+        if shared:
+            assert fid == align(rw + capacity * topk * 4) and fw == align(fid + capacity * (topk + shared) * 4)
+            assert experts == align(fw + capacity * (topk + shared) * 4)
+        else:
+            assert (fid, fw) == (rid, rw) and experts == align(rw + capacity * topk * 4)
+        moe_bytes = _native.library().xp_moe_workspace_bytes(capacity, hidden, intermediate, routed + shared,
+                                                             topk + shared)
+        assert total == align(experts + moe_bytes) == _native.moe_step_workspace_bytes(desc, capacity)
+
+    spec = MoeLayerSpec(routed_expert_count=8, routed_topk=2)
+    good = spec.signature(hidden_size=256, local_intermediate_size=128, payload_row_capacity=4).native_descriptor()
+    for field, value, message in (
+        ("hidden", 260, "multiples of 8"),
+        ("routed_experts", 9, "routed experts"),
+        ("routed_topk", 9, "topk"),
+        ("algorithm", 3, "algorithm"),
+        ("precision", 0, "precision"),
+        ("routed_scaling_factor", 0.0, "scaling"),
+        ("alpha", -1.0, "alpha"),
+        ("limit", -1.0, "limit"),
+    ):
+        bad = _native.MoeLayerDesc.from_buffer_copy(good)
+        setattr(bad, field, value)
+        assert _native.moe_step_workspace_bytes(bad, 4) == 0
+        with pytest.raises(_native.NativeError, match=message):
+            _native.moe_step_workspace_layout(bad, 4)
+    with pytest.raises(_native.NativeError, match="capacity must be positive"):
+        _native.moe_step_workspace_layout(good, 0)
+    with pytest.raises(ValueError, match="TopK"):
+        MoeLayerSpec(routed_expert_count=4, routed_topk=5)
+    with pytest.raises(ValueError, match="1024"):
+        MoeLayerSpec(routed_expert_count=1024, routed_topk=8, shared_expert_count=1)
+    lib = _native.library()
+    assert lib.xp_moe_layer_register(None, 0, 0, ctypes.byref(good), None, None, None, None, None, 1e-6) != 0
+    assert lib.xp_moe_template_capture(None, ctypes.byref(good), 4) != 0
+
+
 def test_abi_rejects_invalid_arguments_before_touching_the_device():
     lib = _native.library()
     p = ctypes.c_void_p
