@@ -689,10 +689,11 @@ using lds_void_t = __attribute__((address_space(3))) void *;
 
 // Direct global -> LDS load of 16 bytes per lane through a buffer resource: lane i's
 // data lands at `lds_row_base + 16 i`; offsets past the resource's end write zeros.
+template <int POLICY = 0>
 __device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t rsrc, void *lds_base, uint32_t voffset,
                                                   uint32_t soffset) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t)(lds_base), 16, static_cast<int>(voffset),
-                                           static_cast<int>(soffset), 0, 0);
+                                           static_cast<int>(soffset), 0, POLICY);
 }
 
 // LDS tiles are rows of 64 bf16 (128 bytes = eight 16-byte chunks).  gfx950 serves
@@ -945,7 +946,8 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs &a, const f32x16 (&
 // meanwhile.  Grid z splits K into ranges of `k_slice` columns; with more than one
 // range each workgroup writes the fp32 partial tile of its range and
 // stream_reduce_kernel, launched next, adds the ranges in order and applies the epilogue.
-template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, bool GATED, bool GROUPED = false>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, bool GATED, bool GROUPED = false,
+          bool STREAM_WEIGHTS = GROUPED>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmArgs a) {
   constexpr int BK = 64;
   constexpr int WAVES = WAVES_M * WAVES_N;
@@ -1100,7 +1102,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
       const int chunk = lane_chunk[(g >> 3) & 1];
       const int weight_row = b_group_row(g - BM) + B_ROW_STEP * row_in_load;
       const uint32_t offset = static_cast<uint32_t>((weight_row * a.k + chunk * 8) * 2);
-      buffer_load_lds16(b_rsrc, b_stage + g * BK, chunk < chunks_left ? offset : kOutOfRange, k_bytes);
+      buffer_load_lds16<STREAM_WEIGHTS ? kLoadNontemporal : 0>(b_rsrc, b_stage + g * BK,
+                                                               chunk < chunks_left ? offset : kOutOfRange, k_bytes);
     }
   };
   auto issue_loads = [&](int64_t kt, int stage) XP_INLINE { issue_part(kt, stage, std::integral_constant<int, 3>{}); };
@@ -1342,17 +1345,20 @@ constexpr TileShape kTileShapes[] = {
 };
 constexpr int kTileShapeCount = sizeof(kTileShapes) / sizeof(kTileShapes[0]);
 
+// STREAM: the grid has one token tile, so each weight tile has one reader and its loads
+// carry the nontemporal hint (a compile-time policy: a per-load branch on an argument cost
+// the loading waves ~2 % at 2048 rows).
 template <bool GATED>
-const void *tile_kernel(int variant) {
+const void *tile_kernel(int variant, bool stream) {
   using Kernel = void (*)(GemmArgs);
-  static const Kernel table[] = {
-      &tile_gemm_kernel<256, 256, 2, 4, 2, GATED>,
-      &tile_gemm_kernel<256, 128, 4, 2, 3, GATED>,
-      &tile_gemm_kernel<128, 128, 2, 2, 3, GATED>,
-      &tile_gemm_kernel<64, 128, 2, 2, 6, GATED>,
+  static const Kernel table[][2] = {
+      {&tile_gemm_kernel<256, 256, 2, 4, 2, GATED>, &tile_gemm_kernel<256, 256, 2, 4, 2, GATED, false, true>},
+      {&tile_gemm_kernel<256, 128, 4, 2, 3, GATED>, &tile_gemm_kernel<256, 128, 4, 2, 3, GATED, false, true>},
+      {&tile_gemm_kernel<128, 128, 2, 2, 3, GATED>, &tile_gemm_kernel<128, 128, 2, 2, 3, GATED, false, true>},
+      {&tile_gemm_kernel<64, 128, 2, 2, 6, GATED>, &tile_gemm_kernel<64, 128, 2, 2, 6, GATED, false, true>},
   };
   static_assert(sizeof(table) / sizeof(table[0]) == kTileShapeCount, "one kernel per tile shape");
-  return reinterpret_cast<const void *>(table[variant]);
+  return reinterpret_cast<const void *>(table[variant][stream ? 1 : 0]);
 }
 
 constexpr int kComputeUnits = 256;
@@ -1629,7 +1635,8 @@ GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmCho
     kernel.shmem = static_cast<unsigned>(16 * (choice.k_slice + 8) * 2);
   } else {
     const TileShape &shape = kTileShapes[choice.variant];
-    kernel.func = gated ? tile_kernel<true>(choice.variant) : tile_kernel<false>(choice.variant);
+    const bool stream = capacity <= shape.bm;
+    kernel.func = gated ? tile_kernel<true>(choice.variant, stream) : tile_kernel<false>(choice.variant, stream);
     kernel.grid = dim3(static_cast<unsigned>((args.n + shape.bn - 1) / shape.bn),
                        static_cast<unsigned>((capacity + shape.bm - 1) / shape.bm),
                        static_cast<unsigned>(choice.k_split));
@@ -1667,6 +1674,8 @@ KernelLaunch make_grouped_gemm(const GemmArgs &args, bool gated, int max_tiles) 
   record.partials = nullptr;
   static_assert(kTileShapes[kGroupedTileVariant].bm == 256 && kTileShapes[kGroupedTileVariant].bn == 128,
                 "the grouped instantiations below are the 256 x 128 tile");
+  // Grouped instantiations load their weights with the nontemporal hint: an expert's
+  // weights are read by its own tiles only (one tile for up to 256 routes).
   KernelLaunch kernel;
   kernel.func = gated ? reinterpret_cast<const void *>(&tile_gemm_kernel<256, 128, 4, 2, 3, true, true>)
                       : reinterpret_cast<const void *>(&tile_gemm_kernel<256, 128, 4, 2, 3, false, true>);

@@ -99,6 +99,14 @@ __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, uint
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, static_cast<int>(offset), 0, 0));
 }
 
+// Cache-policy bits of a buffer load: 2 is the nontemporal hint (`nt`), for data read once
+// in whole 128-byte lines (the tile kernel's weight tiles).  Measured on MI355X: a 4 GiB
+// read reaches 6.1-6.3 TB/s with plain loads and 6.8-7.1 TB/s with nontemporal ones.  The
+// split and stream kernels read each line as two 64-byte halves in consecutive
+// instructions; with the hint their decode layers took 10-12 us longer (the second half no
+// longer found in L2), so they load plainly.
+constexpr int kLoadNontemporal = 2;
+
 __device__ __forceinline__ float wave_sum(float value) {
 #pragma unroll
   for (int offset = 32; offset > 0; offset >>= 1) {
