@@ -88,6 +88,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "xp_dense_step": (_INT, [_P, _P, _I64, _P, _I64, _I64, _I64, _P, _P, _P, _F32, _P, _SIZE, _P, _P]),
     "xp_dense_step_static": (_INT, [_P, _P, _I64, _P, _I64, _I64, _I64, _P, _P, _P, _F32, _P, _P]),
     "xp_gemm_variant": (_SIZE, [_I64, _I64, _I64, _INT, ctypes.c_char_p, _SIZE]),
+    "xp_dense_gate_up_variant": (_SIZE, [_I64, _I64, _I64, ctypes.c_char_p, _SIZE]),
     "xp_agent_create": (_INT, [_INT, ctypes.POINTER(_P)]),
     "xp_agent_destroy": (_INT, [_P]),
     "xp_layer_register": (_INT, [_P, _INT, _INT, _I64, _I64, _P, _P, _P, _F32]),
@@ -193,6 +194,15 @@ def gemm_variant(capacity: int, n: int, k: int, gated: bool) -> str:
     lib = library()
     buffer = ctypes.create_string_buffer(64)
     lib.xp_gemm_variant(capacity, n, k, int(gated), buffer, 64)
+    return buffer.value.decode()
+
+
+def dense_gate_up_variant(capacity: int, hidden: int, intermediate: int) -> str:
+    """The Dense step's gate_up variant at ``capacity`` rows ("+gather" when the gather is fused)."""
+
+    lib = library()
+    buffer = ctypes.create_string_buffer(64)
+    lib.xp_dense_gate_up_variant(capacity, hidden, intermediate, buffer, 64)
     return buffer.value.decode()
 
 

@@ -50,6 +50,151 @@ __device__ __forceinline__ uint16_t *output_row(const GemmArgs &a, int64_t token
 // adding a row's byte offset keeps it below 2^32).
 constexpr uint32_t kOutOfRange = 0x7ffffff0u;
 
+// Fused mailbox gather of token rows [0, TP) into LDS rows of stride `rs` (elements),
+// columns [kbase, kbase + 8 vectors_per_row) of which the first kvalid hold data: token row
+// t is mailbox row gather_slots[t] of a.x ([pool_rows, a.k]), RMS-normalised with a.norm when
+// that is set, bit for bit as gather_rows_kernel computes it; rows past the live rows are
+// zero and a slot outside the mailbox gives a row of quiet NaNs and raises the fault bit.
+// All WAVES waves of the workgroup take part; the caller synchronises before reading.
+template <int TP, int WAVES>
+__device__ __forceinline__ void stage_gathered_rows(const GemmArgs &a, uint16_t *xs, int64_t rs, int kbase,
+                                                    int kvalid, int vectors_per_row, int wave, int lane) {
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+  // Wave w finds rows w, w + WAVES, ... of the slot list and their inverse RMS over the
+  // whole row (the gather kernel's wavefront reduction, so the same bits), then the columns
+  // are staged from the mailbox rows, normalised.  Loads are issued in
+  // batches of independent requests before their results are used, so the dependent
+  // round trips are few (slot, row, and for rows longer than one batch the staging reads).
+  constexpr int ROWS_PER_WAVE = TP / WAVES;
+  constexpr int BATCH = 8;  // 16-byte chunks per lane and row in flight
+  __shared__ float row_scale[TP];
+  __shared__ int64_t row_source[TP];  // mailbox row; -1 past the live rows, -2 bad slot
+  int64_t sources[ROWS_PER_WAVE];
+#pragma unroll
+  for (int r = 0; r < ROWS_PER_WAVE; ++r) {
+    const int t = wave + r * WAVES;
+    sources[r] = -1;
+    if (t < a.rows) {
+      const int32_t slot = a.gather_slots[t];
+      sources[r] = slot < 0 || static_cast<int64_t>(slot) >= a.pool_rows ? -2 : slot;
+    }
+  }
+  float squares[ROWS_PER_WAVE];
+#pragma unroll
+  for (int r = 0; r < ROWS_PER_WAVE; ++r) {
+    squares[r] = 0.0f;
+  }
+  const int64_t row_chunks = a.k / 8;
+  // Rows of at most BATCH * 64 chunks (hidden <= 4096) stay in registers between their sum
+  // of squares and their normalised store into LDS: one round trip for the rows, none for
+  // a second staging pass.  Longer rows are summed in batches and staged in a second pass.
+  const bool one_batch = row_chunks <= BATCH * kWave;
+  u32x4 values[ROWS_PER_WAVE][BATCH];
+  u32x4 weights[BATCH];
+  for (int64_t first = lane; first < row_chunks; first += BATCH * kWave) {
+#pragma unroll
+    for (int b = 0; b < BATCH; ++b) {
+      const int64_t chunk = first + b * kWave;
+      weights[b] = one_batch && a.norm != nullptr && chunk < row_chunks ? load16(a.norm + chunk * 8) : zero;
+#pragma unroll
+      for (int r = 0; r < ROWS_PER_WAVE; ++r) {
+        const bool live = sources[r] >= 0 && chunk < row_chunks && (one_batch || a.norm != nullptr);
+        values[r][b] = live ? load16(a.x + sources[r] * a.ldx + chunk * 8) : zero;
+      }
+    }
+    if (a.norm != nullptr) {
+#pragma unroll
+      for (int r = 0; r < ROWS_PER_WAVE; ++r) {
+#pragma unroll
+        for (int b = 0; b < BATCH; ++b) {
+          add_squares(values[r][b], squares[r]);  // chunk order lane, lane + 64, ...
+        }
+      }
+    }
+  }
+  float scales[ROWS_PER_WAVE];
+#pragma unroll
+  for (int r = 0; r < ROWS_PER_WAVE; ++r) {
+    const int t = wave + r * WAVES;
+    scales[r] = a.norm != nullptr && sources[r] >= 0 ? rms_inverse(squares[r], a.k, a.eps) : 1.0f;
+    if (lane == 0) {
+      if (!one_batch) {
+        row_scale[t] = scales[r];
+        row_source[t] = sources[r];
+      }
+      if (sources[r] == -2 && blockIdx.x == 0) {
+        raise_fault(a.fault, kFaultSlotOutOfRange);
+      }
+    }
+  }
+  const u32x4 poison = {kPoisonBf16x2, kPoisonBf16x2, kPoisonBf16x2, kPoisonBf16x2};
+  if (one_batch) {
+    // Each wave stores its own rows' part of the slice (zeros past the live rows).
+#pragma unroll
+    for (int r = 0; r < ROWS_PER_WAVE; ++r) {
+      const int t = wave + r * WAVES;
+#pragma unroll
+      for (int b = 0; b < BATCH; ++b) {
+        const int64_t chunk = lane + b * kWave;
+        const int64_t c = chunk - kbase / 8;  // chunk within this slice
+        if (chunk >= row_chunks || c < 0 || c >= vectors_per_row) {
+          continue;
+        }
+        u32x4 value = zero;
+        if (sources[r] >= 0) {
+          value = a.norm != nullptr ? normalize_chunk(values[r][b], scales[r], weights[b]) : values[r][b];
+        } else if (sources[r] == -2) {
+          value = poison;
+        }
+        store16(xs + t * rs + c * 8, value);
+      }
+      // Slice columns past the row (the last slice's tail) are zero.
+      for (int64_t c = row_chunks - kbase / 8 + lane; c < vectors_per_row; c += kWave) {
+        if (c >= 0) {
+          store16(xs + t * rs + c * 8, zero);
+        }
+      }
+    }
+  } else {
+    __syncthreads();
+    constexpr int STAGE_BATCH = 4;
+    const int items = TP * vectors_per_row;
+    for (int first = threadIdx.x; first < items; first += STAGE_BATCH * 64 * WAVES) {
+      u32x4 x_chunk[STAGE_BATCH];
+      u32x4 w_chunk[STAGE_BATCH];
+#pragma unroll
+      for (int u = 0; u < STAGE_BATCH; ++u) {
+        const int index = first + u * 64 * WAVES;
+        const int t = index / vectors_per_row;
+        const int c = index - t * vectors_per_row;
+        const int64_t source = index < items ? row_source[t] : -1;
+        const bool live = source >= 0 && c * 8 < kvalid;
+        x_chunk[u] = live ? load16(a.x + source * a.ldx + kbase + c * 8) : zero;
+        w_chunk[u] = live && a.norm != nullptr ? load16(a.norm + kbase + c * 8) : zero;
+      }
+#pragma unroll
+      for (int u = 0; u < STAGE_BATCH; ++u) {
+        const int index = first + u * 64 * WAVES;
+        if (index >= items) {
+          continue;
+        }
+        const int t = index / vectors_per_row;
+        const int c = index - t * vectors_per_row;
+        const int64_t source = row_source[t];
+        u32x4 value = zero;
+        if (c * 8 < kvalid) {
+          if (source >= 0) {
+            value = a.norm != nullptr ? normalize_chunk(x_chunk[u], row_scale[t], w_chunk[u]) : x_chunk[u];
+          } else if (source == -2) {
+            value = poison;
+          }
+        }
+        store16(xs + t * rs + c * 8, value);
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------------------ split (decode)
 // Weight-streaming projection for at most 64 live rows (HBM-bound).  A workgroup of 8
 // waves covers 8 / KSPLIT weight-row blocks of 16 rows; the KSPLIT waves of a block each
@@ -62,8 +207,15 @@ constexpr uint32_t kOutOfRange = 0x7ffffff0u;
 // partial sums leave the chip.
 constexpr int kSplitWaves = 8;
 
-template <int TB, int DEPTH, bool GATED>
+// GATHER (one token block, K <= 4096): the token rows are the mailbox rows gather_slots[t]
+// of a.x, RMS-normalised with a.norm when that is set, staged once per workgroup into LDS
+// (stage_gathered_rows, the gather kernel's bits) while the first DEPTH chunks of weights
+// are in flight; the token fragments are then read from LDS instead of L2.  Dynamic LDS:
+// 16 x (K + 8) bf16.
+template <int TB, int DEPTH, bool GATED, bool GATHER = false>
 __global__ __launch_bounds__(64 * kSplitWaves) void split_gemm_kernel(GemmArgs a) {
+  static_assert(!GATHER || TB == 1, "the fused gather stages one 16-row token block");
+  extern __shared__ __attribute__((aligned(16))) uint16_t staged[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int r16 = lane & 15;
@@ -72,7 +224,9 @@ __global__ __launch_bounds__(64 * kSplitWaves) void split_gemm_kernel(GemmArgs a
   const int part = wave % ksplit;
   const int64_t rb = static_cast<int64_t>(blockIdx.x) * (kSplitWaves / ksplit) + wave / ksplit;
   const int64_t row_blocks = (a.n + 15) / 16;
+  const bool active = rb < row_blocks;
   const u32x4 zero = {0u, 0u, 0u, 0u};
+  const int64_t rs = a.k + 8;  // staged row stride in elements (GATHER)
 
   f32x4 acc[TB];
 #pragma unroll
@@ -80,67 +234,81 @@ __global__ __launch_bounds__(64 * kSplitWaves) void split_gemm_kernel(GemmArgs a
     acc[tb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   }
 
-  if (rb < row_blocks) {
-    const int k0 = part * static_cast<int>(a.k_slice);
-    // 128-wide chunks of this range (k_slice is a multiple of 128; the last range may be
-    // shorter), rounded up to whole groups of DEPTH: the chunks past the range load
-    // through an out-of-range offset, which reads zeros without a memory access.
-    const int k_range = static_cast<int>(a.k - k0 < a.k_slice ? a.k - k0 : a.k_slice);
-    const int chunks = (k_range + 127) / 128;  // >= 1: the host makes no empty range
-    const int padded = (chunks + DEPTH - 1) / DEPTH * DEPTH;
-    // Columns at or past K in the last chunk read the next row (or past the end): zero
-    // both operands there.
-    const int lane_valid = static_cast<int>(a.k) - k0 - kq * 8;
-    // Row blocks start at different chunks of their range (stride-7 rotation), spreading
-    // the concurrently streamed addresses over the memory channels.
-    const int rotation = static_cast<int>((rb * 7) % chunks);
-    const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(a.w, static_cast<uint32_t>(a.n * a.k * 2));
-    const __amdgpu_buffer_rsrc_t x_rsrc = make_rsrc(a.x, static_cast<uint32_t>(a.rows * a.ldx * 2));
-    const uint32_t w_off = static_cast<uint32_t>(((rb * 16 + r16) * a.k + k0 + kq * 8) * 2);
-    uint32_t x_off[TB];
+  const int k0 = part * static_cast<int>(a.k_slice);
+  // 128-wide chunks of this range (k_slice is a multiple of 128; the last range may be
+  // shorter), rounded up to whole groups of DEPTH: the chunks past the range load through
+  // an out-of-range offset, which reads zeros without a memory access.
+  const int k_range = static_cast<int>(a.k - k0 < a.k_slice ? a.k - k0 : a.k_slice);
+  const int chunks = (k_range + 127) / 128;  // >= 1: the host makes no empty range
+  const int padded = (chunks + DEPTH - 1) / DEPTH * DEPTH;
+  // Columns at or past K in the last chunk read the next row (or past the end): zero both
+  // operands there.
+  const int lane_valid = static_cast<int>(a.k) - k0 - kq * 8;
+  // Row blocks start at different chunks of their range (stride-7 rotation), spreading the
+  // concurrently streamed addresses over the memory channels.
+  const int rotation = static_cast<int>((rb * 7) % chunks);
+  const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(a.w, static_cast<uint32_t>(a.n * a.k * 2));
+  const __amdgpu_buffer_rsrc_t x_rsrc = make_rsrc(a.x, static_cast<uint32_t>(a.rows * a.ldx * 2));
+  const uint32_t w_off = static_cast<uint32_t>(((rb * 16 + r16) * a.k + k0 + kq * 8) * 2);
+  uint32_t x_off[TB];
 #pragma unroll
-    for (int tb = 0; tb < TB; ++tb) {
-      x_off[tb] = static_cast<uint32_t>(((tb * 16 + r16) * a.ldx + k0 + kq * 8) * 2);
-    }
-    auto column_of = [&](int chunk) {
-      const int c = chunk + rotation;
-      return (c < chunks ? c : c - chunks) * 128;
-    };
+  for (int tb = 0; tb < TB; ++tb) {
+    x_off[tb] = static_cast<uint32_t>(((tb * 16 + r16) * a.ldx + k0 + kq * 8) * 2);
+  }
+  auto column_of = [&](int chunk) {
+    const int c = chunk + rotation;
+    return (c < chunks ? c : c - chunks) * 128;
+  };
 
-    u32x4 wbuf[DEPTH][4];
-    u32x4 xbuf[DEPTH][TB][4];
-    auto load_chunk = [&](int chunk, u32x4 (&w)[4], u32x4 (&x)[TB][4]) {
-      const bool in_range = chunk < chunks;
-      const uint32_t column = static_cast<uint32_t>(column_of(chunk)) * 2;
+  u32x4 wbuf[DEPTH][4];
+  u32x4 xbuf[DEPTH][GATHER ? 1 : TB][4];
+  auto load_chunk = [&](int chunk, u32x4 (&w)[4], u32x4 (&x)[GATHER ? 1 : TB][4]) {
+    const bool in_range = chunk < chunks;
+    const uint32_t column = static_cast<uint32_t>(column_of(chunk)) * 2;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        w[s] = buffer_load16(w_rsrc, in_range ? w_off + column + s * 64 : kOutOfRange);
+    for (int s = 0; s < 4; ++s) {
+      w[s] = buffer_load16(w_rsrc, in_range ? w_off + column + s * 64 : kOutOfRange);
+      if constexpr (!GATHER) {
 #pragma unroll
         for (int tb = 0; tb < TB; ++tb) {
           x[tb][s] = buffer_load16(x_rsrc, in_range ? x_off[tb] + column + s * 64 : kOutOfRange);
         }
       }
-    };
-    auto compute_chunk = [&](int chunk, const u32x4 (&w)[4], const u32x4 (&x)[TB][4]) {
-      const int column = chunk < chunks ? column_of(chunk) : 0;
+    }
+  };
+  auto compute_chunk = [&](int chunk, const u32x4 (&w)[4], const u32x4 (&x)[GATHER ? 1 : TB][4]) {
+    const int column = chunk < chunks ? column_of(chunk) : 0;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const bool valid = column + s * 32 < lane_valid;
-        const u32x4 wk = valid ? w[s] : zero;
+    for (int s = 0; s < 4; ++s) {
+      const bool valid = column + s * 32 < lane_valid;
+      const u32x4 wk = valid ? w[s] : zero;
 #pragma unroll
-        for (int tb = 0; tb < TB; ++tb) {
-          const u32x4 xk = valid ? x[tb][s] : zero;
-          acc[tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(wk), as_bf16x8(xk), acc[tb], 0, 0, 0);
+      for (int tb = 0; tb < TB; ++tb) {
+        u32x4 xk;
+        if constexpr (GATHER) {
+          xk = valid ? load16(staged + r16 * rs + k0 + column + s * 32 + kq * 8) : zero;
+        } else {
+          xk = valid ? x[tb][s] : zero;
         }
+        acc[tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(wk), as_bf16x8(xk), acc[tb], 0, 0, 0);
       }
-    };
+    }
+  };
 
-    // Every load is unconditional and the trip count has no partial group, so the wait
-    // counts track exactly DEPTH chunks in flight.
+  // Every load is unconditional and the trip count has no partial group, so the wait counts
+  // track exactly DEPTH chunks in flight.
+  if (active) {
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
       load_chunk(d, wbuf[d], xbuf[d]);
     }
+  }
+  if constexpr (GATHER) {
+    const int vectors = static_cast<int>(a.k / 8);
+    stage_gathered_rows<16, kSplitWaves>(a, staged, rs, 0, static_cast<int>(a.k), vectors, wave, lane);
+    __syncthreads();
+  }
+  if (active) {
     int c0 = 0;
     for (; c0 < padded - DEPTH; c0 += DEPTH) {
 #pragma unroll
@@ -425,139 +593,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_gemm_kernel(GemmArgs
   const int kbase = static_cast<int>(k0);
   const int kvalid = static_cast<int>(klen);
   if constexpr (GATHER) {
-    // Fused mailbox gather: wave w finds rows w, w + 8 of the slot list and their inverse
-    // RMS over the whole row (the gather kernel's wavefront reduction, so the same bits),
-    // then the slice is staged from the mailbox rows, normalised.  Loads are issued in
-    // batches of independent requests before their results are used, so the dependent
-    // round trips are few (slot, row, and for rows longer than one batch the staging reads).
-    constexpr int ROWS_PER_WAVE = TP / kStreamWaves;
-    constexpr int BATCH = 8;  // 16-byte chunks per lane and row in flight
-    __shared__ float row_scale[TP];
-    __shared__ int64_t row_source[TP];  // mailbox row; -1 past the live rows, -2 bad slot
-    int64_t sources[ROWS_PER_WAVE];
-#pragma unroll
-    for (int r = 0; r < ROWS_PER_WAVE; ++r) {
-      const int t = wave + r * kStreamWaves;
-      sources[r] = -1;
-      if (t < a.rows) {
-        const int32_t slot = a.gather_slots[t];
-        sources[r] = slot < 0 || static_cast<int64_t>(slot) >= a.pool_rows ? -2 : slot;
-      }
-    }
-    float squares[ROWS_PER_WAVE];
-#pragma unroll
-    for (int r = 0; r < ROWS_PER_WAVE; ++r) {
-      squares[r] = 0.0f;
-    }
-    const int64_t row_chunks = a.k / 8;
-    // Rows of at most BATCH * 64 chunks (hidden <= 4096) stay in registers between their sum
-    // of squares and their normalised store into LDS: one round trip for the rows, none for
-    // a second staging pass.  Longer rows are summed in batches and staged in a second pass.
-    const bool one_batch = row_chunks <= BATCH * kWave;
-    u32x4 values[ROWS_PER_WAVE][BATCH];
-    u32x4 weights[BATCH];
-    for (int64_t first = lane; first < row_chunks; first += BATCH * kWave) {
-#pragma unroll
-      for (int b = 0; b < BATCH; ++b) {
-        const int64_t chunk = first + b * kWave;
-        weights[b] = one_batch && a.norm != nullptr && chunk < row_chunks ? load16(a.norm + chunk * 8) : zero;
-#pragma unroll
-        for (int r = 0; r < ROWS_PER_WAVE; ++r) {
-          const bool live = sources[r] >= 0 && chunk < row_chunks && (one_batch || a.norm != nullptr);
-          values[r][b] = live ? load16(a.x + sources[r] * a.ldx + chunk * 8) : zero;
-        }
-      }
-      if (a.norm != nullptr) {
-#pragma unroll
-        for (int r = 0; r < ROWS_PER_WAVE; ++r) {
-#pragma unroll
-          for (int b = 0; b < BATCH; ++b) {
-            add_squares(values[r][b], squares[r]);  // chunk order lane, lane + 64, ...
-          }
-        }
-      }
-    }
-    float scales[ROWS_PER_WAVE];
-#pragma unroll
-    for (int r = 0; r < ROWS_PER_WAVE; ++r) {
-      const int t = wave + r * kStreamWaves;
-      scales[r] = a.norm != nullptr && sources[r] >= 0 ? rms_inverse(squares[r], a.k, a.eps) : 1.0f;
-      if (lane == 0) {
-        if (!one_batch) {
-          row_scale[t] = scales[r];
-          row_source[t] = sources[r];
-        }
-        if (sources[r] == -2 && blockIdx.x == 0) {
-          raise_fault(a.fault, kFaultSlotOutOfRange);
-        }
-      }
-    }
-    const u32x4 poison = {kPoisonBf16x2, kPoisonBf16x2, kPoisonBf16x2, kPoisonBf16x2};
-    if (one_batch) {
-      // Each wave stores its own rows' part of the slice (zeros past the live rows).
-#pragma unroll
-      for (int r = 0; r < ROWS_PER_WAVE; ++r) {
-        const int t = wave + r * kStreamWaves;
-#pragma unroll
-        for (int b = 0; b < BATCH; ++b) {
-          const int64_t chunk = lane + b * kWave;
-          const int64_t c = chunk - kbase / 8;  // chunk within this slice
-          if (chunk >= row_chunks || c < 0 || c >= vectors_per_row) {
-            continue;
-          }
-          u32x4 value = zero;
-          if (sources[r] >= 0) {
-            value = a.norm != nullptr ? normalize_chunk(values[r][b], scales[r], weights[b]) : values[r][b];
-          } else if (sources[r] == -2) {
-            value = poison;
-          }
-          store16(xs + t * rs + c * 8, value);
-        }
-        // Slice columns past the row (the last slice's tail) are zero.
-        for (int64_t c = row_chunks - kbase / 8 + lane; c < vectors_per_row; c += kWave) {
-          if (c >= 0) {
-            store16(xs + t * rs + c * 8, zero);
-          }
-        }
-      }
-    } else {
-      __syncthreads();
-      constexpr int STAGE_BATCH = 4;
-      const int items = TP * vectors_per_row;
-      for (int first = threadIdx.x; first < items; first += STAGE_BATCH * 64 * kStreamWaves) {
-        u32x4 x_chunk[STAGE_BATCH];
-        u32x4 w_chunk[STAGE_BATCH];
-#pragma unroll
-        for (int u = 0; u < STAGE_BATCH; ++u) {
-          const int index = first + u * 64 * kStreamWaves;
-          const int t = index / vectors_per_row;
-          const int c = index - t * vectors_per_row;
-          const int64_t source = index < items ? row_source[t] : -1;
-          const bool live = source >= 0 && c * 8 < kvalid;
-          x_chunk[u] = live ? load16(a.x + source * a.ldx + kbase + c * 8) : zero;
-          w_chunk[u] = live && a.norm != nullptr ? load16(a.norm + kbase + c * 8) : zero;
-        }
-#pragma unroll
-        for (int u = 0; u < STAGE_BATCH; ++u) {
-          const int index = first + u * 64 * kStreamWaves;
-          if (index >= items) {
-            continue;
-          }
-          const int t = index / vectors_per_row;
-          const int c = index - t * vectors_per_row;
-          const int64_t source = row_source[t];
-          u32x4 value = zero;
-          if (c * 8 < kvalid) {
-            if (source >= 0) {
-              value = a.norm != nullptr ? normalize_chunk(x_chunk[u], row_scale[t], w_chunk[u]) : x_chunk[u];
-            } else if (source == -2) {
-              value = poison;
-            }
-          }
-          store16(xs + t * rs + c * 8, value);
-        }
-      }
-    }
+    stage_gathered_rows<TP, kStreamWaves>(a, xs, rs, kbase, kvalid, vectors_per_row, wave, lane);
   } else {
     const __amdgpu_buffer_rsrc_t x_rsrc = make_rsrc(a.x, static_cast<uint32_t>(a.rows * a.ldx * 2));
     for (int index = threadIdx.x; index < TP * vectors_per_row; index += 64 * kStreamWaves) {
@@ -1320,9 +1356,9 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
 }
 
 // ------------------------------------------------------------------ tables
-template <bool GATED>
+template <bool GATED, bool GATHER = false>
 const void *split_kernel() {
-  return reinterpret_cast<const void *>(&split_gemm_kernel<1, 4, GATED>);
+  return reinterpret_cast<const void *>(&split_gemm_kernel<1, 4, GATED, GATHER>);
 }
 
 template <bool GATED, bool GATHER = false>
@@ -1391,6 +1427,8 @@ constexpr double kStreamReduceUs = 12.0;  // the reduction launch, fitted (it al
 constexpr double kStreamPartialBytesPerUs = 6.0e6;
 constexpr int kSplitDepth = 4;
 constexpr double kGatherUs = 4.0;  // a separate gather launch at decode sizes (measured 3.8-4.0 us)
+constexpr double kSplitGatherUs = 1.0;  // the split kernel's fused gather prologue, beyond its overlap
+constexpr int64_t kSplitGatherMaxK = 4096;  // 16 staged rows of K + 8 bf16 fit the LDS beside the partials
 
 double decode_stream_us(int64_t n, int64_t k, int64_t workgroups, double workgroup_bytes_per_us) {
   const int64_t rounds = (workgroups + kComputeUnits - 1) / kComputeUnits;
@@ -1528,7 +1566,10 @@ GemmChoice choose_gemm(int64_t capacity, int64_t n, int64_t k, bool gated) {
 
 // The fused gather's prologue (slot list, full-row sums of squares, staging) runs in every
 // workgroup, so the fused gate_up takes the fewest K slices that fit LDS (measured: 4
-// slices of Qwen3-8B gate_up took 47 + 5 us against 38 us for one).
+// slices of Qwen3-8B gate_up took 47 + 5 us against 38 us for one).  Up to kSplitMaxRows
+// rows the split kernel can fuse the gather as well: each workgroup stages the rows' whole
+// K (at most kSplitGatherMaxK columns) while its first weight chunks are in flight, which
+// the model prices at kSplitGatherUs over the plain split kernel.
 GemmChoice choose_dense_gate_up(int64_t capacity, int64_t n, int64_t k, bool &fused) {
   fused = capacity <= kDecodeMaxRows && n * k * 2 <= INT32_MAX;
   if (!fused) {
@@ -1554,6 +1595,13 @@ GemmChoice choose_dense_gate_up(int64_t capacity, int64_t n, int64_t k, bool &fu
   }
   double separate_us = 0.0;
   const GemmChoice separate = choose_decode(capacity, n, k, separate_us);
+  if (capacity <= kSplitMaxRows && k <= kSplitGatherMaxK) {
+    double split_us = 0.0;
+    const GemmChoice split = choose_split(capacity, n, k, split_us);
+    if (split_us + kSplitGatherUs < fused_us && split_us + kSplitGatherUs <= kGatherUs + separate_us) {
+      return split;  // fused into the split kernel
+    }
+  }
   if (kGatherUs + separate_us < fused_us) {
     fused = false;
     return separate;
@@ -1603,15 +1651,21 @@ hipError_t enable_large_lds(const void *func) {
       return hipSuccess;
     }
   }
-  const hipError_t status =
-      hipFuncSetAttribute(func, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kStreamLdsBytes));
+  // The dynamic maximum is what the CU's 160 KB leave beside the function's static LDS (the
+  // split kernel's partial sums, the fused gather's row table).
+  hipFuncAttributes attributes{};
+  if (const hipError_t status = hipFuncGetAttributes(&attributes, func); status != hipSuccess) {
+    return status;
+  }
+  const int limit = 160 * 1024 - static_cast<int>(attributes.sharedSizeBytes);
+  const hipError_t status = hipFuncSetAttribute(func, hipFuncAttributeMaxDynamicSharedMemorySize, limit);
   if (status == hipSuccess && count < static_cast<int>(sizeof(enabled) / sizeof(enabled[0]))) {
     enabled[count++] = Enabled{func, device};
   }
   return status;
 }
 
-GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmChoice choice) {
+GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmChoice choice, bool fused_gather) {
   GemmLaunch launches;
   KernelLaunch &kernel = launches.main;
   GemmArgs record = args;
@@ -1621,13 +1675,16 @@ GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmCho
   if (choice.kind == GemmKind::Split) {
     const int64_t row_blocks = (args.n + 15) / 16;
     const int64_t per_group = kSplitWaves / choice.k_split;
-    kernel.func = gated ? split_kernel<true>() : split_kernel<false>();
+    const bool gather = fused_gather && gated;
+    kernel.func = gather ? split_kernel<true, true>() : (gated ? split_kernel<true>() : split_kernel<false>());
     kernel.grid = dim3(static_cast<unsigned>((row_blocks + per_group - 1) / per_group), 1, 1);
     kernel.block = dim3(64 * kSplitWaves, 1, 1);
+    // Dynamic LDS beyond 64 KB: launch() opts the function in (enable_large_lds).
+    kernel.shmem = gather ? static_cast<unsigned>(16 * (args.k + 8) * 2) : 0u;
   } else if (choice.kind == GemmKind::Stream) {
     const int64_t groups = ((args.n + 15) / 16 + kStreamWaves - 1) / kStreamWaves;
     const int64_t slices = stream_slices(args.k, choice.k_slice);
-    const bool gather = args.gather_slots != nullptr;  // only ever set for gate_up
+    const bool gather = fused_gather && gated;
     kernel.func = gather ? stream_kernel<true, true>() : (gated ? stream_kernel<true>() : stream_kernel<false>());
     kernel.grid = dim3(static_cast<unsigned>(slices * groups), 1, 1);
     kernel.block = dim3(64 * kStreamWaves, 1, 1);

@@ -202,7 +202,7 @@ DenseLaunches make_dense_launches(const DenseBinding &b, int64_t capacity) {
     gate_up.pool_rows = b.pool_rows;
     gate_up.eps = b.eps;
   }
-  launches.gate_up = make_gemm(gate_up, capacity, true, gate_up_choice);
+  launches.gate_up = make_gemm(gate_up, capacity, true, gate_up_choice, fused);
 
   GemmArgs down{};
   down.x = activated;
@@ -1359,6 +1359,21 @@ int xp_dense_step_static(const void *pool_in, void *pool_out, int64_t pool_rows,
 
 size_t xp_gemm_variant(int64_t capacity, int64_t n, int64_t k, int gated, char *buffer, size_t size) {
   const std::string name = capacity > 0 ? gemm_name(choose_gemm(capacity, n, k, gated != 0), gated != 0) : "";
+  if (buffer != nullptr && size > 0) {
+    const size_t count = std::min(size - 1, name.size());
+    std::memcpy(buffer, name.data(), count);
+    buffer[count] = '\0';
+  }
+  return name.size();
+}
+
+size_t xp_dense_gate_up_variant(int64_t capacity, int64_t hidden, int64_t intermediate, char *buffer, size_t size) {
+  std::string name;
+  if (capacity > 0 && hidden > 0 && intermediate > 0) {
+    bool fused = false;
+    const GemmChoice choice = choose_dense_gate_up(capacity, 2 * intermediate, hidden, fused);
+    name = gemm_name(choice, true) + (fused ? "+gather" : "");
+  }
   if (buffer != nullptr && size > 0) {
     const size_t count = std::min(size - 1, name.size());
     std::memcpy(buffer, name.data(), count);

@@ -327,7 +327,7 @@ struct GemmArgs {
   int64_t n;         // weight rows
   int64_t k;         // reduction length
   GatedSilu act;
-  // Gather fused into the gate_up of a Dense step at decode sizes (stream kernel only):
+  // Gather fused into the gate_up of a Dense step at decode sizes (stream or split kernel):
   // when set, token row t is row gather_slots[t] of the mailbox `x` ([pool_rows, ldx]),
   // RMS-normalised with `norm` when that is set, bit for bit as gather_rows_kernel does;
   // an out-of-range slot gives a row of quiet NaNs and raises kFaultSlotOutOfRange.
@@ -376,7 +376,12 @@ struct GemmLaunch {
   KernelLaunch main;
   KernelLaunch reduce;
 };
-GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmChoice choice);
+// `fused_gather`: the gate_up of a Dense step whose choose_dense_gate_up decision fused the
+// mailbox gather (the kernel variant follows that decision, not whether the argument record
+// already holds slot pointers, so a template captured with placeholder arguments has the
+// nodes its replays launch).
+GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmChoice choice,
+                     bool fused_gather = false);
 // The grouped projection over an expert tile table of `max_tiles` entries (a multiple of
 // 8; otherwise an empty launch), on the tile kernel whose BM is grouped_tile_rows() (the
 // table must be built for that BM).

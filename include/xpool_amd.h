@@ -210,6 +210,10 @@ int xp_dense_step_static(const void *pool_in, void *pool_out, int64_t pool_rows,
 /* Name of the kernel variant chosen for a projection ("split_..." / "stream_..." / "tile_...").
  * Returns the full name length. */
 size_t xp_gemm_variant(int64_t capacity, int64_t n, int64_t k, int gated, char *buffer, size_t size);
+/* Name of the gate_up variant of a Dense step (xp_dense_step, a Lane template) at `capacity`
+ * rows: xp_gemm_variant's names, with "+gather" when the mailbox gather and RMSNorm run inside
+ * that kernel (no separate gather launch).  Diagnostic only; no counterpart in the reference. */
+size_t xp_dense_gate_up_variant(int64_t capacity, int64_t hidden, int64_t intermediate, char *buffer, size_t size);
 
 /* ------------------------------------------------------------------ runtime */
 

@@ -106,13 +106,25 @@ def test_config3_qwen3_8b_layer(device, rows):
 
 
 @pytest.mark.parametrize("normed", [True, False])
-def test_fused_gather_matches_separate_kernels_bitwise(device, normed):
-    # At up to 16 rows the gather (+ RMSNorm) runs inside gate_up.  At 16 rows the kernel-level
-    # projections take the same stream kernels with the same K slices, so the step must equal
-    # gather kernel -> gate_up -> down -> scatter bit for bit.
+@pytest.mark.parametrize(
+    "hidden,intermediate,rows,variant",
+    [
+        (4096, 12288, 16, "stream_gated_t16+gather"),
+        (1024, 3072, 1, "split_gated_t16_k4+gather"),
+        (1024, 3072, 8, "split_gated_t16_k4+gather"),
+        (2048, 6144, 5, "split_gated_t16_k8+gather"),
+    ],
+)
+def test_fused_gather_matches_separate_kernels_bitwise(device, normed, hidden, intermediate, rows, variant):
+    # At decode sizes the gather (+ RMSNorm) runs inside gate_up: the stream kernel (Qwen3-8B,
+    # 16 rows) or the split kernel (Qwen3-0.6B / 1.7B shapes, up to 8 rows), which stage the
+    # same bits the gather kernel writes.  The kernel-level projections take the same kernels
+    # with the same K ranges, so the step must equal gather kernel -> gate_up -> down ->
+    # scatter bit for bit.
     from crosspool_amd import dense
 
-    hidden, intermediate, pool_rows, rows = 4096, 12288, 256, 16
+    pool_rows = 256
+    assert _native.dense_gate_up_variant(rows, hidden, intermediate) == variant
     pool = o.generate_hidden_states(pool_rows, hidden, 17)
     w_gate_up, w_down, norm_weight = o.generate_layer(hidden, intermediate, 18)
     slots = o.generate_slots(pool_rows, rows, 19)
@@ -130,8 +142,9 @@ def test_fused_gather_matches_separate_kernels_bitwise(device, normed):
     activated = dense.gate_up_silu(x, weights.i_proj.values)
     dense.down(activated, weights.o_proj.values, out=expected, slots=slots_d)
     torch.cuda.synchronize()
-    assert _native.gemm_variant(rows, 2 * intermediate, hidden, True).startswith("stream")
+    assert _native.gemm_variant(rows, 2 * intermediate, hidden, True) == variant.removesuffix("+gather")
     assert_bitwise_equal(pool_gpu.cpu(), expected.cpu())
+    _check_mailbox(pool_gpu, pool, slots, w_gate_up, w_down, norm_weight if normed else None)
 
 
 @pytest.mark.parametrize("rows", [3, 16])

@@ -313,6 +313,19 @@ def test_gemm_variant_selection():
     assert _native.gemm_workspace_bytes(2048, 24576, 4096, True) == 0
 
 
+def test_dense_step_fuses_the_gather_at_decode_sizes():
+    # Qwen3-0.6B / 1.7B gate_up up to 8 rows: the split kernel stages the gathered, normalised
+    # rows itself; Qwen3-8B: the stream kernel; K past 4096 (the 32B TP shard's 5120) does
+    # not fit the split kernel's staging, and past 16 rows the gather is a launch of its own.
+    for rows in (1, 4, 8):
+        assert _native.dense_gate_up_variant(rows, 1024, 3072) == "split_gated_t16_k4+gather"
+        assert _native.dense_gate_up_variant(rows, 4096, 12288) == "stream_gated_t16+gather"
+        assert "+gather" not in _native.dense_gate_up_variant(rows, 5120, 3200)
+    assert _native.dense_gate_up_variant(16, 4096, 12288) == "stream_gated_t16+gather"
+    assert _native.dense_gate_up_variant(32, 4096, 12288) == "tile_gated_64x128"
+    assert _native.dense_gate_up_variant(2048, 4096, 12288) == "tile_gated_256x256"
+
+
 def test_k_split_tiles_fill_the_chip_and_size_their_partials():
     # Qwen3-8B down at 256 rows has only 16 to 64 weight x token tiles: K is split so that
     # the grid covers the 256 CUs, and each range leaves an fp32 partial tile in scratch.
