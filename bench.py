@@ -226,6 +226,7 @@ def main() -> int:
 
     from crosspool_amd import _native, dense
     from crosspool_amd.agent import FfnAgent
+    from crosspool_amd.execution import derive_payload_row_capacities, select_capacity
     from crosspool_amd.weights import DenseFfnWeights
     from oracle import ffn_oracle as o
 
@@ -576,35 +577,35 @@ def main() -> int:
 
     # ---------------------------------------------------------------- MoE layer
     # Qwen3-30B-A3B-shaped MoE layer (no BASELINE config names one; reported beside the
-    # Dense path): Router (128 experts, softmax top-8, renormalised) + Experts (hidden 2048,
-    # moe_intermediate 768), timed with HIP events on the current stream.
+    # Dense path), registered as a MoE layer and replayed through its Lane template like a
+    # Dense layer: gather + RMSNorm, Router (128 experts, softmax top-8, renormalised),
+    # Experts (hidden 2048, moe_intermediate 768), combine written to the slots.  Timed with
+    # HIP events on the current stream.
     moe = None
     if not args.no_sweep:
-        from crosspool_amd.moe import Experts, MoeFfnWeights, MoeRouterWeights, Router
+        from crosspool_amd.moe import MoeFfnWeights, MoeLayerSpec, MoeRouterWeights
 
         m_hidden, m_inter, m_experts, m_topk = MOE_SHAPE
         generator = torch.Generator(device=device).manual_seed(18)
         moe_weights = MoeFfnWeights(
             (torch.randn((m_experts, 2 * m_inter, m_hidden), device=device, generator=generator) * 0.02).bfloat16(),
             (torch.randn((m_experts, m_hidden, m_inter), device=device, generator=generator) * 0.02).bfloat16(),
+            MoeRouterWeights((torch.randn((m_experts, m_hidden), device=device, generator=generator) * 0.02).bfloat16()),
         )
-        router_weights = MoeRouterWeights(
-            (torch.randn((m_experts, m_hidden), device=device, generator=generator) * 0.02).bfloat16()
-        )
+        moe_spec = MoeLayerSpec(routed_expert_count=m_experts, routed_topk=m_topk)
+        moe_agent = FfnAgent(device)
+        moe_agent.register_moe_layer(instance_index=0, layer_ordinal=0, weights=moe_weights, spec=moe_spec,
+                                     norm_weight=torch.ones(m_hidden, dtype=torch.bfloat16, device=device))
+        moe_agent.materialize(maximum_row_capacity=max(MOE_TOKENS))
+        moe_pool = torch.randn((max(MOE_TOKENS) + 64, m_hidden), device=device, generator=generator).bfloat16()
         moe = {"shape": {"hidden": m_hidden, "moe_intermediate": m_inter, "experts": m_experts, "topk": m_topk},
-               "points": []}
+               "execution": "MoE GraphTemplate replay (FfnAgent.register_moe_layer)", "points": []}
         for t in MOE_TOKENS:
-            x = torch.randn((t, m_hidden), device=device, generator=generator).bfloat16()
-            router = Router(row_capacity=t, hidden_size=m_hidden, routed_expert_count=m_experts, routed_topk=m_topk,
-                            device=device)
-            experts_op = Experts(row_capacity=t, hidden_size=m_hidden, local_intermediate_size=m_inter,
-                                 expert_count=m_experts, effective_topk=m_topk, device=device)
-            out = torch.empty_like(x)
+            moe_slots = torch.arange(t, dtype=torch.int32, device=device)
 
             def moe_step() -> None:
-                router.run_into(hidden_states=x, router_weights=router_weights)
-                experts_op.run_into(hidden_states=x, weights=moe_weights, topk_ids=router.ids,
-                                    topk_weights=router.weights, output=out)
+                moe_agent.execute(instance_index=0, layer_ordinal=0, pool=moe_pool, slots=moe_slots,
+                                  stream=torch.cuda.current_stream())
 
             for _ in range(3):
                 moe_step()
@@ -617,7 +618,12 @@ def main() -> int:
             end.record()
             end.synchronize()
             moe_seconds = begin.elapsed_time(end) / 1e3 / launches
-            active = int(torch.unique(router.ids).numel())
+            capacity = select_capacity(derive_payload_row_capacities(max(MOE_TOKENS)), t)
+            desc = moe_spec.signature(hidden_size=m_hidden, local_intermediate_size=m_inter,
+                                      payload_row_capacity=capacity).native_descriptor()
+            ids_at = _native.moe_step_workspace_layout(desc, capacity)[4]
+            ids = moe_agent.lanes[0].workspace[ids_at:ids_at + 4 * t * m_topk].view(torch.int32)
+            active = int(torch.unique(ids).numel())
             flops = 2.0 * t * m_experts * m_hidden + 6.0 * t * m_topk * m_hidden * m_inter
             weight_bytes = 2.0 * m_experts * m_hidden + 6.0 * active * m_hidden * m_inter
             moe["points"].append({
@@ -626,9 +632,10 @@ def main() -> int:
                 "hbm_frac": round((weight_bytes + 4.0 * t * m_hidden) / moe_seconds / 1e9 / HBM_PEAK_GBS, 4),
                 "mfma_frac": round(flops / moe_seconds / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
             })
-            del router, experts_op, x, out
-        del moe_weights, router_weights
-        agent.check_health()
+            del moe_slots
+        moe_agent.check_health()
+        moe_agent.close()
+        del moe_weights, moe_pool
 
     # ---------------------------------------------------------------- ffn_shim transaction
     # Host-timed ffn_shim calls on resident [T, H] hidden states: through the Transport
