@@ -156,13 +156,17 @@ def run_ceilings(device) -> dict:
     best = max(point["tflops"] for point in mfma)
     result["mfma_bf16"] = {"points": mfma, "best_tflops": best, "frac_of_2500": round(best / MFMA_BF16_PEAK_TFLOPS, 4)}
 
-    # HBM reads: a 2 GiB buffer (past the 256 MB last-level cache), 1 KB per wave instruction.
-    buffer = torch.empty(2 << 30, dtype=torch.uint8, device=device)
+    # HBM reads: a 4 GiB buffer (far past the 256 MB last-level cache), 1 KB per wave
+    # instruction, plain loads and loads with the nontemporal hint.
+    buffer = torch.empty(4 << 30, dtype=torch.uint8, device=device)
     contiguous = []
-    for workgroups in (1024, 2048, 4096, 8192):
-        seconds = per_launch(lambda index=0: checked(probes.xp_probe_read_contiguous(
-            ctypes.c_void_p(buffer.data_ptr()), ctypes.c_uint64(buffer.numel()), workgroups, handle)), 10)
-        contiguous.append({"workgroups": workgroups, "gbs": round(buffer.numel() / seconds / 1e9, 1)})
+    for nontemporal in (0, 1):
+        for workgroups in (2048, 8192, 32768):
+            seconds = per_launch(lambda index=0: checked(probes.xp_probe_read_contiguous(
+                ctypes.c_void_p(buffer.data_ptr()), ctypes.c_uint64(buffer.numel()), workgroups, nontemporal,
+                handle)), 10)
+            contiguous.append({"workgroups": workgroups, "nontemporal": bool(nontemporal),
+                               "gbs": round(buffer.numel() / seconds / 1e9, 1)})
     del buffer
     # The decode weight-stream pattern over three copies of the Qwen3-8B gate_up matrix
     # ([24576, 4096] bf16, 201 MB each, rotated so each launch streams from HBM).
@@ -177,7 +181,7 @@ def run_ceilings(device) -> dict:
                            "gbs": round(rows * row_bytes / seconds / 1e9, 1)})
     del copies
     best_read = max(point["gbs"] for point in contiguous + row_points)
-    result["hbm_read"] = {"contiguous_2gib": contiguous, "weight_rows_qwen3_8b_gate_up": row_points,
+    result["hbm_read"] = {"contiguous_4gib": contiguous, "weight_rows_qwen3_8b_gate_up": row_points,
                           "best_gbs": best_read, "frac_of_8000": round(best_read / HBM_PEAK_GBS, 4)}
 
     # GPU time a hipGraphLaunch adds per replay: one Qwen3-0.6B layer at one row replayed

@@ -103,7 +103,7 @@ class ExecutorLane:
         )
         self.handle = handle
         # Replays launch the template's kernels directly unless graph dispatch is asked for
-        # (each hipGraphLaunch adds ~9 us of GPU time per replay on ROCm; same kernels either way).
+        # (each hipGraphLaunch adds 6-9 us of GPU time per replay on ROCm; same kernels either way).
         self.graph_dispatch = bool(graph_dispatch)
         _native.call("xp_lane_set_graph_dispatch", self.handle, int(self.graph_dispatch))
         stream = ctypes.c_void_p()
@@ -171,6 +171,10 @@ class ExecutorLane:
                 raise ValueError(f"{name} must be contiguous")
         if out_pool.shape != pool.shape:
             raise ValueError("input and output mailboxes must have one shape")
+        binding = self.agent.layers.get((instance_index, layer_ordinal))
+        if binding is not None and pool.shape[1] != binding.weights.hidden_size:
+            # The kernels index mailbox rows by the layer's hidden size.
+            raise ValueError(f"mailbox rows must hold the layer's hidden size {binding.weights.hidden_size}")
         if slots.device != self.agent.device or slots.dtype is not torch.int32 or slots.ndim != 1:
             raise ValueError("slots must be a device int32 vector")
         rows = slots.numel() if rows is None else rows
@@ -465,11 +469,8 @@ class FfnAgent:
 
         if not self.materialized:
             raise RuntimeError("FfnAgent has not been materialized")
-        binding = self.layers.get((instance_index, layer_ordinal))
-        if binding is None:
+        if (instance_index, layer_ordinal) not in self.layers:
             raise KeyError(f"no layer registered for instance {instance_index} ordinal {layer_ordinal}")
-        if pool.ndim != 2 or pool.shape[1] != binding.weights.hidden_size:
-            raise ValueError(f"mailbox rows must hold the layer's hidden size {binding.weights.hidden_size}")
         self.lanes[lane].replay(
             instance_index=instance_index, layer_ordinal=layer_ordinal, pool=pool, slots=slots, rows=rows,
             out_pool=out_pool, stream=stream,

@@ -7,7 +7,8 @@
 //    clock it holds under that load.
 //  * probe_read_contiguous: a grid-stride read of a buffer, each wave instruction 1 KB of
 //    consecutive bytes, UNROLL loads in flight per lane: the HBM read rate of the plainest
-//    streaming pattern.
+//    streaming pattern, with plain loads or with the nontemporal hint (`nt`), which the
+//    tile kernels use for weights they read once.
 //  * probe_read_rows: the weight-streaming pattern of the decode projection kernels: a wave
 //    owns 16 rows of a row-major matrix and reads 16 rows x 64 contiguous bytes per
 //    instruction, four 256-byte chunks per row in flight; grid y splits each row into
@@ -63,7 +64,7 @@ __global__ __launch_bounds__(256) void probe_mfma_kernel(int rounds, float *sink
   }
 }
 
-template <int UNROLL>
+template <int UNROLL, bool NONTEMPORAL>
 __global__ __launch_bounds__(256) void probe_read_contiguous_kernel(const u32x4 *source, uint64_t vectors,
                                                                     uint32_t *sink, int write) {
   const uint64_t thread = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -74,7 +75,11 @@ __global__ __launch_bounds__(256) void probe_read_contiguous_kernel(const u32x4 
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
       const uint64_t index = first + u * stride;
-      values[u] = index < vectors ? source[index] : u32x4{0u, 0u, 0u, 0u};
+      if constexpr (NONTEMPORAL) {
+        values[u] = index < vectors ? __builtin_nontemporal_load(source + index) : u32x4{0u, 0u, 0u, 0u};
+      } else {
+        values[u] = index < vectors ? source[index] : u32x4{0u, 0u, 0u, 0u};
+      }
     }
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
@@ -129,10 +134,18 @@ int xp_probe_mfma(int workgroups, int rounds, void *stream) {
   return static_cast<int>(hipGetLastError());
 }
 
-// Reads `bytes` (a multiple of 16) from `source` with `workgroups` 256-thread workgroups.
-int xp_probe_read_contiguous(const void *source, uint64_t bytes, int workgroups, void *stream) {
-  hipLaunchKernelGGL(probe_read_contiguous_kernel<8>, dim3(workgroups), dim3(256), 0, static_cast<hipStream_t>(stream),
-                     static_cast<const u32x4 *>(source), bytes / 16, static_cast<uint32_t *>(nullptr), 0);
+// Reads `bytes` (a multiple of 16) from `source` with `workgroups` 256-thread workgroups,
+// with plain loads or (nontemporal != 0) with the nontemporal hint.
+int xp_probe_read_contiguous(const void *source, uint64_t bytes, int workgroups, int nontemporal, void *stream) {
+  if (nontemporal != 0) {
+    hipLaunchKernelGGL((probe_read_contiguous_kernel<8, true>), dim3(workgroups), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const u32x4 *>(source), bytes / 16,
+                       static_cast<uint32_t *>(nullptr), 0);
+  } else {
+    hipLaunchKernelGGL((probe_read_contiguous_kernel<8, false>), dim3(workgroups), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const u32x4 *>(source), bytes / 16,
+                       static_cast<uint32_t *>(nullptr), 0);
+  }
   return static_cast<int>(hipGetLastError());
 }
 

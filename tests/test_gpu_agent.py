@@ -363,6 +363,10 @@ def test_out_of_range_slot_sets_sticky_fault(device):
         assert agent.lanes[0].check_health() == _native.XP_FAULT_SLOT_OUT_OF_RANGE  # sticky
         agent.lanes[0].clear_fault()
         assert agent.lanes[0].check_health() == 0
+        # A mailbox narrower than the layer's rows is refused before any kernel reads it.
+        narrow = torch.zeros((64, hidden - 8), dtype=torch.bfloat16, device=device)
+        with pytest.raises(ValueError, match="hidden size"):
+            agent.lanes[0].replay(instance_index=0, layer_ordinal=0, pool=narrow, slots=bad)
     got = pool_gpu.cpu()
     untouched = np.setdiff1d(np.arange(64), [1, 2])
     assert_bitwise_equal(got[untouched], pool[untouched])
