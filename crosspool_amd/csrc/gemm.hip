@@ -55,10 +55,13 @@ constexpr uint32_t kOutOfRange = 0x7ffffff0u;
 // t is mailbox row gather_slots[t] of a.x ([pool_rows, a.k]), RMS-normalised with a.norm when
 // that is set, bit for bit as gather_rows_kernel computes it; rows past the live rows are
 // zero and a slot outside the mailbox gives a row of quiet NaNs and raises the fault bit.
-// All WAVES waves of the workgroup take part; the caller synchronises before reading.
+// Only rows [0, staged_rows) are written (the LDS holds no more; staged_rows <= TP covers
+// the live rows).  All WAVES waves of the workgroup take part; the caller synchronises
+// before reading.
 template <int TP, int WAVES>
 __device__ __forceinline__ void stage_gathered_rows(const GemmArgs &a, uint16_t *xs, int64_t rs, int kbase,
-                                                    int kvalid, int vectors_per_row, int wave, int lane) {
+                                                    int kvalid, int vectors_per_row, int wave, int lane,
+                                                    int staged_rows) {
   const u32x4 zero = {0u, 0u, 0u, 0u};
   // Wave w finds rows w, w + WAVES, ... of the slot list and their inverse RMS over the
   // whole row (the gather kernel's wavefront reduction, so the same bits), then the columns
@@ -133,6 +136,9 @@ __device__ __forceinline__ void stage_gathered_rows(const GemmArgs &a, uint16_t 
 #pragma unroll
     for (int r = 0; r < ROWS_PER_WAVE; ++r) {
       const int t = wave + r * WAVES;
+      if (t >= staged_rows) {
+        continue;
+      }
 #pragma unroll
       for (int b = 0; b < BATCH; ++b) {
         const int64_t chunk = lane + b * kWave;
@@ -158,7 +164,7 @@ __device__ __forceinline__ void stage_gathered_rows(const GemmArgs &a, uint16_t 
   } else {
     __syncthreads();
     constexpr int STAGE_BATCH = 4;
-    const int items = TP * vectors_per_row;
+    const int items = staged_rows * vectors_per_row;
     for (int first = threadIdx.x; first < items; first += STAGE_BATCH * 64 * WAVES) {
       u32x4 x_chunk[STAGE_BATCH];
       u32x4 w_chunk[STAGE_BATCH];
@@ -211,7 +217,8 @@ constexpr int kSplitWaves = 8;
 // of a.x, RMS-normalised with a.norm when that is set, staged once per workgroup into LDS
 // (stage_gathered_rows, the gather kernel's bits) while the first DEPTH chunks of weights
 // are in flight; the token fragments are then read from LDS instead of L2.  Dynamic LDS:
-// 16 x (K + 8) bf16.
+// min(capacity, 16) x (K + 8) bf16, so that at one or a few rows several workgroups share a
+// CU.
 template <int TB, int DEPTH, bool GATED, bool GATHER = false>
 __global__ __launch_bounds__(64 * kSplitWaves) void split_gemm_kernel(GemmArgs a) {
   static_assert(!GATHER || TB == 1, "the fused gather stages one 16-row token block");
@@ -227,6 +234,8 @@ __global__ __launch_bounds__(64 * kSplitWaves) void split_gemm_kernel(GemmArgs a
   const bool active = rb < row_blocks;
   const u32x4 zero = {0u, 0u, 0u, 0u};
   const int64_t rs = a.k + 8;  // staged row stride in elements (GATHER)
+  // GATHER: rows staged in LDS, the capacity's (at most 16): rows past them are zero.
+  const int staged_rows = a.capacity < 16 ? static_cast<int>(a.capacity) : 16;
 
   f32x4 acc[TB];
 #pragma unroll
@@ -286,7 +295,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) void split_gemm_kernel(GemmArgs a
       for (int tb = 0; tb < TB; ++tb) {
         u32x4 xk;
         if constexpr (GATHER) {
-          xk = valid ? load16(staged + r16 * rs + k0 + column + s * 32 + kq * 8) : zero;
+          xk = valid && r16 < staged_rows ? load16(staged + r16 * rs + k0 + column + s * 32 + kq * 8) : zero;
         } else {
           xk = valid ? x[tb][s] : zero;
         }
@@ -305,7 +314,8 @@ __global__ __launch_bounds__(64 * kSplitWaves) void split_gemm_kernel(GemmArgs a
   }
   if constexpr (GATHER) {
     const int vectors = static_cast<int>(a.k / 8);
-    stage_gathered_rows<16, kSplitWaves>(a, staged, rs, 0, static_cast<int>(a.k), vectors, wave, lane);
+    stage_gathered_rows<16, kSplitWaves>(a, staged, rs, 0, static_cast<int>(a.k), vectors, wave, lane,
+                                         staged_rows);
     __syncthreads();
   }
   if (active) {
@@ -593,7 +603,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_gemm_kernel(GemmArgs
   const int kbase = static_cast<int>(k0);
   const int kvalid = static_cast<int>(klen);
   if constexpr (GATHER) {
-    stage_gathered_rows<TP, kStreamWaves>(a, xs, rs, kbase, kvalid, vectors_per_row, wave, lane);
+    stage_gathered_rows<TP, kStreamWaves>(a, xs, rs, kbase, kvalid, vectors_per_row, wave, lane, TP);
   } else {
     const __amdgpu_buffer_rsrc_t x_rsrc = make_rsrc(a.x, static_cast<uint32_t>(a.rows * a.ldx * 2));
     for (int index = threadIdx.x; index < TP * vectors_per_row; index += 64 * kStreamWaves) {
@@ -1680,7 +1690,7 @@ GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmCho
     kernel.grid = dim3(static_cast<unsigned>((row_blocks + per_group - 1) / per_group), 1, 1);
     kernel.block = dim3(64 * kSplitWaves, 1, 1);
     // Dynamic LDS beyond 64 KB: launch() opts the function in (enable_large_lds).
-    kernel.shmem = gather ? static_cast<unsigned>(16 * (args.k + 8) * 2) : 0u;
+    kernel.shmem = gather ? static_cast<unsigned>((capacity < 16 ? capacity : 16) * (args.k + 8) * 2) : 0u;
   } else if (choice.kind == GemmKind::Stream) {
     const int64_t groups = ((args.n + 15) / 16 + kStreamWaves - 1) / kStreamWaves;
     const int64_t slices = stream_slices(args.k, choice.k_slice);
