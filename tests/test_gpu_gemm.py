@@ -147,8 +147,14 @@ def test_variant_selection_covers_every_family(device):
     # the Qwen3-8B cases of test_qwen3_8b_projections reach every tile shape and K splits
     chosen = {_native.gemm_variant(rows, n, k, gated) for rows in (32, 64, 128, 256, 512)
               for n, k, gated in ((24576, 4096, True), (4096, 12288, False))}
-    assert {"tile_gated_64x128", "tile_gated_128x128", "tile_gated_256x128", "tile_gated_256x256", "tile_64x128_k8",
-            "tile_128x128_k8", "tile_256x128_k4"} <= chosen
+    assert {"tile_gated_64x64", "tile_gated_64x128", "tile_gated_128x128", "tile_gated_256x128", "tile_gated_256x256",
+            "tile_64x128_k8", "tile_128x128_k8", "tile_256x128_k4"} <= chosen
+    # A gated grid of half-full 64-row token tiles under the CU count takes the 64 x 64 tile
+    # (Qwen3-8B at 32 rows, not at 64); Qwen3-0.6B at 17 rows keeps the 64 x 128 tile with
+    # its K split.
+    assert _native.gemm_variant(32, 24576, 4096, True) == "tile_gated_64x64"
+    assert _native.gemm_variant(64, 24576, 4096, True) == "tile_gated_64x128"
+    assert _native.gemm_variant(17, 6144, 1024, True) == "tile_gated_64x128_k4"
     # The headline sizes of tests/test_gpu_headline.py (config 3 at 1024 / 2048 / 4096 rows,
     # config 5 at 512 / 8192) reach the unsplit tiles and the split 256 x 256 down tile.
     headline = {_native.gemm_variant(rows, n, k, gated) for (hidden, intermediate), sizes in

@@ -304,7 +304,9 @@ def test_gemm_variant_selection():
     assert _native.gemm_variant(1, 2560, 9728, False) == "split_t16_k8"
     assert _native.gemm_variant(1, 1024, 3072, False) == "split_t16_k8"
     assert _native.gemm_workspace_bytes(1, 2560, 9728, False) == 0
-    assert _native.gemm_variant(17, 24576, 4096, True).startswith("tile_gated_64x128")
+    assert _native.gemm_variant(17, 24576, 4096, True) == "tile_gated_64x64"
+    assert _native.gemm_variant(128, 6144, 1024, True) == "tile_gated_64x64"  # 96 tiles of 64 x 128
+    assert _native.gemm_variant(128, 24576, 4096, True) == "tile_gated_128x128"
     assert _native.gemm_variant(64, 4096, 12288, False).startswith("tile_64x128_k")
     assert _native.gemm_workspace_bytes(1, 24576, 4096, True) == 0
     assert _native.gemm_workspace_bytes(16, 4096, 12288, False) > 0
@@ -322,7 +324,7 @@ def test_dense_step_fuses_the_gather_at_decode_sizes():
         assert _native.dense_gate_up_variant(rows, 4096, 12288) == "stream_gated_t16+gather"
         assert "+gather" not in _native.dense_gate_up_variant(rows, 5120, 3200)
     assert _native.dense_gate_up_variant(16, 4096, 12288) == "stream_gated_t16+gather"
-    assert _native.dense_gate_up_variant(32, 4096, 12288) == "tile_gated_64x128"
+    assert _native.dense_gate_up_variant(32, 4096, 12288) == "tile_gated_64x64"
     assert _native.dense_gate_up_variant(2048, 4096, 12288) == "tile_gated_256x256"
 
 
