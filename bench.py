@@ -173,12 +173,13 @@ def run_ceilings(device) -> dict:
     rows, row_bytes = 2 * INTERMEDIATE, 2 * HIDDEN
     copies = [torch.empty(rows * row_bytes, dtype=torch.uint8, device=device) for _ in range(3)]
     row_points = []
-    for ranges in (1, 2, 4, 8):
-        seconds = per_launch(lambda index=0: checked(probes.xp_probe_read_rows(
-            ctypes.c_void_p(copies[index % 3].data_ptr()), ctypes.c_int64(rows), ctypes.c_int64(row_bytes), ranges,
-            handle)), 30)
-        row_points.append({"ranges": ranges, "workgroups": (rows // 16 + 7) // 8 * ranges,
-                           "gbs": round(rows * row_bytes / seconds / 1e9, 1)})
+    for pattern, name in ((0, "half_lines"), (3, "half_lines_nt"), (1, "lines"), (2, "lines_nt")):
+        for ranges in (1, 2, 4, 8):
+            seconds = per_launch(lambda index=0: checked(probes.xp_probe_read_rows(
+                ctypes.c_void_p(copies[index % 3].data_ptr()), ctypes.c_int64(rows), ctypes.c_int64(row_bytes),
+                ranges, pattern, handle)), 30)
+            row_points.append({"pattern": name, "ranges": ranges, "workgroups": (rows // 16 + 7) // 8 * ranges,
+                               "gbs": round(rows * row_bytes / seconds / 1e9, 1)})
     del copies
     best_read = max(point["gbs"] for point in contiguous + row_points)
     result["hbm_read"] = {"contiguous_4gib": contiguous, "weight_rows_qwen3_8b_gate_up": row_points,

@@ -9,12 +9,13 @@
 // Gate/Up (runtime/ffnagent/preparation.py:227).  Accumulation is fp32.
 //
 // Three kernel families, chosen per GraphTemplate capacity (choose_gemm):
-//  * split (up to 4 / 8 rows, HBM-bound): weight rows are the MFMA M operand
-//    (v_mfma_f32_16x16x32_bf16), each lane streams 64 contiguous bytes of one weight row
-//    per 128-wide K chunk with several chunks of loads in flight, the few token rows are
-//    the N operand and come from L2.  A workgroup splits K across its waves and sums the
-//    ranges through LDS in a fixed order (deterministic).  A Gate/Up pair lands in one
-//    lane's accumulator registers, so the SiLU epilogue needs no data exchange.
+//  * split (up to 8 rows, HBM-bound): weight rows are the MFMA M operand
+//    (v_mfma_f32_16x16x32_bf16), read as whole 128-byte lines (8 rows x 128 bytes per load
+//    instruction, nontemporal) with several 128-wide K chunks of loads in flight; the few
+//    token rows are the N operand and come from L2 (or from LDS with the gather fused).  A
+//    workgroup splits K across its waves and sums the ranges through LDS in a fixed order
+//    (deterministic).  A Gate/Up pair lands in one lane's accumulator registers, so the
+//    SiLU epilogue needs no data exchange.
 //  * stream (up to 16 rows, HBM-bound): the same weight streaming with the token rows of
 //    a K slice staged in LDS once per workgroup; sliced K goes through fp32 partial sums
 //    and an ordered reduction kernel.
@@ -202,46 +203,55 @@ __device__ __forceinline__ void stage_gathered_rows(const GemmArgs &a, uint16_t 
 }
 
 // ------------------------------------------------------------------ split (decode)
-// Weight-streaming projection for at most 64 live rows (HBM-bound).  A workgroup of 8
-// waves covers 8 / KSPLIT weight-row blocks of 16 rows; the KSPLIT waves of a block each
-// stream one contiguous K range of `k_slice` columns.  Per 128-wide K chunk a lane loads
-// 16 bytes of its weight row (16 rows x 64 contiguous bytes per load instruction) and the
-// matching token fragments (L2-resident; token rows past the live rows cost no memory
-// access), and the wave multiplies them on v_mfma_f32_16x16x32_bf16 with the weights as
-// the M operand.  DEPTH chunks of loads stay in flight.  The K ranges of a row block are
-// summed through LDS in a fixed order (deterministic), all within the workgroup, so no
-// partial sums leave the chip.
+// Weight-streaming projection for at most 8 live rows (HBM-bound).  A workgroup of 8 waves
+// covers 8 / KSPLIT weight-row blocks of 16 rows; the KSPLIT waves of a block each stream
+// one contiguous K range of `k_slice` columns, 128-wide K chunks with DEPTH chunks of loads
+// in flight, multiplied on v_mfma_f32_16x16x32_bf16 with the weights as the M operand.  The
+// K ranges of a row block are summed through LDS in a fixed order (deterministic), all
+// within the workgroup, so no partial sums leave the chip.
+//
+// Each weight load instruction reads whole 128-byte lines, 8 rows x 128 bytes, with the
+// nontemporal hint (read once; measured on MI355X over Qwen3-8B gate_up: 6.4 TB/s, against
+// 5.6 TB/s for 16 rows x 64 bytes per instruction, which the hint slows down).  Lane
+// (i, q) = (lane & 15, lane >> 4) loads row i & 7 of the half, 16-byte piece p = 2 q + (i >> 3)
+// of the line (K columns 8 p .. 8 p + 7).  As an MFMA operand, operand row i then holds the
+// even pieces of weight row i (i < 8) or the odd pieces of weight row i - 8, and the token
+// operand is laid out the same way: column j holds token j & 7 at piece 2 q + (j >> 3).
+// Products pair matching pieces only in the diagonal blocks, D[r][t] (even pieces) and
+// D[r + 8][t + 8] (odd pieces) for r, t < 8, whose sum is the full dot product of weight
+// row r with token t; the off-diagonal blocks are discarded.  Half the MFMA work is thus
+// wasted, which the decode sizes leave idle anyway (one 16x16x32 per KB of weights).
+// Token pieces come from L2 (rows past the live rows cost no memory access).
 constexpr int kSplitWaves = 8;
+constexpr int kSplitTokens = 8;
 
-// GATHER (one token block, K <= 4096): the token rows are the mailbox rows gather_slots[t]
-// of a.x, RMS-normalised with a.norm when that is set, staged once per workgroup into LDS
+// GATHER (K <= 4096): the token rows are the mailbox rows gather_slots[t] of a.x,
+// RMS-normalised with a.norm when that is set, staged once per workgroup into LDS
 // (stage_gathered_rows, the gather kernel's bits) while the first DEPTH chunks of weights
-// are in flight; the token fragments are then read from LDS instead of L2.  Dynamic LDS:
-// min(capacity, 16) x (K + 8) bf16, so that at one or a few rows several workgroups share a
-// CU.
-template <int TB, int DEPTH, bool GATED, bool GATHER = false>
+// are in flight; the token pieces are then read from LDS instead of L2.  Dynamic LDS:
+// min(capacity, 8) x (K + 16) bf16, so that at one or a few rows several workgroups share a
+// CU (the 32-byte row padding puts the 16 pieces of one read in distinct bank slots).
+template <int DEPTH, bool GATED, bool GATHER = false>
 __global__ __launch_bounds__(64 * kSplitWaves) void split_gemm_kernel(GemmArgs a) {
-  static_assert(!GATHER || TB == 1, "the fused gather stages one 16-row token block");
   extern __shared__ __attribute__((aligned(16))) uint16_t staged[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int r16 = lane & 15;
   const int kq = lane >> 4;
+  const int row = r16 & 7;                  // weight row within its half / token
+  const int piece = 2 * kq + (r16 >> 3);    // 16-byte piece of the 128-byte line
   const int ksplit = static_cast<int>(a.k_split);
   const int part = wave % ksplit;
   const int64_t rb = static_cast<int64_t>(blockIdx.x) * (kSplitWaves / ksplit) + wave / ksplit;
   const int64_t row_blocks = (a.n + 15) / 16;
   const bool active = rb < row_blocks;
   const u32x4 zero = {0u, 0u, 0u, 0u};
-  const int64_t rs = a.k + 8;  // staged row stride in elements (GATHER)
-  // GATHER: rows staged in LDS, the capacity's (at most 16): rows past them are zero.
-  const int staged_rows = a.capacity < 16 ? static_cast<int>(a.capacity) : 16;
+  const int64_t rs = a.k + 16;  // staged row stride in elements (GATHER)
+  // GATHER: rows staged in LDS, the capacity's: rows past them are zero.
+  const int staged_rows = a.capacity < kSplitTokens ? static_cast<int>(a.capacity) : kSplitTokens;
 
-  f32x4 acc[TB];
-#pragma unroll
-  for (int tb = 0; tb < TB; ++tb) {
-    acc[tb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  }
+  // acc[h]: weight rows 16 rb + 8 h + [0, 8).
+  f32x4 acc[2] = {f32x4{0.0f, 0.0f, 0.0f, 0.0f}, f32x4{0.0f, 0.0f, 0.0f, 0.0f}};
 
   const int k0 = part * static_cast<int>(a.k_slice);
   // 128-wide chunks of this range (k_slice is a multiple of 128; the last range may be
@@ -252,54 +262,54 @@ __global__ __launch_bounds__(64 * kSplitWaves) void split_gemm_kernel(GemmArgs a
   const int padded = (chunks + DEPTH - 1) / DEPTH * DEPTH;
   // Columns at or past K in the last chunk read the next row (or past the end): zero both
   // operands there.
-  const int lane_valid = static_cast<int>(a.k) - k0 - kq * 8;
+  const int lane_valid = static_cast<int>(a.k) - k0 - piece * 8;
   // Row blocks start at different chunks of their range (stride-7 rotation), spreading the
   // concurrently streamed addresses over the memory channels.
   const int rotation = static_cast<int>((rb * 7) % chunks);
   const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(a.w, static_cast<uint32_t>(a.n * a.k * 2));
   const __amdgpu_buffer_rsrc_t x_rsrc = make_rsrc(a.x, static_cast<uint32_t>(a.rows * a.ldx * 2));
-  const uint32_t w_off = static_cast<uint32_t>(((rb * 16 + r16) * a.k + k0 + kq * 8) * 2);
-  uint32_t x_off[TB];
-#pragma unroll
-  for (int tb = 0; tb < TB; ++tb) {
-    x_off[tb] = static_cast<uint32_t>(((tb * 16 + r16) * a.ldx + k0 + kq * 8) * 2);
-  }
+  const uint32_t w_off = static_cast<uint32_t>(((rb * 16 + row) * a.k + k0 + piece * 8) * 2);
+  const uint32_t w_half = static_cast<uint32_t>(8 * a.k * 2);  // rows 8 .. 15 of the block
+  const uint32_t x_off = static_cast<uint32_t>((row * a.ldx + k0 + piece * 8) * 2);
   auto column_of = [&](int chunk) {
     const int c = chunk + rotation;
     return (c < chunks ? c : c - chunks) * 128;
   };
 
+  // Per chunk: w[2 line + h] = line `line` (K columns 64 line .. 64 line + 63 of the chunk)
+  // of rows 8 h + [0, 8); x[line] the matching token pieces.
   u32x4 wbuf[DEPTH][4];
-  u32x4 xbuf[DEPTH][GATHER ? 1 : TB][4];
-  auto load_chunk = [&](int chunk, u32x4 (&w)[4], u32x4 (&x)[GATHER ? 1 : TB][4]) {
+  u32x4 xbuf[DEPTH][GATHER ? 1 : 2];
+  auto load_chunk = [&](int chunk, u32x4 (&w)[4], u32x4 (&x)[GATHER ? 1 : 2]) {
     const bool in_range = chunk < chunks;
     const uint32_t column = static_cast<uint32_t>(column_of(chunk)) * 2;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      w[s] = buffer_load16(w_rsrc, in_range ? w_off + column + s * 64 : kOutOfRange);
-      if constexpr (!GATHER) {
+    for (int line = 0; line < 2; ++line) {
 #pragma unroll
-        for (int tb = 0; tb < TB; ++tb) {
-          x[tb][s] = buffer_load16(x_rsrc, in_range ? x_off[tb] + column + s * 64 : kOutOfRange);
-        }
+      for (int h = 0; h < 2; ++h) {
+        w[2 * line + h] = buffer_load16<kLoadNontemporal>(
+            w_rsrc, in_range ? w_off + h * w_half + column + line * 128 : kOutOfRange);
+      }
+      if constexpr (!GATHER) {
+        x[line] = buffer_load16(x_rsrc, in_range ? x_off + column + line * 128 : kOutOfRange);
       }
     }
   };
-  auto compute_chunk = [&](int chunk, const u32x4 (&w)[4], const u32x4 (&x)[GATHER ? 1 : TB][4]) {
+  auto compute_chunk = [&](int chunk, const u32x4 (&w)[4], const u32x4 (&x)[GATHER ? 1 : 2]) {
     const int column = chunk < chunks ? column_of(chunk) : 0;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const bool valid = column + s * 32 < lane_valid;
-      const u32x4 wk = valid ? w[s] : zero;
+    for (int line = 0; line < 2; ++line) {
+      const bool valid = column + line * 64 < lane_valid;
+      u32x4 xk;
+      if constexpr (GATHER) {
+        xk = valid && row < staged_rows ? load16(staged + row * rs + k0 + column + line * 64 + piece * 8) : zero;
+      } else {
+        xk = valid ? x[line] : zero;
+      }
 #pragma unroll
-      for (int tb = 0; tb < TB; ++tb) {
-        u32x4 xk;
-        if constexpr (GATHER) {
-          xk = valid && r16 < staged_rows ? load16(staged + r16 * rs + k0 + column + s * 32 + kq * 8) : zero;
-        } else {
-          xk = valid ? x[tb][s] : zero;
-        }
-        acc[tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(wk), as_bf16x8(xk), acc[tb], 0, 0, 0);
+      for (int h = 0; h < 2; ++h) {
+        const u32x4 wk = valid ? w[2 * line + h] : zero;
+        acc[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(wk), as_bf16x8(xk), acc[h], 0, 0, 0);
       }
     }
   };
@@ -314,8 +324,8 @@ __global__ __launch_bounds__(64 * kSplitWaves) void split_gemm_kernel(GemmArgs a
   }
   if constexpr (GATHER) {
     const int vectors = static_cast<int>(a.k / 8);
-    stage_gathered_rows<16, kSplitWaves>(a, staged, rs, 0, static_cast<int>(a.k), vectors, wave, lane,
-                                         staged_rows);
+    stage_gathered_rows<kSplitTokens, kSplitWaves>(a, staged, rs, 0, static_cast<int>(a.k), vectors, wave, lane,
+                                                   staged_rows);
     __syncthreads();
   }
   if (active) {
@@ -338,20 +348,18 @@ __global__ __launch_bounds__(64 * kSplitWaves) void split_gemm_kernel(GemmArgs a
 
   // Fixed-order sum of the K ranges of each row block: range 0's wave adds ranges
   // 1 .. KSPLIT-1 in order.
-  __shared__ f32x4 partial[kSplitWaves][TB][64];
+  __shared__ f32x4 partial[kSplitWaves][2][64];
   if (ksplit > 1) {
-#pragma unroll
-    for (int tb = 0; tb < TB; ++tb) {
-      partial[wave][tb][lane] = acc[tb];
-    }
+    partial[wave][0][lane] = acc[0];
+    partial[wave][1][lane] = acc[1];
     __syncthreads();
     if (part != 0) {
       return;
     }
 #pragma unroll
-    for (int tb = 0; tb < TB; ++tb) {
+    for (int h = 0; h < 2; ++h) {
       for (int p = 1; p < ksplit; ++p) {
-        acc[tb] += partial[wave + p][tb][lane];
+        acc[h] += partial[wave + p][h][lane];
       }
     }
   }
@@ -359,25 +367,38 @@ __global__ __launch_bounds__(64 * kSplitWaves) void split_gemm_kernel(GemmArgs a
     return;
   }
 
-  // lane holds D[4 kq + i][r16] of each token block: weight rows n .. n+3, one token.
-  const int64_t n = rb * 16 + 4 * kq;
+  // Lane (i, q) holds D[4 q + v][i], v = 0 .. 3.  The lanes with q < 2 and i < 8 add the odd
+  // pieces' block from lane + 40 (D[4 q + 8 + v][i + 8]) and then hold weight rows
+  // 16 rb + 8 h + 4 q + v for token i.
+  f32x4 sum[2];
 #pragma unroll
-  for (int tb = 0; tb < TB; ++tb) {
-    const int64_t token = tb * 16 + r16;
-    if (token >= a.rows || n >= a.n) {
-      continue;
+  for (int h = 0; h < 2; ++h) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      sum[h][v] = acc[h][v] + __shfl(acc[h][v], lane + 40, kWave);
     }
-    uint16_t *row = output_row(a, token);
-    if (row == nullptr) {
+  }
+  const int64_t token = r16;
+  if (kq >= 2 || r16 >= 8 || token >= a.rows) {
+    return;
+  }
+  uint16_t *out = output_row(a, token);
+  if (out == nullptr) {
+    return;
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int64_t n = rb * 16 + 8 * h + 4 * kq;
+    if (n >= a.n) {
       continue;
     }
     if constexpr (GATED) {
-      const float h0 = gated_silu(acc[tb][0], acc[tb][1], a.act);
-      const float h1 = gated_silu(acc[tb][2], acc[tb][3], a.act);
-      *reinterpret_cast<uint32_t *>(row + n / 2) = pack_bf16x2(h0, h1);
+      const float h0 = gated_silu(sum[h][0], sum[h][1], a.act);
+      const float h1 = gated_silu(sum[h][2], sum[h][3], a.act);
+      *reinterpret_cast<uint32_t *>(out + n / 2) = pack_bf16x2(h0, h1);
     } else {
-      u32x2 packed = {pack_bf16x2(acc[tb][0], acc[tb][1]), pack_bf16x2(acc[tb][2], acc[tb][3])};
-      *reinterpret_cast<u32x2 *>(row + n) = packed;
+      u32x2 packed = {pack_bf16x2(sum[h][0], sum[h][1]), pack_bf16x2(sum[h][2], sum[h][3])};
+      *reinterpret_cast<u32x2 *>(out + n) = packed;
     }
   }
 }
@@ -1368,7 +1389,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
 // ------------------------------------------------------------------ tables
 template <bool GATED, bool GATHER = false>
 const void *split_kernel() {
-  return reinterpret_cast<const void *>(&split_gemm_kernel<1, 4, GATED, GATHER>);
+  return reinterpret_cast<const void *>(&split_gemm_kernel<4, GATED, GATHER>);
 }
 
 template <bool GATED, bool GATHER = false>
@@ -1420,49 +1441,51 @@ const void *tile_kernel(int variant, bool stream) {
 constexpr int kComputeUnits = 256;
 
 // Decode sizes (up to 16 rows) take the split or the stream kernel, whichever a cost model
-// in microseconds prefers.  Both stream the weights with 8-wave workgroups, one per CU, at
-// a rate per workgroup (split ~24 GB/s, stream ~28 GB/s: measured, the chip rate scales
-// with the workgroup count), so a grid of few workgroups is the thing to avoid (Qwen3-4B
-// down through the split kernel has 80 workgroups: 24 us; sliced through the stream
-// kernel, 200: 15 us), and workgroups past 256 run as a second round; the chip streams at
-// most ~5.4 TB/s however many workgroups run.  The split kernel
-// reads its token fragments from L2, which costs ~0.8 us per row past the first; the
-// stream kernel's K slices cost the reduction launch and their partial traffic.
-// Fitted to forced split / stream timings of the Qwen3 0.6B / 4B / 8B / 32B-shard
-// projections at 1 to 16 rows (weights streamed from HBM): it picks the faster kernel or
-// one within 10 % of it, except two cases within 23 %.
+// in microseconds prefers.  Both stream the weights with 8-wave workgroups, each at a
+// bounded rate (measured, the chip rate scales with the workgroup count up to the CU
+// count), so a grid of few workgroups is the thing to avoid (Qwen3-4B down through the
+// split kernel with 2 K ranges per row block has 80 workgroups: 41 us; with 8, 320: 16 us),
+// workgroups past 256 run as further rounds, and the chip caps the total: ~6.4 TB/s for the
+// split kernel's whole-line nontemporal reads, ~5.4 TB/s for the stream kernel's half lines.
+// The split kernel reads its token pieces from L2, a little more per row; the stream
+// kernel's K slices cost the reduction launch and their partial traffic.  The split
+// kernel's rounds of 256 workgroups are priced one after another (each at the chip rate or
+// at one workgroup's rate, whichever is slower).  Fitted to forced split (every K split) /
+// stream timings of the Qwen3 0.6B / 4B / 8B / 32B-shard projections at 1 to 16 rows with
+// the weights streamed from HBM: mean modelled error 0.8 us, and the K split it picks is
+// within 6 % of the fastest measured one (0.6 % on average).
 constexpr int64_t kDecodeMaxRows = 16;
-constexpr int64_t kSplitMaxRows = 8;
-constexpr double kSplitWorkgroupBytesPerUs = 27.0e3;
+constexpr int64_t kSplitMaxRows = kSplitTokens;
+constexpr double kSplitWorkgroupBytesPerUs = 26.0e3;
+constexpr double kSplitBytesPerUs = 6.8e6;
+constexpr double kSplitFixedUs = 4.0;
+constexpr double kSplitRowUsPerChunk = 0.02;  // per row past the first and 128-wide chunk of a range (padded)
 constexpr double kStreamWorkgroupBytesPerUs = 28.0e3;
-constexpr double kDecodeBytesPerUs = 5.4e6;
-constexpr double kDecodeFixedUs = 2.0;
-// Token fragments per row past the first: 0.8 us at the 12 chunks per range of Qwen3-8B
-// down (fitted), scaled by the chunks a wave issues, padding included (Qwen3-0.6B gate_up at
-// 8 rows, 2 chunks per range padded to 4: a separate gather plus the split kernel, 20.0 us
-// per layer, against 22.5 us with the gather fused into the stream kernel; 8 ranges of one
-// chunk, each padded to 4, took 23.6 us).
-constexpr double kSplitRowUsPerChunk = 0.8 / 12.0;
+constexpr double kStreamBytesPerUs = 5.4e6;
+constexpr double kStreamFixedUs = 2.0;
 constexpr double kStreamReduceUs = 12.0;  // the reduction launch, fitted (it also ends the overlap of slices)
 constexpr double kStreamPartialBytesPerUs = 6.0e6;
 constexpr int kSplitDepth = 4;
 constexpr double kGatherUs = 4.0;  // a separate gather launch at decode sizes (measured 3.8-4.0 us)
-constexpr double kSplitGatherUs = 1.0;  // the split kernel's fused gather prologue, beyond its overlap
-constexpr int64_t kSplitGatherMaxK = 4096;  // 16 staged rows of K + 8 bf16 fit the LDS beside the partials
+// The split kernel's fused gather runs in every workgroup, one per CU (its registers allow
+// no second), beside only the first weight chunks: measured 2.3 us per round of 256
+// workgroups for Qwen3-0.6B gate_up (one round), 3.3 and 4.4 us for Qwen3-8B (3 and 6).
+constexpr double kSplitGatherRoundUs = 3.0;
+constexpr int64_t kSplitGatherMaxK = 4096;  // 8 staged rows of K + 16 bf16 (66 KB) beside the partial sums
 
-double decode_stream_us(int64_t n, int64_t k, int64_t workgroups, double workgroup_bytes_per_us) {
+double decode_stream_us(int64_t n, int64_t k, int64_t workgroups, double workgroup_bytes_per_us,
+                        double chip_bytes_per_us, double fixed_us) {
   const int64_t rounds = (workgroups + kComputeUnits - 1) / kComputeUnits;
   const double bytes = 2.0 * static_cast<double>(n) * static_cast<double>(k);
   const double per_workgroup = static_cast<double>(rounds) * bytes / workgroups / workgroup_bytes_per_us;
-  const double chip = bytes / kDecodeBytesPerUs;
-  return (per_workgroup > chip ? per_workgroup : chip) + kDecodeFixedUs;
+  const double chip = bytes / chip_bytes_per_us;
+  return (per_workgroup > chip ? per_workgroup : chip) + fixed_us;
 }
 
 // Candidate K splits of the split kernel (1, 2, 4 or 8 ranges per 16-row block, each range
 // a whole number of 128-wide chunks and none empty) and their modelled cost at `capacity`
-// rows.  (With ranges of whole load groups only, Qwen3-0.6B down, K = 3072, could not be
-// split more than twice: 16 workgroups, 15.8 us at one row.)
-GemmChoice choose_split(int64_t capacity, int64_t n, int64_t k, double &cost) {
+// rows, with the gather fused when `gather` is set.
+GemmChoice choose_split(int64_t capacity, int64_t n, int64_t k, double &cost, bool gather = false) {
   const int64_t quantum = 128;
   const int64_t row_blocks = (n + 15) / 16;
   GemmChoice best{GemmKind::Split, 0, 0, 1};
@@ -1473,10 +1496,20 @@ GemmChoice choose_split(int64_t capacity, int64_t n, int64_t k, double &cost) {
       break;
     }
     const int64_t workgroups = (row_blocks * ksplit + kSplitWaves - 1) / kSplitWaves;
-    const double us =
-        decode_stream_us(n, k, workgroups, kSplitWorkgroupBytesPerUs) +
-        kSplitRowUsPerChunk * static_cast<double>((slice / 128 + kSplitDepth - 1) / kSplitDepth * kSplitDepth) *
-            static_cast<double>(capacity - 1);
+    const double workgroup_bytes = 2.0 * static_cast<double>(n) * static_cast<double>(k) / workgroups;
+    double us = kSplitFixedUs;
+    for (int64_t left = workgroups; left > 0; left -= kComputeUnits) {
+      const double round_bytes = static_cast<double>(left < kComputeUnits ? left : kComputeUnits) * workgroup_bytes;
+      const double chip_us = round_bytes / kSplitBytesPerUs;
+      const double workgroup_us = workgroup_bytes / kSplitWorkgroupBytesPerUs;
+      us += chip_us > workgroup_us ? chip_us : workgroup_us;
+    }
+    us += kSplitRowUsPerChunk *
+                    static_cast<double>((slice / 128 + kSplitDepth - 1) / kSplitDepth * kSplitDepth) *
+                    static_cast<double>(capacity - 1);
+    if (gather) {
+      us += kSplitGatherRoundUs * static_cast<double>((workgroups + kComputeUnits - 1) / kComputeUnits);
+    }
     if (cost < 0.0 || us < cost) {
       best = {GemmKind::Split, 0, slice, ksplit};
       cost = us;
@@ -1503,7 +1536,7 @@ GemmChoice choose_stream(int64_t capacity, int64_t n, int64_t k, double &cost) {
     if (tp * (k_slice + 8) * 2 > kStreamLdsBytes || stream_slices(k, k_slice) != slices) {
       continue;  // does not fit LDS, or the same slice length as fewer slices
     }
-    double us = decode_stream_us(n, k, slices * groups, kStreamWorkgroupBytesPerUs);
+    double us = decode_stream_us(n, k, slices * groups, kStreamWorkgroupBytesPerUs, kStreamBytesPerUs, kStreamFixedUs);
     if (slices > 1) {
       us += kStreamReduceUs + 8.0 * static_cast<double>(slices * capacity * n) / kStreamPartialBytesPerUs;
     }
@@ -1599,7 +1632,8 @@ GemmChoice choose_gemm(int64_t capacity, int64_t n, int64_t k, bool gated) {
 // slices of Qwen3-8B gate_up took 47 + 5 us against 38 us for one).  Up to kSplitMaxRows
 // rows the split kernel can fuse the gather as well: each workgroup stages the rows' whole
 // K (at most kSplitGatherMaxK columns) while its first weight chunks are in flight, which
-// the model prices at kSplitGatherUs over the plain split kernel.
+// the model prices at kSplitGatherRoundUs per round of workgroups over the plain split
+// kernel.
 GemmChoice choose_dense_gate_up(int64_t capacity, int64_t n, int64_t k, bool &fused) {
   fused = capacity <= kDecodeMaxRows && n * k * 2 <= INT32_MAX;
   if (!fused) {
@@ -1619,7 +1653,7 @@ GemmChoice choose_dense_gate_up(int64_t capacity, int64_t n, int64_t k, bool &fu
   // more workgroups (Qwen3-0.6B gate_up at one row: 48 fused workgroups, 13.6 us).
   const int64_t groups = ((n + 15) / 16 + kStreamWaves - 1) / kStreamWaves;
   const int64_t slices = stream_slices(k, fused_choice.k_slice);
-  double fused_us = decode_stream_us(n, k, slices * groups, kStreamWorkgroupBytesPerUs);
+  double fused_us = decode_stream_us(n, k, slices * groups, kStreamWorkgroupBytesPerUs, kStreamBytesPerUs, kStreamFixedUs);
   if (slices > 1) {
     fused_us += kStreamReduceUs + 8.0 * static_cast<double>(slices * capacity * n) / kStreamPartialBytesPerUs;
   }
@@ -1627,8 +1661,8 @@ GemmChoice choose_dense_gate_up(int64_t capacity, int64_t n, int64_t k, bool &fu
   const GemmChoice separate = choose_decode(capacity, n, k, separate_us);
   if (capacity <= kSplitMaxRows && k <= kSplitGatherMaxK) {
     double split_us = 0.0;
-    const GemmChoice split = choose_split(capacity, n, k, split_us);
-    if (split_us + kSplitGatherUs < fused_us && split_us + kSplitGatherUs <= kGatherUs + separate_us) {
+    const GemmChoice split = choose_split(capacity, n, k, split_us, true);
+    if (split_us < fused_us && split_us <= kGatherUs + separate_us) {
       return split;  // fused into the split kernel
     }
   }
@@ -1703,6 +1737,7 @@ GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmCho
   record.k_slice = choice.k_slice;
   record.k_split = choice.k_split;
   if (choice.kind == GemmKind::Split) {
+    // choose_split is only consulted up to kSplitMaxRows (= kSplitTokens) rows.
     const int64_t row_blocks = (args.n + 15) / 16;
     const int64_t per_group = kSplitWaves / choice.k_split;
     const bool gather = fused_gather && gated;
@@ -1710,7 +1745,8 @@ GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmCho
     kernel.grid = dim3(static_cast<unsigned>((row_blocks + per_group - 1) / per_group), 1, 1);
     kernel.block = dim3(64 * kSplitWaves, 1, 1);
     // Dynamic LDS beyond 64 KB: launch() opts the function in (enable_large_lds).
-    kernel.shmem = gather ? static_cast<unsigned>((capacity < 16 ? capacity : 16) * (args.k + 8) * 2) : 0u;
+    kernel.shmem = gather ? static_cast<unsigned>((capacity < kSplitTokens ? capacity : kSplitTokens) * (args.k + 16) * 2)
+                          : 0u;
   } else if (choice.kind == GemmKind::Stream) {
     const int64_t groups = ((args.n + 15) / 16 + kStreamWaves - 1) / kStreamWaves;
     const int64_t slices = stream_slices(args.k, choice.k_slice);
@@ -1808,7 +1844,7 @@ KernelLaunch make_grouped_split(const GemmArgs &args, bool gated, int max_tiles,
 std::string gemm_name(GemmChoice choice, bool gated) {
   const std::string prefix = gated ? "_gated" : "";
   if (choice.kind == GemmKind::Split) {
-    return "split" + prefix + "_t16_k" + std::to_string(choice.k_split);
+    return "split" + prefix + "_t8_k" + std::to_string(choice.k_split);
   }
   if (choice.kind == GemmKind::Stream) {
     return "stream" + prefix + "_t16";

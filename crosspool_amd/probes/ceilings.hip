@@ -9,10 +9,11 @@
 //    consecutive bytes, UNROLL loads in flight per lane: the HBM read rate of the plainest
 //    streaming pattern, with plain loads or with the nontemporal hint (`nt`), which the
 //    tile kernels use for weights they read once.
-//  * probe_read_rows: the weight-streaming pattern of the decode projection kernels: a wave
-//    owns 16 rows of a row-major matrix and reads 16 rows x 64 contiguous bytes per
-//    instruction, four 256-byte chunks per row in flight; grid y splits each row into
-//    `ranges` contiguous parts (more workgroups for the same bytes).
+//  * probe_read_rows: weight-streaming patterns of the decode projection kernels: a wave
+//    owns 16 rows of a row-major matrix and reads 16 rows x 64 contiguous bytes (half
+//    lines) or 8 rows x 128 bytes (whole lines) per instruction, 16 KB per wave in flight;
+//    grid y splits each row into `ranges` contiguous parts (more workgroups for the same
+//    bytes).
 //
 // Each kernel folds what it reads (or computes) into registers and stores it only when
 // `write` is set, which the host never does; the compiler cannot drop the work.
@@ -92,7 +93,11 @@ __global__ __launch_bounds__(256) void probe_read_contiguous_kernel(const u32x4 
 }
 
 // 8 waves per workgroup, wave w of workgroup x owns row block 8 x + w (16 rows); grid y is
-// the part of each row (row_bytes / ranges bytes, a multiple of 1 KB).
+// the part of each row (row_bytes / ranges bytes, a multiple of 1 KB).  LINES false: each
+// instruction reads 16 rows x 64 contiguous bytes (the two halves of a 128-byte line in
+// consecutive instructions).  LINES true: each instruction reads 8 rows x 128 bytes (lane
+// l: row l & 7, 16-byte piece (l >> 4) + 4 ((l >> 3) & 1) of the line), whole lines.
+template <bool LINES, bool NONTEMPORAL>
 __global__ __launch_bounds__(512) void probe_read_rows_kernel(const char *matrix, int64_t rows, int64_t row_bytes,
                                                               int64_t part_bytes, uint32_t *sink, int write) {
   const int lane = threadIdx.x & 63;
@@ -101,7 +106,9 @@ __global__ __launch_bounds__(512) void probe_read_rows_kernel(const char *matrix
   if (block * 16 >= rows) {
     return;
   }
-  const char *row = matrix + (block * 16 + (lane & 15)) * row_bytes + blockIdx.y * part_bytes + (lane >> 4) * 16;
+  const int row_in_block = LINES ? (lane & 7) : (lane & 15);
+  const int piece_bytes = LINES ? 16 * ((lane >> 4) + 4 * ((lane >> 3) & 1)) : 16 * (lane >> 4);
+  const char *row = matrix + (block * 16 + row_in_block) * row_bytes + blockIdx.y * part_bytes + piece_bytes;
   u32x4 folded = {0u, 0u, 0u, 0u};
   for (int64_t column = 0; column < part_bytes; column += 1024) {
     u32x4 values[16];
@@ -109,8 +116,15 @@ __global__ __launch_bounds__(512) void probe_read_rows_kernel(const char *matrix
     for (int chunk = 0; chunk < 4; ++chunk) {
 #pragma unroll
       for (int piece = 0; piece < 4; ++piece) {
-        values[chunk * 4 + piece] =
-            *reinterpret_cast<const u32x4 *>(row + column + chunk * 256 + piece * 64);
+        // LINES: line 2 chunk + (piece >> 1) of rows 8 (piece & 1) + [0, 8).
+        const int64_t offset = LINES ? (piece & 1) * 8 * row_bytes + chunk * 256 + (piece >> 1) * 128
+                                     : chunk * 256 + piece * 64;
+        const u32x4 *address = reinterpret_cast<const u32x4 *>(row + column + offset);
+        if constexpr (NONTEMPORAL) {
+          values[chunk * 4 + piece] = __builtin_nontemporal_load(address);
+        } else {
+          values[chunk * 4 + piece] = *address;
+        }
       }
     }
 #pragma unroll
@@ -150,15 +164,20 @@ int xp_probe_read_contiguous(const void *source, uint64_t bytes, int workgroups,
 }
 
 // Reads a [rows, row_bytes] matrix (rows a multiple of 16, row_bytes a multiple of
-// 1024 * ranges) in the weight-streaming pattern.
-int xp_probe_read_rows(const void *matrix, int64_t rows, int64_t row_bytes, int ranges, void *stream) {
-  if (rows % 16 != 0 || ranges < 1 || row_bytes % (1024 * static_cast<int64_t>(ranges)) != 0) {
+// 1024 * ranges) in a weight-streaming pattern: 0 half lines, 1 whole lines, 2 whole lines
+// with the nontemporal hint, 3 half lines with the nontemporal hint.
+int xp_probe_read_rows(const void *matrix, int64_t rows, int64_t row_bytes, int ranges, int pattern, void *stream) {
+  if (rows % 16 != 0 || ranges < 1 || row_bytes % (1024 * static_cast<int64_t>(ranges)) != 0 || pattern < 0 ||
+      pattern > 3) {
     return -1;
   }
   const dim3 grid(static_cast<unsigned>((rows / 16 + 7) / 8), static_cast<unsigned>(ranges));
-  hipLaunchKernelGGL(probe_read_rows_kernel, grid, dim3(512), 0, static_cast<hipStream_t>(stream),
-                     static_cast<const char *>(matrix), rows, row_bytes, row_bytes / ranges,
-                     static_cast<uint32_t *>(nullptr), 0);
+  auto kernel = pattern == 0   ? probe_read_rows_kernel<false, false>
+                : pattern == 1 ? probe_read_rows_kernel<true, false>
+                : pattern == 2 ? probe_read_rows_kernel<true, true>
+                               : probe_read_rows_kernel<false, true>;
+  hipLaunchKernelGGL(kernel, grid, dim3(512), 0, static_cast<hipStream_t>(stream), static_cast<const char *>(matrix),
+                     rows, row_bytes, row_bytes / ranges, static_cast<uint32_t *>(nullptr), 0);
   return static_cast<int>(hipGetLastError());
 }
 

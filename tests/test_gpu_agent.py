@@ -110,14 +110,14 @@ def test_config3_qwen3_8b_layer(device, rows):
     "hidden,intermediate,rows,variant",
     [
         (4096, 12288, 16, "stream_gated_t16+gather"),
-        (1024, 3072, 1, "split_gated_t16_k4+gather"),
-        (1024, 3072, 8, "split_gated_t16_k4+gather"),
-        (2048, 6144, 5, "split_gated_t16_k8+gather"),
+        (1024, 3072, 1, "split_gated_t8_k4+gather"),
+        (1024, 3072, 8, "split_gated_t8_k4+gather"),
+        (2048, 2048, 5, "split_gated_t8_k8+gather"),
     ],
 )
 def test_fused_gather_matches_separate_kernels_bitwise(device, normed, hidden, intermediate, rows, variant):
     # At decode sizes the gather (+ RMSNorm) runs inside gate_up: the stream kernel (Qwen3-8B,
-    # 16 rows) or the split kernel (Qwen3-0.6B / 1.7B shapes, up to 8 rows), which stage the
+    # 16 rows) or the split kernel (hidden sizes up to 4096, up to 8 rows), which stage the
     # same bits the gather kernel writes.  The kernel-level projections take the same kernels
     # with the same K ranges, so the step must equal gather kernel -> gate_up -> down ->
     # scatter bit for bit.

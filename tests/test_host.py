@@ -297,12 +297,12 @@ def test_gemm_variant_selection():
     for rows in (1, 2, 4, 8, 16):
         for n, k, gated in ((24576, 4096, True), (4096, 12288, False), (19456, 2560, True), (2560, 9728, False)):
             assert _native.gemm_variant(rows, n, k, gated).startswith(("split", "stream"))
-    assert _native.gemm_variant(1, 4096, 12288, False) == "split_t16_k8"
+    assert _native.gemm_variant(1, 4096, 12288, False) == "split_t8_k8"
     assert _native.gemm_variant(16, 24576, 4096, True) == "stream_gated_t16"
     # Qwen3-4B and Qwen3-0.6B down: K ranges of whole 128-wide chunks let the split kernel
     # take 8 ranges (160 and 64 workgroups), with no scratch
-    assert _native.gemm_variant(1, 2560, 9728, False) == "split_t16_k8"
-    assert _native.gemm_variant(1, 1024, 3072, False) == "split_t16_k8"
+    assert _native.gemm_variant(1, 2560, 9728, False) == "split_t8_k8"
+    assert _native.gemm_variant(1, 1024, 3072, False) == "split_t8_k8"
     assert _native.gemm_workspace_bytes(1, 2560, 9728, False) == 0
     assert _native.gemm_variant(17, 24576, 4096, True) == "tile_gated_64x64"
     assert _native.gemm_variant(128, 6144, 1024, True) == "tile_gated_64x64"  # 96 tiles of 64 x 128
@@ -317,11 +317,13 @@ def test_gemm_variant_selection():
 
 def test_dense_step_fuses_the_gather_at_decode_sizes():
     # Qwen3-0.6B / 1.7B gate_up up to 8 rows: the split kernel stages the gathered, normalised
-    # rows itself; Qwen3-8B: the stream kernel; K past 4096 (the 32B TP shard's 5120) does
-    # not fit the split kernel's staging, and past 16 rows the gather is a launch of its own.
+    # rows itself (one round of workgroups).  Qwen3-8B up to 8 rows: a gather launch, then the
+    # split kernel with 8 K ranges (six rounds of workgroups, each of which would repeat a
+    # fused gather).  K past 4096 (the 32B TP shard's 5120) does not fit the split kernel's
+    # staging, and past 16 rows the gather is a launch of its own.
     for rows in (1, 4, 8):
-        assert _native.dense_gate_up_variant(rows, 1024, 3072) == "split_gated_t16_k4+gather"
-        assert _native.dense_gate_up_variant(rows, 4096, 12288) == "stream_gated_t16+gather"
+        assert _native.dense_gate_up_variant(rows, 1024, 3072) == "split_gated_t8_k4+gather"
+        assert _native.dense_gate_up_variant(rows, 4096, 12288) == "split_gated_t8_k8"
         assert "+gather" not in _native.dense_gate_up_variant(rows, 5120, 3200)
     assert _native.dense_gate_up_variant(16, 4096, 12288) == "stream_gated_t16+gather"
     assert _native.dense_gate_up_variant(32, 4096, 12288) == "tile_gated_64x64"
