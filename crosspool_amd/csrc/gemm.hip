@@ -203,11 +203,11 @@ __device__ __forceinline__ void stage_gathered_rows(const GemmArgs &a, uint16_t 
 }
 
 // ------------------------------------------------------------------ split (decode)
-// Weight-streaming projection for at most 8 live rows (HBM-bound).  A workgroup of 8 waves
-// covers 8 / KSPLIT weight-row blocks of 16 rows; the KSPLIT waves of a block each stream
-// one contiguous K range of `k_slice` columns, 128-wide K chunks with DEPTH chunks of loads
-// in flight, multiplied on v_mfma_f32_16x16x32_bf16 with the weights as the M operand.  The
-// K ranges of a row block are summed through LDS in a fixed order (deterministic), all
+// Weight-streaming projection for at most 16 live rows (HBM-bound).  A workgroup of 8
+// waves covers 8 / KSPLIT weight-row blocks of 16 rows; the KSPLIT waves of a block each
+// stream one contiguous K range of `k_slice` columns, 128-wide K chunks with DEPTH chunks of
+// loads in flight, multiplied on v_mfma_f32_16x16x32_bf16 with the weights as the M operand.
+// The K ranges of a row block are summed through LDS in a fixed order (deterministic), all
 // within the workgroup, so no partial sums leave the chip.
 //
 // Each weight load instruction reads whole 128-byte lines, 8 rows x 128 bytes, with the
@@ -216,29 +216,32 @@ __device__ __forceinline__ void stage_gathered_rows(const GemmArgs &a, uint16_t 
 // (i, q) = (lane & 15, lane >> 4) loads row i & 7 of the half, 16-byte piece p = 2 q + (i >> 3)
 // of the line (K columns 8 p .. 8 p + 7).  As an MFMA operand, operand row i then holds the
 // even pieces of weight row i (i < 8) or the odd pieces of weight row i - 8, and the token
-// operand is laid out the same way: column j holds token j & 7 at piece 2 q + (j >> 3).
-// Products pair matching pieces only in the diagonal blocks, D[r][t] (even pieces) and
-// D[r + 8][t + 8] (odd pieces) for r, t < 8, whose sum is the full dot product of weight
-// row r with token t; the off-diagonal blocks are discarded.  Half the MFMA work is thus
-// wasted, which the decode sizes leave idle anyway (one 16x16x32 per KB of weights).
-// Token pieces come from L2 (rows past the live rows cost no memory access).
+// operand of token group g (tokens 8 g .. 8 g + 7) is laid out the same way: column j holds
+// token 8 g + (j & 7) at piece 2 q + (j >> 3).  Products pair matching pieces only in the
+// diagonal blocks, D[r][t] (even pieces) and D[r + 8][t + 8] (odd pieces) for r, t < 8,
+// whose sum is the full dot product of weight row r with token 8 g + t; the off-diagonal
+// blocks are discarded.  Half the MFMA work is thus wasted, which the decode sizes leave
+// idle anyway (TG 16x16x32 per KB of weights).  Token pieces come from L2 (rows past the
+// live rows cost no memory access).
 constexpr int kSplitWaves = 8;
-constexpr int kSplitTokens = 8;
+constexpr int kSplitGroupTokens = 8;
+constexpr int kSplitMaxGroups = 2;
 
-// GATHER (K <= 4096): the token rows are the mailbox rows gather_slots[t] of a.x,
-// RMS-normalised with a.norm when that is set, staged once per workgroup into LDS
+// GATHER (one token group, K <= 4096): the token rows are the mailbox rows gather_slots[t]
+// of a.x, RMS-normalised with a.norm when that is set, staged once per workgroup into LDS
 // (stage_gathered_rows, the gather kernel's bits) while the first DEPTH chunks of weights
 // are in flight; the token pieces are then read from LDS instead of L2.  Dynamic LDS:
-// min(capacity, 8) x (K + 16) bf16, so that at one or a few rows several workgroups share a
-// CU (the 32-byte row padding puts the 16 pieces of one read in distinct bank slots).
-template <int DEPTH, bool GATED, bool GATHER = false>
+// min(capacity, 8) x (K + 16) bf16 (the 32-byte row padding puts the 16 pieces of one read
+// in distinct bank slots).
+template <int DEPTH, int TG, bool GATED, bool GATHER = false>
 __global__ __launch_bounds__(64 * kSplitWaves) void split_gemm_kernel(GemmArgs a) {
+  static_assert(!GATHER || TG == 1, "the fused gather stages one token group");
   extern __shared__ __attribute__((aligned(16))) uint16_t staged[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int r16 = lane & 15;
   const int kq = lane >> 4;
-  const int row = r16 & 7;                  // weight row within its half / token
+  const int row = r16 & 7;                  // weight row within its half / token within its group
   const int piece = 2 * kq + (r16 >> 3);    // 16-byte piece of the 128-byte line
   const int ksplit = static_cast<int>(a.k_split);
   const int part = wave % ksplit;
@@ -248,10 +251,15 @@ __global__ __launch_bounds__(64 * kSplitWaves) void split_gemm_kernel(GemmArgs a
   const u32x4 zero = {0u, 0u, 0u, 0u};
   const int64_t rs = a.k + 16;  // staged row stride in elements (GATHER)
   // GATHER: rows staged in LDS, the capacity's: rows past them are zero.
-  const int staged_rows = a.capacity < kSplitTokens ? static_cast<int>(a.capacity) : kSplitTokens;
+  const int staged_rows = a.capacity < kSplitGroupTokens ? static_cast<int>(a.capacity) : kSplitGroupTokens;
 
-  // acc[h]: weight rows 16 rb + 8 h + [0, 8).
-  f32x4 acc[2] = {f32x4{0.0f, 0.0f, 0.0f, 0.0f}, f32x4{0.0f, 0.0f, 0.0f, 0.0f}};
+  // acc[g][h]: token group g, weight rows 16 rb + 8 h + [0, 8).
+  f32x4 acc[TG][2];
+#pragma unroll
+  for (int g = 0; g < TG; ++g) {
+    acc[g][0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    acc[g][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
 
   const int k0 = part * static_cast<int>(a.k_slice);
   // 128-wide chunks of this range (k_slice is a multiple of 128; the last range may be
@@ -271,16 +279,18 @@ __global__ __launch_bounds__(64 * kSplitWaves) void split_gemm_kernel(GemmArgs a
   const uint32_t w_off = static_cast<uint32_t>(((rb * 16 + row) * a.k + k0 + piece * 8) * 2);
   const uint32_t w_half = static_cast<uint32_t>(8 * a.k * 2);  // rows 8 .. 15 of the block
   const uint32_t x_off = static_cast<uint32_t>((row * a.ldx + k0 + piece * 8) * 2);
+  const uint32_t x_group = static_cast<uint32_t>(kSplitGroupTokens * a.ldx * 2);
   auto column_of = [&](int chunk) {
     const int c = chunk + rotation;
     return (c < chunks ? c : c - chunks) * 128;
   };
 
   // Per chunk: w[2 line + h] = line `line` (K columns 64 line .. 64 line + 63 of the chunk)
-  // of rows 8 h + [0, 8); x[line] the matching token pieces.
+  // of rows 8 h + [0, 8); x[line][g] the matching pieces of token group g.
+  constexpr int XG = GATHER ? 0 : TG;
   u32x4 wbuf[DEPTH][4];
-  u32x4 xbuf[DEPTH][GATHER ? 1 : 2];
-  auto load_chunk = [&](int chunk, u32x4 (&w)[4], u32x4 (&x)[GATHER ? 1 : 2]) {
+  u32x4 xbuf[DEPTH][2][XG > 0 ? XG : 1];
+  auto load_chunk = [&](int chunk, u32x4 (&w)[4], u32x4 (&x)[2][XG > 0 ? XG : 1]) {
     const bool in_range = chunk < chunks;
     const uint32_t column = static_cast<uint32_t>(column_of(chunk)) * 2;
 #pragma unroll
@@ -290,26 +300,29 @@ __global__ __launch_bounds__(64 * kSplitWaves) void split_gemm_kernel(GemmArgs a
         w[2 * line + h] = buffer_load16<kLoadNontemporal>(
             w_rsrc, in_range ? w_off + h * w_half + column + line * 128 : kOutOfRange);
       }
-      if constexpr (!GATHER) {
-        x[line] = buffer_load16(x_rsrc, in_range ? x_off + column + line * 128 : kOutOfRange);
+#pragma unroll
+      for (int g = 0; g < XG; ++g) {
+        x[line][g] = buffer_load16(x_rsrc, in_range ? x_off + g * x_group + column + line * 128 : kOutOfRange);
       }
     }
   };
-  auto compute_chunk = [&](int chunk, const u32x4 (&w)[4], const u32x4 (&x)[GATHER ? 1 : 2]) {
+  auto compute_chunk = [&](int chunk, const u32x4 (&w)[4], const u32x4 (&x)[2][XG > 0 ? XG : 1]) {
     const int column = chunk < chunks ? column_of(chunk) : 0;
 #pragma unroll
     for (int line = 0; line < 2; ++line) {
       const bool valid = column + line * 64 < lane_valid;
-      u32x4 xk;
-      if constexpr (GATHER) {
-        xk = valid && row < staged_rows ? load16(staged + row * rs + k0 + column + line * 64 + piece * 8) : zero;
-      } else {
-        xk = valid ? x[line] : zero;
-      }
+      const u32x4 w0 = valid ? w[2 * line] : zero;
+      const u32x4 w1 = valid ? w[2 * line + 1] : zero;
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const u32x4 wk = valid ? w[2 * line + h] : zero;
-        acc[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(wk), as_bf16x8(xk), acc[h], 0, 0, 0);
+      for (int g = 0; g < TG; ++g) {
+        u32x4 xk;
+        if constexpr (GATHER) {
+          xk = valid && row < staged_rows ? load16(staged + row * rs + k0 + column + line * 64 + piece * 8) : zero;
+        } else {
+          xk = valid ? x[line][g] : zero;
+        }
+        acc[g][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(w0), as_bf16x8(xk), acc[g][0], 0, 0, 0);
+        acc[g][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(w1), as_bf16x8(xk), acc[g][1], 0, 0, 0);
       }
     }
   };
@@ -324,8 +337,8 @@ __global__ __launch_bounds__(64 * kSplitWaves) void split_gemm_kernel(GemmArgs a
   }
   if constexpr (GATHER) {
     const int vectors = static_cast<int>(a.k / 8);
-    stage_gathered_rows<kSplitTokens, kSplitWaves>(a, staged, rs, 0, static_cast<int>(a.k), vectors, wave, lane,
-                                                   staged_rows);
+    stage_gathered_rows<kSplitGroupTokens, kSplitWaves>(a, staged, rs, 0, static_cast<int>(a.k), vectors, wave,
+                                                        lane, staged_rows);
     __syncthreads();
   }
   if (active) {
@@ -348,18 +361,24 @@ __global__ __launch_bounds__(64 * kSplitWaves) void split_gemm_kernel(GemmArgs a
 
   // Fixed-order sum of the K ranges of each row block: range 0's wave adds ranges
   // 1 .. KSPLIT-1 in order.
-  __shared__ f32x4 partial[kSplitWaves][2][64];
+  __shared__ f32x4 partial[kSplitWaves][TG][2][64];
   if (ksplit > 1) {
-    partial[wave][0][lane] = acc[0];
-    partial[wave][1][lane] = acc[1];
+#pragma unroll
+    for (int g = 0; g < TG; ++g) {
+      partial[wave][g][0][lane] = acc[g][0];
+      partial[wave][g][1][lane] = acc[g][1];
+    }
     __syncthreads();
     if (part != 0) {
       return;
     }
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      for (int p = 1; p < ksplit; ++p) {
-        acc[h] += partial[wave + p][h][lane];
+    for (int g = 0; g < TG; ++g) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        for (int p = 1; p < ksplit; ++p) {
+          acc[g][h] += partial[wave + p][g][h][lane];
+        }
       }
     }
   }
@@ -369,36 +388,45 @@ __global__ __launch_bounds__(64 * kSplitWaves) void split_gemm_kernel(GemmArgs a
 
   // Lane (i, q) holds D[4 q + v][i], v = 0 .. 3.  The lanes with q < 2 and i < 8 add the odd
   // pieces' block from lane + 40 (D[4 q + 8 + v][i + 8]) and then hold weight rows
-  // 16 rb + 8 h + 4 q + v for token i.
-  f32x4 sum[2];
+  // 16 rb + 8 h + 4 q + v for token 8 g + i.
+  f32x4 sum[TG][2];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
+  for (int g = 0; g < TG; ++g) {
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      sum[h][v] = acc[h][v] + __shfl(acc[h][v], lane + 40, kWave);
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        sum[g][h][v] = acc[g][h][v] + __shfl(acc[g][h][v], lane + 40, kWave);
+      }
     }
   }
-  const int64_t token = r16;
-  if (kq >= 2 || r16 >= 8 || token >= a.rows) {
-    return;
-  }
-  uint16_t *out = output_row(a, token);
-  if (out == nullptr) {
+  if (kq >= 2 || r16 >= 8) {
     return;
   }
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int64_t n = rb * 16 + 8 * h + 4 * kq;
-    if (n >= a.n) {
+  for (int g = 0; g < TG; ++g) {
+    const int64_t token = kSplitGroupTokens * g + r16;
+    if (token >= a.rows) {
       continue;
     }
-    if constexpr (GATED) {
-      const float h0 = gated_silu(sum[h][0], sum[h][1], a.act);
-      const float h1 = gated_silu(sum[h][2], sum[h][3], a.act);
-      *reinterpret_cast<uint32_t *>(out + n / 2) = pack_bf16x2(h0, h1);
-    } else {
-      u32x2 packed = {pack_bf16x2(sum[h][0], sum[h][1]), pack_bf16x2(sum[h][2], sum[h][3])};
-      *reinterpret_cast<u32x2 *>(out + n) = packed;
+    uint16_t *out = output_row(a, token);
+    if (out == nullptr) {
+      continue;
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int64_t n = rb * 16 + 8 * h + 4 * kq;
+      if (n >= a.n) {
+        continue;
+      }
+      if constexpr (GATED) {
+        const float h0 = gated_silu(sum[g][h][0], sum[g][h][1], a.act);
+        const float h1 = gated_silu(sum[g][h][2], sum[g][h][3], a.act);
+        *reinterpret_cast<uint32_t *>(out + n / 2) = pack_bf16x2(h0, h1);
+      } else {
+        u32x2 packed = {pack_bf16x2(sum[g][h][0], sum[g][h][1]), pack_bf16x2(sum[g][h][2], sum[g][h][3])};
+        *reinterpret_cast<u32x2 *>(out + n) = packed;
+      }
     }
   }
 }
@@ -1387,10 +1415,24 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
 }
 
 // ------------------------------------------------------------------ tables
-template <bool GATED, bool GATHER = false>
-const void *split_kernel() {
-  return reinterpret_cast<const void *>(&split_gemm_kernel<4, GATED, GATHER>);
+// Chunks of loads in flight per wave of the split kernel, by token groups (the register
+// budget of two workgroups per CU).
+constexpr int split_depth(int groups) { return groups == 1 ? 4 : 3; }
+
+// The split kernel for `groups` token groups of 8 (1 or 2); the fused gather takes one.
+// (Four groups, 32 tokens, were measured and dropped: the token pieces read from L2 for each
+// weight line then cost more than the tile kernels, 60-77 us against 41-43 us for Qwen3-8B
+// gate_up at 17-32 rows.)
+template <bool GATED>
+const void *split_kernel(int groups, bool gather) {
+  if (gather) {
+    return reinterpret_cast<const void *>(&split_gemm_kernel<split_depth(1), 1, GATED, GATED>);
+  }
+  return groups == 1 ? reinterpret_cast<const void *>(&split_gemm_kernel<split_depth(1), 1, GATED>)
+                     : reinterpret_cast<const void *>(&split_gemm_kernel<split_depth(2), 2, GATED>);
 }
+
+int split_groups(int64_t capacity) { return capacity <= kSplitGroupTokens ? 1 : 2; }
 
 template <bool GATED, bool GATHER = false>
 const void *stream_kernel() {
@@ -1455,10 +1497,13 @@ constexpr int kComputeUnits = 256;
 // the weights streamed from HBM: mean modelled error 0.8 us, and the K split it picks is
 // within 6 % of the fastest measured one (0.6 % on average).
 constexpr int64_t kDecodeMaxRows = 16;
-constexpr int64_t kSplitMaxRows = kSplitTokens;
-constexpr double kSplitWorkgroupBytesPerUs = 26.0e3;
-constexpr double kSplitBytesPerUs = 6.8e6;
-constexpr double kSplitFixedUs = 4.0;
+constexpr int64_t kSplitMaxRows = kSplitGroupTokens * kSplitMaxGroups;
+// Index: token groups - 1.  Two groups read twice the token pieces from L2 per weight line,
+// which lowers the chip rate (Qwen3-8B gate_up at 9-16 rows: 43-53 us, against 40-42 us for
+// the stream kernel; Qwen3-0.6B gate_up: 7.9-8.5 us against 11.0 us).
+constexpr double kSplitWorkgroupBytesPerUs[kSplitMaxGroups] = {26.0e3, 20.0e3};
+constexpr double kSplitBytesPerUs[kSplitMaxGroups] = {6.8e6, 5.2e6};
+constexpr double kSplitFixedUs[kSplitMaxGroups] = {4.0, 3.0};
 constexpr double kSplitRowUsPerChunk = 0.02;  // per row past the first and 128-wide chunk of a range (padded)
 constexpr double kStreamWorkgroupBytesPerUs = 28.0e3;
 constexpr double kStreamBytesPerUs = 5.4e6;
@@ -1488,7 +1533,9 @@ double decode_stream_us(int64_t n, int64_t k, int64_t workgroups, double workgro
 GemmChoice choose_split(int64_t capacity, int64_t n, int64_t k, double &cost, bool gather = false) {
   const int64_t quantum = 128;
   const int64_t row_blocks = (n + 15) / 16;
-  GemmChoice best{GemmKind::Split, 0, 0, 1};
+  const int groups = split_groups(capacity);
+  const int64_t depth = split_depth(groups);
+  GemmChoice best{GemmKind::Split, groups, 0, 1};
   cost = -1.0;
   for (int64_t ksplit = 1; ksplit <= kSplitWaves; ksplit *= 2) {
     const int64_t slice = ((k + ksplit - 1) / ksplit + quantum - 1) / quantum * quantum;
@@ -1497,21 +1544,21 @@ GemmChoice choose_split(int64_t capacity, int64_t n, int64_t k, double &cost, bo
     }
     const int64_t workgroups = (row_blocks * ksplit + kSplitWaves - 1) / kSplitWaves;
     const double workgroup_bytes = 2.0 * static_cast<double>(n) * static_cast<double>(k) / workgroups;
-    double us = kSplitFixedUs;
+    double us = kSplitFixedUs[groups - 1];
     for (int64_t left = workgroups; left > 0; left -= kComputeUnits) {
       const double round_bytes = static_cast<double>(left < kComputeUnits ? left : kComputeUnits) * workgroup_bytes;
-      const double chip_us = round_bytes / kSplitBytesPerUs;
-      const double workgroup_us = workgroup_bytes / kSplitWorkgroupBytesPerUs;
+      const double chip_us = round_bytes / kSplitBytesPerUs[groups - 1];
+      const double workgroup_us = workgroup_bytes / kSplitWorkgroupBytesPerUs[groups - 1];
       us += chip_us > workgroup_us ? chip_us : workgroup_us;
     }
     us += kSplitRowUsPerChunk *
-                    static_cast<double>((slice / 128 + kSplitDepth - 1) / kSplitDepth * kSplitDepth) *
+                    static_cast<double>((slice / 128 + depth - 1) / depth * depth) *
                     static_cast<double>(capacity - 1);
     if (gather) {
       us += kSplitGatherRoundUs * static_cast<double>((workgroups + kComputeUnits - 1) / kComputeUnits);
     }
     if (cost < 0.0 || us < cost) {
-      best = {GemmKind::Split, 0, slice, ksplit};
+      best = {GemmKind::Split, groups, slice, ksplit};
       cost = us;
     }
   }
@@ -1596,16 +1643,16 @@ GemmChoice choose_tile(int64_t capacity, int64_t n, int64_t k) {
 // The split or the stream kernel for a decode size, whichever the cost model prefers, and
 // its modelled cost in microseconds.
 GemmChoice choose_decode(int64_t capacity, int64_t n, int64_t k, double &cost) {
-  const GemmChoice stream = choose_stream(capacity, n, k, cost);
-  if (capacity <= kSplitMaxRows) {
-    double split_us = 0.0;
-    const GemmChoice split = choose_split(capacity, n, k, split_us);
-    if (split_us < cost) {
-      cost = split_us;
-      return split;
+  const GemmChoice split = choose_split(capacity, n, k, cost);
+  if (capacity <= kDecodeMaxRows) {
+    double stream_us = 0.0;
+    const GemmChoice stream = choose_stream(capacity, n, k, stream_us);
+    if (stream_us < cost) {
+      cost = stream_us;
+      return stream;
     }
   }
-  return stream;
+  return split;
 }
 
 GemmChoice choose_gemm(int64_t capacity, int64_t n, int64_t k, bool gated) {
@@ -1659,7 +1706,7 @@ GemmChoice choose_dense_gate_up(int64_t capacity, int64_t n, int64_t k, bool &fu
   }
   double separate_us = 0.0;
   const GemmChoice separate = choose_decode(capacity, n, k, separate_us);
-  if (capacity <= kSplitMaxRows && k <= kSplitGatherMaxK) {
+  if (capacity <= kSplitGroupTokens && k <= kSplitGatherMaxK) {
     double split_us = 0.0;
     const GemmChoice split = choose_split(capacity, n, k, split_us, true);
     if (split_us < fused_us && split_us <= kGatherUs + separate_us) {
@@ -1737,15 +1784,17 @@ GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmCho
   record.k_slice = choice.k_slice;
   record.k_split = choice.k_split;
   if (choice.kind == GemmKind::Split) {
-    // choose_split is only consulted up to kSplitMaxRows (= kSplitTokens) rows.
+    // choose_split is only consulted up to kSplitMaxRows rows (and the fused gather up to
+    // one token group).
     const int64_t row_blocks = (args.n + 15) / 16;
     const int64_t per_group = kSplitWaves / choice.k_split;
     const bool gather = fused_gather && gated;
-    kernel.func = gather ? split_kernel<true, true>() : (gated ? split_kernel<true>() : split_kernel<false>());
+    kernel.func = gated ? split_kernel<true>(choice.variant, gather) : split_kernel<false>(choice.variant, false);
     kernel.grid = dim3(static_cast<unsigned>((row_blocks + per_group - 1) / per_group), 1, 1);
     kernel.block = dim3(64 * kSplitWaves, 1, 1);
     // Dynamic LDS beyond 64 KB: launch() opts the function in (enable_large_lds).
-    kernel.shmem = gather ? static_cast<unsigned>((capacity < kSplitTokens ? capacity : kSplitTokens) * (args.k + 16) * 2)
+    kernel.shmem = gather ? static_cast<unsigned>(
+                                (capacity < kSplitGroupTokens ? capacity : kSplitGroupTokens) * (args.k + 16) * 2)
                           : 0u;
   } else if (choice.kind == GemmKind::Stream) {
     const int64_t groups = ((args.n + 15) / 16 + kStreamWaves - 1) / kStreamWaves;
@@ -1844,7 +1893,8 @@ KernelLaunch make_grouped_split(const GemmArgs &args, bool gated, int max_tiles,
 std::string gemm_name(GemmChoice choice, bool gated) {
   const std::string prefix = gated ? "_gated" : "";
   if (choice.kind == GemmKind::Split) {
-    return "split" + prefix + "_t8_k" + std::to_string(choice.k_split);
+    return "split" + prefix + "_t" + std::to_string(kSplitGroupTokens * choice.variant) + "_k" +
+           std::to_string(choice.k_split);
   }
   if (choice.kind == GemmKind::Stream) {
     return "stream" + prefix + "_t16";

@@ -167,17 +167,20 @@ def test_variant_selection_covers_every_family(device):
 # Ragged geometries of the decode kernels: K not a multiple of their 512-column load
 # groups (a partial last K range) or of the tiles' 64-column slabs, N not a multiple of 16
 # (weight rows past N), one to many K ranges.  Up to 16 rows a cost model picks the split
-# or the stream kernel, from 17 the deep-staged small tiles; both decode kernels must
-# occur on these shapes.
+# (one token group up to 8 rows, two up to 16) or the stream kernel, from 17 the
+# deep-staged small tiles; both decode kernels must occur on these shapes.
 DECODE_SHAPES = [(1032, 1000), (2056, 9992), (4096, 12288), (264, 40)]
 DECODE_ROWS = [1, 3, 4, 5, 8, 9, 16, 17, 32, 33, 64]
 
 
 def test_decode_shapes_reach_both_decode_kernels(device):
-    chosen = {_native.gemm_variant(rows, n, k, gated).split("_")[0] for hidden, intermediate in DECODE_SHAPES
-              for rows in DECODE_ROWS if rows <= 16
-              for n, k, gated in ((2 * intermediate, hidden, True), (hidden, intermediate, False))}
-    assert chosen == {"split", "stream"}
+    names = {_native.gemm_variant(rows, n, k, gated) for hidden, intermediate in DECODE_SHAPES
+             for rows in DECODE_ROWS if rows <= 16
+             for n, k, gated in ((2 * intermediate, hidden, True), (hidden, intermediate, False))}
+    assert {name.split("_")[0] for name in names} == {"split", "stream"}
+    # the split kernel with one and with two token groups, gated and not
+    families = {name.rsplit("_k", 1)[0] for name in names if name.startswith("split")}
+    assert {"split_t8", "split_t16", "split_gated_t8", "split_gated_t16"} <= families
 
 
 @pytest.mark.parametrize("hidden,intermediate", DECODE_SHAPES)
