@@ -582,27 +582,36 @@ __global__ __launch_bounds__(64 * kSplitWaves) void grouped_split_kernel(GemmArg
 }
 
 // ------------------------------------------------------------------ stream (decode)
-// Weight-streaming projection for 5 to 16 live rows.  Workgroup g works on K slice
-// g / groups_per_slice: it stages the activations of that slice in LDS once (rows padded
-// by 16 bytes so the 16 token rows one fragment read touches fall in distinct bank
-// slots), then each of its 8 waves streams one 16-row weight block of the slice with
-// DEPTH 128-wide K chunks of loads in flight (16 rows x 64 contiguous bytes per load
-// instruction), multiplying on v_mfma_f32_16x16x32_bf16 with the weights as the M
-// operand.  With several slices the fp32 partial tiles go to scratch and
-// stream_reduce_kernel, launched next on the same stream, finishes the projection.  (A
-// last-arriver reduction inside this kernel would need an agent-scope release per wave,
-// which writes back the XCD's whole L2 on this part and cost more than the stream itself.)
+// Weight-streaming projection for up to 16 live rows.  Workgroup g works on K slice
+// g / groups_per_slice: it stages the activations of that slice in LDS once, then each of
+// its 8 waves streams one 16-row weight block of the slice with DEPTH 128-wide K chunks of
+// loads in flight, multiplying on v_mfma_f32_16x16x32_bf16 with the weights as the M
+// operand.  The weights are read as whole 128-byte lines with the nontemporal hint and the
+// tokens as two groups of 8, with the even / odd piece pairing of the split kernel (see
+// there): lane (i, q) loads row i & 7 of a half block, piece 2 q + (i >> 3) of the line,
+// and reads token 8 g + (i & 7) at the same piece from LDS; the diagonal blocks of each
+// MFMA are summed at the end.  LDS rows are padded by 32 bytes so that the 16 pieces one
+// read touches fall in distinct bank slots.  With several slices the fp32 partial tiles go
+// to scratch and stream_reduce_kernel, launched next on the same stream, finishes the
+// projection.  (A last-arriver reduction inside this kernel would need an agent-scope
+// release per wave, which writes back the XCD's whole L2 on this part and cost more than
+// the stream itself.)
 constexpr int kStreamWaves = 8;
 constexpr int kStreamDepth = 4;
+constexpr int kStreamTokens = 16;
+constexpr int kStreamRowPad = 16;  // elements of LDS row padding
 
-template <int TB, bool GATED, bool GATHER>
+template <bool GATED, bool GATHER>
 __global__ __launch_bounds__(64 * kStreamWaves) void stream_gemm_kernel(GemmArgs a) {
-  constexpr int TP = 16 * TB;
+  constexpr int TP = kStreamTokens;
+  constexpr int TG = TP / 8;
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int r16 = lane & 15;
   const int kq = lane >> 4;
+  const int row = r16 & 7;                // weight row within its half / token within its group
+  const int piece = 2 * kq + (r16 >> 3);  // 16-byte piece of the 128-byte line
   const int64_t ks = a.k_slice;
   const int64_t slices = (a.k + ks - 1) / ks;
   const int64_t row_blocks = (a.n + 15) / 16;
@@ -611,7 +620,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_gemm_kernel(GemmArgs
   const int64_t rb = (blockIdx.x % groups_per_slice) * kStreamWaves + wave;
   const int64_t k0 = slice * ks;
   const int64_t klen = (a.k - k0) < ks ? (a.k - k0) : ks;
-  const int64_t rs = ks + 8;  // LDS row stride in elements
+  const int64_t rs = ks + kStreamRowPad;  // LDS row stride in elements
   const u32x4 zero = {0u, 0u, 0u, 0u};
 
   // Every slice runs ks / 128 chunks (a multiple of DEPTH, so the loop has no partial
@@ -619,21 +628,26 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_gemm_kernel(GemmArgs
   // as zero, and all loads are unconditional, which lets the wait counts track exactly
   // DEPTH chunks in flight.  Columns past K in the last slice are zeroed by a select.
   const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(a.w, static_cast<uint32_t>(a.n * a.k * 2));
-  const uint32_t w_off = static_cast<uint32_t>(((rb * 16 + r16) * a.k + k0 + kq * 8) * 2);
+  const uint32_t w_off = static_cast<uint32_t>(((rb * 16 + row) * a.k + k0 + piece * 8) * 2);
+  const uint32_t w_half = static_cast<uint32_t>(8 * a.k * 2);  // rows 8 .. 15 of the block
   const int chunks = static_cast<int>(ks / 128);
-  const int lane_valid = static_cast<int>(klen) - kq * 8;
+  const int lane_valid = static_cast<int>(klen) - piece * 8;
   // Waves start at different chunks of the slice (a stride-7 rotation by row block), so the
   // concurrently streamed addresses spread over the memory channels instead of every wave
   // reading the same column range of its rows at the same time.
   const int rotation = static_cast<int>((rb * 7) % chunks);
   auto rotated = [&](int chunk) { return chunk + rotation < chunks ? chunk + rotation : chunk + rotation - chunks; };
 
+  // w[2 line + h]: line `line` of the chunk (K columns 64 line .. 64 line + 63), rows 8 h + [0, 8).
   u32x4 wbuf[kStreamDepth][4];
   auto load_chunk = [&](int chunk, u32x4 (&w)[4]) {
-    const int column = rotated(chunk) * 128;
+    const uint32_t column = static_cast<uint32_t>(rotated(chunk) * 128) * 2;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      w[s] = buffer_load16(w_rsrc, w_off + static_cast<uint32_t>((column + s * 32) * 2));
+    for (int line = 0; line < 2; ++line) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        w[2 * line + h] = buffer_load16<kLoadNontemporal>(w_rsrc, w_off + h * w_half + column + line * 128);
+      }
     }
   };
   // The first DEPTH chunks of weights are requested before the activations are staged, so
@@ -668,20 +682,25 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_gemm_kernel(GemmArgs
     return;
   }
 
-  f32x4 acc[TB];
+  // acc[g][h]: token group g, weight rows 16 rb + 8 h + [0, 8).
+  f32x4 acc[TG][2];
 #pragma unroll
-  for (int tb = 0; tb < TB; ++tb) {
-    acc[tb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int g = 0; g < TG; ++g) {
+    acc[g][0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    acc[g][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   }
   auto compute_chunk = [&](int chunk, const u32x4 (&w)[4]) {
     const int column = rotated(chunk) * 128;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const u32x4 wk = column + s * 32 < lane_valid ? w[s] : zero;
+    for (int line = 0; line < 2; ++line) {
+      const bool valid = column + line * 64 < lane_valid;
+      const u32x4 w0 = valid ? w[2 * line] : zero;
+      const u32x4 w1 = valid ? w[2 * line + 1] : zero;
 #pragma unroll
-      for (int tb = 0; tb < TB; ++tb) {
-        const u32x4 x = load16(xs + (tb * 16 + r16) * rs + column + s * 32 + kq * 8);
-        acc[tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(wk), as_bf16x8(x), acc[tb], 0, 0, 0);
+      for (int g = 0; g < TG; ++g) {
+        const u32x4 x = load16(xs + (8 * g + row) * rs + column + line * 64 + piece * 8);
+        acc[g][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(w0), as_bf16x8(x), acc[g][0], 0, 0, 0);
+        acc[g][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(w1), as_bf16x8(x), acc[g][1], 0, 0, 0);
       }
     }
   };
@@ -702,36 +721,49 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_gemm_kernel(GemmArgs
     compute_chunk(c0 + d, wbuf[d]);
   }
 
-  // lane holds D[4 kq + i][r16] of each token block: weight rows n .. n+3, one token.
-  const int64_t n = rb * 16 + 4 * kq;
-  if (slices > 1) {
-    // Partial tile of this slice; stream_reduce_kernel sums the slices in order.
+  // Lane (i, q) holds D[4 q + v][i]; the lanes with q < 2 and i < 8 add the odd pieces'
+  // block from lane + 40 and then hold weight rows 16 rb + 8 h + 4 q + v for token 8 g + i.
+  f32x4 sum[TG][2];
 #pragma unroll
-    for (int tb = 0; tb < TB; ++tb) {
-      const int64_t token = tb * 16 + r16;
-      if (token < a.rows && n < a.n) {
-        *reinterpret_cast<f32x4 *>(a.partials + (slice * a.rows + token) * a.n + n) = acc[tb];
+  for (int g = 0; g < TG; ++g) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        sum[g][h][v] = acc[g][h][v] + __shfl(acc[g][h][v], lane + 40, kWave);
       }
     }
+  }
+  if (kq >= 2 || r16 >= 8) {
     return;
   }
 #pragma unroll
-  for (int tb = 0; tb < TB; ++tb) {
-    const int64_t token = tb * 16 + r16;
-    if (token >= a.rows || n >= a.n) {
+  for (int g = 0; g < TG; ++g) {
+    const int64_t token = 8 * g + r16;
+    if (token >= a.rows) {
       continue;
     }
-    uint16_t *row = output_row(a, token);
-    if (row == nullptr) {
+    uint16_t *out = slices > 1 ? nullptr : output_row(a, token);
+    if (slices == 1 && out == nullptr) {
       continue;
     }
-    if constexpr (GATED) {
-      const float h0 = gated_silu(acc[tb][0], acc[tb][1], a.act);
-      const float h1 = gated_silu(acc[tb][2], acc[tb][3], a.act);
-      *reinterpret_cast<uint32_t *>(row + n / 2) = pack_bf16x2(h0, h1);
-    } else {
-      u32x2 packed = {pack_bf16x2(acc[tb][0], acc[tb][1]), pack_bf16x2(acc[tb][2], acc[tb][3])};
-      *reinterpret_cast<u32x2 *>(row + n) = packed;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int64_t n = rb * 16 + 8 * h + 4 * kq;
+      if (n >= a.n) {
+        continue;
+      }
+      if (slices > 1) {
+        // Partial tile of this slice; stream_reduce_kernel sums the slices in order.
+        *reinterpret_cast<f32x4 *>(a.partials + (slice * a.rows + token) * a.n + n) = sum[g][h];
+      } else if constexpr (GATED) {
+        const float h0 = gated_silu(sum[g][h][0], sum[g][h][1], a.act);
+        const float h1 = gated_silu(sum[g][h][2], sum[g][h][3], a.act);
+        *reinterpret_cast<uint32_t *>(out + n / 2) = pack_bf16x2(h0, h1);
+      } else {
+        u32x2 packed = {pack_bf16x2(sum[g][h][0], sum[g][h][1]), pack_bf16x2(sum[g][h][2], sum[g][h][3])};
+        *reinterpret_cast<u32x2 *>(out + n) = packed;
+      }
     }
   }
 }
@@ -1436,7 +1468,7 @@ int split_groups(int64_t capacity) { return capacity <= kSplitGroupTokens ? 1 : 
 
 template <bool GATED, bool GATHER = false>
 const void *stream_kernel() {
-  return reinterpret_cast<const void *>(&stream_gemm_kernel<1, GATED, GATHER>);
+  return reinterpret_cast<const void *>(&stream_gemm_kernel<GATED, GATHER>);
 }
 
 struct TileShape {
@@ -1487,8 +1519,8 @@ constexpr int kComputeUnits = 256;
 // bounded rate (measured, the chip rate scales with the workgroup count up to the CU
 // count), so a grid of few workgroups is the thing to avoid (Qwen3-4B down through the
 // split kernel with 2 K ranges per row block has 80 workgroups: 41 us; with 8, 320: 16 us),
-// workgroups past 256 run as further rounds, and the chip caps the total: ~6.4 TB/s for the
-// split kernel's whole-line nontemporal reads, ~5.4 TB/s for the stream kernel's half lines.
+// workgroups past 256 run as further rounds, and the chip caps the total (both read whole
+// 128-byte weight lines with the nontemporal hint).
 // The split kernel reads its token pieces from L2, a little more per row; the stream
 // kernel's K slices cost the reduction launch and their partial traffic.  The split
 // kernel's rounds of 256 workgroups are priced one after another (each at the chip rate or
@@ -1505,8 +1537,8 @@ constexpr double kSplitWorkgroupBytesPerUs[kSplitMaxGroups] = {26.0e3, 20.0e3};
 constexpr double kSplitBytesPerUs[kSplitMaxGroups] = {6.8e6, 5.2e6};
 constexpr double kSplitFixedUs[kSplitMaxGroups] = {4.0, 3.0};
 constexpr double kSplitRowUsPerChunk = 0.02;  // per row past the first and 128-wide chunk of a range (padded)
-constexpr double kStreamWorkgroupBytesPerUs = 28.0e3;
-constexpr double kStreamBytesPerUs = 5.4e6;
+constexpr double kStreamWorkgroupBytesPerUs = 30.0e3;
+constexpr double kStreamBytesPerUs = 6.0e6;
 constexpr double kStreamFixedUs = 2.0;
 constexpr double kStreamReduceUs = 12.0;  // the reduction launch, fitted (it also ends the overlap of slices)
 constexpr double kStreamPartialBytesPerUs = 6.0e6;
@@ -1516,6 +1548,9 @@ constexpr double kGatherUs = 4.0;  // a separate gather launch at decode sizes (
 // no second), beside only the first weight chunks: measured 2.3 us per round of 256
 // workgroups for Qwen3-0.6B gate_up (one round), 3.3 and 4.4 us for Qwen3-8B (3 and 6).
 constexpr double kSplitGatherRoundUs = 3.0;
+// The same for the stream kernel's fused gather, per round of workgroups (measured: Qwen3-8B
+// gate_up at 16 rows, 192 workgroups, 37.0 us plain and ~41 us with the gather fused).
+constexpr double kStreamGatherUs = 3.5;
 constexpr int64_t kSplitGatherMaxK = 4096;  // 8 staged rows of K + 16 bf16 (66 KB) beside the partial sums
 
 double decode_stream_us(int64_t n, int64_t k, int64_t workgroups, double workgroup_bytes_per_us,
@@ -1580,7 +1615,7 @@ GemmChoice choose_stream(int64_t capacity, int64_t n, int64_t k, double &cost) {
   for (int64_t slices = 1; slices <= 64; ++slices) {
     const int64_t k_slice = ((k + slices - 1) / slices + kStreamSliceQuantum - 1) / kStreamSliceQuantum *
                             kStreamSliceQuantum;
-    if (tp * (k_slice + 8) * 2 > kStreamLdsBytes || stream_slices(k, k_slice) != slices) {
+    if (tp * (k_slice + kStreamRowPad) * 2 > kStreamLdsBytes || stream_slices(k, k_slice) != slices) {
       continue;  // does not fit LDS, or the same slice length as fewer slices
     }
     double us = decode_stream_us(n, k, slices * groups, kStreamWorkgroupBytesPerUs, kStreamBytesPerUs, kStreamFixedUs);
@@ -1690,7 +1725,7 @@ GemmChoice choose_dense_gate_up(int64_t capacity, int64_t n, int64_t k, bool &fu
   for (int64_t slices = 1;; ++slices) {
     const int64_t k_slice = ((k + slices - 1) / slices + kStreamSliceQuantum - 1) / kStreamSliceQuantum *
                             kStreamSliceQuantum;
-    if (16 * (k_slice + 8) * 2 <= kStreamLdsBytes) {
+    if (kStreamTokens * (k_slice + kStreamRowPad) * 2 <= kStreamLdsBytes) {
       fused_choice.k_slice = k_slice;
       break;
     }
@@ -1700,7 +1735,9 @@ GemmChoice choose_dense_gate_up(int64_t capacity, int64_t n, int64_t k, bool &fu
   // more workgroups (Qwen3-0.6B gate_up at one row: 48 fused workgroups, 13.6 us).
   const int64_t groups = ((n + 15) / 16 + kStreamWaves - 1) / kStreamWaves;
   const int64_t slices = stream_slices(k, fused_choice.k_slice);
-  double fused_us = decode_stream_us(n, k, slices * groups, kStreamWorkgroupBytesPerUs, kStreamBytesPerUs, kStreamFixedUs);
+  double fused_us = decode_stream_us(n, k, slices * groups, kStreamWorkgroupBytesPerUs, kStreamBytesPerUs,
+                                     kStreamFixedUs) +
+                    kStreamGatherUs * static_cast<double>((slices * groups + kComputeUnits - 1) / kComputeUnits);
   if (slices > 1) {
     fused_us += kStreamReduceUs + 8.0 * static_cast<double>(slices * capacity * n) / kStreamPartialBytesPerUs;
   }
@@ -1804,7 +1841,7 @@ GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmCho
     kernel.grid = dim3(static_cast<unsigned>(slices * groups), 1, 1);
     kernel.block = dim3(64 * kStreamWaves, 1, 1);
     // Dynamic LDS beyond 64 KB: launch() opts the function in (enable_large_lds).
-    kernel.shmem = static_cast<unsigned>(16 * (choice.k_slice + 8) * 2);
+    kernel.shmem = static_cast<unsigned>(kStreamTokens * (choice.k_slice + kStreamRowPad) * 2);
   } else {
     const TileShape &shape = kTileShapes[choice.variant];
     const bool stream = capacity <= shape.bm;
