@@ -98,6 +98,15 @@ DenseWorkspace dense_workspace(int64_t capacity, int64_t hidden, int64_t interme
 // below 2^30 bytes (hidden is bounded by the gather's 16384).
 constexpr int64_t kMaxIntermediate = int64_t{1} << 21;
 
+// The fused gathers (split, stream and grouped tile kernels) read mailbox rows through one
+// buffer resource over the whole pool, and out-of-range lanes use offsets near 2^31, so the
+// pool must stay below 2^31 bytes wherever a step may fuse its gather.
+int validate_mailbox(int64_t pool_rows, int64_t hidden) {
+  XP_REQUIRE(pool_rows * hidden * 2 < (int64_t{1} << 31),
+             "mailbox pool must stay below 2 GiB (32-bit buffer range of the fused gathers)");
+  return XP_OK;
+}
+
 int validate_geometry(int64_t hidden, int64_t intermediate) {
   XP_REQUIRE(hidden > 0 && hidden % 8 == 0, "hidden size must be a positive multiple of 8");
   XP_REQUIRE(intermediate > 0 && intermediate % 8 == 0, "intermediate size must be a positive multiple of 8");
@@ -1248,6 +1257,9 @@ int dense_step_checks(const void *pool_in, const void *pool_out, int64_t pool_ro
   if (const int status = validate_geometry(hidden, intermediate); status != XP_OK) {
     return status;
   }
+  if (const int status = validate_mailbox(pool_rows, hidden); status != XP_OK) {
+    return status;
+  }
   XP_REQUIRE(pool_in != nullptr && pool_out != nullptr && slots != nullptr && w_gate_up != nullptr &&
                  w_down != nullptr,
              "dense step pointers must be non-null");
@@ -1598,6 +1610,10 @@ int xp_replay(xp_lane_t lane, int instance_index, int layer_ordinal, int64_t row
                                           ", ordinal " + std::to_string(layer_ordinal) + ")");
     }
     layer = *found;
+  }
+  if (const int status = validate_mailbox(pool_rows, layer.kind == XP_LAYER_MOE ? layer.moe.hidden : layer.hidden);
+      status != XP_OK) {
+    return status;
   }
   std::lock_guard<std::mutex> guard(lane->mutex);
   Template *selected = nullptr;

@@ -186,7 +186,9 @@ size_t xp_dense_workspace_bytes(int64_t capacity, int64_t hidden, int64_t interm
 int xp_dense_workspace_layout(int64_t capacity, int64_t hidden, int64_t intermediate, size_t *offsets);
 
 /* One eager mailbox step: gather(+RMSNorm) -> gate_up+SiLU -> down -> scatter to
- * pool_out rows slots[i] (pool_out may equal pool_in).  Same kernels as a replay.
+ * pool_out rows slots[i] (pool_out may equal pool_in).  Same kernels as a replay.  The pool
+ * (pool_rows * hidden * 2 bytes) must stay below 2 GiB, the 32-bit buffer range through which
+ * the decode kernels gather it (XP_ERROR_INVALID_ARGUMENT otherwise; xp_replay likewise).
  * Replaces Dense.run_into (operators/dense.py:70-86) plus the Transport copies. */
 int xp_dense_step(const void *pool_in, void *pool_out, int64_t pool_rows, const int32_t *slots, int64_t rows,
                   int64_t hidden, int64_t intermediate, const void *w_gate_up, const void *w_down,

@@ -170,6 +170,20 @@ def test_moe_experts_rejects_buffer_ranges_past_2_gib():
     assert status == _native.XP_ERROR_INVALID_ARGUMENT
 
 
+def test_dense_step_rejects_mailbox_pools_past_2_gib():
+    # The fused gathers address the whole mailbox pool through one 32-bit buffer resource:
+    # 262144 slots of 4096 bf16 are 2 GiB and must be refused before any pointer is used.
+    lib = _native.library()
+    status = lib.xp_dense_step(None, None, 1 << 18, None, 1, 4096, 12288, None, None, None, ctypes.c_float(1e-6),
+                               None, 0, None, None)
+    assert status == _native.XP_ERROR_INVALID_ARGUMENT
+    assert "2 GiB" in _native.last_error()
+    status = lib.xp_dense_step_static(None, None, 1 << 18, None, 1, 4096, 12288, None, None, None,
+                                      ctypes.c_float(1e-6), None, None)
+    assert status == _native.XP_ERROR_INVALID_ARGUMENT
+    assert "2 GiB" in _native.last_error()
+
+
 def test_dense_projections_past_one_buffer_range_take_the_tile_kernel():
     # The split and stream kernels address the whole weight matrix through one 32-bit buffer
     # resource; a gate_up of 2 x 53248 x 16384 bf16 (3.5 GB, a TP-1 shard of a very wide model)
