@@ -115,6 +115,40 @@ def gate_up_bytes(tokens: int) -> float:
     return 4.0 * HIDDEN * INTERMEDIATE + 2.0 * tokens * HIDDEN + 2.0 * tokens * INTERMEDIATE
 
 
+def mfma_ceiling(stream) -> dict:
+    """The bf16 matrix rate a pure-MFMA loop sustains on random operands (no memory
+    traffic), measured on `stream` with HIP events, and the shader clock the chip held."""
+
+    import ctypes
+
+    import torch
+
+    from crosspool_amd import build
+
+    probes = ctypes.CDLL(str(build.PROBE_LIBRARY))
+    clocks = torch.zeros(2, dtype=torch.int64, device=stream.device)
+    workgroups, rounds = 2048, 4000
+
+    def launch() -> None:
+        status = probes.xp_probe_mfma(workgroups, rounds, 1, ctypes.c_void_p(clocks.data_ptr()),
+                                      ctypes.c_void_p(stream.cuda_stream))
+        if status != 0:
+            raise RuntimeError(f"MFMA probe launch failed with status {status}")
+
+    launch()
+    begin = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    begin.record(stream)
+    launch()
+    end.record(stream)
+    end.synchronize()
+    seconds = begin.elapsed_time(end) / 1e3
+    cycles, ticks = (int(value) for value in clocks.cpu())
+    tflops = workgroups * 4 * rounds * 8 * 2.0 * 32 * 32 * 16 / seconds / 1e12
+    return {"tflops": round(tflops, 1), "frac_of_peak": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+            "clock_ghz": round(cycles / (ticks * 10.0), 3) if ticks > 0 else None}
+
+
 def run_ceilings(device) -> dict:
     """Hardware limits measured with HIP events on the current stream (see the module doc)."""
 
@@ -147,14 +181,25 @@ def run_ceilings(device) -> dict:
             raise RuntimeError(f"probe launch failed with status {status}")
 
     result: dict = {}
-    # bf16 MFMA: 4-wave workgroups, 8 independent 32x32x16 chains per wave.
+    # bf16 MFMA: 4-wave workgroups, 8 independent 32x32x16 chains per wave, with low-entropy
+    # constant operands and with rotating random operands (the switching power of a GEMM's
+    # main loop); the clock comes from workgroup 0's shader-cycle and 100 MHz counters.
+    clocks = torch.zeros(2, dtype=torch.int64, device=device)
     mfma = []
-    for workgroups, rounds in ((1024, 20000), (2048, 20000)):
-        seconds = per_launch(lambda index=0: checked(probes.xp_probe_mfma(workgroups, rounds, handle)), 5)
-        flops = workgroups * 4 * rounds * 8 * 2.0 * 32 * 32 * 16
-        mfma.append({"workgroups": workgroups, "tflops": round(flops / seconds / 1e12, 1)})
+    for random in (0, 1):
+        for workgroups, rounds in ((1024, 20000), (2048, 20000)):
+            seconds = per_launch(lambda index=0: checked(probes.xp_probe_mfma(
+                workgroups, rounds, random, ctypes.c_void_p(clocks.data_ptr()), handle)), 5)
+            cycles, ticks = (int(value) for value in clocks.cpu())
+            flops = workgroups * 4 * rounds * 8 * 2.0 * 32 * 32 * 16
+            mfma.append({"operands": "random" if random else "constant", "workgroups": workgroups,
+                         "tflops": round(flops / seconds / 1e12, 1),
+                         "clock_ghz": round(cycles / (ticks * 10.0), 3) if ticks > 0 else None})
     best = max(point["tflops"] for point in mfma)
-    result["mfma_bf16"] = {"points": mfma, "best_tflops": best, "frac_of_2500": round(best / MFMA_BF16_PEAK_TFLOPS, 4)}
+    best_random = max(point["tflops"] for point in mfma if point["operands"] == "random")
+    result["mfma_bf16"] = {"points": mfma, "best_tflops": best, "frac_of_2500": round(best / MFMA_BF16_PEAK_TFLOPS, 4),
+                           "best_random_tflops": best_random,
+                           "random_frac_of_2500": round(best_random / MFMA_BF16_PEAK_TFLOPS, 4)}
 
     # HBM reads: a 4 GiB buffer (far past the 256 MB last-level cache), 1 KB per wave
     # instruction, plain loads and loads with the nontemporal hint.
@@ -317,11 +362,14 @@ def main() -> int:
         # Up to 64 rows the projection streams its weights (HBM-bound); above, MFMA-bound.
         if tokens > 64:
             achieved = gate_up_flops(tokens) / per_launch / 1e12
+            ceiling = mfma_ceiling(lane.stream)
             return {
                 "kernel": variant, "tokens": tokens, "bound": "mfma", "achieved": round(achieved, 1),
                 "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
                 "traffic": traffic, "avg_launch_us": round(per_launch * 1e6, 2),
                 "algorithmic_flops": gate_up_flops(tokens),
+                "sustained_mfma_random_operands": {**ceiling,
+                                                   "kernel_frac_of_it": round(achieved / ceiling["tflops"], 4)},
             }
         achieved = gate_up_bytes(tokens) / per_launch / 1e9
         return {

@@ -4,7 +4,13 @@
 //
 //  * probe_mfma: every wave issues rounds of 8 independent v_mfma_f32_32x32x16_bf16 on
 //    register operands, no memory traffic: the sustained bf16 matrix rate of the chip at the
-//    clock it holds under that load.
+//    clock it holds under that load.  Two operand kinds: low-entropy constants (multiples
+//    of 1/16, one A and one B fragment for every MFMA), and random bf16 values of GEMM-like
+//    magnitude rotated over four A and four B fragments so that every MFMA's operands
+//    differ from the previous one's, as in a GEMM's main loop.  The multipliers' switching
+//    power, and with it the clock the chip can hold, depends on the operands.  Workgroup 0's
+//    first wave records shader cycles (s_memtime) and 100 MHz ticks (s_memrealtime) over
+//    its loop, from which the host reads the clock.
 //  * probe_read_contiguous: a grid-stride read of a buffer, each wave instruction 1 KB of
 //    consecutive bytes, UNROLL loads in flight per lane: the HBM read rate of the plainest
 //    streaming pattern, with plain loads or with the nontemporal hint (`nt`), which the
@@ -30,13 +36,35 @@ using f32x16 = float __attribute__((ext_vector_type(16)));
 
 constexpr int kMfmaChains = 8;
 
-__global__ __launch_bounds__(256) void probe_mfma_kernel(int rounds, float *sink, int write) {
-  bf16x8 a;
-  bf16x8 b;
+// A bf16 of magnitude 2^-3 .. 2^2 with random sign and mantissa from a hashed counter.
+__device__ __forceinline__ __bf16 random_bf16(uint32_t seed) {
+  uint32_t h = seed * 0x9e3779b9u;
+  h ^= h >> 15;
+  h *= 0x85ebca6bu;
+  h ^= h >> 13;
+  const uint32_t exponent = 124u + (h >> 24) % 6u;  // 2^-3 .. 2^2
+  const uint32_t bits = ((h & 0x8000u) << 16) | (exponent << 23) | ((h & 0x7fu) << 16);
+  return static_cast<__bf16>(__uint_as_float(bits));
+}
+
+template <bool RANDOM>
+__global__ __launch_bounds__(256) void probe_mfma_kernel(int rounds, float *sink, int write, uint64_t *clocks) {
+  constexpr int kSets = RANDOM ? 4 : 1;
+  bf16x8 a[kSets];
+  bf16x8 b[kSets];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    a[i] = static_cast<__bf16>(static_cast<float>((threadIdx.x + i) & 7) * 0.125f);
-    b[i] = static_cast<__bf16>(static_cast<float>((threadIdx.x * 3 + i) & 7) * 0.0625f);
+  for (int s = 0; s < kSets; ++s) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if constexpr (RANDOM) {
+        const uint32_t id = (blockIdx.x * blockDim.x + threadIdx.x) * 64u + s * 8u + i;
+        a[s][i] = random_bf16(2u * id);
+        b[s][i] = random_bf16(2u * id + 1u);
+      } else {
+        a[s][i] = static_cast<__bf16>(static_cast<float>((threadIdx.x + i) & 7) * 0.125f);
+        b[s][i] = static_cast<__bf16>(static_cast<float>((threadIdx.x * 3 + i) & 7) * 0.0625f);
+      }
+    }
   }
   f32x16 acc[kMfmaChains];
 #pragma unroll
@@ -46,11 +74,21 @@ __global__ __launch_bounds__(256) void probe_mfma_kernel(int rounds, float *sink
       acc[c][r] = 0.0f;
     }
   }
+  const uint64_t cycles0 = __builtin_readcyclecounter();
+  const uint64_t ticks0 = __builtin_amdgcn_s_memrealtime();
   for (int round = 0; round < rounds; ++round) {
 #pragma unroll
     for (int c = 0; c < kMfmaChains; ++c) {
-      acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[c], 0, 0, 0);
+      // RANDOM: chain c multiplies A set c % 4 by B set (c / 2) % 4, so consecutive MFMAs
+      // never see the same operand pair.
+      acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[c % kSets], b[(c / 2) % kSets], acc[c], 0, 0, 0);
     }
+  }
+  if (clocks != nullptr && blockIdx.x == 0 && threadIdx.x == 0) {
+    // Reading the counters after the loop waits for nothing: the last MFMAs may still be in
+    // the pipe, which is a few hundred cycles of a multi-millisecond loop.
+    clocks[0] = __builtin_readcyclecounter() - cycles0;
+    clocks[1] = __builtin_amdgcn_s_memrealtime() - ticks0;
   }
   if (write) {
     float total = 0.0f;
@@ -141,10 +179,17 @@ __global__ __launch_bounds__(512) void probe_read_rows_kernel(const char *matrix
 
 extern "C" {
 
-// rounds of 8 MFMAs per wave over `workgroups` 4-wave workgroups.
-int xp_probe_mfma(int workgroups, int rounds, void *stream) {
-  hipLaunchKernelGGL(probe_mfma_kernel, dim3(workgroups), dim3(256), 0, static_cast<hipStream_t>(stream), rounds,
-                     static_cast<float *>(nullptr), 0);
+// rounds of 8 MFMAs per wave over `workgroups` 4-wave workgroups; operands low-entropy
+// constants (random == 0) or rotating random bf16 values.  `clocks` (device, 2 words, may
+// be NULL) receives the shader cycles and 100 MHz ticks of workgroup 0's loop.
+int xp_probe_mfma(int workgroups, int rounds, int random, uint64_t *clocks, void *stream) {
+  if (random != 0) {
+    hipLaunchKernelGGL(probe_mfma_kernel<true>, dim3(workgroups), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       rounds, static_cast<float *>(nullptr), 0, clocks);
+  } else {
+    hipLaunchKernelGGL(probe_mfma_kernel<false>, dim3(workgroups), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       rounds, static_cast<float *>(nullptr), 0, clocks);
+  }
   return static_cast<int>(hipGetLastError());
 }
 
