@@ -33,6 +33,10 @@
 #include <type_traits>
 #include <utility>
 
+// Lambdas of the kernels below are forced inline: a lambda left out of line takes the
+// accumulator array by reference, which then lives in scratch memory instead of registers.
+#define XP_INLINE __attribute__((always_inline))
+
 namespace xp {
 namespace {
 
@@ -426,6 +430,157 @@ __global__ __launch_bounds__(64 * kSplitWaves) void split_gemm_kernel(GemmArgs a
       } else {
         u32x2 packed = {pack_bf16x2(sum[g][h][0], sum[g][h][1]), pack_bf16x2(sum[g][h][2], sum[g][h][3])};
         *reinterpret_cast<u32x2 *>(out + n) = packed;
+      }
+    }
+  }
+}
+
+// The split kernel with the mailbox gather fused, for grids smaller than its unit count.
+// A unit is the 8 / ksplit row blocks x ksplit K ranges one workgroup of the split kernel
+// covers (wave w: row block unit * (8 / ksplit) + w / ksplit, K range w % ksplit);
+// workgroup g takes units g, g + gridDim.x, ...  The token rows (one group of 8, K <=
+// kSplitGatherMaxK) are gathered and RMS-normalised into LDS once per workgroup, with no
+// weight loads in flight beside it (their registers would keep the kernel from two
+// workgroups per CU), so the gather costs one round trip per workgroup instead of one per
+// unit, and one workgroup's K-range sum and stores overlap the other's weight stream.  The
+// arithmetic per unit is split_gemm_kernel's (same chunk order, same fixed-order sum), so
+// the results are bit for bit the split kernel's.
+template <int DEPTH, bool GATED>
+__global__ __launch_bounds__(64 * kSplitWaves) void split_gathered_kernel(GemmArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t staged[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int r16 = lane & 15;
+  const int kq = lane >> 4;
+  const int row = r16 & 7;                // weight row within its half / token
+  const int piece = 2 * kq + (r16 >> 3);  // 16-byte piece of the 128-byte line
+  const int ksplit = static_cast<int>(a.k_split);
+  const int part = wave % ksplit;
+  const int block_in_unit = wave / ksplit;
+  const int64_t per_unit = kSplitWaves / ksplit;
+  const int64_t row_blocks = (a.n + 15) / 16;
+  const int64_t units = (row_blocks + per_unit - 1) / per_unit;
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+  const int64_t rs = a.k + 16;  // staged row stride in elements
+  const int staged_rows = a.capacity < kSplitGroupTokens ? static_cast<int>(a.capacity) : kSplitGroupTokens;
+  const int k0 = part * static_cast<int>(a.k_slice);
+  const int k_range = static_cast<int>(a.k - k0 < a.k_slice ? a.k - k0 : a.k_slice);
+  const int chunks = (k_range + 127) / 128;
+  const int padded = (chunks + DEPTH - 1) / DEPTH * DEPTH;
+  const int lane_valid = static_cast<int>(a.k) - k0 - piece * 8;
+  const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(a.w, static_cast<uint32_t>(a.n * a.k * 2));
+  const uint32_t w_half = static_cast<uint32_t>(8 * a.k * 2);
+
+  stage_gathered_rows<kSplitGroupTokens, kSplitWaves>(a, staged, rs, 0, static_cast<int>(a.k),
+                                                      static_cast<int>(a.k / 8), wave, lane, staged_rows);
+  __syncthreads();
+  const uint16_t *token_row = staged + row * rs + k0 + piece * 8;
+  const bool token_live = row < staged_rows;
+
+  // Partial sums of the K ranges p > 0: wave w of range p > 0 writes slot w - w / ksplit - 1.
+  __shared__ f32x4 partial[kSplitWaves - 1][2][64];
+  for (int64_t unit = blockIdx.x; unit < units; unit += gridDim.x) {
+    const int64_t rb = unit * per_unit + block_in_unit;
+    const bool active = rb < row_blocks;
+    const int rotation = static_cast<int>((rb * 7) % chunks);
+    const uint32_t w_off = static_cast<uint32_t>(((rb * 16 + row) * a.k + k0 + piece * 8) * 2);
+    auto column_of = [&](int chunk) XP_INLINE {
+      const int c = chunk + rotation;
+      return (c < chunks ? c : c - chunks) * 128;
+    };
+    u32x4 wbuf[DEPTH][4];
+    auto load_chunk = [&](int chunk, u32x4 (&w)[4]) XP_INLINE {
+      const bool in_range = chunk < chunks;
+      const uint32_t column = static_cast<uint32_t>(column_of(chunk)) * 2;
+#pragma unroll
+      for (int line = 0; line < 2; ++line) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          w[2 * line + h] = buffer_load16<kLoadNontemporal>(
+              w_rsrc, in_range ? w_off + h * w_half + column + line * 128 : kOutOfRange);
+        }
+      }
+    };
+    f32x4 acc[2] = {f32x4{0.0f, 0.0f, 0.0f, 0.0f}, f32x4{0.0f, 0.0f, 0.0f, 0.0f}};
+    auto compute_chunk = [&](int chunk, const u32x4 (&w)[4]) XP_INLINE {
+      const int column = chunk < chunks ? column_of(chunk) : 0;
+#pragma unroll
+      for (int line = 0; line < 2; ++line) {
+        const bool valid = column + line * 64 < lane_valid;
+        const u32x4 w0 = valid ? w[2 * line] : zero;
+        const u32x4 w1 = valid ? w[2 * line + 1] : zero;
+        const u32x4 xk = valid && token_live ? load16(token_row + column + line * 64) : zero;
+        acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(w0), as_bf16x8(xk), acc[0], 0, 0, 0);
+        acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(w1), as_bf16x8(xk), acc[1], 0, 0, 0);
+      }
+    };
+    if (active) {
+#pragma unroll
+      for (int d = 0; d < DEPTH; ++d) {
+        load_chunk(d, wbuf[d]);
+      }
+      int c0 = 0;
+      for (; c0 < padded - DEPTH; c0 += DEPTH) {
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) {
+          compute_chunk(c0 + d, wbuf[d]);
+          load_chunk(c0 + d + DEPTH, wbuf[d]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+#pragma unroll
+      for (int d = 0; d < DEPTH; ++d) {
+        compute_chunk(c0 + d, wbuf[d]);
+      }
+    }
+    // Fixed-order sum of the K ranges of each row block (range 0's wave adds 1 .. ksplit - 1
+    // in order); the barriers wait for LDS only, nothing else is outstanding here.
+    if (ksplit > 1) {
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+      __asm__ volatile("s_barrier" ::: "memory");  // the previous unit's sums have been read
+      if (part != 0) {
+        partial[wave - block_in_unit - 1][0][lane] = acc[0];
+        partial[wave - block_in_unit - 1][1][lane] = acc[1];
+      }
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+      __asm__ volatile("s_barrier" ::: "memory");
+      if (part == 0) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          for (int p = 1; p < ksplit; ++p) {
+            acc[h] += partial[block_in_unit * (ksplit - 1) + p - 1][h][lane];
+          }
+        }
+      }
+    }
+    if (part == 0 && active) {
+      // As in split_gemm_kernel: lanes (i < 8, q < 2) add the odd pieces' block from lane + 40
+      // and hold weight rows 16 rb + 8 h + 4 q + v for token i.
+      f32x4 sum[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          sum[h][v] = acc[h][v] + __shfl(acc[h][v], lane + 40, kWave);
+        }
+      }
+      uint16_t *out = kq < 2 && r16 < 8 && r16 < a.rows ? output_row(a, r16) : nullptr;
+      if (out != nullptr) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int64_t n = rb * 16 + 8 * h + 4 * kq;
+          if (n >= a.n) {
+            continue;
+          }
+          if constexpr (GATED) {
+            const float h0 = gated_silu(sum[h][0], sum[h][1], a.act);
+            const float h1 = gated_silu(sum[h][2], sum[h][3], a.act);
+            *reinterpret_cast<uint32_t *>(out + n / 2) = pack_bf16x2(h0, h1);
+          } else {
+            u32x2 packed = {pack_bf16x2(sum[h][0], sum[h][1]), pack_bf16x2(sum[h][2], sum[h][3])};
+            *reinterpret_cast<u32x2 *>(out + n) = packed;
+          }
+        }
       }
     }
   }
@@ -837,9 +992,6 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
 }
 
-// Lambdas of the kernels below are forced inline: a lambda left out of line takes the
-// accumulator array by reference, which then lives in scratch memory instead of registers.
-#define XP_INLINE __attribute__((always_inline))
 
 // Calls f(std::integral_constant<int, 0>{}) .. f(std::integral_constant<int, N - 1>{}).
 template <class F, int... I>
@@ -1464,6 +1616,12 @@ const void *split_kernel(int groups, bool gather) {
                      : reinterpret_cast<const void *>(&split_gemm_kernel<split_depth(2), 2, GATED>);
 }
 
+// The persistent split kernel with the gather fused (one token group).
+template <bool GATED>
+const void *split_gathered_kernel_ptr() {
+  return reinterpret_cast<const void *>(&split_gathered_kernel<split_depth(1), GATED>);
+}
+
 int split_groups(int64_t capacity) { return capacity <= kSplitGroupTokens ? 1 : 2; }
 
 template <bool GATED, bool GATHER = false>
@@ -1552,6 +1710,14 @@ constexpr double kSplitGatherRoundUs = 3.0;
 // gate_up at 16 rows, 192 workgroups, 37.0 us plain and ~41 us with the gather fused).
 constexpr double kStreamGatherUs = 3.5;
 constexpr int64_t kSplitGatherMaxK = 4096;  // 8 staged rows of K + 16 bf16 (66 KB) beside the partial sums
+// split_gathered_kernel: two workgroups per CU (117 VGPRs; at most 80 KB of LDS each, the
+// 8 staged rows of 4096 + 16 bf16 and the partial sums), for projections with at least that
+// many units.  Its gather is one dependent round trip per workgroup before the weight
+// stream starts, and its token pieces come from LDS (no per-row L2 reads): measured on
+// MI355X, Qwen3-8B gate_up at 1 / 4 / 8 rows 35.7 / 36.0 / 36.9 us against 31.8 / 32.5 /
+// 35.7 us for the plain split kernel after a 4-5 us gather launch.
+constexpr int64_t kSplitGatheredWorkgroups = 2 * kComputeUnits;
+constexpr double kSplitPersistentGatherUs = 3.5;
 
 double decode_stream_us(int64_t n, int64_t k, int64_t workgroups, double workgroup_bytes_per_us,
                         double chip_bytes_per_us, double fixed_us) {
@@ -1715,7 +1881,8 @@ GemmChoice choose_gemm(int64_t capacity, int64_t n, int64_t k, bool gated) {
 // rows the split kernel can fuse the gather as well: each workgroup stages the rows' whole
 // K (at most kSplitGatherMaxK columns) while its first weight chunks are in flight, which
 // the model prices at kSplitGatherRoundUs per round of workgroups over the plain split
-// kernel.
+// kernel; for projections of many units, split_gathered_kernel gathers once per workgroup
+// of a two-per-CU persistent grid instead.
 GemmChoice choose_dense_gate_up(int64_t capacity, int64_t n, int64_t k, bool &fused) {
   fused = capacity <= kDecodeMaxRows && n * k * 2 <= INT32_MAX;
   if (!fused) {
@@ -1746,6 +1913,17 @@ GemmChoice choose_dense_gate_up(int64_t capacity, int64_t n, int64_t k, bool &fu
   if (capacity <= kSplitGroupTokens && k <= kSplitGatherMaxK) {
     double split_us = 0.0;
     const GemmChoice split = choose_split(capacity, n, k, split_us, true);
+    // The persistent variant prices as the split kernel at one row (its token pieces come
+    // from LDS) plus its gather round trip, when the projection has units for every slot.
+    double persistent_us = 0.0;
+    GemmChoice persistent = choose_split(1, n, k, persistent_us);
+    persistent_us += kSplitPersistentGatherUs;
+    const int64_t units = ((n + 15) / 16 * persistent.k_split + kSplitWaves - 1) / kSplitWaves;
+    if (units >= kSplitGatheredWorkgroups && persistent_us < fused_us && persistent_us < split_us &&
+        persistent_us < kGatherUs + separate_us) {
+      persistent.kind = GemmKind::SplitGathered;
+      return persistent;
+    }
     if (split_us < fused_us && split_us <= kGatherUs + separate_us) {
       return split;  // fused into the split kernel
     }
@@ -1833,6 +2011,14 @@ GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmCho
     kernel.shmem = gather ? static_cast<unsigned>(
                                 (capacity < kSplitGroupTokens ? capacity : kSplitGroupTokens) * (args.k + 16) * 2)
                           : 0u;
+  } else if (choice.kind == GemmKind::SplitGathered) {
+    // Chosen only for a Dense step's gate_up with the gather fused.
+    const int64_t row_blocks = (args.n + 15) / 16;
+    const int64_t units = (row_blocks * choice.k_split + kSplitWaves - 1) / kSplitWaves;
+    kernel.func = gated ? split_gathered_kernel_ptr<true>() : split_gathered_kernel_ptr<false>();
+    kernel.grid = dim3(static_cast<unsigned>(units < kSplitGatheredWorkgroups ? units : kSplitGatheredWorkgroups), 1, 1);
+    kernel.block = dim3(64 * kSplitWaves, 1, 1);
+    kernel.shmem = static_cast<unsigned>((capacity < kSplitGroupTokens ? capacity : kSplitGroupTokens) * (args.k + 16) * 2);
   } else if (choice.kind == GemmKind::Stream) {
     const int64_t groups = ((args.n + 15) / 16 + kStreamWaves - 1) / kStreamWaves;
     const int64_t slices = stream_slices(args.k, choice.k_slice);
@@ -1932,6 +2118,9 @@ std::string gemm_name(GemmChoice choice, bool gated) {
   if (choice.kind == GemmKind::Split) {
     return "split" + prefix + "_t" + std::to_string(kSplitGroupTokens * choice.variant) + "_k" +
            std::to_string(choice.k_split);
+  }
+  if (choice.kind == GemmKind::SplitGathered) {
+    return "split" + prefix + "_t8_k" + std::to_string(choice.k_split) + "_persistent";
   }
   if (choice.kind == GemmKind::Stream) {
     return "stream" + prefix + "_t16";

@@ -1384,7 +1384,7 @@ size_t xp_dense_gate_up_variant(int64_t capacity, int64_t hidden, int64_t interm
   if (capacity > 0 && hidden > 0 && intermediate > 0) {
     bool fused = false;
     const GemmChoice choice = choose_dense_gate_up(capacity, 2 * intermediate, hidden, fused);
-    name = gemm_name(choice, true) + (fused ? "+gather" : "");
+    name = gemm_name(choice, true) + (fused ? "+gather" : "");  // SplitGathered names itself
   }
   if (buffer != nullptr && size > 0) {
     const size_t count = std::min(size - 1, name.size());

@@ -351,7 +351,9 @@ struct GemmArgs {
   int64_t gather_divisor;
 };
 
-enum class GemmKind : int { Split = 1, Tile = 2, Stream = 3 };
+// SplitGathered: the split kernel's units walked by a persistent grid that gathers the token
+// rows once per workgroup (gate_up of a Dense step at decode sizes only).
+enum class GemmKind : int { Split = 1, Tile = 2, Stream = 3, SplitGathered = 4 };
 
 struct GemmChoice {
   GemmKind kind;

@@ -110,6 +110,9 @@ def test_config3_qwen3_8b_layer(device, rows):
     "hidden,intermediate,rows,variant",
     [
         (4096, 12288, 16, "stream_gated_t16+gather"),
+        (4096, 12288, 1, "split_gated_t8_k8_persistent+gather"),
+        (4096, 12288, 8, "split_gated_t8_k8_persistent+gather"),
+        (2560, 9728, 3, "split_gated_t8_k4_persistent+gather"),
         (1024, 3072, 1, "split_gated_t8_k4+gather"),
         (1024, 3072, 8, "split_gated_t8_k4+gather"),
         (2048, 2048, 5, "split_gated_t8_k8+gather"),
@@ -117,10 +120,11 @@ def test_config3_qwen3_8b_layer(device, rows):
 )
 def test_fused_gather_matches_separate_kernels_bitwise(device, normed, hidden, intermediate, rows, variant):
     # At decode sizes the gather (+ RMSNorm) runs inside gate_up: the stream kernel (Qwen3-8B,
-    # 16 rows) or the split kernel (hidden sizes up to 4096, up to 8 rows), which stage the
-    # same bits the gather kernel writes.  The kernel-level projections take the same kernels
-    # with the same K ranges, so the step must equal gather kernel -> gate_up -> down ->
-    # scatter bit for bit.
+    # 16 rows), the split kernel (hidden sizes up to 4096, up to 8 rows) or its persistent
+    # variant (projections of at least 512 units), which stage the same bits the gather
+    # kernel writes.  The kernel-level projections take the split or stream kernel with the
+    # same K ranges, so the step must equal gather kernel -> gate_up -> down -> scatter bit
+    # for bit.
     from crosspool_amd import dense
 
     pool_rows = 256
@@ -142,7 +146,8 @@ def test_fused_gather_matches_separate_kernels_bitwise(device, normed, hidden, i
     activated = dense.gate_up_silu(x, weights.i_proj.values)
     dense.down(activated, weights.o_proj.values, out=expected, slots=slots_d)
     torch.cuda.synchronize()
-    assert _native.gemm_variant(rows, 2 * intermediate, hidden, True) == variant.removesuffix("+gather")
+    assert _native.gemm_variant(rows, 2 * intermediate, hidden, True) == (
+        variant.removesuffix("+gather").removesuffix("_persistent"))
     assert_bitwise_equal(pool_gpu.cpu(), expected.cpu())
     _check_mailbox(pool_gpu, pool, slots, w_gate_up, w_down, norm_weight if normed else None)
 

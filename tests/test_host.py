@@ -333,14 +333,16 @@ def test_gemm_variant_selection():
 
 
 def test_dense_step_fuses_the_gather_at_decode_sizes():
-    # Qwen3-0.6B / 1.7B gate_up up to 8 rows: the split kernel stages the gathered, normalised
-    # rows itself (one round of workgroups).  Qwen3-8B up to 8 rows: a gather launch, then the
-    # split kernel with 8 K ranges (six rounds of workgroups, each of which would repeat a
-    # fused gather).  K past 4096 (the 32B TP shard's 5120) does not fit the split kernel's
-    # staging, and past 16 rows the gather is a launch of its own.
+    # Qwen3-0.6B gate_up up to 8 rows: the split kernel stages the gathered, normalised rows
+    # itself (one round of workgroups).  Qwen3-1.7B / 4B / 8B up to 8 rows (768 / 608 / 1536
+    # units): the persistent split kernel, two workgroups per CU, each gathering once.  K past
+    # 4096 (the 32B TP shard's 5120) does not fit the split kernel's staging, and past 16 rows
+    # the gather is a launch of its own.
     for rows in (1, 4, 8):
         assert _native.dense_gate_up_variant(rows, 1024, 3072) == "split_gated_t8_k4+gather"
-        assert _native.dense_gate_up_variant(rows, 4096, 12288) == "split_gated_t8_k8"
+        assert _native.dense_gate_up_variant(rows, 2048, 6144) == "split_gated_t8_k8_persistent+gather"
+        assert _native.dense_gate_up_variant(rows, 2560, 9728) == "split_gated_t8_k4_persistent+gather"
+        assert _native.dense_gate_up_variant(rows, 4096, 12288) == "split_gated_t8_k8_persistent+gather"
         assert "+gather" not in _native.dense_gate_up_variant(rows, 5120, 3200)
     assert _native.dense_gate_up_variant(16, 4096, 12288) == "stream_gated_t16+gather"
     assert _native.dense_gate_up_variant(32, 4096, 12288) == "tile_gated_64x64"
