@@ -353,15 +353,22 @@ def test_two_models_on_two_lanes(device):
         _check_mailbox(pools_gpu[instance], pools[instance], chosen[instance], w_gate_up, w_down, norm_weight)
 
 
-def test_out_of_range_slot_sets_sticky_fault(device):
-    hidden, intermediate = 1024, 3072
+@pytest.mark.parametrize(
+    "hidden,intermediate,capacity",
+    # gate_up with the gather fused: the split kernel (Qwen3-0.6B), the persistent split
+    # kernel (Qwen3-8B up to 8 rows) and the stream kernel (Qwen3-8B at 16 rows).
+    [(1024, 3072, 4), (4096, 12288, 4), (4096, 12288, 16)],
+)
+def test_out_of_range_slot_sets_sticky_fault(device, hidden, intermediate, capacity):
     pool = o.generate_hidden_states(64, hidden, 17)
     w_gate_up, w_down, _ = o.generate_layer(hidden, intermediate, 18)
     with FfnAgent(device) as agent:
         agent.register_layer(instance_index=0, layer_ordinal=0, weights=_weights(w_gate_up, w_down, device))
-        agent.materialize(maximum_row_capacity=4)
+        agent.materialize(maximum_row_capacity=capacity)
         pool_gpu = to_device(pool, device)
-        bad = slots_tensor(np.array([1, 64, 2], dtype=np.int32), device)
+        # Three rows (capacity 4), or twelve for the 16-row template; slot 64 is out of range.
+        live = [1, 2] if capacity <= 8 else [1, 2] + list(range(10, 20))
+        bad = slots_tensor(np.array([live[0], 64, *live[1:]], dtype=np.int32), device)
         agent.execute(instance_index=0, layer_ordinal=0, pool=pool_gpu, slots=bad)
         with pytest.raises(FfnHealthError):
             agent.check_health()
@@ -373,7 +380,7 @@ def test_out_of_range_slot_sets_sticky_fault(device):
         with pytest.raises(ValueError, match="hidden size"):
             agent.lanes[0].replay(instance_index=0, layer_ordinal=0, pool=narrow, slots=bad)
     got = pool_gpu.cpu()
-    untouched = np.setdiff1d(np.arange(64), [1, 2])
+    untouched = np.setdiff1d(np.arange(64), live)
     assert_bitwise_equal(got[untouched], pool[untouched])
 
 
