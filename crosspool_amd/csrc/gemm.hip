@@ -344,6 +344,15 @@ __global__ __launch_bounds__(64 * kSplitWaves) void split_gemm_kernel(GemmArgs a
     stage_gathered_rows<kSplitGroupTokens, kSplitWaves>(a, staged, rs, 0, static_cast<int>(a.k), vectors, wave,
                                                         lane, staged_rows);
     __syncthreads();
+    if (a.gathered_out != nullptr && blockIdx.x == 0) {
+      // The live rows' normalised bits for the stages after this projection.
+      const int64_t live = a.rows < staged_rows ? a.rows : staged_rows;
+      for (int64_t index = threadIdx.x; index < live * vectors; index += 64 * kSplitWaves) {
+        const int64_t t = index / vectors;
+        const int64_t c = index - t * vectors;
+        store16(a.gathered_out + t * a.k + c * 8, load16(staged + t * rs + c * 8));
+      }
+    }
   }
   if (active) {
     int c0 = 0;
@@ -1610,7 +1619,7 @@ constexpr int split_depth(int groups) { return groups == 1 ? 4 : 3; }
 template <bool GATED>
 const void *split_kernel(int groups, bool gather) {
   if (gather) {
-    return reinterpret_cast<const void *>(&split_gemm_kernel<split_depth(1), 1, GATED, GATED>);
+    return reinterpret_cast<const void *>(&split_gemm_kernel<split_depth(1), 1, GATED, true>);
   }
   return groups == 1 ? reinterpret_cast<const void *>(&split_gemm_kernel<split_depth(1), 1, GATED>)
                      : reinterpret_cast<const void *>(&split_gemm_kernel<split_depth(2), 2, GATED>);
@@ -1935,6 +1944,11 @@ GemmChoice choose_dense_gate_up(int64_t capacity, int64_t n, int64_t k, bool &fu
   return fused_choice;
 }
 
+bool split_gather_fusable(int64_t capacity, int64_t n, int64_t k) {
+  const GemmChoice choice = choose_gemm(capacity, n, k, false);
+  return choice.kind == GemmKind::Split && choice.variant == 1 && k <= kSplitGatherMaxK;
+}
+
 // K ranges whose fp32 partial sums go through scratch and the reduction kernel.
 int64_t scratch_slices(GemmChoice choice, int64_t k) {
   switch (choice.kind) {
@@ -2003,8 +2017,9 @@ GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmCho
     // one token group).
     const int64_t row_blocks = (args.n + 15) / 16;
     const int64_t per_group = kSplitWaves / choice.k_split;
-    const bool gather = fused_gather && gated;
-    kernel.func = gated ? split_kernel<true>(choice.variant, gather) : split_kernel<false>(choice.variant, false);
+    // The gather fuses into one token group (gate_up of a Dense step, the MoE router).
+    const bool gather = fused_gather && choice.variant == 1;
+    kernel.func = gated ? split_kernel<true>(choice.variant, gather) : split_kernel<false>(choice.variant, gather);
     kernel.grid = dim3(static_cast<unsigned>((row_blocks + per_group - 1) / per_group), 1, 1);
     kernel.block = dim3(64 * kSplitWaves, 1, 1);
     // Dynamic LDS beyond 64 KB: launch() opts the function in (enable_large_lds).

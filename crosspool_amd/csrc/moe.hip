@@ -52,12 +52,8 @@ __device__ __forceinline__ uint32_t ordered_bits(float value) {
 // One wavefront per row; lane l holds experts l, l + 64, ... (up to 16 each).
 constexpr int kTopkPerLane = kMoeMaxExperts / kWave;
 
-__global__ __launch_bounds__(256) void router_topk_kernel(RouterTopkArgs a) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (row >= a.rows) {
-    return;
-  }
+// TopK of row `row` by the calling wavefront (all 64 lanes).
+__device__ void router_topk_row(const RouterTopkArgs &a, int64_t row, int lane) {
   const int experts = a.experts;
   float logit[kTopkPerLane];
   float maximum = kNegativeInfinity;
@@ -154,6 +150,13 @@ __global__ __launch_bounds__(256) void router_topk_kernel(RouterTopkArgs a) {
     }
     a.ids[row * a.topk + lane] = chosen_id;
     a.weights[row * a.topk + lane] = weight;
+  }
+}
+
+__global__ __launch_bounds__(256) void router_topk_kernel(RouterTopkArgs a) {
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row < a.rows) {
+    router_topk_row(a, row, threadIdx.x & (kWave - 1));
   }
 }
 
@@ -285,6 +288,14 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(MoeSortArgs a) {
   __shared__ int tiles[kMoeMaxExperts + 1];
   __shared__ int totals[1024 / kWave];
   const int tid = threadIdx.x;
+  if (a.fused_topk != 0) {
+    // Decode sizes: the Router's TopK runs here, one wave per row (the same code as
+    // router_topk_kernel), and the routes it writes are read back below by this workgroup.
+    if ((tid >> 6) < a.topk.rows) {
+      router_topk_row(a.topk, tid >> 6, tid & (kWave - 1));
+    }
+    __syncthreads();
+  }
   counts[tid] = 0;
   int32_t held_expert[kSortRoutesPerThread];
   float held_weight[kSortRoutesPerThread];

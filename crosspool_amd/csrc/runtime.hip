@@ -453,13 +453,31 @@ struct RouterBinding {
   int precision;
   int renormalize;
   int weight_rounding;
+  // Gather fused into the MFMA projection (router_gather_fusable): the rows are mailbox rows
+  // slots[t] of pool, RMS-normalised with norm when set, and the projection stores them in
+  // x (the step's batch) as well.
+  bool fused_gather = false;
+  const uint16_t *pool = nullptr;
+  const int32_t *slots = nullptr;
+  const uint16_t *norm = nullptr;
+  uint32_t *fault = nullptr;
+  int64_t pool_rows = 0;
+  float eps = 0.0f;
 };
 
 struct RouterLaunches {
   KernelLaunch logits;         // MFMA projection or the fp32 logits kernel
   KernelLaunch logits_reduce;  // K-slice reduction of the MFMA projection, or empty
   KernelLaunch topk;
+  RouterTopkArgs topk_args;    // the TopK launch's arguments (live rows)
 };
+
+// Whether a MoE step at `capacity` rows runs its gather inside the router projection: the
+// MFMA projection on the split kernel with one token group.
+bool router_gather_fusable(const xp_moe_layer_desc &d, int64_t capacity) {
+  return router_uses_mfma(d.hidden, d.routed_experts, d.precision) &&
+         split_gather_fusable(capacity, d.routed_experts, d.hidden);
+}
 
 RouterLaunches make_router_launches(const RouterBinding &b, int64_t capacity) {
   const RouterWorkspace layout = router_workspace(capacity, b.hidden, b.experts, b.precision);
@@ -469,6 +487,15 @@ RouterLaunches make_router_launches(const RouterBinding &b, int64_t capacity) {
     // logits = bf16(x . w^T): the Dense projection kernels, no epilogue.
     GemmArgs args{};
     args.x = b.x;
+    if (b.fused_gather) {
+      args.x = b.pool;
+      args.gather_slots = b.slots;
+      args.norm = b.norm;
+      args.fault = b.fault;
+      args.pool_rows = b.pool_rows;
+      args.eps = b.eps;
+      args.gathered_out = const_cast<uint16_t *>(b.x);
+    }
     args.w = static_cast<const uint16_t *>(b.w);
     args.out = static_cast<uint16_t *>(logits);
     args.partials = layout.scratch_bytes > 0 ? reinterpret_cast<float *>(b.workspace + layout.scratch) : nullptr;
@@ -479,7 +506,8 @@ RouterLaunches make_router_launches(const RouterBinding &b, int64_t capacity) {
     args.n = b.experts;
     args.k = b.hidden;
     args.act = default_activation();
-    const GemmLaunch gemm = make_gemm(args, capacity, false, choose_gemm(capacity, b.experts, b.hidden, false));
+    const GemmLaunch gemm =
+        make_gemm(args, capacity, false, choose_gemm(capacity, b.experts, b.hidden, false), b.fused_gather);
     launches.logits = gemm.main;
     launches.logits_reduce = gemm.reduce;
   } else {
@@ -511,6 +539,7 @@ RouterLaunches make_router_launches(const RouterBinding &b, int64_t capacity) {
   launches.topk = make_router_topk(topk);
   topk.rows = b.rows;
   launches.topk.set_args(topk);
+  launches.topk_args = topk;
   return launches;
 }
 
@@ -533,6 +562,8 @@ struct ExpertsBinding {
   int64_t topk;
   float scale;
   GatedSilu act;
+  // The Router's TopK run by the sort kernel (at most 16 rows, no shared experts), or null.
+  const RouterTopkArgs *fused_topk = nullptr;
 };
 
 struct ExpertsLaunches {
@@ -570,6 +601,10 @@ int make_experts_launches(const ExpertsBinding &b, int64_t capacity, ExpertsLaun
   sort.experts = static_cast<int32_t>(b.experts);
   sort.tile_rows = tile_rows;
   sort.max_tiles = max_tiles;
+  if (b.fused_topk != nullptr) {
+    sort.topk = *b.fused_topk;
+    sort.fused_topk = 1;
+  }
   out.sort = make_moe_sort(sort);
 
   // gate_up gathers the token row of each sorted route (route / topk) itself and writes the
@@ -743,17 +778,24 @@ int make_moe_step(const Layer &layer, const MoeStepBinding &b, int64_t capacity,
   float *final_weights = reinterpret_cast<float *>(b.workspace + layout.final_weights);
   const int64_t topk = effective_topk(d);
 
-  GatherArgs gather{};
-  gather.pool = b.pool_in;
-  gather.slots = b.slots;
-  gather.norm = layer.norm;
-  gather.out = batch;
-  gather.fault = b.fault;
-  gather.pool_rows = b.pool_rows;
-  gather.hidden = d.hidden;
-  gather.rows = b.rows;
-  gather.eps = layer.eps;
-  chain.add(make_gather(gather, capacity));
+  // At decode sizes the gather runs inside the router projection and the TopK inside the
+  // route sort (two launches fewer; the same kernels' code, so the same bits).  Both follow
+  // from the capacity, so a template's node list matches every replay's.
+  const bool fuse_gather = router_gather_fusable(d, capacity);
+  const bool fuse_topk = capacity <= kMoeFusedTopkRows && topk == d.routed_topk;
+  if (!fuse_gather) {
+    GatherArgs gather{};
+    gather.pool = b.pool_in;
+    gather.slots = b.slots;
+    gather.norm = layer.norm;
+    gather.out = batch;
+    gather.fault = b.fault;
+    gather.pool_rows = b.pool_rows;
+    gather.hidden = d.hidden;
+    gather.rows = b.rows;
+    gather.eps = layer.eps;
+    chain.add(make_gather(gather, capacity));
+  }
 
   RouterBinding router{};
   router.x = batch;
@@ -770,10 +812,21 @@ int make_moe_step(const Layer &layer, const MoeStepBinding &b, int64_t capacity,
   router.precision = d.precision;
   router.renormalize = d.renormalize;
   router.weight_rounding = d.weight_rounding;
+  if (fuse_gather) {
+    router.fused_gather = true;
+    router.pool = b.pool_in;
+    router.slots = b.slots;
+    router.norm = layer.norm;
+    router.fault = b.fault;
+    router.pool_rows = b.pool_rows;
+    router.eps = layer.eps;
+  }
   const RouterLaunches routing = make_router_launches(router, capacity);
   chain.add(routing.logits);
   chain.add(routing.logits_reduce);
-  chain.add(routing.topk);
+  if (!fuse_topk) {
+    chain.add(routing.topk);
+  }
 
   if (topk > d.routed_topk) {
     // Shared experts: every live row also takes slots routed_experts + s (weight
@@ -812,6 +865,9 @@ int make_moe_step(const Layer &layer, const MoeStepBinding &b, int64_t capacity,
   experts.topk = topk;
   experts.scale = d.routed_scaling_factor;
   experts.act = GatedSilu{d.alpha, d.limit, d.up_offset};
+  if (fuse_topk) {
+    experts.fused_topk = &routing.topk_args;
+  }
   ExpertsLaunches launches;
   if (const int status = make_experts_launches(experts, capacity, launches); status != XP_OK) {
     return status;

@@ -211,9 +211,17 @@ struct FinalizeRoutingArgs {
 
 // Route sort: routes (row * topk + slot) grouped by expert, and the expert tile table of
 // the grouped projections.
+// Rows up to which a MoE step's route sort (one 1024-thread workgroup, one wave per row) also
+// runs the Router's TopK.
+constexpr int64_t kMoeFusedTopkRows = 16;
+
 struct MoeSortArgs {
   const int32_t *ids;        // [routes] expert of each route, -1 = no route
   const float *weights;      // [routes] route weights
+  // Router TopK fused into the sort (fused_topk != 0, at most 16 rows): wave w first picks
+  // row w's routes from topk.logits into topk.ids / topk.weights (= ids / weights above).
+  RouterTopkArgs topk;
+  int32_t fused_topk;
   float *sorted_weight;      // [routes] weight of the route at each sorted position
   int32_t *expert_end;       // [experts] one past the expert's last sorted position
   int32_t *sorted_route;     // [routes] route at each sorted position
@@ -336,6 +344,9 @@ struct GemmArgs {
   uint32_t *fault;
   int64_t pool_rows;
   float eps;
+  // Split kernel with the gather fused (the MoE step's router projection): workgroup 0 also
+  // stores the live normalised rows here ([rows, k], row stride k) for the later stages.
+  uint16_t *gathered_out;
   // Grouped projection (MoE experts: the tile kernel without a K split, or the grouped
   // split kernel): grid row y is entry y of an expert tile table over rows sorted by
   // expert; the tile multiplies rows [tile_row0[y], min(tile_row0[y] + BM,
@@ -367,6 +378,10 @@ GemmChoice choose_gemm(int64_t capacity, int64_t n, int64_t k, bool gated);
 // The gate_up of a Dense step: at decode sizes the stream kernel with the mailbox gather
 // fused (`fused` set), otherwise choose_gemm's kernel after a separate gather.
 GemmChoice choose_dense_gate_up(int64_t capacity, int64_t n, int64_t k, bool &fused);
+// Whether choose_gemm's kernel for an ungated projection at `capacity` rows can take the
+// mailbox gather fused: the split kernel with one token group and K <= 4096 (the MoE step's
+// router projection then gathers and normalises the rows itself).
+bool split_gather_fusable(int64_t capacity, int64_t n, int64_t k);
 // Device scratch (fp32 partial sums of the K slices) a projection at `capacity` rows
 // needs; 0 when its kernel reduces K inside one workgroup.
 size_t gemm_scratch_bytes(GemmChoice choice, int64_t capacity, int64_t n, int64_t k);
@@ -379,9 +394,9 @@ struct GemmLaunch {
   KernelLaunch reduce;
 };
 // `fused_gather`: the gate_up of a Dense step whose choose_dense_gate_up decision fused the
-// mailbox gather (the kernel variant follows that decision, not whether the argument record
-// already holds slot pointers, so a template captured with placeholder arguments has the
-// nodes its replays launch).
+// mailbox gather, or a projection for which split_gather_fusable holds (the kernel variant
+// follows that decision, not whether the argument record already holds slot pointers, so a
+// template captured with placeholder arguments has the nodes its replays launch).
 GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmChoice choice,
                      bool fused_gather = false);
 // The grouped projection over an expert tile table of `max_tiles` entries (a multiple of

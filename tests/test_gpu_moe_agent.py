@@ -168,7 +168,9 @@ def _register(agent, spec, hidden, w_gate_up, w_down, projection, correction, no
 # (hidden, intermediate, spec, corrected, normed, maximum capacity, replay rows)
 CASES = [
     pytest.param(
-        512, 256, MoeLayerSpec(routed_expert_count=16, routed_topk=4), False, True, 64, (1, 5, 33, 64),
+        # 1 and 5 rows: gather fused into the router projection and TopK into the route sort;
+        # 12 rows: TopK fused only; 33 and 64: neither.
+        512, 256, MoeLayerSpec(routed_expert_count=16, routed_topk=4), False, True, 64, (1, 5, 12, 33, 64),
         id="softmax-payload-normed",
     ),
     pytest.param(
@@ -268,7 +270,8 @@ def test_moe_graph_dispatch_and_operator_chain_repeat_the_replay(device):
 
 def test_qwen3_30b_a3b_moe_layer_through_the_lane(device):
     # Qwen3-30B-A3B MoE layer: hidden 2048, moe_intermediate 768, 128 experts, top-8, softmax,
-    # renormalised (norm_topk_prob), post-attention RMSNorm fused into the gather.  32 rows take
+    # renormalised (norm_topk_prob), post-attention RMSNorm fused into the gather.  1 row runs
+    # the gather inside the router projection and the TopK inside the route sort, 32 rows take
     # the grouped split kernel (capacity 32), 200 rows the grouped tile kernel (capacity 256).
     hidden, intermediate = 2048, 768
     spec = MoeLayerSpec(routed_expert_count=128, routed_topk=8)
@@ -277,7 +280,7 @@ def test_qwen3_30b_a3b_moe_layer_through_the_lane(device):
     with FfnAgent(device) as agent:
         _register(agent, spec, hidden, w_gate_up, w_down, projection, correction, norm_weight, device)
         agent.materialize(maximum_row_capacity=256)
-        for rows in (32, 200):
+        for rows in (1, 32, 200):
             print(f"case qwen3-30b-a3b rows={rows}", flush=True)
             pool = o.generate_hidden_states(320, hidden, 601 + rows)
             slots = o.generate_slots(320, rows, 602 + rows)
