@@ -113,6 +113,8 @@ def test_config3_qwen3_8b_layer(device, rows):
         (4096, 12288, 1, "split_gated_t8_k8_persistent+gather"),
         (4096, 12288, 8, "split_gated_t8_k8_persistent+gather"),
         (2560, 9728, 3, "split_gated_t8_k4_persistent+gather"),
+        # K = 4088: the last K range ends inside a 128-wide chunk; 513 units over 512 workgroups.
+        (4088, 4104, 5, "split_gated_t8_k8_persistent+gather"),
         (1024, 3072, 1, "split_gated_t8_k4+gather"),
         (1024, 3072, 8, "split_gated_t8_k4+gather"),
         (2048, 2048, 5, "split_gated_t8_k8+gather"),
