@@ -420,11 +420,19 @@ def test_ffn_shim_matches_dense_partial(device):
         agent.close()
 
 
-def test_graph_dispatch_matches_direct_dispatch(device):
+@pytest.mark.parametrize(
+    "hidden,intermediate,sequence",
+    [
+        (1024, 3072, ((0, 3), (1, 3), (0, 3), (0, 150), (1, 17), (1, 17))),
+        # Qwen3-8B: the persistent split kernel (3, 8 rows), the fused stream kernel (12) and
+        # the decode tiles (40), each with its dynamic LDS opt-in under capture.
+        (4096, 12288, ((0, 3), (1, 3), (0, 8), (1, 12), (1, 17), (0, 40))),
+    ],
+)
+def test_graph_dispatch_matches_direct_dispatch(device, hidden, intermediate, sequence):
     # The same replays through the instantiated hipGraphs (rebinding only changed nodes) and
     # through direct kernel launches give identical bits; alternating layers and row counts
     # exercise the rebinding.
-    hidden, intermediate = 1024, 3072
     pool = o.generate_hidden_states(256, hidden, 17)
     layers = [o.generate_layer(hidden, intermediate, 40 + index) for index in range(2)]
     slots = slots_tensor(o.generate_slots(256, 200, 19), device)
@@ -439,7 +447,7 @@ def test_graph_dispatch_matches_direct_dispatch(device):
             agent.materialize(maximum_row_capacity=200)
             assert agent.lanes[0].graph_dispatch is graph_dispatch
             outputs = []
-            for ordinal, rows in ((0, 3), (1, 3), (0, 3), (0, 150), (1, 17), (1, 17)):
+            for ordinal, rows in sequence:
                 pool_gpu = to_device(pool, device)
                 agent.execute(instance_index=0, layer_ordinal=ordinal, pool=pool_gpu, slots=slots, rows=rows)
                 agent.lanes[0].synchronize()
