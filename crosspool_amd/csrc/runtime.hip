@@ -454,9 +454,10 @@ struct RouterBinding {
   int renormalize;
   int weight_rounding;
   // Gather fused into the MFMA projection (router_gather_fusable): the rows are mailbox rows
-  // slots[t] of pool, RMS-normalised with norm when set, and the projection stores them in
-  // x (the step's batch) as well.
+  // slots[t] of pool, RMS-normalised with norm when set, and the projection also stores them
+  // in batch_out (the step's batch, which x names).
   bool fused_gather = false;
+  uint16_t *batch_out = nullptr;
   const uint16_t *pool = nullptr;
   const int32_t *slots = nullptr;
   const uint16_t *norm = nullptr;
@@ -494,7 +495,7 @@ RouterLaunches make_router_launches(const RouterBinding &b, int64_t capacity) {
       args.fault = b.fault;
       args.pool_rows = b.pool_rows;
       args.eps = b.eps;
-      args.gathered_out = const_cast<uint16_t *>(b.x);
+      args.gathered_out = b.batch_out;
     }
     args.w = static_cast<const uint16_t *>(b.w);
     args.out = static_cast<uint16_t *>(logits);
@@ -814,6 +815,7 @@ int make_moe_step(const Layer &layer, const MoeStepBinding &b, int64_t capacity,
   router.weight_rounding = d.weight_rounding;
   if (fuse_gather) {
     router.fused_gather = true;
+    router.batch_out = batch;
     router.pool = b.pool_in;
     router.slots = b.slots;
     router.norm = layer.norm;
