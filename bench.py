@@ -17,8 +17,11 @@ calibration, then gate_up at the headline and decode sizes), for
 ``rocprofv3 --pmc`` runs; ``profiles/traffic.json`` records their result.
 
 ``--ceilings`` instead measures the hardware limits the kernels are judged
-against (libxpool_probes.so): a pure-MFMA loop, two HBM read patterns and the
-GPU idle time a hipGraphLaunch adds per replay, and prints them as one JSON line.
+against (libxpool_probes.so): a pure-MFMA loop, two HBM read patterns, the
+GPU idle time a hipGraphLaunch adds per replay, and the cost of a grid-wide
+dependency (a kernel boundary against an in-kernel counter handoff; with
+``--cooperative`` also the runtime's grid barrier), and prints them as one JSON
+line.
 """
 
 from __future__ import annotations
@@ -79,6 +82,10 @@ def parse_args() -> argparse.Namespace:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--kernels-only", action="store_true", help="launch only the profiled kernels, then exit")
     parser.add_argument("--ceilings", action="store_true", help="measure the hardware ceilings, then exit")
+    parser.add_argument("--cooperative", action="store_true",
+                        help="with --ceilings: also time the runtime's cooperative grid barrier (rocprofv3 "
+                             "ends with a segmentation fault at exit after a cooperative launch, before its "
+                             "trace files are written, so traced runs leave this out)")
     parser.add_argument("--prewarm-seconds", type=float, default=2.0,
                         help="untimed replays before the headline's warmup, so clocks are at steady state")
     return parser.parse_args()
@@ -149,7 +156,7 @@ def mfma_ceiling(stream) -> dict:
             "clock_ghz": round(cycles / (ticks * 10.0), 3) if ticks > 0 else None}
 
 
-def run_ceilings(device) -> dict:
+def run_ceilings(device, cooperative: bool = False) -> dict:
     """Hardware limits measured with HIP events on the current stream (see the module doc)."""
 
     import ctypes
@@ -259,6 +266,40 @@ def run_ceilings(device) -> dict:
             graph_points["graph" if graph_dispatch else "direct"] = begin.elapsed_time(end) * 1e3 / 200
     result["replay_us_qwen3_0_6b_t1"] = {key: round(value, 2) for key, value in graph_points.items()}
     result["graph_launch_extra_us"] = round(graph_points["graph"] - graph_points["direct"], 2)
+
+    # A grid-wide dependency: empty kernels back to back, a producer -> consumer handoff
+    # across a kernel boundary and inside one launch (one counter, or a counter per 8
+    # producers), and the runtime's cooperative grid barrier.
+    result["empty_kernel_us"] = round(per_launch(
+        lambda index=0: checked(probes.xp_probe_empty(256, handle)), 200) * 1e6, 2)
+    words = torch.zeros(512 * 8, dtype=torch.int32, device=device)
+    counters = torch.zeros(64 * 32, dtype=torch.int32, device=device)
+    flag = torch.zeros(1, dtype=torch.int32, device=device)
+    handoff = []
+    for producers, consumers in ((192, 64), (192, 256), (512, 64), (512, 256)):
+        point = {"producers": producers, "consumers": consumers}
+        for mode, name in ((0, "two_kernels_us"), (1, "one_launch_one_counter_us"),
+                           (2, "one_launch_counter_per_8_us")):
+            counters.zero_()
+            epoch = [0]
+
+            def launch(index=0, mode=mode, producers=producers, consumers=consumers):
+                epoch[0] += 1
+                checked(probes.xp_probe_handoff(
+                    producers, consumers, mode, ctypes.c_void_p(words.data_ptr()),
+                    ctypes.c_void_p(counters.data_ptr()), ctypes.c_uint32(epoch[0]), ctypes.c_uint32(epoch[0]),
+                    ctypes.c_void_p(flag.data_ptr()), handle))
+
+            point[name] = round(per_launch(launch, 200) * 1e6, 2)
+        handoff.append(point)
+    torch.cuda.synchronize(device)
+    result["handoff"] = {"points": handoff, "flag": int(flag.item())}
+    if not cooperative:
+        return result
+    sync_times = {syncs: per_launch(lambda index=0, syncs=syncs: checked(probes.xp_probe_grid_sync(256, syncs, handle)),
+                                    20) * 1e6 for syncs in (1, 11)}
+    result["cooperative_grid_sync"] = {"workgroups": 256, "launch_with_one_sync_us": round(sync_times[1], 2),
+                                       "per_further_sync_us": round((sync_times[11] - sync_times[1]) / 10, 2)}
     return result
 
 
@@ -283,7 +324,7 @@ def main() -> int:
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
     if args.ceilings:
-        print(json.dumps({"ceilings": run_ceilings(device)}), flush=True)
+        print(json.dumps({"ceilings": run_ceilings(device, args.cooperative)}), flush=True)
         return 0
     max_tokens = max(SWEEP + (args.tokens, args.decode_tokens))
 

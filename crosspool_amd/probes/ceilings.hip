@@ -20,10 +20,21 @@
 //    lines) or 8 rows x 128 bytes (whole lines) per instruction, 16 KB per wave in flight;
 //    grid y splits each row into `ranges` contiguous parts (more workgroups for the same
 //    bytes).
+//  * probe_handoff: the cost of a grid-wide dependency.  `producers` workgroups each store
+//    8 words; `consumers` workgroups then read all of them.  Three forms: two kernels back
+//    to back (the stream orders them), or one launch in which the producers (the lower
+//    workgroup ids, dispatched first, never waiting) publish with an agent-scope release
+//    and an atomic increment, and the consumers wait for the count with a bounded, sleeping
+//    poll and an agent-scope acquire; the count is one word, or one word per 8 producers on
+//    lines of its own polled lane by lane.  Every consumer checks the words and sets `flag`
+//    on a mismatch (1) or an expired wait (2).
+//  * probe_grid_sync: a cooperative launch whose workgroups pass `syncs` grid-wide
+//    barriers of the HIP runtime (cooperative_groups grid sync).
 //
 // Each kernel folds what it reads (or computes) into registers and stores it only when
 // `write` is set, which the host never does; the compiler cannot drop the work.
 
+#include <hip/hip_cooperative_groups.h>
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -175,6 +186,101 @@ __global__ __launch_bounds__(512) void probe_read_rows_kernel(const char *matrix
   }
 }
 
+__global__ __launch_bounds__(512) void probe_empty_kernel(uint32_t *sink) {
+  if (blockIdx.x == 0x7fffffffu) {
+    sink[0] = 1u;
+  }
+}
+
+constexpr int kHandoffWords = 8;
+constexpr int kHandoffSpinLimit = 1 << 22;  // polls of ~64 cycles each: ~0.1 s, then flag 2
+
+__device__ __forceinline__ void handoff_produce(uint32_t *words, int producer, uint32_t salt) {
+  if (threadIdx.x < kHandoffWords) {
+    words[producer * kHandoffWords + threadIdx.x] = producer * kHandoffWords + threadIdx.x + salt;
+  }
+}
+
+__device__ __forceinline__ void handoff_consume(const uint32_t *words, int producers, uint32_t salt,
+                                                uint32_t *flag) {
+  uint32_t bad = 0;
+  for (int i = threadIdx.x; i < producers * kHandoffWords; i += blockDim.x) {
+    bad |= words[i] != static_cast<uint32_t>(i) + salt ? 1u : 0u;
+  }
+  if (bad != 0) {
+    atomicOr(flag, 1u);
+  }
+}
+
+__global__ __launch_bounds__(512) void probe_produce_kernel(uint32_t *words, uint32_t salt) {
+  handoff_produce(words, blockIdx.x, salt);
+}
+
+__global__ __launch_bounds__(512) void probe_consume_kernel(const uint32_t *words, int producers, uint32_t salt,
+                                                            uint32_t *flag) {
+  handoff_consume(words, producers, salt, flag);
+}
+
+// counters: SPREAD ? one word per 8 producers, 32 words (128 bytes) apart : one word.  Each
+// counter grows by its producers' count per launch; `epoch` is the launch's 1-based number
+// since the counters were zeroed.
+template <bool SPREAD>
+__global__ __launch_bounds__(512) void probe_handoff_kernel(uint32_t *words, int producers, uint32_t *counters,
+                                                            uint32_t epoch, uint32_t salt, uint32_t *flag) {
+  if (static_cast<int>(blockIdx.x) < producers) {
+    handoff_produce(words, blockIdx.x, salt);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+      __hip_atomic_fetch_add(counters + (SPREAD ? (blockIdx.x / 8) * 32 : 0), 1u, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return;
+  }
+  __shared__ int expired;
+  if (threadIdx.x < 64) {
+    const int groups = SPREAD ? (producers + 7) / 8 : 1;
+    bool done = false;
+    for (int spin = 0; spin < kHandoffSpinLimit; ++spin) {
+      bool mine = true;
+      for (int c = threadIdx.x; c < groups; c += 64) {
+        const int members = SPREAD ? (producers - 8 * c < 8 ? producers - 8 * c : 8) : producers;
+        mine = mine && __hip_atomic_load(counters + c * 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >=
+                           epoch * static_cast<uint32_t>(members);
+      }
+      done = __all(mine);
+      if (done) {
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    if (threadIdx.x == 0) {
+      expired = done ? 0 : 1;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  }
+  __syncthreads();
+  if (expired != 0) {
+    if (threadIdx.x == 0) {
+      atomicOr(flag, 2u);
+    }
+    return;
+  }
+  handoff_consume(words, producers, salt, flag);
+}
+
+__global__ __launch_bounds__(512) void probe_grid_sync_kernel(int syncs, uint32_t *sink) {
+  cooperative_groups::grid_group grid = cooperative_groups::this_grid();
+  uint32_t value = 0;
+  for (int i = 0; i < syncs; ++i) {
+    value += blockIdx.x;
+    grid.sync();
+  }
+  if (value == 0xffffffffu) {
+    sink[0] = value;
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -224,6 +330,44 @@ int xp_probe_read_rows(const void *matrix, int64_t rows, int64_t row_bytes, int 
   hipLaunchKernelGGL(kernel, grid, dim3(512), 0, static_cast<hipStream_t>(stream), static_cast<const char *>(matrix),
                      rows, row_bytes, row_bytes / ranges, static_cast<uint32_t *>(nullptr), 0);
   return static_cast<int>(hipGetLastError());
+}
+
+// `workgroups` empty 512-thread workgroups.
+int xp_probe_empty(int workgroups, void *stream) {
+  hipLaunchKernelGGL(probe_empty_kernel, dim3(workgroups), dim3(512), 0, static_cast<hipStream_t>(stream),
+                     static_cast<uint32_t *>(nullptr));
+  return static_cast<int>(hipGetLastError());
+}
+
+// One producer -> consumer handoff (mode 0 two kernels, 1 one launch with one counter, 2 one
+// launch with a counter per 8 producers).  words: producers x 8 words; counters: zeroed
+// before the first launch of a series, 32 x ceil(producers / 8) words (one in mode 1);
+// epoch: the launch's 1-based number in its series; flag: one word, zeroed by the caller.
+int xp_probe_handoff(int producers, int consumers, int mode, uint32_t *words, uint32_t *counters, uint32_t epoch,
+                     uint32_t salt, uint32_t *flag, void *stream) {
+  if (producers < 1 || consumers < 1 || mode < 0 || mode > 2) {
+    return -1;
+  }
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (mode == 0) {
+    hipLaunchKernelGGL(probe_produce_kernel, dim3(producers), dim3(512), 0, s, words, salt);
+    hipLaunchKernelGGL(probe_consume_kernel, dim3(consumers), dim3(512), 0, s, words, producers, salt, flag);
+  } else {
+    auto kernel = mode == 1 ? probe_handoff_kernel<false> : probe_handoff_kernel<true>;
+    hipLaunchKernelGGL(kernel, dim3(producers + consumers), dim3(512), 0, s, words, producers, counters, epoch, salt,
+                       flag);
+  }
+  return static_cast<int>(hipGetLastError());
+}
+
+// A cooperative launch of `workgroups` 512-thread workgroups passing `syncs` grid barriers.
+int xp_probe_grid_sync(int workgroups, int syncs, void *stream) {
+  uint32_t *sink = nullptr;
+  void *args[] = {&syncs, &sink};
+  const hipError_t status = hipLaunchCooperativeKernel(reinterpret_cast<const void *>(probe_grid_sync_kernel),
+                                                       dim3(workgroups), dim3(512), args, 0,
+                                                       static_cast<hipStream_t>(stream));
+  return static_cast<int>(status);
 }
 
 }  // extern "C"
