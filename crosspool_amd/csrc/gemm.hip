@@ -206,6 +206,25 @@ __device__ __forceinline__ void stage_gathered_rows(const GemmArgs &a, uint16_t 
   }
 }
 
+using lds_void_t = __attribute__((address_space(3))) void *;
+
+// Direct global -> LDS load of 16 bytes per lane through a buffer resource: lane i's
+// data lands at `lds_row_base + 16 i`; offsets past the resource's end write zeros.
+template <int POLICY = 0>
+__device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t rsrc, void *lds_base, uint32_t voffset,
+                                                  uint32_t soffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t)(lds_base), 16, static_cast<int>(voffset),
+                                           static_cast<int>(soffset), 0, POLICY);
+}
+
+// s_waitcnt with vmcnt <= N and the LDS / export counters left unconstrained (gfx9 encoding:
+// vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit counter");
+  __builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+}
+
 // ------------------------------------------------------------------ split (decode)
 // Weight-streaming projection for at most 16 live rows (HBM-bound).  A workgroup of 8
 // waves covers 8 / KSPLIT weight-row blocks of 16 rows; the KSPLIT waves of a block each
@@ -448,14 +467,27 @@ __global__ __launch_bounds__(64 * kSplitWaves) void split_gemm_kernel(GemmArgs a
 // A unit is the 8 / ksplit row blocks x ksplit K ranges one workgroup of the split kernel
 // covers (wave w: row block unit * (8 / ksplit) + w / ksplit, K range w % ksplit);
 // workgroup g takes units g, g + gridDim.x, ...  The token rows (one group of 8, K <=
-// kSplitGatherMaxK) are gathered and RMS-normalised into LDS once per workgroup, with no
-// weight loads in flight beside it (their registers would keep the kernel from two
-// workgroups per CU), so the gather costs one round trip per workgroup instead of one per
-// unit, and one workgroup's K-range sum and stores overlap the other's weight stream.  The
-// arithmetic per unit is split_gemm_kernel's (same chunk order, same fixed-order sum), so
-// the results are bit for bit the split kernel's.
+// kSplitGatherMaxK) are gathered and RMS-normalised into LDS once per workgroup, so the
+// gather costs one round trip per workgroup instead of one per unit, and one workgroup's
+// K-range sum and stores overlap the other's weight stream.
+//
+// The gather runs under the first unit's weight stream: the first DEPTH weight chunks are
+// requested first, then the slots, then the mailbox rows and the norm weights, which go
+// straight into LDS (no registers beside the weight buffers, so two workgroups still fit
+// on a CU).  Wave w then sums the squares of row w from LDS in the gather kernel's order
+// (lane i over its chunks i, i + 64, ...; rms_inverse's wave reduction) and normalises the
+// row in place, so the staged bits are gather_rows_kernel's.  The arithmetic per unit is
+// split_gemm_kernel's (same chunk order, same fixed-order sum), so the results are bit for
+// bit the split kernel's.
+//
+// Dynamic LDS: min(capacity, 8) rows of K + 16 bf16, then kSplitGatheredScratchBytes shared
+// by the norm weights (while staging) and the K-range partial sums (after each unit).
+constexpr int kSplitGatheredScratchBytes = (kSplitWaves - 1) * 2 * 64 * 16;
+
 template <int DEPTH, bool GATED>
-__global__ __launch_bounds__(64 * kSplitWaves) void split_gathered_kernel(GemmArgs a) {
+__global__ __launch_bounds__(64 * kSplitWaves) __attribute__((amdgpu_waves_per_eu(4))) void split_gathered_kernel(
+    GemmArgs a) {
+  static_assert(kSplitGroupTokens == kSplitWaves, "wave w stages token row w");
   extern __shared__ __attribute__((aligned(16))) uint16_t staged[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
@@ -472,6 +504,8 @@ __global__ __launch_bounds__(64 * kSplitWaves) void split_gathered_kernel(GemmAr
   const u32x4 zero = {0u, 0u, 0u, 0u};
   const int64_t rs = a.k + 16;  // staged row stride in elements
   const int staged_rows = a.capacity < kSplitGroupTokens ? static_cast<int>(a.capacity) : kSplitGroupTokens;
+  uint16_t *scratch = staged + staged_rows * rs;  // norm weights, then partial sums
+  f32x4(*partial)[2][64] = reinterpret_cast<f32x4(*)[2][64]>(scratch);
   const int k0 = part * static_cast<int>(a.k_slice);
   const int k_range = static_cast<int>(a.k - k0 < a.k_slice ? a.k - k0 : a.k_slice);
   const int chunks = (k_range + 127) / 128;
@@ -480,36 +514,139 @@ __global__ __launch_bounds__(64 * kSplitWaves) void split_gathered_kernel(GemmAr
   const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(a.w, static_cast<uint32_t>(a.n * a.k * 2));
   const uint32_t w_half = static_cast<uint32_t>(8 * a.k * 2);
 
-  stage_gathered_rows<kSplitGroupTokens, kSplitWaves>(a, staged, rs, 0, static_cast<int>(a.k),
-                                                      static_cast<int>(a.k / 8), wave, lane, staged_rows);
-  __syncthreads();
+  // The unit being worked on: its row block, whether this wave has one, its chunk rotation
+  // and its weight offset.
+  int64_t rb = 0;
+  bool active = false;
+  int rotation = 0;
+  uint32_t w_off = 0;
+  auto enter_unit = [&](int64_t unit) XP_INLINE {
+    rb = unit * per_unit + block_in_unit;
+    active = unit < units && rb < row_blocks;
+    rotation = static_cast<int>((rb * 7) % chunks);
+    w_off = static_cast<uint32_t>(((rb * 16 + row) * a.k + k0 + piece * 8) * 2);
+  };
+  auto column_of = [&](int chunk) XP_INLINE {
+    const int c = chunk + rotation;
+    return (c < chunks ? c : c - chunks) * 128;
+  };
+  u32x4 wbuf[DEPTH][4];
+  auto load_chunk = [&](int chunk, u32x4 (&w)[4]) XP_INLINE {
+    const bool in_range = chunk < chunks;
+    const uint32_t column = static_cast<uint32_t>(column_of(chunk)) * 2;
+#pragma unroll
+    for (int line = 0; line < 2; ++line) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        w[2 * line + h] = buffer_load16<kLoadNontemporal>(
+            w_rsrc, in_range ? w_off + h * w_half + column + line * 128 : kOutOfRange);
+      }
+    }
+  };
+
+  // Wave w stages token row w: its mailbox row, -1 past the live rows, -2 for a slot outside
+  // the mailbox.  The slot is read before the weight chunks are requested, so waiting for it
+  // waits for nothing else.
+  const int t = wave;
+  int64_t source = -1;
+  if (t < a.rows) {
+    const int32_t slot = a.gather_slots[t];
+    source = slot < 0 || static_cast<int64_t>(slot) >= a.pool_rows ? -2 : slot;
+  }
+  enter_unit(blockIdx.x);
+  if (active) {
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      load_chunk(d, wbuf[d]);
+    }
+  }
+
+  // Gather (rows past the live rows are zero, a slot outside the mailbox gives a row of
+  // quiet NaNs and raises the fault bit).
+  {
+    const int row_chunks = static_cast<int>(a.k / 8);  // <= 8 * 64
+    uint16_t *token = staged + t * rs;
+    if (source >= 0 && t < staged_rows) {
+      const __amdgpu_buffer_rsrc_t x_rsrc = make_rsrc(a.x, static_cast<uint32_t>(a.pool_rows * a.ldx * 2));
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        if (b * kWave < row_chunks && lane + b * kWave < row_chunks) {
+          buffer_load_lds16(x_rsrc, token + b * kWave * 8,
+                            static_cast<uint32_t>((source * a.ldx + (lane + b * kWave) * 8) * 2), 0u);
+        }
+      }
+    }
+    if (a.norm != nullptr && lane + wave * kWave < row_chunks) {
+      const __amdgpu_buffer_rsrc_t n_rsrc = make_rsrc(a.norm, static_cast<uint32_t>(a.k * 2));
+      buffer_load_lds16(n_rsrc, scratch + wave * kWave * 8, static_cast<uint32_t>((lane + wave * kWave) * 16), 0u);
+    }
+    wait_vmcnt<0>();  // the rows and norm weights (and the weight chunks issued before them)
+    __syncthreads();
+    if (t < staged_rows) {
+      if (source >= 0) {
+        if (a.norm != nullptr) {
+          // Two LDS reads in flight at a time; chunks past the row read chunk 0 and count as
+          // zeros (adding +0 to the non-negative sum leaves its bits unchanged).
+          float squares = 0.0f;
+#pragma unroll
+          for (int pair = 0; pair < 4; ++pair) {
+            u32x4 v[2];
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+              const int c = lane + (2 * pair + u) * kWave;
+              v[u] = load16(token + (c < row_chunks ? c : 0) * 8);
+            }
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+              add_squares(lane + (2 * pair + u) * kWave < row_chunks ? v[u] : zero, squares);
+            }
+          }
+          const float scale = rms_inverse(squares, a.k, a.eps);
+#pragma unroll
+          for (int pair = 0; pair < 4; ++pair) {
+            u32x4 v[2];
+            u32x4 w[2];
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+              const int c = lane + (2 * pair + u) * kWave;
+              v[u] = load16(token + (c < row_chunks ? c : 0) * 8);
+              w[u] = load16(scratch + (c < row_chunks ? c : 0) * 8);
+            }
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+              const int c = lane + (2 * pair + u) * kWave;
+              if (c < row_chunks) {
+                store16(token + c * 8, normalize_chunk(v[u], scale, w[u]));
+              }
+            }
+          }
+        }
+      } else {
+        const u32x4 poison = {kPoisonBf16x2, kPoisonBf16x2, kPoisonBf16x2, kPoisonBf16x2};
+        const u32x4 fill = source == -2 ? poison : zero;
+        for (int c = lane; c < row_chunks; c += kWave) {
+          store16(token + c * 8, fill);
+        }
+      }
+    }
+    if (source == -2 && lane == 0 && blockIdx.x == 0) {
+      raise_fault(a.fault, kFaultSlotOutOfRange);
+    }
+    __syncthreads();  // rows staged; the norm weights' space is free for the partial sums
+  }
   const uint16_t *token_row = staged + row * rs + k0 + piece * 8;
   const bool token_live = row < staged_rows;
 
-  // Partial sums of the K ranges p > 0: wave w of range p > 0 writes slot w - w / ksplit - 1.
-  __shared__ f32x4 partial[kSplitWaves - 1][2][64];
   for (int64_t unit = blockIdx.x; unit < units; unit += gridDim.x) {
-    const int64_t rb = unit * per_unit + block_in_unit;
-    const bool active = rb < row_blocks;
-    const int rotation = static_cast<int>((rb * 7) % chunks);
-    const uint32_t w_off = static_cast<uint32_t>(((rb * 16 + row) * a.k + k0 + piece * 8) * 2);
-    auto column_of = [&](int chunk) XP_INLINE {
-      const int c = chunk + rotation;
-      return (c < chunks ? c : c - chunks) * 128;
-    };
-    u32x4 wbuf[DEPTH][4];
-    auto load_chunk = [&](int chunk, u32x4 (&w)[4]) XP_INLINE {
-      const bool in_range = chunk < chunks;
-      const uint32_t column = static_cast<uint32_t>(column_of(chunk)) * 2;
+    if (unit != blockIdx.x) {
+      enter_unit(unit);
+      if (active) {
 #pragma unroll
-      for (int line = 0; line < 2; ++line) {
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          w[2 * line + h] = buffer_load16<kLoadNontemporal>(
-              w_rsrc, in_range ? w_off + h * w_half + column + line * 128 : kOutOfRange);
+        for (int d = 0; d < DEPTH; ++d) {
+          load_chunk(d, wbuf[d]);
         }
       }
-    };
+    }
     f32x4 acc[2] = {f32x4{0.0f, 0.0f, 0.0f, 0.0f}, f32x4{0.0f, 0.0f, 0.0f, 0.0f}};
     auto compute_chunk = [&](int chunk, const u32x4 (&w)[4]) XP_INLINE {
       const int column = chunk < chunks ? column_of(chunk) : 0;
@@ -524,10 +661,6 @@ __global__ __launch_bounds__(64 * kSplitWaves) void split_gathered_kernel(GemmAr
       }
     };
     if (active) {
-#pragma unroll
-      for (int d = 0; d < DEPTH; ++d) {
-        load_chunk(d, wbuf[d]);
-      }
       int c0 = 0;
       for (; c0 < padded - DEPTH; c0 += DEPTH) {
 #pragma unroll
@@ -543,7 +676,8 @@ __global__ __launch_bounds__(64 * kSplitWaves) void split_gathered_kernel(GemmAr
       }
     }
     // Fixed-order sum of the K ranges of each row block (range 0's wave adds 1 .. ksplit - 1
-    // in order); the barriers wait for LDS only, nothing else is outstanding here.
+    // in order); the barriers wait for LDS only, nothing else is outstanding here.  Wave w
+    // of range p > 0 writes slot w - w / ksplit - 1.
     if (ksplit > 1) {
       __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
       __asm__ volatile("s_barrier" ::: "memory");  // the previous unit's sums have been read
@@ -976,31 +1110,11 @@ __global__ __launch_bounds__(256) void stream_reduce_kernel(GemmArgs a) {
 }
 
 // ------------------------------------------------------------------ tile
-using lds_void_t = __attribute__((address_space(3))) void *;
-
-// Direct global -> LDS load of 16 bytes per lane through a buffer resource: lane i's
-// data lands at `lds_row_base + 16 i`; offsets past the resource's end write zeros.
-template <int POLICY = 0>
-__device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t rsrc, void *lds_base, uint32_t voffset,
-                                                  uint32_t soffset) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t)(lds_base), 16, static_cast<int>(voffset),
-                                           static_cast<int>(soffset), 0, POLICY);
-}
-
 // LDS tiles are rows of 64 bf16 (128 bytes = eight 16-byte chunks).  gfx950 serves
 // ds_read_b128 sixteen lanes at a time from a 256-byte bank line, i.e. two tile rows, so
 // the 16 rows one MFMA fragment read touches must occupy 16 distinct 16-byte slots:
 // logical chunk c of row r is stored at physical chunk c ^ ((r / 2) % 8).
 __device__ __forceinline__ int swizzle(int row) { return (row >> 1) & 7; }
-
-// s_waitcnt with vmcnt <= N and the LDS / export counters left unconstrained (gfx9 encoding:
-// vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit counter");
-  __builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
-}
-
 
 // Calls f(std::integral_constant<int, 0>{}) .. f(std::integral_constant<int, N - 1>{}).
 template <class F, int... I>
@@ -1719,14 +1833,17 @@ constexpr double kSplitGatherRoundUs = 3.0;
 // gate_up at 16 rows, 192 workgroups, 37.0 us plain and ~41 us with the gather fused).
 constexpr double kStreamGatherUs = 3.5;
 constexpr int64_t kSplitGatherMaxK = 4096;  // 8 staged rows of K + 16 bf16 (66 KB) beside the partial sums
-// split_gathered_kernel: two workgroups per CU (117 VGPRs; at most 80 KB of LDS each, the
-// 8 staged rows of 4096 + 16 bf16 and the partial sums), for projections with at least that
-// many units.  Its gather is one dependent round trip per workgroup before the weight
-// stream starts, and its token pieces come from LDS (no per-row L2 reads): measured on
-// MI355X, Qwen3-8B gate_up at 1 / 4 / 8 rows 35.7 / 36.0 / 36.9 us against 31.8 / 32.5 /
-// 35.7 us for the plain split kernel after a 4-5 us gather launch.
+static_assert(kSplitGatherMaxK * 2 <= kSplitGatheredScratchBytes, "the norm weights fit the partial sums' space");
+static_assert(kSplitGatherMaxK / 8 <= 8 * 64, "a staged row is at most 8 chunks per lane");
+// split_gathered_kernel: two workgroups per CU (128 VGPRs; at most 80 KB of LDS each, the
+// 8 staged rows of 4096 + 16 bf16 and the space shared by the norm weights and the partial
+// sums), for projections with at least that many units.  Its gather runs under the first
+// weight chunks' round trip and its token pieces come from LDS (no per-row L2 reads); what
+// the gather still adds is the normalisation pass over LDS and one barrier: measured on
+// MI355X, the Qwen3-8B / 4B / 1.7B layer at one row 52.2 / 36.9 / 24.7 us against 55.0 /
+// 37.7 / 26.6 us when the gather took its own round trip before the weight stream.
 constexpr int64_t kSplitGatheredWorkgroups = 2 * kComputeUnits;
-constexpr double kSplitPersistentGatherUs = 3.5;
+constexpr double kSplitPersistentGatherUs = 1.0;
 
 double decode_stream_us(int64_t n, int64_t k, int64_t workgroups, double workgroup_bytes_per_us,
                         double chip_bytes_per_us, double fixed_us) {
@@ -2033,7 +2150,8 @@ GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmCho
     kernel.func = gated ? split_gathered_kernel_ptr<true>() : split_gathered_kernel_ptr<false>();
     kernel.grid = dim3(static_cast<unsigned>(units < kSplitGatheredWorkgroups ? units : kSplitGatheredWorkgroups), 1, 1);
     kernel.block = dim3(64 * kSplitWaves, 1, 1);
-    kernel.shmem = static_cast<unsigned>((capacity < kSplitGroupTokens ? capacity : kSplitGroupTokens) * (args.k + 16) * 2);
+    kernel.shmem = static_cast<unsigned>((capacity < kSplitGroupTokens ? capacity : kSplitGroupTokens) * (args.k + 16) * 2 +
+                                         kSplitGatheredScratchBytes);
   } else if (choice.kind == GemmKind::Stream) {
     const int64_t groups = ((args.n + 15) / 16 + kStreamWaves - 1) / kStreamWaves;
     const int64_t slices = stream_slices(args.k, choice.k_slice);

@@ -115,6 +115,7 @@ def test_config3_qwen3_8b_layer(device, rows):
         (2560, 9728, 3, "split_gated_t8_k4_persistent+gather"),
         # K = 4088: the last K range ends inside a 128-wide chunk; 513 units over 512 workgroups.
         (4088, 4104, 5, "split_gated_t8_k8_persistent+gather"),
+        (4096, 4096, 4, "split_gated_t8_k8_persistent+gather"),
         (1024, 3072, 1, "split_gated_t8_k4+gather"),
         (1024, 3072, 8, "split_gated_t8_k4+gather"),
         (2048, 2048, 5, "split_gated_t8_k8+gather"),
@@ -151,6 +152,29 @@ def test_fused_gather_matches_separate_kernels_bitwise(device, normed, hidden, i
     assert _native.gemm_variant(rows, 2 * intermediate, hidden, True) == (
         variant.removesuffix("+gather").removesuffix("_persistent"))
     assert_bitwise_equal(pool_gpu.cpu(), expected.cpu())
+    _check_mailbox(pool_gpu, pool, slots, w_gate_up, w_down, norm_weight if normed else None)
+
+
+@pytest.mark.parametrize("normed", [True, False])
+@pytest.mark.parametrize("rows", [1, 6])
+def test_persistent_gather_where_projections_take_the_stream_kernel(device, normed, rows):
+    # Hidden 1536 (three 64-chunk groups per staged row, K ranges of three chunks): the step
+    # takes the persistent gathered split kernel while the kernel-level projection takes the
+    # stream kernel (other K ranges, so no bitwise comparison); checked against the oracle.
+    hidden, intermediate, pool_rows = 1536, 8960, 256
+    assert _native.dense_gate_up_variant(rows, hidden, intermediate) == "split_gated_t8_k4_persistent+gather"
+    pool = o.generate_hidden_states(pool_rows, hidden, 27)
+    w_gate_up, w_down, norm_weight = o.generate_layer(hidden, intermediate, 28)
+    slots = o.generate_slots(pool_rows, rows, 29)
+    with FfnAgent(device) as agent:
+        agent.register_layer(
+            instance_index=0, layer_ordinal=0, weights=_weights(w_gate_up, w_down, device),
+            norm_weight=to_device(norm_weight, device) if normed else None,
+        )
+        agent.materialize(maximum_row_capacity=8)
+        pool_gpu = to_device(pool, device)
+        agent.execute(instance_index=0, layer_ordinal=0, pool=pool_gpu, slots=slots_tensor(slots, device))
+        agent.check_health()
     _check_mailbox(pool_gpu, pool, slots, w_gate_up, w_down, norm_weight if normed else None)
 
 
