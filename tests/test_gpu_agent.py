@@ -405,9 +405,9 @@ def test_out_of_range_slot_sets_sticky_fault(device, hidden, intermediate, capac
         narrow = torch.zeros((64, hidden - 8), dtype=torch.bfloat16, device=device)
         with pytest.raises(ValueError, match="hidden size"):
             agent.lanes[0].replay(instance_index=0, layer_ordinal=0, pool=narrow, slots=bad)
-    got = pool_gpu.cpu()
-    untouched = np.setdiff1d(np.arange(64), live)
-    assert_bitwise_equal(got[untouched], pool[untouched])
+    # The bad slot's row is staged as quiet NaNs and its output is dropped; the live rows
+    # are still the FFN of their own rows and every other mailbox row is untouched.
+    _check_mailbox(pool_gpu, pool, np.array(live, dtype=np.int32), w_gate_up, w_down, None)
 
 
 def test_ffn_shim_matches_dense_partial(device):
