@@ -1802,26 +1802,36 @@ constexpr int kComputeUnits = 256;
 // split kernel with 2 K ranges per row block has 80 workgroups: 41 us; with 8, 320: 16 us),
 // workgroups past 256 run as further rounds, and the chip caps the total (both read whole
 // 128-byte weight lines with the nontemporal hint).
-// The split kernel reads its token pieces from L2, a little more per row; the stream
-// kernel's K slices cost the reduction launch and their partial traffic.  The split
-// kernel's rounds of 256 workgroups are priced one after another (each at the chip rate or
-// at one workgroup's rate, whichever is slower).  Fitted to forced split (every K split) /
-// stream timings of the Qwen3 0.6B / 4B / 8B / 32B-shard projections at 1 to 16 rows with
-// the weights streamed from HBM: mean modelled error 0.8 us, and the K split it picks is
-// within 6 % of the fastest measured one (0.6 % on average).
+// The split kernel reads its token pieces from L2, a little more per row and chunk of its
+// K range; the stream kernel's K slices cost the reduction launch and their partial
+// traffic.  The split kernel's rounds of 256 workgroups are priced one after another (each
+// at the chip rate or at one workgroup's rate, whichever is slower, and never below one load
+// round trip: short rounds are latency-bound).  Least-squares fit (relative error) to 498
+// forced split (every K split) and stream (K slices of 512-4096 columns) timings on MI355X:
+// the Qwen3 0.6B / 1.7B / 4B / 8B projections, the Qwen3-32B TP shard's and a hidden-1536
+// down at 1 to 16 rows, the weights rotated over three copies (streamed from HBM).  Mean
+// modelled error 7.4 % (26 % for the constants it replaced); summed over the 66
+// (projection, rows) cases, its picks are 29 us slower than the fastest measured ones,
+// against 79 us before.  Per layer (alternating builds on one box) that took the 9-16-row
+// Dense steps of Qwen3-4B / 1.7B / the 32B shard from 47-51 / 34-38 / 42-47 us to 44-45 /
+// 33-35 / 39-41 us and hidden 1536 at 1-8 rows from 27-31 to 26-27 us (Qwen3-8B at 9 rows:
+// 61.4 -> 62.5 us, the one loss).
 constexpr int64_t kDecodeMaxRows = 16;
 constexpr int64_t kSplitMaxRows = kSplitGroupTokens * kSplitMaxGroups;
 // Index: token groups - 1.  Two groups read twice the token pieces from L2 per weight line,
-// which lowers the chip rate (Qwen3-8B gate_up at 9-16 rows: 43-53 us, against 40-42 us for
-// the stream kernel; Qwen3-0.6B gate_up: 7.9-8.5 us against 11.0 us).
-constexpr double kSplitWorkgroupBytesPerUs[kSplitMaxGroups] = {26.0e3, 20.0e3};
-constexpr double kSplitBytesPerUs[kSplitMaxGroups] = {6.8e6, 5.2e6};
-constexpr double kSplitFixedUs[kSplitMaxGroups] = {4.0, 3.0};
-constexpr double kSplitRowUsPerChunk = 0.02;  // per row past the first and 128-wide chunk of a range (padded)
-constexpr double kStreamWorkgroupBytesPerUs = 30.0e3;
-constexpr double kStreamBytesPerUs = 6.0e6;
-constexpr double kStreamFixedUs = 2.0;
-constexpr double kStreamReduceUs = 12.0;  // the reduction launch, fitted (it also ends the overlap of slices)
+// which lowers the chip rate.
+constexpr double kSplitWorkgroupBytesPerUs[kSplitMaxGroups] = {32.7e3, 27.6e3};
+constexpr double kSplitBytesPerUs[kSplitMaxGroups] = {6.75e6, 5.06e6};
+constexpr double kSplitFixedUs[kSplitMaxGroups] = {3.54, 4.19};
+constexpr double kSplitRoundFloorUs = 2.7;  // no round of workgroups is shorter (one load round trip)
+constexpr double kSplitTieMargin = 0.02;
+// Per row past the first and 128-wide chunk of a range (padded to the load depth).
+constexpr double kSplitRowUsPerChunk[kSplitMaxGroups] = {0.0406, 0.0314};
+constexpr double kStreamWorkgroupBytesPerUs = 29.2e3;
+constexpr double kStreamBytesPerUs = 6.1e6;
+constexpr double kStreamFixedUs = 1.03;
+constexpr double kStreamRowUs = 0.0071;  // per row past the first and 512 columns of the K slice
+constexpr double kStreamReduceUs = 5.4;  // the reduction launch (it also ends the overlap of slices)
 constexpr double kStreamPartialBytesPerUs = 6.0e6;
 constexpr int kSplitDepth = 4;
 constexpr double kGatherUs = 4.0;  // a separate gather launch at decode sizes (measured 3.8-4.0 us)
@@ -1857,7 +1867,8 @@ double decode_stream_us(int64_t n, int64_t k, int64_t workgroups, double workgro
 // Candidate K splits of the split kernel (1, 2, 4 or 8 ranges per 16-row block, each range
 // a whole number of 128-wide chunks and none empty) and their modelled cost at `capacity`
 // rows, with the gather fused when `gather` is set.
-GemmChoice choose_split(int64_t capacity, int64_t n, int64_t k, double &cost, bool gather = false) {
+GemmChoice choose_split(int64_t capacity, int64_t n, int64_t k, double &cost, bool gather = false,
+                        bool persistent = false) {
   const int64_t quantum = 128;
   const int64_t row_blocks = (n + 15) / 16;
   const int groups = split_groups(capacity);
@@ -1876,15 +1887,20 @@ GemmChoice choose_split(int64_t capacity, int64_t n, int64_t k, double &cost, bo
       const double round_bytes = static_cast<double>(left < kComputeUnits ? left : kComputeUnits) * workgroup_bytes;
       const double chip_us = round_bytes / kSplitBytesPerUs[groups - 1];
       const double workgroup_us = workgroup_bytes / kSplitWorkgroupBytesPerUs[groups - 1];
-      us += chip_us > workgroup_us ? chip_us : workgroup_us;
+      const double round_us = chip_us > workgroup_us ? chip_us : workgroup_us;
+      us += round_us > kSplitRoundFloorUs ? round_us : kSplitRoundFloorUs;
     }
-    us += kSplitRowUsPerChunk *
+    us += kSplitRowUsPerChunk[groups - 1] *
                     static_cast<double>((slice / 128 + depth - 1) / depth * depth) *
                     static_cast<double>(capacity - 1);
     if (gather) {
       us += kSplitGatherRoundUs * static_cast<double>((workgroups + kComputeUnits - 1) / kComputeUnits);
     }
-    if (cost < 0.0 || us < cost) {
+    // The persistent kernel walks units on a fixed grid, so it takes the most K ranges of
+    // at least two chunks (the most units to balance) rather than the cheapest round count.
+    // Otherwise a split within kSplitTieMargin of the cheapest so far takes its place (the
+    // most ranges among near-equal costs: shorter per-wave load chains).
+    if (persistent ? slice >= 2 * quantum : (cost < 0.0 || us < cost * (1.0 + kSplitTieMargin))) {
       best = {GemmKind::Split, groups, slice, ksplit};
       cost = us;
     }
@@ -1910,7 +1926,8 @@ GemmChoice choose_stream(int64_t capacity, int64_t n, int64_t k, double &cost) {
     if (tp * (k_slice + kStreamRowPad) * 2 > kStreamLdsBytes || stream_slices(k, k_slice) != slices) {
       continue;  // does not fit LDS, or the same slice length as fewer slices
     }
-    double us = decode_stream_us(n, k, slices * groups, kStreamWorkgroupBytesPerUs, kStreamBytesPerUs, kStreamFixedUs);
+    double us = decode_stream_us(n, k, slices * groups, kStreamWorkgroupBytesPerUs, kStreamBytesPerUs, kStreamFixedUs) +
+                kStreamRowUs * static_cast<double>(capacity - 1) * static_cast<double>(k_slice) / 512.0;
     if (slices > 1) {
       us += kStreamReduceUs + 8.0 * static_cast<double>(slices * capacity * n) / kStreamPartialBytesPerUs;
     }
@@ -2042,7 +2059,7 @@ GemmChoice choose_dense_gate_up(int64_t capacity, int64_t n, int64_t k, bool &fu
     // The persistent variant prices as the split kernel at one row (its token pieces come
     // from LDS) plus its gather round trip, when the projection has units for every slot.
     double persistent_us = 0.0;
-    GemmChoice persistent = choose_split(1, n, k, persistent_us);
+    GemmChoice persistent = choose_split(1, n, k, persistent_us, false, true);
     persistent_us += kSplitPersistentGatherUs;
     const int64_t units = ((n + 15) / 16 * persistent.k_split + kSplitWaves - 1) / kSplitWaves;
     if (units >= kSplitGatheredWorkgroups && persistent_us < fused_us && persistent_us < split_us &&

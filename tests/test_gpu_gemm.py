@@ -168,8 +168,9 @@ def test_variant_selection_covers_every_family(device):
 # groups (a partial last K range) or of the tiles' 64-column slabs, N not a multiple of 16
 # (weight rows past N), one to many K ranges.  Up to 16 rows a cost model picks the split
 # (one token group up to 8 rows, two up to 16) or the stream kernel, from 17 the
-# deep-staged small tiles; both decode kernels must occur on these shapes.
-DECODE_SHAPES = [(1032, 1000), (2056, 9992), (4096, 12288), (264, 40)]
+# deep-staged small tiles; both decode kernels, and the split kernel with one and with two
+# token groups for both projections, must occur on these shapes.
+DECODE_SHAPES = [(1032, 1000), (2056, 9992), (4096, 12288), (264, 40), (1544, 2056)]
 DECODE_ROWS = [1, 3, 4, 5, 8, 9, 16, 17, 32, 33, 64]
 
 

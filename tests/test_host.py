@@ -324,9 +324,12 @@ def test_gemm_variant_selection():
     assert _native.gemm_variant(64, 4096, 12288, False).startswith("tile_64x128_k")
     assert _native.gemm_workspace_bytes(1, 24576, 4096, True) == 0
     # 9 to 16 rows: the split kernel with two token groups where its modelled cost is lower
-    # (Qwen3-8B down; its K ranges are summed in LDS, no scratch), else the stream kernel
-    assert _native.gemm_variant(16, 4096, 12288, False) == "split_t16_k8"
-    assert _native.gemm_workspace_bytes(16, 4096, 12288, False) == 0
+    # (Qwen3-0.6B down; its K ranges are summed in LDS, no scratch), else the stream kernel
+    # (Qwen3-8B down: 8 K slices of 1536, whose fp32 partials the reduction launch sums)
+    assert _native.gemm_variant(16, 1024, 3072, False) == "split_t16_k8"
+    assert _native.gemm_workspace_bytes(16, 1024, 3072, False) == 0
+    assert _native.gemm_variant(16, 4096, 12288, False) == "stream_t16"
+    assert _native.gemm_workspace_bytes(16, 4096, 12288, False) == 8 * 16 * 4096 * 4
     assert _native.gemm_variant(2048, 24576, 4096, True) == "tile_gated_256x256"
     assert _native.gemm_variant(4096, 4096, 12288, False).startswith("tile")
     assert _native.gemm_workspace_bytes(2048, 24576, 4096, True) == 0
