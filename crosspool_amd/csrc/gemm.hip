@@ -1824,7 +1824,7 @@ constexpr double kSplitWorkgroupBytesPerUs[kSplitMaxGroups] = {32.7e3, 27.6e3};
 constexpr double kSplitBytesPerUs[kSplitMaxGroups] = {6.75e6, 5.06e6};
 constexpr double kSplitFixedUs[kSplitMaxGroups] = {3.54, 4.19};
 constexpr double kSplitRoundFloorUs = 2.7;  // no round of workgroups is shorter (one load round trip)
-constexpr double kSplitTieMargin = 0.02;
+constexpr double kSplitTieMargin = 0.001;
 // Per row past the first and 128-wide chunk of a range (padded to the load depth).
 constexpr double kSplitRowUsPerChunk[kSplitMaxGroups] = {0.0406, 0.0314};
 constexpr double kStreamWorkgroupBytesPerUs = 29.2e3;
@@ -1898,8 +1898,10 @@ GemmChoice choose_split(int64_t capacity, int64_t n, int64_t k, double &cost, bo
     }
     // The persistent kernel walks units on a fixed grid, so it takes the most K ranges of
     // at least two chunks (the most units to balance) rather than the cheapest round count.
-    // Otherwise a split within kSplitTieMargin of the cheapest so far takes its place (the
-    // most ranges among near-equal costs: shorter per-wave load chains).
+    // Otherwise a split whose cost equals the cheapest so far (within kSplitTieMargin, i.e.
+    // rounding) takes its place: the most ranges among equal costs, shorter per-wave load
+    // chains (Qwen3-8B gate_up at one row: 4 and 8 ranges model the same, and 8 is the
+    // persistent kernel's split).
     if (persistent ? slice >= 2 * quantum : (cost < 0.0 || us < cost * (1.0 + kSplitTieMargin))) {
       best = {GemmKind::Split, groups, slice, ksplit};
       cost = us;
