@@ -210,6 +210,19 @@ def gemm_workspace_bytes(rows: int, n: int, k: int, gated: bool) -> int:
     return int(library().xp_gemm_workspace_bytes(rows, n, k, int(gated)))
 
 
+def gemm_workspace_bytes_upto(capacity: int, n: int, k: int, gated: bool) -> int:
+    """Scratch that serves a kernel-level projection at every live row count up to ``capacity``.
+
+    ``xp_gemm_gate_up_silu`` / ``xp_gemm_down`` choose their kernel at the live row count, and a
+    smaller count can take a K split with more ranges than the capacity's choice (down 1024 x
+    3072: 3833856 bytes at 117 rows, 3866624 at 59), so a plan prepared at the capacity sizes
+    its scratch as the largest need over 1..capacity.
+    """
+
+    query = library().xp_gemm_workspace_bytes
+    return max((int(query(rows, n, k, int(gated))) for rows in range(1, capacity + 1)), default=0)
+
+
 def dense_workspace_bytes(capacity: int, hidden: int, intermediate: int) -> int:
     return int(library().xp_dense_workspace_bytes(capacity, hidden, intermediate))
 

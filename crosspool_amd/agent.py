@@ -191,7 +191,9 @@ class ExecutorLane:
             "xp_replay", self.handle, instance_index, layer_ordinal, rows, ctypes.c_void_p(pool.data_ptr()),
             ctypes.c_void_p(out_pool.data_ptr()), pool.shape[0], ctypes.c_void_p(slots.data_ptr()), stream_handle,
         )
-        if run_on.cuda_stream != current.cuda_stream:
+        if run_on.cuda_stream != current.cuda_stream and not torch.cuda.is_current_stream_capturing():
+            # (Under an outer stream capture the kernels become graph nodes and the tensors
+            # belong to the capturing caller; no event may be recorded or queried for them.)
             self._retain(run_on, (pool, out_pool, slots))
 
     def _retain(self, stream: torch.cuda.Stream, tensors: tuple[torch.Tensor, ...]) -> None:

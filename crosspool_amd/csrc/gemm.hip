@@ -2060,12 +2060,15 @@ GemmChoice choose_dense_gate_up(int64_t capacity, int64_t n, int64_t k, bool &fu
     const GemmChoice split = choose_split(capacity, n, k, split_us, true);
     // The persistent variant prices as the split kernel at one row (its token pieces come
     // from LDS) plus its gather round trip, when the projection has units for every slot.
+    // A reduction length of at most 128 has no K range of two chunks: choose_split then finds
+    // no persistent split (k_slice 0, cost -1) and the persistent kernel is not a candidate.
     double persistent_us = 0.0;
     GemmChoice persistent = choose_split(1, n, k, persistent_us, false, true);
+    const bool persistent_found = persistent.k_slice > 0 && persistent_us >= 0.0;
     persistent_us += kSplitPersistentGatherUs;
     const int64_t units = ((n + 15) / 16 * persistent.k_split + kSplitWaves - 1) / kSplitWaves;
-    if (units >= kSplitGatheredWorkgroups && persistent_us < fused_us && persistent_us < split_us &&
-        persistent_us < kGatherUs + separate_us) {
+    if (persistent_found && units >= kSplitGatheredWorkgroups && persistent_us < fused_us &&
+        persistent_us < split_us && persistent_us < kGatherUs + separate_us) {
       persistent.kind = GemmKind::SplitGathered;
       return persistent;
     }
@@ -2148,6 +2151,11 @@ GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmCho
   record.capacity = capacity;
   record.k_slice = choice.k_slice;
   record.k_split = choice.k_split;
+  if ((choice.kind == GemmKind::Split || choice.kind == GemmKind::SplitGathered) &&
+      (choice.k_slice <= 0 || choice.k_split <= 0)) {
+    launches.usable = false;  // an empty K range would read nothing and store zeros
+    return launches;
+  }
   if (choice.kind == GemmKind::Split) {
     // choose_split is only consulted up to kSplitMaxRows rows (and the fused gather up to
     // one token group).

@@ -282,6 +282,9 @@ __device__ int block_inclusive_scan(int value, int *wave_totals) {
 // 2048 rows at top-8, in one pass; more are read again).
 constexpr int kSortRoutesPerThread = 16;
 
+// The fused TopK gives each of the workgroup's waves one row.
+static_assert(kMoeFusedTopkRows <= 1024 / kWave, "one wave of moe_sort_kernel per fused TopK row");
+
 __global__ __launch_bounds__(1024) void moe_sort_kernel(MoeSortArgs a) {
   __shared__ int counts[kMoeMaxExperts];
   __shared__ int offsets[kMoeMaxExperts + 1];

@@ -127,6 +127,8 @@ struct DenseLaunches {
   GemmLaunch gate_up;
   GemmLaunch down;
 
+  bool usable() const { return gate_up.usable && down.usable; }
+
   int chain(const KernelLaunch **out) const {
     int count = 0;
     for (const KernelLaunch *kernel : {&gather, &gate_up.main, &gate_up.reduce, &down.main, &down.reduce}) {
@@ -146,6 +148,7 @@ constexpr int kMaxTemplateKernels = 9;
 struct StepChain {
   KernelLaunch kernels[kMaxTemplateKernels];
   int count = 0;
+  bool usable = true;  // false: a projection of the step has no launchable kernel choice
   void add(const KernelLaunch &kernel) {
     if (!kernel.empty()) {
       kernels[count++] = kernel;
@@ -245,7 +248,12 @@ int bind_scratch(GemmArgs &args, GemmChoice choice, void *workspace, size_t work
   return XP_OK;
 }
 
+constexpr const char *kUnusableChoice = "no launchable projection kernel for this geometry (empty K range)";
+
 int launch_gemm(const GemmLaunch &kernels, hipStream_t stream) {
+  if (!kernels.usable) {
+    return fail(XP_ERROR_INVALID_ARGUMENT, kUnusableChoice);
+  }
   XP_HIP_CHECK(launch(kernels.main, stream));
   XP_HIP_CHECK(launch(kernels.reduce, stream));
   return XP_OK;
@@ -603,6 +611,8 @@ int make_experts_launches(const ExpertsBinding &b, int64_t capacity, ExpertsLaun
   sort.tile_rows = tile_rows;
   sort.max_tiles = max_tiles;
   if (b.fused_topk != nullptr) {
+    // moe_sort_kernel runs the fused TopK with one wave per row.
+    XP_REQUIRE(b.fused_topk->rows <= kMoeFusedTopkRows, "fused TopK rows exceed the route sort's waves");
     sort.topk = *b.fused_topk;
     sort.fused_topk = 1;
   }
@@ -916,6 +926,7 @@ StepChain dense_chain(const DenseBinding &binding, int64_t capacity) {
   const KernelLaunch *kernels[kMaxStepKernels];
   const int count = launches.chain(kernels);
   StepChain chain;
+  chain.usable = launches.usable();
   for (int index = 0; index < count; ++index) {
     chain.add(*kernels[index]);
   }
@@ -925,6 +936,9 @@ StepChain dense_chain(const DenseBinding &binding, int64_t capacity) {
 // Build and instantiate a template's hipGraph: one kernel node per chain entry, each
 // depending on the previous one.
 int instantiate_template(Template &t, const StepChain &chain) {
+  if (!chain.usable) {
+    return fail(XP_ERROR_INVALID_ARGUMENT, kUnusableChoice);
+  }
   XP_HIP_CHECK(hipGraphCreate(&t.graph, 0));
   t.node_count = chain.count;
   for (int index = 0; index < chain.count; ++index) {
@@ -967,10 +981,20 @@ void insert_template(xp_lane *lane, std::unique_ptr<Template> t) {
 // Launch a replay's chain: directly on the stream, or (graph dispatch) by rebinding the
 // template's nodes whose argument record changed and launching its graph.
 int run_chain(xp_lane *lane, Template &t, const StepChain &chain, hipStream_t target) {
+  if (!chain.usable) {
+    return fail(XP_ERROR_INVALID_ARGUMENT, kUnusableChoice);
+  }
   if (chain.count != t.node_count) {
     return fail(XP_ERROR_STATE, "replay kernel sequence differs from the captured template");
   }
-  if (!lane->graph_dispatch) {
+  // Under an outer stream capture (a caller recording its decode step as a graph) the
+  // kernels are launched directly, so that they become nodes of the caller's graph rather
+  // than a graph launched inside a capture.
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  if (lane->graph_dispatch) {
+    XP_HIP_CHECK(hipStreamIsCapturing(target, &capture));
+  }
+  if (!lane->graph_dispatch || capture != hipStreamCaptureStatusNone) {
     for (int index = 0; index < chain.count; ++index) {
       XP_HIP_CHECK(launch(chain.kernels[index], target));
     }
@@ -1345,6 +1369,7 @@ int run_dense_step(const void *pool_in, void *pool_out, int64_t pool_rows, const
   binding.workspace = static_cast<uint8_t *>(workspace);
   binding.fault = fault_word;
   const DenseLaunches launches = make_dense_launches(binding, rows);
+  XP_REQUIRE(launches.usable(), kUnusableChoice);
   const KernelLaunch *chain[kMaxStepKernels];
   const int count = launches.chain(chain);
   for (int index = 0; index < count; ++index) {

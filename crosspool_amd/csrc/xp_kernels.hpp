@@ -392,6 +392,7 @@ size_t gemm_scratch_bytes(GemmChoice choice, int64_t capacity, int64_t n, int64_
 struct GemmLaunch {
   KernelLaunch main;
   KernelLaunch reduce;
+  bool usable = true;  // false: the choice names no launchable kernel (callers fail the call)
 };
 // `fused_gather`: the gate_up of a Dense step whose choose_dense_gate_up decision fused the
 // mailbox gather, or a projection for which split_gather_fusable holds (the kernel variant

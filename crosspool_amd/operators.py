@@ -189,10 +189,10 @@ class GemmPlan:
         aligned = dtype is torch.bfloat16 and weight_layout.bias is None and hidden % 8 == 0 and width % 16 == 0
         if aligned and fused is None and width <= 16384:
             kernel = "down"
-            scratch = _native.gemm_workspace_bytes(rows, width, hidden, False)
+            scratch = _native.gemm_workspace_bytes_upto(rows, width, hidden, False)
         elif aligned and gated_epilogue and isinstance(fused.function, SiluActivation) and hidden <= 16384:
             kernel = "gate_up_silu"
-            scratch = _native.gemm_workspace_bytes(rows, width, hidden, True)
+            scratch = _native.gemm_workspace_bytes_upto(rows, width, hidden, True)
         else:
             kernel = "projection"
             scratch = 0

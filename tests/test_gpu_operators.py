@@ -229,6 +229,33 @@ def test_projection_replays_current_bias_and_activation_without_allocation(devic
         assert_near_oracle(output, oracle)
 
 
+def test_projection_planned_at_capacity_runs_fewer_live_rows(device):
+    # The MFMA projection chooses its kernel at the live row count; Qwen3-0.6B down planned at
+    # 117 rows and run at 59 takes a K split with more ranges than the plan's own choice, and
+    # the plan's scratch must serve it (the largest need over 1..capacity).
+    print("projection plan 117 -> live 59", flush=True)
+    rows, live, hidden, width = 117, 59, 3072, 1024
+    layout = ProjectionLayout(values=TensorLayout((width, hidden), torch.bfloat16))
+    plan = GemmPlan.prepare(
+        input_layout=TensorLayout((rows, hidden), torch.bfloat16), weight_layout=layout,
+        result_layout=TensorLayout((rows, width), torch.bfloat16), activation=None,
+    )
+    assert plan.kernel == "down"
+    generator = torch.Generator(device=device).manual_seed(117)
+    inputs = torch.randn((rows, hidden), device=device, generator=generator).to(torch.bfloat16)
+    projection = layout.zero_probe(device)
+    projection.values.copy_(torch.randn(projection.values.shape, device=device, generator=generator) * 0.02)
+    operation = Gemm(plan, torch.empty(max(plan.workspace.nbytes, 16), device=device, dtype=torch.uint8))
+    for count in (live, rows, 1):
+        output = torch.empty((count, width), device=device, dtype=torch.bfloat16)
+        operation.run_into(inputs[:count], projection, output=output)
+        torch.cuda.synchronize()
+        oracle = o.projection_reference(inputs[:count].cpu(), projection.values.cpu(), None)
+        torch.testing.assert_close(output.cpu(), oracle, rtol=0.02, atol=0.02)
+        same = (output.cpu().view(torch.int16) == oracle.view(torch.int16)).float().mean().item()
+        assert same >= 0.99, f"{count} rows: only {same:.4f} bit-identical to the oracle"
+
+
 # ------------------------------------------------------------------ Dense operator
 ROW_CAPACITY, HIDDEN_SIZE, LOCAL_INTERMEDIATE_SIZE = 4, 16, 8
 

@@ -352,6 +352,28 @@ def test_dense_step_fuses_the_gather_at_decode_sizes():
     assert _native.dense_gate_up_variant(2048, 4096, 12288) == "tile_gated_256x256"
 
 
+def test_short_reductions_never_take_the_persistent_split():
+    # With K <= 128 no K range reaches two 128-wide chunks: the persistent split kernel has no
+    # split to walk and must not be chosen (it would read nothing and store zeros), however
+    # many units the intermediate gives it.
+    for rows in range(1, 9):
+        for hidden in (64, 128):
+            variant = _native.dense_gate_up_variant(rows, hidden, 32768)
+            assert "persistent" not in variant, (rows, hidden, variant)
+    # one K range of two chunks is enough again
+    assert "persistent" in _native.dense_gate_up_variant(1, 256, 32768)
+
+
+def test_operator_scratch_serves_every_live_row_count_up_to_the_plan():
+    # A kernel-level projection chooses its kernel at the live row count, and a smaller count
+    # can take more K ranges than the plan's capacity: the plan's scratch is the largest need.
+    planned = _native.gemm_workspace_bytes_upto(117, 1024, 3072, False)
+    assert planned >= _native.gemm_workspace_bytes(59, 1024, 3072, False) > _native.gemm_workspace_bytes(
+        117, 1024, 3072, False
+    )
+    assert planned == max(_native.gemm_workspace_bytes(r, 1024, 3072, False) for r in range(1, 118))
+
+
 def test_k_split_tiles_fill_the_chip_and_size_their_partials():
     # Qwen3-8B down at 256 rows has only 16 to 64 weight x token tiles: K is split so that
     # the grid covers the 256 CUs, and each range leaves an fp32 partial tile in scratch.
