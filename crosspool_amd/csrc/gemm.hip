@@ -29,6 +29,7 @@
 
 #include "xp_kernels.hpp"
 
+#include <algorithm>
 #include <mutex>
 #include <type_traits>
 #include <utility>
@@ -1109,6 +1110,348 @@ __global__ __launch_bounds__(256) void stream_reduce_kernel(GemmArgs a) {
   }
 }
 
+// ------------------------------------------------------------------ resident (decode, 9-32 rows)
+// Weight streaming for 9 to 32 live rows with the token rows resident in registers.  One
+// workgroup of 8 waves per CU (256 VGPRs per wave, two waves per SIMD).  The K columns of a
+// workgroup's part (k_slice = 8 CPW 128 columns; k_split parts over the grid) are split over
+// its 8 waves, CPW 128-wide chunks each, and every wave loads the token rows' pieces of its
+// own chunks once, in the split kernel's MFMA operand layout (token 8 g + i of group g at
+// piece 2 q + (i >> 3) of each 64-column line), so the main loop reads no token data at all:
+// past the prologue every load of the kernel is a weight load.
+//
+// Workgroup (part p, walker r) walks the 16-row weight blocks r, r + R, ... (R walkers per
+// part).  For each block the 8 waves stream their chunks (whole 128-byte lines, nontemporal,
+// the split kernel's even / odd piece pairing on v_mfma_f32_16x16x32_bf16), then sum their
+// K ranges through LDS in wave order, i.e. in K order (deterministic), and the block's
+// outputs are stored: activated bf16 for gate_up, bf16 (scattered by slot) for down, or,
+// with several parts, fp32 partials [part, rows, n] that stream_reduce_kernel adds in part
+// order.  The weight loads run a ring of chunks ahead across block boundaries: one
+// workgroup per CU leaves no other workgroup to stream while a block is summed, so the stream
+// must not stop there.
+//
+// GATHER (gate_up of a Dense step, one part): token row t is mailbox row gather_slots[t],
+// RMS-normalised with a.norm.  Each wave sums the squares of its pieces of every row (lane
+// order: chunk, then line), the 8 lanes holding a row's pieces add theirs by a butterfly, and
+// the 8 waves' sums are added in the fixed tree ((w0 + w1) + (w2 + w3)) + ((w4 + w5) + (w6 +
+// w7)) through LDS; the scale is 1 / sqrt(sum / K + eps) and each element becomes
+// bf16((x * scale) * w), as in the gather kernel (whose sum of squares runs in another
+// order, so the two agree within one bf16 ulp rather than bit for bit).  Rows past the live
+// rows are zero; a slot outside the mailbox gives a row of quiet NaNs and raises the fault
+// bit.  With gathered_out set, workgroup t stores normalised row t there.
+constexpr int kResidentWaves = 8;
+constexpr int kResidentWorkgroups = 256;  // one per CU
+constexpr int kResidentChunk = 128;       // columns per chunk
+
+// Weight chunks in flight per wave (measured on MI355X for Qwen3-8B gate_up at 16 rows: 8
+// chunks were no faster than 4), and the greatest common divisor for the loop's rounds.
+constexpr int kResidentDepth = 4;
+constexpr int gcd_int(int a, int b) { return b == 0 ? a : gcd_int(b, a % b); }
+
+template <int TG>
+struct ResidentLds {
+  float row_squares[kResidentWaves][8 * TG];
+  // Two buffers of block sums (alternating blocks): wave, token group, half, kq, token.
+  f32x4 block[2][kResidentWaves][TG][2][2][8];
+};
+
+template <int TG, int CPW, bool GATED, bool GATHER>
+__global__ __launch_bounds__(64 * kResidentWaves) __attribute__((amdgpu_waves_per_eu(2))) void resident_gemm_kernel(
+    GemmArgs a) {
+  constexpr int D = kResidentDepth;
+  constexpr int L = D / gcd_int(D, CPW) * CPW;  // chunks per round of the loop: whole blocks and whole rings
+  constexpr int TP = 8 * TG;
+  __shared__ ResidentLds<TG> lds;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int r16 = lane & 15;
+  const int kq = lane >> 4;
+  const int row = r16 & 7;                // weight row within its half / token within its group
+  const int piece = 2 * kq + (r16 >> 3);  // 16-byte piece of the 128-byte line
+  const int parts = static_cast<int>(a.k_split);
+  const int part = static_cast<int>(blockIdx.x) % parts;
+  const int walkers = static_cast<int>(gridDim.x) / parts;
+  const int walker = static_cast<int>(blockIdx.x) / parts;
+  const int64_t row_blocks = (a.n + 15) / 16;
+  const int units = walker < row_blocks ? static_cast<int>((row_blocks - 1 - walker) / walkers) + 1 : 0;
+  const int64_t k0 = static_cast<int64_t>(part * kResidentWaves + wave) * CPW * kResidentChunk;
+  // Columns [k0 + 128 c + 64 l + 8 piece, + 8) of this lane hold data iff 128 c + 64 l < lane_valid.
+  const int64_t lane_valid = a.k - k0 - piece * 8;
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+  auto chunk_column = [](int c) XP_INLINE { return c * kResidentChunk; };
+
+  // Weight chunk c of this wave's part of row block `unit`: w[2 l + h] = line l of rows
+  // 16 rb + 8 h + [0, 8).  Each block is addressed through a buffer resource of its own
+  // (wave-uniform, in scalar registers) whose size ends at the block's last row, so the
+  // per-lane offsets are two constants (one per half) plus immediates, and rows past N,
+  // chunks past K and blocks past the walker's read zeros without a memory access.
+  const uint32_t lane_offset[2] = {static_cast<uint32_t>((row * a.k + k0 + piece * 8) * 2),
+                                   static_cast<uint32_t>(((row + 8) * a.k + k0 + piece * 8) * 2)};
+  auto load_chunk = [&](int unit, int c, u32x4 (&w)[4]) XP_INLINE {
+    const int64_t rb = walker + static_cast<int64_t>(unit) * walkers;
+    const int64_t block_rows = unit < units ? std::min<int64_t>(16, a.n - rb * 16) : 0;
+    const __amdgpu_buffer_rsrc_t rsrc =
+        make_rsrc(a.w + (unit < units ? rb * 16 * a.k : 0), static_cast<uint32_t>(block_rows * a.k * 2));
+#pragma unroll
+    for (int l = 0; l < 2; ++l) {
+      const bool valid = chunk_column(c) + l * 64 < lane_valid;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        w[2 * l + h] = buffer_load16<kLoadNontemporal>(
+            rsrc, valid ? lane_offset[h] + static_cast<uint32_t>((chunk_column(c) + l * 64) * 2) : kOutOfRange);
+      }
+    }
+  };
+
+  // GATHER: mailbox row of token 8 g + row (-1 past the live rows, -2 for a slot outside the
+  // mailbox); read before the weights are requested, so waiting for it waits for nothing else.
+  int source[TG];
+  int mine = -1;
+  if constexpr (GATHER) {
+    if (lane < TP && lane < a.rows) {
+      const int32_t slot = a.gather_slots[lane];
+      mine = slot < 0 || static_cast<int64_t>(slot) >= a.pool_rows ? -2 : slot;
+    }
+#pragma unroll
+    for (int g = 0; g < TG; ++g) {
+      source[g] = __shfl(mine, 8 * g + row, kWave);
+    }
+  } else {
+#pragma unroll
+    for (int g = 0; g < TG; ++g) {
+      source[g] = 8 * g + row;  // activation row
+    }
+  }
+
+  // Token pieces of this wave's chunks: x[c][l][g] = token 8 g + row, columns k0 + 128 c +
+  // 64 l + 8 piece.
+  // The token pieces (and the norm weights) are requested before the weight ring, so the
+  // gather's normalisation runs while the ring is in flight: the wait counts are in order,
+  // and waiting for anything issued after the ring would wait for the ring as well.
+  u32x4 x[CPW][2][TG];
+  // GATHER: the norm weights go straight into LDS (the block buffers, unused until the first
+  // block ends; K <= 8 CPW 128 columns fit them), so they take no registers.
+  static_assert(sizeof(lds.block) >= kResidentWaves * CPW * kResidentChunk * 2, "the norm weights fit the block buffers");
+  uint16_t *norm_lds = reinterpret_cast<uint16_t *>(&lds.block[0][0][0][0][0][0]);
+  if constexpr (GATHER) {
+    if (a.norm != nullptr) {
+      const __amdgpu_buffer_rsrc_t n_rsrc = make_rsrc(a.norm, static_cast<uint32_t>(a.k * 2));
+      for (int v = wave * kWave; v < (a.k + 7) / 8; v += kResidentWaves * kWave) {
+        buffer_load_lds16(n_rsrc, norm_lds + v * 8, static_cast<uint32_t>((v + lane) * 16), 0u);
+      }
+    }
+  }
+  {
+    // GATHER: mailbox rows by slot; otherwise activations [rows, k] (row stride ldx), rows past
+    // the live rows reading as zero.
+    const __amdgpu_buffer_rsrc_t x_rsrc =
+        make_rsrc(a.x, static_cast<uint32_t>((GATHER ? a.pool_rows : a.rows) * a.ldx * 2));
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+#pragma unroll
+      for (int l = 0; l < 2; ++l) {
+        const bool valid = chunk_column(c) + l * 64 < lane_valid;
+        const uint32_t column = static_cast<uint32_t>((k0 + piece * 8 + chunk_column(c) + l * 64) * 2);
+#pragma unroll
+        for (int g = 0; g < TG; ++g) {
+          const int64_t token_row = source[g];
+          x[c][l][g] = buffer_load16(x_rsrc, valid && token_row >= 0
+                                                 ? static_cast<uint32_t>(token_row * a.ldx * 2) + column
+                                                 : kOutOfRange);  // (the pool is below 2 GiB)
+        }
+      }
+    }
+  }
+  u32x4 wbuf[D][4];
+#pragma unroll
+  for (int j = 0; j < D; ++j) {
+    load_chunk(j / CPW, j % CPW, wbuf[j]);
+  }
+
+  if constexpr (GATHER) {
+    wait_vmcnt<4 * D>();  // the token pieces and the norm weights; the ring stays in flight
+    float scale[TG];
+    if (a.norm != nullptr) {
+      float squares[TG];
+#pragma unroll
+      for (int g = 0; g < TG; ++g) {
+        squares[g] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < CPW; ++c) {
+#pragma unroll
+          for (int l = 0; l < 2; ++l) {
+            add_squares(x[c][l][g], squares[g]);  // column order within the lane
+          }
+        }
+        // The 8 lanes of token row (lane & 7) differ in lane bits 3 .. 5.
+        squares[g] += __shfl_xor(squares[g], 8, kWave);
+        squares[g] += __shfl_xor(squares[g], 16, kWave);
+        squares[g] += __shfl_xor(squares[g], 32, kWave);
+        if (lane < 8) {
+          lds.row_squares[wave][8 * g + lane] = squares[g];
+        }
+      }
+      __syncthreads();  // every wave's row sums and norm weights are in LDS
+#pragma unroll
+      for (int g = 0; g < TG; ++g) {
+        const float(*s)[TP] = lds.row_squares;
+        const int t = 8 * g + row;
+        const float total = ((s[0][t] + s[1][t]) + (s[2][t] + s[3][t])) + ((s[4][t] + s[5][t]) + (s[6][t] + s[7][t]));
+        scale[g] = 1.0f / sqrtf(total / static_cast<float>(a.k) + a.eps);
+      }
+    }
+    const u32x4 poison = {kPoisonBf16x2, kPoisonBf16x2, kPoisonBf16x2, kPoisonBf16x2};
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+#pragma unroll
+      for (int l = 0; l < 2; ++l) {
+        const bool valid = chunk_column(c) + l * 64 < lane_valid;
+#pragma unroll
+        for (int g = 0; g < TG; ++g) {
+          if (source[g] == -2) {
+            x[c][l][g] = valid ? poison : zero;
+          } else if (a.norm != nullptr) {
+            const u32x4 weight = valid ? load16(norm_lds + k0 + piece * 8 + chunk_column(c) + l * 64) : zero;
+            x[c][l][g] = normalize_chunk(x[c][l][g], scale[g], weight);
+          }
+        }
+      }
+    }
+    __syncthreads();  // every wave has read the norm weights before the block buffers are reused
+    // Lane t < TP holds slot t's class (mine); one lane of workgroup 0 raises the fault bit.
+    const bool any_bad = __ballot(mine == -2) != 0;
+    if (blockIdx.x == 0 && wave == 0 && lane == 0 && any_bad) {
+      raise_fault(a.fault, kFaultSlotOutOfRange);
+    }
+    if (a.gathered_out != nullptr && blockIdx.x < a.rows && static_cast<int>(blockIdx.x) < TP &&
+        row == static_cast<int>(blockIdx.x % 8)) {
+      // Workgroup t stores normalised row t (the lanes holding its pieces, every wave).
+      const int g = static_cast<int>(blockIdx.x / 8);
+#pragma unroll
+      for (int gg = 0; gg < TG; ++gg) {
+        if (gg != g) {
+          continue;
+        }
+#pragma unroll
+        for (int c = 0; c < CPW; ++c) {
+#pragma unroll
+          for (int l = 0; l < 2; ++l) {
+            if (chunk_column(c) + l * 64 < lane_valid) {
+              store16(a.gathered_out + blockIdx.x * a.k + k0 + piece * 8 + chunk_column(c) + l * 64, x[c][l][gg]);
+            }
+          }
+        }
+      }
+    }
+  }
+
+  f32x4 acc[TG][2];
+#pragma unroll
+  for (int g = 0; g < TG; ++g) {
+    acc[g][0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    acc[g][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+  auto compute_chunk = [&](int c, const u32x4 (&w)[4]) XP_INLINE {
+#pragma unroll
+    for (int l = 0; l < 2; ++l) {
+#pragma unroll
+      for (int g = 0; g < TG; ++g) {
+        acc[g][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(w[2 * l]), as_bf16x8(x[c][l][g]), acc[g][0], 0, 0, 0);
+        acc[g][1] =
+            __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(w[2 * l + 1]), as_bf16x8(x[c][l][g]), acc[g][1], 0, 0, 0);
+      }
+    }
+  };
+
+  // Block sums.  At the end of a block each wave's lanes (i < 8, q < 2) add the odd pieces'
+  // block from lane + 40, which leaves weight rows 16 rb + 8 h + 4 q + v for token 8 g + i,
+  // and store them to the block's LDS buffer; one chunk into the next block, behind a
+  // barrier, 32 TG lanes (16 per wave) add the 8 waves' values in wave order and store the
+  // outputs.  The weight loads in flight meanwhile keep the stream going.
+  auto store_block = [&](int unit) XP_INLINE {
+    f32x4(*block)[TG][2][2][8] = lds.block[unit & 1];
+#pragma unroll
+    for (int g = 0; g < TG; ++g) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          acc[g][h][v] += __shfl(acc[g][h][v], lane + 40, kWave);
+        }
+        if (kq < 2 && r16 < 8) {
+          block[wave][g][h][kq][r16] = acc[g][h];
+        }
+        acc[g][h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+    }
+  };
+  // The reducing lane's item (g, h, q, i) and its output row, looked up once: a dependent
+  // load of the scatter slot inside the loop would wait for every weight load before it.
+  const int item = wave * 16 + r16;
+  const bool reducer = lane < 16 && item < 32 * TG;
+  const int item_i = item & 7;
+  const int item_q = (item >> 3) & 1;
+  const int item_h = (item >> 4) & 1;
+  const int item_g = item >> 5;
+  const int64_t item_token = 8 * item_g + item_i;
+  uint16_t *item_out = reducer && parts == 1 && item_token < a.rows ? output_row(a, item_token) : nullptr;
+  auto reduce_block = [&](int unit) XP_INLINE {
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __asm__ volatile("s_barrier" ::: "memory");
+    if (!reducer) {
+      return;
+    }
+    f32x4(*block)[TG][2][2][8] = lds.block[unit & 1];
+    f32x4 sum = block[0][item_g][item_h][item_q][item_i];
+#pragma unroll
+    for (int w = 1; w < kResidentWaves; ++w) {
+      sum += block[w][item_g][item_h][item_q][item_i];
+    }
+    const int64_t rb = walker + static_cast<int64_t>(unit) * walkers;
+    const int64_t n = rb * 16 + 8 * item_h + 4 * item_q;
+    if (item_token >= a.rows || n >= a.n) {
+      return;
+    }
+    if (parts > 1) {
+      *reinterpret_cast<f32x4 *>(a.partials + (part * a.rows + item_token) * a.n + n) = sum;
+    } else if (item_out != nullptr) {
+      if constexpr (GATED) {
+        const float h0 = gated_silu(sum[0], sum[1], a.act);
+        const float h1 = gated_silu(sum[2], sum[3], a.act);
+        *reinterpret_cast<uint32_t *>(item_out + n / 2) = pack_bf16x2(h0, h1);
+      } else {
+        u32x2 packed = {pack_bf16x2(sum[0], sum[1]), pack_bf16x2(sum[2], sum[3])};
+        *reinterpret_cast<u32x2 *>(item_out + n) = packed;
+      }
+    }
+  };
+
+  // The wave's chunk stream: chunk f is chunk f % CPW of block f / CPW; ring slot f % D.  The
+  // loop runs whole rounds of D chunks (a multiple of CPW); chunks past the last block read
+  // zeros without a memory access, so every load is unconditional and the wait counts track
+  // the chunks in flight exactly.  The block count is workgroup-uniform, so every wave
+  // reaches every barrier.
+  const int rounds = (units * CPW + L - 1) / L;
+  for (int r = 0; r < rounds; ++r) {
+#pragma unroll
+    for (int j = 0; j < L; ++j) {
+      const int unit = r * (L / CPW) + j / CPW;
+      const int c = j % CPW;
+      compute_chunk(c, wbuf[j % D]);
+      load_chunk(r * (L / CPW) + (j + D) / CPW, (j + D) % CPW, wbuf[j % D]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (c == 0 && unit >= 1 && unit <= units) {
+        reduce_block(unit - 1);
+      }
+      if (c == CPW - 1 && unit < units) {
+        store_block(unit);
+      }
+    }
+  }
+  if (units > 0 && rounds * (L / CPW) == units) {
+    reduce_block(units - 1);  // the last block had no next block to reduce it in
+  }
+}
+
 // ------------------------------------------------------------------ tile
 // LDS tiles are rows of 64 bf16 (128 bytes = eight 16-byte chunks).  gfx950 serves
 // ds_read_b128 sixteen lanes at a time from a 256-byte bank line, i.e. two tile rows, so
@@ -1752,6 +2095,29 @@ const void *stream_kernel() {
   return reinterpret_cast<const void *>(&stream_gemm_kernel<GATED, GATHER>);
 }
 
+// The resident kernel for 16 token rows (two groups of 8) and `cpw` chunks per wave (1 to
+// 4); the gather fuses into gate_up only.  (Four groups, 32 rows, were measured and dropped:
+// the token pieces then take 128 registers per lane and the kernel spills, and Qwen3-8B at
+// 32 rows took 77.0 us per layer against 74.8 us on the tile kernels.)
+constexpr int kResidentMaxChunksPerWave = 4;
+constexpr int kResidentGroups = 2;
+
+template <bool GATED, bool GATHER>
+const void *resident_kernel(int cpw) {
+  using Kernel = void (*)(GemmArgs);
+  static const Kernel table[kResidentMaxChunksPerWave] = {
+      &resident_gemm_kernel<kResidentGroups, 1, GATED, GATHER>, &resident_gemm_kernel<kResidentGroups, 2, GATED, GATHER>,
+      &resident_gemm_kernel<kResidentGroups, 3, GATED, GATHER>, &resident_gemm_kernel<kResidentGroups, 4, GATED, GATHER>};
+  return reinterpret_cast<const void *>(table[cpw - 1]);
+}
+
+const void *resident_kernel_for(bool gated, bool gather, int cpw) {
+  if (gated) {
+    return gather ? resident_kernel<true, true>(cpw) : resident_kernel<true, false>(cpw);
+  }
+  return resident_kernel<false, false>(cpw);
+}
+
 struct TileShape {
   int bm;
   int bn;
@@ -1984,6 +2350,52 @@ GemmChoice choose_tile(int64_t capacity, int64_t n, int64_t k) {
   return best;
 }
 
+// The resident kernel's K parts and chunks per wave at `capacity` rows (9 to 16), with its
+// modelled cost in microseconds (-1: not applicable).  Every workgroup streams its blocks'
+// columns of its part at one workgroup's rate after a fixed prologue (launch, the token
+// pieces, the first weight round trip), and the busiest workgroup sets the time; more than
+// one part adds the partial sums and the reduction launch.  With the gather fused the part
+// must cover K (a row's sum of squares needs every column).  Least-squares fit (relative
+// error) to the kernel's durations on MI355X for the Qwen3 0.6B / 1.7B / 4B / 8B gate_up
+// (gather fused) and the Qwen3 1.7B / 4B / 8B and 32B TP-shard down projections at 9 and 16
+// rows, weights streamed from HBM: within 10 %.  The weight rows must fill the grid (N of at
+// least 2048: a Router projection's few experts do not).
+constexpr int64_t kResidentMinRows = 9;
+constexpr int64_t kResidentMaxRows = 8 * kResidentGroups;
+constexpr int64_t kResidentMinN = 2048;
+constexpr double kResidentWorkgroupBytesPerUs[2] = {35.7e3, 24.8e3};  // index: gather fused
+constexpr double kResidentFixedUs[2] = {7.8, 8.0};
+
+GemmChoice choose_resident(int64_t capacity, int64_t n, int64_t k, bool gather, double &cost) {
+  GemmChoice best{GemmKind::Resident, kResidentGroups, 0, 0};
+  cost = -1.0;
+  if (capacity < kResidentMinRows || capacity > kResidentMaxRows || n < kResidentMinN || n * k * 2 > INT32_MAX) {
+    return best;
+  }
+  const int64_t chunks = (k + kResidentChunk - 1) / kResidentChunk;
+  const int64_t row_blocks = (n + 15) / 16;
+  for (int cpw = 1; cpw <= kResidentMaxChunksPerWave; ++cpw) {
+    const int64_t part_chunks = static_cast<int64_t>(kResidentWaves) * cpw;
+    const int64_t parts = (chunks + part_chunks - 1) / part_chunks;
+    if ((gather && parts > 1) || parts > kResidentWorkgroups) {
+      continue;
+    }
+    const int64_t walkers = std::min<int64_t>(kResidentWorkgroups / parts, row_blocks);
+    const int64_t blocks = (row_blocks + walkers - 1) / walkers;
+    const double columns = static_cast<double>(std::min<int64_t>(part_chunks * kResidentChunk, k));
+    double us = kResidentFixedUs[gather ? 1 : 0] +
+                static_cast<double>(blocks) * 16.0 * columns * 2.0 / kResidentWorkgroupBytesPerUs[gather ? 1 : 0];
+    if (parts > 1) {
+      us += kStreamReduceUs + 8.0 * static_cast<double>(parts * capacity * n) / kStreamPartialBytesPerUs;
+    }
+    if (cost < 0.0 || us < cost * (1.0 - kSplitTieMargin)) {
+      best = {GemmKind::Resident, kResidentGroups, part_chunks * kResidentChunk, parts};
+      cost = us;
+    }
+  }
+  return best;
+}
+
 }  // namespace
 
 // The split or the stream kernel for a decode size, whichever the cost model prefers, and
@@ -2002,10 +2414,18 @@ GemmChoice choose_decode(int64_t capacity, int64_t n, int64_t k, double &cost) {
 }
 
 GemmChoice choose_gemm(int64_t capacity, int64_t n, int64_t k, bool gated) {
-  // The split and stream kernels address the weights through one 32-bit buffer range.
+  // 9 to 16 rows: the resident kernel where its model is cheaper than the split / stream
+  // choice's.  Measured on MI355X (kernel durations, weights streamed from HBM): the Qwen3-32B
+  // TP shard's down at 9 / 16 rows 12.8 / 13.3 us + a 4.0 us reduction (stream, 8 slices)
+  // -> 12.3 / 13.2 us (one part, no reduction); Qwen3-4B and 1.7B down stay on the stream
+  // kernel (resident 14.2 / 10.7 us + reduction against 12.5 / 8.5 us + reduction).
+  // The split, stream and resident kernels address the weights through one 32-bit buffer range.
   if (capacity <= kDecodeMaxRows && n * k * 2 <= INT32_MAX) {
-    double cost = 0.0;
-    return choose_decode(capacity, n, k, cost);
+    double decode_us = 0.0;
+    const GemmChoice decode = choose_decode(capacity, n, k, decode_us);
+    double resident_us = 0.0;
+    const GemmChoice resident = choose_resident(capacity, n, k, false, resident_us);
+    return resident_us >= 0.0 && resident_us < decode_us ? resident : decode;
   }
   GemmChoice choice = choose_tile(capacity, n, k);
   // Token tiles more than half full carry twice the MFMA work per weight byte, which the
@@ -2029,6 +2449,18 @@ GemmChoice choose_gemm(int64_t capacity, int64_t n, int64_t k, bool gated) {
 // kernel; for projections of many units, split_gathered_kernel gathers once per workgroup
 // of a two-per-CU persistent grid instead.
 GemmChoice choose_dense_gate_up(int64_t capacity, int64_t n, int64_t k, bool &fused) {
+  // 9 to 16 rows: the resident kernel with the gather fused, wherever one part covers K.
+  // Measured on MI355X (kernel durations at 9 / 16 rows, weights streamed from HBM) against
+  // the choices of the decode models: Qwen3-8B 40.0 / 40.0 us (stream kernel, gather fused)
+  // -> 37.9 / 38.9, Qwen3-4B 28.0 / 28.6 (the same) -> 24.0 / 24.7, Qwen3-1.7B 4.5 + 17.3 /
+  // 4.6 + 19.0 (gather launch, split kernel) -> 17.1 / 17.8, Qwen3-0.6B 3.1 + 8.7 / 3.5 + 9.5
+  // -> 10.0 / 10.4.
+  double resident_us = 0.0;
+  const GemmChoice resident = choose_resident(capacity, n, k, true, resident_us);
+  if (resident_us >= 0.0) {
+    fused = true;
+    return resident;
+  }
   fused = capacity <= kDecodeMaxRows && n * k * 2 <= INT32_MAX;
   if (!fused) {
     return choose_gemm(capacity, n, k, true);
@@ -2094,6 +2526,7 @@ int64_t scratch_slices(GemmChoice choice, int64_t k) {
     case GemmKind::Stream:
       return stream_slices(k, choice.k_slice);
     case GemmKind::Tile:
+    case GemmKind::Resident:
       return choice.k_split;
     default:
       return 1;  // the split kernel sums its K ranges in LDS
@@ -2179,6 +2612,13 @@ GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmCho
     kernel.block = dim3(64 * kSplitWaves, 1, 1);
     kernel.shmem = static_cast<unsigned>((capacity < kSplitGroupTokens ? capacity : kSplitGroupTokens) * (args.k + 16) * 2 +
                                          kSplitGatheredScratchBytes);
+  } else if (choice.kind == GemmKind::Resident) {
+    const int64_t row_blocks = (args.n + 15) / 16;
+    const int cpw = static_cast<int>(choice.k_slice / (kResidentWaves * kResidentChunk));
+    const int64_t walkers = std::min<int64_t>(kResidentWorkgroups / choice.k_split, row_blocks);
+    kernel.func = resident_kernel_for(gated, fused_gather && gated, cpw);
+    kernel.grid = dim3(static_cast<unsigned>(choice.k_split * walkers), 1, 1);
+    kernel.block = dim3(64 * kResidentWaves, 1, 1);
   } else if (choice.kind == GemmKind::Stream) {
     const int64_t groups = ((args.n + 15) / 16 + kStreamWaves - 1) / kStreamWaves;
     const int64_t slices = stream_slices(args.k, choice.k_slice);
@@ -2284,6 +2724,14 @@ std::string gemm_name(GemmChoice choice, bool gated) {
   }
   if (choice.kind == GemmKind::Stream) {
     return "stream" + prefix + "_t16";
+  }
+  if (choice.kind == GemmKind::Resident) {
+    std::string name = "resident" + prefix + "_t" + std::to_string(8 * choice.variant) + "_c" +
+                       std::to_string(choice.k_slice / (kResidentWaves * kResidentChunk));
+    if (choice.k_split > 1) {
+      name += "_p" + std::to_string(choice.k_split);
+    }
+    return name;
   }
   const TileShape &shape = kTileShapes[choice.variant];
   std::string name = "tile" + prefix + "_" + std::to_string(shape.bm) + "x" + std::to_string(shape.bn);

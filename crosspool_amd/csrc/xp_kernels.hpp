@@ -363,8 +363,12 @@ struct GemmArgs {
 };
 
 // SplitGathered: the split kernel's units walked by a persistent grid that gathers the token
-// rows once per workgroup (gate_up of a Dense step at decode sizes only).
-enum class GemmKind : int { Split = 1, Tile = 2, Stream = 3, SplitGathered = 4 };
+// rows once per workgroup (gate_up of a Dense step at decode sizes only).  Resident: the token
+// rows (9 to 32) held in registers by a one-workgroup-per-CU grid that walks 16-row weight
+// blocks; variant = token groups of 8 (2 or 4), k_slice = the columns of one K part (8 waves
+// x 128-wide chunks), k_split = K parts over the grid (more than one: fp32 partial sums and
+// the ordered reduction).
+enum class GemmKind : int { Split = 1, Tile = 2, Stream = 3, SplitGathered = 4, Resident = 5 };
 
 struct GemmChoice {
   GemmKind kind;

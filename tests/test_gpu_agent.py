@@ -109,7 +109,6 @@ def test_config3_qwen3_8b_layer(device, rows):
 @pytest.mark.parametrize(
     "hidden,intermediate,rows,variant",
     [
-        (4096, 12288, 16, "stream_gated_t16+gather"),
         (4096, 12288, 1, "split_gated_t8_k8_persistent+gather"),
         (4096, 12288, 8, "split_gated_t8_k8_persistent+gather"),
         (2560, 9728, 3, "split_gated_t8_k4_persistent+gather"),
@@ -122,12 +121,11 @@ def test_config3_qwen3_8b_layer(device, rows):
     ],
 )
 def test_fused_gather_matches_separate_kernels_bitwise(device, normed, hidden, intermediate, rows, variant):
-    # At decode sizes the gather (+ RMSNorm) runs inside gate_up: the stream kernel (Qwen3-8B,
-    # 16 rows), the split kernel (hidden sizes up to 4096, up to 8 rows) or its persistent
-    # variant (projections of at least 512 units), which stage the same bits the gather
-    # kernel writes.  The kernel-level projections take the split or stream kernel with the
-    # same K ranges, so the step must equal gather kernel -> gate_up -> down -> scatter bit
-    # for bit.
+    # Up to 8 rows the gather (+ RMSNorm) runs inside gate_up: the split kernel (hidden sizes
+    # up to 4096) or its persistent variant (projections of at least 512 units), which stage
+    # the same bits the gather kernel writes.  The kernel-level projections take the split
+    # kernel with the same K ranges, so the step must equal gather kernel -> gate_up -> down
+    # -> scatter bit for bit.
     from crosspool_amd import dense
 
     pool_rows = 256
@@ -153,6 +151,76 @@ def test_fused_gather_matches_separate_kernels_bitwise(device, normed, hidden, i
         variant.removesuffix("+gather").removesuffix("_persistent"))
     assert_bitwise_equal(pool_gpu.cpu(), expected.cpu())
     _check_mailbox(pool_gpu, pool, slots, w_gate_up, w_down, norm_weight if normed else None)
+
+
+@pytest.mark.parametrize("normed", [True, False])
+@pytest.mark.parametrize(
+    "hidden,intermediate,rows,gate_up,down",
+    [
+        (4096, 12288, 16, "resident_gated_t16_c4+gather", "stream_t16"),
+        (4096, 12288, 9, "resident_gated_t16_c4+gather", "stream_t16"),
+        (2560, 9728, 12, "resident_gated_t16_c3+gather", "stream_t16"),
+        (2048, 6144, 16, "resident_gated_t16_c2+gather", "stream_t16"),
+        (1024, 3072, 10, "resident_gated_t16_c1+gather", "split_t16_k8"),
+        # K = 4088 ends inside a 128-wide chunk (a partial last chunk, padded chunks past it);
+        # 2 x 4104 = 8208 gate_up rows end inside a 16-row block.
+        (4088, 4104, 13, "resident_gated_t16_c4+gather", "stream_t16"),
+        # the Qwen3-32B TP shard: gate_up on a separate gather (K = 5120 exceeds one part), down
+        # on the resident kernel with one part
+        (5120, 3200, 11, "stream_gated_t16", "resident_t16_c4"),
+    ],
+)
+def test_resident_step_matches_oracle(device, normed, hidden, intermediate, rows, gate_up, down):
+    # 9 to 16 rows: the token rows stay in registers of a one-per-CU grid; gate_up gathers and
+    # normalises them itself (its sum of squares runs in its own order, so it agrees with the
+    # gather kernel within one bf16 ulp, not bit for bit).  Checked against the oracle's
+    # mailbox step; replays repeat bit for bit, also through graph dispatch.
+    assert _native.dense_gate_up_variant(rows, hidden, intermediate) == gate_up
+    assert _native.gemm_variant(rows, hidden, intermediate, False) == down
+    pool_rows = 96
+    pool = o.generate_hidden_states(pool_rows, hidden, 37)
+    w_gate_up, w_down, norm_weight = o.generate_layer(hidden, intermediate, 38)
+    slots = o.generate_slots(pool_rows, rows, 39)
+    outputs = []
+    for graph_dispatch in (False, True):
+        with FfnAgent(device, graph_dispatch=graph_dispatch) as agent:
+            agent.register_layer(
+                instance_index=0, layer_ordinal=0, weights=_weights(w_gate_up, w_down, device),
+                norm_weight=to_device(norm_weight, device) if normed else None,
+            )
+            agent.materialize(maximum_row_capacity=16)
+            for _ in range(2):
+                pool_gpu = to_device(pool, device)
+                agent.execute(instance_index=0, layer_ordinal=0, pool=pool_gpu, slots=slots_tensor(slots, device))
+                agent.check_health()
+                outputs.append(pool_gpu.cpu())
+    for other in outputs[1:]:
+        assert_bitwise_equal(other, outputs[0])
+    _check_mailbox(outputs[0], pool, slots, w_gate_up, w_down, norm_weight if normed else None)
+
+
+def test_resident_gather_poisons_bad_slots(device):
+    # A slot outside the mailbox: its row is staged as quiet NaNs, its output is dropped, the
+    # fault bit is raised, and the other rows are their own FFN.
+    hidden, intermediate, pool_rows = 2048, 6144, 64
+    assert _native.dense_gate_up_variant(12, hidden, intermediate).startswith("resident")
+    pool = o.generate_hidden_states(pool_rows, hidden, 41)
+    w_gate_up, w_down, norm_weight = o.generate_layer(hidden, intermediate, 42)
+    slots = o.generate_slots(pool_rows, 12, 43)
+    bad = slots.copy()
+    bad[5] = pool_rows + 7
+    with FfnAgent(device) as agent:
+        agent.register_layer(
+            instance_index=0, layer_ordinal=0, weights=_weights(w_gate_up, w_down, device),
+            norm_weight=to_device(norm_weight, device),
+        )
+        agent.materialize(maximum_row_capacity=16)
+        pool_gpu = to_device(pool, device)
+        agent.execute(instance_index=0, layer_ordinal=0, pool=pool_gpu, slots=slots_tensor(bad, device))
+        with pytest.raises(FfnHealthError):
+            agent.check_health()
+    live = np.delete(slots, 5)
+    _check_mailbox(pool_gpu, pool, live, w_gate_up, w_down, norm_weight)
 
 
 @pytest.mark.parametrize("normed", [True, False])

@@ -142,7 +142,8 @@ def test_zero_weights_give_zero_output(device):
 
 def test_variant_selection_covers_every_family(device):
     assert _native.gemm_variant(1, 24576, 4096, True).startswith("split")
-    assert _native.gemm_variant(16, 24576, 4096, True).startswith("stream")
+    assert _native.gemm_variant(16, 6400, 5120, True).startswith("stream")
+    assert _native.gemm_variant(16, 24576, 4096, True).startswith("resident")
     assert _native.gemm_variant(2048, 24576, 4096, True).startswith("tile")
     # the Qwen3-8B cases of test_qwen3_8b_projections reach every tile shape and K splits
     chosen = {_native.gemm_variant(rows, n, k, gated) for rows in (32, 64, 128, 256, 512)
@@ -178,7 +179,7 @@ def test_decode_shapes_reach_both_decode_kernels(device):
     names = {_native.gemm_variant(rows, n, k, gated) for hidden, intermediate in DECODE_SHAPES
              for rows in DECODE_ROWS if rows <= 16
              for n, k, gated in ((2 * intermediate, hidden, True), (hidden, intermediate, False))}
-    assert {name.split("_")[0] for name in names} == {"split", "stream"}
+    assert {name.split("_")[0] for name in names} == {"split", "stream", "resident"}
     # the split kernel with one and with two token groups, gated and not
     families = {name.rsplit("_k", 1)[0] for name in names if name.startswith("split")}
     assert {"split_t8", "split_t16", "split_gated_t8", "split_gated_t16"} <= families
@@ -190,7 +191,7 @@ def test_decode_projections_on_ragged_geometry(device, hidden, intermediate, row
     x = o.generate_hidden_states(rows, hidden, 17)
     w_gate_up, w_down = _layer(hidden, intermediate)
     gu_d, dn_d = to_device(w_gate_up, device), to_device(w_down, device)
-    family = ("split", "stream") if rows <= 16 else ("tile",)
+    family = ("split", "stream", "resident") if rows <= 16 else ("tile", "resident")
     assert _native.gemm_variant(rows, 2 * intermediate, hidden, True).startswith(family)
     assert _native.gemm_variant(rows, hidden, intermediate, False).startswith(family)
     activated = dense.gate_up_silu(to_device(x, device), gu_d)
@@ -200,6 +201,39 @@ def test_decode_projections_on_ragged_geometry(device, hidden, intermediate, row
     torch.cuda.synchronize()
     assert_activated_within_bounds(activated, x, w_gate_up)
     assert_projection_within_bounds(out, activated.cpu(), w_down)
+    assert_bitwise_equal(again.cpu(), out.cpu())
+
+
+@pytest.mark.parametrize("rows", [9, 16])
+@pytest.mark.parametrize(
+    "hidden,intermediate,projection,variant",
+    [
+        (4096, 12288, "gate_up", "resident_gated_t16_c4"),
+        # K = 6000: two parts over the grid (fp32 partials, the ordered reduction with the gated
+        # epilogue), the last 128-wide chunk partial and padded chunks past it.
+        (6000, 6144, "gate_up", "resident_gated_t16_c3_p2"),
+        (5120, 3200, "down", "resident_t16_c4"),  # the Qwen3-32B TP shard's down, one part
+    ],
+)
+def test_resident_projections(device, rows, hidden, intermediate, projection, variant):
+    # The token rows held in registers of a one-per-CU grid walking 16-row weight blocks.
+    x_rows = o.generate_hidden_states(rows, hidden if projection == "gate_up" else intermediate, 51)
+    w_gate_up, w_down = _layer(hidden, intermediate, 52)
+    x = to_device(x_rows, device)
+    if projection == "gate_up":
+        assert _native.gemm_variant(rows, 2 * intermediate, hidden, True) == variant
+        w = to_device(w_gate_up, device)
+        out = dense.gate_up_silu(x, w)
+        again = dense.gate_up_silu(x, w)
+        torch.cuda.synchronize()
+        assert_activated_within_bounds(out, x_rows, w_gate_up)
+    else:
+        assert _native.gemm_variant(rows, hidden, intermediate, False) == variant
+        w = to_device(w_down, device)
+        out = dense.down(x, w)
+        again = dense.down(x, w)
+        torch.cuda.synchronize()
+        assert_projection_within_bounds(out, x_rows, w_down)
     assert_bitwise_equal(again.cpu(), out.cpu())
 
 

@@ -307,12 +307,19 @@ def test_abi_rejects_invalid_arguments_before_touching_the_device():
 
 
 def test_gemm_variant_selection():
-    # decode sizes: the split or the stream kernel by the cost model, never a tile
-    for rows in (1, 2, 4, 8, 16):
+    # decode sizes: the split, stream or resident kernel, never a tile
+    for rows in (1, 2, 4, 8, 9, 16):
         for n, k, gated in ((24576, 4096, True), (4096, 12288, False), (19456, 2560, True), (2560, 9728, False)):
-            assert _native.gemm_variant(rows, n, k, gated).startswith(("split", "stream"))
+            assert _native.gemm_variant(rows, n, k, gated).startswith(("split", "stream", "resident"))
     assert _native.gemm_variant(1, 4096, 12288, False) == "split_t8_k8"
-    assert _native.gemm_variant(16, 24576, 4096, True) == "stream_gated_t16"
+    # 9 to 16 rows: the resident kernel where its weight rows fill the grid (N >= 2048),
+    # K split over the grid when one part of 8 waves x 4 chunks does not cover it
+    assert _native.gemm_variant(16, 24576, 4096, True) == "resident_gated_t16_c4"
+    assert _native.gemm_variant(9, 12288, 6000, True) == "resident_gated_t16_c3_p2"
+    assert _native.gemm_workspace_bytes(9, 12288, 6000, True) == 2 * 9 * 12288 * 4
+    assert _native.gemm_variant(16, 5120, 3200, False) == "resident_t16_c4"
+    assert _native.gemm_workspace_bytes(16, 5120, 3200, False) == 0
+    assert _native.gemm_variant(16, 6400, 5120, True) == "stream_gated_t16"
     # Qwen3-4B and Qwen3-0.6B down: K ranges of whole 128-wide chunks let the split kernel
     # take 8 ranges (160 and 64 workgroups), with no scratch
     assert _native.gemm_variant(1, 2560, 9728, False) == "split_t8_k8"
@@ -328,6 +335,7 @@ def test_gemm_variant_selection():
     # (Qwen3-8B down: 8 K slices of 1536, whose fp32 partials the reduction launch sums)
     assert _native.gemm_variant(16, 1024, 3072, False) == "split_t16_k8"
     assert _native.gemm_workspace_bytes(16, 1024, 3072, False) == 0
+    assert _native.gemm_variant(16, 1536, 8960, False) == "stream_t16"
     assert _native.gemm_variant(16, 4096, 12288, False) == "stream_t16"
     assert _native.gemm_workspace_bytes(16, 4096, 12288, False) == 8 * 16 * 4096 * 4
     assert _native.gemm_variant(2048, 24576, 4096, True) == "tile_gated_256x256"
@@ -347,7 +355,12 @@ def test_dense_step_fuses_the_gather_at_decode_sizes():
         assert _native.dense_gate_up_variant(rows, 2560, 9728) == "split_gated_t8_k4_persistent+gather"
         assert _native.dense_gate_up_variant(rows, 4096, 12288) == "split_gated_t8_k8_persistent+gather"
         assert "+gather" not in _native.dense_gate_up_variant(rows, 5120, 3200)
-    assert _native.dense_gate_up_variant(16, 4096, 12288) == "stream_gated_t16+gather"
+    # 9 to 16 rows: the resident kernel gathers and normalises the rows itself when one part
+    # covers K (not the 32B TP shard's 5120, which keeps a separate gather)
+    for rows in (9, 16):
+        assert _native.dense_gate_up_variant(rows, 4096, 12288) == "resident_gated_t16_c4+gather"
+        assert _native.dense_gate_up_variant(rows, 1024, 3072) == "resident_gated_t16_c1+gather"
+        assert "+gather" not in _native.dense_gate_up_variant(rows, 5120, 3200)
     assert _native.dense_gate_up_variant(32, 4096, 12288) == "tile_gated_64x64"
     assert _native.dense_gate_up_variant(2048, 4096, 12288) == "tile_gated_256x256"
 
