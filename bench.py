@@ -19,9 +19,8 @@ calibration, then gate_up at the headline and decode sizes), for
 ``--ceilings`` instead measures the hardware limits the kernels are judged
 against (libxpool_probes.so): a pure-MFMA loop, two HBM read patterns, the
 GPU idle time a hipGraphLaunch adds per replay, and the cost of a grid-wide
-dependency (a kernel boundary against an in-kernel counter handoff; with
-``--cooperative`` also the runtime's grid barrier), and prints them as one JSON
-line.
+dependency (a kernel boundary against an in-kernel counter handoff), and prints
+them as one JSON line.
 """
 
 from __future__ import annotations
@@ -40,6 +39,7 @@ sys.path.insert(0, str(REPO_ROOT))
 HIDDEN, INTERMEDIATE = 4096, 12288
 POOL_SLOTS = 8192
 SWEEP = (1, 4, 16, 32, 64, 256, 1024, 2048, 4096)
+GRAPH_DISPATCH_TOKENS = (1, 32, 2048)  # replays timed through the instantiated hipGraph too
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 # Copies of the gate_up weights the decode roofline rotates through (3 x 201 MB exceeds
@@ -78,14 +78,9 @@ def parse_args() -> argparse.Namespace:
     parser.add_argument("--decode-tokens", type=int, default=32)
     parser.add_argument("--sweep-steps", type=int, default=30)
     parser.add_argument("--no-sweep", action="store_true")
-    parser.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample length")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--kernels-only", action="store_true", help="launch only the profiled kernels, then exit")
     parser.add_argument("--ceilings", action="store_true", help="measure the hardware ceilings, then exit")
-    parser.add_argument("--cooperative", action="store_true",
-                        help="with --ceilings: also time the runtime's cooperative grid barrier (rocprofv3 "
-                             "ends with a segmentation fault at exit after a cooperative launch, before its "
-                             "trace files are written, so traced runs leave this out)")
     parser.add_argument("--prewarm-seconds", type=float, default=2.0,
                         help="untimed replays before the headline's warmup, so clocks are at steady state")
     return parser.parse_args()
@@ -156,7 +151,7 @@ def mfma_ceiling(stream) -> dict:
             "clock_ghz": round(cycles / (ticks * 10.0), 3) if ticks > 0 else None}
 
 
-def run_ceilings(device, cooperative: bool = False) -> dict:
+def run_ceilings(device) -> dict:
     """Hardware limits measured with HIP events on the current stream (see the module doc)."""
 
     import ctypes
@@ -267,9 +262,9 @@ def run_ceilings(device, cooperative: bool = False) -> dict:
     result["replay_us_qwen3_0_6b_t1"] = {key: round(value, 2) for key, value in graph_points.items()}
     result["graph_launch_extra_us"] = round(graph_points["graph"] - graph_points["direct"], 2)
 
-    # A grid-wide dependency: empty kernels back to back, a producer -> consumer handoff
+    # A grid-wide dependency: empty kernels back to back, and a producer -> consumer handoff
     # across a kernel boundary and inside one launch (one counter, or a counter per 8
-    # producers), and the runtime's cooperative grid barrier.
+    # producers).
     result["empty_kernel_us"] = round(per_launch(
         lambda index=0: checked(probes.xp_probe_empty(256, handle)), 200) * 1e6, 2)
     words = torch.zeros(512 * 8, dtype=torch.int32, device=device)
@@ -294,12 +289,6 @@ def run_ceilings(device, cooperative: bool = False) -> dict:
         handoff.append(point)
     torch.cuda.synchronize(device)
     result["handoff"] = {"points": handoff, "flag": int(flag.item())}
-    if not cooperative:
-        return result
-    sync_times = {syncs: per_launch(lambda index=0, syncs=syncs: checked(probes.xp_probe_grid_sync(256, syncs, handle)),
-                                    20) * 1e6 for syncs in (1, 11)}
-    result["cooperative_grid_sync"] = {"workgroups": 256, "launch_with_one_sync_us": round(sync_times[1], 2),
-                                       "per_further_sync_us": round((sync_times[11] - sync_times[1]) / 10, 2)}
     return result
 
 
@@ -324,7 +313,7 @@ def main() -> int:
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
     if args.ceilings:
-        print(json.dumps({"ceilings": run_ceilings(device, args.cooperative)}), flush=True)
+        print(json.dumps({"ceilings": run_ceilings(device)}), flush=True)
         return 0
     max_tokens = max(SWEEP + (args.tokens, args.decode_tokens))
 
@@ -460,6 +449,24 @@ def main() -> int:
                 "tokens": t, "us": round(s * 1e6, 2), "tokens_per_s": round(t / s, 1),
                 "hbm_frac": round(hbm, 4), "mfma_frac": round(mfma, 4),
             })
+    agent.check_health()
+
+    # ---------------------------------------------------------------- graph dispatch
+    # The same replays launched as the template's instantiated hipGraph (the reference's
+    # design: one captured graph per layer signature) against the default direct launches.
+    graph_dispatch = None
+    if not args.no_sweep:
+        points = []
+        for t in GRAPH_DISPATCH_TOKENS:
+            direct_s = time_replays(t, args.sweep_steps, 5)
+            lane.set_graph_dispatch(True)
+            graph_s = time_replays(t, args.sweep_steps, 5)
+            lane.set_graph_dispatch(False)
+            points.append({"tokens": t, "direct_us": round(direct_s * 1e6, 2), "graph_us": round(graph_s * 1e6, 2),
+                           "graph_extra_us": round((graph_s - direct_s) * 1e6, 2)})
+        graph_dispatch = {"execution": "hipGraphLaunch of the template's instantiated graph per replay "
+                                       "(changed kernel nodes rebound) against direct kernel launches",
+                          "points": points}
     agent.check_health()
 
     # ---------------------------------------------------------------- TP partial fold
@@ -837,6 +844,7 @@ def main() -> int:
         "decode": decode,
         "sweep": sweep,
         "tp_reduce": tp_reduce,
+        "graph_dispatch": graph_dispatch,
         "shim": shim,
         "moe": moe,
         "config2_stack": stack,

@@ -91,7 +91,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "xp_dense_gate_up_variant": (_SIZE, [_I64, _I64, _I64, ctypes.c_char_p, _SIZE]),
     "xp_agent_create": (_INT, [_INT, ctypes.POINTER(_P)]),
     "xp_agent_destroy": (_INT, [_P]),
-    "xp_layer_register": (_INT, [_P, _INT, _INT, _I64, _I64, _P, _P, _P, _F32]),
+    "xp_layer_register": (_INT, [_P, _INT, _INT, _I64, _I64, _INT, _P, _P, _P, _F32]),
     "xp_lane_create": (_INT, [_P, _P, _SIZE, ctypes.POINTER(_P)]),
     "xp_lane_destroy": (_INT, [_P]),
     "xp_lane_stream": (_INT, [_P, ctypes.POINTER(_P)]),
@@ -99,8 +99,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "xp_lane_clear_fault": (_INT, [_P]),
     "xp_lane_synchronize": (_INT, [_P]),
     "xp_lane_set_graph_dispatch": (_INT, [_P, _INT]),
-    "xp_template_capture": (_INT, [_P, _I64, _I64, _I64]),
-    "xp_template_capacities": (_INT, [_P, _I64, _I64, ctypes.POINTER(_I64), _INT, ctypes.POINTER(_INT)]),
+    "xp_template_capture": (_INT, [_P, _I64, _I64, _INT, _I64]),
+    "xp_template_capacities": (_INT, [_P, _I64, _I64, _INT, ctypes.POINTER(_I64), _INT, ctypes.POINTER(_INT)]),
     "xp_replay": (_INT, [_P, _INT, _INT, _I64, _P, _P, _I64, _P, _P]),
     "xp_lane_fault_word": (_INT, [_P, ctypes.POINTER(_P)]),
     "xp_transport_create": (_INT, [_INT, _INT, ctypes.POINTER(_I64), ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(_P)]),
@@ -108,8 +108,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "xp_transport_open": (_INT, [_P, _P]),
     "xp_transport_submit": (_INT, [_P, _INT, _I64, _I64, _INT, _INT, _INT, _P, _I64, _INT, _P]),
     "xp_transport_evaluate": (_INT, [_P, _INT, _P, _P]),
-    "xp_transport_complete": (_INT, [_P, _INT, _P, _I64, _I64, _P]),
-    "xp_transport_settle": (_INT, [_P, _INT, _P, _P, _I64, _P]),
+    "xp_transport_complete": (_INT, [_P, _INT, _P, _I64, _INT, _I64, _P]),
+    "xp_transport_settle": (_INT, [_P, _INT, _P, _P, _I64, _INT, _P]),
     "xp_transport_drain": (_INT, [_P, _P]),
     "xp_transport_publish_failure": (_INT, [_P, _INT, _INT, _P]),
     "xp_transport_snapshot": (_INT, [_P, _INT, _P]),
@@ -188,6 +188,18 @@ def call(name: str, *args: object) -> int:
     status = getattr(library(), name)(*args)
     check(status, name)
     return status
+
+
+def payload_dtype_code(dtype: object) -> int:
+    """XP_DTYPE_BF16 / XP_DTYPE_F16 of a Dense payload dtype (torch.bfloat16 / torch.float16)."""
+
+    import torch
+
+    if dtype is torch.bfloat16:
+        return XP_DTYPE_BF16
+    if dtype is torch.float16:
+        return XP_DTYPE_F16
+    raise ValueError(f"Dense payloads are bf16 or fp16, not {dtype}")
 
 
 def gemm_variant(capacity: int, n: int, k: int, gated: bool) -> str:

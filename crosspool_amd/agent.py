@@ -37,8 +37,8 @@ logger = logging.getLogger(__name__)
 class GraphTemplate:
     """One captured graph identity: the Execution Signature (execution.py:73-149).
 
-    Dense templates are keyed by (hidden, intermediate, capacity); MoE templates by their
-    whole signature.
+    Dense templates are keyed by (payload dtype, hidden, intermediate, capacity); MoE
+    templates by their whole signature.
     """
 
     signature: DenseFfnExecutionSignature | MoeFfnExecutionSignature
@@ -48,11 +48,11 @@ class GraphTemplate:
         return LayerKind.MOE if isinstance(self.signature, MoeFfnExecutionSignature) else LayerKind.DENSE
 
     @property
-    def key(self) -> tuple[int, int, int] | MoeFfnExecutionSignature:
+    def key(self) -> tuple[torch.dtype, int, int, int] | MoeFfnExecutionSignature:
         s = self.signature
         if isinstance(s, MoeFfnExecutionSignature):
             return s
-        return s.hidden_size, s.local_intermediate_size, s.payload_row_capacity
+        return s.payload_dtype, s.hidden_size, s.local_intermediate_size, s.payload_row_capacity
 
     @property
     def workspace_bytes(self) -> int:
@@ -80,6 +80,12 @@ class LayerBinding:
     def kind(self) -> LayerKind:
         return LayerKind.DENSE if self.moe is None else LayerKind.MOE
 
+    @property
+    def payload_dtype(self) -> torch.dtype:
+        """The dtype of the layer's mailboxes: its weights' (Dense: bf16 or fp16; MoE: bf16)."""
+
+        return self.weights.payload_dtype if self.moe is None else torch.bfloat16
+
 
 class FfnHealthError(RuntimeError):
     """A Lane's sticky device fault word is set (canonical asynchronous failure)."""
@@ -103,7 +109,7 @@ class ExecutorLane:
         )
         self.handle = handle
         # Replays launch the template's kernels directly unless graph dispatch is asked for
-        # (each hipGraphLaunch adds 6-9 us of GPU time per replay on ROCm; same kernels either way).
+        # (each hipGraphLaunch adds GPU time per replay on ROCm, measured by bench.py; same kernels).
         self.graph_dispatch = bool(graph_dispatch)
         _native.call("xp_lane_set_graph_dispatch", self.handle, int(self.graph_dispatch))
         stream = ctypes.c_void_p()
@@ -116,6 +122,14 @@ class ExecutorLane:
         self.templates: dict[object, GraphTemplate] = {}
         self._in_flight: deque[tuple[torch.cuda.Event | None, tuple[torch.Tensor, ...], torch.cuda.Stream]] = deque()
 
+    def set_graph_dispatch(self, enabled: bool) -> None:
+        """Launch later replays as the template's instantiated hipGraph (True) or as its
+        kernels directly (False); both run the same kernels with the same arguments."""
+
+        self._require_open()
+        _native.call("xp_lane_set_graph_dispatch", self.handle, int(bool(enabled)))
+        self.graph_dispatch = bool(enabled)
+
     def capture(self, template: GraphTemplate) -> None:
         """Instantiate the template's hipGraph on this Lane (idempotent)."""
 
@@ -126,14 +140,15 @@ class ExecutorLane:
                          s.payload_row_capacity)
         else:
             _native.call("xp_template_capture", self.handle, s.hidden_size, s.local_intermediate_size,
-                         s.payload_row_capacity)
+                         _native.payload_dtype_code(s.payload_dtype), s.payload_row_capacity)
         self.templates[template.key] = template
 
-    def capacities(self, hidden: int, intermediate: int) -> tuple[int, ...]:
+    def capacities(self, hidden: int, intermediate: int, payload_dtype: torch.dtype = torch.bfloat16) -> tuple[int, ...]:
         self._require_open()
         count = ctypes.c_int()
         buffer = (ctypes.c_int64 * 64)()
-        _native.call("xp_template_capacities", self.handle, hidden, intermediate, buffer, 64, ctypes.byref(count))
+        _native.call("xp_template_capacities", self.handle, hidden, intermediate,
+                     _native.payload_dtype_code(payload_dtype), buffer, 64, ctypes.byref(count))
         return tuple(buffer[index] for index in range(min(count.value, 64)))
 
     def replay(
@@ -164,14 +179,15 @@ class ExecutorLane:
 
         self._require_open()
         out_pool = pool if out_pool is None else out_pool
+        binding = self.agent.layers.get((instance_index, layer_ordinal))
+        payload = binding.payload_dtype if binding is not None else torch.bfloat16
         for name, tensor in (("pool", pool), ("out_pool", out_pool)):
-            if tensor.device != self.agent.device or tensor.dtype is not torch.bfloat16 or tensor.ndim != 2:
-                raise ValueError(f"{name} must be a bf16 matrix on the agent's device")
+            if tensor.device != self.agent.device or tensor.dtype is not payload or tensor.ndim != 2:
+                raise ValueError(f"{name} must be a {payload} matrix on the agent's device (the layer's payload dtype)")
             if not tensor.is_contiguous():
                 raise ValueError(f"{name} must be contiguous")
         if out_pool.shape != pool.shape:
             raise ValueError("input and output mailboxes must have one shape")
-        binding = self.agent.layers.get((instance_index, layer_ordinal))
         if binding is not None and pool.shape[1] != binding.weights.hidden_size:
             # The kernels index mailbox rows by the layer's hidden size.
             raise ValueError(f"mailbox rows must hold the layer's hidden size {binding.weights.hidden_size}")
@@ -302,18 +318,20 @@ class FfnAgent:
             raise ValueError("local FFN resources must reside on the agent's device")
         if not weights.template_ready:
             raise ValueError(
-                "captured Dense templates take gated bf16 INTERLEAVED weights without biases and 16-byte rows; "
-                "run other layers through crosspool_amd.operators"
+                "captured Dense templates take gated bf16 or fp16 INTERLEAVED weights without biases and 16-byte "
+                "rows; run other layers through crosspool_amd.operators"
             )
+        payload = weights.payload_dtype
         if norm_weight is not None:
             validate_weight_tensor(norm_weight, name="RMSNorm weight")
-            if norm_weight.dtype is not torch.bfloat16 or tuple(norm_weight.shape) != (weights.hidden_size,):
-                raise ValueError("RMSNorm weight must be a bf16 [H] vector")
+            if norm_weight.dtype is not payload or tuple(norm_weight.shape) != (weights.hidden_size,):
+                raise ValueError(f"RMSNorm weight must be a {payload} [H] vector (the layer's payload dtype)")
             if norm_weight.device != self.device:
                 raise ValueError("RMSNorm weight must reside on the agent's device")
         _native.call(
             "xp_layer_register", self.handle, instance_index, layer_ordinal, weights.hidden_size,
-            weights.local_intermediate_size, ctypes.c_void_p(weights.i_proj.values.data_ptr()),
+            weights.local_intermediate_size, _native.payload_dtype_code(payload),
+            ctypes.c_void_p(weights.i_proj.values.data_ptr()),
             ctypes.c_void_p(weights.o_proj.values.data_ptr()),
             None if norm_weight is None else ctypes.c_void_p(norm_weight.data_ptr()), float(eps),
         )
@@ -414,11 +432,12 @@ class FfnAgent:
         started = monotonic()
         capacities = derive_payload_row_capacities(maximum_row_capacity)
         dense = self._dense_layers()
-        shapes = sorted({(b.weights.hidden_size, b.weights.local_intermediate_size) for b in dense})
-        for hidden, intermediate in shapes:
+        shapes = sorted({(str(b.payload_dtype), b.payload_dtype, b.weights.hidden_size,
+                          b.weights.local_intermediate_size) for b in dense})
+        for _, payload, hidden, intermediate in shapes:
             for capacity in capacities:
                 signature = DenseFfnExecutionSignature(
-                    payload_dtype=torch.bfloat16,
+                    payload_dtype=payload,
                     payload_row_capacity=capacity,
                     hidden_size=hidden,
                     local_intermediate_size=intermediate,

@@ -27,8 +27,9 @@ JSON integer``, ``must be greater than or equal to``, the offending field's name
 
 The post-attention norm weight (``model.layers.{i}.post_attention_layernorm.weight``)
 is read as well, because this build fuses the norm into the gather; the reference
-leaves the norm to SGLang.  Payloads are bf16: bf16 sources are copied bit for bit,
-fp16 / fp32 sources are rounded to nearest even.
+leaves the norm to SGLang.  The payload dtype is the checkpoint's source dtype, bf16 or
+fp16, as the reference's loader keeps it (``loader.py:485-508``): tensors of that dtype
+are copied bit for bit, wider floats are rounded to it (nearest even).
 """
 
 from __future__ import annotations
@@ -209,6 +210,7 @@ class DenseModelSpec:
     layer_count: int
     rms_norm_eps: float
     key_view: dict[str, Path]
+    payload_dtype: torch.dtype = torch.bfloat16  # the source dtype (bf16 or fp16)
 
 
 def load_model_spec(model_path: Path) -> DenseModelSpec:
@@ -226,7 +228,7 @@ def load_model_spec(model_path: Path) -> DenseModelSpec:
                              f"{', '.join(sorted(DENSE_FAMILIES))})")
         fields.text("model_type", DENSE_FAMILIES[architecture])
         fields.text("hidden_act", "silu")
-        fields.source_dtype()
+        source_dtype = fields.source_dtype()
         spec = DenseModelSpec(
             architecture=architecture,
             hidden_size=fields.integer("hidden_size"),
@@ -234,6 +236,7 @@ def load_model_spec(model_path: Path) -> DenseModelSpec:
             layer_count=fields.integer("num_hidden_layers"),
             rms_norm_eps=fields.positive_number("rms_norm_eps", 1e-6),
             key_view=read_checkpoint_key_view(model_path),
+            payload_dtype=torch.float16 if source_dtype == "float16" else torch.bfloat16,
         )
         validate_ffn_coverage(spec.key_view, spec.layer_count)
         return spec
@@ -295,8 +298,10 @@ def layer_reads(spec: DenseModelSpec, geometry: ShardGeometry, layer_ids: Iterab
     return values
 
 
-def _checked_slice(handle, key: str, full_shape: tuple[int, ...], region: tuple[slice, ...]) -> torch.Tensor:
-    """``region`` of tensor ``key`` as bf16, after checking the tensor's full shape and type."""
+def _checked_slice(handle, key: str, full_shape: tuple[int, ...], region: tuple[slice, ...],
+                   dtype: torch.dtype) -> torch.Tensor:
+    """``region`` of tensor ``key`` in the payload ``dtype``, after checking the tensor's full
+    shape and type."""
 
     lazy = handle.get_slice(key)
     found = tuple(lazy.get_shape())
@@ -305,11 +310,11 @@ def _checked_slice(handle, key: str, full_shape: tuple[int, ...], region: tuple[
     data = lazy[region]
     if not data.is_floating_point():
         raise ValueError(f"tensor {key!r} holds {data.dtype}, not a floating-point type")
-    return data.to(torch.bfloat16)  # a copy for bf16, nearest-even rounding for wider floats
+    return data.to(dtype)  # a copy in the payload dtype, nearest-even rounding for wider floats
 
 
 def stage_read(value: StagedValue, geometry: ShardGeometry, key_view: dict[str, Path], out: torch.Tensor) -> None:
-    """Fill the host tensor ``out`` (bf16, ``value.shape``) from the checkpoint; no GPU work.
+    """Fill the host tensor ``out`` (payload dtype, ``value.shape``) from the checkpoint; no GPU work.
 
     ``i_proj``: rows 2j and 2j+1 are gate and up row ``start + j``; ``o_proj``: columns
     ``[start, start + L)`` of down; ``norm``: the whole vector.
@@ -329,11 +334,12 @@ def stage_read(value: StagedValue, geometry: ShardGeometry, key_view: dict[str, 
         # out viewed as [L, 2, H]: plane 0 takes the gate rows, plane 1 the up rows.
         pairs = out.view(geometry.local_width, 2, hidden)
         for plane, (key, path) in enumerate(zip(value.keys, files)):
-            pairs[:, plane].copy_(_checked_slice(handles[path], key, (intermediate, hidden), (rows,)))
+            pairs[:, plane].copy_(_checked_slice(handles[path], key, (intermediate, hidden), (rows,), out.dtype))
     elif value.kind == "o_proj":
-        out.copy_(_checked_slice(handles[files[0]], value.keys[0], (hidden, intermediate), (slice(None), rows)))
+        out.copy_(_checked_slice(handles[files[0]], value.keys[0], (hidden, intermediate), (slice(None), rows),
+                                 out.dtype))
     else:
-        out.copy_(_checked_slice(handles[files[0]], value.keys[0], (hidden,), (slice(None),)))
+        out.copy_(_checked_slice(handles[files[0]], value.keys[0], (hidden,), (slice(None),), out.dtype))
 
 
 # ---------------------------------------------------------------- materialisation
@@ -382,8 +388,9 @@ def load_dense_layers(
 
     values = layer_reads(spec, geometry, layer_ids, norm=norm)
     try:
-        targets = [torch.empty(value.shape, dtype=torch.bfloat16, device=device) for value in values]
-        _PinnedRing(min(parallelism, len(values)), max(value.nbytes for value in values), device).run(
+        targets = [torch.empty(value.shape, dtype=spec.payload_dtype, device=device) for value in values]
+        _PinnedRing(min(parallelism, len(values)), max(value.nbytes for value in values), device,
+                    spec.payload_dtype).run(
             values, targets, geometry, spec.key_view
         )
     except Exception as error:
@@ -405,14 +412,15 @@ class _PinnedRing:
     them overlap.  Worker threads never touch the GPU.
     """
 
-    def __init__(self, count: int, nbytes: int, device: torch.device) -> None:
+    def __init__(self, count: int, nbytes: int, device: torch.device, dtype: torch.dtype = torch.bfloat16) -> None:
         self.buffers = [torch.empty(nbytes, dtype=torch.uint8, pin_memory=True) for _ in range(count)]
         self.copied: list[torch.cuda.Event | None] = [None] * count
         self.device = device
+        self.dtype = dtype
 
     def _view(self, index: int, value: StagedValue) -> torch.Tensor:
         buffer = self.buffers[index % len(self.buffers)]
-        return buffer[: value.nbytes].view(torch.bfloat16).view(value.shape)
+        return buffer[: value.nbytes].view(self.dtype).view(value.shape)
 
     def run(self, values: list[StagedValue], targets: list[torch.Tensor], geometry: ShardGeometry,
             key_view: dict[str, Path]) -> None:

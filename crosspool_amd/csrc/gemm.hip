@@ -64,7 +64,7 @@ constexpr uint32_t kOutOfRange = 0x7ffffff0u;
 // Only rows [0, staged_rows) are written (the LDS holds no more; staged_rows <= TP covers
 // the live rows).  All WAVES waves of the workgroup take part; the caller synchronises
 // before reading.
-template <int TP, int WAVES>
+template <int TP, int WAVES, class P = Bf16Payload>
 __device__ __forceinline__ void stage_gathered_rows(const GemmArgs &a, uint16_t *xs, int64_t rs, int kbase,
                                                     int kvalid, int vectors_per_row, int wave, int lane,
                                                     int staged_rows) {
@@ -116,7 +116,7 @@ __device__ __forceinline__ void stage_gathered_rows(const GemmArgs &a, uint16_t 
       for (int r = 0; r < ROWS_PER_WAVE; ++r) {
 #pragma unroll
         for (int b = 0; b < BATCH; ++b) {
-          add_squares(values[r][b], squares[r]);  // chunk order lane, lane + 64, ...
+          add_squares<P>(values[r][b], squares[r]);  // chunk order lane, lane + 64, ...
         }
       }
     }
@@ -136,7 +136,7 @@ __device__ __forceinline__ void stage_gathered_rows(const GemmArgs &a, uint16_t 
       }
     }
   }
-  const u32x4 poison = {kPoisonBf16x2, kPoisonBf16x2, kPoisonBf16x2, kPoisonBf16x2};
+  const u32x4 poison = {P::kPoison2, P::kPoison2, P::kPoison2, P::kPoison2};
   if (one_batch) {
     // Each wave stores its own rows' part of the slice (zeros past the live rows).
 #pragma unroll
@@ -154,7 +154,7 @@ __device__ __forceinline__ void stage_gathered_rows(const GemmArgs &a, uint16_t 
         }
         u32x4 value = zero;
         if (sources[r] >= 0) {
-          value = a.norm != nullptr ? normalize_chunk(values[r][b], scales[r], weights[b]) : values[r][b];
+          value = a.norm != nullptr ? normalize_chunk<P>(values[r][b], scales[r], weights[b]) : values[r][b];
         } else if (sources[r] == -2) {
           value = poison;
         }
@@ -196,7 +196,7 @@ __device__ __forceinline__ void stage_gathered_rows(const GemmArgs &a, uint16_t 
         u32x4 value = zero;
         if (c * 8 < kvalid) {
           if (source >= 0) {
-            value = a.norm != nullptr ? normalize_chunk(x_chunk[u], row_scale[t], w_chunk[u]) : x_chunk[u];
+            value = a.norm != nullptr ? normalize_chunk<P>(x_chunk[u], row_scale[t], w_chunk[u]) : x_chunk[u];
           } else if (source == -2) {
             value = poison;
           }
@@ -257,7 +257,7 @@ constexpr int kSplitMaxGroups = 2;
 // are in flight; the token pieces are then read from LDS instead of L2.  Dynamic LDS:
 // min(capacity, 8) x (K + 16) bf16 (the 32-byte row padding puts the 16 pieces of one read
 // in distinct bank slots).
-template <int DEPTH, int TG, bool GATED, bool GATHER = false>
+template <int DEPTH, int TG, bool GATED, bool GATHER = false, class P = Bf16Payload>
 __global__ __launch_bounds__(64 * kSplitWaves) void split_gemm_kernel(GemmArgs a) {
   static_assert(!GATHER || TG == 1, "the fused gather stages one token group");
   extern __shared__ __attribute__((aligned(16))) uint16_t staged[];
@@ -345,8 +345,8 @@ __global__ __launch_bounds__(64 * kSplitWaves) void split_gemm_kernel(GemmArgs a
         } else {
           xk = valid ? x[line][g] : zero;
         }
-        acc[g][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(w0), as_bf16x8(xk), acc[g][0], 0, 0, 0);
-        acc[g][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(w1), as_bf16x8(xk), acc[g][1], 0, 0, 0);
+        acc[g][0] = P::mfma16(w0, xk, acc[g][0]);
+        acc[g][1] = P::mfma16(w1, xk, acc[g][1]);
       }
     }
   };
@@ -361,7 +361,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) void split_gemm_kernel(GemmArgs a
   }
   if constexpr (GATHER) {
     const int vectors = static_cast<int>(a.k / 8);
-    stage_gathered_rows<kSplitGroupTokens, kSplitWaves>(a, staged, rs, 0, static_cast<int>(a.k), vectors, wave,
+    stage_gathered_rows<kSplitGroupTokens, kSplitWaves, P>(a, staged, rs, 0, static_cast<int>(a.k), vectors, wave,
                                                         lane, staged_rows);
     __syncthreads();
     if (a.gathered_out != nullptr && blockIdx.x == 0) {
@@ -453,11 +453,11 @@ __global__ __launch_bounds__(64 * kSplitWaves) void split_gemm_kernel(GemmArgs a
         continue;
       }
       if constexpr (GATED) {
-        const float h0 = gated_silu(sum[g][h][0], sum[g][h][1], a.act);
-        const float h1 = gated_silu(sum[g][h][2], sum[g][h][3], a.act);
-        *reinterpret_cast<uint32_t *>(out + n / 2) = pack_bf16x2(h0, h1);
+        const float h0 = gated_silu_payload<P>(sum[g][h][0], sum[g][h][1], a.act);
+        const float h1 = gated_silu_payload<P>(sum[g][h][2], sum[g][h][3], a.act);
+        *reinterpret_cast<uint32_t *>(out + n / 2) = P::pack2(h0, h1);
       } else {
-        u32x2 packed = {pack_bf16x2(sum[g][h][0], sum[g][h][1]), pack_bf16x2(sum[g][h][2], sum[g][h][3])};
+        u32x2 packed = {P::pack2(sum[g][h][0], sum[g][h][1]), P::pack2(sum[g][h][2], sum[g][h][3])};
         *reinterpret_cast<u32x2 *>(out + n) = packed;
       }
     }
@@ -485,7 +485,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) void split_gemm_kernel(GemmArgs a
 // by the norm weights (while staging) and the K-range partial sums (after each unit).
 constexpr int kSplitGatheredScratchBytes = (kSplitWaves - 1) * 2 * 64 * 16;
 
-template <int DEPTH, bool GATED>
+template <int DEPTH, bool GATED, class P = Bf16Payload>
 __global__ __launch_bounds__(64 * kSplitWaves) __attribute__((amdgpu_waves_per_eu(4))) void split_gathered_kernel(
     GemmArgs a) {
   static_assert(kSplitGroupTokens == kSplitWaves, "wave w stages token row w");
@@ -599,7 +599,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) __attribute__((amdgpu_waves_per_e
             }
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
-              add_squares(lane + (2 * pair + u) * kWave < row_chunks ? v[u] : zero, squares);
+              add_squares<P>(lane + (2 * pair + u) * kWave < row_chunks ? v[u] : zero, squares);
             }
           }
           const float scale = rms_inverse(squares, a.k, a.eps);
@@ -617,13 +617,13 @@ __global__ __launch_bounds__(64 * kSplitWaves) __attribute__((amdgpu_waves_per_e
             for (int u = 0; u < 2; ++u) {
               const int c = lane + (2 * pair + u) * kWave;
               if (c < row_chunks) {
-                store16(token + c * 8, normalize_chunk(v[u], scale, w[u]));
+                store16(token + c * 8, normalize_chunk<P>(v[u], scale, w[u]));
               }
             }
           }
         }
       } else {
-        const u32x4 poison = {kPoisonBf16x2, kPoisonBf16x2, kPoisonBf16x2, kPoisonBf16x2};
+        const u32x4 poison = {P::kPoison2, P::kPoison2, P::kPoison2, P::kPoison2};
         const u32x4 fill = source == -2 ? poison : zero;
         for (int c = lane; c < row_chunks; c += kWave) {
           store16(token + c * 8, fill);
@@ -657,8 +657,8 @@ __global__ __launch_bounds__(64 * kSplitWaves) __attribute__((amdgpu_waves_per_e
         const u32x4 w0 = valid ? w[2 * line] : zero;
         const u32x4 w1 = valid ? w[2 * line + 1] : zero;
         const u32x4 xk = valid && token_live ? load16(token_row + column + line * 64) : zero;
-        acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(w0), as_bf16x8(xk), acc[0], 0, 0, 0);
-        acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(w1), as_bf16x8(xk), acc[1], 0, 0, 0);
+        acc[0] = P::mfma16(w0, xk, acc[0]);
+        acc[1] = P::mfma16(w1, xk, acc[1]);
       }
     };
     if (active) {
@@ -717,11 +717,11 @@ __global__ __launch_bounds__(64 * kSplitWaves) __attribute__((amdgpu_waves_per_e
             continue;
           }
           if constexpr (GATED) {
-            const float h0 = gated_silu(sum[h][0], sum[h][1], a.act);
-            const float h1 = gated_silu(sum[h][2], sum[h][3], a.act);
-            *reinterpret_cast<uint32_t *>(out + n / 2) = pack_bf16x2(h0, h1);
+            const float h0 = gated_silu_payload<P>(sum[h][0], sum[h][1], a.act);
+            const float h1 = gated_silu_payload<P>(sum[h][2], sum[h][3], a.act);
+            *reinterpret_cast<uint32_t *>(out + n / 2) = P::pack2(h0, h1);
           } else {
-            u32x2 packed = {pack_bf16x2(sum[h][0], sum[h][1]), pack_bf16x2(sum[h][2], sum[h][3])};
+            u32x2 packed = {P::pack2(sum[h][0], sum[h][1]), P::pack2(sum[h][2], sum[h][3])};
             *reinterpret_cast<u32x2 *>(out + n) = packed;
           }
         }
@@ -900,7 +900,7 @@ constexpr int kStreamDepth = 4;
 constexpr int kStreamTokens = 16;
 constexpr int kStreamRowPad = 16;  // elements of LDS row padding
 
-template <bool GATED, bool GATHER>
+template <bool GATED, bool GATHER, class P = Bf16Payload>
 __global__ __launch_bounds__(64 * kStreamWaves) void stream_gemm_kernel(GemmArgs a) {
   constexpr int TP = kStreamTokens;
   constexpr int TG = TP / 8;
@@ -965,7 +965,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_gemm_kernel(GemmArgs
   const int kbase = static_cast<int>(k0);
   const int kvalid = static_cast<int>(klen);
   if constexpr (GATHER) {
-    stage_gathered_rows<TP, kStreamWaves>(a, xs, rs, kbase, kvalid, vectors_per_row, wave, lane, TP);
+    stage_gathered_rows<TP, kStreamWaves, P>(a, xs, rs, kbase, kvalid, vectors_per_row, wave, lane, TP);
   } else {
     const __amdgpu_buffer_rsrc_t x_rsrc = make_rsrc(a.x, static_cast<uint32_t>(a.rows * a.ldx * 2));
     for (int index = threadIdx.x; index < TP * vectors_per_row; index += 64 * kStreamWaves) {
@@ -998,8 +998,8 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_gemm_kernel(GemmArgs
 #pragma unroll
       for (int g = 0; g < TG; ++g) {
         const u32x4 x = load16(xs + (8 * g + row) * rs + column + line * 64 + piece * 8);
-        acc[g][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(w0), as_bf16x8(x), acc[g][0], 0, 0, 0);
-        acc[g][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(w1), as_bf16x8(x), acc[g][1], 0, 0, 0);
+        acc[g][0] = P::mfma16(w0, x, acc[g][0]);
+        acc[g][1] = P::mfma16(w1, x, acc[g][1]);
       }
     }
   };
@@ -1056,11 +1056,11 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_gemm_kernel(GemmArgs
         // Partial tile of this slice; stream_reduce_kernel sums the slices in order.
         *reinterpret_cast<f32x4 *>(a.partials + (slice * a.rows + token) * a.n + n) = sum[g][h];
       } else if constexpr (GATED) {
-        const float h0 = gated_silu(sum[g][h][0], sum[g][h][1], a.act);
-        const float h1 = gated_silu(sum[g][h][2], sum[g][h][3], a.act);
-        *reinterpret_cast<uint32_t *>(out + n / 2) = pack_bf16x2(h0, h1);
+        const float h0 = gated_silu_payload<P>(sum[g][h][0], sum[g][h][1], a.act);
+        const float h1 = gated_silu_payload<P>(sum[g][h][2], sum[g][h][3], a.act);
+        *reinterpret_cast<uint32_t *>(out + n / 2) = P::pack2(h0, h1);
       } else {
-        u32x2 packed = {pack_bf16x2(sum[g][h][0], sum[g][h][1]), pack_bf16x2(sum[g][h][2], sum[g][h][3])};
+        u32x2 packed = {P::pack2(sum[g][h][0], sum[g][h][1]), P::pack2(sum[g][h][2], sum[g][h][3])};
         *reinterpret_cast<u32x2 *>(out + n) = packed;
       }
     }
@@ -1070,7 +1070,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_gemm_kernel(GemmArgs
 // Sum of the split-K partials [slices, rows, n] in slice order (so results do not depend
 // on which slice finished first), then the projection's epilogue.  One thread per four
 // consecutive outputs of one row: 16-byte partial loads, coalesced along n.
-template <bool GATED>
+template <bool GATED, class P = Bf16Payload>
 __global__ __launch_bounds__(256) void stream_reduce_kernel(GemmArgs a) {
   const int64_t quads = a.n / 4;
   const int64_t index = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -1101,11 +1101,11 @@ __global__ __launch_bounds__(256) void stream_reduce_kernel(GemmArgs a) {
     return;
   }
   if constexpr (GATED) {
-    const float h0 = gated_silu(sum[0], sum[1], a.act);
-    const float h1 = gated_silu(sum[2], sum[3], a.act);
-    *reinterpret_cast<uint32_t *>(row + n / 2) = pack_bf16x2(h0, h1);
+    const float h0 = gated_silu_payload<P>(sum[0], sum[1], a.act);
+    const float h1 = gated_silu_payload<P>(sum[2], sum[3], a.act);
+    *reinterpret_cast<uint32_t *>(row + n / 2) = P::pack2(h0, h1);
   } else {
-    u32x2 packed = {pack_bf16x2(sum[0], sum[1]), pack_bf16x2(sum[2], sum[3])};
+    u32x2 packed = {P::pack2(sum[0], sum[1]), P::pack2(sum[2], sum[3])};
     *reinterpret_cast<u32x2 *>(row + n) = packed;
   }
 }
@@ -1154,7 +1154,7 @@ struct ResidentLds {
   f32x4 block[2][kResidentWaves][TG][2][2][8];
 };
 
-template <int TG, int CPW, bool GATED, bool GATHER>
+template <int TG, int CPW, bool GATED, bool GATHER, class P = Bf16Payload>
 __global__ __launch_bounds__(64 * kResidentWaves) __attribute__((amdgpu_waves_per_eu(2))) void resident_gemm_kernel(
     GemmArgs a) {
   constexpr int D = kResidentDepth;
@@ -1279,7 +1279,7 @@ __global__ __launch_bounds__(64 * kResidentWaves) __attribute__((amdgpu_waves_pe
         for (int c = 0; c < CPW; ++c) {
 #pragma unroll
           for (int l = 0; l < 2; ++l) {
-            add_squares(x[c][l][g], squares[g]);  // column order within the lane
+            add_squares<P>(x[c][l][g], squares[g]);  // column order within the lane
           }
         }
         // The 8 lanes of token row (lane & 7) differ in lane bits 3 .. 5.
@@ -1299,7 +1299,7 @@ __global__ __launch_bounds__(64 * kResidentWaves) __attribute__((amdgpu_waves_pe
         scale[g] = 1.0f / sqrtf(total / static_cast<float>(a.k) + a.eps);
       }
     }
-    const u32x4 poison = {kPoisonBf16x2, kPoisonBf16x2, kPoisonBf16x2, kPoisonBf16x2};
+    const u32x4 poison = {P::kPoison2, P::kPoison2, P::kPoison2, P::kPoison2};
 #pragma unroll
     for (int c = 0; c < CPW; ++c) {
 #pragma unroll
@@ -1311,7 +1311,7 @@ __global__ __launch_bounds__(64 * kResidentWaves) __attribute__((amdgpu_waves_pe
             x[c][l][g] = valid ? poison : zero;
           } else if (a.norm != nullptr) {
             const u32x4 weight = valid ? load16(norm_lds + k0 + piece * 8 + chunk_column(c) + l * 64) : zero;
-            x[c][l][g] = normalize_chunk(x[c][l][g], scale[g], weight);
+            x[c][l][g] = normalize_chunk<P>(x[c][l][g], scale[g], weight);
           }
         }
       }
@@ -1355,9 +1355,8 @@ __global__ __launch_bounds__(64 * kResidentWaves) __attribute__((amdgpu_waves_pe
     for (int l = 0; l < 2; ++l) {
 #pragma unroll
       for (int g = 0; g < TG; ++g) {
-        acc[g][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(w[2 * l]), as_bf16x8(x[c][l][g]), acc[g][0], 0, 0, 0);
-        acc[g][1] =
-            __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(w[2 * l + 1]), as_bf16x8(x[c][l][g]), acc[g][1], 0, 0, 0);
+        acc[g][0] = P::mfma16(w[2 * l], x[c][l][g], acc[g][0]);
+        acc[g][1] = P::mfma16(w[2 * l + 1], x[c][l][g], acc[g][1]);
       }
     }
   };
@@ -1415,11 +1414,11 @@ __global__ __launch_bounds__(64 * kResidentWaves) __attribute__((amdgpu_waves_pe
       *reinterpret_cast<f32x4 *>(a.partials + (part * a.rows + item_token) * a.n + n) = sum;
     } else if (item_out != nullptr) {
       if constexpr (GATED) {
-        const float h0 = gated_silu(sum[0], sum[1], a.act);
-        const float h1 = gated_silu(sum[2], sum[3], a.act);
-        *reinterpret_cast<uint32_t *>(item_out + n / 2) = pack_bf16x2(h0, h1);
+        const float h0 = gated_silu_payload<P>(sum[0], sum[1], a.act);
+        const float h1 = gated_silu_payload<P>(sum[2], sum[3], a.act);
+        *reinterpret_cast<uint32_t *>(item_out + n / 2) = P::pack2(h0, h1);
       } else {
-        u32x2 packed = {pack_bf16x2(sum[0], sum[1]), pack_bf16x2(sum[2], sum[3])};
+        u32x2 packed = {P::pack2(sum[0], sum[1]), P::pack2(sum[2], sum[3])};
         *reinterpret_cast<u32x2 *>(item_out + n) = packed;
       }
     }
@@ -1565,7 +1564,7 @@ __device__ __forceinline__ float row_factor(const RowMeta<WTM> &meta, int row) {
   return value;
 }
 
-template <int MT, int NT, int WTM, int WTN, int WAVES, int LDS_ELEMENTS, bool GATED, bool GROUPED>
+template <int MT, int NT, int WTM, int WTN, int WAVES, int LDS_ELEMENTS, bool GATED, bool GROUPED, class P>
 __device__ __forceinline__ void tile_epilogue(const GemmArgs &a, const f32x16 (&acc)[MT][NT], uint16_t *lds,
                                               int64_t m0, int64_t row_end, int64_t w0, int wave, int wm, int wn,
                                               const RowMeta<WTM> &meta) {
@@ -1644,11 +1643,11 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs &a, const f32x16 (&
           const int col = nt * 32 + frag_row;
           float value;
           if constexpr (GATED) {
-            value = gated_silu_fixed<decltype(clip)::value>(acc[mt][nt][r], acc[mt][nt + NT / 2][r], a.act);
+            value = gated_silu_payload<P, decltype(clip)::value>(acc[mt][nt][r], acc[mt][nt + NT / 2][r], a.act);
           } else {
             value = acc[mt][nt][r] * factor;
           }
-          out_tile[slot_of(row, col >> 3) + (col & 7)] = static_cast<uint16_t>(float_to_bf16(value));
+          out_tile[slot_of(row, col >> 3) + (col & 7)] = static_cast<uint16_t>(P::pack2(value, 0.0f) & 0xffffu);
         }
       }
     }
@@ -1692,7 +1691,7 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs &a, const f32x16 (&
 // range each workgroup writes the fp32 partial tile of its range and
 // stream_reduce_kernel, launched next, adds the ranges in order and applies the epilogue.
 template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, bool GATED, bool GROUPED = false,
-          bool STREAM_WEIGHTS = GROUPED>
+          bool STREAM_WEIGHTS = GROUPED, class PAYLOAD = Bf16Payload>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmArgs a) {
   constexpr int BK = 64;
   constexpr int WAVES = WAVES_M * WAVES_N;
@@ -1903,8 +1902,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
   // steps ahead of their MFMAs, so a wave running alone on its SIMD (its partner blocked on
   // the barrier or on issuing loads) does not wait on LDS latency.
   static_assert(KSTEPS == 4, "the slab schedule below is written for four k steps");
-  bf16x8 af[3][MT];
-  bf16x8 bfrag[3][NT];
+  u32x4 af[3][MT];
+  u32x4 bfrag[3][NT];
   // A grouped tile's wave whose rows all lie past the expert's last route reads no
   // fragments and issues no MFMAs (one wave-uniform branch around the unrolled loops).
   auto read_fragments = [&](int stage, int ks, int slot) XP_INLINE {
@@ -1914,14 +1913,12 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int offset = stage * BM * BK * 2 + mt * 32 * BK * 2;
-      af[slot][mt] = as_bf16x8(
-          *reinterpret_cast<const u32x4 *>(lds_bytes + a_base[offset >> 16][ks] + (offset & 0xffff)));
+      af[slot][mt] = *reinterpret_cast<const u32x4 *>(lds_bytes + a_base[offset >> 16][ks] + (offset & 0xffff));
     }
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       const int offset = B_REGION * 2 + stage * BN * BK * 2 + nt * 32 * BK * 2;
-      bfrag[slot][nt] = as_bf16x8(
-          *reinterpret_cast<const u32x4 *>(lds_bytes + b_base[offset >> 16][ks] + (offset & 0xffff)));
+      bfrag[slot][nt] = *reinterpret_cast<const u32x4 *>(lds_bytes + b_base[offset >> 16][ks] + (offset & 0xffff));
     }
   };
   auto mfma_step = [&](int slot) XP_INLINE {
@@ -1932,7 +1929,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
     for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
-        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[slot][mt], bfrag[slot][nt], acc[mt][nt], 0, 0, 0);
+        acc[mt][nt] = PAYLOAD::mfma32(af[slot][mt], bfrag[slot][nt], acc[mt][nt]);
       }
     }
   };
@@ -2060,7 +2057,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
   // Past-the-end refills may still be landing in the stage buffers the epilogue reuses.
   __builtin_amdgcn_s_waitcnt(0);
 
-  tile_epilogue<MT, NT, WTM, WTN, WAVES, STAGES * STAGE, GATED, GROUPED>(a, acc, lds, m0, row_end, w0, wave, wm, wn,
+  tile_epilogue<MT, NT, WTM, WTN, WAVES, STAGES * STAGE, GATED, GROUPED, PAYLOAD>(a, acc, lds, m0, row_end, w0, wave, wm, wn,
                                                                          meta);
 }
 
@@ -2073,26 +2070,42 @@ constexpr int split_depth(int groups) { return groups == 1 ? 4 : 3; }
 // (Four groups, 32 tokens, were measured and dropped: the token pieces read from L2 for each
 // weight line then cost more than the tile kernels, 60-77 us against 41-43 us for Qwen3-8B
 // gate_up at 17-32 rows.)
+// Every Dense kernel is instantiated for both payload dtypes (bf16, fp16); `payload`
+// (GemmArgs::payload) picks one.  The MoE projections are bf16 only.
 template <bool GATED>
-const void *split_kernel(int groups, bool gather) {
+const void *split_kernel(int groups, bool gather, int32_t payload) {
   if (gather) {
-    return reinterpret_cast<const void *>(&split_gemm_kernel<split_depth(1), 1, GATED, true>);
+    return payload == kPayloadF16
+               ? reinterpret_cast<const void *>(&split_gemm_kernel<split_depth(1), 1, GATED, true, F16Payload>)
+               : reinterpret_cast<const void *>(&split_gemm_kernel<split_depth(1), 1, GATED, true, Bf16Payload>);
   }
-  return groups == 1 ? reinterpret_cast<const void *>(&split_gemm_kernel<split_depth(1), 1, GATED>)
-                     : reinterpret_cast<const void *>(&split_gemm_kernel<split_depth(2), 2, GATED>);
+  if (payload == kPayloadF16) {
+    return groups == 1 ? reinterpret_cast<const void *>(&split_gemm_kernel<split_depth(1), 1, GATED, false, F16Payload>)
+                       : reinterpret_cast<const void *>(&split_gemm_kernel<split_depth(2), 2, GATED, false, F16Payload>);
+  }
+  return groups == 1 ? reinterpret_cast<const void *>(&split_gemm_kernel<split_depth(1), 1, GATED, false, Bf16Payload>)
+                     : reinterpret_cast<const void *>(&split_gemm_kernel<split_depth(2), 2, GATED, false, Bf16Payload>);
 }
 
 // The persistent split kernel with the gather fused (one token group).
 template <bool GATED>
-const void *split_gathered_kernel_ptr() {
-  return reinterpret_cast<const void *>(&split_gathered_kernel<split_depth(1), GATED>);
+const void *split_gathered_kernel_ptr(int32_t payload) {
+  return payload == kPayloadF16 ? reinterpret_cast<const void *>(&split_gathered_kernel<split_depth(1), GATED, F16Payload>)
+                                : reinterpret_cast<const void *>(&split_gathered_kernel<split_depth(1), GATED, Bf16Payload>);
 }
 
 int split_groups(int64_t capacity) { return capacity <= kSplitGroupTokens ? 1 : 2; }
 
 template <bool GATED, bool GATHER = false>
-const void *stream_kernel() {
-  return reinterpret_cast<const void *>(&stream_gemm_kernel<GATED, GATHER>);
+const void *stream_kernel(int32_t payload) {
+  return payload == kPayloadF16 ? reinterpret_cast<const void *>(&stream_gemm_kernel<GATED, GATHER, F16Payload>)
+                                : reinterpret_cast<const void *>(&stream_gemm_kernel<GATED, GATHER, Bf16Payload>);
+}
+
+template <bool GATED>
+const void *stream_reduce(int32_t payload) {
+  return payload == kPayloadF16 ? reinterpret_cast<const void *>(&stream_reduce_kernel<GATED, F16Payload>)
+                                : reinterpret_cast<const void *>(&stream_reduce_kernel<GATED, Bf16Payload>);
 }
 
 // The resident kernel for 16 token rows (two groups of 8) and `cpw` chunks per wave (1 to
@@ -2102,20 +2115,26 @@ const void *stream_kernel() {
 constexpr int kResidentMaxChunksPerWave = 4;
 constexpr int kResidentGroups = 2;
 
-template <bool GATED, bool GATHER>
+template <bool GATED, bool GATHER, class P>
 const void *resident_kernel(int cpw) {
   using Kernel = void (*)(GemmArgs);
   static const Kernel table[kResidentMaxChunksPerWave] = {
-      &resident_gemm_kernel<kResidentGroups, 1, GATED, GATHER>, &resident_gemm_kernel<kResidentGroups, 2, GATED, GATHER>,
-      &resident_gemm_kernel<kResidentGroups, 3, GATED, GATHER>, &resident_gemm_kernel<kResidentGroups, 4, GATED, GATHER>};
+      &resident_gemm_kernel<kResidentGroups, 1, GATED, GATHER, P>, &resident_gemm_kernel<kResidentGroups, 2, GATED, GATHER, P>,
+      &resident_gemm_kernel<kResidentGroups, 3, GATED, GATHER, P>, &resident_gemm_kernel<kResidentGroups, 4, GATED, GATHER, P>};
   return reinterpret_cast<const void *>(table[cpw - 1]);
 }
 
+template <class P>
 const void *resident_kernel_for(bool gated, bool gather, int cpw) {
   if (gated) {
-    return gather ? resident_kernel<true, true>(cpw) : resident_kernel<true, false>(cpw);
+    return gather ? resident_kernel<true, true, P>(cpw) : resident_kernel<true, false, P>(cpw);
   }
-  return resident_kernel<false, false>(cpw);
+  return resident_kernel<false, false, P>(cpw);
+}
+
+const void *resident_kernel_for(bool gated, bool gather, int cpw, int32_t payload) {
+  return payload == kPayloadF16 ? resident_kernel_for<F16Payload>(gated, gather, cpw)
+                                : resident_kernel_for<Bf16Payload>(gated, gather, cpw);
 }
 
 struct TileShape {
@@ -2145,18 +2164,24 @@ constexpr int kNarrowDecodeTile = 4;  // 64 x 64
 // STREAM: the grid has one token tile, so each weight tile has one reader and its loads
 // carry the nontemporal hint (a compile-time policy: a per-load branch on an argument cost
 // the loading waves ~2 % at 2048 rows).
-template <bool GATED>
+template <bool GATED, class P>
 const void *tile_kernel(int variant, bool stream) {
   using Kernel = void (*)(GemmArgs);
   static const Kernel table[][2] = {
-      {&tile_gemm_kernel<256, 256, 2, 4, 2, GATED>, &tile_gemm_kernel<256, 256, 2, 4, 2, GATED, false, true>},
-      {&tile_gemm_kernel<256, 128, 4, 2, 3, GATED>, &tile_gemm_kernel<256, 128, 4, 2, 3, GATED, false, true>},
-      {&tile_gemm_kernel<128, 128, 2, 2, 3, GATED>, &tile_gemm_kernel<128, 128, 2, 2, 3, GATED, false, true>},
-      {&tile_gemm_kernel<64, 128, 2, 2, 6, GATED>, &tile_gemm_kernel<64, 128, 2, 2, 6, GATED, false, true>},
-      {&tile_gemm_kernel<64, 64, 2, 1, 4, GATED>, &tile_gemm_kernel<64, 64, 2, 1, 4, GATED, false, true>},
+      {&tile_gemm_kernel<256, 256, 2, 4, 2, GATED, false, false, P>, &tile_gemm_kernel<256, 256, 2, 4, 2, GATED, false, true, P>},
+      {&tile_gemm_kernel<256, 128, 4, 2, 3, GATED, false, false, P>, &tile_gemm_kernel<256, 128, 4, 2, 3, GATED, false, true, P>},
+      {&tile_gemm_kernel<128, 128, 2, 2, 3, GATED, false, false, P>, &tile_gemm_kernel<128, 128, 2, 2, 3, GATED, false, true, P>},
+      {&tile_gemm_kernel<64, 128, 2, 2, 6, GATED, false, false, P>, &tile_gemm_kernel<64, 128, 2, 2, 6, GATED, false, true, P>},
+      {&tile_gemm_kernel<64, 64, 2, 1, 4, GATED, false, false, P>, &tile_gemm_kernel<64, 64, 2, 1, 4, GATED, false, true, P>},
   };
   static_assert(sizeof(table) / sizeof(table[0]) == kTileShapeCount, "one kernel per tile shape");
   return reinterpret_cast<const void *>(table[variant][stream ? 1 : 0]);
+}
+
+template <bool GATED>
+const void *tile_kernel(int variant, bool stream, int32_t payload) {
+  return payload == kPayloadF16 ? tile_kernel<GATED, F16Payload>(variant, stream)
+                                : tile_kernel<GATED, Bf16Payload>(variant, stream);
 }
 
 constexpr int kComputeUnits = 256;
@@ -2596,7 +2621,8 @@ GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmCho
     const int64_t per_group = kSplitWaves / choice.k_split;
     // The gather fuses into one token group (gate_up of a Dense step, the MoE router).
     const bool gather = fused_gather && choice.variant == 1;
-    kernel.func = gated ? split_kernel<true>(choice.variant, gather) : split_kernel<false>(choice.variant, gather);
+    kernel.func = gated ? split_kernel<true>(choice.variant, gather, args.payload)
+                        : split_kernel<false>(choice.variant, gather, args.payload);
     kernel.grid = dim3(static_cast<unsigned>((row_blocks + per_group - 1) / per_group), 1, 1);
     kernel.block = dim3(64 * kSplitWaves, 1, 1);
     // Dynamic LDS beyond 64 KB: launch() opts the function in (enable_large_lds).
@@ -2607,7 +2633,7 @@ GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmCho
     // Chosen only for a Dense step's gate_up with the gather fused.
     const int64_t row_blocks = (args.n + 15) / 16;
     const int64_t units = (row_blocks * choice.k_split + kSplitWaves - 1) / kSplitWaves;
-    kernel.func = gated ? split_gathered_kernel_ptr<true>() : split_gathered_kernel_ptr<false>();
+    kernel.func = gated ? split_gathered_kernel_ptr<true>(args.payload) : split_gathered_kernel_ptr<false>(args.payload);
     kernel.grid = dim3(static_cast<unsigned>(units < kSplitGatheredWorkgroups ? units : kSplitGatheredWorkgroups), 1, 1);
     kernel.block = dim3(64 * kSplitWaves, 1, 1);
     kernel.shmem = static_cast<unsigned>((capacity < kSplitGroupTokens ? capacity : kSplitGroupTokens) * (args.k + 16) * 2 +
@@ -2616,14 +2642,15 @@ GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmCho
     const int64_t row_blocks = (args.n + 15) / 16;
     const int cpw = static_cast<int>(choice.k_slice / (kResidentWaves * kResidentChunk));
     const int64_t walkers = std::min<int64_t>(kResidentWorkgroups / choice.k_split, row_blocks);
-    kernel.func = resident_kernel_for(gated, fused_gather && gated, cpw);
+    kernel.func = resident_kernel_for(gated, fused_gather && gated, cpw, args.payload);
     kernel.grid = dim3(static_cast<unsigned>(choice.k_split * walkers), 1, 1);
     kernel.block = dim3(64 * kResidentWaves, 1, 1);
   } else if (choice.kind == GemmKind::Stream) {
     const int64_t groups = ((args.n + 15) / 16 + kStreamWaves - 1) / kStreamWaves;
     const int64_t slices = stream_slices(args.k, choice.k_slice);
     const bool gather = fused_gather && gated;
-    kernel.func = gather ? stream_kernel<true, true>() : (gated ? stream_kernel<true>() : stream_kernel<false>());
+    kernel.func = gather ? stream_kernel<true, true>(args.payload)
+                         : (gated ? stream_kernel<true>(args.payload) : stream_kernel<false>(args.payload));
     kernel.grid = dim3(static_cast<unsigned>(slices * groups), 1, 1);
     kernel.block = dim3(64 * kStreamWaves, 1, 1);
     // Dynamic LDS beyond 64 KB: launch() opts the function in (enable_large_lds).
@@ -2631,7 +2658,8 @@ GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmCho
   } else {
     const TileShape &shape = kTileShapes[choice.variant];
     const bool stream = capacity <= shape.bm;
-    kernel.func = gated ? tile_kernel<true>(choice.variant, stream) : tile_kernel<false>(choice.variant, stream);
+    kernel.func = gated ? tile_kernel<true>(choice.variant, stream, args.payload)
+                        : tile_kernel<false>(choice.variant, stream, args.payload);
     kernel.grid = dim3(static_cast<unsigned>((args.n + shape.bn - 1) / shape.bn),
                        static_cast<unsigned>((capacity + shape.bm - 1) / shape.bm),
                        static_cast<unsigned>(choice.k_split));
@@ -2639,8 +2667,7 @@ GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmCho
   }
   if (scratch_slices(choice, args.k) > 1) {
     KernelLaunch &reduce = launches.reduce;
-    reduce.func = gated ? reinterpret_cast<const void *>(&stream_reduce_kernel<true>)
-                        : reinterpret_cast<const void *>(&stream_reduce_kernel<false>);
+    reduce.func = gated ? stream_reduce<true>(args.payload) : stream_reduce<false>(args.payload);
     reduce.grid = dim3(static_cast<unsigned>((capacity * (args.n / 4) + 255) / 256), 1, 1);
     reduce.block = dim3(256, 1, 1);
     reduce.set_args(record);

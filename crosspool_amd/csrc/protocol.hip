@@ -392,17 +392,18 @@ __device__ bool complete_request(const TransportArgs &a) {
   return failed;
 }
 
-// The canonical failure output: every bf16 value a quiet NaN (instance.cu:28-31).
+// The canonical failure output: every value a quiet NaN of the payload dtype
+// (static_cast<Scalar>(NAN), instance.cu:28-31).
 __device__ void fill_failure_output(const TransportArgs &a) {
   const uint64_t elements = a.output_elements;
   const bool aligned = (reinterpret_cast<uintptr_t>(a.output) & 15u) == 0;
   const uint64_t vectors = aligned ? elements / 8 : 0;
-  const u32x4 poison = {kPoisonBf16x2, kPoisonBf16x2, kPoisonBf16x2, kPoisonBf16x2};
+  const u32x4 poison = {a.output_nan2, a.output_nan2, a.output_nan2, a.output_nan2};
   for (uint64_t index = threadIdx.x; index < vectors; index += kCompleteThreads) {
     store16(a.output + index * 8, poison);
   }
   for (uint64_t index = vectors * 8 + threadIdx.x; index < elements; index += kCompleteThreads) {
-    a.output[index] = static_cast<uint16_t>(kPoisonBf16x2 & 0xffffu);
+    a.output[index] = static_cast<uint16_t>(a.output_nan2 & 0xffffu);
   }
 }
 

@@ -117,6 +117,14 @@ int validate_geometry(int64_t hidden, int64_t intermediate) {
 
 GatedSilu default_activation() { return GatedSilu{1.0f, 0.0f, 0.0f}; }
 
+// The Dense payload dtype of the ABI (XP_DTYPE_BF16 / XP_DTYPE_F16, ffn.hpp:83-85) as the
+// kernels' PayloadKind.
+int payload_kind(int dtype, int32_t &out) {
+  XP_REQUIRE(dtype == XP_DTYPE_BF16 || dtype == XP_DTYPE_F16, "Dense payload dtype must be bf16 or fp16");
+  out = dtype == XP_DTYPE_F16 ? kPayloadF16 : kPayloadBf16;
+  return XP_OK;
+}
+
 // The kernels of one mailbox step, for a given capacity: gather (+ RMSNorm), gate_up
 // with the gated SiLU fused (+ its K-slice reduction), down with the scatter fused (+ its
 // reduction).  At decode sizes the gather is fused into gate_up and has no launch of its
@@ -170,6 +178,7 @@ struct DenseBinding {
   float eps;
   uint8_t *workspace;
   uint32_t *fault;
+  int32_t payload;  // PayloadKind
 };
 
 DenseLaunches make_dense_launches(const DenseBinding &b, int64_t capacity) {
@@ -191,6 +200,7 @@ DenseLaunches make_dense_launches(const DenseBinding &b, int64_t capacity) {
     gather.hidden = b.hidden;
     gather.rows = b.rows;
     gather.eps = b.eps;
+    gather.payload = b.payload;
     launches.gather = make_gather(gather, capacity);
   }
 
@@ -206,6 +216,7 @@ DenseLaunches make_dense_launches(const DenseBinding &b, int64_t capacity) {
   gate_up.n = 2 * b.intermediate;
   gate_up.k = b.hidden;
   gate_up.act = default_activation();
+  gate_up.payload = b.payload;
   gate_up.partials = reinterpret_cast<float *>(b.workspace + layout.gate_up_partials_offset);
   if (fused) {
     gate_up.gather_slots = b.slots;
@@ -228,6 +239,7 @@ DenseLaunches make_dense_launches(const DenseBinding &b, int64_t capacity) {
   down.n = b.hidden;
   down.k = b.intermediate;
   down.act = default_activation();
+  down.payload = b.payload;
   down.partials = reinterpret_cast<float *>(b.workspace + layout.down_partials_offset);
   launches.down = make_gemm(down, capacity, false, choose_gemm(capacity, down.n, down.k, false));
   return launches;
@@ -285,6 +297,7 @@ struct Layer {
   const uint16_t *down;
   const uint16_t *norm;
   float eps;
+  int32_t payload = kPayloadBf16;  // Dense layers: PayloadKind of weights, norm and mailbox
   int kind = XP_LAYER_DENSE;
   // MoE layers: the execution identity, the Router projection and its correction bias.
   xp_moe_layer_desc moe{};
@@ -303,6 +316,7 @@ struct Template {
   int kind = XP_LAYER_DENSE;
   int64_t hidden = 0;
   int64_t intermediate = 0;
+  int32_t payload = kPayloadBf16;
   int64_t capacity = 0;
   xp_moe_layer_desc moe{};  // MoE templates: the signature they were captured for
   hipGraph_t graph = nullptr;
@@ -896,6 +910,7 @@ TransportArgs transport_args(xp_transport_t transport, int arena) {
   args.arenas = transport->arenas;
   args.arena = arena;
   args.arena_count = transport->arena_count;
+  args.output_nan2 = Bf16Payload::kPoison2;
   return args;
 }
 
@@ -1505,10 +1520,14 @@ int xp_agent_destroy(xp_agent_t agent) {
 }
 
 int xp_layer_register(xp_agent_t agent, int instance_index, int layer_ordinal, int64_t hidden, int64_t intermediate,
-                      const void *gate_up, const void *down, const void *norm_weight, float eps) {
+                      int payload_dtype, const void *gate_up, const void *down, const void *norm_weight, float eps) {
   XP_REQUIRE(agent != nullptr, "agent must be non-null");
   XP_REQUIRE(instance_index >= 0 && layer_ordinal >= 0, "instance index and layer ordinal must be non-negative");
   if (const int status = validate_geometry(hidden, intermediate); status != XP_OK) {
+    return status;
+  }
+  int32_t payload = kPayloadBf16;
+  if (const int status = payload_kind(payload_dtype, payload); status != XP_OK) {
     return status;
   }
   XP_REQUIRE(gate_up != nullptr && down != nullptr, "layer weights must be non-null");
@@ -1523,7 +1542,8 @@ int xp_layer_register(xp_agent_t agent, int instance_index, int layer_ordinal, i
               static_cast<const uint16_t *>(gate_up),
               static_cast<const uint16_t *>(down),
               static_cast<const uint16_t *>(norm_weight),
-              eps};
+              eps,
+              payload};
   for (Layer &existing : agent->layers) {
     if (existing.instance_index == instance_index && existing.layer_ordinal == layer_ordinal) {
       existing = layer;
@@ -1623,9 +1643,13 @@ int xp_lane_clear_fault(xp_lane_t lane) {
   return XP_OK;
 }
 
-int xp_template_capture(xp_lane_t lane, int64_t hidden, int64_t intermediate, int64_t capacity) {
+int xp_template_capture(xp_lane_t lane, int64_t hidden, int64_t intermediate, int payload_dtype, int64_t capacity) {
   XP_REQUIRE(lane != nullptr, "lane must be non-null");
   if (const int status = validate_geometry(hidden, intermediate); status != XP_OK) {
+    return status;
+  }
+  int32_t payload = kPayloadBf16;
+  if (const int status = payload_kind(payload_dtype, payload); status != XP_OK) {
     return status;
   }
   XP_REQUIRE(capacity > 0, "template capacity must be positive");
@@ -1637,7 +1661,7 @@ int xp_template_capture(xp_lane_t lane, int64_t hidden, int64_t intermediate, in
   std::lock_guard<std::mutex> guard(lane->mutex);
   for (const auto &t : lane->templates) {
     if (t->kind == XP_LAYER_DENSE && t->hidden == hidden && t->intermediate == intermediate &&
-        t->capacity == capacity) {
+        t->payload == payload && t->capacity == capacity) {
       return XP_OK;
     }
   }
@@ -1646,6 +1670,7 @@ int xp_template_capture(xp_lane_t lane, int64_t hidden, int64_t intermediate, in
   DenseBinding binding{};
   binding.hidden = hidden;
   binding.intermediate = intermediate;
+  binding.payload = payload;
   binding.rows = 0;
   binding.workspace = lane->workspace;
   binding.fault = lane->fault;
@@ -1653,6 +1678,7 @@ int xp_template_capture(xp_lane_t lane, int64_t hidden, int64_t intermediate, in
   t->kind = XP_LAYER_DENSE;
   t->hidden = hidden;
   t->intermediate = intermediate;
+  t->payload = payload;
   t->capacity = capacity;
   if (const int status = instantiate_template(*t, dense_chain(binding, capacity)); status != XP_OK) {
     return status;
@@ -1661,13 +1687,17 @@ int xp_template_capture(xp_lane_t lane, int64_t hidden, int64_t intermediate, in
   return XP_OK;
 }
 
-int xp_template_capacities(xp_lane_t lane, int64_t hidden, int64_t intermediate, int64_t *capacities,
-                           int max_count, int *count) {
+int xp_template_capacities(xp_lane_t lane, int64_t hidden, int64_t intermediate, int payload_dtype,
+                           int64_t *capacities, int max_count, int *count) {
   XP_REQUIRE(lane != nullptr && count != nullptr, "lane and count pointer must be non-null");
+  int32_t payload = kPayloadBf16;
+  if (const int status = payload_kind(payload_dtype, payload); status != XP_OK) {
+    return status;
+  }
   std::lock_guard<std::mutex> guard(lane->mutex);
   int found = 0;
   for (const auto &t : lane->templates) {
-    if (t->kind == XP_LAYER_DENSE && t->hidden == hidden && t->intermediate == intermediate) {
+    if (t->kind == XP_LAYER_DENSE && t->hidden == hidden && t->intermediate == intermediate && t->payload == payload) {
       if (capacities != nullptr && found < max_count) {
         capacities[found] = t->capacity;
       }
@@ -1704,7 +1734,8 @@ int xp_replay(xp_lane_t lane, int instance_index, int layer_ordinal, int64_t row
   for (const auto &t : lane->templates) {
     const bool serves = t->kind == layer.kind &&
                         (layer.kind == XP_LAYER_MOE ? same_moe(t->moe, layer.moe)
-                                                    : t->hidden == layer.hidden && t->intermediate == layer.intermediate);
+                                                    : t->hidden == layer.hidden && t->intermediate == layer.intermediate &&
+                                                          t->payload == layer.payload);
     if (serves) {
       largest = std::max(largest, t->capacity);
       if (selected == nullptr && rows <= t->capacity) {
@@ -1747,6 +1778,7 @@ int xp_replay(xp_lane_t lane, int instance_index, int layer_ordinal, int64_t row
   binding.eps = layer.eps;
   binding.workspace = lane->workspace;
   binding.fault = lane->fault;
+  binding.payload = layer.payload;
   return run_chain(lane, *selected, dense_chain(binding, selected->capacity), target);
 }
 
@@ -1861,14 +1893,19 @@ int xp_transport_evaluate(xp_transport_t transport, int arena, const uint32_t *f
 }
 
 int xp_transport_complete(xp_transport_t transport, int arena, void *output, int64_t output_elements,
-                          int64_t timeout_ns, xp_stream_t stream) {
+                          int payload_dtype, int64_t timeout_ns, xp_stream_t stream) {
   XP_REQUIRE(valid_arena(transport, arena), "arena index is outside the transport");
   XP_REQUIRE(output_elements >= 0, "output element count must be non-negative");
   XP_REQUIRE(output != nullptr || output_elements == 0, "output must be non-null when it has elements");
-  XP_REQUIRE((reinterpret_cast<uintptr_t>(output) & 1u) == 0, "output must be 2-byte aligned bf16");
+  XP_REQUIRE((reinterpret_cast<uintptr_t>(output) & 1u) == 0, "output must be 2-byte aligned 16-bit values");
+  int32_t payload = kPayloadBf16;
+  if (const int status = payload_kind(payload_dtype, payload); status != XP_OK) {
+    return status;
+  }
   TransportArgs args = transport_args(transport, arena);
   args.output = static_cast<uint16_t *>(output);
   args.output_elements = static_cast<uint64_t>(output_elements);
+  args.output_nan2 = payload == kPayloadF16 ? F16Payload::kPoison2 : Bf16Payload::kPoison2;
   const uint64_t nanoseconds = timeout_ns > 0 ? static_cast<uint64_t>(timeout_ns) : kTransportDefaultTimeoutNs;
   // ticks = ns * kHz / 1e6, kept in range for timeouts up to hours.
   args.timeout_ticks = nanoseconds / 1000 * transport->wall_clock_khz / 1000 + 1;
@@ -1877,15 +1914,20 @@ int xp_transport_complete(xp_transport_t transport, int arena, void *output, int
 }
 
 int xp_transport_settle(xp_transport_t transport, int arena, const uint32_t *fault_word, void *output,
-                        int64_t output_elements, xp_stream_t stream) {
+                        int64_t output_elements, int payload_dtype, xp_stream_t stream) {
   XP_REQUIRE(valid_arena(transport, arena), "arena index is outside the transport");
   XP_REQUIRE(output_elements >= 0, "output element count must be non-negative");
   XP_REQUIRE(output != nullptr || output_elements == 0, "output must be non-null when it has elements");
-  XP_REQUIRE((reinterpret_cast<uintptr_t>(output) & 1u) == 0, "output must be 2-byte aligned bf16");
+  XP_REQUIRE((reinterpret_cast<uintptr_t>(output) & 1u) == 0, "output must be 2-byte aligned 16-bit values");
+  int32_t payload = kPayloadBf16;
+  if (const int status = payload_kind(payload_dtype, payload); status != XP_OK) {
+    return status;
+  }
   TransportArgs args = transport_args(transport, arena);
   args.fault = fault_word;
   args.output = static_cast<uint16_t *>(output);
   args.output_elements = static_cast<uint64_t>(output_elements);
+  args.output_nan2 = payload == kPayloadF16 ? F16Payload::kPoison2 : Bf16Payload::kPoison2;
   args.timeout_ticks = kTransportDefaultTimeoutNs / 1000 * transport->wall_clock_khz / 1000 + 1;
   std::lock_guard<std::mutex> guard(transport->mutex);
   return launch_transport(transport, make_transport_settle(args), stream);

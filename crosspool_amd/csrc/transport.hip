@@ -35,7 +35,7 @@ __global__ __launch_bounds__(256) void copy_bytes_kernel(CopyArgs a) {
 // One wavefront per row; CHUNKS 16-byte chunks per lane stay in registers between the
 // sum-of-squares reduction and the normalised store (hidden <= CHUNKS * 512).  The norm
 // weight is loaded together with the row, so a row costs one memory round trip, not two.
-template <int CHUNKS>
+template <int CHUNKS, class P>
 __global__ __launch_bounds__(256) void gather_rows_kernel(GatherArgs a) {
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
@@ -47,7 +47,7 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(GatherArgs a) {
   const int32_t slot = a.slots[row];
   if (slot < 0 || static_cast<int64_t>(slot) >= a.pool_rows) {
     // Canonical failure: poison the row with quiet NaNs and raise the sticky fault bit.
-    const u32x4 poison = {kPoisonBf16x2, kPoisonBf16x2, kPoisonBf16x2, kPoisonBf16x2};
+    const u32x4 poison = {P::kPoison2, P::kPoison2, P::kPoison2, P::kPoison2};
     for (int64_t chunk = lane; chunk < chunks; chunk += kWave) {
       store16(destination + chunk * 8, poison);
     }
@@ -79,14 +79,14 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(GatherArgs a) {
   float squares = 0.0f;
 #pragma unroll
   for (int index = 0; index < CHUNKS; ++index) {
-    add_squares(values[index], squares);
+    add_squares<P>(values[index], squares);
   }
   const float inverse = rms_inverse(squares, a.hidden, a.eps);
 #pragma unroll
   for (int index = 0; index < CHUNKS; ++index) {
     const int64_t chunk = lane + index * kWave;
     if (chunk < chunks) {
-      store16(destination + chunk * 8, normalize_chunk(values[index], inverse, weights[index]));
+      store16(destination + chunk * 8, normalize_chunk<P>(values[index], inverse, weights[index]));
     }
   }
 }
@@ -115,8 +115,9 @@ __global__ __launch_bounds__(256) void scatter_rows_kernel(ScatterArgs a) {
 constexpr int64_t kMaxGatherChunks = 32;
 
 template <int CHUNKS>
-const void *gather_kernel_for() {
-  return reinterpret_cast<const void *>(&gather_rows_kernel<CHUNKS>);
+const void *gather_kernel_for(int32_t payload) {
+  return payload == kPayloadF16 ? reinterpret_cast<const void *>(&gather_rows_kernel<CHUNKS, F16Payload>)
+                                : reinterpret_cast<const void *>(&gather_rows_kernel<CHUNKS, Bf16Payload>);
 }
 
 // Fixed-order TP partial sum (the exchange step's arithmetic, src/cext/ffnagent/
@@ -185,17 +186,17 @@ KernelLaunch make_gather(const GatherArgs &args, int64_t capacity) {
   KernelLaunch kernel;
   const int64_t chunks_per_lane = (args.hidden / 8 + kWave - 1) / kWave;
   if (chunks_per_lane <= 1) {
-    kernel.func = gather_kernel_for<1>();
+    kernel.func = gather_kernel_for<1>(args.payload);
   } else if (chunks_per_lane <= 2) {
-    kernel.func = gather_kernel_for<2>();
+    kernel.func = gather_kernel_for<2>(args.payload);
   } else if (chunks_per_lane <= 4) {
-    kernel.func = gather_kernel_for<4>();
+    kernel.func = gather_kernel_for<4>(args.payload);
   } else if (chunks_per_lane <= 8) {
-    kernel.func = gather_kernel_for<8>();
+    kernel.func = gather_kernel_for<8>(args.payload);
   } else if (chunks_per_lane <= 16) {
-    kernel.func = gather_kernel_for<16>();
+    kernel.func = gather_kernel_for<16>(args.payload);
   } else {
-    kernel.func = gather_kernel_for<32>();
+    kernel.func = gather_kernel_for<32>(args.payload);
   }
   kernel.grid = dim3(static_cast<unsigned>((capacity + 3) / 4), 1, 1);
   kernel.block = dim3(256, 1, 1);

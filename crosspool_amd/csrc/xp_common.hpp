@@ -75,6 +75,76 @@ __device__ __forceinline__ float gated_silu(float gate, float up, const GatedSil
   return g * __builtin_amdgcn_rcpf(1.0f + __expf(-act.alpha * g)) * (u + act.up_offset);
 }
 
+// ------------------------------------------------------------------ payload dtypes
+// The 16-bit float of a Dense layer's mailbox, weights and activations: bf16 or fp16 (the
+// reference admits both, ffn.hpp:83-85).  Kernels take the payload as a template argument;
+// everything dtype-specific goes through these: the widening of one 16-bit pattern, the
+// round-to-nearest-even packing of two fp32 values, the quiet-NaN fill of a failed row
+// (static_cast<Scalar>(NAN), instance.cu:28-31) and the MFMA tiles of the projections.
+using f16x8 = _Float16 __attribute__((ext_vector_type(8)));
+
+struct Bf16Payload {
+  static constexpr uint32_t kPoison2 = 0x7fc07fc0u;  // two bf16 quiet NaNs
+  __device__ static __forceinline__ float widen(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+  __device__ static __forceinline__ uint32_t pack2(float lo, float hi) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{lo, hi}), bf16x2_t));
+  }
+  __device__ static __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+  }
+  __device__ static __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+  }
+};
+
+struct F16Payload {
+  static constexpr uint32_t kPoison2 = 0x7e007e00u;  // two fp16 quiet NaNs
+  __device__ static __forceinline__ float widen(uint32_t bits16) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16)));
+  }
+  __device__ static __forceinline__ uint32_t pack2(float lo, float hi) {
+    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{lo, hi}), f16x2_t));
+  }
+  __device__ static __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                  0, 0);
+  }
+  __device__ static __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                  0, 0);
+  }
+};
+
+// Round through the payload dtype and back (the projection's rounding point).
+template <class P>
+__device__ __forceinline__ float round_payload(float value) {
+  return P::widen(P::pack2(value, 0.0f) & 0xffffu);
+}
+
+// gated_silu_fixed / gated_silu with the rounding point in payload P.
+template <class P, bool CLIP>
+__device__ __forceinline__ float gated_silu_payload(float gate, float up, const GatedSilu &act) {
+  const uint32_t both = P::pack2(gate, up);
+  float g = P::widen(both & 0xffffu);
+  float u = P::widen(both >> 16);
+  if constexpr (CLIP) {
+    g = fminf(g, act.limit);
+    u = fminf(fmaxf(u, -act.limit), act.limit);
+  }
+  return g * __builtin_amdgcn_rcpf(1.0f + __expf(-act.alpha * g)) * (u + act.up_offset);
+}
+
+template <class P>
+__device__ __forceinline__ float gated_silu_payload(float gate, float up, const GatedSilu &act) {
+  return act.limit > 0.0f ? gated_silu_payload<P, true>(gate, up, act) : gated_silu_payload<P, false>(gate, up, act);
+}
+
 __device__ __forceinline__ u32x4 load16(const void *address) {
   return *reinterpret_cast<const u32x4 *>(address);
 }
@@ -120,11 +190,12 @@ __device__ __forceinline__ float wave_sum(float value) {
 // the decode projection so that both produce the same bits.  One wavefront takes a row's
 // sum of squares, lane i over its 16-byte chunks i, i + 64, ... in that order (add_squares),
 // reduced with wave_sum (rms_inverse); each element becomes bf16((x * inverse) * w).
+template <class P = Bf16Payload>
 __device__ __forceinline__ void add_squares(u32x4 chunk, float &squares) {
 #pragma unroll
   for (int word = 0; word < 4; ++word) {
-    const float lo = bf16_to_float(chunk[word] & 0xffffu);
-    const float hi = bf16_to_float(chunk[word] >> 16);
+    const float lo = P::widen(chunk[word] & 0xffffu);
+    const float hi = P::widen(chunk[word] >> 16);
     squares += lo * lo;
     squares += hi * hi;
   }
@@ -135,13 +206,14 @@ __device__ __forceinline__ float rms_inverse(float lane_squares, int64_t hidden,
   return 1.0f / sqrtf(squares / static_cast<float>(hidden) + eps);
 }
 
+template <class P = Bf16Payload>
 __device__ __forceinline__ u32x4 normalize_chunk(u32x4 x, float inverse, u32x4 weight) {
   u32x4 result;
 #pragma unroll
   for (int word = 0; word < 4; ++word) {
-    const float lo = bf16_to_float(x[word] & 0xffffu) * inverse;
-    const float hi = bf16_to_float(x[word] >> 16) * inverse;
-    result[word] = pack_bf16x2(lo * bf16_to_float(weight[word] & 0xffffu), hi * bf16_to_float(weight[word] >> 16));
+    const float lo = P::widen(x[word] & 0xffffu) * inverse;
+    const float hi = P::widen(x[word] >> 16) * inverse;
+    result[word] = P::pack2(lo * P::widen(weight[word] & 0xffffu), hi * P::widen(weight[word] >> 16));
   }
   return result;
 }

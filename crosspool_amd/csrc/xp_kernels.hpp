@@ -58,8 +58,11 @@ struct CopyArgs {
   uint64_t bytes;
 };
 
+// Payload dtype of a Dense step's kernels (argument records are zero-initialised: bf16).
+enum PayloadKind : int32_t { kPayloadBf16 = 0, kPayloadF16 = 1 };
+
 struct GatherArgs {
-  const uint16_t *pool;      // [pool_rows, hidden] bf16 mailbox
+  const uint16_t *pool;      // [pool_rows, hidden] payload-dtype mailbox
   const int32_t *slots;      // [rows] slot ids
   const uint16_t *norm;      // [hidden] RMSNorm weight, or null for a plain gather
   uint16_t *out;             // [rows, hidden] contiguous batch
@@ -68,6 +71,7 @@ struct GatherArgs {
   int64_t hidden;
   int64_t rows;              // live rows
   float eps;
+  int32_t payload;           // PayloadKind of the mailbox, norm weight and batch
 };
 
 struct ScatterArgs {
@@ -149,6 +153,7 @@ struct TransportArgs {
   uint16_t *output;             // complete: caller output, NaN-filled on failure; probe: observations
   const uint32_t *fault;        // evaluate: the Lane's sticky fault word, or null
   uint64_t output_elements;     // complete
+  uint32_t output_nan2;         // complete: two quiet NaNs of the output's payload dtype
   uint64_t payload_rows;        // submit
   uint64_t timeout_ticks;       // complete: wall-clock ticks before the wait gives up
   RequestMetadata request;      // submit
@@ -360,6 +365,7 @@ struct GemmArgs {
   const int32_t *expert_end;
   const float *row_scale;
   int64_t gather_divisor;
+  int32_t payload;  // PayloadKind of x, w and out (the MoE projections are bf16 only)
 };
 
 // SplitGathered: the split kernel's units walked by a persistent grid that gathers the token

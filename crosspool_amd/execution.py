@@ -117,8 +117,8 @@ class DenseFfnExecutionSignature:
     gate: GateTransform = GateTransform()
 
     def __post_init__(self) -> None:
-        if self.payload_dtype is not torch.bfloat16:
-            raise ValueError("the MI355X Dense path executes bf16 payloads")
+        if self.payload_dtype not in (torch.bfloat16, torch.float16):
+            raise ValueError("the MI355X Dense path executes bf16 or fp16 payloads (ffn.hpp:83-85)")
         for name in ("payload_row_capacity", "hidden_size", "local_intermediate_size"):
             value = getattr(self, name)
             if isinstance(value, bool) or not isinstance(value, int) or value <= 0:

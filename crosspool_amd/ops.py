@@ -36,6 +36,7 @@ class _Attachment:
     agent: FfnAgent
     instance_index: int
     hidden_size: int
+    payload_dtype: torch.dtype
     capacity: int
     atn_dp_size: int
     lane: int
@@ -70,10 +71,10 @@ def attach(
     global _attachment
     if not agent.materialized:
         raise RuntimeError("attach requires a materialized FfnAgent")
-    shapes = {b.weights.hidden_size for (i, _), b in agent.layers.items() if i == instance_index}
+    shapes = {(b.weights.hidden_size, b.payload_dtype) for (i, _), b in agent.layers.items() if i == instance_index}
     if len(shapes) != 1:
-        raise ValueError("the attached instance must have registered layers of one hidden size")
-    hidden_size = shapes.pop()
+        raise ValueError("the attached instance must have registered layers of one hidden size and payload dtype")
+    hidden_size, payload_dtype = shapes.pop()
     capacity = max(t.signature.payload_row_capacity for t in agent.templates.values())
     transport = None
     if mailbox:
@@ -85,6 +86,7 @@ def attach(
             agent=agent,
             instance_index=instance_index,
             hidden_size=hidden_size,
+            payload_dtype=payload_dtype,
             capacity=capacity,
             atn_dp_size=atn_dp_size,
             lane=lane,
@@ -165,7 +167,7 @@ def ffn_shim(
             raise RuntimeError("xpool FFN shim DP-rank payload rows must be a device int32 or int64 tensor")
     if hidden_states.shape[1] != attachment.hidden_size:
         raise RuntimeError("xpool FFN shim hidden size does not match the attached Transport arena")
-    if hidden_states.dtype is not torch.bfloat16:
+    if hidden_states.dtype is not attachment.payload_dtype:
         raise RuntimeError("xpool FFN shim dtype does not match the attached Transport arena")
     if hidden_states.device != attachment.agent.device:
         raise RuntimeError("xpool FFN shim hidden states must be on the attached Transport arena device")

@@ -28,13 +28,10 @@
 //    poll and an agent-scope acquire; the count is one word, or one word per 8 producers on
 //    lines of its own polled lane by lane.  Every consumer checks the words and sets `flag`
 //    on a mismatch (1) or an expired wait (2).
-//  * probe_grid_sync: a cooperative launch whose workgroups pass `syncs` grid-wide
-//    barriers of the HIP runtime (cooperative_groups grid sync).
 //
 // Each kernel folds what it reads (or computes) into registers and stores it only when
 // `write` is set, which the host never does; the compiler cannot drop the work.
 
-#include <hip/hip_cooperative_groups.h>
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -269,18 +266,6 @@ __global__ __launch_bounds__(512) void probe_handoff_kernel(uint32_t *words, int
   handoff_consume(words, producers, salt, flag);
 }
 
-__global__ __launch_bounds__(512) void probe_grid_sync_kernel(int syncs, uint32_t *sink) {
-  cooperative_groups::grid_group grid = cooperative_groups::this_grid();
-  uint32_t value = 0;
-  for (int i = 0; i < syncs; ++i) {
-    value += blockIdx.x;
-    grid.sync();
-  }
-  if (value == 0xffffffffu) {
-    sink[0] = value;
-  }
-}
-
 }  // namespace
 
 extern "C" {
@@ -358,16 +343,6 @@ int xp_probe_handoff(int producers, int consumers, int mode, uint32_t *words, ui
                        flag);
   }
   return static_cast<int>(hipGetLastError());
-}
-
-// A cooperative launch of `workgroups` 512-thread workgroups passing `syncs` grid barriers.
-int xp_probe_grid_sync(int workgroups, int syncs, void *stream) {
-  uint32_t *sink = nullptr;
-  void *args[] = {&syncs, &sink};
-  const hipError_t status = hipLaunchCooperativeKernel(reinterpret_cast<const void *>(probe_grid_sync_kernel),
-                                                       dim3(workgroups), dim3(512), args, 0,
-                                                       static_cast<hipStream_t>(stream));
-  return static_cast<int>(status);
 }
 
 }  // extern "C"

@@ -99,6 +99,16 @@ class ArenaSnapshot:
     dp_rank_payload_rows: tuple[int, ...]
 
 
+def _completion_output(output: torch.Tensor | None) -> tuple[ctypes.c_void_p | None, int, int]:
+    """Pointer, element count and payload dtype code of a completion's output (bf16 or fp16)."""
+
+    if output is None:
+        return None, 0, _native.XP_DTYPE_BF16
+    if output.dtype not in (torch.bfloat16, torch.float16) or not output.is_contiguous():
+        raise ValueError("the completion output must be a contiguous bf16 or fp16 tensor")
+    return ctypes.c_void_p(output.data_ptr()), output.numel(), _native.payload_dtype_code(output.dtype)
+
+
 class TransportResident:
     """The Transport arenas of one device and the agent that answers their mailboxes.
 
@@ -177,14 +187,13 @@ class TransportResident:
         timeout_ns: int = 0,
         stream: torch.cuda.Stream | None = None,
     ) -> None:
-        """Observe the result; acknowledge, or close and NaN-fill ``output`` (instance.cu:130-201)."""
+        """Observe the result; acknowledge, or close and NaN-fill ``output`` with quiet NaNs of its
+        dtype (instance.cu:130-201)."""
 
         self._require_open()
-        if output is not None and (output.dtype is not torch.bfloat16 or not output.is_contiguous()):
-            raise ValueError("the completion output must be a contiguous bf16 tensor")
-        pointer = ctypes.c_void_p(output.data_ptr()) if output is not None else None
-        elements = output.numel() if output is not None else 0
-        _native.call("xp_transport_complete", self.handle, arena, pointer, elements, int(timeout_ns), self._stream(stream))
+        pointer, elements, dtype = _completion_output(output)
+        _native.call("xp_transport_complete", self.handle, arena, pointer, elements, dtype, int(timeout_ns),
+                     self._stream(stream))
 
     def settle(
         self,
@@ -196,12 +205,9 @@ class TransportResident:
         """:meth:`evaluate` then :meth:`complete` in one launch, after a Dense step on the same stream."""
 
         self._require_open()
-        if output is not None and (output.dtype is not torch.bfloat16 or not output.is_contiguous()):
-            raise ValueError("the completion output must be a contiguous bf16 tensor")
-        pointer = ctypes.c_void_p(output.data_ptr()) if output is not None else None
-        elements = output.numel() if output is not None else 0
+        pointer, elements, dtype = _completion_output(output)
         fault = ctypes.c_void_p(fault_word) if fault_word else None
-        _native.call("xp_transport_settle", self.handle, arena, fault, pointer, elements, self._stream(stream))
+        _native.call("xp_transport_settle", self.handle, arena, fault, pointer, elements, dtype, self._stream(stream))
 
     def drain(self, stream: torch.cuda.Stream | None = None) -> None:
         """Publish shutdown to every arena and finish their mailboxes (atnagent.cu:92-147)."""

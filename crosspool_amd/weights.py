@@ -87,13 +87,18 @@ class DenseFfnWeights:
         return self.i_proj.values.device
 
     @property
+    def payload_dtype(self) -> torch.dtype:
+        return self.i_proj.values.dtype
+
+    @property
     def template_ready(self) -> bool:
-        """Whether the FfnAgent's captured templates can run these weights: gated bf16
-        INTERLEAVED i_proj ``[2I, H]``, bf16 o_proj, no biases, 16-byte aligned rows."""
+        """Whether the FfnAgent's captured templates can run these weights: gated
+        INTERLEAVED i_proj ``[2I, H]`` and o_proj of one payload dtype (bf16 or fp16,
+        ffn.hpp:83-85), no biases, 16-byte aligned rows."""
 
         i_proj, o_proj = self.i_proj, self.o_proj
         return (
-            i_proj.values.dtype is torch.bfloat16 and o_proj.values.dtype is torch.bfloat16
+            i_proj.values.dtype in (torch.bfloat16, torch.float16) and o_proj.values.dtype is i_proj.values.dtype
             and i_proj.bias is None and o_proj.bias is None
             and i_proj.values.shape[0] == 2 * self.local_intermediate_size
             and self.hidden_size % 8 == 0 and self.local_intermediate_size % 8 == 0

@@ -225,13 +225,15 @@ size_t xp_dense_gate_up_variant(int64_t capacity, int64_t hidden, int64_t interm
 int xp_agent_create(int device, xp_agent_t *out);
 int xp_agent_destroy(xp_agent_t agent);
 
-/* Register (or rebind) one Dense layer's borrowed weights.  gate_up is the
- * INTERLEAVED i_proj [2*intermediate, hidden], down is o_proj [hidden,
+/* Register (or rebind) one Dense layer's borrowed weights.  payload_dtype is XP_DTYPE_BF16
+ * or XP_DTYPE_F16 (is_supported_payload_dtype, src/cext-include/xpool/ffn.hpp:83-85), the
+ * dtype of the weights, the norm weight and the mailboxes the layer is replayed on.  gate_up
+ * is the INTERLEAVED i_proj [2*intermediate, hidden], down is o_proj [hidden,
  * intermediate], norm_weight [hidden] or NULL.  Replaces
  * LayerExecutionDescriptor + DenseBindingView (src/cext-bindings/ffnagent.cpp:44-210)
  * and the device-side weight rebinding of bind_compute (src/cext/ffnagent/runtime.cu:336-369). */
 int xp_layer_register(xp_agent_t agent, int instance_index, int layer_ordinal, int64_t hidden, int64_t intermediate,
-                      const void *gate_up, const void *down, const void *norm_weight, float eps);
+                      int payload_dtype, const void *gate_up, const void *down, const void *norm_weight, float eps);
 
 /* Executor Lane: an owned HIP stream (default priority), a borrowed workspace
  * and a sticky device fault word.  Replaces LaneCaptureResources
@@ -252,13 +254,13 @@ int xp_lane_synchronize(xp_lane_t lane);
 int xp_lane_set_graph_dispatch(xp_lane_t lane, int use_graph);
 
 /* GraphTemplate: build and instantiate this Lane's hipGraph for the Execution
- * Signature (bf16, capacity, hidden, intermediate).  Idempotent per signature.
+ * Signature (payload dtype, capacity, hidden, intermediate).  Idempotent per signature.
  * Replaces capture_dense_signature (src/xpool/runtime/ffnagent/registry.py:189-239)
  * and materialize_lane's graph embedding (src/cext/ffnagent/runtime.cu:701-1006). */
-int xp_template_capture(xp_lane_t lane, int64_t hidden, int64_t intermediate, int64_t capacity);
-/* Number of captured templates; capacities of those matching (hidden, intermediate). */
-int xp_template_capacities(xp_lane_t lane, int64_t hidden, int64_t intermediate, int64_t *capacities,
-                           int max_count, int *count);
+int xp_template_capture(xp_lane_t lane, int64_t hidden, int64_t intermediate, int payload_dtype, int64_t capacity);
+/* Number of captured templates; capacities of those matching (hidden, intermediate, dtype). */
+int xp_template_capacities(xp_lane_t lane, int64_t hidden, int64_t intermediate, int payload_dtype,
+                           int64_t *capacities, int max_count, int *count);
 
 /* Replay the smallest captured capacity >= rows for the layer: gather rows
  * slots[0..rows) of pool_in (+ RMSNorm), the layer's FFN (Dense, or MoE from its
@@ -344,15 +346,16 @@ int xp_transport_evaluate(xp_transport_t transport, int arena, const uint32_t *f
 /* Instance side, second half (src/cext/transport/instance.cu:130-201): wait up to timeout_ns
  * (<= 0: 5 s, wait.cuh:17) for the result; OK acknowledges (Evaluated -> Idle, request facts
  * reset) or, after shutdown, closes; any other result closes the mailbox and fills the
- * `output_elements` bf16 values of `output` with quiet NaNs (instance.cu:28-31).  A wait that
- * times out publishes TIMEOUT as the canonical failure (the reference traps there). */
+ * `output_elements` values of `output` (payload_dtype XP_DTYPE_BF16 or XP_DTYPE_F16) with
+ * quiet NaNs of that dtype (instance.cu:28-31).  A wait that times out publishes TIMEOUT as
+ * the canonical failure (the reference traps there). */
 int xp_transport_complete(xp_transport_t transport, int arena, void *output, int64_t output_elements,
-                          int64_t timeout_ns, xp_stream_t stream);
+                          int payload_dtype, int64_t timeout_ns, xp_stream_t stream);
 
 /* xp_transport_evaluate then xp_transport_complete in one launch on one stream, for a
  * request whose Dense step ran on that same stream (the completion then never waits). */
 int xp_transport_settle(xp_transport_t transport, int arena, const uint32_t *fault_word, void *output,
-                        int64_t output_elements, xp_stream_t stream);
+                        int64_t output_elements, int payload_dtype, xp_stream_t stream);
 
 /* Resident drain (atnagent.cu:92-147): publish shutdown to every arena, close Idle
  * mailboxes, answer Published ones with the canonical failure or SHUTDOWN. */

@@ -30,10 +30,10 @@ def bf16_bits(tensor: torch.Tensor) -> np.ndarray:
     return tensor.contiguous().view(torch.int16).numpy().view(np.uint16)
 
 
-def bf16_from_bits(bits: np.ndarray) -> torch.Tensor:
-    """Inverse of :func:`bf16_bits`."""
+def bf16_from_bits(bits: np.ndarray, dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """Inverse of :func:`bf16_bits`; ``dtype`` names the 16-bit payload (bf16 or fp16)."""
 
-    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16)
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(dtype)
 
 
 def bf16_ulp(values: torch.Tensor) -> torch.Tensor:
@@ -72,7 +72,7 @@ def gather(pool: torch.Tensor, slots: np.ndarray) -> torch.Tensor:
     slots = np.asarray(slots, dtype=np.int64)
     if slots.size and (slots.min() < 0 or slots.max() >= bits.shape[0]):
         raise IndexError("slot id outside the mailbox pool")
-    return bf16_from_bits(bits[slots].copy())
+    return bf16_from_bits(bits[slots].copy(), pool.dtype)
 
 
 def scatter(pool: torch.Tensor, slots: np.ndarray, rows: torch.Tensor) -> torch.Tensor:
@@ -83,31 +83,34 @@ def scatter(pool: torch.Tensor, slots: np.ndarray, rows: torch.Tensor) -> torch.
     generalised from a prefix to slot ids.  Slot ids must be distinct.
     """
 
+    if rows.dtype is not pool.dtype:
+        raise ValueError("scatter rows must have the mailbox payload dtype")
     bits = bf16_bits(pool).copy()
     slots = np.asarray(slots, dtype=np.int64)
     if len(set(slots.tolist())) != slots.size:
         raise ValueError("scatter slot ids must be distinct")
     bits[slots] = bf16_bits(rows)
-    return bf16_from_bits(bits)
+    return bf16_from_bits(bits, pool.dtype)
 
 
 # --------------------------------------------------------------------------- #
 # RMSNorm (new fusion; textbook formula)
 # --------------------------------------------------------------------------- #
 def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
-    """``bf16(x * rsqrt(mean(x^2) + eps) * w)`` with fp32 math.
+    """``payload(x * rsqrt(mean(x^2) + eps) * w)`` with fp32 math, in x's payload dtype (bf16
+    or fp16).
 
     The reference path has no RMSNorm (SGLang applies ``post_attention_layernorm``
     before the shim: src/xpool/integrations/sglang/models/qwen2.py:125-126).
     This is the textbook formula as SGLang's native RMSNorm evaluates it: fp32
     mean of squares, ``1/sqrt(. + eps)``, multiply by x then by the weight in
-    fp32, one rounding to bf16.  Parity with SGLang's kernel is unpinned.
+    fp32, one rounding to the payload dtype.  Parity with SGLang's kernel is unpinned.
     """
 
     xf = x.float()
     variance = xf.pow(2).mean(dim=-1, keepdim=True)
     inverse = 1.0 / torch.sqrt(variance + eps)
-    return ((xf * inverse) * weight.float()).to(torch.bfloat16)
+    return ((xf * inverse) * weight.float()).to(x.dtype)
 
 
 # --------------------------------------------------------------------------- #
@@ -127,8 +130,9 @@ def gated_silu(
     alpha: float = 1.0,
     limit: float | None = None,
     up_offset: float = 0.0,
+    dtype: torch.dtype = torch.bfloat16,
 ) -> torch.Tensor:
-    """Gated activation in fp32, rounded to bf16.
+    """Gated activation in fp32, rounded to the payload ``dtype`` (bf16 or fp16).
 
     operators/activation.py:37-51 (``compute_gated``): Gate clipped above at
     ``limit``, Up clamped to ``[-limit, limit]``, ``silu(gate) * (up + up_offset)``;
@@ -142,7 +146,7 @@ def gated_silu(
     if limit is not None:
         gate = torch.clamp(gate, max=limit)
         up = torch.clamp(up, -limit, limit)
-    return (silu(gate, alpha) * (up + up_offset)).to(torch.bfloat16)
+    return (silu(gate, alpha) * (up + up_offset)).to(dtype)
 
 
 def activation_function(value: torch.Tensor, function: str, *, alpha: float = 1.0,
@@ -259,7 +263,7 @@ def dense_partial_reference(x: torch.Tensor, w_gate_up: torch.Tensor, w_down: to
     projected = torch.mm(x64, w_gate_up.double().t())
     gate = projected[:, 0::2].to(x.dtype)
     up = projected[:, 1::2].to(x.dtype)
-    activated = gated_silu(gate, up)
+    activated = gated_silu(gate, up, dtype=x.dtype)
     return torch.mm(activated.double(), w_down.double().t()).to(x.dtype)
 
 

@@ -1,10 +1,11 @@
 """GPU tests of checkpoint loading into the FfnAgent (crosspool_amd.checkpoint).
 
-A synthetic two-layer Qwen3-style checkpoint (bf16 shards plus one fp32 tensor, gate
-and up of a layer in different files) is loaded as TP rank 1 of 2.  The device shards
-must equal the closed-form TP slice of the source tensors bit for bit, and a mailbox
-step through the loaded layers must meet the FFN parity gates against the oracle run
-on those same slices.
+A synthetic two-layer Qwen3-style checkpoint (bf16 or fp16 shards plus one fp32 tensor,
+gate and up of a layer in different files) is loaded as TP rank 1 of 2.  The device
+shards must be the checkpoint's dtype (the payload dtype the reference's loader keeps,
+loader.py:485-508) and equal the closed-form TP slice of the source tensors bit for bit,
+and a mailbox step through the loaded layers must meet the FFN parity gates against the
+oracle run on those same slices.
 """
 
 from __future__ import annotations
@@ -27,20 +28,21 @@ pytestmark = pytest.mark.gpu
 HIDDEN, INTERMEDIATE, LAYERS, TP_SIZE, TP_RANK = 256, 1024, 2, 2, 1
 
 
-def _write_model(path: Path) -> dict[str, torch.Tensor]:
+def _write_model(path: Path, dtype: torch.dtype = torch.bfloat16) -> dict[str, torch.Tensor]:
     generator = torch.Generator().manual_seed(18)
     tensors: dict[str, torch.Tensor] = {}
     for layer in range(LAYERS):
         gate, up, down = ck.mlp_keys(layer)
-        tensors[gate] = (torch.randn(INTERMEDIATE, HIDDEN, generator=generator) * 0.05).to(torch.bfloat16)
-        tensors[up] = (torch.randn(INTERMEDIATE, HIDDEN, generator=generator) * 0.05).to(torch.bfloat16)
-        tensors[down] = (torch.randn(HIDDEN, INTERMEDIATE, generator=generator) * 0.05).to(torch.bfloat16)
-        tensors[ck.norm_key(layer)] = (1.0 + 0.1 * torch.randn(HIDDEN, generator=generator)).to(torch.bfloat16)
-    tensors[ck.mlp_keys(1)[2]] = tensors[ck.mlp_keys(1)[2]].float()  # one fp32 source (exact in bf16)
+        tensors[gate] = (torch.randn(INTERMEDIATE, HIDDEN, generator=generator) * 0.05).to(dtype)
+        tensors[up] = (torch.randn(INTERMEDIATE, HIDDEN, generator=generator) * 0.05).to(dtype)
+        tensors[down] = (torch.randn(HIDDEN, INTERMEDIATE, generator=generator) * 0.05).to(dtype)
+        tensors[ck.norm_key(layer)] = (1.0 + 0.1 * torch.randn(HIDDEN, generator=generator)).to(dtype)
+    tensors[ck.mlp_keys(1)[2]] = tensors[ck.mlp_keys(1)[2]].float()  # one fp32 source (exact in the dtype)
     path.mkdir()
     config = {
         "architectures": ["Qwen3ForCausalLM"], "model_type": "qwen3", "hidden_act": "silu",
-        "torch_dtype": "bfloat16", "hidden_size": HIDDEN, "intermediate_size": INTERMEDIATE,
+        "torch_dtype": "float16" if dtype is torch.float16 else "bfloat16", "hidden_size": HIDDEN,
+        "intermediate_size": INTERMEDIATE,
         "num_hidden_layers": LAYERS, "rms_norm_eps": 1e-6,
     }
     (path / "config.json").write_text(json.dumps(config), encoding="utf-8")
@@ -55,20 +57,22 @@ def _write_model(path: Path) -> dict[str, torch.Tensor]:
     return tensors
 
 
-def _expected_shard(tensors: dict[str, torch.Tensor], layer: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+def _expected_shard(tensors: dict[str, torch.Tensor], layer: int,
+                    dtype: torch.dtype = torch.bfloat16) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     width = INTERMEDIATE // TP_SIZE
     start = TP_RANK * width
-    gate, up, down = (tensors[key].to(torch.bfloat16) for key in ck.mlp_keys(layer))
-    i_proj = torch.empty(2 * width, HIDDEN, dtype=torch.bfloat16)
+    gate, up, down = (tensors[key].to(dtype) for key in ck.mlp_keys(layer))
+    i_proj = torch.empty(2 * width, HIDDEN, dtype=dtype)
     for j in range(width):
         i_proj[2 * j] = gate[start + j]
         i_proj[2 * j + 1] = up[start + j]
     return i_proj, down[:, start : start + width].contiguous(), tensors[ck.norm_key(layer)]
 
 
-def test_checkpoint_layers_load_and_run(device, tmp_path: Path) -> None:
-    tensors = _write_model(tmp_path / "model")
-    pool = o.generate_hidden_states(128, HIDDEN, 17)
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16), ids=("bf16", "fp16"))
+def test_checkpoint_layers_load_and_run(device, tmp_path: Path, dtype: torch.dtype) -> None:
+    tensors = _write_model(tmp_path / "model", dtype)
+    pool = o.generate_hidden_states(128, HIDDEN, 17).to(dtype)
     slots = o.generate_slots(128, 24, 19)
     with FfnAgent(device) as agent:
         loaded = agent.register_checkpoint(
@@ -76,7 +80,8 @@ def test_checkpoint_layers_load_and_run(device, tmp_path: Path) -> None:
         )
         assert [layer.layer_id for layer in loaded] == [0, 1]
         for layer in loaded:
-            i_proj, o_proj, norm = _expected_shard(tensors, layer.layer_id)
+            assert layer.i_proj.dtype is dtype and layer.o_proj.dtype is dtype and layer.norm_weight.dtype is dtype
+            i_proj, o_proj, norm = _expected_shard(tensors, layer.layer_id, dtype)
             assert_bitwise_equal(layer.i_proj.cpu(), i_proj)
             assert_bitwise_equal(layer.o_proj.cpu(), o_proj)
             assert_bitwise_equal(layer.norm_weight.cpu(), norm)
@@ -89,7 +94,7 @@ def test_checkpoint_layers_load_and_run(device, tmp_path: Path) -> None:
             agent.check_health()
             new_pool = pool_gpu.cpu()
             # The oracle step of this layer on the closed-form shard, from the pool as it was.
-            i_proj, o_proj, norm = _expected_shard(tensors, layer)
+            i_proj, o_proj, norm = _expected_shard(tensors, layer, dtype)
             _, normalized, stage_rows = o.mailbox_step(current, slots, i_proj, o_proj, norm_weight=norm, eps=1e-6)
             untouched = np.setdiff1d(np.arange(pool.shape[0]), slots)
             assert_bitwise_equal(new_pool[untouched], pool[untouched])

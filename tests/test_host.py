@@ -115,8 +115,10 @@ def test_native_workspace_covers_signature_layout(capacity, hidden, intermediate
 
 
 def test_signature_validation():
-    with pytest.raises(ValueError, match="bf16"):
-        DenseFfnExecutionSignature(torch.float16, 4, 16, 8)
+    # bf16 and fp16 payloads (is_supported_payload_dtype, ffn.hpp:83-85); fp32 is refused
+    DenseFfnExecutionSignature(torch.float16, 4, 16, 8)
+    with pytest.raises(ValueError, match="bf16 or fp16"):
+        DenseFfnExecutionSignature(torch.float32, 4, 16, 8)
     with pytest.raises(ValueError, match="multiples of 8"):
         DenseFfnExecutionSignature(torch.bfloat16, 4, 12, 8)
     with pytest.raises(ValueError, match="positive"):
@@ -298,7 +300,9 @@ def test_abi_rejects_invalid_arguments_before_touching_the_device():
     assert lib.xp_gemm_down(p(16), 32, 12288, p(16), 4096, p(16), None, 32, None, 0, None) == _native.XP_ERROR_CAPACITY
     assert "xp_gemm_workspace_bytes" in _native.last_error()
     # null handles
-    assert lib.xp_layer_register(None, 0, 0, 16, 8, p(16), p(16), None, 1e-6) == _native.XP_ERROR_INVALID_ARGUMENT
+    assert lib.xp_layer_register(None, 0, 0, 16, 8, _native.XP_DTYPE_BF16, p(16), p(16), None, 1e-6) == (
+        _native.XP_ERROR_INVALID_ARGUMENT
+    )
     assert lib.xp_replay(None, 0, 0, 1, p(16), p(16), 1, p(16), None) == _native.XP_ERROR_INVALID_ARGUMENT
     assert lib.xp_dense_workspace_bytes(0, 16, 8) == 0
     with pytest.raises(_native.NativeError) as error:
@@ -419,6 +423,6 @@ def test_transport_entry_points_validate_before_any_device_call():
     assert lib.xp_transport_create(0, 1, capacities, bad_dp, ctypes.byref(handle)) == _native.XP_ERROR_INVALID_ARGUMENT
     assert lib.xp_transport_submit(None, 0, 1, 0, 2, 1, 0, None, 0, 0, None) == _native.XP_ERROR_INVALID_ARGUMENT
     assert lib.xp_transport_evaluate(None, 0, None, None) == _native.XP_ERROR_INVALID_ARGUMENT
-    assert lib.xp_transport_complete(None, 0, None, 0, 0, None) == _native.XP_ERROR_INVALID_ARGUMENT
+    assert lib.xp_transport_complete(None, 0, None, 0, _native.XP_DTYPE_BF16, 0, None) == _native.XP_ERROR_INVALID_ARGUMENT
     assert lib.xp_transport_probe(None, 0, 0, None, 0) == _native.XP_ERROR_INVALID_ARGUMENT
     assert lib.xp_transport_destroy(None) == _native.XP_OK

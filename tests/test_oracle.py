@@ -190,6 +190,71 @@ def test_dense_partial_matches_exact_brute_force_on_reference_test_shape():
     assert torch.equal(c_out.view(torch.int16), reference.view(torch.int16))
 
 
+def _f16_round_float(value: float) -> float:
+    """Round-to-nearest-even to IEEE binary16 (11 significant bits, subnormal spacing 2^-24)."""
+
+    if value == 0 or not math.isfinite(value):
+        return value
+    _, exponent = math.frexp(value)
+    quantum = Fraction(2) ** max(exponent - 11, -24)
+    return float(_round_half_even(Fraction(value) / quantum) * quantum)
+
+
+def test_fp16_payload_stages_match_exact_brute_force():
+    # The fp16 payload (is_supported_payload_dtype, ffn.hpp:83-85) through the same Dense body
+    # (qualification.py:290-314): exact rational projections rounded through fp32 to binary16,
+    # fp32 SiLU*up rounded to binary16, exact down projection rounded to binary16.  The
+    # brute force rounds with its own binary16 rule, so a bf16 rounding point left in the
+    # oracle (8 significant bits instead of 11) fails here.
+    x = o.generate_hidden_states(4, 16, 17).half()
+    w_gate_up, w_down = (w.half() for w in o.dense_layer_weights(hidden_size=16, intermediate_size=8))
+    xs = [[Fraction(float(v)) for v in row] for row in x.float().tolist()]
+    gu = [[Fraction(float(v)) for v in row] for row in w_gate_up.float().tolist()]
+    dn = [[Fraction(float(v)) for v in row] for row in w_down.float().tolist()]
+
+    def to_f16(value: Fraction) -> float:
+        return _f16_round_float(struct.unpack("f", struct.pack("f", float(value)))[0])
+
+    expected = []
+    for row in xs:
+        activated = []
+        for j in range(8):
+            gate = np.float32(to_f16(sum(a * b for a, b in zip(row, gu[2 * j]))))
+            up = np.float32(to_f16(sum(a * b for a, b in zip(row, gu[2 * j + 1]))))
+            silu = np.float32(gate / (np.float32(1) + np.exp(-gate, dtype=np.float32)))
+            activated.append(Fraction(_f16_round_float(float(np.float32(silu * up)))))
+        expected.append([to_f16(sum(h * w for h, w in zip(activated, dn_row))) for dn_row in dn])
+    reference = o.dense_partial_reference(x, w_gate_up, w_down)
+    assert reference.dtype is torch.float16
+    assert reference.float().tolist() == expected
+    assert not torch.equal(reference.float(), o.dense_partial_reference(x.bfloat16(), w_gate_up.bfloat16(),
+                                                                        w_down.bfloat16()).float())
+
+
+def test_fp16_rmsnorm_gather_scatter_keep_the_payload_dtype():
+    x = o.generate_hidden_states(8, 256, 21).half()
+    weight = (1 + 0.1 * torch.randn(256, generator=torch.Generator().manual_seed(22))).half()
+    result = o.rmsnorm(x, weight, 1e-6)
+    assert result.dtype is torch.float16
+    x64 = x.double()
+    brute = (x64 / torch.sqrt((x64 * x64).mean(-1, keepdim=True) + 1e-6) * weight.double()).tolist()
+    rounded = torch.tensor([[_f16_round_float(v) for v in row] for row in brute], dtype=torch.float64)
+    ulp = torch.pow(2.0, torch.floor(torch.log2(rounded.abs().clamp_min(2.0**-14))) - 10)
+    assert bool(((result.double() - rounded).abs() <= ulp).all())
+    # gather / scatter move raw binary16 patterns, NaN payloads included
+    pool = x.clone()
+    pool.view(torch.int16)[3, :4] = torch.tensor([0x7E00, 0x7C01, -1, 0x0001], dtype=torch.int16)
+    slots = np.array([3, 0, 6])
+    gathered = o.gather(pool, slots)
+    assert gathered.dtype is torch.float16
+    assert torch.equal(gathered.view(torch.int16), pool[slots].view(torch.int16))
+    scattered = o.scatter(pool, slots, gathered.flip(0).contiguous())
+    assert scattered.dtype is torch.float16
+    assert torch.equal(scattered[[6, 0, 3]].view(torch.int16), pool[slots].view(torch.int16))
+    with pytest.raises(ValueError):
+        o.scatter(pool, slots, gathered.bfloat16())
+
+
 def test_dense_partial_matches_c_restatement_at_scale():
     x = o.generate_hidden_states(16, 256, 17)
     w_gate_up, w_down, _ = o.generate_layer(256, 384, 18)
