@@ -1898,12 +1898,17 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
     }
   }
   const char *lds_bytes = reinterpret_cast<const char *>(lds);
-  // Three fragment slots: the fragments of k step g live in slot g % 3 and are read two k
-  // steps ahead of their MFMAs, so a wave running alone on its SIMD (its partner blocked on
-  // the barrier or on issuing loads) does not wait on LDS latency.
+  // Fragment slots.  With three, the fragments of k step g live in slot g % 3 and are read
+  // two k steps ahead of their MFMAs, so a wave running alone on its SIMD (its partner
+  // blocked on the barrier or on issuing loads) does not wait on LDS latency.  A wave tile of
+  // 8 or more 32x32 accumulators (the 256 x 256 tiles) has 8 MFMAs (256 cycles) per k step
+  // to cover one k step of read latency, and its accumulators take 128 of the 256 VGPRs two
+  // waves per SIMD leave: it reads one k step ahead from two slots (slot g % 2), which frees
+  // the 24 VGPRs of a third slot (with three it spilled 88 bytes per lane).
   static_assert(KSTEPS == 4, "the slab schedule below is written for four k steps");
-  u32x4 af[3][MT];
-  u32x4 bfrag[3][NT];
+  constexpr int SLOTS = MT * NT >= 8 ? 2 : 3;
+  u32x4 af[SLOTS][MT];
+  u32x4 bfrag[SLOTS][NT];
   // A grouped tile's wave whose rows all lie past the expert's last route reads no
   // fragments and issues no MFMAs (one wave-uniform branch around the unrolled loops).
   auto read_fragments = [&](int stage, int ks, int slot) XP_INLINE {
@@ -1964,7 +1969,9 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
   wait_vmcnt<LOADS * (STAGES - 1)>();
   __syncthreads();
   read_fragments(0, 0, 0);
-  read_fragments(0, 1, 1);
+  if constexpr (SLOTS == 3) {
+    read_fragments(0, 1, 1);
+  }
 
   // Slab kt runs k steps 4 kt .. 4 kt + 3 from stage kt % STAGES, its fragment slots
   // starting at phase kt % 3.  After k step 1 every fragment of the slab has been read, so
@@ -1975,8 +1982,43 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
   // with them every LDS address but one per-lane term per k step, are compile-time
   // constants.  The loading and the other waves run the same loop (the same barriers),
   // with and without the refills, as separate code so that each has a fixed interleave.
-  constexpr int UNROLL = STAGES % 3 == 0 ? STAGES : 3 * STAGES;
+  constexpr int UNROLL = SLOTS == 2 || STAGES % 3 == 0 ? STAGES : 3 * STAGES;
+  // Two slots: k step g's fragments are read while k step g - 1's MFMAs run; the barrier
+  // follows k step 2's MFMAs (every fragment of the slab read by then), and the refill goes
+  // out under k step 3's.
+  auto slab2 = [&](auto index, auto loads, int64_t kt) XP_INLINE {
+    constexpr int S = decltype(index)::value % STAGES;
+    constexpr int NEXT = (S + 1) % STAGES;
+    constexpr bool LOADING = decltype(loads)::value;
+    read_fragments(S, 1, 1);
+    mfma_step(0);
+    __builtin_amdgcn_sched_barrier(0);
+    read_fragments(S, 2, 0);
+    mfma_step(1);
+    __builtin_amdgcn_sched_barrier(0);
+    read_fragments(S, 3, 1);
+    mfma_step(0);
+    stage_barrier();
+    read_fragments(NEXT, 0, 0);
+    if constexpr (LOADING) {
+      issue_part(kt + STAGES, S, std::integral_constant<int, 3>{});
+    }
+    mfma_step(1);
+#pragma unroll
+    for (int i = 0; i < MT * NT; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+      if constexpr (LOADING) {
+        __builtin_amdgcn_sched_group_barrier(0x020, (LOADS + MT * NT - 1) / (MT * NT), 0);  // memory loads
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
   auto slab = [&](auto index, auto loads, int64_t kt) XP_INLINE {
+    if constexpr (SLOTS == 2) {
+      slab2(index, loads, kt);
+      return;
+    }
     constexpr int P = decltype(index)::value % 3;
     constexpr int S = decltype(index)::value % STAGES;
     constexpr int NEXT = (S + 1) % STAGES;
@@ -2044,14 +2086,24 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
   // Last slab (index ktiles - 1): no barrier and no refill.
   static_for<UNROLL>([&](auto j) XP_INLINE {
     if ((ktiles - 1) % UNROLL == decltype(j)::value) {
-      constexpr int P = decltype(j)::value % 3;
       constexpr int S = decltype(j)::value % STAGES;
-      read_fragments(S, 2, (P + 2) % 3);
-      mfma_step(P);
-      read_fragments(S, 3, P);
-      mfma_step((P + 1) % 3);
-      mfma_step((P + 2) % 3);
-      mfma_step(P);
+      if constexpr (SLOTS == 2) {
+        read_fragments(S, 1, 1);
+        mfma_step(0);
+        read_fragments(S, 2, 0);
+        mfma_step(1);
+        read_fragments(S, 3, 1);
+        mfma_step(0);
+        mfma_step(1);
+      } else {
+        constexpr int P = decltype(j)::value % 3;
+        read_fragments(S, 2, (P + 2) % 3);
+        mfma_step(P);
+        read_fragments(S, 3, P);
+        mfma_step((P + 1) % 3);
+        mfma_step((P + 2) % 3);
+        mfma_step(P);
+      }
     }
   });
   // Past-the-end refills may still be landing in the stage buffers the epilogue reuses.
