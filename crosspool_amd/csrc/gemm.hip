@@ -2398,7 +2398,19 @@ constexpr double kReduceLaunchUs = 4.0;
 constexpr double kOverlap = 0.5;              // share of the faster of compute and streaming exposed
 constexpr int64_t kMaxTileSplit = 16;
 
-GemmChoice choose_tile(int64_t capacity, int64_t n, int64_t k) {
+// A column split: the first n1 weight rows on shape `main` in whole rounds of one tile per
+// CU, the other n - n1 on shape `tail` in a second launch, where one shape alone ends in a
+// partial round (Qwen3-32B TP shard at 8192 rows: gate_up 800 tiles of 256 x 256, 3.125
+// rounds).  Taken when the model prices it at least kColumnSplitGain below the best single
+// shape, which keeps the choice away from near ties.
+constexpr double kTailLaunchUs = 3.0;
+constexpr double kColumnSplitGain = 0.05;
+
+double tile_rounds_us(const TileShape &shape, int64_t rounds, int64_t k) {
+  return static_cast<double>(rounds) * 2.0 * shape.bm * shape.bn * static_cast<double>(k) / shape.flops_per_us;
+}
+
+GemmChoice choose_tile(int64_t capacity, int64_t n, int64_t k, bool split_columns) {
   GemmChoice best{GemmKind::Tile, 0, k, 1};
   double best_cost = 0.0;
   for (int index = 0; index < kRankedTileShapes; ++index) {
@@ -2424,7 +2436,40 @@ GemmChoice choose_tile(int64_t capacity, int64_t n, int64_t k) {
       }
     }
   }
-  return best;
+  if (!split_columns) {
+    return best;
+  }
+  const double stream = 2.0 * static_cast<double>(n) * static_cast<double>(k) / kWeightBytesPerUs;
+  GemmChoice split_best = best;
+  double split_cost = best_cost * (1.0 - kColumnSplitGain);
+  // The first launch runs on the 256 x 256 tile, the most efficient shape: with a 256 x 128
+  // first launch the split measured slower than the best single shape (Qwen3-8B gate_up at
+  // 512 rows 177 -> 186 us, the 32B shard's down at 2048 rows 228 -> 234 us per layer).
+  for (int main = 0; main < 1; ++main) {
+    const TileShape &shape = kTileShapes[main];
+    const int64_t token_tiles = (capacity + shape.bm - 1) / shape.bm;
+    for (int64_t weight_tiles = 1; weight_tiles * shape.bn < n; ++weight_tiles) {
+      if ((token_tiles * weight_tiles) % kComputeUnits != 0) {
+        continue;  // the first launch must be whole rounds
+      }
+      const int64_t n1 = weight_tiles * shape.bn;
+      for (int tail = 0; tail < kRankedTileShapes; ++tail) {
+        const TileShape &other = kTileShapes[tail];
+        const int64_t tail_tiles = ((capacity + other.bm - 1) / other.bm) * ((n - n1 + other.bn - 1) / other.bn);
+        const double compute =
+            tile_rounds_us(shape, token_tiles * weight_tiles / kComputeUnits, k) +
+            tile_rounds_us(other, (tail_tiles + kComputeUnits - 1) / kComputeUnits, k) + kTailLaunchUs;
+        const double cost = compute > stream ? compute + kOverlap * stream : stream + kOverlap * compute;
+        if (cost < split_cost) {
+          split_cost = cost;
+          split_best = {GemmKind::Tile, main, k, 1};
+          split_best.tail_variant = tail;
+          split_best.tail_columns = n - n1;
+        }
+      }
+    }
+  }
+  return split_best;
 }
 
 // The resident kernel's K parts and chunks per wave at `capacity` rows (9 to 16), with its
@@ -2490,7 +2535,7 @@ GemmChoice choose_decode(int64_t capacity, int64_t n, int64_t k, double &cost) {
   return split;
 }
 
-GemmChoice choose_gemm(int64_t capacity, int64_t n, int64_t k, bool gated) {
+GemmChoice choose_gemm(int64_t capacity, int64_t n, int64_t k, bool gated, bool split_columns) {
   // 9 to 16 rows: the resident kernel where its model is cheaper than the split / stream
   // choice's.  Measured on MI355X (kernel durations, weights streamed from HBM): the Qwen3-32B
   // TP shard's down at 9 / 16 rows 12.8 / 13.3 us + a 4.0 us reduction (stream, 8 slices)
@@ -2504,14 +2549,15 @@ GemmChoice choose_gemm(int64_t capacity, int64_t n, int64_t k, bool gated) {
     const GemmChoice resident = choose_resident(capacity, n, k, false, resident_us);
     return resident_us >= 0.0 && resident_us < decode_us ? resident : decode;
   }
-  GemmChoice choice = choose_tile(capacity, n, k);
+  GemmChoice choice = choose_tile(capacity, n, k, split_columns);
   // Token tiles more than half full carry twice the MFMA work per weight byte, which the
   // two-wave tile's lower matrix rate turns into a loss once its grid passes the CU count
   // (Qwen3-8B at 64 rows: 81.2 -> 82.7 us per layer; Qwen3-0.6B at 256 rows: 30.1 -> 31.7).
   const TileShape &decode = kTileShapes[kDecodeTile];
   const int64_t decode_tiles = ((capacity + decode.bm - 1) / decode.bm) * ((n + decode.bn - 1) / decode.bn);
   const int64_t weight = capacity > decode.bm / 2 ? 2 : 1;
-  if (gated && choice.variant == kDecodeTile && choice.k_split == 1 && decode_tiles * weight < kComputeUnits) {
+  if (gated && choice.variant == kDecodeTile && choice.k_split == 1 && choice.tail_variant < 0 &&
+      decode_tiles * weight < kComputeUnits) {
     choice.variant = kNarrowDecodeTile;
   }
   return choice;
@@ -2708,11 +2754,33 @@ GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmCho
     // Dynamic LDS beyond 64 KB: launch() opts the function in (enable_large_lds).
     kernel.shmem = static_cast<unsigned>(kStreamTokens * (choice.k_slice + kStreamRowPad) * 2);
   } else {
+    // Tile grid over weight rows [0, n1) (all of them without a column split); the tail
+    // launch takes [n1, n): its weights, and its output columns (half as many for gate_up).
+    const int64_t n1 = args.n - choice.tail_columns;
+    if (choice.tail_columns > 0) {
+      if (choice.k_split != 1 || choice.tail_variant < 0 || n1 <= 0 || (gated && n1 % 2 != 0)) {
+        launches.usable = false;
+        return launches;
+      }
+      record.n = n1;
+      const TileShape &other = kTileShapes[choice.tail_variant];
+      GemmArgs tail_record = record;
+      tail_record.n = choice.tail_columns;
+      tail_record.w = args.w + n1 * args.k;
+      tail_record.out = args.out + (gated ? n1 / 2 : n1);
+      const bool tail_stream = capacity <= other.bm;
+      launches.tail.func = gated ? tile_kernel<true>(choice.tail_variant, tail_stream, args.payload)
+                                 : tile_kernel<false>(choice.tail_variant, tail_stream, args.payload);
+      launches.tail.grid = dim3(static_cast<unsigned>((tail_record.n + other.bn - 1) / other.bn),
+                                static_cast<unsigned>((capacity + other.bm - 1) / other.bm), 1);
+      launches.tail.block = dim3(static_cast<unsigned>(64 * other.waves), 1, 1);
+      launches.tail.set_args(tail_record);
+    }
     const TileShape &shape = kTileShapes[choice.variant];
     const bool stream = capacity <= shape.bm;
     kernel.func = gated ? tile_kernel<true>(choice.variant, stream, args.payload)
                         : tile_kernel<false>(choice.variant, stream, args.payload);
-    kernel.grid = dim3(static_cast<unsigned>((args.n + shape.bn - 1) / shape.bn),
+    kernel.grid = dim3(static_cast<unsigned>((n1 + shape.bn - 1) / shape.bn),
                        static_cast<unsigned>((capacity + shape.bm - 1) / shape.bm),
                        static_cast<unsigned>(choice.k_split));
     kernel.block = dim3(static_cast<unsigned>(64 * shape.waves), 1, 1);
@@ -2816,6 +2884,10 @@ std::string gemm_name(GemmChoice choice, bool gated) {
   std::string name = "tile" + prefix + "_" + std::to_string(shape.bm) + "x" + std::to_string(shape.bn);
   if (choice.k_split > 1) {
     name += "_k" + std::to_string(choice.k_split);
+  }
+  if (choice.tail_columns > 0) {
+    const TileShape &other = kTileShapes[choice.tail_variant];
+    name += "+" + std::to_string(other.bm) + "x" + std::to_string(other.bn) + "_n" + std::to_string(choice.tail_columns);
   }
   return name;
 }

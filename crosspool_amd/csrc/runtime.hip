@@ -139,7 +139,8 @@ struct DenseLaunches {
 
   int chain(const KernelLaunch **out) const {
     int count = 0;
-    for (const KernelLaunch *kernel : {&gather, &gate_up.main, &gate_up.reduce, &down.main, &down.reduce}) {
+    for (const KernelLaunch *kernel :
+         {&gather, &gate_up.main, &gate_up.reduce, &gate_up.tail, &down.main, &down.reduce, &down.tail}) {
       if (!kernel->empty()) {
         out[count++] = kernel;
       }
@@ -147,9 +148,9 @@ struct DenseLaunches {
     return count;
   }
 };
-constexpr int kMaxStepKernels = 5;
+constexpr int kMaxStepKernels = 7;
 
-// The kernels of one template's step in launch order (a Dense step has at most 5; a MoE
+// The kernels of one template's step in launch order (a Dense step has at most 7; a MoE
 // step at most 9: gather, Router projection and its reduction, TopK, finalisation, sort,
 // gate_up, down, combine).
 constexpr int kMaxTemplateKernels = 9;
@@ -268,6 +269,7 @@ int launch_gemm(const GemmLaunch &kernels, hipStream_t stream) {
   }
   XP_HIP_CHECK(launch(kernels.main, stream));
   XP_HIP_CHECK(launch(kernels.reduce, stream));
+  XP_HIP_CHECK(launch(kernels.tail, stream));
   return XP_OK;
 }
 
@@ -424,7 +426,7 @@ RouterWorkspace router_workspace(int64_t rows, int64_t hidden, int64_t experts, 
   layout.logits = 0;
   layout.scratch = align_up(static_cast<size_t>(rows * experts) * (payload ? 2 : 4), 256);
   layout.scratch_bytes = router_uses_mfma(hidden, experts, precision)
-                             ? gemm_scratch_bytes(choose_gemm(rows, experts, hidden, false), rows, experts, hidden)
+                             ? gemm_scratch_bytes(choose_gemm(rows, experts, hidden, false, false), rows, experts, hidden)
                              : 0;
   layout.bytes = layout.scratch + layout.scratch_bytes;
   return layout;
@@ -529,8 +531,9 @@ RouterLaunches make_router_launches(const RouterBinding &b, int64_t capacity) {
     args.n = b.experts;
     args.k = b.hidden;
     args.act = default_activation();
-    const GemmLaunch gemm =
-        make_gemm(args, capacity, false, choose_gemm(capacity, b.experts, b.hidden, false), b.fused_gather);
+    // (no column split: the Router's launch list has room for one projection kernel)
+    const GemmLaunch gemm = make_gemm(args, capacity, false,
+                                      choose_gemm(capacity, b.experts, b.hidden, false, false), b.fused_gather);
     launches.logits = gemm.main;
     launches.logits_reduce = gemm.reduce;
   } else {

@@ -382,9 +382,15 @@ struct GemmChoice {
   int64_t k_slice;  // K columns per range
   int64_t k_split;  // split kernel: K ranges per weight-row block; tile kernel: K ranges
                     // (grid z); 1 for the stream kernel, whose ranges follow from k_slice
+  // Tile kernel without a K split only: the last tail_columns weight rows (output columns)
+  // go to a second launch on tile shape tail_variant, so that the first launch's grid is
+  // whole rounds of one tile per CU and the second fills what would be a partial round.
+  int tail_variant = -1;
+  int64_t tail_columns = 0;
 };
 
-GemmChoice choose_gemm(int64_t capacity, int64_t n, int64_t k, bool gated);
+// `split_columns`: the caller launches GemmLaunch::tail, so a tile choice may split columns.
+GemmChoice choose_gemm(int64_t capacity, int64_t n, int64_t k, bool gated, bool split_columns = true);
 // The gate_up of a Dense step: at decode sizes the stream kernel with the mailbox gather
 // fused (`fused` set), otherwise choose_gemm's kernel after a separate gather.
 GemmChoice choose_dense_gate_up(int64_t capacity, int64_t n, int64_t k, bool &fused);
@@ -402,6 +408,7 @@ size_t gemm_scratch_bytes(GemmChoice choice, int64_t capacity, int64_t n, int64_
 struct GemmLaunch {
   KernelLaunch main;
   KernelLaunch reduce;
+  KernelLaunch tail;   // the trailing columns of a column-split tile choice (empty otherwise)
   bool usable = true;  // false: the choice names no launchable kernel (callers fail the call)
 };
 // `fused_gather`: the gate_up of a Dense step whose choose_dense_gate_up decision fused the

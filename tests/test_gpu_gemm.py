@@ -157,12 +157,14 @@ def test_variant_selection_covers_every_family(device):
     assert _native.gemm_variant(64, 24576, 4096, True) == "tile_gated_64x128"
     assert _native.gemm_variant(17, 6144, 1024, True) == "tile_gated_64x128_k4"
     # The headline sizes of tests/test_gpu_headline.py (config 3 at 1024 / 2048 / 4096 rows,
-    # config 5 at 512 / 8192) reach the unsplit tiles and the split 256 x 256 down tile.
+    # config 5 at 512 / 8192) reach the unsplit tiles, the K-split 256 x 256 down tile and
+    # the column splits (a second launch for the trailing columns).
     headline = {_native.gemm_variant(rows, n, k, gated) for (hidden, intermediate), sizes in
                 (((4096, 12288), (1024, 2048, 4096)), ((5120, 3200), (512, 8192))) for rows in sizes
                 for n, k, gated in ((2 * intermediate, hidden, True), (hidden, intermediate, False))}
     assert {"tile_256x128", "tile_128x128", "tile_256x256", "tile_256x256_k4", "tile_gated_128x128",
-            "tile_gated_256x128", "tile_gated_256x256"} <= headline
+            "tile_gated_256x256", "tile_gated_256x256+256x128_n8192", "tile_gated_256x256+64x128_n256",
+            "tile_256x256+256x128_n1024"} <= headline
 
 
 # Ragged geometries of the decode kernels: K not a multiple of their 512-column load
@@ -235,6 +237,34 @@ def test_resident_projections(device, rows, hidden, intermediate, projection, va
         torch.cuda.synchronize()
         assert_projection_within_bounds(out, x_rows, w_down)
     assert_bitwise_equal(again.cpu(), out.cpu())
+
+
+@pytest.mark.parametrize(
+    "n,k,gate_up_variant,down_variant",
+    [
+        (2304, 512, "tile_gated_256x256+64x128_n256", "tile_256x256+64x128_n256"),
+        # The second launch's 128 columns are half a 256-wide weight tile of the first shape.
+        (2176, 320, "tile_gated_256x256+64x128_n128", "tile_256x256+64x128_n128"),
+    ],
+)
+def test_column_split_projections(device, n, k, gate_up_variant, down_variant):
+    # 8192 rows: 32 token tiles, so the first 2048 weight rows on 256 x 256 tiles are exactly
+    # one round of 256 workgroups and the remaining columns go to a second launch on smaller
+    # tiles (its weights, and its output columns: half as many for gate_up).
+    rows = 8192
+    print(f"column split n={n} k={k}", flush=True)
+    assert _native.gemm_variant(rows, n, k, True) == gate_up_variant
+    assert _native.gemm_variant(rows, n, k, False) == down_variant
+    assert _native.gemm_workspace_bytes(rows, n, k, True) == 0 and _native.gemm_workspace_bytes(rows, n, k, False) == 0
+    x_rows = o.generate_hidden_states(rows, k, 71)
+    w_gate_up, _ = _layer(k, n // 2, 72)
+    _, w_down = _layer(n, k, 73)
+    x = to_device(x_rows, device)
+    activated = dense.gate_up_silu(x, to_device(w_gate_up, device))
+    out = dense.down(x, to_device(w_down, device))
+    torch.cuda.synchronize()
+    assert_activated_within_bounds(activated, x_rows, w_gate_up)
+    assert_projection_within_bounds(out, x_rows, w_down)
 
 
 @pytest.mark.parametrize("rows", [1, 16, 128])

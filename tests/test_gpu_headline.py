@@ -47,11 +47,12 @@ QWEN3_32B_SHARD = (5120, 3200)
 
 # (hidden, intermediate, rows, pool rows, normed, gate_up variant, down variant)
 CASES = [
-    pytest.param(*QWEN3_8B, 1024, 8192, True, "tile_gated_256x128", "tile_256x256_k4", id="config3-T1024"),
+    pytest.param(*QWEN3_8B, 1024, 8192, True, "tile_gated_256x256+256x128_n8192", "tile_256x256_k4", id="config3-T1024"),
     pytest.param(*QWEN3_8B, 2048, 8192, True, "tile_gated_256x256", "tile_256x128", id="config3-T2048"),
     pytest.param(*QWEN3_8B, 4096, 8192, True, "tile_gated_256x256", "tile_256x256", id="config3-T4096"),
     pytest.param(*QWEN3_32B_SHARD, 512, 8192, False, "tile_gated_128x128", "tile_128x128", id="config5-T512"),
-    pytest.param(*QWEN3_32B_SHARD, 8192, 8192, False, "tile_gated_256x256", "tile_256x128", id="config5-T8192"),
+    pytest.param(*QWEN3_32B_SHARD, 8192, 8192, False, "tile_gated_256x256+64x128_n256", "tile_256x256+256x128_n1024",
+                 id="config5-T8192"),
 ]
 
 

@@ -404,6 +404,28 @@ def test_k_split_tiles_fill_the_chip_and_size_their_partials():
     assert "_k" not in _native.gemm_variant(300, 128, 64, False)
 
 
+def test_column_split_fills_the_last_round():
+    # Qwen3-32B TP shard at 8192 rows: 32 token tiles x 25 weight tiles of 256 x 256 would be
+    # 3.125 rounds of one tile per CU.  The first 24 weight tiles (768 tiles, 3 whole rounds)
+    # stay on 256 x 256 and the last 256 weight rows go to a second launch of 64 x 128 tiles
+    # (256 tiles: one more round of small tiles instead of a round one eighth full).
+    name = _native.gemm_variant(8192, 6400, 5120, True)
+    assert name == "tile_gated_256x256+64x128_n256"
+    main_weight_tiles = (6400 - 256) // 256
+    assert (8192 // 256) * main_weight_tiles % 256 == 0
+    assert (8192 // 64) * (256 // 128) == 256
+    # no K split in either launch: no scratch
+    assert _native.gemm_workspace_bytes(8192, 6400, 5120, True) == 0
+    # Whole rounds already: one shape.
+    assert "+" not in _native.gemm_variant(2048, 24576, 4096, True)
+    assert "+" not in _native.gemm_variant(4096, 4096, 12288, False)
+    # The first launch is always the 256 x 256 tile (a 256 x 128 first launch measured slower).
+    for rows, n, k in ((512, 24576, 4096), (2048, 5120, 3200), (512, 19456, 2560)):
+        for gated in (True, False):
+            name = _native.gemm_variant(rows, n, k, gated)
+            assert "+" not in name or "_256x256+" in name
+
+
 def test_ffn_shim_requires_an_attachment():
     from crosspool_amd.ops import ffn_shim
 
