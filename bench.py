@@ -13,14 +13,16 @@ baseline (the oracle's torch-CPU restatement on the host cores).
 
 ``--kernels-only`` instead launches just the kernels whose hardware counters
 the roofline's ``traffic`` figure comes from (a byte copy of known size for
-calibration, then gate_up at the headline and decode sizes), for
-``rocprofv3 --pmc`` runs; ``profiles/traffic.json`` records their result.
+calibration, then gate_up at the headline and decode sizes), and layer replays
+at 16 rows and one row, for ``rocprofv3 --pmc`` runs; ``profiles/traffic.json``
+records their result.
 
 ``--ceilings`` instead measures the hardware limits the kernels are judged
 against (libxpool_probes.so): a pure-MFMA loop, two HBM read patterns, the
-GPU idle time a hipGraphLaunch adds per replay, and the cost of a grid-wide
-dependency (a kernel boundary against an in-kernel counter handoff), and prints
-them as one JSON line.
+GPU idle time a hipGraphLaunch adds per replay, the cost of a grid-wide
+dependency (a kernel boundary against an in-kernel counter handoff), and
+torch.matmul (hipBLASLt) on the headline's two product shapes, and prints them
+as one JSON line.
 """
 
 from __future__ import annotations
@@ -289,6 +291,22 @@ def run_ceilings(device) -> dict:
         handoff.append(point)
     torch.cuda.synchronize(device)
     result["handoff"] = {"points": handoff, "flag": int(flag.item())}
+
+    # The library GEMM on the headline shapes: torch.matmul (hipBLASLt) of bf16 [2048, 4096] x
+    # [4096, 24576] (gate_up's product, bf16 output of all 2I columns, no activation) and
+    # [2048, 12288] x [12288, 4096] (down's), N(0, 1) activations and N(0, 0.02) weights as
+    # in the headline, timed back to back.
+    library = []
+    for name, m, k, n in (("gate_up_shape", 2048, HIDDEN, 2 * INTERMEDIATE), ("down_shape", 2048, INTERMEDIATE, HIDDEN)):
+        a = torch.randn((m, k), device=device, generator=generator).bfloat16()
+        b = (torch.randn((n, k), device=device, generator=generator) * 0.02).bfloat16()
+        out = torch.empty((m, n), dtype=torch.bfloat16, device=device)
+        bt = b.t()
+        seconds = per_launch(lambda index=0: torch.matmul(a, bt, out=out), 20)
+        library.append({"product": name, "m": m, "k": k, "n": n, "us": round(seconds * 1e6, 1),
+                        "tflops": round(2.0 * m * n * k / seconds / 1e12, 1)})
+        del a, b, out, bt
+    result["hipblaslt_matmul"] = library
     return result
 
 
@@ -415,12 +433,19 @@ def main() -> int:
         target = torch.empty_like(source)
         for _ in range(5):
             dense.copy_bytes(target, source, stream=lane.stream)
+        # gate_up at the headline and decode sizes (the roofline's traffic), then whole layer
+        # replays at 16 rows and one row, whose gate_up kernels (the resident kernel, the
+        # persistent split kernel, both with the gather fused) exist only in a Dense step
         for t in (tokens, args.decode_tokens):
             gate_up_launches(t, 6)
+        for t in (16, 1):
+            for step in range(6):
+                replay(t, step % 2)
         torch.cuda.synchronize()
         agent.close()
         print(json.dumps({"kernels_only": True, "copy_bytes": CALIBRATION_COPY_BYTES,
-                          "gate_up_tokens": [tokens, args.decode_tokens]}), flush=True)
+                          "gate_up_tokens": [tokens, args.decode_tokens], "layer_replay_tokens": [16, 1]}),
+              flush=True)
         return 0
 
     # ---------------------------------------------------------------- headline

@@ -8,9 +8,9 @@
 // instantiated hipGraphExec per signature, built from explicit kernel nodes;
 // the host selects the layer and the smallest capacity that holds the live rows
 // (the rule of runtime.cu:246-253).  A replay either launches the template's kernel
-// nodes directly on the stream (the default: a hipGraphLaunch adds 6-9 us of GPU time
-// per replay on this runtime, direct launches none) or rebinds the nodes' argument
-// records with hipGraphExecKernelNodeSetParams and launches the graph.
+// nodes directly on the stream (the default: a hipGraphLaunch adds about 4-5 us of GPU
+// time per Dense replay at decode sizes on MI355X, direct launches none) or rebinds the
+// nodes' argument records with hipGraphExecKernelNodeSetParams and launches the graph.
 
 #include <algorithm>
 #include <cmath>
@@ -339,8 +339,9 @@ struct xp_lane {
   std::mutex mutex;
   std::vector<std::unique_ptr<Template>> templates;  // sorted by (hidden, intermediate, capacity)
   // Replays launch the template's kernels directly on the stream unless graph dispatch is
-  // selected: on this runtime each hipGraphLaunch adds 6-9 us of GPU time before the
-  // graph's first kernel, while back-to-back kernel launches leave no gap.
+  // selected: each hipGraphLaunch adds GPU time before the graph's first kernel (about
+  // 4-5 us per Dense replay at decode sizes on MI355X), while back-to-back kernel launches
+  // leave no gap.
   bool graph_dispatch = false;
 };
 

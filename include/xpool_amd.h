@@ -249,8 +249,9 @@ int xp_lane_synchronize(xp_lane_t lane);
 /* Replay dispatch of this Lane: 0 (default) launches a template's kernels directly on the
  * stream, nonzero launches its instantiated hipGraph (rebinding only the kernel nodes whose
  * arguments changed).  Both run the same kernels with the same arguments.  No counterpart
- * in the reference, whose CUDA graphs are always launched (runtime.cu:701-1006); on this
- * runtime a hipGraphLaunch adds ~9 us of GPU time per replay (measured, Qwen3-0.6B layer). */
+ * in the reference, whose CUDA graphs are always launched (runtime.cu:701-1006); on MI355X a
+ * hipGraphLaunch adds about 4-5 us of GPU time per Dense replay at decode sizes (measured on
+ * the Qwen3-8B layer at 1 and 32 rows). */
 int xp_lane_set_graph_dispatch(xp_lane_t lane, int use_graph);
 
 /* GraphTemplate: build and instantiate this Lane's hipGraph for the Execution
