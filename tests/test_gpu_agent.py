@@ -14,7 +14,7 @@ import pytest
 import torch
 
 from crosspool_amd import _native
-from crosspool_amd.agent import FfnAgent, FfnHealthError
+from crosspool_amd.agent import FfnAgent, FfnHealthError, derive_payload_row_capacities
 from crosspool_amd.ffn import DpRowLayout, ForwardMode, OutputRequirement
 from crosspool_amd.ops import attach, detach, ffn_shim
 from crosspool_amd.transport import FfnRequestMetadata
@@ -445,6 +445,42 @@ def test_two_models_on_two_lanes(device):
         agent.check_health()
     for instance, (w_gate_up, w_down, norm_weight) in layers.items():
         _check_mailbox(pools_gpu[instance], pools[instance], chosen[instance], w_gate_up, w_down, norm_weight)
+
+
+@pytest.mark.parametrize("instance", [0, 1], ids=["qwen3-1.7b", "qwen3-4b"])
+def test_two_models_every_capacity_bucket(device, instance):
+    # BASELINE config 4 as the bench runs it (ragged 1..512 rows per model per step, both
+    # Lanes busy): every capacity bucket up to 512, at its largest and its smallest row count,
+    # so each template and kernel choice the bench replays is checked against the oracle on
+    # the config's own shapes.  The other model's Lane replays between the steps.
+    shapes = {0: (2048, 6144), 1: (2560, 9728)}
+    hidden, intermediate = shapes[instance]
+    generator = np.random.default_rng(11 + instance)
+    rows_list = sorted({r for c in derive_payload_row_capacities(512) for r in (c, c // 2 + 1)})
+    with FfnAgent(device, executor_lane_count=2) as agent:
+        layers = {}
+        for index, (h, i) in shapes.items():
+            w_gate_up, w_down, norm_weight = o.generate_layer(h, i, 210 + index)
+            layers[index] = (w_gate_up, w_down, norm_weight)
+            agent.register_layer(instance_index=index, layer_ordinal=0, weights=_weights(w_gate_up, w_down, device),
+                                 norm_weight=to_device(norm_weight, device))
+        agent.materialize(maximum_row_capacity=512)
+        other = 1 - instance
+        other_pool = to_device(o.generate_hidden_states(1024, shapes[other][0], 50 + other), device)
+        pool = o.generate_hidden_states(1024, hidden, 50 + instance)
+        pool_gpu = to_device(pool, device)
+        w_gate_up, w_down, norm_weight = layers[instance]
+        for rows in rows_list:
+            print(f"config4 instance={instance} rows={rows} gate_up={_native.dense_gate_up_variant(rows, hidden, intermediate)}",
+                  flush=True)
+            slots = generator.permutation(1024)[:rows].astype(np.int32)
+            before = pool_gpu.cpu()
+            agent.execute(instance_index=instance, layer_ordinal=0, pool=pool_gpu, slots=slots_tensor(slots, device),
+                          lane=instance)
+            other_slots = slots_tensor(generator.permutation(1024)[:int(generator.integers(1, 513))], device)
+            agent.execute(instance_index=other, layer_ordinal=0, pool=other_pool, slots=other_slots, lane=other)
+            agent.check_health()
+            _check_mailbox(pool_gpu, before, slots, w_gate_up, w_down, norm_weight)
 
 
 @pytest.mark.parametrize(
