@@ -2796,31 +2796,63 @@ GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmCho
   return launches;
 }
 
-// Grouped projections run on the 256 x 128 tile.  An expert sees ~T K / E rows (Qwen3-MoE:
-// 128 at 2048 tokens), far below the MFMA ridge, so the projections are bound by streaming
-// each expert's weights: a tile tall enough to hold all of an expert's rows streams them
-// once, where 128-row tiles split about half the experts over two tiles and read their
-// weights twice (Qwen3-30B-A3B at 2048 tokens: down 297 us on 128-row tiles).
-constexpr int kGroupedTileVariant = 1;
+// Grouped projections run on the tile kernel's grouped instantiations, one per expert
+// tile height (choose_moe_tile picks it by routes per expert): 64 x 256 (four stages),
+// 128 x 256 (three stages, nontemporal or plain weight loads) and 256 x 128 (three stages,
+// nontemporal).  Each keeps 144-160 KB of LDS, one workgroup per CU; the shorter the token
+// rows of a tile, the more of that LDS holds weight slabs in flight.  The nontemporal hint
+// suits tiles whose expert's weights no other tile reads; with plain loads an expert split
+// over two 128-row tiles reads its weights from the last-level cache the second time.
+struct GroupedTile {
+  int bm;
+  int bn;
+  int waves;
+};
 
-int grouped_tile_rows() { return kTileShapes[kGroupedTileVariant].bm; }
+GroupedTile grouped_tile(MoeTile tile) {
+  switch (tile) {
+    case MoeTile::Rows64:
+      return {64, 256, 8};
+    case MoeTile::Rows128Stream:
+    case MoeTile::Rows128:
+      return {128, 256, 8};
+    case MoeTile::Rows256:
+      return {256, 128, 8};
+    default:
+      return {0, 0, 0};
+  }
+}
 
-KernelLaunch make_grouped_gemm(const GemmArgs &args, bool gated, int max_tiles) {
-  const TileShape &shape = kTileShapes[kGroupedTileVariant];
-  if (max_tiles % 8 != 0) {
+template <bool GATED>
+const void *grouped_tile_kernel(MoeTile tile) {
+  switch (tile) {
+    case MoeTile::Rows64:
+      return reinterpret_cast<const void *>(&tile_gemm_kernel<64, 256, 2, 4, 4, GATED, true, true>);
+    case MoeTile::Rows128Stream:
+      return reinterpret_cast<const void *>(&tile_gemm_kernel<128, 256, 2, 4, 3, GATED, true, true>);
+    case MoeTile::Rows128:
+      return reinterpret_cast<const void *>(&tile_gemm_kernel<128, 256, 2, 4, 3, GATED, true, false>);
+    case MoeTile::Rows256:
+      return reinterpret_cast<const void *>(&tile_gemm_kernel<256, 128, 4, 2, 3, GATED, true, true>);
+    default:
+      return nullptr;
+  }
+}
+
+int grouped_tile_rows(MoeTile tile) { return grouped_tile(tile).bm; }
+
+KernelLaunch make_grouped_gemm(const GemmArgs &args, bool gated, int max_tiles, MoeTile tile) {
+  const GroupedTile shape = grouped_tile(tile);
+  const void *func = gated ? grouped_tile_kernel<true>(tile) : grouped_tile_kernel<false>(tile);
+  if (max_tiles % 8 != 0 || func == nullptr) {
     return KernelLaunch{};  // grouped_tile_coordinates needs a multiple of 8 (callers pad)
   }
   GemmArgs record = args;
   record.k_slice = args.k;
   record.k_split = 1;
   record.partials = nullptr;
-  static_assert(kTileShapes[kGroupedTileVariant].bm == 256 && kTileShapes[kGroupedTileVariant].bn == 128,
-                "the grouped instantiations below are the 256 x 128 tile");
-  // Grouped instantiations load their weights with the nontemporal hint: an expert's
-  // weights are read by its own tiles only (one tile for up to 256 routes).
   KernelLaunch kernel;
-  kernel.func = gated ? reinterpret_cast<const void *>(&tile_gemm_kernel<256, 128, 4, 2, 3, true, true>)
-                      : reinterpret_cast<const void *>(&tile_gemm_kernel<256, 128, 4, 2, 3, false, true>);
+  kernel.func = func;
   kernel.grid = dim3(static_cast<unsigned>((args.n + shape.bn - 1) / shape.bn), static_cast<unsigned>(max_tiles), 1);
   kernel.block = dim3(static_cast<unsigned>(64 * shape.waves), 1, 1);
   kernel.set_args(record);

@@ -450,16 +450,33 @@ unsigned blocks_for(int64_t items, int64_t per_block) {
 
 }  // namespace
 
-int moe_tile_rows(MoeTile tile) { return tile == MoeTile::Small ? grouped_split_rows() : grouped_tile_rows(); }
+int moe_tile_rows(MoeTile tile) { return tile == MoeTile::Small ? grouped_split_rows() : grouped_tile_rows(tile); }
 
-// Few routes per expert (at most 8 on average) stream each expert's weights through the
-// grouped split kernel in 16-route tiles; more take the grouped 256 x 128 tiles, which
-// stream an expert's weights once for up to 256 routes.  Measured at the Qwen3-30B-A3B
-// shape (128 experts, top-8): 128 tokens 267 us on 16-route tiles; 256 tokens 388 us on
-// 16-route tiles (experts past 16 routes stream their weights twice) against about 340 us
-// on the grouped tiles.
+// Few routes per expert (at most 4 on average) stream each expert's weights through the
+// grouped split kernel in 16-route tiles; more take the grouped tile kernel on the shortest
+// expert tile that holds most experts' routes.  An expert's weights are read once per tile
+// of its routes, and the LDS a tile's token rows do not take holds weight slabs in flight
+// (the grouped projections are bound by the weight bytes each CU has in flight), so:
+// 64-row tiles (four stages, 80 % of the LDS for weights) up to 40 routes per expert on
+// average, 128-row tiles with the weights loaded nontemporally up to 80, 128-row tiles with
+// plain loads (an expert split over two tiles finds its weights in the last-level cache
+// for the second) up to 160, 256-row tiles above.  Measured at the Qwen3-30B-A3B shape
+// (128 experts, top-8), layer us against the 256-row tile everywhere: 256 tokens 335 -> 288,
+// 512 357 -> 304, 1024 391 -> 332, 2048 431 -> 418, 4096 unchanged (647 against 652 on
+// 128-row tiles); 128 tokens (8 routes per expert) 298 us on 16-route tiles -> 279 on 64-row
+// tiles, while at 48 / 64 tokens (3 / 4 routes per expert) the 64-row tiles lost (254 / 263
+// -> 263 / 270 us).
 MoeTile choose_moe_tile(int64_t routes, int64_t experts) {
-  return routes <= 8 * experts ? MoeTile::Small : MoeTile::Large;
+  if (routes <= 4 * experts) {
+    return MoeTile::Small;
+  }
+  if (routes <= 40 * experts) {
+    return MoeTile::Rows64;
+  }
+  if (routes <= 80 * experts) {
+    return MoeTile::Rows128Stream;
+  }
+  return routes <= 160 * experts ? MoeTile::Rows128 : MoeTile::Rows256;
 }
 
 KernelLaunch make_router_topk(const RouterTopkArgs &args) {

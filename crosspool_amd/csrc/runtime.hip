@@ -671,13 +671,14 @@ int make_experts_launches(const ExpertsBinding &b, int64_t capacity, ExpertsLaun
   dn.k = b.intermediate;
   dn.act = default_activation();
 
-  if (tile == MoeTile::Large) {
-    // Many routes per expert: the Dense tile kernel in its grouped mode.
-    if (moe_tile_rows(MoeTile::Large) != grouped_tile_rows()) {
-      return fail(XP_ERROR_STATE, "expert tile table and grouped tile kernel disagree on the tile rows");
+  if (tile != MoeTile::Small) {
+    // Many routes per expert: the Dense tile kernel in its grouped mode, on expert tiles of
+    // moe_tile_rows(tile) rows (the table the sort builds).
+    out.gate_up = make_grouped_gemm(up, true, max_tiles, tile);
+    out.down = make_grouped_gemm(dn, false, max_tiles, tile);
+    if (out.gate_up.empty() || out.down.empty()) {
+      return fail(XP_ERROR_STATE, "no grouped tile kernel for this expert tile table");
     }
-    out.gate_up = make_grouped_gemm(up, true, max_tiles);
-    out.down = make_grouped_gemm(dn, false, max_tiles);
   } else {
     // Few routes per expert: each touched expert's weights streamed by the grouped split
     // kernel; about one tile per touched expert.

@@ -252,8 +252,9 @@ struct MoeCombineArgs {
 };
 
 // Expert tiles of the grouped projections: Small (16 sorted positions, grouped split
-// kernel) for few routes per expert, Large (grouped tile kernel) otherwise.
-enum class MoeTile : int { Small = 0, Large = 1 };
+// kernel) for few routes per expert, otherwise the grouped tile kernel on 64-, 128- or
+// 256-row expert tiles (Rows128Stream: 128 rows with the weights loaded nontemporally).
+enum class MoeTile : int { Small = 0, Rows64 = 1, Rows128Stream = 2, Rows128 = 3, Rows256 = 4 };
 int moe_tile_rows(MoeTile tile);
 MoeTile choose_moe_tile(int64_t routes, int64_t experts);
 
@@ -418,10 +419,10 @@ struct GemmLaunch {
 GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmChoice choice,
                      bool fused_gather = false);
 // The grouped projection over an expert tile table of `max_tiles` entries (a multiple of
-// 8; otherwise an empty launch), on the tile kernel whose BM is grouped_tile_rows() (the
-// table must be built for that BM).
-KernelLaunch make_grouped_gemm(const GemmArgs &args, bool gated, int max_tiles);
-int grouped_tile_rows();
+// 8; otherwise an empty launch), on the grouped tile kernel for `tile` (not Small), whose BM
+// is grouped_tile_rows(tile) (the table must be built for that BM).
+KernelLaunch make_grouped_gemm(const GemmArgs &args, bool gated, int max_tiles, MoeTile tile);
+int grouped_tile_rows(MoeTile tile);
 // The grouped projection for few routes per expert, on the grouped split kernel: tiles of
 // grouped_split_rows() sorted positions, `live_tiles` the expected number of table entries
 // in use (it sizes the K split).
