@@ -49,11 +49,21 @@ __device__ __forceinline__ uint32_t ordered_bits(float value) {
 }
 
 // ------------------------------------------------------------------ router
-// One wavefront per row; lane l holds experts l, l + 64, ... (up to 16 each).
-constexpr int kTopkPerLane = kMoeMaxExperts / kWave;
+// One wavefront per row; lane l holds experts l, l + 64, ... (PER_LANE each: the fewest of
+// 2, 4, 8 or 16 that cover the expert count, so a 128-expert Router selects over two
+// values per lane rather than sixteen).  Experts past the count are padding: a score of 0,
+// which adds exactly nothing to the softmax sum, and a key of 0, which never wins, so the
+// choice of PER_LANE changes no bit of the result.
+constexpr int kTopkMaxPerLane = kMoeMaxExperts / kWave;
 
-// TopK of row `row` by the calling wavefront (all 64 lanes).
+__host__ __device__ constexpr int topk_per_lane(int experts) {
+  return experts <= 2 * kWave ? 2 : experts <= 4 * kWave ? 4 : experts <= 8 * kWave ? 8 : kTopkMaxPerLane;
+}
+
+// TopK of row `row` by the calling wavefront (all 64 lanes); experts <= PER_LANE * 64.
+template <int PER_LANE>
 __device__ void router_topk_row(const RouterTopkArgs &a, int64_t row, int lane) {
+  constexpr int kTopkPerLane = PER_LANE;
   const int experts = a.experts;
   float logit[kTopkPerLane];
   float maximum = kNegativeInfinity;
@@ -153,10 +163,11 @@ __device__ void router_topk_row(const RouterTopkArgs &a, int64_t row, int lane) 
   }
 }
 
+template <int PER_LANE>
 __global__ __launch_bounds__(256) void router_topk_kernel(RouterTopkArgs a) {
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (row < a.rows) {
-    router_topk_row(a, row, threadIdx.x & (kWave - 1));
+    router_topk_row<PER_LANE>(a, row, threadIdx.x & (kWave - 1));
   }
 }
 
@@ -281,6 +292,11 @@ __device__ int block_inclusive_scan(int value, int *wave_totals) {
 // Routes held in registers per thread between the count and the placement (16384 routes,
 // 2048 rows at top-8, in one pass; more are read again).
 constexpr int kSortRoutesPerThread = 16;
+// Up to this many routes the placement goes to LDS first and leaves in contiguous stores:
+// placed straight into global memory, each route is a 4-byte store to its own cache line,
+// and one CU's memory path takes those a few lanes per cycle (2048 rows at top-8: 32768
+// such stores, most of the kernel's time).
+constexpr int kSortStagedRoutes = 1024 * kSortRoutesPerThread;
 
 // The fused TopK gives each of the workgroup's waves one row.
 static_assert(kMoeFusedTopkRows <= 1024 / kWave, "one wave of moe_sort_kernel per fused TopK row");
@@ -290,12 +306,23 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(MoeSortArgs a) {
   __shared__ int offsets[kMoeMaxExperts + 1];
   __shared__ int tiles[kMoeMaxExperts + 1];
   __shared__ int totals[1024 / kWave];
+  __shared__ int32_t staged_route[kSortStagedRoutes];
+  __shared__ float staged_weight[kSortStagedRoutes];
   const int tid = threadIdx.x;
   if (a.fused_topk != 0) {
     // Decode sizes: the Router's TopK runs here, one wave per row (the same code as
     // router_topk_kernel), and the routes it writes are read back below by this workgroup.
     if ((tid >> 6) < a.topk.rows) {
-      router_topk_row(a.topk, tid >> 6, tid & (kWave - 1));
+      const int per_lane = topk_per_lane(a.topk.experts);
+      if (per_lane == 2) {
+        router_topk_row<2>(a.topk, tid >> 6, tid & (kWave - 1));
+      } else if (per_lane == 4) {
+        router_topk_row<4>(a.topk, tid >> 6, tid & (kWave - 1));
+      } else if (per_lane == 8) {
+        router_topk_row<8>(a.topk, tid >> 6, tid & (kWave - 1));
+      } else {
+        router_topk_row<kTopkMaxPerLane>(a.topk, tid >> 6, tid & (kWave - 1));
+      }
     }
     __syncthreads();
   }
@@ -359,13 +386,28 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(MoeSortArgs a) {
     a.tile_row0[tile] = offsets[low] + (tile - tiles[low]) * a.tile_rows;
   }
   __syncthreads();
+  const bool staged = a.routes <= kSortStagedRoutes;  // uniform over the workgroup
 #pragma unroll
   for (int i = 0; i < kSortRoutesPerThread; ++i) {
     if (held_expert[i] >= 0 && held_expert[i] < a.experts) {
       const int position = atomicAdd(&counts[held_expert[i]], 1);
-      a.sorted_route[position] = static_cast<int32_t>(tid + i * 1024);
-      a.sorted_weight[position] = held_weight[i];
+      if (staged) {
+        staged_route[position] = static_cast<int32_t>(tid + i * 1024);
+        staged_weight[position] = held_weight[i];
+      } else {
+        a.sorted_route[position] = static_cast<int32_t>(tid + i * 1024);
+        a.sorted_weight[position] = held_weight[i];
+      }
     }
+  }
+  if (staged) {
+    __syncthreads();
+    const int placed = offsets[a.experts];
+    for (int position = tid; position < placed; position += 1024) {
+      a.sorted_route[position] = staged_route[position];
+      a.sorted_weight[position] = staged_weight[position];
+    }
+    return;
   }
   for (int64_t route = tid + 1024 * kSortRoutesPerThread; route < a.routes; route += 1024) {
     const int expert = a.ids[route];
@@ -480,7 +522,12 @@ MoeTile choose_moe_tile(int64_t routes, int64_t experts) {
 }
 
 KernelLaunch make_router_topk(const RouterTopkArgs &args) {
-  return launch_of(reinterpret_cast<const void *>(&router_topk_kernel), dim3(blocks_for(args.rows, 4)), 256, args);
+  const int per_lane = topk_per_lane(args.experts);
+  const void *kernel = per_lane == 2   ? reinterpret_cast<const void *>(&router_topk_kernel<2>)
+                       : per_lane == 4 ? reinterpret_cast<const void *>(&router_topk_kernel<4>)
+                       : per_lane == 8 ? reinterpret_cast<const void *>(&router_topk_kernel<8>)
+                                       : reinterpret_cast<const void *>(&router_topk_kernel<kTopkMaxPerLane>);
+  return launch_of(kernel, dim3(blocks_for(args.rows, 4)), 256, args);
 }
 
 KernelLaunch make_router_logits(const RouterLogitsArgs &args) {

@@ -116,6 +116,25 @@ def test_qwen3_moe_router_projection_and_topk(device, rows):
     torch.testing.assert_close(weights_only.cpu(), weights, rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("softmax", (True, False), ids=("softmax", "sigmoid"))
+@pytest.mark.parametrize("experts", (17, 128, 129, 256, 300, 512, 700, 1024))
+def test_topk_at_every_expert_width(device, experts, softmax):
+    # The TopK kernel holds 2, 4, 8 or 16 experts per lane (the fewest that cover the count:
+    # 128 / 256 / 512 / 1024 experts), each width its own instantiation.  Logits on a grid of
+    # eighths make ties common, also between experts that sit in different slots of one lane,
+    # so the tie policy (lower id for softmax, higher for sigmoid) is checked at every width.
+    rows, topk = 37, 8
+    generator = torch.Generator().manual_seed(500 + experts)
+    logits = torch.randint(-24, 25, (rows, experts), generator=generator).float() / 8
+    bias = None if softmax else torch.randint(-4, 5, (experts,), generator=generator).float() / 16
+    algorithm = RouterAlgorithm.SOFTMAX if softmax else RouterAlgorithm.SIGMOID
+    ids, weights = router_topk(to_device(logits, device), topk=topk, algorithm=algorithm,
+                               correction_bias=None if bias is None else to_device(bias, device))
+    expected_ids, expected_weights = m.router_topk(logits, topk=topk, softmax=softmax, correction_bias=bias)
+    assert torch.equal(ids.cpu(), expected_ids)
+    torch.testing.assert_close(weights.cpu(), expected_weights, rtol=1e-5, atol=1e-6)
+
+
 def test_finalize_routing_dynamic_live_rows(device):
     # routing/test_metadata.py:8-80
     routed_ids = torch.tensor(((0, 2), (1, 3), (2, 0), (3, 1)), dtype=torch.int32, device=device)

@@ -194,6 +194,17 @@ CASES = [
         True, True, 96, (7, 96),
         id="softmax-fp32logits-shared",
     ),
+    pytest.param(
+        # Wide Routers: the TopK fused into the route sort (up to 16 rows) and the separate
+        # TopK launch (24 rows) at 8 and 4 experts per lane.
+        256, 128, MoeLayerSpec(routed_expert_count=300, routed_topk=6), False, True, 24, (2, 16, 24),
+        id="softmax-300-experts",
+    ),
+    pytest.param(
+        256, 128, MoeLayerSpec(routed_expert_count=200, routed_topk=5, router_algorithm=RouterAlgorithm.SIGMOID),
+        True, False, 24, (4, 24),
+        id="sigmoid-200-experts-corrected",
+    ),
 ]
 
 
