@@ -2786,6 +2786,7 @@ GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmCho
     kernel.block = dim3(static_cast<unsigned>(64 * shape.waves), 1, 1);
   }
   if (scratch_slices(choice, args.k) > 1) {
+    launches.slices = scratch_slices(choice, args.k);
     KernelLaunch &reduce = launches.reduce;
     reduce.func = gated ? stream_reduce<true>(args.payload) : stream_reduce<false>(args.payload);
     reduce.grid = dim3(static_cast<unsigned>((capacity * (args.n / 4) + 255) / 256), 1, 1);

@@ -67,17 +67,61 @@ __device__ void router_topk_row(const RouterTopkArgs &a, int64_t row, int lane) 
   const int experts = a.experts;
   float logit[kTopkPerLane];
   float maximum = kNegativeInfinity;
+  if (a.partials != nullptr) {
+    // The projection's K slices, added here in slice order.  Every slice load of a batch,
+    // for all of the lane's experts, is issued before the first addition (a load per
+    // slice, each waiting for the last, would put the memory latency in series); a batch
+    // keeps 32 values in flight per lane.
+    constexpr int kBatch = 32 / kTopkPerLane > 1 ? 32 / kTopkPerLane : 2;
+    const int64_t plane = a.rows * experts;
+    float sum[kTopkPerLane];
+    for (int first = 0; first < a.slices; first += kBatch) {
+      float part[kTopkPerLane][kBatch];
 #pragma unroll
-  for (int i = 0; i < kTopkPerLane; ++i) {
-    const int expert = lane + i * kWave;
-    float value = kNegativeInfinity;
-    if (expert < experts) {
-      const int64_t index = row * experts + expert;
-      value = a.logits_f32 != 0 ? static_cast<const float *>(a.logits)[index]
-                                : bf16_to_float(static_cast<const uint16_t *>(a.logits)[index]);
+      for (int i = 0; i < kTopkPerLane; ++i) {
+        const int expert = lane + i * kWave;
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+          part[i][j] = expert < experts && first + j < a.slices ? a.partials[(first + j) * plane + row * experts + expert]
+                                                                : 0.0f;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < kTopkPerLane; ++i) {
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+          if (first + j < a.slices) {
+            sum[i] = first + j == 0 ? part[i][j] : sum[i] + part[i][j];
+          }
+        }
+      }
     }
-    logit[i] = value;
-    maximum = fmaxf(maximum, value);
+#pragma unroll
+    for (int i = 0; i < kTopkPerLane; ++i) {
+      const int expert = lane + i * kWave;
+      float value = kNegativeInfinity;
+      if (expert < experts) {
+        // One rounding of the sum to bf16, stored as the logit.
+        const uint32_t bits = float_to_bf16(sum[i]);
+        a.logits_out[row * experts + expert] = static_cast<uint16_t>(bits);
+        value = bf16_to_float(bits);
+      }
+      logit[i] = value;
+      maximum = fmaxf(maximum, value);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kTopkPerLane; ++i) {
+      const int expert = lane + i * kWave;
+      float value = kNegativeInfinity;
+      if (expert < experts) {
+        const int64_t index = row * experts + expert;
+        value = a.logits_f32 != 0 ? static_cast<const float *>(a.logits)[index]
+                                  : bf16_to_float(static_cast<const uint16_t *>(a.logits)[index]);
+      }
+      logit[i] = value;
+      maximum = fmaxf(maximum, value);
+    }
   }
   float score[kTopkPerLane];
   if (a.softmax != 0) {

@@ -493,7 +493,7 @@ struct RouterBinding {
 
 struct RouterLaunches {
   KernelLaunch logits;         // MFMA projection or the fp32 logits kernel
-  KernelLaunch logits_reduce;  // K-slice reduction of the MFMA projection, or empty
+  KernelLaunch logits_reduce;  // K-slice reduction of the MFMA projection (empty: the TopK sums the slices)
   KernelLaunch topk;
   RouterTopkArgs topk_args;    // the TopK launch's arguments (live rows)
 };
@@ -509,6 +509,8 @@ RouterLaunches make_router_launches(const RouterBinding &b, int64_t capacity) {
   const RouterWorkspace layout = router_workspace(capacity, b.hidden, b.experts, b.precision);
   void *logits = b.workspace + layout.logits;
   RouterLaunches launches;
+  const float *partials = nullptr;
+  int64_t slices = 1;
   if (router_uses_mfma(b.hidden, b.experts, b.precision)) {
     // logits = bf16(x . w^T): the Dense projection kernels, no epilogue.
     GemmArgs args{};
@@ -536,7 +538,12 @@ RouterLaunches make_router_launches(const RouterBinding &b, int64_t capacity) {
     const GemmLaunch gemm = make_gemm(args, capacity, false,
                                       choose_gemm(capacity, b.experts, b.hidden, false, false), b.fused_gather);
     launches.logits = gemm.main;
-    launches.logits_reduce = gemm.reduce;
+    if (gemm.slices > 1) {
+      // The TopK adds the K slices itself and stores the logits: no reduction launch (at one
+      // to sixteen rows a quarter of the Router's time, most of it the launch).
+      partials = args.partials;
+      slices = gemm.slices;
+    }
   } else {
     RouterLogitsArgs args{};
     args.x = b.x;
@@ -563,6 +570,9 @@ RouterLaunches make_router_launches(const RouterBinding &b, int64_t capacity) {
   topk.softmax = b.algorithm == XP_ROUTER_SOFTMAX ? 1 : 0;
   topk.renormalize = b.renormalize != 0 ? 1 : 0;
   topk.round_to_logits = b.weight_rounding == XP_TOPK_ROUNDING_LOGITS_DTYPE ? 1 : 0;
+  topk.partials = partials;
+  topk.logits_out = partials != nullptr ? static_cast<uint16_t *>(logits) : nullptr;
+  topk.slices = static_cast<int32_t>(slices);
   launches.topk = make_router_topk(topk);
   topk.rows = b.rows;
   launches.topk.set_args(topk);

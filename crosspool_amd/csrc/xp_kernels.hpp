@@ -186,6 +186,13 @@ struct RouterTopkArgs {
   int32_t softmax;  // 1: softmax scores, ties to the lower id; 0: sigmoid, ties to the higher id
   int32_t renormalize;
   int32_t round_to_logits;
+  // The bf16 projection's K-slice sums [slices, rows, experts] (fp32), or null: the TopK
+  // then adds each logit's slices in slice order, rounds the sum to bf16 once (the order and
+  // rounding of stream_reduce_kernel, whose launch this replaces) and stores it at
+  // logits_out (= logits) before selecting.
+  const float *partials;
+  uint16_t *logits_out;
+  int32_t slices;
 };
 
 // Router logits[rows, experts] = x[rows, hidden] . w[experts, hidden] (w bf16 or fp32) as
@@ -411,6 +418,7 @@ struct GemmLaunch {
   KernelLaunch reduce;
   KernelLaunch tail;   // the trailing columns of a column-split tile choice (empty otherwise)
   bool usable = true;  // false: the choice names no launchable kernel (callers fail the call)
+  int64_t slices = 1;  // K ranges summed by `reduce` (fp32 partials [slices, rows, n]); 1: none
 };
 // `fused_gather`: the gate_up of a Dense step whose choose_dense_gate_up decision fused the
 // mailbox gather, or a projection for which split_gather_fusable holds (the kernel variant
