@@ -2798,12 +2798,16 @@ GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmCho
 }
 
 // Grouped projections run on the tile kernel's grouped instantiations, one per expert
-// tile height (choose_moe_tile picks it by routes per expert): 64 x 256 (four stages),
-// 128 x 256 (three stages, nontemporal or plain weight loads) and 256 x 128 (three stages,
-// nontemporal).  Each keeps 144-160 KB of LDS, one workgroup per CU; the shorter the token
-// rows of a tile, the more of that LDS holds weight slabs in flight.  The nontemporal hint
-// suits tiles whose expert's weights no other tile reads; with plain loads an expert split
-// over two 128-row tiles reads its weights from the last-level cache the second time.
+// tile height (choose_moe_tile picks it by routes per expert): 64 x 128 (four waves, three
+// stages, 72 KB of LDS: two workgroups per CU), 128 x 256 (eight waves, three stages,
+// nontemporal or plain weight loads) and 256 x 128 (eight waves, three stages, nontemporal),
+// the last two at 144-147 KB of LDS, one workgroup per CU.  With few routes per expert a
+// tile's K loop is short against its prologue and epilogue, and the second workgroup of a
+// CU streams while the first fills or drains (Qwen3-30B-A3B layer at 256 / 512 tokens:
+// 281 / 294 us on a 64 x 256 eight-wave tile with four stages, one per CU, against 255 /
+// 265 us).  The nontemporal hint suits tiles whose expert's weights no other tile reads;
+// with plain loads an expert split over two 128-row tiles reads its weights from the
+// last-level cache the second time.
 struct GroupedTile {
   int bm;
   int bn;
@@ -2813,7 +2817,7 @@ struct GroupedTile {
 GroupedTile grouped_tile(MoeTile tile) {
   switch (tile) {
     case MoeTile::Rows64:
-      return {64, 256, 8};
+      return {64, 128, 4};
     case MoeTile::Rows128Stream:
     case MoeTile::Rows128:
       return {128, 256, 8};
@@ -2828,7 +2832,7 @@ template <bool GATED>
 const void *grouped_tile_kernel(MoeTile tile) {
   switch (tile) {
     case MoeTile::Rows64:
-      return reinterpret_cast<const void *>(&tile_gemm_kernel<64, 256, 2, 4, 4, GATED, true, true>);
+      return reinterpret_cast<const void *>(&tile_gemm_kernel<64, 128, 2, 2, 3, GATED, true, true>);
     case MoeTile::Rows128Stream:
       return reinterpret_cast<const void *>(&tile_gemm_kernel<128, 256, 2, 4, 3, GATED, true, true>);
     case MoeTile::Rows128:

@@ -543,7 +543,8 @@ int moe_tile_rows(MoeTile tile) { return tile == MoeTile::Small ? grouped_split_
 // expert tile that holds most experts' routes.  An expert's weights are read once per tile
 // of its routes, and the LDS a tile's token rows do not take holds weight slabs in flight
 // (the grouped projections are bound by the weight bytes each CU has in flight), so:
-// 64-row tiles (four stages, 80 % of the LDS for weights) up to 40 routes per expert on
+// 64-row tiles (two workgroups per CU, each with two of its three 64 x 128 weight slabs in
+// flight) up to 40 routes per expert on
 // average, 128-row tiles with the weights loaded nontemporally up to 80, 128-row tiles with
 // plain loads (an expert split over two tiles finds its weights in the last-level cache
 // for the second) up to 160, 256-row tiles above.  Measured at the Qwen3-30B-A3B shape
@@ -551,7 +552,10 @@ int moe_tile_rows(MoeTile tile) { return tile == MoeTile::Small ? grouped_split_
 // 512 357 -> 304, 1024 391 -> 332, 2048 431 -> 418, 4096 unchanged (647 against 652 on
 // 128-row tiles); 128 tokens (8 routes per expert) 298 us on 16-route tiles -> 279 on 64-row
 // tiles, while at 48 / 64 tokens (3 / 4 routes per expert) the 64-row tiles lost (254 / 263
-// -> 263 / 270 us).
+// -> 263 / 270 us).  (Those 64-row figures are of a 64 x 256 tile, one workgroup per CU; the
+// 64 x 128 tile at two per CU since took 256 / 512 tokens to 255 / 265 us, while in the
+// 80-route regime it won below the capacity's 1024 tokens and lost at them: 377 against
+// 319 us, so the thresholds stand.)
 MoeTile choose_moe_tile(int64_t routes, int64_t experts) {
   if (routes <= 4 * experts) {
     return MoeTile::Small;
