@@ -733,15 +733,19 @@ __global__ __launch_bounds__(64 * kSplitWaves) __attribute__((amdgpu_waves_per_e
 // ------------------------------------------------------------------ grouped split (MoE decode)
 // The split kernel over an expert tile table, for few routes per expert.  Grid y is entry y
 // of the table: up to 16 sorted positions of one expert e (GemmArgs describes the table);
-// grid x covers e's 16-row weight blocks and their K ranges as in split_gemm_kernel.  The
-// token operand row of lane r16 is sorted position p = tile_row0[y] + r16 while p <
-// expert_end[e]: row gather_slots[p] / gather_divisor of x when gather_slots is set, else
-// row p.  The result goes to row p of out, or to row scatter_slots[p] when that is set,
-// times row_scale[p] when that is set.  A wave's chunk count is rounded up to whole groups
-// of DEPTH; the chunks past its range load through an out-of-range offset, which reads
-// zeros without a memory access.
+// grid x covers e's 16-row weight blocks and their K ranges as in split_gemm_kernel, and
+// the weights are read and multiplied the same way: whole 128-byte lines, 8 rows x 128
+// bytes per instruction with the nontemporal hint, on v_mfma_f32_16x16x32_bf16 with the
+// even / odd piece pairing, here over two groups of 8 routes (route 8 g + i of the tile at
+// sorted position p = tile_row0[y] + 8 g + i, live while p < expert_end[e]).  The token
+// operand of route p is row gather_slots[p] / gather_divisor of x when gather_slots is set,
+// else row p.  The result goes to row p of out, or to row scatter_slots[p] when that is
+// set, times row_scale[p] when that is set.  A wave's chunk count is rounded up to whole
+// groups of DEPTH; the chunks past its range load through an out-of-range offset, which
+// reads zeros without a memory access.
 template <int DEPTH, bool GATED>
 __global__ __launch_bounds__(64 * kSplitWaves) void grouped_split_kernel(GemmArgs a) {
+  constexpr int TG = 2;  // groups of 8 routes
   // Both table words are loaded before the branch: the loads that follow depend on them,
   // and each dependent level costs a memory round trip before the weight stream starts.
   const int expert = __builtin_amdgcn_readfirstlane(a.tile_expert[blockIdx.y]);
@@ -754,27 +758,43 @@ __global__ __launch_bounds__(64 * kSplitWaves) void grouped_split_kernel(GemmArg
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int r16 = lane & 15;
   const int kq = lane >> 4;
+  const int row = r16 & 7;                // weight row within its half / route within its group
+  const int piece = 2 * kq + (r16 >> 3);  // 16-byte piece of the 128-byte line
   const int ksplit = static_cast<int>(a.k_split);
   const int part = wave % ksplit;
   const int64_t rb = static_cast<int64_t>(blockIdx.x) * (kSplitWaves / ksplit) + wave / ksplit;
   const int64_t row_blocks = (a.n + 15) / 16;
   const u32x4 zero = {0u, 0u, 0u, 0u};
 
-  // This lane's route: its token row, and for the epilogue its output row and factor, all
-  // loaded before the stream starts.
-  const int64_t position = m0 + r16;
-  const bool live = position < row_end;
-  int64_t x_row = position;
-  if (a.gather_slots != nullptr) {
-    x_row = live ? a.gather_slots[position] / a.gather_divisor : 0;
+  // Route 8 g + row of the tile: its token row for the loads and, for the epilogue (whose
+  // lanes r16 < 8 hold route 8 g + r16 = 8 g + row), its output row and factor, all loaded
+  // before the stream starts.
+  bool live[TG];
+  int64_t x_row[TG];
+  int64_t out_row[TG];
+  float factor[TG];
+#pragma unroll
+  for (int g = 0; g < TG; ++g) {
+    const int64_t position = m0 + 8 * g + row;
+    live[g] = position < row_end;
+    x_row[g] = position;
+    if (a.gather_slots != nullptr) {
+      x_row[g] = live[g] ? a.gather_slots[position] / a.gather_divisor : 0;
+    }
+    out_row[g] = position;
+    if (a.scatter_slots != nullptr) {
+      out_row[g] = live[g] ? a.scatter_slots[position] : -1;
+    }
+    factor[g] = live[g] && a.row_scale != nullptr ? a.row_scale[position] : 1.0f;
   }
-  int64_t out_row = position;
-  if (a.scatter_slots != nullptr) {
-    out_row = live ? a.scatter_slots[position] : -1;
-  }
-  const float factor = live && a.row_scale != nullptr ? a.row_scale[position] : 1.0f;
 
-  f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  // acc[g][h]: route group g, weight rows 16 rb + 8 h + [0, 8).
+  f32x4 acc[TG][2];
+#pragma unroll
+  for (int g = 0; g < TG; ++g) {
+    acc[g][0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    acc[g][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
   if (rb < row_blocks) {
     const int k0 = part * static_cast<int>(a.k_slice);
     const int k_range = static_cast<int>(a.k - k0 < a.k_slice ? a.k - k0 : a.k_slice);
@@ -782,49 +802,69 @@ __global__ __launch_bounds__(64 * kSplitWaves) void grouped_split_kernel(GemmArg
     const int groups = (chunks + DEPTH - 1) / DEPTH;
     // Columns at or past K in the last chunk read the next row (or past the end): zero
     // both operands there.
-    const int lane_valid = static_cast<int>(a.k) - k0 - kq * 8;
+    const int lane_valid = static_cast<int>(a.k) - k0 - piece * 8;
     const int rotation = static_cast<int>((rb * 7) % chunks);
     const uint16_t *weights = a.w + static_cast<int64_t>(expert) * a.n * a.k;
     const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(weights, static_cast<uint32_t>(a.n * a.k * 2));
     const __amdgpu_buffer_rsrc_t x_rsrc =
         make_rsrc(a.x, static_cast<uint32_t>((a.gather_slots != nullptr ? a.pool_rows : a.rows) * a.ldx * 2));
-    const uint32_t w_off = static_cast<uint32_t>(((rb * 16 + r16) * a.k + k0 + kq * 8) * 2);
-    const uint32_t x_off = live ? static_cast<uint32_t>((x_row * a.ldx + k0 + kq * 8) * 2) : kOutOfRange;
-    auto column_of = [&](int chunk) {
+    const uint32_t w_off = static_cast<uint32_t>(((rb * 16 + row) * a.k + k0 + piece * 8) * 2);
+    const uint32_t w_half = static_cast<uint32_t>(8 * a.k * 2);  // rows 8 .. 15 of the block
+    uint32_t x_off[TG];
+#pragma unroll
+    for (int g = 0; g < TG; ++g) {
+      x_off[g] = static_cast<uint32_t>((x_row[g] * a.ldx + k0 + piece * 8) * 2);
+    }
+    auto column_of = [&](int chunk) XP_INLINE {
       const int c = chunk + rotation;
       return (c < chunks ? c : c - chunks) * 128;
     };
 
+    // Per chunk: w[2 line + h] = line `line` (K columns 64 line .. 64 line + 63 of the
+    // chunk) of rows 8 h + [0, 8); x[line][g] the matching pieces of route group g.
     u32x4 wbuf[DEPTH][4];
-    u32x4 xbuf[DEPTH][4];
-    auto load_w = [&](int chunk, u32x4 (&w)[4]) {
+    u32x4 xbuf[DEPTH][2][TG];
+    auto load_w = [&](int chunk, u32x4 (&w)[4]) XP_INLINE {
       const bool in_range = chunk < chunks;
-      const uint32_t base = in_range ? w_off + static_cast<uint32_t>(column_of(chunk)) * 2 : kOutOfRange;
+      const uint32_t column = static_cast<uint32_t>(column_of(chunk)) * 2;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        w[s] = buffer_load16(w_rsrc, base + s * 64);
+      for (int line = 0; line < 2; ++line) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          w[2 * line + h] = buffer_load16<kLoadNontemporal>(
+              w_rsrc, in_range ? w_off + h * w_half + column + line * 128 : kOutOfRange);
+        }
       }
     };
-    auto load_x = [&](int chunk, u32x4 (&x)[4]) {
+    auto load_x = [&](int chunk, u32x4 (&x)[2][TG]) XP_INLINE {
       const bool in_range = chunk < chunks;
-      const uint32_t base = in_range ? x_off + static_cast<uint32_t>(column_of(chunk)) * 2 : kOutOfRange;
+      const uint32_t column = static_cast<uint32_t>(column_of(chunk)) * 2;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        x[s] = buffer_load16(x_rsrc, base + s * 64);
+      for (int line = 0; line < 2; ++line) {
+#pragma unroll
+        for (int g = 0; g < TG; ++g) {
+          x[line][g] = buffer_load16(x_rsrc, in_range && live[g] ? x_off[g] + column + line * 128 : kOutOfRange);
+        }
       }
     };
-    auto compute_chunk = [&](int chunk, const u32x4 (&w)[4], const u32x4 (&x)[4]) {
+    auto compute_chunk = [&](int chunk, const u32x4 (&w)[4], const u32x4 (&x)[2][TG]) XP_INLINE {
       const int column = chunk < chunks ? column_of(chunk) : 0;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const bool valid = column + s * 32 < lane_valid;
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(valid ? w[s] : zero), as_bf16x8(valid ? x[s] : zero),
-                                                      acc, 0, 0, 0);
+      for (int line = 0; line < 2; ++line) {
+        const bool valid = column + line * 64 < lane_valid;
+        const u32x4 w0 = valid ? w[2 * line] : zero;
+        const u32x4 w1 = valid ? w[2 * line + 1] : zero;
+#pragma unroll
+        for (int g = 0; g < TG; ++g) {
+          const u32x4 xk = valid ? x[line][g] : zero;
+          acc[g][0] = Bf16Payload::mfma16(w0, xk, acc[g][0]);
+          acc[g][1] = Bf16Payload::mfma16(w1, xk, acc[g][1]);
+        }
       }
     };
 
     // The weight loads of the first group go out before the token loads, whose offsets
-    // wait on the gather slot load.
+    // wait on the gather slot loads.
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
       load_w(d, wbuf[d]);
@@ -850,33 +890,67 @@ __global__ __launch_bounds__(64 * kSplitWaves) void grouped_split_kernel(GemmArg
   }
 
   // Fixed-order sum of the K ranges of each row block, as in split_gemm_kernel.
-  __shared__ f32x4 partial[kSplitWaves][64];
+  __shared__ f32x4 partial[kSplitWaves][TG][2][64];
   if (ksplit > 1) {
-    partial[wave][lane] = acc;
+#pragma unroll
+    for (int g = 0; g < TG; ++g) {
+      partial[wave][g][0][lane] = acc[g][0];
+      partial[wave][g][1][lane] = acc[g][1];
+    }
     __syncthreads();
     if (part != 0) {
       return;
     }
-    for (int p = 1; p < ksplit; ++p) {
-      acc += partial[wave + p][lane];
+#pragma unroll
+    for (int g = 0; g < TG; ++g) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        for (int p = 1; p < ksplit; ++p) {
+          acc[g][h] += partial[wave + p][g][h][lane];
+        }
+      }
     }
   }
-  if (rb >= row_blocks || !live || out_row < 0 || out_row >= a.out_rows) {
+
+  // Lane (i, q) holds D[4 q + v][i], v = 0 .. 3.  The lanes with q < 2 and i < 8 add the odd
+  // pieces' block from lane + 40 (D[4 q + 8 + v][i + 8]) and then hold weight rows
+  // 16 rb + 8 h + 4 q + v for route 8 g + i.
+  f32x4 sum[TG][2];
+#pragma unroll
+  for (int g = 0; g < TG; ++g) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        sum[g][h][v] = acc[g][h][v] + __shfl(acc[g][h][v], lane + 40, kWave);
+      }
+    }
+  }
+  if (rb >= row_blocks || kq >= 2 || r16 >= 8) {
     return;
   }
-  // lane holds D[4 kq + i][r16]: weight rows n .. n+3 of this lane's route.
-  const int64_t n = rb * 16 + 4 * kq;
-  if (n >= a.n) {
-    return;
-  }
-  uint16_t *row = a.out + out_row * a.ldo;
-  if constexpr (GATED) {
-    const float h0 = gated_silu(acc[0], acc[1], a.act);
-    const float h1 = gated_silu(acc[2], acc[3], a.act);
-    *reinterpret_cast<uint32_t *>(row + n / 2) = pack_bf16x2(h0, h1);
-  } else {
-    u32x2 packed = {pack_bf16x2(acc[0] * factor, acc[1] * factor), pack_bf16x2(acc[2] * factor, acc[3] * factor)};
-    *reinterpret_cast<u32x2 *>(row + n) = packed;
+#pragma unroll
+  for (int g = 0; g < TG; ++g) {
+    if (!live[g] || out_row[g] < 0 || out_row[g] >= a.out_rows) {
+      continue;
+    }
+    uint16_t *out = a.out + out_row[g] * a.ldo;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int64_t n = rb * 16 + 8 * h + 4 * kq;
+      if (n >= a.n) {
+        continue;
+      }
+      if constexpr (GATED) {
+        const float h0 = gated_silu(sum[g][h][0], sum[g][h][1], a.act);
+        const float h1 = gated_silu(sum[g][h][2], sum[g][h][3], a.act);
+        *reinterpret_cast<uint32_t *>(out + n / 2) = pack_bf16x2(h0, h1);
+      } else {
+        const float f = factor[g];
+        u32x2 packed = {pack_bf16x2(sum[g][h][0] * f, sum[g][h][1] * f), pack_bf16x2(sum[g][h][2] * f, sum[g][h][3] * f)};
+        *reinterpret_cast<u32x2 *>(out + n) = packed;
+      }
+    }
   }
 }
 
