@@ -2941,6 +2941,16 @@ KernelLaunch make_grouped_gemm(const GemmArgs &args, bool gated, int max_tiles, 
 // Routes per expert tile of the grouped split kernel: one 16-column MFMA token block.
 int grouped_split_rows() { return 16; }
 
+// Chunks in flight per wave of the grouped split kernel.  Its workgroups are short (a wave
+// streams one 16-row block of one expert: 24 KB of Qwen3-30B-A3B's down projection), so
+// the fixed cost of each (the tile table, the route slots, the first round trip) weighs
+// more than the depth of its ring: at depth 2 the kernel takes 107 VGPRs and two
+// workgroups share a CU, one streaming while the other starts or ends.  Qwen3-30B-A3B
+// layer at 8 / 32 / 64 tokens: 121.5 / 215.7 / 238.1 us at depth 4 (160 VGPRs, one
+// workgroup per CU), 115.0 / 201.2 / 223.3 at depth 2; depth 3 (128 VGPRs, two per CU, and
+// chunk counts that do not divide into its groups) 122.4 / 217.0 / 238.7.
+constexpr int kGroupedSplitDepth = 2;
+
 // K ranges per weight block: the most (1, 2, 4 or 8) that keep the expected live tiles'
 // workgroups within one round of one per CU, with every range at least two 128-wide chunks
 // long.  A workgroup at decode sizes is latency-bound (the tile table, the route slots,
@@ -2962,8 +2972,8 @@ KernelLaunch make_grouped_split(const GemmArgs &args, bool gated, int max_tiles,
   record.k_slice = (chunks + ksplit - 1) / ksplit * 128;
   record.partials = nullptr;
   KernelLaunch kernel;
-  kernel.func = gated ? reinterpret_cast<const void *>(&grouped_split_kernel<kSplitDepth, true>)
-                      : reinterpret_cast<const void *>(&grouped_split_kernel<kSplitDepth, false>);
+  kernel.func = gated ? reinterpret_cast<const void *>(&grouped_split_kernel<kGroupedSplitDepth, true>)
+                      : reinterpret_cast<const void *>(&grouped_split_kernel<kGroupedSplitDepth, false>);
   kernel.grid = dim3(static_cast<unsigned>((row_blocks * ksplit + kSplitWaves - 1) / kSplitWaves),
                      static_cast<unsigned>(max_tiles), 1);
   kernel.block = dim3(64 * kSplitWaves, 1, 1);
