@@ -2888,13 +2888,20 @@ struct GroupedTile {
   int waves;
 };
 
-GroupedTile grouped_tile(MoeTile tile) {
+// The down projection (not gated) of the 128-row regimes takes 128 x 128 tiles of two
+// stages (64 KB of LDS, two workgroups per CU): its K loop is short (Qwen3-30B-A3B: 768
+// columns, 12 slabs), so a tile's fill and drain weigh on it, and the CU's second workgroup
+// streams meanwhile.  Measured on that layer against 128 x 256 three-stage down tiles:
+// 600 / 800 / 1024 tokens 306.8 / 311.6 / 319.6 -> 301.3 / 306.0 / 314.6 us, 1100 / 1400 /
+// 1700 / 2048 tokens 346.3 / 350.2 / 385.1 / 396.4 -> 338.7 / 343.2 / 379.1 / 389.9 us.
+// gate_up (K = 2048) lost on such tiles (2048 tokens: 410-421 against 397 us).
+GroupedTile grouped_tile(MoeTile tile, bool gated) {
   switch (tile) {
     case MoeTile::Rows64:
       return {64, 128, 4};
     case MoeTile::Rows128Stream:
     case MoeTile::Rows128:
-      return {128, 256, 8};
+      return gated ? GroupedTile{128, 256, 8} : GroupedTile{128, 128, 8};
     case MoeTile::Rows256:
       return {256, 128, 8};
     default:
@@ -2908,9 +2915,11 @@ const void *grouped_tile_kernel(MoeTile tile) {
     case MoeTile::Rows64:
       return reinterpret_cast<const void *>(&tile_gemm_kernel<64, 128, 2, 2, 3, GATED, true, true>);
     case MoeTile::Rows128Stream:
-      return reinterpret_cast<const void *>(&tile_gemm_kernel<128, 256, 2, 4, 3, GATED, true, true>);
+      return GATED ? reinterpret_cast<const void *>(&tile_gemm_kernel<128, 256, 2, 4, 3, GATED, true, true>)
+                   : reinterpret_cast<const void *>(&tile_gemm_kernel<128, 128, 4, 2, 2, GATED, true, true>);
     case MoeTile::Rows128:
-      return reinterpret_cast<const void *>(&tile_gemm_kernel<128, 256, 2, 4, 3, GATED, true, false>);
+      return GATED ? reinterpret_cast<const void *>(&tile_gemm_kernel<128, 256, 2, 4, 3, GATED, true, false>)
+                   : reinterpret_cast<const void *>(&tile_gemm_kernel<128, 128, 4, 2, 2, GATED, true, false>);
     case MoeTile::Rows256:
       return reinterpret_cast<const void *>(&tile_gemm_kernel<256, 128, 4, 2, 3, GATED, true, true>);
     default:
@@ -2918,10 +2927,10 @@ const void *grouped_tile_kernel(MoeTile tile) {
   }
 }
 
-int grouped_tile_rows(MoeTile tile) { return grouped_tile(tile).bm; }
+int grouped_tile_rows(MoeTile tile) { return grouped_tile(tile, true).bm; }  // the same for down
 
 KernelLaunch make_grouped_gemm(const GemmArgs &args, bool gated, int max_tiles, MoeTile tile) {
-  const GroupedTile shape = grouped_tile(tile);
+  const GroupedTile shape = grouped_tile(tile, gated);
   const void *func = gated ? grouped_tile_kernel<true>(tile) : grouped_tile_kernel<false>(tile);
   if (max_tiles % 8 != 0 || func == nullptr) {
     return KernelLaunch{};  // grouped_tile_coordinates needs a multiple of 8 (callers pad)
