@@ -1216,9 +1216,11 @@ constexpr int kResidentWaves = 8;
 constexpr int kResidentWorkgroups = 256;  // one per CU
 constexpr int kResidentChunk = 128;       // columns per chunk
 
-// Weight chunks in flight per wave (measured on MI355X for Qwen3-8B gate_up at 16 rows: 8
-// chunks were no faster than 4), and the greatest common divisor for the loop's rounds.
-constexpr int kResidentDepth = 4;
+// Weight chunks in flight per wave: 4 with two token groups (measured on MI355X for
+// Qwen3-8B gate_up at 16 rows: 8 chunks were no faster than 4); 2 with four, whose token
+// pieces take 128 registers per lane (at 4 in flight the kernel spilled; at 2 it takes 240
+// VGPRs and none spill).  And the greatest common divisor for the loop's rounds.
+constexpr int resident_depth(int groups) { return groups >= 4 ? 2 : 4; }
 constexpr int gcd_int(int a, int b) { return b == 0 ? a : gcd_int(b, a % b); }
 
 template <int TG>
@@ -1231,7 +1233,7 @@ struct ResidentLds {
 template <int TG, int CPW, bool GATED, bool GATHER, class P = Bf16Payload>
 __global__ __launch_bounds__(64 * kResidentWaves) __attribute__((amdgpu_waves_per_eu(2))) void resident_gemm_kernel(
     GemmArgs a) {
-  constexpr int D = kResidentDepth;
+  constexpr int D = resident_depth(TG);
   constexpr int L = D / gcd_int(D, CPW) * CPW;  // chunks per round of the loop: whole blocks and whole rings
   constexpr int TP = 8 * TG;
   __shared__ ResidentLds<TG> lds;
@@ -2235,32 +2237,46 @@ const void *stream_reduce(int32_t payload) {
 }
 
 // The resident kernel for 16 token rows (two groups of 8) and `cpw` chunks per wave (1 to
-// 4); the gather fuses into gate_up only.  (Four groups, 32 rows, were measured and dropped:
-// the token pieces then take 128 registers per lane and the kernel spills, and Qwen3-8B at
-// 32 rows took 77.0 us per layer against 74.8 us on the tile kernels.)
+// 4), and for 32 (four groups, two chunks in flight per wave) as the gate_up of a Dense
+// step with the gather fused.  Measured on MI355X, Qwen3 layers at 17-32 rows against the
+// separate gather and the 64 x 64 tiles: 4B (19456 weight rows) 50.3 / 51.2 / 53.4 ->
+// 45.6 / 46.7 / 49.4 us at 20 / 24 / 32 rows, 8B (24576) 71.9 / 72.4 / 74.0 -> 69.4 /
+// 70.4 / 72.4; 1.7B (12288) and 0.6B (6144) within +-1 us either way, so four groups serve
+// only projections of at least kResidentWideMinN weight rows.  (At 9-16 rows four groups
+// were 1.2-4.3 us slower than two.)
 constexpr int kResidentMaxChunksPerWave = 4;
 constexpr int kResidentGroups = 2;
+constexpr int kResidentWideGroups = 4;
 
-template <bool GATED, bool GATHER, class P>
+template <int TG, bool GATED, bool GATHER, class P>
 const void *resident_kernel(int cpw) {
   using Kernel = void (*)(GemmArgs);
   static const Kernel table[kResidentMaxChunksPerWave] = {
-      &resident_gemm_kernel<kResidentGroups, 1, GATED, GATHER, P>, &resident_gemm_kernel<kResidentGroups, 2, GATED, GATHER, P>,
-      &resident_gemm_kernel<kResidentGroups, 3, GATED, GATHER, P>, &resident_gemm_kernel<kResidentGroups, 4, GATED, GATHER, P>};
+      &resident_gemm_kernel<TG, 1, GATED, GATHER, P>, &resident_gemm_kernel<TG, 2, GATED, GATHER, P>,
+      &resident_gemm_kernel<TG, 3, GATED, GATHER, P>, &resident_gemm_kernel<TG, 4, GATED, GATHER, P>};
   return reinterpret_cast<const void *>(table[cpw - 1]);
 }
 
+// Null for a combination without an instantiation (four groups serve gate_up with the
+// gather fused only).
 template <class P>
-const void *resident_kernel_for(bool gated, bool gather, int cpw) {
-  if (gated) {
-    return gather ? resident_kernel<true, true, P>(cpw) : resident_kernel<true, false, P>(cpw);
+const void *resident_kernel_for(bool gated, bool gather, int cpw, int groups) {
+  if (groups == kResidentWideGroups) {
+    return gated && gather ? resident_kernel<kResidentWideGroups, true, true, P>(cpw) : nullptr;
   }
-  return resident_kernel<false, false, P>(cpw);
+  if (groups != kResidentGroups) {
+    return nullptr;
+  }
+  if (gated) {
+    return gather ? resident_kernel<kResidentGroups, true, true, P>(cpw)
+                  : resident_kernel<kResidentGroups, true, false, P>(cpw);
+  }
+  return resident_kernel<kResidentGroups, false, false, P>(cpw);
 }
 
-const void *resident_kernel_for(bool gated, bool gather, int cpw, int32_t payload) {
-  return payload == kPayloadF16 ? resident_kernel_for<F16Payload>(gated, gather, cpw)
-                                : resident_kernel_for<Bf16Payload>(gated, gather, cpw);
+const void *resident_kernel_for(bool gated, bool gather, int cpw, int32_t payload, int groups) {
+  return payload == kPayloadF16 ? resident_kernel_for<F16Payload>(gated, gather, cpw, groups)
+                                : resident_kernel_for<Bf16Payload>(gated, gather, cpw, groups);
 }
 
 struct TileShape {
@@ -2546,8 +2562,9 @@ GemmChoice choose_tile(int64_t capacity, int64_t n, int64_t k, bool split_column
   return split_best;
 }
 
-// The resident kernel's K parts and chunks per wave at `capacity` rows (9 to 16), with its
-// modelled cost in microseconds (-1: not applicable).  Every workgroup streams its blocks'
+// The resident kernel's K parts and chunks per wave at `capacity` rows (9 to 16, or 17 to
+// 32 for a projection with the gather fused and at least kResidentWideMinN weight rows, on
+// four token groups), with its modelled cost in microseconds (-1: not applicable).  Every workgroup streams its blocks'
 // columns of its part at one workgroup's rate after a fixed prologue (launch, the token
 // pieces, the first weight round trip), and the busiest workgroup sets the time; more than
 // one part adds the partial sums and the reduction launch.  With the gather fused the part
@@ -2558,14 +2575,19 @@ GemmChoice choose_tile(int64_t capacity, int64_t n, int64_t k, bool split_column
 // least 2048: a Router projection's few experts do not).
 constexpr int64_t kResidentMinRows = 9;
 constexpr int64_t kResidentMaxRows = 8 * kResidentGroups;
+constexpr int64_t kResidentWideMaxRows = 8 * kResidentWideGroups;
 constexpr int64_t kResidentMinN = 2048;
+constexpr int64_t kResidentWideMinN = 16384;
 constexpr double kResidentWorkgroupBytesPerUs[2] = {35.7e3, 24.8e3};  // index: gather fused
 constexpr double kResidentFixedUs[2] = {7.8, 8.0};
 
 GemmChoice choose_resident(int64_t capacity, int64_t n, int64_t k, bool gather, double &cost) {
-  GemmChoice best{GemmKind::Resident, kResidentGroups, 0, 0};
+  const bool wide = gather && capacity > kResidentMaxRows && capacity <= kResidentWideMaxRows && n >= kResidentWideMinN;
+  const int groups = wide ? kResidentWideGroups : kResidentGroups;
+  GemmChoice best{GemmKind::Resident, groups, 0, 0};
   cost = -1.0;
-  if (capacity < kResidentMinRows || capacity > kResidentMaxRows || n < kResidentMinN || n * k * 2 > INT32_MAX) {
+  if (capacity < kResidentMinRows || (capacity > kResidentMaxRows && !wide) || n < kResidentMinN ||
+      n * k * 2 > INT32_MAX) {
     return best;
   }
   const int64_t chunks = (k + kResidentChunk - 1) / kResidentChunk;
@@ -2585,7 +2607,7 @@ GemmChoice choose_resident(int64_t capacity, int64_t n, int64_t k, bool gather, 
       us += kStreamReduceUs + 8.0 * static_cast<double>(parts * capacity * n) / kStreamPartialBytesPerUs;
     }
     if (cost < 0.0 || us < cost * (1.0 - kSplitTieMargin)) {
-      best = {GemmKind::Resident, kResidentGroups, part_chunks * kResidentChunk, parts};
+      best = {GemmKind::Resident, groups, part_chunks * kResidentChunk, parts};
       cost = us;
     }
   }
@@ -2814,7 +2836,11 @@ GemmLaunch make_gemm(const GemmArgs &args, int64_t capacity, bool gated, GemmCho
     const int64_t row_blocks = (args.n + 15) / 16;
     const int cpw = static_cast<int>(choice.k_slice / (kResidentWaves * kResidentChunk));
     const int64_t walkers = std::min<int64_t>(kResidentWorkgroups / choice.k_split, row_blocks);
-    kernel.func = resident_kernel_for(gated, fused_gather && gated, cpw, args.payload);
+    kernel.func = resident_kernel_for(gated, fused_gather && gated, cpw, args.payload, choice.variant);
+    if (kernel.func == nullptr) {
+      launches.usable = false;
+      return launches;
+    }
     kernel.grid = dim3(static_cast<unsigned>(choice.k_split * walkers), 1, 1);
     kernel.block = dim3(64 * kResidentWaves, 1, 1);
   } else if (choice.kind == GemmKind::Stream) {

@@ -168,10 +168,16 @@ def test_fused_gather_matches_separate_kernels_bitwise(device, normed, hidden, i
         # the Qwen3-32B TP shard: gate_up on a separate gather (K = 5120 exceeds one part), down
         # on the resident kernel with one part
         (5120, 3200, 11, "stream_gated_t16", "resident_t16_c4"),
+        # 17 to 32 rows on four token groups (gate_up of at least 16384 weight rows): the last
+        # group partly live, and full
+        (4096, 12288, 17, "resident_gated_t32_c4+gather", "tile_64x128_k8"),
+        (4096, 12288, 32, "resident_gated_t32_c4+gather", "tile_64x128_k8"),
+        (2560, 9728, 27, "resident_gated_t32_c3+gather", "tile_64x128_k8"),
+        (4088, 8200, 23, "resident_gated_t32_c4+gather", "tile_64x128_k8"),
     ],
 )
 def test_resident_step_matches_oracle(device, normed, hidden, intermediate, rows, gate_up, down):
-    # 9 to 16 rows: the token rows stay in registers of a one-per-CU grid; gate_up gathers and
+    # 9 to 32 rows: the token rows stay in registers of a one-per-CU grid; gate_up gathers and
     # normalises them itself (its sum of squares runs in its own order, so it agrees with the
     # gather kernel within one bf16 ulp, not bit for bit).  Checked against the oracle's
     # mailbox step; replays repeat bit for bit, also through graph dispatch.
@@ -188,7 +194,7 @@ def test_resident_step_matches_oracle(device, normed, hidden, intermediate, rows
                 instance_index=0, layer_ordinal=0, weights=_weights(w_gate_up, w_down, device),
                 norm_weight=to_device(norm_weight, device) if normed else None,
             )
-            agent.materialize(maximum_row_capacity=16)
+            agent.materialize(maximum_row_capacity=32)
             for _ in range(2):
                 pool_gpu = to_device(pool, device)
                 agent.execute(instance_index=0, layer_ordinal=0, pool=pool_gpu, slots=slots_tensor(slots, device))
@@ -199,27 +205,32 @@ def test_resident_step_matches_oracle(device, normed, hidden, intermediate, rows
     _check_mailbox(outputs[0], pool, slots, w_gate_up, w_down, norm_weight if normed else None)
 
 
-def test_resident_gather_poisons_bad_slots(device):
+@pytest.mark.parametrize("hidden,intermediate,rows,gate_up", [
+    (2048, 6144, 12, "resident_gated_t16_c2+gather"),
+    (2048, 8192, 29, "resident_gated_t32_c2+gather"),
+])
+def test_resident_gather_poisons_bad_slots(device, hidden, intermediate, rows, gate_up):
     # A slot outside the mailbox: its row is staged as quiet NaNs, its output is dropped, the
-    # fault bit is raised, and the other rows are their own FFN.
-    hidden, intermediate, pool_rows = 2048, 6144, 64
-    assert _native.dense_gate_up_variant(12, hidden, intermediate).startswith("resident")
+    # fault bit is raised, and the other rows are their own FFN (two and four token groups;
+    # with four the bad row sits in the third group).
+    pool_rows = 64
+    assert _native.dense_gate_up_variant(rows, hidden, intermediate) == gate_up
     pool = o.generate_hidden_states(pool_rows, hidden, 41)
     w_gate_up, w_down, norm_weight = o.generate_layer(hidden, intermediate, 42)
-    slots = o.generate_slots(pool_rows, 12, 43)
+    slots = o.generate_slots(pool_rows, rows, 43)
     bad = slots.copy()
-    bad[5] = pool_rows + 7
+    bad[5 if rows <= 16 else 20] = pool_rows + 7
     with FfnAgent(device) as agent:
         agent.register_layer(
             instance_index=0, layer_ordinal=0, weights=_weights(w_gate_up, w_down, device),
             norm_weight=to_device(norm_weight, device),
         )
-        agent.materialize(maximum_row_capacity=16)
+        agent.materialize(maximum_row_capacity=32)
         pool_gpu = to_device(pool, device)
         agent.execute(instance_index=0, layer_ordinal=0, pool=pool_gpu, slots=slots_tensor(bad, device))
         with pytest.raises(FfnHealthError):
             agent.check_health()
-    live = np.delete(slots, 5)
+    live = np.delete(slots, 5 if rows <= 16 else 20)
     _check_mailbox(pool_gpu, pool, live, w_gate_up, w_down, norm_weight)
 
 

@@ -63,6 +63,7 @@ def _check(new_pool_gpu, pool, slots, w_gate_up, w_down, norm_weight):
         (1024, 3072, 300, "tile_gated_64x128"),
         (4096, 12288, 1, "split_gated_t8_k8_persistent+gather"),
         (4096, 12288, 16, "resident_gated_t16_c4+gather"),
+        (4096, 12288, 32, "resident_gated_t32_c4+gather"),
         (4096, 12288, 2048, "tile_gated_256x256"),
     ],
 )

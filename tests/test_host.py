@@ -365,7 +365,15 @@ def test_dense_step_fuses_the_gather_at_decode_sizes():
         assert _native.dense_gate_up_variant(rows, 4096, 12288) == "resident_gated_t16_c4+gather"
         assert _native.dense_gate_up_variant(rows, 1024, 3072) == "resident_gated_t16_c1+gather"
         assert "+gather" not in _native.dense_gate_up_variant(rows, 5120, 3200)
-    assert _native.dense_gate_up_variant(32, 4096, 12288) == "tile_gated_64x64"
+    # 17 to 32 rows: four token groups where gate_up has at least 16384 weight rows (Qwen3-4B
+    # and 8B), the tile kernels on a separate gather below that (Qwen3-1.7B)
+    for rows in (17, 32):
+        assert _native.dense_gate_up_variant(rows, 4096, 12288) == "resident_gated_t32_c4+gather"
+        assert _native.dense_gate_up_variant(rows, 2560, 9728) == "resident_gated_t32_c3+gather"
+        assert "+gather" not in _native.dense_gate_up_variant(rows, 2048, 6144)
+    assert _native.dense_gate_up_variant(33, 4096, 12288) == "tile_gated_64x128"
+    # kernel-level projections (no gather) keep the 16-row ceiling
+    assert _native.gemm_variant(32, 24576, 4096, True) == "tile_gated_64x64"
     assert _native.dense_gate_up_variant(2048, 4096, 12288) == "tile_gated_256x256"
 
 
