@@ -6,7 +6,8 @@ RMSNorm, gate_up [4096 -> 2 x 12288] + SiLU*mul, down [12288 -> 4096],
 scatter back into the same slots.  Inputs are resident in HBM before timing.
 
 Prints ONE JSON line: the headline at T = --tokens (default 2048, the
-MFMA-bound north-star point), a ``decode`` entry at T = 32 (HBM-bound), the
+MFMA-bound north-star point), a ``decode`` entry at T = 32 (HBM-bound: the layer,
+and the kernel-level gate_up's roofline beside the name of the kernel the layer runs), the
 batch sweep of BASELINE config 3, the roofline of the dominant kernel
 (measured with HIP events on the Lane stream it runs on) and the CPU
 baseline (the oracle's torch-CPU restatement on the host cores).
@@ -460,7 +461,10 @@ def main() -> int:
         "tokens_per_s": round(args.decode_tokens / decode_seconds, 1),
         "us_per_layer": round(decode_seconds * 1e6, 2),
         "layer_hbm_frac": round(layer_bytes(args.decode_tokens) / decode_seconds / 1e9 / HBM_PEAK_GBS, 4),
+        # The kernel-level gate_up at this size (no gather); the Dense step may run another
+        # kernel for it (the gather fused into the resident kernel at 9-32 rows), named here.
         "roofline": kernel_roofline(args.decode_tokens, 200),
+        "layer_gate_up": _native.dense_gate_up_variant(args.decode_tokens, HIDDEN, INTERMEDIATE),
     }
 
     # ---------------------------------------------------------------- sweep
