@@ -34,44 +34,61 @@ __global__ __launch_bounds__(256) void copy_bytes_kernel(CopyArgs a) {
 
 // One wavefront per row; CHUNKS 16-byte chunks per lane stay in registers between the
 // sum-of-squares reduction and the normalised store (hidden <= CHUNKS * 512).  The norm
-// weight is loaded together with the row, so a row costs one memory round trip, not two.
+// weights go to LDS once per workgroup (its four rows share them), requested right behind
+// the rows, so a row still costs one memory round trip, and the registers hold the row
+// only: with a copy of the weights per wave as well, hidden 4096 took 147 VGPRs (three
+// waves per SIMD) and hidden 5120 or 8192 all 256 (one).
+// 16-byte store through a buffer resource: offsets past the resource's end are dropped.
+__device__ __forceinline__ void buffer_store16(__amdgpu_buffer_rsrc_t rsrc, uint32_t offset, u32x4 value) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned int, value),
+                                         rsrc, static_cast<int>(offset), 0, 0);
+}
+
 template <int CHUNKS, class P>
 __global__ __launch_bounds__(256) void gather_rows_kernel(GatherArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t norm_lds[CHUNKS * kWave * 8];
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (row >= a.rows) {
+  const int64_t chunks = a.hidden >> 3;
+  const bool live = row < a.rows;
+  const int32_t slot = live ? a.slots[row] : 0;
+  const bool bad = live && (slot < 0 || static_cast<int64_t>(slot) >= a.pool_rows);
+  const uint32_t row_bytes = static_cast<uint32_t>(a.hidden * 2);
+  // The row through a buffer resource of its own: chunk c of lane l sits at byte offset
+  // 16 l + 1024 c, a constant per chunk, and chunks past the row read as zero.
+  const __amdgpu_buffer_rsrc_t source =
+      make_rsrc(a.pool + static_cast<int64_t>(live && !bad ? slot : 0) * a.hidden, live && !bad ? row_bytes : 0u);
+  const uint32_t lane_bytes = static_cast<uint32_t>(lane * 16);
+  u32x4 values[CHUNKS];
+#pragma unroll
+  for (int index = 0; index < CHUNKS; ++index) {
+    values[index] = buffer_load16(source, lane_bytes + index * kWave * 16);
+  }
+  if (a.norm != nullptr) {  // uniform: every wave reaches the barrier
+    for (int64_t chunk = threadIdx.x; chunk < chunks; chunk += 256) {
+      store16(norm_lds + chunk * 8, load16(a.norm + chunk * 8));
+    }
+    __syncthreads();
+  }
+  if (!live) {
     return;
   }
-  const int64_t chunks = a.hidden >> 3;
-  uint16_t *destination = a.out + row * a.hidden;
-  const int32_t slot = a.slots[row];
-  if (slot < 0 || static_cast<int64_t>(slot) >= a.pool_rows) {
+  const __amdgpu_buffer_rsrc_t destination = make_rsrc(a.out + row * a.hidden, row_bytes);
+  if (bad) {
     // Canonical failure: poison the row with quiet NaNs and raise the sticky fault bit.
     const u32x4 poison = {P::kPoison2, P::kPoison2, P::kPoison2, P::kPoison2};
     for (int64_t chunk = lane; chunk < chunks; chunk += kWave) {
-      store16(destination + chunk * 8, poison);
+      buffer_store16(destination, static_cast<uint32_t>(chunk * 16), poison);
     }
     if (lane == 0) {
       raise_fault(a.fault, kFaultSlotOutOfRange);
     }
     return;
   }
-  const uint16_t *source = a.pool + static_cast<int64_t>(slot) * a.hidden;
-  u32x4 values[CHUNKS];
-  u32x4 weights[CHUNKS];
-#pragma unroll
-  for (int index = 0; index < CHUNKS; ++index) {
-    const int64_t chunk = lane + index * kWave;
-    values[index] = chunk < chunks ? load16(source + chunk * 8) : u32x4{0u, 0u, 0u, 0u};
-    weights[index] = chunk < chunks && a.norm != nullptr ? load16(a.norm + chunk * 8) : u32x4{0u, 0u, 0u, 0u};
-  }
   if (a.norm == nullptr) {
 #pragma unroll
     for (int index = 0; index < CHUNKS; ++index) {
-      const int64_t chunk = lane + index * kWave;
-      if (chunk < chunks) {
-        store16(destination + chunk * 8, values[index]);
-      }
+      buffer_store16(destination, lane_bytes + index * kWave * 16, values[index]);
     }
     return;
   }
@@ -82,12 +99,17 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(GatherArgs a) {
     add_squares<P>(values[index], squares);
   }
   const float inverse = rms_inverse(squares, a.hidden, a.eps);
+  // The row's bits are opaque here, so the compiler widens them again rather than keeping
+  // the sum of squares' fp32 copies (twice the registers) alive across the reduction.
+#pragma unroll
+  for (int index = 0; index < CHUNKS; ++index) {
+    __asm__ volatile("" : "+v"(values[index]));
+  }
 #pragma unroll
   for (int index = 0; index < CHUNKS; ++index) {
     const int64_t chunk = lane + index * kWave;
-    if (chunk < chunks) {
-      store16(destination + chunk * 8, normalize_chunk<P>(values[index], inverse, weights[index]));
-    }
+    const u32x4 weight = chunk < chunks ? load16(norm_lds + chunk * 8) : u32x4{0u, 0u, 0u, 0u};
+    buffer_store16(destination, lane_bytes + index * kWave * 16, normalize_chunk<P>(values[index], inverse, weight));
   }
 }
 
