@@ -55,6 +55,7 @@ class MoeLayerDesc(ctypes.Structure):
         ("alpha", ctypes.c_float),
         ("limit", ctypes.c_float),
         ("up_offset", ctypes.c_float),
+        ("payload", ctypes.c_int),
     ]
 
 
@@ -116,12 +117,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "xp_transport_probe": (_INT, [_P, _INT, _INT, ctypes.POINTER(ctypes.c_uint32), _INT]),
     "xp_moe_router_topk": (_INT, [_P, _INT, _I64, _I64, _I64, _INT, _P, _INT, _INT, _P, _P, _P]),
     "xp_moe_router_workspace_bytes": (_SIZE, [_I64, _I64, _I64, _INT]),
-    "xp_moe_router": (_INT, [_P, _I64, _I64, _P, _I64, _I64, _INT, _INT, _P, _INT, _INT, _P, _P, _P, _SIZE, _P]),
+    "xp_moe_router": (_INT, [_P, _I64, _I64, _P, _I64, _I64, _INT, _INT, _INT, _P, _INT, _INT, _P, _P, _P, _SIZE, _P]),
     "xp_moe_finalize_routing": (_INT, [_P, _P, _I64, _I64, _P, _P, _I64, _P, _I64, _F32, _P]),
     "xp_moe_workspace_bytes": (_SIZE, [_I64, _I64, _I64, _I64, _I64]),
     "xp_moe_workspace_layout": (_INT, [_I64, _I64, _I64, _I64, _I64, ctypes.POINTER(_SIZE)]),
     "xp_moe_experts": (
-        _INT, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _F32, _F32, _F32, _F32, _P, _P, _SIZE, _P]
+        _INT, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _F32, _F32, _F32, _F32, _INT, _P, _P, _SIZE, _P]
     ),
     "xp_moe_layer_register": (_INT, [_P, _INT, _INT, ctypes.POINTER(MoeLayerDesc), _P, _P, _P, _P, _P, _F32]),
     "xp_moe_step_workspace_bytes": (_SIZE, [ctypes.POINTER(MoeLayerDesc), _I64]),
@@ -191,7 +192,7 @@ def call(name: str, *args: object) -> int:
 
 
 def payload_dtype_code(dtype: object) -> int:
-    """XP_DTYPE_BF16 / XP_DTYPE_F16 of a Dense payload dtype (torch.bfloat16 / torch.float16)."""
+    """XP_DTYPE_BF16 / XP_DTYPE_F16 of a payload dtype (torch.bfloat16 / torch.float16)."""
 
     import torch
 
@@ -199,7 +200,7 @@ def payload_dtype_code(dtype: object) -> int:
         return XP_DTYPE_BF16
     if dtype is torch.float16:
         return XP_DTYPE_F16
-    raise ValueError(f"Dense payloads are bf16 or fp16, not {dtype}")
+    raise ValueError(f"payloads are bf16 or fp16, not {dtype}")
 
 
 def gemm_variant(capacity: int, n: int, k: int, gated: bool) -> str:

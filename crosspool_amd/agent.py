@@ -82,9 +82,9 @@ class LayerBinding:
 
     @property
     def payload_dtype(self) -> torch.dtype:
-        """The dtype of the layer's mailboxes: its weights' (Dense: bf16 or fp16; MoE: bf16)."""
+        """The dtype of the layer's mailboxes: its weights' (bf16 or fp16)."""
 
-        return self.weights.payload_dtype if self.moe is None else torch.bfloat16
+        return self.weights.payload_dtype
 
 
 class FfnHealthError(RuntimeError):
@@ -360,13 +360,13 @@ class FfnAgent:
         spec.validate_weights(weights)
         if norm_weight is not None:
             validate_weight_tensor(norm_weight, name="RMSNorm weight")
-            if norm_weight.dtype is not torch.bfloat16 or tuple(norm_weight.shape) != (weights.hidden_size,):
-                raise ValueError("RMSNorm weight must be a bf16 [H] vector")
+            if norm_weight.dtype is not weights.payload_dtype or tuple(norm_weight.shape) != (weights.hidden_size,):
+                raise ValueError(f"RMSNorm weight must be a {weights.payload_dtype} [H] vector")
             if norm_weight.device != self.device:
                 raise ValueError("RMSNorm weight must reside on the agent's device")
         signature = spec.signature(
             hidden_size=weights.hidden_size, local_intermediate_size=weights.local_intermediate_size,
-            payload_row_capacity=1,
+            payload_row_capacity=1, payload_dtype=weights.payload_dtype,
         )
         router = weights.router
         _native.call(
@@ -452,6 +452,7 @@ class FfnAgent:
                     hidden_size=binding.weights.hidden_size,
                     local_intermediate_size=binding.weights.local_intermediate_size,
                     payload_row_capacity=capacity,
+                    payload_dtype=binding.payload_dtype,
                 ))
                 self.templates.setdefault(template.key, template)
         workspace_bytes = max(t.workspace_bytes for t in self.templates.values())

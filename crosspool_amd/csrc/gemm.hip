@@ -743,7 +743,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) __attribute__((amdgpu_waves_per_e
 // set, times row_scale[p] when that is set.  A wave's chunk count is rounded up to whole
 // groups of DEPTH; the chunks past its range load through an out-of-range offset, which
 // reads zeros without a memory access.
-template <int DEPTH, bool GATED>
+template <int DEPTH, bool GATED, class P = Bf16Payload>
 __global__ __launch_bounds__(64 * kSplitWaves) void grouped_split_kernel(GemmArgs a) {
   constexpr int TG = 2;  // groups of 8 routes
   // Both table words are loaded before the branch: the loads that follow depend on them,
@@ -857,8 +857,8 @@ __global__ __launch_bounds__(64 * kSplitWaves) void grouped_split_kernel(GemmArg
 #pragma unroll
         for (int g = 0; g < TG; ++g) {
           const u32x4 xk = valid ? x[line][g] : zero;
-          acc[g][0] = Bf16Payload::mfma16(w0, xk, acc[g][0]);
-          acc[g][1] = Bf16Payload::mfma16(w1, xk, acc[g][1]);
+          acc[g][0] = P::mfma16(w0, xk, acc[g][0]);
+          acc[g][1] = P::mfma16(w1, xk, acc[g][1]);
         }
       }
     };
@@ -942,12 +942,12 @@ __global__ __launch_bounds__(64 * kSplitWaves) void grouped_split_kernel(GemmArg
         continue;
       }
       if constexpr (GATED) {
-        const float h0 = gated_silu(sum[g][h][0], sum[g][h][1], a.act);
-        const float h1 = gated_silu(sum[g][h][2], sum[g][h][3], a.act);
-        *reinterpret_cast<uint32_t *>(out + n / 2) = pack_bf16x2(h0, h1);
+        const float h0 = gated_silu_payload<P>(sum[g][h][0], sum[g][h][1], a.act);
+        const float h1 = gated_silu_payload<P>(sum[g][h][2], sum[g][h][3], a.act);
+        *reinterpret_cast<uint32_t *>(out + n / 2) = P::pack2(h0, h1);
       } else {
         const float f = factor[g];
-        u32x2 packed = {pack_bf16x2(sum[g][h][0] * f, sum[g][h][1] * f), pack_bf16x2(sum[g][h][2] * f, sum[g][h][3] * f)};
+        u32x2 packed = {P::pack2(sum[g][h][0] * f, sum[g][h][1] * f), P::pack2(sum[g][h][2] * f, sum[g][h][3] * f)};
         *reinterpret_cast<u32x2 *>(out + n) = packed;
       }
     }
@@ -2935,29 +2935,35 @@ GroupedTile grouped_tile(MoeTile tile, bool gated) {
   }
 }
 
-template <bool GATED>
+template <bool GATED, class P>
 const void *grouped_tile_kernel(MoeTile tile) {
   switch (tile) {
     case MoeTile::Rows64:
-      return reinterpret_cast<const void *>(&tile_gemm_kernel<64, 128, 2, 2, 3, GATED, true, true>);
+      return reinterpret_cast<const void *>(&tile_gemm_kernel<64, 128, 2, 2, 3, GATED, true, true, P>);
     case MoeTile::Rows128Stream:
-      return GATED ? reinterpret_cast<const void *>(&tile_gemm_kernel<128, 256, 2, 4, 3, GATED, true, true>)
-                   : reinterpret_cast<const void *>(&tile_gemm_kernel<128, 128, 4, 2, 2, GATED, true, true>);
+      return GATED ? reinterpret_cast<const void *>(&tile_gemm_kernel<128, 256, 2, 4, 3, GATED, true, true, P>)
+                   : reinterpret_cast<const void *>(&tile_gemm_kernel<128, 128, 4, 2, 2, GATED, true, true, P>);
     case MoeTile::Rows128:
-      return GATED ? reinterpret_cast<const void *>(&tile_gemm_kernel<128, 256, 2, 4, 3, GATED, true, false>)
-                   : reinterpret_cast<const void *>(&tile_gemm_kernel<128, 128, 4, 2, 2, GATED, true, false>);
+      return GATED ? reinterpret_cast<const void *>(&tile_gemm_kernel<128, 256, 2, 4, 3, GATED, true, false, P>)
+                   : reinterpret_cast<const void *>(&tile_gemm_kernel<128, 128, 4, 2, 2, GATED, true, false, P>);
     case MoeTile::Rows256:
-      return reinterpret_cast<const void *>(&tile_gemm_kernel<256, 128, 4, 2, 3, GATED, true, true>);
+      return reinterpret_cast<const void *>(&tile_gemm_kernel<256, 128, 4, 2, 3, GATED, true, true, P>);
     default:
       return nullptr;
   }
+}
+
+template <bool GATED>
+const void *grouped_tile_kernel(MoeTile tile, int32_t payload) {
+  return payload == kPayloadF16 ? grouped_tile_kernel<GATED, F16Payload>(tile)
+                                : grouped_tile_kernel<GATED, Bf16Payload>(tile);
 }
 
 int grouped_tile_rows(MoeTile tile) { return grouped_tile(tile, true).bm; }  // the same for down
 
 KernelLaunch make_grouped_gemm(const GemmArgs &args, bool gated, int max_tiles, MoeTile tile) {
   const GroupedTile shape = grouped_tile(tile, gated);
-  const void *func = gated ? grouped_tile_kernel<true>(tile) : grouped_tile_kernel<false>(tile);
+  const void *func = gated ? grouped_tile_kernel<true>(tile, args.payload) : grouped_tile_kernel<false>(tile, args.payload);
   if (max_tiles % 8 != 0 || func == nullptr) {
     return KernelLaunch{};  // grouped_tile_coordinates needs a multiple of 8 (callers pad)
   }
@@ -3007,8 +3013,13 @@ KernelLaunch make_grouped_split(const GemmArgs &args, bool gated, int max_tiles,
   record.k_slice = (chunks + ksplit - 1) / ksplit * 128;
   record.partials = nullptr;
   KernelLaunch kernel;
-  kernel.func = gated ? reinterpret_cast<const void *>(&grouped_split_kernel<kGroupedSplitDepth, true>)
-                      : reinterpret_cast<const void *>(&grouped_split_kernel<kGroupedSplitDepth, false>);
+  if (args.payload == kPayloadF16) {
+    kernel.func = gated ? reinterpret_cast<const void *>(&grouped_split_kernel<kGroupedSplitDepth, true, F16Payload>)
+                        : reinterpret_cast<const void *>(&grouped_split_kernel<kGroupedSplitDepth, false, F16Payload>);
+  } else {
+    kernel.func = gated ? reinterpret_cast<const void *>(&grouped_split_kernel<kGroupedSplitDepth, true>)
+                        : reinterpret_cast<const void *>(&grouped_split_kernel<kGroupedSplitDepth, false>);
+  }
   kernel.grid = dim3(static_cast<unsigned>((row_blocks * ksplit + kSplitWaves - 1) / kSplitWaves),
                      static_cast<unsigned>(max_tiles), 1);
   kernel.block = dim3(64 * kSplitWaves, 1, 1);

@@ -48,6 +48,32 @@ __device__ __forceinline__ uint32_t ordered_bits(float value) {
   return (bits & 0x80000000u) != 0 ? ~bits : bits | 0x80000000u;
 }
 
+// One fp32 value rounded to the 16-bit payload P (bf16 or fp16, round to nearest even), as
+// bits and back: the rounding points of the reference's payload-dtype logits and weights.
+template <class P>
+__device__ __forceinline__ uint32_t payload_bits(float value);
+template <>
+__device__ __forceinline__ uint32_t payload_bits<Bf16Payload>(float value) {
+  return float_to_bf16(value);
+}
+template <>
+__device__ __forceinline__ uint32_t payload_bits<F16Payload>(float value) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(value));
+}
+template <class P>
+__device__ __forceinline__ float payload_round(float value) {
+  return P::widen(payload_bits<P>(value));
+}
+
+// The same with the payload chosen at run time (PayloadKind), for the FP32-precision
+// Router logits kernel, whose inner loop is LDS arithmetic.
+__device__ __forceinline__ float payload_widen(uint32_t bits16, int32_t payload) {
+  return payload == kPayloadF16 ? F16Payload::widen(bits16) : Bf16Payload::widen(bits16);
+}
+__device__ __forceinline__ uint32_t payload_bits(float value, int32_t payload) {
+  return payload == kPayloadF16 ? payload_bits<F16Payload>(value) : payload_bits<Bf16Payload>(value);
+}
+
 // ------------------------------------------------------------------ router
 // One wavefront per row; lane l holds experts l, l + 64, ... (PER_LANE each: the fewest of
 // 2, 4, 8 or 16 that cover the expert count, so a 128-expert Router selects over two
@@ -61,7 +87,8 @@ __host__ __device__ constexpr int topk_per_lane(int experts) {
 }
 
 // TopK of row `row` by the calling wavefront (all 64 lanes); experts <= PER_LANE * 64.
-template <int PER_LANE>
+// P is the dtype of 16-bit logits (a.payload): their widening and rounding points.
+template <int PER_LANE, class P>
 __device__ void router_topk_row(const RouterTopkArgs &a, int64_t row, int lane) {
   constexpr int kTopkPerLane = PER_LANE;
   const int experts = a.experts;
@@ -101,10 +128,10 @@ __device__ void router_topk_row(const RouterTopkArgs &a, int64_t row, int lane) 
       const int expert = lane + i * kWave;
       float value = kNegativeInfinity;
       if (expert < experts) {
-        // One rounding of the sum to bf16, stored as the logit.
-        const uint32_t bits = float_to_bf16(sum[i]);
+        // One rounding of the sum to the payload dtype, stored as the logit.
+        const uint32_t bits = payload_bits<P>(sum[i]);
         a.logits_out[row * experts + expert] = static_cast<uint16_t>(bits);
-        value = bf16_to_float(bits);
+        value = P::widen(bits);
       }
       logit[i] = value;
       maximum = fmaxf(maximum, value);
@@ -117,7 +144,7 @@ __device__ void router_topk_row(const RouterTopkArgs &a, int64_t row, int lane) 
       if (expert < experts) {
         const int64_t index = row * experts + expert;
         value = a.logits_f32 != 0 ? static_cast<const float *>(a.logits)[index]
-                                  : bf16_to_float(static_cast<const uint16_t *>(a.logits)[index]);
+                                  : P::widen(static_cast<const uint16_t *>(a.logits)[index]);
       }
       logit[i] = value;
       maximum = fmaxf(maximum, value);
@@ -155,9 +182,9 @@ __device__ void router_topk_row(const RouterTopkArgs &a, int64_t row, int lane) 
       value += a.correction_bias[expert];
     }
     // Sigmoid stores the selection into the logits buffer and reads it back
-    // (routing.py:62-65): bf16 logits round it there.
+    // (routing.py:62-65): 16-bit logits round it there.
     if (a.softmax == 0 && a.logits_f32 == 0) {
-      value = round_bf16(value);
+      value = payload_round<P>(value);
     }
     const uint32_t tie = a.softmax != 0 ? static_cast<uint32_t>(kMoeMaxExperts - 1 - expert)
                                         : static_cast<uint32_t>(expert);
@@ -200,18 +227,18 @@ __device__ void router_topk_row(const RouterTopkArgs &a, int64_t row, int lane) 
       weight = weight / (normalizer > 0.0f ? normalizer : 1.0f);
     }
     if (a.round_to_logits != 0 && a.logits_f32 == 0) {
-      weight = round_bf16(weight);
+      weight = payload_round<P>(weight);
     }
     a.ids[row * a.topk + lane] = chosen_id;
     a.weights[row * a.topk + lane] = weight;
   }
 }
 
-template <int PER_LANE>
+template <int PER_LANE, class P>
 __global__ __launch_bounds__(256) void router_topk_kernel(RouterTopkArgs a) {
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (row < a.rows) {
-    router_topk_row<PER_LANE>(a, row, threadIdx.x & (kWave - 1));
+    router_topk_row<PER_LANE, P>(a, row, threadIdx.x & (kWave - 1));
   }
 }
 
@@ -219,7 +246,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(RouterTopkArgs a) {
 // does not suit the MFMA projection (hidden or expert count not a multiple of 8): a
 // workgroup computes a 16-row x 64-expert block; thread t owns row t / 16 and experts
 // 4 (t % 16) .. + 3, each a sequential fp32 sum over the hidden dimension staged through LDS
-// 64 columns at a time, stored as fp32 or rounded once to bf16.
+// 64 columns at a time, stored as fp32 or rounded once to the payload dtype.
 __global__ __launch_bounds__(256) void router_logits_kernel(RouterLogitsArgs a) {
   constexpr int ROWS = 16;
   constexpr int EXPERTS = 64;
@@ -237,7 +264,7 @@ __global__ __launch_bounds__(256) void router_logits_kernel(RouterLogitsArgs a) 
       const int r = index / CHUNK;
       const int c = index % CHUNK;
       const int64_t row = row0 + r;
-      xs[r][c] = row < a.rows && k0 + c < a.hidden ? bf16_to_float(a.x[row * a.hidden + k0 + c]) : 0.0f;
+      xs[r][c] = row < a.rows && k0 + c < a.hidden ? payload_widen(a.x[row * a.hidden + k0 + c], a.payload) : 0.0f;
     }
     for (int index = tid; index < EXPERTS * CHUNK; index += 256) {
       const int e = index / CHUNK;
@@ -247,7 +274,7 @@ __global__ __launch_bounds__(256) void router_logits_kernel(RouterLogitsArgs a) 
       if (expert < a.experts && k0 + c < a.hidden) {
         const int64_t offset = static_cast<int64_t>(expert) * a.hidden + k0 + c;
         value = a.weights_f32 != 0 ? static_cast<const float *>(a.w)[offset]
-                                   : bf16_to_float(static_cast<const uint16_t *>(a.w)[offset]);
+                                   : payload_widen(static_cast<const uint16_t *>(a.w)[offset], a.payload);
       }
       ws[e][c] = value;
     }
@@ -268,8 +295,8 @@ __global__ __launch_bounds__(256) void router_logits_kernel(RouterLogitsArgs a) 
     for (int j = 0; j < 4; ++j) {
       const int expert = expert0 + my_expert + j;
       if (expert < a.experts) {
-        if (a.out_bf16 != 0) {
-          static_cast<uint16_t *>(a.logits)[row * a.experts + expert] = static_cast<uint16_t>(float_to_bf16(acc[j]));
+        if (a.out_payload != 0) {
+          static_cast<uint16_t *>(a.logits)[row * a.experts + expert] = static_cast<uint16_t>(payload_bits(acc[j], a.payload));
         } else {
           static_cast<float *>(a.logits)[row * a.experts + expert] = acc[j];
         }
@@ -345,6 +372,8 @@ constexpr int kSortStagedRoutes = 1024 * kSortRoutesPerThread;
 // The fused TopK gives each of the workgroup's waves one row.
 static_assert(kMoeFusedTopkRows <= 1024 / kWave, "one wave of moe_sort_kernel per fused TopK row");
 
+// P: the payload of the fused TopK's 16-bit logits (the sort itself is dtype-free).
+template <class P>
 __global__ __launch_bounds__(1024) void moe_sort_kernel(MoeSortArgs a) {
   __shared__ int counts[kMoeMaxExperts];
   __shared__ int offsets[kMoeMaxExperts + 1];
@@ -359,13 +388,13 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(MoeSortArgs a) {
     if ((tid >> 6) < a.topk.rows) {
       const int per_lane = topk_per_lane(a.topk.experts);
       if (per_lane == 2) {
-        router_topk_row<2>(a.topk, tid >> 6, tid & (kWave - 1));
+        router_topk_row<2, P>(a.topk, tid >> 6, tid & (kWave - 1));
       } else if (per_lane == 4) {
-        router_topk_row<4>(a.topk, tid >> 6, tid & (kWave - 1));
+        router_topk_row<4, P>(a.topk, tid >> 6, tid & (kWave - 1));
       } else if (per_lane == 8) {
-        router_topk_row<8>(a.topk, tid >> 6, tid & (kWave - 1));
+        router_topk_row<8, P>(a.topk, tid >> 6, tid & (kWave - 1));
       } else {
-        router_topk_row<kTopkMaxPerLane>(a.topk, tid >> 6, tid & (kWave - 1));
+        router_topk_row<kTopkMaxPerLane, P>(a.topk, tid >> 6, tid & (kWave - 1));
       }
     }
     __syncthreads();
@@ -464,11 +493,12 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(MoeSortArgs a) {
 }
 
 // ------------------------------------------------------------------ combine
-// out[row] = bf16(scale * sum over the row's live routes, in slot order, of float(route
-// output)) -- the route reduction with the routed scaling factor (moe.py:336-343); rows
-// whose slots are all -1 read 0.  With slots the sum of row r goes to out row slots[r]
-// (the mailbox scatter); a slot outside the mailbox is skipped (the gather that read it
-// has raised the Lane's fault bit).
+// out[row] = p(scale * sum over the row's live routes, in slot order, of float(route
+// output)), p the payload rounding (bf16 or fp16) -- the route reduction with the routed
+// scaling factor (moe.py:336-343); rows whose slots are all -1 read 0.  With slots the sum
+// of row r goes to out row slots[r] (the mailbox scatter); a slot outside the mailbox is
+// skipped (the gather that read it has raised the Lane's fault bit).
+template <class P>
 __global__ __launch_bounds__(256) void moe_combine_kernel(MoeCombineArgs a) {
   const int64_t chunks = a.hidden / 8;
   const int64_t index = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
@@ -507,15 +537,15 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(MoeCombineArgs a) {
       }
 #pragma unroll
       for (int word = 0; word < 4; ++word) {
-        sum[2 * word] += bf16_to_float(values[b][word] & 0xffffu);
-        sum[2 * word + 1] += bf16_to_float(values[b][word] >> 16);
+        sum[2 * word] += P::widen(values[b][word] & 0xffffu);
+        sum[2 * word + 1] += P::widen(values[b][word] >> 16);
       }
     }
   }
   u32x4 packed;
 #pragma unroll
   for (int word = 0; word < 4; ++word) {
-    packed[word] = pack_bf16x2(sum[2 * word] * a.scale, sum[2 * word + 1] * a.scale);
+    packed[word] = P::pack2(sum[2 * word] * a.scale, sum[2 * word + 1] * a.scale);
   }
   store16(a.out + out_row * a.hidden + chunk * 8, packed);
 }
@@ -569,12 +599,18 @@ MoeTile choose_moe_tile(int64_t routes, int64_t experts) {
   return routes <= 160 * experts ? MoeTile::Rows128 : MoeTile::Rows256;
 }
 
+template <class P>
+const void *router_topk_kernel_for(int per_lane) {
+  return per_lane == 2   ? reinterpret_cast<const void *>(&router_topk_kernel<2, P>)
+         : per_lane == 4 ? reinterpret_cast<const void *>(&router_topk_kernel<4, P>)
+         : per_lane == 8 ? reinterpret_cast<const void *>(&router_topk_kernel<8, P>)
+                         : reinterpret_cast<const void *>(&router_topk_kernel<kTopkMaxPerLane, P>);
+}
+
 KernelLaunch make_router_topk(const RouterTopkArgs &args) {
   const int per_lane = topk_per_lane(args.experts);
-  const void *kernel = per_lane == 2   ? reinterpret_cast<const void *>(&router_topk_kernel<2>)
-                       : per_lane == 4 ? reinterpret_cast<const void *>(&router_topk_kernel<4>)
-                       : per_lane == 8 ? reinterpret_cast<const void *>(&router_topk_kernel<8>)
-                                       : reinterpret_cast<const void *>(&router_topk_kernel<kTopkMaxPerLane>);
+  const void *kernel = args.payload == kPayloadF16 ? router_topk_kernel_for<F16Payload>(per_lane)
+                                                   : router_topk_kernel_for<Bf16Payload>(per_lane);
   return launch_of(kernel, dim3(blocks_for(args.rows, 4)), 256, args);
 }
 
@@ -589,11 +625,15 @@ KernelLaunch make_finalize_routing(const FinalizeRoutingArgs &args) {
 }
 
 KernelLaunch make_moe_sort(const MoeSortArgs &args) {
-  return launch_of(reinterpret_cast<const void *>(&moe_sort_kernel), dim3(1), 1024, args);
+  const bool f16 = args.fused_topk != 0 && args.topk.payload == kPayloadF16;
+  return launch_of(f16 ? reinterpret_cast<const void *>(&moe_sort_kernel<F16Payload>)
+                       : reinterpret_cast<const void *>(&moe_sort_kernel<Bf16Payload>),
+                   dim3(1), 1024, args);
 }
 
 KernelLaunch make_moe_combine(const MoeCombineArgs &args) {
-  return launch_of(reinterpret_cast<const void *>(&moe_combine_kernel),
+  return launch_of(args.payload == kPayloadF16 ? reinterpret_cast<const void *>(&moe_combine_kernel<F16Payload>)
+                                                : reinterpret_cast<const void *>(&moe_combine_kernel<Bf16Payload>),
                    dim3(blocks_for(args.rows * (args.hidden / 8), 256)), 256, args);
 }
 

@@ -120,7 +120,7 @@ GatedSilu default_activation() { return GatedSilu{1.0f, 0.0f, 0.0f}; }
 // The Dense payload dtype of the ABI (XP_DTYPE_BF16 / XP_DTYPE_F16, ffn.hpp:83-85) as the
 // kernels' PayloadKind.
 int payload_kind(int dtype, int32_t &out) {
-  XP_REQUIRE(dtype == XP_DTYPE_BF16 || dtype == XP_DTYPE_F16, "Dense payload dtype must be bf16 or fp16");
+  XP_REQUIRE(dtype == XP_DTYPE_BF16 || dtype == XP_DTYPE_F16, "payload dtype must be bf16 or fp16");
   out = dtype == XP_DTYPE_F16 ? kPayloadF16 : kPayloadBf16;
   return XP_OK;
 }
@@ -299,7 +299,7 @@ struct Layer {
   const uint16_t *down;
   const uint16_t *norm;
   float eps;
-  int32_t payload = kPayloadBf16;  // Dense layers: PayloadKind of weights, norm and mailbox
+  int32_t payload = kPayloadBf16;  // PayloadKind of the weights, norm and mailbox (Dense and MoE)
   int kind = XP_LAYER_DENSE;
   // MoE layers: the execution identity, the Router projection and its correction bias.
   xp_moe_layer_desc moe{};
@@ -489,6 +489,7 @@ struct RouterBinding {
   uint32_t *fault = nullptr;
   int64_t pool_rows = 0;
   float eps = 0.0f;
+  int32_t payload = kPayloadBf16;  // PayloadKind of x, of the weights unless FP32, of PAYLOAD logits
 };
 
 struct RouterLaunches {
@@ -526,6 +527,7 @@ RouterLaunches make_router_launches(const RouterBinding &b, int64_t capacity) {
     }
     args.w = static_cast<const uint16_t *>(b.w);
     args.out = static_cast<uint16_t *>(logits);
+    args.payload = b.payload;
     args.partials = layout.scratch_bytes > 0 ? reinterpret_cast<float *>(b.workspace + layout.scratch) : nullptr;
     args.ldx = b.hidden;
     args.ldo = b.experts;
@@ -553,7 +555,8 @@ RouterLaunches make_router_launches(const RouterBinding &b, int64_t capacity) {
     args.hidden = b.hidden;
     args.experts = static_cast<int32_t>(b.experts);
     args.weights_f32 = b.precision == XP_ROUTER_PRECISION_FP32 ? 1 : 0;
-    args.out_bf16 = b.precision == XP_ROUTER_PRECISION_PAYLOAD ? 1 : 0;
+    args.out_payload = b.precision == XP_ROUTER_PRECISION_PAYLOAD ? 1 : 0;
+    args.payload = b.payload;
     launches.logits = make_router_logits(args);
     args.rows = b.rows;
     launches.logits.set_args(args);
@@ -573,6 +576,7 @@ RouterLaunches make_router_launches(const RouterBinding &b, int64_t capacity) {
   topk.partials = partials;
   topk.logits_out = partials != nullptr ? static_cast<uint16_t *>(logits) : nullptr;
   topk.slices = static_cast<int32_t>(slices);
+  topk.payload = b.payload;
   launches.topk = make_router_topk(topk);
   topk.rows = b.rows;
   launches.topk.set_args(topk);
@@ -599,6 +603,7 @@ struct ExpertsBinding {
   int64_t topk;
   float scale;
   GatedSilu act;
+  int32_t payload = kPayloadBf16;  // PayloadKind of x, the weights, the routes and out
   // The Router's TopK run by the sort kernel (at most 16 rows, no shared experts), or null.
   const RouterTopkArgs *fused_topk = nullptr;
 };
@@ -667,6 +672,7 @@ int make_experts_launches(const ExpertsBinding &b, int64_t capacity, ExpertsLaun
   up.tile_expert = tile_expert;
   up.tile_row0 = tile_row0;
   up.expert_end = expert_end;
+  up.payload = b.payload;
 
   GemmArgs dn = up;
   dn.x = activated;
@@ -711,6 +717,7 @@ int make_experts_launches(const ExpertsBinding &b, int64_t capacity, ExpertsLaun
   combine.topk = static_cast<int32_t>(b.topk);
   combine.experts = static_cast<int32_t>(b.experts);
   combine.scale = b.scale;
+  combine.payload = b.payload;
   out.combine = make_moe_combine(combine);
   combine.rows = b.rows;
   out.combine.set_args(combine);
@@ -725,7 +732,7 @@ bool same_moe(const xp_moe_layer_desc &a, const xp_moe_layer_desc &b) {
          a.routed_experts == b.routed_experts && a.routed_topk == b.routed_topk && a.algorithm == b.algorithm &&
          a.precision == b.precision && (a.renormalize != 0) == (b.renormalize != 0) &&
          a.weight_rounding == b.weight_rounding && a.routed_scaling_factor == b.routed_scaling_factor &&
-         a.alpha == b.alpha && a.limit == b.limit && a.up_offset == b.up_offset;
+         a.alpha == b.alpha && a.limit == b.limit && a.up_offset == b.up_offset && a.payload == b.payload;
 }
 
 int validate_moe_desc(const xp_moe_layer_desc *d) {
@@ -748,7 +755,8 @@ int validate_moe_desc(const xp_moe_layer_desc *d) {
              "gate limit must be finite and non-negative (0 = none) and the up offset finite");
   XP_REQUIRE(2 * d->intermediate * d->hidden * 2 < (int64_t{1} << 31),
              "one expert's gate_up must stay below 2 GiB (32-bit buffer range)");
-  return XP_OK;
+  int32_t payload = kPayloadBf16;
+  return payload_kind(d->payload, payload);
 }
 
 // Lane workspace of a MoE step at `capacity`: the gathered batch, the Router workspace
@@ -823,6 +831,10 @@ int make_moe_step(const Layer &layer, const MoeStepBinding &b, int64_t capacity,
   // from the capacity, so a template's node list matches every replay's.
   const bool fuse_gather = router_gather_fusable(d, capacity);
   const bool fuse_topk = capacity <= kMoeFusedTopkRows && topk == d.routed_topk;
+  int32_t payload = kPayloadBf16;
+  if (const int status = payload_kind(d.payload, payload); status != XP_OK) {
+    return status;
+  }
   if (!fuse_gather) {
     GatherArgs gather{};
     gather.pool = b.pool_in;
@@ -834,6 +846,7 @@ int make_moe_step(const Layer &layer, const MoeStepBinding &b, int64_t capacity,
     gather.hidden = d.hidden;
     gather.rows = b.rows;
     gather.eps = layer.eps;
+    gather.payload = payload;
     chain.add(make_gather(gather, capacity));
   }
 
@@ -852,6 +865,7 @@ int make_moe_step(const Layer &layer, const MoeStepBinding &b, int64_t capacity,
   router.precision = d.precision;
   router.renormalize = d.renormalize;
   router.weight_rounding = d.weight_rounding;
+  router.payload = payload;
   if (fuse_gather) {
     router.fused_gather = true;
     router.batch_out = batch;
@@ -906,6 +920,7 @@ int make_moe_step(const Layer &layer, const MoeStepBinding &b, int64_t capacity,
   experts.topk = topk;
   experts.scale = d.routed_scaling_factor;
   experts.act = GatedSilu{d.alpha, d.limit, d.up_offset};
+  experts.payload = payload;
   if (fuse_topk) {
     experts.fused_topk = &routing.topk_args;
   }
@@ -2026,10 +2041,12 @@ size_t xp_moe_router_workspace_bytes(int64_t rows, int64_t hidden, int64_t exper
   return router_workspace(rows, hidden, experts, precision).bytes;
 }
 
-int xp_moe_router_topk(const void *logits, int logits_f32, int64_t rows, int64_t experts, int64_t topk, int algorithm,
-                       const float *correction_bias, int renormalize, int weight_rounding, int32_t *ids,
-                       float *weights, xp_stream_t stream) {
+int xp_moe_router_topk(const void *logits, int logits_dtype, int64_t rows, int64_t experts, int64_t topk,
+                       int algorithm, const float *correction_bias, int renormalize, int weight_rounding,
+                       int32_t *ids, float *weights, xp_stream_t stream) {
   XP_REQUIRE(rows >= 0, "row count must be non-negative");
+  XP_REQUIRE(logits_dtype == XP_DTYPE_BF16 || logits_dtype == XP_DTYPE_F16 || logits_dtype == XP_DTYPE_F32,
+             "logits must be bf16, fp16 or fp32");
   XP_REQUIRE(experts >= 1 && experts <= kMoeMaxExperts, "the router supports 1 to 1024 experts");
   XP_REQUIRE(topk >= 1 && topk <= experts && topk <= 64, "topk must be between 1 and min(experts, 64)");
   XP_REQUIRE(algorithm == XP_ROUTER_SOFTMAX || algorithm == XP_ROUTER_SIGMOID, "router algorithm is unknown");
@@ -2047,7 +2064,8 @@ int xp_moe_router_topk(const void *logits, int logits_f32, int64_t rows, int64_t
   args.rows = rows;
   args.experts = static_cast<int32_t>(experts);
   args.topk = static_cast<int32_t>(topk);
-  args.logits_f32 = logits_f32 != 0 ? 1 : 0;
+  args.logits_f32 = logits_dtype == XP_DTYPE_F32 ? 1 : 0;
+  args.payload = logits_dtype == XP_DTYPE_F16 ? kPayloadF16 : kPayloadBf16;
   args.softmax = algorithm == XP_ROUTER_SOFTMAX ? 1 : 0;
   args.renormalize = renormalize != 0 ? 1 : 0;
   args.round_to_logits = weight_rounding == XP_TOPK_ROUNDING_LOGITS_DTYPE ? 1 : 0;
@@ -2056,11 +2074,15 @@ int xp_moe_router_topk(const void *logits, int logits_f32, int64_t rows, int64_t
 }
 
 int xp_moe_router(const void *hidden_states, int64_t rows, int64_t hidden, const void *router_weights,
-                  int64_t experts, int64_t topk, int algorithm, int precision, const float *correction_bias,
-                  int renormalize, int weight_rounding, int32_t *ids, float *weights, void *workspace,
-                  size_t workspace_bytes, xp_stream_t stream) {
+                  int64_t experts, int64_t topk, int algorithm, int precision, int payload_dtype,
+                  const float *correction_bias, int renormalize, int weight_rounding, int32_t *ids, float *weights,
+                  void *workspace, size_t workspace_bytes, xp_stream_t stream) {
   XP_REQUIRE(rows >= 0, "row count must be non-negative");
   XP_REQUIRE(hidden > 0, "hidden size must be positive");
+  int32_t payload = kPayloadBf16;
+  if (const int status = payload_kind(payload_dtype, payload); status != XP_OK) {
+    return status;
+  }
   if (const int status = validate_router(experts, topk, algorithm, precision, weight_rounding); status != XP_OK) {
     return status;
   }
@@ -2089,6 +2111,7 @@ int xp_moe_router(const void *hidden_states, int64_t rows, int64_t hidden, const
   binding.precision = precision;
   binding.renormalize = renormalize;
   binding.weight_rounding = weight_rounding;
+  binding.payload = payload;
   const RouterLaunches launches = make_router_launches(binding, rows);
   const hipStream_t hip_stream = static_cast<hipStream_t>(stream);
   for (const KernelLaunch *kernel : {&launches.logits, &launches.logits_reduce, &launches.topk}) {
@@ -2150,8 +2173,12 @@ int xp_moe_workspace_layout(int64_t rows, int64_t hidden, int64_t intermediate, 
 int xp_moe_experts(const void *hidden_states, int64_t rows, int64_t hidden, int64_t intermediate, int64_t experts,
                    int64_t topk, const void *w_gate_up, const void *w_down, const int32_t *topk_ids,
                    const float *topk_weights, float routed_scaling_factor, float alpha, float limit, float up_offset,
-                   void *output, void *workspace, size_t workspace_bytes, xp_stream_t stream) {
+                   int payload_dtype, void *output, void *workspace, size_t workspace_bytes, xp_stream_t stream) {
   XP_REQUIRE(rows >= 0, "row count must be non-negative");
+  int32_t payload = kPayloadBf16;
+  if (const int status = payload_kind(payload_dtype, payload); status != XP_OK) {
+    return status;
+  }
   if (const int status = validate_experts(rows, hidden, intermediate, experts, topk); status != XP_OK) {
     return status;
   }
@@ -2182,6 +2209,7 @@ int xp_moe_experts(const void *hidden_states, int64_t rows, int64_t hidden, int6
   binding.topk = topk;
   binding.scale = routed_scaling_factor;
   binding.act = GatedSilu{alpha, limit, up_offset};
+  binding.payload = payload;
   ExpertsLaunches launches;
   if (const int status = make_experts_launches(binding, rows, launches); status != XP_OK) {
     return status;
@@ -2219,6 +2247,9 @@ int xp_moe_layer_register(xp_agent_t agent, int instance_index, int layer_ordina
   layer.kind = XP_LAYER_MOE;
   layer.moe = *desc;
   layer.moe.renormalize = desc->renormalize != 0 ? 1 : 0;
+  if (const int status = payload_kind(desc->payload, layer.payload); status != XP_OK) {
+    return status;
+  }
   layer.router = router;
   layer.correction_bias = correction_bias;
   std::lock_guard<std::mutex> guard(agent->mutex);

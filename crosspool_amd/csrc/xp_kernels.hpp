@@ -193,6 +193,7 @@ struct RouterTopkArgs {
   const float *partials;
   uint16_t *logits_out;
   int32_t slices;
+  int32_t payload;  // PayloadKind of 16-bit logits (logits_f32 == 0) and of their roundings
 };
 
 // Router logits[rows, experts] = x[rows, hidden] . w[experts, hidden] (w bf16 or fp32) as
@@ -205,7 +206,8 @@ struct RouterLogitsArgs {
   int64_t hidden;
   int32_t experts;
   int32_t weights_f32;
-  int32_t out_bf16;
+  int32_t out_payload;  // logits stored in the payload dtype (else fp32)
+  int32_t payload;      // PayloadKind of x, of w unless weights_f32, and of payload logits
 };
 
 struct FinalizeRoutingArgs {
@@ -256,6 +258,7 @@ struct MoeCombineArgs {
   int32_t topk;
   int32_t experts;
   float scale;               // routed scaling factor
+  int32_t payload;           // PayloadKind of routes and out
 };
 
 // Expert tiles of the grouped projections: Small (16 sorted positions, grouped split

@@ -192,8 +192,8 @@ class MoeFfnExecutionSignature:
     gate: GateTransform = GateTransform()
 
     def __post_init__(self) -> None:
-        if self.payload_dtype is not torch.bfloat16:
-            raise ValueError("the MI355X MoE path executes bf16 payloads")
+        if self.payload_dtype not in (torch.bfloat16, torch.float16):
+            raise ValueError("MoE payloads must be bf16 or fp16")
         for name in ("payload_row_capacity", "hidden_size", "local_intermediate_size", "expert_count", "effective_topk"):
             value = getattr(self, name)
             if isinstance(value, bool) or not isinstance(value, int) or value <= 0:
@@ -239,4 +239,5 @@ class MoeFfnExecutionSignature:
             alpha=alpha,
             limit=limit,
             up_offset=up_offset,
+            payload=_native.payload_dtype_code(self.payload_dtype),
         )

@@ -65,8 +65,8 @@ class MoeRouterWeights:
 
     def __post_init__(self) -> None:
         validate_weight_tensor(self.projection, name="router projection")
-        if self.projection.ndim != 2 or self.projection.dtype not in (torch.bfloat16, torch.float32):
-            raise ValueError("Router projection requires a bf16 or fp32 matrix")
+        if self.projection.ndim != 2 or self.projection.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+            raise ValueError("Router projection requires a bf16, fp16 or fp32 matrix")
         if self.correction_bias is not None:
             validate_weight_tensor(self.correction_bias, name="router correction bias")
             if self.correction_bias.dtype is not torch.float32 or self.correction_bias.ndim != 1:
@@ -81,8 +81,9 @@ class MoeRouterWeights:
 class MoeFfnWeights:
     """Expert projections and the optional Router (weights.py:190-230).
 
-    ``i_proj`` is ``[experts, 2 I, H]`` bf16 with INTERLEAVED Gate/Up rows per expert,
-    ``o_proj`` is ``[experts, H, I]`` bf16.
+    ``i_proj`` is ``[experts, 2 I, H]`` with INTERLEAVED Gate/Up rows per expert,
+    ``o_proj`` is ``[experts, H, I]``, both of the payload dtype (bf16 or fp16, the
+    reference's supported payloads, src/cext-include/xpool/ffn.hpp:83-85).
     """
 
     i_proj: torch.Tensor
@@ -92,8 +93,8 @@ class MoeFfnWeights:
     def __post_init__(self) -> None:
         validate_weight_tensor(self.i_proj, name="Expert i_proj")
         validate_weight_tensor(self.o_proj, name="Expert o_proj")
-        if self.i_proj.dtype is not torch.bfloat16 or self.o_proj.dtype is not torch.bfloat16:
-            raise ValueError("Expert projections must be bf16")
+        if self.i_proj.dtype not in (torch.bfloat16, torch.float16) or self.o_proj.dtype is not self.i_proj.dtype:
+            raise ValueError("Expert projections must both be bf16 or both fp16")
         if self.i_proj.ndim != 3 or self.o_proj.ndim != 3:
             raise ValueError("Expert projections must be [experts, N, K] tensors")
         experts, two_i, hidden = self.i_proj.shape
@@ -105,6 +106,12 @@ class MoeFfnWeights:
     @property
     def expert_count(self) -> int:
         return int(self.i_proj.shape[0])
+
+    @property
+    def payload_dtype(self) -> torch.dtype:
+        """The dtype of the layer's payloads: its expert projections'."""
+
+        return self.i_proj.dtype
 
     @property
     def hidden_size(self) -> int:
@@ -162,7 +169,8 @@ class MoeLayerSpec:
         if weights.router is None:
             raise ValueError("the Lane owns the Router on one device: MoE weights need a Router projection")
         weight_dtype = (
-            torch.float32 if self.router_projection_precision is RouterProjectionPrecision.FP32 else torch.bfloat16
+            torch.float32 if self.router_projection_precision is RouterProjectionPrecision.FP32
+            else weights.payload_dtype
         )
         projection = weights.router.projection
         if projection.dtype is not weight_dtype or tuple(projection.shape) != (
@@ -174,13 +182,16 @@ class MoeLayerSpec:
         if weights.router.projection.device != weights.i_proj.device:
             raise ValueError("Router and Expert resources must share one device")
 
-    def signature(self, *, hidden_size: int, local_intermediate_size: int, payload_row_capacity: int):
+    def signature(
+        self, *, hidden_size: int, local_intermediate_size: int, payload_row_capacity: int,
+        payload_dtype: torch.dtype = torch.bfloat16,
+    ):
         """The MoeFfnExecutionSignature of this layer at one capacity."""
 
         from crosspool_amd.execution import MoeFfnExecutionSignature, MoeRouterExecutionSignature
 
         return MoeFfnExecutionSignature(
-            payload_dtype=torch.bfloat16,
+            payload_dtype=payload_dtype,
             payload_row_capacity=payload_row_capacity,
             hidden_size=hidden_size,
             local_intermediate_size=local_intermediate_size,
@@ -219,6 +230,7 @@ class Router:
         renormalize: bool = True,
         weight_rounding: TopKWeightRounding = TopKWeightRounding.NONE,
         device: torch.device | None = None,
+        payload_dtype: torch.dtype = torch.bfloat16,
     ) -> None:
         if not 1 <= routed_topk <= min(routed_expert_count, 64) or routed_expert_count > 1024:
             raise ValueError("Router supports up to 1024 experts and a TopK of at most min(experts, 64)")
@@ -233,13 +245,15 @@ class Router:
         self.precision = RouterProjectionPrecision(precision)
         self.renormalize = bool(renormalize)
         self.weight_rounding = TopKWeightRounding(weight_rounding)
+        self.payload_dtype = payload_dtype
+        self._payload_code = _native.payload_dtype_code(payload_dtype)
         nbytes = _native.library().xp_moe_router_workspace_bytes(
             row_capacity, hidden_size, routed_expert_count, int(self.precision)
         )
         self.workspace = torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device=self.device)
         self.ids = torch.empty((row_capacity, routed_topk), dtype=torch.int32, device=self.device)
         self.weights = torch.empty((row_capacity, routed_topk), dtype=torch.float32, device=self.device)
-        logits_dtype = torch.bfloat16 if self.precision is RouterProjectionPrecision.PAYLOAD else torch.float32
+        logits_dtype = payload_dtype if self.precision is RouterProjectionPrecision.PAYLOAD else torch.float32
         count = row_capacity * routed_expert_count
         # The projection's logits, the first region of the workspace.
         self.logits = self.workspace[: count * logits_dtype.itemsize].view(logits_dtype).view(
@@ -250,11 +264,11 @@ class Router:
         rows = self.row_capacity if rows is None else rows
         if not 0 < rows <= self.row_capacity:
             raise ValueError("router rows must be positive and within the capacity")
-        if hidden_states.dtype is not torch.bfloat16 or hidden_states.shape[1:] != (self.hidden_size,):
-            raise ValueError("router hidden states must be bf16 [rows, hidden]")
+        if hidden_states.dtype is not self.payload_dtype or hidden_states.shape[1:] != (self.hidden_size,):
+            raise ValueError(f"router hidden states must be {self.payload_dtype} [rows, hidden]")
         if hidden_states.shape[0] < rows or not hidden_states.is_contiguous():
             raise ValueError("router hidden states must be contiguous and cover the rows")
-        weight_dtype = torch.float32 if self.precision is RouterProjectionPrecision.FP32 else torch.bfloat16
+        weight_dtype = torch.float32 if self.precision is RouterProjectionPrecision.FP32 else self.payload_dtype
         projection = router_weights.projection
         if projection.dtype is not weight_dtype or tuple(projection.shape) != (
             self.routed_expert_count, self.hidden_size
@@ -262,7 +276,8 @@ class Router:
             raise ValueError(f"router projection must be {weight_dtype} [{self.routed_expert_count}, {self.hidden_size}]")
         _native.call(
             "xp_moe_router", _ptr(hidden_states), rows, self.hidden_size, _ptr(projection), self.routed_expert_count,
-            self.routed_topk, int(self.algorithm), int(self.precision), _ptr(router_weights.correction_bias),
+            self.routed_topk, int(self.algorithm), int(self.precision), self._payload_code,
+            _ptr(router_weights.correction_bias),
             int(self.renormalize), int(self.weight_rounding), _ptr(self.ids), _ptr(self.weights),
             _ptr(self.workspace), self.workspace.numel(), _stream(),
         )
@@ -279,17 +294,19 @@ def router_topk(
     ids: torch.Tensor | None = None,
     weights: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    """TopK alone over given bf16 or fp32 logits ``[rows, experts]`` (router_topk_kernel, routing.py:21-89)."""
+    """TopK alone over given bf16, fp16 or fp32 logits ``[rows, experts]`` (router_topk_kernel, routing.py:21-89)."""
 
-    if logits.dtype not in (torch.bfloat16, torch.float32) or logits.ndim != 2 or not logits.is_contiguous():
-        raise ValueError("logits must be a contiguous bf16 or fp32 matrix")
+    if logits.dtype not in (torch.bfloat16, torch.float16, torch.float32) or logits.ndim != 2 or not logits.is_contiguous():
+        raise ValueError("logits must be a contiguous bf16, fp16 or fp32 matrix")
     rows, experts = logits.shape
     ids = torch.empty((rows, topk), dtype=torch.int32, device=logits.device) if ids is None else ids
     weights = torch.empty((rows, topk), dtype=torch.float32, device=logits.device) if weights is None else weights
     _require(ids, "ids", torch.int32, (rows, topk))
     _require(weights, "weights", torch.float32, (rows, topk))
     _native.call(
-        "xp_moe_router_topk", _ptr(logits), int(logits.dtype is torch.float32), rows, experts, topk, int(algorithm),
+        "xp_moe_router_topk", _ptr(logits),
+        _native.XP_DTYPE_F32 if logits.dtype is torch.float32 else _native.payload_dtype_code(logits.dtype),
+        rows, experts, topk, int(algorithm),
         _ptr(correction_bias), int(renormalize), int(weight_rounding), _ptr(ids), _ptr(weights), _stream(),
     )
     return ids, weights
@@ -357,6 +374,7 @@ class Experts:
         activation: SiluActivation | None = None,
         gate: GateTransform | None = None,
         device: torch.device | None = None,
+        payload_dtype: torch.dtype = torch.bfloat16,
     ) -> None:
         if not math.isfinite(routed_scaling_factor) or routed_scaling_factor <= 0:
             raise ValueError("routed scaling factor must be finite and positive")
@@ -370,6 +388,8 @@ class Experts:
         self.effective_topk = effective_topk
         self.routed_scaling_factor = float(routed_scaling_factor)
         self.act = activation_arguments(activation or SiluActivation(), gate or GateTransform())
+        self.payload_dtype = payload_dtype
+        self._payload_code = _native.payload_dtype_code(payload_dtype)
         nbytes = _native.library().xp_moe_workspace_bytes(
             row_capacity, hidden_size, local_intermediate_size, expert_count, effective_topk
         )
@@ -394,8 +414,8 @@ class Experts:
         return {
             "expert_end": view(0, torch.int32, (self.expert_count,)),
             "sorted_route": view(1, torch.int32, (routes,)),
-            "activated": view(4, torch.bfloat16, (routes, self.local_intermediate_size)),
-            "route_out": view(5, torch.bfloat16, (routes, self.hidden_size)),
+            "activated": view(4, self.payload_dtype, (routes, self.local_intermediate_size)),
+            "route_out": view(5, self.payload_dtype, (routes, self.hidden_size)),
         }
 
     def run_into(
@@ -408,8 +428,10 @@ class Experts:
         output: torch.Tensor,
     ) -> None:
         c, h, k = self.row_capacity, self.hidden_size, self.effective_topk
-        _require(hidden_states, "hidden states", torch.bfloat16, (c, h))
-        _require(output, "output", torch.bfloat16, (c, h))
+        _require(hidden_states, "hidden states", self.payload_dtype, (c, h))
+        _require(output, "output", self.payload_dtype, (c, h))
+        if weights.payload_dtype is not self.payload_dtype:
+            raise ValueError(f"Expert weights must be {self.payload_dtype}")
         _require(topk_ids, "TopK ids", torch.int32, (c, k))
         _require(topk_weights, "TopK weights", torch.float32, (c, k))
         if (weights.expert_count, weights.hidden_size, weights.local_intermediate_size) != (
@@ -420,6 +442,6 @@ class Experts:
         _native.call(
             "xp_moe_experts", _ptr(hidden_states), c, h, self.local_intermediate_size, self.expert_count, k,
             _ptr(weights.i_proj), _ptr(weights.o_proj), _ptr(topk_ids), _ptr(topk_weights),
-            self.routed_scaling_factor, alpha, limit, up_offset, _ptr(output), _ptr(self.workspace),
-            self.workspace.numel(), _stream(),
+            self.routed_scaling_factor, alpha, limit, up_offset, self._payload_code, _ptr(output),
+            _ptr(self.workspace), self.workspace.numel(), _stream(),
         )

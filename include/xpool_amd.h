@@ -384,30 +384,31 @@ enum { XP_ROUTER_SOFTMAX = 1, XP_ROUTER_SIGMOID = 2 };
 enum { XP_ROUTER_PRECISION_PAYLOAD = 1, XP_ROUTER_PRECISION_FP32 = 2, XP_ROUTER_PRECISION_FP32_LOGITS = 3 };
 enum { XP_TOPK_ROUNDING_NONE = 1, XP_TOPK_ROUNDING_LOGITS_DTYPE = 2 };
 
-/* TopK over logits [rows, experts] (bf16, or fp32 when logits_f32): scores are softmax or
- * sigmoid in fp32; selection = score (+ correction_bias[e], fp32, may be NULL; sigmoid over
- * bf16 logits rounds the selection to bf16); ties go to the lower id for softmax and the
- * higher id for sigmoid; the weight of a pick is its score (softmax without correction: the
- * selected maximum); renormalize divides by the sum of picked weights when positive;
- * LOGITS_DTYPE rounding then rounds weights through bf16 for bf16 logits.  Writes ids
- * [rows, topk] int32 and weights [rows, topk] fp32.  experts <= 1024, topk <= 64.
- * Replaces router_topk_kernel (src/xpool/runtime/ffnagent/operators/routing.py:21-89). */
-int xp_moe_router_topk(const void *logits, int logits_f32, int64_t rows, int64_t experts, int64_t topk, int algorithm,
-                       const float *correction_bias, int renormalize, int weight_rounding, int32_t *ids,
-                       float *weights, xp_stream_t stream);
+/* TopK over logits [rows, experts] of logits_dtype (XP_DTYPE_BF16, F16 or F32): scores are
+ * softmax or sigmoid in fp32; selection = score (+ correction_bias[e], fp32, may be NULL;
+ * sigmoid over 16-bit logits rounds the selection to the logits dtype); ties go to the lower
+ * id for softmax and the higher id for sigmoid; the weight of a pick is its score (softmax
+ * without correction: the selected maximum); renormalize divides by the sum of picked
+ * weights when positive; LOGITS_DTYPE rounding then rounds weights through the dtype of
+ * 16-bit logits.  Writes ids [rows, topk] int32 and weights [rows, topk] fp32.
+ * experts <= 1024, topk <= 64.  Replaces router_topk_kernel
+ * (src/xpool/runtime/ffnagent/operators/routing.py:21-89). */
+int xp_moe_router_topk(const void *logits, int logits_dtype, int64_t rows, int64_t experts, int64_t topk,
+                       int algorithm, const float *correction_bias, int renormalize, int weight_rounding,
+                       int32_t *ids, float *weights, xp_stream_t stream);
 
 /* Workspace bytes of xp_moe_router (the logits and the projection's K-slice scratch). */
 size_t xp_moe_router_workspace_bytes(int64_t rows, int64_t hidden, int64_t experts, int precision);
 
-/* Router: logits = hidden_states [rows, hidden] bf16 . router_weights^T, where the weights
- * are [experts, hidden] bf16 (PAYLOAD: bf16 logits, through the MFMA projection kernels
- * when hidden and experts are multiples of 8; FP32_LOGITS: fp32 logits) or fp32 (FP32: fp32
- * logits of the widened input), then xp_moe_router_topk.  Replaces Router.run_into
- * (routing.py:148-190). */
+/* Router: logits = hidden_states [rows, hidden] . router_weights^T, with hidden_states of
+ * payload_dtype (XP_DTYPE_BF16 or F16) and weights [experts, hidden] of the payload dtype
+ * (PAYLOAD: logits of the payload dtype, through the MFMA projection kernels when hidden and
+ * experts are multiples of 8; FP32_LOGITS: fp32 logits) or fp32 (FP32: fp32 logits of the
+ * widened input), then xp_moe_router_topk.  Replaces Router.run_into (routing.py:148-190). */
 int xp_moe_router(const void *hidden_states, int64_t rows, int64_t hidden, const void *router_weights,
-                  int64_t experts, int64_t topk, int algorithm, int precision, const float *correction_bias,
-                  int renormalize, int weight_rounding, int32_t *ids, float *weights, void *workspace,
-                  size_t workspace_bytes, xp_stream_t stream);
+                  int64_t experts, int64_t topk, int algorithm, int precision, int payload_dtype,
+                  const float *correction_bias, int renormalize, int weight_rounding, int32_t *ids, float *weights,
+                  void *workspace, size_t workspace_bytes, xp_stream_t stream);
 
 /* Final Routing Metadata [capacity, effective_topk]: routed slots copy the Router's ids and
  * weights, shared slots s name expert routed_expert_count + s with weight
@@ -425,24 +426,24 @@ size_t xp_moe_workspace_bytes(int64_t rows, int64_t hidden, int64_t intermediate
  * keeps them until the next call): [0] expert ends (int32 [experts], one past each expert's
  * last sorted position), [1] sorted routes (int32 [rows * topk], route = row * topk + slot
  * at each sorted position), [2] tile experts and [3] tile first positions (int32), [4] the
- * activated routes (bf16 [rows * topk, intermediate], sorted order), [5] the route outputs
- * (bf16 [rows * topk, hidden], by route).  No counterpart in the reference, whose test
- * harness reads its workspace views directly (moe.py:181-215). */
+ * activated routes ([rows * topk, intermediate] of the payload dtype, sorted order), [5] the
+ * route outputs ([rows * topk, hidden] of the payload dtype, by route).  No counterpart in
+ * the reference, whose test harness reads its workspace views directly (moe.py:181-215). */
 int xp_moe_workspace_layout(int64_t rows, int64_t hidden, int64_t intermediate, int64_t experts, int64_t topk,
                             size_t *offsets);
 
 /* Experts: for every route (row, slot) with 0 <= e = topk_ids[row, slot] < experts,
- * h = bf16(act(bf16(x[row] . w_gate_up[e][2j]), bf16(x[row] . w_gate_up[e][2j+1]))) and
- * r = bf16((h . w_down[e][n]) * topk_weights[row, slot]); then
- * output[row] = bf16(routed_scaling_factor * sum over slots in order of float(r)), 0 for
- * rows without routes.  w_gate_up is [experts, 2*intermediate, hidden] (Gate/Up
- * INTERLEAVED), w_down [experts, hidden, intermediate], all bf16; act as in
- * xp_gemm_gate_up_silu.  Replaces Experts.run_into
- * (src/xpool/runtime/ffnagent/operators/moe.py:168-343). */
+ * h = p(act(p(x[row] . w_gate_up[e][2j]), p(x[row] . w_gate_up[e][2j+1]))) and
+ * r = p((h . w_down[e][n]) * topk_weights[row, slot]); then
+ * output[row] = p(routed_scaling_factor * sum over slots in order of float(r)), 0 for
+ * rows without routes, where p rounds to payload_dtype (XP_DTYPE_BF16 or F16), the dtype of
+ * x, the weights and the output.  w_gate_up is [experts, 2*intermediate, hidden] (Gate/Up
+ * INTERLEAVED), w_down [experts, hidden, intermediate]; act as in xp_gemm_gate_up_silu.
+ * Replaces Experts.run_into (src/xpool/runtime/ffnagent/operators/moe.py:168-343). */
 int xp_moe_experts(const void *hidden_states, int64_t rows, int64_t hidden, int64_t intermediate, int64_t experts,
                    int64_t topk, const void *w_gate_up, const void *w_down, const int32_t *topk_ids,
                    const float *topk_weights, float routed_scaling_factor, float alpha, float limit, float up_offset,
-                   void *output, void *workspace, size_t workspace_bytes, xp_stream_t stream);
+                   int payload_dtype, void *output, void *workspace, size_t workspace_bytes, xp_stream_t stream);
 
 /* ---------------------------------------------------------------- MoE layer kind
  * One MoE layer's execution identity: the fields of MoeFfnExecutionSignature
@@ -466,12 +467,13 @@ typedef struct {
   float alpha;              /* SiLU slope */
   float limit;              /* Gate/Up clip, 0 = none */
   float up_offset;
+  int payload;              /* XP_DTYPE_BF16 or XP_DTYPE_F16: the mailbox rows and weights */
 } xp_moe_layer_desc;
 
-/* Register (or rebind) one MoE layer's borrowed weights: gate_up [experts, 2*intermediate,
- * hidden] bf16 (Gate/Up INTERLEAVED per expert), down [experts, hidden, intermediate] bf16,
- * router [routed_experts, hidden] (fp32 for the FP32 precision, bf16 otherwise),
- * correction_bias [routed_experts] fp32 or NULL, norm_weight [hidden] bf16 or NULL.
+/* Register (or rebind) one MoE layer's borrowed weights, of desc->payload unless stated:
+ * gate_up [experts, 2*intermediate, hidden] (Gate/Up INTERLEAVED per expert), down
+ * [experts, hidden, intermediate], router [routed_experts, hidden] (fp32 for the FP32
+ * precision), correction_bias [routed_experts] fp32 or NULL, norm_weight [hidden] or NULL.
  * Replaces LayerExecutionDescriptor + MoeBindingView (src/cext-bindings/ffnagent.cpp) and
  * the MoE branch of validate_layer_weights_against_layout (registry.py:153-174). */
 int xp_moe_layer_register(xp_agent_t agent, int instance_index, int layer_ordinal, const xp_moe_layer_desc *desc,
@@ -484,8 +486,8 @@ int xp_moe_layer_register(xp_agent_t agent, int instance_index, int layer_ordina
 size_t xp_moe_step_workspace_bytes(const xp_moe_layer_desc *desc, int64_t capacity);
 
 /* Byte offsets of the MoE step's workspace regions: [0] the gathered (normalised) batch
- * bf16 [capacity, hidden], [1] the Router logits ([capacity, routed_experts], bf16 for the
- * PAYLOAD precision, fp32 otherwise), [2] routed ids int32 and [3] routed weights fp32
+ * [capacity, hidden] of the payload dtype, [1] the Router logits ([capacity, routed_experts],
+ * of the payload dtype for the PAYLOAD precision, fp32 otherwise), [2] routed ids int32 and [3] routed weights fp32
  * [capacity, routed_topk], [4] final ids int32 and [5] final weights fp32 [capacity,
  * effective topk] (the routed ones when there are no shared experts), [6] the Experts
  * workspace (xp_moe_workspace_layout's regions at capacity rows), [7] the total.  No

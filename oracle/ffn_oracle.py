@@ -44,6 +44,14 @@ def bf16_ulp(values: torch.Tensor) -> torch.Tensor:
     return torch.pow(2.0, exponent - 7)
 
 
+def f16_ulp(values: torch.Tensor) -> torch.Tensor:
+    """Spacing of fp16 values at |values| (11 significant bits; 2^-24 below 2^-14)."""
+
+    magnitude = values.abs().float().clamp_min(2.0**-14)
+    exponent = torch.floor(torch.log2(magnitude))
+    return torch.pow(2.0, exponent - 10)
+
+
 # --------------------------------------------------------------------------- #
 # Transport: byte copy, gather, scatter
 # --------------------------------------------------------------------------- #

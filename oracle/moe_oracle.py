@@ -14,9 +14,9 @@ checkout:
 * ``finalize_routing`` follows finalize_moe_routing_kernel (routing.py:193-227).
 * ``experts_reference`` is the reference's own expected-value formula for Experts,
   tests/suites/integration/runtime/ffnagent/test_operators.py:255-281, with fp64 instead of
-  fp32 matrix-vector products: projection rounded to bf16, activation in fp32 rounded to
-  bf16, down projection times the route weight rounded to bf16, fp32 sum over the row's
-  slots in order, times the routed scaling factor, rounded to bf16.
+  fp32 matrix-vector products: projection rounded to the payload dtype (bf16 or fp16),
+  activation in fp32 rounded to it, down projection times the route weight rounded to it,
+  fp32 sum over the row's slots in order, times the routed scaling factor, rounded to it.
 * ``experts_fp32`` is the same without any intermediate rounding (the pure-fp32 side of the
   parity bar).
 
@@ -35,11 +35,12 @@ import torch
 from oracle import ffn_oracle as o
 
 
-def router_logits(x: torch.Tensor, w: torch.Tensor, *, payload: bool) -> torch.Tensor:
-    """fp32 logits as the Router projection produces them (bf16-rounded for PAYLOAD)."""
+def router_logits(x: torch.Tensor, w: torch.Tensor, *, payload: bool, dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """fp32 logits as the Router projection produces them (rounded to the payload ``dtype``,
+    bf16 or fp16, for PAYLOAD)."""
 
     exact = x.double() @ w.double().t()
-    return exact.to(torch.bfloat16).float() if payload else exact.float()
+    return exact.to(dtype).float() if payload else exact.float()
 
 
 def router_topk(
@@ -51,9 +52,15 @@ def router_topk(
     renormalize: bool = True,
     round_weights: bool = False,
     logits_bf16: bool = False,
+    logits_dtype: torch.dtype | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    """ids [rows, topk] int32 and weights [rows, topk] fp32 of router_topk_kernel."""
+    """ids [rows, topk] int32 and weights [rows, topk] fp32 of router_topk_kernel.
 
+    ``logits_dtype`` (or ``logits_bf16``) names the 16-bit dtype the logits are stored in,
+    whose rounding the sigmoid selection and the LOGITS_DTYPE weight rounding take."""
+
+    if logits_dtype is None and logits_bf16:
+        logits_dtype = torch.bfloat16
     logits = logits.float()
     rows, experts = logits.shape
     if softmax:
@@ -65,8 +72,8 @@ def router_topk(
     selection = scores.clone()
     if correction_bias is not None:
         selection = selection + correction_bias.float()
-    if not softmax and logits_bf16:
-        selection = selection.to(torch.bfloat16).float()
+    if not softmax and logits_dtype is not None:
+        selection = selection.to(logits_dtype).float()
     ids = torch.empty((rows, topk), dtype=torch.int32)
     weights = torch.empty((rows, topk), dtype=torch.float32)
     for row in range(rows):
@@ -83,8 +90,8 @@ def router_topk(
             remaining[expert] = float("-inf")
         if renormalize:
             weights[row] = weights[row] / (normalizer if normalizer > 0 else torch.ones(()))
-        if round_weights and logits_bf16:
-            weights[row] = weights[row].to(torch.bfloat16).float()
+        if round_weights and logits_dtype is not None:
+            weights[row] = weights[row].to(logits_dtype).float()
     return ids, weights
 
 
@@ -130,24 +137,26 @@ def experts_routes(
     alpha: float = 1.0,
     limit: float | None = None,
     up_offset: float = 0.0,
+    dtype: torch.dtype = torch.bfloat16,
 ) -> torch.Tensor:
-    """Route outputs [rows, slots, hidden] (bf16 values held in fp32; 0 where no route).
+    """Route outputs [rows, slots, hidden] (payload-dtype values held in fp32; 0 where no route).
 
-    Projection rounded to bf16, activation in fp32 rounded to bf16, down projection times
-    the route weight in fp32 rounded to bf16 (test_operators.py:266-278).
+    Projection rounded to the payload ``dtype`` (bf16 or fp16), activation in fp32 rounded
+    to it, down projection times the route weight in fp32 rounded to it
+    (test_operators.py:266-278, where the reference runs the formula for each payload dtype).
     """
 
     rows, hidden = x.shape
     experts = w_gate_up.shape[0]
     routes = torch.zeros((rows, topk_ids.shape[1], hidden), dtype=torch.float32)
     for expert, row_index, slot_index in _routes_by_expert(topk_ids, experts):
-        projected = (x[row_index].double() @ w_gate_up[expert].double().t()).to(torch.bfloat16)
+        projected = (x[row_index].double() @ w_gate_up[expert].double().t()).to(dtype)
         activated = o.gated_silu(
-            projected[:, 0::2], projected[:, 1::2], alpha=alpha, limit=limit, up_offset=up_offset
+            projected[:, 0::2], projected[:, 1::2], alpha=alpha, limit=limit, up_offset=up_offset, dtype=dtype
         )
         route = activated.double() @ w_down[expert].double().t()
         gamma = topk_weights[row_index, slot_index].double().unsqueeze(1)
-        routes[row_index, slot_index] = (route.float() * gamma.float()).to(torch.bfloat16).float()
+        routes[row_index, slot_index] = (route.float() * gamma.float()).to(dtype).float()
     return routes
 
 
@@ -162,27 +171,30 @@ def experts_reference(
     alpha: float = 1.0,
     limit: float | None = None,
     up_offset: float = 0.0,
+    dtype: torch.dtype = torch.bfloat16,
 ) -> torch.Tensor:
-    """Expected Experts output with the reference's rounding points (bf16 [rows, hidden])."""
+    """Expected Experts output with the reference's rounding points ([rows, hidden] of ``dtype``)."""
 
     routes = experts_routes(x, w_gate_up, w_down, topk_ids, topk_weights, alpha=alpha, limit=limit,
-                            up_offset=up_offset)
+                            up_offset=up_offset, dtype=dtype)
     total = torch.zeros(routes.shape[::2], dtype=torch.float32)
     for slot in range(topk_ids.shape[1]):
         total = total + routes[:, slot]
-    return (total * routed_scaling_factor).to(torch.bfloat16)
+    return (total * routed_scaling_factor).to(dtype)
 
 
-def rounding_slack(routes: torch.Tensor, expected: torch.Tensor, routed_scaling_factor: float = 1.0) -> torch.Tensor:
+def rounding_slack(routes: torch.Tensor, expected: torch.Tensor, routed_scaling_factor: float = 1.0,
+                   dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
     """Per-element gap two correct implementations may show at the reference's rounding points.
 
-    Each route output is rounded to bf16 before the sum, so an implementation whose fp32
-    accumulation differs may land one bf16 ulp away on every route; the scaled sum is then
-    rounded once more: scale * sum_k ulp(r_k) + ulp(y).
+    Each route output is rounded to the payload ``dtype`` before the sum, so an
+    implementation whose fp32 accumulation differs may land one ulp away on every route; the
+    scaled sum is then rounded once more: scale * sum_k ulp(r_k) + ulp(y).
     """
 
-    route_ulps = o.bf16_ulp(routes.abs()) * (routes != 0)
-    return routed_scaling_factor * route_ulps.sum(dim=1) + o.bf16_ulp(expected.float().abs())
+    ulp = o.bf16_ulp if dtype is torch.bfloat16 else o.f16_ulp
+    route_ulps = ulp(routes.abs()) * (routes != 0)
+    return routed_scaling_factor * route_ulps.sum(dim=1) + ulp(expected.float().abs())
 
 
 def experts_fp32(
@@ -214,12 +226,13 @@ def experts_fp32(
     return (total * routed_scaling_factor).float()
 
 
-def generate_moe_layer(hidden: int, intermediate: int, experts: int, seed: int, std: float = 0.02):
-    """Seeded bf16 Expert weights: i_proj [E, 2I, H] (interleaved), o_proj [E, H, I]."""
+def generate_moe_layer(hidden: int, intermediate: int, experts: int, seed: int, std: float = 0.02,
+                       dtype: torch.dtype = torch.bfloat16):
+    """Seeded Expert weights of ``dtype``: i_proj [E, 2I, H] (interleaved), o_proj [E, H, I]."""
 
     generator = torch.Generator().manual_seed(seed)
-    w_gate_up = (torch.randn((experts, 2 * intermediate, hidden), generator=generator) * std).to(torch.bfloat16)
-    w_down = (torch.randn((experts, hidden, intermediate), generator=generator) * std).to(torch.bfloat16)
+    w_gate_up = (torch.randn((experts, 2 * intermediate, hidden), generator=generator) * std).to(dtype)
+    w_down = (torch.randn((experts, hidden, intermediate), generator=generator) * std).to(dtype)
     return w_gate_up, w_down
 
 

@@ -55,8 +55,9 @@ def assert_moe_parity(actual: torch.Tensor, stage_reference: torch.Tensor, fp32_
                       slack: torch.Tensor) -> None:
     """The MoE Experts end-to-end bar.
 
-    Every route output is rounded to bf16 before the row sum (test_operators.py:278), so an
-    element may differ from the oracle by one bf16 ulp per route (scaled) plus one for the
+    Every route output is rounded to the payload dtype before the row sum
+    (test_operators.py:278), so an element may differ from the oracle by one ulp per route
+    (scaled) plus one for the
     final rounding: ``slack`` is that bound per element (moe_oracle.rounding_slack).  A
     legitimate one-ulp flip of an activation (fp32 accumulation order, the epilogue's exp)
     moves every column of its route a little further, so up to 0.1 % of elements may exceed
@@ -81,14 +82,15 @@ def assert_moe_parity(actual: torch.Tensor, stage_reference: torch.Tensor, fp32_
 
 
 def assert_within_ulps(actual: torch.Tensor, expected: torch.Tensor, ulps: float = 1.0, exact_fraction: float = 0.99):
-    """Elementwise |a - e| <= ulps * ulp(e) and at least ``exact_fraction`` bit-identical."""
+    """Elementwise |a - e| <= ulps * ulp(e) (ulp of e's dtype, bf16 or fp16) and at least
+    ``exact_fraction`` bit-identical."""
 
     a = actual.detach().cpu().float()
     e = expected.detach().cpu().float()
     assert torch.isfinite(a).all()
-    bound = ulps * o.bf16_ulp(e)
+    bound = ulps * _ulp(e, expected.dtype)
     over = int(((a - e).abs() > bound).sum().item())
-    assert over == 0, f"{over} elements beyond {ulps} bf16 ulp (max diff {(a - e).abs().max().item():.3e})"
+    assert over == 0, f"{over} elements beyond {ulps} ulp (max diff {(a - e).abs().max().item():.3e})"
     exact = float((actual.detach().cpu().view(torch.int16) == expected.detach().cpu().view(torch.int16)).float().mean())
     assert exact >= exact_fraction, f"only {exact:.4f} of elements are bit-identical"
 
@@ -108,49 +110,67 @@ def assert_within_ulps(actual: torch.Tensor, expected: torch.Tensor, ulps: float
 ACCUMULATION_BOUND = 2.0**-17
 
 
-def _bf16_key(b: torch.Tensor) -> torch.Tensor:
+def _ulp(values: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    return o.bf16_ulp(values) if dtype is torch.bfloat16 else o.f16_ulp(values)
+
+
+def _key(b: torch.Tensor) -> torch.Tensor:
+    """Order-preserving integer key of 16-bit floats (sign-magnitude bits: bf16 and fp16)."""
+
     bits = b.contiguous().view(torch.int16).to(torch.int32) & 0xFFFF
     magnitude = bits & 0x7FFF
     return torch.where(bits >= 0x8000, -magnitude, magnitude)
 
 
-def _bf16_from_key(key: torch.Tensor) -> torch.Tensor:
+def _from_key(key: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     bits = torch.where(key >= 0, key, 0x8000 | (-key))
     signed = bits - 0x10000 * (bits >= 0x8000).to(torch.int32)  # two's-complement int16 range
-    return signed.to(torch.int16).view(torch.bfloat16)
+    return signed.to(torch.int16).view(dtype)
+
+
+def step16(b: torch.Tensor, steps: int) -> torch.Tensor:
+    """The value of b's dtype ``steps`` representable values above (negative: below) ``b``."""
+
+    return _from_key(_key(b) + steps, b.dtype)
+
+
+def floor16(v: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    b = v.to(dtype)
+    return torch.where(b.double() > v, step16(b, -1), b)
+
+
+def ceil16(v: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    b = v.to(dtype)
+    return torch.where(b.double() < v, step16(b, 1), b)
 
 
 def bf16_step(b: torch.Tensor, steps: int) -> torch.Tensor:
-    """The bf16 value ``steps`` representable values above (negative: below) ``b``."""
-
-    return _bf16_from_key(_bf16_key(b) + steps)
+    return step16(b, steps)
 
 
 def bf16_floor(v: torch.Tensor) -> torch.Tensor:
-    b = v.to(torch.bfloat16)
-    return torch.where(b.double() > v, bf16_step(b, -1), b)
+    return floor16(v, torch.bfloat16)
 
 
 def bf16_ceil(v: torch.Tensor) -> torch.Tensor:
-    b = v.to(torch.bfloat16)
-    return torch.where(b.double() < v, bf16_step(b, 1), b)
+    return ceil16(v, torch.bfloat16)
 
 
-def projection_interval(x: torch.Tensor, w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """bf16 interval a correctly implemented fp32-accumulated ``round(x w^T)`` must land in."""
+def projection_interval(x: torch.Tensor, w: torch.Tensor, dtype: torch.dtype = torch.bfloat16):
+    """Interval (of ``dtype``) a correctly implemented fp32-accumulated ``round(x w^T)`` must land in."""
 
     exact = x.double() @ w.double().t()
     delta = (x.double().abs() @ w.double().abs().t()) * ACCUMULATION_BOUND
-    return bf16_floor(exact - delta), bf16_ceil(exact + delta)
+    return floor16(exact - delta, dtype), ceil16(exact + delta, dtype)
 
 
 def assert_projection_within_bounds(actual: torch.Tensor, x: torch.Tensor, w: torch.Tensor, exact_fraction=0.99):
-    lo, hi = projection_interval(x, w)
     a = actual.detach().cpu()
+    lo, hi = projection_interval(x, w, a.dtype)
     assert torch.isfinite(a.float()).all()
     outside = int(((a.double() < lo.double()) | (a.double() > hi.double())).sum().item())
     assert outside == 0, f"{outside} of {a.numel()} projections outside their fp32-accumulation interval"
-    nominal = (x.double() @ w.double().t()).to(torch.bfloat16)
+    nominal = (x.double() @ w.double().t()).to(a.dtype)
     exact = float((a.view(torch.int16) == nominal.view(torch.int16)).float().mean())
     assert exact >= exact_fraction, f"only {exact:.4f} of projections are bit-identical to the fp64 oracle"
 
@@ -158,7 +178,7 @@ def assert_projection_within_bounds(actual: torch.Tensor, x: torch.Tensor, w: to
 def _candidates(lo: torch.Tensor, hi: torch.Tensor) -> list[torch.Tensor]:
     values = [lo, hi]
     for steps in (1, 2):
-        stepped = bf16_step(lo, steps)
+        stepped = step16(lo, steps)
         values.append(torch.where(stepped.double() <= hi.double(), stepped, hi))
     return values
 
@@ -166,22 +186,23 @@ def _candidates(lo: torch.Tensor, hi: torch.Tensor) -> list[torch.Tensor]:
 def assert_activated_within_bounds(
     actual: torch.Tensor, x: torch.Tensor, w_gate_up: torch.Tensor, exact_fraction: float = 0.99, **act
 ) -> None:
-    g_lo, g_hi = projection_interval(x, w_gate_up[0::2])
-    u_lo, u_hi = projection_interval(x, w_gate_up[1::2])
+    dtype = actual.dtype
+    g_lo, g_hi = projection_interval(x, w_gate_up[0::2], dtype)
+    u_lo, u_hi = projection_interval(x, w_gate_up[1::2], dtype)
     low = high = None
     for g in _candidates(g_lo, g_hi):
         for u in _candidates(u_lo, u_hi):
-            h = o.gated_silu(g, u, **act).double()
+            h = o.gated_silu(g, u, dtype=dtype, **act).double()
             low = h if low is None else torch.minimum(low, h)
             high = h if high is None else torch.maximum(high, h)
-    slack_low = o.bf16_ulp(low.float()).double()
-    slack_high = o.bf16_ulp(high.float()).double()
+    slack_low = _ulp(low.float(), dtype).double()
+    slack_high = _ulp(high.float(), dtype).double()
     a = actual.detach().cpu()
     assert torch.isfinite(a.float()).all()
     value = a.double()
     outside = int(((value < low - slack_low) | (value > high + slack_high)).sum().item())
     assert outside == 0, f"{outside} of {a.numel()} activations outside their rounding-point interval"
-    nominal = stage_activated(x, w_gate_up, **act)
+    nominal = stage_activated(x, w_gate_up, dtype=dtype, **act)
     exact = float((a.view(torch.int16) == nominal.view(torch.int16)).float().mean())
     assert exact >= exact_fraction, f"only {exact:.4f} of activations are bit-identical to the oracle"
 
@@ -192,9 +213,11 @@ def assert_moe_stages(intermediates: dict, x, w_gate_up, w_down, ids, weights, o
 
     * the sort: every live route appears once, grouped by expert, ``expert_end`` consistent;
     * activations within their fp32-accumulation intervals (assert_activated_within_bounds);
-    * route outputs ``bf16(fp32(h . w_down[e]) * gamma)`` within the interval of the GPU's
-      activations (widened by the fp32 product's rounding);
-    * the combine ``bf16(scale * sum over slots in order of float(route))`` bit for bit.
+    * route outputs ``p(fp32(h . w_down[e]) * gamma)`` within the interval of the GPU's
+      activations (widened by the fp32 product's rounding), p the payload rounding;
+    * the combine ``p(scale * sum over slots in order of float(route))`` bit for bit.
+
+    The payload dtype (bf16 or fp16) is the activations'.
     """
 
     rows, topk = ids.shape
@@ -205,11 +228,12 @@ def assert_moe_stages(intermediates: dict, x, w_gate_up, w_down, ids, weights, o
     activated = intermediates["activated"].cpu()[:live]
     route_out = intermediates["route_out"].cpu()
     expert_end = intermediates["expert_end"].cpu().long()
+    dtype = activated.dtype
     assert torch.equal(sorted_route.sort().values, torch.nonzero(flat_ids >= 0).flatten())
     experts_of = flat_ids[sorted_route]
     assert bool((experts_of[1:] >= experts_of[:-1]).all()), "routes are not grouped by expert"
     assert torch.equal(expert_end, torch.bincount(experts_of, minlength=experts).cumsum(0))
-    by_route = torch.zeros((rows * topk, activated.shape[1]), dtype=torch.bfloat16)
+    by_route = torch.zeros((rows * topk, activated.shape[1]), dtype=dtype)
     by_route[sorted_route] = activated
     gammas = weights.flatten().double()
     identical = 0
@@ -218,7 +242,7 @@ def assert_moe_stages(intermediates: dict, x, w_gate_up, w_down, ids, weights, o
         if q.numel() == 0:
             continue
         assert_activated_within_bounds(by_route[q], x[q // topk], w_gate_up[expert], exact_fraction=0.0, **act)
-        nominal = stage_activated(x[q // topk], w_gate_up[expert], **act)
+        nominal = stage_activated(x[q // topk], w_gate_up[expert], dtype=dtype, **act)
         identical += int((by_route[q].view(torch.int16) == nominal.view(torch.int16)).sum())
         h = by_route[q].double()
         w = w_down[expert].double()
@@ -229,7 +253,7 @@ def assert_moe_stages(intermediates: dict, x, w_gate_up, w_down, ids, weights, o
         low = low - low.abs() * 2.0**-23
         high = high + high.abs() * 2.0**-23
         got = route_out[q].double()
-        outside = int(((got < bf16_floor(low).double()) | (got > bf16_ceil(high).double())).sum())
+        outside = int(((got < floor16(low, dtype).double()) | (got > ceil16(high, dtype).double())).sum())
         assert outside == 0, f"expert {expert}: {outside} route outputs outside their interval"
     assert identical >= 0.99 * live * activated.shape[1], "fewer than 99 % of activations match the oracle's bits"
     total = torch.zeros((rows, route_out.shape[1]), dtype=torch.float32)
@@ -237,14 +261,14 @@ def assert_moe_stages(intermediates: dict, x, w_gate_up, w_down, ids, weights, o
         valid = ((ids[:, slot] >= 0) & (ids[:, slot] < experts)).unsqueeze(1)
         routes = route_out[torch.arange(rows) * topk + slot].float()
         total = total + torch.where(valid, routes, torch.zeros_like(routes))
-    assert_bitwise_equal(output, (total * torch.tensor(scale, dtype=torch.float32)).to(torch.bfloat16))
+    assert_bitwise_equal(output, (total * torch.tensor(scale, dtype=torch.float32)).to(dtype))
 
 
-def stage_activated(x: torch.Tensor, w_gate_up: torch.Tensor, **act) -> torch.Tensor:
-    """Oracle gate_up + gated SiLU with the reference's rounding points."""
+def stage_activated(x: torch.Tensor, w_gate_up: torch.Tensor, dtype: torch.dtype = torch.bfloat16, **act) -> torch.Tensor:
+    """Oracle gate_up + gated SiLU with the reference's rounding points, in the payload ``dtype``."""
 
     projected = x.double() @ w_gate_up.double().t()
-    return o.gated_silu(projected[:, 0::2].to(torch.bfloat16), projected[:, 1::2].to(torch.bfloat16), **act)
+    return o.gated_silu(projected[:, 0::2].to(dtype), projected[:, 1::2].to(dtype), dtype=dtype, **act)
 
 
 def to_device(tensor: torch.Tensor, device) -> torch.Tensor:

@@ -1,14 +1,16 @@
 """GPU parity of the MoE Router, routing finalisation and Experts against oracle/moe_oracle.py.
 
 Router cases are the reference's own routing tests (routing/test_softmax_payload.py,
-test_softmax_fp32.py, test_sigmoid.py, test_metadata.py): ids must match exactly and
-weights within rtol 1e-5 / atol 1e-6, the reference's tolerance.  On random Qwen3-MoE-shaped
+test_softmax_fp32.py, test_sigmoid.py, test_metadata.py), with bf16 and fp16 payloads as
+those tests parametrize them: ids must match exactly and weights within rtol 1e-5 /
+atol 1e-6, the reference's tolerance.  On random Qwen3-MoE-shaped
 inputs the projection's bf16 logits must lie in their fp32-accumulation intervals and the
 TopK over those logits must match the oracle's TopK on the same logits.  Experts outputs meet
 the MoE bar of tests/parity.py against the reference's expected-value formula
 (test_operators.py:255-281) and its pure-fp32 counterpart, every stage (sort, activations,
 route outputs, combine) is checked rigorously on the GPU's own intermediates, and outputs
-repeat bit for bit.
+repeat bit for bit.  fp16 Experts (test_operators.py:114) run on every grouped kernel
+family with fp16 rounding points in the oracle.
 """
 
 from __future__ import annotations
@@ -27,6 +29,7 @@ from parity import to_device
 pytestmark = pytest.mark.gpu
 
 TWO_ROWS = ((3.0, 1.0, -1.0, -3.0), (-2.0, 0.0, 2.0, 4.0))
+PAYLOADS = pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16), ids=("bfloat16", "float16"))
 
 
 def _router(device, hidden_states, projection, **kwargs):
@@ -36,26 +39,32 @@ def _router(device, hidden_states, projection, **kwargs):
     return router
 
 
+@PAYLOADS
 @pytest.mark.parametrize("rounding", tuple(TopKWeightRounding))
-def test_softmax_payload_router(device, rounding):
-    hidden = torch.tensor(TWO_ROWS, dtype=torch.bfloat16)
-    projection = torch.eye(4, dtype=torch.bfloat16)
+def test_softmax_payload_router(device, rounding, dtype):
+    # routing/test_softmax_payload.py:16-60
+    hidden = torch.tensor(TWO_ROWS, dtype=dtype)
+    projection = torch.eye(4, dtype=dtype)
     router = _router(device, hidden, projection, routed_topk=2, algorithm=RouterAlgorithm.SOFTMAX,
-                     precision=RouterProjectionPrecision.PAYLOAD, renormalize=True, weight_rounding=rounding)
+                     precision=RouterProjectionPrecision.PAYLOAD, renormalize=True, weight_rounding=rounding,
+                     payload_dtype=dtype)
     router.run_into(hidden_states=to_device(hidden, device), router_weights=MoeRouterWeights(to_device(projection, device)))
-    ids, weights = m.router_topk(m.router_logits(hidden, projection, payload=True), topk=2, softmax=True,
-                                 round_weights=rounding is TopKWeightRounding.LOGITS_DTYPE, logits_bf16=True)
+    assert router.logits.dtype is dtype
+    ids, weights = m.router_topk(m.router_logits(hidden, projection, payload=True, dtype=dtype), topk=2, softmax=True,
+                                 round_weights=rounding is TopKWeightRounding.LOGITS_DTYPE, logits_dtype=dtype)
     assert torch.equal(router.ids.cpu(), ids) and ids.tolist() == [[0, 1], [3, 2]]
     torch.testing.assert_close(router.weights.cpu(), weights, rtol=1e-5, atol=1e-6)
 
 
+@PAYLOADS
 @pytest.mark.parametrize("corrected", (False, True))
-def test_softmax_fp32_logits_router_with_correction(device, corrected):
-    hidden = torch.tensor(TWO_ROWS, dtype=torch.bfloat16)
-    projection = torch.eye(4, dtype=torch.bfloat16)
+def test_softmax_fp32_logits_router_with_correction(device, corrected, dtype):
+    # routing/test_softmax_fp32.py:15-60
+    hidden = torch.tensor(TWO_ROWS, dtype=dtype)
+    projection = torch.eye(4, dtype=dtype)
     bias = torch.tensor((-0.75, -0.25, 0.5, 0.8)) if corrected else None
     router = _router(device, hidden, projection, routed_topk=2, algorithm=RouterAlgorithm.SOFTMAX,
-                     precision=RouterProjectionPrecision.FP32_LOGITS, renormalize=False)
+                     precision=RouterProjectionPrecision.FP32_LOGITS, renormalize=False, payload_dtype=dtype)
     weights_gpu = MoeRouterWeights(to_device(projection, device), None if bias is None else to_device(bias, device))
     router.run_into(hidden_states=to_device(hidden, device), router_weights=weights_gpu)
     ids, weights = m.router_topk(m.router_logits(hidden, projection, payload=False), topk=2, softmax=True,
@@ -64,13 +73,15 @@ def test_softmax_fp32_logits_router_with_correction(device, corrected):
     torch.testing.assert_close(router.weights.cpu(), weights, rtol=1e-5, atol=1e-6)
 
 
+@PAYLOADS
 @pytest.mark.parametrize("experts,topk,scale", ((64, 4, 4096.0), (48, 3, None), (17, 1, 1.0), (17, 17, 1.0)))
-def test_sigmoid_fp32_router_diagonal(device, experts, topk, scale):
-    hidden = (torch.arange(2 * experts, dtype=torch.float32).view(2, experts) / (2 * experts)).to(torch.bfloat16)
+def test_sigmoid_fp32_router_diagonal(device, experts, topk, scale, dtype):
+    # routing/test_sigmoid.py:15-73
+    hidden = (torch.arange(2 * experts, dtype=torch.float32).view(2, experts) / (2 * experts)).to(dtype)
     bias = torch.linspace(-0.25, 0.25, experts) * scale if scale is not None else None
     projection = torch.diag(torch.linspace(0.101, 1.909, experts))
     router = _router(device, hidden, projection, routed_topk=topk, algorithm=RouterAlgorithm.SIGMOID,
-                     precision=RouterProjectionPrecision.FP32, renormalize=True)
+                     precision=RouterProjectionPrecision.FP32, renormalize=True, payload_dtype=dtype)
     weights_gpu = MoeRouterWeights(to_device(projection, device), None if bias is None else to_device(bias, device))
     router.run_into(hidden_states=to_device(hidden, device), router_weights=weights_gpu)
     ids, weights = m.router_topk(m.router_logits(hidden, projection, payload=False), topk=topk, softmax=False,
@@ -96,18 +107,21 @@ def test_router_tie_policy(device, algorithm):
                                atol=1e-6)
 
 
+@PAYLOADS
 @pytest.mark.parametrize("rows", (1, 16, 200))
-def test_qwen3_moe_router_projection_and_topk(device, rows):
+def test_qwen3_moe_router_projection_and_topk(device, rows, dtype):
     # Qwen3-30B-A3B router: 128 experts over hidden 2048, top-8, softmax, renormalised.
     hidden, experts = 2048, 128
-    x = o.generate_hidden_states(rows, hidden, 70 + rows)
+    x = o.generate_hidden_states(rows, hidden, 70 + rows).to(dtype)
     generator = torch.Generator().manual_seed(71)
-    projection = (torch.randn((experts, hidden), generator=generator) * 0.02).to(torch.bfloat16)
-    router = Router(row_capacity=rows, hidden_size=hidden, routed_expert_count=experts, routed_topk=8, device=device)
+    projection = (torch.randn((experts, hidden), generator=generator) * 0.02).to(dtype)
+    router = Router(row_capacity=rows, hidden_size=hidden, routed_expert_count=experts, routed_topk=8, device=device,
+                    payload_dtype=dtype)
     router.run_into(hidden_states=to_device(x, device), router_weights=MoeRouterWeights(to_device(projection, device)))
     logits = router.logits.cpu()
+    assert logits.dtype is dtype
     assert_projection_within_bounds(logits, x, projection)
-    ids, weights = m.router_topk(logits.float(), topk=8, softmax=True, logits_bf16=True)
+    ids, weights = m.router_topk(logits.float(), topk=8, softmax=True, logits_dtype=dtype)
     assert torch.equal(router.ids.cpu(), ids)
     torch.testing.assert_close(router.weights.cpu(), weights, rtol=1e-5, atol=1e-6)
     # TopK alone over the same logits.
@@ -135,6 +149,27 @@ def test_topk_at_every_expert_width(device, experts, softmax):
     torch.testing.assert_close(weights.cpu(), expected_weights, rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("softmax", (True, False), ids=("softmax", "sigmoid"))
+@pytest.mark.parametrize("experts", (17, 128, 300))
+def test_topk_over_fp16_logits(device, experts, softmax):
+    # fp16 logits (an fp16 layer's PAYLOAD projection): the sigmoid selection is rounded to
+    # fp16, as the LOGITS_DTYPE weight rounding is; values on a grid of sixteenths keep ties.
+    rows, topk = 29, 6
+    generator = torch.Generator().manual_seed(600 + experts)
+    logits = (torch.randint(-48, 49, (rows, experts), generator=generator).float() / 16).half()
+    bias = None if softmax else torch.randint(-4, 5, (experts,), generator=generator).float() / 1024
+    algorithm = RouterAlgorithm.SOFTMAX if softmax else RouterAlgorithm.SIGMOID
+    for rounding in tuple(TopKWeightRounding):
+        ids, weights = router_topk(to_device(logits, device), topk=topk, algorithm=algorithm,
+                                   correction_bias=None if bias is None else to_device(bias, device),
+                                   weight_rounding=rounding)
+        expected_ids, expected_weights = m.router_topk(
+            logits.float(), topk=topk, softmax=softmax, correction_bias=bias, logits_dtype=torch.float16,
+            round_weights=rounding is TopKWeightRounding.LOGITS_DTYPE)
+        assert torch.equal(ids.cpu(), expected_ids)
+        torch.testing.assert_close(weights.cpu(), expected_weights, rtol=1e-5, atol=1e-6)
+
+
 def test_finalize_routing_dynamic_live_rows(device):
     # routing/test_metadata.py:8-80
     routed_ids = torch.tensor(((0, 2), (1, 3), (2, 0), (3, 1)), dtype=torch.int32, device=device)
@@ -158,39 +193,47 @@ def _run_experts(device, x, w_gate_up, w_down, ids, weights, scale=1.0, activati
     experts, two_i, _ = w_gate_up.shape
     operator = Experts(row_capacity=rows, hidden_size=hidden, local_intermediate_size=two_i // 2,
                        expert_count=experts, effective_topk=ids.shape[1], routed_scaling_factor=scale,
-                       activation=activation, gate=gate, device=device)
+                       activation=activation, gate=gate, device=device, payload_dtype=x.dtype)
     weights_gpu = MoeFfnWeights(to_device(w_gate_up, device), to_device(w_down, device))
-    output = torch.empty((rows, hidden), dtype=torch.bfloat16, device=device)
+    output = torch.empty((rows, hidden), dtype=x.dtype, device=device)
     operator.run_into(hidden_states=to_device(x, device), weights=weights_gpu, topk_ids=to_device(ids, device),
                       topk_weights=to_device(weights, device), output=output)
     return output.cpu(), operator, weights_gpu
 
 
 def _check_experts(got, x, w_gate_up, w_down, ids, weights, scale=1.0, **act):
-    routes = m.experts_routes(x, w_gate_up, w_down, ids, weights, **act)
-    stage = m.experts_reference(x, w_gate_up, w_down, ids, weights, routed_scaling_factor=scale, **act)
+    dtype = x.dtype
+    assert got.dtype is dtype
+    routes = m.experts_routes(x, w_gate_up, w_down, ids, weights, dtype=dtype, **act)
+    stage = m.experts_reference(x, w_gate_up, w_down, ids, weights, routed_scaling_factor=scale, dtype=dtype, **act)
     pure = m.experts_fp32(x, w_gate_up, w_down, ids, weights, routed_scaling_factor=scale, **act)
-    assert_moe_parity(got, stage, pure, m.rounding_slack(routes, stage, scale))
+    assert_moe_parity(got, stage, pure, m.rounding_slack(routes, stage, scale, dtype=dtype))
 
 
-@pytest.mark.parametrize("act", ({}, {"alpha": 1.702, "limit": 7.0, "up_offset": 1.0}))
-def test_experts_reference_operator_case(device, act):
-    # test_operators.py:121-281: four experts, two slots, a dead row, scale 1.5.
+@pytest.mark.parametrize(
+    "dtype,act",
+    ((torch.bfloat16, {}), (torch.float16, {}), (torch.bfloat16, {"alpha": 1.702, "limit": 7.0, "up_offset": 1.0})),
+    ids=("bfloat16", "float16", "bfloat16-swiglu"),
+)
+def test_experts_reference_operator_case(device, dtype, act):
+    # test_operators.py:110-281: four experts, two slots, a dead row, scale 1.5, the
+    # reference's bf16 and fp16 payload cases.
     generator = torch.Generator().manual_seed(31)
-    x = (torch.randn((4, 16), generator=generator) / 4).to(torch.bfloat16)
-    w_gate_up = (torch.randn((4, 16, 16), generator=generator) / 4).to(torch.bfloat16)
-    w_down = (torch.randn((4, 16, 8), generator=generator) / 4).to(torch.bfloat16)
+    x = (torch.randn((4, 16), generator=generator) / 4).to(dtype)
+    w_gate_up = (torch.randn((4, 16, 16), generator=generator) / 4).to(dtype)
+    w_down = (torch.randn((4, 16, 8), generator=generator) / 4).to(dtype)
     ids = torch.tensor(((0, 1), (2, 3), (1, 3), (-1, -1)), dtype=torch.int32)
     weights = torch.tensor(((0.75, 0.25), (0.6, 0.4), (0.9, 0.1), (0.0, 0.0)))
     activation = SiluActivation(act.get("alpha", 1.0))
     gate = GateTransform(limit=act.get("limit"), up_offset=act.get("up_offset", 0.0))
     got, operator, _ = _run_experts(device, x, w_gate_up, w_down, ids, weights, 1.5, activation, gate)
     assert_moe_stages(operator.intermediates(), x, w_gate_up, w_down, ids, weights, got, 1.5, **act)
-    stage = m.experts_reference(x, w_gate_up, w_down, ids, weights, routed_scaling_factor=1.5, **act)
-    routes = m.experts_routes(x, w_gate_up, w_down, ids, weights, **act)
+    stage = m.experts_reference(x, w_gate_up, w_down, ids, weights, routed_scaling_factor=1.5, dtype=dtype, **act)
+    routes = m.experts_routes(x, w_gate_up, w_down, ids, weights, dtype=dtype, **act)
+    assert got.dtype is dtype
     torch.testing.assert_close(got, stage, rtol=0.02, atol=0.1)
     gap = (got.float() - stage.float()).abs()
-    assert (gap <= m.rounding_slack(routes, stage, 1.5)).all()
+    assert (gap <= m.rounding_slack(routes, stage, 1.5, dtype=dtype)).all()
     assert o.compare(stage, got).normalized_rmse <= 0.01
     assert got[3].abs().sum() == 0
 
@@ -249,6 +292,36 @@ def test_experts_decode_tiles_skewed_routing(device, hidden, intermediate):
     _check_experts(got, x, w_gate_up, w_down, ids, weights, scale=1.25)
     assert_moe_stages(operator.intermediates(), x, w_gate_up, w_down, ids, weights, got, 1.25)
     again = torch.empty((rows, hidden), dtype=torch.bfloat16, device=device)
+    operator.run_into(hidden_states=to_device(x, device), weights=weights_gpu, topk_ids=to_device(ids, device),
+                      topk_weights=to_device(weights, device), output=again)
+    assert_bitwise_equal(again.cpu(), got)
+
+
+@pytest.mark.parametrize(
+    "rows,hidden,intermediate,experts,topk",
+    (
+        (1, 2048, 768, 128, 8),     # grouped split, one route per expert
+        (48, 2048, 768, 128, 8),    # grouped split, 16-route tiles
+        (320, 2048, 768, 128, 8),   # 64-row grouped tiles
+        (240, 256, 128, 8, 2),      # 128-row grouped tiles, nontemporal weight loads
+        (480, 256, 128, 8, 2),      # 128-row grouped tiles
+        (1024, 256, 128, 8, 2),     # 256-row grouped tiles
+    ),
+)
+def test_experts_fp16_every_tile_family(device, rows, hidden, intermediate, experts, topk):
+    # fp16 payloads (test_operators.py:114) through each grouped kernel the chooser takes,
+    # with fp16 rounding points in the oracle and every stage checked.  Weights are drawn in
+    # fp32 and stored in fp16, as an fp16 checkpoint holds them.
+    w_gate_up, w_down = m.generate_moe_layer(hidden, intermediate, experts, 140 + rows, std=0.05,
+                                             dtype=torch.float16)
+    x = o.generate_hidden_states(rows, hidden, 141 + rows).half()
+    ids, weights = m.generate_routes(rows, experts, topk, 142 + rows)
+    ids[rows // 2: rows // 2 + rows // 8] = -1
+    weights[rows // 2: rows // 2 + rows // 8] = 0.0
+    got, operator, weights_gpu = _run_experts(device, x, w_gate_up, w_down, ids, weights, scale=1.25)
+    _check_experts(got, x, w_gate_up, w_down, ids, weights, scale=1.25)
+    assert_moe_stages(operator.intermediates(), x, w_gate_up, w_down, ids, weights, got, 1.25)
+    again = torch.empty((rows, hidden), dtype=torch.float16, device=device)
     operator.run_into(hidden_states=to_device(x, device), weights=weights_gpu, topk_ids=to_device(ids, device),
                       topk_weights=to_device(weights, device), output=again)
     assert_bitwise_equal(again.cpu(), got)

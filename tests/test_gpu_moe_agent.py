@@ -7,8 +7,9 @@ reference's captured MoE body, registry.py:242-339, on the Router-owner role).  
 is checked on the GPU's own previous stage, read from the Lane workspace
 (xp_moe_step_workspace_layout):
 
-* the gathered batch within one bf16 ulp of the oracle's RMSNorm (bitwise without a norm);
-* bf16 logits in their fp32-accumulation intervals (fp32 logits within the fp32 sum bound);
+* the gathered batch within one ulp of the oracle's RMSNorm (bitwise without a norm);
+* payload-dtype logits in their fp32-accumulation intervals (fp32 logits within the fp32
+  sum bound);
 * routed ids equal to the oracle's TopK over the GPU's logits, weights within the
   reference's rtol 1e-5 / atol 1e-6; final ids and weights equal to the oracle's finalisation;
 * the Experts stages (assert_moe_stages) and the MoE output bar (assert_moe_parity) on the
@@ -16,7 +17,8 @@ is checked on the GPU's own previous stage, read from the Lane workspace
 * mailbox rows outside the slots untouched bit for bit.
 
 Replays through the hipGraph (graph dispatch) and the standalone operator chain at the
-template's capacity repeat the direct replay bit for bit.
+template's capacity repeat the direct replay bit for bit.  Layers registered with fp16
+weights replay with fp16 payloads and are checked at fp16 rounding points.
 """
 
 from __future__ import annotations
@@ -43,14 +45,14 @@ from parity import assert_projection_within_bounds, assert_within_ulps, slots_te
 pytestmark = pytest.mark.gpu
 
 
-def _layer(hidden, intermediate, spec, seed, std=0.05):
-    w_gate_up, w_down = m.generate_moe_layer(hidden, intermediate, spec.expert_count, seed, std=std)
+def _layer(hidden, intermediate, spec, seed, std=0.05, dtype=torch.bfloat16):
+    w_gate_up, w_down = m.generate_moe_layer(hidden, intermediate, spec.expert_count, seed, std=std, dtype=dtype)
     generator = torch.Generator().manual_seed(seed + 1)
     projection = torch.randn((spec.routed_expert_count, hidden), generator=generator) * 0.05
     if spec.router_projection_precision is not RouterProjectionPrecision.FP32:
-        projection = projection.to(torch.bfloat16)
+        projection = projection.to(dtype)
     correction = torch.randn((spec.routed_expert_count,), generator=generator) * 0.01
-    norm_weight = (1.0 + 0.1 * torch.randn((hidden,), generator=generator)).to(torch.bfloat16)
+    norm_weight = (1.0 + 0.1 * torch.randn((hidden,), generator=generator)).to(dtype)
     return w_gate_up, w_down, projection, correction, norm_weight
 
 
@@ -65,11 +67,11 @@ def _act(spec):
     return act
 
 
-def _lane_stages(lane, spec, hidden, intermediate, capacity, rows):
+def _lane_stages(lane, spec, hidden, intermediate, capacity, rows, dtype=torch.bfloat16):
     """The Lane workspace regions of one MoE replay at ``capacity`` (live ``rows``)."""
 
     desc = spec.signature(
-        hidden_size=hidden, local_intermediate_size=intermediate, payload_row_capacity=capacity
+        hidden_size=hidden, local_intermediate_size=intermediate, payload_row_capacity=capacity, payload_dtype=dtype
     ).native_descriptor()
     batch_at, logits_at, rid_at, rw_at, fid_at, fw_at, experts_at, total = _native.moe_step_workspace_layout(
         desc, capacity
@@ -87,8 +89,8 @@ def _lane_stages(lane, spec, hidden, intermediate, capacity, rows):
     _native.call("xp_moe_workspace_layout", capacity, hidden, intermediate, experts, effective, offsets)
     routes = rows * effective
     return {
-        "batch": view(batch_at, torch.bfloat16, (rows, hidden)),
-        "logits": view(logits_at, torch.float32 if fp32_logits else torch.bfloat16, (rows, spec.routed_expert_count)),
+        "batch": view(batch_at, dtype, (rows, hidden)),
+        "logits": view(logits_at, torch.float32 if fp32_logits else dtype, (rows, spec.routed_expert_count)),
         "routed_ids": view(rid_at, torch.int32, (rows, routed)),
         "routed_weights": view(rw_at, torch.float32, (rows, routed)),
         "final_ids": view(fid_at, torch.int32, (rows, effective)),
@@ -96,14 +98,15 @@ def _lane_stages(lane, spec, hidden, intermediate, capacity, rows):
         "experts": {
             "expert_end": view(experts_at + offsets[0], torch.int32, (experts,)),
             "sorted_route": view(experts_at + offsets[1], torch.int32, (routes,)),
-            "activated": view(experts_at + offsets[4], torch.bfloat16, (routes, intermediate)),
-            "route_out": view(experts_at + offsets[5], torch.bfloat16, (routes, hidden)),
+            "activated": view(experts_at + offsets[4], dtype, (routes, intermediate)),
+            "route_out": view(experts_at + offsets[5], dtype, (routes, hidden)),
         },
     }
 
 
 def _check_replay(stages, pool, new_pool, slots, spec, w_gate_up, w_down, projection, correction, norm_weight):
     rows = len(slots)
+    dtype = pool.dtype
     untouched = np.setdiff1d(np.arange(pool.shape[0]), slots)
     assert_bitwise_equal(new_pool[untouched], pool[untouched])
     batch = stages["batch"]
@@ -120,7 +123,7 @@ def _check_replay(stages, pool, new_pool, slots, spec, w_gate_up, w_down, projec
         # enough logits to be meaningful (one differing logit of 72 is 1.4 %).
         assert_projection_within_bounds(logits, batch, projection, exact_fraction=0.99 if logits.numel() >= 1024 else 0.9)
     else:
-        # fp32 sums of exact products (bf16 x bf16 or widened bf16 x fp32): the ordered-sum
+        # fp32 sums of exact products (16-bit x 16-bit or widened 16-bit x fp32): the ordered-sum
         # bound K * 2^-24 * sum |x w|, doubled for the product rounding of fp32 weights.
         exact = batch.double() @ projection.double().t()
         bound = (batch.double().abs() @ projection.double().abs().t()) * (batch.shape[1] * 2.0**-23) + 1e-30
@@ -131,7 +134,7 @@ def _check_replay(stages, pool, new_pool, slots, spec, w_gate_up, w_down, projec
         logits.float(), topk=spec.routed_topk, softmax=softmax, correction_bias=correction,
         renormalize=spec.renormalize,
         round_weights=spec.topk_weight_rounding is TopKWeightRounding.LOGITS_DTYPE,
-        logits_bf16=precision is RouterProjectionPrecision.PAYLOAD,
+        logits_dtype=dtype if precision is RouterProjectionPrecision.PAYLOAD else None,
     )
     assert torch.equal(stages["routed_ids"], ids)
     torch.testing.assert_close(stages["routed_weights"], weights, rtol=1e-5, atol=1e-6)
@@ -147,11 +150,12 @@ def _check_replay(stages, pool, new_pool, slots, spec, w_gate_up, w_down, projec
     act = _act(spec)
     scale = spec.routed_scaling_factor
     assert_moe_stages(stages["experts"], batch, w_gate_up, w_down, final_ids, final_weights, output, scale, **act)
-    routes = m.experts_routes(batch, w_gate_up, w_down, final_ids, final_weights, **act)
+    routes = m.experts_routes(batch, w_gate_up, w_down, final_ids, final_weights, dtype=dtype, **act)
     stage = m.experts_reference(batch, w_gate_up, w_down, final_ids, final_weights, routed_scaling_factor=scale,
-                                **act)
+                                dtype=dtype, **act)
     pure = m.experts_fp32(batch, w_gate_up, w_down, final_ids, final_weights, routed_scaling_factor=scale, **act)
-    assert_moe_parity(output, stage, pure, m.rounding_slack(routes, stage, scale))
+    assert output.dtype is dtype
+    assert_moe_parity(output, stage, pure, m.rounding_slack(routes, stage, scale, dtype=dtype))
 
 
 def _register(agent, spec, hidden, w_gate_up, w_down, projection, correction, norm_weight, device, ordinal=0,
@@ -208,10 +212,51 @@ CASES = [
 ]
 
 
-@pytest.mark.parametrize("hidden,intermediate,spec,corrected,normed,maximum,replays", CASES)
+FP16_CASES = [
+    pytest.param(
+        512, 256, MoeLayerSpec(routed_expert_count=16, routed_topk=4), False, True, 64, (1, 5, 12, 33, 64),
+        id="fp16-softmax-payload-normed",
+    ),
+    pytest.param(
+        256, 128,
+        MoeLayerSpec(
+            routed_expert_count=12, routed_topk=3, shared_expert_count=2, renormalize=False,
+            routed_scaling_factor=2.5, router_algorithm=RouterAlgorithm.SIGMOID,
+            router_projection_precision=RouterProjectionPrecision.FP32,
+            activation=SiluActivation(1.702), gate=GateTransform(limit=7.0, up_offset=1.0),
+        ),
+        True, False, 24, (3, 24),
+        id="fp16-sigmoid-fp32-shared-corrected-clipped",
+    ),
+    pytest.param(
+        512, 192,
+        MoeLayerSpec(
+            routed_expert_count=24, routed_topk=2, shared_expert_count=1,
+            router_projection_precision=RouterProjectionPrecision.FP32_LOGITS,
+            topk_weight_rounding=TopKWeightRounding.LOGITS_DTYPE, routed_scaling_factor=1.5,
+        ),
+        True, True, 96, (7, 96),
+        id="fp16-softmax-fp32logits-shared",
+    ),
+    pytest.param(
+        256, 128,
+        MoeLayerSpec(routed_expert_count=200, routed_topk=5, router_algorithm=RouterAlgorithm.SIGMOID,
+                     topk_weight_rounding=TopKWeightRounding.LOGITS_DTYPE),
+        True, False, 24, (4, 24),
+        id="fp16-sigmoid-200-experts-corrected-rounded",
+    ),
+]
+
+
+@pytest.mark.parametrize(
+    "hidden,intermediate,spec,corrected,normed,maximum,replays,dtype",
+    [pytest.param(*case.values, torch.bfloat16, id=case.id) for case in CASES]
+    + [pytest.param(*case.values, torch.float16, id=case.id) for case in FP16_CASES],
+)
 def test_moe_layer_replays_through_its_template(device, hidden, intermediate, spec, corrected, normed, maximum,
-                                                replays):
-    w_gate_up, w_down, projection, correction, norm_weight = _layer(hidden, intermediate, spec, 300 + hidden)
+                                                replays, dtype):
+    w_gate_up, w_down, projection, correction, norm_weight = _layer(hidden, intermediate, spec, 300 + hidden,
+                                                                    dtype=dtype)
     if not normed:
         norm_weight = None
     pool_rows = 2 * maximum + 3
@@ -224,12 +269,12 @@ def test_moe_layer_replays_through_its_template(device, hidden, intermediate, sp
         lane = agent.lanes[0]
         for rows in replays:
             print(f"case hidden={hidden} intermediate={intermediate} rows={rows} spec={spec}", flush=True)
-            pool = o.generate_hidden_states(pool_rows, hidden, 400 + rows)
+            pool = o.generate_hidden_states(pool_rows, hidden, 400 + rows).to(dtype)
             slots = o.generate_slots(pool_rows, rows, 401 + rows)
             pool_gpu = to_device(pool, device)
             agent.execute(instance_index=0, layer_ordinal=0, pool=pool_gpu, slots=slots_tensor(slots, device))
             agent.check_health()
-            stages = _lane_stages(lane, spec, hidden, intermediate, select_capacity(capacities, rows), rows)
+            stages = _lane_stages(lane, spec, hidden, intermediate, select_capacity(capacities, rows), rows, dtype)
             _check_replay(stages, pool, pool_gpu.cpu(), slots, spec, w_gate_up, w_down, projection,
                           correction if corrected else None, norm_weight)
 
@@ -279,26 +324,29 @@ def test_moe_graph_dispatch_and_operator_chain_repeat_the_replay(device):
     assert_bitwise_equal(o.gather(outputs[rows][0], slots), output.cpu())
 
 
-def test_qwen3_30b_a3b_moe_layer_through_the_lane(device):
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16), ids=("bfloat16", "float16"))
+def test_qwen3_30b_a3b_moe_layer_through_the_lane(device, dtype):
     # Qwen3-30B-A3B MoE layer: hidden 2048, moe_intermediate 768, 128 experts, top-8, softmax,
     # renormalised (norm_topk_prob), post-attention RMSNorm fused into the gather.  1 row runs
     # the gather inside the router projection and the TopK inside the route sort, 32 rows take
     # the grouped split kernel (capacity 32), 200 rows the grouped tile kernel (capacity 256).
     hidden, intermediate = 2048, 768
     spec = MoeLayerSpec(routed_expert_count=128, routed_topk=8)
-    w_gate_up, w_down, projection, correction, norm_weight = _layer(hidden, intermediate, spec, 600, std=0.02)
+    w_gate_up, w_down, projection, correction, norm_weight = _layer(hidden, intermediate, spec, 600, std=0.02,
+                                                                    dtype=dtype)
     capacities = derive_payload_row_capacities(256)
     with FfnAgent(device) as agent:
         _register(agent, spec, hidden, w_gate_up, w_down, projection, correction, norm_weight, device)
         agent.materialize(maximum_row_capacity=256)
         for rows in (1, 32, 200):
-            print(f"case qwen3-30b-a3b rows={rows}", flush=True)
-            pool = o.generate_hidden_states(320, hidden, 601 + rows)
+            print(f"case qwen3-30b-a3b {dtype} rows={rows}", flush=True)
+            pool = o.generate_hidden_states(320, hidden, 601 + rows).to(dtype)
             slots = o.generate_slots(320, rows, 602 + rows)
             pool_gpu = to_device(pool, device)
             agent.execute(instance_index=0, layer_ordinal=0, pool=pool_gpu, slots=slots_tensor(slots, device))
             agent.check_health()
-            stages = _lane_stages(agent.lanes[0], spec, hidden, intermediate, select_capacity(capacities, rows), rows)
+            stages = _lane_stages(agent.lanes[0], spec, hidden, intermediate, select_capacity(capacities, rows), rows,
+                                  dtype)
             _check_replay(stages, pool, pool_gpu.cpu(), slots, spec, w_gate_up, w_down, projection, None,
                           norm_weight)
 
@@ -366,3 +414,18 @@ def test_moe_registration_rejects_mismatched_resources(device):
                 instance_index=0, layer_ordinal=0,
                 weights=MoeFfnWeights(to_device(w_gate_up, device), to_device(w_down, device), wide), spec=spec,
             )
+        # Payload dtypes must agree: an fp16 Router projection beside bf16 experts, an fp16
+        # expert pair with a bf16 norm weight, and bf16 gate_up with fp16 down are refused.
+        half_router = MoeRouterWeights(to_device(projection.half(), device))
+        with pytest.raises(ValueError, match="router projection"):
+            agent.register_moe_layer(
+                instance_index=0, layer_ordinal=0,
+                weights=MoeFfnWeights(to_device(w_gate_up, device), to_device(w_down, device), half_router),
+                spec=spec,
+            )
+        fp16 = MoeFfnWeights(to_device(w_gate_up.half(), device), to_device(w_down.half(), device), half_router)
+        with pytest.raises(ValueError, match="RMSNorm weight"):
+            agent.register_moe_layer(instance_index=0, layer_ordinal=0, weights=fp16, spec=spec,
+                                     norm_weight=torch.ones((hidden,), dtype=torch.bfloat16, device=device))
+        with pytest.raises(ValueError, match="both"):
+            MoeFfnWeights(to_device(w_gate_up, device), to_device(w_down.half(), device), router)

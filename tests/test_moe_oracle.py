@@ -11,11 +11,18 @@ the CrossPool checkout):
   time in fp32 with torch.mv exactly as the test writes it).
 
 The Experts oracle is also tied to the already-pinned Dense oracle: one expert, one route
-per row, weight 1 and scale 1 reduce it to ``dense_partial_reference`` bit for bit.
+per row, weight 1 and scale 1 reduce it to ``dense_partial_reference`` bit for bit.  The
+router and Experts pins run with bf16 and fp16 payloads, as the reference's tests are
+parametrized; the fp16 rounding points are pinned further by an exact-rational brute force
+with its own binary16 rounding rule.
 """
 
 from __future__ import annotations
 
+import math
+from fractions import Fraction
+
+import numpy as np
 import pytest
 import torch
 
@@ -23,29 +30,39 @@ from oracle import ffn_oracle as o
 from oracle import moe_oracle as m
 
 TWO_ROWS = ((3.0, 1.0, -1.0, -3.0), (-2.0, 0.0, 2.0, 4.0))
+PAYLOADS = pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16), ids=("bfloat16", "float16"))
 
 
+@PAYLOADS
 @pytest.mark.parametrize("round_weights", (False, True))
-def test_softmax_payload_router(round_weights):
-    hidden = torch.tensor(TWO_ROWS, dtype=torch.bfloat16)
-    logits = m.router_logits(hidden, torch.eye(4, dtype=torch.bfloat16), payload=True)
+def test_softmax_payload_router(round_weights, dtype):
+    hidden = torch.tensor(TWO_ROWS, dtype=dtype)
+    logits = m.router_logits(hidden, torch.eye(4, dtype=dtype), payload=True, dtype=dtype)
     ids, weights = m.router_topk(logits, topk=2, softmax=True, renormalize=True, round_weights=round_weights,
-                                 logits_bf16=True)
+                                 logits_dtype=dtype)
     scores = torch.softmax(hidden.float(), dim=-1)
     expected_weights, expected_ids = torch.topk(scores, 2, dim=-1)
     expected_weights = expected_weights / expected_weights.sum(dim=-1, keepdim=True)
+    unrounded = expected_weights
     if round_weights:
-        expected_weights = expected_weights.to(torch.bfloat16).float()
+        # The reference takes the LOGITS_DTYPE weights from a TopK over the payload-dtype
+        # logits, whose values are in that dtype.
+        expected_weights = expected_weights.to(dtype).float()
     assert torch.equal(ids, expected_ids.to(torch.int32))
     assert ids.tolist() == [[0, 1], [3, 2]]
     torch.testing.assert_close(weights, expected_weights, rtol=1e-5, atol=1e-6)
+    if round_weights:
+        # The other 16-bit rounding is far outside the tolerance: the dtype is pinned.
+        other = torch.float16 if dtype is torch.bfloat16 else torch.bfloat16
+        assert not torch.allclose(weights, unrounded.to(other).float(), rtol=1e-5, atol=1e-6)
 
 
+@PAYLOADS
 @pytest.mark.parametrize("corrected", (False, True))
-def test_softmax_fp32_router_selection_only_correction(corrected):
-    hidden = torch.tensor(TWO_ROWS, dtype=torch.bfloat16)
+def test_softmax_fp32_router_selection_only_correction(corrected, dtype):
+    hidden = torch.tensor(TWO_ROWS, dtype=dtype)
     bias = torch.tensor((-0.75, -0.25, 0.5, 0.8)) if corrected else None
-    logits = m.router_logits(hidden, torch.eye(4, dtype=torch.bfloat16), payload=False)
+    logits = m.router_logits(hidden, torch.eye(4, dtype=dtype), payload=False)
     ids, weights = m.router_topk(logits, topk=2, softmax=True, correction_bias=bias, renormalize=False)
     scores = torch.softmax(hidden.float(), dim=-1)
     selection = scores if bias is None else scores + bias
@@ -56,9 +73,10 @@ def test_softmax_fp32_router_selection_only_correction(corrected):
         assert not torch.equal(expected_ids, torch.topk(scores, 2, dim=-1).indices)
 
 
+@PAYLOADS
 @pytest.mark.parametrize("experts,topk,scale", ((64, 4, 4096.0), (48, 3, None), (17, 1, 1.0), (17, 17, 1.0)))
-def test_sigmoid_router_diagonal(experts, topk, scale):
-    hidden = (torch.arange(2 * experts, dtype=torch.float32).view(2, experts) / (2 * experts)).to(torch.bfloat16)
+def test_sigmoid_router_diagonal(experts, topk, scale, dtype):
+    hidden = torch.arange(2 * experts, dtype=torch.float32).view(2, experts).to(dtype) / (2 * experts)
     bias = torch.linspace(-0.25, 0.25, experts) * scale if scale is not None else None
     projection = torch.diag(torch.linspace(0.101, 1.909, experts))
     logits = m.router_logits(hidden, projection, payload=False)
@@ -136,16 +154,19 @@ def _reference_test_formula(x, w_gate_up, w_down, ids, weights, scale, alpha=1.0
     return expected.to(x.dtype)
 
 
+@PAYLOADS
 @pytest.mark.parametrize("act", ({}, {"alpha": 1.702, "limit": 7.0, "up_offset": 1.0}))
-def test_experts_match_the_reference_test_formula(act):
-    x, w_gate_up, w_down, ids, weights = _operator_test_case()
-    got = m.experts_reference(x, w_gate_up, w_down, ids, weights, routed_scaling_factor=1.5, **act)
+def test_experts_match_the_reference_test_formula(act, dtype):
+    # test_operators.py:110-121 runs the formula with bf16 and fp16 payloads.
+    x, w_gate_up, w_down, ids, weights = _operator_test_case(dtype)
+    got = m.experts_reference(x, w_gate_up, w_down, ids, weights, routed_scaling_factor=1.5, dtype=dtype, **act)
+    assert got.dtype is dtype
     expected = _reference_test_formula(x, w_gate_up, w_down, ids, weights, 1.5, **act)
     torch.testing.assert_close(got, expected, rtol=0.02, atol=0.1)
-    routes = m.experts_routes(x, w_gate_up, w_down, ids, weights, **act)
-    assert ((got.float() - expected.float()).abs() <= m.rounding_slack(routes, got, 1.5)).all()
+    routes = m.experts_routes(x, w_gate_up, w_down, ids, weights, dtype=dtype, **act)
+    assert ((got.float() - expected.float()).abs() <= m.rounding_slack(routes, got, 1.5, dtype=dtype)).all()
     same = (got.view(torch.int16) == expected.view(torch.int16)).float().mean().item()
-    assert same >= 0.95, f"only {same:.3f} of the bf16 outputs agree"
+    assert same >= 0.95, f"only {same:.3f} of the outputs agree"
     assert got[3].abs().sum() == 0  # the dead row
     pure = m.experts_fp32(x, w_gate_up, w_down, ids, weights, routed_scaling_factor=1.5, **act)
     assert o.compare(pure, got.float()).rel_l2 < 1e-2
@@ -179,3 +200,82 @@ def test_experts_invariants_and_planted_mistakes():
         m.experts_reference(x, w_gate_up, w_down, ids, weights, routed_scaling_factor=1.0),
     ):
         assert o.compare(expected.float(), wrong.float()).rel_l2 > 0.05
+
+
+def _f16(value: float) -> float:
+    """Round-to-nearest-even to IEEE binary16 (11 significant bits, subnormal spacing 2^-24),
+    computed on exact rationals (independent of torch's conversion)."""
+
+    if value == 0:
+        return value
+    _, exponent = math.frexp(value)  # 2^(exponent-1) <= |value| < 2^exponent
+    quantum = Fraction(2) ** max(exponent - 11, -24)
+    scaled = Fraction(value) / quantum
+    floor = math.floor(scaled)
+    remainder = scaled - floor
+    if remainder > Fraction(1, 2) or (remainder == Fraction(1, 2) and floor % 2 == 1):
+        floor += 1
+    return float(floor * quantum)
+
+
+def test_fp16_experts_match_exact_brute_force():
+    # The reference's operator case (test_operators.py:114, fp16 payload) by exact rationals:
+    # projections rounded through fp32 to binary16, fp32 SiLU*up rounded to binary16, exact
+    # down projection times the route weight in fp32 rounded to binary16, fp32 sum over the
+    # slots in order times the scale rounded to binary16.  A bf16 rounding point left in the
+    # oracle (8 significant bits instead of 11) fails here.
+    x, w_gate_up, w_down, ids, weights = _operator_test_case(torch.float16)
+
+    def exact(row, matrix):
+        return [sum(Fraction(float(a)) * Fraction(float(b)) for a, b in zip(row, w_row)) for w_row in matrix]
+
+    expected = []
+    for row in range(4):
+        columns = [np.float32(0)] * x.shape[1]
+        for slot in range(2):
+            expert = int(ids[row, slot])
+            if expert < 0:
+                continue
+            projected = [_f16(float(np.float32(float(v)))) for v in exact(x[row].tolist(), w_gate_up[expert].tolist())]
+            activated = []
+            for gate, up in zip(projected[0::2], projected[1::2]):
+                g = np.float32(gate)
+                silu = np.float32(g / (np.float32(1) + np.exp(-g, dtype=np.float32)))
+                activated.append(_f16(float(np.float32(silu * np.float32(up)))))
+            gamma = np.float32(float(weights[row, slot]))
+            routes = [_f16(float(np.float32(np.float32(float(r)) * gamma)))
+                      for r in exact(activated, w_down[expert].tolist())]
+            columns = [np.float32(c + np.float32(r)) for c, r in zip(columns, routes)]
+        expected.append([_f16(float(np.float32(c * np.float32(1.5)))) for c in columns])
+    got = m.experts_reference(x, w_gate_up, w_down, ids, weights, routed_scaling_factor=1.5, dtype=torch.float16)
+    assert got.dtype is torch.float16
+    assert got.float().tolist() == expected
+    # The bf16 oracle on the same values is a different function.
+    bf16 = m.experts_reference(x.bfloat16(), w_gate_up.bfloat16(), w_down.bfloat16(), ids, weights,
+                               routed_scaling_factor=1.5)
+    assert not torch.equal(got.float(), bf16.float())
+
+
+def test_fp16_router_logits_round_to_binary16():
+    x, w_gate_up, _, _, _ = _operator_test_case(torch.float16)
+    projection = w_gate_up[0, :6]
+    logits = m.router_logits(x, projection, payload=True, dtype=torch.float16)
+    brute = [[_f16(float(np.float32(float(sum(Fraction(float(a)) * Fraction(float(b)) for a, b in zip(row, w))))))
+              for w in projection.tolist()] for row in x.tolist()]
+    assert logits.tolist() == brute
+    # fp16 sigmoid selection: rounding the selection to binary16 can merge two scores that
+    # fp32 keeps apart; the tie then goes to the higher id.
+    scores = torch.tensor(((0.0, 0.0),))
+    bias = torch.tensor((2.0**-11, 0.0))
+    ids, _ = m.router_topk(scores, topk=1, softmax=False, correction_bias=bias, logits_dtype=torch.float16)
+    assert ids.tolist() == [[0]]  # 0.5 + 2^-11 is representable in binary16 (spacing 2^-11 at 0.5)
+    bias = torch.tensor((2.0**-12, 0.0))
+    ids, _ = m.router_topk(scores, topk=1, softmax=False, correction_bias=bias, logits_dtype=torch.float16)
+    assert ids.tolist() == [[1]]  # 0.5 + 2^-12 rounds to 0.5 (ties to even): a tie, won by the higher id
+    ids, _ = m.router_topk(scores, topk=1, softmax=False, correction_bias=bias)
+    assert ids.tolist() == [[0]]  # in fp32 the two stay apart
+    bias = torch.tensor((2.0**-9, 0.0))
+    ids, _ = m.router_topk(scores, topk=1, softmax=False, correction_bias=bias, logits_dtype=torch.bfloat16)
+    assert ids.tolist() == [[1]]  # bf16 (spacing 2^-8 at 0.5) merges what binary16 keeps apart
+    ids, _ = m.router_topk(scores, topk=1, softmax=False, correction_bias=bias, logits_dtype=torch.float16)
+    assert ids.tolist() == [[0]]
