@@ -10,7 +10,9 @@ the MoE bar of tests/parity.py against the reference's expected-value formula
 (test_operators.py:255-281) and its pure-fp32 counterpart, every stage (sort, activations,
 route outputs, combine) is checked rigorously on the GPU's own intermediates, and outputs
 repeat bit for bit.  fp16 Experts (test_operators.py:114) run on every grouped kernel
-family with fp16 rounding points in the oracle.
+family with fp16 rounding points in the oracle.  As in the reference's routing and operator
+tests, the Router and Experts are captured into graphs without allocation and replayed over
+inputs changed in place, each replay checked against the oracle and an eager call.
 """
 
 from __future__ import annotations
@@ -325,6 +327,147 @@ def test_experts_fp16_every_tile_family(device, rows, hidden, intermediate, expe
     operator.run_into(hidden_states=to_device(x, device), weights=weights_gpu, topk_ids=to_device(ids, device),
                       topk_weights=to_device(weights, device), output=again)
     assert_bitwise_equal(again.cpu(), got)
+
+
+def _capture_no_alloc(run):
+    run()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        before = torch.cuda.memory_stats()["allocation.all.allocated"]
+        run()
+        after = torch.cuda.memory_stats()["allocation.all.allocated"]
+    assert before == after, "capture allocated memory"
+    return graph
+
+
+@PAYLOADS
+@pytest.mark.parametrize("experts,topk,scale", ((64, 4, 4096.0), (17, 17, 1.0)))
+def test_sigmoid_router_graph_replay_with_new_inputs(device, experts, topk, scale, dtype):
+    # routing/test_sigmoid.py:48-73: the Router captured into a graph (no allocation), then
+    # the hidden states halved and the correction negated in place before each replay.  Every
+    # replay matches the oracle on the new inputs and an eager call on the same inputs.
+    hidden = (torch.arange(2 * experts, dtype=torch.float32).view(2, experts) / (2 * experts)).to(dtype)
+    projection = torch.diag(torch.linspace(0.101, 1.909, experts))
+    router = _router(device, hidden, projection, routed_topk=topk, algorithm=RouterAlgorithm.SIGMOID,
+                     precision=RouterProjectionPrecision.FP32, renormalize=True, payload_dtype=dtype)
+    hidden_gpu = to_device(hidden, device)
+    weights_gpu = MoeRouterWeights(to_device(projection, device),
+                                   to_device(torch.linspace(-0.25, 0.25, experts) * scale, device))
+    graph = _capture_no_alloc(lambda: router.run_into(hidden_states=hidden_gpu, router_weights=weights_gpu))
+    for _ in range(3):
+        hidden_gpu.mul_(0.5)
+        weights_gpu.correction_bias.neg_()
+        graph.replay()
+        torch.cuda.synchronize()
+        got_ids, got_weights = router.ids.cpu(), router.weights.cpu()
+        ids, weights = m.router_topk(m.router_logits(hidden_gpu.cpu(), projection, payload=False), topk=topk,
+                                     softmax=False, correction_bias=weights_gpu.correction_bias.cpu(),
+                                     renormalize=True)
+        assert torch.equal(got_ids, ids)
+        torch.testing.assert_close(got_weights, weights, rtol=1e-5, atol=1e-6)
+        router.run_into(hidden_states=hidden_gpu, router_weights=weights_gpu)
+        torch.cuda.synchronize()
+        assert torch.equal(router.ids.cpu(), got_ids) and torch.equal(router.weights.cpu(), got_weights)
+
+
+@PAYLOADS
+@pytest.mark.parametrize("rows", (1, 16, 200))
+def test_qwen3_router_graph_replay_with_new_inputs(device, rows, dtype):
+    # The PAYLOAD Router on the MFMA projection (K-slice sums in the TopK at decode sizes)
+    # captured once and replayed over new token rows.
+    hidden, experts = 2048, 128
+    generator = torch.Generator().manual_seed(72)
+    projection = (torch.randn((experts, hidden), generator=generator) * 0.02).to(dtype)
+    router = Router(row_capacity=rows, hidden_size=hidden, routed_expert_count=experts, routed_topk=8, device=device,
+                    payload_dtype=dtype)
+    x_gpu = to_device(o.generate_hidden_states(rows, hidden, 73).to(dtype), device)
+    weights_gpu = MoeRouterWeights(to_device(projection, device))
+    graph = _capture_no_alloc(lambda: router.run_into(hidden_states=x_gpu, router_weights=weights_gpu))
+    for step in range(3):
+        x = o.generate_hidden_states(rows, hidden, 74 + step).to(dtype)
+        x_gpu.copy_(to_device(x, device))
+        graph.replay()
+        torch.cuda.synchronize()
+        got_ids, got_weights, got_logits = router.ids.cpu(), router.weights.cpu(), router.logits.cpu()
+        assert_projection_within_bounds(got_logits, x, projection)
+        ids, weights = m.router_topk(got_logits.float(), topk=8, softmax=True, logits_dtype=dtype)
+        assert torch.equal(got_ids, ids)
+        torch.testing.assert_close(got_weights, weights, rtol=1e-5, atol=1e-6)
+        router.run_into(hidden_states=x_gpu, router_weights=weights_gpu)
+        torch.cuda.synchronize()
+        assert torch.equal(router.ids.cpu(), got_ids) and torch.equal(router.weights.cpu(), got_weights)
+        assert_bitwise_equal(router.logits.cpu(), got_logits)
+
+
+@PAYLOADS
+def test_experts_graph_replay_with_new_inputs(device, dtype):
+    # test_operators.py:234-281: the Experts operator captured without allocation, the
+    # hidden states refilled with 3 before the replay, the output against the reference's
+    # formula on the new inputs (its tolerance and the rounding-point slack), and the replay
+    # equal to an eager call.
+    generator = torch.Generator().manual_seed(31)
+    x = (torch.randn((4, 16), generator=generator) / 4).to(dtype)
+    w_gate_up = (torch.randn((4, 16, 16), generator=generator) / 4).to(dtype)
+    w_down = (torch.randn((4, 16, 8), generator=generator) / 4).to(dtype)
+    ids = torch.tensor(((0, 1), (2, 3), (1, 3), (-1, -1)), dtype=torch.int32)
+    weights = torch.tensor(((0.75, 0.25), (0.6, 0.4), (0.9, 0.1), (0.0, 0.0)))
+    operator = Experts(row_capacity=4, hidden_size=16, local_intermediate_size=8, expert_count=4, effective_topk=2,
+                       routed_scaling_factor=1.5, device=device, payload_dtype=dtype)
+    x_gpu = to_device(x, device)
+    layer = MoeFfnWeights(to_device(w_gate_up, device), to_device(w_down, device))
+    ids_gpu, weights_gpu = to_device(ids, device), to_device(weights, device)
+    output = torch.empty_like(x_gpu)
+    run = lambda: operator.run_into(hidden_states=x_gpu, weights=layer, topk_ids=ids_gpu, topk_weights=weights_gpu,
+                                    output=output)  # noqa: E731
+    graph = _capture_no_alloc(run)
+    for fill in (3.0, -0.5):
+        x_gpu.fill_(fill)
+        graph.replay()
+        torch.cuda.synchronize()
+        got = output.cpu()
+        new_x = x_gpu.cpu()
+        stage = m.experts_reference(new_x, w_gate_up, w_down, ids, weights, routed_scaling_factor=1.5, dtype=dtype)
+        routes = m.experts_routes(new_x, w_gate_up, w_down, ids, weights, dtype=dtype)
+        torch.testing.assert_close(got, stage, rtol=0.02, atol=0.1)
+        assert ((got.float() - stage.float()).abs() <= m.rounding_slack(routes, stage, 1.5, dtype=dtype)).all()
+        assert got[3].abs().sum() == 0
+        run()
+        torch.cuda.synchronize()
+        assert_bitwise_equal(output.cpu(), got)
+
+
+@PAYLOADS
+@pytest.mark.parametrize("rows", (48, 320))
+def test_experts_graph_replay_with_new_routing(device, rows, dtype):
+    # Qwen3-30B-A3B experts captured once (grouped split kernel at 48 rows, grouped tiles at
+    # 320) and replayed over new token rows and new routing: the route sort and tile table
+    # are built on the device, so each replay serves its own routing.
+    hidden, intermediate, experts, topk = 2048, 768, 128, 8
+    w_gate_up, w_down = m.generate_moe_layer(hidden, intermediate, experts, 150, dtype=dtype)
+    operator = Experts(row_capacity=rows, hidden_size=hidden, local_intermediate_size=intermediate,
+                       expert_count=experts, effective_topk=topk, device=device, payload_dtype=dtype)
+    layer = MoeFfnWeights(to_device(w_gate_up, device), to_device(w_down, device))
+    first_ids, first_weights = m.generate_routes(rows, experts, topk, 151)
+    x_gpu = to_device(o.generate_hidden_states(rows, hidden, 152).to(dtype), device)
+    ids_gpu, weights_gpu = to_device(first_ids, device), to_device(first_weights, device)
+    output = torch.empty_like(x_gpu)
+    run = lambda: operator.run_into(hidden_states=x_gpu, weights=layer, topk_ids=ids_gpu, topk_weights=weights_gpu,
+                                    output=output)  # noqa: E731
+    graph = _capture_no_alloc(run)
+    for step in range(2):
+        x = o.generate_hidden_states(rows, hidden, 153 + step).to(dtype)
+        ids, weights = m.generate_routes(rows, experts, topk, 155 + step)
+        x_gpu.copy_(to_device(x, device))
+        ids_gpu.copy_(to_device(ids, device))
+        weights_gpu.copy_(to_device(weights, device))
+        graph.replay()
+        torch.cuda.synchronize()
+        got = output.cpu()
+        _check_experts(got, x, w_gate_up, w_down, ids, weights)
+        run()
+        torch.cuda.synchronize()
+        assert_bitwise_equal(output.cpu(), got)
 
 
 def test_moe_layer_router_finalize_experts(device):
