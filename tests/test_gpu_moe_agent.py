@@ -28,7 +28,7 @@ import pytest
 import torch
 
 from crosspool_amd import _native
-from crosspool_amd.agent import FfnAgent
+from crosspool_amd.agent import FfnAgent, FfnHealthError
 from crosspool_amd.execution import derive_payload_row_capacities, select_capacity
 from crosspool_amd.ffn import DpRowLayout, ForwardMode, GateTransform, OutputRequirement, RouterAlgorithm
 from crosspool_amd.ffn import RouterProjectionPrecision, SiluActivation, TopKWeightRounding
@@ -277,6 +277,42 @@ def test_moe_layer_replays_through_its_template(device, hidden, intermediate, sp
             stages = _lane_stages(lane, spec, hidden, intermediate, select_capacity(capacities, rows), rows, dtype)
             _check_replay(stages, pool, pool_gpu.cpu(), slots, spec, w_gate_up, w_down, projection,
                           correction if corrected else None, norm_weight)
+
+
+@pytest.mark.parametrize("capacity,rows", ((4, 3), (16, 12), (64, 40)))
+def test_moe_out_of_range_slot_sets_sticky_fault(device, capacity, rows):
+    # A slot outside the mailbox: the gather (inside the Router projection at up to 8 rows,
+    # its own kernel above) poisons the row and raises the Lane's sticky fault bit, and the
+    # combine drops that row's output.  Every other row's result is bit for bit the one it
+    # has when a valid slot takes the bad one's place (a route's output depends only on its
+    # own row and expert), and mailbox rows outside the live slots stay untouched.
+    hidden, intermediate, pool_rows = 512, 256, 96
+    spec = MoeLayerSpec(routed_expert_count=16, routed_topk=4)
+    w_gate_up, w_down, projection, correction, norm_weight = _layer(hidden, intermediate, spec, 900)
+    pool = o.generate_hidden_states(pool_rows, hidden, 901)
+    slots = np.asarray(o.generate_slots(pool_rows, rows, 902), dtype=np.int32)
+    bad = slots.copy()
+    bad[1] = pool_rows + 5
+    with FfnAgent(device) as agent:
+        _register(agent, spec, hidden, w_gate_up, w_down, projection, correction, norm_weight, device)
+        agent.materialize(maximum_row_capacity=capacity)
+        print(f"case moe bad slot capacity={capacity} rows={rows}", flush=True)
+        faulty = to_device(pool, device)
+        agent.execute(instance_index=0, layer_ordinal=0, pool=faulty, slots=slots_tensor(bad, device))
+        with pytest.raises(FfnHealthError):
+            agent.check_health()
+        assert agent.lanes[0].check_health() == _native.XP_FAULT_SLOT_OUT_OF_RANGE  # sticky
+        agent.lanes[0].clear_fault()
+        assert agent.lanes[0].check_health() == 0
+        valid = to_device(pool, device)
+        agent.execute(instance_index=0, layer_ordinal=0, pool=valid, slots=slots_tensor(slots, device))
+        agent.check_health()
+        faulty, valid = faulty.cpu(), valid.cpu()
+    live = np.delete(slots, 1)
+    assert_bitwise_equal(faulty[live], valid[live])
+    untouched = np.setdiff1d(np.arange(pool_rows), live)
+    assert_bitwise_equal(faulty[untouched], pool[untouched])
+    assert not torch.equal(valid[slots[1]], pool[slots[1]])  # the valid replay did write that row
 
 
 def test_moe_graph_dispatch_and_operator_chain_repeat_the_replay(device):
