@@ -64,6 +64,10 @@ XP_DTYPE_F16 = 2
 XP_DTYPE_F32 = 3
 XP_GATE_UP_CONCATENATED = 1
 XP_GATE_UP_INTERLEAVED = 2
+XP_ACTIVATION_NONE = 0
+XP_ACTIVATION_SILU = 1
+XP_ACTIVATION_RELU = 2
+XP_ACTIVATION_GELU = 3
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -122,7 +126,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "xp_moe_workspace_bytes": (_SIZE, [_I64, _I64, _I64, _I64, _I64]),
     "xp_moe_workspace_layout": (_INT, [_I64, _I64, _I64, _I64, _I64, ctypes.POINTER(_SIZE)]),
     "xp_moe_experts": (
-        _INT, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _F32, _F32, _F32, _F32, _INT, _P, _P, _SIZE, _P]
+        _INT,
+        [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _F32, _INT, _INT, _F32, _F32, _F32, _INT, _P, _P,
+         _SIZE, _P],
     ),
     "xp_moe_layer_register": (_INT, [_P, _INT, _INT, ctypes.POINTER(MoeLayerDesc), _P, _P, _P, _P, _P, _F32]),
     "xp_moe_step_workspace_bytes": (_SIZE, [ctypes.POINTER(MoeLayerDesc), _I64]),

@@ -485,6 +485,38 @@ __global__ __launch_bounds__(64 * kSplitWaves) void split_gemm_kernel(GemmArgs a
 // by the norm weights (while staging) and the K-range partial sums (after each unit).
 constexpr int kSplitGatheredScratchBytes = (kSplitWaves - 1) * 2 * 64 * 16;
 
+// The gated epilogue of the grouped MoE projections: SiLU exactly as the Dense kernels
+// evaluate it (gated_silu_payload), or ReLU (NaN kept) / GELU (erf or tanh) of the rounded
+// Gate, as compute_gated does (operators/activation.py:19-51), times the rounded Up plus
+// the offset, with the same clipping.
+template <class P, bool CLIP>
+__device__ __forceinline__ float moe_gated_payload(float gate, float up, const GatedSilu &act) {
+  if (act.function != kActivationRelu && act.function != kActivationGelu) {
+    return gated_silu_payload<P, CLIP>(gate, up, act);
+  }
+  const uint32_t both = P::pack2(gate, up);
+  float g = P::widen(both & 0xffffu);
+  float u = P::widen(both >> 16);
+  if constexpr (CLIP) {
+    g = fminf(g, act.limit);
+    u = fminf(fmaxf(u, -act.limit), act.limit);
+  }
+  float f;
+  if (act.function == kActivationRelu) {
+    f = (g > 0.0f || g != g) ? g : 0.0f;
+  } else if (act.approximate_tanh != 0) {
+    f = 0.5f * g * (1.0f + tanhf(0.7978845608028654f * (g + 0.044715f * g * g * g)));
+  } else {
+    f = 0.5f * g * (1.0f + erff(g * 0.7071067811865476f));
+  }
+  return f * (u + act.up_offset);
+}
+
+template <class P>
+__device__ __forceinline__ float moe_gated_payload(float gate, float up, const GatedSilu &act) {
+  return act.limit > 0.0f ? moe_gated_payload<P, true>(gate, up, act) : moe_gated_payload<P, false>(gate, up, act);
+}
+
 template <int DEPTH, bool GATED, class P = Bf16Payload>
 __global__ __launch_bounds__(64 * kSplitWaves) __attribute__((amdgpu_waves_per_eu(4))) void split_gathered_kernel(
     GemmArgs a) {
@@ -941,13 +973,18 @@ __global__ __launch_bounds__(64 * kSplitWaves) void grouped_split_kernel(GemmArg
       if (n >= a.n) {
         continue;
       }
+      f32x4 value = sum[g][h];
+      if (a.bias != nullptr) {
+        // Rows n .. n + 3 of the expert's bias (n + 3 < N: N is a multiple of 8).
+        value += *reinterpret_cast<const f32x4 *>(a.bias + expert * a.bias_stride + n);
+      }
       if constexpr (GATED) {
-        const float h0 = gated_silu_payload<P>(sum[g][h][0], sum[g][h][1], a.act);
-        const float h1 = gated_silu_payload<P>(sum[g][h][2], sum[g][h][3], a.act);
+        const float h0 = moe_gated_payload<P>(value[0], value[1], a.act);
+        const float h1 = moe_gated_payload<P>(value[2], value[3], a.act);
         *reinterpret_cast<uint32_t *>(out + n / 2) = P::pack2(h0, h1);
       } else {
         const float f = factor[g];
-        u32x2 packed = {P::pack2(sum[g][h][0] * f, sum[g][h][1] * f), P::pack2(sum[g][h][2] * f, sum[g][h][3] * f)};
+        u32x2 packed = {P::pack2(value[0] * f, value[1] * f), P::pack2(value[2] * f, value[3] * f)};
         *reinterpret_cast<u32x2 *>(out + n) = packed;
       }
     }
@@ -1643,7 +1680,7 @@ __device__ __forceinline__ float row_factor(const RowMeta<WTM> &meta, int row) {
 template <int MT, int NT, int WTM, int WTN, int WAVES, int LDS_ELEMENTS, bool GATED, bool GROUPED, class P>
 __device__ __forceinline__ void tile_epilogue(const GemmArgs &a, const f32x16 (&acc)[MT][NT], uint16_t *lds,
                                               int64_t m0, int64_t row_end, int64_t w0, int wave, int wm, int wn,
-                                              const RowMeta<WTM> &meta) {
+                                              const RowMeta<WTM> &meta, int expert) {
   const int lane = threadIdx.x & 63;
   const int frag_row = lane & 31;
   const int frag_half = lane >> 5;
@@ -1701,6 +1738,14 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs &a, const f32x16 (&
   // Chunk c of row r sits at physical chunk c ^ ((r / 4) % CPR): the two row groups one
   // write instruction covers (rows r and r + 4) then fall in different banks.
   auto slot_of = [](int row, int chunk) { return row * OUT_N + ((chunk ^ ((row >> 2) & (CPR - 1))) << 3); };
+  const int64_t row0 = m0 + wm * WTM;
+  const int64_t col0 = GATED ? w0 / 2 + wn * (WTN / 2) : w0 + wn * WTN;
+  // Grouped projections with a bias: the expert's fp32 bias, indexed by weight row (gate_up:
+  // Gate and Up of output column c are weight rows 2 c and 2 c + 1).
+  const float *bias = nullptr;
+  if constexpr (GROUPED) {
+    bias = a.bias != nullptr ? a.bias + static_cast<int64_t>(expert) * a.bias_stride : nullptr;
+  }
   // The gated activation is the epilogue's VALU cost (two quarter-rate transcendentals per
   // output); its clipping is chosen once per tile, not per element.
   auto stage = [&](auto clip) XP_INLINE {
@@ -1718,8 +1763,23 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs &a, const f32x16 (&
         for (int nt = 0; nt < OUT_N / 32; ++nt) {
           const int col = nt * 32 + frag_row;
           float value;
-          if constexpr (GATED) {
+          if constexpr (GATED && GROUPED) {
+            float gate = acc[mt][nt][r];
+            float up = acc[mt][nt + NT / 2][r];
+            if (bias != nullptr) {
+              const int64_t c = col0 + col < a.n / 2 ? col0 + col : 0;  // (columns past N are not stored)
+              gate += bias[2 * c];
+              up += bias[2 * c + 1];
+            }
+            value = moe_gated_payload<P, decltype(clip)::value>(gate, up, a.act);
+          } else if constexpr (GATED) {
             value = gated_silu_payload<P, decltype(clip)::value>(acc[mt][nt][r], acc[mt][nt + NT / 2][r], a.act);
+          } else if constexpr (GROUPED) {
+            float sum = acc[mt][nt][r];
+            if (bias != nullptr) {
+              sum += bias[col0 + col < a.n ? col0 + col : 0];
+            }
+            value = sum * factor;
           } else {
             value = acc[mt][nt][r] * factor;
           }
@@ -1734,8 +1794,6 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs &a, const f32x16 (&
     stage(std::false_type{});
   }
   __syncthreads();
-  const int64_t row0 = m0 + wm * WTM;
-  const int64_t col0 = GATED ? w0 / 2 + wn * (WTN / 2) : w0 + wn * WTN;
   const int64_t out_cols = GATED ? a.n / 2 : a.n;
 #pragma unroll 4
   for (int index = lane; index < WTM * CPR; index += 64) {
@@ -1806,8 +1864,9 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
   int64_t m0 = static_cast<int64_t>(tm) * BM;
   int64_t row_end = a.rows;
   const uint16_t *weights = a.w;
+  [[maybe_unused]] int expert = 0;
   if constexpr (GROUPED) {
-    const int expert = __builtin_amdgcn_readfirstlane(a.tile_expert[tm]);
+    expert = __builtin_amdgcn_readfirstlane(a.tile_expert[tm]);
     if (expert < 0) {
       return;
     }
@@ -2186,7 +2245,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
   __builtin_amdgcn_s_waitcnt(0);
 
   tile_epilogue<MT, NT, WTM, WTN, WAVES, STAGES * STAGE, GATED, GROUPED, PAYLOAD>(a, acc, lds, m0, row_end, w0, wave, wm, wn,
-                                                                         meta);
+                                                                         meta, expert);
 }
 
 // ------------------------------------------------------------------ tables

@@ -58,7 +58,7 @@ __device__ __forceinline__ uint32_t payload_bits<Bf16Payload>(float value) {
 }
 template <>
 __device__ __forceinline__ uint32_t payload_bits<F16Payload>(float value) {
-  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(value));
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f32_rounding_point(value)));
 }
 template <class P>
 __device__ __forceinline__ float payload_round(float value) {

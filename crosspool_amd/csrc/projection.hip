@@ -41,7 +41,7 @@ __device__ __forceinline__ float load_value(const void *base, int64_t index, int
 __device__ __forceinline__ float round_to(float value, int dtype) {
   switch (dtype) {
     case kDtypeF16:
-      return __half2float(__float2half_rn(value));
+      return __half2float(__float2half_rn(f32_rounding_point(value)));
     case kDtypeF32:
       return value;
     default:
@@ -52,7 +52,7 @@ __device__ __forceinline__ float round_to(float value, int dtype) {
 __device__ __forceinline__ void store_value(void *base, int64_t index, float value, int dtype) {
   switch (dtype) {
     case kDtypeF16:
-      reinterpret_cast<__half *>(base)[index] = __float2half_rn(value);
+      reinterpret_cast<__half *>(base)[index] = __float2half_rn(f32_rounding_point(value));
       break;
     case kDtypeF32:
       reinterpret_cast<float *>(base)[index] = value;

@@ -606,6 +606,9 @@ struct ExpertsBinding {
   int32_t payload = kPayloadBf16;  // PayloadKind of x, the weights, the routes and out
   // The Router's TopK run by the sort kernel (at most 16 rows, no shared experts), or null.
   const RouterTopkArgs *fused_topk = nullptr;
+  // fp32 projection biases ([experts, 2 intermediate] and [experts, hidden]), or null.
+  const float *bias_gate_up = nullptr;
+  const float *bias_down = nullptr;
 };
 
 struct ExpertsLaunches {
@@ -673,6 +676,8 @@ int make_experts_launches(const ExpertsBinding &b, int64_t capacity, ExpertsLaun
   up.tile_row0 = tile_row0;
   up.expert_end = expert_end;
   up.payload = b.payload;
+  up.bias = b.bias_gate_up;
+  up.bias_stride = 2 * b.intermediate;
 
   GemmArgs dn = up;
   dn.x = activated;
@@ -686,6 +691,8 @@ int make_experts_launches(const ExpertsBinding &b, int64_t capacity, ExpertsLaun
   dn.n = b.hidden;
   dn.k = b.intermediate;
   dn.act = default_activation();
+  dn.bias = b.bias_down;
+  dn.bias_stride = b.hidden;
 
   if (tile != MoeTile::Small) {
     // Many routes per expert: the Dense tile kernel in its grouped mode, on expert tiles of
@@ -2171,9 +2178,11 @@ int xp_moe_workspace_layout(int64_t rows, int64_t hidden, int64_t intermediate, 
 }
 
 int xp_moe_experts(const void *hidden_states, int64_t rows, int64_t hidden, int64_t intermediate, int64_t experts,
-                   int64_t topk, const void *w_gate_up, const void *w_down, const int32_t *topk_ids,
-                   const float *topk_weights, float routed_scaling_factor, float alpha, float limit, float up_offset,
-                   int payload_dtype, void *output, void *workspace, size_t workspace_bytes, xp_stream_t stream) {
+                   int64_t topk, const void *w_gate_up, const void *w_down, const float *gate_up_bias,
+                   const float *down_bias, const int32_t *topk_ids, const float *topk_weights,
+                   float routed_scaling_factor, int activation, int approximate_tanh, float alpha, float limit,
+                   float up_offset, int payload_dtype, void *output, void *workspace, size_t workspace_bytes,
+                   xp_stream_t stream) {
   XP_REQUIRE(rows >= 0, "row count must be non-negative");
   int32_t payload = kPayloadBf16;
   if (const int status = payload_kind(payload_dtype, payload); status != XP_OK) {
@@ -2182,14 +2191,18 @@ int xp_moe_experts(const void *hidden_states, int64_t rows, int64_t hidden, int6
   if (const int status = validate_experts(rows, hidden, intermediate, experts, topk); status != XP_OK) {
     return status;
   }
-  XP_REQUIRE(alpha > 0.0f, "SiLU alpha must be positive");
+  XP_REQUIRE(activation == XP_ACTIVATION_SILU || activation == XP_ACTIVATION_RELU || activation == XP_ACTIVATION_GELU,
+             "Experts activation must be SiLU, ReLU or GELU");
+  XP_REQUIRE(approximate_tanh == 0 || activation == XP_ACTIVATION_GELU, "the tanh approximation is GELU's only");
+  XP_REQUIRE(activation != XP_ACTIVATION_SILU || alpha > 0.0f, "SiLU alpha must be positive");
   if (rows == 0) {
     return XP_OK;
   }
   XP_REQUIRE(hidden_states != nullptr && w_gate_up != nullptr && w_down != nullptr && topk_ids != nullptr &&
                  topk_weights != nullptr && output != nullptr,
              "Experts pointers must be non-null");
-  XP_REQUIRE(aligned16(hidden_states) && aligned16(w_gate_up) && aligned16(w_down) && aligned16(output),
+  XP_REQUIRE(aligned16(hidden_states) && aligned16(w_gate_up) && aligned16(w_down) && aligned16(output) &&
+                 aligned16(gate_up_bias) && aligned16(down_bias),
              "Experts tensors must be 16-byte aligned");
   const MoeWorkspace layout = moe_workspace(rows, hidden, intermediate, experts, topk);
   XP_REQUIRE(workspace != nullptr && workspace_bytes >= layout.bytes && aligned16(workspace),
@@ -2208,8 +2221,14 @@ int xp_moe_experts(const void *hidden_states, int64_t rows, int64_t hidden, int6
   binding.experts = experts;
   binding.topk = topk;
   binding.scale = routed_scaling_factor;
-  binding.act = GatedSilu{alpha, limit, up_offset};
+  binding.act = GatedSilu{alpha, limit, up_offset,
+                          activation == XP_ACTIVATION_RELU   ? kActivationRelu
+                          : activation == XP_ACTIVATION_GELU ? kActivationGelu
+                                                             : kActivationSilu,
+                          approximate_tanh != 0 ? 1 : 0};
   binding.payload = payload;
+  binding.bias_gate_up = gate_up_bias;
+  binding.bias_down = down_bias;
   ExpertsLaunches launches;
   if (const int status = make_experts_launches(binding, rows, launches); status != XP_OK) {
     return status;

@@ -40,11 +40,15 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 }
 
 // Gated activation parameters: silu(min(g, limit)) * (clamp(u, -limit, limit) + up_offset),
-// with silu(v) = v / (1 + exp(-alpha v)); limit <= 0 disables clipping.
+// with silu(v) = v / (1 + exp(-alpha v)); limit <= 0 disables clipping.  The grouped MoE
+// projections also take ReLU and GELU in place of SiLU (function: kActivationRelu /
+// kActivationGelu; anything else is SiLU).
 struct GatedSilu {
   float alpha;
   float limit;
   float up_offset;
+  int32_t function;
+  int32_t approximate_tanh;  // GELU: the tanh approximation instead of erf
 };
 
 // The projection is first rounded to bf16 (payload dtype), then evaluated in fp32.  CLIP is
@@ -101,6 +105,16 @@ struct Bf16Payload {
   }
 };
 
+// An fp32 value at a rounding point, made opaque to the compiler before it is converted to
+// fp16.  Without it the backend may fuse the multiply that produced the value into the
+// conversion (v_fma_mix*_f16), which rounds the exact product to fp16 once instead of
+// rounding it to fp32 first, as the reference (an fp32 product, then .to(float16)) does; at
+// an fp16 tie the two results differ by one ulp.  (bf16 has no such fused form.)
+__device__ __forceinline__ float f32_rounding_point(float value) {
+  __asm__ volatile("" : "+v"(value));
+  return value;
+}
+
 struct F16Payload {
   static constexpr uint32_t kPoison2 = 0x7e007e00u;  // two fp16 quiet NaNs
   __device__ static __forceinline__ float widen(uint32_t bits16) {
@@ -109,7 +123,8 @@ struct F16Payload {
   __device__ static __forceinline__ uint32_t pack2(float lo, float hi) {
     typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
     typedef float f32x2_t __attribute__((ext_vector_type(2)));
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{lo, hi}), f16x2_t));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(
+                                            (f32x2_t{f32_rounding_point(lo), f32_rounding_point(hi)}), f16x2_t));
   }
   __device__ static __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,

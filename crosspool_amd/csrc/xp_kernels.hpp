@@ -376,7 +376,11 @@ struct GemmArgs {
   const int32_t *expert_end;
   const float *row_scale;
   int64_t gather_divisor;
-  int32_t payload;  // PayloadKind of x, w and out (the MoE projections are bf16 only)
+  int32_t payload;  // PayloadKind of x, w and out
+  // Grouped projections: fp32 bias of expert e at bias + e bias_stride ([n] per expert), added
+  // to the fp32 sum before the rounding point (and before the row scale), or null.
+  const float *bias;
+  int64_t bias_stride;
 };
 
 // SplitGathered: the split kernel's units walked by a persistent grid that gathers the token

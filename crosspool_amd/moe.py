@@ -23,6 +23,8 @@ import torch
 from crosspool_amd import _native
 from crosspool_amd.ffn import (
     GateTransform,
+    GeluActivation,
+    ReluActivation,
     RouterAlgorithm,
     RouterProjectionPrecision,
     SiluActivation,
@@ -83,12 +85,16 @@ class MoeFfnWeights:
 
     ``i_proj`` is ``[experts, 2 I, H]`` with INTERLEAVED Gate/Up rows per expert,
     ``o_proj`` is ``[experts, H, I]``, both of the payload dtype (bf16 or fp16, the
-    reference's supported payloads, src/cext-include/xpool/ffn.hpp:83-85).
+    reference's supported payloads, src/cext-include/xpool/ffn.hpp:83-85).  The optional
+    projection biases (``ProjectionWeights.bias``, weights.py:96-130) are fp32
+    ``[experts, 2 I]`` (i_proj's row order) and ``[experts, H]``.
     """
 
     i_proj: torch.Tensor
     o_proj: torch.Tensor
     router: MoeRouterWeights | None = None
+    i_proj_bias: torch.Tensor | None = None
+    o_proj_bias: torch.Tensor | None = None
 
     def __post_init__(self) -> None:
         validate_weight_tensor(self.i_proj, name="Expert i_proj")
@@ -102,6 +108,17 @@ class MoeFfnWeights:
             raise ValueError("Expert projections disagree: i_proj [E, 2I, H] needs o_proj [E, H, I]")
         if self.i_proj.device != self.o_proj.device:
             raise ValueError("Expert projections must share one device")
+        for bias, name, shape in (
+            (self.i_proj_bias, "i_proj bias", (experts, two_i)),
+            (self.o_proj_bias, "o_proj bias", (experts, hidden)),
+        ):
+            if bias is None:
+                continue
+            validate_weight_tensor(bias, name=f"Expert {name}")
+            if bias.dtype is not torch.float32 or tuple(bias.shape) != shape:
+                raise ValueError(f"Expert {name} must be an fp32 [{shape[0]}, {shape[1]}] tensor")
+            if bias.device != self.i_proj.device:
+                raise ValueError("Expert projections and biases must share one device")
 
     @property
     def expert_count(self) -> int:
@@ -168,6 +185,8 @@ class MoeLayerSpec:
             )
         if weights.router is None:
             raise ValueError("the Lane owns the Router on one device: MoE weights need a Router projection")
+        if weights.i_proj_bias is not None or weights.o_proj_bias is not None:
+            raise ValueError("MoE layers take projections without biases (the Experts operator takes biases)")
         weight_dtype = (
             torch.float32 if self.router_projection_precision is RouterProjectionPrecision.FP32
             else weights.payload_dtype
@@ -371,7 +390,7 @@ class Experts:
         expert_count: int,
         effective_topk: int,
         routed_scaling_factor: float = 1.0,
-        activation: SiluActivation | None = None,
+        activation: SiluActivation | ReluActivation | GeluActivation | None = None,
         gate: GateTransform | None = None,
         device: torch.device | None = None,
         payload_dtype: torch.dtype = torch.bfloat16,
@@ -387,7 +406,14 @@ class Experts:
         self.expert_count = expert_count
         self.effective_topk = effective_topk
         self.routed_scaling_factor = float(routed_scaling_factor)
-        self.act = activation_arguments(activation or SiluActivation(), gate or GateTransform())
+        activation = SiluActivation() if activation is None else activation
+        if not isinstance(activation, (SiluActivation, ReluActivation, GeluActivation)):
+            raise ValueError("Experts activation must be SiLU, ReLU or GELU")
+        gate = GateTransform() if gate is None else gate
+        alpha = float(activation.alpha) if isinstance(activation, SiluActivation) else 1.0
+        _, limit, up_offset = activation_arguments(SiluActivation(alpha), gate)
+        approximate = int(isinstance(activation, GeluActivation) and activation.approximate == "tanh")
+        self.act = (int(activation.kind), approximate, alpha, limit, up_offset)
         self.payload_dtype = payload_dtype
         self._payload_code = _native.payload_dtype_code(payload_dtype)
         nbytes = _native.library().xp_moe_workspace_bytes(
@@ -438,10 +464,10 @@ class Experts:
             self.expert_count, h, self.local_intermediate_size
         ):
             raise ValueError("Expert weights disagree with the operator geometry")
-        alpha, limit, up_offset = self.act
+        function, approximate, alpha, limit, up_offset = self.act
         _native.call(
             "xp_moe_experts", _ptr(hidden_states), c, h, self.local_intermediate_size, self.expert_count, k,
-            _ptr(weights.i_proj), _ptr(weights.o_proj), _ptr(topk_ids), _ptr(topk_weights),
-            self.routed_scaling_factor, alpha, limit, up_offset, self._payload_code, _ptr(output),
-            _ptr(self.workspace), self.workspace.numel(), _stream(),
+            _ptr(weights.i_proj), _ptr(weights.o_proj), _ptr(weights.i_proj_bias), _ptr(weights.o_proj_bias),
+            _ptr(topk_ids), _ptr(topk_weights), self.routed_scaling_factor, function, approximate, alpha, limit,
+            up_offset, self._payload_code, _ptr(output), _ptr(self.workspace), self.workspace.numel(), _stream(),
         )

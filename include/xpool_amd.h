@@ -433,17 +433,24 @@ int xp_moe_workspace_layout(int64_t rows, int64_t hidden, int64_t intermediate, 
                             size_t *offsets);
 
 /* Experts: for every route (row, slot) with 0 <= e = topk_ids[row, slot] < experts,
- * h = p(act(p(x[row] . w_gate_up[e][2j]), p(x[row] . w_gate_up[e][2j+1]))) and
- * r = p((h . w_down[e][n]) * topk_weights[row, slot]); then
+ * h = p(act(p(x[row] . w_gate_up[e][2j] + bg[e][2j]), p(x[row] . w_gate_up[e][2j+1] + bg[e][2j+1])))
+ * and r = p((h . w_down[e][n] + bd[e][n]) * topk_weights[row, slot]); then
  * output[row] = p(routed_scaling_factor * sum over slots in order of float(r)), 0 for
  * rows without routes, where p rounds to payload_dtype (XP_DTYPE_BF16 or F16), the dtype of
- * x, the weights and the output.  w_gate_up is [experts, 2*intermediate, hidden] (Gate/Up
- * INTERLEAVED), w_down [experts, hidden, intermediate]; act as in xp_gemm_gate_up_silu.
- * Replaces Experts.run_into (src/xpool/runtime/ffnagent/operators/moe.py:168-343). */
+ * x, the weights and the output, and the fp32 biases bg = gate_up_bias [experts,
+ * 2*intermediate] and bd = down_bias [experts, hidden] read as 0 when NULL.  w_gate_up is
+ * [experts, 2*intermediate, hidden] (Gate/Up INTERLEAVED), w_down [experts, hidden,
+ * intermediate].  act(g, u) = f(min(g, limit)) * (clamp(u, -limit, limit) + up_offset)
+ * (no clipping for limit <= 0) with f of `activation`: XP_ACTIVATION_SILU (v / (1 +
+ * exp(-alpha v))), XP_ACTIVATION_RELU (NaN kept) or XP_ACTIVATION_GELU (erf, or the tanh
+ * approximation with approximate_tanh).  Replaces Experts.run_into
+ * (src/xpool/runtime/ffnagent/operators/moe.py:168-343). */
 int xp_moe_experts(const void *hidden_states, int64_t rows, int64_t hidden, int64_t intermediate, int64_t experts,
-                   int64_t topk, const void *w_gate_up, const void *w_down, const int32_t *topk_ids,
-                   const float *topk_weights, float routed_scaling_factor, float alpha, float limit, float up_offset,
-                   int payload_dtype, void *output, void *workspace, size_t workspace_bytes, xp_stream_t stream);
+                   int64_t topk, const void *w_gate_up, const void *w_down, const float *gate_up_bias,
+                   const float *down_bias, const int32_t *topk_ids, const float *topk_weights,
+                   float routed_scaling_factor, int activation, int approximate_tanh, float alpha, float limit,
+                   float up_offset, int payload_dtype, void *output, void *workspace, size_t workspace_bytes,
+                   xp_stream_t stream);
 
 /* ---------------------------------------------------------------- MoE layer kind
  * One MoE layer's execution identity: the fields of MoeFfnExecutionSignature

@@ -127,6 +127,19 @@ def _routes_by_expert(topk_ids: torch.Tensor, experts: int):
             yield expert, where[:, 0], where[:, 1]
 
 
+def gated(gate: torch.Tensor, up: torch.Tensor, *, function: str = "silu", approximate: str = "none",
+          alpha: float = 1.0, limit: float | None = None, up_offset: float = 0.0,
+          dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """The Experts' gated activation of rounded Gate / Up values, rounded to ``dtype``:
+    ``o.gated_silu`` for SiLU, ``o.gated_activation`` (compute_gated, activation.py:44-51)
+    for ReLU and GELU."""
+
+    if function == "silu":
+        return o.gated_silu(gate, up, alpha=alpha, limit=limit, up_offset=up_offset, dtype=dtype)
+    return o.gated_activation(gate, up, function=function, approximate=approximate, limit=limit,
+                              up_offset=up_offset).to(dtype)
+
+
 def experts_routes(
     x: torch.Tensor,
     w_gate_up: torch.Tensor,
@@ -138,23 +151,33 @@ def experts_routes(
     limit: float | None = None,
     up_offset: float = 0.0,
     dtype: torch.dtype = torch.bfloat16,
+    function: str = "silu",
+    approximate: str = "none",
+    i_bias: torch.Tensor | None = None,
+    o_bias: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Route outputs [rows, slots, hidden] (payload-dtype values held in fp32; 0 where no route).
 
-    Projection rounded to the payload ``dtype`` (bf16 or fp16), activation in fp32 rounded
-    to it, down projection times the route weight in fp32 rounded to it
-    (test_operators.py:266-278, where the reference runs the formula for each payload dtype).
+    Projection plus its fp32 bias (``i_bias`` [E, 2I]) rounded to the payload ``dtype``
+    (bf16 or fp16), activation (``function``: silu, relu or gelu) in fp32 rounded to it,
+    down projection plus its bias (``o_bias`` [E, H]) times the route weight in fp32
+    rounded to it (test_operators.py:255-278, where the reference runs the formula for each
+    payload dtype, activation and bias case).
     """
 
     rows, hidden = x.shape
     experts = w_gate_up.shape[0]
     routes = torch.zeros((rows, topk_ids.shape[1], hidden), dtype=torch.float32)
     for expert, row_index, slot_index in _routes_by_expert(topk_ids, experts):
-        projected = (x[row_index].double() @ w_gate_up[expert].double().t()).to(dtype)
-        activated = o.gated_silu(
-            projected[:, 0::2], projected[:, 1::2], alpha=alpha, limit=limit, up_offset=up_offset, dtype=dtype
-        )
+        projected = x[row_index].double() @ w_gate_up[expert].double().t()
+        if i_bias is not None:
+            projected = projected + i_bias[expert].double()
+        projected = projected.to(dtype)
+        activated = gated(projected[:, 0::2], projected[:, 1::2], function=function, approximate=approximate,
+                          alpha=alpha, limit=limit, up_offset=up_offset, dtype=dtype)
         route = activated.double() @ w_down[expert].double().t()
+        if o_bias is not None:
+            route = route + o_bias[expert].double()
         gamma = topk_weights[row_index, slot_index].double().unsqueeze(1)
         routes[row_index, slot_index] = (route.float() * gamma.float()).to(dtype).float()
     return routes
@@ -168,15 +191,13 @@ def experts_reference(
     topk_weights: torch.Tensor,
     *,
     routed_scaling_factor: float = 1.0,
-    alpha: float = 1.0,
-    limit: float | None = None,
-    up_offset: float = 0.0,
     dtype: torch.dtype = torch.bfloat16,
+    **act,
 ) -> torch.Tensor:
-    """Expected Experts output with the reference's rounding points ([rows, hidden] of ``dtype``)."""
+    """Expected Experts output with the reference's rounding points ([rows, hidden] of ``dtype``);
+    ``act`` as :func:`experts_routes` takes it."""
 
-    routes = experts_routes(x, w_gate_up, w_down, topk_ids, topk_weights, alpha=alpha, limit=limit,
-                            up_offset=up_offset, dtype=dtype)
+    routes = experts_routes(x, w_gate_up, w_down, topk_ids, topk_weights, dtype=dtype, **act)
     total = torch.zeros(routes.shape[::2], dtype=torch.float32)
     for slot in range(topk_ids.shape[1]):
         total = total + routes[:, slot]
@@ -208,6 +229,10 @@ def experts_fp32(
     alpha: float = 1.0,
     limit: float | None = None,
     up_offset: float = 0.0,
+    function: str = "silu",
+    approximate: str = "none",
+    i_bias: torch.Tensor | None = None,
+    o_bias: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """The same Experts output in fp32 with no intermediate rounding."""
 
@@ -216,12 +241,19 @@ def experts_fp32(
     total = torch.zeros((rows, hidden), dtype=torch.float64)
     for expert, row_index, slot_index in _routes_by_expert(topk_ids, experts):
         projected = x[row_index].double() @ w_gate_up[expert].double().t()
+        if i_bias is not None:
+            projected = projected + i_bias[expert].double()
         gate, up = projected[:, 0::2], projected[:, 1::2]
         if limit is not None:
             gate = torch.clamp(gate, max=limit)
             up = torch.clamp(up, -limit, limit)
-        activated = gate * torch.sigmoid(alpha * gate) * (up + up_offset)
+        if function == "silu":
+            activated = gate * torch.sigmoid(alpha * gate) * (up + up_offset)
+        else:
+            activated = o.activation_function(gate, function, approximate=approximate).double() * (up + up_offset)
         route = activated @ w_down[expert].double().t()
+        if o_bias is not None:
+            route = route + o_bias[expert].double()
         total.index_add_(0, row_index, route * topk_weights[row_index, slot_index].double().unsqueeze(1))
     return (total * routed_scaling_factor).float()
 

@@ -156,12 +156,29 @@ def bf16_ceil(v: torch.Tensor) -> torch.Tensor:
     return ceil16(v, torch.bfloat16)
 
 
-def projection_interval(x: torch.Tensor, w: torch.Tensor, dtype: torch.dtype = torch.bfloat16):
-    """Interval (of ``dtype``) a correctly implemented fp32-accumulated ``round(x w^T)`` must land in."""
+def projection_interval(x: torch.Tensor, w: torch.Tensor, dtype: torch.dtype = torch.bfloat16,
+                        bias: torch.Tensor | None = None):
+    """Interval (of ``dtype``) a correctly implemented fp32-accumulated ``round(x w^T + bias)``
+    must land in (the fp32 bias added to the fp32 sum: one more fp32 rounding)."""
 
     exact = x.double() @ w.double().t()
     delta = (x.double().abs() @ w.double().abs().t()) * ACCUMULATION_BOUND
+    if bias is not None:
+        exact = exact + bias.double()
+        delta = delta + (exact.abs() + delta) * 2.0**-23
     return floor16(exact - delta, dtype), ceil16(exact + delta, dtype)
+
+
+def _gated(gate: torch.Tensor, up: torch.Tensor, dtype: torch.dtype, *, function: str = "silu",
+           approximate: str = "none", alpha: float = 1.0, limit: float | None = None,
+           up_offset: float = 0.0) -> torch.Tensor:
+    """The gated activation at the reference's rounding point: o.gated_silu for SiLU (the
+    Dense oracle's), o.gated_activation rounded to ``dtype`` for ReLU and GELU."""
+
+    if function == "silu":
+        return o.gated_silu(gate, up, dtype=dtype, alpha=alpha, limit=limit, up_offset=up_offset)
+    return o.gated_activation(gate, up, function=function, approximate=approximate, limit=limit,
+                              up_offset=up_offset).to(dtype)
 
 
 def assert_projection_within_bounds(actual: torch.Tensor, x: torch.Tensor, w: torch.Tensor, exact_fraction=0.99):
@@ -184,15 +201,20 @@ def _candidates(lo: torch.Tensor, hi: torch.Tensor) -> list[torch.Tensor]:
 
 
 def assert_activated_within_bounds(
-    actual: torch.Tensor, x: torch.Tensor, w_gate_up: torch.Tensor, exact_fraction: float = 0.99, **act
+    actual: torch.Tensor, x: torch.Tensor, w_gate_up: torch.Tensor, exact_fraction: float = 0.99,
+    bias: torch.Tensor | None = None, **act
 ) -> None:
+    """Activations within the interval their Gate / Up projections (plus the fp32 ``bias``
+    [2 I] when given) allow, through the gated activation of ``act`` (function, alpha,
+    limit, up_offset) at the payload rounding points, plus one ulp."""
+
     dtype = actual.dtype
-    g_lo, g_hi = projection_interval(x, w_gate_up[0::2], dtype)
-    u_lo, u_hi = projection_interval(x, w_gate_up[1::2], dtype)
+    g_lo, g_hi = projection_interval(x, w_gate_up[0::2], dtype, None if bias is None else bias[0::2])
+    u_lo, u_hi = projection_interval(x, w_gate_up[1::2], dtype, None if bias is None else bias[1::2])
     low = high = None
     for g in _candidates(g_lo, g_hi):
         for u in _candidates(u_lo, u_hi):
-            h = o.gated_silu(g, u, dtype=dtype, **act).double()
+            h = _gated(g, u, dtype, **act).double()
             low = h if low is None else torch.minimum(low, h)
             high = h if high is None else torch.maximum(high, h)
     slack_low = _ulp(low.float(), dtype).double()
@@ -202,7 +224,7 @@ def assert_activated_within_bounds(
     value = a.double()
     outside = int(((value < low - slack_low) | (value > high + slack_high)).sum().item())
     assert outside == 0, f"{outside} of {a.numel()} activations outside their rounding-point interval"
-    nominal = stage_activated(x, w_gate_up, dtype=dtype, **act)
+    nominal = stage_activated(x, w_gate_up, dtype=dtype, bias=bias, **act)
     exact = float((a.view(torch.int16) == nominal.view(torch.int16)).float().mean())
     assert exact >= exact_fraction, f"only {exact:.4f} of activations are bit-identical to the oracle"
 
@@ -217,8 +239,14 @@ def assert_moe_stages(intermediates: dict, x, w_gate_up, w_down, ids, weights, o
       activations (widened by the fp32 product's rounding), p the payload rounding;
     * the combine ``p(scale * sum over slots in order of float(route))`` bit for bit.
 
-    The payload dtype (bf16 or fp16) is the activations'.
+    The payload dtype (bf16 or fp16) is the activations'.  ``act`` holds the activation
+    (function, approximate, alpha, limit, up_offset) and the optional fp32 projection biases
+    ``i_bias`` [E, 2I] and ``o_bias`` [E, H], added before their rounding points.
     """
+
+    act = dict(act)
+    i_bias = act.pop("i_bias", None)
+    o_bias = act.pop("o_bias", None)
 
     rows, topk = ids.shape
     experts = w_gate_up.shape[0]
@@ -241,13 +269,18 @@ def assert_moe_stages(intermediates: dict, x, w_gate_up, w_down, ids, weights, o
         q = torch.nonzero(flat_ids == expert).flatten()
         if q.numel() == 0:
             continue
-        assert_activated_within_bounds(by_route[q], x[q // topk], w_gate_up[expert], exact_fraction=0.0, **act)
-        nominal = stage_activated(x[q // topk], w_gate_up[expert], dtype=dtype, **act)
+        expert_bias = None if i_bias is None else i_bias[expert]
+        assert_activated_within_bounds(by_route[q], x[q // topk], w_gate_up[expert], exact_fraction=0.0,
+                                       bias=expert_bias, **act)
+        nominal = stage_activated(x[q // topk], w_gate_up[expert], dtype=dtype, bias=expert_bias, **act)
         identical += int((by_route[q].view(torch.int16) == nominal.view(torch.int16)).sum())
         h = by_route[q].double()
         w = w_down[expert].double()
         exact = h @ w.t()
         delta = (h.abs() @ w.abs().t()) * ACCUMULATION_BOUND
+        if o_bias is not None:
+            exact = exact + o_bias[expert].double()
+            delta = delta + (exact.abs() + delta) * 2.0**-23
         gamma = gammas[q].unsqueeze(1)
         low, high = (exact - delta) * gamma, (exact + delta) * gamma
         low = low - low.abs() * 2.0**-23
@@ -264,11 +297,15 @@ def assert_moe_stages(intermediates: dict, x, w_gate_up, w_down, ids, weights, o
     assert_bitwise_equal(output, (total * torch.tensor(scale, dtype=torch.float32)).to(dtype))
 
 
-def stage_activated(x: torch.Tensor, w_gate_up: torch.Tensor, dtype: torch.dtype = torch.bfloat16, **act) -> torch.Tensor:
-    """Oracle gate_up + gated SiLU with the reference's rounding points, in the payload ``dtype``."""
+def stage_activated(x: torch.Tensor, w_gate_up: torch.Tensor, dtype: torch.dtype = torch.bfloat16,
+                    bias: torch.Tensor | None = None, **act) -> torch.Tensor:
+    """Oracle gate_up (plus the fp32 ``bias`` when given) and gated activation with the
+    reference's rounding points, in the payload ``dtype``."""
 
     projected = x.double() @ w_gate_up.double().t()
-    return o.gated_silu(projected[:, 0::2].to(dtype), projected[:, 1::2].to(dtype), dtype=dtype, **act)
+    if bias is not None:
+        projected = projected + bias.double()
+    return _gated(projected[:, 0::2].to(dtype), projected[:, 1::2].to(dtype), dtype, **act)
 
 
 def to_device(tensor: torch.Tensor, device) -> torch.Tensor:

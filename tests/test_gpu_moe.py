@@ -20,13 +20,14 @@ from __future__ import annotations
 import pytest
 import torch
 
-from crosspool_amd.ffn import GateTransform, RouterAlgorithm, RouterProjectionPrecision, SiluActivation
+from crosspool_amd.ffn import GateTransform, GeluActivation, ReluActivation, RouterAlgorithm, RouterProjectionPrecision
+from crosspool_amd.ffn import SiluActivation
 from crosspool_amd.ffn import TopKWeightRounding
 from crosspool_amd.moe import Experts, MoeFfnWeights, MoeRouterWeights, Router, finalize_moe_routing, router_topk
 from oracle import ffn_oracle as o
 from oracle import moe_oracle as m
 from parity import assert_bitwise_equal, assert_moe_parity, assert_moe_stages, assert_projection_within_bounds
-from parity import to_device
+from parity import stage_activated, to_device
 
 pytestmark = pytest.mark.gpu
 
@@ -190,13 +191,16 @@ def test_finalize_routing_dynamic_live_rows(device):
     assert final_ids.cpu()[:2].tolist() == [[0, 2, 4], [1, 3, 4]]
 
 
-def _run_experts(device, x, w_gate_up, w_down, ids, weights, scale=1.0, activation=None, gate=None):
+def _run_experts(device, x, w_gate_up, w_down, ids, weights, scale=1.0, activation=None, gate=None, i_bias=None,
+                 o_bias=None):
     rows, hidden = x.shape
     experts, two_i, _ = w_gate_up.shape
     operator = Experts(row_capacity=rows, hidden_size=hidden, local_intermediate_size=two_i // 2,
                        expert_count=experts, effective_topk=ids.shape[1], routed_scaling_factor=scale,
                        activation=activation, gate=gate, device=device, payload_dtype=x.dtype)
-    weights_gpu = MoeFfnWeights(to_device(w_gate_up, device), to_device(w_down, device))
+    weights_gpu = MoeFfnWeights(to_device(w_gate_up, device), to_device(w_down, device),
+                                i_proj_bias=None if i_bias is None else to_device(i_bias, device),
+                                o_proj_bias=None if o_bias is None else to_device(o_bias, device))
     output = torch.empty((rows, hidden), dtype=x.dtype, device=device)
     operator.run_into(hidden_states=to_device(x, device), weights=weights_gpu, topk_ids=to_device(ids, device),
                       topk_weights=to_device(weights, device), output=output)
@@ -212,23 +216,45 @@ def _check_experts(got, x, w_gate_up, w_down, ids, weights, scale=1.0, **act):
     assert_moe_parity(got, stage, pure, m.rounding_slack(routes, stage, scale, dtype=dtype))
 
 
-@pytest.mark.parametrize(
-    "dtype,act",
-    ((torch.bfloat16, {}), (torch.float16, {}), (torch.bfloat16, {"alpha": 1.702, "limit": 7.0, "up_offset": 1.0})),
-    ids=("bfloat16", "float16", "bfloat16-swiglu"),
-)
-def test_experts_reference_operator_case(device, dtype, act):
-    # test_operators.py:110-281: four experts, two slots, a dead row, scale 1.5, the
-    # reference's bf16 and fp16 payload cases.
+def _activation_of(act):
+    function = act.get("function", "silu")
+    if function == "relu":
+        return ReluActivation()
+    if function == "gelu":
+        return GeluActivation(act.get("approximate", "none"))
+    return SiluActivation(act.get("alpha", 1.0))
+
+
+# test_operators.py:110-121: payload dtype, projection biases, activation and gate transform.
+OPERATOR_CASES = [
+    pytest.param(torch.bfloat16, False, {}, id="bf16-silu"),
+    pytest.param(torch.float16, False, {}, id="fp16-silu"),
+    pytest.param(torch.bfloat16, True, {}, id="bf16-bias-silu"),
+    pytest.param(torch.bfloat16, True, {"alpha": 1.702, "limit": 7.0, "up_offset": 1.0}, id="bf16-bias-swiglu"),
+    pytest.param(torch.bfloat16, False, {"alpha": 1.702, "limit": 7.0, "up_offset": 1.0}, id="bf16-swiglu"),
+    pytest.param(torch.bfloat16, True, {"function": "relu", "limit": 4.0, "up_offset": -0.5}, id="bf16-bias-relu"),
+    pytest.param(torch.bfloat16, True, {"function": "gelu"}, id="bf16-bias-gelu"),
+    pytest.param(torch.bfloat16, True, {"function": "gelu", "approximate": "tanh"}, id="bf16-bias-gelu-tanh"),
+]
+
+
+@pytest.mark.parametrize("dtype,with_bias,act", OPERATOR_CASES)
+def test_experts_reference_operator_case(device, dtype, with_bias, act):
+    # test_operators.py:110-281: four experts, two slots, a dead row, scale 1.5, every
+    # payload / bias / activation case of the reference's parametrization.
     generator = torch.Generator().manual_seed(31)
     x = (torch.randn((4, 16), generator=generator) / 4).to(dtype)
     w_gate_up = (torch.randn((4, 16, 16), generator=generator) / 4).to(dtype)
     w_down = (torch.randn((4, 16, 8), generator=generator) / 4).to(dtype)
     ids = torch.tensor(((0, 1), (2, 3), (1, 3), (-1, -1)), dtype=torch.int32)
     weights = torch.tensor(((0.75, 0.25), (0.6, 0.4), (0.9, 0.1), (0.0, 0.0)))
-    activation = SiluActivation(act.get("alpha", 1.0))
+    if with_bias:
+        bias_generator = torch.Generator().manual_seed(32)
+        act = {**act, "i_bias": torch.randn((4, 16), generator=bias_generator),
+               "o_bias": torch.randn((4, 16), generator=bias_generator)}
     gate = GateTransform(limit=act.get("limit"), up_offset=act.get("up_offset", 0.0))
-    got, operator, _ = _run_experts(device, x, w_gate_up, w_down, ids, weights, 1.5, activation, gate)
+    got, operator, _ = _run_experts(device, x, w_gate_up, w_down, ids, weights, 1.5, _activation_of(act), gate,
+                                    act.get("i_bias"), act.get("o_bias"))
     assert_moe_stages(operator.intermediates(), x, w_gate_up, w_down, ids, weights, got, 1.5, **act)
     stage = m.experts_reference(x, w_gate_up, w_down, ids, weights, routed_scaling_factor=1.5, dtype=dtype, **act)
     routes = m.experts_routes(x, w_gate_up, w_down, ids, weights, dtype=dtype, **act)
@@ -327,6 +353,32 @@ def test_experts_fp16_every_tile_family(device, rows, hidden, intermediate, expe
     operator.run_into(hidden_states=to_device(x, device), weights=weights_gpu, topk_ids=to_device(ids, device),
                       topk_weights=to_device(weights, device), output=again)
     assert_bitwise_equal(again.cpu(), got)
+
+
+@PAYLOADS
+def test_experts_rows_independent_of_their_tile_position(device, dtype):
+    # Every route carries the same token row to the same expert (640 routes: ten 64-row
+    # tiles), so every tile row must store the same activations and every output row the same
+    # bits.  The token / expert pair holds an exact fp16 tie: at column 442 the fp32 product
+    # silu(g) * u lies on the midpoint of two fp16 values, and the reference rounds it to fp32
+    # first and then to fp16 (to even).  A multiply fused into the fp16 conversion rounds the
+    # exact product once and lands one ulp higher, in some unrolled epilogue slots only.
+    rows, hidden, intermediate, experts = 640, 2048, 768, 128
+    w_gate_up, w_down = m.generate_moe_layer(hidden, intermediate, experts, 460, std=0.05, dtype=dtype)
+    token = o.generate_hidden_states(320, hidden, 461).to(dtype)[264]
+    x = token.unsqueeze(0).repeat(rows, 1).contiguous()
+    ids = torch.full((rows, 1), 103, dtype=torch.int32)
+    weights = torch.ones((rows, 1))
+    got, operator, _ = _run_experts(device, x, w_gate_up, w_down, ids, weights)
+    activated = operator.intermediates()["activated"][:rows].cpu()
+    bits = activated.view(torch.int16)
+    assert bool((bits == bits[0]).all()), "a route's activations depend on its row in the expert tile"
+    nominal = stage_activated(token.unsqueeze(0), w_gate_up[103], dtype=dtype)[0]
+    if dtype is torch.float16:
+        assert float(activated[0, 442]) == float(nominal[442]) == 2.11328125
+    out = got.view(torch.int16)
+    assert bool((out == out[0]).all())
+    _check_experts(got, x, w_gate_up, w_down, ids, weights)
 
 
 def _capture_no_alloc(run):
@@ -468,6 +520,43 @@ def test_experts_graph_replay_with_new_routing(device, rows, dtype):
         run()
         torch.cuda.synchronize()
         assert_bitwise_equal(output.cpu(), got)
+
+
+@pytest.mark.parametrize(
+    "rows,hidden,intermediate,experts,topk",
+    (
+        (1, 2048, 768, 128, 8),     # grouped split
+        (48, 2048, 768, 128, 8),    # grouped split, 16-route tiles
+        (320, 2048, 768, 128, 8),   # 64-row grouped tiles
+        (240, 256, 128, 8, 2),      # 128-row grouped tiles, nontemporal weight loads
+        (1024, 256, 128, 8, 2),     # 256-row grouped tiles
+    ),
+)
+@pytest.mark.parametrize(
+    "act",
+    ({"function": "relu", "limit": 4.0, "up_offset": -0.5}, {"function": "gelu", "approximate": "tanh"},
+     {"function": "gelu"}, {"alpha": 1.702, "limit": 7.0, "up_offset": 1.0}),
+    ids=("relu", "gelu-tanh", "gelu", "swiglu"),
+)
+def test_experts_bias_and_activation_every_tile_family(device, rows, hidden, intermediate, experts, topk, act):
+    # Projection biases and the non-SiLU activations on each grouped kernel the chooser
+    # takes; every stage against the oracle, the output against the rounding-point slack,
+    # and a repeat bit for bit.
+    w_gate_up, w_down = m.generate_moe_layer(hidden, intermediate, experts, 160 + rows, std=0.05)
+    x = o.generate_hidden_states(rows, hidden, 161 + rows)
+    ids, weights = m.generate_routes(rows, experts, topk, 162 + rows)
+    generator = torch.Generator().manual_seed(163)
+    act = {**act, "i_bias": torch.randn((experts, 2 * intermediate), generator=generator) * 0.5,
+           "o_bias": torch.randn((experts, hidden), generator=generator) * 0.05}
+    gate = GateTransform(limit=act.get("limit"), up_offset=act.get("up_offset", 0.0))
+    got, operator, weights_gpu = _run_experts(device, x, w_gate_up, w_down, ids, weights, 1.25, _activation_of(act),
+                                              gate, act["i_bias"], act["o_bias"])
+    _check_experts(got, x, w_gate_up, w_down, ids, weights, scale=1.25, **act)
+    assert_moe_stages(operator.intermediates(), x, w_gate_up, w_down, ids, weights, got, 1.25, **act)
+    again = torch.empty((rows, hidden), dtype=torch.bfloat16, device=device)
+    operator.run_into(hidden_states=to_device(x, device), weights=weights_gpu, topk_ids=to_device(ids, device),
+                      topk_weights=to_device(weights, device), output=again)
+    assert_bitwise_equal(again.cpu(), got)
 
 
 def test_moe_layer_router_finalize_experts(device):

@@ -162,13 +162,23 @@ def test_moe_experts_rejects_buffer_ranges_past_2_gib():
     lib = _native.library()
     f = ctypes.c_float
     # 2^21 rows of 1024 bf16 = 4 GiB of token rows: refused before any pointer is used.
-    status = lib.xp_moe_experts(None, 1 << 21, 1024, 256, 8, 2, None, None, None, None, f(1.0), f(1.0), f(0.0),
-                                f(0.0), _native.XP_DTYPE_BF16, None, None, 0, None)
+    status = lib.xp_moe_experts(None, 1 << 21, 1024, 256, 8, 2, None, None, None, None, None, None, f(1.0),
+                                _native.XP_ACTIVATION_SILU, 0, f(1.0), f(0.0), f(0.0), _native.XP_DTYPE_BF16, None,
+                                None, 0, None)
     assert status == _native.XP_ERROR_INVALID_ARGUMENT
     assert "2 GiB" in _native.last_error()
     # An expert of 2 x 32768 x 16384 bf16 gate_up rows is past one range as well.
-    status = lib.xp_moe_experts(None, 4, 16384, 32768, 8, 2, None, None, None, None, f(1.0), f(1.0), f(0.0),
-                                f(0.0), _native.XP_DTYPE_BF16, None, None, 0, None)
+    status = lib.xp_moe_experts(None, 4, 16384, 32768, 8, 2, None, None, None, None, None, None, f(1.0),
+                                _native.XP_ACTIVATION_SILU, 0, f(1.0), f(0.0), f(0.0), _native.XP_DTYPE_BF16, None,
+                                None, 0, None)
+    assert status == _native.XP_ERROR_INVALID_ARGUMENT
+    # An activation outside SiLU / ReLU / GELU, and the tanh form on anything but GELU.
+    status = lib.xp_moe_experts(None, 4, 1024, 256, 8, 2, None, None, None, None, None, None, f(1.0), 0, 0,
+                                f(1.0), f(0.0), f(0.0), _native.XP_DTYPE_BF16, None, None, 0, None)
+    assert status == _native.XP_ERROR_INVALID_ARGUMENT and "activation" in _native.last_error()
+    status = lib.xp_moe_experts(None, 4, 1024, 256, 8, 2, None, None, None, None, None, None, f(1.0),
+                                _native.XP_ACTIVATION_RELU, 1, f(1.0), f(0.0), f(0.0), _native.XP_DTYPE_BF16, None,
+                                None, 0, None)
     assert status == _native.XP_ERROR_INVALID_ARGUMENT
 
 

@@ -133,8 +133,10 @@ def _operator_test_case(payload_dtype=torch.bfloat16):
     return x, w_gate_up, w_down, ids, weights
 
 
-def _reference_test_formula(x, w_gate_up, w_down, ids, weights, scale, alpha=1.0, limit=None, up_offset=0.0):
-    """test_operators.py:255-281 transcribed literally (fp32 torch.mv, per route)."""
+def _reference_test_formula(x, w_gate_up, w_down, ids, weights, scale, alpha=1.0, limit=None, up_offset=0.0,
+                            function="silu", approximate="none", i_bias=None, o_bias=None):
+    """test_operators.py:255-281 transcribed literally (fp32 torch.mv, per route; torch's own
+    relu / gelu for the other activations)."""
 
     expected = torch.zeros_like(x, dtype=torch.float32)
     for row in range(x.shape[0]):
@@ -142,23 +144,54 @@ def _reference_test_formula(x, w_gate_up, w_down, ids, weights, scale, alpha=1.0
             expert = int(ids[row, slot])
             if expert < 0:
                 continue
-            projected = torch.mv(w_gate_up[expert].float(), x[row].float()).to(x.dtype)
+            projected = torch.mv(w_gate_up[expert].float(), x[row].float())
+            if i_bias is not None:
+                projected += i_bias[expert]
+            projected = projected.to(x.dtype)
             gate, up = projected[::2].float(), projected[1::2].float()
             if limit is not None:
                 gate = gate.clamp(max=limit)
                 up = up.clamp(min=-limit, max=limit)
-            activated = (gate * torch.sigmoid(alpha * gate) * (up + up_offset)).to(x.dtype)
+            if function == "relu":
+                activated = gate.relu()
+            elif function == "gelu":
+                activated = torch.nn.functional.gelu(gate, approximate=approximate)
+            else:
+                activated = gate * torch.sigmoid(alpha * gate)
+            activated = (activated * (up + up_offset)).to(x.dtype)
             route = torch.mv(w_down[expert].float(), activated.float())
+            if o_bias is not None:
+                route += o_bias[expert]
             expected[row] += (route * weights[row, slot]).to(x.dtype).float()
         expected[row] *= scale
     return expected.to(x.dtype)
 
 
-@PAYLOADS
-@pytest.mark.parametrize("act", ({}, {"alpha": 1.702, "limit": 7.0, "up_offset": 1.0}))
-def test_experts_match_the_reference_test_formula(act, dtype):
-    # test_operators.py:110-121 runs the formula with bf16 and fp16 payloads.
+# test_operators.py:110-121: payload dtype, projection biases, activation and gate transform.
+OPERATOR_CASES = [
+    pytest.param(torch.bfloat16, False, {}, id="bf16-silu"),
+    pytest.param(torch.float16, False, {}, id="fp16-silu"),
+    pytest.param(torch.bfloat16, True, {}, id="bf16-bias-silu"),
+    pytest.param(torch.bfloat16, True, {"alpha": 1.702, "limit": 7.0, "up_offset": 1.0}, id="bf16-bias-swiglu"),
+    pytest.param(torch.bfloat16, True, {"function": "relu", "limit": 4.0, "up_offset": -0.5}, id="bf16-bias-relu"),
+    pytest.param(torch.bfloat16, True, {"function": "gelu"}, id="bf16-bias-gelu"),
+    pytest.param(torch.bfloat16, True, {"function": "gelu", "approximate": "tanh"}, id="bf16-bias-gelu-tanh"),
+]
+
+
+def _operator_biases(with_bias: bool):
+    # test_operators.py:216-226: randn fp32 biases of i_proj [E, 2I] and o_proj [E, H].
+    if not with_bias:
+        return {}
+    generator = torch.Generator().manual_seed(32)
+    return {"i_bias": torch.randn((4, 16), generator=generator), "o_bias": torch.randn((4, 16), generator=generator)}
+
+
+@pytest.mark.parametrize("dtype,with_bias,act", OPERATOR_CASES)
+def test_experts_match_the_reference_test_formula(dtype, with_bias, act):
+    # Every parametrization of test_operators.py:110-121.
     x, w_gate_up, w_down, ids, weights = _operator_test_case(dtype)
+    act = {**act, **_operator_biases(with_bias)}
     got = m.experts_reference(x, w_gate_up, w_down, ids, weights, routed_scaling_factor=1.5, dtype=dtype, **act)
     assert got.dtype is dtype
     expected = _reference_test_formula(x, w_gate_up, w_down, ids, weights, 1.5, **act)
@@ -279,3 +312,25 @@ def test_fp16_router_logits_round_to_binary16():
     assert ids.tolist() == [[1]]  # bf16 (spacing 2^-8 at 0.5) merges what binary16 keeps apart
     ids, _ = m.router_topk(scores, topk=1, softmax=False, correction_bias=bias, logits_dtype=torch.float16)
     assert ids.tolist() == [[0]]
+
+
+def test_experts_bias_and_activation_planted_mistakes():
+    # With the reference's biased cases, dropping either bias, or evaluating another
+    # activation, moves the output by more than 5 % rel-L2 from the reference's formula;
+    # the oracle stays within 1 %.
+    x, w_gate_up, w_down, ids, weights = _operator_test_case()
+    biases = _operator_biases(True)
+    for act in ({"function": "relu", "limit": 4.0, "up_offset": -0.5}, {"function": "gelu"}, {}):
+        expected = _reference_test_formula(x, w_gate_up, w_down, ids, weights, 1.5, **act, **biases).float()
+        good = m.experts_reference(x, w_gate_up, w_down, ids, weights, routed_scaling_factor=1.5, **act, **biases)
+        assert o.compare(expected, good.float()).rel_l2 < 0.01
+        other = {"function": "silu"} if act.get("function") else {"function": "gelu"}
+        for wrong in (
+            m.experts_reference(x, w_gate_up, w_down, ids, weights, routed_scaling_factor=1.5, **act,
+                                o_bias=biases["o_bias"]),
+            m.experts_reference(x, w_gate_up, w_down, ids, weights, routed_scaling_factor=1.5, **act,
+                                i_bias=biases["i_bias"]),
+            m.experts_reference(x, w_gate_up, w_down, ids, weights, routed_scaling_factor=1.5,
+                                **{**act, **other}, **biases),
+        ):
+            assert o.compare(expected, wrong.float()).rel_l2 > 0.05
