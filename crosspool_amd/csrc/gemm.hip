@@ -1677,7 +1677,7 @@ __device__ __forceinline__ float row_factor(const RowMeta<WTM> &meta, int row) {
   return value;
 }
 
-template <int MT, int NT, int WTM, int WTN, int WAVES, int LDS_ELEMENTS, bool GATED, bool GROUPED, class P>
+template <int MT, int NT, int WTM, int WTN, int WAVES, int LDS_ELEMENTS, bool GATED, bool GROUPED, class P, bool EXTENDED>
 __device__ __forceinline__ void tile_epilogue(const GemmArgs &a, const f32x16 (&acc)[MT][NT], uint16_t *lds,
                                               int64_t m0, int64_t row_end, int64_t w0, int wave, int wm, int wn,
                                               const RowMeta<WTM> &meta, int expert) {
@@ -1738,13 +1738,14 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs &a, const f32x16 (&
   // Chunk c of row r sits at physical chunk c ^ ((r / 4) % CPR): the two row groups one
   // write instruction covers (rows r and r + 4) then fall in different banks.
   auto slot_of = [](int row, int chunk) { return row * OUT_N + ((chunk ^ ((row >> 2) & (CPR - 1))) << 3); };
-  const int64_t row0 = m0 + wm * WTM;
-  const int64_t col0 = GATED ? w0 / 2 + wn * (WTN / 2) : w0 + wn * WTN;
-  // Grouped projections with a bias: the expert's fp32 bias, indexed by weight row (gate_up:
-  // Gate and Up of output column c are weight rows 2 c and 2 c + 1).
+  // EXTENDED (grouped projections with a bias or a ReLU / GELU activation): the expert's
+  // fp32 bias, indexed by weight row (gate_up: Gate and Up of output column c are weight
+  // rows 2 c and 2 c + 1), and the first output column of this wave's tile.
   const float *bias = nullptr;
-  if constexpr (GROUPED) {
+  int64_t bias_col0 = 0;
+  if constexpr (EXTENDED) {
     bias = a.bias != nullptr ? a.bias + static_cast<int64_t>(expert) * a.bias_stride : nullptr;
+    bias_col0 = GATED ? w0 / 2 + wn * (WTN / 2) : w0 + wn * WTN;
   }
   // The gated activation is the epilogue's VALU cost (two quarter-rate transcendentals per
   // output); its clipping is chosen once per tile, not per element.
@@ -1763,21 +1764,21 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs &a, const f32x16 (&
         for (int nt = 0; nt < OUT_N / 32; ++nt) {
           const int col = nt * 32 + frag_row;
           float value;
-          if constexpr (GATED && GROUPED) {
+          if constexpr (GATED && EXTENDED) {
             float gate = acc[mt][nt][r];
             float up = acc[mt][nt + NT / 2][r];
             if (bias != nullptr) {
-              const int64_t c = col0 + col < a.n / 2 ? col0 + col : 0;  // (columns past N are not stored)
+              const int64_t c = bias_col0 + col < a.n / 2 ? bias_col0 + col : 0;  // (columns past N are not stored)
               gate += bias[2 * c];
               up += bias[2 * c + 1];
             }
             value = moe_gated_payload<P, decltype(clip)::value>(gate, up, a.act);
           } else if constexpr (GATED) {
             value = gated_silu_payload<P, decltype(clip)::value>(acc[mt][nt][r], acc[mt][nt + NT / 2][r], a.act);
-          } else if constexpr (GROUPED) {
+          } else if constexpr (EXTENDED) {
             float sum = acc[mt][nt][r];
             if (bias != nullptr) {
-              sum += bias[col0 + col < a.n ? col0 + col : 0];
+              sum += bias[bias_col0 + col < a.n ? bias_col0 + col : 0];
             }
             value = sum * factor;
           } else {
@@ -1794,6 +1795,8 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs &a, const f32x16 (&
     stage(std::false_type{});
   }
   __syncthreads();
+  const int64_t row0 = m0 + wm * WTM;
+  const int64_t col0 = GATED ? w0 / 2 + wn * (WTN / 2) : w0 + wn * WTN;
   const int64_t out_cols = GATED ? a.n / 2 : a.n;
 #pragma unroll 4
   for (int index = lane; index < WTM * CPR; index += 64) {
@@ -1825,7 +1828,7 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs &a, const f32x16 (&
 // range each workgroup writes the fp32 partial tile of its range and
 // stream_reduce_kernel, launched next, adds the ranges in order and applies the epilogue.
 template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, bool GATED, bool GROUPED = false,
-          bool STREAM_WEIGHTS = GROUPED, class PAYLOAD = Bf16Payload>
+          bool STREAM_WEIGHTS = GROUPED, class PAYLOAD = Bf16Payload, bool EXTENDED = false>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmArgs a) {
   constexpr int BK = 64;
   constexpr int WAVES = WAVES_M * WAVES_N;
@@ -2244,7 +2247,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void tile_gemm_kernel(GemmA
   // Past-the-end refills may still be landing in the stage buffers the epilogue reuses.
   __builtin_amdgcn_s_waitcnt(0);
 
-  tile_epilogue<MT, NT, WTM, WTN, WAVES, STAGES * STAGE, GATED, GROUPED, PAYLOAD>(a, acc, lds, m0, row_end, w0, wave, wm, wn,
+  tile_epilogue<MT, NT, WTM, WTN, WAVES, STAGES * STAGE, GATED, GROUPED, PAYLOAD, EXTENDED>(a, acc, lds, m0, row_end, w0, wave, wm, wn,
                                                                          meta, expert);
 }
 
@@ -2994,35 +2997,42 @@ GroupedTile grouped_tile(MoeTile tile, bool gated) {
   }
 }
 
-template <bool GATED, class P>
+// X: the EXTENDED epilogue (a bias or a ReLU / GELU activation), a separate instantiation so
+// that the SiLU projections without bias keep their code (the general epilogue cost the
+// 128-row gate_up tiles 3 % at 2048 tokens).
+template <bool GATED, class P, bool X>
 const void *grouped_tile_kernel(MoeTile tile) {
   switch (tile) {
     case MoeTile::Rows64:
-      return reinterpret_cast<const void *>(&tile_gemm_kernel<64, 128, 2, 2, 3, GATED, true, true, P>);
+      return reinterpret_cast<const void *>(&tile_gemm_kernel<64, 128, 2, 2, 3, GATED, true, true, P, X>);
     case MoeTile::Rows128Stream:
-      return GATED ? reinterpret_cast<const void *>(&tile_gemm_kernel<128, 256, 2, 4, 3, GATED, true, true, P>)
-                   : reinterpret_cast<const void *>(&tile_gemm_kernel<128, 128, 4, 2, 2, GATED, true, true, P>);
+      return GATED ? reinterpret_cast<const void *>(&tile_gemm_kernel<128, 256, 2, 4, 3, GATED, true, true, P, X>)
+                   : reinterpret_cast<const void *>(&tile_gemm_kernel<128, 128, 4, 2, 2, GATED, true, true, P, X>);
     case MoeTile::Rows128:
-      return GATED ? reinterpret_cast<const void *>(&tile_gemm_kernel<128, 256, 2, 4, 3, GATED, true, false, P>)
-                   : reinterpret_cast<const void *>(&tile_gemm_kernel<128, 128, 4, 2, 2, GATED, true, false, P>);
+      return GATED ? reinterpret_cast<const void *>(&tile_gemm_kernel<128, 256, 2, 4, 3, GATED, true, false, P, X>)
+                   : reinterpret_cast<const void *>(&tile_gemm_kernel<128, 128, 4, 2, 2, GATED, true, false, P, X>);
     case MoeTile::Rows256:
-      return reinterpret_cast<const void *>(&tile_gemm_kernel<256, 128, 4, 2, 3, GATED, true, true, P>);
+      return reinterpret_cast<const void *>(&tile_gemm_kernel<256, 128, 4, 2, 3, GATED, true, true, P, X>);
     default:
       return nullptr;
   }
 }
 
 template <bool GATED>
-const void *grouped_tile_kernel(MoeTile tile, int32_t payload) {
-  return payload == kPayloadF16 ? grouped_tile_kernel<GATED, F16Payload>(tile)
-                                : grouped_tile_kernel<GATED, Bf16Payload>(tile);
+const void *grouped_tile_kernel(MoeTile tile, const GemmArgs &args) {
+  const bool extended =
+      args.bias != nullptr || args.act.function == kActivationRelu || args.act.function == kActivationGelu;
+  if (args.payload == kPayloadF16) {
+    return extended ? grouped_tile_kernel<GATED, F16Payload, true>(tile) : grouped_tile_kernel<GATED, F16Payload, false>(tile);
+  }
+  return extended ? grouped_tile_kernel<GATED, Bf16Payload, true>(tile) : grouped_tile_kernel<GATED, Bf16Payload, false>(tile);
 }
 
 int grouped_tile_rows(MoeTile tile) { return grouped_tile(tile, true).bm; }  // the same for down
 
 KernelLaunch make_grouped_gemm(const GemmArgs &args, bool gated, int max_tiles, MoeTile tile) {
   const GroupedTile shape = grouped_tile(tile, gated);
-  const void *func = gated ? grouped_tile_kernel<true>(tile, args.payload) : grouped_tile_kernel<false>(tile, args.payload);
+  const void *func = gated ? grouped_tile_kernel<true>(tile, args) : grouped_tile_kernel<false>(tile, args);
   if (max_tiles % 8 != 0 || func == nullptr) {
     return KernelLaunch{};  // grouped_tile_coordinates needs a multiple of 8 (callers pad)
   }
