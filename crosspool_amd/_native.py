@@ -56,6 +56,9 @@ class MoeLayerDesc(ctypes.Structure):
         ("limit", ctypes.c_float),
         ("up_offset", ctypes.c_float),
         ("payload", ctypes.c_int),
+        ("activation", ctypes.c_int),
+        ("approximate_tanh", ctypes.c_int),
+        ("biases", ctypes.c_int),
     ]
 
 
@@ -130,7 +133,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _F32, _INT, _INT, _F32, _F32, _F32, _INT, _P, _P,
          _SIZE, _P],
     ),
-    "xp_moe_layer_register": (_INT, [_P, _INT, _INT, ctypes.POINTER(MoeLayerDesc), _P, _P, _P, _P, _P, _F32]),
+    "xp_moe_layer_register": (_INT, [_P, _INT, _INT, ctypes.POINTER(MoeLayerDesc), _P, _P, _P, _P, _P, _P, _P, _F32]),
     "xp_moe_step_workspace_bytes": (_SIZE, [ctypes.POINTER(MoeLayerDesc), _I64]),
     "xp_moe_step_workspace_layout": (_INT, [ctypes.POINTER(MoeLayerDesc), _I64, ctypes.POINTER(_SIZE)]),
     "xp_moe_template_capture": (_INT, [_P, ctypes.POINTER(MoeLayerDesc), _I64]),

@@ -33,6 +33,12 @@ from crosspool_amd.weights import DenseFfnWeights, validate_weight_tensor
 logger = logging.getLogger(__name__)
 
 
+def _moe_biases(weights) -> int:
+    """The projection-bias bits of MoE weights (bit 0 i_proj, bit 1 o_proj)."""
+
+    return int(weights.i_proj_bias is not None) | 2 * int(weights.o_proj_bias is not None)
+
+
 @dataclass(frozen=True, slots=True)
 class GraphTemplate:
     """One captured graph identity: the Execution Signature (execution.py:73-149).
@@ -366,13 +372,16 @@ class FfnAgent:
                 raise ValueError("RMSNorm weight must reside on the agent's device")
         signature = spec.signature(
             hidden_size=weights.hidden_size, local_intermediate_size=weights.local_intermediate_size,
-            payload_row_capacity=1, payload_dtype=weights.payload_dtype,
+            payload_row_capacity=1, payload_dtype=weights.payload_dtype, biases=_moe_biases(weights),
         )
         router = weights.router
         _native.call(
             "xp_moe_layer_register", self.handle, instance_index, layer_ordinal,
             ctypes.byref(signature.native_descriptor()), ctypes.c_void_p(weights.i_proj.data_ptr()),
-            ctypes.c_void_p(weights.o_proj.data_ptr()), ctypes.c_void_p(router.projection.data_ptr()),
+            ctypes.c_void_p(weights.o_proj.data_ptr()),
+            None if weights.i_proj_bias is None else ctypes.c_void_p(weights.i_proj_bias.data_ptr()),
+            None if weights.o_proj_bias is None else ctypes.c_void_p(weights.o_proj_bias.data_ptr()),
+            ctypes.c_void_p(router.projection.data_ptr()),
             None if router.correction_bias is None else ctypes.c_void_p(router.correction_bias.data_ptr()),
             None if norm_weight is None else ctypes.c_void_p(norm_weight.data_ptr()), float(eps),
         )
@@ -453,6 +462,7 @@ class FfnAgent:
                     local_intermediate_size=binding.weights.local_intermediate_size,
                     payload_row_capacity=capacity,
                     payload_dtype=binding.payload_dtype,
+                    biases=_moe_biases(binding.weights),
                 ))
                 self.templates.setdefault(template.key, template)
         workspace_bytes = max(t.workspace_bytes for t in self.templates.values())

@@ -305,6 +305,8 @@ struct Layer {
   xp_moe_layer_desc moe{};
   const void *router = nullptr;
   const float *correction_bias = nullptr;
+  const float *gate_up_bias = nullptr;  // fp32 projection biases (moe.biases), or null
+  const float *down_bias = nullptr;
 };
 
 struct xp_agent {
@@ -739,7 +741,8 @@ bool same_moe(const xp_moe_layer_desc &a, const xp_moe_layer_desc &b) {
          a.routed_experts == b.routed_experts && a.routed_topk == b.routed_topk && a.algorithm == b.algorithm &&
          a.precision == b.precision && (a.renormalize != 0) == (b.renormalize != 0) &&
          a.weight_rounding == b.weight_rounding && a.routed_scaling_factor == b.routed_scaling_factor &&
-         a.alpha == b.alpha && a.limit == b.limit && a.up_offset == b.up_offset && a.payload == b.payload;
+         a.alpha == b.alpha && a.limit == b.limit && a.up_offset == b.up_offset && a.payload == b.payload &&
+         a.activation == b.activation && a.approximate_tanh == b.approximate_tanh && a.biases == b.biases;
 }
 
 int validate_moe_desc(const xp_moe_layer_desc *d) {
@@ -757,6 +760,12 @@ int validate_moe_desc(const xp_moe_layer_desc *d) {
   }
   XP_REQUIRE(d->routed_scaling_factor > 0.0f && d->routed_scaling_factor < __builtin_inff(),
              "routed scaling factor must be finite and positive");
+  XP_REQUIRE(d->activation == XP_ACTIVATION_SILU || d->activation == XP_ACTIVATION_RELU ||
+                 d->activation == XP_ACTIVATION_GELU,
+             "MoE activation must be SiLU, ReLU or GELU");
+  XP_REQUIRE(d->approximate_tanh == 0 || (d->activation == XP_ACTIVATION_GELU && d->approximate_tanh == 1),
+             "the tanh approximation is GELU's only");
+  XP_REQUIRE(d->biases >= 0 && d->biases <= 3, "MoE biases are bit 0 (gate_up) and bit 1 (down)");
   XP_REQUIRE(d->alpha > 0.0f && d->alpha < __builtin_inff(), "SiLU alpha must be positive and finite");
   XP_REQUIRE(d->limit >= 0.0f && d->limit < __builtin_inff() && std::isfinite(d->up_offset),
              "gate limit must be finite and non-negative (0 = none) and the up offset finite");
@@ -926,7 +935,13 @@ int make_moe_step(const Layer &layer, const MoeStepBinding &b, int64_t capacity,
   experts.experts = d.experts;
   experts.topk = topk;
   experts.scale = d.routed_scaling_factor;
-  experts.act = GatedSilu{d.alpha, d.limit, d.up_offset};
+  experts.act = GatedSilu{d.alpha, d.limit, d.up_offset,
+                          d.activation == XP_ACTIVATION_RELU   ? kActivationRelu
+                          : d.activation == XP_ACTIVATION_GELU ? kActivationGelu
+                                                               : kActivationSilu,
+                          d.approximate_tanh};
+  experts.bias_gate_up = layer.gate_up_bias;
+  experts.bias_down = layer.down_bias;
   experts.payload = payload;
   if (fuse_topk) {
     experts.fused_topk = &routing.topk_args;
@@ -2243,8 +2258,8 @@ int xp_moe_experts(const void *hidden_states, int64_t rows, int64_t hidden, int6
 // ------------------------------------------------------------------ MoE layer kind
 
 int xp_moe_layer_register(xp_agent_t agent, int instance_index, int layer_ordinal, const xp_moe_layer_desc *desc,
-                          const void *gate_up, const void *down, const void *router, const float *correction_bias,
-                          const void *norm_weight, float eps) {
+                          const void *gate_up, const void *down, const float *gate_up_bias, const float *down_bias,
+                          const void *router, const float *correction_bias, const void *norm_weight, float eps) {
   XP_REQUIRE(agent != nullptr, "agent must be non-null");
   XP_REQUIRE(instance_index >= 0 && layer_ordinal >= 0, "instance index and layer ordinal must be non-negative");
   if (const int status = validate_moe_desc(desc); status != XP_OK) {
@@ -2254,6 +2269,9 @@ int xp_moe_layer_register(xp_agent_t agent, int instance_index, int layer_ordina
   XP_REQUIRE(aligned16(gate_up) && aligned16(down) && aligned16(router) &&
                  (norm_weight == nullptr || aligned16(norm_weight)) && aligned_to(correction_bias, 4),
              "MoE layer weights must be 16-byte aligned (the correction bias 4-byte aligned)");
+  XP_REQUIRE((gate_up_bias != nullptr) == ((desc->biases & 1) != 0) && (down_bias != nullptr) == ((desc->biases & 2) != 0),
+             "MoE projection biases must be given exactly as the descriptor's biases say");
+  XP_REQUIRE(aligned16(gate_up_bias) && aligned16(down_bias), "MoE projection biases must be 16-byte aligned");
   XP_REQUIRE(norm_weight == nullptr || eps >= 0.0f, "RMSNorm epsilon must be non-negative");
   Layer layer{instance_index,
               layer_ordinal,
@@ -2271,6 +2289,8 @@ int xp_moe_layer_register(xp_agent_t agent, int instance_index, int layer_ordina
   }
   layer.router = router;
   layer.correction_bias = correction_bias;
+  layer.gate_up_bias = gate_up_bias;
+  layer.down_bias = down_bias;
   std::lock_guard<std::mutex> guard(agent->mutex);
   for (Layer &existing : agent->layers) {
     if (existing.instance_index == instance_index && existing.layer_ordinal == layer_ordinal) {

@@ -12,6 +12,8 @@ import torch
 
 from crosspool_amd.ffn import (
     GateTransform,
+    GeluActivation,
+    ReluActivation,
     RouterAlgorithm,
     RouterProjectionPrecision,
     SiluActivation,
@@ -188,8 +190,10 @@ class MoeFfnExecutionSignature:
     effective_topk: int
     routed_scaling_factor: float
     router: MoeRouterExecutionSignature
-    activation: SiluActivation = SiluActivation()
+    activation: SiluActivation | ReluActivation | GeluActivation = SiluActivation()
     gate: GateTransform = GateTransform()
+    # Projection biases of the layer's experts (ProjectionLayout.bias): bit 0 i_proj, bit 1 o_proj.
+    biases: int = 0
 
     def __post_init__(self) -> None:
         if self.payload_dtype not in (torch.bfloat16, torch.float16):
@@ -223,7 +227,8 @@ class MoeFfnExecutionSignature:
 
         from crosspool_amd import _native
 
-        alpha, limit, up_offset = activation_arguments(self.activation, self.gate)
+        silu = isinstance(self.activation, SiluActivation)
+        alpha, limit, up_offset = activation_arguments(self.activation if silu else SiluActivation(), self.gate)
         router = self.router
         return _native.MoeLayerDesc(
             hidden=self.hidden_size,
@@ -240,4 +245,7 @@ class MoeFfnExecutionSignature:
             limit=limit,
             up_offset=up_offset,
             payload=_native.payload_dtype_code(self.payload_dtype),
+            activation=int(self.activation.kind),
+            approximate_tanh=int(isinstance(self.activation, GeluActivation) and self.activation.approximate == "tanh"),
+            biases=int(self.biases),
         )

@@ -157,7 +157,7 @@ class MoeLayerSpec:
     router_algorithm: RouterAlgorithm = RouterAlgorithm.SOFTMAX
     router_projection_precision: RouterProjectionPrecision = RouterProjectionPrecision.PAYLOAD
     topk_weight_rounding: TopKWeightRounding = TopKWeightRounding.NONE
-    activation: SiluActivation = SiluActivation()
+    activation: SiluActivation | ReluActivation | GeluActivation = SiluActivation()
     gate: GateTransform = GateTransform()
 
     def __post_init__(self) -> None:
@@ -185,8 +185,6 @@ class MoeLayerSpec:
             )
         if weights.router is None:
             raise ValueError("the Lane owns the Router on one device: MoE weights need a Router projection")
-        if weights.i_proj_bias is not None or weights.o_proj_bias is not None:
-            raise ValueError("MoE layers take projections without biases (the Experts operator takes biases)")
         weight_dtype = (
             torch.float32 if self.router_projection_precision is RouterProjectionPrecision.FP32
             else weights.payload_dtype
@@ -203,7 +201,7 @@ class MoeLayerSpec:
 
     def signature(
         self, *, hidden_size: int, local_intermediate_size: int, payload_row_capacity: int,
-        payload_dtype: torch.dtype = torch.bfloat16,
+        payload_dtype: torch.dtype = torch.bfloat16, biases: int = 0,
     ):
         """The MoeFfnExecutionSignature of this layer at one capacity."""
 
@@ -227,6 +225,7 @@ class MoeLayerSpec:
             ),
             activation=self.activation,
             gate=self.gate,
+            biases=biases,
         )
 
 

@@ -475,17 +475,22 @@ typedef struct {
   float limit;              /* Gate/Up clip, 0 = none */
   float up_offset;
   int payload;              /* XP_DTYPE_BF16 or XP_DTYPE_F16: the mailbox rows and weights */
+  int activation;           /* XP_ACTIVATION_SILU / RELU / GELU (alpha is SiLU's slope) */
+  int approximate_tanh;     /* GELU: the tanh approximation */
+  int biases;               /* projection biases bound at registration: bit 0 gate_up, bit 1 down */
 } xp_moe_layer_desc;
 
 /* Register (or rebind) one MoE layer's borrowed weights, of desc->payload unless stated:
  * gate_up [experts, 2*intermediate, hidden] (Gate/Up INTERLEAVED per expert), down
- * [experts, hidden, intermediate], router [routed_experts, hidden] (fp32 for the FP32
- * precision), correction_bias [routed_experts] fp32 or NULL, norm_weight [hidden] or NULL.
+ * [experts, hidden, intermediate], the fp32 projection biases gate_up_bias [experts,
+ * 2*intermediate] and down_bias [experts, hidden] (given exactly as desc->biases says, else
+ * NULL), router [routed_experts, hidden] (fp32 for the FP32 precision), correction_bias
+ * [routed_experts] fp32 or NULL, norm_weight [hidden] or NULL.
  * Replaces LayerExecutionDescriptor + MoeBindingView (src/cext-bindings/ffnagent.cpp) and
  * the MoE branch of validate_layer_weights_against_layout (registry.py:153-174). */
 int xp_moe_layer_register(xp_agent_t agent, int instance_index, int layer_ordinal, const xp_moe_layer_desc *desc,
-                          const void *gate_up, const void *down, const void *router, const float *correction_bias,
-                          const void *norm_weight, float eps);
+                          const void *gate_up, const void *down, const float *gate_up_bias, const float *down_bias,
+                          const void *router, const float *correction_bias, const void *norm_weight, float eps);
 
 /* Lane workspace bytes of one MoE template at `capacity` rows (0 for an invalid
  * descriptor).  Replaces the MoE branch of the capture workspace sizing

@@ -31,7 +31,8 @@ from crosspool_amd import _native
 from crosspool_amd.agent import FfnAgent, FfnHealthError
 from crosspool_amd.execution import derive_payload_row_capacities, select_capacity
 from crosspool_amd.ffn import DpRowLayout, ForwardMode, GateTransform, OutputRequirement, RouterAlgorithm
-from crosspool_amd.ffn import RouterProjectionPrecision, SiluActivation, TopKWeightRounding
+from crosspool_amd.ffn import GeluActivation, ReluActivation, RouterProjectionPrecision, SiluActivation
+from crosspool_amd.ffn import TopKWeightRounding
 from crosspool_amd.moe import Experts, MoeFfnWeights, MoeLayerSpec, MoeRouterWeights, Router, finalize_moe_routing
 from crosspool_amd.ops import attach, detach, ffn_shim
 from crosspool_amd.dense import gather_rmsnorm
@@ -56,10 +57,19 @@ def _layer(hidden, intermediate, spec, seed, std=0.05, dtype=torch.bfloat16):
     return w_gate_up, w_down, projection, correction, norm_weight
 
 
-def _act(spec):
+def _act(spec, i_bias=None, o_bias=None):
     act = {}
-    if spec.activation.alpha != 1.0:
+    if isinstance(spec.activation, ReluActivation):
+        act["function"] = "relu"
+    elif isinstance(spec.activation, GeluActivation):
+        act["function"] = "gelu"
+        act["approximate"] = spec.activation.approximate
+    elif spec.activation.alpha != 1.0:
         act["alpha"] = spec.activation.alpha
+    if i_bias is not None:
+        act["i_bias"] = i_bias
+    if o_bias is not None:
+        act["o_bias"] = o_bias
     if spec.gate.limit is not None:
         act["limit"] = spec.gate.limit
     if spec.gate.up_offset:
@@ -104,7 +114,8 @@ def _lane_stages(lane, spec, hidden, intermediate, capacity, rows, dtype=torch.b
     }
 
 
-def _check_replay(stages, pool, new_pool, slots, spec, w_gate_up, w_down, projection, correction, norm_weight):
+def _check_replay(stages, pool, new_pool, slots, spec, w_gate_up, w_down, projection, correction, norm_weight,
+                  i_bias=None, o_bias=None):
     rows = len(slots)
     dtype = pool.dtype
     untouched = np.setdiff1d(np.arange(pool.shape[0]), slots)
@@ -147,7 +158,7 @@ def _check_replay(stages, pool, new_pool, slots, spec, w_gate_up, w_down, projec
     assert torch.equal(stages["final_weights"], final_weights)
 
     output = o.gather(new_pool, slots)
-    act = _act(spec)
+    act = _act(spec, i_bias, o_bias)
     scale = spec.routed_scaling_factor
     assert_moe_stages(stages["experts"], batch, w_gate_up, w_down, final_ids, final_weights, output, scale, **act)
     routes = m.experts_routes(batch, w_gate_up, w_down, final_ids, final_weights, dtype=dtype, **act)
@@ -159,9 +170,11 @@ def _check_replay(stages, pool, new_pool, slots, spec, w_gate_up, w_down, projec
 
 
 def _register(agent, spec, hidden, w_gate_up, w_down, projection, correction, norm_weight, device, ordinal=0,
-              corrected=False):
+              corrected=False, i_bias=None, o_bias=None):
     router = MoeRouterWeights(to_device(projection, device), to_device(correction, device) if corrected else None)
-    weights = MoeFfnWeights(to_device(w_gate_up, device), to_device(w_down, device), router)
+    weights = MoeFfnWeights(to_device(w_gate_up, device), to_device(w_down, device), router,
+                            i_proj_bias=None if i_bias is None else to_device(i_bias, device),
+                            o_proj_bias=None if o_bias is None else to_device(o_bias, device))
     agent.register_moe_layer(
         instance_index=0, layer_ordinal=ordinal, weights=weights, spec=spec,
         norm_weight=None if norm_weight is None else to_device(norm_weight, device),
@@ -313,6 +326,52 @@ def test_moe_out_of_range_slot_sets_sticky_fault(device, capacity, rows):
     untouched = np.setdiff1d(np.arange(pool_rows), live)
     assert_bitwise_equal(faulty[untouched], pool[untouched])
     assert not torch.equal(valid[slots[1]], pool[slots[1]])  # the valid replay did write that row
+
+
+@pytest.mark.parametrize(
+    "spec,biases,replays",
+    [
+        pytest.param(  # GPT-OSS-style SwiGLU experts with both projection biases
+            MoeLayerSpec(routed_expert_count=16, routed_topk=4, activation=SiluActivation(1.702),
+                         gate=GateTransform(limit=7.0, up_offset=1.0)),
+            3, (1, 5, 12, 33, 64), id="swiglu-both-biases",
+        ),
+        pytest.param(
+            MoeLayerSpec(routed_expert_count=16, routed_topk=4, activation=ReluActivation(),
+                         gate=GateTransform(limit=4.0, up_offset=-0.5)),
+            1, (3, 40), id="relu-gate-up-bias",
+        ),
+        pytest.param(
+            MoeLayerSpec(routed_expert_count=16, routed_topk=4, activation=GeluActivation("tanh")),
+            2, (2, 64), id="gelu-tanh-down-bias",
+        ),
+    ],
+)
+def test_moe_layer_biases_and_activations_through_its_template(device, spec, biases, replays):
+    # A MoE layer's projection biases (ProjectionSpec.bias_key) and the model's activation
+    # go into its signature and its replays: decode sizes on the grouped split kernel, 64-row
+    # grouped tiles above, every stage against the oracle.
+    hidden, intermediate, maximum = 512, 256, 64
+    w_gate_up, w_down, projection, correction, norm_weight = _layer(hidden, intermediate, spec, 950)
+    generator = torch.Generator().manual_seed(951)
+    i_bias = torch.randn((16, 2 * intermediate), generator=generator) * 0.5 if biases & 1 else None
+    o_bias = torch.randn((16, hidden), generator=generator) * 0.05 if biases & 2 else None
+    pool_rows = 2 * maximum + 3
+    capacities = derive_payload_row_capacities(maximum)
+    with FfnAgent(device) as agent:
+        _register(agent, spec, hidden, w_gate_up, w_down, projection, correction, norm_weight, device,
+                  i_bias=i_bias, o_bias=o_bias)
+        agent.materialize(maximum_row_capacity=maximum)
+        for rows in replays:
+            print(f"case biases={biases} rows={rows} spec={spec}", flush=True)
+            pool = o.generate_hidden_states(pool_rows, hidden, 952 + rows)
+            slots = o.generate_slots(pool_rows, rows, 953 + rows)
+            pool_gpu = to_device(pool, device)
+            agent.execute(instance_index=0, layer_ordinal=0, pool=pool_gpu, slots=slots_tensor(slots, device))
+            agent.check_health()
+            stages = _lane_stages(agent.lanes[0], spec, hidden, intermediate, select_capacity(capacities, rows), rows)
+            _check_replay(stages, pool, pool_gpu.cpu(), slots, spec, w_gate_up, w_down, projection, None,
+                          norm_weight, i_bias, o_bias)
 
 
 def test_moe_graph_dispatch_and_operator_chain_repeat_the_replay(device):

@@ -273,6 +273,9 @@ def test_moe_step_workspace_layout_and_descriptor_checks():
         ("routed_scaling_factor", 0.0, "scaling"),
         ("alpha", -1.0, "alpha"),
         ("limit", -1.0, "limit"),
+        ("activation", 0, "activation"),
+        ("approximate_tanh", 1, "tanh"),
+        ("biases", 4, "biases"),
     ):
         bad = _native.MoeLayerDesc.from_buffer_copy(good)
         setattr(bad, field, value)
@@ -286,7 +289,8 @@ def test_moe_step_workspace_layout_and_descriptor_checks():
     with pytest.raises(ValueError, match="1024"):
         MoeLayerSpec(routed_expert_count=1024, routed_topk=8, shared_expert_count=1)
     lib = _native.library()
-    assert lib.xp_moe_layer_register(None, 0, 0, ctypes.byref(good), None, None, None, None, None, 1e-6) != 0
+    assert lib.xp_moe_layer_register(None, 0, 0, ctypes.byref(good), None, None, None, None, None, None, None,
+                                     1e-6) != 0
     assert lib.xp_moe_template_capture(None, ctypes.byref(good), 4) != 0
 
 
