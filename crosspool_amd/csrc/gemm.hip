@@ -2260,8 +2260,8 @@ constexpr int split_depth(int groups) { return groups == 1 ? 4 : 3; }
 // (Four groups, 32 tokens, were measured and dropped: the token pieces read from L2 for each
 // weight line then cost more than the tile kernels, 60-77 us against 41-43 us for Qwen3-8B
 // gate_up at 17-32 rows.)
-// Every Dense kernel is instantiated for both payload dtypes (bf16, fp16); `payload`
-// (GemmArgs::payload) picks one.  The MoE projections are bf16 only.
+// Every Dense and grouped MoE kernel is instantiated for both payload dtypes (bf16, fp16);
+// `payload` (GemmArgs::payload) picks one.
 template <bool GATED>
 const void *split_kernel(int groups, bool gather, int32_t payload) {
   if (gather) {

@@ -13,8 +13,9 @@
  *     calling thread's message is available through xp_last_error().
  *     (Replaces the synchronous TORCH_CHECK -> RuntimeError errors of
  *     src/cext/transport/instance.cpp:82-119 and src/cext-bindings/ops.cpp:17-26.)
- *   - Payload rows are bf16 (`uint16_t` bit patterns), rows contiguous,
- *     hidden and intermediate sizes multiples of 8, pointers 16-byte aligned.
+ *   - Payload rows are bf16 or fp16 (`uint16_t` bit patterns, the dtype named by the call
+ *     or the layer), rows contiguous, hidden and intermediate sizes multiples of 8,
+ *     pointers 16-byte aligned.
  *   - Work is stream-ordered and never synchronises the host, except the
  *     functions documented as synchronous (health / synchronize).
  *   - Kernels that find a slot id outside the mailbox poison the gathered row
@@ -35,7 +36,7 @@
 extern "C" {
 #endif
 
-#define XP_ABI_VERSION 1
+#define XP_ABI_VERSION 2
 
 /* Status codes. */
 enum {

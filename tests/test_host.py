@@ -49,7 +49,7 @@ def test_library_exports_every_declared_symbol():
     for name in declared:
         assert hasattr(lib, name), f"{name} missing from {_native.LIBRARY_PATH}"
     assert set(declared) == set(_native.SIGNATURES), "ctypes signatures and header disagree"
-    assert lib.xp_abi_version() == 1
+    assert lib.xp_abi_version() == 2  # the MoE calls take payload dtypes, biases and activations
 
 
 def test_header_enums_match_the_reference_values():
