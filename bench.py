@@ -10,7 +10,9 @@ MFMA-bound north-star point), a ``decode`` entry at T = 32 (HBM-bound: the layer
 and the kernel-level gate_up's roofline beside the name of the kernel the layer runs), the
 batch sweep of BASELINE config 3, the roofline of the dominant kernel
 (measured with HIP events on the Lane stream it runs on) and the CPU
-baseline (the oracle's torch-CPU restatement on the host cores).
+baseline (the oracle's torch-CPU restatement on the host cores); beside them the
+other configs, a Qwen3-30B-A3B-shaped MoE layer with bf16 (``moe``) and fp16
+(``moe_fp16``) payloads, and the Qwen3-8B layer with fp16 payloads (``dense_fp16``).
 
 ``--kernels-only`` instead launches just the kernels whose hardware counters
 the roofline's ``traffic`` figure comes from (a byte copy of known size for
@@ -711,25 +713,25 @@ def main() -> int:
     # Dense layer: gather + RMSNorm, Router (128 experts, softmax top-8, renormalised),
     # Experts (hidden 2048, moe_intermediate 768), combine written to the slots.  Timed with
     # HIP events on the current stream.
-    moe = None
-    if not args.no_sweep:
+    def measure_moe(dtype: torch.dtype) -> dict:
         from crosspool_amd.moe import MoeFfnWeights, MoeLayerSpec, MoeRouterWeights
 
         m_hidden, m_inter, m_experts, m_topk = MOE_SHAPE
         generator = torch.Generator(device=device).manual_seed(18)
         moe_weights = MoeFfnWeights(
-            (torch.randn((m_experts, 2 * m_inter, m_hidden), device=device, generator=generator) * 0.02).bfloat16(),
-            (torch.randn((m_experts, m_hidden, m_inter), device=device, generator=generator) * 0.02).bfloat16(),
-            MoeRouterWeights((torch.randn((m_experts, m_hidden), device=device, generator=generator) * 0.02).bfloat16()),
+            (torch.randn((m_experts, 2 * m_inter, m_hidden), device=device, generator=generator) * 0.02).to(dtype),
+            (torch.randn((m_experts, m_hidden, m_inter), device=device, generator=generator) * 0.02).to(dtype),
+            MoeRouterWeights((torch.randn((m_experts, m_hidden), device=device, generator=generator) * 0.02).to(dtype)),
         )
         moe_spec = MoeLayerSpec(routed_expert_count=m_experts, routed_topk=m_topk)
         moe_agent = FfnAgent(device)
         moe_agent.register_moe_layer(instance_index=0, layer_ordinal=0, weights=moe_weights, spec=moe_spec,
-                                     norm_weight=torch.ones(m_hidden, dtype=torch.bfloat16, device=device))
+                                     norm_weight=torch.ones(m_hidden, dtype=dtype, device=device))
         moe_agent.materialize(maximum_row_capacity=max(MOE_TOKENS))
-        moe_pool = torch.randn((max(MOE_TOKENS) + 64, m_hidden), device=device, generator=generator).bfloat16()
-        moe = {"shape": {"hidden": m_hidden, "moe_intermediate": m_inter, "experts": m_experts, "topk": m_topk},
-               "execution": "MoE GraphTemplate replay (FfnAgent.register_moe_layer)", "points": []}
+        moe_pool = torch.randn((max(MOE_TOKENS) + 64, m_hidden), device=device, generator=generator).to(dtype)
+        entry = {"shape": {"hidden": m_hidden, "moe_intermediate": m_inter, "experts": m_experts, "topk": m_topk},
+                 "payload": str(dtype).removeprefix("torch."),
+                 "execution": "MoE GraphTemplate replay (FfnAgent.register_moe_layer)", "points": []}
         for t in MOE_TOKENS:
             moe_slots = torch.arange(t, dtype=torch.int32, device=device)
 
@@ -750,13 +752,13 @@ def main() -> int:
             moe_seconds = begin.elapsed_time(end) / 1e3 / launches
             capacity = select_capacity(derive_payload_row_capacities(max(MOE_TOKENS)), t)
             desc = moe_spec.signature(hidden_size=m_hidden, local_intermediate_size=m_inter,
-                                      payload_row_capacity=capacity).native_descriptor()
+                                      payload_row_capacity=capacity, payload_dtype=dtype).native_descriptor()
             ids_at = _native.moe_step_workspace_layout(desc, capacity)[4]
             ids = moe_agent.lanes[0].workspace[ids_at:ids_at + 4 * t * m_topk].view(torch.int32)
             active = int(torch.unique(ids).numel())
             flops = 2.0 * t * m_experts * m_hidden + 6.0 * t * m_topk * m_hidden * m_inter
             weight_bytes = 2.0 * m_experts * m_hidden + 6.0 * active * m_hidden * m_inter
-            moe["points"].append({
+            entry["points"].append({
                 "tokens": t, "us": round(moe_seconds * 1e6, 2), "tokens_per_s": round(t / moe_seconds, 1),
                 "active_experts": active,
                 "hbm_frac": round((weight_bytes + 4.0 * t * m_hidden) / moe_seconds / 1e9 / HBM_PEAK_GBS, 4),
@@ -765,7 +767,52 @@ def main() -> int:
             del moe_slots
         moe_agent.check_health()
         moe_agent.close()
-        del moe_weights, moe_pool
+        return entry
+
+    moe = moe_fp16 = None
+    if not args.no_sweep:
+        moe = measure_moe(torch.bfloat16)
+        moe_fp16 = measure_moe(torch.float16)
+
+    # ---------------------------------------------------------------- fp16 Dense layer
+    # The same Qwen3-8B layer with fp16 payloads (weights, norm and mailbox; the fp16
+    # instantiation of every kernel), two alternating copies, at a decode and the headline
+    # size.  The fp16 dense MFMA peak is the bf16 one.
+    dense_fp16 = None
+    if not args.no_sweep:
+        half_agent = FfnAgent(device)
+        for ordinal in (0, 1):
+            half_agent.register_layer(
+                instance_index=0, layer_ordinal=ordinal,
+                weights=DenseFfnWeights.from_tensors(weights.i_proj.values.half(), weights.o_proj.values.half()),
+                norm_weight=norm.half(), eps=1e-6,
+            )
+        half_agent.materialize(maximum_row_capacity=max_tokens)
+        half_lane = half_agent.lanes[0]
+        half_pool = pool.half()
+        dense_fp16 = {"payload": "float16", "points": []}
+        for t in (1, args.decode_tokens, args.tokens):
+            def half_replay(step: int, t=t) -> None:
+                half_lane.replay(instance_index=0, layer_ordinal=step % 2, pool=half_pool, slots=slots, rows=t,
+                                 stream=half_lane.stream)
+
+            for step in range(10):
+                half_replay(step)
+            torch.cuda.synchronize()
+            steps = 2 * args.sweep_steps
+            start = time.perf_counter()
+            for step in range(steps):
+                half_replay(step)
+            torch.cuda.synchronize()
+            seconds = (time.perf_counter() - start) / steps
+            dense_fp16["points"].append({
+                "tokens": t, "us": round(seconds * 1e6, 2), "tokens_per_s": round(t / seconds, 1),
+                "hbm_frac": round(layer_bytes(t) / seconds / 1e9 / HBM_PEAK_GBS, 4),
+                "mfma_frac": round(layer_flops(t) / seconds / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+            })
+        half_agent.check_health()
+        half_agent.close()
+        del half_pool
 
     # ---------------------------------------------------------------- ffn_shim transaction
     # Host-timed ffn_shim calls on resident [T, H] hidden states: through the Transport
@@ -876,6 +923,8 @@ def main() -> int:
         "graph_dispatch": graph_dispatch,
         "shim": shim,
         "moe": moe,
+        "moe_fp16": moe_fp16,
+        "dense_fp16": dense_fp16,
         "config2_stack": stack,
         "config4_colocated": colocated,
         "config5_shard": shard,
