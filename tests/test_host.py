@@ -470,3 +470,35 @@ def test_transport_entry_points_validate_before_any_device_call():
     assert lib.xp_transport_complete(None, 0, None, 0, _native.XP_DTYPE_BF16, 0, None) == _native.XP_ERROR_INVALID_ARGUMENT
     assert lib.xp_transport_probe(None, 0, 0, None, 0) == _native.XP_ERROR_INVALID_ARGUMENT
     assert lib.xp_transport_destroy(None) == _native.XP_OK
+
+
+def test_integration_argtypes_match_the_library():
+    # Every ctypes binding INTEGRATION.md shows a maintainer must match the signature table
+    # the package binds the library with (names and argument types, in order).
+    import re
+    from pathlib import Path
+
+    doc = (Path(__file__).resolve().parents[1] / "INTEGRATION.md").read_text()
+    kinds = {"P": ctypes.c_void_p, "INT": ctypes.c_int, "I64": ctypes.c_int64, "F32": ctypes.c_float,
+             "SIZE": ctypes.c_size_t}
+    checked = 0
+    for match in re.finditer(r"lib\.(xp_\w+)\.argtypes = \[", doc):
+        name = match.group(1)
+        depth, body = 0, ""
+        for ch in doc[match.end() - 1:]:
+            body += ch
+            depth += ch == "["
+            depth -= ch == "]"
+            if depth == 0:
+                break
+        body = re.sub(r"#[^\n]*", "", body)[1:-1]
+        tokens = [t.strip() for t in re.split(r",(?![^()]*\))", body.replace("\n", " ")) if t.strip()]
+        expected = _native.SIGNATURES[name][1]
+        assert len(tokens) == len(expected), name
+        for token, want in zip(tokens, expected):
+            if token in kinds:
+                assert kinds[token] is want, (name, token, want)
+            else:
+                assert token.startswith("ctypes.POINTER("), (name, token)
+        checked += 1
+    assert checked >= 20
